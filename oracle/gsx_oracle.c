@@ -1,0 +1,1533 @@
+/*
+ * gsx_oracle.c - CPU restatement of the gsx CPU backend algorithms on the training hot path.
+ *
+ * TEST INFRASTRUCTURE (see gsx_oracle.h): the checker for the gfx950 kernels, never part of
+ * the product. Compiled like the reference (C11, -O3, no -march => no FMA contraction) so
+ * that, on the same inputs, results are bit-identical to the reference CPU backend.
+ *
+ * Each function cites the reference lines whose arithmetic it restates, operation by
+ * operation: the order of float operations is part of the contract (a reordered sum moves
+ * alpha across the 1/255 threshold, gsx/src/gsx-cpu/render.c:106-111).
+ */
+#include "gsx_oracle.h"
+
+#include "../gsx_amd/csrc/gsx_math.h"
+
+#include <float.h>
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ---------------------------------------------------------------------------------------
+ * Constants: gsx/src/gsx-cpu/render.c:85-111, loss.c:120-132.
+ * ------------------------------------------------------------------------------------- */
+#define SH_C0 0.28209479177387814f
+#define SH_C1 0.4886025119029199f
+static const float k_sh_c2[5] = { 1.0925484305920792f, -1.0925484305920792f, 0.31539156525252005f,
+    -1.0925484305920792f, 0.5462742152960396f };
+static const float k_sh_c3[7] = { -0.5900435899266435f, 2.890611442640554f, -0.4570457994644658f,
+    0.3731763325901154f, -0.4570457994644658f, 1.445305721320277f, -0.5900435899266435f };
+#define MIN_ABS_Z 1.0e-8f
+#define MIN_QUAT_NORM_SQ 1.0e-20f
+#define COV2D_DILATION 0.3f
+#define POWER_THRESHOLD (-4.5f)
+#define MIN_ALPHA (1.0f / 255.0f)
+#define OPACITY_LOGIT_CULL (-5.537334267018537f)
+#define MAX_FRAGMENT_ALPHA 0.999f
+#define T_THRESHOLD 1.0e-4f
+
+typedef struct v3 {
+    float x, y, z;
+} v3;
+
+typedef struct m3 {
+    float m[3][3];
+} m3;
+
+typedef struct cam {
+    float fx, fy, cx, cy;
+    int32_t width, height;
+    float qx, qy, qz, qw;
+    float tx, ty, tz;
+    float near_plane, far_plane;
+    float bg[3];
+} cam;
+
+static cam cam_from(const float *c)
+{
+    cam k;
+
+    k.fx = c[0];
+    k.fy = c[1];
+    k.cx = c[2];
+    k.cy = c[3];
+    k.width = (int32_t)c[4];
+    k.height = (int32_t)c[5];
+    k.qx = c[6];
+    k.qy = c[7];
+    k.qz = c[8];
+    k.qw = c[9];
+    k.tx = c[10];
+    k.ty = c[11];
+    k.tz = c[12];
+    k.near_plane = c[13];
+    k.far_plane = c[14];
+    k.bg[0] = c[15];
+    k.bg[1] = c[16];
+    k.bg[2] = c[17];
+    return k;
+}
+
+static v3 mk3(float x, float y, float z)
+{
+    v3 v;
+
+    v.x = x;
+    v.y = y;
+    v.z = z;
+    return v;
+}
+
+/* render.c:397-407 */
+static float sigmoid_render(float x)
+{
+    if(x >= 0.0f) {
+        float z = expf(-x);
+        return 1.0f / (1.0f + z);
+    }
+    {
+        float z = expf(x);
+        return z / (1.0f + z);
+    }
+}
+
+/* render.c:421-451: normalised quaternion, identity below 1e-20 squared norm. */
+static int quat_normalize(float qx, float qy, float qz, float qw, float *nx, float *ny, float *nz, float *nw)
+{
+    float norm_sq = qx * qx + qy * qy + qz * qz + qw * qw;
+    float inv_norm;
+
+    if(norm_sq <= MIN_QUAT_NORM_SQ) {
+        *nx = 0.0f;
+        *ny = 0.0f;
+        *nz = 0.0f;
+        *nw = 1.0f;
+        return 0;
+    }
+    inv_norm = 1.0f / sqrtf(norm_sq);
+    *nx = qx * inv_norm;
+    *ny = qy * inv_norm;
+    *nz = qz * inv_norm;
+    *nw = qw * inv_norm;
+    return 1;
+}
+
+/* render.c:543-559 (zero-initialised triple-loop product) */
+static m3 m3_mul(m3 a, m3 b)
+{
+    m3 r;
+    int i, j, k;
+
+    for(i = 0; i < 3; ++i) {
+        for(j = 0; j < 3; ++j) {
+            r.m[i][j] = 0.0f;
+            for(k = 0; k < 3; ++k) {
+                r.m[i][j] += a.m[i][k] * b.m[k][j];
+            }
+        }
+    }
+    return r;
+}
+
+static m3 m3_t(m3 a)
+{
+    m3 r;
+    int i, j;
+
+    for(i = 0; i < 3; ++i) {
+        for(j = 0; j < 3; ++j) {
+            r.m[i][j] = a.m[j][i];
+        }
+    }
+    return r;
+}
+
+static v3 m3_v(m3 a, v3 v)
+{
+    return mk3(a.m[0][0] * v.x + a.m[0][1] * v.y + a.m[0][2] * v.z,
+        a.m[1][0] * v.x + a.m[1][1] * v.y + a.m[1][2] * v.z,
+        a.m[2][0] * v.x + a.m[2][1] * v.y + a.m[2][2] * v.z);
+}
+
+/* render.c:561-581 */
+static m3 rotation_from_xyzw(float qx_raw, float qy_raw, float qz_raw, float qw_raw)
+{
+    m3 r;
+    float qx, qy, qz, qw;
+
+    (void)quat_normalize(qx_raw, qy_raw, qz_raw, qw_raw, &qx, &qy, &qz, &qw);
+    r.m[0][0] = 1.0f - 2.0f * (qy * qy + qz * qz);
+    r.m[0][1] = 2.0f * (qx * qy - qw * qz);
+    r.m[0][2] = 2.0f * (qx * qz + qw * qy);
+    r.m[1][0] = 2.0f * (qx * qy + qw * qz);
+    r.m[1][1] = 1.0f - 2.0f * (qx * qx + qz * qz);
+    r.m[1][2] = 2.0f * (qy * qz - qw * qx);
+    r.m[2][0] = 2.0f * (qx * qz - qw * qy);
+    r.m[2][1] = 2.0f * (qy * qz + qw * qx);
+    r.m[2][2] = 1.0f - 2.0f * (qx * qx + qy * qy);
+    return r;
+}
+
+/* render.c:583-601: Sigma = (R S)(R S)^T, S = diag(exp(logscale)). */
+static m3 cov3d_from(const float *q, const float *ls)
+{
+    m3 rs = rotation_from_xyzw(q[0], q[1], q[2], q[3]);
+    float sx = expf(ls[0]);
+    float sy = expf(ls[1]);
+    float sz = expf(ls[2]);
+    int row;
+
+    for(row = 0; row < 3; ++row) {
+        rs.m[row][0] *= sx;
+        rs.m[row][1] *= sy;
+        rs.m[row][2] *= sz;
+    }
+    return m3_mul(rs, m3_t(rs));
+}
+
+typedef struct projected {
+    float mx, my, a, b, c, depth, xc, yc, zc;
+} projected;
+
+/* render.c:611-668: EWA projection without Jacobian clamp, +0.3 dilation. */
+static int project(v3 mean, m3 cov3d, const cam *k, m3 w, projected *out)
+{
+    v3 mc = m3_v(w, mean);
+    m3 cov_cam;
+    float inv_z, inv_z2, j00, j02, j11, j12, jc00, jc01, jc02, jc11, jc12;
+
+    mc = mk3(mc.x + k->tx, mc.y + k->ty, mc.z + k->tz);
+    cov_cam = m3_mul(m3_mul(w, cov3d), m3_t(w));
+    if(fabsf(mc.z) < MIN_ABS_Z) {
+        memset(out, 0, sizeof(*out));
+        return 0;
+    }
+    inv_z = 1.0f / mc.z;
+    inv_z2 = inv_z * inv_z;
+    j00 = k->fx * inv_z;
+    j02 = -k->fx * mc.x * inv_z2;
+    j11 = k->fy * inv_z;
+    j12 = -k->fy * mc.y * inv_z2;
+    jc00 = j00 * cov_cam.m[0][0] + j02 * cov_cam.m[2][0];
+    jc01 = j00 * cov_cam.m[0][1] + j02 * cov_cam.m[2][1];
+    jc02 = j00 * cov_cam.m[0][2] + j02 * cov_cam.m[2][2];
+    jc11 = j11 * cov_cam.m[1][1] + j12 * cov_cam.m[2][1];
+    jc12 = j11 * cov_cam.m[1][2] + j12 * cov_cam.m[2][2];
+    out->mx = k->fx * mc.x * inv_z + k->cx;
+    out->my = k->fy * mc.y * inv_z + k->cy;
+    out->a = jc00 * j00 + jc02 * j02 + COV2D_DILATION;
+    out->b = jc01 * j11 + jc02 * j12;
+    out->c = jc11 * j11 + jc12 * j12 + COV2D_DILATION;
+    out->depth = mc.z;
+    out->xc = mc.x;
+    out->yc = mc.y;
+    out->zc = mc.z;
+    return 1;
+}
+
+/* render.c:670-694: 3-sigma pixel box from the larger eigenvalue, clamped to the image. */
+static void bbox_of(float a, float b, float c, float mx, float my, int32_t width, int32_t height, int32_t *bb)
+{
+    float trace = a + c;
+    float det = a * c - b * b;
+    float disc = sqrtf(fmaxf(0.0f, trace * trace * 0.25f - det));
+    float l1 = trace * 0.5f + disc;
+    float l2 = trace * 0.5f - disc;
+    float radius = 3.0f * sqrtf(fmaxf(l1, l2));
+
+    bb[0] = (int32_t)fmaxf(0.0f, floorf(mx - radius));
+    bb[1] = (int32_t)fminf((float)(width - 1), ceilf(mx + radius));
+    bb[2] = (int32_t)fmaxf(0.0f, floorf(my - radius));
+    bb[3] = (int32_t)fminf((float)(height - 1), ceilf(my + radius));
+}
+
+static v3 sh_coeff(const float *sh, int64_t g, int count, int idx)
+{
+    const float *p = sh + ((size_t)g * (size_t)count + (size_t)idx) * 3u;
+
+    return mk3(p[0], p[1], p[2]);
+}
+
+static v3 v3_add_scaled(v3 acc, v3 c, float s)
+{
+    return mk3(acc.x + c.x * s, acc.y + c.y * s, acc.z + c.z * s);
+}
+
+/* render.c:730-828: SH colour, clamped at max(c + 0.5, 0). */
+static v3 eval_sh(int64_t g, int deg, v3 d, const float *sh0, const float *sh1, const float *sh2, const float *sh3)
+{
+    v3 r = mk3(SH_C0 * sh0[g * 3 + 0], SH_C0 * sh0[g * 3 + 1], SH_C0 * sh0[g * 3 + 2]);
+
+    if(deg >= 1) {
+        float x = d.x, y = d.y, z = d.z;
+
+        r = v3_add_scaled(r, sh_coeff(sh1, g, 3, 0), -SH_C1 * y);
+        r = v3_add_scaled(r, sh_coeff(sh1, g, 3, 1), SH_C1 * z);
+        r = v3_add_scaled(r, sh_coeff(sh1, g, 3, 2), -SH_C1 * x);
+        if(deg >= 2) {
+            float xx = x * x, yy = y * y, zz = z * z, xy = x * y, yz = y * z, xz = x * z;
+            float basis2[5];
+            int i;
+
+            basis2[0] = k_sh_c2[0] * xy;
+            basis2[1] = k_sh_c2[1] * yz;
+            basis2[2] = k_sh_c2[2] * (2.0f * zz - xx - yy);
+            basis2[3] = k_sh_c2[3] * xz;
+            basis2[4] = k_sh_c2[4] * (xx - yy);
+            for(i = 0; i < 5; ++i) {
+                r = v3_add_scaled(r, sh_coeff(sh2, g, 5, i), basis2[i]);
+            }
+            if(deg >= 3) {
+                float basis3[7];
+
+                basis3[0] = k_sh_c3[0] * y * (3.0f * xx - yy);
+                basis3[1] = k_sh_c3[1] * xy * z;
+                basis3[2] = k_sh_c3[2] * y * (4.0f * zz - xx - yy);
+                basis3[3] = k_sh_c3[3] * z * (2.0f * zz - 3.0f * xx - 3.0f * yy);
+                basis3[4] = k_sh_c3[4] * x * (4.0f * zz - xx - yy);
+                basis3[5] = k_sh_c3[5] * z * (xx - yy);
+                basis3[6] = k_sh_c3[6] * x * (xx - 3.0f * yy);
+                for(i = 0; i < 7; ++i) {
+                    r = v3_add_scaled(r, sh_coeff(sh3, g, 7, i), basis3[i]);
+                }
+            }
+        }
+    }
+    r.x = fmaxf(r.x + 0.5f, 0.0f);
+    r.y = fmaxf(r.y + 0.5f, 0.0f);
+    r.z = fmaxf(r.z + 0.5f, 0.0f);
+    return r;
+}
+
+/* render.c:603-609 */
+static v3 camera_centre(const cam *k, m3 w)
+{
+    v3 c = m3_v(m3_t(w), mk3(k->tx, k->ty, k->tz));
+
+    return mk3(c.x * -1.0f, c.y * -1.0f, c.z * -1.0f);
+}
+
+typedef struct vis {
+    int64_t g;
+    int32_t bb[4];
+    float rec[ORACLE_REC_FLOATS];
+} vis;
+
+/* render.c:850-1016 (count_visible + fill_visible in one pass): culls, projection, bbox,
+ * sigmoid opacity and SH colour, in ascending Gaussian order. Returns the visible count. */
+static int64_t collect_visible(int64_t n, int deg, const float *mean3d, const float *rot, const float *ls,
+    const float *op, const float *sh0, const float *sh1, const float *sh2, const float *sh3, const cam *k,
+    vis *out, float *visible_counter)
+{
+    m3 w = rotation_from_xyzw(k->qx, k->qy, k->qz, k->qw);
+    v3 cc = camera_centre(k, w);
+    int64_t count = 0;
+    int64_t i;
+
+    for(i = 0; i < n; ++i) {
+        v3 mean = mk3(mean3d[i * 3 + 0], mean3d[i * 3 + 1], mean3d[i * 3 + 2]);
+        m3 cov3d = cov3d_from(rot + i * 4, ls + i * 3);
+        projected p;
+        float det;
+        int32_t bb[4];
+
+        if(op[i] <= OPACITY_LOGIT_CULL) {
+            continue;
+        }
+        if(!project(mean, cov3d, k, w, &p)) {
+            continue;
+        }
+        det = p.a * p.c - p.b * p.b;
+        if(p.depth < k->near_plane || p.depth > k->far_plane || det <= 0.0f) {
+            continue;
+        }
+        bbox_of(p.a, p.b, p.c, p.mx, p.my, k->width, k->height, bb);
+        if(bb[0] > bb[1] || bb[2] > bb[3]) {
+            continue;
+        }
+        if(visible_counter != NULL) {
+            visible_counter[i] += 1.0f;
+        }
+        if(out != NULL) {
+            vis *v = &out[count];
+            v3 d;
+            v3 col;
+            float len;
+
+            v->g = i;
+            memcpy(v->bb, bb, sizeof(bb));
+            v->rec[ORACLE_REC_MEAN2D_X] = p.mx;
+            v->rec[ORACLE_REC_MEAN2D_Y] = p.my;
+            v->rec[ORACLE_REC_COV_A] = p.a;
+            v->rec[ORACLE_REC_COV_B] = p.b;
+            v->rec[ORACLE_REC_COV_C] = p.c;
+            v->rec[ORACLE_REC_INV_DET] = 1.0f / det;
+            v->rec[ORACLE_REC_DEPTH] = p.depth;
+            v->rec[ORACLE_REC_X_CAM] = p.xc;
+            v->rec[ORACLE_REC_Y_CAM] = p.yc;
+            v->rec[ORACLE_REC_Z_CAM] = p.zc;
+            v->rec[ORACLE_REC_RAW_OPACITY] = op[i];
+            v->rec[ORACLE_REC_OPACITY] = sigmoid_render(op[i]);
+            /* render.c:487-496 normalise(mean - camera centre) */
+            d = mk3(mean.x - cc.x, mean.y - cc.y, mean.z - cc.z);
+            len = sqrtf(d.x * d.x + d.y * d.y + d.z * d.z);
+            if(len <= 0.0f) {
+                d = mk3(0.0f, 0.0f, 0.0f);
+            } else {
+                float s = 1.0f / len;
+                d = mk3(d.x * s, d.y * s, d.z * s);
+            }
+            col = eval_sh(i, deg, d, sh0, sh1, sh2, sh3);
+            v->rec[ORACLE_REC_DIR_X] = d.x;
+            v->rec[ORACLE_REC_DIR_Y] = d.y;
+            v->rec[ORACLE_REC_DIR_Z] = d.z;
+            v->rec[ORACLE_REC_COLOR_R] = col.x;
+            v->rec[ORACLE_REC_COLOR_G] = col.y;
+            v->rec[ORACLE_REC_COLOR_B] = col.z;
+        }
+        count += 1;
+    }
+    return count;
+}
+
+/* render.c:830-848: total order by (depth, Gaussian index). */
+static int cmp_vis(const void *pa, const void *pb)
+{
+    const vis *a = (const vis *)pa;
+    const vis *b = (const vis *)pb;
+
+    if(a->rec[ORACLE_REC_DEPTH] < b->rec[ORACLE_REC_DEPTH]) return -1;
+    if(a->rec[ORACLE_REC_DEPTH] > b->rec[ORACLE_REC_DEPTH]) return 1;
+    if(a->g < b->g) return -1;
+    if(a->g > b->g) return 1;
+    return 0;
+}
+
+/* Per-visible preprocess output in Gaussian-index order (the order fill_visible emits).
+ * out_index[v] = Gaussian index, out_rec[v*ORACLE_REC_FLOATS..], out_bbox[v*4..] =
+ * x_min, x_max, y_min, y_max. Returns V. Buffers must hold n entries. */
+int64_t oracle_preprocess(int64_t n, int sh_degree, const float *mean3d, const float *rotation,
+    const float *logscale, const float *opacity, const float *sh0, const float *sh1, const float *sh2,
+    const float *sh3, const float *camera, int64_t *out_index, float *out_rec, int32_t *out_bbox)
+{
+    cam k = cam_from(camera);
+    vis *v = (vis *)malloc(sizeof(vis) * (size_t)(n > 0 ? n : 1));
+    int64_t count, i;
+
+    if(v == NULL) return -1;
+    count = collect_visible(n, sh_degree, mean3d, rotation, logscale, opacity, sh0, sh1, sh2, sh3, &k, v, NULL);
+    for(i = 0; i < count; ++i) {
+        out_index[i] = v[i].g;
+        memcpy(out_rec + i * ORACLE_REC_FLOATS, v[i].rec, sizeof(v[i].rec));
+        memcpy(out_bbox + i * 4, v[i].bb, sizeof(v[i].bb));
+    }
+    free(v);
+    return count;
+}
+
+/* ---------------------------------------------------------------------------------------
+ * Tile restatement (no CPU counterpart; the CPU rasterises per Gaussian bbox,
+ * render.c:1035-1079). tiles(g) = { (tx,ty): x_min/T <= tx <= x_max/T, y_min/T <= ty <= y_max/T }
+ * key = (ty * ceil(W/T) + tx) << 32 | float_bits(depth), value = Gaussian index, emitted in
+ * ascending Gaussian order, then stably sorted by key. Since depth > near > 0, the float
+ * bits order like the values, so each tile's list is the CPU (depth, index) order restricted
+ * to the Gaussians whose bbox meets the tile.
+ * ------------------------------------------------------------------------------------- */
+typedef struct kv {
+    uint64_t key;
+    uint32_t value;
+    uint64_t seq;
+} kv;
+
+static int cmp_kv(const void *pa, const void *pb)
+{
+    const kv *a = (const kv *)pa;
+    const kv *b = (const kv *)pb;
+
+    if(a->key < b->key) return -1;
+    if(a->key > b->key) return 1;
+    if(a->seq < b->seq) return -1;
+    if(a->seq > b->seq) return 1;
+    return 0;
+}
+
+/* Returns the instance count I; writes sorted keys/values when capacity allows (else -I-1). */
+int64_t oracle_tile_keys(int64_t n, int sh_degree, const float *mean3d, const float *rotation,
+    const float *logscale, const float *opacity, const float *sh0, const float *sh1, const float *sh2,
+    const float *sh3, const float *camera, int32_t tile_size, int64_t capacity, uint64_t *out_keys,
+    uint32_t *out_values)
+{
+    cam k = cam_from(camera);
+    vis *v = (vis *)malloc(sizeof(vis) * (size_t)(n > 0 ? n : 1));
+    int64_t count, i, total = 0;
+    int32_t tiles_x = (k.width + tile_size - 1) / tile_size;
+    kv *pairs;
+
+    if(v == NULL) return -1;
+    count = collect_visible(n, sh_degree, mean3d, rotation, logscale, opacity, sh0, sh1, sh2, sh3, &k, v, NULL);
+    for(i = 0; i < count; ++i) {
+        total += (int64_t)(v[i].bb[1] / tile_size - v[i].bb[0] / tile_size + 1)
+            * (int64_t)(v[i].bb[3] / tile_size - v[i].bb[2] / tile_size + 1);
+    }
+    if(total > capacity) {
+        free(v);
+        return -total - 1;
+    }
+    pairs = (kv *)malloc(sizeof(kv) * (size_t)(total > 0 ? total : 1));
+    if(pairs == NULL) {
+        free(v);
+        return -1;
+    }
+    total = 0;
+    for(i = 0; i < count; ++i) {
+        int32_t tx, ty;
+        uint32_t depth_bits = gsx_f32_bits(v[i].rec[ORACLE_REC_DEPTH]);
+
+        for(ty = v[i].bb[2] / tile_size; ty <= v[i].bb[3] / tile_size; ++ty) {
+            for(tx = v[i].bb[0] / tile_size; tx <= v[i].bb[1] / tile_size; ++tx) {
+                uint64_t tile = (uint64_t)ty * (uint64_t)tiles_x + (uint64_t)tx;
+
+                pairs[total].key = (tile << 32) | (uint64_t)depth_bits;
+                pairs[total].value = (uint32_t)v[i].g;
+                pairs[total].seq = (uint64_t)total;
+                total += 1;
+            }
+        }
+    }
+    qsort(pairs, (size_t)total, sizeof(kv), cmp_kv);
+    for(i = 0; i < total; ++i) {
+        out_keys[i] = pairs[i].key;
+        out_values[i] = pairs[i].value;
+    }
+    free(pairs);
+    free(v);
+    return total;
+}
+
+/* [start, end) of every tile in the sorted key array; empty tiles get (0, 0). */
+void oracle_tile_ranges(int64_t instance_count, const uint64_t *keys, int64_t tile_count, uint32_t *out_ranges)
+{
+    int64_t i;
+
+    memset(out_ranges, 0, sizeof(uint32_t) * 2u * (size_t)tile_count);
+    for(i = 0; i < instance_count; ++i) {
+        uint64_t tile = keys[i] >> 32;
+
+        if(i == 0 || (keys[i - 1] >> 32) != tile) {
+            out_ranges[tile * 2 + 0] = (uint32_t)i;
+        }
+        if(i == instance_count - 1 || (keys[i + 1] >> 32) != tile) {
+            out_ranges[tile * 2 + 1] = (uint32_t)(i + 1);
+        }
+    }
+}
+
+/* ---------------------------------------------------------------------------------------
+ * Forward blend: render.c:1018-1088, 1254-1365.
+ * out_rgb [3,H,W]; out_t (nullable) [H,W] final transmittance; visible_counter (nullable)
+ * incremented as a TRAIN forward does (render.c:980-982).
+ * ------------------------------------------------------------------------------------- */
+int oracle_render_forward(int64_t n, int sh_degree, const float *mean3d, const float *rotation,
+    const float *logscale, const float *opacity, const float *sh0, const float *sh1, const float *sh2,
+    const float *sh3, const float *camera, float *out_rgb, float *out_t, float *visible_counter)
+{
+    cam k = cam_from(camera);
+    size_t pixels = (size_t)k.width * (size_t)k.height;
+    vis *v = (vis *)malloc(sizeof(vis) * (size_t)(n > 0 ? n : 1));
+    float *t = (float *)malloc(sizeof(float) * (pixels > 0 ? pixels : 1));
+    int64_t count, vi;
+    size_t p;
+
+    if(v == NULL || t == NULL) {
+        free(v);
+        free(t);
+        return -1;
+    }
+    count = collect_visible(n, sh_degree, mean3d, rotation, logscale, opacity, sh0, sh1, sh2, sh3, &k, v,
+        visible_counter);
+    memset(out_rgb, 0, sizeof(float) * 3u * pixels);
+    for(p = 0; p < pixels; ++p) {
+        t[p] = 1.0f;
+    }
+    qsort(v, (size_t)count, sizeof(vis), cmp_vis);
+    for(vi = 0; vi < count; ++vi) {
+        const float *r = v[vi].rec;
+        float inv_a = r[ORACLE_REC_COV_C] * r[ORACLE_REC_INV_DET];
+        float inv_b = -r[ORACLE_REC_COV_B] * r[ORACLE_REC_INV_DET];
+        float inv_c = r[ORACLE_REC_COV_A] * r[ORACLE_REC_INV_DET];
+        int32_t px, py;
+
+        for(py = v[vi].bb[2]; py <= v[vi].bb[3]; ++py) {
+            for(px = v[vi].bb[0]; px <= v[vi].bb[1]; ++px) {
+                float dx = ((float)px + 0.5f) - r[ORACLE_REC_MEAN2D_X];
+                float dy = ((float)py + 0.5f) - r[ORACLE_REC_MEAN2D_Y];
+                float power = -0.5f * (inv_a * dx * dx + 2.0f * inv_b * dx * dy + inv_c * dy * dy);
+                size_t pix = (size_t)py * (size_t)k.width + (size_t)px;
+                float alpha, tb, wgt;
+
+                if(power > 0.0f) power = 0.0f;
+                if(power < POWER_THRESHOLD) continue;
+                alpha = fminf(MAX_FRAGMENT_ALPHA, r[ORACLE_REC_OPACITY] * expf(power));
+                if(alpha < MIN_ALPHA) continue;
+                tb = t[pix];
+                if(tb < T_THRESHOLD) continue;
+                wgt = alpha * tb;
+                out_rgb[0 * pixels + pix] += wgt * r[ORACLE_REC_COLOR_R];
+                out_rgb[1 * pixels + pix] += wgt * r[ORACLE_REC_COLOR_G];
+                out_rgb[2 * pixels + pix] += wgt * r[ORACLE_REC_COLOR_B];
+                t[pix] = tb * (1.0f - alpha);
+            }
+        }
+    }
+    for(p = 0; p < pixels; ++p) {
+        out_rgb[0 * pixels + p] += t[p] * k.bg[0];
+        out_rgb[1 * pixels + p] += t[p] * k.bg[1];
+        out_rgb[2 * pixels + p] += t[p] * k.bg[2];
+    }
+    if(out_t != NULL) {
+        memcpy(out_t, t, sizeof(float) * pixels);
+    }
+    free(t);
+    free(v);
+    return 0;
+}
+
+/* ---------------------------------------------------------------------------------------
+ * Backward: render.c:1367-1975. Gradient sinks are overwritten (zeroed, then accumulated,
+ * render.c:1537-1550). Per-Gaussian accumulation runs back to front exactly as the CPU.
+ * ------------------------------------------------------------------------------------- */
+typedef struct contrib {
+    int32_t pixel;
+    float alpha;
+    float t_before;
+} contrib;
+
+static void add_sh_grad(float *g, int64_t gi, int count, int idx, v3 d)
+{
+    float *p = g + ((size_t)gi * (size_t)count + (size_t)idx) * 3u;
+
+    p[0] += d.x;
+    p[1] += d.y;
+    p[2] += d.z;
+}
+
+/* render.c:714-728 */
+static void add_dir_grad(v3 *ddir, v3 dcol, v3 coeff, float bx, float by, float bz)
+{
+    float s = dcol.x * coeff.x + dcol.y * coeff.y + dcol.z * coeff.z;
+
+    ddir->x += s * bx;
+    ddir->y += s * by;
+    ddir->z += s * bz;
+}
+
+static v3 v3_scale(v3 a, float s)
+{
+    return mk3(a.x * s, a.y * s, a.z * s);
+}
+
+int oracle_render_backward(int64_t n, int deg, const float *mean3d, const float *rotation, const float *logscale,
+    const float *opacity, const float *sh0, const float *sh1, const float *sh2, const float *sh3,
+    const float *camera, const float *grad_rgb, float *g_mean3d, float *g_rotation, float *g_logscale,
+    float *g_opacity, float *g_sh0, float *g_sh1, float *g_sh2, float *g_sh3)
+{
+    cam k = cam_from(camera);
+    m3 w = rotation_from_xyzw(k.qx, k.qy, k.qz, k.qw);
+    v3 cc = camera_centre(&k, w);
+    size_t pixels = (size_t)k.width * (size_t)k.height;
+    vis *v = (vis *)malloc(sizeof(vis) * (size_t)(n > 0 ? n : 1));
+    float *t = (float *)malloc(sizeof(float) * (pixels > 0 ? pixels : 1));
+    v3 *suffix = (v3 *)malloc(sizeof(v3) * (pixels > 0 ? pixels : 1));
+    int64_t *offsets = NULL;
+    contrib *contribs = NULL;
+    int64_t count, vi, capacity = 0, total = 0;
+    size_t p;
+
+    if(v == NULL || t == NULL || suffix == NULL) {
+        free(v);
+        free(t);
+        free(suffix);
+        return -1;
+    }
+    count = collect_visible(n, deg, mean3d, rotation, logscale, opacity, sh0, sh1, sh2, sh3, &k, v, NULL);
+    for(vi = 0; vi < count; ++vi) {
+        capacity += (int64_t)(v[vi].bb[1] - v[vi].bb[0] + 1) * (int64_t)(v[vi].bb[3] - v[vi].bb[2] + 1);
+    }
+    offsets = (int64_t *)malloc(sizeof(int64_t) * (size_t)(count + 1));
+    contribs = (contrib *)malloc(sizeof(contrib) * (size_t)(capacity > 0 ? capacity : 1));
+    if(offsets == NULL || contribs == NULL) {
+        free(v);
+        free(t);
+        free(suffix);
+        free(offsets);
+        free(contribs);
+        return -1;
+    }
+    qsort(v, (size_t)count, sizeof(vis), cmp_vis);
+    for(p = 0; p < pixels; ++p) {
+        t[p] = 1.0f;
+    }
+    /* render.c:1476-1515: re-raster, recording (alpha, T_before) per contribution. */
+    for(vi = 0; vi < count; ++vi) {
+        const float *r = v[vi].rec;
+        float inv_a = r[ORACLE_REC_COV_C] * r[ORACLE_REC_INV_DET];
+        float inv_b = -r[ORACLE_REC_COV_B] * r[ORACLE_REC_INV_DET];
+        float inv_c = r[ORACLE_REC_COV_A] * r[ORACLE_REC_INV_DET];
+        int32_t px, py;
+
+        offsets[vi] = total;
+        for(py = v[vi].bb[2]; py <= v[vi].bb[3]; ++py) {
+            for(px = v[vi].bb[0]; px <= v[vi].bb[1]; ++px) {
+                float dx = ((float)px + 0.5f) - r[ORACLE_REC_MEAN2D_X];
+                float dy = ((float)py + 0.5f) - r[ORACLE_REC_MEAN2D_Y];
+                float power = -0.5f * (inv_a * dx * dx + 2.0f * inv_b * dx * dy + inv_c * dy * dy);
+                size_t pix = (size_t)py * (size_t)k.width + (size_t)px;
+                float tb = t[pix];
+                float alpha;
+
+                if(power > 0.0f) power = 0.0f;
+                if(power < POWER_THRESHOLD) continue;
+                alpha = fminf(MAX_FRAGMENT_ALPHA, r[ORACLE_REC_OPACITY] * expf(power));
+                if(alpha < MIN_ALPHA || tb < T_THRESHOLD) continue;
+                contribs[total].pixel = (int32_t)pix;
+                contribs[total].alpha = alpha;
+                contribs[total].t_before = tb;
+                total += 1;
+                t[pix] = tb * (1.0f - alpha);
+            }
+        }
+    }
+    offsets[count] = total;
+
+    memset(g_mean3d, 0, sizeof(float) * 3u * (size_t)n);
+    memset(g_rotation, 0, sizeof(float) * 4u * (size_t)n);
+    memset(g_logscale, 0, sizeof(float) * 3u * (size_t)n);
+    memset(g_sh0, 0, sizeof(float) * 3u * (size_t)n);
+    memset(g_opacity, 0, sizeof(float) * (size_t)n);
+    if(deg >= 1 && g_sh1 != NULL) memset(g_sh1, 0, sizeof(float) * 9u * (size_t)n);
+    if(deg >= 2 && g_sh2 != NULL) memset(g_sh2, 0, sizeof(float) * 15u * (size_t)n);
+    if(deg >= 3 && g_sh3 != NULL) memset(g_sh3, 0, sizeof(float) * 21u * (size_t)n);
+    for(p = 0; p < pixels; ++p) {
+        suffix[p] = mk3(t[p] * k.bg[0], t[p] * k.bg[1], t[p] * k.bg[2]);
+    }
+
+    for(vi = count; vi > 0; --vi) {
+        const vis *e = &v[vi - 1];
+        const float *r = e->rec;
+        int64_t gi = e->g;
+        float ca = r[ORACLE_REC_COV_A], cb = r[ORACLE_REC_COV_B], cc2 = r[ORACLE_REC_COV_C];
+        float inv_det = r[ORACLE_REC_INV_DET];
+        float inv_a = cc2 * inv_det;
+        float inv_b = -cb * inv_det;
+        float inv_c = ca * inv_det;
+        float det = ca * cc2 - cb * cb;
+        float inv_det2 = 1.0f / (det * det);
+        float dcx = 0.0f, dcy = 0.0f, dcz = 0.0f, dmx = 0.0f, dmy = 0.0f;
+        float dca = 0.0f, dcb = 0.0f, dcc = 0.0f, dop = 0.0f;
+        const float *q = rotation + gi * 4;
+        const float *ls = logscale + gi * 3;
+        m3 cov3d = cov3d_from(q, ls);
+        m3 rot = rotation_from_xyzw(q[0], q[1], q[2], q[3]);
+        m3 srot = rot;
+        m3 d_cov3d, d_rs, d_r, dsum;
+        float sx = expf(ls[0]), sy = expf(ls[1]), sz = expf(ls[2]);
+        float zc = r[ORACLE_REC_Z_CAM], xc = r[ORACLE_REC_X_CAM], yc = r[ORACLE_REC_Y_CAM];
+        float j00 = k.fx / zc;
+        float j02 = -k.fx * xc / (zc * zc);
+        float j11 = k.fy / zc;
+        float j12 = -k.fy * yc / (zc * zc);
+        float mm[2][3];
+        int row, col;
+        int64_t ci;
+
+        /* render.c:1608-1656 */
+        for(ci = offsets[vi - 1]; ci < offsets[vi]; ++ci) {
+            const contrib *c = &contribs[ci];
+            size_t pix = (size_t)c->pixel;
+            int32_t py = c->pixel / k.width;
+            int32_t px = c->pixel % k.width;
+            float dox = grad_rgb[0 * pixels + pix];
+            float doy = grad_rgb[1 * pixels + pix];
+            float doz = grad_rgb[2 * pixels + pix];
+            float dx = ((float)px + 0.5f) - r[ORACLE_REC_MEAN2D_X];
+            float dy = ((float)py + 0.5f) - r[ORACLE_REC_MEAN2D_Y];
+            float power = -0.5f * (inv_a * dx * dx + 2.0f * inv_b * dx * dy + inv_c * dy * dy);
+            float gv = expf(power > 0.0f ? 0.0f : power);
+            float alpha = c->alpha;
+            float tb = c->t_before;
+            float wgt = alpha * tb;
+            v3 s = suffix[pix];
+            float dalpha = tb * (r[ORACLE_REC_COLOR_R] * dox + r[ORACLE_REC_COLOR_G] * doy + r[ORACLE_REC_COLOR_B] * doz);
+            float dg = 0.0f, dpow, dia, dib, dic;
+
+            dcx += wgt * dox;
+            dcy += wgt * doy;
+            dcz += wgt * doz;
+            if(fabsf(1.0f - alpha) > 1.0e-6f) {
+                dalpha -= (s.x * dox + s.y * doy + s.z * doz) / (1.0f - alpha);
+            }
+            if(r[ORACLE_REC_OPACITY] * gv < MAX_FRAGMENT_ALPHA) {
+                dg = dalpha * r[ORACLE_REC_OPACITY];
+                dop += dalpha * gv;
+            }
+            dpow = dg * gv;
+            dmx += dpow * (inv_a * dx + inv_b * dy);
+            dmy += dpow * (inv_b * dx + inv_c * dy);
+            dia = dpow * (-0.5f * dx * dx);
+            dib = dpow * (-dx * dy);
+            dic = dpow * (-0.5f * dy * dy);
+            dca += dia * (-cc2 * cc2 * inv_det2) + dib * (cb * cc2 * inv_det2) + dic * (-cb * cb * inv_det2);
+            dcb += dia * (2.0f * cb * cc2 * inv_det2) + dib * (-(ca * cc2 + cb * cb) * inv_det2)
+                + dic * (2.0f * ca * cb * inv_det2);
+            dcc += dia * (-cb * cb * inv_det2) + dib * (ca * cb * inv_det2) + dic * (-ca * ca * inv_det2);
+        }
+        /* render.c:1658-1665 */
+        for(ci = offsets[vi - 1]; ci < offsets[vi]; ++ci) {
+            size_t pix = (size_t)contribs[ci].pixel;
+            float wgt = contribs[ci].alpha * contribs[ci].t_before;
+
+            suffix[pix].x += wgt * r[ORACLE_REC_COLOR_R];
+            suffix[pix].y += wgt * r[ORACLE_REC_COLOR_G];
+            suffix[pix].z += wgt * r[ORACLE_REC_COLOR_B];
+        }
+        /* render.c:1667-1828: colour clamp mask, SH and view-direction gradients. */
+        {
+            v3 dcol = mk3(dcx * (r[ORACLE_REC_COLOR_R] > 0.0f ? 1.0f : 0.0f),
+                dcy * (r[ORACLE_REC_COLOR_G] > 0.0f ? 1.0f : 0.0f),
+                dcz * (r[ORACLE_REC_COLOR_B] > 0.0f ? 1.0f : 0.0f));
+            v3 ddir = mk3(0.0f, 0.0f, 0.0f);
+            float x = r[ORACLE_REC_DIR_X], y = r[ORACLE_REC_DIR_Y], z = r[ORACLE_REC_DIR_Z];
+            float xx = x * x, yy = y * y, zz = z * z, xy = x * y, yz = y * z, xz = x * z;
+
+            g_sh0[gi * 3 + 0] += SH_C0 * dcol.x;
+            g_sh0[gi * 3 + 1] += SH_C0 * dcol.y;
+            g_sh0[gi * 3 + 2] += SH_C0 * dcol.z;
+            if(deg >= 1 && g_sh1 != NULL) {
+                add_sh_grad(g_sh1, gi, 3, 0, v3_scale(dcol, -SH_C1 * y));
+                add_sh_grad(g_sh1, gi, 3, 1, v3_scale(dcol, SH_C1 * z));
+                add_sh_grad(g_sh1, gi, 3, 2, v3_scale(dcol, -SH_C1 * x));
+                add_dir_grad(&ddir, dcol, sh_coeff(sh1, gi, 3, 0), 0.0f, -SH_C1, 0.0f);
+                add_dir_grad(&ddir, dcol, sh_coeff(sh1, gi, 3, 1), 0.0f, 0.0f, SH_C1);
+                add_dir_grad(&ddir, dcol, sh_coeff(sh1, gi, 3, 2), -SH_C1, 0.0f, 0.0f);
+            }
+            if(deg >= 2 && g_sh2 != NULL) {
+                add_sh_grad(g_sh2, gi, 5, 0, v3_scale(dcol, k_sh_c2[0] * xy));
+                add_dir_grad(&ddir, dcol, sh_coeff(sh2, gi, 5, 0), k_sh_c2[0] * y, k_sh_c2[0] * x, 0.0f);
+                add_sh_grad(g_sh2, gi, 5, 1, v3_scale(dcol, k_sh_c2[1] * yz));
+                add_dir_grad(&ddir, dcol, sh_coeff(sh2, gi, 5, 1), 0.0f, k_sh_c2[1] * z, k_sh_c2[1] * y);
+                add_sh_grad(g_sh2, gi, 5, 2, v3_scale(dcol, k_sh_c2[2] * (2.0f * zz - xx - yy)));
+                add_dir_grad(&ddir, dcol, sh_coeff(sh2, gi, 5, 2), -2.0f * k_sh_c2[2] * x, -2.0f * k_sh_c2[2] * y,
+                    4.0f * k_sh_c2[2] * z);
+                add_sh_grad(g_sh2, gi, 5, 3, v3_scale(dcol, k_sh_c2[3] * xz));
+                add_dir_grad(&ddir, dcol, sh_coeff(sh2, gi, 5, 3), k_sh_c2[3] * z, 0.0f, k_sh_c2[3] * x);
+                add_sh_grad(g_sh2, gi, 5, 4, v3_scale(dcol, k_sh_c2[4] * (xx - yy)));
+                add_dir_grad(&ddir, dcol, sh_coeff(sh2, gi, 5, 4), 2.0f * k_sh_c2[4] * x, -2.0f * k_sh_c2[4] * y, 0.0f);
+            }
+            if(deg >= 3 && g_sh3 != NULL) {
+                add_sh_grad(g_sh3, gi, 7, 0, v3_scale(dcol, k_sh_c3[0] * y * (3.0f * xx - yy)));
+                add_dir_grad(&ddir, dcol, sh_coeff(sh3, gi, 7, 0), 6.0f * k_sh_c3[0] * x * y,
+                    3.0f * k_sh_c3[0] * (xx - yy), 0.0f);
+                add_sh_grad(g_sh3, gi, 7, 1, v3_scale(dcol, k_sh_c3[1] * xy * z));
+                add_dir_grad(&ddir, dcol, sh_coeff(sh3, gi, 7, 1), k_sh_c3[1] * y * z, k_sh_c3[1] * x * z,
+                    k_sh_c3[1] * xy);
+                add_sh_grad(g_sh3, gi, 7, 2, v3_scale(dcol, k_sh_c3[2] * y * (4.0f * zz - xx - yy)));
+                add_dir_grad(&ddir, dcol, sh_coeff(sh3, gi, 7, 2), -2.0f * k_sh_c3[2] * x * y,
+                    k_sh_c3[2] * (4.0f * zz - xx - 3.0f * yy), 8.0f * k_sh_c3[2] * y * z);
+                add_sh_grad(g_sh3, gi, 7, 3, v3_scale(dcol, k_sh_c3[3] * z * (2.0f * zz - 3.0f * xx - 3.0f * yy)));
+                add_dir_grad(&ddir, dcol, sh_coeff(sh3, gi, 7, 3), -6.0f * k_sh_c3[3] * x * z,
+                    -6.0f * k_sh_c3[3] * y * z, k_sh_c3[3] * (6.0f * zz - 3.0f * xx - 3.0f * yy));
+                add_sh_grad(g_sh3, gi, 7, 4, v3_scale(dcol, k_sh_c3[4] * x * (4.0f * zz - xx - yy)));
+                add_dir_grad(&ddir, dcol, sh_coeff(sh3, gi, 7, 4), k_sh_c3[4] * (4.0f * zz - 3.0f * xx - yy),
+                    -2.0f * k_sh_c3[4] * x * y, 8.0f * k_sh_c3[4] * x * z);
+                add_sh_grad(g_sh3, gi, 7, 5, v3_scale(dcol, k_sh_c3[5] * z * (xx - yy)));
+                add_dir_grad(&ddir, dcol, sh_coeff(sh3, gi, 7, 5), 2.0f * k_sh_c3[5] * x * z,
+                    -2.0f * k_sh_c3[5] * y * z, k_sh_c3[5] * (xx - yy));
+                add_sh_grad(g_sh3, gi, 7, 6, v3_scale(dcol, k_sh_c3[6] * x * (xx - 3.0f * yy)));
+                add_dir_grad(&ddir, dcol, sh_coeff(sh3, gi, 7, 6), 3.0f * k_sh_c3[6] * (xx - yy),
+                    -6.0f * k_sh_c3[6] * x * y, 0.0f);
+            }
+            if(deg >= 1) {
+                v3 view = mk3(mean3d[gi * 3 + 0] - cc.x, mean3d[gi * 3 + 1] - cc.y, mean3d[gi * 3 + 2] - cc.z);
+                float vn = sqrtf(view.x * view.x + view.y * view.y + view.z * view.z);
+
+                if(vn > 0.0f) {
+                    float dd = ddir.x * x + ddir.y * y + ddir.z * z;
+                    v3 dv = mk3(ddir.x - x * dd, ddir.y - y * dd, ddir.z - z * dd);
+                    float s = 1.0f / vn;
+
+                    g_mean3d[gi * 3 + 0] += dv.x * s;
+                    g_mean3d[gi * 3 + 1] += dv.y * s;
+                    g_mean3d[gi * 3 + 2] += dv.z * s;
+                }
+            }
+        }
+        /* render.c:1830 */
+        {
+            float sg = sigmoid_render(r[ORACLE_REC_RAW_OPACITY]);
+
+            g_opacity[gi] += dop * (sg * (1.0f - sg));
+        }
+        /* render.c:1832-1845 */
+        {
+            float inv_z = 1.0f / zc;
+            float inv_z2 = inv_z * inv_z;
+            v3 dmc = mk3(dmx * k.fx * inv_z, dmy * k.fy * inv_z,
+                dmx * (-k.fx * xc * inv_z2) + dmy * (-k.fy * yc * inv_z2));
+            v3 dmw = m3_v(m3_t(w), dmc);
+
+            g_mean3d[gi * 3 + 0] += dmw.x;
+            g_mean3d[gi * 3 + 1] += dmw.y;
+            g_mean3d[gi * 3 + 2] += dmw.z;
+        }
+        /* render.c:1847-1875 */
+        for(col = 0; col < 3; ++col) {
+            mm[0][col] = j00 * w.m[0][col] + j02 * w.m[2][col];
+            mm[1][col] = j11 * w.m[1][col] + j12 * w.m[2][col];
+        }
+        for(row = 0; row < 3; ++row) {
+            for(col = 0; col < 3; ++col) {
+                d_cov3d.m[row][col] = mm[0][row] * (dca * mm[0][col] + 0.5f * dcb * mm[1][col])
+                    + mm[1][row] * (0.5f * dcb * mm[0][col] + dcc * mm[1][col]);
+            }
+        }
+        for(row = 0; row < 3; ++row) {
+            srot.m[row][0] *= sx;
+            srot.m[row][1] *= sy;
+            srot.m[row][2] *= sz;
+        }
+        for(row = 0; row < 3; ++row) {
+            for(col = 0; col < 3; ++col) {
+                dsum.m[row][col] = d_cov3d.m[row][col] + d_cov3d.m[col][row];
+            }
+        }
+        d_rs = m3_mul(dsum, srot);
+        g_logscale[gi * 3 + 0] += (d_rs.m[0][0] * rot.m[0][0] + d_rs.m[1][0] * rot.m[1][0] + d_rs.m[2][0] * rot.m[2][0]) * sx;
+        g_logscale[gi * 3 + 1] += (d_rs.m[0][1] * rot.m[0][1] + d_rs.m[1][1] * rot.m[1][1] + d_rs.m[2][1] * rot.m[2][1]) * sy;
+        g_logscale[gi * 3 + 2] += (d_rs.m[0][2] * rot.m[0][2] + d_rs.m[1][2] * rot.m[1][2] + d_rs.m[2][2] * rot.m[2][2]) * sz;
+        for(row = 0; row < 3; ++row) {
+            d_r.m[row][0] = d_rs.m[row][0] * sx;
+            d_r.m[row][1] = d_rs.m[row][1] * sy;
+            d_r.m[row][2] = d_rs.m[row][2] * sz;
+        }
+        /* render.c:1877-1937: through the quaternion normalisation. */
+        {
+            float nx, ny, nz, nw;
+
+            if(quat_normalize(q[0], q[1], q[2], q[3], &nx, &ny, &nz, &nw)) {
+                float inv_norm = 1.0f / sqrtf(q[0] * q[0] + q[1] * q[1] + q[2] * q[2] + q[3] * q[3]);
+                float dqw = 0.0f, dqx = 0.0f, dqy = 0.0f, dqz = 0.0f, dot;
+
+                dqw += d_r.m[0][1] * (-2.0f * nz);
+                dqw += d_r.m[0][2] * (2.0f * ny);
+                dqw += d_r.m[1][0] * (2.0f * nz);
+                dqw += d_r.m[1][2] * (-2.0f * nx);
+                dqw += d_r.m[2][0] * (-2.0f * ny);
+                dqw += d_r.m[2][1] * (2.0f * nx);
+
+                dqx += d_r.m[0][1] * (2.0f * ny);
+                dqx += d_r.m[0][2] * (2.0f * nz);
+                dqx += d_r.m[1][0] * (2.0f * ny);
+                dqx += d_r.m[1][1] * (-4.0f * nx);
+                dqx += d_r.m[1][2] * (-2.0f * nw);
+                dqx += d_r.m[2][0] * (2.0f * nz);
+                dqx += d_r.m[2][1] * (2.0f * nw);
+                dqx += d_r.m[2][2] * (-4.0f * nx);
+
+                dqy += d_r.m[0][0] * (-4.0f * ny);
+                dqy += d_r.m[0][1] * (2.0f * nx);
+                dqy += d_r.m[0][2] * (2.0f * nw);
+                dqy += d_r.m[1][0] * (2.0f * nx);
+                dqy += d_r.m[1][2] * (2.0f * nz);
+                dqy += d_r.m[2][0] * (-2.0f * nw);
+                dqy += d_r.m[2][1] * (2.0f * nz);
+                dqy += d_r.m[2][2] * (-4.0f * ny);
+
+                dqz += d_r.m[0][0] * (-4.0f * nz);
+                dqz += d_r.m[0][1] * (-2.0f * nw);
+                dqz += d_r.m[0][2] * (2.0f * nx);
+                dqz += d_r.m[1][0] * (2.0f * nw);
+                dqz += d_r.m[1][1] * (-4.0f * nz);
+                dqz += d_r.m[1][2] * (2.0f * ny);
+                dqz += d_r.m[2][0] * (2.0f * nx);
+                dqz += d_r.m[2][1] * (2.0f * ny);
+
+                dot = nx * dqx + ny * dqy + nz * dqz + nw * dqw;
+                g_rotation[gi * 4 + 0] += (dqx - nx * dot) * inv_norm;
+                g_rotation[gi * 4 + 1] += (dqy - ny * dot) * inv_norm;
+                g_rotation[gi * 4 + 2] += (dqz - nz * dot) * inv_norm;
+                g_rotation[gi * 4 + 3] += (dqw - nw * dot) * inv_norm;
+            }
+        }
+        /* render.c:1939-1969: the Jacobian's dependence on the camera-space mean. */
+        {
+            m3 cov_cam = m3_mul(m3_mul(w, cov3d), m3_t(w));
+            float dj[2][3];
+            float inv_z = 1.0f / zc;
+            float inv_z2 = inv_z * inv_z;
+            float inv_z3 = inv_z2 * inv_z;
+            v3 dmj, dmwj;
+
+            for(col = 0; col < 3; ++col) {
+                dj[0][col] = 2.0f * dca * (j00 * cov_cam.m[0][col] + j02 * cov_cam.m[2][col])
+                    + dcb * (j11 * cov_cam.m[1][col] + j12 * cov_cam.m[2][col]);
+                dj[1][col] = dcb * (j00 * cov_cam.m[0][col] + j02 * cov_cam.m[2][col])
+                    + 2.0f * dcc * (j11 * cov_cam.m[1][col] + j12 * cov_cam.m[2][col]);
+            }
+            dmj.x = dj[0][2] * (-k.fx * inv_z2);
+            dmj.y = dj[1][2] * (-k.fy * inv_z2);
+            dmj.z = dj[0][0] * (-k.fx * inv_z2) + dj[0][2] * (2.0f * k.fx * xc * inv_z3)
+                + dj[1][1] * (-k.fy * inv_z2) + dj[1][2] * (2.0f * k.fy * yc * inv_z3);
+            dmwj = m3_v(m3_t(w), dmj);
+            g_mean3d[gi * 3 + 0] += dmwj.x;
+            g_mean3d[gi * 3 + 1] += dmwj.y;
+            g_mean3d[gi * 3 + 2] += dmwj.z;
+        }
+    }
+    free(contribs);
+    free(offsets);
+    free(suffix);
+    free(t);
+    free(v);
+    return 0;
+}
+
+/* ---------------------------------------------------------------------------------------
+ * Losses: gsx/src/gsx-cpu/loss.c:316-709, gradient scale gsx-tensor-helpers.h:236-244.
+ * Images are [outer, C, H, W] CHW float32; map and grad are accumulators.
+ * ------------------------------------------------------------------------------------- */
+void oracle_loss_l1(int64_t count, const float *pred, const float *target, float scale, float grad_scale,
+    float *loss_map, float *grad)
+{
+    int64_t i;
+
+    for(i = 0; i < count; ++i) {
+        float d = pred[i] - target[i];
+
+        if(loss_map != NULL) {
+            loss_map[i] += scale * fabsf(d);
+        }
+        if(grad != NULL) {
+            float s = 0.0f;
+
+            if(d > 0.0f) s = 1.0f;
+            else if(d < 0.0f) s = -1.0f;
+            grad[i] += s * grad_scale;
+        }
+    }
+}
+
+void oracle_loss_mse(int64_t count, const float *pred, const float *target, float scale, float grad_scale,
+    float *loss_map, float *grad)
+{
+    int64_t i;
+
+    for(i = 0; i < count; ++i) {
+        float d = pred[i] - target[i];
+
+        if(loss_map != NULL) {
+            loss_map[i] += scale * (d * d);
+        }
+        if(grad != NULL) {
+            grad[i] += 2.0f * d * grad_scale;
+        }
+    }
+}
+
+static const double k_ssim_w[11] = { 0.001028380123898387, 0.0075987582094967365, 0.036000773310661316,
+    0.10936068743467331, 0.21300552785396576, 0.26601171493530273, 0.21300552785396576, 0.10936068743467331,
+    0.036000773310661316, 0.0075987582094967365, 0.001028380123898387 };
+
+/* loss.c:397-556 and :632-709: direct 2D 11x11 window in float64 with zero padding;
+ * C1 = 0.01^2, C2 = 0.03^2; 5-pixel boundary set to 0 in the map; dm/dmu1, dm/dsigma1^2,
+ * dm/dsigma12 convolved again for the gradient. grad_scale is already normalised. */
+int oracle_loss_ssim(int64_t outer, int64_t channels, int64_t height, int64_t width, const float *pred,
+    const float *target, float scale, float grad_scale, float *loss_map, float *grad)
+{
+    int64_t plane = height * width;
+    int64_t total = outer * channels * plane;
+    double *dmu = NULL, *ds1 = NULL, *ds12 = NULL;
+    int64_t o, y, x;
+    const double ls = (double)scale;
+    const double gs = (double)grad_scale;
+
+    if(grad != NULL) {
+        dmu = (double *)calloc((size_t)total, sizeof(double));
+        ds1 = (double *)calloc((size_t)total, sizeof(double));
+        ds12 = (double *)calloc((size_t)total, sizeof(double));
+        if(dmu == NULL || ds1 == NULL || ds12 == NULL) {
+            free(dmu);
+            free(ds1);
+            free(ds12);
+            return -1;
+        }
+    }
+    for(o = 0; o < outer * channels; ++o) {
+        const float *pp = pred + o * plane;
+        const float *tp = target + o * plane;
+
+        for(y = 0; y < height; ++y) {
+            for(x = 0; x < width; ++x) {
+                double mu1 = 0.0, mu2 = 0.0, ex2 = 0.0, ey2 = 0.0, exy = 0.0;
+                int64_t ky, kx, idx = o * plane + y * width + x;
+                double m1s, m2s, s1, s2, s12, a, b, ct, dt, ssim;
+                int boundary = y < 5 || y >= height - 5 || x < 5 || x >= width - 5;
+
+                for(ky = -5; ky <= 5; ++ky) {
+                    double wy = k_ssim_w[ky + 5];
+
+                    for(kx = -5; kx <= 5; ++kx) {
+                        double wgt = wy * k_ssim_w[kx + 5];
+                        int64_t yy = y + ky, xx = x + kx;
+                        double ps = 0.0, ts = 0.0;
+
+                        if(yy >= 0 && xx >= 0 && yy < height && xx < width) {
+                            ps = (double)pp[yy * width + xx];
+                            ts = (double)tp[yy * width + xx];
+                        }
+                        mu1 += ps * wgt;
+                        mu2 += ts * wgt;
+                        ex2 += ps * ps * wgt;
+                        ey2 += ts * ts * wgt;
+                        exy += ps * ts * wgt;
+                    }
+                }
+                m1s = mu1 * mu1;
+                m2s = mu2 * mu2;
+                s1 = ex2 - m1s;
+                s2 = ey2 - m2s;
+                s12 = exy - mu1 * mu2;
+                a = m1s + m2s + 0.01 * 0.01;
+                b = s1 + s2 + 0.03 * 0.03;
+                ct = 2.0 * mu1 * mu2 + 0.01 * 0.01;
+                dt = 2.0 * s12 + 0.03 * 0.03;
+                ssim = (a * b) == 0.0 ? 1.0 : (ct * dt) / (a * b);
+                if(loss_map != NULL) {
+                    if(boundary) {
+                        loss_map[idx] = 0.0f;
+                    } else {
+                        loss_map[idx] += (float)((1.0 - ssim) * ls);
+                    }
+                }
+                if(grad != NULL) {
+                    if(boundary || a == 0.0 || b == 0.0) {
+                        dmu[idx] = 0.0;
+                        ds1[idx] = 0.0;
+                        ds12[idx] = 0.0;
+                    } else {
+                        double ab = a * b, aab = a * ab, abb = ab * b;
+
+                        dmu[idx] = (2.0 * mu2 * dt) / ab - (2.0 * mu2 * ct) / ab - (2.0 * mu1 * ct * dt) / aab
+                            + (2.0 * mu1 * ct * dt) / abb;
+                        ds1[idx] = -(ct * dt) / abb;
+                        ds12[idx] = (2.0 * ct) / ab;
+                    }
+                }
+            }
+        }
+    }
+    if(grad != NULL) {
+        for(o = 0; o < outer * channels; ++o) {
+            for(y = 0; y < height; ++y) {
+                for(x = 0; x < width; ++x) {
+                    double cm = 0.0, c1 = 0.0, c12 = 0.0;
+                    int64_t ky, kx, idx = o * plane + y * width + x;
+
+                    for(ky = -5; ky <= 5; ++ky) {
+                        double wy = k_ssim_w[ky + 5];
+
+                        for(kx = -5; kx <= 5; ++kx) {
+                            double wgt = wy * k_ssim_w[kx + 5];
+                            int64_t yy = y + ky, xx = x + kx;
+                            double a = 0.0, b = 0.0, c = 0.0;
+
+                            if(yy >= 0 && xx >= 0 && yy < height && xx < width) {
+                                int64_t j = o * plane + yy * width + xx;
+
+                                a = dmu[j];
+                                b = ds1[j];
+                                c = ds12[j];
+                            }
+                            cm += a * wgt;
+                            c1 += b * wgt;
+                            c12 += c * wgt;
+                        }
+                    }
+                    grad[idx] += (float)(-(cm + 2.0 * (double)pred[idx] * c1 + (double)target[idx] * c12) * gs);
+                }
+            }
+        }
+    }
+    free(dmu);
+    free(ds1);
+    free(ds12);
+    return 0;
+}
+
+/* ---------------------------------------------------------------------------------------
+ * Adam: gsx/src/gsx-cpu/optim.c:712-780. `step` is the post-increment step count.
+ * ------------------------------------------------------------------------------------- */
+void oracle_adam_step(int64_t count, float *param, const float *grad, float *m, float *v, float lr, float beta1,
+    float beta2, float weight_decay, float epsilon, float max_grad, int64_t step)
+{
+    double bc1 = 1.0 - pow((double)beta1, (double)step);
+    double bc2 = 1.0 - pow((double)beta2, (double)step);
+    int64_t i;
+
+    for(i = 0; i < count; ++i) {
+        float g = grad[i];
+        float m1, v1, mh, vh, p;
+
+        if(max_grad > 0.0f) {
+            if(g > max_grad) g = max_grad;
+            else if(g < -max_grad) g = -max_grad;
+        }
+        m1 = beta1 * m[i] + (1.0f - beta1) * g;
+        v1 = beta2 * v[i] + (1.0f - beta2) * g * g;
+        mh = (float)((double)m1 / bc1);
+        vh = (float)((double)v1 / bc2);
+        p = param[i];
+        m[i] = m1;
+        v[i] = v1;
+        if(weight_decay > 0.0f) {
+            p -= lr * weight_decay * p;
+        }
+        p -= lr * (mh / (sqrtf(vh) + epsilon));
+        param[i] = p;
+    }
+}
+
+/* ---------------------------------------------------------------------------------------
+ * Row gather: gsx/src/gsx-cpu/core.c:1248-1333. Returns 0, or -1 for an index out of range.
+ * ------------------------------------------------------------------------------------- */
+int oracle_gather_rows(const void *src, int64_t src_rows, int64_t row_bytes, const int32_t *index, int64_t count,
+    void *dst)
+{
+    int64_t i;
+
+    for(i = 0; i < count; ++i) {
+        if(index[i] < 0 || index[i] >= src_rows) {
+            return -1;
+        }
+        memcpy((unsigned char *)dst + i * row_bytes, (const unsigned char *)src + (int64_t)index[i] * row_bytes,
+            (size_t)row_bytes);
+    }
+    return 0;
+}
+
+/* ---------------------------------------------------------------------------------------
+ * ADC default / ABSGS refine: gsx/src/gsx-cpu/adc/default.c:160-527, adc.c:48-80,229-248,
+ * 491-559, host math gsx/src/gsx-core.c:2915-2940, Box-Muller gsx/src/gsx-random.c:86-112.
+ * Fields are SH0-only SoA arrays with capacity for the grown set. The optimizer moments of
+ * grown rows are zero and of kept rows are gathered; moments are passed as 5 (m, v) pairs
+ * over the same row layout (mean3d 3, rotation 4, logscale 3, opacity 1, sh0 3 floats).
+ * ------------------------------------------------------------------------------------- */
+typedef struct oracle_adc_params {
+    int32_t algorithm; /* 0 default, 1 absgs */
+    float pruning_opacity_threshold;
+    float opacity_clamp_value;
+    float max_world_scale;
+    float duplicate_grad_threshold;
+    float duplicate_scale_threshold;
+    float duplicate_absgrad_threshold;
+    float scene_scale;
+    int64_t refine_every, start_refine, end_refine, max_num_gaussians, reset_every, global_step;
+    uint64_t seed;
+} oracle_adc_params;
+
+static float host_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+static float host_logit(float p) { return logf(p / (1.0f - p)); }
+
+static float prob_to_logit(float p)
+{
+    float c = p;
+
+    if(c <= 1e-6f) c = 1e-6f;
+    if(c >= 1.0f - 1e-6f) c = 1.0f - 1e-6f;
+    return host_logit(c);
+}
+
+static float next_normal(gsx_amd_pcg32 *rng)
+{
+    float u1 = gsx_pcg32_next_f32(rng);
+    float u2 = gsx_pcg32_next_f32(rng);
+    float mag;
+
+    u1 = fmaxf(1e-7f, u1);
+    mag = sqrtf(-2.0f * logf(u1));
+    return mag * cosf(2.0f * (float)3.14159265358979323846264338327950288 * u2);
+}
+
+static int64_t nonneg(int64_t v) { return v <= 0 ? 0 : v; }
+
+static int in_refine_window(const oracle_adc_params *p)
+{
+    uint64_t s = (uint64_t)p->global_step;
+
+    if(p->refine_every == 0) return 0;
+    if(s % (uint64_t)p->refine_every != 0) return 0;
+    if(s < (uint64_t)nonneg(p->start_refine) || s > (uint64_t)nonneg(p->end_refine)) return 0;
+    return 1;
+}
+
+static int in_reset_window(const oracle_adc_params *p)
+{
+    uint64_t s = (uint64_t)p->global_step;
+
+    if(p->reset_every == 0) return 0;
+    if(s % (uint64_t)p->reset_every != 0) return 0;
+    if(s < (uint64_t)nonneg(p->start_refine) || s >= (uint64_t)nonneg(p->end_refine)) return 0;
+    return 1;
+}
+
+static const int k_adc_widths[5] = { 3, 4, 3, 1, 3 };
+
+/* fields[5] = mean3d, rotation, logscale, opacity, sh0 (row widths 3, 4, 3, 1, 3); moments[10]
+ * = m, v per field (nullable => optimizer disabled). aux[3] = grad_acc, absgrad_acc,
+ * visible_counter (each nullable). Arrays must have room for max(n, max_num_gaussians) rows.
+ * Returns the new count; counts[4] = pruned, duplicated, grown, reset. Returns -1 on error. */
+int64_t oracle_adc_step(int64_t n, float **fields, float **moments, float **aux, const oracle_adc_params *p,
+    int64_t *counts)
+{
+    int64_t i, f, grow = 0, split_count = 0, dup_count = 0, keep = 0, n_after;
+    int32_t *sources = NULL;
+    uint8_t *modes = NULL;
+    int64_t budget = 0, cap = nonneg(p->max_num_gaussians);
+    float *mean3d = fields[0], *rot = fields[1], *ls = fields[2], *op = fields[3];
+    const float *acc = p->algorithm == 1 ? aux[1] : aux[0];
+    float grow_thr = p->algorithm == 1 ? p->duplicate_absgrad_threshold : p->duplicate_grad_threshold;
+    gsx_amd_pcg32 rng;
+    int32_t *keep_idx = NULL;
+
+    counts[0] = counts[1] = counts[2] = counts[3] = 0;
+    gsx_pcg32_seed2(&rng, p->seed, p->seed);
+    n_after = n;
+    if(in_refine_window(p) && n > 0) {
+        if(acc == NULL) return -1;
+        if(cap > n) budget = cap - n;
+        if(budget > 0) {
+            sources = (int32_t *)malloc(sizeof(int32_t) * (size_t)budget);
+            modes = (uint8_t *)malloc((size_t)budget);
+            if(sources == NULL || modes == NULL) {
+                free(sources);
+                free(modes);
+                return -1;
+            }
+            /* default.c:160-219, 373-386: first-come by index until the budget is spent. */
+            for(i = 0; i < n && grow < budget; ++i) {
+                float counter = aux[2] != NULL ? aux[2][i] : 1.0f;
+                float g, sx, sy, sz, mx;
+
+                if(counter <= 0.0f) continue;
+                g = acc[i] / (counter > 1.0f ? counter : 1.0f);
+                if(g <= grow_thr) continue;
+                sx = expf(ls[i * 3 + 0]);
+                sy = expf(ls[i * 3 + 1]);
+                sz = expf(ls[i * 3 + 2]);
+                mx = sx;
+                if(sy > mx) mx = sy;
+                if(sz > mx) mx = sz;
+                sources[grow] = (int32_t)i;
+                modes[grow] = mx > p->duplicate_scale_threshold * p->scene_scale ? 2 : 1;
+                if(modes[grow] == 2) split_count += 1;
+                else dup_count += 1;
+                grow += 1;
+            }
+        }
+        if(grow > 0) {
+            /* default.c:396-403: gather [0..n) ++ sources, i.e. append copies; moments of
+             * the appended rows are zero (adc.c:438-444). */
+            for(f = 0; f < 5; ++f) {
+                int wdt = k_adc_widths[f];
+
+                for(i = 0; i < grow; ++i) {
+                    memcpy(fields[f] + (n + i) * wdt, fields[f] + (int64_t)sources[i] * wdt, sizeof(float) * (size_t)wdt);
+                    if(moments != NULL) {
+                        memset(moments[2 * f] + (n + i) * wdt, 0, sizeof(float) * (size_t)wdt);
+                        memset(moments[2 * f + 1] + (n + i) * wdt, 0, sizeof(float) * (size_t)wdt);
+                    }
+                }
+            }
+            for(f = 0; f < 3; ++f) {
+                if(aux[f] != NULL) {
+                    for(i = 0; i < grow; ++i) aux[f][n + i] = aux[f][sources[i]];
+                }
+            }
+            /* default.c:38-158 mutations in grow order; splits draw 6 normals each from the
+             * single sequential stream. */
+            for(i = 0; i < grow; ++i) {
+                int64_t src = sources[i], tgt = n + i;
+
+                if(modes[i] == 1) {
+                    continue; /* duplicate: the gathered copy is already the mutation */
+                }
+                {
+                    float qx = rot[src * 4 + 0], qy = rot[src * 4 + 1], qz = rot[src * 4 + 2], qw = rot[src * 4 + 3];
+                    float sx = expf(ls[src * 3 + 0]), sy = expf(ls[src * 3 + 1]), sz = expf(ls[src * 3 + 2]);
+                    float so = host_sigmoid(op[src]);
+                    float r1x, r1y, r1z, r2x, r2y, r2z, t1x, t1y, t1z, t2x, t2y, t2z, qn, nsx, nsy, nsz, sop;
+                    float m00, m01, m02, m10, m11, m12, m20, m21, m22;
+
+                    nsx = sx / 1.6f;
+                    nsy = sy / 1.6f;
+                    nsz = sz / 1.6f;
+                    r1x = next_normal(&rng);
+                    r1y = next_normal(&rng);
+                    r1z = next_normal(&rng);
+                    r2x = next_normal(&rng);
+                    r2y = next_normal(&rng);
+                    r2z = next_normal(&rng);
+                    t1x = r1x * (sx + 1e-5f);
+                    t1y = r1y * (sy + 1e-5f);
+                    t1z = r1z * (sz + 1e-5f);
+                    t2x = r2x * (sx + 1e-5f);
+                    t2y = r2y * (sy + 1e-5f);
+                    t2z = r2z * (sz + 1e-5f);
+                    /* adc.c:290-309 */
+                    qn = sqrtf(qx * qx + qy * qy + qz * qz + qw * qw);
+                    if(qn > 1e-8f) {
+                        float iq = 1.0f / qn;
+
+                        qx *= iq;
+                        qy *= iq;
+                        qz *= iq;
+                        qw *= iq;
+                    }
+                    m00 = 1.0f - 2.0f * (qy * qy + qz * qz);
+                    m01 = 2.0f * (qx * qy - qw * qz);
+                    m02 = 2.0f * (qx * qz + qw * qy);
+                    m10 = 2.0f * (qx * qy + qw * qz);
+                    m11 = 1.0f - 2.0f * (qx * qx + qz * qz);
+                    m12 = 2.0f * (qy * qz - qw * qx);
+                    m20 = 2.0f * (qx * qz - qw * qy);
+                    m21 = 2.0f * (qy * qz + qw * qx);
+                    m22 = 1.0f - 2.0f * (qx * qx + qy * qy);
+                    if(so < 0.0f) so = 0.0f;
+                    if(so > 1.0f - 1e-6f) so = 1.0f - 1e-6f;
+                    sop = 1.0f - sqrtf(1.0f - so);
+                    mean3d[tgt * 3 + 0] = mean3d[src * 3 + 0] + (m00 * t1x + m01 * t1y + m02 * t1z);
+                    mean3d[tgt * 3 + 1] = mean3d[src * 3 + 1] + (m10 * t1x + m11 * t1y + m12 * t1z);
+                    mean3d[tgt * 3 + 2] = mean3d[src * 3 + 2] + (m20 * t1x + m21 * t1y + m22 * t1z);
+                    ls[tgt * 3 + 0] = logf(nsx);
+                    ls[tgt * 3 + 1] = logf(nsy);
+                    ls[tgt * 3 + 2] = logf(nsz);
+                    op[tgt] = prob_to_logit(sop);
+                    mean3d[src * 3 + 0] = mean3d[src * 3 + 0] + (m00 * t2x + m01 * t2y + m02 * t2z);
+                    mean3d[src * 3 + 1] = mean3d[src * 3 + 1] + (m10 * t2x + m11 * t2y + m12 * t2z);
+                    mean3d[src * 3 + 2] = mean3d[src * 3 + 2] + (m20 * t2x + m21 * t2y + m22 * t2z);
+                    ls[src * 3 + 0] = logf(nsx);
+                    ls[src * 3 + 1] = logf(nsy);
+                    ls[src * 3 + 2] = logf(nsz);
+                    op[src] = prob_to_logit(sop);
+                }
+            }
+            counts[1] = dup_count;
+            counts[2] = split_count;
+            n_after = n + grow;
+        }
+        /* default.c:221-273 keep predicate, then compaction (default.c:488-522). */
+        keep_idx = (int32_t *)malloc(sizeof(int32_t) * (size_t)(n_after > 0 ? n_after : 1));
+        if(keep_idx == NULL) {
+            free(sources);
+            free(modes);
+            return -1;
+        }
+        {
+            int prune_large = (uint64_t)p->global_step > (uint64_t)nonneg(p->reset_every);
+
+            for(i = 0; i < n_after; ++i) {
+                float o = host_sigmoid(op[i]);
+                float sx = expf(ls[i * 3 + 0]), sy = expf(ls[i * 3 + 1]), sz = expf(ls[i * 3 + 2]);
+                float mx = sx, rn;
+                int not_large_ws = 1;
+
+                if(sy > mx) mx = sy;
+                if(sz > mx) mx = sz;
+                if(p->max_world_scale > 0.0f) {
+                    not_large_ws = mx < (p->max_world_scale * p->scene_scale);
+                }
+                rn = fabsf(rot[i * 4 + 0]) + fabsf(rot[i * 4 + 1]) + fabsf(rot[i * 4 + 2]) + fabsf(rot[i * 4 + 3]);
+                if((o > p->pruning_opacity_threshold) && (not_large_ws || !prune_large) && rn > FLT_EPSILON) {
+                    keep_idx[keep++] = (int32_t)i;
+                }
+            }
+        }
+        if(keep == 0) {
+            keep_idx[0] = 0;
+            keep = 1;
+        }
+        if(keep < n_after) {
+            for(f = 0; f < 5; ++f) {
+                int wdt = k_adc_widths[f];
+
+                for(i = 0; i < keep; ++i) {
+                    memmove(fields[f] + i * wdt, fields[f] + (int64_t)keep_idx[i] * wdt, sizeof(float) * (size_t)wdt);
+                    if(moments != NULL) {
+                        memmove(moments[2 * f] + i * wdt, moments[2 * f] + (int64_t)keep_idx[i] * wdt,
+                            sizeof(float) * (size_t)wdt);
+                        memmove(moments[2 * f + 1] + i * wdt, moments[2 * f + 1] + (int64_t)keep_idx[i] * wdt,
+                            sizeof(float) * (size_t)wdt);
+                    }
+                }
+            }
+            counts[0] = n_after - keep;
+            n_after = keep;
+        }
+        /* adc.c:446-452: aux statistics are zeroed after a refine. */
+        for(f = 0; f < 3; ++f) {
+            if(aux[f] != NULL) memset(aux[f], 0, sizeof(float) * (size_t)n_after);
+        }
+        free(keep_idx);
+        free(sources);
+        free(modes);
+    }
+    if(in_reset_window(p)) {
+        /* default.c:275-314: clamp opacity logits to logit(clamp value), reset the opacity
+         * optimizer moments. */
+        float c = p->opacity_clamp_value;
+        float mx;
+
+        if(c > 1.0f) c = 1.0f;
+        if(c < 1e-6f) c = 1e-6f;
+        mx = prob_to_logit(c);
+        for(i = 0; i < n_after; ++i) {
+            if(op[i] < -FLT_MAX) op[i] = -FLT_MAX;
+            if(op[i] > mx) op[i] = mx;
+        }
+        if(moments != NULL) {
+            memset(moments[6], 0, sizeof(float) * (size_t)n_after);
+            memset(moments[7], 0, sizeof(float) * (size_t)n_after);
+        }
+        counts[3] = 1;
+    }
+    return n_after;
+}
+
+/* Number of float inputs in [lo_bits, hi_bits] where gsx_expf differs from libm expf. */
+uint64_t oracle_expf_mismatches(uint32_t lo_bits, uint32_t hi_bits, uint32_t stride)
+{
+    uint64_t bad = 0;
+    uint64_t u;
+
+    if(stride == 0) stride = 1;
+    for(u = lo_bits; u <= hi_bits; u += stride) {
+        float x = gsx_f32_from_bits((uint32_t)u);
+        float a = expf(x);
+        float b = gsx_expf(x);
+
+        if(gsx_f32_bits(a) != gsx_f32_bits(b) && !(a != a && b != b)) {
+            bad += 1;
+        }
+    }
+    return bad;
+}

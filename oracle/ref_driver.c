@@ -1,0 +1,763 @@
+/*
+ * ref_driver.c - a thin driver over gsx's PUBLIC C API, linked against the unmodified
+ * gsx core + CPU backend compiled from the reference sources (see oracle/Makefile).
+ *
+ * TEST INFRASTRUCTURE ONLY. It is loaded by tests/ and by bench.py's cpu_baseline leg
+ * (ctypes, host memory in and out) and never by the product path.
+ *
+ * Every entry point takes plain host arrays, uploads them into CPU-backend tensors, runs
+ * the reference code path through the public front-ends, and downloads the results:
+ *   - gsxref_render       gsx_renderer_render          (gsx/src/gsx-render.c:799-826)
+ *   - gsxref_render_grad  TRAIN render + gsx_renderer_backward (gsx-render.c:828-854)
+ *   - gsxref_loss         gsx_loss_forward / gsx_loss_backward (gsx/src/gsx-loss.c)
+ *   - gsxref_adam         gsx_optim_step               (gsx/src/gsx-optim.c:498)
+ *   - gsxref_adc          gsx_adc_step                 (gsx/src/gsx-adc.c:231)
+ *   - gsxref_train_step   one image-fit style step (render, L1+SSIM, backward, Adam) with
+ *                         per-stage wall-clock timings, used as the CPU baseline.
+ * Return value: 0 on success, otherwise the gsx_error_code; gsxref_last_error() gives the
+ * reference's static message.
+ */
+#define _POSIX_C_SOURCE 200809L
+#include "gsx/gsx.h"
+
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#include <time.h>
+
+static const char *g_last_message = NULL;
+static gsx_backend_t g_backend = NULL;
+static gsx_backend_buffer_type_t g_device_type = NULL;
+
+const char *gsxref_last_error(void) { return g_last_message != NULL ? g_last_message : ""; }
+
+#define TRY(expr)                                                   \
+    do {                                                            \
+        gsx_error e_ = (expr);                                      \
+        if(!gsx_error_is_success(e_)) {                             \
+            g_last_message = e_.message;                            \
+            rc = (int)e_.code != 0 ? (int)e_.code : -1;             \
+            goto done;                                              \
+        }                                                           \
+    } while(0)
+
+static int ensure_backend(void)
+{
+    gsx_backend_device_t device = NULL;
+    gsx_backend_desc desc = { 0 };
+    gsx_error e;
+
+    if(g_backend != NULL) {
+        return 0;
+    }
+    e = gsx_backend_registry_init();
+    if(!gsx_error_is_success(e)) { g_last_message = e.message; return (int)e.code; }
+    e = gsx_get_backend_device_by_type(GSX_BACKEND_TYPE_CPU, 0, &device);
+    if(!gsx_error_is_success(e)) { g_last_message = e.message; return (int)e.code; }
+    desc.device = device;
+    e = gsx_backend_init(&g_backend, &desc);
+    if(!gsx_error_is_success(e)) { g_last_message = e.message; return (int)e.code; }
+    e = gsx_backend_find_buffer_type(g_backend, GSX_BACKEND_BUFFER_TYPE_DEVICE, &g_device_type);
+    if(!gsx_error_is_success(e)) { g_last_message = e.message; return (int)e.code; }
+    return 0;
+}
+
+static gsx_error make_tensor(gsx_arena_t arena, gsx_tensor_t *out, int rank, int d0, int d1, int d2, const void *src)
+{
+    gsx_tensor_desc desc = { 0 };
+    gsx_error e;
+
+    desc.rank = rank;
+    desc.shape[0] = d0;
+    desc.shape[1] = d1;
+    desc.shape[2] = d2;
+    desc.data_type = GSX_DATA_TYPE_F32;
+    desc.storage_format = GSX_STORAGE_FORMAT_CHW;
+    desc.arena = arena;
+    e = gsx_tensor_init(out, &desc);
+    if(!gsx_error_is_success(e)) {
+        return e;
+    }
+    if(src != NULL) {
+        size_t count = (size_t)d0 * (size_t)(rank > 1 ? d1 : 1) * (size_t)(rank > 2 ? d2 : 1);
+        return gsx_tensor_upload(*out, src, count * sizeof(float));
+    }
+    return gsx_tensor_set_zero(*out);
+}
+
+/* camera[17] = fx, fy, cx, cy, width, height, qx, qy, qz, qw, tx, ty, tz, near, far, bg_r, bg_g, bg_b
+ * (18 floats; width/height are carried as floats holding integers). */
+static void unpack_camera(const float *camera, gsx_camera_intrinsics *intr, gsx_camera_pose *pose,
+    float *near_plane, float *far_plane, gsx_vec3 *bg)
+{
+    memset(intr, 0, sizeof(*intr));
+    memset(pose, 0, sizeof(*pose));
+    intr->model = GSX_CAMERA_MODEL_PINHOLE;
+    intr->fx = camera[0];
+    intr->fy = camera[1];
+    intr->cx = camera[2];
+    intr->cy = camera[3];
+    intr->width = (gsx_index_t)camera[4];
+    intr->height = (gsx_index_t)camera[5];
+    pose->rot.x = camera[6];
+    pose->rot.y = camera[7];
+    pose->rot.z = camera[8];
+    pose->rot.w = camera[9];
+    pose->transl.x = camera[10];
+    pose->transl.y = camera[11];
+    pose->transl.z = camera[12];
+    *near_plane = camera[13];
+    *far_plane = camera[14];
+    bg->x = camera[15];
+    bg->y = camera[16];
+    bg->z = camera[17];
+}
+
+typedef struct ref_scene {
+    gsx_arena_t arena;
+    gsx_tensor_t mean3d, rotation, logscale, opacity, sh0, sh1, sh2, sh3;
+} ref_scene;
+
+static gsx_error scene_upload(ref_scene *s, int n, int sh_degree, const float *mean3d, const float *rotation,
+    const float *logscale, const float *opacity, const float *sh0, const float *sh1, const float *sh2, const float *sh3)
+{
+    gsx_arena_desc adesc = { 0 };
+    gsx_error e;
+
+    memset(s, 0, sizeof(*s));
+    adesc.initial_capacity_bytes = (gsx_size_t)n * 256u + 4096u;
+    e = gsx_arena_init(&s->arena, g_device_type, &adesc);
+    if(!gsx_error_is_success(e)) return e;
+    e = make_tensor(s->arena, &s->mean3d, 2, n, 3, 0, mean3d);
+    if(!gsx_error_is_success(e)) return e;
+    e = make_tensor(s->arena, &s->rotation, 2, n, 4, 0, rotation);
+    if(!gsx_error_is_success(e)) return e;
+    e = make_tensor(s->arena, &s->logscale, 2, n, 3, 0, logscale);
+    if(!gsx_error_is_success(e)) return e;
+    e = make_tensor(s->arena, &s->opacity, 1, n, 0, 0, opacity);
+    if(!gsx_error_is_success(e)) return e;
+    e = make_tensor(s->arena, &s->sh0, 2, n, 3, 0, sh0);
+    if(!gsx_error_is_success(e)) return e;
+    if(sh_degree >= 1) {
+        e = make_tensor(s->arena, &s->sh1, 3, n, 3, 3, sh1);
+        if(!gsx_error_is_success(e)) return e;
+    }
+    if(sh_degree >= 2) {
+        e = make_tensor(s->arena, &s->sh2, 3, n, 5, 3, sh2);
+        if(!gsx_error_is_success(e)) return e;
+    }
+    if(sh_degree >= 3) {
+        e = make_tensor(s->arena, &s->sh3, 3, n, 7, 3, sh3);
+        if(!gsx_error_is_success(e)) return e;
+    }
+    {
+        gsx_error ok = { GSX_ERROR_SUCCESS, NULL };
+        return ok;
+    }
+}
+
+static void scene_free(ref_scene *s)
+{
+    gsx_tensor_t *all[] = { &s->mean3d, &s->rotation, &s->logscale, &s->opacity, &s->sh0, &s->sh1, &s->sh2, &s->sh3 };
+    size_t i;
+
+    for(i = 0; i < sizeof(all) / sizeof(all[0]); ++i) {
+        if(*all[i] != NULL) {
+            (void)gsx_tensor_free(*all[i]);
+            *all[i] = NULL;
+        }
+    }
+    if(s->arena != NULL) {
+        (void)gsx_arena_free(s->arena);
+        s->arena = NULL;
+    }
+}
+
+/* Forward render. forward_type: 0 inference, 1 train. visible_counter (nullable, [n]) is
+ * read, bound as gs_visible_counter for TRAIN forwards, and written back. */
+int gsxref_render(int n, int sh_degree, const float *mean3d, const float *rotation, const float *logscale,
+    const float *opacity, const float *sh0, const float *sh1, const float *sh2, const float *sh3,
+    const float *camera, int forward_type, float *out_rgb, float *visible_counter)
+{
+    int rc = 0;
+    ref_scene s = { 0 };
+    gsx_renderer_t renderer = NULL;
+    gsx_render_context_t context = NULL;
+    gsx_renderer_desc rdesc = { 0 };
+    gsx_render_forward_request req = { 0 };
+    gsx_camera_intrinsics intr;
+    gsx_camera_pose pose;
+    gsx_tensor_t out = NULL;
+    gsx_tensor_t counter = NULL;
+    float near_plane = 0.0f;
+    float far_plane = 0.0f;
+    gsx_vec3 bg;
+
+    rc = ensure_backend();
+    if(rc != 0) return rc;
+    unpack_camera(camera, &intr, &pose, &near_plane, &far_plane, &bg);
+    TRY(scene_upload(&s, n, sh_degree, mean3d, rotation, logscale, opacity, sh0, sh1, sh2, sh3));
+    TRY(make_tensor(s.arena, &out, 3, 3, intr.height, intr.width, NULL));
+    if(visible_counter != NULL) {
+        TRY(make_tensor(s.arena, &counter, 1, n, 0, 0, visible_counter));
+    }
+    rdesc.width = intr.width;
+    rdesc.height = intr.height;
+    rdesc.output_data_type = GSX_DATA_TYPE_F32;
+    TRY(gsx_renderer_init(&renderer, g_backend, &rdesc));
+    TRY(gsx_render_context_init(&context, renderer));
+    req.intrinsics = &intr;
+    req.pose = &pose;
+    req.near_plane = near_plane;
+    req.far_plane = far_plane;
+    req.background_color = bg;
+    req.precision = GSX_RENDER_PRECISION_FLOAT32;
+    req.sh_degree = sh_degree;
+    req.forward_type = forward_type != 0 ? GSX_RENDER_FORWARD_TYPE_TRAIN : GSX_RENDER_FORWARD_TYPE_INFERENCE;
+    req.borrow_train_state = true;
+    req.gs_mean3d = s.mean3d;
+    req.gs_rotation = s.rotation;
+    req.gs_logscale = s.logscale;
+    req.gs_opacity = s.opacity;
+    req.gs_sh0 = s.sh0;
+    req.gs_sh1 = s.sh1;
+    req.gs_sh2 = s.sh2;
+    req.gs_sh3 = s.sh3;
+    req.out_rgb = out;
+    req.gs_visible_counter = counter;
+    TRY(gsx_renderer_render(renderer, context, &req));
+    TRY(gsx_tensor_download(out, out_rgb, (gsx_size_t)3 * intr.height * intr.width * sizeof(float)));
+    if(counter != NULL) {
+        TRY(gsx_tensor_download(counter, visible_counter, (gsx_size_t)n * sizeof(float)));
+    }
+done:
+    if(context != NULL) (void)gsx_render_context_free(context);
+    if(renderer != NULL) (void)gsx_renderer_free(renderer);
+    if(out != NULL) (void)gsx_tensor_free(out);
+    if(counter != NULL) (void)gsx_tensor_free(counter);
+    scene_free(&s);
+    return rc;
+}
+
+/* TRAIN forward + backward. grads: mean3d [n,3], rotation [n,4], logscale [n,3], opacity [n],
+ * sh0 [n,3], sh1..sh3 per sh_degree (nullable otherwise). Sinks are overwritten, as in the
+ * reference (gsx-cpu/render.c:1537-1550). out_rgb receives the forward image. */
+int gsxref_render_grad(int n, int sh_degree, const float *mean3d, const float *rotation, const float *logscale,
+    const float *opacity, const float *sh0, const float *sh1, const float *sh2, const float *sh3,
+    const float *camera, const float *grad_rgb, float *out_rgb,
+    float *g_mean3d, float *g_rotation, float *g_logscale, float *g_opacity, float *g_sh0,
+    float *g_sh1, float *g_sh2, float *g_sh3)
+{
+    int rc = 0;
+    ref_scene s = { 0 };
+    gsx_renderer_t renderer = NULL;
+    gsx_render_context_t context = NULL;
+    gsx_renderer_desc rdesc = { 0 };
+    gsx_render_forward_request req = { 0 };
+    gsx_render_backward_request breq = { 0 };
+    gsx_camera_intrinsics intr;
+    gsx_camera_pose pose;
+    gsx_tensor_t out = NULL, gout = NULL;
+    gsx_tensor_t gm = NULL, gr = NULL, gl = NULL, go = NULL, gs0 = NULL, gs1 = NULL, gs2 = NULL, gs3 = NULL;
+    float near_plane = 0.0f;
+    float far_plane = 0.0f;
+    gsx_vec3 bg;
+    gsx_size_t img_bytes;
+
+    rc = ensure_backend();
+    if(rc != 0) return rc;
+    unpack_camera(camera, &intr, &pose, &near_plane, &far_plane, &bg);
+    img_bytes = (gsx_size_t)3 * intr.height * intr.width * sizeof(float);
+    TRY(scene_upload(&s, n, sh_degree, mean3d, rotation, logscale, opacity, sh0, sh1, sh2, sh3));
+    TRY(make_tensor(s.arena, &out, 3, 3, intr.height, intr.width, NULL));
+    TRY(make_tensor(s.arena, &gout, 3, 3, intr.height, intr.width, grad_rgb));
+    TRY(make_tensor(s.arena, &gm, 2, n, 3, 0, NULL));
+    TRY(make_tensor(s.arena, &gr, 2, n, 4, 0, NULL));
+    TRY(make_tensor(s.arena, &gl, 2, n, 3, 0, NULL));
+    TRY(make_tensor(s.arena, &go, 1, n, 0, 0, NULL));
+    TRY(make_tensor(s.arena, &gs0, 2, n, 3, 0, NULL));
+    if(sh_degree >= 1) TRY(make_tensor(s.arena, &gs1, 3, n, 3, 3, NULL));
+    if(sh_degree >= 2) TRY(make_tensor(s.arena, &gs2, 3, n, 5, 3, NULL));
+    if(sh_degree >= 3) TRY(make_tensor(s.arena, &gs3, 3, n, 7, 3, NULL));
+    rdesc.width = intr.width;
+    rdesc.height = intr.height;
+    rdesc.output_data_type = GSX_DATA_TYPE_F32;
+    TRY(gsx_renderer_init(&renderer, g_backend, &rdesc));
+    TRY(gsx_render_context_init(&context, renderer));
+    req.intrinsics = &intr;
+    req.pose = &pose;
+    req.near_plane = near_plane;
+    req.far_plane = far_plane;
+    req.background_color = bg;
+    req.precision = GSX_RENDER_PRECISION_FLOAT32;
+    req.sh_degree = sh_degree;
+    req.forward_type = GSX_RENDER_FORWARD_TYPE_TRAIN;
+    req.borrow_train_state = true;
+    req.gs_mean3d = s.mean3d;
+    req.gs_rotation = s.rotation;
+    req.gs_logscale = s.logscale;
+    req.gs_opacity = s.opacity;
+    req.gs_sh0 = s.sh0;
+    req.gs_sh1 = s.sh1;
+    req.gs_sh2 = s.sh2;
+    req.gs_sh3 = s.sh3;
+    req.out_rgb = out;
+    TRY(gsx_renderer_render(renderer, context, &req));
+    breq.grad_rgb = gout;
+    breq.grad_gs_mean3d = gm;
+    breq.grad_gs_rotation = gr;
+    breq.grad_gs_logscale = gl;
+    breq.grad_gs_opacity = go;
+    breq.grad_gs_sh0 = gs0;
+    breq.grad_gs_sh1 = gs1;
+    breq.grad_gs_sh2 = gs2;
+    breq.grad_gs_sh3 = gs3;
+    TRY(gsx_renderer_backward(renderer, context, &breq));
+    TRY(gsx_tensor_download(out, out_rgb, img_bytes));
+    TRY(gsx_tensor_download(gm, g_mean3d, (gsx_size_t)n * 3u * sizeof(float)));
+    TRY(gsx_tensor_download(gr, g_rotation, (gsx_size_t)n * 4u * sizeof(float)));
+    TRY(gsx_tensor_download(gl, g_logscale, (gsx_size_t)n * 3u * sizeof(float)));
+    TRY(gsx_tensor_download(go, g_opacity, (gsx_size_t)n * sizeof(float)));
+    TRY(gsx_tensor_download(gs0, g_sh0, (gsx_size_t)n * 3u * sizeof(float)));
+    if(gs1 != NULL) TRY(gsx_tensor_download(gs1, g_sh1, (gsx_size_t)n * 9u * sizeof(float)));
+    if(gs2 != NULL) TRY(gsx_tensor_download(gs2, g_sh2, (gsx_size_t)n * 15u * sizeof(float)));
+    if(gs3 != NULL) TRY(gsx_tensor_download(gs3, g_sh3, (gsx_size_t)n * 21u * sizeof(float)));
+done:
+    if(context != NULL) (void)gsx_render_context_free(context);
+    if(renderer != NULL) (void)gsx_renderer_free(renderer);
+    {
+        gsx_tensor_t all[] = { out, gout, gm, gr, gl, go, gs0, gs1, gs2, gs3 };
+        size_t i;
+        for(i = 0; i < sizeof(all) / sizeof(all[0]); ++i) {
+            if(all[i] != NULL) (void)gsx_tensor_free(all[i]);
+        }
+    }
+    scene_free(&s);
+    return rc;
+}
+
+/* Loss forward then backward on [outer, C, H, W] CHW images.
+ * algorithm: 0 L1, 1 MSE, 2 SSIM (gsx_loss_algorithm). grad_norm: 0 MEAN, 1 SUM.
+ * loss_map and grad are accumulators: read, accumulated into, written back. grad may be NULL
+ * to skip the backward. */
+int gsxref_loss(int algorithm, int grad_norm, int outer, int channels, int height, int width,
+    const float *prediction, const float *target, float scale, float *loss_map, float *grad)
+{
+    int rc = 0;
+    gsx_arena_t arena = NULL;
+    gsx_arena_desc adesc = { 0 };
+    gsx_tensor_desc desc = { 0 };
+    gsx_tensor_t pred = NULL, tgt = NULL, map = NULL, g = NULL;
+    gsx_loss_t loss = NULL;
+    gsx_loss_context_t context = NULL;
+    gsx_loss_desc ldesc = { 0 };
+    gsx_loss_forward_request freq = { 0 };
+    gsx_loss_backward_request breq = { 0 };
+    gsx_size_t bytes = (gsx_size_t)outer * channels * height * width * sizeof(float);
+
+    rc = ensure_backend();
+    if(rc != 0) return rc;
+    adesc.initial_capacity_bytes = bytes * 4u + 4096u;
+    TRY(gsx_arena_init(&arena, g_device_type, &adesc));
+    desc.rank = outer > 1 ? 4 : 3;
+    if(outer > 1) {
+        desc.shape[0] = outer; desc.shape[1] = channels; desc.shape[2] = height; desc.shape[3] = width;
+    } else {
+        desc.shape[0] = channels; desc.shape[1] = height; desc.shape[2] = width;
+    }
+    desc.data_type = GSX_DATA_TYPE_F32;
+    desc.storage_format = GSX_STORAGE_FORMAT_CHW;
+    desc.arena = arena;
+    TRY(gsx_tensor_init(&pred, &desc));
+    TRY(gsx_tensor_init(&tgt, &desc));
+    TRY(gsx_tensor_init(&map, &desc));
+    TRY(gsx_tensor_init(&g, &desc));
+    TRY(gsx_tensor_upload(pred, prediction, bytes));
+    TRY(gsx_tensor_upload(tgt, target, bytes));
+    TRY(gsx_tensor_upload(map, loss_map, bytes));
+    if(grad != NULL) TRY(gsx_tensor_upload(g, grad, bytes));
+    ldesc.algorithm = (gsx_loss_algorithm)algorithm;
+    ldesc.grad_normalization = (gsx_loss_grad_normalization_type)grad_norm;
+    TRY(gsx_loss_init(&loss, g_backend, &ldesc));
+    TRY(gsx_loss_context_init(&context, loss));
+    freq.prediction = pred;
+    freq.target = tgt;
+    freq.loss_map_accumulator = map;
+    freq.train = grad != NULL;
+    freq.scale = scale;
+    TRY(gsx_loss_forward(loss, context, &freq));
+    if(grad != NULL) {
+        breq.grad_prediction_accumulator = g;
+        breq.scale = scale;
+        TRY(gsx_loss_backward(loss, context, &breq));
+        TRY(gsx_tensor_download(g, grad, bytes));
+    }
+    TRY(gsx_tensor_download(map, loss_map, bytes));
+done:
+    if(context != NULL) (void)gsx_loss_context_free(context);
+    if(loss != NULL) (void)gsx_loss_free(loss);
+    if(pred != NULL) (void)gsx_tensor_free(pred);
+    if(tgt != NULL) (void)gsx_tensor_free(tgt);
+    if(map != NULL) (void)gsx_tensor_free(map);
+    if(g != NULL) (void)gsx_tensor_free(g);
+    if(arena != NULL) (void)gsx_arena_free(arena);
+    return rc;
+}
+
+/* Adam over one parameter group of `count` floats for `steps` steps, with the same gradient
+ * each step. hyper[6] = lr, beta1, beta2, weight_decay, epsilon, max_grad.
+ * param is updated in place; m and v receive the final moments. */
+int gsxref_adam(int count, int steps, float *param, const float *grad, const float *hyper, float *m, float *v)
+{
+    int rc = 0;
+    gsx_arena_t arena = NULL;
+    gsx_arena_desc adesc = { 0 };
+    gsx_tensor_t p = NULL, g = NULL;
+    gsx_optim_t optim = NULL;
+    gsx_optim_desc odesc = { 0 };
+    gsx_optim_param_group_desc group = { 0 };
+    gsx_optim_step_request sreq = { 0 };
+    int i;
+
+    (void)m;
+    (void)v;
+    rc = ensure_backend();
+    if(rc != 0) return rc;
+    adesc.initial_capacity_bytes = (gsx_size_t)count * 16u + 4096u;
+    TRY(gsx_arena_init(&arena, g_device_type, &adesc));
+    TRY(make_tensor(arena, &p, 1, count, 0, 0, param));
+    TRY(make_tensor(arena, &g, 1, count, 0, 0, grad));
+    group.role = GSX_OPTIM_PARAM_ROLE_MEAN3D;
+    group.label = "p";
+    group.parameter = p;
+    group.gradient = g;
+    group.learning_rate = hyper[0];
+    group.beta1 = hyper[1];
+    group.beta2 = hyper[2];
+    group.weight_decay = hyper[3];
+    group.epsilon = hyper[4];
+    group.max_grad = hyper[5];
+    odesc.algorithm = GSX_OPTIM_ALGORITHM_ADAM;
+    odesc.param_groups = &group;
+    odesc.param_group_count = 1;
+    TRY(gsx_optim_init(&optim, g_backend, &odesc));
+    sreq.force_all = true;
+    for(i = 0; i < steps; ++i) {
+        TRY(gsx_optim_step(optim, &sreq));
+    }
+    TRY(gsx_tensor_download(p, param, (gsx_size_t)count * sizeof(float)));
+done:
+    if(optim != NULL) (void)gsx_optim_free(optim);
+    if(p != NULL) (void)gsx_tensor_free(p);
+    if(g != NULL) (void)gsx_tensor_free(g);
+    if(arena != NULL) (void)gsx_arena_free(arena);
+    return rc;
+}
+
+/* One ADC step (DEFAULT or ABSGS) on a Gaussian set with SH0 only and an Adam optimizer over
+ * the 5 built-in roles. params[10] = pruning_opacity_threshold, opacity_clamp_value,
+ * max_world_scale, max_screen_scale, duplicate_grad_threshold, duplicate_scale_threshold,
+ * duplicate_absgrad_threshold, scene_scale, (unused), (unused).
+ * iparams[8] = algorithm, refine_every, start_refine, end_refine, max_num_gaussians,
+ * reset_every, global_step, seed.
+ * In: n rows of mean3d/rotation/logscale/opacity/sh0 + grad_acc, absgrad_acc, visible_counter.
+ * Out: *out_n rows written to out_* (capacity out_capacity rows); counters[4] = pruned,
+ * duplicated, grown, reset. */
+int gsxref_adc(int n, const float *mean3d, const float *rotation, const float *logscale, const float *opacity,
+    const float *sh0, const float *grad_acc, const float *absgrad_acc, const float *visible_counter,
+    const float *params, const int64_t *iparams, int out_capacity, int *out_n,
+    float *o_mean3d, float *o_rotation, float *o_logscale, float *o_opacity, float *o_sh0, int64_t *counters)
+{
+    int rc = 0;
+    gsx_gs_t gs = NULL;
+    gsx_gs_desc gdesc = { 0 };
+    gsx_tensor_t t = NULL;
+    gsx_adc_t adc = NULL;
+    gsx_adc_desc adesc = { 0 };
+    gsx_adc_request areq = { 0 };
+    gsx_adc_result ares = { 0 };
+    gsx_optim_t optim = NULL;
+    gsx_optim_desc odesc = { 0 };
+    gsx_optim_param_group_desc groups[5];
+    gsx_gs_info info = { 0 };
+    const gsx_gs_field fields[5] = { GSX_GS_FIELD_MEAN3D, GSX_GS_FIELD_LOGSCALE, GSX_GS_FIELD_ROTATION,
+        GSX_GS_FIELD_OPACITY, GSX_GS_FIELD_SH0 };
+    const gsx_gs_field grad_fields[5] = { GSX_GS_FIELD_GRAD_MEAN3D, GSX_GS_FIELD_GRAD_LOGSCALE,
+        GSX_GS_FIELD_GRAD_ROTATION, GSX_GS_FIELD_GRAD_OPACITY, GSX_GS_FIELD_GRAD_SH0 };
+    const gsx_optim_param_role roles[5] = { GSX_OPTIM_PARAM_ROLE_MEAN3D, GSX_OPTIM_PARAM_ROLE_LOGSCALE,
+        GSX_OPTIM_PARAM_ROLE_ROTATION, GSX_OPTIM_PARAM_ROLE_OPACITY, GSX_OPTIM_PARAM_ROLE_SH0 };
+    int k;
+
+    rc = ensure_backend();
+    if(rc != 0) return rc;
+    gdesc.buffer_type = g_device_type;
+    gdesc.count = (gsx_size_t)n;
+    gdesc.aux_flags = GSX_GS_AUX_VISIBLE_COUNTER | GSX_GS_AUX_GRAD_ACC | GSX_GS_AUX_ABSGRAD_ACC;
+    TRY(gsx_gs_init(&gs, &gdesc));
+    TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_MEAN3D, &t));
+    TRY(gsx_tensor_upload(t, mean3d, (gsx_size_t)n * 3u * sizeof(float)));
+    TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_ROTATION, &t));
+    TRY(gsx_tensor_upload(t, rotation, (gsx_size_t)n * 4u * sizeof(float)));
+    TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_LOGSCALE, &t));
+    TRY(gsx_tensor_upload(t, logscale, (gsx_size_t)n * 3u * sizeof(float)));
+    TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_OPACITY, &t));
+    TRY(gsx_tensor_upload(t, opacity, (gsx_size_t)n * sizeof(float)));
+    TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_SH0, &t));
+    TRY(gsx_tensor_upload(t, sh0, (gsx_size_t)n * 3u * sizeof(float)));
+    TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_GRAD_ACC, &t));
+    TRY(gsx_tensor_upload(t, grad_acc, (gsx_size_t)n * sizeof(float)));
+    TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_ABSGRAD_ACC, &t));
+    TRY(gsx_tensor_upload(t, absgrad_acc, (gsx_size_t)n * sizeof(float)));
+    TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_VISIBLE_COUNTER, &t));
+    TRY(gsx_tensor_upload(t, visible_counter, (gsx_size_t)n * sizeof(float)));
+
+    memset(groups, 0, sizeof(groups));
+    for(k = 0; k < 5; ++k) {
+        TRY(gsx_gs_get_field(gs, fields[k], &groups[k].parameter));
+        TRY(gsx_gs_get_field(gs, grad_fields[k], &groups[k].gradient));
+        groups[k].role = roles[k];
+        groups[k].label = "g";
+        groups[k].learning_rate = 1e-3f;
+        groups[k].beta1 = 0.9f;
+        groups[k].beta2 = 0.999f;
+        groups[k].epsilon = 1e-8f;
+    }
+    odesc.algorithm = GSX_OPTIM_ALGORITHM_ADAM;
+    odesc.param_groups = groups;
+    odesc.param_group_count = 5;
+    TRY(gsx_optim_init(&optim, g_backend, &odesc));
+
+    adesc.algorithm = (gsx_adc_algorithm)iparams[0];
+    adesc.pruning_opacity_threshold = params[0];
+    adesc.opacity_clamp_value = params[1];
+    adesc.max_world_scale = params[2];
+    adesc.max_screen_scale = params[3];
+    adesc.duplicate_grad_threshold = params[4];
+    adesc.duplicate_scale_threshold = params[5];
+    adesc.duplicate_absgrad_threshold = params[6];
+    adesc.refine_every = (gsx_index_t)iparams[1];
+    adesc.start_refine = (gsx_index_t)iparams[2];
+    adesc.end_refine = (gsx_index_t)iparams[3];
+    adesc.max_num_gaussians = (gsx_index_t)iparams[4];
+    adesc.reset_every = (gsx_index_t)iparams[5];
+    adesc.seed = (gsx_size_t)iparams[7];
+    TRY(gsx_adc_init(&adc, g_backend, &adesc));
+    areq.gs = gs;
+    areq.optim = optim;
+    areq.global_step = (gsx_size_t)iparams[6];
+    areq.scene_scale = params[7];
+    TRY(gsx_adc_step(adc, &areq, &ares));
+    TRY(gsx_gs_get_info(gs, &info));
+    *out_n = (int)info.count;
+    counters[0] = (int64_t)ares.pruned_count;
+    counters[1] = (int64_t)ares.duplicated_count;
+    counters[2] = (int64_t)ares.grown_count;
+    counters[3] = (int64_t)ares.reset_count;
+    if((int)info.count > out_capacity) {
+        g_last_message = "adc output exceeds out_capacity";
+        rc = -2;
+        goto done;
+    }
+    TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_MEAN3D, &t));
+    TRY(gsx_tensor_download(t, o_mean3d, info.count * 3u * sizeof(float)));
+    TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_ROTATION, &t));
+    TRY(gsx_tensor_download(t, o_rotation, info.count * 4u * sizeof(float)));
+    TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_LOGSCALE, &t));
+    TRY(gsx_tensor_download(t, o_logscale, info.count * 3u * sizeof(float)));
+    TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_OPACITY, &t));
+    TRY(gsx_tensor_download(t, o_opacity, info.count * sizeof(float)));
+    TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_SH0, &t));
+    TRY(gsx_tensor_download(t, o_sh0, info.count * 3u * sizeof(float)));
+done:
+    if(adc != NULL) (void)gsx_adc_free(adc);
+    if(optim != NULL) (void)gsx_optim_free(optim);
+    if(gs != NULL) (void)gsx_gs_free(gs);
+    return rc;
+}
+
+static double now_seconds(void)
+{
+    struct timespec ts;
+
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return (double)ts.tv_sec + 1e-9 * (double)ts.tv_nsec;
+}
+
+/* `iters` image-fit style training steps on one camera: TRAIN render, L1 (scale w_l1) and
+ * SSIM (scale w_ssim) forward + backward, render backward, Adam over the 5 SH0 roles.
+ * hyper[2] = lr_mean3d, lr_other. stage_seconds[5] accumulates render fwd, loss fwd,
+ * loss bwd, render bwd, Adam (wall clock, single thread). The scene arrays are updated. */
+int gsxref_train_step(int n, int iters, float *mean3d, float *rotation, float *logscale, float *opacity,
+    float *sh0, const float *camera, const float *target_rgb, float w_l1, float w_ssim, const float *hyper,
+    double *stage_seconds)
+{
+    int rc = 0;
+    gsx_gs_t gs = NULL;
+    gsx_gs_desc gdesc = { 0 };
+    gsx_tensor_t t = NULL;
+    gsx_arena_t arena = NULL;
+    gsx_arena_desc adesc = { 0 };
+    gsx_tensor_t out = NULL, tgt = NULL, map = NULL, gout = NULL;
+    gsx_renderer_t renderer = NULL;
+    gsx_render_context_t rctx = NULL;
+    gsx_renderer_desc rdesc = { 0 };
+    gsx_loss_t l1 = NULL, ssim = NULL;
+    gsx_loss_context_t l1ctx = NULL, ssimctx = NULL;
+    gsx_loss_desc ldesc = { 0 };
+    gsx_optim_t optim = NULL;
+    gsx_optim_desc odesc = { 0 };
+    gsx_optim_param_group_desc groups[5];
+    gsx_optim_step_request sreq = { 0 };
+    gsx_camera_intrinsics intr;
+    gsx_camera_pose pose;
+    float near_plane, far_plane;
+    gsx_vec3 bg;
+    gsx_size_t img_bytes;
+    const gsx_gs_field fields[5] = { GSX_GS_FIELD_MEAN3D, GSX_GS_FIELD_LOGSCALE, GSX_GS_FIELD_ROTATION,
+        GSX_GS_FIELD_OPACITY, GSX_GS_FIELD_SH0 };
+    const gsx_gs_field grad_fields[5] = { GSX_GS_FIELD_GRAD_MEAN3D, GSX_GS_FIELD_GRAD_LOGSCALE,
+        GSX_GS_FIELD_GRAD_ROTATION, GSX_GS_FIELD_GRAD_OPACITY, GSX_GS_FIELD_GRAD_SH0 };
+    const gsx_optim_param_role roles[5] = { GSX_OPTIM_PARAM_ROLE_MEAN3D, GSX_OPTIM_PARAM_ROLE_LOGSCALE,
+        GSX_OPTIM_PARAM_ROLE_ROTATION, GSX_OPTIM_PARAM_ROLE_OPACITY, GSX_OPTIM_PARAM_ROLE_SH0 };
+    int k, it;
+
+    rc = ensure_backend();
+    if(rc != 0) return rc;
+    unpack_camera(camera, &intr, &pose, &near_plane, &far_plane, &bg);
+    img_bytes = (gsx_size_t)3 * intr.height * intr.width * sizeof(float);
+    gdesc.buffer_type = g_device_type;
+    gdesc.count = (gsx_size_t)n;
+    gdesc.aux_flags = GSX_GS_AUX_NONE;
+    TRY(gsx_gs_init(&gs, &gdesc));
+    TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_MEAN3D, &t));
+    TRY(gsx_tensor_upload(t, mean3d, (gsx_size_t)n * 3u * sizeof(float)));
+    TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_ROTATION, &t));
+    TRY(gsx_tensor_upload(t, rotation, (gsx_size_t)n * 4u * sizeof(float)));
+    TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_LOGSCALE, &t));
+    TRY(gsx_tensor_upload(t, logscale, (gsx_size_t)n * 3u * sizeof(float)));
+    TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_OPACITY, &t));
+    TRY(gsx_tensor_upload(t, opacity, (gsx_size_t)n * sizeof(float)));
+    TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_SH0, &t));
+    TRY(gsx_tensor_upload(t, sh0, (gsx_size_t)n * 3u * sizeof(float)));
+    adesc.initial_capacity_bytes = img_bytes * 4u + 4096u;
+    TRY(gsx_arena_init(&arena, g_device_type, &adesc));
+    TRY(make_tensor(arena, &out, 3, 3, intr.height, intr.width, NULL));
+    TRY(make_tensor(arena, &tgt, 3, 3, intr.height, intr.width, target_rgb));
+    TRY(make_tensor(arena, &map, 3, 3, intr.height, intr.width, NULL));
+    TRY(make_tensor(arena, &gout, 3, 3, intr.height, intr.width, NULL));
+    rdesc.width = intr.width;
+    rdesc.height = intr.height;
+    rdesc.output_data_type = GSX_DATA_TYPE_F32;
+    TRY(gsx_renderer_init(&renderer, g_backend, &rdesc));
+    TRY(gsx_render_context_init(&rctx, renderer));
+    ldesc.grad_normalization = GSX_LOSS_GRAD_NORMALIZATION_TYPE_MEAN;
+    ldesc.algorithm = GSX_LOSS_ALGORITHM_L1;
+    TRY(gsx_loss_init(&l1, g_backend, &ldesc));
+    TRY(gsx_loss_context_init(&l1ctx, l1));
+    ldesc.algorithm = GSX_LOSS_ALGORITHM_SSIM;
+    TRY(gsx_loss_init(&ssim, g_backend, &ldesc));
+    TRY(gsx_loss_context_init(&ssimctx, ssim));
+    memset(groups, 0, sizeof(groups));
+    for(k = 0; k < 5; ++k) {
+        TRY(gsx_gs_get_field(gs, fields[k], &groups[k].parameter));
+        TRY(gsx_gs_get_field(gs, grad_fields[k], &groups[k].gradient));
+        groups[k].role = roles[k];
+        groups[k].label = "g";
+        groups[k].learning_rate = k == 0 ? hyper[0] : hyper[1];
+        groups[k].beta1 = 0.9f;
+        groups[k].beta2 = 0.999f;
+        groups[k].epsilon = 1e-8f;
+    }
+    odesc.algorithm = GSX_OPTIM_ALGORITHM_ADAM;
+    odesc.param_groups = groups;
+    odesc.param_group_count = 5;
+    TRY(gsx_optim_init(&optim, g_backend, &odesc));
+    sreq.force_all = true;
+    for(it = 0; it < iters; ++it) {
+        gsx_render_forward_request req = { 0 };
+        gsx_render_backward_request breq = { 0 };
+        gsx_loss_forward_request lf = { 0 };
+        gsx_loss_backward_request lb = { 0 };
+        double t0, t1, t2, t3, t4, t5;
+
+        TRY(gsx_tensor_set_zero(map));
+        TRY(gsx_tensor_set_zero(gout));
+        TRY(gsx_gs_zero_gradients(gs));
+        req.intrinsics = &intr;
+        req.pose = &pose;
+        req.near_plane = near_plane;
+        req.far_plane = far_plane;
+        req.background_color = bg;
+        req.precision = GSX_RENDER_PRECISION_FLOAT32;
+        req.sh_degree = 0;
+        req.forward_type = GSX_RENDER_FORWARD_TYPE_TRAIN;
+        req.borrow_train_state = true;
+        TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_MEAN3D, &req.gs_mean3d));
+        TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_ROTATION, &req.gs_rotation));
+        TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_LOGSCALE, &req.gs_logscale));
+        TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_OPACITY, &req.gs_opacity));
+        TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_SH0, &req.gs_sh0));
+        req.out_rgb = out;
+        t0 = now_seconds();
+        TRY(gsx_renderer_render(renderer, rctx, &req));
+        t1 = now_seconds();
+        lf.prediction = out;
+        lf.target = tgt;
+        lf.loss_map_accumulator = map;
+        lf.train = true;
+        lf.scale = w_l1;
+        TRY(gsx_loss_forward(l1, l1ctx, &lf));
+        lf.scale = w_ssim;
+        TRY(gsx_loss_forward(ssim, ssimctx, &lf));
+        t2 = now_seconds();
+        lb.grad_prediction_accumulator = gout;
+        lb.scale = w_l1;
+        TRY(gsx_loss_backward(l1, l1ctx, &lb));
+        lb.scale = w_ssim;
+        TRY(gsx_loss_backward(ssim, ssimctx, &lb));
+        t3 = now_seconds();
+        breq.grad_rgb = gout;
+        TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_GRAD_MEAN3D, &breq.grad_gs_mean3d));
+        TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_GRAD_ROTATION, &breq.grad_gs_rotation));
+        TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_GRAD_LOGSCALE, &breq.grad_gs_logscale));
+        TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_GRAD_OPACITY, &breq.grad_gs_opacity));
+        TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_GRAD_SH0, &breq.grad_gs_sh0));
+        TRY(gsx_renderer_backward(renderer, rctx, &breq));
+        t4 = now_seconds();
+        TRY(gsx_optim_step(optim, &sreq));
+        t5 = now_seconds();
+        stage_seconds[0] += t1 - t0;
+        stage_seconds[1] += t2 - t1;
+        stage_seconds[2] += t3 - t2;
+        stage_seconds[3] += t4 - t3;
+        stage_seconds[4] += t5 - t4;
+    }
+    TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_MEAN3D, &t));
+    TRY(gsx_tensor_download(t, mean3d, (gsx_size_t)n * 3u * sizeof(float)));
+    TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_ROTATION, &t));
+    TRY(gsx_tensor_download(t, rotation, (gsx_size_t)n * 4u * sizeof(float)));
+    TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_LOGSCALE, &t));
+    TRY(gsx_tensor_download(t, logscale, (gsx_size_t)n * 3u * sizeof(float)));
+    TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_OPACITY, &t));
+    TRY(gsx_tensor_download(t, opacity, (gsx_size_t)n * sizeof(float)));
+    TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_SH0, &t));
+    TRY(gsx_tensor_download(t, sh0, (gsx_size_t)n * 3u * sizeof(float)));
+done:
+    if(optim != NULL) (void)gsx_optim_free(optim);
+    if(l1ctx != NULL) (void)gsx_loss_context_free(l1ctx);
+    if(ssimctx != NULL) (void)gsx_loss_context_free(ssimctx);
+    if(l1 != NULL) (void)gsx_loss_free(l1);
+    if(ssim != NULL) (void)gsx_loss_free(ssim);
+    if(rctx != NULL) (void)gsx_render_context_free(rctx);
+    if(renderer != NULL) (void)gsx_renderer_free(renderer);
+    {
+        gsx_tensor_t all[] = { out, tgt, map, gout };
+        size_t i;
+        for(i = 0; i < sizeof(all) / sizeof(all[0]); ++i) {
+            if(all[i] != NULL) (void)gsx_tensor_free(all[i]);
+        }
+    }
+    if(arena != NULL) (void)gsx_arena_free(arena);
+    if(gs != NULL) (void)gsx_gs_free(gs);
+    return rc;
+}
