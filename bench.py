@@ -1,0 +1,264 @@
+#!/usr/bin/env python3
+"""Headline benchmark: one gsx training step on one MI355X.
+
+Workload (BASELINE.json metric "fwd+bwd train iters/sec @1M Gaussians 1920x1080"): the
+config-3 scene generator at N = 1,000,000 (64 anisotropic clusters + 20% radius-10 shell,
+logscale N(-4.5, 0.6), opacity N(0, 1.5), SH0), 1920x1080 pinhole f = 1600, one of 24 orbit
+poses (radius 6) per step, seeded blurred-noise targets. One step = TRAIN render forward,
+0.8 L1 + 0.2 (1 - SSIM) forward and backward, render backward, Adam over the five parameter
+groups (mean3d lr 1e-3, others 1e-2). All inputs are resident in HBM before the timed region.
+
+Printed (rank 0, one JSON line): the train it/s as `value`, plus the inference render FPS, the
+sort bandwidth, a per-kernel table, the roofline entry of the dominant kernel and the CPU
+baseline (the unmodified gsx CPU backend built from the reference sources, when present).
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBPS = 8000.0
+FP32_PEAK_TFLOPS = 157.3
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def algorithmic_bytes(stage, n, visible, instances, tiles, pixels, sort_passes):
+    """Bytes each stage must move at minimum (the roofline numerators)."""
+    if stage == "preprocess":
+        return 56 * n + 52 * visible
+    if stage == "scan":
+        return 8 * n
+    if stage == "emit":
+        return 32 * visible + 12 * instances
+    if stage == "sort":
+        return 8 * instances + sort_passes * 24 * instances
+    if stage == "ranges":
+        return 8 * instances + 8 * tiles
+    if stage == "blend_forward":
+        return 52 * instances + 8 * tiles + 20 * pixels
+    if stage == "grad_zero":
+        return 36 * n
+    if stage == "blend_backward":
+        return 84 * instances + 8 * tiles + 20 * pixels + 36 * visible
+    if stage == "projection_backward":
+        return 56 * n + 36 * visible + 56 * n
+    if stage == "loss_forward":
+        return 28 * 3 * pixels
+    if stage == "loss_backward":
+        return 28 * 3 * pixels
+    if stage == "adam":
+        return 28 * 14 * n
+    return 0
+
+
+def cpu_baseline(workload, iters):
+    from oracle.oracle import Reference
+    if not Reference.available():
+        return None
+    ref = Reference()
+    t0 = time.perf_counter()
+    _, stages = ref.train_steps(workload.scene, workload.camera, workload.target, iters)
+    elapsed = time.perf_counter() - t0
+    return elapsed, stages
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--gaussians", type=int, default=1_000_000)
+    ap.add_argument("--width", type=int, default=1920)
+    ap.add_argument("--height", type=int, default=1080)
+    ap.add_argument("--poses", type=int, default=24)
+    ap.add_argument("--cpu-baseline-iters", type=int, default=1,
+                    help="reference CPU steps to time on the full workload (0 disables)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; multi-GPU scaling is design-only "
+                                   "(see DESIGN.md, 'How the path would shard')", "n_gpus": args.gpus}))
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from gsx_amd import _lib, scenes
+    from gsx_amd.backend import Adam, Camera, GaussianTensors, Renderer, ptr, stream_handle
+
+    lib = _lib.load()
+    dev_name = torch.cuda.get_device_name(0)
+    log(f"device {dev_name}; generating the metric scene (N={args.gaussians})")
+    t0 = time.perf_counter()
+    base = scenes.metric_scene(args.gaussians, args.width, args.height, 0)
+    cams = []
+    targets = []
+    for k in range(args.poses):
+        pose = scenes.orbit_pose(k)
+        block = scenes.camera(args.width, args.height, 1600.0 * args.width / 1920.0, pose=tuple(pose), near=0.01,
+                              far=100.0)
+        cams.append(Camera.from_block(block))
+        tgt = base.target if k == 0 else scenes.target_image(0, 103 + k, args.width, args.height, 2)
+        targets.append(torch.from_numpy(tgt).cuda())
+    log(f"scene + {args.poses} targets ready in {time.perf_counter() - t0:.1f}s")
+
+    g = GaussianTensors.from_scene(base.scene)
+    grads = g.zeros_like_grads()
+    renderer = Renderer(args.width, args.height)
+    img = torch.empty((3, args.height, args.width), dtype=torch.float32, device="cuda")
+    loss_map = torch.empty_like(img)
+    grad_img = torch.empty_like(img)
+    ssim_ws = torch.empty(3 * img.numel(), dtype=torch.float32, device="cuda")
+    opt = Adam([dict(parameter=g.mean3d, gradient=grads.mean3d, learning_rate=1e-3),
+                dict(parameter=g.logscale, gradient=grads.logscale, learning_rate=1e-2),
+                dict(parameter=g.rotation, gradient=grads.rotation, learning_rate=1e-2),
+                dict(parameter=g.opacity, gradient=grads.opacity, learning_rate=1e-2),
+                dict(parameter=g.sh0, gradient=grads.sh0, learning_rate=1e-2)])
+    numel = img.numel()
+    gs_l1 = float(np.float32(0.8) / np.float32(numel))
+    gs_ssim = float(np.float32(0.2) / np.float32(numel))
+    H, W = args.height, args.width
+
+    ev = {k: [] for k in ("loss_forward", "loss_backward", "adam")}
+
+    def step(i, record=False):
+        cam = cams[i % args.poses]
+        tgt = targets[i % args.poses]
+        st = stream_handle()
+        renderer.render(cam, g, train=True, out_rgb=img)
+        loss_map.zero_()
+        grad_img.zero_()
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(4)] if record else None
+        if record:
+            e[0].record()
+        # 0.8 L1 + 0.2 (1 - SSIM), fused in one pass each way (bit-identical to separate calls)
+        _lib.check(lib.gsx_hip_loss_ssim_chw_f32_forward_kernel_launch(
+            ptr(loss_map), ptr(img), ptr(tgt), 1, 3, H, W, 0.2, ptr(ssim_ws), 0.8, 1, st), "loss forward")
+        if record:
+            e[1].record()
+        _lib.check(lib.gsx_hip_loss_ssim_chw_f32_backward_kernel_launch(
+            ptr(grad_img), ptr(img), ptr(tgt), 1, 3, H, W, gs_ssim, ptr(ssim_ws), gs_l1, 1, st), "loss backward")
+        if record:
+            e[2].record()
+        renderer.backward(grad_img, grads)
+        if record:
+            e[3].record()
+        opt.step()
+        if record:
+            e4 = torch.cuda.Event(enable_timing=True)
+            e4.record()
+            ev["loss_forward"].append((e[0], e[1]))
+            ev["loss_backward"].append((e[1], e[2]))
+            ev["adam"].append((e[3], e4))
+
+    log(f"warmup {args.warmup} steps")
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+
+    renderer.set_timing(args.steps)
+    log(f"timing {args.steps} steps")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(args.warmup + i, record=True)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    it_s = args.steps / elapsed
+    stage_ms = renderer.timings()
+    renderer.set_timing(0)
+    for k, pairs in ev.items():
+        stage_ms[k] = sum(a.elapsed_time(b) for a, b in pairs) / len(pairs)
+    stats = renderer.stats()
+    instances = int(stats.instance_count)
+    visible = int((torch.zeros(1)).item())  # filled below
+    # visible Gaussians of the last pose (tile count > 0), for the byte model
+    buf = renderer.buffers()
+    tc = torch.empty(args.gaussians, dtype=torch.int32, device="cuda")
+    _lib.check(lib.gsx_hip_memcpy_dtod_async(ctypes.c_void_p(tc.data_ptr()), buf.tile_counts, tc.numel() * 4, None))
+    torch.cuda.synchronize()
+    visible = int((tc > 0).sum().item())
+    log(f"train: {it_s:.1f} it/s ({1000.0 / it_s:.3f} ms/step), instances {instances}, visible {visible}")
+
+    # inference forward FPS on the same scene (cycling poses)
+    fps_steps = max(args.steps, 20)
+    for i in range(3):
+        renderer.render(cams[i % args.poses], g, train=False, out_rgb=img)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(fps_steps):
+        renderer.render(cams[i % args.poses], g, train=False, out_rgb=img)
+    torch.cuda.synchronize()
+    fps = fps_steps / (time.perf_counter() - t0)
+    log(f"inference forward: {fps:.1f} FPS")
+
+    pixels = H * W
+    tiles = int(stats.tile_count)
+    kernels = []
+    for name, ms in stage_ms.items():
+        b = algorithmic_bytes(name, args.gaussians, visible, instances, tiles, pixels, int(stats.sort_passes))
+        gbps = b / (ms * 1e-3) / 1e9 if ms > 0 else 0.0
+        kernels.append({"stage": name, "ms": round(ms, 4), "algorithmic_bytes": int(b), "gbps": round(gbps, 1),
+                        "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4)})
+    kernels.sort(key=lambda k: -k["ms"])
+    dominant = kernels[0]
+    sort_entry = next(k for k in kernels if k["stage"] == "sort")
+
+    result = {
+        "metric": "fwd+bwd train iters/sec @1M Gaussians 1920x1080; fwd render FPS; sort GB/s",
+        "value": round(it_s, 2),
+        "unit": "it/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(1000.0 * elapsed / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded config-3 generator, blurred-noise targets)",
+        "config": {"workload": "metric: config-3 generator at N=1M, 1920x1080, f=1600, 24 orbit poses, SH0, "
+                               "fwd+bwd+0.8*L1+0.2*(1-SSIM)+Adam",
+                   "gaussians": args.gaussians, "width": W, "height": H, "poses": args.poses,
+                   "instances_last_pose": instances, "visible_last_pose": visible},
+        "render_fps": round(fps, 1),
+        "sort_gbps": sort_entry["gbps"],
+        "sort_hbm_frac": sort_entry["hbm_frac"],
+        "kernels": kernels,
+        "roofline": {"bound": "hbm", "kernel": dominant["stage"], "achieved": dominant["gbps"],
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": dominant["hbm_frac"], "traffic": None},
+        "device": dev_name,
+    }
+
+    if args.cpu_baseline_iters > 0:
+        log(f"CPU baseline: reference CPU backend, {args.cpu_baseline_iters} step(s) of the full workload, 1 thread")
+        res = cpu_baseline(scenes.Workload("metric", base.scene, np.array(
+            [1600.0 * W / 1920.0, 1600.0 * W / 1920.0, W / 2.0, H / 2.0, W, H, *scenes.orbit_pose(0), 0.01, 100.0,
+             0, 0, 0], np.float32), base.target), args.cpu_baseline_iters)
+        if res is not None:
+            secs, stages = res
+            result["cpu_baseline"] = {
+                "value": round(args.cpu_baseline_iters / secs, 5), "unit": "it/s", "cores": 1, "kind": "reference",
+                "sample": f"{args.cpu_baseline_iters} full step(s) of the same workload (pose 0) through the "
+                          "unmodified gsx CPU backend, single-threaded by construction",
+                "seconds_per_step": round(secs / args.cpu_baseline_iters, 3),
+                "stage_seconds": {k: round(float(v) / args.cpu_baseline_iters, 3) for k, v in
+                                  zip(("render_forward", "loss_forward", "loss_backward", "render_backward",
+                                       "adam"), stages)}}
+        else:
+            result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

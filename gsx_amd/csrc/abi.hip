@@ -1,0 +1,559 @@
+// abi.hip - host side of libgsx_hip.so: device plumbing, the render context (pooled buffers,
+// retained TRAIN state, stage timing) and the forward/backward pipelines.
+//
+// Forward (one stream, in order):
+//   preprocess -> exclusive scan of per-Gaussian tile counts -> [host reads the instance count]
+//   -> key emission -> stable radix sort on (tile << 32 | depth bits) -> tile ranges -> blend.
+// Backward:
+//   zero the screen-space accumulator -> blend backward (atomics into it) -> projection backward.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <new>
+
+#include "../../include/gsx_hip.h"
+#include "common.hpp"
+
+// The render kernels are compiled in this translation unit so their launches need no
+// relocatable device code.
+#include "render.hip"
+
+using namespace gsx_amd;
+
+namespace {
+
+thread_local char g_message[256] = "";
+
+gsx_hip_status fail(gsx_hip_status code, const char* what) {
+    snprintf(g_message, sizeof(g_message), "%s", what);
+    return code;
+}
+
+gsx_hip_status hip_fail(hipError_t e, const char* what) {
+    snprintf(g_message, sizeof(g_message), "%s: %s", what, hipGetErrorString(e));
+    return (gsx_hip_status)e;
+}
+
+#define GSX_HIP_TRY(expr, what)                 \
+    do {                                        \
+        hipError_t e_ = (expr);                 \
+        if (e_ != hipSuccess) return hip_fail(e_, what); \
+    } while (0)
+
+#define GSX_TRY(expr)                           \
+    do {                                        \
+        gsx_hip_status s_ = (expr);             \
+        if (s_ != GSX_HIP_SUCCESS) return s_;   \
+    } while (0)
+
+// Grow-only device buffer: the render context keeps its intermediates across calls, so steady
+// state training performs no allocation (gsx's CPU/CUDA contexts reset and re-grow arenas on
+// every forward, gsx/src/gsx-cuda/render.c:346-377).
+struct DeviceBuffer {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+
+    gsx_hip_status reserve(size_t need, const char* what) {
+        if (need <= bytes) return GSX_HIP_SUCCESS;
+        size_t grow = need + need / 4 + 4096;
+        if (ptr != nullptr) {
+            hipError_t e = hipFree(ptr);
+            ptr = nullptr;
+            bytes = 0;
+            if (e != hipSuccess) return hip_fail(e, what);
+        }
+        hipError_t e = hipMalloc(&ptr, grow);
+        if (e != hipSuccess) {
+            ptr = nullptr;
+            return hip_fail(e, what);
+        }
+        bytes = grow;
+        return GSX_HIP_SUCCESS;
+    }
+    void release() {
+        if (ptr != nullptr) (void)hipFree(ptr);
+        ptr = nullptr;
+        bytes = 0;
+    }
+    template <typename T>
+    T* as() const {
+        return static_cast<T*>(ptr);
+    }
+};
+
+unsigned blocks_for(int64_t n, int threads) {
+    int64_t b = (n + threads - 1) / threads;
+    return (unsigned)(b < 1 ? 1 : b);
+}
+
+// Pose quaternion to world-to-camera matrix and camera centre, with the CPU's arithmetic
+// (render.c:561-581, 603-609), evaluated once on the host.
+CameraParams make_camera_params(const gsx_hip_camera& c) {
+    CameraParams p;
+    float qx = c.rot[0], qy = c.rot[1], qz = c.rot[2], qw = c.rot[3];
+    float norm_sq = qx * qx + qy * qy + qz * qz + qw * qw;
+    if (norm_sq <= kMinQuatNormSq) {
+        qx = 0.0f;
+        qy = 0.0f;
+        qz = 0.0f;
+        qw = 1.0f;
+    } else {
+        float inv_norm = 1.0f / sqrtf(norm_sq);
+        qx = qx * inv_norm;
+        qy = qy * inv_norm;
+        qz = qz * inv_norm;
+        qw = qw * inv_norm;
+    }
+    p.w[0][0] = 1.0f - 2.0f * (qy * qy + qz * qz);
+    p.w[0][1] = 2.0f * (qx * qy - qw * qz);
+    p.w[0][2] = 2.0f * (qx * qz + qw * qy);
+    p.w[1][0] = 2.0f * (qx * qy + qw * qz);
+    p.w[1][1] = 1.0f - 2.0f * (qx * qx + qz * qz);
+    p.w[1][2] = 2.0f * (qy * qz - qw * qx);
+    p.w[2][0] = 2.0f * (qx * qz - qw * qy);
+    p.w[2][1] = 2.0f * (qy * qz + qw * qx);
+    p.w[2][2] = 1.0f - 2.0f * (qx * qx + qy * qy);
+    for (int i = 0; i < 3; ++i) p.t[i] = c.transl[i];
+    for (int i = 0; i < 3; ++i) {
+        float v = p.w[0][i] * c.transl[0] + p.w[1][i] * c.transl[1] + p.w[2][i] * c.transl[2];
+        p.centre[i] = v * -1.0f;
+    }
+    p.fx = c.fx;
+    p.fy = c.fy;
+    p.cx = c.cx;
+    p.cy = c.cy;
+    p.near_plane = c.near_plane;
+    p.far_plane = c.far_plane;
+    for (int i = 0; i < 3; ++i) p.bg[i] = c.background[i];
+    p.width = c.width;
+    p.height = c.height;
+    p.tiles_x = (c.width + kTile - 1) / kTile;
+    p.tiles_y = (c.height + kTile - 1) / kTile;
+    return p;
+}
+
+int bits_for(uint32_t v) {
+    int b = 0;
+    while (b < 32 && (1ull << b) < (uint64_t)v + 1ull) ++b;
+    return b;
+}
+
+}  // namespace
+
+struct gsx_hip_render_context {
+    DeviceBuffer rec, cov_coef, ckpt, tile_count, offsets, scan_temp, keys, vals, keys_alt, vals_alt, sort_temp, ranges, final_t,
+        last, grad2d;
+    uint32_t* host_count = nullptr;  // pinned
+    CameraParams cam{};
+    gsx_hip_gaussians gs{};
+    int64_t instance_count = 0;
+    int64_t gaussian_count = 0;
+    int32_t tile_count_total = 0;
+    int32_t sort_passes = 0;
+    bool sorted_in_alt = false;
+    bool has_train_state = false;
+    // Stage timing: a ring of event sets, one set per forward/backward pair, so that a timed
+    // loop records without synchronising; get_timings averages over the recorded sets.
+    static constexpr int kEventsPerSet = GSX_HIP_RENDER_STAGE_COUNT + 2;
+    bool timing = false;
+    int32_t ring = 0;           // number of event sets
+    hipEvent_t* events = nullptr;
+    int32_t cur = -1;           // set of the current forward/backward pair
+    int32_t fwd_sets = 0;       // sets with a recorded forward (capped at ring)
+    int32_t bwd_sets = 0;
+    uint8_t* has_fwd = nullptr;
+    uint8_t* has_bwd = nullptr;
+};
+
+namespace {
+
+gsx_hip_status record(gsx_hip_render_context* ctx, int idx, hipStream_t stream) {
+    if (!ctx->timing || ctx->cur < 0) return GSX_HIP_SUCCESS;
+    GSX_HIP_TRY(hipEventRecord(ctx->events[ctx->cur * gsx_hip_render_context::kEventsPerSet + idx], stream),
+                "hipEventRecord");
+    return GSX_HIP_SUCCESS;
+}
+
+void release_events(gsx_hip_render_context* ctx) {
+    if (ctx->events != nullptr) {
+        for (int i = 0; i < ctx->ring * gsx_hip_render_context::kEventsPerSet; ++i) (void)hipEventDestroy(ctx->events[i]);
+    }
+    delete[] ctx->events;
+    delete[] ctx->has_fwd;
+    delete[] ctx->has_bwd;
+    ctx->events = nullptr;
+    ctx->has_fwd = nullptr;
+    ctx->has_bwd = nullptr;
+    ctx->ring = 0;
+}
+
+gsx_hip_status validate_gaussians(const gsx_hip_gaussians* g) {
+    if (g == nullptr) return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "gaussians must be non-null");
+    if (g->count < 0 || g->count > 0x7fffffffll) return fail(GSX_HIP_ERROR_OUT_OF_RANGE, "gaussian count out of range");
+    if (g->sh_degree < 0 || g->sh_degree > 3) return fail(GSX_HIP_ERROR_OUT_OF_RANGE, "sh_degree must be in [0,3]");
+    if (g->count > 0 && (g->mean3d == nullptr || g->rotation == nullptr || g->logscale == nullptr ||
+                         g->opacity == nullptr || g->sh0 == nullptr)) {
+        return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "mean3d, rotation, logscale, opacity and sh0 must be non-null");
+    }
+    if ((g->sh_degree >= 1 && g->sh1 == nullptr) || (g->sh_degree >= 2 && g->sh2 == nullptr) ||
+        (g->sh_degree >= 3 && g->sh3 == nullptr)) {
+        return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "sh1..sh3 must be non-null up to sh_degree");
+    }
+    if ((reinterpret_cast<uintptr_t>(g->rotation) & 15u) != 0) {
+        return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "rotation must be 16-byte aligned");
+    }
+    return GSX_HIP_SUCCESS;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* gsx_hip_last_error_message(void) { return g_message; }
+
+gsx_hip_status gsx_hip_device_count(int32_t* out_count) {
+    if (out_count == nullptr) return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "out_count must be non-null");
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess) {
+        *out_count = 0;
+        return hip_fail(e, "hipGetDeviceCount");
+    }
+    *out_count = n;
+    return GSX_HIP_SUCCESS;
+}
+
+gsx_hip_status gsx_hip_device_name(int32_t device, char* out_name, size_t capacity) {
+    if (out_name == nullptr || capacity == 0) return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "out_name must be non-null");
+    hipDeviceProp_t prop;
+    GSX_HIP_TRY(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
+    snprintf(out_name, capacity, "%s (%s)", prop.name, prop.gcnArchName);
+    return GSX_HIP_SUCCESS;
+}
+
+gsx_hip_status gsx_hip_malloc(void** out_ptr, size_t bytes) {
+    if (out_ptr == nullptr) return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "out_ptr must be non-null");
+    GSX_HIP_TRY(hipMalloc(out_ptr, bytes == 0 ? 1 : bytes), "hipMalloc");
+    return GSX_HIP_SUCCESS;
+}
+
+gsx_hip_status gsx_hip_free(void* ptr) {
+    GSX_HIP_TRY(hipFree(ptr), "hipFree");
+    return GSX_HIP_SUCCESS;
+}
+
+gsx_hip_status gsx_hip_memcpy_htod(void* dst, const void* src, size_t bytes) {
+    GSX_HIP_TRY(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice), "hipMemcpy H2D");
+    return GSX_HIP_SUCCESS;
+}
+
+gsx_hip_status gsx_hip_memcpy_dtoh(void* dst, const void* src, size_t bytes) {
+    GSX_HIP_TRY(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost), "hipMemcpy D2H");
+    return GSX_HIP_SUCCESS;
+}
+
+gsx_hip_status gsx_hip_memcpy_dtod_async(void* dst, const void* src, size_t bytes, hipStream_t stream) {
+    GSX_HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, stream), "hipMemcpyAsync D2D");
+    return GSX_HIP_SUCCESS;
+}
+
+gsx_hip_status gsx_hip_stream_create(hipStream_t* out_stream) {
+    if (out_stream == nullptr) return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "out_stream must be non-null");
+    GSX_HIP_TRY(hipStreamCreateWithFlags(out_stream, hipStreamNonBlocking), "hipStreamCreateWithFlags");
+    return GSX_HIP_SUCCESS;
+}
+
+gsx_hip_status gsx_hip_stream_destroy(hipStream_t stream) {
+    GSX_HIP_TRY(hipStreamDestroy(stream), "hipStreamDestroy");
+    return GSX_HIP_SUCCESS;
+}
+
+gsx_hip_status gsx_hip_stream_synchronize(hipStream_t stream) {
+    GSX_HIP_TRY(hipStreamSynchronize(stream), "hipStreamSynchronize");
+    return GSX_HIP_SUCCESS;
+}
+
+gsx_hip_status gsx_hip_fill_f32(float* dst, int64_t count, float value, hipStream_t stream) {
+    if (count <= 0) return GSX_HIP_SUCCESS;
+    if (dst == nullptr) return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "dst must be non-null");
+    hipLaunchKernelGGL(fill_f32_kernel, dim3(blocks_for(count, 256)), dim3(256), 0, stream, dst, count, value);
+    GSX_HIP_TRY(hipGetLastError(), "fill_f32_kernel");
+    return GSX_HIP_SUCCESS;
+}
+
+gsx_hip_status gsx_hip_render_context_create(gsx_hip_render_context** out_context) {
+    if (out_context == nullptr) return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "out_context must be non-null");
+    *out_context = nullptr;
+    gsx_hip_render_context* ctx = new (std::nothrow) gsx_hip_render_context();
+    if (ctx == nullptr) return fail(GSX_HIP_ERROR_OUT_OF_MEMORY, "render context allocation failed");
+    hipError_t e = hipHostMalloc(reinterpret_cast<void**>(&ctx->host_count), sizeof(uint32_t) * 2, hipHostMallocDefault);
+    if (e != hipSuccess) {
+        delete ctx;
+        return hip_fail(e, "hipHostMalloc");
+    }
+    *out_context = ctx;
+    return GSX_HIP_SUCCESS;
+}
+
+gsx_hip_status gsx_hip_render_context_destroy(gsx_hip_render_context* ctx) {
+    if (ctx == nullptr) return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "context must be non-null");
+    DeviceBuffer* all[] = {&ctx->rec, &ctx->cov_coef, &ctx->ckpt, &ctx->tile_count, &ctx->offsets,  &ctx->scan_temp, &ctx->keys,
+                           &ctx->vals,    &ctx->keys_alt,   &ctx->vals_alt, &ctx->sort_temp, &ctx->ranges,
+                           &ctx->final_t, &ctx->last,       &ctx->grad2d};
+    for (DeviceBuffer* b : all) b->release();
+    if (ctx->host_count != nullptr) (void)hipHostFree(ctx->host_count);
+    release_events(ctx);
+    delete ctx;
+    return GSX_HIP_SUCCESS;
+}
+
+gsx_hip_status gsx_hip_render_context_set_timing(gsx_hip_render_context* ctx, int32_t capacity) {
+    if (ctx == nullptr) return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "context must be non-null");
+    if (capacity < 0 || capacity > 100000) return fail(GSX_HIP_ERROR_OUT_OF_RANGE, "timing capacity out of range");
+    release_events(ctx);
+    ctx->timing = capacity > 0;
+    ctx->cur = -1;
+    ctx->fwd_sets = 0;
+    ctx->bwd_sets = 0;
+    if (capacity == 0) return GSX_HIP_SUCCESS;
+    const int total = capacity * gsx_hip_render_context::kEventsPerSet;
+    ctx->events = new (std::nothrow) hipEvent_t[total];
+    ctx->has_fwd = new (std::nothrow) uint8_t[capacity]();
+    ctx->has_bwd = new (std::nothrow) uint8_t[capacity]();
+    if (ctx->events == nullptr || ctx->has_fwd == nullptr || ctx->has_bwd == nullptr) {
+        release_events(ctx);
+        ctx->timing = false;
+        return fail(GSX_HIP_ERROR_OUT_OF_MEMORY, "timing ring allocation failed");
+    }
+    for (int i = 0; i < total; ++i) {
+        hipError_t e = hipEventCreate(&ctx->events[i]);
+        if (e != hipSuccess) {
+            for (int k = 0; k < i; ++k) (void)hipEventDestroy(ctx->events[k]);
+            delete[] ctx->events;
+            ctx->events = nullptr;
+            ctx->ring = 0;
+            release_events(ctx);
+            ctx->timing = false;
+            return hip_fail(e, "hipEventCreate");
+        }
+    }
+    ctx->ring = capacity;
+    return GSX_HIP_SUCCESS;
+}
+
+gsx_hip_status gsx_hip_render_context_get_timings(gsx_hip_render_context* ctx, float* out_ms, int32_t capacity,
+                                                  int32_t* out_written) {
+    if (ctx == nullptr || out_ms == nullptr) return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "context/out_ms null");
+    if (!ctx->timing) return fail(GSX_HIP_ERROR_INVALID_STATE, "timing is not enabled");
+    // per set: 0 fwd start, 1 preprocess, 2 scan (+count readback), 3 emit, 4 sort, 5 ranges,
+    //          6 blend; 7 bwd start, 8 zero, 9 blend bwd, 10 projection bwd
+    double sum[GSX_HIP_RENDER_STAGE_COUNT] = {0.0};
+    int nf = 0, nb = 0;
+    for (int set = 0; set < ctx->ring; ++set) {
+        hipEvent_t* ev = ctx->events + set * gsx_hip_render_context::kEventsPerSet;
+        if (ctx->has_fwd[set]) {
+            GSX_HIP_TRY(hipEventSynchronize(ev[6]), "hipEventSynchronize");
+            for (int i = 0; i < 6; ++i) {
+                float ms = 0.0f;
+                GSX_HIP_TRY(hipEventElapsedTime(&ms, ev[i], ev[i + 1]), "hipEventElapsedTime");
+                sum[i] += ms;
+            }
+            ++nf;
+        }
+        if (ctx->has_bwd[set]) {
+            GSX_HIP_TRY(hipEventSynchronize(ev[10]), "hipEventSynchronize");
+            for (int i = 0; i < 3; ++i) {
+                float ms = 0.0f;
+                GSX_HIP_TRY(hipEventElapsedTime(&ms, ev[7 + i], ev[8 + i]), "hipEventElapsedTime");
+                sum[6 + i] += ms;
+            }
+            ++nb;
+        }
+    }
+    const int n = capacity < GSX_HIP_RENDER_STAGE_COUNT ? capacity : GSX_HIP_RENDER_STAGE_COUNT;
+    for (int i = 0; i < n; ++i) {
+        const int denom = i < 6 ? nf : nb;
+        out_ms[i] = denom > 0 ? (float)(sum[i] / denom) : 0.0f;
+    }
+    if (out_written) *out_written = n;
+    return GSX_HIP_SUCCESS;
+}
+
+gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip_camera* camera,
+                                      const gsx_hip_gaussians* gaussians, int32_t train, float* out_rgb,
+                                      float* visible_counter, hipStream_t stream) {
+    if (ctx == nullptr || camera == nullptr || out_rgb == nullptr) {
+        return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "context, camera and out_rgb must be non-null");
+    }
+    GSX_TRY(validate_gaussians(gaussians));
+    if (camera->width <= 0 || camera->height <= 0 || camera->width > 32767 || camera->height > 32767) {
+        return fail(GSX_HIP_ERROR_OUT_OF_RANGE, "image width/height must be in [1, 32767]");
+    }
+    if (!(camera->near_plane > 0.0f) || !(camera->far_plane > camera->near_plane) || !isfinite(camera->far_plane)) {
+        return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "near_plane and far_plane must be finite with 0 < near < far");
+    }
+    ctx->has_train_state = false;
+    const CameraParams cam = make_camera_params(*camera);
+    const int64_t n = gaussians->count;
+    const int32_t tiles = cam.tiles_x * cam.tiles_y;
+    const int64_t pixels = (int64_t)cam.width * cam.height;
+    const int tile_bits = bits_for((uint32_t)(tiles > 0 ? tiles - 1 : 0));
+    ctx->cam = cam;
+    ctx->gs = *gaussians;
+    ctx->gaussian_count = n;
+    ctx->tile_count_total = tiles;
+
+    GSX_TRY(ctx->rec.reserve((size_t)(n > 0 ? n : 1) * 3 * sizeof(float4), "rec"));
+    if (train) GSX_TRY(ctx->cov_coef.reserve((size_t)(n > 0 ? n : 1) * 2 * sizeof(float4), "cov_coef"));
+    GSX_TRY(ctx->tile_count.reserve((size_t)(n > 0 ? n : 1) * sizeof(uint32_t), "tile_count"));
+    GSX_TRY(ctx->offsets.reserve((size_t)(n + 1) * sizeof(uint32_t), "offsets"));
+    GSX_TRY(ctx->scan_temp.reserve(gsx_hip_scan_temp_bytes(n), "scan_temp"));
+    GSX_TRY(ctx->ranges.reserve((size_t)tiles * sizeof(uint2), "ranges"));
+    GSX_TRY(ctx->final_t.reserve((size_t)pixels * sizeof(float), "final_t"));
+    GSX_TRY(ctx->last.reserve((size_t)pixels * sizeof(uint32_t), "last"));
+
+    if (ctx->timing) {
+        ctx->cur = (ctx->cur + 1) % ctx->ring;
+        ctx->has_fwd[ctx->cur] = 0;
+        ctx->has_bwd[ctx->cur] = 0;
+    }
+    GSX_TRY(record(ctx, 0, stream));
+    if (n > 0) {
+        hipLaunchKernelGGL(preprocess_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, n, gaussians->mean3d,
+                           gaussians->rotation, gaussians->logscale, gaussians->opacity, gaussians->sh0,
+                           gaussians->sh1, gaussians->sh2, gaussians->sh3, (int)gaussians->sh_degree, cam,
+                           ctx->rec.as<float4>(), train ? ctx->cov_coef.as<float4>() : nullptr,
+                           ctx->tile_count.as<uint32_t>(), train ? visible_counter : nullptr);
+        GSX_HIP_TRY(hipGetLastError(), "preprocess_kernel");
+    }
+    GSX_TRY(record(ctx, 1, stream));
+    GSX_TRY(gsx_hip_scan_exclusive_u32(ctx->tile_count.as<uint32_t>(), ctx->offsets.as<uint32_t>(), n,
+                                       ctx->scan_temp.ptr, stream));
+    GSX_HIP_TRY(hipMemcpyAsync(ctx->host_count, ctx->offsets.as<uint32_t>() + n, sizeof(uint32_t),
+                               hipMemcpyDeviceToHost, stream),
+                "instance count readback");
+    GSX_HIP_TRY(hipStreamSynchronize(stream), "instance count sync");
+    GSX_TRY(record(ctx, 2, stream));
+    const int64_t count = (int64_t)ctx->host_count[0];
+    ctx->instance_count = count;
+    GSX_TRY(ctx->keys.reserve((size_t)(count > 0 ? count : 1) * sizeof(uint64_t), "keys"));
+    GSX_TRY(ctx->keys_alt.reserve((size_t)(count > 0 ? count : 1) * sizeof(uint64_t), "keys_alt"));
+    GSX_TRY(ctx->vals.reserve((size_t)(count > 0 ? count : 1) * sizeof(uint32_t), "vals"));
+    GSX_TRY(ctx->vals_alt.reserve((size_t)(count > 0 ? count : 1) * sizeof(uint32_t), "vals_alt"));
+    GSX_TRY(ctx->sort_temp.reserve(gsx_hip_radix_sort_temp_bytes(count), "sort_temp"));
+    if (train) {
+        // bucket checkpoints: at most I/32 + tiles + 1 slots of 256 floats
+        GSX_TRY(ctx->ckpt.reserve(((size_t)count / 32 + (size_t)tiles + 2) * 256 * sizeof(float), "checkpoints"));
+    }
+    if (n > 0) {
+        hipLaunchKernelGGL(emit_keys_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, n, ctx->rec.as<float4>(),
+                           ctx->tile_count.as<uint32_t>(), ctx->offsets.as<uint32_t>(), cam.tiles_x,
+                           ctx->keys.as<uint64_t>(), ctx->vals.as<uint32_t>());
+        GSX_HIP_TRY(hipGetLastError(), "emit_keys_kernel");
+    }
+    GSX_TRY(record(ctx, 3, stream));
+    int in_alt = 0;
+    const int end_bit = 32 + tile_bits;
+    ctx->sort_passes = (end_bit + 7) / 8;
+    GSX_TRY(gsx_hip_radix_sort_pairs_u64(ctx->keys.as<uint64_t>(), ctx->vals.as<uint32_t>(),
+                                         ctx->keys_alt.as<uint64_t>(), ctx->vals_alt.as<uint32_t>(), count, 0,
+                                         ctx->sort_passes * 8, ctx->sort_temp.ptr, &in_alt, stream));
+    ctx->sorted_in_alt = in_alt != 0;
+    GSX_TRY(record(ctx, 4, stream));
+    const uint64_t* skeys = ctx->sorted_in_alt ? ctx->keys_alt.as<uint64_t>() : ctx->keys.as<uint64_t>();
+    const uint32_t* svals = ctx->sorted_in_alt ? ctx->vals_alt.as<uint32_t>() : ctx->vals.as<uint32_t>();
+    hipLaunchKernelGGL(fill_u32_kernel, dim3(blocks_for((int64_t)tiles * 2, 256)), dim3(256), 0, stream,
+                       ctx->ranges.as<uint32_t>(), (int64_t)tiles * 2, 0u);
+    if (count > 0) {
+        hipLaunchKernelGGL(tile_ranges_kernel, dim3(blocks_for(count, 256)), dim3(256), 0, stream, skeys,
+                           ctx->offsets.as<uint32_t>() + n, ctx->ranges.as<uint2>());
+    }
+    GSX_HIP_TRY(hipGetLastError(), "tile_ranges_kernel");
+    GSX_TRY(record(ctx, 5, stream));
+    const int tiles_padded = ((tiles + 7) / 8) * 8;
+    hipLaunchKernelGGL(blend_forward_kernel, dim3((unsigned)tiles_padded), dim3(256), 0, stream,
+                       ctx->ranges.as<uint2>(), svals, ctx->rec.as<float4>(), cam, out_rgb, ctx->final_t.as<float>(),
+                       ctx->last.as<uint32_t>(), train ? ctx->ckpt.as<float>() : nullptr);
+    GSX_HIP_TRY(hipGetLastError(), "blend_forward_kernel");
+    GSX_TRY(record(ctx, 6, stream));
+    if (ctx->timing && ctx->cur >= 0) ctx->has_fwd[ctx->cur] = 1;
+    ctx->has_train_state = train != 0;
+    return GSX_HIP_SUCCESS;
+}
+
+gsx_hip_status gsx_hip_render_backward(gsx_hip_render_context* ctx, const float* grad_rgb,
+                                       const gsx_hip_gaussian_grads* grads, hipStream_t stream) {
+    if (ctx == nullptr || grad_rgb == nullptr || grads == nullptr) {
+        return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "context, grad_rgb and grads must be non-null");
+    }
+    if (!ctx->has_train_state) {
+        return fail(GSX_HIP_ERROR_INVALID_STATE, "backward requires a retained TRAIN forward on the same context");
+    }
+    const int64_t n = ctx->gaussian_count;
+    const gsx_hip_gaussians& gs = ctx->gs;
+    if (n > 0 && (grads->mean3d == nullptr || grads->rotation == nullptr || grads->logscale == nullptr ||
+                  grads->opacity == nullptr || grads->sh0 == nullptr)) {
+        return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "gradient sinks mean3d..sh0 must be non-null");
+    }
+    if ((gs.sh_degree >= 1 && grads->sh1 == nullptr) || (gs.sh_degree >= 2 && grads->sh2 == nullptr) ||
+        (gs.sh_degree >= 3 && grads->sh3 == nullptr)) {
+        return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "sh gradient sinks must be non-null up to sh_degree");
+    }
+    if ((reinterpret_cast<uintptr_t>(grads->rotation) & 15u) != 0) {
+        return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "rotation gradient must be 16-byte aligned");
+    }
+    GSX_TRY(ctx->grad2d.reserve((size_t)(n > 0 ? n : 1) * 9 * sizeof(float), "grad2d"));
+    const CameraParams& cam = ctx->cam;
+    const int32_t tiles = cam.tiles_x * cam.tiles_y;
+    const uint32_t* svals = ctx->sorted_in_alt ? ctx->vals_alt.as<uint32_t>() : ctx->vals.as<uint32_t>();
+    GSX_TRY(record(ctx, 7, stream));
+    hipLaunchKernelGGL(fill_f32_kernel, dim3(blocks_for(n * 9, 256)), dim3(256), 0, stream, ctx->grad2d.as<float>(),
+                       n * 9, 0.0f);
+    GSX_HIP_TRY(hipGetLastError(), "fill_f32_kernel");
+    GSX_TRY(record(ctx, 8, stream));
+    const int tiles_padded = ((tiles + 7) / 8) * 8;
+    hipLaunchKernelGGL(blend_backward_kernel, dim3((unsigned)tiles_padded), dim3(256), 0, stream,
+                       ctx->ranges.as<uint2>(), svals, ctx->rec.as<float4>(), ctx->cov_coef.as<float4>(),
+                       ctx->ckpt.as<float>(), cam, grad_rgb, ctx->final_t.as<float>(),
+                       ctx->last.as<uint32_t>(), ctx->grad2d.as<float>());
+    GSX_HIP_TRY(hipGetLastError(), "blend_backward_kernel");
+    GSX_TRY(record(ctx, 9, stream));
+    if (n > 0) {
+        hipLaunchKernelGGL(projection_backward_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, n, gs.mean3d,
+                           gs.rotation, gs.logscale, gs.opacity, gs.sh0, gs.sh1, gs.sh2, gs.sh3, (int)gs.sh_degree,
+                           cam, ctx->grad2d.as<float>(), grads->mean3d, grads->rotation, grads->logscale,
+                           grads->opacity, grads->sh0, grads->sh1, grads->sh2, grads->sh3);
+        GSX_HIP_TRY(hipGetLastError(), "projection_backward_kernel");
+    }
+    GSX_TRY(record(ctx, 10, stream));
+    if (ctx->timing && ctx->cur >= 0) ctx->has_bwd[ctx->cur] = 1;
+    ctx->has_train_state = false;
+    return GSX_HIP_SUCCESS;
+}
+
+gsx_hip_status gsx_hip_render_context_get_stats(const gsx_hip_render_context* ctx, gsx_hip_render_stats* out) {
+    if (ctx == nullptr || out == nullptr) return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "context/out must be non-null");
+    out->gaussian_count = ctx->gaussian_count;
+    out->visible_count = -1;
+    out->instance_count = ctx->instance_count;
+    out->tile_count = ctx->tile_count_total;
+    out->sort_passes = ctx->sort_passes;
+    return GSX_HIP_SUCCESS;
+}
+
+gsx_hip_status gsx_hip_render_context_get_buffers(const gsx_hip_render_context* ctx, gsx_hip_render_buffers* out) {
+    if (ctx == nullptr || out == nullptr) return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "context/out must be non-null");
+    out->sorted_keys = ctx->sorted_in_alt ? ctx->keys_alt.as<uint64_t>() : ctx->keys.as<uint64_t>();
+    out->sorted_values = ctx->sorted_in_alt ? ctx->vals_alt.as<uint32_t>() : ctx->vals.as<uint32_t>();
+    out->tile_ranges = ctx->ranges.as<uint32_t>();
+    out->records = ctx->rec.as<float>();
+    out->tile_counts = ctx->tile_count.as<uint32_t>();
+    out->final_transmittance = ctx->final_t.as<float>();
+    out->last_contributor = ctx->last.as<uint32_t>();
+    return GSX_HIP_SUCCESS;
+}
+
+}  // extern "C"

@@ -1,0 +1,322 @@
+// common.hpp - device-side building blocks shared by the gfx950 kernels.
+//
+// All float arithmetic that decides visibility, footprints or blend contributions follows the
+// gsx CPU backend operation by operation (gsx/src/gsx-cpu/render.c:397-1088). The library is
+// compiled with -ffp-contract=off, correctly rounded f32 division/sqrt and no denormal flush, so
+// each expression below rounds exactly as its CPU counterpart does.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "gsx_math.h"
+
+namespace gsx_amd {
+
+constexpr int kWave = 64;
+constexpr int kTile = 16;                    // screen tile edge in pixels
+constexpr int kTilePixels = kTile * kTile;   // one workgroup (4 waves) per tile
+
+// Constants of the CPU renderer: render.c:85-111.
+constexpr float kShC0 = 0.28209479177387814f;
+constexpr float kShC1 = 0.4886025119029199f;
+constexpr float kMinAbsZ = 1.0e-8f;
+constexpr float kMinQuatNormSq = 1.0e-20f;
+constexpr float kCov2dDilation = 0.3f;
+constexpr float kPowerThreshold = -4.5f;
+constexpr float kMinAlpha = 1.0f / 255.0f;
+constexpr float kOpacityLogitCull = -5.537334267018537f;
+constexpr float kMaxFragmentAlpha = 0.999f;
+constexpr float kTransmittanceThreshold = 1.0e-4f;
+
+__device__ __constant__ const float kShC2[5] = {1.0925484305920792f, -1.0925484305920792f, 0.31539156525252005f,
+                                                -1.0925484305920792f, 0.5462742152960396f};
+__device__ __constant__ const float kShC3[7] = {-0.5900435899266435f, 2.890611442640554f, -0.4570457994644658f,
+                                                0.3731763325901154f, -0.4570457994644658f, 1.445305721320277f,
+                                                -0.5900435899266435f};
+
+// Camera block shared by every render kernel (passed by value as a kernel argument).
+struct CameraParams {
+    float w[3][3];      // world-to-camera rotation (render.c:561-581 of the pose quaternion)
+    float t[3];         // world-to-camera translation
+    float centre[3];    // camera centre in world space, -W^T t (render.c:603-609)
+    float fx, fy, cx, cy;
+    float near_plane, far_plane;
+    float bg[3];
+    int32_t width, height;
+    int32_t tiles_x, tiles_y;
+};
+
+struct Mat3 {
+    float m[3][3];
+};
+
+__device__ inline float sigmoid_render(float x) {
+    // render.c:397-407
+    if (x >= 0.0f) {
+        float z = gsx_expf(-x);
+        return 1.0f / (1.0f + z);
+    }
+    float z = gsx_expf(x);
+    return z / (1.0f + z);
+}
+
+__device__ inline bool quat_normalize(float qx, float qy, float qz, float qw, float& nx, float& ny, float& nz,
+                                      float& nw) {
+    // render.c:421-451
+    float norm_sq = qx * qx + qy * qy + qz * qz + qw * qw;
+    if (norm_sq <= kMinQuatNormSq) {
+        nx = 0.0f;
+        ny = 0.0f;
+        nz = 0.0f;
+        nw = 1.0f;
+        return false;
+    }
+    float inv_norm = 1.0f / sqrtf(norm_sq);
+    nx = qx * inv_norm;
+    ny = qy * inv_norm;
+    nz = qz * inv_norm;
+    nw = qw * inv_norm;
+    return true;
+}
+
+__device__ inline Mat3 rotation_from_xyzw(float qx_raw, float qy_raw, float qz_raw, float qw_raw) {
+    // render.c:561-581
+    float qx, qy, qz, qw;
+    (void)quat_normalize(qx_raw, qy_raw, qz_raw, qw_raw, qx, qy, qz, qw);
+    Mat3 r;
+    r.m[0][0] = 1.0f - 2.0f * (qy * qy + qz * qz);
+    r.m[0][1] = 2.0f * (qx * qy - qw * qz);
+    r.m[0][2] = 2.0f * (qx * qz + qw * qy);
+    r.m[1][0] = 2.0f * (qx * qy + qw * qz);
+    r.m[1][1] = 1.0f - 2.0f * (qx * qx + qz * qz);
+    r.m[1][2] = 2.0f * (qy * qz - qw * qx);
+    r.m[2][0] = 2.0f * (qx * qz - qw * qy);
+    r.m[2][1] = 2.0f * (qy * qz + qw * qx);
+    r.m[2][2] = 1.0f - 2.0f * (qx * qx + qy * qy);
+    return r;
+}
+
+// Zero-initialised triple loop product (render.c:543-559): r = ((0 + a0 b0) + a1 b1) + a2 b2.
+__device__ inline Mat3 mat3_mul(const Mat3& a, const Mat3& b) {
+    Mat3 r;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 3; ++k) acc += a.m[i][k] * b.m[k][j];
+            r.m[i][j] = acc;
+        }
+    }
+    return r;
+}
+
+// a * b^T with the same accumulation order as mat3_mul(a, transpose(b)).
+__device__ inline Mat3 mat3_mul_t(const Mat3& a, const Mat3& b) {
+    Mat3 r;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 3; ++k) acc += a.m[i][k] * b.m[j][k];
+            r.m[i][j] = acc;
+        }
+    }
+    return r;
+}
+
+__device__ inline Mat3 camera_rotation(const CameraParams& cam) {
+    Mat3 w;
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+        for (int j = 0; j < 3; ++j) w.m[i][j] = cam.w[i][j];
+    return w;
+}
+
+// Result of the per-Gaussian preprocess: the CPU's gsx_cpu_render_visible record
+// (render.c:19-39) plus the visibility verdict.
+struct Projected {
+    bool visible;
+    int32_t x_min, x_max, y_min, y_max;
+    float mx, my, a, b, c, inv_det, depth, xc, yc, zc;
+    float color[3];
+    float opacity;
+    float dir[3];
+};
+
+// Covariance of a Gaussian: Sigma = (R S)(R S)^T with S = diag(exp(logscale)) (render.c:583-601).
+__device__ inline Mat3 cov3d_from(const float4 q, const float ls[3]) {
+    Mat3 rs = rotation_from_xyzw(q.x, q.y, q.z, q.w);
+    float sx = gsx_expf(ls[0]);
+    float sy = gsx_expf(ls[1]);
+    float sz = gsx_expf(ls[2]);
+#pragma unroll
+    for (int row = 0; row < 3; ++row) {
+        rs.m[row][0] *= sx;
+        rs.m[row][1] *= sy;
+        rs.m[row][2] *= sz;
+    }
+    return mat3_mul_t(rs, rs);
+}
+
+// SH colour with the CPU clamp max(c + 0.5, 0) (render.c:730-828). sh1..sh3 are [N,k,3].
+__device__ inline void eval_sh(int64_t g, int deg, const float d[3], const float* __restrict__ sh0,
+                               const float* __restrict__ sh1, const float* __restrict__ sh2,
+                               const float* __restrict__ sh3, float out[3]) {
+    float r0 = kShC0 * sh0[g * 3 + 0];
+    float r1 = kShC0 * sh0[g * 3 + 1];
+    float r2 = kShC0 * sh0[g * 3 + 2];
+    if (deg >= 1) {
+        const float x = d[0], y = d[1], z = d[2];
+        const float* c1 = sh1 + g * 9;
+        float s0 = -kShC1 * y, s1 = kShC1 * z, s2 = -kShC1 * x;
+        r0 = r0 + c1[0] * s0;
+        r1 = r1 + c1[1] * s0;
+        r2 = r2 + c1[2] * s0;
+        r0 = r0 + c1[3] * s1;
+        r1 = r1 + c1[4] * s1;
+        r2 = r2 + c1[5] * s1;
+        r0 = r0 + c1[6] * s2;
+        r1 = r1 + c1[7] * s2;
+        r2 = r2 + c1[8] * s2;
+        if (deg >= 2) {
+            float xx = x * x, yy = y * y, zz = z * z, xy = x * y, yz = y * z, xz = x * z;
+            float basis[5];
+            basis[0] = kShC2[0] * xy;
+            basis[1] = kShC2[1] * yz;
+            basis[2] = kShC2[2] * (2.0f * zz - xx - yy);
+            basis[3] = kShC2[3] * xz;
+            basis[4] = kShC2[4] * (xx - yy);
+            const float* c2 = sh2 + g * 15;
+#pragma unroll
+            for (int i = 0; i < 5; ++i) {
+                r0 = r0 + c2[i * 3 + 0] * basis[i];
+                r1 = r1 + c2[i * 3 + 1] * basis[i];
+                r2 = r2 + c2[i * 3 + 2] * basis[i];
+            }
+            if (deg >= 3) {
+                float b3[7];
+                b3[0] = kShC3[0] * y * (3.0f * xx - yy);
+                b3[1] = kShC3[1] * xy * z;
+                b3[2] = kShC3[2] * y * (4.0f * zz - xx - yy);
+                b3[3] = kShC3[3] * z * (2.0f * zz - 3.0f * xx - 3.0f * yy);
+                b3[4] = kShC3[4] * x * (4.0f * zz - xx - yy);
+                b3[5] = kShC3[5] * z * (xx - yy);
+                b3[6] = kShC3[6] * x * (xx - 3.0f * yy);
+                const float* c3 = sh3 + g * 21;
+#pragma unroll
+                for (int i = 0; i < 7; ++i) {
+                    r0 = r0 + c3[i * 3 + 0] * b3[i];
+                    r1 = r1 + c3[i * 3 + 1] * b3[i];
+                    r2 = r2 + c3[i * 3 + 2] * b3[i];
+                }
+            }
+        }
+    }
+    out[0] = fmaxf(r0 + 0.5f, 0.0f);
+    out[1] = fmaxf(r1 + 0.5f, 0.0f);
+    out[2] = fmaxf(r2 + 0.5f, 0.0f);
+}
+
+// One Gaussian through the CPU's visibility culls, EWA projection, pixel box and colour
+// (render.c:850-1016 per entry; projection :611-668, box :670-694).
+__device__ inline Projected preprocess_one(int64_t g, const float* __restrict__ mean3d,
+                                           const float* __restrict__ rotation, const float* __restrict__ logscale,
+                                           const float* __restrict__ opacity, const float* __restrict__ sh0,
+                                           const float* __restrict__ sh1, const float* __restrict__ sh2,
+                                           const float* __restrict__ sh3, int sh_degree, const CameraParams& cam,
+                                           bool want_color) {
+    Projected p;
+    p.visible = false;
+    const float raw_op = opacity[g];
+    if (raw_op <= kOpacityLogitCull) return p;
+    const float mx = mean3d[g * 3 + 0], my = mean3d[g * 3 + 1], mz = mean3d[g * 3 + 2];
+    const float4 q = reinterpret_cast<const float4*>(rotation)[g];
+    const float ls[3] = {logscale[g * 3 + 0], logscale[g * 3 + 1], logscale[g * 3 + 2]};
+    const Mat3 cov3d = cov3d_from(q, ls);
+    const Mat3 w = camera_rotation(cam);
+    // mean_cam = W mean + t
+    float xc = w.m[0][0] * mx + w.m[0][1] * my + w.m[0][2] * mz;
+    float yc = w.m[1][0] * mx + w.m[1][1] * my + w.m[1][2] * mz;
+    float zc = w.m[2][0] * mx + w.m[2][1] * my + w.m[2][2] * mz;
+    xc = xc + cam.t[0];
+    yc = yc + cam.t[1];
+    zc = zc + cam.t[2];
+    const Mat3 cov_cam = mat3_mul_t(mat3_mul(w, cov3d), w);
+    if (fabsf(zc) < kMinAbsZ) return p;
+    const float inv_z = 1.0f / zc;
+    const float inv_z2 = inv_z * inv_z;
+    const float j00 = cam.fx * inv_z;
+    const float j02 = -cam.fx * xc * inv_z2;
+    const float j11 = cam.fy * inv_z;
+    const float j12 = -cam.fy * yc * inv_z2;
+    const float jc00 = j00 * cov_cam.m[0][0] + j02 * cov_cam.m[2][0];
+    const float jc01 = j00 * cov_cam.m[0][1] + j02 * cov_cam.m[2][1];
+    const float jc02 = j00 * cov_cam.m[0][2] + j02 * cov_cam.m[2][2];
+    const float jc11 = j11 * cov_cam.m[1][1] + j12 * cov_cam.m[2][1];
+    const float jc12 = j11 * cov_cam.m[1][2] + j12 * cov_cam.m[2][2];
+    p.mx = cam.fx * xc * inv_z + cam.cx;
+    p.my = cam.fy * yc * inv_z + cam.cy;
+    p.a = jc00 * j00 + jc02 * j02 + kCov2dDilation;
+    p.b = jc01 * j11 + jc02 * j12;
+    p.c = jc11 * j11 + jc12 * j12 + kCov2dDilation;
+    p.depth = zc;
+    p.xc = xc;
+    p.yc = yc;
+    p.zc = zc;
+    const float det = p.a * p.c - p.b * p.b;
+    if (p.depth < cam.near_plane || p.depth > cam.far_plane || det <= 0.0f) return p;
+    {
+        const float trace = p.a + p.c;
+        const float det2 = p.a * p.c - p.b * p.b;
+        const float disc = sqrtf(fmaxf(0.0f, trace * trace * 0.25f - det2));
+        const float l1 = trace * 0.5f + disc;
+        const float l2 = trace * 0.5f - disc;
+        const float radius = 3.0f * sqrtf(fmaxf(l1, l2));
+        p.x_min = (int32_t)fmaxf(0.0f, floorf(p.mx - radius));
+        p.x_max = (int32_t)fminf((float)(cam.width - 1), ceilf(p.mx + radius));
+        p.y_min = (int32_t)fmaxf(0.0f, floorf(p.my - radius));
+        p.y_max = (int32_t)fminf((float)(cam.height - 1), ceilf(p.my + radius));
+    }
+    if (p.x_min > p.x_max || p.y_min > p.y_max) return p;
+    p.visible = true;
+    p.inv_det = 1.0f / det;
+    p.opacity = sigmoid_render(raw_op);
+    if (want_color) {
+        // render.c:487-496 normalise(mean - centre)
+        float dx = mx - cam.centre[0], dy = my - cam.centre[1], dz = mz - cam.centre[2];
+        float len = sqrtf(dx * dx + dy * dy + dz * dz);
+        if (len <= 0.0f) {
+            p.dir[0] = 0.0f;
+            p.dir[1] = 0.0f;
+            p.dir[2] = 0.0f;
+        } else {
+            float s = 1.0f / len;
+            p.dir[0] = dx * s;
+            p.dir[1] = dy * s;
+            p.dir[2] = dz * s;
+        }
+        eval_sh(g, sh_degree, p.dir, sh0, sh1, sh2, sh3, p.color);
+    }
+    return p;
+}
+
+// ---- wave64 helpers ------------------------------------------------------------------------
+
+__device__ inline uint64_t lanemask_lt() {
+    const uint32_t lane = __lane_id();
+    return lane == 0 ? 0ull : (~0ull >> (64 - lane));
+}
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+}  // namespace gsx_amd

@@ -1,0 +1,684 @@
+// render.hip - the gfx950 render path: preprocess, tile-key emission, tile ranges, blend
+// forward, blend backward and projection backward.
+//
+// Semantics are those of the gsx CPU backend (gsx/src/gsx-cpu/render.c), which is the parity
+// oracle: per-pixel order is (depth, Gaussian index), each pixel honours the Gaussian's 3-sigma
+// pixel box, the -4.5 power cut, the 1/255 alpha cut and the 1e-4 transmittance cut, and the
+// colour clamp max(c + 0.5, 0). The CUDA design this replaces (fastgs, kernels_forward.cuh /
+// kernels_backward.cuh) differs in all of those, so none of its arithmetic is used here.
+//
+// Data layout in HBM (per Gaussian g, written by preprocess, read by emission and both blends):
+//   rec[3g+0] = {mean2d_x, mean2d_y, inv_a, 2*inv_b}      (conic of the dilated 2D covariance)
+//   rec[3g+1] = {inv_c, opacity, color_r, color_g}
+//   rec[3g+2] = {color_b, x_min | x_max << 16, y_min | y_max << 16, depth}   (ints as f32 bits)
+// 48 B per visible Gaussian, three 16 B loads; culled Gaussians only write tile_count = 0.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "common.hpp"
+
+namespace gsx_amd {
+
+constexpr int kBlendThreads = kTilePixels;  // 256: one pixel per thread, 4 waves per tile
+
+// ---------------------------------------------------------------------------------------------
+// Preprocess: render.c:850-1016 per Gaussian (culls, EWA projection, box, sigmoid, SH colour),
+// plus the tile count of the box and, for TRAIN forwards, visible_counter += 1 (:980-982).
+// ---------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void preprocess_kernel(
+    int64_t n, const float* __restrict__ mean3d, const float* __restrict__ rotation,
+    const float* __restrict__ logscale, const float* __restrict__ opacity, const float* __restrict__ sh0,
+    const float* __restrict__ sh1, const float* __restrict__ sh2, const float* __restrict__ sh3, int sh_degree,
+    CameraParams cam, float4* __restrict__ rec, float4* __restrict__ cov_coef, uint32_t* __restrict__ tile_count,
+    float* __restrict__ visible_counter) {
+    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= n) return;
+    const Projected p =
+        preprocess_one(g, mean3d, rotation, logscale, opacity, sh0, sh1, sh2, sh3, sh_degree, cam, true);
+    if (!p.visible) {
+        tile_count[g] = 0;
+        return;
+    }
+    if (visible_counter != nullptr) visible_counter[g] += 1.0f;
+    const float inv_a = p.c * p.inv_det;
+    const float inv_b = -p.b * p.inv_det;
+    const float inv_c = p.a * p.inv_det;
+    const uint32_t bx = (uint32_t)p.x_min | ((uint32_t)p.x_max << 16);
+    const uint32_t by = (uint32_t)p.y_min | ((uint32_t)p.y_max << 16);
+    rec[3 * g + 0] = make_float4(p.mx, p.my, inv_a, 2.0f * inv_b);
+    rec[3 * g + 1] = make_float4(inv_c, p.opacity, p.color[0], p.color[1]);
+    rec[3 * g + 2] = make_float4(p.color[2], __uint_as_float(bx), __uint_as_float(by), p.depth);
+    if (cov_coef != nullptr) {
+        // d(conic)/d(cov2d) coefficients with the CPU's rounding (render.c:1578-1579, 1647-1655):
+        // the backward applies them per contribution, as the CPU does, because for near-plane
+        // Gaussians with huge footprints the map is close to singular and summing the conic
+        // gradients first would round very differently.
+        const float det = p.a * p.c - p.b * p.b;
+        const float k = 1.0f / (det * det);
+        cov_coef[2 * g + 0] = make_float4(-p.c * p.c * k, p.b * p.c * k, -p.b * p.b * k, -(p.a * p.c + p.b * p.b) * k);
+        cov_coef[2 * g + 1] = make_float4(p.a * p.b * k, -p.a * p.a * k, 0.0f, 0.0f);
+    }
+    const uint32_t tx0 = (uint32_t)p.x_min / kTile, tx1 = (uint32_t)p.x_max / kTile;
+    const uint32_t ty0 = (uint32_t)p.y_min / kTile, ty1 = (uint32_t)p.y_max / kTile;
+    tile_count[g] = (tx1 - tx0 + 1) * (ty1 - ty0 + 1);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Key emission: Gaussian g owns keys[offset[g] .. offset[g+1]); key = tile << 32 | bits(depth),
+// value = g. Offsets come from an exclusive scan in Gaussian order, so equal keys appear in
+// ascending Gaussian order and a stable sort reproduces the CPU (depth, index) order per tile.
+// ---------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void emit_keys_kernel(int64_t n, const float4* __restrict__ rec,
+                                                        const uint32_t* __restrict__ tile_count,
+                                                        const uint32_t* __restrict__ offsets, int32_t tiles_x,
+                                                        uint64_t* __restrict__ keys, uint32_t* __restrict__ values) {
+    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= n) return;
+    if (tile_count[g] == 0) return;
+    const float4 r2 = rec[3 * g + 2];
+    const uint32_t bx = __float_as_uint(r2.y), by = __float_as_uint(r2.z);
+    const uint32_t tx0 = (bx & 0xffffu) / kTile, tx1 = (bx >> 16) / kTile;
+    const uint32_t ty0 = (by & 0xffffu) / kTile, ty1 = (by >> 16) / kTile;
+    const uint64_t depth_bits = (uint64_t)__float_as_uint(r2.w);
+    uint32_t o = offsets[g];
+    for (uint32_t ty = ty0; ty <= ty1; ++ty) {
+        for (uint32_t tx = tx0; tx <= tx1; ++tx) {
+            const uint64_t tile = (uint64_t)ty * (uint64_t)tiles_x + tx;
+            keys[o] = (tile << 32) | depth_bits;
+            values[o] = (uint32_t)g;
+            ++o;
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void fill_u32_kernel(uint32_t* __restrict__ p, int64_t count, uint32_t v) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < count) p[i] = v;
+}
+
+__global__ __launch_bounds__(256) void fill_f32_kernel(float* __restrict__ p, int64_t count, float v) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < count) p[i] = v;
+}
+
+// [start, end) of each tile's run in the sorted keys; tiles without keys keep (0, 0).
+__global__ __launch_bounds__(256) void tile_ranges_kernel(const uint64_t* __restrict__ keys, const uint32_t* count_ptr,
+                                                          uint2* __restrict__ ranges) {
+    const uint32_t count = *count_ptr;
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= count) return;
+    const uint32_t tile = (uint32_t)(keys[i] >> 32);
+    if (i == 0 || (uint32_t)(keys[i - 1] >> 32) != tile) ranges[tile].x = i;
+    if (i == count - 1 || (uint32_t)(keys[i + 1] >> 32) != tile) ranges[tile].y = i + 1;
+}
+
+// Workgroup -> tile mapping: consecutive workgroups are dealt round-robin to the 8 XCDs, so give
+// each XCD a contiguous band of tiles (neighbouring tiles share Gaussians, and each XCD has its
+// own L2).
+__device__ inline int xcd_tile_index(int block, int tiles) {
+    const int per = (tiles + 7) / 8;
+    const int xcd = block & 7;
+    const int local = block >> 3;
+    const int t = xcd * per + local;
+    return t;
+}
+
+__device__ inline bool in_box(int px, int py, uint32_t bx, uint32_t by) {
+    return px >= (int)(bx & 0xffffu) && px <= (int)(bx >> 16) && py >= (int)(by & 0xffffu) && py <= (int)(by >> 16);
+}
+
+// Transmittance checkpoints: the backward needs every contribution's exact T_before (the CPU
+// records it, render.c:1501-1506; recomputing it by division perturbs the last bit, which the
+// near-singular covariance gradient of near-plane Gaussians amplifies without bound). A TRAIN
+// forward therefore stores each pixel's T at the start of every 32-entry bucket of its tile's
+// list. Bucket k of a tile whose list starts at position x lives in slot x/32 + tile + k, which
+// is collision-free and needs at most I/32 + tiles + 1 slots of 256 floats.
+constexpr int kBucket = 32;
+
+__device__ inline size_t checkpoint_slot(uint32_t range_start, int tile, uint32_t position) {
+    return (size_t)(range_start / kBucket) + (size_t)tile + (size_t)((position - range_start) / kBucket);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Blend forward: render.c:1018-1088, per pixel in per-tile (depth, index) order. Records of the
+// tile's Gaussians are staged through LDS in batches of 256; a tile stops early once every pixel
+// has T < 1e-4. Writes out_rgb (CHW, background composed: C + T*bg), final T, the exclusive end
+// of the last contributing position, and (TRAIN) the bucket checkpoints.
+// ---------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(kBlendThreads) void blend_forward_kernel(
+    const uint2* __restrict__ ranges, const uint32_t* __restrict__ values, const float4* __restrict__ rec,
+    CameraParams cam, float* __restrict__ out_rgb, float* __restrict__ out_t, uint32_t* __restrict__ out_last,
+    float* __restrict__ ckpt) {
+    __shared__ float4 s_r0[kBlendThreads];
+    __shared__ float4 s_r1[kBlendThreads];
+    __shared__ float4 s_r2[kBlendThreads];
+    const int tiles = cam.tiles_x * cam.tiles_y;
+    const int tile = xcd_tile_index(blockIdx.x, tiles);
+    if (tile >= tiles) return;
+    const int tx = tile % cam.tiles_x, ty = tile / cam.tiles_x;
+    const int px = tx * kTile + (threadIdx.x & (kTile - 1));
+    const int py = ty * kTile + (threadIdx.x / kTile);
+    const bool inside = px < cam.width && py < cam.height;
+    const uint2 range = ranges[tile];
+    const float fpx = (float)px + 0.5f;
+    const float fpy = (float)py + 0.5f;
+    float t = 1.0f, c0 = 0.0f, c1 = 0.0f, c2 = 0.0f;
+    uint32_t last = range.x;
+    bool done = !inside;
+    for (uint32_t base = range.x; base < range.y; base += kBlendThreads) {
+        if (__syncthreads_count(done ? 1 : 0) == kBlendThreads) break;
+        const uint32_t j = base + threadIdx.x;
+        if (j < range.y) {
+            const uint32_t g = values[j];
+            s_r0[threadIdx.x] = rec[3 * (size_t)g + 0];
+            s_r1[threadIdx.x] = rec[3 * (size_t)g + 1];
+            s_r2[threadIdx.x] = rec[3 * (size_t)g + 2];
+        }
+        __syncthreads();
+        const int count = (int)min((uint32_t)kBlendThreads, range.y - base);
+        if (!done) {
+            for (int k = 0; k < count; ++k) {
+                if (ckpt != nullptr && (k & (kBucket - 1)) == 0) {
+                    ckpt[checkpoint_slot(range.x, tile, base + (uint32_t)k) * kBlendThreads + threadIdx.x] = t;
+                }
+                const float4 r2 = s_r2[k];
+                if (!in_box(px, py, __float_as_uint(r2.y), __float_as_uint(r2.z))) continue;
+                const float4 r0 = s_r0[k];
+                const float4 r1 = s_r1[k];
+                const float dx = fpx - r0.x;
+                const float dy = fpy - r0.y;
+                float power = -0.5f * (r0.z * dx * dx + r0.w * dx * dy + r1.x * dy * dy);
+                if (power > 0.0f) power = 0.0f;
+                if (power < kPowerThreshold) continue;
+                const float alpha = fminf(kMaxFragmentAlpha, r1.y * gsx_expf(power));
+                if (alpha < kMinAlpha) continue;
+                const float w = alpha * t;
+                c0 += w * r1.z;
+                c1 += w * r1.w;
+                c2 += w * r2.x;
+                t = t * (1.0f - alpha);
+                last = base + (uint32_t)k + 1u;
+                if (t < kTransmittanceThreshold) {
+                    done = true;
+                    break;
+                }
+            }
+        }
+        __syncthreads();
+    }
+    if (inside) {
+        const size_t pix = (size_t)py * (size_t)cam.width + (size_t)px;
+        const size_t plane = (size_t)cam.width * (size_t)cam.height;
+        out_rgb[pix] = c0 + t * cam.bg[0];
+        out_rgb[plane + pix] = c1 + t * cam.bg[1];
+        out_rgb[2 * plane + pix] = c2 + t * cam.bg[2];
+        out_t[pix] = t;
+        out_last[pix] = last;
+    }
+}
+
+// Per-Gaussian screen-space gradient accumulator, 9 floats per Gaussian:
+//   dmean2d x, y | dcov2d a, b, c | dcolor r, g, b | dopacity (w.r.t. the sigmoid value)
+constexpr int kGrad2d = 9;
+
+// ---------------------------------------------------------------------------------------------
+// Blend backward: render.c:1559-1666 restated per pixel, back to front, with the CPU's exact
+// T_before: for each 32-entry bucket (last first) the pixel reloads the bucket's checkpointed T,
+// replays the bucket forward (same operations as the forward, so T_before, G and the contribution
+// set are bit-identical to the CPU's) and then walks it backwards accumulating the suffix colour
+// exactly as the CPU does. Per contribution the gradient terms are the CPU's, including the
+// d(conic)/d(cov2d) map applied per contribution; each wave sums its lanes' 9 partials per
+// Gaussian and issues one set of atomics.
+// ---------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
+    const uint2* __restrict__ ranges, const uint32_t* __restrict__ values, const float4* __restrict__ rec,
+    const float4* __restrict__ cov_coef, const float* __restrict__ ckpt, CameraParams cam,
+    const float* __restrict__ grad_rgb, const float* __restrict__ final_t, const uint32_t* __restrict__ last_contrib,
+    float* __restrict__ grad2d) {
+    __shared__ float4 s_r0[kBlendThreads];
+    __shared__ float4 s_r1[kBlendThreads];
+    __shared__ float4 s_r2[kBlendThreads];
+    __shared__ float4 s_k0[kBlendThreads];
+    __shared__ float2 s_k1[kBlendThreads];
+    __shared__ uint32_t s_g[kBlendThreads];
+    __shared__ uint32_t s_max_last;
+    const int tiles = cam.tiles_x * cam.tiles_y;
+    const int tile = xcd_tile_index(blockIdx.x, tiles);
+    if (tile >= tiles) return;
+    const int tx = tile % cam.tiles_x, ty = tile / cam.tiles_x;
+    const int px = tx * kTile + (threadIdx.x & (kTile - 1));
+    const int py = ty * kTile + (threadIdx.x / kTile);
+    const bool inside = px < cam.width && py < cam.height;
+    const uint2 range = ranges[tile];
+    const size_t pix = (size_t)py * (size_t)cam.width + (size_t)px;
+    const size_t plane = (size_t)cam.width * (size_t)cam.height;
+    const float fpx = (float)px + 0.5f;
+    const float fpy = (float)py + 0.5f;
+    float t_final = 0.0f, d0 = 0.0f, d1 = 0.0f, d2 = 0.0f;
+    uint32_t last = range.x;
+    if (inside) {
+        t_final = final_t[pix];
+        last = last_contrib[pix];
+        d0 = grad_rgb[pix];
+        d1 = grad_rgb[plane + pix];
+        d2 = grad_rgb[2 * plane + pix];
+    }
+    // render.c:1552-1557: the suffix starts as T_final * background
+    float s0 = t_final * cam.bg[0], s1 = t_final * cam.bg[1], s2 = t_final * cam.bg[2];
+    if (threadIdx.x == 0) s_max_last = range.x;
+    __syncthreads();
+    atomicMax(&s_max_last, last);
+    __syncthreads();
+    const uint32_t end_all = s_max_last;
+    if (end_all <= range.x) return;  // uniform: no pixel of this tile has a contribution
+    const int lane = threadIdx.x & (kWave - 1);
+    const uint32_t first_batch = range.x + ((end_all - 1u - range.x) / kBlendThreads) * kBlendThreads;
+    for (int64_t bstart = first_batch; bstart >= (int64_t)range.x; bstart -= kBlendThreads) {
+        const int count = (int)min((uint32_t)kBlendThreads, range.y - (uint32_t)bstart);
+        if (threadIdx.x < count) {
+            const uint32_t g = values[bstart + threadIdx.x];
+            s_g[threadIdx.x] = g;
+            s_r0[threadIdx.x] = rec[3 * (size_t)g + 0];
+            s_r1[threadIdx.x] = rec[3 * (size_t)g + 1];
+            s_r2[threadIdx.x] = rec[3 * (size_t)g + 2];
+            s_k0[threadIdx.x] = cov_coef[2 * (size_t)g + 0];
+            const float4 k1 = cov_coef[2 * (size_t)g + 1];
+            s_k1[threadIdx.x] = make_float2(k1.x, k1.y);
+        }
+        __syncthreads();
+        for (int sb = (count - 1) / kBucket; sb >= 0; --sb) {
+            const uint32_t j0 = (uint32_t)bstart + (uint32_t)(sb * kBucket);
+            if (j0 >= end_all) continue;  // uniform
+            const int n_in = min(kBucket, count - sb * kBucket);
+            float tb[kBucket];
+            float gv[kBucket];
+            uint32_t mask = 0u;
+            // forward replay of the bucket from its checkpoint (render.c:1476-1515)
+            if (inside && j0 < last) {
+                float tt = ckpt[checkpoint_slot(range.x, tile, j0) * kBlendThreads + threadIdx.x];
+#pragma unroll
+                for (int i = 0; i < kBucket; ++i) {
+                    tb[i] = tt;
+                    gv[i] = 0.0f;
+                    if (i < n_in && j0 + (uint32_t)i < last) {
+                        const int kk = sb * kBucket + i;
+                        const float4 r2 = s_r2[kk];
+                        if (in_box(px, py, __float_as_uint(r2.y), __float_as_uint(r2.z))) {
+                            const float4 r0 = s_r0[kk];
+                            const float4 r1 = s_r1[kk];
+                            const float dx = fpx - r0.x;
+                            const float dy = fpy - r0.y;
+                            float power = -0.5f * (r0.z * dx * dx + r0.w * dx * dy + r1.x * dy * dy);
+                            if (power > 0.0f) power = 0.0f;
+                            if (power >= kPowerThreshold) {
+                                const float gval = gsx_expf(power);
+                                const float alpha = fminf(kMaxFragmentAlpha, r1.y * gval);
+                                if (alpha >= kMinAlpha) {
+                                    mask |= 1u << i;
+                                    gv[i] = gval;
+                                    tt = tt * (1.0f - alpha);
+                                }
+                            }
+                        }
+                    }
+                }
+            }
+            // back to front over the bucket (render.c:1559-1666 per contribution)
+#pragma unroll
+            for (int i = kBucket - 1; i >= 0; --i) {
+                if (i >= n_in) continue;  // uniform
+                const int kk = sb * kBucket + i;
+                const bool contrib = ((mask >> i) & 1u) != 0u;
+                float g_mx = 0.0f, g_my = 0.0f, g_ca = 0.0f, g_cb = 0.0f, g_cc = 0.0f;
+                float g_c0 = 0.0f, g_c1 = 0.0f, g_c2 = 0.0f, g_op = 0.0f;
+                if (contrib) {
+                    const float4 r0 = s_r0[kk];
+                    const float4 r1 = s_r1[kk];
+                    const float4 r2 = s_r2[kk];
+                    const float dx = fpx - r0.x;
+                    const float dy = fpy - r0.y;
+                    const float gval = gv[i];
+                    const float op = r1.y;
+                    const float alpha = fminf(kMaxFragmentAlpha, op * gval);
+                    const float t_before = tb[i];
+                    const float w = alpha * t_before;
+                    float dalpha = t_before * (r1.z * d0 + r1.w * d1 + r2.x * d2);
+                    g_c0 = w * d0;
+                    g_c1 = w * d1;
+                    g_c2 = w * d2;
+                    if (fabsf(1.0f - alpha) > 1.0e-6f) {
+                        dalpha -= (s0 * d0 + s1 * d1 + s2 * d2) / (1.0f - alpha);
+                    }
+                    float dg = 0.0f;
+                    if (op * gval < kMaxFragmentAlpha) {
+                        dg = dalpha * op;
+                        g_op = dalpha * gval;
+                    }
+                    const float dpow = dg * gval;
+                    const float inv_a = r0.z, inv_b = r0.w * 0.5f, inv_c = r1.x;
+                    g_mx = dpow * (inv_a * dx + inv_b * dy);
+                    g_my = dpow * (inv_b * dx + inv_c * dy);
+                    const float dia = dpow * (-0.5f * dx * dx);
+                    const float dib = dpow * (-dx * dy);
+                    const float dic = dpow * (-0.5f * dy * dy);
+                    const float4 k0 = s_k0[kk];
+                    const float2 k1 = s_k1[kk];
+                    g_ca = dia * k0.x + dib * k0.y + dic * k0.z;
+                    g_cb = dia * (2.0f * k0.y) + dib * k0.w + dic * (2.0f * k1.x);
+                    g_cc = dia * k0.z + dib * k1.x + dic * k1.y;
+                    s0 += w * r1.z;
+                    s1 += w * r1.w;
+                    s2 += w * r2.x;
+                }
+                if (__ballot(contrib) != 0ull) {
+                    g_mx = wave_sum(g_mx);
+                    g_my = wave_sum(g_my);
+                    g_ca = wave_sum(g_ca);
+                    g_cb = wave_sum(g_cb);
+                    g_cc = wave_sum(g_cc);
+                    g_c0 = wave_sum(g_c0);
+                    g_c1 = wave_sum(g_c1);
+                    g_c2 = wave_sum(g_c2);
+                    g_op = wave_sum(g_op);
+                    if (lane == 0) {
+                        float* dst = grad2d + (size_t)s_g[kk] * kGrad2d;
+                        atomicAdd(dst + 0, g_mx);
+                        atomicAdd(dst + 1, g_my);
+                        atomicAdd(dst + 2, g_ca);
+                        atomicAdd(dst + 3, g_cb);
+                        atomicAdd(dst + 4, g_cc);
+                        atomicAdd(dst + 5, g_c0);
+                        atomicAdd(dst + 6, g_c1);
+                        atomicAdd(dst + 7, g_c2);
+                        atomicAdd(dst + 8, g_op);
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    }
+}
+
+__device__ inline void add3(float* p, float x, float y, float z) {
+    p[0] += x;
+    p[1] += y;
+    p[2] += z;
+}
+
+// render.c:714-728
+__device__ inline void add_dir(float ddir[3], const float dcol[3], const float* coeff, float bx, float by, float bz) {
+    const float s = dcol[0] * coeff[0] + dcol[1] * coeff[1] + dcol[2] * coeff[2];
+    ddir[0] += s * bx;
+    ddir[1] += s * by;
+    ddir[2] += s * bz;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Projection backward: render.c:1667-1969 per Gaussian, from the accumulated screen-space
+// gradients. Sinks are overwritten (the CPU zeroes them first, render.c:1537-1550); invisible
+// Gaussians get zeros.
+// ---------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void projection_backward_kernel(
+    int64_t n, const float* __restrict__ mean3d, const float* __restrict__ rotation,
+    const float* __restrict__ logscale, const float* __restrict__ opacity, const float* __restrict__ sh0,
+    const float* __restrict__ sh1, const float* __restrict__ sh2, const float* __restrict__ sh3, int sh_degree,
+    CameraParams cam, const float* __restrict__ grad2d, float* __restrict__ g_mean3d, float* __restrict__ g_rotation,
+    float* __restrict__ g_logscale, float* __restrict__ g_opacity, float* __restrict__ g_sh0,
+    float* __restrict__ g_sh1, float* __restrict__ g_sh2, float* __restrict__ g_sh3) {
+    const int64_t gi = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gi >= n) return;
+    const Projected p =
+        preprocess_one(gi, mean3d, rotation, logscale, opacity, sh0, sh1, sh2, sh3, sh_degree, cam, true);
+    float gm[3] = {0.0f, 0.0f, 0.0f};
+    float gr[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float gl[3] = {0.0f, 0.0f, 0.0f};
+    float gop = 0.0f;
+    float gs0[3] = {0.0f, 0.0f, 0.0f};
+    float gs1[9];
+    float gs2[15];
+    float gs3[21];
+#pragma unroll
+    for (int i = 0; i < 9; ++i) gs1[i] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 15; ++i) gs2[i] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 21; ++i) gs3[i] = 0.0f;
+    if (p.visible) {
+        const float* a2 = grad2d + (size_t)gi * kGrad2d;
+        const float dmx = a2[0], dmy = a2[1];
+        const float dca = a2[2], dcb = a2[3], dcc = a2[4];
+        const float dcx = a2[5], dcy = a2[6], dcz = a2[7];
+        const float dop = a2[8];
+        const Mat3 w = camera_rotation(cam);
+        const float4 q = reinterpret_cast<const float4*>(rotation)[gi];
+        const float ls[3] = {logscale[gi * 3 + 0], logscale[gi * 3 + 1], logscale[gi * 3 + 2]};
+        const Mat3 cov3d = cov3d_from(q, ls);
+        const Mat3 rot = rotation_from_xyzw(q.x, q.y, q.z, q.w);
+        const float sx = gsx_expf(ls[0]), sy = gsx_expf(ls[1]), sz = gsx_expf(ls[2]);
+        const float zc = p.zc, xc = p.xc, yc = p.yc;
+        const float j00 = cam.fx / zc;
+        const float j02 = -cam.fx * xc / (zc * zc);
+        const float j11 = cam.fy / zc;
+        const float j12 = -cam.fy * yc / (zc * zc);
+        // colour: render.c:1667-1828
+        {
+            const float dcol[3] = {dcx * (p.color[0] > 0.0f ? 1.0f : 0.0f), dcy * (p.color[1] > 0.0f ? 1.0f : 0.0f),
+                                   dcz * (p.color[2] > 0.0f ? 1.0f : 0.0f)};
+            float ddir[3] = {0.0f, 0.0f, 0.0f};
+            const float x = p.dir[0], y = p.dir[1], z = p.dir[2];
+            const float xx = x * x, yy = y * y, zz = z * z, xy = x * y, yz = y * z, xz = x * z;
+            gs0[0] = kShC0 * dcol[0];
+            gs0[1] = kShC0 * dcol[1];
+            gs0[2] = kShC0 * dcol[2];
+            if (sh_degree >= 1) {
+                const float* c1 = sh1 + gi * 9;
+                float s;
+                s = -kShC1 * y;
+                add3(gs1 + 0, dcol[0] * s, dcol[1] * s, dcol[2] * s);
+                s = kShC1 * z;
+                add3(gs1 + 3, dcol[0] * s, dcol[1] * s, dcol[2] * s);
+                s = -kShC1 * x;
+                add3(gs1 + 6, dcol[0] * s, dcol[1] * s, dcol[2] * s);
+                add_dir(ddir, dcol, c1 + 0, 0.0f, -kShC1, 0.0f);
+                add_dir(ddir, dcol, c1 + 3, 0.0f, 0.0f, kShC1);
+                add_dir(ddir, dcol, c1 + 6, -kShC1, 0.0f, 0.0f);
+            }
+            if (sh_degree >= 2) {
+                const float* c2 = sh2 + gi * 15;
+                float s;
+                s = kShC2[0] * xy;
+                add3(gs2 + 0, dcol[0] * s, dcol[1] * s, dcol[2] * s);
+                add_dir(ddir, dcol, c2 + 0, kShC2[0] * y, kShC2[0] * x, 0.0f);
+                s = kShC2[1] * yz;
+                add3(gs2 + 3, dcol[0] * s, dcol[1] * s, dcol[2] * s);
+                add_dir(ddir, dcol, c2 + 3, 0.0f, kShC2[1] * z, kShC2[1] * y);
+                s = kShC2[2] * (2.0f * zz - xx - yy);
+                add3(gs2 + 6, dcol[0] * s, dcol[1] * s, dcol[2] * s);
+                add_dir(ddir, dcol, c2 + 6, -2.0f * kShC2[2] * x, -2.0f * kShC2[2] * y, 4.0f * kShC2[2] * z);
+                s = kShC2[3] * xz;
+                add3(gs2 + 9, dcol[0] * s, dcol[1] * s, dcol[2] * s);
+                add_dir(ddir, dcol, c2 + 9, kShC2[3] * z, 0.0f, kShC2[3] * x);
+                s = kShC2[4] * (xx - yy);
+                add3(gs2 + 12, dcol[0] * s, dcol[1] * s, dcol[2] * s);
+                add_dir(ddir, dcol, c2 + 12, 2.0f * kShC2[4] * x, -2.0f * kShC2[4] * y, 0.0f);
+            }
+            if (sh_degree >= 3) {
+                const float* c3 = sh3 + gi * 21;
+                float s;
+                s = kShC3[0] * y * (3.0f * xx - yy);
+                add3(gs3 + 0, dcol[0] * s, dcol[1] * s, dcol[2] * s);
+                add_dir(ddir, dcol, c3 + 0, 6.0f * kShC3[0] * x * y, 3.0f * kShC3[0] * (xx - yy), 0.0f);
+                s = kShC3[1] * xy * z;
+                add3(gs3 + 3, dcol[0] * s, dcol[1] * s, dcol[2] * s);
+                add_dir(ddir, dcol, c3 + 3, kShC3[1] * y * z, kShC3[1] * x * z, kShC3[1] * xy);
+                s = kShC3[2] * y * (4.0f * zz - xx - yy);
+                add3(gs3 + 6, dcol[0] * s, dcol[1] * s, dcol[2] * s);
+                add_dir(ddir, dcol, c3 + 6, -2.0f * kShC3[2] * x * y, kShC3[2] * (4.0f * zz - xx - 3.0f * yy),
+                        8.0f * kShC3[2] * y * z);
+                s = kShC3[3] * z * (2.0f * zz - 3.0f * xx - 3.0f * yy);
+                add3(gs3 + 9, dcol[0] * s, dcol[1] * s, dcol[2] * s);
+                add_dir(ddir, dcol, c3 + 9, -6.0f * kShC3[3] * x * z, -6.0f * kShC3[3] * y * z,
+                        kShC3[3] * (6.0f * zz - 3.0f * xx - 3.0f * yy));
+                s = kShC3[4] * x * (4.0f * zz - xx - yy);
+                add3(gs3 + 12, dcol[0] * s, dcol[1] * s, dcol[2] * s);
+                add_dir(ddir, dcol, c3 + 12, kShC3[4] * (4.0f * zz - 3.0f * xx - yy), -2.0f * kShC3[4] * x * y,
+                        8.0f * kShC3[4] * x * z);
+                s = kShC3[5] * z * (xx - yy);
+                add3(gs3 + 15, dcol[0] * s, dcol[1] * s, dcol[2] * s);
+                add_dir(ddir, dcol, c3 + 15, 2.0f * kShC3[5] * x * z, -2.0f * kShC3[5] * y * z, kShC3[5] * (xx - yy));
+                s = kShC3[6] * x * (xx - 3.0f * yy);
+                add3(gs3 + 18, dcol[0] * s, dcol[1] * s, dcol[2] * s);
+                add_dir(ddir, dcol, c3 + 18, 3.0f * kShC3[6] * (xx - yy), -6.0f * kShC3[6] * x * y, 0.0f);
+            }
+            if (sh_degree >= 1) {
+                const float vx = mean3d[gi * 3 + 0] - cam.centre[0];
+                const float vy = mean3d[gi * 3 + 1] - cam.centre[1];
+                const float vz = mean3d[gi * 3 + 2] - cam.centre[2];
+                const float vn = sqrtf(vx * vx + vy * vy + vz * vz);
+                if (vn > 0.0f) {
+                    const float dd = ddir[0] * x + ddir[1] * y + ddir[2] * z;
+                    const float s = 1.0f / vn;
+                    gm[0] += (ddir[0] - x * dd) * s;
+                    gm[1] += (ddir[1] - y * dd) * s;
+                    gm[2] += (ddir[2] - z * dd) * s;
+                }
+            }
+        }
+        // opacity: render.c:1830
+        {
+            const float sg = sigmoid_render(opacity[gi]);
+            gop += dop * (sg * (1.0f - sg));
+        }
+        // mean through the projection: render.c:1832-1845
+        {
+            const float inv_z = 1.0f / zc;
+            const float inv_z2 = inv_z * inv_z;
+            const float dmc0 = dmx * cam.fx * inv_z;
+            const float dmc1 = dmy * cam.fy * inv_z;
+            const float dmc2 = dmx * (-cam.fx * xc * inv_z2) + dmy * (-cam.fy * yc * inv_z2);
+            gm[0] += w.m[0][0] * dmc0 + w.m[1][0] * dmc1 + w.m[2][0] * dmc2;
+            gm[1] += w.m[0][1] * dmc0 + w.m[1][1] * dmc1 + w.m[2][1] * dmc2;
+            gm[2] += w.m[0][2] * dmc0 + w.m[1][2] * dmc1 + w.m[2][2] * dmc2;
+        }
+        // covariance to scale and rotation: render.c:1847-1937
+        {
+            float mm[2][3];
+#pragma unroll
+            for (int col = 0; col < 3; ++col) {
+                mm[0][col] = j00 * w.m[0][col] + j02 * w.m[2][col];
+                mm[1][col] = j11 * w.m[1][col] + j12 * w.m[2][col];
+            }
+            Mat3 dcov3;
+#pragma unroll
+            for (int row = 0; row < 3; ++row)
+#pragma unroll
+                for (int col = 0; col < 3; ++col)
+                    dcov3.m[row][col] = mm[0][row] * (dca * mm[0][col] + 0.5f * dcb * mm[1][col]) +
+                                        mm[1][row] * (0.5f * dcb * mm[0][col] + dcc * mm[1][col]);
+            Mat3 srot = rot;
+#pragma unroll
+            for (int row = 0; row < 3; ++row) {
+                srot.m[row][0] *= sx;
+                srot.m[row][1] *= sy;
+                srot.m[row][2] *= sz;
+            }
+            Mat3 dsum;
+#pragma unroll
+            for (int row = 0; row < 3; ++row)
+#pragma unroll
+                for (int col = 0; col < 3; ++col) dsum.m[row][col] = dcov3.m[row][col] + dcov3.m[col][row];
+            const Mat3 drs = mat3_mul(dsum, srot);
+            gl[0] = (drs.m[0][0] * rot.m[0][0] + drs.m[1][0] * rot.m[1][0] + drs.m[2][0] * rot.m[2][0]) * sx;
+            gl[1] = (drs.m[0][1] * rot.m[0][1] + drs.m[1][1] * rot.m[1][1] + drs.m[2][1] * rot.m[2][1]) * sy;
+            gl[2] = (drs.m[0][2] * rot.m[0][2] + drs.m[1][2] * rot.m[1][2] + drs.m[2][2] * rot.m[2][2]) * sz;
+            Mat3 dr;
+#pragma unroll
+            for (int row = 0; row < 3; ++row) {
+                dr.m[row][0] = drs.m[row][0] * sx;
+                dr.m[row][1] = drs.m[row][1] * sy;
+                dr.m[row][2] = drs.m[row][2] * sz;
+            }
+            float nx, ny, nz, nw;
+            if (quat_normalize(q.x, q.y, q.z, q.w, nx, ny, nz, nw)) {
+                const float inv_norm = 1.0f / sqrtf(q.x * q.x + q.y * q.y + q.z * q.z + q.w * q.w);
+                float dqw = 0.0f, dqx = 0.0f, dqy = 0.0f, dqz = 0.0f;
+                dqw += dr.m[0][1] * (-2.0f * nz);
+                dqw += dr.m[0][2] * (2.0f * ny);
+                dqw += dr.m[1][0] * (2.0f * nz);
+                dqw += dr.m[1][2] * (-2.0f * nx);
+                dqw += dr.m[2][0] * (-2.0f * ny);
+                dqw += dr.m[2][1] * (2.0f * nx);
+                dqx += dr.m[0][1] * (2.0f * ny);
+                dqx += dr.m[0][2] * (2.0f * nz);
+                dqx += dr.m[1][0] * (2.0f * ny);
+                dqx += dr.m[1][1] * (-4.0f * nx);
+                dqx += dr.m[1][2] * (-2.0f * nw);
+                dqx += dr.m[2][0] * (2.0f * nz);
+                dqx += dr.m[2][1] * (2.0f * nw);
+                dqx += dr.m[2][2] * (-4.0f * nx);
+                dqy += dr.m[0][0] * (-4.0f * ny);
+                dqy += dr.m[0][1] * (2.0f * nx);
+                dqy += dr.m[0][2] * (2.0f * nw);
+                dqy += dr.m[1][0] * (2.0f * nx);
+                dqy += dr.m[1][2] * (2.0f * nz);
+                dqy += dr.m[2][0] * (-2.0f * nw);
+                dqy += dr.m[2][1] * (2.0f * nz);
+                dqy += dr.m[2][2] * (-4.0f * ny);
+                dqz += dr.m[0][0] * (-4.0f * nz);
+                dqz += dr.m[0][1] * (-2.0f * nw);
+                dqz += dr.m[0][2] * (2.0f * nx);
+                dqz += dr.m[1][0] * (2.0f * nw);
+                dqz += dr.m[1][1] * (-4.0f * nz);
+                dqz += dr.m[1][2] * (2.0f * ny);
+                dqz += dr.m[2][0] * (2.0f * nx);
+                dqz += dr.m[2][1] * (2.0f * ny);
+                const float dot = nx * dqx + ny * dqy + nz * dqz + nw * dqw;
+                gr[0] = (dqx - nx * dot) * inv_norm;
+                gr[1] = (dqy - ny * dot) * inv_norm;
+                gr[2] = (dqz - nz * dot) * inv_norm;
+                gr[3] = (dqw - nw * dot) * inv_norm;
+            }
+        }
+        // Jacobian's dependence on the camera-space mean: render.c:1939-1969
+        {
+            const Mat3 cov_cam = mat3_mul_t(mat3_mul(w, cov3d), w);
+            const float inv_z = 1.0f / zc;
+            const float inv_z2 = inv_z * inv_z;
+            const float inv_z3 = inv_z2 * inv_z;
+            float dj[2][3];
+#pragma unroll
+            for (int col = 0; col < 3; ++col) {
+                dj[0][col] = 2.0f * dca * (j00 * cov_cam.m[0][col] + j02 * cov_cam.m[2][col]) +
+                             dcb * (j11 * cov_cam.m[1][col] + j12 * cov_cam.m[2][col]);
+                dj[1][col] = dcb * (j00 * cov_cam.m[0][col] + j02 * cov_cam.m[2][col]) +
+                             2.0f * dcc * (j11 * cov_cam.m[1][col] + j12 * cov_cam.m[2][col]);
+            }
+            const float m0 = dj[0][2] * (-cam.fx * inv_z2);
+            const float m1 = dj[1][2] * (-cam.fy * inv_z2);
+            const float m2 = dj[0][0] * (-cam.fx * inv_z2) + dj[0][2] * (2.0f * cam.fx * xc * inv_z3) +
+                             dj[1][1] * (-cam.fy * inv_z2) + dj[1][2] * (2.0f * cam.fy * yc * inv_z3);
+            gm[0] += w.m[0][0] * m0 + w.m[1][0] * m1 + w.m[2][0] * m2;
+            gm[1] += w.m[0][1] * m0 + w.m[1][1] * m1 + w.m[2][1] * m2;
+            gm[2] += w.m[0][2] * m0 + w.m[1][2] * m1 + w.m[2][2] * m2;
+        }
+    }
+    g_mean3d[gi * 3 + 0] = gm[0];
+    g_mean3d[gi * 3 + 1] = gm[1];
+    g_mean3d[gi * 3 + 2] = gm[2];
+    reinterpret_cast<float4*>(g_rotation)[gi] = make_float4(gr[0], gr[1], gr[2], gr[3]);
+    g_logscale[gi * 3 + 0] = gl[0];
+    g_logscale[gi * 3 + 1] = gl[1];
+    g_logscale[gi * 3 + 2] = gl[2];
+    g_opacity[gi] = gop;
+    g_sh0[gi * 3 + 0] = gs0[0];
+    g_sh0[gi * 3 + 1] = gs0[1];
+    g_sh0[gi * 3 + 2] = gs0[2];
+    if (sh_degree >= 1 && g_sh1 != nullptr)
+        for (int i = 0; i < 9; ++i) g_sh1[gi * 9 + i] = gs1[i];
+    if (sh_degree >= 2 && g_sh2 != nullptr)
+        for (int i = 0; i < 15; ++i) g_sh2[gi * 15 + i] = gs2[i];
+    if (sh_degree >= 3 && g_sh3 != nullptr)
+        for (int i = 0; i < 21; ++i) g_sh3[gi * 21 + i] = gs3[i];
+}
+
+}  // namespace gsx_amd

@@ -1,0 +1,225 @@
+/*
+ * gsx_hip.h - C ABI of the gfx950 (MI355X) backend library libgsx_hip.so.
+ *
+ * This is the layer the gsx backend vtables call (gsx/src/gsx-impl.h:229-533 for the vtables,
+ * gsx/src/gsx-cuda/internal.h:274-675 for the launcher layer it replaces): plain device
+ * pointers, sizes and a hipStream_t, C linkage, no C++ or framework types. All device work is
+ * enqueued on the given stream in order; nothing here synchronises the host except where a
+ * function says so. Every call returns 0 on success, a hipError_t value (> 0) for a HIP
+ * runtime error, or a negative GSX_HIP_ERROR_* code; gsx_hip_last_error_message() names the
+ * failing condition (thread-local, static storage).
+ *
+ * Conventions shared with gsx (gsx/include/gsx/gsx-render.h:64-140, gsx-base.h:207-216):
+ *   Gaussians: mean3d [N,3], rotation [N,4] (xyzw), logscale [N,3], opacity [N] (logit),
+ *   sh0 [N,3], sh1 [N,3,3], sh2 [N,5,3], sh3 [N,7,3], all float32 row-major on the device;
+ *   images: float32 CHW [3,H,W]; camera: pinhole, world-to-camera pose, +z forward, y down.
+ */
+#ifndef GSX_HIP_H
+#define GSX_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#ifndef HIP_INCLUDE_HIP_HIP_RUNTIME_API_H
+typedef struct ihipStream_t* hipStream_t;
+#endif
+
+typedef int gsx_hip_status;
+
+enum {
+    GSX_HIP_SUCCESS = 0,
+    GSX_HIP_ERROR_INVALID_ARGUMENT = -1, /* gsx GSX_ERROR_INVALID_ARGUMENT */
+    GSX_HIP_ERROR_INVALID_STATE = -2,    /* gsx GSX_ERROR_INVALID_STATE (e.g. backward w/o TRAIN forward) */
+    GSX_HIP_ERROR_OUT_OF_RANGE = -3,     /* gsx GSX_ERROR_OUT_OF_RANGE (sizes, gather indices) */
+    GSX_HIP_ERROR_OUT_OF_MEMORY = -4,    /* gsx GSX_ERROR_OUT_OF_MEMORY */
+    GSX_HIP_ERROR_NOT_SUPPORTED = -5     /* gsx GSX_ERROR_NOT_SUPPORTED */
+};
+
+/* Human-readable reason for the last non-zero status returned on this thread. */
+const char* gsx_hip_last_error_message(void);
+
+/* ---- device plumbing (replaces the cudaMalloc/cudaMemcpy use of gsx-cuda/buffer.c) -------- */
+gsx_hip_status gsx_hip_device_count(int32_t* out_count);
+gsx_hip_status gsx_hip_device_name(int32_t device, char* out_name, size_t capacity);
+gsx_hip_status gsx_hip_malloc(void** out_ptr, size_t bytes);
+gsx_hip_status gsx_hip_free(void* ptr);
+gsx_hip_status gsx_hip_memcpy_htod(void* dst, const void* src, size_t bytes);
+gsx_hip_status gsx_hip_memcpy_dtoh(void* dst, const void* src, size_t bytes);
+gsx_hip_status gsx_hip_memcpy_dtod_async(void* dst, const void* src, size_t bytes, hipStream_t stream);
+gsx_hip_status gsx_hip_stream_create(hipStream_t* out_stream);
+gsx_hip_status gsx_hip_stream_destroy(hipStream_t stream);
+gsx_hip_status gsx_hip_stream_synchronize(hipStream_t stream);
+/* Fill `count` floats with `value` (a kernel, not hipMemset, so it is safe under graph capture). */
+gsx_hip_status gsx_hip_fill_f32(float* dst, int64_t count, float value, hipStream_t stream);
+
+/* ---- render ---------------------------------------------------------------------------------
+ * Replaces gsx_cuda_fastgs_forward_launch / gsx_cuda_fastgs_backward_launch
+ * (gsx/src/gsx-cuda/internal.h:534-628) and the renderer vtable behaviour of the CPU oracle
+ * (gsx/src/gsx-cpu/render.c:1254-1975). The render context owns every intermediate buffer
+ * (pooled, grow-only; the fastgs resize callbacks and per-forward allocations are gone) and
+ * the state a TRAIN forward retains for the backward.
+ */
+typedef struct gsx_hip_camera {
+    float fx, fy, cx, cy;   /* gsx_camera_intrinsics (gsx-base.h:183-197) */
+    int32_t width, height;
+    float rot[4];           /* gsx_camera_pose.rot, world-to-camera quaternion, xyzw */
+    float transl[3];        /* gsx_camera_pose.transl */
+    float near_plane, far_plane;
+    float background[3];
+} gsx_hip_camera;
+
+typedef struct gsx_hip_gaussians {
+    int64_t count;
+    int32_t sh_degree;      /* 0..3; sh1..sh3 required up to this degree, ignored above */
+    const float* mean3d;
+    const float* rotation;
+    const float* logscale;
+    const float* opacity;
+    const float* sh0;
+    const float* sh1;
+    const float* sh2;
+    const float* sh3;
+} gsx_hip_gaussians;
+
+typedef struct gsx_hip_gaussian_grads {
+    float* mean3d;          /* sinks are overwritten, as gsx-cpu/render.c:1537-1550 */
+    float* rotation;
+    float* logscale;
+    float* opacity;
+    float* sh0;
+    float* sh1;
+    float* sh2;
+    float* sh3;
+} gsx_hip_gaussian_grads;
+
+typedef struct gsx_hip_render_context gsx_hip_render_context;
+
+typedef struct gsx_hip_render_stats {
+    int64_t gaussian_count;
+    int64_t visible_count;   /* Gaussians with at least one tile (-1 until computed) */
+    int64_t instance_count;  /* (tile, Gaussian) pairs sorted */
+    int32_t tile_count;
+    int32_t sort_passes;
+} gsx_hip_render_stats;
+
+/* Device pointers of the intermediates a forward retains (valid until the next forward). */
+typedef struct gsx_hip_render_buffers {
+    const uint64_t* sorted_keys;   /* [instance_count] (tile << 32) | float_bits(depth) */
+    const uint32_t* sorted_values; /* [instance_count] Gaussian index */
+    const uint32_t* tile_ranges;   /* [tile_count][2] start, end */
+    const float* records;          /* [N][12] packed per-Gaussian blend records */
+    const uint32_t* tile_counts;   /* [N] tiles touched per Gaussian (0 = culled) */
+    const float* final_transmittance; /* [H*W] */
+    const uint32_t* last_contributor; /* [H*W] exclusive end of the last contributing position */
+} gsx_hip_render_buffers;
+
+gsx_hip_status gsx_hip_render_context_create(gsx_hip_render_context** out_context);
+gsx_hip_status gsx_hip_render_context_destroy(gsx_hip_render_context* context);
+
+/* Forward render into out_rgb [3,H,W]. train != 0 retains the state for one backward and, if
+ * visible_counter is non-null, adds 1 to it for every visible Gaussian (gsx-cpu/render.c:
+ * 980-982). The Gaussian arrays are borrowed: the backward reads them again, so they must be
+ * unchanged until then (gsx borrow_train_state = true). One host synchronisation per forward
+ * reads the instance count. */
+gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* context, const gsx_hip_camera* camera,
+                                      const gsx_hip_gaussians* gaussians, int32_t train, float* out_rgb,
+                                      float* visible_counter, hipStream_t stream);
+
+/* Backward of the retained TRAIN forward; consumes the state (a second call fails with
+ * GSX_HIP_ERROR_INVALID_STATE, as gsx-cpu/render.c:1406-1408, 1973). */
+gsx_hip_status gsx_hip_render_backward(gsx_hip_render_context* context, const float* grad_rgb,
+                                       const gsx_hip_gaussian_grads* grads, hipStream_t stream);
+
+gsx_hip_status gsx_hip_render_context_get_stats(const gsx_hip_render_context* context,
+                                                gsx_hip_render_stats* out_stats);
+gsx_hip_status gsx_hip_render_context_get_buffers(const gsx_hip_render_context* context,
+                                                  gsx_hip_render_buffers* out_buffers);
+
+/* Per-stage device timing: set_timing(capacity > 0) allocates a ring of `capacity` HIP event
+ * sets; each forward (and the following backward) records one set on its launch stream, so a
+ * timed loop pays no synchronisation. get_timings synchronises on the recorded events and writes
+ * the per-stage average over the recorded sets, in milliseconds, in this order: preprocess,
+ * scan (including the instance-count readback), emit, sort, ranges, blend_forward, grad_zero,
+ * blend_backward, projection_backward. set_timing(0) disables timing. */
+enum { GSX_HIP_RENDER_STAGE_COUNT = 9 };
+gsx_hip_status gsx_hip_render_context_set_timing(gsx_hip_render_context* context, int32_t capacity);
+gsx_hip_status gsx_hip_render_context_get_timings(gsx_hip_render_context* context, float* out_ms, int32_t capacity,
+                                                  int32_t* out_written);
+
+/* ---- sort / scan ------------------------------------------------------------------------------
+ * Replace cub::DeviceScan::ExclusiveSum (fastgs/forward.cu:180-185) and
+ * cub::DeviceRadixSort::SortPairs (fastgs/forward.cu:155-161, 214-220). */
+size_t gsx_hip_scan_temp_bytes(int64_t n);
+gsx_hip_status gsx_hip_scan_exclusive_u32(const uint32_t* in, uint32_t* out, int64_t n, void* temp,
+                                          hipStream_t stream);
+size_t gsx_hip_radix_sort_temp_bytes(int64_t n);
+gsx_hip_status gsx_hip_radix_sort_pairs_u64(uint64_t* keys, uint32_t* values, uint64_t* keys_alt,
+                                            uint32_t* values_alt, int64_t n, int begin_bit, int end_bit, void* temp,
+                                            int* out_result_in_alt, hipStream_t stream);
+
+/* ---- losses -----------------------------------------------------------------------------------
+ * Replace gsx_cuda_loss_*_kernel_launch (gsx/src/gsx-cuda/internal.h:314-371); semantics of
+ * gsx/src/gsx-cpu/loss.c:316-709 (accumulate into loss_map / grad_prediction; grad_scale is
+ * already normalised as gsx_loss_scale_grad, gsx-tensor-helpers.h:236-244). */
+gsx_hip_status gsx_hip_loss_l1_f32_forward_kernel_launch(float* loss_map, const float* prediction,
+                                                         const float* target, int64_t total_elements, float scale,
+                                                         hipStream_t stream);
+gsx_hip_status gsx_hip_loss_l1_f32_backward_kernel_launch(float* grad_prediction, const float* prediction,
+                                                          const float* target, int64_t total_elements,
+                                                          float grad_scale, hipStream_t stream);
+gsx_hip_status gsx_hip_loss_mse_f32_forward_kernel_launch(float* loss_map, const float* prediction,
+                                                          const float* target, int64_t total_elements, float scale,
+                                                          hipStream_t stream);
+gsx_hip_status gsx_hip_loss_mse_f32_backward_kernel_launch(float* grad_prediction, const float* prediction,
+                                                           const float* target, int64_t total_elements,
+                                                           float grad_scale, hipStream_t stream);
+/* SSIM on [outer, channels, H, W] CHW images; ssim_workspace = 3 * outer*channels*H*W floats
+ * written by the forward and read by the backward. fuse_l1 != 0 also applies an L1 term of
+ * l1_scale (forward) / l1_grad_scale (backward) first, bit-identical to calling the L1
+ * launcher before. */
+gsx_hip_status gsx_hip_loss_ssim_chw_f32_forward_kernel_launch(float* loss_map, const float* prediction,
+                                                               const float* target, int64_t outer_count,
+                                                               int32_t channels, int32_t height, int32_t width,
+                                                               float scale, float* ssim_workspace, float l1_scale,
+                                                               int fuse_l1, hipStream_t stream);
+gsx_hip_status gsx_hip_loss_ssim_chw_f32_backward_kernel_launch(float* grad_prediction, const float* prediction,
+                                                                const float* target, int64_t outer_count,
+                                                                int32_t channels, int32_t height, int32_t width,
+                                                                float grad_scale, const float* ssim_workspace,
+                                                                float l1_grad_scale, int fuse_l1,
+                                                                hipStream_t stream);
+
+/* ---- optimizer --------------------------------------------------------------------------------
+ * Adam, element arithmetic of gsx/src/gsx-cpu/optim.c:712-780; bias corrections
+ * 1 - beta^step are computed by the caller in float64 (as the CPU does with pow). */
+#define GSX_HIP_ADAM_MAX_GROUPS 16
+typedef struct gsx_hip_adam_group {
+    float* parameter;
+    const float* gradient;
+    float* first_moment;
+    float* second_moment;
+    int64_t count;
+    float beta1, beta2, learning_rate, weight_decay, epsilon, max_grad;
+    double bias_correction1, bias_correction2;
+} gsx_hip_adam_group;
+
+/* Replaces gsx_cuda_adam_step_f32_kernel_launch (gsx/src/gsx-cuda/internal.h:296-311). */
+gsx_hip_status gsx_hip_adam_step_f32_kernel_launch(float* parameter, const float* gradient, float* first_moment,
+                                                   float* second_moment, int64_t total_elements, float beta1,
+                                                   float beta2, float learning_rate, float weight_decay,
+                                                   float epsilon, float max_grad, double bias_correction1,
+                                                   double bias_correction2, hipStream_t stream);
+/* All groups of one optimizer step in a single launch (the CUDA backend issues one launch
+ * per group, gsx/src/gsx-cuda/optim.c:757-796). */
+gsx_hip_status gsx_hip_adam_step_multi_launch(const gsx_hip_adam_group* groups, int32_t group_count,
+                                              hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GSX_HIP_H */

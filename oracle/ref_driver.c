@@ -118,14 +118,14 @@ typedef struct ref_scene {
     gsx_tensor_t mean3d, rotation, logscale, opacity, sh0, sh1, sh2, sh3;
 } ref_scene;
 
-static gsx_error scene_upload(ref_scene *s, int n, int sh_degree, const float *mean3d, const float *rotation,
+static gsx_error scene_upload(ref_scene *s, int n, gsx_size_t extra_bytes, int sh_degree, const float *mean3d, const float *rotation,
     const float *logscale, const float *opacity, const float *sh0, const float *sh1, const float *sh2, const float *sh3)
 {
     gsx_arena_desc adesc = { 0 };
     gsx_error e;
 
     memset(s, 0, sizeof(*s));
-    adesc.initial_capacity_bytes = (gsx_size_t)n * 256u + 4096u;
+    adesc.initial_capacity_bytes = (gsx_size_t)n * 512u + extra_bytes + 65536u;
     e = gsx_arena_init(&s->arena, g_device_type, &adesc);
     if(!gsx_error_is_success(e)) return e;
     e = make_tensor(s->arena, &s->mean3d, 2, n, 3, 0, mean3d);
@@ -196,7 +196,7 @@ int gsxref_render(int n, int sh_degree, const float *mean3d, const float *rotati
     rc = ensure_backend();
     if(rc != 0) return rc;
     unpack_camera(camera, &intr, &pose, &near_plane, &far_plane, &bg);
-    TRY(scene_upload(&s, n, sh_degree, mean3d, rotation, logscale, opacity, sh0, sh1, sh2, sh3));
+    TRY(scene_upload(&s, n, (gsx_size_t)intr.width * (gsx_size_t)intr.height * 64u, sh_degree, mean3d, rotation, logscale, opacity, sh0, sh1, sh2, sh3));
     TRY(make_tensor(s.arena, &out, 3, 3, intr.height, intr.width, NULL));
     if(visible_counter != NULL) {
         TRY(make_tensor(s.arena, &counter, 1, n, 0, 0, visible_counter));
@@ -268,7 +268,7 @@ int gsxref_render_grad(int n, int sh_degree, const float *mean3d, const float *r
     if(rc != 0) return rc;
     unpack_camera(camera, &intr, &pose, &near_plane, &far_plane, &bg);
     img_bytes = (gsx_size_t)3 * intr.height * intr.width * sizeof(float);
-    TRY(scene_upload(&s, n, sh_degree, mean3d, rotation, logscale, opacity, sh0, sh1, sh2, sh3));
+    TRY(scene_upload(&s, n, (gsx_size_t)intr.width * (gsx_size_t)intr.height * 64u, sh_degree, mean3d, rotation, logscale, opacity, sh0, sh1, sh2, sh3));
     TRY(make_tensor(s.arena, &out, 3, 3, intr.height, intr.width, NULL));
     TRY(make_tensor(s.arena, &gout, 3, 3, intr.height, intr.width, grad_rgb));
     TRY(make_tensor(s.arena, &gm, 2, n, 3, 0, NULL));
@@ -480,6 +480,7 @@ int gsxref_adc(int n, const float *mean3d, const float *rotation, const float *l
     gsx_optim_desc odesc = { 0 };
     gsx_optim_param_group_desc groups[5];
     gsx_gs_info info = { 0 };
+    gsx_renderer_t adc_renderer = NULL;
     const gsx_gs_field fields[5] = { GSX_GS_FIELD_MEAN3D, GSX_GS_FIELD_LOGSCALE, GSX_GS_FIELD_ROTATION,
         GSX_GS_FIELD_OPACITY, GSX_GS_FIELD_SH0 };
     const gsx_gs_field grad_fields[5] = { GSX_GS_FIELD_GRAD_MEAN3D, GSX_GS_FIELD_GRAD_LOGSCALE,
@@ -544,6 +545,18 @@ int gsxref_adc(int n, const float *mean3d, const float *rotation, const float *l
     TRY(gsx_adc_init(&adc, g_backend, &adesc));
     areq.gs = gs;
     areq.optim = optim;
+    /* default/ABSGS never use the dataloader; the reference's own ADC tests pass a placeholder
+     * the same way (tests/adc_runtime.cpp:457). The renderer must belong to the backend. */
+    {
+        gsx_renderer_desc rdesc = { 0 };
+
+        rdesc.width = 1;
+        rdesc.height = 1;
+        rdesc.output_data_type = GSX_DATA_TYPE_F32;
+        TRY(gsx_renderer_init(&adc_renderer, g_backend, &rdesc));
+    }
+    areq.dataloader = (gsx_dataloader_t)0x1;
+    areq.renderer = adc_renderer;
     areq.global_step = (gsx_size_t)iparams[6];
     areq.scene_scale = params[7];
     TRY(gsx_adc_step(adc, &areq, &ares));
@@ -569,6 +582,7 @@ int gsxref_adc(int n, const float *mean3d, const float *rotation, const float *l
     TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_SH0, &t));
     TRY(gsx_tensor_download(t, o_sh0, info.count * 3u * sizeof(float)));
 done:
+    if(adc_renderer != NULL) (void)gsx_renderer_free(adc_renderer);
     if(adc != NULL) (void)gsx_adc_free(adc);
     if(optim != NULL) (void)gsx_optim_free(optim);
     if(gs != NULL) (void)gsx_gs_free(gs);

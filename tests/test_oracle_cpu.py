@@ -1,0 +1,265 @@
+"""CPU checks of the oracle restatement, the reference build and the host-side pieces.
+
+These pin the checker itself, so the GPU parity tests mean something:
+  - the restatement is bit-identical to the unmodified reference CPU backend compiled from its
+    own sources (oracle/_ref), on seeded scenes, for render forward/backward, losses, Adam, ADC;
+  - the reference's own known answer (tests/render_runtime.cpp:671-722) and closed forms;
+  - the glibc-exact expf restatement used by the kernels against the host libm;
+  - the scene generator's pcg32 stream against gsx's own pcg32 (exported by the reference lib).
+"""
+import ctypes
+import math
+
+import numpy as np
+import pytest
+
+from gsx_amd import scenes
+from oracle.oracle import AdcParams
+
+
+def _closed_form_scene():
+    sc = scenes.Scene(np.array([[0, 0, 4]], np.float32), np.array([[0, 0, 0, 1]], np.float32),
+                      np.zeros((1, 3), np.float32), np.zeros(1, np.float32), np.array([[1, 0, 0]], np.float32))
+    cam = np.array([1, 1, 0.5, 0.5, 1, 1, 0, 0, 0, 1, 0, 0, 0, 0.1, 10, 0, 0, 0], np.float32)
+    return sc, cam
+
+
+def test_closed_form_render(oracle):
+    # tests/render_runtime.cpp:671-722: 1x1 image, f=1, c=0.5, identity pose -> (0.3910474, 0.25, 0.25)
+    sc, cam = _closed_form_scene()
+    out, t = oracle.render(sc, cam)
+    assert abs(out[0, 0, 0] - 0.3910474) <= 1e-5
+    assert abs(out[1, 0, 0] - 0.25) <= 1e-5 and abs(out[2, 0, 0] - 0.25) <= 1e-5
+    # the same number from first principles: alpha = 0.999-clamped sigmoid(0) * exp(0) = 0.5,
+    # colour = SH_C0 * sh0 + 0.5
+    sh_c0 = 0.28209479177387814
+    assert abs(out[0, 0, 0] - 0.5 * (sh_c0 + 0.5)) <= 1e-6
+    assert abs(t[0, 0] - 0.5) <= 1e-7
+
+
+def test_background_only_transmittance(oracle):
+    sc = scenes.cube_scene(0, 10)
+    sc.opacity[:] = -20.0  # every Gaussian culled by the opacity logit cut
+    cam = scenes.camera(32, 24, 20.0, background=(0.1, 0.2, 0.3))
+    out, t = oracle.render(sc, cam)
+    assert np.all(t == 1.0)
+    assert np.allclose(out[0], 0.1) and np.allclose(out[1], 0.2) and np.allclose(out[2], 0.3)
+
+
+@pytest.mark.parametrize("deg", [0, 1, 3])
+def test_restatement_matches_reference_render(oracle, reference, deg):
+    w = scenes.config1(n=6000, width=96, height=72)
+    sc = w.scene
+    if deg > 0:
+        rng = np.random.default_rng(deg)
+        sc.sh_degree = deg
+        sc.sh1 = (0.2 * rng.standard_normal((sc.count, 3, 3))).astype(np.float32)
+        sc.sh2 = (0.2 * rng.standard_normal((sc.count, 5, 3))).astype(np.float32) if deg >= 2 else None
+        sc.sh3 = (0.2 * rng.standard_normal((sc.count, 7, 3))).astype(np.float32) if deg >= 3 else None
+    cam = w.camera.copy()
+    cam[15:18] = (0.2, 0.1, 0.05)
+    got, _ = oracle.render(sc, cam)
+    ref = reference.render(sc, cam)
+    assert np.array_equal(got, ref)
+    counter_a = np.zeros(sc.count, np.float32)
+    counter_b = np.zeros(sc.count, np.float32)
+    oracle.render(sc, cam, visible_counter=counter_a)
+    reference.render(sc, cam, train=True, visible_counter=counter_b)
+    assert np.array_equal(counter_a, counter_b)
+    grad_rgb = np.random.default_rng(11).standard_normal(got.shape).astype(np.float32)
+    g_o = oracle.render_backward(sc, cam, grad_rgb)
+    _, g_r = reference.render_grad(sc, cam, grad_rgb)
+    for k in g_r:
+        assert np.array_equal(g_o[k], g_r[k]), k
+
+
+def test_restatement_matches_reference_cluster_scene(oracle, reference):
+    w = scenes.config3(n=20000, width=160, height=90)
+    got, _ = oracle.render(w.scene, w.camera)
+    assert np.array_equal(got, reference.render(w.scene, w.camera))
+
+
+@pytest.mark.parametrize("alg", ["l1", "mse", "ssim"])
+def test_restatement_matches_reference_losses(oracle, reference, alg):
+    rng = np.random.default_rng(3)
+    p = rng.random((3, 23, 31), dtype=np.float32)
+    t = rng.random((3, 23, 31), dtype=np.float32)
+    m_o = rng.random(p.shape, dtype=np.float32)
+    g_o = rng.random(p.shape, dtype=np.float32)
+    m_r, g_r = m_o.copy(), g_o.copy()
+    oracle.loss(alg, p, t, 0.3, m_o, g_o)
+    reference.loss(alg, p, t, 0.3, m_r, g_r)
+    assert np.array_equal(m_o, m_r)
+    assert np.array_equal(g_o, g_r)
+
+
+def test_ssim_against_independent_float64(oracle):
+    """SSIM map from a separate numpy float64 evaluation (scipy-free 2D correlation)."""
+    rng = np.random.default_rng(9)
+    p = rng.random((1, 20, 24), dtype=np.float32)
+    t = rng.random((1, 20, 24), dtype=np.float32)
+    x = np.arange(11) - 5
+    g = np.exp(-(x ** 2) / (2 * 1.5 ** 2))
+    g = g / g.sum()
+    w2 = np.outer(g, g)
+
+    def conv(a):
+        pad = np.pad(a.astype(np.float64), 5)
+        out = np.zeros(a.shape)
+        for dy in range(11):
+            for dx in range(11):
+                out += w2[dy, dx] * pad[dy:dy + a.shape[0], dx:dx + a.shape[1]]
+        return out
+
+    a, b = p[0], t[0]
+    mu1, mu2 = conv(a), conv(b)
+    s1 = conv(a * a.astype(np.float64)) - mu1 ** 2
+    s2 = conv(b * b.astype(np.float64)) - mu2 ** 2
+    s12 = conv(a.astype(np.float64) * b) - mu1 * mu2
+    ssim = ((2 * mu1 * mu2 + 1e-4) * (2 * s12 + 9e-4)) / ((mu1 ** 2 + mu2 ** 2 + 1e-4) * (s1 + s2 + 9e-4))
+    expect = (1 - ssim)[5:-5, 5:-5]
+    m = np.zeros_like(p)
+    oracle.loss("ssim", p, t, 1.0, m, None)
+    assert np.abs(m[0, 5:-5, 5:-5] - expect).max() < 2e-6
+    assert np.all(m[0, :5] == 0) and np.all(m[0, :, :5] == 0)
+
+
+def test_ssim_gradient_finite_difference(oracle):
+    rng = np.random.default_rng(12)
+    p = rng.random((1, 16, 16), dtype=np.float32)
+    t = rng.random((1, 16, 16), dtype=np.float32)
+    g = np.zeros_like(p)
+    m = np.zeros_like(p)
+    oracle.loss("ssim", p, t, 1.0, m, g, mean=False)
+
+    def total(pp):
+        mm = np.zeros_like(pp)
+        oracle.loss("ssim", pp, t, 1.0, mm, None)
+        return float(mm.astype(np.float64).sum())
+
+    for (y, x) in [(8, 8), (5, 10), (7, 3)]:
+        e = 1e-3
+        pp, pm = p.copy(), p.copy()
+        pp[0, y, x] += e
+        pm[0, y, x] -= e
+        fd = (total(pp) - total(pm)) / (2 * e)
+        assert abs(fd - g[0, y, x]) <= 2e-2 * max(1.0, abs(fd))
+
+
+def test_restatement_matches_reference_adam(oracle, reference):
+    rng = np.random.default_rng(4)
+    p0 = rng.standard_normal(1000).astype(np.float32)
+    g = (0.1 * rng.standard_normal(1000)).astype(np.float32)
+    hyper = (1e-2, 0.9, 0.999, 0.01, 1e-8, 0.05)
+    p_ref = p0.copy()
+    reference.adam(p_ref, g, hyper, 5)
+    p_o = p0.copy()
+    m = np.zeros_like(p0)
+    v = np.zeros_like(p0)
+    for step in range(1, 6):
+        oracle.adam_step(p_o, g, m, v, *hyper, step)
+    assert np.array_equal(p_o, p_ref)
+
+
+def test_adam_textbook(oracle):
+    """One step from zero moments: p -= lr * sign-ish(g) as Kingma & Ba (m_hat = g, v_hat = g^2)."""
+    g = np.array([0.5, -2.0, 1e-3], np.float32)
+    p = np.zeros(3, np.float32)
+    m = np.zeros(3, np.float32)
+    v = np.zeros(3, np.float32)
+    oracle.adam_step(p, g, m, v, 0.1, 0.9, 0.999, 0.0, 1e-8, 0.0, 1)
+    expect = -0.1 * g.astype(np.float64) / (np.abs(g.astype(np.float64)) + 1e-8)
+    assert np.allclose(p, expect, rtol=1e-5, atol=1e-7)
+
+
+def _adc_inputs(n, seed):
+    sc = scenes.cube_scene(seed, n)
+    rng = np.random.default_rng(seed)
+    aux = {"grad_acc": (rng.random(n) * 2e-3).astype(np.float32),
+           "absgrad_acc": (rng.random(n) * 4e-3).astype(np.float32),
+           "visible_counter": rng.integers(0, 4, n).astype(np.float32)}
+    fields = {"mean3d": sc.mean3d, "rotation": sc.rotation, "logscale": sc.logscale, "opacity": sc.opacity,
+              "sh0": sc.sh0}
+    return fields, aux
+
+
+@pytest.mark.parametrize("algorithm,step,max_num", [(0, 100, 5000), (1, 200, 5000), (0, 100, 2100), (1, 600, 3000)])
+def test_restatement_matches_reference_adc(oracle, reference, algorithm, step, max_num):
+    fields, aux = _adc_inputs(2000, 21 + algorithm)
+    p = AdcParams(algorithm=algorithm, pruning_opacity_threshold=0.1, opacity_clamp_value=0.3, max_world_scale=0.05,
+                  duplicate_grad_threshold=2e-4, duplicate_scale_threshold=0.01,
+                  duplicate_absgrad_threshold=4e-4, scene_scale=1.0, refine_every=100, start_refine=0,
+                  end_refine=1000, max_num_gaussians=max_num, reset_every=300, global_step=step, seed=77)
+    out_o, _, counts_o = oracle.adc_step({k: v.copy() for k, v in fields.items()}, None,
+                                         {k: v.copy() for k, v in aux.items()}, p, max_num)
+    out_r, counts_r = reference.adc({k: v.copy() for k, v in fields.items()}, aux, p, max_num)
+    assert list(counts_o) == list(counts_r)
+    for k in out_r:
+        assert np.array_equal(out_o[k].reshape(out_r[k].shape), out_r[k]), k
+
+
+def test_expf_restatement_matches_libm(oracle):
+    """gsx_expf (gsx_amd/csrc/gsx_math.h) == host expf: exhaustive over the blend's power range
+    [-4.5, 0] and the sigmoid/exp argument range, strided over all other floats."""
+    neg_zero, neg_4_5 = 0x80000000, 0xC0900000
+    assert oracle.expf_mismatches(neg_zero, neg_4_5) == 0
+    assert oracle.expf_mismatches(0x00000000, 0x42B17218, 3) == 0   # [0, 88.72]
+    assert oracle.expf_mismatches(0x80000000, 0xC2D00000, 3) == 0   # [-104, 0]
+    assert oracle.expf_mismatches(0x00000000, 0xFFFFFFFF, 977) == 0  # everything else, sampled
+
+
+def test_scene_pcg32_matches_gsx(reference):
+    """The scene generator's uniform/normal streams equal gsx_pcg32_next_float/_next_normal."""
+    lib = reference.lib
+    lib.gsx_pcg32_init.restype = None
+    handle = ctypes.c_void_p()
+    lib.gsx_pcg32_init.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint64]
+    lib.gsx_pcg32_next_float.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_float)]
+    lib.gsx_pcg32_next_normal.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_float)]
+    for normal in (False, True):
+        lib.gsx_pcg32_init(ctypes.byref(handle), 1234)
+        ref = []
+        f = ctypes.c_float()
+        for _ in range(500):
+            (lib.gsx_pcg32_next_normal if normal else lib.gsx_pcg32_next_float)(handle, ctypes.byref(f))
+            ref.append(f.value)
+        got = scenes.pcg32_stream(1234, 500, normal)
+        assert np.array_equal(got, np.array(ref, np.float32))
+
+
+def test_tile_restatement_brute_force(oracle):
+    """Every tile list equals the brute-force set of visible Gaussians whose pixel box meets the
+    tile, ordered by (depth, index)."""
+    w = scenes.config0(n=3000, width=80, height=56)
+    keys, vals = oracle.tile_keys(w.scene, w.camera, 16)
+    idx, rec, bbox = oracle.preprocess(w.scene, w.camera)
+    tiles_x = (80 + 15) // 16
+    ranges = oracle.tile_ranges(keys, tiles_x * ((56 + 15) // 16))
+    depth = rec[:, 6]
+    for tile in range(ranges.shape[0]):
+        tx, ty = tile % tiles_x, tile // tiles_x
+        x0, y0, x1, y1 = tx * 16, ty * 16, tx * 16 + 15, ty * 16 + 15
+        hit = (bbox[:, 0] <= x1) & (bbox[:, 1] >= x0) & (bbox[:, 2] <= y1) & (bbox[:, 3] >= y0)
+        order = np.lexsort((idx[hit], depth[hit]))
+        expect = idx[hit][order]
+        s, e = ranges[tile]
+        assert np.array_equal(vals[s:e].astype(np.int64), expect)
+    assert np.all(keys[1:] >= keys[:-1])
+
+
+def test_gather_rows(oracle):
+    src = np.arange(40, dtype=np.float32).reshape(10, 4)
+    idx = np.array([3, 3, 0, 9], np.int32)
+    assert np.array_equal(oracle.gather_rows(src, idx), src[idx])
+    with pytest.raises(IndexError):
+        oracle.gather_rows(src, np.array([10], np.int32))
+
+
+def test_camera_look_at_convention():
+    """look_at yields the documented pose for 'at (0,0,4) looking at the origin'."""
+    pose = scenes.look_at((0.0, 0.0, 4.0))
+    q = pose[:4]
+    # 180 degrees about x up to sign: (1,0,0,0) xyzw
+    assert abs(abs(q[0]) - 1.0) < 1e-6 and np.allclose(q[1:], 0, atol=1e-6)
+    assert np.allclose(pose[4:], (0, 0, 4), atol=1e-6)
+    assert math.isclose(float(np.linalg.norm(scenes.orbit_pose(5)[:4])), 1.0, rel_tol=1e-6)
