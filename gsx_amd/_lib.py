@@ -58,7 +58,8 @@ class RenderStats(ctypes.Structure):
 
 class RenderBuffers(ctypes.Structure):
     _fields_ = [("sorted_keys", _vp), ("sorted_values", _vp), ("tile_ranges", _vp), ("records", _vp),
-                ("tile_counts", _vp), ("final_transmittance", _vp), ("last_contributor", _vp)]
+                ("tile_counts", _vp), ("instance_gaussian", _vp), ("final_transmittance", _vp),
+                ("last_contributor", _vp)]
 
 
 ADAM_MAX_GROUPS = 16

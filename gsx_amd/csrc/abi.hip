@@ -144,7 +144,7 @@ int bits_for(uint32_t v) {
 }  // namespace
 
 struct gsx_hip_render_context {
-    DeviceBuffer rec, cov_coef, ckpt, tile_count, offsets, scan_temp, keys, vals, keys_alt, vals_alt, sort_temp, ranges, final_t,
+    DeviceBuffer rec, cov_coef, ckpt, inst_gauss, inst_grad, tile_count, offsets, scan_temp, keys, vals, keys_alt, vals_alt, sort_temp, ranges, final_t,
         last, grad2d;
     uint32_t* host_count = nullptr;  // pinned
     CameraParams cam{};
@@ -300,7 +300,7 @@ gsx_hip_status gsx_hip_render_context_create(gsx_hip_render_context** out_contex
 
 gsx_hip_status gsx_hip_render_context_destroy(gsx_hip_render_context* ctx) {
     if (ctx == nullptr) return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "context must be non-null");
-    DeviceBuffer* all[] = {&ctx->rec, &ctx->cov_coef, &ctx->ckpt, &ctx->tile_count, &ctx->offsets,  &ctx->scan_temp, &ctx->keys,
+    DeviceBuffer* all[] = {&ctx->rec, &ctx->cov_coef, &ctx->ckpt, &ctx->inst_gauss, &ctx->inst_grad, &ctx->tile_count, &ctx->offsets,  &ctx->scan_temp, &ctx->keys,
                            &ctx->vals,    &ctx->keys_alt,   &ctx->vals_alt, &ctx->sort_temp, &ctx->ranges,
                            &ctx->final_t, &ctx->last,       &ctx->grad2d};
     for (DeviceBuffer* b : all) b->release();
@@ -349,7 +349,7 @@ gsx_hip_status gsx_hip_render_context_get_timings(gsx_hip_render_context* ctx, f
     if (ctx == nullptr || out_ms == nullptr) return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "context/out_ms null");
     if (!ctx->timing) return fail(GSX_HIP_ERROR_INVALID_STATE, "timing is not enabled");
     // per set: 0 fwd start, 1 preprocess, 2 scan (+count readback), 3 emit, 4 sort, 5 ranges,
-    //          6 blend; 7 bwd start, 8 zero, 9 blend bwd, 10 projection bwd
+    //          6 blend; 7 bwd start, 8 blend bwd, 9 instance reduce, 10 projection bwd
     double sum[GSX_HIP_RENDER_STAGE_COUNT] = {0.0};
     int nf = 0, nb = 0;
     for (int set = 0; set < ctx->ring; ++set) {
@@ -443,6 +443,7 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     GSX_TRY(ctx->keys_alt.reserve((size_t)(count > 0 ? count : 1) * sizeof(uint64_t), "keys_alt"));
     GSX_TRY(ctx->vals.reserve((size_t)(count > 0 ? count : 1) * sizeof(uint32_t), "vals"));
     GSX_TRY(ctx->vals_alt.reserve((size_t)(count > 0 ? count : 1) * sizeof(uint32_t), "vals_alt"));
+    GSX_TRY(ctx->inst_gauss.reserve((size_t)(count > 0 ? count : 1) * sizeof(uint32_t), "instance_gaussian"));
     GSX_TRY(ctx->sort_temp.reserve(gsx_hip_radix_sort_temp_bytes(count), "sort_temp"));
     if (train) {
         // bucket checkpoints: at most I/32 + tiles + 1 slots of 256 floats
@@ -451,7 +452,7 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     if (n > 0) {
         hipLaunchKernelGGL(emit_keys_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, n, ctx->rec.as<float4>(),
                            ctx->tile_count.as<uint32_t>(), ctx->offsets.as<uint32_t>(), cam.tiles_x,
-                           ctx->keys.as<uint64_t>(), ctx->vals.as<uint32_t>());
+                           ctx->keys.as<uint64_t>(), ctx->vals.as<uint32_t>(), ctx->inst_gauss.as<uint32_t>());
         GSX_HIP_TRY(hipGetLastError(), "emit_keys_kernel");
     }
     GSX_TRY(record(ctx, 3, stream));
@@ -475,7 +476,8 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     GSX_TRY(record(ctx, 5, stream));
     const int tiles_padded = ((tiles + 7) / 8) * 8;
     hipLaunchKernelGGL(blend_forward_kernel, dim3((unsigned)tiles_padded), dim3(256), 0, stream,
-                       ctx->ranges.as<uint2>(), svals, ctx->rec.as<float4>(), cam, out_rgb, ctx->final_t.as<float>(),
+                       ctx->ranges.as<uint2>(), svals, ctx->rec.as<float4>(), ctx->inst_gauss.as<uint32_t>(), cam,
+                       out_rgb, ctx->final_t.as<float>(),
                        ctx->last.as<uint32_t>(), train ? ctx->ckpt.as<float>() : nullptr);
     GSX_HIP_TRY(hipGetLastError(), "blend_forward_kernel");
     GSX_TRY(record(ctx, 6, stream));
@@ -506,20 +508,24 @@ gsx_hip_status gsx_hip_render_backward(gsx_hip_render_context* ctx, const float*
         return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "rotation gradient must be 16-byte aligned");
     }
     GSX_TRY(ctx->grad2d.reserve((size_t)(n > 0 ? n : 1) * 9 * sizeof(float), "grad2d"));
+    GSX_TRY(ctx->inst_grad.reserve((size_t)(ctx->instance_count > 0 ? ctx->instance_count : 1) * 9 * sizeof(float),
+                                   "instance_grad"));
     const CameraParams& cam = ctx->cam;
     const int32_t tiles = cam.tiles_x * cam.tiles_y;
     const uint32_t* svals = ctx->sorted_in_alt ? ctx->vals_alt.as<uint32_t>() : ctx->vals.as<uint32_t>();
     GSX_TRY(record(ctx, 7, stream));
-    hipLaunchKernelGGL(fill_f32_kernel, dim3(blocks_for(n * 9, 256)), dim3(256), 0, stream, ctx->grad2d.as<float>(),
-                       n * 9, 0.0f);
-    GSX_HIP_TRY(hipGetLastError(), "fill_f32_kernel");
-    GSX_TRY(record(ctx, 8, stream));
     const int tiles_padded = ((tiles + 7) / 8) * 8;
     hipLaunchKernelGGL(blend_backward_kernel, dim3((unsigned)tiles_padded), dim3(256), 0, stream,
-                       ctx->ranges.as<uint2>(), svals, ctx->rec.as<float4>(), ctx->cov_coef.as<float4>(),
-                       ctx->ckpt.as<float>(), cam, grad_rgb, ctx->final_t.as<float>(),
-                       ctx->last.as<uint32_t>(), ctx->grad2d.as<float>());
+                       ctx->ranges.as<uint2>(), svals, ctx->inst_gauss.as<uint32_t>(), ctx->rec.as<float4>(),
+                       ctx->cov_coef.as<float4>(), ctx->ckpt.as<float>(), cam, grad_rgb, ctx->final_t.as<float>(),
+                       ctx->last.as<uint32_t>(), ctx->inst_grad.as<float>());
     GSX_HIP_TRY(hipGetLastError(), "blend_backward_kernel");
+    GSX_TRY(record(ctx, 8, stream));
+    if (n > 0) {
+        hipLaunchKernelGGL(reduce_instance_grads_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, n,
+                           ctx->offsets.as<uint32_t>(), ctx->inst_grad.as<float>(), ctx->grad2d.as<float>());
+        GSX_HIP_TRY(hipGetLastError(), "reduce_instance_grads_kernel");
+    }
     GSX_TRY(record(ctx, 9, stream));
     if (n > 0) {
         hipLaunchKernelGGL(projection_backward_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, n, gs.mean3d,
@@ -551,6 +557,7 @@ gsx_hip_status gsx_hip_render_context_get_buffers(const gsx_hip_render_context* 
     out->tile_ranges = ctx->ranges.as<uint32_t>();
     out->records = ctx->rec.as<float>();
     out->tile_counts = ctx->tile_count.as<uint32_t>();
+    out->instance_gaussian = ctx->inst_gauss.as<uint32_t>();
     out->final_transmittance = ctx->final_t.as<float>();
     out->last_contributor = ctx->last.as<uint32_t>();
     return GSX_HIP_SUCCESS;

@@ -319,4 +319,24 @@ __device__ inline float wave_sum(float v) {
     return v;
 }
 
+// Sum over the 64 lanes of a wave with DPP lane moves only (no LDS traffic): quad swaps, the
+// half-row and row mirrors leave each 16-lane row's sum in all its lanes, then two row
+// broadcasts carry rows 0-2 into row 3. Every lane must be active. The total is returned as a
+// wave-uniform value (read from lane 63).
+template <int kCtrl, int kRowMask>
+__device__ inline float dpp_move(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl, kRowMask, 0xf,
+                                                                 false));
+}
+
+__device__ inline float wave_reduce_sum(float v) {
+    v += dpp_move<0xb1, 0xf>(v);   // quad_perm [1,0,3,2]
+    v += dpp_move<0x4e, 0xf>(v);   // quad_perm [2,3,0,1]
+    v += dpp_move<0x141, 0xf>(v);  // row_half_mirror
+    v += dpp_move<0x140, 0xf>(v);  // row_mirror
+    v += dpp_move<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
+    v += dpp_move<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
 }  // namespace gsx_amd

@@ -64,30 +64,53 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
 }
 
 // ---------------------------------------------------------------------------------------------
-// Key emission: Gaussian g owns keys[offset[g] .. offset[g+1]); key = tile << 32 | bits(depth),
-// value = g. Offsets come from an exclusive scan in Gaussian order, so equal keys appear in
-// ascending Gaussian order and a stable sort reproduces the CPU (depth, index) order per tile.
+// Key emission: Gaussian g owns positions offset[g] .. offset[g+1]) of the instance array, one
+// per tile of its box in row-major tile order; key = tile << 32 | bits(depth). Offsets come from
+// an exclusive scan in Gaussian order, so equal keys appear in ascending Gaussian order and a
+// stable sort reproduces the CPU (depth, index) order per tile. The sorted value is the emission
+// position; instance_gaussian[position] = g. Boxes of more than 32 tiles (near-plane Gaussians
+// can cover the whole image) are written by the whole wave instead of one lane.
 // ---------------------------------------------------------------------------------------------
+__device__ inline void emit_range(uint32_t g, uint32_t o, uint32_t bx, uint32_t by, uint64_t depth_bits,
+                                  int32_t tiles_x, uint32_t first, uint32_t stride, uint64_t* __restrict__ keys,
+                                  uint32_t* __restrict__ values, uint32_t* __restrict__ instance_gaussian) {
+    const uint32_t tx0 = (bx & 0xffffu) / kTile, tx1 = (bx >> 16) / kTile;
+    const uint32_t ty0 = (by & 0xffffu) / kTile, ty1 = (by >> 16) / kTile;
+    const uint32_t wx = tx1 - tx0 + 1;
+    const uint32_t total = wx * (ty1 - ty0 + 1);
+    for (uint32_t k = first; k < total; k += stride) {
+        const uint32_t ty = ty0 + k / wx;
+        const uint32_t tx = tx0 + k % wx;
+        const uint64_t tile = (uint64_t)ty * (uint64_t)tiles_x + tx;
+        keys[o + k] = (tile << 32) | depth_bits;
+        values[o + k] = o + k;
+        instance_gaussian[o + k] = g;
+    }
+}
+
 __global__ __launch_bounds__(256) void emit_keys_kernel(int64_t n, const float4* __restrict__ rec,
                                                         const uint32_t* __restrict__ tile_count,
                                                         const uint32_t* __restrict__ offsets, int32_t tiles_x,
-                                                        uint64_t* __restrict__ keys, uint32_t* __restrict__ values) {
+                                                        uint64_t* __restrict__ keys, uint32_t* __restrict__ values,
+                                                        uint32_t* __restrict__ instance_gaussian) {
+    constexpr uint32_t kWaveEmit = 32;
     const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (g >= n) return;
-    if (tile_count[g] == 0) return;
-    const float4 r2 = rec[3 * g + 2];
-    const uint32_t bx = __float_as_uint(r2.y), by = __float_as_uint(r2.z);
-    const uint32_t tx0 = (bx & 0xffffu) / kTile, tx1 = (bx >> 16) / kTile;
-    const uint32_t ty0 = (by & 0xffffu) / kTile, ty1 = (by >> 16) / kTile;
-    const uint64_t depth_bits = (uint64_t)__float_as_uint(r2.w);
-    uint32_t o = offsets[g];
-    for (uint32_t ty = ty0; ty <= ty1; ++ty) {
-        for (uint32_t tx = tx0; tx <= tx1; ++tx) {
-            const uint64_t tile = (uint64_t)ty * (uint64_t)tiles_x + tx;
-            keys[o] = (tile << 32) | depth_bits;
-            values[o] = (uint32_t)g;
-            ++o;
-        }
+    const uint32_t count = g < n ? tile_count[g] : 0u;
+    if (count > 0 && count <= kWaveEmit) {
+        const float4 r2 = rec[3 * g + 2];
+        emit_range((uint32_t)g, offsets[g], __float_as_uint(r2.y), __float_as_uint(r2.z),
+                   (uint64_t)__float_as_uint(r2.w), tiles_x, 0u, 1u, keys, values, instance_gaussian);
+    }
+    uint64_t big = __ballot(count > kWaveEmit);
+    const uint32_t lane = __lane_id();
+    const int64_t wave_base = g - (int64_t)lane;
+    while (big != 0ull) {
+        const uint32_t l = (uint32_t)__builtin_ctzll(big);
+        big &= big - 1ull;
+        const int64_t gb = wave_base + l;
+        const float4 r2 = rec[3 * gb + 2];
+        emit_range((uint32_t)gb, offsets[gb], __float_as_uint(r2.y), __float_as_uint(r2.z),
+                   (uint64_t)__float_as_uint(r2.w), tiles_x, lane, (uint32_t)kWave, keys, values, instance_gaussian);
     }
 }
 
@@ -147,8 +170,8 @@ __device__ inline size_t checkpoint_slot(uint32_t range_start, int tile, uint32_
 // ---------------------------------------------------------------------------------------------
 __global__ __launch_bounds__(kBlendThreads) void blend_forward_kernel(
     const uint2* __restrict__ ranges, const uint32_t* __restrict__ values, const float4* __restrict__ rec,
-    CameraParams cam, float* __restrict__ out_rgb, float* __restrict__ out_t, uint32_t* __restrict__ out_last,
-    float* __restrict__ ckpt) {
+    const uint32_t* __restrict__ instance_gaussian, CameraParams cam, float* __restrict__ out_rgb,
+    float* __restrict__ out_t, uint32_t* __restrict__ out_last, float* __restrict__ ckpt) {
     __shared__ float4 s_r0[kBlendThreads];
     __shared__ float4 s_r1[kBlendThreads];
     __shared__ float4 s_r2[kBlendThreads];
@@ -169,7 +192,7 @@ __global__ __launch_bounds__(kBlendThreads) void blend_forward_kernel(
         if (__syncthreads_count(done ? 1 : 0) == kBlendThreads) break;
         const uint32_t j = base + threadIdx.x;
         if (j < range.y) {
-            const uint32_t g = values[j];
+            const uint32_t g = instance_gaussian[values[j]];
             s_r0[threadIdx.x] = rec[3 * (size_t)g + 0];
             s_r1[threadIdx.x] = rec[3 * (size_t)g + 1];
             s_r2[threadIdx.x] = rec[3 * (size_t)g + 2];
@@ -227,20 +250,28 @@ constexpr int kGrad2d = 9;
 // replays the bucket forward (same operations as the forward, so T_before, G and the contribution
 // set are bit-identical to the CPU's) and then walks it backwards accumulating the suffix colour
 // exactly as the CPU does. Per contribution the gradient terms are the CPU's, including the
-// d(conic)/d(cov2d) map applied per contribution; each wave sums its lanes' 9 partials per
-// Gaussian and issues one set of atomics.
+// d(conic)/d(cov2d) map applied per contribution.
+// Reduction without atomics: each wave sums its lanes' 9 partials per entry with DPP moves, the
+// four waves combine through LDS, and the tile writes one 9-float partial per instance into
+// instance_grad[emission position]; reduce_instance_grads_kernel then sums each Gaussian's
+// contiguous run of positions. The result is deterministic and immune to the contention of
+// full-screen Gaussians (present in every tile).
 // ---------------------------------------------------------------------------------------------
+constexpr int kWavesPerTile = kBlendThreads / kWave;
+
 __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
-    const uint2* __restrict__ ranges, const uint32_t* __restrict__ values, const float4* __restrict__ rec,
+    const uint2* __restrict__ ranges, const uint32_t* __restrict__ values,
+    const uint32_t* __restrict__ instance_gaussian, const float4* __restrict__ rec,
     const float4* __restrict__ cov_coef, const float* __restrict__ ckpt, CameraParams cam,
     const float* __restrict__ grad_rgb, const float* __restrict__ final_t, const uint32_t* __restrict__ last_contrib,
-    float* __restrict__ grad2d) {
+    float* __restrict__ instance_grad) {
     __shared__ float4 s_r0[kBlendThreads];
     __shared__ float4 s_r1[kBlendThreads];
     __shared__ float4 s_r2[kBlendThreads];
     __shared__ float4 s_k0[kBlendThreads];
     __shared__ float2 s_k1[kBlendThreads];
-    __shared__ uint32_t s_g[kBlendThreads];
+    __shared__ uint32_t s_pos[kBlendThreads];
+    __shared__ float s_acc[kWavesPerTile][kBucket][kGrad2d];
     __shared__ uint32_t s_max_last;
     const int tiles = cam.tiles_x * cam.tiles_y;
     const int tile = xcd_tile_index(blockIdx.x, tiles);
@@ -270,14 +301,24 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
     atomicMax(&s_max_last, last);
     __syncthreads();
     const uint32_t end_all = s_max_last;
-    if (end_all <= range.x) return;  // uniform: no pixel of this tile has a contribution
     const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    // entries no pixel of the tile reaches: their partials are zero
+    const uint32_t zero_from =
+        end_all <= range.x ? range.x : range.x + ((end_all - range.x + kBucket - 1) / kBucket) * kBucket;
+    for (uint32_t j = zero_from + threadIdx.x; j < range.y; j += kBlendThreads) {
+        float* dst = instance_grad + (size_t)values[j] * kGrad2d;
+#pragma unroll
+        for (int c = 0; c < kGrad2d; ++c) dst[c] = 0.0f;
+    }
+    if (end_all <= range.x) return;  // uniform
     const uint32_t first_batch = range.x + ((end_all - 1u - range.x) / kBlendThreads) * kBlendThreads;
     for (int64_t bstart = first_batch; bstart >= (int64_t)range.x; bstart -= kBlendThreads) {
         const int count = (int)min((uint32_t)kBlendThreads, range.y - (uint32_t)bstart);
         if (threadIdx.x < count) {
-            const uint32_t g = values[bstart + threadIdx.x];
-            s_g[threadIdx.x] = g;
+            const uint32_t p = values[bstart + threadIdx.x];
+            const uint32_t g = instance_gaussian[p];
+            s_pos[threadIdx.x] = p;
             s_r0[threadIdx.x] = rec[3 * (size_t)g + 0];
             s_r1[threadIdx.x] = rec[3 * (size_t)g + 1];
             s_r2[threadIdx.x] = rec[3 * (size_t)g + 2];
@@ -288,7 +329,7 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
         __syncthreads();
         for (int sb = (count - 1) / kBucket; sb >= 0; --sb) {
             const uint32_t j0 = (uint32_t)bstart + (uint32_t)(sb * kBucket);
-            if (j0 >= end_all) continue;  // uniform
+            if (j0 >= end_all) continue;  // uniform; zeroed above
             const int n_in = min(kBucket, count - sb * kBucket);
             float tb[kBucket];
             float gv[kBucket];
@@ -370,32 +411,89 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
                     s1 += w * r1.w;
                     s2 += w * r2.x;
                 }
+                float* acc = &s_acc[wave][i][0];
                 if (__ballot(contrib) != 0ull) {
-                    g_mx = wave_sum(g_mx);
-                    g_my = wave_sum(g_my);
-                    g_ca = wave_sum(g_ca);
-                    g_cb = wave_sum(g_cb);
-                    g_cc = wave_sum(g_cc);
-                    g_c0 = wave_sum(g_c0);
-                    g_c1 = wave_sum(g_c1);
-                    g_c2 = wave_sum(g_c2);
-                    g_op = wave_sum(g_op);
+                    const float v0 = wave_reduce_sum(g_mx);
+                    const float v1 = wave_reduce_sum(g_my);
+                    const float v2 = wave_reduce_sum(g_ca);
+                    const float v3 = wave_reduce_sum(g_cb);
+                    const float v4 = wave_reduce_sum(g_cc);
+                    const float v5 = wave_reduce_sum(g_c0);
+                    const float v6 = wave_reduce_sum(g_c1);
+                    const float v7 = wave_reduce_sum(g_c2);
+                    const float v8 = wave_reduce_sum(g_op);
                     if (lane == 0) {
-                        float* dst = grad2d + (size_t)s_g[kk] * kGrad2d;
-                        atomicAdd(dst + 0, g_mx);
-                        atomicAdd(dst + 1, g_my);
-                        atomicAdd(dst + 2, g_ca);
-                        atomicAdd(dst + 3, g_cb);
-                        atomicAdd(dst + 4, g_cc);
-                        atomicAdd(dst + 5, g_c0);
-                        atomicAdd(dst + 6, g_c1);
-                        atomicAdd(dst + 7, g_c2);
-                        atomicAdd(dst + 8, g_op);
+                        acc[0] = v0;
+                        acc[1] = v1;
+                        acc[2] = v2;
+                        acc[3] = v3;
+                        acc[4] = v4;
+                        acc[5] = v5;
+                        acc[6] = v6;
+                        acc[7] = v7;
+                        acc[8] = v8;
                     }
+                } else if (lane < kGrad2d) {
+                    acc[lane] = 0.0f;
                 }
             }
+            __syncthreads();
+            // combine the four waves and write the bucket's per-instance partials
+            for (int o = threadIdx.x; o < n_in * kGrad2d; o += kBlendThreads) {
+                const int e = o / kGrad2d, c = o % kGrad2d;
+                const float v = (s_acc[0][e][c] + s_acc[1][e][c]) + (s_acc[2][e][c] + s_acc[3][e][c]);
+                instance_grad[(size_t)s_pos[sb * kBucket + e] * kGrad2d + c] = v;
+            }
+            __syncthreads();
         }
-        __syncthreads();
+    }
+}
+
+// grad2d[g] = sum of instance_grad over g's emission positions [offset[g], offset[g+1]).
+// Lanes sum their own Gaussian when it has at most 32 instances; larger runs (full-screen
+// Gaussians have thousands) are summed by the whole wave. Overwrites grad2d, so no zero fill.
+__global__ __launch_bounds__(256) void reduce_instance_grads_kernel(int64_t n, const uint32_t* __restrict__ offsets,
+                                                                    const float* __restrict__ instance_grad,
+                                                                    float* __restrict__ grad2d) {
+    constexpr uint32_t kLaneMax = 32;
+    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    uint32_t b = 0, e = 0;
+    if (g < n) {
+        b = offsets[g];
+        e = offsets[g + 1];
+    }
+    const uint32_t count = e - b;
+    if (g < n && count <= kLaneMax) {
+        float acc[kGrad2d];
+#pragma unroll
+        for (int c = 0; c < kGrad2d; ++c) acc[c] = 0.0f;
+        for (uint32_t p = b; p < e; ++p) {
+#pragma unroll
+            for (int c = 0; c < kGrad2d; ++c) acc[c] += instance_grad[(size_t)p * kGrad2d + c];
+        }
+#pragma unroll
+        for (int c = 0; c < kGrad2d; ++c) grad2d[g * kGrad2d + c] = acc[c];
+    }
+    uint64_t big = __ballot(g < n && count > kLaneMax);
+    const uint32_t lane = __lane_id();
+    const int64_t wave_base = g - (int64_t)lane;
+    while (big != 0ull) {
+        const uint32_t l = (uint32_t)__builtin_ctzll(big);
+        big &= big - 1ull;
+        const int64_t gb = wave_base + l;
+        const uint32_t bb = offsets[gb], ee = offsets[gb + 1];
+        float acc[kGrad2d];
+#pragma unroll
+        for (int c = 0; c < kGrad2d; ++c) acc[c] = 0.0f;
+        for (uint32_t p = bb + lane; p < ee; p += kWave) {
+#pragma unroll
+            for (int c = 0; c < kGrad2d; ++c) acc[c] += instance_grad[(size_t)p * kGrad2d + c];
+        }
+#pragma unroll
+        for (int c = 0; c < kGrad2d; ++c) {
+            const float v = wave_reduce_sum(acc[c]);
+            if (lane == 0) grad2d[gb * kGrad2d + c] = v;
+        }
     }
 }
 

@@ -109,10 +109,11 @@ typedef struct gsx_hip_render_stats {
 /* Device pointers of the intermediates a forward retains (valid until the next forward). */
 typedef struct gsx_hip_render_buffers {
     const uint64_t* sorted_keys;   /* [instance_count] (tile << 32) | float_bits(depth) */
-    const uint32_t* sorted_values; /* [instance_count] Gaussian index */
+    const uint32_t* sorted_values; /* [instance_count] emission position of each sorted key */
     const uint32_t* tile_ranges;   /* [tile_count][2] start, end */
     const float* records;          /* [N][12] packed per-Gaussian blend records */
     const uint32_t* tile_counts;   /* [N] tiles touched per Gaussian (0 = culled) */
+    const uint32_t* instance_gaussian; /* [instance_count] Gaussian index of each emission position */
     const float* final_transmittance; /* [H*W] */
     const uint32_t* last_contributor; /* [H*W] exclusive end of the last contributing position */
 } gsx_hip_render_buffers;
@@ -143,8 +144,8 @@ gsx_hip_status gsx_hip_render_context_get_buffers(const gsx_hip_render_context* 
  * sets; each forward (and the following backward) records one set on its launch stream, so a
  * timed loop pays no synchronisation. get_timings synchronises on the recorded events and writes
  * the per-stage average over the recorded sets, in milliseconds, in this order: preprocess,
- * scan (including the instance-count readback), emit, sort, ranges, blend_forward, grad_zero,
- * blend_backward, projection_backward. set_timing(0) disables timing. */
+ * scan (including the instance-count readback), emit, sort, ranges, blend_forward,
+ * blend_backward, instance_reduce, projection_backward. set_timing(0) disables timing. */
 enum { GSX_HIP_RENDER_STAGE_COUNT = 9 };
 gsx_hip_status gsx_hip_render_context_set_timing(gsx_hip_render_context* context, int32_t capacity);
 gsx_hip_status gsx_hip_render_context_get_timings(gsx_hip_render_context* context, float* out_ms, int32_t capacity,

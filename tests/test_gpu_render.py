@@ -79,8 +79,13 @@ def test_sorted_keys_and_ranges_bit_exact(oracle, name):
         lib.gsx_hip_memcpy_dtoh(keys.ctypes.data_as(ctypes.c_void_p), buf.sorted_keys, keys.nbytes)
         lib.gsx_hip_memcpy_dtoh(vals.ctypes.data_as(ctypes.c_void_p), buf.sorted_values, vals.nbytes)
     lib.gsx_hip_memcpy_dtoh(ranges.ctypes.data_as(ctypes.c_void_p), buf.tile_ranges, ranges.nbytes)
+    inst_g = np.empty(st.instance_count, np.uint32)
+    if st.instance_count:
+        lib.gsx_hip_memcpy_dtoh(inst_g.ctypes.data_as(ctypes.c_void_p), buf.instance_gaussian, inst_g.nbytes)
     assert np.array_equal(keys, keys_ref)
-    assert np.array_equal(vals, vals_ref)
+    assert np.array_equal(inst_g[vals], vals_ref)  # sorted values are emission positions
+    # emission positions of one Gaussian are contiguous and in row-major tile order
+    assert np.all(np.diff(inst_g.astype(np.int64)) >= 0)
     assert np.array_equal(ranges, oracle.tile_ranges(keys_ref, st.tile_count))
     # invariants: keys non-decreasing, ranges partition [0, I)
     assert np.all(keys[1:] >= keys[:-1])
