@@ -94,6 +94,8 @@ def main():
     ap.add_argument("--width", type=int, default=1920)
     ap.add_argument("--height", type=int, default=1080)
     ap.add_argument("--poses", type=int, default=24)
+    ap.add_argument("--calibrate-copy-mib", type=int, default=0,
+                    help="run one plain copy kernel of this size first (reference for traffic counters)")
     ap.add_argument("--cpu-baseline-iters", type=int, default=1,
                     help="reference CPU steps to time on the full workload (0 disables)")
     args = ap.parse_args()
@@ -172,6 +174,16 @@ def main():
             ev["loss_forward"].append((e[0], e[1]))
             ev["loss_backward"].append((e[1], e[2]))
             ev["adam"].append((e[3], e4))
+
+    if args.calibrate_copy_mib > 0:
+        nf = args.calibrate_copy_mib * (1 << 20) // 4
+        a = torch.ones(nf, dtype=torch.float32, device="cuda")
+        b = torch.empty_like(a)
+        torch.cuda.synchronize()
+        _lib.check(lib.gsx_hip_copy_f32(ptr(b), ptr(a), nf, stream_handle()), "calibration copy")
+        torch.cuda.synchronize()
+        log(f"calibration copy: {args.calibrate_copy_mib} MiB read + {args.calibrate_copy_mib} MiB written")
+        del a, b
 
     log(f"warmup {args.warmup} steps")
     for i in range(args.warmup):

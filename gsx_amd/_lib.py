@@ -71,6 +71,21 @@ class AdamGroup(ctypes.Structure):
                 ("max_grad", _f), ("bias_correction1", _d), ("bias_correction2", _d)]
 
 
+class AdcParams(ctypes.Structure):
+    _fields_ = [("algorithm", _i32), ("pruning_opacity_threshold", _f), ("opacity_clamp_value", _f),
+                ("max_world_scale", _f), ("max_screen_scale", _f), ("duplicate_grad_threshold", _f),
+                ("duplicate_scale_threshold", _f), ("duplicate_absgrad_threshold", _f), ("scene_scale", _f),
+                ("refine_every", _i64), ("start_refine", _i64), ("end_refine", _i64), ("max_num_gaussians", _i64),
+                ("reset_every", _i64)]
+
+
+class GsRows(ctypes.Structure):
+    _fields_ = [("count", _i64), ("sh_degree", _i32), ("mean3d", _vp), ("rotation", _vp), ("logscale", _vp),
+                ("opacity", _vp), ("sh0", _vp), ("sh1", _vp), ("sh2", _vp), ("sh3", _vp), ("grad_acc", _vp),
+                ("absgrad_acc", _vp), ("visible_counter", _vp), ("max_screen_radius", _vp),
+                ("first_moment", _vp * 8), ("second_moment", _vp * 8)]
+
+
 # name -> (restype, argtypes); this table is also the symbol list tests check against the header.
 SIGNATURES = {
     "gsx_hip_last_error_message": (ctypes.c_char_p, []),
@@ -85,6 +100,7 @@ SIGNATURES = {
     "gsx_hip_stream_destroy": (_st, [_vp]),
     "gsx_hip_stream_synchronize": (_st, [_vp]),
     "gsx_hip_fill_f32": (_st, [_vp, _i64, _f, _vp]),
+    "gsx_hip_copy_f32": (_st, [_vp, _vp, _i64, _vp]),
     "gsx_hip_render_context_create": (_st, [ctypes.POINTER(_vp)]),
     "gsx_hip_render_context_destroy": (_st, [_vp]),
     "gsx_hip_render_forward": (_st, [_vp, ctypes.POINTER(Camera), ctypes.POINTER(Gaussians), _i32, _vp, _vp, _vp]),
@@ -108,6 +124,11 @@ SIGNATURES = {
                                                                ctypes.c_int, _vp]),
     "gsx_hip_adam_step_f32_kernel_launch": (_st, [_vp, _vp, _vp, _vp, _i64, _f, _f, _f, _f, _f, _f, _d, _d, _vp]),
     "gsx_hip_adam_step_multi_launch": (_st, [ctypes.POINTER(AdamGroup), _i32, _vp]),
+    "gsx_hip_adc_context_create": (_st, [ctypes.POINTER(_vp), ctypes.c_uint64]),
+    "gsx_hip_adc_context_destroy": (_st, [_vp]),
+    "gsx_hip_adc_step": (_st, [_vp, ctypes.POINTER(AdcParams), ctypes.c_uint64, ctypes.POINTER(GsRows), _i64,
+                               ctypes.POINTER(GsRows), ctypes.POINTER(_i32), ctypes.POINTER(_i64), _vp]),
+    "gsx_hip_gather_rows_kernel_launch": (_st, [_vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp]),
 }
 
 _LIB = None

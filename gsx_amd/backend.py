@@ -17,7 +17,7 @@ import torch
 from . import _lib
 from ._lib import Camera, GaussianGrads, Gaussians, GsxHipError, check
 
-__all__ = ["Camera", "Renderer", "Loss", "Adam", "GsxHipError", "stream_handle", "ptr"]
+__all__ = ["Camera", "Renderer", "Loss", "Adam", "DensityControl", "GsxHipError", "stream_handle", "ptr"]
 
 
 def ptr(t: torch.Tensor | None):
@@ -247,3 +247,62 @@ class Adam:
             a.bias_correction1 = 1.0 - math.pow(b1, float(g["step"]))
             a.bias_correction2 = 1.0 - math.pow(b2, float(g["step"]))
         check(self.lib.gsx_hip_adam_step_multi_launch(arr, len(self.groups), stream_handle(stream)), "adam step")
+
+
+FIELD_WIDTHS = {"mean3d": 3, "rotation": 4, "logscale": 3, "opacity": 1, "sh0": 3, "sh1": 9, "sh2": 15, "sh3": 21}
+PARAM_FIELDS = ("mean3d", "rotation", "logscale", "opacity", "sh0", "sh1", "sh2", "sh3")
+AUX_FIELDS = ("grad_acc", "absgrad_acc", "visible_counter", "max_screen_radius")
+
+
+class DensityControl:
+    """gsx_adc (DEFAULT / ABSGS) on the HIP backend (gsx-adc.h). Rows live in capacity-sized
+    device buffers: growth appends in place, pruning compacts into a second buffer set."""
+
+    def __init__(self, params: dict, seed: int = 0):
+        self.lib = _lib.load()
+        p = _lib.AdcParams()
+        for name, _ in _lib.AdcParams._fields_:
+            if name in params:
+                setattr(p, name, params[name])
+        self.params = p
+        h = ctypes.c_void_p()
+        check(self.lib.gsx_hip_adc_context_create(ctypes.byref(h), int(seed)), "adc context create")
+        self.handle = h
+
+    def close(self):
+        if getattr(self, "handle", None) is not None and self.handle.value:
+            self.lib.gsx_hip_adc_context_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @staticmethod
+    def rows_struct(count: int, sh_degree: int, fields: dict, moments: dict | None) -> _lib.GsRows:
+        r = _lib.GsRows()
+        r.count = count
+        r.sh_degree = sh_degree
+        for name in PARAM_FIELDS + AUX_FIELDS:
+            setattr(r, name, ptr(fields.get(name)))
+        if moments is not None:
+            for k, name in enumerate(PARAM_FIELDS):
+                if name in moments:
+                    r.first_moment[k] = ptr(moments[name][0])
+                    r.second_moment[k] = ptr(moments[name][1])
+        return r
+
+    def step(self, global_step: int, count: int, sh_degree: int, fields: dict, moments: dict | None,
+             capacity: int, out_fields: dict, out_moments: dict | None, stream=None):
+        """Returns (new_count, result_in_out, counts[pruned, duplicated, grown, reset])."""
+        rows = self.rows_struct(count, sh_degree, fields, moments)
+        out = self.rows_struct(0, sh_degree, out_fields, out_moments)
+        in_out = ctypes.c_int32(0)
+        counts = (ctypes.c_int64 * 4)()
+        check(self.lib.gsx_hip_adc_step(self.handle, ctypes.byref(self.params), int(global_step), ctypes.byref(rows),
+                                        int(capacity), ctypes.byref(out), ctypes.byref(in_out), counts,
+                                        stream_handle(stream)), "adc step")
+        new_count = out.count if in_out.value else rows.count
+        return int(new_count), bool(in_out.value), list(counts)

@@ -23,6 +23,15 @@
 
 using namespace gsx_amd;
 
+namespace gsx_amd {
+// Plain streaming copy: 16 B per lane per iteration, grid-stride.
+__global__ __launch_bounds__(256) void copy_f32_kernel(const float4* __restrict__ src, float4* __restrict__ dst,
+                                                       int64_t n4) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (int64_t)gridDim.x * blockDim.x)
+        dst[i] = src[i];
+}
+}  // namespace gsx_amd
+
 namespace {
 
 thread_local char g_message[256] = "";
@@ -31,6 +40,14 @@ gsx_hip_status fail(gsx_hip_status code, const char* what) {
     snprintf(g_message, sizeof(g_message), "%s", what);
     return code;
 }
+
+}  // namespace
+
+namespace gsx_amd {
+void set_last_error(const char* what) { snprintf(g_message, sizeof(g_message), "%s", what); }
+}  // namespace gsx_amd
+
+namespace {
 
 gsx_hip_status hip_fail(hipError_t e, const char* what) {
     snprintf(g_message, sizeof(g_message), "%s: %s", what, hipGetErrorString(e));
@@ -281,6 +298,21 @@ gsx_hip_status gsx_hip_fill_f32(float* dst, int64_t count, float value, hipStrea
     if (dst == nullptr) return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "dst must be non-null");
     hipLaunchKernelGGL(fill_f32_kernel, dim3(blocks_for(count, 256)), dim3(256), 0, stream, dst, count, value);
     GSX_HIP_TRY(hipGetLastError(), "fill_f32_kernel");
+    return GSX_HIP_SUCCESS;
+}
+
+gsx_hip_status gsx_hip_copy_f32(float* dst, const float* src, int64_t count, hipStream_t stream) {
+    if (count <= 0) return GSX_HIP_SUCCESS;
+    if (dst == nullptr || src == nullptr || (count & 3) != 0 ||
+        ((reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src)) & 15u) != 0) {
+        return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "copy needs 16-byte aligned buffers and a multiple of 4 floats");
+    }
+    const int64_t n4 = count / 4;
+    unsigned blocks = blocks_for(n4, 256);
+    if (blocks > 8192) blocks = 8192;
+    hipLaunchKernelGGL(copy_f32_kernel, dim3(blocks), dim3(256), 0, stream, reinterpret_cast<const float4*>(src),
+                       reinterpret_cast<float4*>(dst), n4);
+    GSX_HIP_TRY(hipGetLastError(), "copy_f32_kernel");
     return GSX_HIP_SUCCESS;
 }
 

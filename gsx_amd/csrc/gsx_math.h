@@ -10,7 +10,7 @@
  * 0x1.8p52 shift. x86-64 glibc dispatches to its FMA build on FMA-capable CPUs, so the
  * reduction and the polynomial use fused multiply-adds at exactly the points that build
  * fuses them. The restatement was compared against the host's glibc expf for all 2^32
- * float inputs with zero mismatches; tests/test_math_pins.py repeats that check.
+ * float inputs with zero mismatches; tests/test_oracle_cpu.py repeats that check.
  *
  * Every function here is pure IEEE arithmetic and must be compiled without floating-point
  * contraction (-ffp-contract=off): the explicit fma() calls are the only fused operations.
@@ -41,8 +41,8 @@ __host__ __device__ inline uint64_t gsx_exp2_table_entry(uint32_t i)
 static inline uint64_t gsx_exp2_table_entry(uint32_t i)
 #endif
 {
-    /* A switch keeps the table in instruction immediates on the GPU (no constant-memory
-     * load on the hot path of the blend). */
+    /* Values as immediates; kernels with many expf calls per lane copy them to LDS once and
+     * use gsx_expf_table (see below). */
     switch(i & 31u) {
     case 0: return 0x3ff0000000000000ULL;
     case 1: return 0x3fefd9b0d3158574ULL;
@@ -123,8 +123,10 @@ GSX_HD double gsx_f64_from_bits(uint64_t u)
 #endif
 }
 
-/* expf with glibc's (FMA build) results for every float input. */
-GSX_HD float gsx_expf(float x)
+/* expf with glibc's (FMA build) results for every float input. `table` supplies the 32
+ * entries of gsx_exp2_table_entry (a kernel stages them in LDS: a per-lane switch would become
+ * a divergent branch tree); pass NULL to use the switch. */
+GSX_HD float gsx_expf_table(float x, const uint64_t *table)
 {
     const double inv_ln2_n = 0x1.71547652b82fep+0 * 32.0;
     const double shift = 0x1.8p+52;
@@ -161,7 +163,7 @@ GSX_HD float gsx_expf(float x)
     ki = gsx_f64_bits(kd);
     kd -= shift;
     r = GSX_FMA(inv_ln2_n, xd, -kd);
-    t = gsx_exp2_table_entry((uint32_t)(ki % 32u));
+    t = table != 0 ? table[ki % 32u] : gsx_exp2_table_entry((uint32_t)(ki % 32u));
     t += ki << (52 - GSX_EXP2_TABLE_BITS);
     s = gsx_f64_from_bits(t);
     z = GSX_FMA(c0, r, c1);
@@ -170,6 +172,11 @@ GSX_HD float gsx_expf(float x)
     y = GSX_FMA(z, r2, y);
     y = y * s;
     return (float)y;
+}
+
+GSX_HD float gsx_expf(float x)
+{
+    return gsx_expf_table(x, 0);
 }
 
 /* PCG32 as in gsx/src/pcg32.h:41-119 (O'Neill's pcg32 with the tiny-cuda-nn packaging):

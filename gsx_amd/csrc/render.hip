@@ -175,9 +175,11 @@ __global__ __launch_bounds__(kBlendThreads) void blend_forward_kernel(
     __shared__ float4 s_r0[kBlendThreads];
     __shared__ float4 s_r1[kBlendThreads];
     __shared__ float4 s_r2[kBlendThreads];
+    __shared__ uint64_t s_exp2[GSX_EXP2_TABLE_SIZE];
     const int tiles = cam.tiles_x * cam.tiles_y;
     const int tile = xcd_tile_index(blockIdx.x, tiles);
     if (tile >= tiles) return;
+    if (threadIdx.x < GSX_EXP2_TABLE_SIZE) s_exp2[threadIdx.x] = gsx_exp2_table_entry(threadIdx.x);
     const int tx = tile % cam.tiles_x, ty = tile / cam.tiles_x;
     const int px = tx * kTile + (threadIdx.x & (kTile - 1));
     const int py = ty * kTile + (threadIdx.x / kTile);
@@ -213,7 +215,7 @@ __global__ __launch_bounds__(kBlendThreads) void blend_forward_kernel(
                 float power = -0.5f * (r0.z * dx * dx + r0.w * dx * dy + r1.x * dy * dy);
                 if (power > 0.0f) power = 0.0f;
                 if (power < kPowerThreshold) continue;
-                const float alpha = fminf(kMaxFragmentAlpha, r1.y * gsx_expf(power));
+                const float alpha = fminf(kMaxFragmentAlpha, r1.y * gsx_expf_table(power, s_exp2));
                 if (alpha < kMinAlpha) continue;
                 const float w = alpha * t;
                 c0 += w * r1.z;
@@ -272,10 +274,12 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
     __shared__ float2 s_k1[kBlendThreads];
     __shared__ uint32_t s_pos[kBlendThreads];
     __shared__ float s_acc[kWavesPerTile][kBucket][kGrad2d];
+    __shared__ uint64_t s_exp2[GSX_EXP2_TABLE_SIZE];
     __shared__ uint32_t s_max_last;
     const int tiles = cam.tiles_x * cam.tiles_y;
     const int tile = xcd_tile_index(blockIdx.x, tiles);
     if (tile >= tiles) return;
+    if (threadIdx.x < GSX_EXP2_TABLE_SIZE) s_exp2[threadIdx.x] = gsx_exp2_table_entry(threadIdx.x);
     const int tx = tile % cam.tiles_x, ty = tile / cam.tiles_x;
     const int px = tx * kTile + (threadIdx.x & (kTile - 1));
     const int py = ty * kTile + (threadIdx.x / kTile);
@@ -352,7 +356,7 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
                             float power = -0.5f * (r0.z * dx * dx + r0.w * dx * dy + r1.x * dy * dy);
                             if (power > 0.0f) power = 0.0f;
                             if (power >= kPowerThreshold) {
-                                const float gval = gsx_expf(power);
+                                const float gval = gsx_expf_table(power, s_exp2);
                                 const float alpha = fminf(kMaxFragmentAlpha, r1.y * gval);
                                 if (alpha >= kMinAlpha) {
                                     mask |= 1u << i;

@@ -55,6 +55,9 @@ gsx_hip_status gsx_hip_stream_destroy(hipStream_t stream);
 gsx_hip_status gsx_hip_stream_synchronize(hipStream_t stream);
 /* Fill `count` floats with `value` (a kernel, not hipMemset, so it is safe under graph capture). */
 gsx_hip_status gsx_hip_fill_f32(float* dst, int64_t count, float value, hipStream_t stream);
+/* Streaming device copy of `count` floats (16-byte aligned, count % 4 == 0); also the known-size
+ * reference kernel against which HBM traffic counters are calibrated. */
+gsx_hip_status gsx_hip_copy_f32(float* dst, const float* src, int64_t count, hipStream_t stream);
 
 /* ---- render ---------------------------------------------------------------------------------
  * Replaces gsx_cuda_fastgs_forward_launch / gsx_cuda_fastgs_backward_launch
@@ -218,6 +221,60 @@ gsx_hip_status gsx_hip_adam_step_f32_kernel_launch(float* parameter, const float
  * per group, gsx/src/gsx-cuda/optim.c:757-796). */
 gsx_hip_status gsx_hip_adam_step_multi_launch(const gsx_hip_adam_group* groups, int32_t group_count,
                                               hipStream_t stream);
+
+/* ---- adaptive density control -----------------------------------------------------------------
+ * Replaces the CUDA thrust pipeline (gsx/src/gsx-cuda/adc.cu:757-927) with the semantics of
+ * the CPU default/ABSGS refine and opacity reset (gsx/src/gsx-cpu/adc/default.c:160-527,
+ * gsx/src/gsx-cpu/adc.c:48-80, 380-559): identical grow/split/prune decisions and row order;
+ * split k draws the CPU's pcg32 stream advanced by 12 * k draws. */
+#define GSX_HIP_ADC_MAX_FIELDS 16
+typedef struct gsx_hip_adc_params {
+    int32_t algorithm; /* 0 GSX_ADC_ALGORITHM_DEFAULT, 1 GSX_ADC_ALGORITHM_ABSGS */
+    float pruning_opacity_threshold;
+    float opacity_clamp_value;
+    float max_world_scale;
+    float max_screen_scale;
+    float duplicate_grad_threshold;
+    float duplicate_scale_threshold;
+    float duplicate_absgrad_threshold;
+    float scene_scale;
+    int64_t refine_every, start_refine, end_refine, max_num_gaussians, reset_every;
+} gsx_hip_adc_params;
+
+/* Rows of a Gaussian set on the device (the gsx_gs fields, gsx/include/gsx/gsx-core.h:286-308)
+ * plus the Adam moments of each parameter field, all nullable except mean3d..sh0. Moment index
+ * k follows the field order mean3d, rotation, logscale, opacity, sh0, sh1, sh2, sh3. */
+typedef struct gsx_hip_gs_rows {
+    int64_t count;
+    int32_t sh_degree;
+    float *mean3d, *rotation, *logscale, *opacity, *sh0, *sh1, *sh2, *sh3;
+    float *grad_acc, *absgrad_acc, *visible_counter, *max_screen_radius;
+    float *first_moment[8];
+    float *second_moment[8];
+} gsx_hip_gs_rows;
+
+typedef struct gsx_hip_adc_context gsx_hip_adc_context;
+/* The context owns the split RNG (pcg32 seeded (seed, seed), gsx/src/gsx-cpu/adc.c:466) and
+ * the scratch buffers; the RNG advances across steps like the CPU adc object's. */
+gsx_hip_status gsx_hip_adc_context_create(gsx_hip_adc_context** out_context, uint64_t seed);
+gsx_hip_status gsx_hip_adc_context_destroy(gsx_hip_adc_context* context);
+/* One gsx_adc_step at global_step. Growth appends rows in place, so every buffer of `rows` needs
+ * `capacity` >= count + (max_num_gaussians - count) rows; when rows are pruned the compacted set
+ * is written to `out` (same fields bound) and *out_result_in_out = 1, otherwise the result stays
+ * in `rows`. The final count is stored in the result's `count`. out_counts[4] = pruned,
+ * duplicated, grown (split), reset, as gsx_adc_result. Synchronises the stream twice per refine
+ * (candidate and survivor counts). */
+gsx_hip_status gsx_hip_adc_step(gsx_hip_adc_context* context, const gsx_hip_adc_params* params, uint64_t global_step,
+                                gsx_hip_gs_rows* rows, int64_t capacity, gsx_hip_gs_rows* out,
+                                int32_t* out_result_in_out, int64_t* out_counts, hipStream_t stream);
+
+/* Replaces gsx_cuda_gather_rows_kernel_launch (gsx/src/gsx-cuda/internal.h:372-381): out row r
+ * = src row src_indices[r]; an index outside [0, src_row_count) sets *out_has_out_of_range
+ * (a device int, may be null; the CPU returns GSX_ERROR_OUT_OF_RANGE, gsx-cpu/core.c:1322-1324).
+ * No host synchronisation. */
+gsx_hip_status gsx_hip_gather_rows_kernel_launch(const void* src, void* dst, int64_t row_bytes, int64_t row_count,
+                                                 const int32_t* src_indices, int64_t src_row_count,
+                                                 int* out_has_out_of_range, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -1243,6 +1243,7 @@ typedef struct oracle_adc_params {
     float scene_scale;
     int64_t refine_every, start_refine, end_refine, max_num_gaussians, reset_every, global_step;
     uint64_t seed;
+    uint64_t rng_draws_consumed; /* draws earlier steps took from the adc object's stream */
 } oracle_adc_params;
 
 static float host_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
@@ -1311,6 +1312,7 @@ int64_t oracle_adc_step(int64_t n, float **fields, float **moments, float **aux,
 
     counts[0] = counts[1] = counts[2] = counts[3] = 0;
     gsx_pcg32_seed2(&rng, p->seed, p->seed);
+    gsx_pcg32_advance(&rng, p->rng_draws_consumed);
     n_after = n;
     if(in_refine_window(p) && n > 0) {
         if(acc == NULL) return -1;

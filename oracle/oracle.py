@@ -44,7 +44,8 @@ class AdcParams(ctypes.Structure):
                 ("max_world_scale", _f), ("duplicate_grad_threshold", _f), ("duplicate_scale_threshold", _f),
                 ("duplicate_absgrad_threshold", _f), ("scene_scale", _f), ("refine_every", _i64),
                 ("start_refine", _i64), ("end_refine", _i64), ("max_num_gaussians", _i64),
-                ("reset_every", _i64), ("global_step", _i64), ("seed", ctypes.c_uint64)]
+                ("reset_every", _i64), ("global_step", _i64), ("seed", ctypes.c_uint64),
+                ("rng_draws_consumed", ctypes.c_uint64)]
 
 
 class Oracle:
