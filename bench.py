@@ -64,6 +64,26 @@ def algorithmic_bytes(stage, n, visible, instances, tiles, pixels, sort_passes):
 
 CPU_SAMPLE_STRIDE = 10
 
+STAGE_KERNEL = {"preprocess": "preprocess_kernel", "emit": "emit_keys_kernel", "ranges": "tile_ranges_kernel",
+                "blend_forward": "blend_forward_kernel", "blend_backward": "blend_backward_kernel",
+                "instance_reduce": "reduce_instance_grads_kernel",
+                "projection_backward": "projection_backward_kernel", "loss_forward": "ssim_forward_kernel",
+                "loss_backward": "ssim_backward_kernel", "adam": "adam_multi_kernel"}
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_metric.txt")
+
+
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+    summary (already scaled by the copy-kernel calibration there), or None."""
+    if kernel is None or not os.path.exists(TRAFFIC_FILE):
+        return None
+    with open(TRAFFIC_FILE) as f:
+        for line in f:
+            parts = line.split()
+            if len(parts) >= 4 and parts[0] == "traffic" and parts[1] == kernel:
+                return int(float(parts[-1]))
+    return None
+
 
 def cpu_baseline(scene, camera_block, target, iters):
     """Time the unmodified gsx CPU backend (oracle/_ref) on a bounded sample of the workload:
@@ -259,8 +279,10 @@ def main():
         "sort_gbps": sort_entry["gbps"],
         "sort_hbm_frac": sort_entry["hbm_frac"],
         "kernels": kernels,
-        "roofline": {"bound": "hbm", "kernel": dominant["stage"], "achieved": dominant["gbps"],
-                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": dominant["hbm_frac"], "traffic": None},
+        "roofline": {"bound": "hbm", "kernel": STAGE_KERNEL.get(dominant["stage"], dominant["stage"]),
+                     "achieved": dominant["gbps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": dominant["hbm_frac"], "traffic": measured_traffic(STAGE_KERNEL.get(dominant["stage"])),
+                     "algorithmic_bytes": dominant["algorithmic_bytes"], "launch_ms": dominant["ms"]},
         "device": dev_name,
     }
 

@@ -101,6 +101,9 @@ struct DeviceBuffer {
     }
 };
 
+// Workgroups of the big-box passes (grid-stride over the list of big boxes).
+constexpr unsigned kBigBlocks = 1024;
+
 unsigned blocks_for(int64_t n, int threads) {
     int64_t b = (n + threads - 1) / threads;
     return (unsigned)(b < 1 ? 1 : b);
@@ -161,8 +164,8 @@ int bits_for(uint32_t v) {
 }  // namespace
 
 struct gsx_hip_render_context {
-    DeviceBuffer rec, cov_coef, ckpt, inst_gauss, inst_grad, tile_count, offsets, scan_temp, keys, vals, keys_alt, vals_alt, sort_temp, ranges, final_t,
-        last, grad2d;
+    DeviceBuffer rec, cov_coef, ckpt, inst_gauss, inst_grad, tile_count, big_list, offsets, scan_temp, keys, vals,
+        keys_alt, vals_alt, sort_temp, ranges, final_t, last, grad2d;
     uint32_t* host_count = nullptr;  // pinned
     CameraParams cam{};
     gsx_hip_gaussians gs{};
@@ -441,6 +444,8 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     GSX_TRY(ctx->rec.reserve((size_t)(n > 0 ? n : 1) * 3 * sizeof(float4), "rec"));
     if (train) GSX_TRY(ctx->cov_coef.reserve((size_t)(n > 0 ? n : 1) * 2 * sizeof(float4), "cov_coef"));
     GSX_TRY(ctx->tile_count.reserve((size_t)(n > 0 ? n : 1) * sizeof(uint32_t), "tile_count"));
+    // [0] = number of big boxes, [1..n] = their Gaussians
+    GSX_TRY(ctx->big_list.reserve((size_t)(n + 1) * sizeof(uint32_t), "big_list"));
     GSX_TRY(ctx->offsets.reserve((size_t)(n + 1) * sizeof(uint32_t), "offsets"));
     GSX_TRY(ctx->scan_temp.reserve(gsx_hip_scan_temp_bytes(n), "scan_temp"));
     GSX_TRY(ctx->ranges.reserve((size_t)tiles * sizeof(uint2), "ranges"));
@@ -454,12 +459,19 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     }
     GSX_TRY(record(ctx, 0, stream));
     if (n > 0) {
+        hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(64), 0, stream, ctx->big_list.as<uint32_t>(), (int64_t)1,
+                           0u);
         hipLaunchKernelGGL(preprocess_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, n, gaussians->mean3d,
                            gaussians->rotation, gaussians->logscale, gaussians->opacity, gaussians->sh0,
                            gaussians->sh1, gaussians->sh2, gaussians->sh3, (int)gaussians->sh_degree, cam,
                            ctx->rec.as<float4>(), train ? ctx->cov_coef.as<float4>() : nullptr,
-                           ctx->tile_count.as<uint32_t>(), train ? visible_counter : nullptr);
+                           ctx->tile_count.as<uint32_t>(), train ? visible_counter : nullptr,
+                           ctx->big_list.as<uint32_t>() + 1, ctx->big_list.as<uint32_t>());
         GSX_HIP_TRY(hipGetLastError(), "preprocess_kernel");
+        hipLaunchKernelGGL(big_tiles_kernel<false>, dim3(kBigBlocks), dim3(256), 0, stream,
+                           ctx->big_list.as<uint32_t>() + 1, ctx->big_list.as<uint32_t>(), ctx->rec.as<float4>(),
+                           cam.tiles_x, ctx->tile_count.as<uint32_t>(), nullptr, nullptr, nullptr, nullptr);
+        GSX_HIP_TRY(hipGetLastError(), "big_tiles_kernel<count>");
     }
     GSX_TRY(record(ctx, 1, stream));
     GSX_TRY(gsx_hip_scan_exclusive_u32(ctx->tile_count.as<uint32_t>(), ctx->offsets.as<uint32_t>(), n,
@@ -486,6 +498,11 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
                            ctx->tile_count.as<uint32_t>(), ctx->offsets.as<uint32_t>(), cam.tiles_x,
                            ctx->keys.as<uint64_t>(), ctx->vals.as<uint32_t>(), ctx->inst_gauss.as<uint32_t>());
         GSX_HIP_TRY(hipGetLastError(), "emit_keys_kernel");
+        hipLaunchKernelGGL(big_tiles_kernel<true>, dim3(kBigBlocks), dim3(256), 0, stream,
+                           ctx->big_list.as<uint32_t>() + 1, ctx->big_list.as<uint32_t>(), ctx->rec.as<float4>(),
+                           cam.tiles_x, nullptr, ctx->offsets.as<uint32_t>(), ctx->keys.as<uint64_t>(),
+                           ctx->vals.as<uint32_t>(), ctx->inst_gauss.as<uint32_t>());
+        GSX_HIP_TRY(hipGetLastError(), "big_tiles_kernel<emit>");
     }
     GSX_TRY(record(ctx, 3, stream));
     int in_alt = 0;

@@ -10,6 +10,7 @@
 #include <stdint.h>
 
 #include "gsx_math.h"
+#include "tile_cull.h"
 
 namespace gsx_amd {
 

@@ -25,92 +25,254 @@ constexpr int kBlendThreads = kTilePixels;  // 256: one pixel per thread, 4 wave
 // Preprocess: render.c:850-1016 per Gaussian (culls, EWA projection, box, sigmoid, SH colour),
 // plus the tile count of the box and, for TRAIN forwards, visible_counter += 1 (:980-982).
 // ---------------------------------------------------------------------------------------------
+// ---------------------------------------------------------------------------------------------
+// Kept tiles (tile_cull.h). The tiles of the boxes of a wave's 64 Gaussians are walked as one
+// flattened sequence, 64 (Gaussian, tile) pairs per step, so lanes stay busy whatever the box
+// sizes (a near-plane Gaussian can cover the whole image, most cover a handful of tiles). Each
+// lane's box lives in LDS; a lane finds the owner of its pair by binary search over the wave's
+// exclusive prefix of box sizes. Owners occupy contiguous lanes of a step, so ranks among kept
+// pairs come from one ballot; per-owner running counts live in LDS (LDS operations of one wave
+// complete in order).
+// ---------------------------------------------------------------------------------------------
+constexpr int kWavesPerBlock = 4;
+// Boxes of more tiles than this are walked by a whole workgroup in a pass of their own (see
+// big_tiles_kernel): a wave holding a full-image box would otherwise serialise hundreds of steps.
+constexpr uint32_t kBigTiles = 256;
+
+__device__ inline uint32_t box_tiles(float4 r2) {
+    const uint32_t bx = __float_as_uint(r2.y), by = __float_as_uint(r2.z);
+    return ((bx >> 16) / kTile - (bx & 0xffffu) / kTile + 1) * ((by >> 16) / kTile - (by & 0xffffu) / kTile + 1);
+}
+
+struct WaveBoxes {
+    float mx[kWave], my[kWave], a[kWave], b[kWave], c[kWave], qcut[kWave];
+    int32_t x0[kWave], x1[kWave], y0[kWave], y1[kWave];
+    uint32_t tx0[kWave], ty0[kWave], wx[kWave], excl[kWave], kept[kWave], out[kWave];
+    uint64_t depth[kWave];
+    uint32_t g[kWave];
+};
+
+// Stores lane's box (zero tiles when !valid) and returns the wave's total tile count.
+__device__ inline uint32_t stage_box(WaveBoxes& w, bool valid, float4 r0, float4 r1, float4 r2, uint32_t g,
+                                     uint32_t out) {
+    const uint32_t lane = __lane_id();
+    uint32_t total = 0;
+    if (valid) {
+        const uint32_t bx = __float_as_uint(r2.y), by = __float_as_uint(r2.z);
+        const int x0 = (int)(bx & 0xffffu), x1 = (int)(bx >> 16), y0 = (int)(by & 0xffffu), y1 = (int)(by >> 16);
+        w.mx[lane] = r0.x;
+        w.my[lane] = r0.y;
+        w.a[lane] = r0.z;
+        w.b[lane] = r0.w * 0.5f;  // the record holds 2 * inv_b (exact)
+        w.c[lane] = r1.x;
+        w.qcut[lane] = gsx_tile_qcut(r1.y);
+        w.x0[lane] = x0;
+        w.x1[lane] = x1;
+        w.y0[lane] = y0;
+        w.y1[lane] = y1;
+        w.tx0[lane] = (uint32_t)x0 / kTile;
+        w.ty0[lane] = (uint32_t)y0 / kTile;
+        w.wx[lane] = (uint32_t)x1 / kTile - (uint32_t)x0 / kTile + 1;
+        w.depth[lane] = (uint64_t)__float_as_uint(r2.w);
+        total = w.wx[lane] * ((uint32_t)y1 / kTile - (uint32_t)y0 / kTile + 1);
+    }
+    w.g[lane] = g;
+    w.out[lane] = out;
+    w.kept[lane] = 0;
+    // inclusive wave scan of the box sizes
+    uint32_t incl = total;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+        const uint32_t t = (uint32_t)__shfl_up((int)incl, d, kWave);
+        if ((int)lane >= d) incl += t;
+    }
+    w.excl[lane] = incl - total;
+    __builtin_amdgcn_wave_barrier();
+    return (uint32_t)__shfl((int)incl, kWave - 1, kWave);
+}
+
+// Walks the wave's flattened tiles. kEmit: writes kept instances (key, value = position,
+// instance_gaussian) at out[owner] + rank; always accumulates kept[owner].
+template <bool kEmit>
+__device__ inline void walk_wave_tiles(WaveBoxes& w, uint32_t wave_total, int32_t tiles_x,
+                                       uint64_t* __restrict__ keys, uint32_t* __restrict__ values,
+                                       uint32_t* __restrict__ instance_gaussian) {
+    const uint32_t lane = __lane_id();
+    const uint64_t lt = lanemask_lt();
+    for (uint32_t base = 0; base < wave_total; base += kWave) {
+        const uint32_t p = base + lane;
+        const bool active = p < wave_total;
+        uint32_t owner = 0;
+#pragma unroll
+        for (uint32_t step = kWave / 2; step > 0; step >>= 1) {
+            if (w.excl[owner + step] <= p) owner += step;
+        }
+        bool keep = false;
+        uint32_t tile = 0;
+        if (active) {
+            const uint32_t k = p - w.excl[owner];
+            const uint32_t wx = w.wx[owner];
+            const uint32_t ty = w.ty0[owner] + k / wx;
+            const uint32_t tx = w.tx0[owner] + k % wx;
+            tile = ty * (uint32_t)tiles_x + tx;
+            const int px0 = max((int)tx * kTile, w.x0[owner]), px1 = min((int)tx * kTile + kTile - 1, w.x1[owner]);
+            const int py0 = max((int)ty * kTile, w.y0[owner]), py1 = min((int)ty * kTile + kTile - 1, w.y1[owner]);
+            keep = gsx_tile_may_contribute(w.mx[owner], w.my[owner], w.a[owner], w.b[owner], w.c[owner],
+                                           w.qcut[owner], px0, px1, py0, py1) != 0;
+        }
+        const uint64_t mask = __ballot(keep);
+        // first lane of this step holding the owner's pairs
+        const uint32_t seg_first = w.excl[owner] > base ? w.excl[owner] - base : 0u;
+        const uint64_t seg = ~((seg_first == 0 ? 0ull : (~0ull >> (64 - seg_first))));
+        const uint32_t before = w.kept[owner];
+        if (kEmit && keep) {
+            const uint32_t pos = w.out[owner] + before + (uint32_t)__popcll(mask & lt & seg);
+            keys[pos] = ((uint64_t)tile << 32) | w.depth[owner];
+            values[pos] = pos;
+            instance_gaussian[pos] = w.g[owner];
+        }
+        // the last lane of each owner segment advances that owner's running count
+        const uint32_t next_owner = (uint32_t)__shfl_down((int)owner, 1, kWave);
+        const bool seg_last = active && (lane == kWave - 1 || p + 1 >= wave_total || next_owner != owner);
+        if (seg_last) w.kept[owner] = before + (uint32_t)__popcll(mask & (lt | (1ull << lane)) & seg);
+        __builtin_amdgcn_wave_barrier();
+    }
+}
+
 __global__ __launch_bounds__(256) void preprocess_kernel(
     int64_t n, const float* __restrict__ mean3d, const float* __restrict__ rotation,
     const float* __restrict__ logscale, const float* __restrict__ opacity, const float* __restrict__ sh0,
     const float* __restrict__ sh1, const float* __restrict__ sh2, const float* __restrict__ sh3, int sh_degree,
     CameraParams cam, float4* __restrict__ rec, float4* __restrict__ cov_coef, uint32_t* __restrict__ tile_count,
-    float* __restrict__ visible_counter) {
+    float* __restrict__ visible_counter, uint32_t* __restrict__ big_list, uint32_t* __restrict__ big_count) {
+    __shared__ WaveBoxes s_boxes[kWavesPerBlock];
+    WaveBoxes& wb = s_boxes[threadIdx.x / kWave];
     const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (g >= n) return;
-    const Projected p =
-        preprocess_one(g, mean3d, rotation, logscale, opacity, sh0, sh1, sh2, sh3, sh_degree, cam, true);
-    if (!p.visible) {
-        tile_count[g] = 0;
-        return;
+    bool visible = false;
+    float4 r0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), r1 = r0, r2 = r0;
+    if (g < n) {
+        const Projected p =
+            preprocess_one(g, mean3d, rotation, logscale, opacity, sh0, sh1, sh2, sh3, sh_degree, cam, true);
+        visible = p.visible;
+        if (visible) {
+            if (visible_counter != nullptr) visible_counter[g] += 1.0f;
+            const float inv_a = p.c * p.inv_det;
+            const float inv_b = -p.b * p.inv_det;
+            const float inv_c = p.a * p.inv_det;
+            const uint32_t bx = (uint32_t)p.x_min | ((uint32_t)p.x_max << 16);
+            const uint32_t by = (uint32_t)p.y_min | ((uint32_t)p.y_max << 16);
+            r0 = make_float4(p.mx, p.my, inv_a, 2.0f * inv_b);
+            r1 = make_float4(inv_c, p.opacity, p.color[0], p.color[1]);
+            r2 = make_float4(p.color[2], __uint_as_float(bx), __uint_as_float(by), p.depth);
+            rec[3 * g + 0] = r0;
+            rec[3 * g + 1] = r1;
+            rec[3 * g + 2] = r2;
+            if (cov_coef != nullptr) {
+                // d(conic)/d(cov2d) coefficients with the CPU's rounding (render.c:1578-1579,
+                // 1647-1655): the backward applies them per contribution, as the CPU does,
+                // because for near-plane Gaussians with huge footprints the map is close to
+                // singular and summing the conic gradients first would round very differently.
+                const float det = p.a * p.c - p.b * p.b;
+                const float k = 1.0f / (det * det);
+                cov_coef[2 * g + 0] =
+                    make_float4(-p.c * p.c * k, p.b * p.c * k, -p.b * p.b * k, -(p.a * p.c + p.b * p.b) * k);
+                cov_coef[2 * g + 1] = make_float4(p.a * p.b * k, -p.a * p.a * k, 0.0f, 0.0f);
+            }
+        }
     }
-    if (visible_counter != nullptr) visible_counter[g] += 1.0f;
-    const float inv_a = p.c * p.inv_det;
-    const float inv_b = -p.b * p.inv_det;
-    const float inv_c = p.a * p.inv_det;
-    const uint32_t bx = (uint32_t)p.x_min | ((uint32_t)p.x_max << 16);
-    const uint32_t by = (uint32_t)p.y_min | ((uint32_t)p.y_max << 16);
-    rec[3 * g + 0] = make_float4(p.mx, p.my, inv_a, 2.0f * inv_b);
-    rec[3 * g + 1] = make_float4(inv_c, p.opacity, p.color[0], p.color[1]);
-    rec[3 * g + 2] = make_float4(p.color[2], __uint_as_float(bx), __uint_as_float(by), p.depth);
-    if (cov_coef != nullptr) {
-        // d(conic)/d(cov2d) coefficients with the CPU's rounding (render.c:1578-1579, 1647-1655):
-        // the backward applies them per contribution, as the CPU does, because for near-plane
-        // Gaussians with huge footprints the map is close to singular and summing the conic
-        // gradients first would round very differently.
-        const float det = p.a * p.c - p.b * p.b;
-        const float k = 1.0f / (det * det);
-        cov_coef[2 * g + 0] = make_float4(-p.c * p.c * k, p.b * p.c * k, -p.b * p.b * k, -(p.a * p.c + p.b * p.b) * k);
-        cov_coef[2 * g + 1] = make_float4(p.a * p.b * k, -p.a * p.a * k, 0.0f, 0.0f);
-    }
-    const uint32_t tx0 = (uint32_t)p.x_min / kTile, tx1 = (uint32_t)p.x_max / kTile;
-    const uint32_t ty0 = (uint32_t)p.y_min / kTile, ty1 = (uint32_t)p.y_max / kTile;
-    tile_count[g] = (tx1 - tx0 + 1) * (ty1 - ty0 + 1);
+    const bool big = visible && box_tiles(r2) > kBigTiles;
+    if (big) big_list[atomicAdd(big_count, 1u)] = (uint32_t)g;  // counted by big_tiles_kernel
+    const uint32_t total = stage_box(wb, visible && !big, r0, r1, r2, (uint32_t)g, 0u);
+    walk_wave_tiles<false>(wb, total, cam.tiles_x, nullptr, nullptr, nullptr);
+    if (g < n && !big) tile_count[g] = wb.kept[__lane_id()];
 }
 
 // ---------------------------------------------------------------------------------------------
 // Key emission: Gaussian g owns positions offset[g] .. offset[g+1]) of the instance array, one
-// per tile of its box in row-major tile order; key = tile << 32 | bits(depth). Offsets come from
-// an exclusive scan in Gaussian order, so equal keys appear in ascending Gaussian order and a
-// stable sort reproduces the CPU (depth, index) order per tile. The sorted value is the emission
-// position; instance_gaussian[position] = g. Boxes of more than 32 tiles (near-plane Gaussians
-// can cover the whole image) are written by the whole wave instead of one lane.
+// per kept tile of its box in row-major tile order; key = tile << 32 | bits(depth). Offsets come
+// from an exclusive scan in Gaussian order, so equal keys appear in ascending Gaussian order and
+// a stable sort reproduces the CPU (depth, index) order per tile. The sorted value is the
+// emission position; instance_gaussian[position] = g.
 // ---------------------------------------------------------------------------------------------
-__device__ inline void emit_range(uint32_t g, uint32_t o, uint32_t bx, uint32_t by, uint64_t depth_bits,
-                                  int32_t tiles_x, uint32_t first, uint32_t stride, uint64_t* __restrict__ keys,
-                                  uint32_t* __restrict__ values, uint32_t* __restrict__ instance_gaussian) {
-    const uint32_t tx0 = (bx & 0xffffu) / kTile, tx1 = (bx >> 16) / kTile;
-    const uint32_t ty0 = (by & 0xffffu) / kTile, ty1 = (by >> 16) / kTile;
-    const uint32_t wx = tx1 - tx0 + 1;
-    const uint32_t total = wx * (ty1 - ty0 + 1);
-    for (uint32_t k = first; k < total; k += stride) {
-        const uint32_t ty = ty0 + k / wx;
-        const uint32_t tx = tx0 + k % wx;
-        const uint64_t tile = (uint64_t)ty * (uint64_t)tiles_x + tx;
-        keys[o + k] = (tile << 32) | depth_bits;
-        values[o + k] = o + k;
-        instance_gaussian[o + k] = g;
-    }
-}
-
 __global__ __launch_bounds__(256) void emit_keys_kernel(int64_t n, const float4* __restrict__ rec,
                                                         const uint32_t* __restrict__ tile_count,
                                                         const uint32_t* __restrict__ offsets, int32_t tiles_x,
                                                         uint64_t* __restrict__ keys, uint32_t* __restrict__ values,
                                                         uint32_t* __restrict__ instance_gaussian) {
-    constexpr uint32_t kWaveEmit = 32;
+    __shared__ WaveBoxes s_boxes[kWavesPerBlock];
+    WaveBoxes& wb = s_boxes[threadIdx.x / kWave];
     const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const uint32_t count = g < n ? tile_count[g] : 0u;
-    if (count > 0 && count <= kWaveEmit) {
-        const float4 r2 = rec[3 * g + 2];
-        emit_range((uint32_t)g, offsets[g], __float_as_uint(r2.y), __float_as_uint(r2.z),
-                   (uint64_t)__float_as_uint(r2.w), tiles_x, 0u, 1u, keys, values, instance_gaussian);
+    bool any = g < n && tile_count[g] > 0;
+    float4 r0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), r1 = r0, r2 = r0;
+    uint32_t o = 0;
+    if (any) {
+        r2 = rec[3 * g + 2];
+        any = box_tiles(r2) <= kBigTiles;  // big boxes are emitted by big_tiles_kernel
     }
-    uint64_t big = __ballot(count > kWaveEmit);
-    const uint32_t lane = __lane_id();
-    const int64_t wave_base = g - (int64_t)lane;
-    while (big != 0ull) {
-        const uint32_t l = (uint32_t)__builtin_ctzll(big);
-        big &= big - 1ull;
-        const int64_t gb = wave_base + l;
-        const float4 r2 = rec[3 * gb + 2];
-        emit_range((uint32_t)gb, offsets[gb], __float_as_uint(r2.y), __float_as_uint(r2.z),
-                   (uint64_t)__float_as_uint(r2.w), tiles_x, lane, (uint32_t)kWave, keys, values, instance_gaussian);
+    if (any) {
+        r0 = rec[3 * g + 0];
+        r1 = rec[3 * g + 1];
+        o = offsets[g];
+    }
+    const uint32_t total = stage_box(wb, any, r0, r1, r2, (uint32_t)g, o);
+    walk_wave_tiles<true>(wb, total, tiles_x, keys, values, instance_gaussian);
+}
+
+// Big boxes: one workgroup per Gaussian of big_list (grid-stride over the list), 256 tiles per
+// step in row-major order. kEmit = false writes tile_count[g]; kEmit = true writes the kept
+// instances at offsets[g] + rank, ranks from per-wave ballots and a 4-wave prefix.
+template <bool kEmit>
+__global__ __launch_bounds__(256) void big_tiles_kernel(const uint32_t* __restrict__ big_list,
+                                                        const uint32_t* __restrict__ big_count,
+                                                        const float4* __restrict__ rec, int32_t tiles_x,
+                                                        uint32_t* __restrict__ tile_count,
+                                                        const uint32_t* __restrict__ offsets,
+                                                        uint64_t* __restrict__ keys, uint32_t* __restrict__ values,
+                                                        uint32_t* __restrict__ instance_gaussian) {
+    __shared__ uint32_t s_wave[kWavesPerBlock];
+    const uint32_t count = *big_count;
+    const uint32_t lane = __lane_id(), wave = threadIdx.x / kWave;
+    for (uint32_t i = blockIdx.x; i < count; i += gridDim.x) {
+        const uint32_t g = big_list[i];
+        const float4 r0 = rec[3 * (size_t)g + 0], r1 = rec[3 * (size_t)g + 1], r2 = rec[3 * (size_t)g + 2];
+        const uint32_t bx = __float_as_uint(r2.y), by = __float_as_uint(r2.z);
+        const int x0 = (int)(bx & 0xffffu), x1 = (int)(bx >> 16), y0 = (int)(by & 0xffffu), y1 = (int)(by >> 16);
+        const uint32_t tx0 = (uint32_t)x0 / kTile, ty0 = (uint32_t)y0 / kTile;
+        const uint32_t wx = (uint32_t)x1 / kTile - tx0 + 1;
+        const uint32_t total = wx * ((uint32_t)y1 / kTile - ty0 + 1);
+        const float qcut = gsx_tile_qcut(r1.y);
+        const uint64_t depth = (uint64_t)__float_as_uint(r2.w);
+        const uint32_t o = kEmit ? offsets[g] : 0u;
+        uint32_t running = 0;
+        for (uint32_t base = 0; base < total; base += blockDim.x) {
+            const uint32_t k = base + threadIdx.x;
+            bool keep = false;
+            uint32_t tile = 0;
+            if (k < total) {
+                const uint32_t ty = ty0 + k / wx, tx = tx0 + k % wx;
+                tile = ty * (uint32_t)tiles_x + tx;
+                const int px0 = max((int)tx * kTile, x0), px1 = min((int)tx * kTile + kTile - 1, x1);
+                const int py0 = max((int)ty * kTile, y0), py1 = min((int)ty * kTile + kTile - 1, y1);
+                keep = gsx_tile_may_contribute(r0.x, r0.y, r0.z, r0.w * 0.5f, r1.x, qcut, px0, px1, py0, py1) != 0;
+            }
+            const uint64_t mask = __ballot(keep);
+            if (lane == 0) s_wave[wave] = (uint32_t)__popcll(mask);
+            __syncthreads();
+            uint32_t before = 0, step_total = 0;
+            for (int w = 0; w < kWavesPerBlock; ++w) {
+                before += w < (int)wave ? s_wave[w] : 0u;
+                step_total += s_wave[w];
+            }
+            if (kEmit && keep) {
+                const uint32_t pos = o + running + before + (uint32_t)__popcll(mask & lanemask_lt());
+                keys[pos] = ((uint64_t)tile << 32) | depth;
+                values[pos] = pos;
+                instance_gaussian[pos] = g;
+            }
+            running += step_total;
+            __syncthreads();
+        }
+        if (!kEmit && threadIdx.x == 0) tile_count[g] = running;
     }
 }
 

@@ -1,0 +1,110 @@
+/*
+ * tile_cull.h - the conservative tile test of key emission, shared by the gfx950 kernels and the
+ * CPU restatement in oracle/ (both compile it with -ffp-contract=off and IEEE division, so they
+ * take the same decision bit for bit).
+ *
+ * The gsx CPU backend visits every pixel of a Gaussian's 3-sigma box (gsx/src/gsx-cpu/render.c:
+ * 1042-1079) and skips the pixel when power < -4.5 or opacity * expf(power) < 1/255, with
+ * power = -0.5 * (inv_a dx^2 + 2 inv_b dx dy + inv_c dy^2) in float. A tile of the box whose
+ * pixels all fail those tests contributes nothing to the image or to any gradient, so its
+ * (tile, Gaussian) instance can be left out of the sort. The test drops an instance only when a
+ * bound of power over the whole clipped tile rectangle (continuous, so it covers every pixel
+ * centre) lies below the skip threshold with room to spare:
+ *   thr    = max(-4.5, ln(1/255) - ln(opacity)) - 1e-3     (per Gaussian; the pixel is skipped
+ *            when power < thr + 1e-3, and the 1e-3 dwarfs every float rounding in between),
+ *   q_cut  = -2 * thr,
+ *   q_min  = minimum of the quadratic form over the rectangle (0 when it holds the centre,
+ *            otherwise the least of its four edge minima),
+ *   margin = 1e-4 * (largest term magnitude over the rectangle) + 1e-3, which exceeds the float
+ *            rounding of both q_min and the per-pixel power by orders of magnitude,
+ *   drop   iff q_min - margin > q_cut.
+ * Then every pixel centre has power <= -0.5 * (q_min - margin) < thr, so it fails a cut.
+ */
+#ifndef GSX_AMD_TILE_CULL_H
+#define GSX_AMD_TILE_CULL_H
+
+#include "gsx_math.h"
+
+GSX_HD float gsx_cull_minf(float a, float b) { return b < a ? b : a; }
+GSX_HD float gsx_cull_absf(float a) { return a < 0.0f ? -a : a; }
+GSX_HD float gsx_cull_clampf(float v, float lo, float hi) { return v < lo ? lo : (v > hi ? hi : v); }
+
+/* Natural logarithm of a positive normal float from IEEE operations only, so the CPU and the
+ * GPU agree bit for bit: x = m 2^e with m in [sqrt(1/2), sqrt(2)), ln m = 2 atanh(s),
+ * s = (m - 1) / (m + 1), |s| < 0.172, series to s^11 (relative error below 1e-7). */
+GSX_HD float gsx_cull_logf(float x)
+{
+    uint32_t u = gsx_f32_bits(x);
+    int e = (int)((u >> 23) & 0xffu) - 127;
+    float m = gsx_f32_from_bits((u & 0x007fffffu) | 0x3f800000u);
+    float s, s2, t;
+
+    if(m > 1.41421356f) {
+        m = m * 0.5f;
+        e += 1;
+    }
+    s = (m - 1.0f) / (m + 1.0f);
+    s2 = s * s;
+    t = 1.0f / 11.0f;
+    t = t * s2 + 1.0f / 9.0f;
+    t = t * s2 + 1.0f / 7.0f;
+    t = t * s2 + 1.0f / 5.0f;
+    t = t * s2 + 1.0f / 3.0f;
+    t = t * s2 + 1.0f;
+    return 2.0f * s * t + (float)e * 0.693147180559945f;
+}
+
+/* q_cut of the Gaussian with activated opacity `opacity` (> 1/255 for every visible one). */
+GSX_HD float gsx_tile_qcut(float opacity)
+{
+    float thr = -5.54126354f - gsx_cull_logf(opacity); /* ln(1/255) - ln(opacity) */
+
+    if(thr < -4.5f) {
+        thr = -4.5f;
+    }
+    return -2.0f * (thr - 1e-3f);
+}
+
+/* Minimum of A u^2 + 2 B u v + C v^2 over the segment u = ue, v in [v0, v1]; rC = 1 / C. */
+GSX_HD float gsx_cull_edge_min(float A, float B, float C, float rC, float ue, float v0, float v1)
+{
+    float q0 = A * ue * ue + 2.0f * B * ue * v0 + C * v0 * v0;
+    float q1 = A * ue * ue + 2.0f * B * ue * v1 + C * v1 * v1;
+    float m = gsx_cull_minf(q0, q1);
+
+    if(C > 0.0f) {
+        float v = gsx_cull_clampf(-(B * ue) * rC, v0, v1);
+        m = gsx_cull_minf(m, A * ue * ue + 2.0f * B * ue * v + C * v * v);
+    }
+    return m;
+}
+
+/* Nonzero when some pixel centre of the inclusive pixel rectangle [px0, px1] x [py0, py1] (the
+ * tile clipped to the Gaussian's box) may receive a contribution from the Gaussian with 2D mean
+ * (mx, my), conic (A, B, C) = (inv_a, inv_b, inv_c) and q_cut from gsx_tile_qcut. */
+GSX_HD int gsx_tile_may_contribute(float mx, float my, float A, float B, float C, float qcut, int px0, int px1,
+    int py0, int py1)
+{
+    const float dx0 = ((float)px0 + 0.5f) - mx;
+    const float dx1 = ((float)px1 + 0.5f) - mx;
+    const float dy0 = ((float)py0 + 0.5f) - my;
+    const float dy1 = ((float)py1 + 0.5f) - my;
+    const float X = gsx_cull_absf(dx0) > gsx_cull_absf(dx1) ? gsx_cull_absf(dx0) : gsx_cull_absf(dx1);
+    const float Y = gsx_cull_absf(dy0) > gsx_cull_absf(dy1) ? gsx_cull_absf(dy0) : gsx_cull_absf(dy1);
+    const float scale = gsx_cull_absf(A) * X * X + 2.0f * gsx_cull_absf(B) * X * Y + gsx_cull_absf(C) * Y * Y;
+    const float margin = 1e-4f * scale + 1e-3f;
+    const float rA = 1.0f / A;
+    const float rC = 1.0f / C;
+    float qmin;
+
+    if(dx0 <= 0.0f && dx1 >= 0.0f && dy0 <= 0.0f && dy1 >= 0.0f) {
+        return 1;
+    }
+    qmin = gsx_cull_edge_min(A, B, C, rC, dx0, dy0, dy1);
+    qmin = gsx_cull_minf(qmin, gsx_cull_edge_min(A, B, C, rC, dx1, dy0, dy1));
+    qmin = gsx_cull_minf(qmin, gsx_cull_edge_min(C, B, A, rA, dy0, dx0, dx1));
+    qmin = gsx_cull_minf(qmin, gsx_cull_edge_min(C, B, A, rA, dy1, dx0, dx1));
+    return !(qmin - margin > qcut); /* keeps the instance for NaN input too */
+}
+
+#endif /* GSX_AMD_TILE_CULL_H */

@@ -12,6 +12,7 @@
 #include "gsx_oracle.h"
 
 #include "../gsx_amd/csrc/gsx_math.h"
+#include "../gsx_amd/csrc/tile_cull.h"
 
 #include <float.h>
 #include <math.h>
@@ -462,7 +463,31 @@ static int cmp_kv(const void *pa, const void *pb)
     return 0;
 }
 
-/* Returns the instance count I; writes sorted keys/values when capacity allows (else -I-1). */
+/* Whether visible Gaussian v keeps its instance for tile (tx, ty): the tile clipped to the
+ * pixel box, tested with the conservative contribution bound shared with the kernels
+ * (gsx_amd/csrc/tile_cull.h). Dropped instances are ones whose pixels all fail the power or
+ * alpha cut of render.c:1055-1066, so the per-pixel lists lose only entries that are skipped. */
+static int tile_kept(const vis *v, int32_t tx, int32_t ty, int32_t tile_size)
+{
+    const float inv_det = v->rec[ORACLE_REC_INV_DET];
+    const float inv_a = v->rec[ORACLE_REC_COV_C] * inv_det;
+    const float inv_b = -v->rec[ORACLE_REC_COV_B] * inv_det;
+    const float inv_c = v->rec[ORACLE_REC_COV_A] * inv_det;
+    int32_t px0 = tx * tile_size, px1 = tx * tile_size + tile_size - 1;
+    int32_t py0 = ty * tile_size, py1 = ty * tile_size + tile_size - 1;
+
+    if(px0 < v->bb[0]) px0 = v->bb[0];
+    if(px1 > v->bb[1]) px1 = v->bb[1];
+    if(py0 < v->bb[2]) py0 = v->bb[2];
+    if(py1 > v->bb[3]) py1 = v->bb[3];
+    return gsx_tile_may_contribute(v->rec[ORACLE_REC_MEAN2D_X], v->rec[ORACLE_REC_MEAN2D_Y], inv_a, inv_b, inv_c,
+        gsx_tile_qcut(v->rec[ORACLE_REC_OPACITY]), px0, px1, py0, py1);
+}
+
+/* Tile-key restatement (no CPU counterpart): visible Gaussians in Gaussian-index order, each
+ * emitting key = tile << 32 | bits(depth) for the kept tiles of its box in row-major order,
+ * then a stable sort by key. Per tile this is the CPU's (depth, index) order. Returns the
+ * instance count I; writes sorted keys/values when capacity allows (else returns -I-1). */
 int64_t oracle_tile_keys(int64_t n, int sh_degree, const float *mean3d, const float *rotation,
     const float *logscale, const float *opacity, const float *sh0, const float *sh1, const float *sh2,
     const float *sh3, const float *camera, int32_t tile_size, int64_t capacity, uint64_t *out_keys,
@@ -473,12 +498,16 @@ int64_t oracle_tile_keys(int64_t n, int sh_degree, const float *mean3d, const fl
     int64_t count, i, total = 0;
     int32_t tiles_x = (k.width + tile_size - 1) / tile_size;
     kv *pairs;
+    int32_t tx, ty;
 
     if(v == NULL) return -1;
     count = collect_visible(n, sh_degree, mean3d, rotation, logscale, opacity, sh0, sh1, sh2, sh3, &k, v, NULL);
     for(i = 0; i < count; ++i) {
-        total += (int64_t)(v[i].bb[1] / tile_size - v[i].bb[0] / tile_size + 1)
-            * (int64_t)(v[i].bb[3] / tile_size - v[i].bb[2] / tile_size + 1);
+        for(ty = v[i].bb[2] / tile_size; ty <= v[i].bb[3] / tile_size; ++ty) {
+            for(tx = v[i].bb[0] / tile_size; tx <= v[i].bb[1] / tile_size; ++tx) {
+                total += tile_kept(&v[i], tx, ty, tile_size);
+            }
+        }
     }
     if(total > capacity) {
         free(v);
@@ -491,13 +520,13 @@ int64_t oracle_tile_keys(int64_t n, int sh_degree, const float *mean3d, const fl
     }
     total = 0;
     for(i = 0; i < count; ++i) {
-        int32_t tx, ty;
         uint32_t depth_bits = gsx_f32_bits(v[i].rec[ORACLE_REC_DEPTH]);
 
         for(ty = v[i].bb[2] / tile_size; ty <= v[i].bb[3] / tile_size; ++ty) {
             for(tx = v[i].bb[0] / tile_size; tx <= v[i].bb[1] / tile_size; ++tx) {
                 uint64_t tile = (uint64_t)ty * (uint64_t)tiles_x + (uint64_t)tx;
 
+                if(!tile_kept(&v[i], tx, ty, tile_size)) continue;
                 pairs[total].key = (tile << 32) | (uint64_t)depth_bits;
                 pairs[total].value = (uint32_t)v[i].g;
                 pairs[total].seq = (uint64_t)total;
@@ -513,6 +542,15 @@ int64_t oracle_tile_keys(int64_t n, int sh_degree, const float *mean3d, const fl
     free(pairs);
     free(v);
     return total;
+}
+
+/* The tile test alone, for tests: 1 when the instance is kept. */
+float oracle_tile_logf(float x) { return gsx_cull_logf(x); }
+
+int oracle_tile_may_contribute(float mx, float my, float inv_a, float inv_b, float inv_c, float opacity, int px0,
+    int px1, int py0, int py1)
+{
+    return gsx_tile_may_contribute(mx, my, inv_a, inv_b, inv_c, gsx_tile_qcut(opacity), px0, px1, py0, py1);
 }
 
 /* [start, end) of every tile in the sorted key array; empty tiles get (0, 0). */

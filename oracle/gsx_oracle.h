@@ -13,7 +13,10 @@
  *   oracle_render_forward / oracle_render_backward: bit-exact against the reference CPU
  *     backend built from its own sources (oracle/_ref), on seeded scenes and on the
  *     reference's finite-difference scenes; closed form (tests/render_runtime.cpp:671-722).
- *   oracle_tile_*: brute force (per-pixel membership of every tile list) and invariants.
+ *   oracle_tile_*: brute force (per-pixel membership of every tile list) and invariants; the
+ *     tile test (oracle_tile_may_contribute) against per-pixel evaluation of the CPU's power and
+ *     alpha cuts on random and adversarial Gaussians (it may keep, never drop, a contributing
+ *     tile), and end to end by rendering from the culled lists bit-exactly like oracle/_ref.
  *   oracle_loss_*: against oracle/_ref bit-exact; SSIM also against an independent numpy
  *     float64 evaluation and the identical-image property.
  *   oracle_adam_step: against oracle/_ref bit-exact and the textbook Adam formula.

@@ -59,6 +59,10 @@ class Oracle:
         lib.oracle_tile_keys.restype = _i64
         lib.oracle_tile_keys.argtypes = [_i64, ctypes.c_int] + [_vp] * 9 + [ctypes.c_int32, _i64, _vp, _vp]
         lib.oracle_tile_ranges.argtypes = [_i64, _vp, _i64, _vp]
+        lib.oracle_tile_may_contribute.restype = ctypes.c_int
+        lib.oracle_tile_may_contribute.argtypes = [_f] * 6 + [ctypes.c_int] * 4
+        lib.oracle_tile_logf.restype = _f
+        lib.oracle_tile_logf.argtypes = [_f]
         lib.oracle_render_forward.restype = ctypes.c_int
         lib.oracle_render_forward.argtypes = [_i64, ctypes.c_int] + [_vp] * 12
         lib.oracle_render_backward.restype = ctypes.c_int
@@ -101,6 +105,9 @@ class Oracle:
             if r >= 0:
                 return keys[:r], vals[:r]
             cap = -r - 1 + 16
+
+    def tile_may_contribute(self, mx, my, inv_a, inv_b, inv_c, opacity, px0, px1, py0, py1) -> bool:
+        return bool(self.lib.oracle_tile_may_contribute(mx, my, inv_a, inv_b, inv_c, opacity, px0, px1, py0, py1))
 
     def tile_ranges(self, keys, tile_count):
         ranges = np.zeros((tile_count, 2), np.uint32)
