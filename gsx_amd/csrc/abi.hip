@@ -165,7 +165,7 @@ int bits_for(uint32_t v) {
 
 struct gsx_hip_render_context {
     DeviceBuffer rec, cov_coef, ckpt, inst_gauss, inst_grad, tile_count, big_list, offsets, scan_temp, keys, vals,
-        keys_alt, vals_alt, sort_temp, ranges, final_t, last, grad2d;
+        keys_alt, vals_alt, sort_temp, ranges, sorted_g, final_t, last, grad2d;
     uint32_t* host_count = nullptr;  // pinned
     CameraParams cam{};
     gsx_hip_gaussians gs{};
@@ -335,9 +335,10 @@ gsx_hip_status gsx_hip_render_context_create(gsx_hip_render_context** out_contex
 
 gsx_hip_status gsx_hip_render_context_destroy(gsx_hip_render_context* ctx) {
     if (ctx == nullptr) return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "context must be non-null");
-    DeviceBuffer* all[] = {&ctx->rec, &ctx->cov_coef, &ctx->ckpt, &ctx->inst_gauss, &ctx->inst_grad, &ctx->tile_count, &ctx->offsets,  &ctx->scan_temp, &ctx->keys,
-                           &ctx->vals,    &ctx->keys_alt,   &ctx->vals_alt, &ctx->sort_temp, &ctx->ranges,
-                           &ctx->final_t, &ctx->last,       &ctx->grad2d};
+    DeviceBuffer* all[] = {&ctx->rec,       &ctx->cov_coef, &ctx->ckpt,      &ctx->inst_gauss, &ctx->inst_grad,
+                           &ctx->tile_count, &ctx->big_list, &ctx->offsets,   &ctx->scan_temp,  &ctx->keys,
+                           &ctx->vals,       &ctx->keys_alt, &ctx->vals_alt,  &ctx->sort_temp,  &ctx->ranges,
+                           &ctx->sorted_g,   &ctx->final_t,  &ctx->last,      &ctx->grad2d};
     for (DeviceBuffer* b : all) b->release();
     if (ctx->host_count != nullptr) (void)hipHostFree(ctx->host_count);
     release_events(ctx);
@@ -488,6 +489,7 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     GSX_TRY(ctx->vals.reserve((size_t)(count > 0 ? count : 1) * sizeof(uint32_t), "vals"));
     GSX_TRY(ctx->vals_alt.reserve((size_t)(count > 0 ? count : 1) * sizeof(uint32_t), "vals_alt"));
     GSX_TRY(ctx->inst_gauss.reserve((size_t)(count > 0 ? count : 1) * sizeof(uint32_t), "instance_gaussian"));
+    GSX_TRY(ctx->sorted_g.reserve((size_t)(count > 0 ? count : 1) * sizeof(uint32_t), "sorted_g"));
     GSX_TRY(ctx->sort_temp.reserve(gsx_hip_radix_sort_temp_bytes(count), "sort_temp"));
     if (train) {
         // bucket checkpoints: at most I/32 + tiles + 1 slots of 256 floats
@@ -518,14 +520,15 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     hipLaunchKernelGGL(fill_u32_kernel, dim3(blocks_for((int64_t)tiles * 2, 256)), dim3(256), 0, stream,
                        ctx->ranges.as<uint32_t>(), (int64_t)tiles * 2, 0u);
     if (count > 0) {
-        hipLaunchKernelGGL(tile_ranges_kernel, dim3(blocks_for(count, 256)), dim3(256), 0, stream, skeys,
-                           ctx->offsets.as<uint32_t>() + n, ctx->ranges.as<uint2>());
+        hipLaunchKernelGGL(tile_ranges_kernel, dim3(blocks_for(count, 256)), dim3(256), 0, stream, skeys, svals,
+                           ctx->inst_gauss.as<uint32_t>(), ctx->offsets.as<uint32_t>() + n, ctx->ranges.as<uint2>(),
+                           ctx->sorted_g.as<uint32_t>());
     }
     GSX_HIP_TRY(hipGetLastError(), "tile_ranges_kernel");
     GSX_TRY(record(ctx, 5, stream));
     const int tiles_padded = ((tiles + 7) / 8) * 8;
     hipLaunchKernelGGL(blend_forward_kernel, dim3((unsigned)tiles_padded), dim3(256), 0, stream,
-                       ctx->ranges.as<uint2>(), svals, ctx->rec.as<float4>(), ctx->inst_gauss.as<uint32_t>(), cam,
+                       ctx->ranges.as<uint2>(), ctx->sorted_g.as<uint32_t>(), ctx->rec.as<float4>(), cam,
                        out_rgb, ctx->final_t.as<float>(),
                        ctx->last.as<uint32_t>(), train ? ctx->ckpt.as<float>() : nullptr);
     GSX_HIP_TRY(hipGetLastError(), "blend_forward_kernel");
@@ -565,7 +568,7 @@ gsx_hip_status gsx_hip_render_backward(gsx_hip_render_context* ctx, const float*
     GSX_TRY(record(ctx, 7, stream));
     const int tiles_padded = ((tiles + 7) / 8) * 8;
     hipLaunchKernelGGL(blend_backward_kernel, dim3((unsigned)tiles_padded), dim3(256), 0, stream,
-                       ctx->ranges.as<uint2>(), svals, ctx->inst_gauss.as<uint32_t>(), ctx->rec.as<float4>(),
+                       ctx->ranges.as<uint2>(), svals, ctx->sorted_g.as<uint32_t>(), ctx->rec.as<float4>(),
                        ctx->cov_coef.as<float4>(), ctx->ckpt.as<float>(), cam, grad_rgb, ctx->final_t.as<float>(),
                        ctx->last.as<uint32_t>(), ctx->inst_grad.as<float>());
     GSX_HIP_TRY(hipGetLastError(), "blend_backward_kernel");

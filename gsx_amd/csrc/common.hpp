@@ -340,4 +340,19 @@ __device__ inline float wave_reduce_sum(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
+// Sums each of v[0..kN) over the 16 lanes of its DPP row (every lane of the row receives the
+// row total). The four steps are applied to all values in turn, so consecutive DPP reads never
+// depend on the instruction just before them.
+template <int kN>
+__device__ inline void row_reduce_sums(float (&v)[kN]) {
+#pragma unroll
+    for (int i = 0; i < kN; ++i) v[i] += dpp_move<0xb1, 0xf>(v[i]);   // quad_perm [1,0,3,2]
+#pragma unroll
+    for (int i = 0; i < kN; ++i) v[i] += dpp_move<0x4e, 0xf>(v[i]);   // quad_perm [2,3,0,1]
+#pragma unroll
+    for (int i = 0; i < kN; ++i) v[i] += dpp_move<0x141, 0xf>(v[i]);  // row_half_mirror
+#pragma unroll
+    for (int i = 0; i < kN; ++i) v[i] += dpp_move<0x140, 0xf>(v[i]);  // row_mirror
+}
+
 }  // namespace gsx_amd

@@ -286,15 +286,21 @@ __global__ __launch_bounds__(256) void fill_f32_kernel(float* __restrict__ p, in
     if (i < count) p[i] = v;
 }
 
-// [start, end) of each tile's run in the sorted keys; tiles without keys keep (0, 0).
-__global__ __launch_bounds__(256) void tile_ranges_kernel(const uint64_t* __restrict__ keys, const uint32_t* count_ptr,
-                                                          uint2* __restrict__ ranges) {
+// [start, end) of each tile's run in the sorted keys (tiles without keys keep (0, 0)), and the
+// Gaussian of every sorted position (sorted_g[i] = instance_gaussian[values[i]]), which spares
+// both blends a dependent load per entry.
+__global__ __launch_bounds__(256) void tile_ranges_kernel(const uint64_t* __restrict__ keys,
+                                                          const uint32_t* __restrict__ values,
+                                                          const uint32_t* __restrict__ instance_gaussian,
+                                                          const uint32_t* count_ptr, uint2* __restrict__ ranges,
+                                                          uint32_t* __restrict__ sorted_g) {
     const uint32_t count = *count_ptr;
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= count) return;
     const uint32_t tile = (uint32_t)(keys[i] >> 32);
     if (i == 0 || (uint32_t)(keys[i - 1] >> 32) != tile) ranges[tile].x = i;
     if (i == count - 1 || (uint32_t)(keys[i + 1] >> 32) != tile) ranges[tile].y = i + 1;
+    sorted_g[i] = instance_gaussian[values[i]];
 }
 
 // Workgroup -> tile mapping: consecutive workgroups are dealt round-robin to the 8 XCDs, so give
@@ -331,8 +337,8 @@ __device__ inline size_t checkpoint_slot(uint32_t range_start, int tile, uint32_
 // of the last contributing position, and (TRAIN) the bucket checkpoints.
 // ---------------------------------------------------------------------------------------------
 __global__ __launch_bounds__(kBlendThreads) void blend_forward_kernel(
-    const uint2* __restrict__ ranges, const uint32_t* __restrict__ values, const float4* __restrict__ rec,
-    const uint32_t* __restrict__ instance_gaussian, CameraParams cam, float* __restrict__ out_rgb,
+    const uint2* __restrict__ ranges, const uint32_t* __restrict__ sorted_g, const float4* __restrict__ rec,
+    CameraParams cam, float* __restrict__ out_rgb,
     float* __restrict__ out_t, uint32_t* __restrict__ out_last, float* __restrict__ ckpt) {
     __shared__ float4 s_r0[kBlendThreads];
     __shared__ float4 s_r1[kBlendThreads];
@@ -356,7 +362,7 @@ __global__ __launch_bounds__(kBlendThreads) void blend_forward_kernel(
         if (__syncthreads_count(done ? 1 : 0) == kBlendThreads) break;
         const uint32_t j = base + threadIdx.x;
         if (j < range.y) {
-            const uint32_t g = instance_gaussian[values[j]];
+            const uint32_t g = sorted_g[j];
             s_r0[threadIdx.x] = rec[3 * (size_t)g + 0];
             s_r1[threadIdx.x] = rec[3 * (size_t)g + 1];
             s_r2[threadIdx.x] = rec[3 * (size_t)g + 2];
@@ -422,20 +428,23 @@ constexpr int kGrad2d = 9;
 // full-screen Gaussians (present in every tile).
 // ---------------------------------------------------------------------------------------------
 constexpr int kWavesPerTile = kBlendThreads / kWave;
+constexpr int kRowsPerTile = kTile;  // 16 pixel rows = 16 DPP rows of 16 lanes
+
+constexpr int kBatchBuckets = kBlendThreads / kBucket;  // 8 buckets per 256-entry batch
 
 __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
-    const uint2* __restrict__ ranges, const uint32_t* __restrict__ values,
-    const uint32_t* __restrict__ instance_gaussian, const float4* __restrict__ rec,
-    const float4* __restrict__ cov_coef, const float* __restrict__ ckpt, CameraParams cam,
-    const float* __restrict__ grad_rgb, const float* __restrict__ final_t, const uint32_t* __restrict__ last_contrib,
-    float* __restrict__ instance_grad) {
+    const uint2* __restrict__ ranges, const uint32_t* __restrict__ values, const uint32_t* __restrict__ sorted_g,
+    const float4* __restrict__ rec, const float4* __restrict__ cov_coef, const float* __restrict__ ckpt,
+    CameraParams cam, const float* __restrict__ grad_rgb, const float* __restrict__ final_t,
+    const uint32_t* __restrict__ last_contrib, float* __restrict__ instance_grad) {
     __shared__ float4 s_r0[kBlendThreads];
     __shared__ float4 s_r1[kBlendThreads];
     __shared__ float4 s_r2[kBlendThreads];
     __shared__ float4 s_k0[kBlendThreads];
     __shared__ float2 s_k1[kBlendThreads];
     __shared__ uint32_t s_pos[kBlendThreads];
-    __shared__ float s_acc[kWavesPerTile][kBucket][kGrad2d];
+    __shared__ float s_ck[kBatchBuckets][kBlendThreads];
+    __shared__ float s_acc[kRowsPerTile][kBucket][kGrad2d];
     __shared__ uint64_t s_exp2[GSX_EXP2_TABLE_SIZE];
     __shared__ uint32_t s_max_last;
     const int tiles = cam.tiles_x * cam.tiles_y;
@@ -445,6 +454,7 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
     const int tx = tile % cam.tiles_x, ty = tile / cam.tiles_x;
     const int px = tx * kTile + (threadIdx.x & (kTile - 1));
     const int py = ty * kTile + (threadIdx.x / kTile);
+    const int row = threadIdx.x / kTile;  // pixel row of the tile = DPP row of the wave
     const bool inside = px < cam.width && py < cam.height;
     const uint2 range = ranges[tile];
     const size_t pix = (size_t)py * (size_t)cam.width + (size_t)px;
@@ -478,31 +488,66 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
         for (int c = 0; c < kGrad2d; ++c) dst[c] = 0.0f;
     }
     if (end_all <= range.x) return;  // uniform
+
+    // Batches are walked back to front and staged one ahead in registers: the ids of batch b-1
+    // are loaded when batch b starts, its records and checkpoints after b's first bucket, and
+    // they reach LDS when b-1 starts, so global latency overlaps the replay.
+    uint32_t nx_p = 0, nx_g = 0;
+    float4 nx_r0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), nx_r1 = nx_r0, nx_r2 = nx_r0, nx_k0 = nx_r0;
+    float2 nx_k1 = make_float2(0.0f, 0.0f);
+    float nx_ck[kBatchBuckets];
+    auto load_ids = [&](uint32_t bstart) {
+        if (bstart + threadIdx.x < range.y) {
+            nx_p = values[bstart + threadIdx.x];
+            nx_g = sorted_g[bstart + threadIdx.x];
+        }
+    };
+    auto load_records = [&](uint32_t bstart) {
+        if (bstart + threadIdx.x < range.y) {
+            nx_r0 = rec[3 * (size_t)nx_g + 0];
+            nx_r1 = rec[3 * (size_t)nx_g + 1];
+            nx_r2 = rec[3 * (size_t)nx_g + 2];
+            nx_k0 = cov_coef[2 * (size_t)nx_g + 0];
+            const float4 k1 = cov_coef[2 * (size_t)nx_g + 1];
+            nx_k1 = make_float2(k1.x, k1.y);
+        }
+#pragma unroll
+        for (int b = 0; b < kBatchBuckets; ++b) {
+            const uint32_t j0 = bstart + (uint32_t)(b * kBucket);
+            nx_ck[b] = (inside && j0 < last) ? ckpt[checkpoint_slot(range.x, tile, j0) * kBlendThreads + threadIdx.x]
+                                             : 0.0f;
+        }
+    };
     const uint32_t first_batch = range.x + ((end_all - 1u - range.x) / kBlendThreads) * kBlendThreads;
+    load_ids(first_batch);
+    load_records(first_batch);
     for (int64_t bstart = first_batch; bstart >= (int64_t)range.x; bstart -= kBlendThreads) {
         const int count = (int)min((uint32_t)kBlendThreads, range.y - (uint32_t)bstart);
         if (threadIdx.x < count) {
-            const uint32_t p = values[bstart + threadIdx.x];
-            const uint32_t g = instance_gaussian[p];
-            s_pos[threadIdx.x] = p;
-            s_r0[threadIdx.x] = rec[3 * (size_t)g + 0];
-            s_r1[threadIdx.x] = rec[3 * (size_t)g + 1];
-            s_r2[threadIdx.x] = rec[3 * (size_t)g + 2];
-            s_k0[threadIdx.x] = cov_coef[2 * (size_t)g + 0];
-            const float4 k1 = cov_coef[2 * (size_t)g + 1];
-            s_k1[threadIdx.x] = make_float2(k1.x, k1.y);
+            s_pos[threadIdx.x] = nx_p;
+            s_r0[threadIdx.x] = nx_r0;
+            s_r1[threadIdx.x] = nx_r1;
+            s_r2[threadIdx.x] = nx_r2;
+            s_k0[threadIdx.x] = nx_k0;
+            s_k1[threadIdx.x] = nx_k1;
         }
+#pragma unroll
+        for (int b = 0; b < kBatchBuckets; ++b) s_ck[b][threadIdx.x] = nx_ck[b];
         __syncthreads();
-        for (int sb = (count - 1) / kBucket; sb >= 0; --sb) {
+        const bool has_next = bstart - kBlendThreads >= (int64_t)range.x;  // uniform
+        const uint32_t next = (uint32_t)(bstart - kBlendThreads);
+        if (has_next) load_ids(next);
+        const int sb_first = (count - 1) / kBucket;
+        for (int sb = sb_first; sb >= 0; --sb) {
             const uint32_t j0 = (uint32_t)bstart + (uint32_t)(sb * kBucket);
-            if (j0 >= end_all) continue;  // uniform; zeroed above
+            if (j0 < end_all) {  // uniform; entries beyond end_all were zeroed above
             const int n_in = min(kBucket, count - sb * kBucket);
             float tb[kBucket];
             float gv[kBucket];
             uint32_t mask = 0u;
             // forward replay of the bucket from its checkpoint (render.c:1476-1515)
             if (inside && j0 < last) {
-                float tt = ckpt[checkpoint_slot(range.x, tile, j0) * kBlendThreads + threadIdx.x];
+                float tt = s_ck[sb][threadIdx.x];
 #pragma unroll
                 for (int i = 0; i < kBucket; ++i) {
                     tb[i] = tt;
@@ -577,40 +622,35 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
                     s1 += w * r1.w;
                     s2 += w * r2.x;
                 }
-                float* acc = &s_acc[wave][i][0];
                 if (__ballot(contrib) != 0ull) {
-                    const float v0 = wave_reduce_sum(g_mx);
-                    const float v1 = wave_reduce_sum(g_my);
-                    const float v2 = wave_reduce_sum(g_ca);
-                    const float v3 = wave_reduce_sum(g_cb);
-                    const float v4 = wave_reduce_sum(g_cc);
-                    const float v5 = wave_reduce_sum(g_c0);
-                    const float v6 = wave_reduce_sum(g_c1);
-                    const float v7 = wave_reduce_sum(g_c2);
-                    const float v8 = wave_reduce_sum(g_op);
-                    if (lane == 0) {
-                        acc[0] = v0;
-                        acc[1] = v1;
-                        acc[2] = v2;
-                        acc[3] = v3;
-                        acc[4] = v4;
-                        acc[5] = v5;
-                        acc[6] = v6;
-                        acc[7] = v7;
-                        acc[8] = v8;
+                    float v[kGrad2d] = {g_mx, g_my, g_ca, g_cb, g_cc, g_c0, g_c1, g_c2, g_op};
+                    row_reduce_sums(v);
+                    if ((threadIdx.x & (kTile - 1)) == 0) {
+                        float* acc = &s_acc[row][i][0];
+#pragma unroll
+                        for (int c = 0; c < kGrad2d; ++c) acc[c] = v[c];
                     }
-                } else if (lane < kGrad2d) {
-                    acc[lane] = 0.0f;
+                } else if (lane < 4 * kGrad2d) {
+                    s_acc[wave * 4 + lane / kGrad2d][i][lane % kGrad2d] = 0.0f;
                 }
             }
             __syncthreads();
-            // combine the four waves and write the bucket's per-instance partials
+            // combine the 16 row partials and write the bucket's per-instance partials
             for (int o = threadIdx.x; o < n_in * kGrad2d; o += kBlendThreads) {
                 const int e = o / kGrad2d, c = o % kGrad2d;
-                const float v = (s_acc[0][e][c] + s_acc[1][e][c]) + (s_acc[2][e][c] + s_acc[3][e][c]);
-                instance_grad[(size_t)s_pos[sb * kBucket + e] * kGrad2d + c] = v;
+                float q[kRowsPerTile];
+#pragma unroll
+                for (int r = 0; r < kRowsPerTile; ++r) q[r] = s_acc[r][e][c];
+#pragma unroll
+                for (int h = kRowsPerTile / 2; h > 0; h >>= 1) {
+#pragma unroll
+                    for (int r = 0; r < h; ++r) q[r] += q[r + h];
+                }
+                instance_grad[(size_t)s_pos[sb * kBucket + e] * kGrad2d + c] = q[0];
             }
             __syncthreads();
+            }
+            if (has_next && sb == sb_first) load_records(next);
         }
     }
 }
