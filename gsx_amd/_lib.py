@@ -53,7 +53,8 @@ class GaussianGrads(ctypes.Structure):
 
 class RenderStats(ctypes.Structure):
     _fields_ = [("gaussian_count", _i64), ("visible_count", _i64), ("instance_count", _i64), ("tile_count", _i32),
-                ("sort_passes", _i32)]
+                ("sort_passes", _i32), ("key_tile_shift", _i32), ("key_depth_shift", _i32),
+                ("key_depth_base", ctypes.c_uint32), ("key_payload_bits", _i32)]
 
 
 class RenderBuffers(ctypes.Structure):
@@ -114,6 +115,8 @@ SIGNATURES = {
     "gsx_hip_radix_sort_temp_bytes": (ctypes.c_size_t, [_i64]),
     "gsx_hip_radix_sort_pairs_u64": (_st, [_vp, _vp, _vp, _vp, _i64, ctypes.c_int, ctypes.c_int, _vp,
                                            ctypes.POINTER(ctypes.c_int), _vp]),
+    "gsx_hip_radix_sort_keys_u64": (_st, [_vp, _vp, _i64, ctypes.c_int, ctypes.c_int, _vp,
+                                          ctypes.POINTER(ctypes.c_int), _vp]),
     "gsx_hip_loss_l1_f32_forward_kernel_launch": (_st, [_vp, _vp, _vp, _i64, _f, _vp]),
     "gsx_hip_loss_l1_f32_backward_kernel_launch": (_st, [_vp, _vp, _vp, _i64, _f, _vp]),
     "gsx_hip_loss_mse_f32_forward_kernel_launch": (_st, [_vp, _vp, _vp, _i64, _f, _vp]),

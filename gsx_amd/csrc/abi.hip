@@ -7,6 +7,8 @@
 // Backward:
 //   zero the screen-space accumulator -> blend backward (atomics into it) -> projection backward.
 #include <hip/hip_runtime.h>
+
+#include <algorithm>
 #include <math.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -174,6 +176,8 @@ struct gsx_hip_render_context {
     int32_t tile_count_total = 0;
     int32_t sort_passes = 0;
     bool sorted_in_alt = false;
+    KeyLayout layout{};
+    uint32_t* sorted_vals = nullptr;  // emission position of each sorted key
     bool has_train_state = false;
     // Stage timing: a ring of event sets, one set per forward/backward pair, so that a timed
     // loop records without synchronising; get_timings averages over the recorded sets.
@@ -471,7 +475,8 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
         GSX_HIP_TRY(hipGetLastError(), "preprocess_kernel");
         hipLaunchKernelGGL(big_tiles_kernel<false>, dim3(kBigBlocks), dim3(256), 0, stream,
                            ctx->big_list.as<uint32_t>() + 1, ctx->big_list.as<uint32_t>(), ctx->rec.as<float4>(),
-                           cam.tiles_x, ctx->tile_count.as<uint32_t>(), nullptr, nullptr, nullptr, nullptr);
+                           cam.tiles_x, KeyLayout{}, ctx->tile_count.as<uint32_t>(), nullptr, nullptr, nullptr,
+                           nullptr);
         GSX_HIP_TRY(hipGetLastError(), "big_tiles_kernel<count>");
     }
     GSX_TRY(record(ctx, 1, stream));
@@ -491,38 +496,62 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     GSX_TRY(ctx->inst_gauss.reserve((size_t)(count > 0 ? count : 1) * sizeof(uint32_t), "instance_gaussian"));
     GSX_TRY(ctx->sorted_g.reserve((size_t)(count > 0 ? count : 1) * sizeof(uint32_t), "sorted_g"));
     GSX_TRY(ctx->sort_temp.reserve(gsx_hip_radix_sort_temp_bytes(count), "sort_temp"));
+    // key layout for this forward (see KeyLayout): tile bits, depth bits relative to bits(near),
+    // and the emission position packed in the low bits when everything fits in 64 bits
+    const uint32_t near_bits = gsx_f32_bits(cam.near_plane), far_bits = gsx_f32_bits(cam.far_plane);
+    const int depth_bits = bits_for(far_bits - near_bits);
+    const int pos_bits = bits_for((uint32_t)(count > 0 ? count - 1 : 0));
+    KeyLayout layout{};
+    layout.depth_base = near_bits;
+    layout.depth_max = far_bits - near_bits;
+    if (tile_bits + depth_bits + pos_bits <= 64) {
+        layout.payload_bits = pos_bits > 0 ? pos_bits : 1;
+        layout.depth_shift = layout.payload_bits;
+    } else {
+        layout.payload_bits = 0;
+        layout.depth_shift = 0;
+    }
+    layout.tile_shift = layout.depth_shift + depth_bits;
+    ctx->layout = layout;
     if (train) {
         // bucket checkpoints: at most I/32 + tiles + 1 slots of 256 floats
         GSX_TRY(ctx->ckpt.reserve(((size_t)count / 32 + (size_t)tiles + 2) * 256 * sizeof(float), "checkpoints"));
     }
     if (n > 0) {
         hipLaunchKernelGGL(emit_keys_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, n, ctx->rec.as<float4>(),
-                           ctx->tile_count.as<uint32_t>(), ctx->offsets.as<uint32_t>(), cam.tiles_x,
+                           ctx->tile_count.as<uint32_t>(), ctx->offsets.as<uint32_t>(), cam.tiles_x, layout,
                            ctx->keys.as<uint64_t>(), ctx->vals.as<uint32_t>(), ctx->inst_gauss.as<uint32_t>());
         GSX_HIP_TRY(hipGetLastError(), "emit_keys_kernel");
         hipLaunchKernelGGL(big_tiles_kernel<true>, dim3(kBigBlocks), dim3(256), 0, stream,
                            ctx->big_list.as<uint32_t>() + 1, ctx->big_list.as<uint32_t>(), ctx->rec.as<float4>(),
-                           cam.tiles_x, nullptr, ctx->offsets.as<uint32_t>(), ctx->keys.as<uint64_t>(),
+                           cam.tiles_x, layout, nullptr, ctx->offsets.as<uint32_t>(), ctx->keys.as<uint64_t>(),
                            ctx->vals.as<uint32_t>(), ctx->inst_gauss.as<uint32_t>());
         GSX_HIP_TRY(hipGetLastError(), "big_tiles_kernel<emit>");
     }
     GSX_TRY(record(ctx, 3, stream));
     int in_alt = 0;
-    const int end_bit = 32 + tile_bits;
-    ctx->sort_passes = (end_bit + 7) / 8;
-    GSX_TRY(gsx_hip_radix_sort_pairs_u64(ctx->keys.as<uint64_t>(), ctx->vals.as<uint32_t>(),
-                                         ctx->keys_alt.as<uint64_t>(), ctx->vals_alt.as<uint32_t>(), count, 0,
-                                         ctx->sort_passes * 8, ctx->sort_temp.ptr, &in_alt, stream));
+    const int sort_bits = depth_bits + tile_bits;
+    ctx->sort_passes = (sort_bits + 7) / 8;
+    if (layout.payload_bits > 0) {
+        const int end_bit = std::min(64, layout.depth_shift + ctx->sort_passes * 8);  // same pass count
+        GSX_TRY(gsx_hip_radix_sort_keys_u64(ctx->keys.as<uint64_t>(), ctx->keys_alt.as<uint64_t>(), count,
+                                            layout.depth_shift, end_bit, ctx->sort_temp.ptr, &in_alt, stream));
+        ctx->sorted_vals = ctx->vals.as<uint32_t>();  // written by tile_ranges_kernel
+    } else {
+        GSX_TRY(gsx_hip_radix_sort_pairs_u64(ctx->keys.as<uint64_t>(), ctx->vals.as<uint32_t>(),
+                                             ctx->keys_alt.as<uint64_t>(), ctx->vals_alt.as<uint32_t>(), count, 0,
+                                             ctx->sort_passes * 8, ctx->sort_temp.ptr, &in_alt, stream));
+        ctx->sorted_vals = in_alt ? ctx->vals_alt.as<uint32_t>() : ctx->vals.as<uint32_t>();
+    }
     ctx->sorted_in_alt = in_alt != 0;
     GSX_TRY(record(ctx, 4, stream));
     const uint64_t* skeys = ctx->sorted_in_alt ? ctx->keys_alt.as<uint64_t>() : ctx->keys.as<uint64_t>();
-    const uint32_t* svals = ctx->sorted_in_alt ? ctx->vals_alt.as<uint32_t>() : ctx->vals.as<uint32_t>();
     hipLaunchKernelGGL(fill_u32_kernel, dim3(blocks_for((int64_t)tiles * 2, 256)), dim3(256), 0, stream,
                        ctx->ranges.as<uint32_t>(), (int64_t)tiles * 2, 0u);
     if (count > 0) {
-        hipLaunchKernelGGL(tile_ranges_kernel, dim3(blocks_for(count, 256)), dim3(256), 0, stream, skeys, svals,
-                           ctx->inst_gauss.as<uint32_t>(), ctx->offsets.as<uint32_t>() + n, ctx->ranges.as<uint2>(),
-                           ctx->sorted_g.as<uint32_t>());
+        hipLaunchKernelGGL(tile_ranges_kernel, dim3(blocks_for(count, 256)), dim3(256), 0, stream, skeys, layout,
+                           ctx->sorted_vals, ctx->inst_gauss.as<uint32_t>(), ctx->offsets.as<uint32_t>() + n,
+                           ctx->ranges.as<uint2>(), ctx->sorted_g.as<uint32_t>());
     }
     GSX_HIP_TRY(hipGetLastError(), "tile_ranges_kernel");
     GSX_TRY(record(ctx, 5, stream));
@@ -564,7 +593,7 @@ gsx_hip_status gsx_hip_render_backward(gsx_hip_render_context* ctx, const float*
                                    "instance_grad"));
     const CameraParams& cam = ctx->cam;
     const int32_t tiles = cam.tiles_x * cam.tiles_y;
-    const uint32_t* svals = ctx->sorted_in_alt ? ctx->vals_alt.as<uint32_t>() : ctx->vals.as<uint32_t>();
+    const uint32_t* svals = ctx->sorted_vals;
     GSX_TRY(record(ctx, 7, stream));
     const int tiles_padded = ((tiles + 7) / 8) * 8;
     hipLaunchKernelGGL(blend_backward_kernel, dim3((unsigned)tiles_padded), dim3(256), 0, stream,
@@ -599,13 +628,17 @@ gsx_hip_status gsx_hip_render_context_get_stats(const gsx_hip_render_context* ct
     out->instance_count = ctx->instance_count;
     out->tile_count = ctx->tile_count_total;
     out->sort_passes = ctx->sort_passes;
+    out->key_tile_shift = ctx->layout.tile_shift;
+    out->key_depth_shift = ctx->layout.depth_shift;
+    out->key_depth_base = ctx->layout.depth_base;
+    out->key_payload_bits = ctx->layout.payload_bits;
     return GSX_HIP_SUCCESS;
 }
 
 gsx_hip_status gsx_hip_render_context_get_buffers(const gsx_hip_render_context* ctx, gsx_hip_render_buffers* out) {
     if (ctx == nullptr || out == nullptr) return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "context/out must be non-null");
     out->sorted_keys = ctx->sorted_in_alt ? ctx->keys_alt.as<uint64_t>() : ctx->keys.as<uint64_t>();
-    out->sorted_values = ctx->sorted_in_alt ? ctx->vals_alt.as<uint32_t>() : ctx->vals.as<uint32_t>();
+    out->sorted_values = ctx->sorted_vals;
     out->tile_ranges = ctx->ranges.as<uint32_t>();
     out->records = ctx->rec.as<float>();
     out->tile_counts = ctx->tile_count.as<uint32_t>();

@@ -39,6 +39,32 @@ constexpr int kWavesPerBlock = 4;
 // big_tiles_kernel): a wave holding a full-image box would otherwise serialise hundreds of steps.
 constexpr uint32_t kBigTiles = 256;
 
+// Sort key of an instance: tile << tile_shift | (bits(depth) - depth_base) << depth_shift | payload.
+// Visible depths lie in [near, far] (preprocess culls the rest), and positive floats order like
+// their bit patterns, so bits(depth) - bits(near) keeps the depth order in fewer bits than the
+// full pattern (27 instead of 32 for near 0.01, far 100): one radix pass fewer. When everything
+// fits in 64 bits the emission position rides in the low payload_bits bits and the sort moves
+// keys only; otherwise payload_bits = 0 and the position travels as the sort value.
+struct KeyLayout {
+    int tile_shift;
+    int depth_shift;
+    uint32_t depth_base;
+    uint32_t depth_max;  // largest depth offset (bits(far) - bits(near)); larger ones are clamped
+    int payload_bits;
+};
+
+__device__ inline uint64_t make_key(const KeyLayout& k, uint32_t tile, uint32_t depth_bits, uint32_t pos) {
+    uint32_t rel = depth_bits - k.depth_base;
+    if (rel > k.depth_max) rel = k.depth_max;  // only for non-finite depths
+    uint64_t key = ((uint64_t)rel << k.depth_shift) | (k.payload_bits > 0 ? (uint64_t)pos : 0ull);
+    if (k.tile_shift < 64) key |= (uint64_t)tile << k.tile_shift;
+    return key;
+}
+
+__device__ inline uint32_t key_tile(const KeyLayout& k, uint64_t key) {
+    return k.tile_shift < 64 ? (uint32_t)(key >> k.tile_shift) : 0u;
+}
+
 __device__ inline uint32_t box_tiles(float4 r2) {
     const uint32_t bx = __float_as_uint(r2.y), by = __float_as_uint(r2.z);
     return ((bx >> 16) / kTile - (bx & 0xffffu) / kTile + 1) * ((by >> 16) / kTile - (by & 0xffffu) / kTile + 1);
@@ -48,7 +74,7 @@ struct WaveBoxes {
     float mx[kWave], my[kWave], a[kWave], b[kWave], c[kWave], qcut[kWave];
     int32_t x0[kWave], x1[kWave], y0[kWave], y1[kWave];
     uint32_t tx0[kWave], ty0[kWave], wx[kWave], excl[kWave], kept[kWave], out[kWave];
-    uint64_t depth[kWave];
+    uint32_t depth[kWave];
     uint32_t g[kWave];
 };
 
@@ -73,7 +99,7 @@ __device__ inline uint32_t stage_box(WaveBoxes& w, bool valid, float4 r0, float4
         w.tx0[lane] = (uint32_t)x0 / kTile;
         w.ty0[lane] = (uint32_t)y0 / kTile;
         w.wx[lane] = (uint32_t)x1 / kTile - (uint32_t)x0 / kTile + 1;
-        w.depth[lane] = (uint64_t)__float_as_uint(r2.w);
+        w.depth[lane] = __float_as_uint(r2.w);
         total = w.wx[lane] * ((uint32_t)y1 / kTile - (uint32_t)y0 / kTile + 1);
     }
     w.g[lane] = g;
@@ -94,7 +120,7 @@ __device__ inline uint32_t stage_box(WaveBoxes& w, bool valid, float4 r0, float4
 // Walks the wave's flattened tiles. kEmit: writes kept instances (key, value = position,
 // instance_gaussian) at out[owner] + rank; always accumulates kept[owner].
 template <bool kEmit>
-__device__ inline void walk_wave_tiles(WaveBoxes& w, uint32_t wave_total, int32_t tiles_x,
+__device__ inline void walk_wave_tiles(WaveBoxes& w, uint32_t wave_total, int32_t tiles_x, const KeyLayout& layout,
                                        uint64_t* __restrict__ keys, uint32_t* __restrict__ values,
                                        uint32_t* __restrict__ instance_gaussian) {
     const uint32_t lane = __lane_id();
@@ -127,8 +153,8 @@ __device__ inline void walk_wave_tiles(WaveBoxes& w, uint32_t wave_total, int32_
         const uint32_t before = w.kept[owner];
         if (kEmit && keep) {
             const uint32_t pos = w.out[owner] + before + (uint32_t)__popcll(mask & lt & seg);
-            keys[pos] = ((uint64_t)tile << 32) | w.depth[owner];
-            values[pos] = pos;
+            keys[pos] = make_key(layout, tile, w.depth[owner], pos);
+            if (layout.payload_bits == 0) values[pos] = pos;
             instance_gaussian[pos] = w.g[owner];
         }
         // the last lane of each owner segment advances that owner's running count
@@ -183,7 +209,7 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
     const bool big = visible && box_tiles(r2) > kBigTiles;
     if (big) big_list[atomicAdd(big_count, 1u)] = (uint32_t)g;  // counted by big_tiles_kernel
     const uint32_t total = stage_box(wb, visible && !big, r0, r1, r2, (uint32_t)g, 0u);
-    walk_wave_tiles<false>(wb, total, cam.tiles_x, nullptr, nullptr, nullptr);
+    walk_wave_tiles<false>(wb, total, cam.tiles_x, KeyLayout{}, nullptr, nullptr, nullptr);
     if (g < n && !big) tile_count[g] = wb.kept[__lane_id()];
 }
 
@@ -197,7 +223,8 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
 __global__ __launch_bounds__(256) void emit_keys_kernel(int64_t n, const float4* __restrict__ rec,
                                                         const uint32_t* __restrict__ tile_count,
                                                         const uint32_t* __restrict__ offsets, int32_t tiles_x,
-                                                        uint64_t* __restrict__ keys, uint32_t* __restrict__ values,
+                                                        KeyLayout layout, uint64_t* __restrict__ keys,
+                                                        uint32_t* __restrict__ values,
                                                         uint32_t* __restrict__ instance_gaussian) {
     __shared__ WaveBoxes s_boxes[kWavesPerBlock];
     WaveBoxes& wb = s_boxes[threadIdx.x / kWave];
@@ -215,7 +242,7 @@ __global__ __launch_bounds__(256) void emit_keys_kernel(int64_t n, const float4*
         o = offsets[g];
     }
     const uint32_t total = stage_box(wb, any, r0, r1, r2, (uint32_t)g, o);
-    walk_wave_tiles<true>(wb, total, tiles_x, keys, values, instance_gaussian);
+    walk_wave_tiles<true>(wb, total, tiles_x, layout, keys, values, instance_gaussian);
 }
 
 // Big boxes: one workgroup per Gaussian of big_list (grid-stride over the list), 256 tiles per
@@ -225,7 +252,7 @@ template <bool kEmit>
 __global__ __launch_bounds__(256) void big_tiles_kernel(const uint32_t* __restrict__ big_list,
                                                         const uint32_t* __restrict__ big_count,
                                                         const float4* __restrict__ rec, int32_t tiles_x,
-                                                        uint32_t* __restrict__ tile_count,
+                                                        KeyLayout layout, uint32_t* __restrict__ tile_count,
                                                         const uint32_t* __restrict__ offsets,
                                                         uint64_t* __restrict__ keys, uint32_t* __restrict__ values,
                                                         uint32_t* __restrict__ instance_gaussian) {
@@ -241,7 +268,7 @@ __global__ __launch_bounds__(256) void big_tiles_kernel(const uint32_t* __restri
         const uint32_t wx = (uint32_t)x1 / kTile - tx0 + 1;
         const uint32_t total = wx * ((uint32_t)y1 / kTile - ty0 + 1);
         const float qcut = gsx_tile_qcut(r1.y);
-        const uint64_t depth = (uint64_t)__float_as_uint(r2.w);
+        const uint32_t depth = __float_as_uint(r2.w);
         const uint32_t o = kEmit ? offsets[g] : 0u;
         uint32_t running = 0;
         for (uint32_t base = 0; base < total; base += blockDim.x) {
@@ -265,8 +292,8 @@ __global__ __launch_bounds__(256) void big_tiles_kernel(const uint32_t* __restri
             }
             if (kEmit && keep) {
                 const uint32_t pos = o + running + before + (uint32_t)__popcll(mask & lanemask_lt());
-                keys[pos] = ((uint64_t)tile << 32) | depth;
-                values[pos] = pos;
+                keys[pos] = make_key(layout, tile, depth, pos);
+                if (layout.payload_bits == 0) values[pos] = pos;
                 instance_gaussian[pos] = g;
             }
             running += step_total;
@@ -286,21 +313,30 @@ __global__ __launch_bounds__(256) void fill_f32_kernel(float* __restrict__ p, in
     if (i < count) p[i] = v;
 }
 
-// [start, end) of each tile's run in the sorted keys (tiles without keys keep (0, 0)), and the
-// Gaussian of every sorted position (sorted_g[i] = instance_gaussian[values[i]]), which spares
-// both blends a dependent load per entry.
-__global__ __launch_bounds__(256) void tile_ranges_kernel(const uint64_t* __restrict__ keys,
-                                                          const uint32_t* __restrict__ values,
+// [start, end) of each tile's run in the sorted keys (tiles without keys keep (0, 0)); with a
+// packed layout the emission position of every sorted key (values[i], from the payload bits);
+// and the Gaussian of every sorted position (sorted_g[i] = instance_gaussian[values[i]]), which
+// spares both blends a dependent load per entry.
+__global__ __launch_bounds__(256) void tile_ranges_kernel(const uint64_t* __restrict__ keys, KeyLayout layout,
+                                                          uint32_t* __restrict__ values,
                                                           const uint32_t* __restrict__ instance_gaussian,
                                                           const uint32_t* count_ptr, uint2* __restrict__ ranges,
                                                           uint32_t* __restrict__ sorted_g) {
     const uint32_t count = *count_ptr;
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= count) return;
-    const uint32_t tile = (uint32_t)(keys[i] >> 32);
-    if (i == 0 || (uint32_t)(keys[i - 1] >> 32) != tile) ranges[tile].x = i;
-    if (i == count - 1 || (uint32_t)(keys[i + 1] >> 32) != tile) ranges[tile].y = i + 1;
-    sorted_g[i] = instance_gaussian[values[i]];
+    const uint64_t key = keys[i];
+    const uint32_t tile = key_tile(layout, key);
+    if (i == 0 || key_tile(layout, keys[i - 1]) != tile) ranges[tile].x = i;
+    if (i == count - 1 || key_tile(layout, keys[i + 1]) != tile) ranges[tile].y = i + 1;
+    uint32_t p;
+    if (layout.payload_bits > 0) {
+        p = (uint32_t)(key & ((1ull << layout.payload_bits) - 1ull));
+        values[i] = p;
+    } else {
+        p = values[i];
+    }
+    sorted_g[i] = instance_gaussian[p];
 }
 
 // Workgroup -> tile mapping: consecutive workgroups are dealt round-robin to the 8 XCDs, so give

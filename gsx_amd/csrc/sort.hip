@@ -3,14 +3,8 @@
 // Replaces cub::DeviceScan::ExclusiveSum (gsx/src/gsx-cuda/fastgs/forward.cu:180-185) and
 // cub::DeviceRadixSort::SortPairs (forward.cu:155-161, 214-220).
 //
-// Radix sort: 8-bit digits, one "reduce then scan" pass per digit:
-//   1. digit histogram per 4096-key block (LDS counters)                 -> hist[digit][block]
-//   2. exclusive scan of hist in digit-major order                       -> global bases
-//   3. scatter: every 256-key round is ranked with wave64 ballots (8 ballots give each lane
-//      the mask of lanes holding the same digit); waves are ordered through LDS counters, so
-//      the rank of a key is its position among equal digits in input order: the sort is
-//      stable, which the tile lists rely on (equal (tile, depth) keys keep Gaussian order).
-// No kernel waits on another workgroup, so every wave always runs to completion.
+// Radix sort: 8-bit digits, LSD, stable (the tile lists rely on it: equal (tile, depth) keys keep
+// Gaussian order); see the pass description above radix_upsweep_kernel.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -121,87 +115,194 @@ __global__ __launch_bounds__(kScanThreads) void scan_downsweep_kernel(const uint
     }
 }
 
-__global__ __launch_bounds__(kSortThreads) void radix_hist_kernel(const uint64_t* __restrict__ keys, int64_t n,
-                                                                  int shift, int64_t num_blocks,
-                                                                  uint32_t* __restrict__ hist) {
-    __shared__ uint32_t s_hist[kRadix];
-    s_hist[threadIdx.x] = 0;
+// ---------------------------------------------------------------------------------------------
+// One LSD pass on the 8-bit digit at `shift`, reduce-then-scan, three launches:
+//   upsweep: digit counts of each 4096-key chunk                       -> hist[digit][chunk]
+//   rowscan: one workgroup per digit scans its row over the chunks    -> offsets, totals[digit]
+//   downsweep: each wave ranks its 1024 keys (16 rounds of 64) stably with 8 ballots per round
+//      and wave-private digit counters; the chunk is then reordered by digit in LDS and written
+//      out in order, so consecutive lanes store consecutive addresses of one digit's run.
+// Stability: a chunk's keys keep input order within a digit (waves own consecutive quarters,
+// rounds and lanes follow input order), and chunks are laid out in order inside each digit.
+// No workgroup waits on another, so every wave runs to completion.
+// ---------------------------------------------------------------------------------------------
+constexpr int kChunkWaves = kSortThreads / kWave;            // 4
+constexpr int kWaveKeys = kSortChunk / kChunkWaves;           // 1024 keys per wave
+constexpr int kWaveRounds = kWaveKeys / kWave;                // 16
+
+__device__ inline uint32_t digit_of(uint64_t key, int shift) { return (uint32_t)(key >> shift) & (kRadix - 1); }
+
+__global__ __launch_bounds__(kSortThreads) void radix_upsweep_kernel(const uint64_t* __restrict__ keys, int64_t n,
+                                                                     int shift, int64_t num_chunks,
+                                                                     uint32_t* __restrict__ hist) {
+    __shared__ uint32_t s_hist[kChunkWaves][kRadix];
+    const int wave = threadIdx.x / kWave;
+#pragma unroll
+    for (int w = 0; w < kChunkWaves; ++w) s_hist[w][threadIdx.x] = 0;
     __syncthreads();
     const int64_t base = (int64_t)blockIdx.x * kSortChunk;
 #pragma unroll 4
     for (int r = 0; r < kSortRounds; ++r) {
-        int64_t i = base + (int64_t)r * kSortThreads + threadIdx.x;
-        if (i < n) {
-            uint32_t d = (uint32_t)(keys[i] >> shift) & (kRadix - 1);
-            atomicAdd(&s_hist[d], 1u);
-        }
+        const int64_t i = base + (int64_t)r * kSortThreads + threadIdx.x;
+        if (i < n) atomicAdd(&s_hist[wave][digit_of(keys[i], shift)], 1u);
     }
     __syncthreads();
-    hist[(int64_t)threadIdx.x * num_blocks + blockIdx.x] = s_hist[threadIdx.x];
+    const uint32_t c = s_hist[0][threadIdx.x] + s_hist[1][threadIdx.x] + s_hist[2][threadIdx.x] + s_hist[3][threadIdx.x];
+    hist[(int64_t)threadIdx.x * num_chunks + blockIdx.x] = c;
 }
 
-__global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
+// Workgroup d: exclusive scan of hist[d][0..num_chunks) into offsets[d][..], row total into
+// totals[d].
+__global__ __launch_bounds__(kSortThreads) void radix_rowscan_kernel(const uint32_t* __restrict__ hist,
+                                                                     int64_t num_chunks,
+                                                                     uint32_t* __restrict__ offsets,
+                                                                     uint32_t* __restrict__ totals) {
+    __shared__ uint32_t s_wave[kSortThreads / kWave];
+    const uint32_t* row = hist + (int64_t)blockIdx.x * num_chunks;
+    uint32_t* out = offsets + (int64_t)blockIdx.x * num_chunks;
+    uint32_t carry = 0;
+    for (int64_t base = 0; base < num_chunks; base += kScanChunk) {
+        uint32_t vals[kScanItems];
+        uint32_t sum = 0;
+#pragma unroll
+        for (int k = 0; k < kScanItems; ++k) {
+            const int64_t i = base + (int64_t)threadIdx.x * kScanItems + k;
+            vals[k] = i < num_chunks ? row[i] : 0u;
+            sum += vals[k];
+        }
+        uint32_t total;
+        uint32_t prefix = block_exclusive_scan_256(sum, s_wave, total) + carry;
+#pragma unroll
+        for (int k = 0; k < kScanItems; ++k) {
+            const int64_t i = base + (int64_t)threadIdx.x * kScanItems + k;
+            if (i < num_chunks) out[i] = prefix;
+            prefix += vals[k];
+        }
+        carry += total;
+    }
+    if (threadIdx.x == 0) totals[blockIdx.x] = carry;
+}
+
+template <bool kPairs>
+__global__ __launch_bounds__(kSortThreads) void radix_downsweep_kernel(
     const uint64_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, int64_t n, int shift,
-    int64_t num_blocks, const uint32_t* __restrict__ offsets, uint64_t* __restrict__ keys_out,
-    uint32_t* __restrict__ vals_out) {
-    __shared__ uint32_t s_base[kRadix];                       // global base of each digit for this block
-    __shared__ uint32_t s_wave_cnt[kSortThreads / kWave][kRadix];
+    int64_t num_chunks, const uint32_t* __restrict__ offsets, const uint32_t* __restrict__ totals,
+    uint64_t* __restrict__ keys_out, uint32_t* __restrict__ vals_out) {
+    __shared__ uint64_t s_keys[kSortChunk];
+    __shared__ uint32_t s_vals[kPairs ? kSortChunk : 1];
+    __shared__ uint32_t s_cnt[kChunkWaves][kRadix];  // wave-private counters, then wave starts
+    __shared__ uint32_t s_local[kRadix];             // start of each digit in the reordered chunk
+    __shared__ uint32_t s_global[kRadix];            // output position of that start
+    __shared__ uint32_t s_wave[kSortThreads / kWave];
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
-    s_base[threadIdx.x] = offsets[(int64_t)threadIdx.x * num_blocks + blockIdx.x];
     const int64_t base = (int64_t)blockIdx.x * kSortChunk;
-    const uint64_t lt = lanemask_lt();
-    for (int r = 0; r < kSortRounds; ++r) {
-        const int64_t i = base + (int64_t)r * kSortThreads + threadIdx.x;
-        const bool valid = i < n;
-        uint64_t key = 0;
-        uint32_t val = 0;
-        uint32_t d = 0;
-        if (valid) {
-            key = keys_in[i];
-            val = vals_in[i];
-            d = (uint32_t)(key >> shift) & (kRadix - 1);
-        }
+    const int chunk_count = (int)min((int64_t)kSortChunk, n - base);
 #pragma unroll
-        for (int w = 0; w < kSortThreads / kWave; ++w) s_wave_cnt[w][threadIdx.x] = 0;
-        __syncthreads();
+    for (int w = 0; w < kChunkWaves; ++w) s_cnt[w][threadIdx.x] = 0;
+    __syncthreads();
+    // 1. per wave: stable ranks among equal digits (rank = keys of the digit before it in this
+    //    wave's quarter), packed as digit << 16 | rank
+    const uint64_t lt = lanemask_lt();
+    uint64_t key[kWaveRounds];
+    uint32_t val[kWaveRounds];
+    uint32_t dr[kWaveRounds];
+#pragma unroll
+    for (int r = 0; r < kWaveRounds; ++r) {
+        const int local = wave * kWaveKeys + r * kWave + lane;
+        const bool valid = local < chunk_count;
+        key[r] = valid ? keys_in[base + local] : 0ull;
+        val[r] = (kPairs && valid) ? vals_in[base + local] : 0u;
+        const uint32_t d = digit_of(key[r], shift);
         uint64_t peers = __ballot(valid);
 #pragma unroll
         for (int b = 0; b < kRadixBits; ++b) {
             const bool bit = ((d >> b) & 1u) != 0;
-            const uint64_t m = __ballot(valid && bit);
+            const uint64_t m = __ballot(bit);
             peers &= bit ? m : ~m;
         }
+        const uint32_t before = s_cnt[wave][d];  // read by all lanes before the leader updates
         const uint32_t rank = (uint32_t)__popcll(peers & lt);
-        if (valid && rank == 0) s_wave_cnt[wave][d] = (uint32_t)__popcll(peers);
-        __syncthreads();
-        {
-            // thread t owns digit t: turn per-wave counts into per-wave bases, advance s_base
-            const uint32_t c0 = s_wave_cnt[0][threadIdx.x];
-            const uint32_t c1 = s_wave_cnt[1][threadIdx.x];
-            const uint32_t c2 = s_wave_cnt[2][threadIdx.x];
-            const uint32_t c3 = s_wave_cnt[3][threadIdx.x];
-            const uint32_t b0 = s_base[threadIdx.x];
-            s_wave_cnt[0][threadIdx.x] = b0;
-            s_wave_cnt[1][threadIdx.x] = b0 + c0;
-            s_wave_cnt[2][threadIdx.x] = b0 + c0 + c1;
-            s_wave_cnt[3][threadIdx.x] = b0 + c0 + c1 + c2;
-            s_base[threadIdx.x] = b0 + c0 + c1 + c2 + c3;
-        }
-        __syncthreads();
-        if (valid) {
-            const uint32_t pos = s_wave_cnt[wave][d] + rank;
-            keys_out[pos] = key;
-            vals_out[pos] = val;
-        }
-        __syncthreads();
+        if (valid && rank == 0) s_cnt[wave][d] = before + (uint32_t)__popcll(peers);
+        __builtin_amdgcn_wave_barrier();
+        dr[r] = valid ? (d << 16) | (before + rank) : 0xffffffffu;
     }
-    (void)lane;
+    __syncthreads();
+    // 2. thread t = digit t: wave starts inside the digit, digit starts inside the chunk, and
+    //    the digit's output position for this chunk
+    {
+        const uint32_t c0 = s_cnt[0][threadIdx.x], c1 = s_cnt[1][threadIdx.x];
+        const uint32_t c2 = s_cnt[2][threadIdx.x], c3 = s_cnt[3][threadIdx.x];
+        uint32_t dummy;
+        const uint32_t start = block_exclusive_scan_256(c0 + c1 + c2 + c3, s_wave, dummy);
+        uint32_t tot_dummy;
+        const uint32_t digit_base = block_exclusive_scan_256(totals[threadIdx.x], s_wave, tot_dummy);
+        s_local[threadIdx.x] = start;
+        s_global[threadIdx.x] = digit_base + offsets[(int64_t)threadIdx.x * num_chunks + blockIdx.x];
+        s_cnt[0][threadIdx.x] = start;
+        s_cnt[1][threadIdx.x] = start + c0;
+        s_cnt[2][threadIdx.x] = start + c0 + c1;
+        s_cnt[3][threadIdx.x] = start + c0 + c1 + c2;
+    }
+    __syncthreads();
+    // 3. reorder the chunk by digit in LDS
+#pragma unroll
+    for (int r = 0; r < kWaveRounds; ++r) {
+        if (dr[r] != 0xffffffffu) {
+            const uint32_t pos = s_cnt[wave][dr[r] >> 16] + (dr[r] & 0xffffu);
+            s_keys[pos] = key[r];
+            if (kPairs) s_vals[pos] = val[r];
+        }
+    }
+    __syncthreads();
+    // 4. write out in order: runs of one digit go to consecutive addresses
+    for (int i = threadIdx.x; i < chunk_count; i += kSortThreads) {
+        const uint64_t k = s_keys[i];
+        const uint32_t d = digit_of(k, shift);
+        const uint32_t pos = s_global[d] + ((uint32_t)i - s_local[d]);
+        keys_out[pos] = k;
+        if (kPairs) vals_out[pos] = s_vals[i];
+    }
 }
 
 }  // namespace gsx_amd
 
 using namespace gsx_amd;
+
+namespace {
+
+template <bool kPairs>
+gsx_hip_status radix_sort_u64(uint64_t* keys, uint32_t* vals, uint64_t* keys_alt, uint32_t* vals_alt, int64_t n,
+                              int begin_bit, int end_bit, void* temp, int* out_in_alt, hipStream_t stream) {
+    if (begin_bit < 0 || end_bit > 64 || begin_bit > end_bit) return GSX_HIP_ERROR_INVALID_ARGUMENT;
+    if (n > (int64_t)UINT32_MAX) return GSX_HIP_ERROR_OUT_OF_RANGE;
+    int64_t chunks = (n + kSortChunk - 1) / kSortChunk;
+    if (chunks < 1) chunks = 1;
+    const int64_t hist_count = chunks * kRadix;
+    uint32_t* hist = static_cast<uint32_t*>(temp);
+    uint32_t* offsets = hist + hist_count;
+    uint32_t* totals = offsets + hist_count;
+    int in_alt = 0;
+    if (n > 0) {
+        for (int shift = begin_bit; shift < end_bit; shift += kRadixBits) {
+            uint64_t* kin = in_alt ? keys_alt : keys;
+            uint32_t* vin = in_alt ? vals_alt : vals;
+            uint64_t* kout = in_alt ? keys : keys_alt;
+            uint32_t* vout = in_alt ? vals : vals_alt;
+            hipLaunchKernelGGL(radix_upsweep_kernel, dim3((unsigned)chunks), dim3(kSortThreads), 0, stream, kin, n,
+                               shift, chunks, hist);
+            hipLaunchKernelGGL(radix_rowscan_kernel, dim3(kRadix), dim3(kSortThreads), 0, stream, hist, chunks,
+                               offsets, totals);
+            hipLaunchKernelGGL(radix_downsweep_kernel<kPairs>, dim3((unsigned)chunks), dim3(kSortThreads), 0, stream,
+                               kin, vin, n, shift, chunks, offsets, totals, kout, vout);
+            in_alt ^= 1;
+        }
+    }
+    if (out_in_alt) *out_in_alt = in_alt;
+    return (gsx_hip_status)hipGetLastError();
+}
+
+}  // namespace
 
 extern "C" {
 
@@ -224,42 +325,27 @@ gsx_hip_status gsx_hip_scan_exclusive_u32(const uint32_t* in, uint32_t* out, int
 }
 
 size_t gsx_hip_radix_sort_temp_bytes(int64_t n) {
-    int64_t blocks = (n + kSortChunk - 1) / kSortChunk;
-    if (blocks < 1) blocks = 1;
-    const int64_t hist_count = blocks * kRadix;
-    // hist + scanned offsets (hist_count + 1) + scan partials
-    return (size_t)(hist_count + hist_count + 1) * sizeof(uint32_t) + gsx_hip_scan_temp_bytes(hist_count) + 256;
+    int64_t chunks = (n + kSortChunk - 1) / kSortChunk;
+    if (chunks < 1) chunks = 1;
+    const int64_t hist_count = chunks * kRadix;
+    // hist + offsets + totals
+    return (size_t)(2 * hist_count + kRadix) * sizeof(uint32_t) + 256;
 }
+
 
 // Stable LSD sort of n pairs on key bits [begin_bit, end_bit). The result ends in (keys, vals)
 // when *out_in_alt == 0, else in (keys_alt, vals_alt).
 gsx_hip_status gsx_hip_radix_sort_pairs_u64(uint64_t* keys, uint32_t* vals, uint64_t* keys_alt, uint32_t* vals_alt,
-                                        int64_t n, int begin_bit, int end_bit, void* temp, int* out_in_alt,
-                                        hipStream_t stream) {
-    int64_t blocks = (n + kSortChunk - 1) / kSortChunk;
-    if (blocks < 1) blocks = 1;
-    const int64_t hist_count = blocks * kRadix;
-    uint32_t* hist = static_cast<uint32_t*>(temp);
-    uint32_t* offsets = hist + hist_count;
-    void* scan_temp = offsets + hist_count + 1;
-    int in_alt = 0;
-    if (n > 0) {
-        for (int shift = begin_bit; shift < end_bit; shift += kRadixBits) {
-            uint64_t* kin = in_alt ? keys_alt : keys;
-            uint32_t* vin = in_alt ? vals_alt : vals;
-            uint64_t* kout = in_alt ? keys : keys_alt;
-            uint32_t* vout = in_alt ? vals : vals_alt;
-            hipLaunchKernelGGL(radix_hist_kernel, dim3((unsigned)blocks), dim3(kSortThreads), 0, stream, kin, n,
-                               shift, blocks, hist);
-            gsx_hip_status e = gsx_hip_scan_exclusive_u32(hist, offsets, hist_count, scan_temp, stream);
-            if (e != GSX_HIP_SUCCESS) return e;
-            hipLaunchKernelGGL(radix_scatter_kernel, dim3((unsigned)blocks), dim3(kSortThreads), 0, stream, kin, vin,
-                               n, shift, blocks, offsets, kout, vout);
-            in_alt ^= 1;
-        }
-    }
-    if (out_in_alt) *out_in_alt = in_alt;
-    return (gsx_hip_status)hipGetLastError();
+                                            int64_t n, int begin_bit, int end_bit, void* temp, int* out_in_alt,
+                                            hipStream_t stream) {
+    return radix_sort_u64<true>(keys, vals, keys_alt, vals_alt, n, begin_bit, end_bit, temp, out_in_alt, stream);
+}
+
+// Stable LSD sort of n keys on bits [begin_bit, end_bit); bits outside the range travel with
+// the key (a payload packed into the low bits keeps input order among equal sort bits).
+gsx_hip_status gsx_hip_radix_sort_keys_u64(uint64_t* keys, uint64_t* keys_alt, int64_t n, int begin_bit, int end_bit,
+                                           void* temp, int* out_in_alt, hipStream_t stream) {
+    return radix_sort_u64<false>(keys, nullptr, keys_alt, nullptr, n, begin_bit, end_bit, temp, out_in_alt, stream);
 }
 
 }  // extern "C"

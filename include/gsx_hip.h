@@ -107,11 +107,17 @@ typedef struct gsx_hip_render_stats {
     int64_t instance_count;  /* (tile, Gaussian) pairs sorted */
     int32_t tile_count;
     int32_t sort_passes;
+    /* layout of sorted_keys: tile << key_tile_shift | (bits(depth) - key_depth_base) <<
+     * key_depth_shift | emission position in the low key_payload_bits bits (0: not packed) */
+    int32_t key_tile_shift;
+    int32_t key_depth_shift;
+    uint32_t key_depth_base;
+    int32_t key_payload_bits;
 } gsx_hip_render_stats;
 
 /* Device pointers of the intermediates a forward retains (valid until the next forward). */
 typedef struct gsx_hip_render_buffers {
-    const uint64_t* sorted_keys;   /* [instance_count] (tile << 32) | float_bits(depth) */
+    const uint64_t* sorted_keys;   /* [instance_count] see gsx_hip_render_stats for the layout */
     const uint32_t* sorted_values; /* [instance_count] emission position of each sorted key */
     const uint32_t* tile_ranges;   /* [tile_count][2] start, end */
     const float* records;          /* [N][12] packed per-Gaussian blend records */
@@ -161,9 +167,15 @@ size_t gsx_hip_scan_temp_bytes(int64_t n);
 gsx_hip_status gsx_hip_scan_exclusive_u32(const uint32_t* in, uint32_t* out, int64_t n, void* temp,
                                           hipStream_t stream);
 size_t gsx_hip_radix_sort_temp_bytes(int64_t n);
+/* Stable LSD sort of (key, value) pairs on key bits [begin_bit, end_bit), 8 bits per pass. */
 gsx_hip_status gsx_hip_radix_sort_pairs_u64(uint64_t* keys, uint32_t* values, uint64_t* keys_alt,
                                             uint32_t* values_alt, int64_t n, int begin_bit, int end_bit, void* temp,
                                             int* out_result_in_alt, hipStream_t stream);
+/* Stable LSD sort of keys alone on bits [begin_bit, end_bit); the other bits travel with the key
+ * (the render path packs the emission position below begin_bit). No counterpart in the CUDA
+ * backend, which always sorts pairs. */
+gsx_hip_status gsx_hip_radix_sort_keys_u64(uint64_t* keys, uint64_t* keys_alt, int64_t n, int begin_bit,
+                                           int end_bit, void* temp, int* out_result_in_alt, hipStream_t stream);
 
 /* ---- losses -----------------------------------------------------------------------------------
  * Replace gsx_cuda_loss_*_kernel_launch (gsx/src/gsx-cuda/internal.h:314-371); semantics of

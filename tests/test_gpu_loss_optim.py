@@ -157,6 +157,32 @@ def test_radix_sort_stable(n, end_bit):
     assert np.array_equal(vo.cpu().numpy().view(np.uint32), vals[order])
 
 
+@pytest.mark.parametrize("n,lo,hi", [(1, 23, 63), (4096, 23, 63), (4097, 5, 45), (1_000_003, 23, 63),
+                                     (3_000_000, 20, 60)])
+def test_radix_sort_keys_stable(n, lo, hi):
+    """Keys-only sort on bits [lo, hi): the low payload (an index) keeps input order among equal
+    sort bits, i.e. the result equals a stable sort by the sort bits; duplicates are dense."""
+    from gsx_amd import _lib
+    lib = _lib.load()
+    rng = np.random.default_rng(n + lo)
+    span = hi - lo
+    sort_part = rng.integers(0, 1 << min(span, 12), size=n, dtype=np.uint64) << np.uint64(span - min(span, 12))
+    payload = rng.permutation(n).astype(np.uint64) & np.uint64((1 << lo) - 1)
+    keys = (sort_part << np.uint64(lo)) | payload
+    k = torch.from_numpy(keys.view(np.int64)).cuda()
+    k2 = torch.empty_like(k)
+    temp = torch.empty(lib.gsx_hip_radix_sort_temp_bytes(n), dtype=torch.uint8, device="cuda")
+    in_alt = ctypes.c_int(0)
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    print(f"[case] keys sort n={n} bits=[{lo},{hi})", flush=True)
+    _lib.check(lib.gsx_hip_radix_sort_keys_u64(k.data_ptr(), k2.data_ptr(), n, lo, lo + ((span + 7) // 8) * 8,
+                                               temp.data_ptr(), ctypes.byref(in_alt), s))
+    torch.cuda.synchronize()
+    ko = (k2 if in_alt.value else k).cpu().numpy().view(np.uint64)
+    order = np.argsort(keys >> np.uint64(lo), kind="stable")
+    assert np.array_equal(ko, keys[order])
+
+
 def test_scan_exclusive():
     from gsx_amd import _lib
     lib = _lib.load()
