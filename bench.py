@@ -33,28 +33,30 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def algorithmic_bytes(stage, n, visible, instances, tiles, pixels, sort_passes):
-    """Bytes each stage must move at minimum (the roofline numerators)."""
+def algorithmic_bytes(stage, n, visible, instances, tiles, pixels, sort_passes, keys_only, train=True):
+    """Bytes each stage must move at minimum, given this build's data layout (the roofline
+    numerators). n Gaussians, visible V, instances I, tiles T, pixels Px, E = 3 Px elements."""
+    i = instances
     if stage == "preprocess":
-        return 56 * n + 52 * visible
+        return 60 * n + (80 if train else 48) * visible
     if stage == "scan":
         return 8 * n
     if stage == "emit":
-        return 32 * visible + 12 * instances
+        return 8 * n + 48 * visible + 12 * i
     if stage == "sort":
-        return 8 * instances + sort_passes * 24 * instances
+        return 8 * i + sort_passes * (16 if keys_only else 24) * i
     if stage == "ranges":
-        return 8 * instances + 8 * tiles
+        return 20 * i + 8 * tiles
     if stage == "blend_forward":
-        return 52 * instances + 8 * tiles + 20 * pixels
+        return 52 * i + 20 * pixels + (32 * i if train else 0)
     if stage == "blend_backward":
-        return 84 * instances + 8 * tiles + 20 * pixels + 36 * instances
+        return 156 * i + 20 * pixels
     if stage == "instance_reduce":
-        return 36 * instances + 8 * n + 36 * n
+        return 36 * i + 40 * n
     if stage == "projection_backward":
-        return 56 * n + 36 * visible + 56 * n
+        return 148 * n
     if stage == "loss_forward":
-        return 28 * 3 * pixels
+        return 24 * 3 * pixels
     if stage == "loss_backward":
         return 28 * 3 * pixels
     if stage == "adam":
@@ -116,7 +118,7 @@ def main():
     ap.add_argument("--poses", type=int, default=24)
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="run one plain copy kernel of this size first (reference for traffic counters)")
-    ap.add_argument("--cpu-baseline-iters", type=int, default=1,
+    ap.add_argument("--cpu-baseline-iters", type=int, default=3,
                     help="reference CPU steps to time on the full workload (0 disables)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -250,7 +252,8 @@ def main():
     tiles = int(stats.tile_count)
     kernels = []
     for name, ms in stage_ms.items():
-        b = algorithmic_bytes(name, args.gaussians, visible, instances, tiles, pixels, int(stats.sort_passes))
+        b = algorithmic_bytes(name, args.gaussians, visible, instances, tiles, pixels, int(stats.sort_passes),
+                              int(stats.key_payload_bits) > 0)
         gbps = b / (ms * 1e-3) / 1e9 if ms > 0 else 0.0
         kernels.append({"stage": name, "ms": round(ms, 4), "algorithmic_bytes": int(b), "gbps": round(gbps, 1),
                         "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4)})

@@ -568,7 +568,7 @@ gsx_hip_status gsx_hip_adc_step(gsx_hip_adc_context* ctx, const gsx_hip_adc_para
     return GSX_HIP_SUCCESS;
 }
 
-// Replaces gsx_cuda_gather_rows_kernel_launch (gsx/src/gsx-cuda/internal.h:372-381): out row r =
+// Replaces gsx_cuda_gather_rows_kernel_launch (gsx/src/gsx-cuda/internal.h:396-405): out row r =
 // src row index[r]. An index outside [0, src_row_count) sets *out_has_out_of_range (device int,
 // may be null) and leaves that row unwritten; the host decides when to read the flag, so no
 // synchronisation happens here (the CUDA backend syncs per gather, gsx-cuda/buffer.c:1179-1207).

@@ -236,7 +236,7 @@ static unsigned pointwise_blocks(int64_t n) {
 
 extern "C" {
 
-// Replace gsx_cuda_loss_{l1,mse}_f32_{forward,backward}_kernel_launch (gsx-cuda/internal.h:314-345).
+// Replace gsx_cuda_loss_{l1,mse}_f32_{forward,backward}_kernel_launch (gsx-cuda/internal.h:312-343).
 gsx_hip_status gsx_hip_loss_l1_f32_forward_kernel_launch(float* loss_map, const float* prediction, const float* target,
                                                      int64_t total_elements, float scale, hipStream_t stream) {
     hipLaunchKernelGGL(l1_forward_kernel, dim3(pointwise_blocks(total_elements)), dim3(256), 0, stream, loss_map,
@@ -267,7 +267,7 @@ gsx_hip_status gsx_hip_loss_mse_f32_backward_kernel_launch(float* grad_predictio
     return (gsx_hip_status)hipGetLastError();
 }
 
-// Replace gsx_cuda_loss_ssim_chw_f32_{forward,backward}_kernel_launch (internal.h:346-371).
+// Replace gsx_cuda_loss_ssim_chw_f32_{forward,backward}_kernel_launch (gsx-cuda/internal.h:344-369).
 // ssim_workspace holds the three dm maps: 3 * outer_count * channels * height * width floats.
 // l1_scale/l1_grad_scale fuse a preceding L1 term in the same pass (0 disables the fusion);
 // the result is bit-identical to running the L1 launcher first.

@@ -9,7 +9,7 @@
  * runtime error, or a negative GSX_HIP_ERROR_* code; gsx_hip_last_error_message() names the
  * failing condition (thread-local, static storage).
  *
- * Conventions shared with gsx (gsx/include/gsx/gsx-render.h:64-140, gsx-base.h:207-216):
+ * Conventions shared with gsx (gsx/include/gsx/gsx-render.h:64-140, gsx-base.h:191-216):
  *   Gaussians: mean3d [N,3], rotation [N,4] (xyzw), logscale [N,3], opacity [N] (logit),
  *   sh0 [N,3], sh1 [N,3,3], sh2 [N,5,3], sh3 [N,7,3], all float32 row-major on the device;
  *   images: float32 CHW [3,H,W]; camera: pinhole, world-to-camera pose, +z forward, y down.
@@ -61,13 +61,13 @@ gsx_hip_status gsx_hip_copy_f32(float* dst, const float* src, int64_t count, hip
 
 /* ---- render ---------------------------------------------------------------------------------
  * Replaces gsx_cuda_fastgs_forward_launch / gsx_cuda_fastgs_backward_launch
- * (gsx/src/gsx-cuda/internal.h:534-628) and the renderer vtable behaviour of the CPU oracle
+ * (gsx/src/gsx-cuda/internal.h:545-630) and the renderer vtable behaviour of the CPU oracle
  * (gsx/src/gsx-cpu/render.c:1254-1975). The render context owns every intermediate buffer
  * (pooled, grow-only; the fastgs resize callbacks and per-forward allocations are gone) and
  * the state a TRAIN forward retains for the backward.
  */
 typedef struct gsx_hip_camera {
-    float fx, fy, cx, cy;   /* gsx_camera_intrinsics (gsx-base.h:183-197) */
+    float fx, fy, cx, cy;   /* gsx_camera_intrinsics (gsx-base.h:191-205) */
     int32_t width, height;
     float rot[4];           /* gsx_camera_pose.rot, world-to-camera quaternion, xyzw */
     float transl[3];        /* gsx_camera_pose.transl */
@@ -178,7 +178,7 @@ gsx_hip_status gsx_hip_radix_sort_keys_u64(uint64_t* keys, uint64_t* keys_alt, i
                                            int end_bit, void* temp, int* out_result_in_alt, hipStream_t stream);
 
 /* ---- losses -----------------------------------------------------------------------------------
- * Replace gsx_cuda_loss_*_kernel_launch (gsx/src/gsx-cuda/internal.h:314-371); semantics of
+ * Replace gsx_cuda_loss_*_kernel_launch (gsx/src/gsx-cuda/internal.h:312-369, CHW forms); semantics of
  * gsx/src/gsx-cpu/loss.c:316-709 (accumulate into loss_map / grad_prediction; grad_scale is
  * already normalised as gsx_loss_scale_grad, gsx-tensor-helpers.h:236-244). */
 gsx_hip_status gsx_hip_loss_l1_f32_forward_kernel_launch(float* loss_map, const float* prediction,
@@ -280,7 +280,7 @@ gsx_hip_status gsx_hip_adc_step(gsx_hip_adc_context* context, const gsx_hip_adc_
                                 gsx_hip_gs_rows* rows, int64_t capacity, gsx_hip_gs_rows* out,
                                 int32_t* out_result_in_out, int64_t* out_counts, hipStream_t stream);
 
-/* Replaces gsx_cuda_gather_rows_kernel_launch (gsx/src/gsx-cuda/internal.h:372-381): out row r
+/* Replaces gsx_cuda_gather_rows_kernel_launch (gsx/src/gsx-cuda/internal.h:396-405): out row r
  * = src row src_indices[r]; an index outside [0, src_row_count) sets *out_has_out_of_range
  * (a device int, may be null; the CPU returns GSX_ERROR_OUT_OF_RANGE, gsx-cpu/core.c:1322-1324).
  * No host synchronisation. */
