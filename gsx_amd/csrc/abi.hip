@@ -606,6 +606,10 @@ gsx_hip_status gsx_hip_render_backward(gsx_hip_render_context* ctx, const float*
         hipLaunchKernelGGL(reduce_instance_grads_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, n,
                            ctx->offsets.as<uint32_t>(), ctx->inst_grad.as<float>(), ctx->grad2d.as<float>());
         GSX_HIP_TRY(hipGetLastError(), "reduce_instance_grads_kernel");
+        hipLaunchKernelGGL(reduce_long_runs_kernel, dim3(kBigBlocks), dim3(256), 0, stream,
+                           ctx->big_list.as<uint32_t>() + 1, ctx->big_list.as<uint32_t>(), ctx->offsets.as<uint32_t>(),
+                           ctx->inst_grad.as<float>(), ctx->grad2d.as<float>());
+        GSX_HIP_TRY(hipGetLastError(), "reduce_long_runs_kernel");
     }
     GSX_TRY(record(ctx, 9, stream));
     if (n > 0) {

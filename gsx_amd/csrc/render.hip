@@ -691,51 +691,90 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
     }
 }
 
-// grad2d[g] = sum of instance_grad over g's emission positions [offset[g], offset[g+1]).
-// Lanes sum their own Gaussian when it has at most 32 instances; larger runs (full-screen
-// Gaussians have thousands) are summed by the whole wave. Overwrites grad2d, so no zero fill.
+// grad2d[g] = sum of instance_grad over g's emission positions [offset[g], offset[g+1]), in two
+// kernels with disjoint outputs (both overwrite, so no zero fill):
+//  * runs of at most kLaneRun instances: a workgroup covers 256 consecutive Gaussians, whose
+//    runs are one contiguous range; the range is staged through LDS in instance-aligned pieces
+//    with coalesced loads, and each thread sums its own run from LDS;
+//  * longer runs (only boxes of more than kBigTiles tiles have them, so they are all on the
+//    big-box list): one workgroup per Gaussian, 256 instances per step, then a DPP/LDS tree.
+constexpr uint32_t kLaneRun = kBigTiles;
+constexpr uint32_t kPieceInstances = 448;  // 4032 floats = 15.75 KB of LDS per piece
+
 __global__ __launch_bounds__(256) void reduce_instance_grads_kernel(int64_t n, const uint32_t* __restrict__ offsets,
                                                                     const float* __restrict__ instance_grad,
                                                                     float* __restrict__ grad2d) {
-    constexpr uint32_t kLaneMax = 32;
-    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    __shared__ float s_piece[kPieceInstances * kGrad2d];
+    const int64_t g0 = (int64_t)blockIdx.x * blockDim.x;
+    const int64_t g = g0 + threadIdx.x;
+    const int64_t g_end = min(g0 + (int64_t)blockDim.x, n);
     uint32_t b = 0, e = 0;
     if (g < n) {
         b = offsets[g];
         e = offsets[g + 1];
     }
-    const uint32_t count = e - b;
-    if (g < n && count <= kLaneMax) {
-        float acc[kGrad2d];
+    const bool mine = g < n && e - b <= kLaneRun;
+    float acc[kGrad2d];
 #pragma unroll
-        for (int c = 0; c < kGrad2d; ++c) acc[c] = 0.0f;
-        for (uint32_t p = b; p < e; ++p) {
+    for (int c = 0; c < kGrad2d; ++c) acc[c] = 0.0f;
+    const uint32_t r0 = offsets[g0], r1 = offsets[g_end];
+    for (uint32_t p0 = r0; p0 < r1; p0 += kPieceInstances) {
+        const uint32_t p1 = min(p0 + kPieceInstances, r1);
+        // pieces that lie inside long runs only are skipped (uniform)
+        const bool need = mine && b < p1 && e > p0;
+        if (__syncthreads_or(need ? 1 : 0) == 0) continue;
+        const uint32_t floats = (p1 - p0) * kGrad2d;
+        const float* src = instance_grad + (size_t)p0 * kGrad2d;
+        for (uint32_t i = threadIdx.x; i < floats; i += blockDim.x) s_piece[i] = src[i];
+        __syncthreads();
+        if (need) {
+            const uint32_t lo = max(b, p0), hi = min(e, p1);
+            for (uint32_t p = lo; p < hi; ++p) {
+                const float* v = &s_piece[(p - p0) * kGrad2d];
 #pragma unroll
-            for (int c = 0; c < kGrad2d; ++c) acc[c] += instance_grad[(size_t)p * kGrad2d + c];
+                for (int c = 0; c < kGrad2d; ++c) acc[c] += v[c];
+            }
         }
+        __syncthreads();
+    }
+    if (mine) {
 #pragma unroll
         for (int c = 0; c < kGrad2d; ++c) grad2d[g * kGrad2d + c] = acc[c];
     }
-    uint64_t big = __ballot(g < n && count > kLaneMax);
-    const uint32_t lane = __lane_id();
-    const int64_t wave_base = g - (int64_t)lane;
-    while (big != 0ull) {
-        const uint32_t l = (uint32_t)__builtin_ctzll(big);
-        big &= big - 1ull;
-        const int64_t gb = wave_base + l;
-        const uint32_t bb = offsets[gb], ee = offsets[gb + 1];
+}
+
+__global__ __launch_bounds__(256) void reduce_long_runs_kernel(const uint32_t* __restrict__ big_list,
+                                                               const uint32_t* __restrict__ big_count,
+                                                               const uint32_t* __restrict__ offsets,
+                                                               const float* __restrict__ instance_grad,
+                                                               float* __restrict__ grad2d) {
+    __shared__ float s_wave[kBlendThreads / kWave][kGrad2d];
+    const uint32_t count = *big_count;
+    const uint32_t lane = __lane_id(), wave = threadIdx.x / kWave;
+    for (uint32_t i = blockIdx.x; i < count; i += gridDim.x) {
+        const uint32_t g = big_list[i];
+        const uint32_t b = offsets[g], e = offsets[g + 1];
+        if (e - b <= kLaneRun) continue;  // uniform; summed by reduce_instance_grads_kernel
         float acc[kGrad2d];
 #pragma unroll
         for (int c = 0; c < kGrad2d; ++c) acc[c] = 0.0f;
-        for (uint32_t p = bb + lane; p < ee; p += kWave) {
+        for (uint32_t p = b + threadIdx.x; p < e; p += blockDim.x) {
+            const float* v = instance_grad + (size_t)p * kGrad2d;
 #pragma unroll
-            for (int c = 0; c < kGrad2d; ++c) acc[c] += instance_grad[(size_t)p * kGrad2d + c];
+            for (int c = 0; c < kGrad2d; ++c) acc[c] += v[c];
         }
 #pragma unroll
-        for (int c = 0; c < kGrad2d; ++c) {
-            const float v = wave_reduce_sum(acc[c]);
-            if (lane == 0) grad2d[gb * kGrad2d + c] = v;
+        for (int c = 0; c < kGrad2d; ++c) acc[c] = wave_reduce_sum(acc[c]);
+        if (lane == 0) {
+#pragma unroll
+            for (int c = 0; c < kGrad2d; ++c) s_wave[wave][c] = acc[c];
         }
+        __syncthreads();
+        if (threadIdx.x < kGrad2d) {
+            const int c = threadIdx.x;
+            grad2d[(size_t)g * kGrad2d + c] = (s_wave[0][c] + s_wave[1][c]) + (s_wave[2][c] + s_wave[3][c]);
+        }
+        __syncthreads();
     }
 }
 
