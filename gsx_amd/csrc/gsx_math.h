@@ -179,6 +179,36 @@ GSX_HD float gsx_expf(float x)
     return gsx_expf_table(x, 0);
 }
 
+/* gsx_expf_table for |x| < 88 (finite), without the special-case branch: bit-identical to it
+ * there. The blend kernels only evaluate powers in [-4.5, 0]. */
+GSX_HD float gsx_expf_small(float x, const uint64_t *table)
+{
+    const double inv_ln2_n = 0x1.71547652b82fep+0 * 32.0;
+    const double shift = 0x1.8p+52;
+    const double c0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
+    const double c1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
+    const double c2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+    double xd = (double)x;
+    double z = inv_ln2_n * xd;
+    double kd = z + shift;
+    uint64_t ki = gsx_f64_bits(kd);
+    double r;
+    double r2;
+    double y;
+    uint64_t t;
+
+    kd -= shift;
+    r = GSX_FMA(inv_ln2_n, xd, -kd);
+    t = table[ki % 32u];
+    t += ki << (52 - GSX_EXP2_TABLE_BITS);
+    z = GSX_FMA(c0, r, c1);
+    r2 = r * r;
+    y = GSX_FMA(c2, r, 1.0);
+    y = GSX_FMA(z, r2, y);
+    y = y * gsx_f64_from_bits(t);
+    return (float)y;
+}
+
 /* PCG32 as in gsx/src/pcg32.h:41-119 (O'Neill's pcg32 with the tiny-cuda-nn packaging):
  * 64-bit LCG state, XSH-RR output, seeding init(seed, seed) as gsx/src/gsx-random.c:25. */
 #define GSX_PCG32_MULT 0x5851f42d4c957f2dULL

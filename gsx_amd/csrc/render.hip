@@ -405,33 +405,32 @@ __global__ __launch_bounds__(kBlendThreads) void blend_forward_kernel(
         }
         __syncthreads();
         const int count = (int)min((uint32_t)kBlendThreads, range.y - base);
-        if (!done) {
-            for (int k = 0; k < count; ++k) {
-                if (ckpt != nullptr && (k & (kBucket - 1)) == 0) {
-                    ckpt[checkpoint_slot(range.x, tile, base + (uint32_t)k) * kBlendThreads + threadIdx.x] = t;
-                }
-                const float4 r2 = s_r2[k];
-                if (!in_box(px, py, __float_as_uint(r2.y), __float_as_uint(r2.z))) continue;
-                const float4 r0 = s_r0[k];
-                const float4 r1 = s_r1[k];
-                const float dx = fpx - r0.x;
-                const float dy = fpy - r0.y;
-                float power = -0.5f * (r0.z * dx * dx + r0.w * dx * dy + r1.x * dy * dy);
-                if (power > 0.0f) power = 0.0f;
-                if (power < kPowerThreshold) continue;
-                const float alpha = fminf(kMaxFragmentAlpha, r1.y * gsx_expf_table(power, s_exp2));
-                if (alpha < kMinAlpha) continue;
-                const float w = alpha * t;
-                c0 += w * r1.z;
-                c1 += w * r1.w;
-                c2 += w * r2.x;
-                t = t * (1.0f - alpha);
-                last = base + (uint32_t)k + 1u;
-                if (t < kTransmittanceThreshold) {
-                    done = true;
-                    break;
-                }
+        for (int k = 0; k < count; ++k) {
+            if (__ballot(!done) == 0ull) break;  // uniform: every pixel of this wave is saturated
+            if (ckpt != nullptr && !done && (k & (kBucket - 1)) == 0) {
+                ckpt[checkpoint_slot(range.x, tile, base + (uint32_t)k) * kBlendThreads + threadIdx.x] = t;
             }
+            const float4 r2 = s_r2[k];
+            const bool live = !done && in_box(px, py, __float_as_uint(r2.y), __float_as_uint(r2.z));
+            if (__ballot(live) == 0ull) continue;  // uniform
+            // branch-free evaluation for the wave; lanes outside the box or done keep their state
+            const float4 r0 = s_r0[k];
+            const float4 r1 = s_r1[k];
+            const float dx = fpx - r0.x;
+            const float dy = fpy - r0.y;
+            float power = -0.5f * (r0.z * dx * dx + r0.w * dx * dy + r1.x * dy * dy);
+            power = power > 0.0f ? 0.0f : power;
+            bool ok = live && power >= kPowerThreshold;
+            const float gval = gsx_expf_small(ok ? power : 0.0f, s_exp2);
+            const float alpha = fminf(kMaxFragmentAlpha, r1.y * gval);
+            ok = ok && alpha >= kMinAlpha;
+            const float w = alpha * t;
+            c0 = ok ? c0 + w * r1.z : c0;
+            c1 = ok ? c1 + w * r1.w : c1;
+            c2 = ok ? c2 + w * r2.x : c2;
+            t = ok ? t * (1.0f - alpha) : t;
+            last = ok ? base + (uint32_t)k + 1u : last;
+            done = done || (ok && t < kTransmittanceThreshold);
         }
         __syncthreads();
     }
@@ -582,33 +581,32 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
             float gv[kBucket];
             uint32_t mask = 0u;
             // forward replay of the bucket from its checkpoint (render.c:1476-1515)
-            if (inside && j0 < last) {
+            {
                 float tt = s_ck[sb][threadIdx.x];
+                const bool pixel_live = inside && j0 < last;
 #pragma unroll
                 for (int i = 0; i < kBucket; ++i) {
                     tb[i] = tt;
                     gv[i] = 0.0f;
-                    if (i < n_in && j0 + (uint32_t)i < last) {
-                        const int kk = sb * kBucket + i;
-                        const float4 r2 = s_r2[kk];
-                        if (in_box(px, py, __float_as_uint(r2.y), __float_as_uint(r2.z))) {
-                            const float4 r0 = s_r0[kk];
-                            const float4 r1 = s_r1[kk];
-                            const float dx = fpx - r0.x;
-                            const float dy = fpy - r0.y;
-                            float power = -0.5f * (r0.z * dx * dx + r0.w * dx * dy + r1.x * dy * dy);
-                            if (power > 0.0f) power = 0.0f;
-                            if (power >= kPowerThreshold) {
-                                const float gval = gsx_expf_table(power, s_exp2);
-                                const float alpha = fminf(kMaxFragmentAlpha, r1.y * gval);
-                                if (alpha >= kMinAlpha) {
-                                    mask |= 1u << i;
-                                    gv[i] = gval;
-                                    tt = tt * (1.0f - alpha);
-                                }
-                            }
-                        }
-                    }
+                    if (i >= n_in) continue;  // uniform
+                    const int kk = sb * kBucket + i;
+                    const float4 r2 = s_r2[kk];
+                    const bool live = pixel_live && j0 + (uint32_t)i < last &&
+                                      in_box(px, py, __float_as_uint(r2.y), __float_as_uint(r2.z));
+                    if (__ballot(live) == 0ull) continue;  // uniform
+                    const float4 r0 = s_r0[kk];
+                    const float4 r1 = s_r1[kk];
+                    const float dx = fpx - r0.x;
+                    const float dy = fpy - r0.y;
+                    float power = -0.5f * (r0.z * dx * dx + r0.w * dx * dy + r1.x * dy * dy);
+                    power = power > 0.0f ? 0.0f : power;
+                    bool ok = live && power >= kPowerThreshold;
+                    const float gval = gsx_expf_small(ok ? power : 0.0f, s_exp2);
+                    const float alpha = fminf(kMaxFragmentAlpha, r1.y * gval);
+                    ok = ok && alpha >= kMinAlpha;
+                    mask |= ok ? (1u << i) : 0u;
+                    gv[i] = ok ? gval : 0.0f;
+                    tt = ok ? tt * (1.0f - alpha) : tt;
                 }
             }
             // back to front over the bucket (render.c:1559-1666 per contribution)
@@ -617,57 +615,54 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
                 if (i >= n_in) continue;  // uniform
                 const int kk = sb * kBucket + i;
                 const bool contrib = ((mask >> i) & 1u) != 0u;
-                float g_mx = 0.0f, g_my = 0.0f, g_ca = 0.0f, g_cb = 0.0f, g_cc = 0.0f;
-                float g_c0 = 0.0f, g_c1 = 0.0f, g_c2 = 0.0f, g_op = 0.0f;
-                if (contrib) {
-                    const float4 r0 = s_r0[kk];
-                    const float4 r1 = s_r1[kk];
-                    const float4 r2 = s_r2[kk];
-                    const float dx = fpx - r0.x;
-                    const float dy = fpy - r0.y;
-                    const float gval = gv[i];
-                    const float op = r1.y;
-                    const float alpha = fminf(kMaxFragmentAlpha, op * gval);
-                    const float t_before = tb[i];
-                    const float w = alpha * t_before;
-                    float dalpha = t_before * (r1.z * d0 + r1.w * d1 + r2.x * d2);
-                    g_c0 = w * d0;
-                    g_c1 = w * d1;
-                    g_c2 = w * d2;
-                    if (fabsf(1.0f - alpha) > 1.0e-6f) {
-                        dalpha -= (s0 * d0 + s1 * d1 + s2 * d2) / (1.0f - alpha);
-                    }
-                    float dg = 0.0f;
-                    if (op * gval < kMaxFragmentAlpha) {
-                        dg = dalpha * op;
-                        g_op = dalpha * gval;
-                    }
-                    const float dpow = dg * gval;
-                    const float inv_a = r0.z, inv_b = r0.w * 0.5f, inv_c = r1.x;
-                    g_mx = dpow * (inv_a * dx + inv_b * dy);
-                    g_my = dpow * (inv_b * dx + inv_c * dy);
-                    const float dia = dpow * (-0.5f * dx * dx);
-                    const float dib = dpow * (-dx * dy);
-                    const float dic = dpow * (-0.5f * dy * dy);
-                    const float4 k0 = s_k0[kk];
-                    const float2 k1 = s_k1[kk];
-                    g_ca = dia * k0.x + dib * k0.y + dic * k0.z;
-                    g_cb = dia * (2.0f * k0.y) + dib * k0.w + dic * (2.0f * k1.x);
-                    g_cc = dia * k0.z + dib * k1.x + dic * k1.y;
-                    s0 += w * r1.z;
-                    s1 += w * r1.w;
-                    s2 += w * r2.x;
+                if (__ballot(contrib) == 0ull) {  // uniform: no pixel of this wave
+                    if (lane < 4 * kGrad2d) s_acc[wave * 4 + lane / kGrad2d][i][lane % kGrad2d] = 0.0f;
+                    continue;
                 }
-                if (__ballot(contrib) != 0ull) {
-                    float v[kGrad2d] = {g_mx, g_my, g_ca, g_cb, g_cc, g_c0, g_c1, g_c2, g_op};
-                    row_reduce_sums(v);
-                    if ((threadIdx.x & (kTile - 1)) == 0) {
-                        float* acc = &s_acc[row][i][0];
+                const float4 r0 = s_r0[kk];
+                const float4 r1 = s_r1[kk];
+                const float4 r2 = s_r2[kk];
+                const float dx = fpx - r0.x;
+                const float dy = fpy - r0.y;
+                const float gval = gv[i];
+                const float op = r1.y;
+                const float alpha = fminf(kMaxFragmentAlpha, op * gval);
+                const float t_before = tb[i];
+                const float w = contrib ? alpha * t_before : 0.0f;
+                float dalpha = t_before * (r1.z * d0 + r1.w * d1 + r2.x * d2);
+                const float one_minus = 1.0f - alpha;
+                // an exact division as the CPU's: near-plane Gaussians' covariance gradients
+                // amplify even 1-ulp differences of this term
+                if (fabsf(one_minus) > 1.0e-6f) {
+                    dalpha -= (s0 * d0 + s1 * d1 + s2 * d2) / one_minus;
+                }
+                const bool unclamped = op * gval < kMaxFragmentAlpha;
+                const float dg = (contrib && unclamped) ? dalpha * op : 0.0f;
+                const float g_op = (contrib && unclamped) ? dalpha * gval : 0.0f;
+                const float dpow = dg * gval;
+                const float inv_a = r0.z, inv_b = r0.w * 0.5f, inv_c = r1.x;
+                const float dia = dpow * (-0.5f * dx * dx);
+                const float dib = dpow * (-dx * dy);
+                const float dic = dpow * (-0.5f * dy * dy);
+                const float4 k0 = s_k0[kk];
+                const float2 k1 = s_k1[kk];
+                float v[kGrad2d] = {dpow * (inv_a * dx + inv_b * dy),
+                                    dpow * (inv_b * dx + inv_c * dy),
+                                    dia * k0.x + dib * k0.y + dic * k0.z,
+                                    dia * (2.0f * k0.y) + dib * k0.w + dic * (2.0f * k1.x),
+                                    dia * k0.z + dib * k1.x + dic * k1.y,
+                                    w * d0,
+                                    w * d1,
+                                    w * d2,
+                                    g_op};
+                s0 += w * r1.z;
+                s1 += w * r1.w;
+                s2 += w * r2.x;
+                row_reduce_sums(v);
+                if ((threadIdx.x & (kTile - 1)) == 0) {
+                    float* acc = &s_acc[row][i][0];
 #pragma unroll
-                        for (int c = 0; c < kGrad2d; ++c) acc[c] = v[c];
-                    }
-                } else if (lane < 4 * kGrad2d) {
-                    s_acc[wave * 4 + lane / kGrad2d][i][lane % kGrad2d] = 0.0f;
+                    for (int c = 0; c < kGrad2d; ++c) acc[c] = v[c];
                 }
             }
             __syncthreads();
