@@ -524,28 +524,10 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
     }
     if (end_all <= range.x) return;  // uniform
 
-    // Batches are walked back to front and staged one ahead in registers: the ids of batch b-1
-    // are loaded when batch b starts, its records and checkpoints after b's first bucket, and
-    // they reach LDS when b-1 starts, so global latency overlaps the replay.
-    uint32_t nx_p = 0, nx_g = 0;
-    float4 nx_r0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), nx_r1 = nx_r0, nx_r2 = nx_r0, nx_k0 = nx_r0;
-    float2 nx_k1 = make_float2(0.0f, 0.0f);
+    // Batches are walked back to front. Records reach LDS at the start of each batch; the
+    // checkpoints of batch b-1 are loaded into registers while batch b is processed.
     float nx_ck[kBatchBuckets];
-    auto load_ids = [&](uint32_t bstart) {
-        if (bstart + threadIdx.x < range.y) {
-            nx_p = values[bstart + threadIdx.x];
-            nx_g = sorted_g[bstart + threadIdx.x];
-        }
-    };
-    auto load_records = [&](uint32_t bstart) {
-        if (bstart + threadIdx.x < range.y) {
-            nx_r0 = rec[3 * (size_t)nx_g + 0];
-            nx_r1 = rec[3 * (size_t)nx_g + 1];
-            nx_r2 = rec[3 * (size_t)nx_g + 2];
-            nx_k0 = cov_coef[2 * (size_t)nx_g + 0];
-            const float4 k1 = cov_coef[2 * (size_t)nx_g + 1];
-            nx_k1 = make_float2(k1.x, k1.y);
-        }
+    auto load_checkpoints = [&](uint32_t bstart) {
 #pragma unroll
         for (int b = 0; b < kBatchBuckets; ++b) {
             const uint32_t j0 = bstart + (uint32_t)(b * kBucket);
@@ -554,24 +536,25 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
         }
     };
     const uint32_t first_batch = range.x + ((end_all - 1u - range.x) / kBlendThreads) * kBlendThreads;
-    load_ids(first_batch);
-    load_records(first_batch);
+    load_checkpoints(first_batch);
     for (int64_t bstart = first_batch; bstart >= (int64_t)range.x; bstart -= kBlendThreads) {
         const int count = (int)min((uint32_t)kBlendThreads, range.y - (uint32_t)bstart);
         if (threadIdx.x < count) {
-            s_pos[threadIdx.x] = nx_p;
-            s_r0[threadIdx.x] = nx_r0;
-            s_r1[threadIdx.x] = nx_r1;
-            s_r2[threadIdx.x] = nx_r2;
-            s_k0[threadIdx.x] = nx_k0;
-            s_k1[threadIdx.x] = nx_k1;
+            const uint32_t j = (uint32_t)bstart + threadIdx.x;
+            const uint32_t g = sorted_g[j];
+            s_pos[threadIdx.x] = values[j];
+            s_r0[threadIdx.x] = rec[3 * (size_t)g + 0];
+            s_r1[threadIdx.x] = rec[3 * (size_t)g + 1];
+            s_r2[threadIdx.x] = rec[3 * (size_t)g + 2];
+            s_k0[threadIdx.x] = cov_coef[2 * (size_t)g + 0];
+            const float4 k1 = cov_coef[2 * (size_t)g + 1];
+            s_k1[threadIdx.x] = make_float2(k1.x, k1.y);
         }
 #pragma unroll
         for (int b = 0; b < kBatchBuckets; ++b) s_ck[b][threadIdx.x] = nx_ck[b];
         __syncthreads();
         const bool has_next = bstart - kBlendThreads >= (int64_t)range.x;  // uniform
-        const uint32_t next = (uint32_t)(bstart - kBlendThreads);
-        if (has_next) load_ids(next);
+        if (has_next) load_checkpoints((uint32_t)(bstart - kBlendThreads));
         const int sb_first = (count - 1) / kBucket;
         for (int sb = sb_first; sb >= 0; --sb) {
             const uint32_t j0 = (uint32_t)bstart + (uint32_t)(sb * kBucket);
@@ -681,7 +664,6 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
             }
             __syncthreads();
             }
-            if (has_next && sb == sb_first) load_records(next);
         }
     }
 }
