@@ -514,8 +514,9 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     layout.tile_shift = layout.depth_shift + depth_bits;
     ctx->layout = layout;
     if (train) {
-        // bucket checkpoints: at most I/32 + tiles + 1 slots of 256 floats
-        GSX_TRY(ctx->ckpt.reserve(((size_t)count / 32 + (size_t)tiles + 2) * 256 * sizeof(float), "checkpoints"));
+        // bucket checkpoints: at most I/kBucket + tiles + 1 slots of 256 floats
+        GSX_TRY(ctx->ckpt.reserve(((size_t)count / kBucket + (size_t)tiles + 2) * 256 * sizeof(float),
+                                  "checkpoints"));
     }
     if (n > 0) {
         hipLaunchKernelGGL(emit_keys_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, n, ctx->rec.as<float4>(),

@@ -357,10 +357,10 @@ __device__ inline bool in_box(int px, int py, uint32_t bx, uint32_t by) {
 // Transmittance checkpoints: the backward needs every contribution's exact T_before (the CPU
 // records it, render.c:1501-1506; recomputing it by division perturbs the last bit, which the
 // near-singular covariance gradient of near-plane Gaussians amplifies without bound). A TRAIN
-// forward therefore stores each pixel's T at the start of every 32-entry bucket of its tile's
-// list. Bucket k of a tile whose list starts at position x lives in slot x/32 + tile + k, which
-// is collision-free and needs at most I/32 + tiles + 1 slots of 256 floats.
-constexpr int kBucket = 32;
+// forward therefore stores each pixel's T at the start of every 16-entry bucket of its tile's
+// list. Bucket k of a tile whose list starts at position x lives in slot x/16 + tile + k, which
+// is collision-free and needs at most I/16 + tiles + 1 slots of 256 floats.
+constexpr int kBucket = 16;
 
 __device__ inline size_t checkpoint_slot(uint32_t range_start, int tile, uint32_t position) {
     return (size_t)(range_start / kBucket) + (size_t)tile + (size_t)((position - range_start) / kBucket);
@@ -465,19 +465,22 @@ constexpr int kGrad2d = 9;
 constexpr int kWavesPerTile = kBlendThreads / kWave;
 constexpr int kRowsPerTile = kTile;  // 16 pixel rows = 16 DPP rows of 16 lanes
 
-constexpr int kBatchBuckets = kBlendThreads / kBucket;  // 8 buckets per 256-entry batch
+// The backward stages 128 entries per batch (8 buckets): with 16-entry buckets the kernel fits
+// 128 VGPRs and 40 KB of LDS, i.e. 4 waves per SIMD.
+constexpr int kBackBatch = 128;
+constexpr int kBatchBuckets = kBackBatch / kBucket;
 
 __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
     const uint2* __restrict__ ranges, const uint32_t* __restrict__ values, const uint32_t* __restrict__ sorted_g,
     const float4* __restrict__ rec, const float4* __restrict__ cov_coef, const float* __restrict__ ckpt,
     CameraParams cam, const float* __restrict__ grad_rgb, const float* __restrict__ final_t,
     const uint32_t* __restrict__ last_contrib, float* __restrict__ instance_grad) {
-    __shared__ float4 s_r0[kBlendThreads];
-    __shared__ float4 s_r1[kBlendThreads];
-    __shared__ float4 s_r2[kBlendThreads];
-    __shared__ float4 s_k0[kBlendThreads];
-    __shared__ float2 s_k1[kBlendThreads];
-    __shared__ uint32_t s_pos[kBlendThreads];
+    __shared__ float4 s_r0[kBackBatch];
+    __shared__ float4 s_r1[kBackBatch];
+    __shared__ float4 s_r2[kBackBatch];
+    __shared__ float4 s_k0[kBackBatch];
+    __shared__ float2 s_k1[kBackBatch];
+    __shared__ uint32_t s_pos[kBackBatch];
     __shared__ float s_ck[kBatchBuckets][kBlendThreads];
     __shared__ float s_acc[kRowsPerTile][kBucket][kGrad2d];
     __shared__ uint64_t s_exp2[GSX_EXP2_TABLE_SIZE];
@@ -524,21 +527,11 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
     }
     if (end_all <= range.x) return;  // uniform
 
-    // Batches are walked back to front. Records reach LDS at the start of each batch; the
-    // checkpoints of batch b-1 are loaded into registers while batch b is processed.
-    float nx_ck[kBatchBuckets];
-    auto load_checkpoints = [&](uint32_t bstart) {
-#pragma unroll
-        for (int b = 0; b < kBatchBuckets; ++b) {
-            const uint32_t j0 = bstart + (uint32_t)(b * kBucket);
-            nx_ck[b] = (inside && j0 < last) ? ckpt[checkpoint_slot(range.x, tile, j0) * kBlendThreads + threadIdx.x]
-                                             : 0.0f;
-        }
-    };
-    const uint32_t first_batch = range.x + ((end_all - 1u - range.x) / kBlendThreads) * kBlendThreads;
-    load_checkpoints(first_batch);
-    for (int64_t bstart = first_batch; bstart >= (int64_t)range.x; bstart -= kBlendThreads) {
-        const int count = (int)min((uint32_t)kBlendThreads, range.y - (uint32_t)bstart);
+    // Batches of 128 entries are walked back to front; records and the batch's bucket
+    // checkpoints reach LDS at the start of each batch.
+    const uint32_t first_batch = range.x + ((end_all - 1u - range.x) / kBackBatch) * kBackBatch;
+    for (int64_t bstart = first_batch; bstart >= (int64_t)range.x; bstart -= kBackBatch) {
+        const int count = (int)min((uint32_t)kBackBatch, range.y - (uint32_t)bstart);
         if (threadIdx.x < count) {
             const uint32_t j = (uint32_t)bstart + threadIdx.x;
             const uint32_t g = sorted_g[j];
@@ -551,10 +544,13 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
             s_k1[threadIdx.x] = make_float2(k1.x, k1.y);
         }
 #pragma unroll
-        for (int b = 0; b < kBatchBuckets; ++b) s_ck[b][threadIdx.x] = nx_ck[b];
+        for (int b = 0; b < kBatchBuckets; ++b) {
+            const uint32_t j0 = (uint32_t)bstart + (uint32_t)(b * kBucket);
+            s_ck[b][threadIdx.x] = (inside && j0 < last)
+                                       ? ckpt[checkpoint_slot(range.x, tile, j0) * kBlendThreads + threadIdx.x]
+                                       : 0.0f;
+        }
         __syncthreads();
-        const bool has_next = bstart - kBlendThreads >= (int64_t)range.x;  // uniform
-        if (has_next) load_checkpoints((uint32_t)(bstart - kBlendThreads));
         const int sb_first = (count - 1) / kBucket;
         for (int sb = sb_first; sb >= 0; --sb) {
             const uint32_t j0 = (uint32_t)bstart + (uint32_t)(sb * kBucket);
