@@ -70,8 +70,17 @@ __device__ inline uint32_t box_tiles(float4 r2) {
     return ((bx >> 16) / kTile - (bx & 0xffffu) / kTile + 1) * ((by >> 16) / kTile - (by & 0xffffu) / kTile + 1);
 }
 
+// k / d for k < 2^24 and 1 <= d from a float reciprocal, corrected to the exact quotient.
+__device__ inline uint32_t div_small(uint32_t k, uint32_t d, float rd) {
+    uint32_t q = (uint32_t)((float)k * rd);
+    if (q * d > k) q -= 1;
+    if ((q + 1) * d <= k) q += 1;
+    return q;
+}
+
 struct WaveBoxes {
-    float mx[kWave], my[kWave], a[kWave], b[kWave], c[kWave], qcut[kWave];
+    gsx_tile_conic conic[kWave];
+    float rwx[kWave];  // 1 / wx, for the row of a flattened tile index
     int32_t x0[kWave], x1[kWave], y0[kWave], y1[kWave];
     uint32_t tx0[kWave], ty0[kWave], wx[kWave], excl[kWave], kept[kWave], out[kWave];
     uint32_t depth[kWave];
@@ -86,12 +95,8 @@ __device__ inline uint32_t stage_box(WaveBoxes& w, bool valid, float4 r0, float4
     if (valid) {
         const uint32_t bx = __float_as_uint(r2.y), by = __float_as_uint(r2.z);
         const int x0 = (int)(bx & 0xffffu), x1 = (int)(bx >> 16), y0 = (int)(by & 0xffffu), y1 = (int)(by >> 16);
-        w.mx[lane] = r0.x;
-        w.my[lane] = r0.y;
-        w.a[lane] = r0.z;
-        w.b[lane] = r0.w * 0.5f;  // the record holds 2 * inv_b (exact)
-        w.c[lane] = r1.x;
-        w.qcut[lane] = gsx_tile_qcut(r1.y);
+        // the record holds 2 * inv_b (halving is exact)
+        w.conic[lane] = gsx_tile_conic_make(r0.x, r0.y, r0.z, r0.w * 0.5f, r1.x, r1.y);
         w.x0[lane] = x0;
         w.x1[lane] = x1;
         w.y0[lane] = y0;
@@ -99,6 +104,7 @@ __device__ inline uint32_t stage_box(WaveBoxes& w, bool valid, float4 r0, float4
         w.tx0[lane] = (uint32_t)x0 / kTile;
         w.ty0[lane] = (uint32_t)y0 / kTile;
         w.wx[lane] = (uint32_t)x1 / kTile - (uint32_t)x0 / kTile + 1;
+        w.rwx[lane] = 1.0f / (float)w.wx[lane];
         w.depth[lane] = __float_as_uint(r2.w);
         total = w.wx[lane] * ((uint32_t)y1 / kTile - (uint32_t)y0 / kTile + 1);
     }
@@ -138,13 +144,14 @@ __device__ inline void walk_wave_tiles(WaveBoxes& w, uint32_t wave_total, int32_
         if (active) {
             const uint32_t k = p - w.excl[owner];
             const uint32_t wx = w.wx[owner];
-            const uint32_t ty = w.ty0[owner] + k / wx;
-            const uint32_t tx = w.tx0[owner] + k % wx;
+            const uint32_t row = div_small(k, wx, w.rwx[owner]);
+            const uint32_t ty = w.ty0[owner] + row;
+            const uint32_t tx = w.tx0[owner] + (k - row * wx);
             tile = ty * (uint32_t)tiles_x + tx;
             const int px0 = max((int)tx * kTile, w.x0[owner]), px1 = min((int)tx * kTile + kTile - 1, w.x1[owner]);
             const int py0 = max((int)ty * kTile, w.y0[owner]), py1 = min((int)ty * kTile + kTile - 1, w.y1[owner]);
-            keep = gsx_tile_may_contribute(w.mx[owner], w.my[owner], w.a[owner], w.b[owner], w.c[owner],
-                                           w.qcut[owner], px0, px1, py0, py1) != 0;
+            const gsx_tile_conic con = w.conic[owner];
+            keep = gsx_tile_conic_test(&con, px0, px1, py0, py1) != 0;
         }
         const uint64_t mask = __ballot(keep);
         // first lane of this step holding the owner's pairs
@@ -267,7 +274,8 @@ __global__ __launch_bounds__(256) void big_tiles_kernel(const uint32_t* __restri
         const uint32_t tx0 = (uint32_t)x0 / kTile, ty0 = (uint32_t)y0 / kTile;
         const uint32_t wx = (uint32_t)x1 / kTile - tx0 + 1;
         const uint32_t total = wx * ((uint32_t)y1 / kTile - ty0 + 1);
-        const float qcut = gsx_tile_qcut(r1.y);
+        const gsx_tile_conic con = gsx_tile_conic_make(r0.x, r0.y, r0.z, r0.w * 0.5f, r1.x, r1.y);
+        const float rwx = 1.0f / (float)wx;
         const uint32_t depth = __float_as_uint(r2.w);
         const uint32_t o = kEmit ? offsets[g] : 0u;
         uint32_t running = 0;
@@ -276,11 +284,12 @@ __global__ __launch_bounds__(256) void big_tiles_kernel(const uint32_t* __restri
             bool keep = false;
             uint32_t tile = 0;
             if (k < total) {
-                const uint32_t ty = ty0 + k / wx, tx = tx0 + k % wx;
+                const uint32_t row = div_small(k, wx, rwx);
+                const uint32_t ty = ty0 + row, tx = tx0 + (k - row * wx);
                 tile = ty * (uint32_t)tiles_x + tx;
                 const int px0 = max((int)tx * kTile, x0), px1 = min((int)tx * kTile + kTile - 1, x1);
                 const int py0 = max((int)ty * kTile, y0), py1 = min((int)ty * kTile + kTile - 1, y1);
-                keep = gsx_tile_may_contribute(r0.x, r0.y, r0.z, r0.w * 0.5f, r1.x, qcut, px0, px1, py0, py1) != 0;
+                keep = gsx_tile_conic_test(&con, px0, px1, py0, py1) != 0;
             }
             const uint64_t mask = __ballot(keep);
             if (lane == 0) s_wave[wave] = (uint32_t)__popcll(mask);

@@ -79,12 +79,32 @@ GSX_HD float gsx_cull_edge_min(float A, float B, float C, float rC, float ue, fl
     return m;
 }
 
-/* Nonzero when some pixel centre of the inclusive pixel rectangle [px0, px1] x [py0, py1] (the
- * tile clipped to the Gaussian's box) may receive a contribution from the Gaussian with 2D mean
- * (mx, my), conic (A, B, C) = (inv_a, inv_b, inv_c) and q_cut from gsx_tile_qcut. */
-GSX_HD int gsx_tile_may_contribute(float mx, float my, float A, float B, float C, float qcut, int px0, int px1,
-    int py0, int py1)
+/* Per-Gaussian constants of the test: conic (A, B, C) = (inv_a, inv_b, inv_c), their
+ * reciprocals for the edge minima, and q_cut. */
+typedef struct gsx_tile_conic {
+    float mx, my, A, B, C, rA, rC, qcut;
+} gsx_tile_conic;
+
+GSX_HD gsx_tile_conic gsx_tile_conic_make(float mx, float my, float inv_a, float inv_b, float inv_c, float opacity)
 {
+    gsx_tile_conic k;
+
+    k.mx = mx;
+    k.my = my;
+    k.A = inv_a;
+    k.B = inv_b;
+    k.C = inv_c;
+    k.rA = 1.0f / inv_a;
+    k.rC = 1.0f / inv_c;
+    k.qcut = gsx_tile_qcut(opacity);
+    return k;
+}
+
+/* Nonzero when some pixel centre of the inclusive pixel rectangle [px0, px1] x [py0, py1] (the
+ * tile clipped to the Gaussian's box) may receive a contribution from the Gaussian. */
+GSX_HD int gsx_tile_conic_test(const gsx_tile_conic *k, int px0, int px1, int py0, int py1)
+{
+    const float mx = k->mx, my = k->my, A = k->A, B = k->B, C = k->C, rA = k->rA, rC = k->rC, qcut = k->qcut;
     const float dx0 = ((float)px0 + 0.5f) - mx;
     const float dx1 = ((float)px1 + 0.5f) - mx;
     const float dy0 = ((float)py0 + 0.5f) - my;
@@ -93,8 +113,6 @@ GSX_HD int gsx_tile_may_contribute(float mx, float my, float A, float B, float C
     const float Y = gsx_cull_absf(dy0) > gsx_cull_absf(dy1) ? gsx_cull_absf(dy0) : gsx_cull_absf(dy1);
     const float scale = gsx_cull_absf(A) * X * X + 2.0f * gsx_cull_absf(B) * X * Y + gsx_cull_absf(C) * Y * Y;
     const float margin = 1e-4f * scale + 1e-3f;
-    const float rA = 1.0f / A;
-    const float rC = 1.0f / C;
     float qmin;
 
     if(dx0 <= 0.0f && dx1 >= 0.0f && dy0 <= 0.0f && dy1 >= 0.0f) {
@@ -105,6 +123,14 @@ GSX_HD int gsx_tile_may_contribute(float mx, float my, float A, float B, float C
     qmin = gsx_cull_minf(qmin, gsx_cull_edge_min(C, B, A, rA, dy0, dx0, dx1));
     qmin = gsx_cull_minf(qmin, gsx_cull_edge_min(C, B, A, rA, dy1, dx0, dx1));
     return !(qmin - margin > qcut); /* keeps the instance for NaN input too */
+}
+
+GSX_HD int gsx_tile_may_contribute(float mx, float my, float inv_a, float inv_b, float inv_c, float opacity, int px0,
+    int px1, int py0, int py1)
+{
+    const gsx_tile_conic k = gsx_tile_conic_make(mx, my, inv_a, inv_b, inv_c, opacity);
+
+    return gsx_tile_conic_test(&k, px0, px1, py0, py1);
 }
 
 #endif /* GSX_AMD_TILE_CULL_H */

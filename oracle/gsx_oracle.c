@@ -481,7 +481,7 @@ static int tile_kept(const vis *v, int32_t tx, int32_t ty, int32_t tile_size)
     if(py0 < v->bb[2]) py0 = v->bb[2];
     if(py1 > v->bb[3]) py1 = v->bb[3];
     return gsx_tile_may_contribute(v->rec[ORACLE_REC_MEAN2D_X], v->rec[ORACLE_REC_MEAN2D_Y], inv_a, inv_b, inv_c,
-        gsx_tile_qcut(v->rec[ORACLE_REC_OPACITY]), px0, px1, py0, py1);
+        v->rec[ORACLE_REC_OPACITY], px0, px1, py0, py1);
 }
 
 /* Tile-key restatement (no CPU counterpart): visible Gaussians in Gaussian-index order, each
@@ -550,7 +550,7 @@ float oracle_tile_logf(float x) { return gsx_cull_logf(x); }
 int oracle_tile_may_contribute(float mx, float my, float inv_a, float inv_b, float inv_c, float opacity, int px0,
     int px1, int py0, int py1)
 {
-    return gsx_tile_may_contribute(mx, my, inv_a, inv_b, inv_c, gsx_tile_qcut(opacity), px0, px1, py0, py1);
+    return gsx_tile_may_contribute(mx, my, inv_a, inv_b, inv_c, opacity, px0, px1, py0, py1);
 }
 
 /* [start, end) of every tile in the sorted key array; empty tiles get (0, 0). */
