@@ -7,8 +7,8 @@
 //   - the SSIM gradient convolves dm/dmu1, dm/dsigma1^2, dm/dsigma12 (0 at the boundary) and
 //     adds -(conv_mu + 2 p conv_s1 + t conv_s12) * grad_scale.
 // The CPU evaluates SSIM as a direct 2D sum in float64; here the window is applied as two
-// separable 11-tap passes in float32 through LDS (16x16 output tile, 26x26 halo), which is
-// within 1e-5 of the float64 value on [0,1] images.
+// separable 11-tap passes of fused multiply-adds in float32 through LDS (32x16 output tile,
+// 42x26 halo), which is within 1e-5 of the float64 value on [0,1] images.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -23,8 +23,6 @@ __device__ __constant__ const float kSsimW[11] = {
     0.21300552785396576f,  0.26601171493530273f,   0.21300552785396576f,  0.10936068743467331f,
     0.036000773310661316f, 0.0075987582094967365f, 0.001028380123898387f};
 
-constexpr int kSsimTile = 16;
-constexpr int kSsimHalo = kSsimTile + 10;  // 26
 
 __global__ __launch_bounds__(256) void l1_forward_kernel(float* __restrict__ map, const float* __restrict__ pred,
                                                          const float* __restrict__ target, int64_t n, float scale) {
@@ -61,99 +59,112 @@ __global__ __launch_bounds__(256) void mse_backward_kernel(float* __restrict__ g
     }
 }
 
-// One 16x16 output tile of one image plane per workgroup (256 threads).
-// Forward: 5 moments (mu_p, mu_t, E[p^2], E[t^2], E[pt]) by a horizontal pass over 26 halo rows
-// then a vertical pass; writes the loss map (optionally fused with a preceding L1 term) and the
-// three dm maps [3][planes][H][W] consumed by the backward.
+// One 32x16 output tile of one image plane per workgroup (256 threads). The window sums use
+// explicit fused multiply-adds: the SSIM bar is a tolerance (the CPU sums in float64), unlike
+// the L1 term fused into the same pass, which keeps the L1 kernel's exact operations.
+constexpr int kSsimTW = 32, kSsimTH = 16;
+constexpr int kSsimHW = kSsimTW + 10, kSsimHH = kSsimTH + 10;  // 42 x 26 halo
+
+// Forward: p and t of the halo in LDS; a horizontal 11-tap pass where each thread forms the
+// five moments (p, t, p^2, t^2, p t) of two adjacent output columns from 12 loads per plane;
+// then a vertical pass where each thread produces two adjacent output rows from 12 loads per
+// moment plane. Writes the loss map (optionally after a fused L1 term) and the three dm maps
+// [3][planes][H][W] that the backward convolves.
 __global__ __launch_bounds__(256) void ssim_forward_kernel(float* __restrict__ map, const float* __restrict__ pred,
                                                            const float* __restrict__ target, int32_t height,
                                                            int32_t width, int64_t planes, float scale, float l1_scale,
                                                            int fuse_l1, float* __restrict__ dm) {
-    __shared__ float s_p[kSsimHalo][kSsimHalo + 1];
-    __shared__ float s_t[kSsimHalo][kSsimHalo + 1];
-    __shared__ float s_h[5][kSsimHalo][kSsimTile + 1];
-    const int tiles_x = (width + kSsimTile - 1) / kSsimTile;
-    const int tile = blockIdx.x;
+    __shared__ float s_in[2][kSsimHH][kSsimHW + 1];
+    __shared__ float s_h[5][kSsimHH][kSsimTW + 1];
+    const int tiles_x = (width + kSsimTW - 1) / kSsimTW;
+    const int ox = (int)(blockIdx.x % tiles_x) * kSsimTW;
+    const int oy = (int)(blockIdx.x / tiles_x) * kSsimTH;
     const int64_t plane = blockIdx.y;
-    const int ox = (tile % tiles_x) * kSsimTile;
-    const int oy = (tile / tiles_x) * kSsimTile;
-    const float* pp = pred + plane * (int64_t)height * width;
-    const float* tp = target + plane * (int64_t)height * width;
-    for (int i = threadIdx.x; i < kSsimHalo * kSsimHalo; i += 256) {
-        const int hy = i / kSsimHalo, hx = i % kSsimHalo;
+    const int64_t pbase = plane * (int64_t)height * width;
+    for (int i = threadIdx.x; i < kSsimHH * kSsimHW; i += 256) {
+        const int hy = i / kSsimHW, hx = i % kSsimHW;
         const int y = oy + hy - 5, x = ox + hx - 5;
         float pv = 0.0f, tv = 0.0f;
         if (y >= 0 && y < height && x >= 0 && x < width) {
-            pv = pp[(int64_t)y * width + x];
-            tv = tp[(int64_t)y * width + x];
+            pv = pred[pbase + (int64_t)y * width + x];
+            tv = target[pbase + (int64_t)y * width + x];
         }
-        s_p[hy][hx] = pv;
-        s_t[hy][hx] = tv;
+        s_in[0][hy][hx] = pv;
+        s_in[1][hy][hx] = tv;
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < kSsimHalo * kSsimTile; i += 256) {
-        const int hy = i / kSsimTile, cx = i % kSsimTile;
-        float a = 0.0f, b = 0.0f, c = 0.0f, d = 0.0f, e = 0.0f;
+    for (int i = threadIdx.x; i < kSsimHH * (kSsimTW / 2); i += 256) {
+        const int hy = i / (kSsimTW / 2), cx = 2 * (i % (kSsimTW / 2));
+        float a0[5] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f}, a1[5] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int k = 0; k < 11; ++k) {
-            const float w = kSsimW[k];
-            const float pv = s_p[hy][cx + k];
-            const float tv = s_t[hy][cx + k];
-            a += w * pv;
-            b += w * tv;
-            c += w * (pv * pv);
-            d += w * (tv * tv);
-            e += w * (pv * tv);
+        for (int k = 0; k < 12; ++k) {
+            const float pv = s_in[0][hy][cx + k], tv = s_in[1][hy][cx + k];
+            const float m[5] = {pv, tv, pv * pv, tv * tv, pv * tv};
+            if (k < 11) {
+#pragma unroll
+                for (int c = 0; c < 5; ++c) a0[c] = __builtin_fmaf(kSsimW[k], m[c], a0[c]);
+            }
+            if (k > 0) {
+#pragma unroll
+                for (int c = 0; c < 5; ++c) a1[c] = __builtin_fmaf(kSsimW[k - 1], m[c], a1[c]);
+            }
         }
-        s_h[0][hy][cx] = a;
-        s_h[1][hy][cx] = b;
-        s_h[2][hy][cx] = c;
-        s_h[3][hy][cx] = d;
-        s_h[4][hy][cx] = e;
+#pragma unroll
+        for (int c = 0; c < 5; ++c) {
+            s_h[c][hy][cx] = a0[c];
+            s_h[c][hy][cx + 1] = a1[c];
+        }
     }
     __syncthreads();
-    const int lx = threadIdx.x % kSsimTile, ly = threadIdx.x / kSsimTile;
-    const int x = ox + lx, y = oy + ly;
-    if (x >= width || y >= height) return;
-    float mu1 = 0.0f, mu2 = 0.0f, ex2 = 0.0f, ey2 = 0.0f, exy = 0.0f;
+    const int lx = threadIdx.x % kSsimTW;
+    const int ly0 = 2 * (threadIdx.x / kSsimTW);
+    float mom[2][5] = {{0.0f, 0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f, 0.0f}};
 #pragma unroll
-    for (int k = 0; k < 11; ++k) {
-        const float w = kSsimW[k];
-        mu1 += w * s_h[0][ly + k][lx];
-        mu2 += w * s_h[1][ly + k][lx];
-        ex2 += w * s_h[2][ly + k][lx];
-        ey2 += w * s_h[3][ly + k][lx];
-        exy += w * s_h[4][ly + k][lx];
-    }
-    const float c1 = 0.01f * 0.01f, c2 = 0.03f * 0.03f;
-    const float m1s = mu1 * mu1, m2s = mu2 * mu2;
-    const float s1 = ex2 - m1s, s2 = ey2 - m2s, s12 = exy - mu1 * mu2;
-    const float a = m1s + m2s + c1;
-    const float b = s1 + s2 + c2;
-    const float ct = 2.0f * mu1 * mu2 + c1;
-    const float dt = 2.0f * s12 + c2;
-    const float ab = a * b;
-    const float ssim = ab == 0.0f ? 1.0f : (ct * dt) / ab;
-    const bool boundary = y < 5 || y >= height - 5 || x < 5 || x >= width - 5;
-    const int64_t idx = plane * (int64_t)height * width + (int64_t)y * width + x;
-    if (map != nullptr) {
-        float m = map[idx];
-        if (fuse_l1) m += l1_scale * fabsf(s_p[ly + 5][lx + 5] - s_t[ly + 5][lx + 5]);
-        map[idx] = boundary ? 0.0f : m + (1.0f - ssim) * scale;
-    }
-    if (dm != nullptr) {
-        const int64_t total = planes * (int64_t)height * width;
-        float g_mu = 0.0f, g_s1 = 0.0f, g_s12 = 0.0f;
-        if (!(boundary || a == 0.0f || b == 0.0f)) {
-            const float aab = a * ab, abb = ab * b;
-            g_mu = (2.0f * mu2 * dt) / ab - (2.0f * mu2 * ct) / ab - (2.0f * mu1 * ct * dt) / aab +
-                   (2.0f * mu1 * ct * dt) / abb;
-            g_s1 = -(ct * dt) / abb;
-            g_s12 = (2.0f * ct) / ab;
+    for (int k = 0; k < 12; ++k) {
+#pragma unroll
+        for (int c = 0; c < 5; ++c) {
+            const float v = s_h[c][ly0 + k][lx];
+            if (k < 11) mom[0][c] = __builtin_fmaf(kSsimW[k], v, mom[0][c]);
+            if (k > 0) mom[1][c] = __builtin_fmaf(kSsimW[k - 1], v, mom[1][c]);
         }
-        dm[idx] = g_mu;
-        dm[total + idx] = g_s1;
-        dm[2 * total + idx] = g_s12;
+    }
+    const int64_t total = planes * (int64_t)height * width;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const int ly = ly0 + r;
+        const int x = ox + lx, y = oy + ly;
+        if (x >= width || y >= height) continue;
+        const float mu1 = mom[r][0], mu2 = mom[r][1], ex2 = mom[r][2], ey2 = mom[r][3], exy = mom[r][4];
+        const float c1 = 0.01f * 0.01f, c2 = 0.03f * 0.03f;
+        const float m1s = mu1 * mu1, m2s = mu2 * mu2;
+        const float s1 = ex2 - m1s, s2 = ey2 - m2s, s12 = exy - mu1 * mu2;
+        const float a = m1s + m2s + c1;
+        const float b = s1 + s2 + c2;
+        const float ct = 2.0f * mu1 * mu2 + c1;
+        const float dt = 2.0f * s12 + c2;
+        const float ab = a * b;
+        const float ssim = ab == 0.0f ? 1.0f : (ct * dt) / ab;
+        const bool boundary = y < 5 || y >= height - 5 || x < 5 || x >= width - 5;
+        const int64_t idx = pbase + (int64_t)y * width + x;
+        if (map != nullptr) {
+            float m = map[idx];
+            // exactly the L1 kernel's operations (loss.c:354-371)
+            if (fuse_l1) m += l1_scale * fabsf(s_in[0][ly + 5][lx + 5] - s_in[1][ly + 5][lx + 5]);
+            map[idx] = boundary ? 0.0f : m + (1.0f - ssim) * scale;
+        }
+        if (dm != nullptr) {
+            float g_mu = 0.0f, g_s1 = 0.0f, g_s12 = 0.0f;
+            if (!(boundary || a == 0.0f || b == 0.0f)) {
+                const float aab = a * ab, abb = ab * b;
+                g_mu = (2.0f * mu2 * dt) / ab - (2.0f * mu2 * ct) / ab - (2.0f * mu1 * ct * dt) / aab +
+                       (2.0f * mu1 * ct * dt) / abb;
+                g_s1 = -(ct * dt) / abb;
+                g_s12 = (2.0f * ct) / ab;
+            }
+            dm[idx] = g_mu;
+            dm[total + idx] = g_s1;
+            dm[2 * total + idx] = g_s12;
+        }
     }
 }
 
@@ -162,17 +173,16 @@ __global__ __launch_bounds__(256) void ssim_backward_kernel(float* __restrict__ 
                                                             int32_t width, int64_t planes, float grad_scale,
                                                             float l1_grad_scale, int fuse_l1,
                                                             const float* __restrict__ dm) {
-    __shared__ float s_m[3][kSsimHalo][kSsimHalo + 1];
-    __shared__ float s_h[3][kSsimHalo][kSsimTile + 1];
-    const int tiles_x = (width + kSsimTile - 1) / kSsimTile;
-    const int tile = blockIdx.x;
+    __shared__ float s_m[3][kSsimHH][kSsimHW + 1];
+    __shared__ float s_h[3][kSsimHH][kSsimTW + 1];
+    const int tiles_x = (width + kSsimTW - 1) / kSsimTW;
+    const int ox = (int)(blockIdx.x % tiles_x) * kSsimTW;
+    const int oy = (int)(blockIdx.x / tiles_x) * kSsimTH;
     const int64_t plane = blockIdx.y;
-    const int ox = (tile % tiles_x) * kSsimTile;
-    const int oy = (tile / tiles_x) * kSsimTile;
     const int64_t total = planes * (int64_t)height * width;
     const int64_t pbase = plane * (int64_t)height * width;
-    for (int i = threadIdx.x; i < kSsimHalo * kSsimHalo; i += 256) {
-        const int hy = i / kSsimHalo, hx = i % kSsimHalo;
+    for (int i = threadIdx.x; i < kSsimHH * kSsimHW; i += 256) {
+        const int hy = i / kSsimHW, hx = i % kSsimHW;
         const int y = oy + hy - 5, x = ox + hx - 5;
         float v0 = 0.0f, v1 = 0.0f, v2 = 0.0f;
         if (y >= 0 && y < height && x >= 0 && x < width) {
@@ -186,41 +196,51 @@ __global__ __launch_bounds__(256) void ssim_backward_kernel(float* __restrict__ 
         s_m[2][hy][hx] = v2;
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < kSsimHalo * kSsimTile; i += 256) {
-        const int hy = i / kSsimTile, cx = i % kSsimTile;
-        float a = 0.0f, b = 0.0f, c = 0.0f;
+    for (int i = threadIdx.x; i < kSsimHH * (kSsimTW / 2); i += 256) {
+        const int hy = i / (kSsimTW / 2), cx = 2 * (i % (kSsimTW / 2));
+        float a0[3] = {0.0f, 0.0f, 0.0f}, a1[3] = {0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int k = 0; k < 11; ++k) {
-            const float w = kSsimW[k];
-            a += w * s_m[0][hy][cx + k];
-            b += w * s_m[1][hy][cx + k];
-            c += w * s_m[2][hy][cx + k];
+        for (int k = 0; k < 12; ++k) {
+#pragma unroll
+            for (int c = 0; c < 3; ++c) {
+                const float v = s_m[c][hy][cx + k];
+                if (k < 11) a0[c] = __builtin_fmaf(kSsimW[k], v, a0[c]);
+                if (k > 0) a1[c] = __builtin_fmaf(kSsimW[k - 1], v, a1[c]);
+            }
         }
-        s_h[0][hy][cx] = a;
-        s_h[1][hy][cx] = b;
-        s_h[2][hy][cx] = c;
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+            s_h[c][hy][cx] = a0[c];
+            s_h[c][hy][cx + 1] = a1[c];
+        }
     }
     __syncthreads();
-    const int lx = threadIdx.x % kSsimTile, ly = threadIdx.x / kSsimTile;
-    const int x = ox + lx, y = oy + ly;
-    if (x >= width || y >= height) return;
-    float cm = 0.0f, c1 = 0.0f, c12 = 0.0f;
+    const int lx = threadIdx.x % kSsimTW;
+    const int ly0 = 2 * (threadIdx.x / kSsimTW);
+    float cv[2][3] = {{0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f}};
 #pragma unroll
-    for (int k = 0; k < 11; ++k) {
-        const float w = kSsimW[k];
-        cm += w * s_h[0][ly + k][lx];
-        c1 += w * s_h[1][ly + k][lx];
-        c12 += w * s_h[2][ly + k][lx];
+    for (int k = 0; k < 12; ++k) {
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+            const float v = s_h[c][ly0 + k][lx];
+            if (k < 11) cv[0][c] = __builtin_fmaf(kSsimW[k], v, cv[0][c]);
+            if (k > 0) cv[1][c] = __builtin_fmaf(kSsimW[k - 1], v, cv[1][c]);
+        }
     }
-    const int64_t idx = pbase + (int64_t)y * width + x;
-    const float pv = pred[idx], tv = target[idx];
-    float g = grad[idx];
-    if (fuse_l1) {
-        const float d = pv - tv;
-        const float s = d > 0.0f ? 1.0f : (d < 0.0f ? -1.0f : 0.0f);
-        g += s * l1_grad_scale;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const int x = ox + lx, y = oy + ly0 + r;
+        if (x >= width || y >= height) continue;
+        const int64_t idx = pbase + (int64_t)y * width + x;
+        const float pv = pred[idx], tv = target[idx];
+        float g = grad[idx];
+        if (fuse_l1) {  // exactly the L1 kernel's operations
+            const float d = pv - tv;
+            const float s = d > 0.0f ? 1.0f : (d < 0.0f ? -1.0f : 0.0f);
+            g += s * l1_grad_scale;
+        }
+        grad[idx] = g + (-(cv[r][0] + 2.0f * pv * cv[r][1] + tv * cv[r][2]) * grad_scale);
     }
-    grad[idx] = g + (-(cm + 2.0f * pv * c1 + tv * c12) * grad_scale);
 }
 
 }  // namespace gsx_amd
@@ -279,7 +299,7 @@ gsx_hip_status gsx_hip_loss_ssim_chw_f32_forward_kernel_launch(float* loss_map, 
     const int64_t planes = outer_count * channels;
     if (planes <= 0 || height <= 0 || width <= 0) return GSX_HIP_ERROR_INVALID_ARGUMENT;
     if (planes > 65535) return GSX_HIP_ERROR_OUT_OF_RANGE;
-    const int tiles = ((width + kSsimTile - 1) / kSsimTile) * ((height + kSsimTile - 1) / kSsimTile);
+    const int tiles = ((width + kSsimTW - 1) / kSsimTW) * ((height + kSsimTH - 1) / kSsimTH);
     hipLaunchKernelGGL(ssim_forward_kernel, dim3((unsigned)tiles, (unsigned)planes), dim3(256), 0, stream, loss_map,
                        prediction, target, height, width, planes, scale, l1_scale, fuse_l1, ssim_workspace);
     return (gsx_hip_status)hipGetLastError();
@@ -293,7 +313,7 @@ gsx_hip_status gsx_hip_loss_ssim_chw_f32_backward_kernel_launch(float* grad_pred
     const int64_t planes = outer_count * channels;
     if (planes <= 0 || height <= 0 || width <= 0) return GSX_HIP_ERROR_INVALID_ARGUMENT;
     if (planes > 65535) return GSX_HIP_ERROR_OUT_OF_RANGE;
-    const int tiles = ((width + kSsimTile - 1) / kSsimTile) * ((height + kSsimTile - 1) / kSsimTile);
+    const int tiles = ((width + kSsimTW - 1) / kSsimTW) * ((height + kSsimTH - 1) / kSsimTH);
     hipLaunchKernelGGL(ssim_backward_kernel, dim3((unsigned)tiles, (unsigned)planes), dim3(256), 0, stream,
                        grad_prediction, prediction, target, height, width, planes, grad_scale, l1_grad_scale, fuse_l1,
                        ssim_workspace);
