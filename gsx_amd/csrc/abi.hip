@@ -551,15 +551,15 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
                        ctx->ranges.as<uint32_t>(), (int64_t)tiles * 2, 0u);
     if (count > 0) {
         hipLaunchKernelGGL(tile_ranges_kernel, dim3(blocks_for(count, 256)), dim3(256), 0, stream, skeys, layout,
-                           ctx->sorted_vals, ctx->inst_gauss.as<uint32_t>(), ctx->offsets.as<uint32_t>() + n,
-                           ctx->ranges.as<uint2>(), ctx->sorted_g.as<uint32_t>());
+                           ctx->sorted_vals, ctx->offsets.as<uint32_t>() + n, ctx->ranges.as<uint2>());
     }
     GSX_HIP_TRY(hipGetLastError(), "tile_ranges_kernel");
     GSX_TRY(record(ctx, 5, stream));
     const int tiles_padded = ((tiles + 7) / 8) * 8;
     hipLaunchKernelGGL(blend_forward_kernel, dim3((unsigned)tiles_padded), dim3(256), 0, stream,
-                       ctx->ranges.as<uint2>(), ctx->sorted_g.as<uint32_t>(), ctx->rec.as<float4>(), cam,
-                       out_rgb, ctx->final_t.as<float>(),
+                       ctx->ranges.as<uint2>(), ctx->sorted_vals, ctx->inst_gauss.as<uint32_t>(),
+                       ctx->rec.as<float4>(), train ? ctx->sorted_g.as<uint32_t>() : nullptr, cam, out_rgb,
+                       ctx->final_t.as<float>(),
                        ctx->last.as<uint32_t>(), train ? ctx->ckpt.as<float>() : nullptr);
     GSX_HIP_TRY(hipGetLastError(), "blend_forward_kernel");
     GSX_TRY(record(ctx, 6, stream));

@@ -322,15 +322,11 @@ __global__ __launch_bounds__(256) void fill_f32_kernel(float* __restrict__ p, in
     if (i < count) p[i] = v;
 }
 
-// [start, end) of each tile's run in the sorted keys (tiles without keys keep (0, 0)); with a
-// packed layout the emission position of every sorted key (values[i], from the payload bits);
-// and the Gaussian of every sorted position (sorted_g[i] = instance_gaussian[values[i]]), which
-// spares both blends a dependent load per entry.
+// [start, end) of each tile's run in the sorted keys (tiles without keys keep (0, 0)), and with a
+// packed layout the emission position of every sorted key (values[i], from the payload bits).
 __global__ __launch_bounds__(256) void tile_ranges_kernel(const uint64_t* __restrict__ keys, KeyLayout layout,
-                                                          uint32_t* __restrict__ values,
-                                                          const uint32_t* __restrict__ instance_gaussian,
-                                                          const uint32_t* count_ptr, uint2* __restrict__ ranges,
-                                                          uint32_t* __restrict__ sorted_g) {
+                                                          uint32_t* __restrict__ values, const uint32_t* count_ptr,
+                                                          uint2* __restrict__ ranges) {
     const uint32_t count = *count_ptr;
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= count) return;
@@ -338,14 +334,7 @@ __global__ __launch_bounds__(256) void tile_ranges_kernel(const uint64_t* __rest
     const uint32_t tile = key_tile(layout, key);
     if (i == 0 || key_tile(layout, keys[i - 1]) != tile) ranges[tile].x = i;
     if (i == count - 1 || key_tile(layout, keys[i + 1]) != tile) ranges[tile].y = i + 1;
-    uint32_t p;
-    if (layout.payload_bits > 0) {
-        p = (uint32_t)(key & ((1ull << layout.payload_bits) - 1ull));
-        values[i] = p;
-    } else {
-        p = values[i];
-    }
-    sorted_g[i] = instance_gaussian[p];
+    if (layout.payload_bits > 0) values[i] = (uint32_t)(key & ((1ull << layout.payload_bits) - 1ull));
 }
 
 // Workgroup -> tile mapping: consecutive workgroups are dealt round-robin to the 8 XCDs, so give
@@ -382,7 +371,8 @@ __device__ inline size_t checkpoint_slot(uint32_t range_start, int tile, uint32_
 // of the last contributing position, and (TRAIN) the bucket checkpoints.
 // ---------------------------------------------------------------------------------------------
 __global__ __launch_bounds__(kBlendThreads) void blend_forward_kernel(
-    const uint2* __restrict__ ranges, const uint32_t* __restrict__ sorted_g, const float4* __restrict__ rec,
+    const uint2* __restrict__ ranges, const uint32_t* __restrict__ values,
+    const uint32_t* __restrict__ instance_gaussian, const float4* __restrict__ rec, uint32_t* __restrict__ sorted_g,
     CameraParams cam, float* __restrict__ out_rgb,
     float* __restrict__ out_t, uint32_t* __restrict__ out_last, float* __restrict__ ckpt) {
     __shared__ float4 s_r0[kBlendThreads];
@@ -407,7 +397,8 @@ __global__ __launch_bounds__(kBlendThreads) void blend_forward_kernel(
         if (__syncthreads_count(done ? 1 : 0) == kBlendThreads) break;
         const uint32_t j = base + threadIdx.x;
         if (j < range.y) {
-            const uint32_t g = sorted_g[j];
+            const uint32_t g = instance_gaussian[values[j]];
+            if (sorted_g != nullptr) sorted_g[j] = g;  // TRAIN: the backward reads it
             s_r0[threadIdx.x] = rec[3 * (size_t)g + 0];
             s_r1[threadIdx.x] = rec[3 * (size_t)g + 1];
             s_r2[threadIdx.x] = rec[3 * (size_t)g + 2];
@@ -543,14 +534,25 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
         const int count = (int)min((uint32_t)kBackBatch, range.y - (uint32_t)bstart);
         if (threadIdx.x < count) {
             const uint32_t j = (uint32_t)bstart + threadIdx.x;
-            const uint32_t g = sorted_g[j];
             s_pos[threadIdx.x] = values[j];
-            s_r0[threadIdx.x] = rec[3 * (size_t)g + 0];
-            s_r1[threadIdx.x] = rec[3 * (size_t)g + 1];
-            s_r2[threadIdx.x] = rec[3 * (size_t)g + 2];
-            s_k0[threadIdx.x] = cov_coef[2 * (size_t)g + 0];
-            const float4 k1 = cov_coef[2 * (size_t)g + 1];
-            s_k1[threadIdx.x] = make_float2(k1.x, k1.y);
+            // sorted_g is written by the TRAIN forward for every batch it loaded, and every entry
+            // below end_all lies in such a batch; entries from end_all on contribute nothing
+            if (j < end_all) {
+                const uint32_t g = sorted_g[j];
+                s_r0[threadIdx.x] = rec[3 * (size_t)g + 0];
+                s_r1[threadIdx.x] = rec[3 * (size_t)g + 1];
+                s_r2[threadIdx.x] = rec[3 * (size_t)g + 2];
+                s_k0[threadIdx.x] = cov_coef[2 * (size_t)g + 0];
+                const float4 k1 = cov_coef[2 * (size_t)g + 1];
+                s_k1[threadIdx.x] = make_float2(k1.x, k1.y);
+            } else {
+                const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                s_r0[threadIdx.x] = z;
+                s_r1[threadIdx.x] = z;
+                s_r2[threadIdx.x] = make_float4(0.0f, __uint_as_float(1u), 0.0f, 0.0f);  // empty box
+                s_k0[threadIdx.x] = z;
+                s_k1[threadIdx.x] = make_float2(0.0f, 0.0f);
+            }
         }
 #pragma unroll
         for (int b = 0; b < kBatchBuckets; ++b) {
