@@ -63,6 +63,14 @@ __global__ __launch_bounds__(256) void mse_backward_kernel(float* __restrict__ g
 // explicit fused multiply-adds: the SSIM bar is a tolerance (the CPU sums in float64), unlike
 // the L1 term fused into the same pass, which keeps the L1 kernel's exact operations.
 constexpr int kSsimTW = 32, kSsimTH = 16;
+
+// Workgroup -> tile of the plane: consecutive workgroups go round-robin to the 8 XCDs, so each
+// XCD takes a contiguous band of tiles and neighbouring tiles' halos meet in the same L2. The
+// grid has 8 * ceil(tiles / 8) workgroups per plane; those past the last tile exit.
+__device__ inline int ssim_tile_of(int block, int tiles) {
+    const int per = (tiles + 7) / 8;
+    return (block & 7) * per + (block >> 3);
+}
 constexpr int kSsimHW = kSsimTW + 10, kSsimHH = kSsimTH + 10;  // 42 x 26 halo
 
 // Forward: p and t of the halo in LDS; a horizontal 11-tap pass where each thread forms the
@@ -77,8 +85,11 @@ __global__ __launch_bounds__(256) void ssim_forward_kernel(float* __restrict__ m
     __shared__ float s_in[2][kSsimHH][kSsimHW + 1];
     __shared__ float s_h[5][kSsimHH][kSsimTW + 1];
     const int tiles_x = (width + kSsimTW - 1) / kSsimTW;
-    const int ox = (int)(blockIdx.x % tiles_x) * kSsimTW;
-    const int oy = (int)(blockIdx.x / tiles_x) * kSsimTH;
+    const int tiles = tiles_x * ((height + kSsimTH - 1) / kSsimTH);
+    const int tile = ssim_tile_of((int)blockIdx.x, tiles);
+    if (tile >= tiles) return;
+    const int ox = (tile % tiles_x) * kSsimTW;
+    const int oy = (tile / tiles_x) * kSsimTH;
     const int64_t plane = blockIdx.y;
     const int64_t pbase = plane * (int64_t)height * width;
     for (int i = threadIdx.x; i < kSsimHH * kSsimHW; i += 256) {
@@ -176,8 +187,11 @@ __global__ __launch_bounds__(256) void ssim_backward_kernel(float* __restrict__ 
     __shared__ float s_m[3][kSsimHH][kSsimHW + 1];
     __shared__ float s_h[3][kSsimHH][kSsimTW + 1];
     const int tiles_x = (width + kSsimTW - 1) / kSsimTW;
-    const int ox = (int)(blockIdx.x % tiles_x) * kSsimTW;
-    const int oy = (int)(blockIdx.x / tiles_x) * kSsimTH;
+    const int tiles = tiles_x * ((height + kSsimTH - 1) / kSsimTH);
+    const int tile = ssim_tile_of((int)blockIdx.x, tiles);
+    if (tile >= tiles) return;
+    const int ox = (tile % tiles_x) * kSsimTW;
+    const int oy = (tile / tiles_x) * kSsimTH;
     const int64_t plane = blockIdx.y;
     const int64_t total = planes * (int64_t)height * width;
     const int64_t pbase = plane * (int64_t)height * width;
@@ -300,7 +314,7 @@ gsx_hip_status gsx_hip_loss_ssim_chw_f32_forward_kernel_launch(float* loss_map, 
     if (planes <= 0 || height <= 0 || width <= 0) return GSX_HIP_ERROR_INVALID_ARGUMENT;
     if (planes > 65535) return GSX_HIP_ERROR_OUT_OF_RANGE;
     const int tiles = ((width + kSsimTW - 1) / kSsimTW) * ((height + kSsimTH - 1) / kSsimTH);
-    hipLaunchKernelGGL(ssim_forward_kernel, dim3((unsigned)tiles, (unsigned)planes), dim3(256), 0, stream, loss_map,
+    hipLaunchKernelGGL(ssim_forward_kernel, dim3((unsigned)(8 * ((tiles + 7) / 8)), (unsigned)planes), dim3(256), 0, stream, loss_map,
                        prediction, target, height, width, planes, scale, l1_scale, fuse_l1, ssim_workspace);
     return (gsx_hip_status)hipGetLastError();
 }
@@ -314,7 +328,7 @@ gsx_hip_status gsx_hip_loss_ssim_chw_f32_backward_kernel_launch(float* grad_pred
     if (planes <= 0 || height <= 0 || width <= 0) return GSX_HIP_ERROR_INVALID_ARGUMENT;
     if (planes > 65535) return GSX_HIP_ERROR_OUT_OF_RANGE;
     const int tiles = ((width + kSsimTW - 1) / kSsimTW) * ((height + kSsimTH - 1) / kSsimTH);
-    hipLaunchKernelGGL(ssim_backward_kernel, dim3((unsigned)tiles, (unsigned)planes), dim3(256), 0, stream,
+    hipLaunchKernelGGL(ssim_backward_kernel, dim3((unsigned)(8 * ((tiles + 7) / 8)), (unsigned)planes), dim3(256), 0, stream,
                        grad_prediction, prediction, target, height, width, planes, grad_scale, l1_grad_scale, fuse_l1,
                        ssim_workspace);
     return (gsx_hip_status)hipGetLastError();
