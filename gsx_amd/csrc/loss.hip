@@ -154,7 +154,10 @@ __global__ __launch_bounds__(256) void ssim_forward_kernel(float* __restrict__ m
         const float ct = 2.0f * mu1 * mu2 + c1;
         const float dt = 2.0f * s12 + c2;
         const float ab = a * b;
-        const float ssim = ab == 0.0f ? 1.0f : (ct * dt) / ab;
+        // one hardware reciprocal serves all quotients (the SSIM bar is a tolerance): 1/ab,
+        // 1/(a ab) = r/a and 1/(ab b) = r/b with r = 1/ab
+        const float r_ab = __builtin_amdgcn_rcpf(ab);
+        const float ssim = ab == 0.0f ? 1.0f : (ct * dt) * r_ab;
         const bool boundary = y < 5 || y >= height - 5 || x < 5 || x >= width - 5;
         const int64_t idx = pbase + (int64_t)y * width + x;
         if (map != nullptr) {
@@ -166,11 +169,11 @@ __global__ __launch_bounds__(256) void ssim_forward_kernel(float* __restrict__ m
         if (dm != nullptr) {
             float g_mu = 0.0f, g_s1 = 0.0f, g_s12 = 0.0f;
             if (!(boundary || a == 0.0f || b == 0.0f)) {
-                const float aab = a * ab, abb = ab * b;
-                g_mu = (2.0f * mu2 * dt) / ab - (2.0f * mu2 * ct) / ab - (2.0f * mu1 * ct * dt) / aab +
-                       (2.0f * mu1 * ct * dt) / abb;
-                g_s1 = -(ct * dt) / abb;
-                g_s12 = (2.0f * ct) / ab;
+                const float r_aab = r_ab * __builtin_amdgcn_rcpf(a), r_abb = r_ab * __builtin_amdgcn_rcpf(b);
+                const float ctdt = ct * dt;
+                g_mu = 2.0f * mu2 * (dt - ct) * r_ab + 2.0f * mu1 * ctdt * (r_abb - r_aab);
+                g_s1 = -ctdt * r_abb;
+                g_s12 = 2.0f * ct * r_ab;
             }
             dm[idx] = g_mu;
             dm[total + idx] = g_s1;
