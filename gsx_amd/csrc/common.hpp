@@ -355,4 +355,16 @@ __device__ inline void row_reduce_sums(float (&v)[kN]) {
     for (int i = 0; i < kN; ++i) v[i] += dpp_move<0x140, 0xf>(v[i]);  // row_mirror
 }
 
+// n / d rounded to nearest for normal, finite operands whose quotient is normal (no scaling
+// steps): a hardware reciprocal refined once, a quotient and one residual correction, all with
+// fused multiply-adds (Markstein's sequence).
+__device__ inline float div_rn_normal(float n, float d) {
+    float y = __builtin_amdgcn_rcpf(d);
+    const float e = __builtin_fmaf(-d, y, 1.0f);
+    y = __builtin_fmaf(e, y, y);
+    const float q = n * y;
+    const float r = __builtin_fmaf(-d, q, n);
+    return __builtin_fmaf(r, y, q);
+}
+
 }  // namespace gsx_amd

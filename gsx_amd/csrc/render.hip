@@ -621,10 +621,13 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
                 const float w = contrib ? alpha * t_before : 0.0f;
                 float dalpha = t_before * (r1.z * d0 + r1.w * d1 + r2.x * d2);
                 const float one_minus = 1.0f - alpha;
-                // an exact division as the CPU's: near-plane Gaussians' covariance gradients
-                // amplify even 1-ulp differences of this term
+                // a correctly rounded division as the CPU's: near-plane Gaussians' covariance
+                // gradients amplify even 1-ulp differences of this term (1 - alpha lies in
+                // [0.001, 1], so the scaling steps of the general division are not needed;
+                // a zero numerator gives 0 either way)
                 if (fabsf(one_minus) > 1.0e-6f) {
-                    dalpha -= (s0 * d0 + s1 * d1 + s2 * d2) / one_minus;
+                    const float num = s0 * d0 + s1 * d1 + s2 * d2;
+                    dalpha -= num == 0.0f ? 0.0f : div_rn_normal(num, one_minus);
                 }
                 const bool unclamped = op * gval < kMaxFragmentAlpha;
                 const float dg = (contrib && unclamped) ? dalpha * op : 0.0f;
@@ -636,8 +639,10 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
                 const float dic = dpow * (-0.5f * dy * dy);
                 const float4 k0 = s_k0[kk];
                 const float2 k1 = s_k1[kk];
-                float v[kGrad2d] = {dpow * (inv_a * dx + inv_b * dy),
-                                    dpow * (inv_b * dx + inv_c * dy),
+                // the mean2d terms may fuse; the covariance terms keep the CPU's rounding, since
+                // near-plane Gaussians' covariance maps are close to singular
+                float v[kGrad2d] = {dpow * __builtin_fmaf(inv_a, dx, inv_b * dy),
+                                    dpow * __builtin_fmaf(inv_b, dx, inv_c * dy),
                                     dia * k0.x + dib * k0.y + dic * k0.z,
                                     dia * (2.0f * k0.y) + dib * k0.w + dic * (2.0f * k1.x),
                                     dia * k0.z + dib * k1.x + dic * k1.y,
