@@ -183,36 +183,72 @@ __global__ __launch_bounds__(kSortThreads) void radix_rowscan_kernel(const uint3
     if (threadIdx.x == 0) totals[blockIdx.x] = carry;
 }
 
+// The downsweep runs 512 threads (8 waves of 512 keys, 8 rounds each): the serial ranking chain
+// of a chunk is half as long as with 4 waves.
+constexpr int kDownThreads = 512;
+constexpr int kDownWaves = kDownThreads / kWave;           // 8
+constexpr int kDownWaveKeys = kSortChunk / kDownWaves;     // 512
+constexpr int kDownRounds = kDownWaveKeys / kWave;         // 8
+
+// Exclusive scan over the 256 digits held by threads 0..255 of a 512-thread workgroup (threads
+// 256..511 pass 0 and get garbage); `total` receives the sum over the digits.
+__device__ inline uint32_t digit_exclusive_scan(uint32_t v, uint32_t* s_wave, uint32_t& total) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    uint32_t incl = v;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+        const uint32_t o = __shfl_up(incl, off, kWave);
+        if (lane >= off) incl += o;
+    }
+    if (lane == kWave - 1) s_wave[wave] = incl;
+    __syncthreads();
+    uint32_t wave_base = 0;
+    total = 0;
+#pragma unroll
+    for (int w = 0; w < kRadix / kWave; ++w) {
+        const uint32_t sw = s_wave[w];
+        if (w < wave) wave_base += sw;
+        total += sw;
+    }
+    __syncthreads();
+    return wave_base + incl - v;
+}
+
 template <bool kPairs>
-__global__ __launch_bounds__(kSortThreads) void radix_downsweep_kernel(
+__global__ __launch_bounds__(kDownThreads) void radix_downsweep_kernel(
     const uint64_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, int64_t n, int shift,
     int64_t num_chunks, const uint32_t* __restrict__ offsets, const uint32_t* __restrict__ totals,
     uint64_t* __restrict__ keys_out, uint32_t* __restrict__ vals_out) {
     __shared__ uint64_t s_keys[kSortChunk];
     __shared__ uint32_t s_vals[kPairs ? kSortChunk : 1];
-    __shared__ uint32_t s_cnt[kChunkWaves][kRadix];  // wave-private counters, then wave starts
-    __shared__ uint32_t s_local[kRadix];             // start of each digit in the reordered chunk
-    __shared__ uint32_t s_global[kRadix];            // output position of that start
-    __shared__ uint32_t s_wave[kSortThreads / kWave];
+    __shared__ uint32_t s_cnt[kDownWaves][kRadix];  // wave-private counters, then wave starts
+    __shared__ uint32_t s_local[kRadix];            // start of each digit in the reordered chunk
+    __shared__ uint32_t s_global[kRadix];           // output position of that start
+    __shared__ uint32_t s_wave[kDownWaves];
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
     const int64_t base = (int64_t)blockIdx.x * kSortChunk;
     const int chunk_count = (int)min((int64_t)kSortChunk, n - base);
-#pragma unroll
-    for (int w = 0; w < kChunkWaves; ++w) s_cnt[w][threadIdx.x] = 0;
+    for (int i = threadIdx.x; i < kDownWaves * kRadix; i += kDownThreads) (&s_cnt[0][0])[i] = 0;
     __syncthreads();
     // 1. per wave: stable ranks among equal digits (rank = keys of the digit before it in this
-    //    wave's quarter), packed as digit << 16 | rank
+    //    wave's eighth of the chunk), packed as digit << 16 | rank
     const uint64_t lt = lanemask_lt();
-    uint64_t key[kWaveRounds];
-    uint32_t val[kWaveRounds];
-    uint32_t dr[kWaveRounds];
+    uint64_t key[kDownRounds];
+    uint32_t val[kDownRounds];
+    uint32_t dr[kDownRounds];
 #pragma unroll
-    for (int r = 0; r < kWaveRounds; ++r) {
-        const int local = wave * kWaveKeys + r * kWave + lane;
+    for (int r = 0; r < kDownRounds; ++r) {
+        const int local = wave * kDownWaveKeys + r * kWave + lane;
         const bool valid = local < chunk_count;
         key[r] = valid ? keys_in[base + local] : 0ull;
         val[r] = (kPairs && valid) ? vals_in[base + local] : 0u;
+    }
+#pragma unroll
+    for (int r = 0; r < kDownRounds; ++r) {
+        const int local = wave * kDownWaveKeys + r * kWave + lane;
+        const bool valid = local < chunk_count;
         const uint32_t d = digit_of(key[r], shift);
         uint64_t peers = __ballot(valid);
 #pragma unroll
@@ -228,26 +264,35 @@ __global__ __launch_bounds__(kSortThreads) void radix_downsweep_kernel(
         dr[r] = valid ? (d << 16) | (before + rank) : 0xffffffffu;
     }
     __syncthreads();
-    // 2. thread t = digit t: wave starts inside the digit, digit starts inside the chunk, and
-    //    the digit's output position for this chunk
+    // 2. threads 0..255 = digits: wave starts inside the digit, digit starts inside the chunk,
+    //    and the digit's output position for this chunk
     {
-        const uint32_t c0 = s_cnt[0][threadIdx.x], c1 = s_cnt[1][threadIdx.x];
-        const uint32_t c2 = s_cnt[2][threadIdx.x], c3 = s_cnt[3][threadIdx.x];
+        const int t = threadIdx.x;
+        uint32_t c[kDownWaves];
+        uint32_t cnt = 0;
+#pragma unroll
+        for (int w = 0; w < kDownWaves; ++w) {
+            c[w] = t < kRadix ? s_cnt[w][t] : 0u;
+            cnt += c[w];
+        }
         uint32_t dummy;
-        const uint32_t start = block_exclusive_scan_256(c0 + c1 + c2 + c3, s_wave, dummy);
-        uint32_t tot_dummy;
-        const uint32_t digit_base = block_exclusive_scan_256(totals[threadIdx.x], s_wave, tot_dummy);
-        s_local[threadIdx.x] = start;
-        s_global[threadIdx.x] = digit_base + offsets[(int64_t)threadIdx.x * num_chunks + blockIdx.x];
-        s_cnt[0][threadIdx.x] = start;
-        s_cnt[1][threadIdx.x] = start + c0;
-        s_cnt[2][threadIdx.x] = start + c0 + c1;
-        s_cnt[3][threadIdx.x] = start + c0 + c1 + c2;
+        const uint32_t start = digit_exclusive_scan(cnt, s_wave, dummy);
+        const uint32_t digit_base = digit_exclusive_scan(t < kRadix ? totals[t] : 0u, s_wave, dummy);
+        if (t < kRadix) {
+            s_local[t] = start;
+            s_global[t] = digit_base + offsets[(int64_t)t * num_chunks + blockIdx.x];
+            uint32_t run = start;
+#pragma unroll
+            for (int w = 0; w < kDownWaves; ++w) {
+                s_cnt[w][t] = run;
+                run += c[w];
+            }
+        }
     }
     __syncthreads();
     // 3. reorder the chunk by digit in LDS
 #pragma unroll
-    for (int r = 0; r < kWaveRounds; ++r) {
+    for (int r = 0; r < kDownRounds; ++r) {
         if (dr[r] != 0xffffffffu) {
             const uint32_t pos = s_cnt[wave][dr[r] >> 16] + (dr[r] & 0xffffu);
             s_keys[pos] = key[r];
@@ -256,7 +301,7 @@ __global__ __launch_bounds__(kSortThreads) void radix_downsweep_kernel(
     }
     __syncthreads();
     // 4. write out in order: runs of one digit go to consecutive addresses
-    for (int i = threadIdx.x; i < chunk_count; i += kSortThreads) {
+    for (int i = threadIdx.x; i < chunk_count; i += kDownThreads) {
         const uint64_t k = s_keys[i];
         const uint32_t d = digit_of(k, shift);
         const uint32_t pos = s_global[d] + ((uint32_t)i - s_local[d]);
@@ -293,7 +338,7 @@ gsx_hip_status radix_sort_u64(uint64_t* keys, uint32_t* vals, uint64_t* keys_alt
                                shift, chunks, hist);
             hipLaunchKernelGGL(radix_rowscan_kernel, dim3(kRadix), dim3(kSortThreads), 0, stream, hist, chunks,
                                offsets, totals);
-            hipLaunchKernelGGL(radix_downsweep_kernel<kPairs>, dim3((unsigned)chunks), dim3(kSortThreads), 0, stream,
+            hipLaunchKernelGGL(radix_downsweep_kernel<kPairs>, dim3((unsigned)chunks), dim3(kDownThreads), 0, stream,
                                kin, vin, n, shift, chunks, offsets, totals, kout, vout);
             in_alt ^= 1;
         }
