@@ -33,18 +33,20 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def algorithmic_bytes(stage, n, visible, instances, tiles, pixels, sort_passes, keys_only, train=True):
+def algorithmic_bytes(stage, n, visible, instances, tiles, pixels, sort_passes, depth_sort_passes, train=True):
     """Bytes each stage must move at minimum, given this build's data layout (the roofline
     numerators). n Gaussians, visible V, instances I, tiles T, pixels Px, E = 3 Px elements."""
     i = instances
     if stage == "preprocess":
-        return 60 * n + (80 if train else 48) * visible
-    if stage == "scan":
-        return 8 * n
+        return 68 * n + (80 if train else 48) * visible
+    if stage == "depth_order":
+        # depth-key sort (keys only: read for the histogram, read + write to scatter), rank
+        # gather (key, count, three index writes), count scan
+        return depth_sort_passes * 24 * n + 28 * n + 8 * n
     if stage == "emit":
-        return 8 * n + 48 * visible + 12 * i
+        return 12 * n + 48 * visible + 12 * i
     if stage == "sort":
-        return 8 * i + sort_passes * (16 if keys_only else 24) * i
+        return sort_passes * 24 * i
     if stage == "ranges":
         return 20 * i + 8 * tiles
     if stage == "blend_forward":
@@ -253,7 +255,7 @@ def main():
     kernels = []
     for name, ms in stage_ms.items():
         b = algorithmic_bytes(name, args.gaussians, visible, instances, tiles, pixels, int(stats.sort_passes),
-                              int(stats.key_payload_bits) > 0)
+                              int(stats.depth_sort_passes))
         gbps = b / (ms * 1e-3) / 1e9 if ms > 0 else 0.0
         kernels.append({"stage": name, "ms": round(ms, 4), "algorithmic_bytes": int(b), "gbps": round(gbps, 1),
                         "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4)})

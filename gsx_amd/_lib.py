@@ -53,8 +53,8 @@ class GaussianGrads(ctypes.Structure):
 
 class RenderStats(ctypes.Structure):
     _fields_ = [("gaussian_count", _i64), ("visible_count", _i64), ("instance_count", _i64), ("tile_count", _i32),
-                ("sort_passes", _i32), ("key_tile_shift", _i32), ("key_depth_shift", _i32),
-                ("key_depth_base", ctypes.c_uint32), ("key_payload_bits", _i32)]
+                ("sort_passes", _i32), ("depth_sort_passes", _i32), ("key_tile_shift", _i32),
+                ("key_payload_bits", _i32)]
 
 
 class RenderBuffers(ctypes.Structure):

@@ -134,7 +134,7 @@ class Renderer:
         """Record per-stage HIP events for the next `capacity` forward/backward pairs (0 = off)."""
         check(self.lib.gsx_hip_render_context_set_timing(self.handle, int(capacity)), "set timing")
 
-    STAGES = ("preprocess", "scan", "emit", "sort", "ranges", "blend_forward", "blend_backward", "instance_reduce",
+    STAGES = ("preprocess", "depth_order", "emit", "sort", "ranges", "blend_forward", "blend_backward", "instance_reduce",
               "projection_backward")
 
     def timings(self) -> dict:

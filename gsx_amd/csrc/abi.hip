@@ -2,10 +2,12 @@
 // retained TRAIN state, stage timing) and the forward/backward pipelines.
 //
 // Forward (one stream, in order):
-//   preprocess -> exclusive scan of per-Gaussian tile counts -> [host reads the instance count]
-//   -> key emission -> stable radix sort on (tile << 32 | depth bits) -> tile ranges -> blend.
+//   preprocess (+ per-Gaussian depth keys) -> radix sort of the depth keys -> tile counts in
+//   depth order -> exclusive scan -> [host reads the instance count] -> key emission in depth
+//   order -> stable radix sort on the tile bits -> tile ranges -> blend.
 // Backward:
-//   zero the screen-space accumulator -> blend backward (atomics into it) -> projection backward.
+//   blend backward (per-instance partials, no atomics) -> per-Gaussian sums of each Gaussian's
+//   run of partials -> projection backward.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -105,6 +107,9 @@ struct DeviceBuffer {
 
 // Workgroups of the big-box passes (grid-stride over the list of big boxes).
 constexpr unsigned kBigBlocks = 1024;
+// Workgroups per chunk column of reduce_long_chunks_kernel (4 waves each, grid-stride over the
+// list of long runs), and of combine_long_runs_kernel.
+constexpr unsigned kLongRunBlocks = 512;
 
 unsigned blocks_for(int64_t n, int threads) {
     int64_t b = (n + threads - 1) / threads;
@@ -167,7 +172,8 @@ int bits_for(uint32_t v) {
 
 struct gsx_hip_render_context {
     DeviceBuffer rec, cov_coef, ckpt, inst_gauss, inst_grad, tile_count, big_list, offsets, scan_temp, keys, vals,
-        keys_alt, vals_alt, sort_temp, ranges, sorted_g, final_t, last, grad2d;
+        keys_alt, sort_temp, ranges, sorted_g, final_t, last, grad2d, depth_keys, depth_keys_alt, rank_g, rank_count,
+        g_rank, long_list;
     uint32_t* host_count = nullptr;  // pinned
     CameraParams cam{};
     gsx_hip_gaussians gs{};
@@ -175,6 +181,7 @@ struct gsx_hip_render_context {
     int64_t gaussian_count = 0;
     int32_t tile_count_total = 0;
     int32_t sort_passes = 0;
+    int32_t depth_sort_passes = 0;
     bool sorted_in_alt = false;
     KeyLayout layout{};
     uint32_t* sorted_vals = nullptr;  // emission position of each sorted key
@@ -341,8 +348,10 @@ gsx_hip_status gsx_hip_render_context_destroy(gsx_hip_render_context* ctx) {
     if (ctx == nullptr) return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "context must be non-null");
     DeviceBuffer* all[] = {&ctx->rec,       &ctx->cov_coef, &ctx->ckpt,      &ctx->inst_gauss, &ctx->inst_grad,
                            &ctx->tile_count, &ctx->big_list, &ctx->offsets,   &ctx->scan_temp,  &ctx->keys,
-                           &ctx->vals,       &ctx->keys_alt, &ctx->vals_alt,  &ctx->sort_temp,  &ctx->ranges,
-                           &ctx->sorted_g,   &ctx->final_t,  &ctx->last,      &ctx->grad2d};
+                           &ctx->vals,       &ctx->keys_alt, &ctx->sort_temp,  &ctx->ranges,
+                           &ctx->sorted_g,   &ctx->final_t,  &ctx->last,      &ctx->grad2d,     &ctx->depth_keys,
+                           &ctx->depth_keys_alt, &ctx->rank_g, &ctx->rank_count, &ctx->g_rank,
+                           &ctx->long_list};
     for (DeviceBuffer* b : all) b->release();
     if (ctx->host_count != nullptr) (void)hipHostFree(ctx->host_count);
     release_events(ctx);
@@ -388,7 +397,7 @@ gsx_hip_status gsx_hip_render_context_get_timings(gsx_hip_render_context* ctx, f
                                                   int32_t* out_written) {
     if (ctx == nullptr || out_ms == nullptr) return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "context/out_ms null");
     if (!ctx->timing) return fail(GSX_HIP_ERROR_INVALID_STATE, "timing is not enabled");
-    // per set: 0 fwd start, 1 preprocess, 2 scan (+count readback), 3 emit, 4 sort, 5 ranges,
+    // per set: 0 fwd start, 1 preprocess, 2 depth order (+count readback), 3 emit, 4 sort, 5 ranges,
     //          6 blend; 7 bwd start, 8 blend bwd, 9 instance reduce, 10 projection bwd
     double sum[GSX_HIP_RENDER_STAGE_COUNT] = {0.0};
     int nf = 0, nb = 0;
@@ -446,16 +455,33 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     ctx->gaussian_count = n;
     ctx->tile_count_total = tiles;
 
-    GSX_TRY(ctx->rec.reserve((size_t)(n > 0 ? n : 1) * 3 * sizeof(float4), "rec"));
-    if (train) GSX_TRY(ctx->cov_coef.reserve((size_t)(n > 0 ? n : 1) * 2 * sizeof(float4), "cov_coef"));
-    GSX_TRY(ctx->tile_count.reserve((size_t)(n > 0 ? n : 1) * sizeof(uint32_t), "tile_count"));
+    const size_t n1 = (size_t)(n > 0 ? n : 1);
+    GSX_TRY(ctx->rec.reserve(n1 * 3 * sizeof(float4), "rec"));
+    if (train) GSX_TRY(ctx->cov_coef.reserve(n1 * 2 * sizeof(float4), "cov_coef"));
+    GSX_TRY(ctx->tile_count.reserve(n1 * sizeof(uint32_t), "tile_count"));
     // [0] = number of big boxes, [1..n] = their Gaussians
     GSX_TRY(ctx->big_list.reserve((size_t)(n + 1) * sizeof(uint32_t), "big_list"));
     GSX_TRY(ctx->offsets.reserve((size_t)(n + 1) * sizeof(uint32_t), "offsets"));
     GSX_TRY(ctx->scan_temp.reserve(gsx_hip_scan_temp_bytes(n), "scan_temp"));
+    GSX_TRY(ctx->depth_keys.reserve(n1 * sizeof(uint64_t), "depth_keys"));
+    GSX_TRY(ctx->depth_keys_alt.reserve(n1 * sizeof(uint64_t), "depth_keys_alt"));
+    GSX_TRY(ctx->rank_g.reserve(n1 * sizeof(uint32_t), "rank_gaussian"));
+    GSX_TRY(ctx->rank_count.reserve(n1 * sizeof(uint32_t), "rank_count"));
+    GSX_TRY(ctx->g_rank.reserve(n1 * sizeof(uint32_t), "gaussian_rank"));
+    // [0] = number of ranks with long instance runs, [1..n] = those ranks
+    GSX_TRY(ctx->long_list.reserve((size_t)(n + 1) * sizeof(uint32_t), "long_list"));
+    GSX_TRY(ctx->sort_temp.reserve(gsx_hip_radix_sort_temp_bytes(n), "sort_temp"));
     GSX_TRY(ctx->ranges.reserve((size_t)tiles * sizeof(uint2), "ranges"));
     GSX_TRY(ctx->final_t.reserve((size_t)pixels * sizeof(float), "final_t"));
     GSX_TRY(ctx->last.reserve((size_t)pixels * sizeof(uint32_t), "last"));
+
+    // depth keys: (bits(depth) - bits(near)) << index_bits | index, invisible ones after every
+    // visible depth (see KeyLayout); at most 31 + 32 bits
+    const uint32_t near_bits = gsx_f32_bits(cam.near_plane), far_bits = gsx_f32_bits(cam.far_plane);
+    const uint32_t depth_max = far_bits - near_bits;
+    const int index_bits = std::max(1, bits_for((uint32_t)(n > 0 ? n - 1 : 0)));
+    const int depth_bits = bits_for(depth_max + 1u);
+    ctx->depth_sort_passes = (depth_bits + 7) / 8;
 
     if (ctx->timing) {
         ctx->cur = (ctx->cur + 1) % ctx->ring;
@@ -471,7 +497,9 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
                            gaussians->sh1, gaussians->sh2, gaussians->sh3, (int)gaussians->sh_degree, cam,
                            ctx->rec.as<float4>(), train ? ctx->cov_coef.as<float4>() : nullptr,
                            ctx->tile_count.as<uint32_t>(), train ? visible_counter : nullptr,
-                           ctx->big_list.as<uint32_t>() + 1, ctx->big_list.as<uint32_t>());
+                           ctx->big_list.as<uint32_t>() + 1, ctx->big_list.as<uint32_t>(),
+                           ctx->depth_keys.as<uint64_t>(), near_bits, depth_max, index_bits,
+                           ctx->long_list.as<uint32_t>());
         GSX_HIP_TRY(hipGetLastError(), "preprocess_kernel");
         hipLaunchKernelGGL(big_tiles_kernel<false>, dim3(kBigBlocks), dim3(256), 0, stream,
                            ctx->big_list.as<uint32_t>() + 1, ctx->big_list.as<uint32_t>(), ctx->rec.as<float4>(),
@@ -480,7 +508,21 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
         GSX_HIP_TRY(hipGetLastError(), "big_tiles_kernel<count>");
     }
     GSX_TRY(record(ctx, 1, stream));
-    GSX_TRY(gsx_hip_scan_exclusive_u32(ctx->tile_count.as<uint32_t>(), ctx->offsets.as<uint32_t>(), n,
+    // depth order of the Gaussians, then their tile counts in that order and its scan
+    const uint64_t* sorted_depth = ctx->depth_keys.as<uint64_t>();
+    if (n > 0) {
+        int depth_in_alt = 0;
+        const int end_bit = std::min(64, index_bits + ctx->depth_sort_passes * 8);
+        GSX_TRY(gsx_hip_radix_sort_keys_u64(ctx->depth_keys.as<uint64_t>(), ctx->depth_keys_alt.as<uint64_t>(), n,
+                                            index_bits, end_bit, ctx->sort_temp.ptr, &depth_in_alt, stream));
+        if (depth_in_alt) sorted_depth = ctx->depth_keys_alt.as<uint64_t>();
+        hipLaunchKernelGGL(rank_gather_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, n, sorted_depth,
+                           (uint64_t)((1ull << index_bits) - 1ull), ctx->tile_count.as<uint32_t>(),
+                           ctx->rank_g.as<uint32_t>(), ctx->rank_count.as<uint32_t>(), ctx->g_rank.as<uint32_t>(),
+                           ctx->long_list.as<uint32_t>());
+        GSX_HIP_TRY(hipGetLastError(), "rank_gather_kernel");
+    }
+    GSX_TRY(gsx_hip_scan_exclusive_u32(ctx->rank_count.as<uint32_t>(), ctx->offsets.as<uint32_t>(), n,
                                        ctx->scan_temp.ptr, stream));
     GSX_HIP_TRY(hipMemcpyAsync(ctx->host_count, ctx->offsets.as<uint32_t>() + n, sizeof(uint32_t),
                                hipMemcpyDeviceToHost, stream),
@@ -489,29 +531,18 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     GSX_TRY(record(ctx, 2, stream));
     const int64_t count = (int64_t)ctx->host_count[0];
     ctx->instance_count = count;
-    GSX_TRY(ctx->keys.reserve((size_t)(count > 0 ? count : 1) * sizeof(uint64_t), "keys"));
-    GSX_TRY(ctx->keys_alt.reserve((size_t)(count > 0 ? count : 1) * sizeof(uint64_t), "keys_alt"));
-    GSX_TRY(ctx->vals.reserve((size_t)(count > 0 ? count : 1) * sizeof(uint32_t), "vals"));
-    GSX_TRY(ctx->vals_alt.reserve((size_t)(count > 0 ? count : 1) * sizeof(uint32_t), "vals_alt"));
-    GSX_TRY(ctx->inst_gauss.reserve((size_t)(count > 0 ? count : 1) * sizeof(uint32_t), "instance_gaussian"));
-    GSX_TRY(ctx->sorted_g.reserve((size_t)(count > 0 ? count : 1) * sizeof(uint32_t), "sorted_g"));
+    const size_t c1 = (size_t)(count > 0 ? count : 1);
+    GSX_TRY(ctx->keys.reserve(c1 * sizeof(uint64_t), "keys"));
+    GSX_TRY(ctx->keys_alt.reserve(c1 * sizeof(uint64_t), "keys_alt"));
+    GSX_TRY(ctx->vals.reserve(c1 * sizeof(uint32_t), "vals"));
+    GSX_TRY(ctx->inst_gauss.reserve(c1 * sizeof(uint32_t), "instance_gaussian"));
+    GSX_TRY(ctx->sorted_g.reserve(c1 * sizeof(uint32_t), "sorted_g"));
     GSX_TRY(ctx->sort_temp.reserve(gsx_hip_radix_sort_temp_bytes(count), "sort_temp"));
-    // key layout for this forward (see KeyLayout): tile bits, depth bits relative to bits(near),
-    // and the emission position packed in the low bits when everything fits in 64 bits
-    const uint32_t near_bits = gsx_f32_bits(cam.near_plane), far_bits = gsx_f32_bits(cam.far_plane);
-    const int depth_bits = bits_for(far_bits - near_bits);
-    const int pos_bits = bits_for((uint32_t)(count > 0 ? count - 1 : 0));
+    // instance keys: tile << payload_bits | emission position (at most 32 + 32 bits)
+    const int pos_bits = std::max(1, bits_for((uint32_t)(count > 0 ? count - 1 : 0)));
     KeyLayout layout{};
-    layout.depth_base = near_bits;
-    layout.depth_max = far_bits - near_bits;
-    if (tile_bits + depth_bits + pos_bits <= 64) {
-        layout.payload_bits = pos_bits > 0 ? pos_bits : 1;
-        layout.depth_shift = layout.payload_bits;
-    } else {
-        layout.payload_bits = 0;
-        layout.depth_shift = 0;
-    }
-    layout.tile_shift = layout.depth_shift + depth_bits;
+    layout.payload_bits = pos_bits;
+    layout.tile_shift = pos_bits;
     ctx->layout = layout;
     if (train) {
         // bucket checkpoints: at most I/kBucket + tiles + 1 slots of 256 floats
@@ -520,29 +551,23 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     }
     if (n > 0) {
         hipLaunchKernelGGL(emit_keys_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, n, ctx->rec.as<float4>(),
-                           ctx->tile_count.as<uint32_t>(), ctx->offsets.as<uint32_t>(), cam.tiles_x, layout,
-                           ctx->keys.as<uint64_t>(), ctx->vals.as<uint32_t>(), ctx->inst_gauss.as<uint32_t>());
+                           ctx->rank_g.as<uint32_t>(), ctx->rank_count.as<uint32_t>(), ctx->offsets.as<uint32_t>(),
+                           cam.tiles_x, layout, ctx->keys.as<uint64_t>(), ctx->inst_gauss.as<uint32_t>());
         GSX_HIP_TRY(hipGetLastError(), "emit_keys_kernel");
         hipLaunchKernelGGL(big_tiles_kernel<true>, dim3(kBigBlocks), dim3(256), 0, stream,
                            ctx->big_list.as<uint32_t>() + 1, ctx->big_list.as<uint32_t>(), ctx->rec.as<float4>(),
-                           cam.tiles_x, layout, nullptr, ctx->offsets.as<uint32_t>(), ctx->keys.as<uint64_t>(),
-                           ctx->vals.as<uint32_t>(), ctx->inst_gauss.as<uint32_t>());
+                           cam.tiles_x, layout, nullptr, ctx->offsets.as<uint32_t>(), ctx->g_rank.as<uint32_t>(),
+                           ctx->keys.as<uint64_t>(), ctx->inst_gauss.as<uint32_t>());
         GSX_HIP_TRY(hipGetLastError(), "big_tiles_kernel<emit>");
     }
     GSX_TRY(record(ctx, 3, stream));
     int in_alt = 0;
-    const int sort_bits = depth_bits + tile_bits;
-    ctx->sort_passes = (sort_bits + 7) / 8;
-    if (layout.payload_bits > 0) {
-        const int end_bit = std::min(64, layout.depth_shift + ctx->sort_passes * 8);  // same pass count
+    ctx->sort_passes = (tile_bits + 7) / 8;
+    {
+        const int end_bit = std::min(64, layout.tile_shift + ctx->sort_passes * 8);  // same pass count
         GSX_TRY(gsx_hip_radix_sort_keys_u64(ctx->keys.as<uint64_t>(), ctx->keys_alt.as<uint64_t>(), count,
-                                            layout.depth_shift, end_bit, ctx->sort_temp.ptr, &in_alt, stream));
+                                            layout.tile_shift, end_bit, ctx->sort_temp.ptr, &in_alt, stream));
         ctx->sorted_vals = ctx->vals.as<uint32_t>();  // written by tile_ranges_kernel
-    } else {
-        GSX_TRY(gsx_hip_radix_sort_pairs_u64(ctx->keys.as<uint64_t>(), ctx->vals.as<uint32_t>(),
-                                             ctx->keys_alt.as<uint64_t>(), ctx->vals_alt.as<uint32_t>(), count, 0,
-                                             ctx->sort_passes * 8, ctx->sort_temp.ptr, &in_alt, stream));
-        ctx->sorted_vals = in_alt ? ctx->vals_alt.as<uint32_t>() : ctx->vals.as<uint32_t>();
     }
     ctx->sorted_in_alt = in_alt != 0;
     GSX_TRY(record(ctx, 4, stream));
@@ -595,22 +620,32 @@ gsx_hip_status gsx_hip_render_backward(gsx_hip_render_context* ctx, const float*
     const CameraParams& cam = ctx->cam;
     const int32_t tiles = cam.tiles_x * cam.tiles_y;
     const uint32_t* svals = ctx->sorted_vals;
+    // per-instance partials: [I][8] records, then the [I] opacity terms
+    float* inst_grad_op = ctx->inst_grad.as<float>() + (size_t)ctx->instance_count * 8;
     GSX_TRY(record(ctx, 7, stream));
     const int tiles_padded = ((tiles + 7) / 8) * 8;
     hipLaunchKernelGGL(blend_backward_kernel, dim3((unsigned)tiles_padded), dim3(256), 0, stream,
                        ctx->ranges.as<uint2>(), svals, ctx->sorted_g.as<uint32_t>(), ctx->rec.as<float4>(),
                        ctx->cov_coef.as<float4>(), ctx->ckpt.as<float>(), cam, grad_rgb, ctx->final_t.as<float>(),
-                       ctx->last.as<uint32_t>(), ctx->inst_grad.as<float>());
+                       ctx->last.as<uint32_t>(), ctx->inst_grad.as<float>(), inst_grad_op);
     GSX_HIP_TRY(hipGetLastError(), "blend_backward_kernel");
     GSX_TRY(record(ctx, 8, stream));
     if (n > 0) {
         hipLaunchKernelGGL(reduce_instance_grads_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, n,
-                           ctx->offsets.as<uint32_t>(), ctx->inst_grad.as<float>(), ctx->grad2d.as<float>());
+                           ctx->offsets.as<uint32_t>(), ctx->rank_g.as<uint32_t>(), ctx->inst_grad.as<float>(),
+                           inst_grad_op, ctx->grad2d.as<float>());
         GSX_HIP_TRY(hipGetLastError(), "reduce_instance_grads_kernel");
-        hipLaunchKernelGGL(reduce_long_runs_kernel, dim3(kBigBlocks), dim3(256), 0, stream,
-                           ctx->big_list.as<uint32_t>() + 1, ctx->big_list.as<uint32_t>(), ctx->offsets.as<uint32_t>(),
-                           ctx->inst_grad.as<float>(), ctx->grad2d.as<float>());
-        GSX_HIP_TRY(hipGetLastError(), "reduce_long_runs_kernel");
+        // chunk length: a run has at most `tiles` instances, so at most kLongChunks chunks
+        const uint32_t chunk = std::max<uint32_t>(
+            kWave, ((uint32_t)(tiles + (int)kLongChunks - 1) / kLongChunks + kWave - 1) / kWave * kWave);
+        hipLaunchKernelGGL(reduce_long_chunks_kernel, dim3(kLongRunBlocks, kLongChunks), dim3(256), 0, stream,
+                           ctx->long_list.as<uint32_t>(), ctx->offsets.as<uint32_t>(), chunk,
+                           ctx->inst_grad.as<float>(), inst_grad_op);
+        GSX_HIP_TRY(hipGetLastError(), "reduce_long_chunks_kernel");
+        hipLaunchKernelGGL(combine_long_runs_kernel, dim3(kLongRunBlocks), dim3(256), 0, stream,
+                           ctx->long_list.as<uint32_t>(), ctx->offsets.as<uint32_t>(), ctx->rank_g.as<uint32_t>(),
+                           chunk, ctx->inst_grad.as<float>(), inst_grad_op, ctx->grad2d.as<float>());
+        GSX_HIP_TRY(hipGetLastError(), "combine_long_runs_kernel");
     }
     GSX_TRY(record(ctx, 9, stream));
     if (n > 0) {
@@ -633,9 +668,8 @@ gsx_hip_status gsx_hip_render_context_get_stats(const gsx_hip_render_context* ct
     out->instance_count = ctx->instance_count;
     out->tile_count = ctx->tile_count_total;
     out->sort_passes = ctx->sort_passes;
+    out->depth_sort_passes = ctx->depth_sort_passes;
     out->key_tile_shift = ctx->layout.tile_shift;
-    out->key_depth_shift = ctx->layout.depth_shift;
-    out->key_depth_base = ctx->layout.depth_base;
     out->key_payload_bits = ctx->layout.payload_bits;
     return GSX_HIP_SUCCESS;
 }

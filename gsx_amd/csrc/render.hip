@@ -39,24 +39,19 @@ constexpr int kWavesPerBlock = 4;
 // big_tiles_kernel): a wave holding a full-image box would otherwise serialise hundreds of steps.
 constexpr uint32_t kBigTiles = 256;
 
-// Sort key of an instance: tile << tile_shift | (bits(depth) - depth_base) << depth_shift | payload.
-// Visible depths lie in [near, far] (preprocess culls the rest), and positive floats order like
-// their bit patterns, so bits(depth) - bits(near) keeps the depth order in fewer bits than the
-// full pattern (27 instead of 32 for near 0.01, far 100): one radix pass fewer. When everything
-// fits in 64 bits the emission position rides in the low payload_bits bits and the sort moves
-// keys only; otherwise payload_bits = 0 and the position travels as the sort value.
+// Sort keys. Gaussians are first sorted by depth: key = (bits(depth) - bits(near)) << index_bits
+// | index (visible depths lie in [near, far], where positive floats order like their bit
+// patterns, so the offset keeps the order in fewer bits; invisible Gaussians get the offset
+// bits(far) - bits(near) + 1 and sort last). Instances are then emitted in that depth order,
+// key = tile << tile_shift | emission position, and sorted stably on the tile bits alone: each
+// tile's run is in (depth, index) order, the CPU backend's order, after two passes at 1080p.
 struct KeyLayout {
-    int tile_shift;
-    int depth_shift;
-    uint32_t depth_base;
-    uint32_t depth_max;  // largest depth offset (bits(far) - bits(near)); larger ones are clamped
+    int tile_shift;    // = payload bits (emission position)
     int payload_bits;
 };
 
-__device__ inline uint64_t make_key(const KeyLayout& k, uint32_t tile, uint32_t depth_bits, uint32_t pos) {
-    uint32_t rel = depth_bits - k.depth_base;
-    if (rel > k.depth_max) rel = k.depth_max;  // only for non-finite depths
-    uint64_t key = ((uint64_t)rel << k.depth_shift) | (k.payload_bits > 0 ? (uint64_t)pos : 0ull);
+__device__ inline uint64_t make_key(const KeyLayout& k, uint32_t tile, uint32_t pos) {
+    uint64_t key = (uint64_t)pos;
     if (k.tile_shift < 64) key |= (uint64_t)tile << k.tile_shift;
     return key;
 }
@@ -83,7 +78,6 @@ struct WaveBoxes {
     float rwx[kWave];  // 1 / wx, for the row of a flattened tile index
     int32_t x0[kWave], x1[kWave], y0[kWave], y1[kWave];
     uint32_t tx0[kWave], ty0[kWave], wx[kWave], excl[kWave], kept[kWave], out[kWave];
-    uint32_t depth[kWave];
     uint32_t g[kWave];
 };
 
@@ -105,7 +99,6 @@ __device__ inline uint32_t stage_box(WaveBoxes& w, bool valid, float4 r0, float4
         w.ty0[lane] = (uint32_t)y0 / kTile;
         w.wx[lane] = (uint32_t)x1 / kTile - (uint32_t)x0 / kTile + 1;
         w.rwx[lane] = 1.0f / (float)w.wx[lane];
-        w.depth[lane] = __float_as_uint(r2.w);
         total = w.wx[lane] * ((uint32_t)y1 / kTile - (uint32_t)y0 / kTile + 1);
     }
     w.g[lane] = g;
@@ -127,8 +120,7 @@ __device__ inline uint32_t stage_box(WaveBoxes& w, bool valid, float4 r0, float4
 // instance_gaussian) at out[owner] + rank; always accumulates kept[owner].
 template <bool kEmit>
 __device__ inline void walk_wave_tiles(WaveBoxes& w, uint32_t wave_total, int32_t tiles_x, const KeyLayout& layout,
-                                       uint64_t* __restrict__ keys, uint32_t* __restrict__ values,
-                                       uint32_t* __restrict__ instance_gaussian) {
+                                       uint64_t* __restrict__ keys, uint32_t* __restrict__ instance_gaussian) {
     const uint32_t lane = __lane_id();
     const uint64_t lt = lanemask_lt();
     for (uint32_t base = 0; base < wave_total; base += kWave) {
@@ -160,8 +152,7 @@ __device__ inline void walk_wave_tiles(WaveBoxes& w, uint32_t wave_total, int32_
         const uint32_t before = w.kept[owner];
         if (kEmit && keep) {
             const uint32_t pos = w.out[owner] + before + (uint32_t)__popcll(mask & lt & seg);
-            keys[pos] = make_key(layout, tile, w.depth[owner], pos);
-            if (layout.payload_bits == 0) values[pos] = pos;
+            keys[pos] = make_key(layout, tile, pos);
             instance_gaussian[pos] = w.g[owner];
         }
         // the last lane of each owner segment advances that owner's running count
@@ -177,7 +168,9 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
     const float* __restrict__ logscale, const float* __restrict__ opacity, const float* __restrict__ sh0,
     const float* __restrict__ sh1, const float* __restrict__ sh2, const float* __restrict__ sh3, int sh_degree,
     CameraParams cam, float4* __restrict__ rec, float4* __restrict__ cov_coef, uint32_t* __restrict__ tile_count,
-    float* __restrict__ visible_counter, uint32_t* __restrict__ big_list, uint32_t* __restrict__ big_count) {
+    float* __restrict__ visible_counter, uint32_t* __restrict__ big_list, uint32_t* __restrict__ big_count,
+    uint64_t* __restrict__ depth_keys, uint32_t depth_base, uint32_t depth_max, int index_bits,
+    uint32_t* __restrict__ long_count) {
     __shared__ WaveBoxes s_boxes[kWavesPerBlock];
     WaveBoxes& wb = s_boxes[threadIdx.x / kWave];
     const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -213,55 +206,90 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
             }
         }
     }
+    if (g == 0) *long_count = 0;  // for rank_gather_kernel, which runs after this kernel
+    if (g < n) {
+        uint32_t rel = depth_max + 1u;  // invisible: after every visible depth
+        if (visible) {
+            rel = __float_as_uint(r2.w) - depth_base;
+            if (rel > depth_max) rel = depth_max;  // only for non-finite depths
+        }
+        depth_keys[g] = ((uint64_t)rel << index_bits) | (uint64_t)g;
+    }
     const bool big = visible && box_tiles(r2) > kBigTiles;
     if (big) big_list[atomicAdd(big_count, 1u)] = (uint32_t)g;  // counted by big_tiles_kernel
     const uint32_t total = stage_box(wb, visible && !big, r0, r1, r2, (uint32_t)g, 0u);
-    walk_wave_tiles<false>(wb, total, cam.tiles_x, KeyLayout{}, nullptr, nullptr, nullptr);
+    walk_wave_tiles<false>(wb, total, cam.tiles_x, KeyLayout{}, nullptr, nullptr);
     if (g < n && !big) tile_count[g] = wb.kept[__lane_id()];
 }
 
+// Instance runs longer than this are summed by a wave each in the backward (see
+// reduce_long_runs_kernel), shorter ones by one thread each.
+constexpr uint32_t kLaneRun = 32;
+
+// After the depth sort: the Gaussian of every depth rank, its kept-tile count, its rank, and the
+// list of ranks whose count exceeds kLaneRun (long_list[0] = length, zeroed by preprocess).
+__global__ __launch_bounds__(256) void rank_gather_kernel(int64_t n, const uint64_t* __restrict__ sorted_depth_keys,
+                                                          uint64_t index_mask, const uint32_t* __restrict__ tile_count,
+                                                          uint32_t* __restrict__ rank_gaussian,
+                                                          uint32_t* __restrict__ rank_count,
+                                                          uint32_t* __restrict__ gaussian_rank,
+                                                          uint32_t* __restrict__ long_list) {
+    const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= n) return;
+    const uint32_t g = (uint32_t)(sorted_depth_keys[r] & index_mask);
+    const uint32_t c = tile_count[g];
+    rank_gaussian[r] = g;
+    rank_count[r] = c;
+    gaussian_rank[g] = (uint32_t)r;
+    if (c > kLaneRun) long_list[1 + atomicAdd(long_list, 1u)] = (uint32_t)r;
+}
+
 // ---------------------------------------------------------------------------------------------
-// Key emission: Gaussian g owns positions offset[g] .. offset[g+1]) of the instance array, one
-// per kept tile of its box in row-major tile order; key = tile << 32 | bits(depth). Offsets come
-// from an exclusive scan in Gaussian order, so equal keys appear in ascending Gaussian order and
-// a stable sort reproduces the CPU (depth, index) order per tile. The sorted value is the
-// emission position; instance_gaussian[position] = g.
+// Key emission in depth order: the Gaussian of rank r owns positions offset[r] .. offset[r+1])
+// of the instance array, one per kept tile of its box in row-major tile order (offsets are the
+// exclusive scan of the counts in rank order). key = tile << tile_shift | position, and
+// instance_gaussian[position] = g. A stable sort on the tile bits then leaves every tile's run
+// in (depth, index) order.
 // ---------------------------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void emit_keys_kernel(int64_t n, const float4* __restrict__ rec,
-                                                        const uint32_t* __restrict__ tile_count,
+                                                        const uint32_t* __restrict__ rank_gaussian,
+                                                        const uint32_t* __restrict__ rank_count,
                                                         const uint32_t* __restrict__ offsets, int32_t tiles_x,
                                                         KeyLayout layout, uint64_t* __restrict__ keys,
-                                                        uint32_t* __restrict__ values,
                                                         uint32_t* __restrict__ instance_gaussian) {
     __shared__ WaveBoxes s_boxes[kWavesPerBlock];
     WaveBoxes& wb = s_boxes[threadIdx.x / kWave];
-    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    bool any = g < n && tile_count[g] > 0;
+    const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    bool any = r < n && rank_count[r] > 0;
+    uint32_t g = 0;
     float4 r0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), r1 = r0, r2 = r0;
     uint32_t o = 0;
     if (any) {
-        r2 = rec[3 * g + 2];
+        g = rank_gaussian[r];
+        r2 = rec[3 * (size_t)g + 2];
         any = box_tiles(r2) <= kBigTiles;  // big boxes are emitted by big_tiles_kernel
     }
     if (any) {
-        r0 = rec[3 * g + 0];
-        r1 = rec[3 * g + 1];
-        o = offsets[g];
+        r0 = rec[3 * (size_t)g + 0];
+        r1 = rec[3 * (size_t)g + 1];
+        o = offsets[r];
     }
-    const uint32_t total = stage_box(wb, any, r0, r1, r2, (uint32_t)g, o);
-    walk_wave_tiles<true>(wb, total, tiles_x, layout, keys, values, instance_gaussian);
+    const uint32_t total = stage_box(wb, any, r0, r1, r2, g, o);
+    walk_wave_tiles<true>(wb, total, tiles_x, layout, keys, instance_gaussian);
 }
 
 // Big boxes: one workgroup per Gaussian of big_list (grid-stride over the list), 256 tiles per
 // step in row-major order. kEmit = false writes tile_count[g]; kEmit = true writes the kept
-// instances at offsets[g] + rank, ranks from per-wave ballots and a 4-wave prefix.
+// instances at offsets[rank of g] + their rank among the kept tiles (per-wave ballots and a
+// 4-wave prefix).
 template <bool kEmit>
 __global__ __launch_bounds__(256) void big_tiles_kernel(const uint32_t* __restrict__ big_list,
                                                         const uint32_t* __restrict__ big_count,
                                                         const float4* __restrict__ rec, int32_t tiles_x,
                                                         KeyLayout layout, uint32_t* __restrict__ tile_count,
                                                         const uint32_t* __restrict__ offsets,
-                                                        uint64_t* __restrict__ keys, uint32_t* __restrict__ values,
+                                                        const uint32_t* __restrict__ gaussian_rank,
+                                                        uint64_t* __restrict__ keys,
                                                         uint32_t* __restrict__ instance_gaussian) {
     __shared__ uint32_t s_wave[kWavesPerBlock];
     const uint32_t count = *big_count;
@@ -276,8 +304,7 @@ __global__ __launch_bounds__(256) void big_tiles_kernel(const uint32_t* __restri
         const uint32_t total = wx * ((uint32_t)y1 / kTile - ty0 + 1);
         const gsx_tile_conic con = gsx_tile_conic_make(r0.x, r0.y, r0.z, r0.w * 0.5f, r1.x, r1.y);
         const float rwx = 1.0f / (float)wx;
-        const uint32_t depth = __float_as_uint(r2.w);
-        const uint32_t o = kEmit ? offsets[g] : 0u;
+        const uint32_t o = kEmit ? offsets[gaussian_rank[g]] : 0u;
         uint32_t running = 0;
         for (uint32_t base = 0; base < total; base += blockDim.x) {
             const uint32_t k = base + threadIdx.x;
@@ -301,8 +328,7 @@ __global__ __launch_bounds__(256) void big_tiles_kernel(const uint32_t* __restri
             }
             if (kEmit && keep) {
                 const uint32_t pos = o + running + before + (uint32_t)__popcll(mask & lanemask_lt());
-                keys[pos] = make_key(layout, tile, depth, pos);
-                if (layout.payload_bits == 0) values[pos] = pos;
+                keys[pos] = make_key(layout, tile, pos);
                 instance_gaussian[pos] = g;
             }
             running += step_total;
@@ -322,8 +348,8 @@ __global__ __launch_bounds__(256) void fill_f32_kernel(float* __restrict__ p, in
     if (i < count) p[i] = v;
 }
 
-// [start, end) of each tile's run in the sorted keys (tiles without keys keep (0, 0)), and with a
-// packed layout the emission position of every sorted key (values[i], from the payload bits).
+// [start, end) of each tile's run in the sorted keys (tiles without keys keep (0, 0)), and the
+// emission position of every sorted key (values[i], the payload bits).
 __global__ __launch_bounds__(256) void tile_ranges_kernel(const uint64_t* __restrict__ keys, KeyLayout layout,
                                                           uint32_t* __restrict__ values, const uint32_t* count_ptr,
                                                           uint2* __restrict__ ranges) {
@@ -334,7 +360,7 @@ __global__ __launch_bounds__(256) void tile_ranges_kernel(const uint64_t* __rest
     const uint32_t tile = key_tile(layout, key);
     if (i == 0 || key_tile(layout, keys[i - 1]) != tile) ranges[tile].x = i;
     if (i == count - 1 || key_tile(layout, keys[i + 1]) != tile) ranges[tile].y = i + 1;
-    if (layout.payload_bits > 0) values[i] = (uint32_t)(key & ((1ull << layout.payload_bits) - 1ull));
+    values[i] = (uint32_t)(key & ((1ull << layout.payload_bits) - 1ull));
 }
 
 // Workgroup -> tile mapping: consecutive workgroups are dealt round-robin to the 8 XCDs, so give
@@ -448,17 +474,19 @@ __global__ __launch_bounds__(kBlendThreads) void blend_forward_kernel(
 // Per-Gaussian screen-space gradient accumulator, 9 floats per Gaussian:
 //   dmean2d x, y | dcov2d a, b, c | dcolor r, g, b | dopacity (w.r.t. the sigmoid value)
 constexpr int kGrad2d = 9;
+constexpr int kGradRecord = 8;  // per-instance partials: channels 0-7 in one 32-byte record
 
 // ---------------------------------------------------------------------------------------------
 // Blend backward: render.c:1559-1666 restated per pixel, back to front, with the CPU's exact
-// T_before: for each 32-entry bucket (last first) the pixel reloads the bucket's checkpointed T,
+// T_before: for each 16-entry bucket (last first) the pixel reloads the bucket's checkpointed T,
 // replays the bucket forward (same operations as the forward, so T_before, G and the contribution
 // set are bit-identical to the CPU's) and then walks it backwards accumulating the suffix colour
 // exactly as the CPU does. Per contribution the gradient terms are the CPU's, including the
 // d(conic)/d(cov2d) map applied per contribution.
 // Reduction without atomics: each wave sums its lanes' 9 partials per entry with DPP moves, the
-// four waves combine through LDS, and the tile writes one 9-float partial per instance into
-// instance_grad[emission position]; reduce_instance_grads_kernel then sums each Gaussian's
+// four waves combine through LDS, and the tile writes one 9-float partial per instance at its
+// emission position (channels 0-7 as one 32-byte record of instance_grad, channel 8, the
+// opacity term, in instance_grad_op); reduce_instance_grads_kernel then sums each Gaussian's
 // contiguous run of positions. The result is deterministic and immune to the contention of
 // full-screen Gaussians (present in every tile).
 // ---------------------------------------------------------------------------------------------
@@ -474,7 +502,8 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
     const uint2* __restrict__ ranges, const uint32_t* __restrict__ values, const uint32_t* __restrict__ sorted_g,
     const float4* __restrict__ rec, const float4* __restrict__ cov_coef, const float* __restrict__ ckpt,
     CameraParams cam, const float* __restrict__ grad_rgb, const float* __restrict__ final_t,
-    const uint32_t* __restrict__ last_contrib, float* __restrict__ instance_grad) {
+    const uint32_t* __restrict__ last_contrib, float* __restrict__ instance_grad,
+    float* __restrict__ instance_grad_op) {
     __shared__ float4 s_r0[kBackBatch];
     __shared__ float4 s_r1[kBackBatch];
     __shared__ float4 s_r2[kBackBatch];
@@ -521,9 +550,11 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
     const uint32_t zero_from =
         end_all <= range.x ? range.x : range.x + ((end_all - range.x + kBucket - 1) / kBucket) * kBucket;
     for (uint32_t j = zero_from + threadIdx.x; j < range.y; j += kBlendThreads) {
-        float* dst = instance_grad + (size_t)values[j] * kGrad2d;
-#pragma unroll
-        for (int c = 0; c < kGrad2d; ++c) dst[c] = 0.0f;
+        const size_t pos = values[j];
+        float4* dst = reinterpret_cast<float4*>(instance_grad) + 2 * pos;
+        dst[0] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        dst[1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        instance_grad_op[pos] = 0.0f;
     }
     if (end_all <= range.x) return;  // uniform
 
@@ -672,7 +703,12 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
 #pragma unroll
                     for (int r = 0; r < h; ++r) q[r] += q[r + h];
                 }
-                instance_grad[(size_t)s_pos[sb * kBucket + e] * kGrad2d + c] = q[0];
+                const size_t pos = s_pos[sb * kBucket + e];
+                if (c < kGradRecord) {
+                    instance_grad[pos * kGradRecord + c] = q[0];
+                } else {
+                    instance_grad_op[pos] = q[0];
+                }
             }
             __syncthreads();
             }
@@ -680,90 +716,142 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
     }
 }
 
-// grad2d[g] = sum of instance_grad over g's emission positions [offset[g], offset[g+1]), in two
-// kernels with disjoint outputs (both overwrite, so no zero fill):
-//  * runs of at most kLaneRun instances: a workgroup covers 256 consecutive Gaussians, whose
-//    runs are one contiguous range; the range is staged through LDS in instance-aligned pieces
-//    with coalesced loads, and each thread sums its own run from LDS;
-//  * longer runs (only boxes of more than kBigTiles tiles have them, so they are all on the
-//    big-box list): one workgroup per Gaussian, 256 instances per step, then a DPP/LDS tree.
-constexpr uint32_t kLaneRun = kBigTiles;
-constexpr uint32_t kPieceInstances = 448;  // 4032 floats = 15.75 KB of LDS per piece
+// grad2d[g] = sum of the partials over the emission positions [offset[r], offset[r+1]) of g, r its
+// depth rank; every Gaussian's sum is taken in a fixed order, so the result is deterministic.
+//  * runs of at most kLaneRun instances (reduce_instance_grads_kernel): the 64 runs of a wave's
+//    ranks are one contiguous span; the wave stages it through its own LDS piece by piece with
+//    coalesced loads, jumping over long runs, and each lane sums its run in position order;
+//  * longer runs (listed by rank_gather_kernel; in depth order the near, large Gaussians sit
+//    side by side, and the largest cover nearly every tile): each run is cut into at most
+//    kLongChunks chunks of `chunk` positions, one wave sums a chunk (DPP tree) and leaves the
+//    partial in place at the chunk's first position (reduce_long_chunks_kernel), then one thread
+//    per run adds its chunk partials in chunk order (combine_long_runs_kernel).
+constexpr uint32_t kShortPiece = 256;  // instances per LDS piece and wave (9 KB)
+constexpr uint32_t kLongChunks = 16;
+
+__device__ inline void add_record(float acc[kGrad2d], float4 a, float4 b, float op) {
+    acc[0] += a.x;
+    acc[1] += a.y;
+    acc[2] += a.z;
+    acc[3] += a.w;
+    acc[4] += b.x;
+    acc[5] += b.y;
+    acc[6] += b.z;
+    acc[7] += b.w;
+    acc[8] += op;
+}
+
+__device__ inline void add_instance_grad(float acc[kGrad2d], const float* __restrict__ instance_grad,
+                                         const float* __restrict__ instance_grad_op, uint32_t p) {
+    const float4* rec4 = reinterpret_cast<const float4*>(instance_grad) + 2 * (size_t)p;
+    add_record(acc, rec4[0], rec4[1], instance_grad_op[p]);
+}
 
 __global__ __launch_bounds__(256) void reduce_instance_grads_kernel(int64_t n, const uint32_t* __restrict__ offsets,
+                                                                    const uint32_t* __restrict__ rank_gaussian,
                                                                     const float* __restrict__ instance_grad,
+                                                                    const float* __restrict__ instance_grad_op,
                                                                     float* __restrict__ grad2d) {
-    __shared__ float s_piece[kPieceInstances * kGrad2d];
-    const int64_t g0 = (int64_t)blockIdx.x * blockDim.x;
-    const int64_t g = g0 + threadIdx.x;
-    const int64_t g_end = min(g0 + (int64_t)blockDim.x, n);
+    __shared__ float4 s_rec[kWavesPerBlock][2 * kShortPiece];
+    __shared__ float s_op[kWavesPerBlock][kShortPiece];
+    const uint32_t lane = __lane_id(), wave = threadIdx.x / kWave;
+    const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t r_first = r - lane;  // first rank of this wave (waves wholly past n find no work)
+    const bool valid = r < n;
     uint32_t b = 0, e = 0;
-    if (g < n) {
-        b = offsets[g];
-        e = offsets[g + 1];
+    if (valid) {
+        b = offsets[r];
+        e = offsets[r + 1];
     }
-    const bool mine = g < n && e - b <= kLaneRun;
+    const bool mine = valid && e - b <= kLaneRun;
+    const bool has = mine && e > b;
+    const uint32_t span_end = offsets[min(r_first + (int64_t)kWave, n)];
+    const float4* rec4 = reinterpret_cast<const float4*>(instance_grad);
+    float4* sr = s_rec[wave];
+    float* so = s_op[wave];
     float acc[kGrad2d];
 #pragma unroll
     for (int c = 0; c < kGrad2d; ++c) acc[c] = 0.0f;
-    const uint32_t r0 = offsets[g0], r1 = offsets[g_end];
-    for (uint32_t p0 = r0; p0 < r1; p0 += kPieceInstances) {
-        const uint32_t p1 = min(p0 + kPieceInstances, r1);
-        // pieces that lie inside long runs only are skipped (uniform)
-        const bool need = mine && b < p1 && e > p0;
-        if (__syncthreads_or(need ? 1 : 0) == 0) continue;
-        const uint32_t floats = (p1 - p0) * kGrad2d;
-        const float* src = instance_grad + (size_t)p0 * kGrad2d;
-        for (uint32_t i = threadIdx.x; i < floats; i += blockDim.x) s_piece[i] = src[i];
-        __syncthreads();
-        if (need) {
-            const uint32_t lo = max(b, p0), hi = min(e, p1);
-            for (uint32_t p = lo; p < hi; ++p) {
-                const float* v = &s_piece[(p - p0) * kGrad2d];
-#pragma unroll
-                for (int c = 0; c < kGrad2d; ++c) acc[c] += v[c];
-            }
+    for (uint32_t cur = offsets[min(r_first, n)];;) {
+        // the piece starts at the lowest position a short run of the wave still needs
+        const uint32_t p0 = wave_min_u32(has && e > cur ? max(b, cur) : UINT32_MAX);
+        if (p0 == UINT32_MAX) break;  // uniform
+        const uint32_t p1 = min(p0 + kShortPiece, span_end);
+        wave_lds_sync();  // the previous piece has been read
+        for (uint32_t q = lane; q < p1 - p0; q += kWave) {
+            sr[2 * q] = rec4[2 * (size_t)(p0 + q)];
+            sr[2 * q + 1] = rec4[2 * (size_t)(p0 + q) + 1];
+            so[q] = instance_grad_op[p0 + q];
         }
-        __syncthreads();
+        wave_lds_sync();
+        if (has) {
+            const uint32_t lo = max(b, p0), hi = min(e, p1);
+            for (uint32_t p = lo; p < hi; ++p) add_record(acc, sr[2 * (p - p0)], sr[2 * (p - p0) + 1], so[p - p0]);
+        }
+        cur = p1;
     }
     if (mine) {
+        const size_t g = rank_gaussian[r];
 #pragma unroll
         for (int c = 0; c < kGrad2d; ++c) grad2d[g * kGrad2d + c] = acc[c];
     }
 }
 
-__global__ __launch_bounds__(256) void reduce_long_runs_kernel(const uint32_t* __restrict__ big_list,
-                                                               const uint32_t* __restrict__ big_count,
-                                                               const uint32_t* __restrict__ offsets,
-                                                               const float* __restrict__ instance_grad,
-                                                               float* __restrict__ grad2d) {
-    __shared__ float s_wave[kBlendThreads / kWave][kGrad2d];
-    const uint32_t count = *big_count;
-    const uint32_t lane = __lane_id(), wave = threadIdx.x / kWave;
-    for (uint32_t i = blockIdx.x; i < count; i += gridDim.x) {
-        const uint32_t g = big_list[i];
-        const uint32_t b = offsets[g], e = offsets[g + 1];
-        if (e - b <= kLaneRun) continue;  // uniform; summed by reduce_instance_grads_kernel
+// grid (x, kLongChunks): the waves of column y = k sum chunk k of the listed runs (grid-stride
+// over the list) and store the 9 sums in place of the chunk's first partial.
+__global__ __launch_bounds__(256) void reduce_long_chunks_kernel(const uint32_t* __restrict__ long_list,
+                                                                 const uint32_t* __restrict__ offsets, uint32_t chunk,
+                                                                 float* __restrict__ instance_grad,
+                                                                 float* __restrict__ instance_grad_op) {
+    const uint32_t count = long_list[0];
+    const uint32_t lane = __lane_id();
+    const uint32_t waves = gridDim.x * (blockDim.x / kWave);
+    const uint32_t k = blockIdx.y;
+    for (uint32_t i = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave; i < count; i += waves) {
+        const uint32_t r = long_list[1 + i];
+        const uint32_t b = offsets[r], e = offsets[r + 1];
+        const uint32_t cb = b + k * chunk;
+        if (cb >= e) continue;  // uniform
+        const uint32_t ce = min(e, cb + chunk);
         float acc[kGrad2d];
 #pragma unroll
         for (int c = 0; c < kGrad2d; ++c) acc[c] = 0.0f;
-        for (uint32_t p = b + threadIdx.x; p < e; p += blockDim.x) {
-            const float* v = instance_grad + (size_t)p * kGrad2d;
+        for (uint32_t p0 = cb; p0 < ce; p0 += 4 * kWave) {
 #pragma unroll
-            for (int c = 0; c < kGrad2d; ++c) acc[c] += v[c];
+            for (uint32_t u = 0; u < 4; ++u) {
+                const uint32_t p = p0 + u * kWave + lane;
+                if (p < ce) add_instance_grad(acc, instance_grad, instance_grad_op, p);
+            }
         }
 #pragma unroll
         for (int c = 0; c < kGrad2d; ++c) acc[c] = wave_reduce_sum(acc[c]);
+        // every lane's loads of the chunk fed the sums above, so overwriting position cb is safe
         if (lane == 0) {
+            float4* dst = reinterpret_cast<float4*>(instance_grad) + 2 * (size_t)cb;
+            dst[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+            dst[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+            instance_grad_op[cb] = acc[8];
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void combine_long_runs_kernel(const uint32_t* __restrict__ long_list,
+                                                                const uint32_t* __restrict__ offsets,
+                                                                const uint32_t* __restrict__ rank_gaussian,
+                                                                uint32_t chunk, const float* __restrict__ instance_grad,
+                                                                const float* __restrict__ instance_grad_op,
+                                                                float* __restrict__ grad2d) {
+    const uint32_t count = long_list[0];
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < count; i += gridDim.x * blockDim.x) {
+        const uint32_t r = long_list[1 + i];
+        const uint32_t b = offsets[r], e = offsets[r + 1];
+        float acc[kGrad2d];
 #pragma unroll
-            for (int c = 0; c < kGrad2d; ++c) s_wave[wave][c] = acc[c];
-        }
-        __syncthreads();
-        if (threadIdx.x < kGrad2d) {
-            const int c = threadIdx.x;
-            grad2d[(size_t)g * kGrad2d + c] = (s_wave[0][c] + s_wave[1][c]) + (s_wave[2][c] + s_wave[3][c]);
-        }
-        __syncthreads();
+        for (int c = 0; c < kGrad2d; ++c) acc[c] = 0.0f;
+        for (uint32_t p = b; p < e; p += chunk) add_instance_grad(acc, instance_grad, instance_grad_op, p);
+        const size_t g = rank_gaussian[r];
+#pragma unroll
+        for (int c = 0; c < kGrad2d; ++c) grad2d[g * kGrad2d + c] = acc[c];
     }
 }
 

@@ -106,12 +106,12 @@ typedef struct gsx_hip_render_stats {
     int64_t visible_count;   /* Gaussians with at least one tile (-1 until computed) */
     int64_t instance_count;  /* (tile, Gaussian) pairs sorted */
     int32_t tile_count;
-    int32_t sort_passes;
-    /* layout of sorted_keys: tile << key_tile_shift | (bits(depth) - key_depth_base) <<
-     * key_depth_shift | emission position in the low key_payload_bits bits (0: not packed) */
+    int32_t sort_passes;       /* radix passes over the instance keys (tile bits) */
+    int32_t depth_sort_passes; /* radix passes over the per-Gaussian depth keys */
+    /* layout of sorted_keys: tile << key_tile_shift | emission position in the low
+     * key_payload_bits bits; instances are emitted in (depth, index) order of their Gaussians,
+     * so a stable sort on the tile bits yields the gsx per-tile (depth, index) order */
     int32_t key_tile_shift;
-    int32_t key_depth_shift;
-    uint32_t key_depth_base;
     int32_t key_payload_bits;
 } gsx_hip_render_stats;
 
@@ -153,8 +153,9 @@ gsx_hip_status gsx_hip_render_context_get_buffers(const gsx_hip_render_context* 
  * sets; each forward (and the following backward) records one set on its launch stream, so a
  * timed loop pays no synchronisation. get_timings synchronises on the recorded events and writes
  * the per-stage average over the recorded sets, in milliseconds, in this order: preprocess,
- * scan (including the instance-count readback), emit, sort, ranges, blend_forward,
- * blend_backward, instance_reduce, projection_backward. set_timing(0) disables timing. */
+ * depth_order (depth-key sort, tile counts in depth order, their scan and the instance-count
+ * readback), emit, sort, ranges, blend_forward, blend_backward, instance_reduce,
+ * projection_backward. set_timing(0) disables timing. */
 enum { GSX_HIP_RENDER_STAGE_COUNT = 9 };
 gsx_hip_status gsx_hip_render_context_set_timing(gsx_hip_render_context* context, int32_t capacity);
 gsx_hip_status gsx_hip_render_context_get_timings(gsx_hip_render_context* context, float* out_ms, int32_t capacity,

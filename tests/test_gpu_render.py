@@ -82,20 +82,26 @@ def test_sorted_keys_and_ranges_bit_exact(oracle, name):
     inst_g = np.empty(st.instance_count, np.uint32)
     if st.instance_count:
         lib.gsx_hip_memcpy_dtoh(inst_g.ctypes.data_as(ctypes.c_void_p), buf.instance_gaussian, inst_g.nbytes)
-    # sorted keys: tile << key_tile_shift | (bits(depth) - key_depth_base) << key_depth_shift |
-    # payload; the oracle's keys are tile << 32 | bits(depth)
+    # sorted keys: tile << key_tile_shift | emission position (key_payload_bits bits); the
+    # oracle's keys are tile << 32 | bits(depth) with the Gaussian index as value
+    assert st.key_tile_shift == st.key_payload_bits
     tile = keys >> np.uint64(st.key_tile_shift) if st.key_tile_shift < 64 else np.zeros_like(keys)
-    dmask = np.uint64((1 << (st.key_tile_shift - st.key_depth_shift)) - 1)
-    depth = ((keys >> np.uint64(st.key_depth_shift)) & dmask) + np.uint64(st.key_depth_base)
-    assert np.array_equal((tile << np.uint64(32)) | depth, keys_ref)
-    if st.key_payload_bits > 0:
-        assert np.array_equal(keys & np.uint64((1 << st.key_payload_bits) - 1), vals.astype(np.uint64))
+    assert np.array_equal(keys & np.uint64((1 << st.key_payload_bits) - 1), vals.astype(np.uint64))
     assert np.array_equal(inst_g[vals], vals_ref)  # sorted values are emission positions
-    # emission positions of one Gaussian are contiguous and in row-major tile order
-    assert np.all(np.diff(inst_g.astype(np.int64)) >= 0)
+    depth_of = np.zeros(w.scene.count, np.uint64)
+    depth_of[vals_ref] = keys_ref & np.uint64(0xFFFFFFFF)
+    assert np.array_equal((tile << np.uint64(32)) | depth_of[inst_g[vals]], keys_ref)
+    # emission order: each Gaussian's positions are one contiguous run, runs in (depth, index)
+    # order of their Gaussians
+    if st.instance_count:
+        starts = np.flatnonzero(np.r_[True, inst_g[1:] != inst_g[:-1]])
+        run_g = inst_g[starts].astype(np.int64)
+        assert len(np.unique(run_g)) == len(run_g)
+        order = np.lexsort((run_g, depth_of[run_g]))
+        assert np.array_equal(order, np.arange(len(run_g)))
     assert np.array_equal(ranges, oracle.tile_ranges(keys_ref, st.tile_count))
-    # invariants: keys non-decreasing in their sort bits, ranges partition [0, I)
-    assert np.all((keys[1:] >> np.uint64(st.key_depth_shift)) >= (keys[:-1] >> np.uint64(st.key_depth_shift)))
+    # invariants: tiles non-decreasing, ranges partition [0, I)
+    assert np.all(tile[1:] >= tile[:-1])
     nonempty = ranges[ranges[:, 1] > ranges[:, 0]]
     assert int((nonempty[:, 1] - nonempty[:, 0]).sum()) == st.instance_count
 
