@@ -106,7 +106,7 @@ struct DeviceBuffer {
 };
 
 // Workgroups of the big-box passes (grid-stride over the list of big boxes).
-constexpr unsigned kBigBlocks = 1024;
+constexpr unsigned kBigBlocks = 512;
 // Workgroups per chunk column of reduce_long_chunks_kernel (4 waves each, grid-stride over the
 // list of long runs), and of combine_long_runs_kernel.
 constexpr unsigned kLongRunBlocks = 512;
@@ -173,7 +173,7 @@ int bits_for(uint32_t v) {
 struct gsx_hip_render_context {
     DeviceBuffer rec, cov_coef, ckpt, inst_gauss, inst_grad, tile_count, big_list, offsets, scan_temp, keys, vals,
         keys_alt, sort_temp, ranges, sorted_g, final_t, last, grad2d, depth_keys, depth_keys_alt, rank_g, rank_count,
-        g_rank, long_list;
+        g_rank, long_list, counters, big_chunk_counts;
     uint32_t* host_count = nullptr;  // pinned
     CameraParams cam{};
     gsx_hip_gaussians gs{};
@@ -351,7 +351,7 @@ gsx_hip_status gsx_hip_render_context_destroy(gsx_hip_render_context* ctx) {
                            &ctx->vals,       &ctx->keys_alt, &ctx->sort_temp,  &ctx->ranges,
                            &ctx->sorted_g,   &ctx->final_t,  &ctx->last,      &ctx->grad2d,     &ctx->depth_keys,
                            &ctx->depth_keys_alt, &ctx->rank_g, &ctx->rank_count, &ctx->g_rank,
-                           &ctx->long_list};
+                           &ctx->long_list, &ctx->counters, &ctx->big_chunk_counts};
     for (DeviceBuffer* b : all) b->release();
     if (ctx->host_count != nullptr) (void)hipHostFree(ctx->host_count);
     release_events(ctx);
@@ -459,8 +459,10 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     GSX_TRY(ctx->rec.reserve(n1 * 3 * sizeof(float4), "rec"));
     if (train) GSX_TRY(ctx->cov_coef.reserve(n1 * 2 * sizeof(float4), "cov_coef"));
     GSX_TRY(ctx->tile_count.reserve(n1 * sizeof(uint32_t), "tile_count"));
-    // [0] = number of big boxes, [1..n] = their Gaussians
-    GSX_TRY(ctx->big_list.reserve((size_t)(n + 1) * sizeof(uint32_t), "big_list"));
+    // list counters: [0] visible Gaussians (depth keys), [1] big boxes, [2] long instance runs
+    GSX_TRY(ctx->counters.reserve(4 * sizeof(uint32_t), "counters"));
+    GSX_TRY(ctx->big_list.reserve(n1 * sizeof(uint32_t), "big_list"));
+    GSX_TRY(ctx->big_chunk_counts.reserve(n1 * kBigChunks * sizeof(uint32_t), "big_chunk_counts"));
     GSX_TRY(ctx->offsets.reserve((size_t)(n + 1) * sizeof(uint32_t), "offsets"));
     GSX_TRY(ctx->scan_temp.reserve(gsx_hip_scan_temp_bytes(n), "scan_temp"));
     GSX_TRY(ctx->depth_keys.reserve(n1 * sizeof(uint64_t), "depth_keys"));
@@ -468,19 +470,24 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     GSX_TRY(ctx->rank_g.reserve(n1 * sizeof(uint32_t), "rank_gaussian"));
     GSX_TRY(ctx->rank_count.reserve(n1 * sizeof(uint32_t), "rank_count"));
     GSX_TRY(ctx->g_rank.reserve(n1 * sizeof(uint32_t), "gaussian_rank"));
-    // [0] = number of ranks with long instance runs, [1..n] = those ranks
-    GSX_TRY(ctx->long_list.reserve((size_t)(n + 1) * sizeof(uint32_t), "long_list"));
+    GSX_TRY(ctx->long_list.reserve(n1 * sizeof(uint32_t), "long_list"));
     GSX_TRY(ctx->sort_temp.reserve(gsx_hip_radix_sort_temp_bytes(n), "sort_temp"));
     GSX_TRY(ctx->ranges.reserve((size_t)tiles * sizeof(uint2), "ranges"));
     GSX_TRY(ctx->final_t.reserve((size_t)pixels * sizeof(float), "final_t"));
     GSX_TRY(ctx->last.reserve((size_t)pixels * sizeof(uint32_t), "last"));
+    uint32_t* counters = ctx->counters.as<uint32_t>();
+    // big boxes: chunks of at least 1024 tiles, at most kBigChunks per box (a box has at most
+    // `tiles` tiles)
+    const uint32_t big_chunk =
+        std::max<uint32_t>(1024u, ((uint32_t)(tiles + (int)kBigChunks - 1) / kBigChunks + 255u) / 256u * 256u);
+    const unsigned big_chunks = (unsigned)std::max<uint32_t>(1u, ((uint32_t)tiles + big_chunk - 1) / big_chunk);
 
-    // depth keys: (bits(depth) - bits(near)) << index_bits | index, invisible ones after every
-    // visible depth (see KeyLayout); at most 31 + 32 bits
+    // depth keys of the visible Gaussians: (bits(depth) - bits(near)) << index_bits | index (see
+    // KeyLayout), at most 31 + 32 bits, so never the all-ones key that marks invisible ones
     const uint32_t near_bits = gsx_f32_bits(cam.near_plane), far_bits = gsx_f32_bits(cam.far_plane);
     const uint32_t depth_max = far_bits - near_bits;
     const int index_bits = std::max(1, bits_for((uint32_t)(n > 0 ? n - 1 : 0)));
-    const int depth_bits = bits_for(depth_max + 1u);
+    const int depth_bits = bits_for(depth_max);
     ctx->depth_sort_passes = (depth_bits + 7) / 8;
 
     if (ctx->timing) {
@@ -490,21 +497,19 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     }
     GSX_TRY(record(ctx, 0, stream));
     if (n > 0) {
-        hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(64), 0, stream, ctx->big_list.as<uint32_t>(), (int64_t)1,
-                           0u);
+        hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(64), 0, stream, counters, (int64_t)4, 0u);
         hipLaunchKernelGGL(preprocess_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, n, gaussians->mean3d,
                            gaussians->rotation, gaussians->logscale, gaussians->opacity, gaussians->sh0,
                            gaussians->sh1, gaussians->sh2, gaussians->sh3, (int)gaussians->sh_degree, cam,
                            ctx->rec.as<float4>(), train ? ctx->cov_coef.as<float4>() : nullptr,
                            ctx->tile_count.as<uint32_t>(), train ? visible_counter : nullptr,
-                           ctx->big_list.as<uint32_t>() + 1, ctx->big_list.as<uint32_t>(),
-                           ctx->depth_keys.as<uint64_t>(), near_bits, depth_max, index_bits,
-                           ctx->long_list.as<uint32_t>());
+                           ctx->big_list.as<uint32_t>(), counters + 1, ctx->depth_keys.as<uint64_t>(), near_bits,
+                           depth_max, index_bits);
         GSX_HIP_TRY(hipGetLastError(), "preprocess_kernel");
-        hipLaunchKernelGGL(big_tiles_kernel<false>, dim3(kBigBlocks), dim3(256), 0, stream,
-                           ctx->big_list.as<uint32_t>() + 1, ctx->big_list.as<uint32_t>(), ctx->rec.as<float4>(),
-                           cam.tiles_x, KeyLayout{}, ctx->tile_count.as<uint32_t>(), nullptr, nullptr, nullptr,
-                           nullptr);
+        hipLaunchKernelGGL(big_tiles_kernel<false>, dim3(kBigBlocks, big_chunks), dim3(256), 0, stream,
+                           ctx->big_list.as<uint32_t>(), counters + 1, ctx->rec.as<float4>(), cam.tiles_x,
+                           KeyLayout{}, big_chunk, ctx->tile_count.as<uint32_t>(),
+                           ctx->big_chunk_counts.as<uint32_t>(), nullptr, nullptr, nullptr, nullptr);
         GSX_HIP_TRY(hipGetLastError(), "big_tiles_kernel<count>");
     }
     GSX_TRY(record(ctx, 1, stream));
@@ -513,13 +518,14 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     if (n > 0) {
         int depth_in_alt = 0;
         const int end_bit = std::min(64, index_bits + ctx->depth_sort_passes * 8);
-        GSX_TRY(gsx_hip_radix_sort_keys_u64(ctx->depth_keys.as<uint64_t>(), ctx->depth_keys_alt.as<uint64_t>(), n,
-                                            index_bits, end_bit, ctx->sort_temp.ptr, &depth_in_alt, stream));
+        GSX_TRY(radix_sort_keys_u64_compacting(ctx->depth_keys.as<uint64_t>(), ctx->depth_keys_alt.as<uint64_t>(), n,
+                                               counters, index_bits, end_bit, ctx->sort_temp.ptr, &depth_in_alt,
+                                               stream));
         if (depth_in_alt) sorted_depth = ctx->depth_keys_alt.as<uint64_t>();
-        hipLaunchKernelGGL(rank_gather_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, n, sorted_depth,
-                           (uint64_t)((1ull << index_bits) - 1ull), ctx->tile_count.as<uint32_t>(),
+        hipLaunchKernelGGL(rank_gather_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, n, counters,
+                           sorted_depth, (uint64_t)((1ull << index_bits) - 1ull), ctx->tile_count.as<uint32_t>(),
                            ctx->rank_g.as<uint32_t>(), ctx->rank_count.as<uint32_t>(), ctx->g_rank.as<uint32_t>(),
-                           ctx->long_list.as<uint32_t>());
+                           ctx->long_list.as<uint32_t>(), counters + 2);
         GSX_HIP_TRY(hipGetLastError(), "rank_gather_kernel");
     }
     GSX_TRY(gsx_hip_scan_exclusive_u32(ctx->rank_count.as<uint32_t>(), ctx->offsets.as<uint32_t>(), n,
@@ -554,10 +560,10 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
                            ctx->rank_g.as<uint32_t>(), ctx->rank_count.as<uint32_t>(), ctx->offsets.as<uint32_t>(),
                            cam.tiles_x, layout, ctx->keys.as<uint64_t>(), ctx->inst_gauss.as<uint32_t>());
         GSX_HIP_TRY(hipGetLastError(), "emit_keys_kernel");
-        hipLaunchKernelGGL(big_tiles_kernel<true>, dim3(kBigBlocks), dim3(256), 0, stream,
-                           ctx->big_list.as<uint32_t>() + 1, ctx->big_list.as<uint32_t>(), ctx->rec.as<float4>(),
-                           cam.tiles_x, layout, nullptr, ctx->offsets.as<uint32_t>(), ctx->g_rank.as<uint32_t>(),
-                           ctx->keys.as<uint64_t>(), ctx->inst_gauss.as<uint32_t>());
+        hipLaunchKernelGGL(big_tiles_kernel<true>, dim3(kBigBlocks, big_chunks), dim3(256), 0, stream,
+                           ctx->big_list.as<uint32_t>(), counters + 1, ctx->rec.as<float4>(), cam.tiles_x, layout,
+                           big_chunk, nullptr, ctx->big_chunk_counts.as<uint32_t>(), ctx->offsets.as<uint32_t>(),
+                           ctx->g_rank.as<uint32_t>(), ctx->keys.as<uint64_t>(), ctx->inst_gauss.as<uint32_t>());
         GSX_HIP_TRY(hipGetLastError(), "big_tiles_kernel<emit>");
     }
     GSX_TRY(record(ctx, 3, stream));
@@ -620,6 +626,7 @@ gsx_hip_status gsx_hip_render_backward(gsx_hip_render_context* ctx, const float*
     const CameraParams& cam = ctx->cam;
     const int32_t tiles = cam.tiles_x * cam.tiles_y;
     const uint32_t* svals = ctx->sorted_vals;
+    const uint32_t* counters = ctx->counters.as<uint32_t>();  // as the forward left them
     // per-instance partials: [I][8] records, then the [I] opacity terms
     float* inst_grad_op = ctx->inst_grad.as<float>() + (size_t)ctx->instance_count * 8;
     GSX_TRY(record(ctx, 7, stream));
@@ -631,7 +638,7 @@ gsx_hip_status gsx_hip_render_backward(gsx_hip_render_context* ctx, const float*
     GSX_HIP_TRY(hipGetLastError(), "blend_backward_kernel");
     GSX_TRY(record(ctx, 8, stream));
     if (n > 0) {
-        hipLaunchKernelGGL(reduce_instance_grads_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, n,
+        hipLaunchKernelGGL(reduce_instance_grads_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, n, counters,
                            ctx->offsets.as<uint32_t>(), ctx->rank_g.as<uint32_t>(), ctx->inst_grad.as<float>(),
                            inst_grad_op, ctx->grad2d.as<float>());
         GSX_HIP_TRY(hipGetLastError(), "reduce_instance_grads_kernel");
@@ -639,11 +646,12 @@ gsx_hip_status gsx_hip_render_backward(gsx_hip_render_context* ctx, const float*
         const uint32_t chunk = std::max<uint32_t>(
             kWave, ((uint32_t)(tiles + (int)kLongChunks - 1) / kLongChunks + kWave - 1) / kWave * kWave);
         hipLaunchKernelGGL(reduce_long_chunks_kernel, dim3(kLongRunBlocks, kLongChunks), dim3(256), 0, stream,
-                           ctx->long_list.as<uint32_t>(), ctx->offsets.as<uint32_t>(), chunk,
+                           ctx->long_list.as<uint32_t>(), counters + 2, ctx->offsets.as<uint32_t>(), chunk,
                            ctx->inst_grad.as<float>(), inst_grad_op);
         GSX_HIP_TRY(hipGetLastError(), "reduce_long_chunks_kernel");
         hipLaunchKernelGGL(combine_long_runs_kernel, dim3(kLongRunBlocks), dim3(256), 0, stream,
-                           ctx->long_list.as<uint32_t>(), ctx->offsets.as<uint32_t>(), ctx->rank_g.as<uint32_t>(),
+                           ctx->long_list.as<uint32_t>(), counters + 2, ctx->offsets.as<uint32_t>(),
+                           ctx->rank_g.as<uint32_t>(),
                            chunk, ctx->inst_grad.as<float>(), inst_grad_op, ctx->grad2d.as<float>());
         GSX_HIP_TRY(hipGetLastError(), "combine_long_runs_kernel");
     }

@@ -11,6 +11,7 @@
 
 #include "gsx_math.h"
 #include "tile_cull.h"
+#include "../../include/gsx_hip.h"
 
 namespace gsx_amd {
 
@@ -383,5 +384,14 @@ __device__ inline float div_rn_normal(float n, float d) {
     const float r = __builtin_fmaf(-d, q, n);
     return __builtin_fmaf(r, y, q);
 }
+
+// Keys-only stable radix sort (sort.hip) that also drops every key equal to ~0: the first pass
+// reads all n keys and moves the others, in input order within each digit, to the front, and
+// stores their number in *n_live (which must be zero beforehand); the later passes sort that
+// many (grids are sized for n, so no host round trip is needed). Output positions >= *n_live
+// are not written.
+gsx_hip_status radix_sort_keys_u64_compacting(uint64_t* keys, uint64_t* keys_alt, int64_t n, uint32_t* n_live,
+                                              int begin_bit, int end_bit, void* temp, int* out_in_alt,
+                                              hipStream_t stream);
 
 }  // namespace gsx_amd

@@ -169,8 +169,7 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
     const float* __restrict__ sh1, const float* __restrict__ sh2, const float* __restrict__ sh3, int sh_degree,
     CameraParams cam, float4* __restrict__ rec, float4* __restrict__ cov_coef, uint32_t* __restrict__ tile_count,
     float* __restrict__ visible_counter, uint32_t* __restrict__ big_list, uint32_t* __restrict__ big_count,
-    uint64_t* __restrict__ depth_keys, uint32_t depth_base, uint32_t depth_max, int index_bits,
-    uint32_t* __restrict__ long_count) {
+    uint64_t* __restrict__ depth_keys, uint32_t depth_base, uint32_t depth_max, int index_bits) {
     __shared__ WaveBoxes s_boxes[kWavesPerBlock];
     WaveBoxes& wb = s_boxes[threadIdx.x / kWave];
     const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -206,42 +205,50 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
             }
         }
     }
-    if (g == 0) *long_count = 0;  // for rank_gather_kernel, which runs after this kernel
+    // depth key of every Gaussian (~0 for invisible ones, which the depth sort drops)
     if (g < n) {
-        uint32_t rel = depth_max + 1u;  // invisible: after every visible depth
+        uint64_t key = ~0ull;
         if (visible) {
-            rel = __float_as_uint(r2.w) - depth_base;
+            uint32_t rel = __float_as_uint(r2.w) - depth_base;
             if (rel > depth_max) rel = depth_max;  // only for non-finite depths
+            key = ((uint64_t)rel << index_bits) | (uint64_t)g;
         }
-        depth_keys[g] = ((uint64_t)rel << index_bits) | (uint64_t)g;
+        depth_keys[g] = key;
     }
     const bool big = visible && box_tiles(r2) > kBigTiles;
     if (big) big_list[atomicAdd(big_count, 1u)] = (uint32_t)g;  // counted by big_tiles_kernel
     const uint32_t total = stage_box(wb, visible && !big, r0, r1, r2, (uint32_t)g, 0u);
     walk_wave_tiles<false>(wb, total, cam.tiles_x, KeyLayout{}, nullptr, nullptr);
-    if (g < n && !big) tile_count[g] = wb.kept[__lane_id()];
+    if (g < n) tile_count[g] = big ? 0u : wb.kept[__lane_id()];  // big boxes: summed by big_tiles_kernel
 }
 
-// Instance runs longer than this are summed by a wave each in the backward (see
-// reduce_long_runs_kernel), shorter ones by one thread each.
+// Instance runs longer than this are summed in chunks by whole waves in the backward (see
+// reduce_long_chunks_kernel), shorter ones by one lane each.
 constexpr uint32_t kLaneRun = 32;
 
-// After the depth sort: the Gaussian of every depth rank, its kept-tile count, its rank, and the
-// list of ranks whose count exceeds kLaneRun (long_list[0] = length, zeroed by preprocess).
-__global__ __launch_bounds__(256) void rank_gather_kernel(int64_t n, const uint64_t* __restrict__ sorted_depth_keys,
+// After the depth sort of the V visible Gaussians (V = *depth_count): the Gaussian of every
+// depth rank, its kept-tile count, its rank, and the list of ranks whose count exceeds kLaneRun.
+// Ranks V..n-1 get count 0 (so the scan over n covers them) and no Gaussian.
+__global__ __launch_bounds__(256) void rank_gather_kernel(int64_t n, const uint32_t* __restrict__ depth_count,
+                                                          const uint64_t* __restrict__ sorted_depth_keys,
                                                           uint64_t index_mask, const uint32_t* __restrict__ tile_count,
                                                           uint32_t* __restrict__ rank_gaussian,
                                                           uint32_t* __restrict__ rank_count,
                                                           uint32_t* __restrict__ gaussian_rank,
-                                                          uint32_t* __restrict__ long_list) {
+                                                          uint32_t* __restrict__ long_list,
+                                                          uint32_t* __restrict__ long_count) {
     const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (r >= n) return;
+    if (r >= (int64_t)*depth_count) {
+        rank_count[r] = 0;
+        return;
+    }
     const uint32_t g = (uint32_t)(sorted_depth_keys[r] & index_mask);
     const uint32_t c = tile_count[g];
     rank_gaussian[r] = g;
     rank_count[r] = c;
     gaussian_rank[g] = (uint32_t)r;
-    if (c > kLaneRun) long_list[1 + atomicAdd(long_list, 1u)] = (uint32_t)r;
+    if (c > kLaneRun) long_list[atomicAdd(long_count, 1u)] = (uint32_t)r;
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -278,15 +285,22 @@ __global__ __launch_bounds__(256) void emit_keys_kernel(int64_t n, const float4*
     walk_wave_tiles<true>(wb, total, tiles_x, layout, keys, instance_gaussian);
 }
 
-// Big boxes: one workgroup per Gaussian of big_list (grid-stride over the list), 256 tiles per
-// step in row-major order. kEmit = false writes tile_count[g]; kEmit = true writes the kept
-// instances at offsets[rank of g] + their rank among the kept tiles (per-wave ballots and a
-// 4-wave prefix).
+// Big boxes: the row-major tile range of each box on big_list is cut into chunks of `chunk`
+// tiles (at most kBigChunks per box); workgroup (x, c) takes chunk c of the boxes x, x + gridDim.x,
+// ... and walks it 256 tiles per step. kEmit = false stores the chunk's kept-tile count in
+// chunk_counts[i][c] and adds it to tile_count[g] (zeroed by preprocess); kEmit = true writes
+// the chunk's kept instances at offsets[rank of g] + the counts of the box's earlier chunks +
+// their rank within the chunk (per-wave ballots and a 4-wave prefix), i.e. in the same
+// row-major order as a single walk.
+constexpr uint32_t kBigChunks = 16;
+
 template <bool kEmit>
 __global__ __launch_bounds__(256) void big_tiles_kernel(const uint32_t* __restrict__ big_list,
                                                         const uint32_t* __restrict__ big_count,
                                                         const float4* __restrict__ rec, int32_t tiles_x,
-                                                        KeyLayout layout, uint32_t* __restrict__ tile_count,
+                                                        KeyLayout layout, uint32_t chunk,
+                                                        uint32_t* __restrict__ tile_count,
+                                                        uint32_t* __restrict__ chunk_counts,
                                                         const uint32_t* __restrict__ offsets,
                                                         const uint32_t* __restrict__ gaussian_rank,
                                                         uint64_t* __restrict__ keys,
@@ -294,6 +308,7 @@ __global__ __launch_bounds__(256) void big_tiles_kernel(const uint32_t* __restri
     __shared__ uint32_t s_wave[kWavesPerBlock];
     const uint32_t count = *big_count;
     const uint32_t lane = __lane_id(), wave = threadIdx.x / kWave;
+    const uint32_t c = blockIdx.y;
     for (uint32_t i = blockIdx.x; i < count; i += gridDim.x) {
         const uint32_t g = big_list[i];
         const float4 r0 = rec[3 * (size_t)g + 0], r1 = rec[3 * (size_t)g + 1], r2 = rec[3 * (size_t)g + 2];
@@ -302,15 +317,22 @@ __global__ __launch_bounds__(256) void big_tiles_kernel(const uint32_t* __restri
         const uint32_t tx0 = (uint32_t)x0 / kTile, ty0 = (uint32_t)y0 / kTile;
         const uint32_t wx = (uint32_t)x1 / kTile - tx0 + 1;
         const uint32_t total = wx * ((uint32_t)y1 / kTile - ty0 + 1);
+        const uint32_t t0 = c * chunk;
+        if (t0 >= total) continue;  // uniform: the box has fewer chunks
+        const uint32_t t1 = min(total, t0 + chunk);
         const gsx_tile_conic con = gsx_tile_conic_make(r0.x, r0.y, r0.z, r0.w * 0.5f, r1.x, r1.y);
         const float rwx = 1.0f / (float)wx;
-        const uint32_t o = kEmit ? offsets[gaussian_rank[g]] : 0u;
+        uint32_t o = 0;
+        if (kEmit) {
+            o = offsets[gaussian_rank[g]];
+            for (uint32_t cc = 0; cc < c; ++cc) o += chunk_counts[(size_t)i * kBigChunks + cc];
+        }
         uint32_t running = 0;
-        for (uint32_t base = 0; base < total; base += blockDim.x) {
+        for (uint32_t base = t0; base < t1; base += blockDim.x) {
             const uint32_t k = base + threadIdx.x;
             bool keep = false;
             uint32_t tile = 0;
-            if (k < total) {
+            if (k < t1) {
                 const uint32_t row = div_small(k, wx, rwx);
                 const uint32_t ty = ty0 + row, tx = tx0 + (k - row * wx);
                 tile = ty * (uint32_t)tiles_x + tx;
@@ -334,7 +356,10 @@ __global__ __launch_bounds__(256) void big_tiles_kernel(const uint32_t* __restri
             running += step_total;
             __syncthreads();
         }
-        if (!kEmit && threadIdx.x == 0) tile_count[g] = running;
+        if (!kEmit && threadIdx.x == 0) {
+            chunk_counts[(size_t)i * kBigChunks + c] = running;
+            if (running > 0) atomicAdd(&tile_count[g], running);
+        }
     }
 }
 
@@ -747,7 +772,8 @@ __device__ inline void add_instance_grad(float acc[kGrad2d], const float* __rest
     add_record(acc, rec4[0], rec4[1], instance_grad_op[p]);
 }
 
-__global__ __launch_bounds__(256) void reduce_instance_grads_kernel(int64_t n, const uint32_t* __restrict__ offsets,
+__global__ __launch_bounds__(256) void reduce_instance_grads_kernel(int64_t n, const uint32_t* __restrict__ depth_count,
+                                                                    const uint32_t* __restrict__ offsets,
                                                                     const uint32_t* __restrict__ rank_gaussian,
                                                                     const float* __restrict__ instance_grad,
                                                                     const float* __restrict__ instance_grad_op,
@@ -755,6 +781,7 @@ __global__ __launch_bounds__(256) void reduce_instance_grads_kernel(int64_t n, c
     __shared__ float4 s_rec[kWavesPerBlock][2 * kShortPiece];
     __shared__ float s_op[kWavesPerBlock][kShortPiece];
     const uint32_t lane = __lane_id(), wave = threadIdx.x / kWave;
+    n = min(n, (int64_t)*depth_count);  // ranks of visible Gaussians
     const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t r_first = r - lane;  // first rank of this wave (waves wholly past n find no work)
     const bool valid = r < n;
@@ -800,15 +827,16 @@ __global__ __launch_bounds__(256) void reduce_instance_grads_kernel(int64_t n, c
 // grid (x, kLongChunks): the waves of column y = k sum chunk k of the listed runs (grid-stride
 // over the list) and store the 9 sums in place of the chunk's first partial.
 __global__ __launch_bounds__(256) void reduce_long_chunks_kernel(const uint32_t* __restrict__ long_list,
+                                                                 const uint32_t* __restrict__ long_count,
                                                                  const uint32_t* __restrict__ offsets, uint32_t chunk,
                                                                  float* __restrict__ instance_grad,
                                                                  float* __restrict__ instance_grad_op) {
-    const uint32_t count = long_list[0];
+    const uint32_t count = *long_count;
     const uint32_t lane = __lane_id();
     const uint32_t waves = gridDim.x * (blockDim.x / kWave);
     const uint32_t k = blockIdx.y;
     for (uint32_t i = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave; i < count; i += waves) {
-        const uint32_t r = long_list[1 + i];
+        const uint32_t r = long_list[i];
         const uint32_t b = offsets[r], e = offsets[r + 1];
         const uint32_t cb = b + k * chunk;
         if (cb >= e) continue;  // uniform
@@ -836,14 +864,15 @@ __global__ __launch_bounds__(256) void reduce_long_chunks_kernel(const uint32_t*
 }
 
 __global__ __launch_bounds__(256) void combine_long_runs_kernel(const uint32_t* __restrict__ long_list,
+                                                                const uint32_t* __restrict__ long_count,
                                                                 const uint32_t* __restrict__ offsets,
                                                                 const uint32_t* __restrict__ rank_gaussian,
                                                                 uint32_t chunk, const float* __restrict__ instance_grad,
                                                                 const float* __restrict__ instance_grad_op,
                                                                 float* __restrict__ grad2d) {
-    const uint32_t count = long_list[0];
+    const uint32_t count = *long_count;
     for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < count; i += gridDim.x * blockDim.x) {
-        const uint32_t r = long_list[1 + i];
+        const uint32_t r = long_list[i];
         const uint32_t b = offsets[r], e = offsets[r + 1];
         float acc[kGrad2d];
 #pragma unroll

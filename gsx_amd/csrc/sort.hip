@@ -132,10 +132,17 @@ constexpr int kWaveRounds = kWaveKeys / kWave;                // 16
 
 __device__ inline uint32_t digit_of(uint64_t key, int shift) { return (uint32_t)(key >> shift) & (kRadix - 1); }
 
+constexpr uint64_t kSentinelKey = ~0ull;  // dropped by a pass with drop_sentinel set
+
+// n_dev (may be null): live key count, n = min(n, *n_dev); chunks past it count nothing.
+// drop_sentinel: keys equal to kSentinelKey are left out (they vanish from the output).
 __global__ __launch_bounds__(kSortThreads) void radix_upsweep_kernel(const uint64_t* __restrict__ keys, int64_t n,
-                                                                     int shift, int64_t num_chunks,
+                                                                     const uint32_t* __restrict__ n_dev,
+                                                                     bool drop_sentinel, int shift,
+                                                                     int64_t num_chunks,
                                                                      uint32_t* __restrict__ hist) {
     __shared__ uint32_t s_hist[kChunkWaves][kRadix];
+    if (n_dev != nullptr) n = min(n, (int64_t)*n_dev);
     const int wave = threadIdx.x / kWave;
 #pragma unroll
     for (int w = 0; w < kChunkWaves; ++w) s_hist[w][threadIdx.x] = 0;
@@ -144,7 +151,10 @@ __global__ __launch_bounds__(kSortThreads) void radix_upsweep_kernel(const uint6
 #pragma unroll 4
     for (int r = 0; r < kSortRounds; ++r) {
         const int64_t i = base + (int64_t)r * kSortThreads + threadIdx.x;
-        if (i < n) atomicAdd(&s_hist[wave][digit_of(keys[i], shift)], 1u);
+        if (i < n) {
+            const uint64_t k = keys[i];
+            if (!drop_sentinel || k != kSentinelKey) atomicAdd(&s_hist[wave][digit_of(k, shift)], 1u);
+        }
     }
     __syncthreads();
     const uint32_t c = s_hist[0][threadIdx.x] + s_hist[1][threadIdx.x] + s_hist[2][threadIdx.x] + s_hist[3][threadIdx.x];
@@ -152,11 +162,12 @@ __global__ __launch_bounds__(kSortThreads) void radix_upsweep_kernel(const uint6
 }
 
 // Workgroup d: exclusive scan of hist[d][0..num_chunks) into offsets[d][..], row total into
-// totals[d].
+// totals[d]; with key_count non-null (zero beforehand) the row totals are also added to it.
 __global__ __launch_bounds__(kSortThreads) void radix_rowscan_kernel(const uint32_t* __restrict__ hist,
                                                                      int64_t num_chunks,
                                                                      uint32_t* __restrict__ offsets,
-                                                                     uint32_t* __restrict__ totals) {
+                                                                     uint32_t* __restrict__ totals,
+                                                                     uint32_t* __restrict__ key_count) {
     __shared__ uint32_t s_wave[kSortThreads / kWave];
     const uint32_t* row = hist + (int64_t)blockIdx.x * num_chunks;
     uint32_t* out = offsets + (int64_t)blockIdx.x * num_chunks;
@@ -180,7 +191,10 @@ __global__ __launch_bounds__(kSortThreads) void radix_rowscan_kernel(const uint3
         }
         carry += total;
     }
-    if (threadIdx.x == 0) totals[blockIdx.x] = carry;
+    if (threadIdx.x == 0) {
+        totals[blockIdx.x] = carry;
+        if (key_count != nullptr && carry > 0) atomicAdd(key_count, carry);
+    }
 }
 
 // The downsweep runs 512 threads (8 waves of 512 keys, 8 rounds each): the serial ranking chain
@@ -217,18 +231,22 @@ __device__ inline uint32_t digit_exclusive_scan(uint32_t v, uint32_t* s_wave, ui
 
 template <bool kPairs>
 __global__ __launch_bounds__(kDownThreads) void radix_downsweep_kernel(
-    const uint64_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, int64_t n, int shift,
-    int64_t num_chunks, const uint32_t* __restrict__ offsets, const uint32_t* __restrict__ totals,
-    uint64_t* __restrict__ keys_out, uint32_t* __restrict__ vals_out) {
+    const uint64_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, int64_t n,
+    const uint32_t* __restrict__ n_dev, bool drop_sentinel, int shift, int64_t num_chunks,
+    const uint32_t* __restrict__ offsets, const uint32_t* __restrict__ totals, uint64_t* __restrict__ keys_out,
+    uint32_t* __restrict__ vals_out) {
     __shared__ uint64_t s_keys[kSortChunk];
     __shared__ uint32_t s_vals[kPairs ? kSortChunk : 1];
     __shared__ uint32_t s_cnt[kDownWaves][kRadix];  // wave-private counters, then wave starts
     __shared__ uint32_t s_local[kRadix];            // start of each digit in the reordered chunk
     __shared__ uint32_t s_global[kRadix];           // output position of that start
     __shared__ uint32_t s_wave[kDownWaves];
+    __shared__ uint32_t s_kept;                     // keys of the chunk that are moved
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
     const int64_t base = (int64_t)blockIdx.x * kSortChunk;
+    if (n_dev != nullptr) n = min(n, (int64_t)*n_dev);
+    if (base >= n) return;  // uniform: a chunk past the live count has nothing to move
     const int chunk_count = (int)min((int64_t)kSortChunk, n - base);
     for (int i = threadIdx.x; i < kDownWaves * kRadix; i += kDownThreads) (&s_cnt[0][0])[i] = 0;
     __syncthreads();
@@ -248,7 +266,7 @@ __global__ __launch_bounds__(kDownThreads) void radix_downsweep_kernel(
 #pragma unroll
     for (int r = 0; r < kDownRounds; ++r) {
         const int local = wave * kDownWaveKeys + r * kWave + lane;
-        const bool valid = local < chunk_count;
+        const bool valid = local < chunk_count && !(drop_sentinel && key[r] == kSentinelKey);
         const uint32_t d = digit_of(key[r], shift);
         uint64_t peers = __ballot(valid);
 #pragma unroll
@@ -275,9 +293,10 @@ __global__ __launch_bounds__(kDownThreads) void radix_downsweep_kernel(
             c[w] = t < kRadix ? s_cnt[w][t] : 0u;
             cnt += c[w];
         }
-        uint32_t dummy;
-        const uint32_t start = digit_exclusive_scan(cnt, s_wave, dummy);
+        uint32_t kept, dummy;
+        const uint32_t start = digit_exclusive_scan(cnt, s_wave, kept);
         const uint32_t digit_base = digit_exclusive_scan(t < kRadix ? totals[t] : 0u, s_wave, dummy);
+        if (t == 0) s_kept = kept;
         if (t < kRadix) {
             s_local[t] = start;
             s_global[t] = digit_base + offsets[(int64_t)t * num_chunks + blockIdx.x];
@@ -301,7 +320,8 @@ __global__ __launch_bounds__(kDownThreads) void radix_downsweep_kernel(
     }
     __syncthreads();
     // 4. write out in order: runs of one digit go to consecutive addresses
-    for (int i = threadIdx.x; i < chunk_count; i += kDownThreads) {
+    const int kept_count = (int)s_kept;
+    for (int i = threadIdx.x; i < kept_count; i += kDownThreads) {
         const uint64_t k = s_keys[i];
         const uint32_t d = digit_of(k, shift);
         const uint32_t pos = s_global[d] + ((uint32_t)i - s_local[d]);
@@ -316,9 +336,13 @@ using namespace gsx_amd;
 
 namespace {
 
+// n_dev: see radix_upsweep_kernel. compact_first: the first pass reads all n keys and drops the
+// sentinel keys (stably compacting the rest to the front), its row scan adds the number of kept
+// keys to *n_dev (zero beforehand), and the later passes sort that many.
 template <bool kPairs>
 gsx_hip_status radix_sort_u64(uint64_t* keys, uint32_t* vals, uint64_t* keys_alt, uint32_t* vals_alt, int64_t n,
-                              int begin_bit, int end_bit, void* temp, int* out_in_alt, hipStream_t stream) {
+                              uint32_t* n_dev, bool compact_first, int begin_bit, int end_bit, void* temp,
+                              int* out_in_alt, hipStream_t stream) {
     if (begin_bit < 0 || end_bit > 64 || begin_bit > end_bit) return GSX_HIP_ERROR_INVALID_ARGUMENT;
     if (n > (int64_t)UINT32_MAX) return GSX_HIP_ERROR_OUT_OF_RANGE;
     int64_t chunks = (n + kSortChunk - 1) / kSortChunk;
@@ -334,12 +358,14 @@ gsx_hip_status radix_sort_u64(uint64_t* keys, uint32_t* vals, uint64_t* keys_alt
             uint32_t* vin = in_alt ? vals_alt : vals;
             uint64_t* kout = in_alt ? keys : keys_alt;
             uint32_t* vout = in_alt ? vals : vals_alt;
+            const bool drop = compact_first && shift == begin_bit;
+            const uint32_t* live = drop ? nullptr : n_dev;
             hipLaunchKernelGGL(radix_upsweep_kernel, dim3((unsigned)chunks), dim3(kSortThreads), 0, stream, kin, n,
-                               shift, chunks, hist);
+                               live, drop, shift, chunks, hist);
             hipLaunchKernelGGL(radix_rowscan_kernel, dim3(kRadix), dim3(kSortThreads), 0, stream, hist, chunks,
-                               offsets, totals);
+                               offsets, totals, drop ? n_dev : nullptr);
             hipLaunchKernelGGL(radix_downsweep_kernel<kPairs>, dim3((unsigned)chunks), dim3(kDownThreads), 0, stream,
-                               kin, vin, n, shift, chunks, offsets, totals, kout, vout);
+                               kin, vin, n, live, drop, shift, chunks, offsets, totals, kout, vout);
             in_alt ^= 1;
         }
     }
@@ -383,14 +409,28 @@ size_t gsx_hip_radix_sort_temp_bytes(int64_t n) {
 gsx_hip_status gsx_hip_radix_sort_pairs_u64(uint64_t* keys, uint32_t* vals, uint64_t* keys_alt, uint32_t* vals_alt,
                                             int64_t n, int begin_bit, int end_bit, void* temp, int* out_in_alt,
                                             hipStream_t stream) {
-    return radix_sort_u64<true>(keys, vals, keys_alt, vals_alt, n, begin_bit, end_bit, temp, out_in_alt, stream);
+    return radix_sort_u64<true>(keys, vals, keys_alt, vals_alt, n, nullptr, false, begin_bit, end_bit, temp,
+                                out_in_alt, stream);
 }
 
 // Stable LSD sort of n keys on bits [begin_bit, end_bit); bits outside the range travel with
 // the key (a payload packed into the low bits keeps input order among equal sort bits).
 gsx_hip_status gsx_hip_radix_sort_keys_u64(uint64_t* keys, uint64_t* keys_alt, int64_t n, int begin_bit, int end_bit,
                                            void* temp, int* out_in_alt, hipStream_t stream) {
-    return radix_sort_u64<false>(keys, nullptr, keys_alt, nullptr, n, begin_bit, end_bit, temp, out_in_alt, stream);
+    return radix_sort_u64<false>(keys, nullptr, keys_alt, nullptr, n, nullptr, false, begin_bit, end_bit, temp,
+                                 out_in_alt, stream);
 }
 
 }  // extern "C"
+
+namespace gsx_amd {
+
+gsx_hip_status radix_sort_keys_u64_compacting(uint64_t* keys, uint64_t* keys_alt, int64_t n, uint32_t* n_live,
+                                              int begin_bit, int end_bit, void* temp, int* out_in_alt,
+                                              hipStream_t stream) {
+    if (begin_bit >= end_bit) return GSX_HIP_ERROR_INVALID_ARGUMENT;  // the compacting pass must run
+    return radix_sort_u64<false>(keys, nullptr, keys_alt, nullptr, n, n_live, true, begin_bit, end_bit, temp,
+                                 out_in_alt, stream);
+}
+
+}  // namespace gsx_amd
