@@ -10,8 +10,8 @@ groups (mean3d lr 1e-3, others 1e-2). All inputs are resident in HBM before the 
 
 Printed (rank 0, one JSON line): the train it/s as `value` (K steps with nothing else on the
 stream), plus the inference render FPS, the sort bandwidth, a per-kernel table and the roofline
-entry of the dominant kernel (both from K further steps with HIP events at every stage
-boundary), and the CPU baseline (the unmodified gsx CPU backend built from the reference
+entry of the dominant kernel (both from a replay of the same K steps from the same parameter
+and Adam state, with HIP events at every stage boundary), and the CPU baseline (the unmodified gsx CPU backend built from the reference
 sources, when present).
 """
 from __future__ import annotations
@@ -216,6 +216,15 @@ def main():
         step(i)
     torch.cuda.synchronize()
 
+    # training moves the Gaussians, so pass 2 restarts from this state and replays pass 1's steps
+    def opt_state():
+        out = []
+        for grp in opt.groups:
+            out += [grp["parameter"], grp["m"], grp["v"]]
+        return out
+
+    snapshot = [t.clone() for t in opt_state()]
+    steps_before = [grp["step"] for grp in opt.groups]
     # 1. throughput: K steps with nothing but the work on the stream (the per-stage HIP events
     #    of pass 2 cost about 45 us per step, so they stay out of this loop)
     log(f"timing {args.steps} steps")
@@ -226,14 +235,19 @@ def main():
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     it_s = args.steps / elapsed
-    # 2. per-kernel times: K more steps of the same workload with HIP events at every stage
+    # 2. per-kernel times: the same K steps from the same state, with HIP events at every stage
     #    boundary, recorded on the launch stream inside the library and around the loss and
     #    Adam launches here
+    for t, saved in zip(opt_state(), snapshot):
+        t.copy_(saved)
+    for grp, k in zip(opt.groups, steps_before):
+        grp["step"] = k
+    del snapshot
     renderer.set_timing(args.steps)
-    log(f"per-stage timing over {args.steps} more steps")
+    log(f"per-stage timing over the same {args.steps} steps")
     torch.cuda.synchronize()
     for i in range(args.steps):
-        step(args.warmup + args.steps + i, record=True)
+        step(args.warmup + i, record=True)  # the poses of pass 1 again
     torch.cuda.synchronize()
     stage_ms = renderer.timings()
     renderer.set_timing(0)

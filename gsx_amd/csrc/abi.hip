@@ -173,8 +173,9 @@ int bits_for(uint32_t v) {
 struct gsx_hip_render_context {
     DeviceBuffer rec, cov_coef, ckpt, inst_gauss, inst_grad, tile_count, big_list, offsets, scan_temp, keys, vals,
         keys_alt, sort_temp, ranges, sorted_g, final_t, last, grad2d, depth_keys, depth_keys_alt, rank_g, rank_count,
-        g_rank, long_list, counters, big_chunk_counts;
+        g_rank, long_list, counters, big_chunk_counts, depth_sort_temp;
     uint32_t* host_count = nullptr;  // pinned
+    hipEvent_t count_ev = nullptr;   // the instance count has reached host_count
     CameraParams cam{};
     gsx_hip_gaussians gs{};
     int64_t instance_count = 0;
@@ -336,9 +337,10 @@ gsx_hip_status gsx_hip_render_context_create(gsx_hip_render_context** out_contex
     gsx_hip_render_context* ctx = new (std::nothrow) gsx_hip_render_context();
     if (ctx == nullptr) return fail(GSX_HIP_ERROR_OUT_OF_MEMORY, "render context allocation failed");
     hipError_t e = hipHostMalloc(reinterpret_cast<void**>(&ctx->host_count), sizeof(uint32_t) * 2, hipHostMallocDefault);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->count_ev, hipEventDisableTiming);
     if (e != hipSuccess) {
-        delete ctx;
-        return hip_fail(e, "hipHostMalloc");
+        (void)gsx_hip_render_context_destroy(ctx);
+        return hip_fail(e, "render context creation");
     }
     *out_context = ctx;
     return GSX_HIP_SUCCESS;
@@ -351,9 +353,10 @@ gsx_hip_status gsx_hip_render_context_destroy(gsx_hip_render_context* ctx) {
                            &ctx->vals,       &ctx->keys_alt, &ctx->sort_temp,  &ctx->ranges,
                            &ctx->sorted_g,   &ctx->final_t,  &ctx->last,      &ctx->grad2d,     &ctx->depth_keys,
                            &ctx->depth_keys_alt, &ctx->rank_g, &ctx->rank_count, &ctx->g_rank,
-                           &ctx->long_list, &ctx->counters, &ctx->big_chunk_counts};
+                           &ctx->long_list, &ctx->counters, &ctx->big_chunk_counts, &ctx->depth_sort_temp};
     for (DeviceBuffer* b : all) b->release();
     if (ctx->host_count != nullptr) (void)hipHostFree(ctx->host_count);
+    if (ctx->count_ev != nullptr) (void)hipEventDestroy(ctx->count_ev);
     release_events(ctx);
     delete ctx;
     return GSX_HIP_SUCCESS;
@@ -459,7 +462,8 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     GSX_TRY(ctx->rec.reserve(n1 * 3 * sizeof(float4), "rec"));
     if (train) GSX_TRY(ctx->cov_coef.reserve(n1 * 2 * sizeof(float4), "cov_coef"));
     GSX_TRY(ctx->tile_count.reserve(n1 * sizeof(uint32_t), "tile_count"));
-    // list counters: [0] visible Gaussians (depth keys), [1] big boxes, [2] long instance runs
+    // list counters: [0] visible Gaussians (depth keys), [1] big boxes, [2] long instance runs,
+    // [3] instances
     GSX_TRY(ctx->counters.reserve(4 * sizeof(uint32_t), "counters"));
     GSX_TRY(ctx->big_list.reserve(n1 * sizeof(uint32_t), "big_list"));
     GSX_TRY(ctx->big_chunk_counts.reserve(n1 * kBigChunks * sizeof(uint32_t), "big_chunk_counts"));
@@ -471,7 +475,7 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     GSX_TRY(ctx->rank_count.reserve(n1 * sizeof(uint32_t), "rank_count"));
     GSX_TRY(ctx->g_rank.reserve(n1 * sizeof(uint32_t), "gaussian_rank"));
     GSX_TRY(ctx->long_list.reserve(n1 * sizeof(uint32_t), "long_list"));
-    GSX_TRY(ctx->sort_temp.reserve(gsx_hip_radix_sort_temp_bytes(n), "sort_temp"));
+    GSX_TRY(ctx->depth_sort_temp.reserve(gsx_hip_radix_sort_temp_bytes(n), "depth_sort_temp"));
     GSX_TRY(ctx->ranges.reserve((size_t)tiles * sizeof(uint2), "ranges"));
     GSX_TRY(ctx->final_t.reserve((size_t)pixels * sizeof(float), "final_t"));
     GSX_TRY(ctx->last.reserve((size_t)pixels * sizeof(uint32_t), "last"));
@@ -512,6 +516,17 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
                            ctx->big_chunk_counts.as<uint32_t>(), nullptr, nullptr, nullptr, nullptr);
         GSX_HIP_TRY(hipGetLastError(), "big_tiles_kernel<count>");
     }
+    // the instance count (the sum of the kept-tile counts) goes to the host first; the depth
+    // order and the count scan are queued behind it, so the GPU keeps working while the host
+    // waits for the count and sizes the instance buffers
+    if (n > 0) {
+        hipLaunchKernelGGL(sum_u32_kernel, dim3(std::min(blocks_for(n, 256 * 16), 1024u)), dim3(256), 0, stream,
+                           ctx->tile_count.as<uint32_t>(), n, counters + 3);
+        GSX_HIP_TRY(hipGetLastError(), "sum_u32_kernel");
+    }
+    GSX_HIP_TRY(hipMemcpyAsync(ctx->host_count, counters + 3, sizeof(uint32_t), hipMemcpyDeviceToHost, stream),
+                "instance count readback");
+    GSX_HIP_TRY(hipEventRecord(ctx->count_ev, stream), "hipEventRecord(count)");
     GSX_TRY(record(ctx, 1, stream));
     // depth order of the Gaussians, then their tile counts in that order and its scan
     const uint64_t* sorted_depth = ctx->depth_keys.as<uint64_t>();
@@ -519,8 +534,8 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
         int depth_in_alt = 0;
         const int end_bit = std::min(64, index_bits + ctx->depth_sort_passes * 8);
         GSX_TRY(radix_sort_keys_u64_compacting(ctx->depth_keys.as<uint64_t>(), ctx->depth_keys_alt.as<uint64_t>(), n,
-                                               counters, index_bits, end_bit, ctx->sort_temp.ptr, &depth_in_alt,
-                                               stream));
+                                               counters, index_bits, end_bit, ctx->depth_sort_temp.ptr,
+                                               &depth_in_alt, stream));
         if (depth_in_alt) sorted_depth = ctx->depth_keys_alt.as<uint64_t>();
         hipLaunchKernelGGL(rank_gather_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, n, counters,
                            sorted_depth, (uint64_t)((1ull << index_bits) - 1ull), ctx->tile_count.as<uint32_t>(),
@@ -530,11 +545,8 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     }
     GSX_TRY(gsx_hip_scan_exclusive_u32(ctx->rank_count.as<uint32_t>(), ctx->offsets.as<uint32_t>(), n,
                                        ctx->scan_temp.ptr, stream));
-    GSX_HIP_TRY(hipMemcpyAsync(ctx->host_count, ctx->offsets.as<uint32_t>() + n, sizeof(uint32_t),
-                               hipMemcpyDeviceToHost, stream),
-                "instance count readback");
-    GSX_HIP_TRY(hipStreamSynchronize(stream), "instance count sync");
     GSX_TRY(record(ctx, 2, stream));
+    GSX_HIP_TRY(hipEventSynchronize(ctx->count_ev), "instance count sync");
     const int64_t count = (int64_t)ctx->host_count[0];
     ctx->instance_count = count;
     const size_t c1 = (size_t)(count > 0 ? count : 1);

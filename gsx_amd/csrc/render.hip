@@ -363,6 +363,24 @@ __global__ __launch_bounds__(256) void big_tiles_kernel(const uint32_t* __restri
     }
 }
 
+// *out += sum of in[0..n) (out zeroed beforehand; one atomic per workgroup, grid-stride).
+__global__ __launch_bounds__(256) void sum_u32_kernel(const uint32_t* __restrict__ in, int64_t n,
+                                                      uint32_t* __restrict__ out) {
+    __shared__ uint32_t s_wave[kWavesPerBlock];
+    uint32_t v = 0;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        v += in[i];
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) v += (uint32_t)__shfl_xor((int)v, off, kWave);
+    if (__lane_id() == 0) s_wave[threadIdx.x / kWave] = v;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t total = 0;
+        for (int w = 0; w < kWavesPerBlock; ++w) total += s_wave[w];
+        if (total > 0) atomicAdd(out, total);
+    }
+}
+
 __global__ __launch_bounds__(256) void fill_u32_kernel(uint32_t* __restrict__ p, int64_t count, uint32_t v) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < count) p[i] = v;
