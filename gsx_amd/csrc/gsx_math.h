@@ -35,49 +35,40 @@
 #define GSX_EXP2_TABLE_BITS 5
 #define GSX_EXP2_TABLE_SIZE 32
 
+/* The table entries (those of ARM's optimized-routines expf, which glibc ships). Host code reads
+ * a static array; device code a constant array in each code object, so a lookup is one load
+ * instead of a per-lane branch tree. Kernels with many expf calls per lane also copy
+ * it to LDS once and use gsx_expf_table / gsx_expf_small with that copy (see below). */
+#define GSX_EXP2_TABLE_INIT                                                                        \
+  { \
+    0x3ff0000000000000ULL, 0x3fefd9b0d3158574ULL, 0x3fefb5586cf9890fULL, 0x3fef9301d0125b51ULL, \
+    0x3fef72b83c7d517bULL, 0x3fef54873168b9aaULL, 0x3fef387a6e756238ULL, 0x3fef1e9df51fdee1ULL, \
+    0x3fef06fe0a31b715ULL, 0x3feef1a7373aa9cbULL, 0x3feedea64c123422ULL, 0x3feece086061892dULL, \
+    0x3feebfdad5362a27ULL, 0x3feeb42b569d4f82ULL, 0x3feeab07dd485429ULL, 0x3feea47eb03a5585ULL, \
+    0x3feea09e667f3bcdULL, 0x3fee9f75e8ec5f74ULL, 0x3feea11473eb0187ULL, 0x3feea589994cce13ULL, \
+    0x3feeace5422aa0dbULL, 0x3feeb737b0cdc5e5ULL, 0x3feec49182a3f090ULL, 0x3feed503b23e255dULL, \
+    0x3feee89f995ad3adULL, 0x3feeff76f2fb5e47ULL, 0x3fef199bdd85529cULL, 0x3fef3720dcef9069ULL, \
+    0x3fef5818dcfba487ULL, 0x3fef7c97337b9b5fULL, 0x3fefa4afa2a490daULL, 0x3fefd0765b6e4540ULL \
+  }
+
+static const uint64_t gsx_exp2_table_host[GSX_EXP2_TABLE_SIZE] = GSX_EXP2_TABLE_INIT;
 #if defined(__HIPCC__)
+static __device__ const uint64_t gsx_exp2_table_dev[GSX_EXP2_TABLE_SIZE] = GSX_EXP2_TABLE_INIT;
+
 __host__ __device__ inline uint64_t gsx_exp2_table_entry(uint32_t i)
+{
+#if defined(__HIP_DEVICE_COMPILE__)
+    return gsx_exp2_table_dev[i & 31u];
+#else
+    return gsx_exp2_table_host[i & 31u];
+#endif
+}
 #else
 static inline uint64_t gsx_exp2_table_entry(uint32_t i)
-#endif
 {
-    /* Values as immediates; kernels with many expf calls per lane copy them to LDS once and
-     * use gsx_expf_table (see below). */
-    switch(i & 31u) {
-    case 0: return 0x3ff0000000000000ULL;
-    case 1: return 0x3fefd9b0d3158574ULL;
-    case 2: return 0x3fefb5586cf9890fULL;
-    case 3: return 0x3fef9301d0125b51ULL;
-    case 4: return 0x3fef72b83c7d517bULL;
-    case 5: return 0x3fef54873168b9aaULL;
-    case 6: return 0x3fef387a6e756238ULL;
-    case 7: return 0x3fef1e9df51fdee1ULL;
-    case 8: return 0x3fef06fe0a31b715ULL;
-    case 9: return 0x3feef1a7373aa9cbULL;
-    case 10: return 0x3feedea64c123422ULL;
-    case 11: return 0x3feece086061892dULL;
-    case 12: return 0x3feebfdad5362a27ULL;
-    case 13: return 0x3feeb42b569d4f82ULL;
-    case 14: return 0x3feeab07dd485429ULL;
-    case 15: return 0x3feea47eb03a5585ULL;
-    case 16: return 0x3feea09e667f3bcdULL;
-    case 17: return 0x3fee9f75e8ec5f74ULL;
-    case 18: return 0x3feea11473eb0187ULL;
-    case 19: return 0x3feea589994cce13ULL;
-    case 20: return 0x3feeace5422aa0dbULL;
-    case 21: return 0x3feeb737b0cdc5e5ULL;
-    case 22: return 0x3feec49182a3f090ULL;
-    case 23: return 0x3feed503b23e255dULL;
-    case 24: return 0x3feee89f995ad3adULL;
-    case 25: return 0x3feeff76f2fb5e47ULL;
-    case 26: return 0x3fef199bdd85529cULL;
-    case 27: return 0x3fef3720dcef9069ULL;
-    case 28: return 0x3fef5818dcfba487ULL;
-    case 29: return 0x3fef7c97337b9b5fULL;
-    case 30: return 0x3fefa4afa2a490daULL;
-    default: return 0x3fefd0765b6e4540ULL;
-    }
+    return gsx_exp2_table_host[i & 31u];
 }
+#endif
 
 GSX_HD uint32_t gsx_f32_bits(float x)
 {
