@@ -526,8 +526,9 @@ constexpr int kGradRecord = 8;  // per-instance partials: channels 0-7 in one 32
 // set are bit-identical to the CPU's) and then walks it backwards accumulating the suffix colour
 // exactly as the CPU does. Per contribution the gradient terms are the CPU's, including the
 // d(conic)/d(cov2d) map applied per contribution.
-// Reduction without atomics: each wave sums its lanes' 9 partials per entry with DPP moves, the
-// four waves combine through LDS, and the tile writes one 9-float partial per instance at its
+// Reduction without atomics: each 16-pixel row sums its lanes' 9 partials per entry with DPP
+// moves (row_reduce_scatter9), the 16 row totals are combined through LDS, and the tile writes
+// one 9-float partial per instance at its
 // emission position (channels 0-7 as one 32-byte record of instance_grad, channel 8, the
 // opacity term, in instance_grad_op); reduce_instance_grads_kernel then sums each Gaussian's
 // contiguous run of positions. The result is deterministic and immune to the contention of
@@ -727,12 +728,11 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
                 s0 += w * r1.z;
                 s1 += w * r1.w;
                 s2 += w * r2.x;
-                row_reduce_sums(v);
-                if ((threadIdx.x & (kTile - 1)) == 0) {
-                    float* acc = &s_acc[row][i][0];
-#pragma unroll
-                    for (int c = 0; c < kGrad2d; ++c) acc[c] = v[c];
-                }
+                float total8;
+                const float scattered = row_reduce_scatter9(v, total8);
+                const uint32_t col = threadIdx.x & (kTile - 1);  // lane within the DPP row
+                if ((col & 1u) == 0u) s_acc[row][i][col >> 1] = scattered;
+                if (col == 0u) s_acc[row][i][8] = total8;
             }
             __syncthreads();
             // combine the 16 row partials and write the bucket's per-instance partials
