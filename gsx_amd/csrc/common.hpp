@@ -358,42 +358,36 @@ __device__ inline float wave_reduce_sum(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
-// DPP move in which only the banks (groups of 4 lanes of a 16-lane row) enabled by kBankMask
-// receive src from the lane kCtrl selects; the other lanes return their own `old`.
-template <int kCtrl, int kBankMask>
-__device__ inline float dpp_banks(float old, float src) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old), __builtin_bit_cast(int, src),
-                                                                 kCtrl, 0xf, kBankMask, false));
-}
-
 // Row totals (over the 16 lanes of each DPP row) of v[0..8], scattered over the row: the returned
 // value of lane l (l = lane index within its row) is the row total of v[(l >> 1) & 7], and
-// total8 receives the row total of v[8] in every lane. Each step halves the values a lane
-// carries: lanes l and l ^ 8 split v[0..7] into two halves (two bank-masked row shifts and an
-// add per kept value), then l and l ^ 4 split again, then l and l ^ 2 (quad permute of the value
-// the partner keeps), and l, l ^ 1 add their last value: 22 lane operations instead of 32 for
-// the 8 values (plus 4 for v[8]), and 8 lanes of a row can store the 8 totals with one write.
+// total8 receives the row total of v[8] in every lane. Each step pairs every lane with a partner
+// whose lane-group bit differs and halves the values a lane carries: the lane keeps one half and
+// sends its partner the other (two lane-constant selects), and adds what the partner sent (one
+// fused DPP add). Partners: row rotate by 8 (l ^ 8, group bit 3), row half mirror (l ^ 7 within
+// each 8-lane half, group bit 2), quad permute l ^ 2 (bit 1), then l ^ 1 adds the last value:
+// 22 lane operations for the 8 values instead of 32, plus 4 for v[8], and 8 lanes of a row hold
+// the 8 totals, so one store writes them all.
 __device__ inline float row_reduce_scatter9(const float (&v)[9], float& total8) {
+    const uint32_t l = __lane_id();
+    const bool b3 = (l & 8u) != 0, b2 = (l & 4u) != 0, b1 = (l & 2u) != 0;
     float b[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        // lanes 0-7 keep v[i] (+ lane l + 8), lanes 8-15 keep v[4 + i] (+ lane l - 8)
-        const float x = dpp_banks<0x108, 0x3>(v[4 + i], v[i]);  // row_shl:8 into banks 0, 1
-        const float y = dpp_banks<0x118, 0xc>(v[i], v[4 + i]);  // row_shr:8 into banks 2, 3
-        b[i] = x + y;
+        // lanes 0-7 of the row keep v[i], lanes 8-15 keep v[4 + i]
+        const float keep = b3 ? v[4 + i] : v[i];
+        const float send = b3 ? v[i] : v[4 + i];
+        b[i] = keep + dpp_move<0x128, 0xf>(send);  // row_ror:8
     }
     float c[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-        // banks 0, 2 keep b[i] (+ lane l + 4), banks 1, 3 keep b[2 + i] (+ lane l - 4)
-        const float x = dpp_banks<0x104, 0x5>(b[2 + i], b[i]);  // row_shl:4 into banks 0, 2
-        const float y = dpp_banks<0x114, 0xa>(b[i], b[2 + i]);  // row_shr:4 into banks 1, 3
-        c[i] = x + y;
+        // lanes with bit 2 clear keep b[i], the others b[2 + i]
+        const float keep = b2 ? b[2 + i] : b[i];
+        const float send = b2 ? b[i] : b[2 + i];
+        c[i] = keep + dpp_move<0x141, 0xf>(send);  // row_half_mirror
     }
-    // lanes with bit 1 clear keep c[0], the others c[1]; each sends the one its partner keeps
-    const bool hi = (__lane_id() & 2u) != 0;
-    const float send = hi ? c[0] : c[1];
-    const float keep = hi ? c[1] : c[0];
+    const float keep = b1 ? c[1] : c[0];
+    const float send = b1 ? c[0] : c[1];
     float d = keep + dpp_move<0x4e, 0xf>(send);  // quad_perm [2,3,0,1]
     d += dpp_move<0xb1, 0xf>(d);                 // quad_perm [1,0,3,2]
     float t = v[8];
