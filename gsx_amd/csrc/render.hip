@@ -767,8 +767,8 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
 //  * longer runs (listed by rank_gather_kernel; in depth order the near, large Gaussians sit
 //    side by side, and the largest cover nearly every tile): each run is cut into at most
 //    kLongChunks chunks of `chunk` positions, one wave sums a chunk (DPP tree) and leaves the
-//    partial in place at the chunk's first position (reduce_long_chunks_kernel), then one thread
-//    per run adds its chunk partials in chunk order (combine_long_runs_kernel).
+//    partial in place at the chunk's first position (reduce_long_chunks_kernel), then one wave
+//    per run adds its chunk partials with a DPP tree (combine_long_runs_kernel).
 constexpr uint32_t kShortPiece = 256;  // instances per LDS piece and wave (9 KB)
 constexpr uint32_t kLongChunks = 16;
 
@@ -881,6 +881,8 @@ __global__ __launch_bounds__(256) void reduce_long_chunks_kernel(const uint32_t*
     }
 }
 
+// One wave per listed run: lane k (k < number of chunks) loads chunk k's partial, a DPP tree sums
+// them (a fixed order, so the result is deterministic), and lane 0 writes grad2d.
 __global__ __launch_bounds__(256) void combine_long_runs_kernel(const uint32_t* __restrict__ long_list,
                                                                 const uint32_t* __restrict__ long_count,
                                                                 const uint32_t* __restrict__ offsets,
@@ -889,16 +891,23 @@ __global__ __launch_bounds__(256) void combine_long_runs_kernel(const uint32_t* 
                                                                 const float* __restrict__ instance_grad_op,
                                                                 float* __restrict__ grad2d) {
     const uint32_t count = *long_count;
-    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < count; i += gridDim.x * blockDim.x) {
+    const uint32_t lane = __lane_id();
+    const uint32_t waves = gridDim.x * (blockDim.x / kWave);
+    for (uint32_t i = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave; i < count; i += waves) {
         const uint32_t r = long_list[i];
         const uint32_t b = offsets[r], e = offsets[r + 1];
         float acc[kGrad2d];
 #pragma unroll
         for (int c = 0; c < kGrad2d; ++c) acc[c] = 0.0f;
-        for (uint32_t p = b; p < e; p += chunk) add_instance_grad(acc, instance_grad, instance_grad_op, p);
-        const size_t g = rank_gaussian[r];
+        const uint32_t p = b + lane * chunk;  // at most kLongChunks (16) chunks per run
+        if (lane < kLongChunks && p < e) add_instance_grad(acc, instance_grad, instance_grad_op, p);
 #pragma unroll
-        for (int c = 0; c < kGrad2d; ++c) grad2d[g * kGrad2d + c] = acc[c];
+        for (int c = 0; c < kGrad2d; ++c) acc[c] = wave_reduce_sum(acc[c]);
+        if (lane == 0) {
+            const size_t g = rank_gaussian[r];
+#pragma unroll
+            for (int c = 0; c < kGrad2d; ++c) grad2d[g * kGrad2d + c] = acc[c];
+        }
     }
 }
 
