@@ -493,6 +493,8 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     const int index_bits = std::max(1, bits_for((uint32_t)(n > 0 ? n - 1 : 0)));
     const int depth_bits = bits_for(depth_max);
     ctx->depth_sort_passes = (depth_bits + 7) / 8;
+    // big boxes are flagged in bit 63 of their depth key when the sort never reaches that bit
+    const bool big_flag = index_bits + ctx->depth_sort_passes * 8 <= 63;
 
     if (ctx->timing) {
         ctx->cur = (ctx->cur + 1) % ctx->ring;
@@ -508,7 +510,7 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
                            ctx->rec.as<float4>(), train ? ctx->cov_coef.as<float4>() : nullptr,
                            ctx->tile_count.as<uint32_t>(), train ? visible_counter : nullptr,
                            ctx->big_list.as<uint32_t>(), counters + 1, ctx->depth_keys.as<uint64_t>(), near_bits,
-                           depth_max, index_bits);
+                           depth_max, index_bits, big_flag ? kBigKeyFlag : 0ull);
         GSX_HIP_TRY(hipGetLastError(), "preprocess_kernel");
         hipLaunchKernelGGL(big_tiles_kernel<false>, dim3(kBigBlocks, big_chunks), dim3(256), 0, stream,
                            ctx->big_list.as<uint32_t>(), counters + 1, ctx->rec.as<float4>(), cam.tiles_x,
@@ -538,7 +540,8 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
                                                &depth_in_alt, stream));
         if (depth_in_alt) sorted_depth = ctx->depth_keys_alt.as<uint64_t>();
         hipLaunchKernelGGL(rank_gather_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, n, counters,
-                           sorted_depth, (uint64_t)((1ull << index_bits) - 1ull), ctx->tile_count.as<uint32_t>(),
+                           sorted_depth, (uint64_t)((1ull << index_bits) - 1ull), big_flag,
+                           ctx->tile_count.as<uint32_t>(),
                            ctx->rank_g.as<uint32_t>(), ctx->rank_count.as<uint32_t>(), ctx->g_rank.as<uint32_t>(),
                            ctx->long_list.as<uint32_t>(), counters + 2);
         GSX_HIP_TRY(hipGetLastError(), "rank_gather_kernel");

@@ -169,7 +169,8 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
     const float* __restrict__ sh1, const float* __restrict__ sh2, const float* __restrict__ sh3, int sh_degree,
     CameraParams cam, float4* __restrict__ rec, float4* __restrict__ cov_coef, uint32_t* __restrict__ tile_count,
     float* __restrict__ visible_counter, uint32_t* __restrict__ big_list, uint32_t* __restrict__ big_count,
-    uint64_t* __restrict__ depth_keys, uint32_t depth_base, uint32_t depth_max, int index_bits) {
+    uint64_t* __restrict__ depth_keys, uint32_t depth_base, uint32_t depth_max, int index_bits,
+    uint64_t big_key_flag) {
     __shared__ WaveBoxes s_boxes[kWavesPerBlock];
     WaveBoxes& wb = s_boxes[threadIdx.x / kWave];
     const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -205,33 +206,40 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
             }
         }
     }
-    // depth key of every Gaussian (~0 for invisible ones, which the depth sort drops)
+    const bool big = visible && box_tiles(r2) > kBigTiles;
+    // depth key of every Gaussian (~0 for invisible ones, which the depth sort drops);
+    // big_key_flag (kBigKeyFlag or 0, see there) marks the big boxes for rank_gather_kernel
     if (g < n) {
         uint64_t key = ~0ull;
         if (visible) {
             uint32_t rel = __float_as_uint(r2.w) - depth_base;
             if (rel > depth_max) rel = depth_max;  // only for non-finite depths
-            key = ((uint64_t)rel << index_bits) | (uint64_t)g;
+            key = ((uint64_t)rel << index_bits) | (uint64_t)g | (big ? big_key_flag : 0ull);
         }
         depth_keys[g] = key;
     }
-    const bool big = visible && box_tiles(r2) > kBigTiles;
     if (big) big_list[atomicAdd(big_count, 1u)] = (uint32_t)g;  // counted by big_tiles_kernel
     const uint32_t total = stage_box(wb, visible && !big, r0, r1, r2, (uint32_t)g, 0u);
     walk_wave_tiles<false>(wb, total, cam.tiles_x, KeyLayout{}, nullptr, nullptr);
     if (g < n) tile_count[g] = big ? 0u : wb.kept[__lane_id()];  // big boxes: summed by big_tiles_kernel
 }
 
+// Marks a big box's depth key (big_tiles_kernel needs its rank). Used only when the sorted depth
+// bits end below bit 63, which holds for fewer than 2^31 Gaussians.
+constexpr uint64_t kBigKeyFlag = 1ull << 63;
+
 // Instance runs longer than this are summed in chunks by whole waves in the backward (see
 // reduce_long_chunks_kernel), shorter ones by one lane each.
 constexpr uint32_t kLaneRun = 32;
 
 // After the depth sort of the V visible Gaussians (V = *depth_count): the Gaussian of every
-// depth rank, its kept-tile count, its rank, and the list of ranks whose count exceeds kLaneRun.
-// Ranks V..n-1 get count 0 (so the scan over n covers them) and no Gaussian.
+// depth rank, its kept-tile count, the rank of each big box (the only ranks looked up by
+// Gaussian; every Gaussian's when flagged_only is false), and the list of ranks whose count
+// exceeds kLaneRun. Ranks V..n-1 get count 0 (so the scan over n covers them) and no Gaussian.
 __global__ __launch_bounds__(256) void rank_gather_kernel(int64_t n, const uint32_t* __restrict__ depth_count,
                                                           const uint64_t* __restrict__ sorted_depth_keys,
-                                                          uint64_t index_mask, const uint32_t* __restrict__ tile_count,
+                                                          uint64_t index_mask, bool flagged_only,
+                                                          const uint32_t* __restrict__ tile_count,
                                                           uint32_t* __restrict__ rank_gaussian,
                                                           uint32_t* __restrict__ rank_count,
                                                           uint32_t* __restrict__ gaussian_rank,
@@ -243,11 +251,12 @@ __global__ __launch_bounds__(256) void rank_gather_kernel(int64_t n, const uint3
         rank_count[r] = 0;
         return;
     }
-    const uint32_t g = (uint32_t)(sorted_depth_keys[r] & index_mask);
+    const uint64_t key = sorted_depth_keys[r];
+    const uint32_t g = (uint32_t)(key & index_mask);
     const uint32_t c = tile_count[g];
     rank_gaussian[r] = g;
     rank_count[r] = c;
-    gaussian_rank[g] = (uint32_t)r;
+    if (!flagged_only || (key & kBigKeyFlag) != 0) gaussian_rank[g] = (uint32_t)r;
     if (c > kLaneRun) long_list[atomicAdd(long_count, 1u)] = (uint32_t)r;
 }
 
