@@ -475,7 +475,7 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     GSX_TRY(ctx->rank_count.reserve(n1 * sizeof(uint32_t), "rank_count"));
     GSX_TRY(ctx->g_rank.reserve(n1 * sizeof(uint32_t), "gaussian_rank"));
     GSX_TRY(ctx->long_list.reserve(n1 * sizeof(uint32_t), "long_list"));
-    GSX_TRY(ctx->depth_sort_temp.reserve(gsx_hip_radix_sort_temp_bytes(n), "depth_sort_temp"));
+    GSX_TRY(ctx->depth_sort_temp.reserve(radix_sort_keys_u64_compacting_temp_bytes(n), "depth_sort_temp"));
     GSX_TRY(ctx->ranges.reserve((size_t)tiles * sizeof(uint2), "ranges"));
     GSX_TRY(ctx->final_t.reserve((size_t)pixels * sizeof(float), "final_t"));
     GSX_TRY(ctx->last.reserve((size_t)pixels * sizeof(uint32_t), "last"));
@@ -492,9 +492,10 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     const uint32_t depth_max = far_bits - near_bits;
     const int index_bits = std::max(1, bits_for((uint32_t)(n > 0 ? n - 1 : 0)));
     const int depth_bits = bits_for(depth_max);
-    ctx->depth_sort_passes = (depth_bits + 7) / 8;
+    ctx->depth_sort_passes = (depth_bits + kCompactingRadixBits - 1) / kCompactingRadixBits;
+    const int depth_end_bit = std::min(64, index_bits + ctx->depth_sort_passes * kCompactingRadixBits);
     // big boxes are flagged in bit 63 of their depth key when the sort never reaches that bit
-    const bool big_flag = index_bits + ctx->depth_sort_passes * 8 <= 63;
+    const bool big_flag = depth_end_bit <= 63;
 
     if (ctx->timing) {
         ctx->cur = (ctx->cur + 1) % ctx->ring;
@@ -534,9 +535,8 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     const uint64_t* sorted_depth = ctx->depth_keys.as<uint64_t>();
     if (n > 0) {
         int depth_in_alt = 0;
-        const int end_bit = std::min(64, index_bits + ctx->depth_sort_passes * 8);
         GSX_TRY(radix_sort_keys_u64_compacting(ctx->depth_keys.as<uint64_t>(), ctx->depth_keys_alt.as<uint64_t>(), n,
-                                               counters, index_bits, end_bit, ctx->depth_sort_temp.ptr,
+                                               counters, index_bits, depth_end_bit, ctx->depth_sort_temp.ptr,
                                                &depth_in_alt, stream));
         if (depth_in_alt) sorted_depth = ctx->depth_keys_alt.as<uint64_t>();
         hipLaunchKernelGGL(rank_gather_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, n, counters,

@@ -416,8 +416,12 @@ __device__ inline float div_rn_normal(float n, float d) {
 // stores their number in *n_live (which must be zero beforehand); the later passes sort that
 // many (grids are sized for n, so no host round trip is needed). Output positions >= *n_live
 // are not written.
+// Its digits are kCompactingRadixBits wide (passes = ceil((end_bit - begin_bit) / 9)), and temp
+// holds radix_sort_keys_u64_compacting_temp_bytes(n) bytes.
+constexpr int kCompactingRadixBits = 9;
 gsx_hip_status radix_sort_keys_u64_compacting(uint64_t* keys, uint64_t* keys_alt, int64_t n, uint32_t* n_live,
                                               int begin_bit, int end_bit, void* temp, int* out_in_alt,
                                               hipStream_t stream);
+size_t radix_sort_keys_u64_compacting_temp_bytes(int64_t n);
 
 }  // namespace gsx_amd

@@ -20,8 +20,7 @@ constexpr int kScanChunk = kScanThreads * kScanItems;  // 4096 elements per bloc
 constexpr int kSortThreads = 256;
 constexpr int kSortRounds = 16;
 constexpr int kSortChunk = kSortThreads * kSortRounds;  // 4096 keys per block
-constexpr int kRadixBits = 8;
-constexpr int kRadix = 1 << kRadixBits;
+constexpr int kRadixBits = 8;  // digit width of the public sorts
 
 // Exclusive scan of the 256 per-thread values of a block; returns this thread's prefix and
 // the block total through `total`.
@@ -116,7 +115,8 @@ __global__ __launch_bounds__(kScanThreads) void scan_downsweep_kernel(const uint
 }
 
 // ---------------------------------------------------------------------------------------------
-// One LSD pass on the 8-bit digit at `shift`, reduce-then-scan, three launches:
+// One LSD pass on the kBits-bit digit at `shift` (8, or 9 for the compacting sort: 512 bins,
+// three passes for 27 depth bits), reduce-then-scan, three launches:
 //   upsweep: digit counts of each 4096-key chunk                       -> hist[digit][chunk]
 //   rowscan: one workgroup per digit scans its row over the chunks    -> offsets, totals[digit]
 //   downsweep: each wave ranks its 1024 keys (16 rounds of 64) stably with 8 ballots per round
@@ -130,22 +130,26 @@ constexpr int kChunkWaves = kSortThreads / kWave;            // 4
 constexpr int kWaveKeys = kSortChunk / kChunkWaves;           // 1024 keys per wave
 constexpr int kWaveRounds = kWaveKeys / kWave;                // 16
 
-__device__ inline uint32_t digit_of(uint64_t key, int shift) { return (uint32_t)(key >> shift) & (kRadix - 1); }
+template <int kBits>
+__device__ inline uint32_t digit_of(uint64_t key, int shift) {
+    return (uint32_t)(key >> shift) & ((1u << kBits) - 1u);
+}
 
 constexpr uint64_t kSentinelKey = ~0ull;  // dropped by a pass with drop_sentinel set
 
 // n_dev (may be null): live key count, n = min(n, *n_dev); chunks past it count nothing.
 // drop_sentinel: keys equal to kSentinelKey are left out (they vanish from the output).
+template <int kBits>
 __global__ __launch_bounds__(kSortThreads) void radix_upsweep_kernel(const uint64_t* __restrict__ keys, int64_t n,
                                                                      const uint32_t* __restrict__ n_dev,
                                                                      bool drop_sentinel, int shift,
                                                                      int64_t num_chunks,
                                                                      uint32_t* __restrict__ hist) {
-    __shared__ uint32_t s_hist[kChunkWaves][kRadix];
+    constexpr int kBins = 1 << kBits;
+    __shared__ uint32_t s_hist[kChunkWaves][kBins];
     if (n_dev != nullptr) n = min(n, (int64_t)*n_dev);
     const int wave = threadIdx.x / kWave;
-#pragma unroll
-    for (int w = 0; w < kChunkWaves; ++w) s_hist[w][threadIdx.x] = 0;
+    for (int i = threadIdx.x; i < kChunkWaves * kBins; i += kSortThreads) (&s_hist[0][0])[i] = 0;
     __syncthreads();
     const int64_t base = (int64_t)blockIdx.x * kSortChunk;
 #pragma unroll 4
@@ -153,12 +157,14 @@ __global__ __launch_bounds__(kSortThreads) void radix_upsweep_kernel(const uint6
         const int64_t i = base + (int64_t)r * kSortThreads + threadIdx.x;
         if (i < n) {
             const uint64_t k = keys[i];
-            if (!drop_sentinel || k != kSentinelKey) atomicAdd(&s_hist[wave][digit_of(k, shift)], 1u);
+            if (!drop_sentinel || k != kSentinelKey) atomicAdd(&s_hist[wave][digit_of<kBits>(k, shift)], 1u);
         }
     }
     __syncthreads();
-    const uint32_t c = s_hist[0][threadIdx.x] + s_hist[1][threadIdx.x] + s_hist[2][threadIdx.x] + s_hist[3][threadIdx.x];
-    hist[(int64_t)threadIdx.x * num_chunks + blockIdx.x] = c;
+    for (int d = threadIdx.x; d < kBins; d += kSortThreads) {
+        const uint32_t c = s_hist[0][d] + s_hist[1][d] + s_hist[2][d] + s_hist[3][d];
+        hist[(int64_t)d * num_chunks + blockIdx.x] = c;
+    }
 }
 
 // Workgroup d: exclusive scan of hist[d][0..num_chunks) into offsets[d][..], row total into
@@ -204,8 +210,9 @@ constexpr int kDownWaves = kDownThreads / kWave;           // 8
 constexpr int kDownWaveKeys = kSortChunk / kDownWaves;     // 512
 constexpr int kDownRounds = kDownWaveKeys / kWave;         // 8
 
-// Exclusive scan over the 256 digits held by threads 0..255 of a 512-thread workgroup (threads
-// 256..511 pass 0 and get garbage); `total` receives the sum over the digits.
+// Exclusive scan over the kBins digits held by threads 0..kBins-1 of a 512-thread workgroup
+// (threads past kBins pass 0 and get garbage); `total` receives the sum over the digits.
+template <int kBins>
 __device__ inline uint32_t digit_exclusive_scan(uint32_t v, uint32_t* s_wave, uint32_t& total) {
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
@@ -220,7 +227,7 @@ __device__ inline uint32_t digit_exclusive_scan(uint32_t v, uint32_t* s_wave, ui
     uint32_t wave_base = 0;
     total = 0;
 #pragma unroll
-    for (int w = 0; w < kRadix / kWave; ++w) {
+    for (int w = 0; w < kBins / kWave; ++w) {
         const uint32_t sw = s_wave[w];
         if (w < wave) wave_base += sw;
         total += sw;
@@ -229,7 +236,7 @@ __device__ inline uint32_t digit_exclusive_scan(uint32_t v, uint32_t* s_wave, ui
     return wave_base + incl - v;
 }
 
-template <bool kPairs>
+template <bool kPairs, int kBits>
 __global__ __launch_bounds__(kDownThreads) void radix_downsweep_kernel(
     const uint64_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, int64_t n,
     const uint32_t* __restrict__ n_dev, bool drop_sentinel, int shift, int64_t num_chunks,
@@ -237,9 +244,11 @@ __global__ __launch_bounds__(kDownThreads) void radix_downsweep_kernel(
     uint32_t* __restrict__ vals_out) {
     __shared__ uint64_t s_keys[kSortChunk];
     __shared__ uint32_t s_vals[kPairs ? kSortChunk : 1];
-    __shared__ uint32_t s_cnt[kDownWaves][kRadix];  // wave-private counters, then wave starts
-    __shared__ uint32_t s_local[kRadix];            // start of each digit in the reordered chunk
-    __shared__ uint32_t s_global[kRadix];           // output position of that start
+    constexpr int kBins = 1 << kBits;
+    static_assert(kBins <= kDownThreads, "one thread per digit");
+    __shared__ uint32_t s_cnt[kDownWaves][kBins];  // wave-private counters, then wave starts
+    __shared__ uint32_t s_local[kBins];            // start of each digit in the reordered chunk
+    __shared__ uint32_t s_global[kBins];           // output position of that start
     __shared__ uint32_t s_wave[kDownWaves];
     __shared__ uint32_t s_kept;                     // keys of the chunk that are moved
     const int lane = threadIdx.x & (kWave - 1);
@@ -248,7 +257,7 @@ __global__ __launch_bounds__(kDownThreads) void radix_downsweep_kernel(
     if (n_dev != nullptr) n = min(n, (int64_t)*n_dev);
     if (base >= n) return;  // uniform: a chunk past the live count has nothing to move
     const int chunk_count = (int)min((int64_t)kSortChunk, n - base);
-    for (int i = threadIdx.x; i < kDownWaves * kRadix; i += kDownThreads) (&s_cnt[0][0])[i] = 0;
+    for (int i = threadIdx.x; i < kDownWaves * kBins; i += kDownThreads) (&s_cnt[0][0])[i] = 0;
     __syncthreads();
     // 1. per wave: stable ranks among equal digits (rank = keys of the digit before it in this
     //    wave's eighth of the chunk), packed as digit << 16 | rank
@@ -267,10 +276,10 @@ __global__ __launch_bounds__(kDownThreads) void radix_downsweep_kernel(
     for (int r = 0; r < kDownRounds; ++r) {
         const int local = wave * kDownWaveKeys + r * kWave + lane;
         const bool valid = local < chunk_count && !(drop_sentinel && key[r] == kSentinelKey);
-        const uint32_t d = digit_of(key[r], shift);
+        const uint32_t d = digit_of<kBits>(key[r], shift);
         uint64_t peers = __ballot(valid);
 #pragma unroll
-        for (int b = 0; b < kRadixBits; ++b) {
+        for (int b = 0; b < kBits; ++b) {
             const bool bit = ((d >> b) & 1u) != 0;
             const uint64_t m = __ballot(bit);
             peers &= bit ? m : ~m;
@@ -290,14 +299,14 @@ __global__ __launch_bounds__(kDownThreads) void radix_downsweep_kernel(
         uint32_t cnt = 0;
 #pragma unroll
         for (int w = 0; w < kDownWaves; ++w) {
-            c[w] = t < kRadix ? s_cnt[w][t] : 0u;
+            c[w] = t < kBins ? s_cnt[w][t] : 0u;
             cnt += c[w];
         }
         uint32_t kept, dummy;
-        const uint32_t start = digit_exclusive_scan(cnt, s_wave, kept);
-        const uint32_t digit_base = digit_exclusive_scan(t < kRadix ? totals[t] : 0u, s_wave, dummy);
+        const uint32_t start = digit_exclusive_scan<kBins>(cnt, s_wave, kept);
+        const uint32_t digit_base = digit_exclusive_scan<kBins>(t < kBins ? totals[t] : 0u, s_wave, dummy);
         if (t == 0) s_kept = kept;
-        if (t < kRadix) {
+        if (t < kBins) {
             s_local[t] = start;
             s_global[t] = digit_base + offsets[(int64_t)t * num_chunks + blockIdx.x];
             uint32_t run = start;
@@ -323,7 +332,7 @@ __global__ __launch_bounds__(kDownThreads) void radix_downsweep_kernel(
     const int kept_count = (int)s_kept;
     for (int i = threadIdx.x; i < kept_count; i += kDownThreads) {
         const uint64_t k = s_keys[i];
-        const uint32_t d = digit_of(k, shift);
+        const uint32_t d = digit_of<kBits>(k, shift);
         const uint32_t pos = s_global[d] + ((uint32_t)i - s_local[d]);
         keys_out[pos] = k;
         if (kPairs) vals_out[pos] = s_vals[i];
@@ -339,32 +348,43 @@ namespace {
 // n_dev: see radix_upsweep_kernel. compact_first: the first pass reads all n keys and drops the
 // sentinel keys (stably compacting the rest to the front), its row scan adds the number of kept
 // keys to *n_dev (zero beforehand), and the later passes sort that many.
-template <bool kPairs>
+template <int kBits>
+size_t radix_temp_bytes(int64_t n) {
+    int64_t chunks = (n + kSortChunk - 1) / kSortChunk;
+    if (chunks < 1) chunks = 1;
+    const int64_t hist_count = chunks * (1 << kBits);
+    // hist + offsets + totals
+    return (size_t)(2 * hist_count + (1 << kBits)) * sizeof(uint32_t) + 256;
+}
+
+template <bool kPairs, int kBits>
 gsx_hip_status radix_sort_u64(uint64_t* keys, uint32_t* vals, uint64_t* keys_alt, uint32_t* vals_alt, int64_t n,
                               uint32_t* n_dev, bool compact_first, int begin_bit, int end_bit, void* temp,
                               int* out_in_alt, hipStream_t stream) {
+    constexpr int kBins = 1 << kBits;
     if (begin_bit < 0 || end_bit > 64 || begin_bit > end_bit) return GSX_HIP_ERROR_INVALID_ARGUMENT;
     if (n > (int64_t)UINT32_MAX) return GSX_HIP_ERROR_OUT_OF_RANGE;
     int64_t chunks = (n + kSortChunk - 1) / kSortChunk;
     if (chunks < 1) chunks = 1;
-    const int64_t hist_count = chunks * kRadix;
+    const int64_t hist_count = chunks * kBins;
     uint32_t* hist = static_cast<uint32_t*>(temp);
     uint32_t* offsets = hist + hist_count;
     uint32_t* totals = offsets + hist_count;
     int in_alt = 0;
     if (n > 0) {
-        for (int shift = begin_bit; shift < end_bit; shift += kRadixBits) {
+        for (int shift = begin_bit; shift < end_bit; shift += kBits) {
             uint64_t* kin = in_alt ? keys_alt : keys;
             uint32_t* vin = in_alt ? vals_alt : vals;
             uint64_t* kout = in_alt ? keys : keys_alt;
             uint32_t* vout = in_alt ? vals : vals_alt;
             const bool drop = compact_first && shift == begin_bit;
             const uint32_t* live = drop ? nullptr : n_dev;
-            hipLaunchKernelGGL(radix_upsweep_kernel, dim3((unsigned)chunks), dim3(kSortThreads), 0, stream, kin, n,
-                               live, drop, shift, chunks, hist);
-            hipLaunchKernelGGL(radix_rowscan_kernel, dim3(kRadix), dim3(kSortThreads), 0, stream, hist, chunks,
+            hipLaunchKernelGGL(radix_upsweep_kernel<kBits>, dim3((unsigned)chunks), dim3(kSortThreads), 0, stream, kin,
+                               n, live, drop, shift, chunks, hist);
+            hipLaunchKernelGGL(radix_rowscan_kernel, dim3(kBins), dim3(kSortThreads), 0, stream, hist, chunks,
                                offsets, totals, drop ? n_dev : nullptr);
-            hipLaunchKernelGGL(radix_downsweep_kernel<kPairs>, dim3((unsigned)chunks), dim3(kDownThreads), 0, stream,
+            hipLaunchKernelGGL((radix_downsweep_kernel<kPairs, kBits>), dim3((unsigned)chunks), dim3(kDownThreads), 0,
+                               stream,
                                kin, vin, n, live, drop, shift, chunks, offsets, totals, kout, vout);
             in_alt ^= 1;
         }
@@ -395,30 +415,23 @@ gsx_hip_status gsx_hip_scan_exclusive_u32(const uint32_t* in, uint32_t* out, int
     return (gsx_hip_status)hipGetLastError();
 }
 
-size_t gsx_hip_radix_sort_temp_bytes(int64_t n) {
-    int64_t chunks = (n + kSortChunk - 1) / kSortChunk;
-    if (chunks < 1) chunks = 1;
-    const int64_t hist_count = chunks * kRadix;
-    // hist + offsets + totals
-    return (size_t)(2 * hist_count + kRadix) * sizeof(uint32_t) + 256;
-}
-
+size_t gsx_hip_radix_sort_temp_bytes(int64_t n) { return radix_temp_bytes<kRadixBits>(n); }
 
 // Stable LSD sort of n pairs on key bits [begin_bit, end_bit). The result ends in (keys, vals)
 // when *out_in_alt == 0, else in (keys_alt, vals_alt).
 gsx_hip_status gsx_hip_radix_sort_pairs_u64(uint64_t* keys, uint32_t* vals, uint64_t* keys_alt, uint32_t* vals_alt,
                                             int64_t n, int begin_bit, int end_bit, void* temp, int* out_in_alt,
                                             hipStream_t stream) {
-    return radix_sort_u64<true>(keys, vals, keys_alt, vals_alt, n, nullptr, false, begin_bit, end_bit, temp,
-                                out_in_alt, stream);
+    return radix_sort_u64<true, kRadixBits>(keys, vals, keys_alt, vals_alt, n, nullptr, false, begin_bit, end_bit,
+                                            temp, out_in_alt, stream);
 }
 
 // Stable LSD sort of n keys on bits [begin_bit, end_bit); bits outside the range travel with
 // the key (a payload packed into the low bits keeps input order among equal sort bits).
 gsx_hip_status gsx_hip_radix_sort_keys_u64(uint64_t* keys, uint64_t* keys_alt, int64_t n, int begin_bit, int end_bit,
                                            void* temp, int* out_in_alt, hipStream_t stream) {
-    return radix_sort_u64<false>(keys, nullptr, keys_alt, nullptr, n, nullptr, false, begin_bit, end_bit, temp,
-                                 out_in_alt, stream);
+    return radix_sort_u64<false, kRadixBits>(keys, nullptr, keys_alt, nullptr, n, nullptr, false, begin_bit, end_bit,
+                                             temp, out_in_alt, stream);
 }
 
 }  // extern "C"
@@ -429,8 +442,10 @@ gsx_hip_status radix_sort_keys_u64_compacting(uint64_t* keys, uint64_t* keys_alt
                                               int begin_bit, int end_bit, void* temp, int* out_in_alt,
                                               hipStream_t stream) {
     if (begin_bit >= end_bit) return GSX_HIP_ERROR_INVALID_ARGUMENT;  // the compacting pass must run
-    return radix_sort_u64<false>(keys, nullptr, keys_alt, nullptr, n, n_live, true, begin_bit, end_bit, temp,
-                                 out_in_alt, stream);
+    return radix_sort_u64<false, kCompactingRadixBits>(keys, nullptr, keys_alt, nullptr, n, n_live, true, begin_bit,
+                                                       end_bit, temp, out_in_alt, stream);
 }
+
+size_t radix_sort_keys_u64_compacting_temp_bytes(int64_t n) { return radix_temp_bytes<kCompactingRadixBits>(n); }
 
 }  // namespace gsx_amd
