@@ -23,11 +23,13 @@
 #if defined(__HIPCC__)
 #define GSX_HD __host__ __device__ inline
 #define GSX_FMA(a, b, c) __builtin_fma((a), (b), (c))
+#define GSX_FMAF(a, b, c) __builtin_fmaf((a), (b), (c))
 #else
 #include <math.h>
 #include <string.h>
 #define GSX_HD static inline
 #define GSX_FMA(a, b, c) fma((a), (b), (c))
+#define GSX_FMAF(a, b, c) fmaf((a), (b), (c))
 #endif
 
 /* 2^(i/32) rounded to nearest double, with i << 47 subtracted from the bit pattern so that

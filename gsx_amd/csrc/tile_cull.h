@@ -14,7 +14,8 @@
  *            when power < thr + 1e-3, and the 1e-3 dwarfs every float rounding in between),
  *   q_cut  = -2 * thr,
  *   q_min  = minimum of the quadratic form over the rectangle (0 when it holds the centre,
- *            otherwise the least of its four edge minima),
+ *            otherwise the least of its four corner values and the values at the edges'
+ *            interior stationary points),
  *   margin = 1e-4 * (largest term magnitude over the rectangle) + 1e-3, which exceeds the float
  *            rounding of both q_min and the per-pixel power by orders of magnitude,
  *   drop   iff q_min - margin > q_cut.
@@ -65,20 +66,6 @@ GSX_HD float gsx_tile_qcut(float opacity)
     return -2.0f * (thr - 1e-3f);
 }
 
-/* Minimum of A u^2 + 2 B u v + C v^2 over the segment u = ue, v in [v0, v1]; rC = 1 / C. */
-GSX_HD float gsx_cull_edge_min(float A, float B, float C, float rC, float ue, float v0, float v1)
-{
-    float q0 = A * ue * ue + 2.0f * B * ue * v0 + C * v0 * v0;
-    float q1 = A * ue * ue + 2.0f * B * ue * v1 + C * v1 * v1;
-    float m = gsx_cull_minf(q0, q1);
-
-    if(C > 0.0f) {
-        float v = gsx_cull_clampf(-(B * ue) * rC, v0, v1);
-        m = gsx_cull_minf(m, A * ue * ue + 2.0f * B * ue * v + C * v * v);
-    }
-    return m;
-}
-
 /* Per-Gaussian constants of the test: conic (A, B, C) = (inv_a, inv_b, inv_c), their
  * reciprocals for the edge minima, and q_cut. */
 typedef struct gsx_tile_conic {
@@ -101,27 +88,56 @@ GSX_HD gsx_tile_conic gsx_tile_conic_make(float mx, float my, float inv_a, float
 }
 
 /* Nonzero when some pixel centre of the inclusive pixel rectangle [px0, px1] x [py0, py1] (the
- * tile clipped to the Gaussian's box) may receive a contribution from the Gaussian. */
+ * tile clipped to the Gaussian's box) may receive a contribution from the Gaussian.
+ * q(u, v) = A u^2 + 2 B u v + C v^2 is evaluated as fma(C v, v, fma(2 B u, v, (A u) u)); the four
+ * corner values are shared by the two edges through each corner, and each edge adds the value at
+ * its interior stationary point (clamped to the edge) when the quadratic is convex along it. */
 GSX_HD int gsx_tile_conic_test(const gsx_tile_conic *k, int px0, int px1, int py0, int py1)
 {
-    const float mx = k->mx, my = k->my, A = k->A, B = k->B, C = k->C, rA = k->rA, rC = k->rC, qcut = k->qcut;
-    const float dx0 = ((float)px0 + 0.5f) - mx;
-    const float dx1 = ((float)px1 + 0.5f) - mx;
-    const float dy0 = ((float)py0 + 0.5f) - my;
-    const float dy1 = ((float)py1 + 0.5f) - my;
+    const float A = k->A, B = k->B, C = k->C, rA = k->rA, rC = k->rC, qcut = k->qcut;
+    const float B2 = 2.0f * B;
+    const float dx0 = ((float)px0 + 0.5f) - k->mx;
+    const float dx1 = ((float)px1 + 0.5f) - k->mx;
+    const float dy0 = ((float)py0 + 0.5f) - k->my;
+    const float dy1 = ((float)py1 + 0.5f) - k->my;
     const float X = gsx_cull_absf(dx0) > gsx_cull_absf(dx1) ? gsx_cull_absf(dx0) : gsx_cull_absf(dx1);
     const float Y = gsx_cull_absf(dy0) > gsx_cull_absf(dy1) ? gsx_cull_absf(dy0) : gsx_cull_absf(dy1);
     const float scale = gsx_cull_absf(A) * X * X + 2.0f * gsx_cull_absf(B) * X * Y + gsx_cull_absf(C) * Y * Y;
     const float margin = 1e-4f * scale + 1e-3f;
-    float qmin;
+    float au0, au1, bu0, bu1, cv0, cv1, qmin, s, q;
 
     if(dx0 <= 0.0f && dx1 >= 0.0f && dy0 <= 0.0f && dy1 >= 0.0f) {
         return 1;
     }
-    qmin = gsx_cull_edge_min(A, B, C, rC, dx0, dy0, dy1);
-    qmin = gsx_cull_minf(qmin, gsx_cull_edge_min(A, B, C, rC, dx1, dy0, dy1));
-    qmin = gsx_cull_minf(qmin, gsx_cull_edge_min(C, B, A, rA, dy0, dx0, dx1));
-    qmin = gsx_cull_minf(qmin, gsx_cull_edge_min(C, B, A, rA, dy1, dx0, dx1));
+    au0 = (A * dx0) * dx0;
+    au1 = (A * dx1) * dx1;
+    bu0 = B2 * dx0;
+    bu1 = B2 * dx1;
+    cv0 = C * dy0;
+    cv1 = C * dy1;
+    /* corners */
+    qmin = GSX_FMAF(cv0, dy0, GSX_FMAF(bu0, dy0, au0));
+    qmin = gsx_cull_minf(qmin, GSX_FMAF(cv1, dy1, GSX_FMAF(bu0, dy1, au0)));
+    qmin = gsx_cull_minf(qmin, GSX_FMAF(cv0, dy0, GSX_FMAF(bu1, dy0, au1)));
+    qmin = gsx_cull_minf(qmin, GSX_FMAF(cv1, dy1, GSX_FMAF(bu1, dy1, au1)));
+    /* vertical edges u = dx0, dx1: stationary point v = -(B u) / C */
+    if(C > 0.0f) {
+        s = gsx_cull_clampf(-(B * dx0) * rC, dy0, dy1);
+        q = GSX_FMAF(C * s, s, GSX_FMAF(bu0, s, au0));
+        qmin = gsx_cull_minf(qmin, q);
+        s = gsx_cull_clampf(-(B * dx1) * rC, dy0, dy1);
+        q = GSX_FMAF(C * s, s, GSX_FMAF(bu1, s, au1));
+        qmin = gsx_cull_minf(qmin, q);
+    }
+    /* horizontal edges v = dy0, dy1: stationary point u = -(B v) / A */
+    if(A > 0.0f) {
+        s = gsx_cull_clampf(-(B * dy0) * rA, dx0, dx1);
+        q = GSX_FMAF(cv0, dy0, GSX_FMAF(B2 * s, dy0, (A * s) * s));
+        qmin = gsx_cull_minf(qmin, q);
+        s = gsx_cull_clampf(-(B * dy1) * rA, dx0, dx1);
+        q = GSX_FMAF(cv1, dy1, GSX_FMAF(B2 * s, dy1, (A * s) * s));
+        qmin = gsx_cull_minf(qmin, q);
+    }
     return !(qmin - margin > qcut); /* keeps the instance for NaN input too */
 }
 
