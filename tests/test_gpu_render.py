@@ -37,10 +37,18 @@ def _workloads():
         "c2_small": lambda: scenes.config2(n=20_000, size=128),
         "c3_small": lambda: scenes.config3(n=30_000, width=240, height=135),
         "c4_small": lambda: scenes.config4(n=3_000, width=160, height=96),
+        # 1080p with few Gaussians: five near-plane boxes cover all 8160 tiles (emitted in 1024-tile
+        # chunks, their instance runs summed in 16 chunks), fifteen runs exceed 32 instances
+        "c3_1080": lambda: scenes.config3(n=20_000, width=1920, height=1080),
+        # every Gaussian at depth exactly 4 (z = 0 facing the default camera): each tile's list is
+        # ordered by Gaussian index alone, which the depth sort must keep through its compaction
+        "ties": lambda: scenes.Workload("ties", scenes.plane_scene(5, 3_000, logscale=(-4.0, -3.0), z_sd=0.0),
+                                        scenes.camera(160, 120, 200.0)),
     }
 
 
-@pytest.mark.parametrize("name", ["c0_small", "c1_small", "c0_full", "c2_small", "c3_small", "c4_small"])
+@pytest.mark.parametrize("name", ["c0_small", "c1_small", "c0_full", "c2_small", "c3_small", "c4_small", "c3_1080",
+                                  "ties"])
 def test_forward_image_bit_exact(oracle, name):
     w = _workloads()[name]()
     print(f"[case] forward {name} n={w.scene.count} {int(w.camera[4])}x{int(w.camera[5])}", flush=True)
@@ -59,7 +67,7 @@ def test_forward_image_bit_exact(oracle, name):
     assert np.array_equal(t.cpu().numpy().reshape(ref_t.shape), ref_t)
 
 
-@pytest.mark.parametrize("name", ["c0_small", "c3_small", "c4_small"])
+@pytest.mark.parametrize("name", ["c0_small", "c3_small", "c4_small", "c3_1080", "ties"])
 def test_sorted_keys_and_ranges_bit_exact(oracle, name):
     import ctypes
     w = _workloads()[name]()
@@ -106,7 +114,7 @@ def test_sorted_keys_and_ranges_bit_exact(oracle, name):
     assert int((nonempty[:, 1] - nonempty[:, 0]).sum()) == st.instance_count
 
 
-@pytest.mark.parametrize("name", ["c0_small", "c1_small", "c3_small"])
+@pytest.mark.parametrize("name", ["c0_small", "c1_small", "c3_small", "c3_1080", "ties"])
 def test_backward_gradients(oracle, name):
     w = _workloads()[name]()
     print(f"[case] backward {name}", flush=True)
