@@ -174,8 +174,8 @@ struct gsx_hip_render_context {
     DeviceBuffer rec, cov_coef, ckpt, inst_gauss, inst_grad, tile_count, big_list, offsets, scan_temp, keys, vals,
         keys_alt, sort_temp, ranges, sorted_g, final_t, last, grad2d, depth_keys, depth_keys_alt, rank_g, rank_count,
         g_rank, long_list, counters, big_chunk_counts, depth_sort_temp;
-    uint32_t* host_count = nullptr;  // pinned
-    hipEvent_t count_ev = nullptr;   // the instance count has reached host_count
+    unsigned long long* host_count = nullptr;  // pinned
+    hipEvent_t count_ev = nullptr;             // the instance count has reached host_count
     CameraParams cam{};
     gsx_hip_gaussians gs{};
     int64_t instance_count = 0;
@@ -336,7 +336,8 @@ gsx_hip_status gsx_hip_render_context_create(gsx_hip_render_context** out_contex
     *out_context = nullptr;
     gsx_hip_render_context* ctx = new (std::nothrow) gsx_hip_render_context();
     if (ctx == nullptr) return fail(GSX_HIP_ERROR_OUT_OF_MEMORY, "render context allocation failed");
-    hipError_t e = hipHostMalloc(reinterpret_cast<void**>(&ctx->host_count), sizeof(uint32_t) * 2, hipHostMallocDefault);
+    hipError_t e =
+        hipHostMalloc(reinterpret_cast<void**>(&ctx->host_count), sizeof(unsigned long long), hipHostMallocDefault);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->count_ev, hipEventDisableTiming);
     if (e != hipSuccess) {
         (void)gsx_hip_render_context_destroy(ctx);
@@ -463,8 +464,8 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     if (train) GSX_TRY(ctx->cov_coef.reserve(n1 * 2 * sizeof(float4), "cov_coef"));
     GSX_TRY(ctx->tile_count.reserve(n1 * sizeof(uint32_t), "tile_count"));
     // list counters: [0] visible Gaussians (depth keys), [1] big boxes, [2] long instance runs,
-    // [3] instances
-    GSX_TRY(ctx->counters.reserve(4 * sizeof(uint32_t), "counters"));
+    // [4..5] instances (64 bits)
+    GSX_TRY(ctx->counters.reserve(8 * sizeof(uint32_t), "counters"));
     GSX_TRY(ctx->big_list.reserve(n1 * sizeof(uint32_t), "big_list"));
     GSX_TRY(ctx->big_chunk_counts.reserve(n1 * kBigChunks * sizeof(uint32_t), "big_chunk_counts"));
     GSX_TRY(ctx->offsets.reserve((size_t)(n + 1) * sizeof(uint32_t), "offsets"));
@@ -504,7 +505,7 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     }
     GSX_TRY(record(ctx, 0, stream));
     if (n > 0) {
-        hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(64), 0, stream, counters, (int64_t)4, 0u);
+        hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(64), 0, stream, counters, (int64_t)8, 0u);
         hipLaunchKernelGGL(preprocess_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, n, gaussians->mean3d,
                            gaussians->rotation, gaussians->logscale, gaussians->opacity, gaussians->sh0,
                            gaussians->sh1, gaussians->sh2, gaussians->sh3, (int)gaussians->sh_degree, cam,
@@ -524,11 +525,14 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     // waits for the count and sizes the instance buffers
     if (n > 0) {
         hipLaunchKernelGGL(sum_u32_kernel, dim3(std::min(blocks_for(n, 256 * 16), 1024u)), dim3(256), 0, stream,
-                           ctx->tile_count.as<uint32_t>(), n, counters + 3);
+                           ctx->tile_count.as<uint32_t>(), n, reinterpret_cast<unsigned long long*>(counters + 4));
         GSX_HIP_TRY(hipGetLastError(), "sum_u32_kernel");
+        GSX_HIP_TRY(hipMemcpyAsync(ctx->host_count, counters + 4, sizeof(unsigned long long), hipMemcpyDeviceToHost,
+                                   stream),
+                    "instance count readback");
+    } else {
+        ctx->host_count[0] = 0;  // no kernel wrote the counters
     }
-    GSX_HIP_TRY(hipMemcpyAsync(ctx->host_count, counters + 3, sizeof(uint32_t), hipMemcpyDeviceToHost, stream),
-                "instance count readback");
     GSX_HIP_TRY(hipEventRecord(ctx->count_ev, stream), "hipEventRecord(count)");
     GSX_TRY(record(ctx, 1, stream));
     // depth order of the Gaussians, then their tile counts in that order and its scan
@@ -550,6 +554,10 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
                                        ctx->scan_temp.ptr, stream));
     GSX_TRY(record(ctx, 2, stream));
     GSX_HIP_TRY(hipEventSynchronize(ctx->count_ev), "instance count sync");
+    if (ctx->host_count[0] > (unsigned long long)UINT32_MAX) {
+        // positions, offsets and the sort run in 32 bits; nothing has been emitted yet
+        return fail(GSX_HIP_ERROR_OUT_OF_RANGE, "more than 2^32 - 1 (tile, Gaussian) instances");
+    }
     const int64_t count = (int64_t)ctx->host_count[0];
     ctx->instance_count = count;
     const size_t c1 = (size_t)(count > 0 ? count : 1);

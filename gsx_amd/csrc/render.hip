@@ -372,22 +372,20 @@ __global__ __launch_bounds__(256) void big_tiles_kernel(const uint32_t* __restri
     }
 }
 
-// *out += sum of in[0..n) (out zeroed beforehand; one atomic per workgroup, grid-stride).
+// *out += sum of in[0..n) in 64 bits (out zeroed beforehand; grid-stride, each thread adds its
+// partial to an LDS total, one global atomic per workgroup), so a total past 2^32 is seen
+// rather than wrapped.
 __global__ __launch_bounds__(256) void sum_u32_kernel(const uint32_t* __restrict__ in, int64_t n,
-                                                      uint32_t* __restrict__ out) {
-    __shared__ uint32_t s_wave[kWavesPerBlock];
-    uint32_t v = 0;
+                                                      unsigned long long* __restrict__ out) {
+    __shared__ unsigned long long s_total;
+    if (threadIdx.x == 0) s_total = 0ull;
+    __syncthreads();
+    unsigned long long v = 0;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
         v += in[i];
-#pragma unroll
-    for (int off = kWave / 2; off > 0; off >>= 1) v += (uint32_t)__shfl_xor((int)v, off, kWave);
-    if (__lane_id() == 0) s_wave[threadIdx.x / kWave] = v;
+    if (v != 0ull) atomicAdd(&s_total, v);
     __syncthreads();
-    if (threadIdx.x == 0) {
-        uint32_t total = 0;
-        for (int w = 0; w < kWavesPerBlock; ++w) total += s_wave[w];
-        if (total > 0) atomicAdd(out, total);
-    }
+    if (threadIdx.x == 0 && s_total != 0ull) atomicAdd(out, s_total);
 }
 
 __global__ __launch_bounds__(256) void fill_u32_kernel(uint32_t* __restrict__ p, int64_t count, uint32_t v) {

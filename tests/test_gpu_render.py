@@ -175,6 +175,24 @@ def test_empty_and_fully_culled_scenes(oracle):
     assert float(grads.mean3d.abs().max()) == 0.0
 
 
+def test_context_reuse_then_empty_scene(oracle):
+    # the list counters of a context are rebuilt by every forward, also by one without Gaussians
+    from gsx_amd import scenes
+    from gsx_amd.backend import GaussianTensors
+    w = scenes.config0(n=500, width=64, height=48)
+    r, cam, g = _setup(w)
+    r.render(cam, g, train=False)
+    torch.cuda.synchronize()
+    assert r.stats().instance_count > 0
+    sc = w.scene
+    empty = scenes.Scene(*(np.ascontiguousarray(a[:0]) for a in (sc.mean3d, sc.rotation, sc.logscale, sc.opacity,
+                                                                  sc.sh0)))
+    img = r.render(cam, GaussianTensors.from_scene(empty), train=False)
+    torch.cuda.synchronize()
+    assert r.stats().instance_count == 0
+    assert np.array_equal(img.cpu().numpy(), oracle.render(empty, w.camera)[0])
+
+
 def test_background_only_pixels(oracle):
     from gsx_amd import scenes
     w = scenes.config0(n=50, width=64, height=48)
