@@ -134,7 +134,9 @@ gsx_hip_status gsx_hip_render_context_destroy(gsx_hip_render_context* context);
  * visible_counter is non-null, adds 1 to it for every visible Gaussian (gsx-cpu/render.c:
  * 980-982). The Gaussian arrays are borrowed: the backward reads them again, so they must be
  * unchanged until then (gsx borrow_train_state = true). One host synchronisation per forward
- * reads the instance count. */
+ * reads the instance count (the GPU keeps working on the depth order meanwhile); a count above
+ * 2^32 - 1 (tile, Gaussian) instances fails with GSX_HIP_ERROR_OUT_OF_RANGE before anything is
+ * emitted. */
 gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* context, const gsx_hip_camera* camera,
                                       const gsx_hip_gaussians* gaussians, int32_t train, float* out_rgb,
                                       float* visible_counter, hipStream_t stream);
