@@ -76,6 +76,10 @@ STAGE_KERNEL = {"preprocess": "preprocess_kernel", "emit": "emit_keys_kernel", "
                 "projection_backward": "projection_backward_kernel", "loss_forward": "ssim_forward_kernel",
                 "loss_backward": "ssim_backward_kernel", "adam": "adam_multi_kernel"}
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_metric.txt")
+SQ_FILE = os.path.join(ROOT, "profiles", "sq_counters_metric.md")
+# Nominal VALU issue peak: 256 CUs x 4 SIMDs x 2.4 GHz, one wave64 instruction per 4 cycles on a
+# 16-lane SIMD (some instruction mixes issue faster, so this is a reference, not a hard ceiling).
+VALU_PEAK_GINSTR = 256 * 4 * 2.4 / 4.0
 
 
 def measured_traffic(kernel):
@@ -88,6 +92,22 @@ def measured_traffic(kernel):
             parts = line.split()
             if len(parts) >= 4 and parts[0] == "traffic" and parts[1] == kernel:
                 return int(float(parts[-1]))
+    return None
+
+
+def profiled_valu_instructions(kernel):
+    """VALU wave instructions per launch of `kernel` from the committed rocprofv3 SQ_INSTS_VALU
+    summary, or None."""
+    if kernel is None or not os.path.exists(SQ_FILE):
+        return None
+    with open(SQ_FILE) as f:
+        for line in f:
+            cells = [c.strip() for c in line.strip().strip("|").split("|")]
+            if len(cells) >= 7 and cells[0] == kernel:
+                try:
+                    return int(float(cells[6]))
+                except ValueError:
+                    return None
     return None
 
 
@@ -288,6 +308,15 @@ def main():
     kernels.sort(key=lambda k: -k["ms"])
     dominant = kernels[0]
     sort_entry = next(k for k in kernels if k["stage"] == "sort")
+    # the dominant kernel is bound by VALU issue rather than HBM: its wave instructions per launch
+    # (committed SQ profile of this workload) over the launch time measured above
+    valu_instr = profiled_valu_instructions(STAGE_KERNEL.get(dominant["stage"]))
+    valu_issue = None
+    if valu_instr is not None and dominant["ms"] > 0:
+        rate = valu_instr / (dominant["ms"] * 1e-3) / 1e9
+        valu_issue = {"kernel": STAGE_KERNEL.get(dominant["stage"]), "instructions": valu_instr,
+                      "achieved": round(rate, 1), "peak": VALU_PEAK_GINSTR, "unit": "G wave-instr/s",
+                      "frac": round(rate / VALU_PEAK_GINSTR, 4)}
 
     result = {
         "metric": "fwd+bwd train iters/sec @1M Gaussians 1920x1080; fwd render FPS; sort GB/s",
@@ -314,6 +343,7 @@ def main():
                      "achieved": dominant["gbps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": dominant["hbm_frac"], "traffic": measured_traffic(STAGE_KERNEL.get(dominant["stage"])),
                      "algorithmic_bytes": dominant["algorithmic_bytes"], "launch_ms": dominant["ms"]},
+        "valu_issue": valu_issue,
         "device": dev_name,
     }
 
