@@ -310,6 +310,19 @@ __device__ inline Projected preprocess_one(int64_t g, const float* __restrict__ 
 
 // ---- wave64 helpers ------------------------------------------------------------------------
 
+// Mask of the active lanes whose p is true. A bool that the compiler already holds as a lane
+// mask is copied with scalar instructions (HIP's __ballot compares an integer and spends two
+// vector instructions on it).
+__device__ inline uint64_t wave_ballot(bool p) { return __builtin_amdgcn_ballot_w64(p); }
+
+// True when no active lane has p: the mask is pinned in scalar registers first, so the test is a
+// scalar compare (a branch on `ballot == 0` is otherwise selected as a vector select + compare).
+__device__ inline bool wave_none(bool p) {
+    uint64_t m = __builtin_amdgcn_ballot_w64(p);
+    asm volatile("" : "+s"(m));
+    return m == 0ull;
+}
+
 __device__ inline uint64_t lanemask_lt() {
     const uint32_t lane = __lane_id();
     return lane == 0 ? 0ull : (~0ull >> (64 - lane));

@@ -145,7 +145,7 @@ __device__ inline void walk_wave_tiles(WaveBoxes& w, uint32_t wave_total, int32_
             const gsx_tile_conic con = w.conic[owner];
             keep = gsx_tile_conic_test(&con, px0, px1, py0, py1) != 0;
         }
-        const uint64_t mask = __ballot(keep);
+        const uint64_t mask = wave_ballot(keep);
         // first lane of this step holding the owner's pairs
         const uint32_t seg_first = w.excl[owner] > base ? w.excl[owner] - base : 0u;
         const uint64_t seg = ~((seg_first == 0 ? 0ull : (~0ull >> (64 - seg_first))));
@@ -349,7 +349,7 @@ __global__ __launch_bounds__(256) void big_tiles_kernel(const uint32_t* __restri
                 const int py0 = max((int)ty * kTile, y0), py1 = min((int)ty * kTile + kTile - 1, y1);
                 keep = gsx_tile_conic_test(&con, px0, px1, py0, py1) != 0;
             }
-            const uint64_t mask = __ballot(keep);
+            const uint64_t mask = wave_ballot(keep);
             if (lane == 0) s_wave[wave] = (uint32_t)__popcll(mask);
             __syncthreads();
             uint32_t before = 0, step_total = 0;
@@ -425,7 +425,7 @@ __device__ inline int xcd_tile_index(int block, int tiles) {
 }
 
 __device__ inline bool in_box(int px, int py, uint32_t bx, uint32_t by) {
-    return px >= (int)(bx & 0xffffu) && px <= (int)(bx >> 16) && py >= (int)(by & 0xffffu) && py <= (int)(by >> 16);
+    return (px >= (int)(bx & 0xffffu)) & (px <= (int)(bx >> 16)) & (py >= (int)(by & 0xffffu)) & (py <= (int)(by >> 16));
 }
 
 // Transmittance checkpoints: the backward needs every contribution's exact T_before (the CPU
@@ -466,11 +466,13 @@ __global__ __launch_bounds__(kBlendThreads) void blend_forward_kernel(
     const uint2 range = ranges[tile];
     const float fpx = (float)px + 0.5f;
     const float fpy = (float)py + 0.5f;
-    float t = 1.0f, c0 = 0.0f, c1 = 0.0f, c2 = 0.0f;
+    // t only falls, and a pixel is done once an accepted contribution takes it below the
+    // threshold, so "done" is t < threshold; pixels outside the image start done (t = 0, never
+    // written out)
+    float t = inside ? 1.0f : 0.0f, c0 = 0.0f, c1 = 0.0f, c2 = 0.0f;
     uint32_t last = range.x;
-    bool done = !inside;
     for (uint32_t base = range.x; base < range.y; base += kBlendThreads) {
-        if (__syncthreads_count(done ? 1 : 0) == kBlendThreads) break;
+        if (__syncthreads_count(t < kTransmittanceThreshold ? 1 : 0) == kBlendThreads) break;
         const uint32_t j = base + threadIdx.x;
         if (j < range.y) {
             const uint32_t g = instance_gaussian[values[j]];
@@ -482,13 +484,14 @@ __global__ __launch_bounds__(kBlendThreads) void blend_forward_kernel(
         __syncthreads();
         const int count = (int)min((uint32_t)kBlendThreads, range.y - base);
         for (int k = 0; k < count; ++k) {
-            if (__ballot(!done) == 0ull) break;  // uniform: every pixel of this wave is saturated
-            if (ckpt != nullptr && !done && (k & (kBucket - 1)) == 0) {
+            const bool open = t >= kTransmittanceThreshold;  // not done
+            if (wave_none(open)) break;  // uniform: every pixel of this wave is saturated
+            if (ckpt != nullptr && open && (k & (kBucket - 1)) == 0) {
                 ckpt[checkpoint_slot(range.x, tile, base + (uint32_t)k) * kBlendThreads + threadIdx.x] = t;
             }
             const float4 r2 = s_r2[k];
-            const bool live = !done && in_box(px, py, __float_as_uint(r2.y), __float_as_uint(r2.z));
-            if (__ballot(live) == 0ull) continue;  // uniform
+            const bool live = open & in_box(px, py, __float_as_uint(r2.y), __float_as_uint(r2.z));  // bitwise: one lane mask
+            if (wave_none(live)) continue;  // uniform
             // branch-free evaluation for the wave; lanes outside the box or done keep their state
             const float4 r0 = s_r0[k];
             const float4 r1 = s_r1[k];
@@ -496,17 +499,16 @@ __global__ __launch_bounds__(kBlendThreads) void blend_forward_kernel(
             const float dy = fpy - r0.y;
             float power = -0.5f * (r0.z * dx * dx + r0.w * dx * dy + r1.x * dy * dy);
             power = power > 0.0f ? 0.0f : power;
-            bool ok = live && power >= kPowerThreshold;
+            bool ok = live & (power >= kPowerThreshold);
             const float gval = gsx_expf_small(ok ? power : 0.0f, s_exp2);
             const float alpha = fminf(kMaxFragmentAlpha, r1.y * gval);
-            ok = ok && alpha >= kMinAlpha;
+            ok = ok & (alpha >= kMinAlpha);
             const float w = alpha * t;
             c0 = ok ? c0 + w * r1.z : c0;
             c1 = ok ? c1 + w * r1.w : c1;
             c2 = ok ? c2 + w * r2.x : c2;
             t = ok ? t * (1.0f - alpha) : t;
             last = ok ? base + (uint32_t)k + 1u : last;
-            done = done || (ok && t < kTransmittanceThreshold);
         }
         __syncthreads();
     }
@@ -663,19 +665,19 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
                     if (i >= n_in) continue;  // uniform
                     const int kk = sb * kBucket + i;
                     const float4 r2 = s_r2[kk];
-                    const bool live = pixel_live && j0 + (uint32_t)i < last &&
+                    const bool live = pixel_live & (j0 + (uint32_t)i < last) &
                                       in_box(px, py, __float_as_uint(r2.y), __float_as_uint(r2.z));
-                    if (__ballot(live) == 0ull) continue;  // uniform
+                    if (wave_none(live)) continue;  // uniform
                     const float4 r0 = s_r0[kk];
                     const float4 r1 = s_r1[kk];
                     const float dx = fpx - r0.x;
                     const float dy = fpy - r0.y;
                     float power = -0.5f * (r0.z * dx * dx + r0.w * dx * dy + r1.x * dy * dy);
                     power = power > 0.0f ? 0.0f : power;
-                    bool ok = live && power >= kPowerThreshold;
+                    bool ok = live & (power >= kPowerThreshold);
                     const float gval = gsx_expf_small(ok ? power : 0.0f, s_exp2);
                     const float alpha = fminf(kMaxFragmentAlpha, r1.y * gval);
-                    ok = ok && alpha >= kMinAlpha;
+                    ok = ok & (alpha >= kMinAlpha);
                     mask |= ok ? (1u << i) : 0u;
                     gv[i] = ok ? gval : 0.0f;
                     tt = ok ? tt * (1.0f - alpha) : tt;
@@ -687,7 +689,7 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
                 if (i >= n_in) continue;  // uniform
                 const int kk = sb * kBucket + i;
                 const bool contrib = ((mask >> i) & 1u) != 0u;
-                if (__ballot(contrib) == 0ull) {  // uniform: no pixel of this wave
+                if (wave_none(contrib)) {  // uniform: no pixel of this wave
                     if (lane < 4 * kGrad2d) s_acc[wave * 4 + lane / kGrad2d][i][lane % kGrad2d] = 0.0f;
                     continue;
                 }
@@ -736,7 +738,10 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
                 s1 += w * r1.w;
                 s2 += w * r2.x;
                 float total8;
-                const float scattered = row_reduce_scatter9(v, total8);
+                float scattered = row_reduce_scatter9(v, total8);
+                // both totals are complete before the stores below: otherwise the compiler sinks the
+                // last DPP adds into the masked store blocks, where they cannot fuse
+                asm volatile("" : "+v"(scattered), "+v"(total8));
                 const uint32_t col = threadIdx.x & (kTile - 1);  // lane within the DPP row
                 if ((col & 1u) == 0u) s_acc[row][i][col >> 1] = scattered;
                 if (col == 0u) s_acc[row][i][8] = total8;

@@ -277,11 +277,11 @@ __global__ __launch_bounds__(kDownThreads) void radix_downsweep_kernel(
         const int local = wave * kDownWaveKeys + r * kWave + lane;
         const bool valid = local < chunk_count && !(drop_sentinel && key[r] == kSentinelKey);
         const uint32_t d = digit_of<kBits>(key[r], shift);
-        uint64_t peers = __ballot(valid);
+        uint64_t peers = wave_ballot(valid);
 #pragma unroll
         for (int b = 0; b < kBits; ++b) {
             const bool bit = ((d >> b) & 1u) != 0;
-            const uint64_t m = __ballot(bit);
+            const uint64_t m = wave_ballot(bit);
             peers &= bit ? m : ~m;
         }
         const uint32_t before = s_cnt[wave][d];  // read by all lanes before the leader updates
