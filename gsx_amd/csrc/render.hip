@@ -482,7 +482,8 @@ __global__ __launch_bounds__(kBlendThreads) void blend_forward_kernel(
             s_r2[threadIdx.x] = rec[3 * (size_t)g + 2];
         }
         __syncthreads();
-        const int count = (int)min((uint32_t)kBlendThreads, range.y - base);
+        // wave-uniform bound, held in a scalar register
+        const int count = __builtin_amdgcn_readfirstlane((int)min((uint32_t)kBlendThreads, range.y - base));
         for (int k = 0; k < count; ++k) {
             const bool open = t >= kTransmittanceThreshold;  // not done
             if (wave_none(open)) break;  // uniform: every pixel of this wave is saturated
@@ -500,7 +501,7 @@ __global__ __launch_bounds__(kBlendThreads) void blend_forward_kernel(
             float power = -0.5f * (r0.z * dx * dx + r0.w * dx * dy + r1.x * dy * dy);
             power = power > 0.0f ? 0.0f : power;
             bool ok = live & (power >= kPowerThreshold);
-            const float gval = gsx_expf_small(ok ? power : 0.0f, s_exp2);
+            const float gval = gsx_expf_small(fmaxf(power, kPowerThreshold), s_exp2);
             const float alpha = fminf(kMaxFragmentAlpha, r1.y * gval);
             ok = ok & (alpha >= kMinAlpha);
             const float w = alpha * t;
@@ -675,7 +676,7 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
                     float power = -0.5f * (r0.z * dx * dx + r0.w * dx * dy + r1.x * dy * dy);
                     power = power > 0.0f ? 0.0f : power;
                     bool ok = live & (power >= kPowerThreshold);
-                    const float gval = gsx_expf_small(ok ? power : 0.0f, s_exp2);
+                    const float gval = gsx_expf_small(fmaxf(power, kPowerThreshold), s_exp2);
                     const float alpha = fminf(kMaxFragmentAlpha, r1.y * gval);
                     ok = ok & (alpha >= kMinAlpha);
                     mask |= ok ? (1u << i) : 0u;
