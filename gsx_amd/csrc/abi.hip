@@ -105,6 +105,34 @@ struct DeviceBuffer {
     }
 };
 
+// Grow-only pinned host buffer that kernels write through its device mapping (the per-workgroup
+// partial instance counts the host sums once the counting kernels have run).
+struct PinnedBuffer {
+    void* host = nullptr;
+    void* dev = nullptr;
+    size_t bytes = 0;
+
+    gsx_hip_status reserve(size_t need, const char* what) {
+        if (need <= bytes) return GSX_HIP_SUCCESS;
+        const size_t grow = need + need / 4 + 4096;
+        release();
+        hipError_t e = hipHostMalloc(&host, grow, hipHostMallocDefault);
+        if (e == hipSuccess) e = hipHostGetDevicePointer(&dev, host, 0);
+        if (e != hipSuccess) {
+            release();
+            return hip_fail(e, what);
+        }
+        bytes = grow;
+        return GSX_HIP_SUCCESS;
+    }
+    void release() {
+        if (host != nullptr) (void)hipHostFree(host);
+        host = nullptr;
+        dev = nullptr;
+        bytes = 0;
+    }
+};
+
 // Workgroups of the big-box passes (grid-stride over the list of big boxes).
 constexpr unsigned kBigBlocks = 512;
 // Workgroups per chunk column of reduce_long_chunks_kernel (4 waves each, grid-stride over the
@@ -174,8 +202,14 @@ struct gsx_hip_render_context {
     DeviceBuffer rec, cov_coef, ckpt, inst_gauss, inst_grad, tile_count, big_list, offsets, scan_temp, keys, vals,
         keys_alt, sort_temp, ranges, sorted_g, final_t, last, grad2d, depth_keys, depth_keys_alt, rank_g, rank_count,
         g_rank, long_list, counters, big_chunk_counts, depth_sort_temp;
-    unsigned long long* host_count = nullptr;  // pinned
-    hipEvent_t count_ev = nullptr;             // the instance count has reached host_count
+    // partial instance counts written by the counting kernels (preprocess: one u32 per workgroup;
+    // big boxes: one u64 per workgroup), summed on the host after count_ev
+    PinnedBuffer kept_parts;
+    hipEvent_t count_ev = nullptr;
+    // counters: [0] visible Gaussians (depth keys), [1] long instance runs, [2 + big_slot] big boxes
+    // of the next forward (each forward's preprocess clears the other slot for its successor)
+    bool counters_ready = false;
+    int big_slot = 0;
     CameraParams cam{};
     gsx_hip_gaussians gs{};
     int64_t instance_count = 0;
@@ -336,9 +370,7 @@ gsx_hip_status gsx_hip_render_context_create(gsx_hip_render_context** out_contex
     *out_context = nullptr;
     gsx_hip_render_context* ctx = new (std::nothrow) gsx_hip_render_context();
     if (ctx == nullptr) return fail(GSX_HIP_ERROR_OUT_OF_MEMORY, "render context allocation failed");
-    hipError_t e =
-        hipHostMalloc(reinterpret_cast<void**>(&ctx->host_count), sizeof(unsigned long long), hipHostMallocDefault);
-    if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->count_ev, hipEventDisableTiming);
+    hipError_t e = hipEventCreateWithFlags(&ctx->count_ev, hipEventDisableTiming);
     if (e != hipSuccess) {
         (void)gsx_hip_render_context_destroy(ctx);
         return hip_fail(e, "render context creation");
@@ -356,7 +388,7 @@ gsx_hip_status gsx_hip_render_context_destroy(gsx_hip_render_context* ctx) {
                            &ctx->depth_keys_alt, &ctx->rank_g, &ctx->rank_count, &ctx->g_rank,
                            &ctx->long_list, &ctx->counters, &ctx->big_chunk_counts, &ctx->depth_sort_temp};
     for (DeviceBuffer* b : all) b->release();
-    if (ctx->host_count != nullptr) (void)hipHostFree(ctx->host_count);
+    ctx->kept_parts.release();
     if (ctx->count_ev != nullptr) (void)hipEventDestroy(ctx->count_ev);
     release_events(ctx);
     delete ctx;
@@ -463,8 +495,6 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     GSX_TRY(ctx->rec.reserve(n1 * 3 * sizeof(float4), "rec"));
     if (train) GSX_TRY(ctx->cov_coef.reserve(n1 * 2 * sizeof(float4), "cov_coef"));
     GSX_TRY(ctx->tile_count.reserve(n1 * sizeof(uint32_t), "tile_count"));
-    // list counters: [0] visible Gaussians (depth keys), [1] big boxes, [2] long instance runs,
-    // [4..5] instances (64 bits)
     GSX_TRY(ctx->counters.reserve(8 * sizeof(uint32_t), "counters"));
     GSX_TRY(ctx->big_list.reserve(n1 * sizeof(uint32_t), "big_list"));
     GSX_TRY(ctx->big_chunk_counts.reserve(n1 * kBigChunks * sizeof(uint32_t), "big_chunk_counts"));
@@ -486,6 +516,11 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     const uint32_t big_chunk =
         std::max<uint32_t>(1024u, ((uint32_t)(tiles + (int)kBigChunks - 1) / kBigChunks + 255u) / 256u * 256u);
     const unsigned big_chunks = (unsigned)std::max<uint32_t>(1u, ((uint32_t)tiles + big_chunk - 1) / big_chunk);
+    const unsigned pre_blocks = blocks_for(n, 256);
+    const size_t big_parts_at = ((size_t)pre_blocks * sizeof(uint32_t) + 7u) / 8u * 8u;
+    const size_t big_parts = (size_t)kBigBlocks * big_chunks;
+    GSX_TRY(ctx->kept_parts.reserve(big_parts_at + big_parts * sizeof(unsigned long long), "kept_parts"));
+    uint32_t* big_count = counters + 2 + ctx->big_slot;
 
     // depth keys of the visible Gaussians: (bits(depth) - bits(near)) << index_bits | index (see
     // KeyLayout), at most 31 + 32 bits, so never the all-ones key that marks invisible ones
@@ -505,34 +540,32 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     }
     GSX_TRY(record(ctx, 0, stream));
     if (n > 0) {
-        hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(64), 0, stream, counters, (int64_t)8, 0u);
-        hipLaunchKernelGGL(preprocess_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, n, gaussians->mean3d,
+        if (!ctx->counters_ready) {
+            hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(64), 0, stream, counters, (int64_t)8, 0u);
+            GSX_HIP_TRY(hipGetLastError(), "fill_u32_kernel");
+            ctx->counters_ready = true;
+        }
+        hipLaunchKernelGGL(preprocess_kernel, dim3(pre_blocks), dim3(256), 0, stream, n, gaussians->mean3d,
                            gaussians->rotation, gaussians->logscale, gaussians->opacity, gaussians->sh0,
                            gaussians->sh1, gaussians->sh2, gaussians->sh3, (int)gaussians->sh_degree, cam,
                            ctx->rec.as<float4>(), train ? ctx->cov_coef.as<float4>() : nullptr,
                            ctx->tile_count.as<uint32_t>(), train ? visible_counter : nullptr,
-                           ctx->big_list.as<uint32_t>(), counters + 1, ctx->depth_keys.as<uint64_t>(), near_bits,
+                           ctx->big_list.as<uint32_t>(), big_count, counters + 1, counters + 2 + (ctx->big_slot ^ 1),
+                           static_cast<uint32_t*>(ctx->kept_parts.dev), ctx->depth_keys.as<uint64_t>(), near_bits,
                            depth_max, index_bits, big_flag ? kBigKeyFlag : 0ull);
         GSX_HIP_TRY(hipGetLastError(), "preprocess_kernel");
+        ctx->big_slot ^= 1;  // the slot this preprocess cleared
         hipLaunchKernelGGL(big_tiles_kernel<false>, dim3(kBigBlocks, big_chunks), dim3(256), 0, stream,
-                           ctx->big_list.as<uint32_t>(), counters + 1, ctx->rec.as<float4>(), cam.tiles_x,
+                           ctx->big_list.as<uint32_t>(), big_count, ctx->rec.as<float4>(), cam.tiles_x,
                            KeyLayout{}, big_chunk, ctx->tile_count.as<uint32_t>(),
-                           ctx->big_chunk_counts.as<uint32_t>(), nullptr, nullptr, nullptr, nullptr);
+                           ctx->big_chunk_counts.as<uint32_t>(),
+                           reinterpret_cast<unsigned long long*>(static_cast<char*>(ctx->kept_parts.dev) + big_parts_at),
+                           nullptr, nullptr, nullptr, nullptr);
         GSX_HIP_TRY(hipGetLastError(), "big_tiles_kernel<count>");
     }
-    // the instance count (the sum of the kept-tile counts) goes to the host first; the depth
-    // order and the count scan are queued behind it, so the GPU keeps working while the host
-    // waits for the count and sizes the instance buffers
-    if (n > 0) {
-        hipLaunchKernelGGL(sum_u32_kernel, dim3(std::min(blocks_for(n, 256 * 16), 1024u)), dim3(256), 0, stream,
-                           ctx->tile_count.as<uint32_t>(), n, reinterpret_cast<unsigned long long*>(counters + 4));
-        GSX_HIP_TRY(hipGetLastError(), "sum_u32_kernel");
-        GSX_HIP_TRY(hipMemcpyAsync(ctx->host_count, counters + 4, sizeof(unsigned long long), hipMemcpyDeviceToHost,
-                                   stream),
-                    "instance count readback");
-    } else {
-        ctx->host_count[0] = 0;  // no kernel wrote the counters
-    }
+    // the counting kernels leave the instance count as per-workgroup partials in host memory;
+    // the depth order and the count scan are queued behind them, so the GPU keeps working while
+    // the host waits for the partials, sums them and sizes the instance buffers
     GSX_HIP_TRY(hipEventRecord(ctx->count_ev, stream), "hipEventRecord(count)");
     GSX_TRY(record(ctx, 1, stream));
     // depth order of the Gaussians, then their tile counts in that order and its scan
@@ -547,18 +580,26 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
                            sorted_depth, (uint64_t)((1ull << index_bits) - 1ull), big_flag,
                            ctx->tile_count.as<uint32_t>(),
                            ctx->rank_g.as<uint32_t>(), ctx->rank_count.as<uint32_t>(), ctx->g_rank.as<uint32_t>(),
-                           ctx->long_list.as<uint32_t>(), counters + 2);
+                           ctx->long_list.as<uint32_t>(), counters + 1);
         GSX_HIP_TRY(hipGetLastError(), "rank_gather_kernel");
     }
     GSX_TRY(gsx_hip_scan_exclusive_u32(ctx->rank_count.as<uint32_t>(), ctx->offsets.as<uint32_t>(), n,
                                        ctx->scan_temp.ptr, stream));
     GSX_TRY(record(ctx, 2, stream));
     GSX_HIP_TRY(hipEventSynchronize(ctx->count_ev), "instance count sync");
-    if (ctx->host_count[0] > (unsigned long long)UINT32_MAX) {
+    unsigned long long total = 0;
+    if (n > 0) {
+        const uint32_t* pre = static_cast<const uint32_t*>(ctx->kept_parts.host);
+        const unsigned long long* big =
+            reinterpret_cast<const unsigned long long*>(static_cast<const char*>(ctx->kept_parts.host) + big_parts_at);
+        for (unsigned b = 0; b < pre_blocks; ++b) total += pre[b];
+        for (size_t b = 0; b < big_parts; ++b) total += big[b];
+    }
+    if (total > (unsigned long long)UINT32_MAX) {
         // positions, offsets and the sort run in 32 bits; nothing has been emitted yet
         return fail(GSX_HIP_ERROR_OUT_OF_RANGE, "more than 2^32 - 1 (tile, Gaussian) instances");
     }
-    const int64_t count = (int64_t)ctx->host_count[0];
+    const int64_t count = (int64_t)total;
     ctx->instance_count = count;
     const size_t c1 = (size_t)(count > 0 ? count : 1);
     GSX_TRY(ctx->keys.reserve(c1 * sizeof(uint64_t), "keys"));
@@ -584,8 +625,8 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
                            cam.tiles_x, layout, ctx->keys.as<uint64_t>(), ctx->inst_gauss.as<uint32_t>());
         GSX_HIP_TRY(hipGetLastError(), "emit_keys_kernel");
         hipLaunchKernelGGL(big_tiles_kernel<true>, dim3(kBigBlocks, big_chunks), dim3(256), 0, stream,
-                           ctx->big_list.as<uint32_t>(), counters + 1, ctx->rec.as<float4>(), cam.tiles_x, layout,
-                           big_chunk, nullptr, ctx->big_chunk_counts.as<uint32_t>(), ctx->offsets.as<uint32_t>(),
+                           ctx->big_list.as<uint32_t>(), big_count, ctx->rec.as<float4>(), cam.tiles_x, layout,
+                           big_chunk, nullptr, ctx->big_chunk_counts.as<uint32_t>(), nullptr, ctx->offsets.as<uint32_t>(),
                            ctx->g_rank.as<uint32_t>(), ctx->keys.as<uint64_t>(), ctx->inst_gauss.as<uint32_t>());
         GSX_HIP_TRY(hipGetLastError(), "big_tiles_kernel<emit>");
     }
@@ -601,11 +642,13 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     ctx->sorted_in_alt = in_alt != 0;
     GSX_TRY(record(ctx, 4, stream));
     const uint64_t* skeys = ctx->sorted_in_alt ? ctx->keys_alt.as<uint64_t>() : ctx->keys.as<uint64_t>();
-    hipLaunchKernelGGL(fill_u32_kernel, dim3(blocks_for((int64_t)tiles * 2, 256)), dim3(256), 0, stream,
-                       ctx->ranges.as<uint32_t>(), (int64_t)tiles * 2, 0u);
     if (count > 0) {
         hipLaunchKernelGGL(tile_ranges_kernel, dim3(blocks_for(count, 256)), dim3(256), 0, stream, skeys, layout,
-                           ctx->sorted_vals, ctx->offsets.as<uint32_t>() + n, ctx->ranges.as<uint2>());
+                           ctx->sorted_vals, ctx->offsets.as<uint32_t>() + n, (uint32_t)tiles,
+                           ctx->ranges.as<uint2>());
+    } else {
+        hipLaunchKernelGGL(fill_u32_kernel, dim3(blocks_for((int64_t)tiles * 2, 256)), dim3(256), 0, stream,
+                           ctx->ranges.as<uint32_t>(), (int64_t)tiles * 2, 0u);
     }
     GSX_HIP_TRY(hipGetLastError(), "tile_ranges_kernel");
     GSX_TRY(record(ctx, 5, stream));
@@ -669,11 +712,11 @@ gsx_hip_status gsx_hip_render_backward(gsx_hip_render_context* ctx, const float*
         const uint32_t chunk = std::max<uint32_t>(
             kWave, ((uint32_t)(tiles + (int)kLongChunks - 1) / kLongChunks + kWave - 1) / kWave * kWave);
         hipLaunchKernelGGL(reduce_long_chunks_kernel, dim3(kLongRunBlocks, kLongChunks), dim3(256), 0, stream,
-                           ctx->long_list.as<uint32_t>(), counters + 2, ctx->offsets.as<uint32_t>(), chunk,
+                           ctx->long_list.as<uint32_t>(), counters + 1, ctx->offsets.as<uint32_t>(), chunk,
                            ctx->inst_grad.as<float>(), inst_grad_op);
         GSX_HIP_TRY(hipGetLastError(), "reduce_long_chunks_kernel");
         hipLaunchKernelGGL(combine_long_runs_kernel, dim3(kLongRunBlocks), dim3(256), 0, stream,
-                           ctx->long_list.as<uint32_t>(), counters + 2, ctx->offsets.as<uint32_t>(),
+                           ctx->long_list.as<uint32_t>(), counters + 1, ctx->offsets.as<uint32_t>(),
                            ctx->rank_g.as<uint32_t>(),
                            chunk, ctx->inst_grad.as<float>(), inst_grad_op, ctx->grad2d.as<float>());
         GSX_HIP_TRY(hipGetLastError(), "combine_long_runs_kernel");

@@ -371,6 +371,22 @@ __device__ inline float wave_reduce_sum(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
+// wave_reduce_sum for unsigned integers (wraps modulo 2^32; every lane must be active).
+template <int kCtrl, int kRowMask>
+__device__ inline uint32_t dpp_move_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kCtrl, kRowMask, 0xf, false);
+}
+
+__device__ inline uint32_t wave_reduce_sum_u32(uint32_t v) {
+    v += dpp_move_u32<0xb1, 0xf>(v);
+    v += dpp_move_u32<0x4e, 0xf>(v);
+    v += dpp_move_u32<0x141, 0xf>(v);
+    v += dpp_move_u32<0x140, 0xf>(v);
+    v += dpp_move_u32<0x142, 0xa>(v);
+    v += dpp_move_u32<0x143, 0xc>(v);
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
 // Row totals (over the 16 lanes of each DPP row) of v[0..8], scattered over the row: the returned
 // value of lane l (l = lane index within its row) is the row total of v[(l >> 1) & 7], and
 // total8 receives the row total of v[8] in every lane. Each step pairs every lane with a partner
@@ -426,7 +442,7 @@ __device__ inline float div_rn_normal(float n, float d) {
 
 // Keys-only stable radix sort (sort.hip) that also drops every key equal to ~0: the first pass
 // reads all n keys and moves the others, in input order within each digit, to the front, and
-// stores their number in *n_live (which must be zero beforehand); the later passes sort that
+// stores their number in *n_live (overwritten; no initial value needed); the later passes sort that
 // many (grids are sized for n, so no host round trip is needed). Output positions >= *n_live
 // are not written.
 // Its digits are kCompactingRadixBits wide (passes = ceil((end_bit - begin_bit) / 9)), and temp

@@ -169,11 +169,18 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
     const float* __restrict__ sh1, const float* __restrict__ sh2, const float* __restrict__ sh3, int sh_degree,
     CameraParams cam, float4* __restrict__ rec, float4* __restrict__ cov_coef, uint32_t* __restrict__ tile_count,
     float* __restrict__ visible_counter, uint32_t* __restrict__ big_list, uint32_t* __restrict__ big_count,
+    uint32_t* __restrict__ clear0, uint32_t* __restrict__ clear1, uint32_t* __restrict__ kept_part,
     uint64_t* __restrict__ depth_keys, uint32_t depth_base, uint32_t depth_max, int index_bits,
     uint64_t big_key_flag) {
     __shared__ WaveBoxes s_boxes[kWavesPerBlock];
+    __shared__ uint32_t s_kept[kWavesPerBlock];
     WaveBoxes& wb = s_boxes[threadIdx.x / kWave];
     const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    // counters that later kernels accumulate into start at zero (plain stores, no fill launch)
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        *clear0 = 0u;
+        *clear1 = 0u;
+    }
     bool visible = false;
     float4 r0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), r1 = r0, r2 = r0;
     if (g < n) {
@@ -221,7 +228,19 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
     if (big) big_list[atomicAdd(big_count, 1u)] = (uint32_t)g;  // counted by big_tiles_kernel
     const uint32_t total = stage_box(wb, visible && !big, r0, r1, r2, (uint32_t)g, 0u);
     walk_wave_tiles<false>(wb, total, cam.tiles_x, KeyLayout{}, nullptr, nullptr);
-    if (g < n) tile_count[g] = big ? 0u : wb.kept[__lane_id()];  // big boxes: summed by big_tiles_kernel
+    const uint32_t kept = big ? 0u : wb.kept[__lane_id()];  // big boxes: counted by big_tiles_kernel
+    if (g < n) tile_count[g] = kept;
+    // the workgroup's kept tiles (at most 256 * kBigTiles) to kept_part[block], host memory that
+    // the host sums for the instance count
+    const uint32_t wave_kept = wave_reduce_sum_u32(kept);
+    if (__lane_id() == 0) s_kept[threadIdx.x / kWave] = wave_kept;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t sum = 0;
+#pragma unroll
+        for (int w = 0; w < kWavesPerBlock; ++w) sum += s_kept[w];
+        kept_part[blockIdx.x] = sum;
+    }
 }
 
 // Marks a big box's depth key (big_tiles_kernel needs its rank). Used only when the sorted depth
@@ -297,7 +316,8 @@ __global__ __launch_bounds__(256) void emit_keys_kernel(int64_t n, const float4*
 // Big boxes: the row-major tile range of each box on big_list is cut into chunks of `chunk`
 // tiles (at most kBigChunks per box); workgroup (x, c) takes chunk c of the boxes x, x + gridDim.x,
 // ... and walks it 256 tiles per step. kEmit = false stores the chunk's kept-tile count in
-// chunk_counts[i][c] and adds it to tile_count[g] (zeroed by preprocess); kEmit = true writes
+// chunk_counts[i][c] and adds it to tile_count[g] (zeroed by preprocess), and the workgroup's
+// kept tiles in total to kept_part[y * gridDim.x + x] (host memory); kEmit = true writes
 // the chunk's kept instances at offsets[rank of g] + the counts of the box's earlier chunks +
 // their rank within the chunk (per-wave ballots and a 4-wave prefix), i.e. in the same
 // row-major order as a single walk.
@@ -310,6 +330,7 @@ __global__ __launch_bounds__(256) void big_tiles_kernel(const uint32_t* __restri
                                                         KeyLayout layout, uint32_t chunk,
                                                         uint32_t* __restrict__ tile_count,
                                                         uint32_t* __restrict__ chunk_counts,
+                                                        unsigned long long* __restrict__ kept_part,
                                                         const uint32_t* __restrict__ offsets,
                                                         const uint32_t* __restrict__ gaussian_rank,
                                                         uint64_t* __restrict__ keys,
@@ -318,6 +339,7 @@ __global__ __launch_bounds__(256) void big_tiles_kernel(const uint32_t* __restri
     const uint32_t count = *big_count;
     const uint32_t lane = __lane_id(), wave = threadIdx.x / kWave;
     const uint32_t c = blockIdx.y;
+    unsigned long long block_kept = 0;
     for (uint32_t i = blockIdx.x; i < count; i += gridDim.x) {
         const uint32_t g = big_list[i];
         const float4 r0 = rec[3 * (size_t)g + 0], r1 = rec[3 * (size_t)g + 1], r2 = rec[3 * (size_t)g + 2];
@@ -369,23 +391,9 @@ __global__ __launch_bounds__(256) void big_tiles_kernel(const uint32_t* __restri
             chunk_counts[(size_t)i * kBigChunks + c] = running;
             if (running > 0) atomicAdd(&tile_count[g], running);
         }
+        block_kept += running;
     }
-}
-
-// *out += sum of in[0..n) in 64 bits (out zeroed beforehand; grid-stride, each thread adds its
-// partial to an LDS total, one global atomic per workgroup), so a total past 2^32 is seen
-// rather than wrapped.
-__global__ __launch_bounds__(256) void sum_u32_kernel(const uint32_t* __restrict__ in, int64_t n,
-                                                      unsigned long long* __restrict__ out) {
-    __shared__ unsigned long long s_total;
-    if (threadIdx.x == 0) s_total = 0ull;
-    __syncthreads();
-    unsigned long long v = 0;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
-        v += in[i];
-    if (v != 0ull) atomicAdd(&s_total, v);
-    __syncthreads();
-    if (threadIdx.x == 0 && s_total != 0ull) atomicAdd(out, s_total);
+    if (!kEmit && threadIdx.x == 0) kept_part[(size_t)blockIdx.y * gridDim.x + blockIdx.x] = block_kept;
 }
 
 __global__ __launch_bounds__(256) void fill_u32_kernel(uint32_t* __restrict__ p, int64_t count, uint32_t v) {
@@ -398,18 +406,27 @@ __global__ __launch_bounds__(256) void fill_f32_kernel(float* __restrict__ p, in
     if (i < count) p[i] = v;
 }
 
-// [start, end) of each tile's run in the sorted keys (tiles without keys keep (0, 0)), and the
-// emission position of every sorted key (values[i], the payload bits).
+// [start, end) of each tile's run in the sorted keys, and the emission position of every sorted
+// key (values[i], the payload bits). Tiles without keys get (0, 0): the thread of the last key
+// before such a gap (or of the first key, for the tiles before it) writes them, so no fill of
+// all tiles is needed beforehand. count >= 1 (with no keys the caller fills the ranges).
 __global__ __launch_bounds__(256) void tile_ranges_kernel(const uint64_t* __restrict__ keys, KeyLayout layout,
                                                           uint32_t* __restrict__ values, const uint32_t* count_ptr,
-                                                          uint2* __restrict__ ranges) {
+                                                          uint32_t tiles, uint2* __restrict__ ranges) {
     const uint32_t count = *count_ptr;
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= count) return;
     const uint64_t key = keys[i];
     const uint32_t tile = key_tile(layout, key);
+    if (i == 0) {
+        for (uint32_t t = 0; t < tile; ++t) ranges[t] = make_uint2(0u, 0u);
+    }
     if (i == 0 || key_tile(layout, keys[i - 1]) != tile) ranges[tile].x = i;
-    if (i == count - 1 || key_tile(layout, keys[i + 1]) != tile) ranges[tile].y = i + 1;
+    const uint32_t next = i == count - 1 ? tiles : key_tile(layout, keys[i + 1]);
+    if (next != tile) {
+        ranges[tile].y = i + 1;
+        for (uint32_t t = tile + 1; t < next; ++t) ranges[t] = make_uint2(0u, 0u);
+    }
     values[i] = (uint32_t)(key & ((1ull << layout.payload_bits) - 1ull));
 }
 

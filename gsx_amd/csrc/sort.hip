@@ -14,13 +14,17 @@
 namespace gsx_amd {
 
 constexpr int kScanThreads = 256;
-constexpr int kScanItems = 16;
-constexpr int kScanChunk = kScanThreads * kScanItems;  // 4096 elements per block
+constexpr int kScanItems = 4;
+constexpr int kScanChunk = kScanThreads * kScanItems;  // 1024 elements per block
 
 constexpr int kSortThreads = 256;
-constexpr int kSortRounds = 16;
-constexpr int kSortChunk = kSortThreads * kSortRounds;  // 4096 keys per block
-constexpr int kRadixBits = 8;  // digit width of the public sorts
+constexpr int kSortChunk = 4096;  // keys per chunk (one upsweep / downsweep workgroup), public sorts
+constexpr int kRadixBits = 8;     // digit width of the public sorts
+// The depth order sorts about a million keys: 1024-key chunks give ~1000 workgroups per launch
+// (with 4096 a launch has fewer workgroups than the GPU has CUs, one wave per SIMD)
+constexpr int kCompactingChunk = 1024;
+constexpr int kRowItems = 16;  // row scan: 16 chunk counts per thread and step
+constexpr int kRowChunk = kSortThreads * kRowItems;
 
 // Exclusive scan of the 256 per-thread values of a block; returns this thread's prefix and
 // the block total through `total`.
@@ -117,18 +121,17 @@ __global__ __launch_bounds__(kScanThreads) void scan_downsweep_kernel(const uint
 // ---------------------------------------------------------------------------------------------
 // One LSD pass on the kBits-bit digit at `shift` (8, or 9 for the compacting sort: 512 bins,
 // three passes for 27 depth bits), reduce-then-scan, three launches:
-//   upsweep: digit counts of each 4096-key chunk                       -> hist[digit][chunk]
+//   upsweep: digit counts of each chunk (4096 keys, 1024 in the depth order) -> hist[digit][chunk]
 //   rowscan: one workgroup per digit scans its row over the chunks    -> offsets, totals[digit]
-//   downsweep: each wave ranks its 1024 keys (16 rounds of 64) stably with 8 ballots per round
-//      and wave-private digit counters; the chunk is then reordered by digit in LDS and written
-//      out in order, so consecutive lanes store consecutive addresses of one digit's run.
-// Stability: a chunk's keys keep input order within a digit (waves own consecutive quarters,
+//   downsweep: 8 waves each rank an eighth of the chunk (rounds of 64 keys) stably with kBits
+//      ballots per round and wave-private digit counters; the chunk is then reordered by digit
+//      in LDS and written out in order, so consecutive lanes store consecutive addresses of one
+//      digit's run.
+// Stability: a chunk's keys keep input order within a digit (waves own consecutive eighths,
 // rounds and lanes follow input order), and chunks are laid out in order inside each digit.
 // No workgroup waits on another, so every wave runs to completion.
 // ---------------------------------------------------------------------------------------------
-constexpr int kChunkWaves = kSortThreads / kWave;            // 4
-constexpr int kWaveKeys = kSortChunk / kChunkWaves;           // 1024 keys per wave
-constexpr int kWaveRounds = kWaveKeys / kWave;                // 16
+constexpr int kChunkWaves = kSortThreads / kWave;  // 4 (upsweep)
 
 template <int kBits>
 __device__ inline uint32_t digit_of(uint64_t key, int shift) {
@@ -139,7 +142,7 @@ constexpr uint64_t kSentinelKey = ~0ull;  // dropped by a pass with drop_sentine
 
 // n_dev (may be null): live key count, n = min(n, *n_dev); chunks past it count nothing.
 // drop_sentinel: keys equal to kSentinelKey are left out (they vanish from the output).
-template <int kBits>
+template <int kBits, int kChunk>
 __global__ __launch_bounds__(kSortThreads) void radix_upsweep_kernel(const uint64_t* __restrict__ keys, int64_t n,
                                                                      const uint32_t* __restrict__ n_dev,
                                                                      bool drop_sentinel, int shift,
@@ -151,9 +154,9 @@ __global__ __launch_bounds__(kSortThreads) void radix_upsweep_kernel(const uint6
     const int wave = threadIdx.x / kWave;
     for (int i = threadIdx.x; i < kChunkWaves * kBins; i += kSortThreads) (&s_hist[0][0])[i] = 0;
     __syncthreads();
-    const int64_t base = (int64_t)blockIdx.x * kSortChunk;
+    const int64_t base = (int64_t)blockIdx.x * kChunk;
 #pragma unroll 4
-    for (int r = 0; r < kSortRounds; ++r) {
+    for (int r = 0; r < kChunk / kSortThreads; ++r) {
         const int64_t i = base + (int64_t)r * kSortThreads + threadIdx.x;
         if (i < n) {
             const uint64_t k = keys[i];
@@ -168,47 +171,41 @@ __global__ __launch_bounds__(kSortThreads) void radix_upsweep_kernel(const uint6
 }
 
 // Workgroup d: exclusive scan of hist[d][0..num_chunks) into offsets[d][..], row total into
-// totals[d]; with key_count non-null (zero beforehand) the row totals are also added to it.
+// totals[d].
 __global__ __launch_bounds__(kSortThreads) void radix_rowscan_kernel(const uint32_t* __restrict__ hist,
                                                                      int64_t num_chunks,
                                                                      uint32_t* __restrict__ offsets,
-                                                                     uint32_t* __restrict__ totals,
-                                                                     uint32_t* __restrict__ key_count) {
+                                                                     uint32_t* __restrict__ totals) {
     __shared__ uint32_t s_wave[kSortThreads / kWave];
     const uint32_t* row = hist + (int64_t)blockIdx.x * num_chunks;
     uint32_t* out = offsets + (int64_t)blockIdx.x * num_chunks;
     uint32_t carry = 0;
-    for (int64_t base = 0; base < num_chunks; base += kScanChunk) {
-        uint32_t vals[kScanItems];
+    for (int64_t base = 0; base < num_chunks; base += kRowChunk) {
+        uint32_t vals[kRowItems];
         uint32_t sum = 0;
 #pragma unroll
-        for (int k = 0; k < kScanItems; ++k) {
-            const int64_t i = base + (int64_t)threadIdx.x * kScanItems + k;
+        for (int k = 0; k < kRowItems; ++k) {
+            const int64_t i = base + (int64_t)threadIdx.x * kRowItems + k;
             vals[k] = i < num_chunks ? row[i] : 0u;
             sum += vals[k];
         }
         uint32_t total;
         uint32_t prefix = block_exclusive_scan_256(sum, s_wave, total) + carry;
 #pragma unroll
-        for (int k = 0; k < kScanItems; ++k) {
-            const int64_t i = base + (int64_t)threadIdx.x * kScanItems + k;
+        for (int k = 0; k < kRowItems; ++k) {
+            const int64_t i = base + (int64_t)threadIdx.x * kRowItems + k;
             if (i < num_chunks) out[i] = prefix;
             prefix += vals[k];
         }
         carry += total;
     }
-    if (threadIdx.x == 0) {
-        totals[blockIdx.x] = carry;
-        if (key_count != nullptr && carry > 0) atomicAdd(key_count, carry);
-    }
+    if (threadIdx.x == 0) totals[blockIdx.x] = carry;
 }
 
 // The downsweep runs 512 threads (8 waves of 512 keys, 8 rounds each): the serial ranking chain
 // of a chunk is half as long as with 4 waves.
 constexpr int kDownThreads = 512;
 constexpr int kDownWaves = kDownThreads / kWave;           // 8
-constexpr int kDownWaveKeys = kSortChunk / kDownWaves;     // 512
-constexpr int kDownRounds = kDownWaveKeys / kWave;         // 8
 
 // Exclusive scan over the kBins digits held by threads 0..kBins-1 of a 512-thread workgroup
 // (threads past kBins pass 0 and get garbage); `total` receives the sum over the digits.
@@ -236,14 +233,17 @@ __device__ inline uint32_t digit_exclusive_scan(uint32_t v, uint32_t* s_wave, ui
     return wave_base + incl - v;
 }
 
-template <bool kPairs, int kBits>
+template <bool kPairs, int kBits, int kChunk>
 __global__ __launch_bounds__(kDownThreads) void radix_downsweep_kernel(
     const uint64_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, int64_t n,
     const uint32_t* __restrict__ n_dev, bool drop_sentinel, int shift, int64_t num_chunks,
     const uint32_t* __restrict__ offsets, const uint32_t* __restrict__ totals, uint64_t* __restrict__ keys_out,
-    uint32_t* __restrict__ vals_out) {
-    __shared__ uint64_t s_keys[kSortChunk];
-    __shared__ uint32_t s_vals[kPairs ? kSortChunk : 1];
+    uint32_t* __restrict__ vals_out, uint32_t* __restrict__ kept_total) {
+    constexpr int kDownWaveKeys = kChunk / kDownWaves;  // keys ranked by one wave
+    constexpr int kDownRounds = kDownWaveKeys / kWave;
+    static_assert(kDownRounds >= 1 && kDownWaveKeys % kWave == 0, "whole rounds per wave");
+    __shared__ uint64_t s_keys[kChunk];
+    __shared__ uint32_t s_vals[kPairs ? kChunk : 1];
     constexpr int kBins = 1 << kBits;
     static_assert(kBins <= kDownThreads, "one thread per digit");
     __shared__ uint32_t s_cnt[kDownWaves][kBins];  // wave-private counters, then wave starts
@@ -253,10 +253,10 @@ __global__ __launch_bounds__(kDownThreads) void radix_downsweep_kernel(
     __shared__ uint32_t s_kept;                     // keys of the chunk that are moved
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
-    const int64_t base = (int64_t)blockIdx.x * kSortChunk;
+    const int64_t base = (int64_t)blockIdx.x * kChunk;
     if (n_dev != nullptr) n = min(n, (int64_t)*n_dev);
     if (base >= n) return;  // uniform: a chunk past the live count has nothing to move
-    const int chunk_count = (int)min((int64_t)kSortChunk, n - base);
+    const int chunk_count = (int)min((int64_t)kChunk, n - base);
     for (int i = threadIdx.x; i < kDownWaves * kBins; i += kDownThreads) (&s_cnt[0][0])[i] = 0;
     __syncthreads();
     // 1. per wave: stable ranks among equal digits (rank = keys of the digit before it in this
@@ -302,10 +302,12 @@ __global__ __launch_bounds__(kDownThreads) void radix_downsweep_kernel(
             c[w] = t < kBins ? s_cnt[w][t] : 0u;
             cnt += c[w];
         }
-        uint32_t kept, dummy;
+        uint32_t kept, all_kept;
         const uint32_t start = digit_exclusive_scan<kBins>(cnt, s_wave, kept);
-        const uint32_t digit_base = digit_exclusive_scan<kBins>(t < kBins ? totals[t] : 0u, s_wave, dummy);
+        const uint32_t digit_base = digit_exclusive_scan<kBins>(t < kBins ? totals[t] : 0u, s_wave, all_kept);
         if (t == 0) s_kept = kept;
+        // the number of keys this pass keeps, for the later passes (a plain store: one writer)
+        if (kept_total != nullptr && blockIdx.x == 0 && t == 0) *kept_total = all_kept;
         if (t < kBins) {
             s_local[t] = start;
             s_global[t] = digit_base + offsets[(int64_t)t * num_chunks + blockIdx.x];
@@ -346,25 +348,25 @@ using namespace gsx_amd;
 namespace {
 
 // n_dev: see radix_upsweep_kernel. compact_first: the first pass reads all n keys and drops the
-// sentinel keys (stably compacting the rest to the front), its row scan adds the number of kept
-// keys to *n_dev (zero beforehand), and the later passes sort that many.
-template <int kBits>
+// sentinel keys (stably compacting the rest to the front), its downsweep stores the number of
+// kept keys in *n_dev, and the later passes sort that many.
+template <int kBits, int kChunk>
 size_t radix_temp_bytes(int64_t n) {
-    int64_t chunks = (n + kSortChunk - 1) / kSortChunk;
+    int64_t chunks = (n + kChunk - 1) / kChunk;
     if (chunks < 1) chunks = 1;
     const int64_t hist_count = chunks * (1 << kBits);
     // hist + offsets + totals
     return (size_t)(2 * hist_count + (1 << kBits)) * sizeof(uint32_t) + 256;
 }
 
-template <bool kPairs, int kBits>
+template <bool kPairs, int kBits, int kChunk>
 gsx_hip_status radix_sort_u64(uint64_t* keys, uint32_t* vals, uint64_t* keys_alt, uint32_t* vals_alt, int64_t n,
                               uint32_t* n_dev, bool compact_first, int begin_bit, int end_bit, void* temp,
                               int* out_in_alt, hipStream_t stream) {
     constexpr int kBins = 1 << kBits;
     if (begin_bit < 0 || end_bit > 64 || begin_bit > end_bit) return GSX_HIP_ERROR_INVALID_ARGUMENT;
     if (n > (int64_t)UINT32_MAX) return GSX_HIP_ERROR_OUT_OF_RANGE;
-    int64_t chunks = (n + kSortChunk - 1) / kSortChunk;
+    int64_t chunks = (n + kChunk - 1) / kChunk;
     if (chunks < 1) chunks = 1;
     const int64_t hist_count = chunks * kBins;
     uint32_t* hist = static_cast<uint32_t*>(temp);
@@ -379,13 +381,13 @@ gsx_hip_status radix_sort_u64(uint64_t* keys, uint32_t* vals, uint64_t* keys_alt
             uint32_t* vout = in_alt ? vals : vals_alt;
             const bool drop = compact_first && shift == begin_bit;
             const uint32_t* live = drop ? nullptr : n_dev;
-            hipLaunchKernelGGL(radix_upsweep_kernel<kBits>, dim3((unsigned)chunks), dim3(kSortThreads), 0, stream, kin,
+            hipLaunchKernelGGL((radix_upsweep_kernel<kBits, kChunk>), dim3((unsigned)chunks), dim3(kSortThreads), 0, stream, kin,
                                n, live, drop, shift, chunks, hist);
             hipLaunchKernelGGL(radix_rowscan_kernel, dim3(kBins), dim3(kSortThreads), 0, stream, hist, chunks,
-                               offsets, totals, drop ? n_dev : nullptr);
-            hipLaunchKernelGGL((radix_downsweep_kernel<kPairs, kBits>), dim3((unsigned)chunks), dim3(kDownThreads), 0,
-                               stream,
-                               kin, vin, n, live, drop, shift, chunks, offsets, totals, kout, vout);
+                               offsets, totals);
+            hipLaunchKernelGGL((radix_downsweep_kernel<kPairs, kBits, kChunk>), dim3((unsigned)chunks),
+                               dim3(kDownThreads), 0, stream, kin, vin, n, live, drop, shift, chunks, offsets, totals,
+                               kout, vout, drop ? n_dev : nullptr);
             in_alt ^= 1;
         }
     }
@@ -415,23 +417,23 @@ gsx_hip_status gsx_hip_scan_exclusive_u32(const uint32_t* in, uint32_t* out, int
     return (gsx_hip_status)hipGetLastError();
 }
 
-size_t gsx_hip_radix_sort_temp_bytes(int64_t n) { return radix_temp_bytes<kRadixBits>(n); }
+size_t gsx_hip_radix_sort_temp_bytes(int64_t n) { return radix_temp_bytes<kRadixBits, kSortChunk>(n); }
 
 // Stable LSD sort of n pairs on key bits [begin_bit, end_bit). The result ends in (keys, vals)
 // when *out_in_alt == 0, else in (keys_alt, vals_alt).
 gsx_hip_status gsx_hip_radix_sort_pairs_u64(uint64_t* keys, uint32_t* vals, uint64_t* keys_alt, uint32_t* vals_alt,
                                             int64_t n, int begin_bit, int end_bit, void* temp, int* out_in_alt,
                                             hipStream_t stream) {
-    return radix_sort_u64<true, kRadixBits>(keys, vals, keys_alt, vals_alt, n, nullptr, false, begin_bit, end_bit,
-                                            temp, out_in_alt, stream);
+    return radix_sort_u64<true, kRadixBits, kSortChunk>(keys, vals, keys_alt, vals_alt, n, nullptr, false, begin_bit,
+                                                        end_bit, temp, out_in_alt, stream);
 }
 
 // Stable LSD sort of n keys on bits [begin_bit, end_bit); bits outside the range travel with
 // the key (a payload packed into the low bits keeps input order among equal sort bits).
 gsx_hip_status gsx_hip_radix_sort_keys_u64(uint64_t* keys, uint64_t* keys_alt, int64_t n, int begin_bit, int end_bit,
                                            void* temp, int* out_in_alt, hipStream_t stream) {
-    return radix_sort_u64<false, kRadixBits>(keys, nullptr, keys_alt, nullptr, n, nullptr, false, begin_bit, end_bit,
-                                             temp, out_in_alt, stream);
+    return radix_sort_u64<false, kRadixBits, kSortChunk>(keys, nullptr, keys_alt, nullptr, n, nullptr, false,
+                                                         begin_bit, end_bit, temp, out_in_alt, stream);
 }
 
 }  // extern "C"
@@ -442,10 +444,13 @@ gsx_hip_status radix_sort_keys_u64_compacting(uint64_t* keys, uint64_t* keys_alt
                                               int begin_bit, int end_bit, void* temp, int* out_in_alt,
                                               hipStream_t stream) {
     if (begin_bit >= end_bit) return GSX_HIP_ERROR_INVALID_ARGUMENT;  // the compacting pass must run
-    return radix_sort_u64<false, kCompactingRadixBits>(keys, nullptr, keys_alt, nullptr, n, n_live, true, begin_bit,
-                                                       end_bit, temp, out_in_alt, stream);
+    return radix_sort_u64<false, kCompactingRadixBits, kCompactingChunk>(keys, nullptr, keys_alt, nullptr, n, n_live,
+                                                                         true, begin_bit, end_bit, temp, out_in_alt,
+                                                                         stream);
 }
 
-size_t radix_sort_keys_u64_compacting_temp_bytes(int64_t n) { return radix_temp_bytes<kCompactingRadixBits>(n); }
+size_t radix_sort_keys_u64_compacting_temp_bytes(int64_t n) {
+    return radix_temp_bytes<kCompactingRadixBits, kCompactingChunk>(n);
+}
 
 }  // namespace gsx_amd

@@ -193,6 +193,31 @@ def test_context_reuse_then_empty_scene(oracle):
     assert np.array_equal(img.cpu().numpy(), oracle.render(empty, w.camera)[0])
 
 
+def test_context_reuse_alternating_scenes(oracle):
+    # one context, forwards that alternate between a scene with near-plane boxes covering every
+    # tile and a subset of it: the big-box counter slots alternate between forwards, and the
+    # tile ranges of the tiles a forward leaves empty are rewritten by that forward
+    from gsx_amd import scenes
+    from gsx_amd.backend import GaussianTensors
+    w = _workloads()["c3_1080"]()
+    sc = w.scene
+    part = scenes.Scene(*(np.ascontiguousarray(a[:3000]) for a in (sc.mean3d, sc.rotation, sc.logscale, sc.opacity,
+                                                                   sc.sh0)))
+    r, cam, g_full = _setup(w)
+    g_part = GaussianTensors.from_scene(part)
+    refs = {"full": oracle.render(sc, w.camera)[0], "part": oracle.render(part, w.camera)[0]}
+    counts = {}
+    for name, g in (("full", g_full), ("part", g_part), ("full", g_full), ("part", g_part)):
+        print(f"[case] reuse {name}", flush=True)
+        img = r.render(cam, g, train=False)
+        torch.cuda.synchronize()
+        assert np.array_equal(img.cpu().numpy(), refs[name])
+        st = r.stats()
+        counts.setdefault(name, st.instance_count)
+        assert st.instance_count == counts[name]
+    assert counts["full"] > counts["part"] > 0
+
+
 def test_background_only_pixels(oracle):
     from gsx_amd import scenes
     w = scenes.config0(n=50, width=64, height=48)
