@@ -176,8 +176,10 @@ def main():
     grads = g.zeros_like_grads()
     renderer = Renderer(args.width, args.height)
     img = torch.empty((3, args.height, args.width), dtype=torch.float32, device="cuda")
-    loss_map = torch.empty_like(img)
-    grad_img = torch.empty_like(img)
+    # the loss launchers accumulate (+=) into the loss map and the image gradient, so both start
+    # each step at zero: one allocation, cleared by one fill
+    loss_and_grad = torch.empty((2,) + tuple(img.shape), dtype=torch.float32, device="cuda")
+    loss_map, grad_img = loss_and_grad[0], loss_and_grad[1]
     ssim_ws = torch.empty(3 * img.numel(), dtype=torch.float32, device="cuda")
     opt = Adam([dict(parameter=g.mean3d, gradient=grads.mean3d, learning_rate=1e-3),
                 dict(parameter=g.logscale, gradient=grads.logscale, learning_rate=1e-2),
@@ -196,8 +198,7 @@ def main():
         tgt = targets[i % args.poses]
         st = stream_handle()
         renderer.render(cam, g, train=True, out_rgb=img)
-        loss_map.zero_()
-        grad_img.zero_()
+        loss_and_grad.zero_()
         e = [torch.cuda.Event(enable_timing=True) for _ in range(4)] if record else None
         if record:
             e[0].record()

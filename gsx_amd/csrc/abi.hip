@@ -499,7 +499,7 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     GSX_TRY(ctx->big_list.reserve(n1 * sizeof(uint32_t), "big_list"));
     GSX_TRY(ctx->big_chunk_counts.reserve(n1 * kBigChunks * sizeof(uint32_t), "big_chunk_counts"));
     GSX_TRY(ctx->offsets.reserve((size_t)(n + 1) * sizeof(uint32_t), "offsets"));
-    GSX_TRY(ctx->scan_temp.reserve(gsx_hip_scan_temp_bytes(n), "scan_temp"));
+    GSX_TRY(ctx->scan_temp.reserve(((size_t)blocks_for(n, 256) + 1) * sizeof(uint32_t), "rank_block_sums"));
     GSX_TRY(ctx->depth_keys.reserve(n1 * sizeof(uint64_t), "depth_keys"));
     GSX_TRY(ctx->depth_keys_alt.reserve(n1 * sizeof(uint64_t), "depth_keys_alt"));
     GSX_TRY(ctx->rank_g.reserve(n1 * sizeof(uint32_t), "rank_gaussian"));
@@ -580,11 +580,11 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
                            sorted_depth, (uint64_t)((1ull << index_bits) - 1ull), big_flag,
                            ctx->tile_count.as<uint32_t>(),
                            ctx->rank_g.as<uint32_t>(), ctx->rank_count.as<uint32_t>(), ctx->g_rank.as<uint32_t>(),
-                           ctx->long_list.as<uint32_t>(), counters + 1);
+                           ctx->long_list.as<uint32_t>(), counters + 1, ctx->scan_temp.as<uint32_t>());
         GSX_HIP_TRY(hipGetLastError(), "rank_gather_kernel");
+        // exclusive scan of the 256-rank sums; emit_keys_kernel completes the offsets
+        GSX_TRY(scan_partials_in_place(ctx->scan_temp.as<uint32_t>(), pre_blocks, stream));
     }
-    GSX_TRY(gsx_hip_scan_exclusive_u32(ctx->rank_count.as<uint32_t>(), ctx->offsets.as<uint32_t>(), n,
-                                       ctx->scan_temp.ptr, stream));
     GSX_TRY(record(ctx, 2, stream));
     GSX_HIP_TRY(hipEventSynchronize(ctx->count_ev), "instance count sync");
     unsigned long long total = 0;
@@ -620,8 +620,9 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
                                   "checkpoints"));
     }
     if (n > 0) {
-        hipLaunchKernelGGL(emit_keys_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, n, ctx->rec.as<float4>(),
-                           ctx->rank_g.as<uint32_t>(), ctx->rank_count.as<uint32_t>(), ctx->offsets.as<uint32_t>(),
+        hipLaunchKernelGGL(emit_keys_kernel, dim3(pre_blocks), dim3(256), 0, stream, n, ctx->rec.as<float4>(),
+                           ctx->rank_g.as<uint32_t>(), ctx->rank_count.as<uint32_t>(), ctx->scan_temp.as<uint32_t>(),
+                           ctx->offsets.as<uint32_t>(),
                            cam.tiles_x, layout, ctx->keys.as<uint64_t>(), ctx->inst_gauss.as<uint32_t>());
         GSX_HIP_TRY(hipGetLastError(), "emit_keys_kernel");
         hipLaunchKernelGGL(big_tiles_kernel<true>, dim3(kBigBlocks, big_chunks), dim3(256), 0, stream,

@@ -440,6 +440,32 @@ __device__ inline float div_rn_normal(float n, float d) {
     return __builtin_fmaf(r, y, q);
 }
 
+// Exclusive scan of the 256 per-thread values of a 256-thread workgroup (a wave scan with
+// shuffles, then the 4 wave totals through LDS); returns this thread's prefix and the workgroup
+// total through `total`. s_wave holds 4 words of LDS. Contains two workgroup barriers.
+__device__ inline uint32_t block_exclusive_scan_256(uint32_t v, uint32_t* s_wave, uint32_t& total) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    uint32_t incl = v;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+        uint32_t o = __shfl_up(incl, off, kWave);
+        if (lane >= off) incl += o;
+    }
+    if (lane == kWave - 1) s_wave[wave] = incl;
+    __syncthreads();
+    uint32_t wave_base = 0;
+    total = 0;
+#pragma unroll
+    for (int w = 0; w < 256 / kWave; ++w) {
+        uint32_t sw = s_wave[w];
+        if (w < wave) wave_base += sw;
+        total += sw;
+    }
+    __syncthreads();
+    return wave_base + incl - v;
+}
+
 // Keys-only stable radix sort (sort.hip) that also drops every key equal to ~0: the first pass
 // reads all n keys and moves the others, in input order within each digit, to the front, and
 // stores their number in *n_live (overwritten; no initial value needed); the later passes sort that
@@ -452,5 +478,8 @@ gsx_hip_status radix_sort_keys_u64_compacting(uint64_t* keys, uint64_t* keys_alt
                                               int begin_bit, int end_bit, void* temp, int* out_in_alt,
                                               hipStream_t stream);
 size_t radix_sort_keys_u64_compacting_temp_bytes(int64_t n);
+
+// Single-workgroup exclusive scan of partials[0..count) in place, the total stored at [count].
+gsx_hip_status scan_partials_in_place(uint32_t* partials, int64_t count, hipStream_t stream);
 
 }  // namespace gsx_amd

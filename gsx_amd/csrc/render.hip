@@ -254,7 +254,9 @@ constexpr uint32_t kLaneRun = 32;
 // After the depth sort of the V visible Gaussians (V = *depth_count): the Gaussian of every
 // depth rank, its kept-tile count, the rank of each big box (the only ranks looked up by
 // Gaussian; every Gaussian's when flagged_only is false), and the list of ranks whose count
-// exceeds kLaneRun. Ranks V..n-1 get count 0 (so the scan over n covers them) and no Gaussian.
+// exceeds kLaneRun. Ranks V..n-1 get count 0 and no Gaussian. Each workgroup also stores the sum
+// of its 256 counts in block_sums[block], the first step of the offsets scan (emit_keys_kernel
+// finishes it).
 __global__ __launch_bounds__(256) void rank_gather_kernel(int64_t n, const uint32_t* __restrict__ depth_count,
                                                           const uint64_t* __restrict__ sorted_depth_keys,
                                                           uint64_t index_mask, bool flagged_only,
@@ -263,20 +265,31 @@ __global__ __launch_bounds__(256) void rank_gather_kernel(int64_t n, const uint3
                                                           uint32_t* __restrict__ rank_count,
                                                           uint32_t* __restrict__ gaussian_rank,
                                                           uint32_t* __restrict__ long_list,
-                                                          uint32_t* __restrict__ long_count) {
+                                                          uint32_t* __restrict__ long_count,
+                                                          uint32_t* __restrict__ block_sums) {
+    __shared__ uint32_t s_sum[kWavesPerBlock];
     const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (r >= n) return;
-    if (r >= (int64_t)*depth_count) {
-        rank_count[r] = 0;
-        return;
+    uint32_t c = 0;
+    if (r < n) {
+        if (r < (int64_t)*depth_count) {
+            const uint64_t key = sorted_depth_keys[r];
+            const uint32_t g = (uint32_t)(key & index_mask);
+            c = tile_count[g];
+            rank_gaussian[r] = g;
+            if (!flagged_only || (key & kBigKeyFlag) != 0) gaussian_rank[g] = (uint32_t)r;
+            if (c > kLaneRun) long_list[atomicAdd(long_count, 1u)] = (uint32_t)r;
+        }
+        rank_count[r] = c;
     }
-    const uint64_t key = sorted_depth_keys[r];
-    const uint32_t g = (uint32_t)(key & index_mask);
-    const uint32_t c = tile_count[g];
-    rank_gaussian[r] = g;
-    rank_count[r] = c;
-    if (!flagged_only || (key & kBigKeyFlag) != 0) gaussian_rank[g] = (uint32_t)r;
-    if (c > kLaneRun) long_list[atomicAdd(long_count, 1u)] = (uint32_t)r;
+    const uint32_t wave_sum = wave_reduce_sum_u32(c);
+    if (__lane_id() == 0) s_sum[threadIdx.x / kWave] = wave_sum;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t sum = 0;
+#pragma unroll
+        for (int w = 0; w < kWavesPerBlock; ++w) sum += s_sum[w];
+        block_sums[blockIdx.x] = sum;
+    }
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -285,20 +298,29 @@ __global__ __launch_bounds__(256) void rank_gather_kernel(int64_t n, const uint3
 // exclusive scan of the counts in rank order). key = tile << tile_shift | position, and
 // instance_gaussian[position] = g. A stable sort on the tile bits then leaves every tile's run
 // in (depth, index) order.
+// The offsets are finished here: block_prefix[b] is the exclusive scan of rank_gather_kernel's
+// 256-rank sums (same workgroup size and grid), and each workgroup scans its own 256 counts;
+// offsets[0..n] are stored for the later kernels (offsets[n] = total).
 // ---------------------------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void emit_keys_kernel(int64_t n, const float4* __restrict__ rec,
                                                         const uint32_t* __restrict__ rank_gaussian,
                                                         const uint32_t* __restrict__ rank_count,
-                                                        const uint32_t* __restrict__ offsets, int32_t tiles_x,
+                                                        const uint32_t* __restrict__ block_prefix,
+                                                        uint32_t* __restrict__ offsets, int32_t tiles_x,
                                                         KeyLayout layout, uint64_t* __restrict__ keys,
                                                         uint32_t* __restrict__ instance_gaussian) {
     __shared__ WaveBoxes s_boxes[kWavesPerBlock];
+    __shared__ uint32_t s_wave[kWavesPerBlock];
     WaveBoxes& wb = s_boxes[threadIdx.x / kWave];
     const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    bool any = r < n && rank_count[r] > 0;
+    const uint32_t cnt = r < n ? rank_count[r] : 0u;
+    uint32_t block_total;
+    const uint32_t o = block_prefix[blockIdx.x] + block_exclusive_scan_256(cnt, s_wave, block_total);
+    if (r < n) offsets[r] = o;
+    if (r == n - 1) offsets[n] = o + cnt;
+    bool any = cnt > 0;
     uint32_t g = 0;
     float4 r0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), r1 = r0, r2 = r0;
-    uint32_t o = 0;
     if (any) {
         g = rank_gaussian[r];
         r2 = rec[3 * (size_t)g + 2];
@@ -307,7 +329,6 @@ __global__ __launch_bounds__(256) void emit_keys_kernel(int64_t n, const float4*
     if (any) {
         r0 = rec[3 * (size_t)g + 0];
         r1 = rec[3 * (size_t)g + 1];
-        o = offsets[r];
     }
     const uint32_t total = stage_box(wb, any, r0, r1, r2, g, o);
     walk_wave_tiles<true>(wb, total, tiles_x, layout, keys, instance_gaussian);

@@ -26,31 +26,6 @@ constexpr int kCompactingChunk = 1024;
 constexpr int kRowItems = 16;  // row scan: 16 chunk counts per thread and step
 constexpr int kRowChunk = kSortThreads * kRowItems;
 
-// Exclusive scan of the 256 per-thread values of a block; returns this thread's prefix and
-// the block total through `total`.
-__device__ inline uint32_t block_exclusive_scan_256(uint32_t v, uint32_t* s_wave, uint32_t& total) {
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wave = threadIdx.x / kWave;
-    uint32_t incl = v;
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-        uint32_t o = __shfl_up(incl, off, kWave);
-        if (lane >= off) incl += o;
-    }
-    if (lane == kWave - 1) s_wave[wave] = incl;
-    __syncthreads();
-    uint32_t wave_base = 0;
-    total = 0;
-#pragma unroll
-    for (int w = 0; w < kScanThreads / kWave; ++w) {
-        uint32_t s = s_wave[w];
-        if (w < wave) wave_base += s;
-        total += s;
-    }
-    __syncthreads();
-    return wave_base + incl - v;
-}
-
 __global__ __launch_bounds__(kScanThreads) void scan_reduce_kernel(const uint32_t* __restrict__ in, int64_t n,
                                                                    uint32_t* __restrict__ partials) {
     __shared__ uint32_t s_wave[kScanThreads / kWave];
@@ -439,6 +414,11 @@ gsx_hip_status gsx_hip_radix_sort_keys_u64(uint64_t* keys, uint64_t* keys_alt, i
 }  // extern "C"
 
 namespace gsx_amd {
+
+gsx_hip_status scan_partials_in_place(uint32_t* partials, int64_t count, hipStream_t stream) {
+    hipLaunchKernelGGL(scan_partials_kernel, dim3(1), dim3(kScanThreads), 0, stream, partials, count);
+    return (gsx_hip_status)hipGetLastError();
+}
 
 gsx_hip_status radix_sort_keys_u64_compacting(uint64_t* keys, uint64_t* keys_alt, int64_t n, uint32_t* n_live,
                                               int begin_bit, int end_bit, void* temp, int* out_in_alt,
