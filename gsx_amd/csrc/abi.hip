@@ -555,13 +555,11 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
                            depth_max, index_bits, big_flag ? kBigKeyFlag : 0ull);
         GSX_HIP_TRY(hipGetLastError(), "preprocess_kernel");
         ctx->big_slot ^= 1;  // the slot this preprocess cleared
-        hipLaunchKernelGGL(big_tiles_kernel<false>, dim3(kBigBlocks, big_chunks), dim3(256), 0, stream,
-                           ctx->big_list.as<uint32_t>(), big_count, ctx->rec.as<float4>(), cam.tiles_x,
-                           KeyLayout{}, big_chunk, ctx->tile_count.as<uint32_t>(),
-                           ctx->big_chunk_counts.as<uint32_t>(),
-                           reinterpret_cast<unsigned long long*>(static_cast<char*>(ctx->kept_parts.dev) + big_parts_at),
-                           nullptr, nullptr, nullptr, nullptr);
-        GSX_HIP_TRY(hipGetLastError(), "big_tiles_kernel<count>");
+        hipLaunchKernelGGL(big_tiles_count_kernel, dim3(kBigBlocks, big_chunks), dim3(256), 0, stream,
+                           ctx->big_list.as<uint32_t>(), big_count, ctx->rec.as<float4>(), cam.tiles_x, big_chunk,
+                           ctx->tile_count.as<uint32_t>(), ctx->big_chunk_counts.as<uint32_t>(),
+                           reinterpret_cast<unsigned long long*>(static_cast<char*>(ctx->kept_parts.dev) + big_parts_at));
+        GSX_HIP_TRY(hipGetLastError(), "big_tiles_count_kernel");
     }
     // the counting kernels leave the instance count as per-workgroup partials in host memory;
     // the depth order and the count scan are queued behind them, so the GPU keeps working while
@@ -620,16 +618,13 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
                                   "checkpoints"));
     }
     if (n > 0) {
-        hipLaunchKernelGGL(emit_keys_kernel, dim3(pre_blocks), dim3(256), 0, stream, n, ctx->rec.as<float4>(),
+        const uint32_t big_blocks = kBigBlocks * big_chunks;
+        hipLaunchKernelGGL(emit_kernel, dim3(big_blocks + pre_blocks), dim3(256), 0, stream, n, ctx->rec.as<float4>(),
                            ctx->rank_g.as<uint32_t>(), ctx->rank_count.as<uint32_t>(), ctx->scan_temp.as<uint32_t>(),
-                           ctx->offsets.as<uint32_t>(),
-                           cam.tiles_x, layout, ctx->keys.as<uint64_t>(), ctx->inst_gauss.as<uint32_t>());
-        GSX_HIP_TRY(hipGetLastError(), "emit_keys_kernel");
-        hipLaunchKernelGGL(big_tiles_kernel<true>, dim3(kBigBlocks, big_chunks), dim3(256), 0, stream,
-                           ctx->big_list.as<uint32_t>(), big_count, ctx->rec.as<float4>(), cam.tiles_x, layout,
-                           big_chunk, nullptr, ctx->big_chunk_counts.as<uint32_t>(), nullptr, ctx->offsets.as<uint32_t>(),
+                           ctx->offsets.as<uint32_t>(), cam.tiles_x, layout, ctx->big_list.as<uint32_t>(), big_count,
+                           kBigBlocks, big_blocks, big_chunk, ctx->big_chunk_counts.as<uint32_t>(),
                            ctx->g_rank.as<uint32_t>(), ctx->keys.as<uint64_t>(), ctx->inst_gauss.as<uint32_t>());
-        GSX_HIP_TRY(hipGetLastError(), "big_tiles_kernel<emit>");
+        GSX_HIP_TRY(hipGetLastError(), "emit_kernel");
     }
     GSX_TRY(record(ctx, 3, stream));
     int in_alt = 0;

@@ -299,23 +299,20 @@ __global__ __launch_bounds__(256) void rank_gather_kernel(int64_t n, const uint3
 // instance_gaussian[position] = g. A stable sort on the tile bits then leaves every tile's run
 // in (depth, index) order.
 // The offsets are finished here: block_prefix[b] is the exclusive scan of rank_gather_kernel's
-// 256-rank sums (same workgroup size and grid), and each workgroup scans its own 256 counts;
-// offsets[0..n] are stored for the later kernels (offsets[n] = total).
+// 256-rank sums, and emission workgroup b (ranks 256 b .. 256 b + 255, rank_gather_kernel's
+// blocking) scans its own 256 counts; offsets[0..n] are stored for the later kernels
+// (offsets[n] = total).
 // ---------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void emit_keys_kernel(int64_t n, const float4* __restrict__ rec,
-                                                        const uint32_t* __restrict__ rank_gaussian,
-                                                        const uint32_t* __restrict__ rank_count,
-                                                        const uint32_t* __restrict__ block_prefix,
-                                                        uint32_t* __restrict__ offsets, int32_t tiles_x,
-                                                        KeyLayout layout, uint64_t* __restrict__ keys,
-                                                        uint32_t* __restrict__ instance_gaussian) {
-    __shared__ WaveBoxes s_boxes[kWavesPerBlock];
-    __shared__ uint32_t s_wave[kWavesPerBlock];
+__device__ inline void emit_block(uint32_t b, int64_t n, const float4* __restrict__ rec,
+                                  const uint32_t* __restrict__ rank_gaussian, const uint32_t* __restrict__ rank_count,
+                                  const uint32_t* __restrict__ block_prefix, uint32_t* __restrict__ offsets,
+                                  int32_t tiles_x, KeyLayout layout, uint64_t* __restrict__ keys,
+                                  uint32_t* __restrict__ instance_gaussian, WaveBoxes* s_boxes, uint32_t* s_wave) {
     WaveBoxes& wb = s_boxes[threadIdx.x / kWave];
-    const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t r = (int64_t)b * blockDim.x + threadIdx.x;
     const uint32_t cnt = r < n ? rank_count[r] : 0u;
     uint32_t block_total;
-    const uint32_t o = block_prefix[blockIdx.x] + block_exclusive_scan_256(cnt, s_wave, block_total);
+    const uint32_t o = block_prefix[b] + block_exclusive_scan_256(cnt, s_wave, block_total);
     if (r < n) offsets[r] = o;
     if (r == n - 1) offsets[n] = o + cnt;
     bool any = cnt > 0;
@@ -324,7 +321,7 @@ __global__ __launch_bounds__(256) void emit_keys_kernel(int64_t n, const float4*
     if (any) {
         g = rank_gaussian[r];
         r2 = rec[3 * (size_t)g + 2];
-        any = box_tiles(r2) <= kBigTiles;  // big boxes are emitted by big_tiles_kernel
+        any = box_tiles(r2) <= kBigTiles;  // big boxes are emitted by big_tiles_block
     }
     if (any) {
         r0 = rec[3 * (size_t)g + 0];
@@ -335,33 +332,31 @@ __global__ __launch_bounds__(256) void emit_keys_kernel(int64_t n, const float4*
 }
 
 // Big boxes: the row-major tile range of each box on big_list is cut into chunks of `chunk`
-// tiles (at most kBigChunks per box); workgroup (x, c) takes chunk c of the boxes x, x + gridDim.x,
-// ... and walks it 256 tiles per step. kEmit = false stores the chunk's kept-tile count in
-// chunk_counts[i][c] and adds it to tile_count[g] (zeroed by preprocess), and the workgroup's
-// kept tiles in total to kept_part[y * gridDim.x + x] (host memory); kEmit = true writes
-// the chunk's kept instances at offsets[rank of g] + the counts of the box's earlier chunks +
-// their rank within the chunk (per-wave ballots and a 4-wave prefix), i.e. in the same
-// row-major order as a single walk.
+// tiles (at most kBigChunks per box); workgroup (x, c) of the gx * chunks big-box workgroups
+// takes chunk c of the boxes x, x + gx, ... and walks it 256 tiles per step.
+// kEmit = false stores the chunk's kept-tile count in chunk_counts[i][c] and adds it to
+// tile_count[g] (zeroed by preprocess), and the workgroup's kept tiles in total to
+// kept_part[c * gx + x] (host memory). kEmit = true writes the chunk's kept instances at
+// offset(rank of g) + the counts of the box's earlier chunks + their rank within the chunk
+// (per-wave ballots and a 4-wave prefix), i.e. in the same row-major order as a single walk;
+// it runs beside emit_block in one launch, so it forms the offset itself: block_prefix of the
+// rank's 256-rank block plus the counts of the ranks before it in that block.
 constexpr uint32_t kBigChunks = 16;
 
 template <bool kEmit>
-__global__ __launch_bounds__(256) void big_tiles_kernel(const uint32_t* __restrict__ big_list,
-                                                        const uint32_t* __restrict__ big_count,
-                                                        const float4* __restrict__ rec, int32_t tiles_x,
-                                                        KeyLayout layout, uint32_t chunk,
-                                                        uint32_t* __restrict__ tile_count,
-                                                        uint32_t* __restrict__ chunk_counts,
-                                                        unsigned long long* __restrict__ kept_part,
-                                                        const uint32_t* __restrict__ offsets,
-                                                        const uint32_t* __restrict__ gaussian_rank,
-                                                        uint64_t* __restrict__ keys,
-                                                        uint32_t* __restrict__ instance_gaussian) {
-    __shared__ uint32_t s_wave[kWavesPerBlock];
+__device__ inline void big_tiles_block(uint32_t x, uint32_t c, uint32_t gx, const uint32_t* __restrict__ big_list,
+                                       const uint32_t* __restrict__ big_count, const float4* __restrict__ rec,
+                                       int32_t tiles_x, KeyLayout layout, uint32_t chunk,
+                                       uint32_t* __restrict__ tile_count, uint32_t* __restrict__ chunk_counts,
+                                       unsigned long long* __restrict__ kept_part,
+                                       const uint32_t* __restrict__ rank_count,
+                                       const uint32_t* __restrict__ block_prefix,
+                                       const uint32_t* __restrict__ gaussian_rank, uint64_t* __restrict__ keys,
+                                       uint32_t* __restrict__ instance_gaussian, uint32_t* s_wave, uint32_t* s_red) {
     const uint32_t count = *big_count;
     const uint32_t lane = __lane_id(), wave = threadIdx.x / kWave;
-    const uint32_t c = blockIdx.y;
     unsigned long long block_kept = 0;
-    for (uint32_t i = blockIdx.x; i < count; i += gridDim.x) {
+    for (uint32_t i = x; i < count; i += gx) {
         const uint32_t g = big_list[i];
         const float4 r0 = rec[3 * (size_t)g + 0], r1 = rec[3 * (size_t)g + 1], r2 = rec[3 * (size_t)g + 2];
         const uint32_t bx = __float_as_uint(r2.y), by = __float_as_uint(r2.z);
@@ -376,7 +371,16 @@ __global__ __launch_bounds__(256) void big_tiles_kernel(const uint32_t* __restri
         const float rwx = 1.0f / (float)wx;
         uint32_t o = 0;
         if (kEmit) {
-            o = offsets[gaussian_rank[g]];
+            // offset of the box's rank; s_red is rewritten only after the tile loop's barriers
+            const uint32_t rr = gaussian_rank[g];
+            const uint32_t b0 = rr & ~255u;
+            const uint32_t v = b0 + threadIdx.x < rr ? rank_count[b0 + threadIdx.x] : 0u;
+            const uint32_t ws = wave_reduce_sum_u32(v);
+            if (lane == 0) s_red[wave] = ws;
+            __syncthreads();
+            o = block_prefix[rr >> 8];
+#pragma unroll
+            for (int w = 0; w < kWavesPerBlock; ++w) o += s_red[w];
             for (uint32_t cc = 0; cc < c; ++cc) o += chunk_counts[(size_t)i * kBigChunks + cc];
         }
         uint32_t running = 0;
@@ -414,7 +418,47 @@ __global__ __launch_bounds__(256) void big_tiles_kernel(const uint32_t* __restri
         }
         block_kept += running;
     }
-    if (!kEmit && threadIdx.x == 0) kept_part[(size_t)blockIdx.y * gridDim.x + blockIdx.x] = block_kept;
+    if (!kEmit && threadIdx.x == 0) kept_part[(size_t)c * gx + x] = block_kept;
+}
+
+// Kept-tile counts of the big boxes: grid (gx, chunks).
+__global__ __launch_bounds__(256) void big_tiles_count_kernel(const uint32_t* __restrict__ big_list,
+                                                              const uint32_t* __restrict__ big_count,
+                                                              const float4* __restrict__ rec, int32_t tiles_x,
+                                                              uint32_t chunk, uint32_t* __restrict__ tile_count,
+                                                              uint32_t* __restrict__ chunk_counts,
+                                                              unsigned long long* __restrict__ kept_part) {
+    __shared__ uint32_t s_wave[kWavesPerBlock];
+    big_tiles_block<false>(blockIdx.x, blockIdx.y, gridDim.x, big_list, big_count, rec, tiles_x, KeyLayout{}, chunk,
+                           tile_count, chunk_counts, kept_part, nullptr, nullptr, nullptr, nullptr, nullptr, s_wave,
+                           nullptr);
+}
+
+// All emission in one launch: workgroups [0, big_blocks) are the big-box workgroups
+// (x = index % gx, chunk = index / gx), first so that their longer walks start early; the rest
+// are the emission workgroups of the ranks.
+__global__ __launch_bounds__(256) void emit_kernel(int64_t n, const float4* __restrict__ rec,
+                                                   const uint32_t* __restrict__ rank_gaussian,
+                                                   const uint32_t* __restrict__ rank_count,
+                                                   const uint32_t* __restrict__ block_prefix,
+                                                   uint32_t* __restrict__ offsets, int32_t tiles_x, KeyLayout layout,
+                                                   const uint32_t* __restrict__ big_list,
+                                                   const uint32_t* __restrict__ big_count, uint32_t gx,
+                                                   uint32_t big_blocks, uint32_t chunk,
+                                                   const uint32_t* __restrict__ chunk_counts,
+                                                   const uint32_t* __restrict__ gaussian_rank,
+                                                   uint64_t* __restrict__ keys, uint32_t* __restrict__ instance_gaussian) {
+    __shared__ WaveBoxes s_boxes[kWavesPerBlock];
+    __shared__ uint32_t s_wave[kWavesPerBlock];
+    __shared__ uint32_t s_red[kWavesPerBlock];
+    if (blockIdx.x < big_blocks) {
+        big_tiles_block<true>(blockIdx.x % gx, blockIdx.x / gx, gx, big_list, big_count, rec, tiles_x, layout, chunk,
+                              nullptr, const_cast<uint32_t*>(chunk_counts), nullptr, rank_count, block_prefix,
+                              gaussian_rank, keys, instance_gaussian, s_wave, s_red);
+        return;
+    }
+    emit_block(blockIdx.x - big_blocks, n, rec, rank_gaussian, rank_count, block_prefix, offsets, tiles_x, layout, keys,
+               instance_gaussian, s_boxes, s_wave);
 }
 
 __global__ __launch_bounds__(256) void fill_u32_kernel(uint32_t* __restrict__ p, int64_t count, uint32_t v) {
