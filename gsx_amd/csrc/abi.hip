@@ -135,8 +135,8 @@ struct PinnedBuffer {
 
 // Workgroups of the big-box passes (grid-stride over the list of big boxes).
 constexpr unsigned kBigBlocks = 512;
-// Workgroups per chunk column of reduce_long_chunks_kernel (4 waves each, grid-stride over the
-// list of long runs), and of combine_long_runs_kernel.
+// Workgroups per chunk column of the long-run reduction (4 waves each, grid-stride over the list
+// of long runs).
 constexpr unsigned kLongRunBlocks = 512;
 
 unsigned blocks_for(int64_t n, int threads) {
@@ -691,6 +691,10 @@ gsx_hip_status gsx_hip_render_backward(gsx_hip_render_context* ctx, const float*
     const uint32_t* counters = ctx->counters.as<uint32_t>();  // as the forward left them
     // per-instance partials: [I][8] records, then the [I] opacity terms
     float* inst_grad_op = ctx->inst_grad.as<float>() + (size_t)ctx->instance_count * 8;
+    // long instance runs are summed in chunks of long_chunk positions: a run has at most `tiles`
+    // instances, so at most kLongChunks chunks
+    const uint32_t long_chunk = std::max<uint32_t>(
+        kWave, ((uint32_t)(tiles + (int)kLongChunks - 1) / kLongChunks + kWave - 1) / kWave * kWave);
     GSX_TRY(record(ctx, 7, stream));
     const int tiles_padded = ((tiles + 7) / 8) * 8;
     hipLaunchKernelGGL(blend_backward_kernel, dim3((unsigned)tiles_padded), dim3(256), 0, stream,
@@ -700,29 +704,20 @@ gsx_hip_status gsx_hip_render_backward(gsx_hip_render_context* ctx, const float*
     GSX_HIP_TRY(hipGetLastError(), "blend_backward_kernel");
     GSX_TRY(record(ctx, 8, stream));
     if (n > 0) {
-        hipLaunchKernelGGL(reduce_instance_grads_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, n, counters,
-                           ctx->offsets.as<uint32_t>(), ctx->rank_g.as<uint32_t>(), ctx->inst_grad.as<float>(),
-                           inst_grad_op, ctx->grad2d.as<float>());
+        hipLaunchKernelGGL(reduce_instance_grads_kernel, dim3(kLongRunBlocks * kLongChunks + blocks_for(n, 256)),
+                           dim3(256), 0, stream, n, counters, ctx->offsets.as<uint32_t>(), ctx->rank_g.as<uint32_t>(),
+                           ctx->long_list.as<uint32_t>(), counters + 1, kLongRunBlocks, long_chunk,
+                           ctx->inst_grad.as<float>(), inst_grad_op, ctx->grad2d.as<float>());
         GSX_HIP_TRY(hipGetLastError(), "reduce_instance_grads_kernel");
-        // chunk length: a run has at most `tiles` instances, so at most kLongChunks chunks
-        const uint32_t chunk = std::max<uint32_t>(
-            kWave, ((uint32_t)(tiles + (int)kLongChunks - 1) / kLongChunks + kWave - 1) / kWave * kWave);
-        hipLaunchKernelGGL(reduce_long_chunks_kernel, dim3(kLongRunBlocks, kLongChunks), dim3(256), 0, stream,
-                           ctx->long_list.as<uint32_t>(), counters + 1, ctx->offsets.as<uint32_t>(), chunk,
-                           ctx->inst_grad.as<float>(), inst_grad_op);
-        GSX_HIP_TRY(hipGetLastError(), "reduce_long_chunks_kernel");
-        hipLaunchKernelGGL(combine_long_runs_kernel, dim3(kLongRunBlocks), dim3(256), 0, stream,
-                           ctx->long_list.as<uint32_t>(), counters + 1, ctx->offsets.as<uint32_t>(),
-                           ctx->rank_g.as<uint32_t>(),
-                           chunk, ctx->inst_grad.as<float>(), inst_grad_op, ctx->grad2d.as<float>());
-        GSX_HIP_TRY(hipGetLastError(), "combine_long_runs_kernel");
     }
     GSX_TRY(record(ctx, 9, stream));
     if (n > 0) {
         hipLaunchKernelGGL(projection_backward_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, n, gs.mean3d,
                            gs.rotation, gs.logscale, gs.opacity, gs.sh0, gs.sh1, gs.sh2, gs.sh3, (int)gs.sh_degree,
-                           cam, ctx->grad2d.as<float>(), grads->mean3d, grads->rotation, grads->logscale,
-                           grads->opacity, grads->sh0, grads->sh1, grads->sh2, grads->sh3);
+                           cam, ctx->grad2d.as<float>(), ctx->tile_count.as<uint32_t>(), ctx->g_rank.as<uint32_t>(),
+                           ctx->offsets.as<uint32_t>(), long_chunk, ctx->inst_grad.as<float>(), inst_grad_op,
+                           grads->mean3d, grads->rotation, grads->logscale, grads->opacity, grads->sh0, grads->sh1,
+                           grads->sh2, grads->sh3);
         GSX_HIP_TRY(hipGetLastError(), "projection_backward_kernel");
     }
     GSX_TRY(record(ctx, 10, stream));

@@ -243,18 +243,18 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
     }
 }
 
-// Marks a big box's depth key (big_tiles_kernel needs its rank). Used only when the sorted depth
+// Marks a big box's depth key (big_tiles_block needs its rank). Used only when the sorted depth
 // bits end below bit 63, which holds for fewer than 2^31 Gaussians.
 constexpr uint64_t kBigKeyFlag = 1ull << 63;
 
 // Instance runs longer than this are summed in chunks by whole waves in the backward (see
-// reduce_long_chunks_kernel), shorter ones by one lane each.
+// reduce_long_block), shorter ones by one lane each.
 constexpr uint32_t kLaneRun = 32;
 
 // After the depth sort of the V visible Gaussians (V = *depth_count): the Gaussian of every
-// depth rank, its kept-tile count, the rank of each big box (the only ranks looked up by
-// Gaussian; every Gaussian's when flagged_only is false), and the list of ranks whose count
-// exceeds kLaneRun. Ranks V..n-1 get count 0 and no Gaussian. Each workgroup also stores the sum
+// depth rank, its kept-tile count, the rank of each big box and of each Gaussian whose count
+// exceeds kLaneRun (the only ranks looked up by Gaussian; every Gaussian's when flagged_only is
+// false), and the list of ranks whose count exceeds kLaneRun. Ranks V..n-1 get count 0 and no Gaussian. Each workgroup also stores the sum
 // of its 256 counts in block_sums[block], the first step of the offsets scan (emit_keys_kernel
 // finishes it).
 __global__ __launch_bounds__(256) void rank_gather_kernel(int64_t n, const uint32_t* __restrict__ depth_count,
@@ -276,7 +276,7 @@ __global__ __launch_bounds__(256) void rank_gather_kernel(int64_t n, const uint3
             const uint32_t g = (uint32_t)(key & index_mask);
             c = tile_count[g];
             rank_gaussian[r] = g;
-            if (!flagged_only || (key & kBigKeyFlag) != 0) gaussian_rank[g] = (uint32_t)r;
+            if (!flagged_only || (key & kBigKeyFlag) != 0 || c > kLaneRun) gaussian_rank[g] = (uint32_t)r;
             if (c > kLaneRun) long_list[atomicAdd(long_count, 1u)] = (uint32_t)r;
         }
         rank_count[r] = c;
@@ -856,14 +856,15 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
 
 // grad2d[g] = sum of the partials over the emission positions [offset[r], offset[r+1]) of g, r its
 // depth rank; every Gaussian's sum is taken in a fixed order, so the result is deterministic.
-//  * runs of at most kLaneRun instances (reduce_instance_grads_kernel): the 64 runs of a wave's
-//    ranks are one contiguous span; the wave stages it through its own LDS piece by piece with
-//    coalesced loads, jumping over long runs, and each lane sums its run in position order;
+//  * runs of at most kLaneRun instances (reduce_short_block): the 64 runs of a wave's ranks are
+//    one contiguous span; the wave stages it through its own LDS piece by piece with coalesced
+//    loads, jumping over long runs, and each lane sums its run in position order into grad2d;
 //  * longer runs (listed by rank_gather_kernel; in depth order the near, large Gaussians sit
 //    side by side, and the largest cover nearly every tile): each run is cut into at most
-//    kLongChunks chunks of `chunk` positions, one wave sums a chunk (DPP tree) and leaves the
-//    partial in place at the chunk's first position (reduce_long_chunks_kernel), then one wave
-//    per run adds its chunk partials with a DPP tree (combine_long_runs_kernel).
+//    kLongChunks chunks of `chunk` positions, one wave sums a chunk (DPP tree); a run of one
+//    chunk is done, the others leave each chunk's sums in place at its first position
+//    (reduce_long_block), and projection_backward_kernel adds them in chunk order.
+// Both run in one launch (reduce_instance_grads_kernel).
 constexpr uint32_t kShortPiece = 256;  // instances per LDS piece and wave (9 KB)
 constexpr uint32_t kLongChunks = 16;
 
@@ -885,17 +886,15 @@ __device__ inline void add_instance_grad(float acc[kGrad2d], const float* __rest
     add_record(acc, rec4[0], rec4[1], instance_grad_op[p]);
 }
 
-__global__ __launch_bounds__(256) void reduce_instance_grads_kernel(int64_t n, const uint32_t* __restrict__ depth_count,
-                                                                    const uint32_t* __restrict__ offsets,
-                                                                    const uint32_t* __restrict__ rank_gaussian,
-                                                                    const float* __restrict__ instance_grad,
-                                                                    const float* __restrict__ instance_grad_op,
-                                                                    float* __restrict__ grad2d) {
-    __shared__ float4 s_rec[kWavesPerBlock][2 * kShortPiece];
-    __shared__ float s_op[kWavesPerBlock][kShortPiece];
+__device__ inline void reduce_short_block(uint32_t blk, int64_t n, const uint32_t* __restrict__ depth_count,
+                                          const uint32_t* __restrict__ offsets,
+                                          const uint32_t* __restrict__ rank_gaussian,
+                                          const float* __restrict__ instance_grad,
+                                          const float* __restrict__ instance_grad_op, float* __restrict__ grad2d,
+                                          float4 (*s_rec)[2 * kShortPiece], float (*s_op)[kShortPiece]) {
     const uint32_t lane = __lane_id(), wave = threadIdx.x / kWave;
     n = min(n, (int64_t)*depth_count);  // ranks of visible Gaussians
-    const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t r = (int64_t)blk * blockDim.x + threadIdx.x;
     const int64_t r_first = r - lane;  // first rank of this wave (waves wholly past n find no work)
     const bool valid = r < n;
     uint32_t b = 0, e = 0;
@@ -937,18 +936,19 @@ __global__ __launch_bounds__(256) void reduce_instance_grads_kernel(int64_t n, c
     }
 }
 
-// grid (x, kLongChunks): the waves of column y = k sum chunk k of the listed runs (grid-stride
-// over the list) and store the 9 sums in place of the chunk's first partial.
-__global__ __launch_bounds__(256) void reduce_long_chunks_kernel(const uint32_t* __restrict__ long_list,
-                                                                 const uint32_t* __restrict__ long_count,
-                                                                 const uint32_t* __restrict__ offsets, uint32_t chunk,
-                                                                 float* __restrict__ instance_grad,
-                                                                 float* __restrict__ instance_grad_op) {
+// Chunk k of the listed long runs, by the waves of the gx workgroups of column k (grid-stride over
+// the list). A run of one chunk gets its sums in grad2d; otherwise the 9 sums of each chunk replace
+// the chunk's first partial and projection_backward_kernel adds the run's chunk sums.
+__device__ inline void reduce_long_block(uint32_t x, uint32_t k, uint32_t gx, const uint32_t* __restrict__ long_list,
+                                         const uint32_t* __restrict__ long_count,
+                                         const uint32_t* __restrict__ offsets,
+                                         const uint32_t* __restrict__ rank_gaussian, uint32_t chunk,
+                                         float* __restrict__ instance_grad, float* __restrict__ instance_grad_op,
+                                         float* __restrict__ grad2d) {
     const uint32_t count = *long_count;
     const uint32_t lane = __lane_id();
-    const uint32_t waves = gridDim.x * (blockDim.x / kWave);
-    const uint32_t k = blockIdx.y;
-    for (uint32_t i = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave; i < count; i += waves) {
+    const uint32_t waves = gx * (blockDim.x / kWave);
+    for (uint32_t i = x * (blockDim.x / kWave) + threadIdx.x / kWave; i < count; i += waves) {
         const uint32_t r = long_list[i];
         const uint32_t b = offsets[r], e = offsets[r + 1];
         const uint32_t cb = b + k * chunk;
@@ -966,6 +966,14 @@ __global__ __launch_bounds__(256) void reduce_long_chunks_kernel(const uint32_t*
         }
 #pragma unroll
         for (int c = 0; c < kGrad2d; ++c) acc[c] = wave_reduce_sum(acc[c]);
+        if (e - b <= chunk) {  // uniform: the run is this one chunk
+            if (lane == 0) {
+                const size_t g = rank_gaussian[r];
+#pragma unroll
+                for (int c = 0; c < kGrad2d; ++c) grad2d[g * kGrad2d + c] = acc[c];
+            }
+            continue;
+        }
         // every lane's loads of the chunk fed the sums above, so overwriting position cb is safe
         if (lane == 0) {
             float4* dst = reinterpret_cast<float4*>(instance_grad) + 2 * (size_t)cb;
@@ -976,34 +984,23 @@ __global__ __launch_bounds__(256) void reduce_long_chunks_kernel(const uint32_t*
     }
 }
 
-// One wave per listed run: lane k (k < number of chunks) loads chunk k's partial, a DPP tree sums
-// them (a fixed order, so the result is deterministic), and lane 0 writes grad2d.
-__global__ __launch_bounds__(256) void combine_long_runs_kernel(const uint32_t* __restrict__ long_list,
-                                                                const uint32_t* __restrict__ long_count,
-                                                                const uint32_t* __restrict__ offsets,
-                                                                const uint32_t* __restrict__ rank_gaussian,
-                                                                uint32_t chunk, const float* __restrict__ instance_grad,
-                                                                const float* __restrict__ instance_grad_op,
-                                                                float* __restrict__ grad2d) {
-    const uint32_t count = *long_count;
-    const uint32_t lane = __lane_id();
-    const uint32_t waves = gridDim.x * (blockDim.x / kWave);
-    for (uint32_t i = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave; i < count; i += waves) {
-        const uint32_t r = long_list[i];
-        const uint32_t b = offsets[r], e = offsets[r + 1];
-        float acc[kGrad2d];
-#pragma unroll
-        for (int c = 0; c < kGrad2d; ++c) acc[c] = 0.0f;
-        const uint32_t p = b + lane * chunk;  // at most kLongChunks (16) chunks per run
-        if (lane < kLongChunks && p < e) add_instance_grad(acc, instance_grad, instance_grad_op, p);
-#pragma unroll
-        for (int c = 0; c < kGrad2d; ++c) acc[c] = wave_reduce_sum(acc[c]);
-        if (lane == 0) {
-            const size_t g = rank_gaussian[r];
-#pragma unroll
-            for (int c = 0; c < kGrad2d; ++c) grad2d[g * kGrad2d + c] = acc[c];
-        }
+// Both reductions in one launch: workgroups [0, gx * kLongChunks) sum the long runs' chunks
+// (x = index % gx, chunk = index / gx), the rest the short runs (256 ranks each).
+__global__ __launch_bounds__(256) void reduce_instance_grads_kernel(
+    int64_t n, const uint32_t* __restrict__ depth_count, const uint32_t* __restrict__ offsets,
+    const uint32_t* __restrict__ rank_gaussian, const uint32_t* __restrict__ long_list,
+    const uint32_t* __restrict__ long_count, uint32_t gx, uint32_t chunk, float* __restrict__ instance_grad,
+    float* __restrict__ instance_grad_op, float* __restrict__ grad2d) {
+    __shared__ float4 s_rec[kWavesPerBlock][2 * kShortPiece];
+    __shared__ float s_op[kWavesPerBlock][kShortPiece];
+    const uint32_t long_blocks = gx * kLongChunks;
+    if (blockIdx.x < long_blocks) {
+        reduce_long_block(blockIdx.x % gx, blockIdx.x / gx, gx, long_list, long_count, offsets, rank_gaussian, chunk,
+                          instance_grad, instance_grad_op, grad2d);
+        return;
     }
+    reduce_short_block(blockIdx.x - long_blocks, n, depth_count, offsets, rank_gaussian, instance_grad,
+                       instance_grad_op, grad2d, s_rec, s_op);
 }
 
 __device__ inline void add3(float* p, float x, float y, float z) {
@@ -1029,11 +1026,15 @@ __global__ __launch_bounds__(256) void projection_backward_kernel(
     int64_t n, const float* __restrict__ mean3d, const float* __restrict__ rotation,
     const float* __restrict__ logscale, const float* __restrict__ opacity, const float* __restrict__ sh0,
     const float* __restrict__ sh1, const float* __restrict__ sh2, const float* __restrict__ sh3, int sh_degree,
-    CameraParams cam, const float* __restrict__ grad2d, float* __restrict__ g_mean3d, float* __restrict__ g_rotation,
-    float* __restrict__ g_logscale, float* __restrict__ g_opacity, float* __restrict__ g_sh0,
-    float* __restrict__ g_sh1, float* __restrict__ g_sh2, float* __restrict__ g_sh3) {
+    CameraParams cam, const float* __restrict__ grad2d, const uint32_t* __restrict__ tile_count,
+    const uint32_t* __restrict__ gaussian_rank, const uint32_t* __restrict__ offsets, uint32_t chunk,
+    const float* __restrict__ instance_grad, const float* __restrict__ instance_grad_op, float* __restrict__ g_mean3d,
+    float* __restrict__ g_rotation, float* __restrict__ g_logscale, float* __restrict__ g_opacity,
+    float* __restrict__ g_sh0, float* __restrict__ g_sh1, float* __restrict__ g_sh2, float* __restrict__ g_sh3) {
     const int64_t gi = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (gi >= n) return;
+    // issued first: its latency overlaps the recomputation below (only visible Gaussians use it)
+    const uint32_t run_length = tile_count[gi];
     const Projected p =
         preprocess_one(gi, mean3d, rotation, logscale, opacity, sh0, sh1, sh2, sh3, sh_degree, cam, true);
     float gm[3] = {0.0f, 0.0f, 0.0f};
@@ -1051,7 +1052,18 @@ __global__ __launch_bounds__(256) void projection_backward_kernel(
 #pragma unroll
     for (int i = 0; i < 21; ++i) gs3[i] = 0.0f;
     if (p.visible) {
-        const float* a2 = grad2d + (size_t)gi * kGrad2d;
+        float a2[kGrad2d];
+        if (run_length > chunk) {
+            // a run of several chunks: the sums of its chunks, in chunk order (reduce_long_block)
+            const uint32_t r = gaussian_rank[gi];
+            const uint32_t b = offsets[r], e = offsets[r + 1];
+#pragma unroll
+            for (int c = 0; c < kGrad2d; ++c) a2[c] = 0.0f;
+            for (uint32_t cb = b; cb < e; cb += chunk) add_instance_grad(a2, instance_grad, instance_grad_op, cb);
+        } else {
+#pragma unroll
+            for (int c = 0; c < kGrad2d; ++c) a2[c] = grad2d[(size_t)gi * kGrad2d + c];
+        }
         const float dmx = a2[0], dmy = a2[1];
         const float dca = a2[2], dcb = a2[3], dcc = a2[4];
         const float dcx = a2[5], dcy = a2[6], dcz = a2[7];
