@@ -323,6 +323,13 @@ __device__ inline bool wave_none(bool p) {
     return m == 0ull;
 }
 
+// True when mask (a ballot) has no lane set; the mask is pinned to scalar registers so the test
+// is one scalar compare.
+__device__ inline bool mask_none(uint64_t m) {
+    asm volatile("" : "+s"(m));
+    return m == 0ull;
+}
+
 __device__ inline uint64_t lanemask_lt() {
     const uint32_t lane = __lane_id();
     return lane == 0 ? 0ull : (~0ull >> (64 - lane));

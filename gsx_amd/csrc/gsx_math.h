@@ -40,7 +40,8 @@
 /* The table entries (those of ARM's optimized-routines expf, which glibc ships). Host code reads
  * a static array; device code a constant array in each code object, so a lookup is one load
  * instead of a per-lane branch tree. Kernels with many expf calls per lane also copy
- * it to LDS once and use gsx_expf_table / gsx_expf_small with that copy (see below). */
+ * it to LDS once and use gsx_expf_table with that copy, or build gsx_expf_blend's folded
+ * table (see below). */
 #define GSX_EXP2_TABLE_INIT                                                                        \
   { \
     0x3ff0000000000000ULL, 0x3fefd9b0d3158574ULL, 0x3fefb5586cf9890fULL, 0x3fef9301d0125b51ULL, \
@@ -172,9 +173,23 @@ GSX_HD float gsx_expf(float x)
     return gsx_expf_table(x, 0);
 }
 
-/* gsx_expf_table for |x| < 88 (finite), without the special-case branch: bit-identical to it
- * there. The blend kernels only evaluate powers in [-4.5, 0]. */
-GSX_HD float gsx_expf_small(float x, const uint64_t *table)
+/* gsx_expf_table on [-4.5, 0], the blend kernels' clamped powers, with the exponent folded into
+ * the table: there round(x * 32/ln2) = k lies in [-208, 0], ki (the bits of kd) is
+ * 0x4338000000000000 + k, so gsx_expf_table's  t = table[ki % 32] + (ki << 47)  equals
+ * table[k mod 32] + (k << 47) (mod 2^64), a function of k alone. Entry k + 208 of a
+ * GSX_EXPF_BLEND_TABLE_SIZE-entry table holds it (gsx_expf_blend_entry), and k + 208 is the low
+ * word of ki plus 208: one add and one load instead of masking, shifting and a 64-bit add.
+ * Bit-identical to gsx_expf for every float in [-4.5, 0] (checked exhaustively on the host). */
+#define GSX_EXPF_BLEND_BIAS 208
+#define GSX_EXPF_BLEND_TABLE_SIZE 209
+
+GSX_HD uint64_t gsx_expf_blend_entry(uint32_t j)
+{
+    const int32_t k = (int32_t)j - GSX_EXPF_BLEND_BIAS;
+    return gsx_exp2_table_entry((uint32_t)k & 31u) + ((uint64_t)(int64_t)k << (52 - GSX_EXP2_TABLE_BITS));
+}
+
+GSX_HD float gsx_expf_blend(float x, const uint64_t *table)
 {
     const double inv_ln2_n = 0x1.71547652b82fep+0 * 32.0;
     const double shift = 0x1.8p+52;
@@ -184,7 +199,7 @@ GSX_HD float gsx_expf_small(float x, const uint64_t *table)
     double xd = (double)x;
     double z = inv_ln2_n * xd;
     double kd = z + shift;
-    uint64_t ki = gsx_f64_bits(kd);
+    uint32_t klo = (uint32_t)gsx_f64_bits(kd);
     double r;
     double r2;
     double y;
@@ -192,8 +207,7 @@ GSX_HD float gsx_expf_small(float x, const uint64_t *table)
 
     kd -= shift;
     r = GSX_FMA(inv_ln2_n, xd, -kd);
-    t = table[ki % 32u];
-    t += ki << (52 - GSX_EXP2_TABLE_BITS);
+    t = table[klo + GSX_EXPF_BLEND_BIAS];
     z = GSX_FMA(c0, r, c1);
     r2 = r * r;
     y = GSX_FMA(c2, r, 1.0);

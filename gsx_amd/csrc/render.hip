@@ -510,6 +510,15 @@ __device__ inline bool in_box(int px, int py, uint32_t bx, uint32_t by) {
     return (px >= (int)(bx & 0xffffu)) & (px <= (int)(bx >> 16)) & (py >= (int)(by & 0xffffu)) & (py <= (int)(by >> 16));
 }
 
+// The lanes for which `open & in_box(...)` holds, as the AND of the ballots of the five
+// conditions: each ballot is its compare's lane mask, so the wave-uniform test costs no vector
+// instruction (a ballot of the combined bool is formed through a vector register).
+// open_mask is the ballot of `open`, taken where `open` is a compare.
+__device__ inline uint64_t in_box_ballot(uint64_t open_mask, int px, int py, uint32_t bx, uint32_t by) {
+    return open_mask & wave_ballot(px >= (int)(bx & 0xffffu)) & wave_ballot(px <= (int)(bx >> 16)) &
+           wave_ballot(py >= (int)(by & 0xffffu)) & wave_ballot(py <= (int)(by >> 16));
+}
+
 // Transmittance checkpoints: the backward needs every contribution's exact T_before (the CPU
 // records it, render.c:1501-1506; recomputing it by division perturbs the last bit, which the
 // near-singular covariance gradient of near-plane Gaussians amplifies without bound). A TRAIN
@@ -536,11 +545,11 @@ __global__ __launch_bounds__(kBlendThreads) void blend_forward_kernel(
     __shared__ float4 s_r0[kBlendThreads];
     __shared__ float4 s_r1[kBlendThreads];
     __shared__ float4 s_r2[kBlendThreads];
-    __shared__ uint64_t s_exp2[GSX_EXP2_TABLE_SIZE];
+    __shared__ uint64_t s_exp2[GSX_EXPF_BLEND_TABLE_SIZE];
     const int tiles = cam.tiles_x * cam.tiles_y;
     const int tile = xcd_tile_index(blockIdx.x, tiles);
     if (tile >= tiles) return;
-    if (threadIdx.x < GSX_EXP2_TABLE_SIZE) s_exp2[threadIdx.x] = gsx_exp2_table_entry(threadIdx.x);
+    if (threadIdx.x < GSX_EXPF_BLEND_TABLE_SIZE) s_exp2[threadIdx.x] = gsx_expf_blend_entry(threadIdx.x);
     const int tx = tile % cam.tiles_x, ty = tile / cam.tiles_x;
     const int px = tx * kTile + (threadIdx.x & (kTile - 1));
     const int py = ty * kTile + (threadIdx.x / kTile);
@@ -568,13 +577,15 @@ __global__ __launch_bounds__(kBlendThreads) void blend_forward_kernel(
         const int count = __builtin_amdgcn_readfirstlane((int)min((uint32_t)kBlendThreads, range.y - base));
         for (int k = 0; k < count; ++k) {
             const bool open = t >= kTransmittanceThreshold;  // not done
-            if (wave_none(open)) break;  // uniform: every pixel of this wave is saturated
+            const uint64_t open_mask = wave_ballot(open);
+            if (mask_none(open_mask)) break;  // uniform: every pixel of this wave is saturated
             if (ckpt != nullptr && open && (k & (kBucket - 1)) == 0) {
                 ckpt[checkpoint_slot(range.x, tile, base + (uint32_t)k) * kBlendThreads + threadIdx.x] = t;
             }
             const float4 r2 = s_r2[k];
-            const bool live = open & in_box(px, py, __float_as_uint(r2.y), __float_as_uint(r2.z));  // bitwise: one lane mask
-            if (wave_none(live)) continue;  // uniform
+            const uint32_t bx = __float_as_uint(r2.y), by = __float_as_uint(r2.z);
+            const bool live = open & in_box(px, py, bx, by);  // bitwise: one lane mask
+            if (mask_none(in_box_ballot(open_mask, px, py, bx, by))) continue;  // uniform
             // branch-free evaluation for the wave; lanes outside the box or done keep their state
             const float4 r0 = s_r0[k];
             const float4 r1 = s_r1[k];
@@ -583,7 +594,7 @@ __global__ __launch_bounds__(kBlendThreads) void blend_forward_kernel(
             float power = -0.5f * (r0.z * dx * dx + r0.w * dx * dy + r1.x * dy * dy);
             power = power > 0.0f ? 0.0f : power;
             bool ok = live & (power >= kPowerThreshold);
-            const float gval = gsx_expf_small(fmaxf(power, kPowerThreshold), s_exp2);
+            const float gval = gsx_expf_blend(fmaxf(power, kPowerThreshold), s_exp2);
             const float alpha = fminf(kMaxFragmentAlpha, r1.y * gval);
             ok = ok & (alpha >= kMinAlpha);
             const float w = alpha * t;
@@ -648,12 +659,12 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
     __shared__ uint32_t s_pos[kBackBatch];
     __shared__ float s_ck[kBatchBuckets][kBlendThreads];
     __shared__ float s_acc[kRowsPerTile][kBucket][kGrad2d];
-    __shared__ uint64_t s_exp2[GSX_EXP2_TABLE_SIZE];
+    __shared__ uint64_t s_exp2[GSX_EXPF_BLEND_TABLE_SIZE];
     __shared__ uint32_t s_max_last;
     const int tiles = cam.tiles_x * cam.tiles_y;
     const int tile = xcd_tile_index(blockIdx.x, tiles);
     if (tile >= tiles) return;
-    if (threadIdx.x < GSX_EXP2_TABLE_SIZE) s_exp2[threadIdx.x] = gsx_exp2_table_entry(threadIdx.x);
+    if (threadIdx.x < GSX_EXPF_BLEND_TABLE_SIZE) s_exp2[threadIdx.x] = gsx_expf_blend_entry(threadIdx.x);
     const int tx = tile % cam.tiles_x, ty = tile / cam.tiles_x;
     const int px = tx * kTile + (threadIdx.x & (kTile - 1));
     const int py = ty * kTile + (threadIdx.x / kTile);
@@ -741,6 +752,7 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
             {
                 float tt = s_ck[sb][threadIdx.x];
                 const bool pixel_live = inside && j0 < last;
+                const uint64_t pixel_mask = wave_ballot(pixel_live);
 #pragma unroll
                 for (int i = 0; i < kBucket; ++i) {
                     tb[i] = tt;
@@ -748,9 +760,10 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
                     if (i >= n_in) continue;  // uniform
                     const int kk = sb * kBucket + i;
                     const float4 r2 = s_r2[kk];
-                    const bool live = pixel_live & (j0 + (uint32_t)i < last) &
-                                      in_box(px, py, __float_as_uint(r2.y), __float_as_uint(r2.z));
-                    if (wave_none(live)) continue;  // uniform
+                    const uint32_t bx = __float_as_uint(r2.y), by = __float_as_uint(r2.z);
+                    const bool before_last = j0 + (uint32_t)i < last;
+                    const bool live = pixel_live & before_last & in_box(px, py, bx, by);
+                    if (mask_none(in_box_ballot(pixel_mask & wave_ballot(before_last), px, py, bx, by))) continue;
                     const float4 r0 = s_r0[kk];
                     const float4 r1 = s_r1[kk];
                     const float dx = fpx - r0.x;
@@ -758,7 +771,7 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
                     float power = -0.5f * (r0.z * dx * dx + r0.w * dx * dy + r1.x * dy * dy);
                     power = power > 0.0f ? 0.0f : power;
                     bool ok = live & (power >= kPowerThreshold);
-                    const float gval = gsx_expf_small(fmaxf(power, kPowerThreshold), s_exp2);
+                    const float gval = gsx_expf_blend(fmaxf(power, kPowerThreshold), s_exp2);
                     const float alpha = fminf(kMaxFragmentAlpha, r1.y * gval);
                     ok = ok & (alpha >= kMinAlpha);
                     mask |= ok ? (1u << i) : 0u;

@@ -1554,6 +1554,31 @@ int64_t oracle_adc_step(int64_t n, float **fields, float **moments, float **aux,
 }
 
 /* Number of float inputs in [lo_bits, hi_bits] where gsx_expf differs from libm expf. */
+/* gsx_expf_blend (the blend kernels' expf, exponent folded into a 209-entry table) against the
+ * host expf over [lo_bits, hi_bits]; its domain is [-4.5, 0]. */
+uint64_t oracle_expf_blend_mismatches(uint32_t lo_bits, uint32_t hi_bits, uint32_t stride)
+{
+    uint64_t table[GSX_EXPF_BLEND_TABLE_SIZE];
+    uint64_t bad = 0;
+    uint64_t u;
+    uint32_t j;
+
+    for(j = 0; j < GSX_EXPF_BLEND_TABLE_SIZE; ++j) {
+        table[j] = gsx_expf_blend_entry(j);
+    }
+    if(stride == 0) stride = 1;
+    for(u = lo_bits; u <= hi_bits; u += stride) {
+        float x = gsx_f32_from_bits((uint32_t)u);
+        float a = expf(x);
+        float b = gsx_expf_blend(x, table);
+
+        if(gsx_f32_bits(a) != gsx_f32_bits(b)) {
+            bad += 1;
+        }
+    }
+    return bad;
+}
+
 uint64_t oracle_expf_mismatches(uint32_t lo_bits, uint32_t hi_bits, uint32_t stride)
 {
     uint64_t bad = 0;

@@ -78,6 +78,8 @@ class Oracle:
         lib.oracle_adc_step.argtypes = [_i64, _vp, _vp, _vp, ctypes.POINTER(AdcParams), _vp]
         lib.oracle_expf_mismatches.restype = ctypes.c_uint64
         lib.oracle_expf_mismatches.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32]
+        lib.oracle_expf_blend_mismatches.restype = ctypes.c_uint64
+        lib.oracle_expf_blend_mismatches.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32]
         self.lib = lib
 
     # -- render -----------------------------------------------------------------------------
@@ -204,6 +206,9 @@ class Oracle:
 
     def expf_mismatches(self, lo_bits, hi_bits, stride=1):
         return int(self.lib.oracle_expf_mismatches(lo_bits, hi_bits, stride))
+
+    def expf_blend_mismatches(self, lo_bits, hi_bits, stride=1):
+        return int(self.lib.oracle_expf_blend_mismatches(lo_bits, hi_bits, stride))
 
 
 class Reference:

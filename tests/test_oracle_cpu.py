@@ -208,6 +208,14 @@ def test_expf_restatement_matches_libm(oracle):
     assert oracle.expf_mismatches(0x00000000, 0xFFFFFFFF, 977) == 0  # everything else, sampled
 
 
+def test_expf_blend_table_matches_libm(oracle):
+    """gsx_expf_blend (exponent folded into a 209-entry table, the blend kernels' expf) == host
+    expf for every float of its domain [-4.5, 0], -0 and the subnormals included; the endpoints
+    are the table's first and last entries."""
+    assert oracle.expf_blend_mismatches(0x80000000, 0xC0900000) == 0
+    assert oracle.expf_blend_mismatches(0x00000000, 0x00000000) == 0  # +0
+
+
 def test_scene_pcg32_matches_gsx(reference):
     """The scene generator's uniform/normal streams equal gsx_pcg32_next_float/_next_normal."""
     lib = reference.lib
