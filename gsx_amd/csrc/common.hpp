@@ -404,8 +404,11 @@ __device__ inline uint32_t wave_reduce_sum_u32(uint32_t v) {
 // 22 lane operations for the 8 values instead of 32, plus 4 for v[8], and 8 lanes of a row hold
 // the 8 totals, so one store writes them all.
 __device__ inline float row_reduce_scatter9(const float (&v)[9], float& total8) {
-    const uint32_t l = __lane_id();
-    const bool b3 = (l & 8u) != 0, b2 = (l & 4u) != 0, b1 = (l & 2u) != 0;
+    // lane-constant predicates from constant lane masks (scalar moves; (l & 8) != 0 etc. would be
+    // recomputed with vector instructions wherever scalar registers run short)
+    const bool b3 = __builtin_amdgcn_inverse_ballot_w64(0xff00ff00ff00ff00ull);  // lane bit 3
+    const bool b2 = __builtin_amdgcn_inverse_ballot_w64(0xf0f0f0f0f0f0f0f0ull);  // lane bit 2
+    const bool b1 = __builtin_amdgcn_inverse_ballot_w64(0xccccccccccccccccull);  // lane bit 1
     float b[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {

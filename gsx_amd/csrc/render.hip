@@ -784,8 +784,10 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
             for (int i = kBucket - 1; i >= 0; --i) {
                 if (i >= n_in) continue;  // uniform
                 const int kk = sb * kBucket + i;
-                const bool contrib = ((mask >> i) & 1u) != 0u;
-                if (wave_none(contrib)) {  // uniform: no pixel of this wave
+                // one compare: the ballot, and the lane predicate read back from it
+                const uint64_t contrib_mask = wave_ballot((mask & (1u << i)) != 0u);
+                const bool contrib = __builtin_amdgcn_inverse_ballot_w64(contrib_mask);
+                if (mask_none(contrib_mask)) {  // uniform: no pixel of this wave
                     if (lane < 4 * kGrad2d) s_acc[wave * 4 + lane / kGrad2d][i][lane % kGrad2d] = 0.0f;
                     continue;
                 }
