@@ -747,7 +747,6 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
             const int n_in = min(kBucket, count - sb * kBucket);
             float tb[kBucket];
             float gv[kBucket];
-            uint32_t mask = 0u;
             // forward replay of the bucket from its checkpoint (render.c:1476-1515)
             {
                 float tt = s_ck[sb][threadIdx.x];
@@ -774,7 +773,6 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
                     const float gval = gsx_expf_blend(fmaxf(power, kPowerThreshold), s_exp2);
                     const float alpha = fminf(kMaxFragmentAlpha, r1.y * gval);
                     ok = ok & (alpha >= kMinAlpha);
-                    mask |= ok ? (1u << i) : 0u;
                     gv[i] = ok ? gval : 0.0f;
                     tt = ok ? tt * (1.0f - alpha) : tt;
                 }
@@ -784,8 +782,9 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
             for (int i = kBucket - 1; i >= 0; --i) {
                 if (i >= n_in) continue;  // uniform
                 const int kk = sb * kBucket + i;
-                // one compare: the ballot, and the lane predicate read back from it
-                const uint64_t contrib_mask = wave_ballot((mask & (1u << i)) != 0u);
+                // a contribution has G = exp(power) >= exp(-4.5) > 0 and the others keep G = 0;
+                // one compare gives the ballot, and the lane predicate is read back from it
+                const uint64_t contrib_mask = wave_ballot(gv[i] != 0.0f);
                 const bool contrib = __builtin_amdgcn_inverse_ballot_w64(contrib_mask);
                 if (mask_none(contrib_mask)) {  // uniform: no pixel of this wave
                     if (lane < 4 * kGrad2d) s_acc[wave * 4 + lane / kGrad2d][i][lane % kGrad2d] = 0.0f;
