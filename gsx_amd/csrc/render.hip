@@ -522,10 +522,10 @@ __device__ inline uint64_t in_box_ballot(uint64_t open_mask, int px, int py, uin
 // Transmittance checkpoints: the backward needs every contribution's exact T_before (the CPU
 // records it, render.c:1501-1506; recomputing it by division perturbs the last bit, which the
 // near-singular covariance gradient of near-plane Gaussians amplifies without bound). A TRAIN
-// forward therefore stores each pixel's T at the start of every 16-entry bucket of its tile's
-// list. Bucket k of a tile whose list starts at position x lives in slot x/16 + tile + k, which
-// is collision-free and needs at most I/16 + tiles + 1 slots of 256 floats.
-constexpr int kBucket = 16;
+// forward therefore stores each pixel's T at the start of every 8-entry bucket of its tile's
+// list. Bucket k of a tile whose list starts at position x lives in slot x/8 + tile + k, which
+// is collision-free and needs at most I/8 + tiles + 1 slots of 256 floats.
+constexpr int kBucket = 8;
 
 __device__ inline size_t checkpoint_slot(uint32_t range_start, int tile, uint32_t position) {
     return (size_t)(range_start / kBucket) + (size_t)tile + (size_t)((position - range_start) / kBucket);
@@ -624,7 +624,7 @@ constexpr int kGradRecord = 8;  // per-instance partials: channels 0-7 in one 32
 
 // ---------------------------------------------------------------------------------------------
 // Blend backward: render.c:1559-1666 restated per pixel, back to front, with the CPU's exact
-// T_before: for each 16-entry bucket (last first) the pixel reloads the bucket's checkpointed T,
+// T_before: for each 8-entry bucket (last first) the pixel reloads the bucket's checkpointed T,
 // replays the bucket forward (same operations as the forward, so T_before, G and the contribution
 // set are bit-identical to the CPU's) and then walks it backwards accumulating the suffix colour
 // exactly as the CPU does. Per contribution the gradient terms are the CPU's, including the
@@ -640,9 +640,10 @@ constexpr int kGradRecord = 8;  // per-instance partials: channels 0-7 in one 32
 constexpr int kWavesPerTile = kBlendThreads / kWave;
 constexpr int kRowsPerTile = kTile;  // 16 pixel rows = 16 DPP rows of 16 lanes
 
-// The backward stages 128 entries per batch (8 buckets): with 16-entry buckets the kernel fits
-// 128 VGPRs and 40 KB of LDS, i.e. 4 waves per SIMD.
-constexpr int kBackBatch = 128;
+// The backward stages 64 entries per batch (8 buckets of 8): the kernel fits 71 VGPRs and 19 KB
+// of LDS, i.e. 7 waves per SIMD (16-entry buckets need 87 VGPRs and 28 KB: 5 waves; the
+// checkpoints of the smaller buckets cost the forward less than the occupancy gains here).
+constexpr int kBackBatch = 64;
 constexpr int kBatchBuckets = kBackBatch / kBucket;
 
 __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
@@ -705,7 +706,7 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
     }
     if (end_all <= range.x) return;  // uniform
 
-    // Batches of 128 entries are walked back to front; records and the batch's bucket
+    // Batches of kBackBatch entries are walked back to front; records and the batch's bucket
     // checkpoints reach LDS at the start of each batch.
     const uint32_t first_batch = range.x + ((end_all - 1u - range.x) / kBackBatch) * kBackBatch;
     for (int64_t bstart = first_batch; bstart >= (int64_t)range.x; bstart -= kBackBatch) {
