@@ -628,11 +628,14 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     }
     GSX_TRY(record(ctx, 3, stream));
     int in_alt = 0;
+    // tile bits in ceil(bits / 8) passes of equal digits of 6 to 8 bits (1080p: 13 bits, 2 x 7)
     ctx->sort_passes = (tile_bits + 7) / 8;
     {
-        const int end_bit = std::min(64, layout.tile_shift + ctx->sort_passes * 8);  // same pass count
-        GSX_TRY(gsx_hip_radix_sort_keys_u64(ctx->keys.as<uint64_t>(), ctx->keys_alt.as<uint64_t>(), count,
-                                            layout.tile_shift, end_bit, ctx->sort_temp.ptr, &in_alt, stream));
+        const int digit_bits =
+            ctx->sort_passes == 0 ? 8 : std::max(6, (tile_bits + ctx->sort_passes - 1) / ctx->sort_passes);
+        GSX_TRY(radix_sort_keys_u64_digits(ctx->keys.as<uint64_t>(), ctx->keys_alt.as<uint64_t>(), count,
+                                           layout.tile_shift, ctx->sort_passes, digit_bits, ctx->sort_temp.ptr,
+                                           &in_alt, stream));
         ctx->sorted_vals = ctx->vals.as<uint32_t>();  // written by tile_ranges_kernel
     }
     ctx->sorted_in_alt = in_alt != 0;

@@ -429,6 +429,24 @@ gsx_hip_status radix_sort_keys_u64_compacting(uint64_t* keys, uint64_t* keys_alt
                                                                          stream);
 }
 
+gsx_hip_status radix_sort_keys_u64_digits(uint64_t* keys, uint64_t* keys_alt, int64_t n, int begin_bit, int passes,
+                                         int digit_bits, void* temp, int* out_in_alt, hipStream_t stream) {
+    const int end_bit = begin_bit + passes * digit_bits;
+    switch (digit_bits) {
+        case 6:
+            return radix_sort_u64<false, 6, kSortChunk>(keys, nullptr, keys_alt, nullptr, n, nullptr, false, begin_bit,
+                                                         end_bit, temp, out_in_alt, stream);
+        case 7:
+            return radix_sort_u64<false, 7, kSortChunk>(keys, nullptr, keys_alt, nullptr, n, nullptr, false, begin_bit,
+                                                         end_bit, temp, out_in_alt, stream);
+        case 8:
+            return radix_sort_u64<false, 8, kSortChunk>(keys, nullptr, keys_alt, nullptr, n, nullptr, false, begin_bit,
+                                                         end_bit, temp, out_in_alt, stream);
+        default:
+            return GSX_HIP_ERROR_INVALID_ARGUMENT;
+    }
+}
+
 size_t radix_sort_keys_u64_compacting_temp_bytes(int64_t n) {
     return radix_temp_bytes<kCompactingRadixBits, kCompactingChunk>(n);
 }
