@@ -642,7 +642,8 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     GSX_TRY(record(ctx, 4, stream));
     const uint64_t* skeys = ctx->sorted_in_alt ? ctx->keys_alt.as<uint64_t>() : ctx->keys.as<uint64_t>();
     if (count > 0) {
-        hipLaunchKernelGGL(tile_ranges_kernel, dim3(blocks_for(count, 256)), dim3(256), 0, stream, skeys, layout,
+        hipLaunchKernelGGL(tile_ranges_kernel, dim3(blocks_for((count + 3) / 4, 256)), dim3(256), 0, stream, skeys,
+                           layout,
                            ctx->sorted_vals, ctx->offsets.as<uint32_t>() + n, (uint32_t)tiles,
                            ctx->ranges.as<uint2>());
     } else {

@@ -475,24 +475,54 @@ __global__ __launch_bounds__(256) void fill_f32_kernel(float* __restrict__ p, in
 // key (values[i], the payload bits). Tiles without keys get (0, 0): the thread of the last key
 // before such a gap (or of the first key, for the tiles before it) writes them, so no fill of
 // all tiles is needed beforehand. count >= 1 (with no keys the caller fills the ranges).
+// Each thread takes 4 consecutive sorted keys (two 16-byte loads, one 16-byte store of their
+// positions), plus the keys just before and after them for the boundaries.
 __global__ __launch_bounds__(256) void tile_ranges_kernel(const uint64_t* __restrict__ keys, KeyLayout layout,
                                                           uint32_t* __restrict__ values, const uint32_t* count_ptr,
                                                           uint32_t tiles, uint2* __restrict__ ranges) {
     const uint32_t count = *count_ptr;
-    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= count) return;
-    const uint64_t key = keys[i];
-    const uint32_t tile = key_tile(layout, key);
-    if (i == 0) {
-        for (uint32_t t = 0; t < tile; ++t) ranges[t] = make_uint2(0u, 0u);
+    const uint32_t i0 = 4u * (blockIdx.x * blockDim.x + threadIdx.x);
+    if (i0 >= count) return;
+    const uint32_t m = min(4u, count - i0);
+    uint64_t k[4];
+    if (m == 4) {
+        const ulonglong2* p = reinterpret_cast<const ulonglong2*>(keys + i0);
+        const ulonglong2 a = p[0], b = p[1];
+        k[0] = a.x;
+        k[1] = a.y;
+        k[2] = b.x;
+        k[3] = b.y;
+    } else {
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j) k[j] = j < m ? keys[i0 + j] : 0ull;
     }
-    if (i == 0 || key_tile(layout, keys[i - 1]) != tile) ranges[tile].x = i;
-    const uint32_t next = i == count - 1 ? tiles : key_tile(layout, keys[i + 1]);
-    if (next != tile) {
-        ranges[tile].y = i + 1;
-        for (uint32_t t = tile + 1; t < next; ++t) ranges[t] = make_uint2(0u, 0u);
+    uint32_t t[4];
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j) t[j] = key_tile(layout, k[j]);
+    const uint32_t prev = i0 == 0 ? UINT32_MAX : key_tile(layout, keys[i0 - 1]);
+    const uint32_t next = i0 + m == count ? tiles : key_tile(layout, keys[i0 + m]);
+    if (i0 == 0) {
+        for (uint32_t u = 0; u < t[0]; ++u) ranges[u] = make_uint2(0u, 0u);
     }
-    values[i] = (uint32_t)(key & ((1ull << layout.payload_bits) - 1ull));
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j) {
+        if (j < m) {
+            const uint32_t before = j == 0 ? prev : t[j - 1];
+            const uint32_t after = j == m - 1 ? next : t[j + 1];
+            if (before != t[j]) ranges[t[j]].x = i0 + j;
+            if (after != t[j]) {
+                ranges[t[j]].y = i0 + j + 1;
+                for (uint32_t u = t[j] + 1; u < after; ++u) ranges[u] = make_uint2(0u, 0u);
+            }
+        }
+    }
+    const uint64_t payload = (1ull << layout.payload_bits) - 1ull;
+    if (m == 4) {
+        *reinterpret_cast<uint4*>(values + i0) = make_uint4((uint32_t)(k[0] & payload), (uint32_t)(k[1] & payload),
+                                                            (uint32_t)(k[2] & payload), (uint32_t)(k[3] & payload));
+    } else {
+        for (uint32_t j = 0; j < m; ++j) values[i0 + j] = (uint32_t)(k[j] & payload);
+    }
 }
 
 // Workgroup -> tile mapping: consecutive workgroups are dealt round-robin to the 8 XCDs, so give
