@@ -605,7 +605,7 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     GSX_TRY(ctx->vals.reserve(c1 * sizeof(uint32_t), "vals"));
     GSX_TRY(ctx->inst_gauss.reserve(c1 * sizeof(uint32_t), "instance_gaussian"));
     GSX_TRY(ctx->sorted_g.reserve(c1 * sizeof(uint32_t), "sorted_g"));
-    GSX_TRY(ctx->sort_temp.reserve(gsx_hip_radix_sort_temp_bytes(count), "sort_temp"));
+    GSX_TRY(ctx->sort_temp.reserve(radix_sort_keys_u64_digits_temp_bytes(count), "sort_temp"));
     // instance keys: tile << payload_bits | emission position (at most 32 + 32 bits)
     const int pos_bits = std::max(1, bits_for((uint32_t)(count > 0 ? count - 1 : 0)));
     KeyLayout layout{};

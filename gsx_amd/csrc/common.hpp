@@ -492,9 +492,10 @@ size_t radix_sort_keys_u64_compacting_temp_bytes(int64_t n);
 // Keys-only stable radix sort (the public sort's kernels) on bits [begin_bit, begin_bit + passes *
 // digit_bits) with digits of 6, 7 or 8 bits: a key field of b bits sorts in ceil(b / 8) passes of
 // ceil(b / passes) bits, fewer ballots and bins than 8-bit digits (13-bit tiles: 2 passes of 7).
-// temp holds gsx_hip_radix_sort_temp_bytes(n) bytes (the 8-bit need, the largest).
+// temp holds radix_sort_keys_u64_digits_temp_bytes(n) bytes (the 8-bit need, the largest).
 gsx_hip_status radix_sort_keys_u64_digits(uint64_t* keys, uint64_t* keys_alt, int64_t n, int begin_bit, int passes,
                                          int digit_bits, void* temp, int* out_in_alt, hipStream_t stream);
+size_t radix_sort_keys_u64_digits_temp_bytes(int64_t n);
 
 // Single-workgroup exclusive scan of partials[0..count) in place, the total stored at [count].
 gsx_hip_status scan_partials_in_place(uint32_t* partials, int64_t count, hipStream_t stream);

@@ -23,6 +23,8 @@ constexpr int kRadixBits = 8;     // digit width of the public sorts
 // The depth order sorts about a million keys: 1024-key chunks give ~1000 workgroups per launch
 // (with 4096 a launch has fewer workgroups than the GPU has CUs, one wave per SIMD)
 constexpr int kCompactingChunk = 1024;
+// Chunk of the tile sort's passes (radix_sort_keys_u64_digits)
+constexpr int kDigitsChunk = 4096;
 constexpr int kRowItems = 16;  // row scan: 16 chunk counts per thread and step
 constexpr int kRowChunk = kSortThreads * kRowItems;
 
@@ -434,18 +436,20 @@ gsx_hip_status radix_sort_keys_u64_digits(uint64_t* keys, uint64_t* keys_alt, in
     const int end_bit = begin_bit + passes * digit_bits;
     switch (digit_bits) {
         case 6:
-            return radix_sort_u64<false, 6, kSortChunk>(keys, nullptr, keys_alt, nullptr, n, nullptr, false, begin_bit,
-                                                         end_bit, temp, out_in_alt, stream);
+            return radix_sort_u64<false, 6, kDigitsChunk>(keys, nullptr, keys_alt, nullptr, n, nullptr, false,
+                                                           begin_bit, end_bit, temp, out_in_alt, stream);
         case 7:
-            return radix_sort_u64<false, 7, kSortChunk>(keys, nullptr, keys_alt, nullptr, n, nullptr, false, begin_bit,
-                                                         end_bit, temp, out_in_alt, stream);
+            return radix_sort_u64<false, 7, kDigitsChunk>(keys, nullptr, keys_alt, nullptr, n, nullptr, false,
+                                                           begin_bit, end_bit, temp, out_in_alt, stream);
         case 8:
-            return radix_sort_u64<false, 8, kSortChunk>(keys, nullptr, keys_alt, nullptr, n, nullptr, false, begin_bit,
-                                                         end_bit, temp, out_in_alt, stream);
+            return radix_sort_u64<false, 8, kDigitsChunk>(keys, nullptr, keys_alt, nullptr, n, nullptr, false,
+                                                           begin_bit, end_bit, temp, out_in_alt, stream);
         default:
             return GSX_HIP_ERROR_INVALID_ARGUMENT;
     }
 }
+
+size_t radix_sort_keys_u64_digits_temp_bytes(int64_t n) { return radix_temp_bytes<8, kDigitsChunk>(n); }
 
 size_t radix_sort_keys_u64_compacting_temp_bytes(int64_t n) {
     return radix_temp_bytes<kCompactingRadixBits, kCompactingChunk>(n);
