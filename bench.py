@@ -70,7 +70,7 @@ def algorithmic_bytes(stage, n, visible, instances, tiles, pixels, sort_passes, 
 
 CPU_SAMPLE_STRIDE = 10
 
-STAGE_KERNEL = {"preprocess": "preprocess_kernel", "emit": "emit_keys_kernel", "ranges": "tile_ranges_kernel",
+STAGE_KERNEL = {"preprocess": "preprocess_kernel", "emit": "emit_kernel", "ranges": "tile_ranges_kernel",
                 "blend_forward": "blend_forward_kernel", "blend_backward": "blend_backward_kernel",
                 "instance_reduce": "reduce_instance_grads_kernel",
                 "projection_backward": "projection_backward_kernel", "loss_forward": "ssim_forward_kernel",
