@@ -716,12 +716,21 @@ gsx_hip_status gsx_hip_render_backward(gsx_hip_render_context* ctx, const float*
     }
     GSX_TRY(record(ctx, 9, stream));
     if (n > 0) {
-        hipLaunchKernelGGL(projection_backward_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, n, gs.mean3d,
-                           gs.rotation, gs.logscale, gs.opacity, gs.sh0, gs.sh1, gs.sh2, gs.sh3, (int)gs.sh_degree,
-                           cam, ctx->grad2d.as<float>(), ctx->tile_count.as<uint32_t>(), ctx->g_rank.as<uint32_t>(),
-                           ctx->offsets.as<uint32_t>(), long_chunk, ctx->inst_grad.as<float>(), inst_grad_op,
-                           grads->mean3d, grads->rotation, grads->logscale, grads->opacity, grads->sh0, grads->sh1,
-                           grads->sh2, grads->sh3);
+        const unsigned pblocks = blocks_for(n, 256);
+        float* const gi_op = inst_grad_op;
+#define GSX_PROJECTION_BACKWARD(D)                                                                              \
+    hipLaunchKernelGGL(projection_backward_kernel<D>, dim3(pblocks), dim3(256), 0, stream, n, gs.mean3d, gs.rotation, \
+                       gs.logscale, gs.opacity, gs.sh0, gs.sh1, gs.sh2, gs.sh3, cam, ctx->grad2d.as<float>(),        \
+                       ctx->tile_count.as<uint32_t>(), ctx->g_rank.as<uint32_t>(), ctx->offsets.as<uint32_t>(),      \
+                       long_chunk, ctx->inst_grad.as<float>(), gi_op, grads->mean3d, grads->rotation,                  \
+                       grads->logscale, grads->opacity, grads->sh0, grads->sh1, grads->sh2, grads->sh3)
+        switch (gs.sh_degree) {
+            case 0: GSX_PROJECTION_BACKWARD(0); break;
+            case 1: GSX_PROJECTION_BACKWARD(1); break;
+            case 2: GSX_PROJECTION_BACKWARD(2); break;
+            default: GSX_PROJECTION_BACKWARD(3); break;
+        }
+#undef GSX_PROJECTION_BACKWARD
         GSX_HIP_TRY(hipGetLastError(), "projection_backward_kernel");
     }
     GSX_TRY(record(ctx, 10, stream));

@@ -1067,15 +1067,19 @@ __device__ inline void add_dir(float ddir[3], const float dcol[3], const float* 
 // gradients. Sinks are overwritten (the CPU zeroes them first, render.c:1537-1550); invisible
 // Gaussians get zeros.
 // ---------------------------------------------------------------------------------------------
+// Instantiated per SH degree (0-3): the higher degrees' gradient arrays then exist only where
+// they are used (degree 0 needs 45 fewer live registers).
+template <int kShDegree>
 __global__ __launch_bounds__(256) void projection_backward_kernel(
     int64_t n, const float* __restrict__ mean3d, const float* __restrict__ rotation,
     const float* __restrict__ logscale, const float* __restrict__ opacity, const float* __restrict__ sh0,
-    const float* __restrict__ sh1, const float* __restrict__ sh2, const float* __restrict__ sh3, int sh_degree,
+    const float* __restrict__ sh1, const float* __restrict__ sh2, const float* __restrict__ sh3,
     CameraParams cam, const float* __restrict__ grad2d, const uint32_t* __restrict__ tile_count,
     const uint32_t* __restrict__ gaussian_rank, const uint32_t* __restrict__ offsets, uint32_t chunk,
     const float* __restrict__ instance_grad, const float* __restrict__ instance_grad_op, float* __restrict__ g_mean3d,
     float* __restrict__ g_rotation, float* __restrict__ g_logscale, float* __restrict__ g_opacity,
     float* __restrict__ g_sh0, float* __restrict__ g_sh1, float* __restrict__ g_sh2, float* __restrict__ g_sh3) {
+    constexpr int sh_degree = kShDegree;
     const int64_t gi = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (gi >= n) return;
     // issued first: its latency overlaps the recomputation below (only visible Gaussians use it)
