@@ -72,9 +72,12 @@ __device__ inline int ssim_tile_of(int block, int tiles) {
     return (block & 7) * per + (block >> 3);
 }
 constexpr int kSsimHW = kSsimTW + 10, kSsimHH = kSsimTH + 10;  // 42 x 26 halo
+// Output columns per work item of the horizontal passes: 26 rows x 8 items fill the workgroup
+// once, and each loaded input pixel (and its moments) serves 4 outputs.
+constexpr int kHCols = 4;
 
 // Forward: p and t of the halo in LDS; a horizontal 11-tap pass where each thread forms the
-// five moments (p, t, p^2, t^2, p t) of two adjacent output columns from 12 loads per plane;
+// five moments (p, t, p^2, t^2, p t) of four adjacent output columns from 14 loads per plane;
 // then a vertical pass where each thread produces two adjacent output rows from 12 loads per
 // moment plane. Writes the loss map (optionally after a fused L1 term) and the three dm maps
 // [3][planes][H][W] that the backward convolves.
@@ -104,27 +107,30 @@ __global__ __launch_bounds__(256) void ssim_forward_kernel(float* __restrict__ m
         s_in[1][hy][hx] = tv;
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < kSsimHH * (kSsimTW / 2); i += 256) {
-        const int hy = i / (kSsimTW / 2), cx = 2 * (i % (kSsimTW / 2));
-        float a0[5] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f}, a1[5] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i = threadIdx.x; i < kSsimHH * (kSsimTW / kHCols); i += 256) {
+        const int hy = i / (kSsimTW / kHCols), cx = kHCols * (i % (kSsimTW / kHCols));
+        float a[kHCols][5];
 #pragma unroll
-        for (int k = 0; k < 12; ++k) {
+        for (int j = 0; j < kHCols; ++j)
+#pragma unroll
+            for (int c = 0; c < 5; ++c) a[j][c] = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 10 + kHCols; ++k) {
             const float pv = s_in[0][hy][cx + k], tv = s_in[1][hy][cx + k];
             const float m[5] = {pv, tv, pv * pv, tv * tv, pv * tv};
-            if (k < 11) {
 #pragma unroll
-                for (int c = 0; c < 5; ++c) a0[c] = __builtin_fmaf(kSsimW[k], m[c], a0[c]);
-            }
-            if (k > 0) {
+            for (int j = 0; j < kHCols; ++j) {
+                // input column cx + k is tap k - j of output column cx + j (taps in order 0..10)
+                if (k - j >= 0 && k - j < 11) {
 #pragma unroll
-                for (int c = 0; c < 5; ++c) a1[c] = __builtin_fmaf(kSsimW[k - 1], m[c], a1[c]);
+                    for (int c = 0; c < 5; ++c) a[j][c] = __builtin_fmaf(kSsimW[k - j], m[c], a[j][c]);
+                }
             }
         }
 #pragma unroll
-        for (int c = 0; c < 5; ++c) {
-            s_h[c][hy][cx] = a0[c];
-            s_h[c][hy][cx + 1] = a1[c];
-        }
+        for (int j = 0; j < kHCols; ++j)
+#pragma unroll
+            for (int c = 0; c < 5; ++c) s_h[c][hy][cx + j] = a[j][c];
     }
     __syncthreads();
     const int lx = threadIdx.x % kSsimTW;
@@ -213,23 +219,28 @@ __global__ __launch_bounds__(256) void ssim_backward_kernel(float* __restrict__ 
         s_m[2][hy][hx] = v2;
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < kSsimHH * (kSsimTW / 2); i += 256) {
-        const int hy = i / (kSsimTW / 2), cx = 2 * (i % (kSsimTW / 2));
-        float a0[3] = {0.0f, 0.0f, 0.0f}, a1[3] = {0.0f, 0.0f, 0.0f};
+    for (int i = threadIdx.x; i < kSsimHH * (kSsimTW / kHCols); i += 256) {
+        const int hy = i / (kSsimTW / kHCols), cx = kHCols * (i % (kSsimTW / kHCols));
+        float a[kHCols][3];
 #pragma unroll
-        for (int k = 0; k < 12; ++k) {
+        for (int j = 0; j < kHCols; ++j)
+#pragma unroll
+            for (int c = 0; c < 3; ++c) a[j][c] = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 10 + kHCols; ++k) {
 #pragma unroll
             for (int c = 0; c < 3; ++c) {
                 const float v = s_m[c][hy][cx + k];
-                if (k < 11) a0[c] = __builtin_fmaf(kSsimW[k], v, a0[c]);
-                if (k > 0) a1[c] = __builtin_fmaf(kSsimW[k - 1], v, a1[c]);
+#pragma unroll
+                for (int j = 0; j < kHCols; ++j) {
+                    if (k - j >= 0 && k - j < 11) a[j][c] = __builtin_fmaf(kSsimW[k - j], v, a[j][c]);
+                }
             }
         }
 #pragma unroll
-        for (int c = 0; c < 3; ++c) {
-            s_h[c][hy][cx] = a0[c];
-            s_h[c][hy][cx + 1] = a1[c];
-        }
+        for (int j = 0; j < kHCols; ++j)
+#pragma unroll
+            for (int c = 0; c < 3; ++c) s_h[c][hy][cx + j] = a[j][c];
     }
     __syncthreads();
     const int lx = threadIdx.x % kSsimTW;
