@@ -813,11 +813,8 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
             for (int i = kBucket - 1; i >= 0; --i) {
                 if (i >= n_in) continue;  // uniform
                 const int kk = sb * kBucket + i;
-                // a contribution has G = exp(power) >= exp(-4.5) > 0 and the others keep G = 0;
-                // one compare gives the ballot, and the lane predicate is read back from it
-                const uint64_t contrib_mask = wave_ballot(gv[i] != 0.0f);
-                const bool contrib = __builtin_amdgcn_inverse_ballot_w64(contrib_mask);
-                if (mask_none(contrib_mask)) {  // uniform: no pixel of this wave
+                // a contribution has G = exp(power) >= exp(-4.5) > 0 and the others keep G = 0
+                if (mask_none(wave_ballot(gv[i] != 0.0f))) {  // uniform: no pixel of this wave
                     if (lane < 4 * kGrad2d) s_acc[wave * 4 + lane / kGrad2d][i][lane % kGrad2d] = 0.0f;
                     continue;
                 }
@@ -830,20 +827,22 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
                 const float op = r1.y;
                 const float alpha = fminf(kMaxFragmentAlpha, op * gval);
                 const float t_before = tb[i];
-                const float w = contrib ? alpha * t_before : 0.0f;
+                // A lane that does not contribute holds G = 0, hence alpha = 0: its weight w, dpow
+                // and opacity term below are (signed) zeros by arithmetic, and it leaves the suffix
+                // unchanged, so no per-lane select on the contribution is needed (all values are
+                // finite).
+                const float w = alpha * t_before;
                 float dalpha = t_before * (r1.z * d0 + r1.w * d1 + r2.x * d2);
-                const float one_minus = 1.0f - alpha;
                 // a correctly rounded division as the CPU's: near-plane Gaussians' covariance
-                // gradients amplify even 1-ulp differences of this term (1 - alpha lies in
-                // [0.001, 1], so the scaling steps of the general division are not needed;
-                // a zero numerator gives 0 either way)
-                if (fabsf(one_minus) > 1.0e-6f) {
-                    const float num = s0 * d0 + s1 * d1 + s2 * d2;
-                    dalpha -= num == 0.0f ? 0.0f : div_rn_normal(num, one_minus);
-                }
+                // gradients amplify even 1-ulp differences of this term. alpha <= 0.999, so
+                // 1 - alpha lies in [0.001, 1]: the CPU's |1 - alpha| > 1e-6 guard always holds,
+                // the scaling steps of the general division are not needed, and a zero numerator
+                // gives a zero quotient.
+                const float num = s0 * d0 + s1 * d1 + s2 * d2;
+                dalpha -= div_rn_normal(num, 1.0f - alpha);
                 const bool unclamped = op * gval < kMaxFragmentAlpha;
-                const float dg = (contrib && unclamped) ? dalpha * op : 0.0f;
-                const float g_op = (contrib && unclamped) ? dalpha * gval : 0.0f;
+                const float dg = unclamped ? dalpha * op : 0.0f;
+                const float g_op = unclamped ? dalpha * gval : 0.0f;
                 const float dpow = dg * gval;
                 const float inv_a = r0.z, inv_b = r0.w * 0.5f, inv_c = r1.x;
                 const float dia = dpow * (-0.5f * dx * dx);
