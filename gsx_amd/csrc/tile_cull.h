@@ -26,9 +26,20 @@
 
 #include "gsx_math.h"
 
-GSX_HD float gsx_cull_minf(float a, float b) { return b < a ? b : a; }
-GSX_HD float gsx_cull_absf(float a) { return a < 0.0f ? -a : a; }
-GSX_HD float gsx_cull_clampf(float v, float lo, float hi) { return v < lo ? lo : (v > hi ? hi : v); }
+/* min / max / |x| / clamp as the IEEE operations (one instruction each, or a free source
+ * modifier on the GPU). The test's operands are finite, where these equal the compare-and-select
+ * forms; a signed zero can differ, and a zero of either sign leaves every quantity below
+ * unchanged. lo <= hi in every clamp. */
+#if defined(__HIPCC__)
+GSX_HD float gsx_cull_minf(float a, float b) { return __builtin_fminf(a, b); }
+GSX_HD float gsx_cull_maxf(float a, float b) { return __builtin_fmaxf(a, b); }
+GSX_HD float gsx_cull_absf(float a) { return __builtin_fabsf(a); }
+#else
+GSX_HD float gsx_cull_minf(float a, float b) { return fminf(a, b); }
+GSX_HD float gsx_cull_maxf(float a, float b) { return fmaxf(a, b); }
+GSX_HD float gsx_cull_absf(float a) { return fabsf(a); }
+#endif
+GSX_HD float gsx_cull_clampf(float v, float lo, float hi) { return gsx_cull_minf(gsx_cull_maxf(v, lo), hi); }
 
 /* Natural logarithm of a positive normal float from IEEE operations only, so the CPU and the
  * GPU agree bit for bit: x = m 2^e with m in [sqrt(1/2), sqrt(2)), ln m = 2 atanh(s),
@@ -100,8 +111,8 @@ GSX_HD int gsx_tile_conic_test(const gsx_tile_conic *k, int px0, int px1, int py
     const float dx1 = ((float)px1 + 0.5f) - k->mx;
     const float dy0 = ((float)py0 + 0.5f) - k->my;
     const float dy1 = ((float)py1 + 0.5f) - k->my;
-    const float X = gsx_cull_absf(dx0) > gsx_cull_absf(dx1) ? gsx_cull_absf(dx0) : gsx_cull_absf(dx1);
-    const float Y = gsx_cull_absf(dy0) > gsx_cull_absf(dy1) ? gsx_cull_absf(dy0) : gsx_cull_absf(dy1);
+    const float X = gsx_cull_maxf(gsx_cull_absf(dx0), gsx_cull_absf(dx1));
+    const float Y = gsx_cull_maxf(gsx_cull_absf(dy0), gsx_cull_absf(dy1));
     const float scale = gsx_cull_absf(A) * X * X + 2.0f * gsx_cull_absf(B) * X * Y + gsx_cull_absf(C) * Y * Y;
     const float margin = 1e-4f * scale + 1e-3f;
     float au0, au1, bu0, bu1, cv0, cv1, qmin, s, q;
