@@ -79,7 +79,20 @@ struct WaveBoxes {
     int32_t x0[kWave], x1[kWave], y0[kWave], y1[kWave];
     uint32_t tx0[kWave], ty0[kWave], wx[kWave], excl[kWave], kept[kWave], out[kWave];
     uint32_t g[kWave];
+    uint32_t mark[kWave];  // walk step: base + owner at the lane where that owner's pairs start
 };
+
+// Inclusive prefix maximum over the 64 lanes of a wave (DPP row shifts, then the two row
+// broadcasts), for non-negative values; every lane must be active.
+__device__ inline int wave_inclusive_max(int v) {
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, true));  // row_shr:1
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, true));  // row_shr:2
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, true));  // row_shr:4
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, true));  // row_shr:8
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false));  // row_bcast:15
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false));  // row_bcast:31
+    return v;
+}
 
 // Stores lane's box (zero tiles when !valid) and returns the wave's total tile count.
 __device__ inline uint32_t stage_box(WaveBoxes& w, bool valid, float4 r0, float4 r1, float4 r2, uint32_t g,
@@ -123,14 +136,23 @@ __device__ inline void walk_wave_tiles(WaveBoxes& w, uint32_t wave_total, int32_
                                        uint64_t* __restrict__ keys, uint32_t* __restrict__ instance_gaussian) {
     const uint32_t lane = __lane_id();
     const uint64_t lt = lanemask_lt();
+    // the owner of pair p is the last box starting at or before p, i.e. the last non-empty one
+    // (an empty box shares its start with the next box): each non-empty box whose pairs start in
+    // the step marks that lane with base + its lane, and a prefix maximum over the lanes, carried
+    // from step to step, names every lane's owner (marks of earlier steps fall below base)
+    const uint32_t my_start = w.excl[lane];
+    const uint32_t my_count = (lane + 1 < kWave ? w.excl[lane + 1] : wave_total) - my_start;
+    w.mark[lane] = UINT32_MAX;
+    uint32_t carry = 0;
     for (uint32_t base = 0; base < wave_total; base += kWave) {
         const uint32_t p = base + lane;
         const bool active = p < wave_total;
-        uint32_t owner = 0;
-#pragma unroll
-        for (uint32_t step = kWave / 2; step > 0; step >>= 1) {
-            if (w.excl[owner + step] <= p) owner += step;
-        }
+        wave_lds_sync();  // the previous step's reads of the marks are done
+        if (my_count > 0 && my_start - base < (uint32_t)kWave) w.mark[my_start - base] = base + lane;
+        wave_lds_sync();
+        const uint32_t m = w.mark[lane] - base;
+        const uint32_t owner = max(carry, (uint32_t)wave_inclusive_max(m < (uint32_t)kWave ? (int)m : 0));
+        carry = (uint32_t)__builtin_amdgcn_readlane((int)owner, kWave - 1);
         bool keep = false;
         uint32_t tile = 0;
         if (active) {
