@@ -38,6 +38,7 @@ constexpr int kWavesPerBlock = 4;
 // Boxes of more tiles than this are walked by a whole workgroup in a pass of their own (see
 // big_tiles_kernel): a wave holding a full-image box would otherwise serialise hundreds of steps.
 constexpr uint32_t kBigTiles = 256;
+static_assert(kBigTiles <= 256, "the tile walk divides indices below 2^8 by box widths of at most 2^8");
 
 // Sort keys. Gaussians are first sorted by depth: key = (bits(depth) - bits(near)) << index_bits
 // | index (visible depths lie in [near, far], where positive floats order like their bit
@@ -75,7 +76,7 @@ __device__ inline uint32_t div_small(uint32_t k, uint32_t d, float rd) {
 
 struct WaveBoxes {
     gsx_tile_conic conic[kWave];
-    float rwx[kWave];  // 1 / wx, for the row of a flattened tile index
+    uint32_t mdiv[kWave];  // ceil(2^16 / wx): row of flattened index k (< 256) = (k * mdiv) >> 16
     int32_t x0[kWave], x1[kWave], y0[kWave], y1[kWave];
     uint32_t tx0[kWave], ty0[kWave], wx[kWave], excl[kWave], kept[kWave], out[kWave];
     uint32_t g[kWave];
@@ -111,7 +112,7 @@ __device__ inline uint32_t stage_box(WaveBoxes& w, bool valid, float4 r0, float4
         w.tx0[lane] = (uint32_t)x0 / kTile;
         w.ty0[lane] = (uint32_t)y0 / kTile;
         w.wx[lane] = (uint32_t)x1 / kTile - (uint32_t)x0 / kTile + 1;
-        w.rwx[lane] = 1.0f / (float)w.wx[lane];
+        w.mdiv[lane] = 65535u / w.wx[lane] + 1u;
         total = w.wx[lane] * ((uint32_t)y1 / kTile - (uint32_t)y0 / kTile + 1);
     }
     w.g[lane] = g;
@@ -158,7 +159,9 @@ __device__ inline void walk_wave_tiles(WaveBoxes& w, uint32_t wave_total, int32_
         if (active) {
             const uint32_t k = p - w.excl[owner];
             const uint32_t wx = w.wx[owner];
-            const uint32_t row = div_small(k, wx, w.rwx[owner]);
+            // exact for k < 2^8 and wx <= 2^8: ceil(2^16 / wx) * wx - 2^16 < wx <= 2^(16 - 8)
+            // (Granlund-Montgomery); the walked boxes have at most kBigTiles = 256 tiles
+            const uint32_t row = (k * w.mdiv[owner]) >> 16;
             const uint32_t ty = w.ty0[owner] + row;
             const uint32_t tx = w.tx0[owner] + (k - row * wx);
             tile = ty * (uint32_t)tiles_x + tx;
