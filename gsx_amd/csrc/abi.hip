@@ -139,6 +139,13 @@ constexpr unsigned kBigBlocks = 512;
 // of long runs).
 constexpr unsigned kLongRunBlocks = 512;
 
+// Long instance runs are summed in chunks of this many positions: a run has at most `tiles`
+// instances, so at most kLongChunks chunks.
+uint32_t long_chunk_of(int32_t tiles) {
+    return std::max<uint32_t>(kWave,
+                              ((uint32_t)(tiles + (int)kLongChunks - 1) / kLongChunks + kWave - 1) / kWave * kWave);
+}
+
 unsigned blocks_for(int64_t n, int threads) {
     int64_t b = (n + threads - 1) / threads;
     return (unsigned)(b < 1 ? 1 : b);
@@ -201,13 +208,14 @@ int bits_for(uint32_t v) {
 struct gsx_hip_render_context {
     DeviceBuffer rec, cov_coef, ckpt, inst_gauss, inst_grad, tile_count, big_list, offsets, scan_temp, keys, vals,
         keys_alt, sort_temp, ranges, sorted_g, final_t, last, grad2d, depth_keys, depth_keys_alt, rank_g, rank_count,
-        g_rank, long_list, counters, big_chunk_counts, depth_sort_temp;
+        g_rank, long_list, multi_list, counters, big_chunk_counts, depth_sort_temp;
     // partial instance counts written by the counting kernels (preprocess: one u32 per workgroup;
     // big boxes: one u64 per workgroup), summed on the host after count_ev
     PinnedBuffer kept_parts;
     hipEvent_t count_ev = nullptr;
     // counters: [0] visible Gaussians (depth keys), [1] long instance runs, [2 + big_slot] big boxes
-    // of the next forward (each forward's preprocess clears the other slot for its successor)
+    // of the next forward (each forward's preprocess clears the other slot for its successor),
+    // [4] runs of more than one long-run chunk
     bool counters_ready = false;
     int big_slot = 0;
     CameraParams cam{};
@@ -386,7 +394,8 @@ gsx_hip_status gsx_hip_render_context_destroy(gsx_hip_render_context* ctx) {
                            &ctx->vals,       &ctx->keys_alt, &ctx->sort_temp,  &ctx->ranges,
                            &ctx->sorted_g,   &ctx->final_t,  &ctx->last,      &ctx->grad2d,     &ctx->depth_keys,
                            &ctx->depth_keys_alt, &ctx->rank_g, &ctx->rank_count, &ctx->g_rank,
-                           &ctx->long_list, &ctx->counters, &ctx->big_chunk_counts, &ctx->depth_sort_temp};
+                           &ctx->long_list, &ctx->multi_list, &ctx->counters, &ctx->big_chunk_counts,
+                           &ctx->depth_sort_temp};
     for (DeviceBuffer* b : all) b->release();
     ctx->kept_parts.release();
     if (ctx->count_ev != nullptr) (void)hipEventDestroy(ctx->count_ev);
@@ -506,6 +515,7 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     GSX_TRY(ctx->rank_count.reserve(n1 * sizeof(uint32_t), "rank_count"));
     GSX_TRY(ctx->g_rank.reserve(n1 * sizeof(uint32_t), "gaussian_rank"));
     GSX_TRY(ctx->long_list.reserve(n1 * sizeof(uint32_t), "long_list"));
+    GSX_TRY(ctx->multi_list.reserve(n1 * sizeof(uint32_t), "multi_list"));
     GSX_TRY(ctx->depth_sort_temp.reserve(radix_sort_keys_u64_compacting_temp_bytes(n), "depth_sort_temp"));
     GSX_TRY(ctx->ranges.reserve((size_t)tiles * sizeof(uint2), "ranges"));
     GSX_TRY(ctx->final_t.reserve((size_t)pixels * sizeof(float), "final_t"));
@@ -551,6 +561,7 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
                            ctx->rec.as<float4>(), train ? ctx->cov_coef.as<float4>() : nullptr,
                            ctx->tile_count.as<uint32_t>(), train ? visible_counter : nullptr,
                            ctx->big_list.as<uint32_t>(), big_count, counters + 1, counters + 2 + (ctx->big_slot ^ 1),
+                           counters + 4,
                            static_cast<uint32_t*>(ctx->kept_parts.dev), ctx->depth_keys.as<uint64_t>(), near_bits,
                            depth_max, index_bits, big_flag ? kBigKeyFlag : 0ull);
         GSX_HIP_TRY(hipGetLastError(), "preprocess_kernel");
@@ -578,7 +589,8 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
                            sorted_depth, (uint64_t)((1ull << index_bits) - 1ull), big_flag,
                            ctx->tile_count.as<uint32_t>(),
                            ctx->rank_g.as<uint32_t>(), ctx->rank_count.as<uint32_t>(), ctx->g_rank.as<uint32_t>(),
-                           ctx->long_list.as<uint32_t>(), counters + 1, ctx->scan_temp.as<uint32_t>());
+                           ctx->long_list.as<uint32_t>(), counters + 1, long_chunk_of(tiles),
+                           ctx->multi_list.as<uint32_t>(), counters + 4, ctx->scan_temp.as<uint32_t>());
         GSX_HIP_TRY(hipGetLastError(), "rank_gather_kernel");
         // exclusive scan of the 256-rank sums; emit_keys_kernel completes the offsets
         GSX_TRY(scan_partials_in_place(ctx->scan_temp.as<uint32_t>(), pre_blocks, stream));
@@ -695,10 +707,7 @@ gsx_hip_status gsx_hip_render_backward(gsx_hip_render_context* ctx, const float*
     const uint32_t* counters = ctx->counters.as<uint32_t>();  // as the forward left them
     // per-instance partials: [I][8] records, then the [I] opacity terms
     float* inst_grad_op = ctx->inst_grad.as<float>() + (size_t)ctx->instance_count * 8;
-    // long instance runs are summed in chunks of long_chunk positions: a run has at most `tiles`
-    // instances, so at most kLongChunks chunks
-    const uint32_t long_chunk = std::max<uint32_t>(
-        kWave, ((uint32_t)(tiles + (int)kLongChunks - 1) / kLongChunks + kWave - 1) / kWave * kWave);
+    const uint32_t long_chunk = long_chunk_of(tiles);
     GSX_TRY(record(ctx, 7, stream));
     const int tiles_padded = ((tiles + 7) / 8) * 8;
     hipLaunchKernelGGL(blend_backward_kernel, dim3((unsigned)tiles_padded), dim3(256), 0, stream,
@@ -710,7 +719,8 @@ gsx_hip_status gsx_hip_render_backward(gsx_hip_render_context* ctx, const float*
     if (n > 0) {
         hipLaunchKernelGGL(reduce_instance_grads_kernel, dim3(kLongRunBlocks * kLongChunks + blocks_for(n, 256)),
                            dim3(256), 0, stream, n, counters, ctx->offsets.as<uint32_t>(), ctx->rank_g.as<uint32_t>(),
-                           ctx->long_list.as<uint32_t>(), counters + 1, kLongRunBlocks, long_chunk,
+                           ctx->long_list.as<uint32_t>(), counters + 1, ctx->multi_list.as<uint32_t>(), counters + 4,
+                           kLongRunBlocks, long_chunk,
                            ctx->inst_grad.as<float>(), inst_grad_op, ctx->grad2d.as<float>());
         GSX_HIP_TRY(hipGetLastError(), "reduce_instance_grads_kernel");
     }

@@ -194,7 +194,8 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
     const float* __restrict__ sh1, const float* __restrict__ sh2, const float* __restrict__ sh3, int sh_degree,
     CameraParams cam, float4* __restrict__ rec, float4* __restrict__ cov_coef, uint32_t* __restrict__ tile_count,
     float* __restrict__ visible_counter, uint32_t* __restrict__ big_list, uint32_t* __restrict__ big_count,
-    uint32_t* __restrict__ clear0, uint32_t* __restrict__ clear1, uint32_t* __restrict__ kept_part,
+    uint32_t* __restrict__ clear0, uint32_t* __restrict__ clear1, uint32_t* __restrict__ clear2,
+    uint32_t* __restrict__ kept_part,
     uint64_t* __restrict__ depth_keys, uint32_t depth_base, uint32_t depth_max, int index_bits,
     uint64_t big_key_flag) {
     __shared__ WaveBoxes s_boxes[kWavesPerBlock];
@@ -205,6 +206,7 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         *clear0 = 0u;
         *clear1 = 0u;
+        *clear2 = 0u;
     }
     bool visible = false;
     float4 r0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), r1 = r0, r2 = r0;
@@ -279,9 +281,10 @@ constexpr uint32_t kLaneRun = 32;
 // After the depth sort of the V visible Gaussians (V = *depth_count): the Gaussian of every
 // depth rank, its kept-tile count, the rank of each big box and of each Gaussian whose count
 // exceeds kLaneRun (the only ranks looked up by Gaussian; every Gaussian's when flagged_only is
-// false), and the list of ranks whose count exceeds kLaneRun. Ranks V..n-1 get count 0 and no Gaussian. Each workgroup also stores the sum
-// of its 256 counts in block_sums[block], the first step of the offsets scan (emit_keys_kernel
-// finishes it).
+// false), the list of ranks whose count exceeds kLaneRun, and the list of those longer than one
+// long_chunk (the backward sums long runs in chunks of that many positions). Ranks V..n-1 get
+// count 0 and no Gaussian. Each workgroup also stores the sum of its 256 counts in
+// block_sums[block], the first step of the offsets scan (emit_block finishes it).
 __global__ __launch_bounds__(256) void rank_gather_kernel(int64_t n, const uint32_t* __restrict__ depth_count,
                                                           const uint64_t* __restrict__ sorted_depth_keys,
                                                           uint64_t index_mask, bool flagged_only,
@@ -290,7 +293,9 @@ __global__ __launch_bounds__(256) void rank_gather_kernel(int64_t n, const uint3
                                                           uint32_t* __restrict__ rank_count,
                                                           uint32_t* __restrict__ gaussian_rank,
                                                           uint32_t* __restrict__ long_list,
-                                                          uint32_t* __restrict__ long_count,
+                                                          uint32_t* __restrict__ long_count, uint32_t long_chunk,
+                                                          uint32_t* __restrict__ multi_list,
+                                                          uint32_t* __restrict__ multi_count,
                                                           uint32_t* __restrict__ block_sums) {
     __shared__ uint32_t s_sum[kWavesPerBlock];
     const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -303,6 +308,7 @@ __global__ __launch_bounds__(256) void rank_gather_kernel(int64_t n, const uint3
             rank_gaussian[r] = g;
             if (!flagged_only || (key & kBigKeyFlag) != 0 || c > kLaneRun) gaussian_rank[g] = (uint32_t)r;
             if (c > kLaneRun) long_list[atomicAdd(long_count, 1u)] = (uint32_t)r;
+            if (c > long_chunk) multi_list[atomicAdd(multi_count, 1u)] = (uint32_t)r;
         }
         rank_count[r] = c;
     }
@@ -1054,18 +1060,21 @@ __device__ inline void reduce_long_block(uint32_t x, uint32_t k, uint32_t gx, co
 }
 
 // Both reductions in one launch: workgroups [0, gx * kLongChunks) sum the long runs' chunks
-// (x = index % gx, chunk = index / gx), the rest the short runs (256 ranks each).
+// (x = index % gx, chunk k = index / gx): chunk 0 of every long run, chunks 1.. of the runs
+// longer than one chunk (their own, short list); the rest sum the short runs (256 ranks each).
 __global__ __launch_bounds__(256) void reduce_instance_grads_kernel(
     int64_t n, const uint32_t* __restrict__ depth_count, const uint32_t* __restrict__ offsets,
     const uint32_t* __restrict__ rank_gaussian, const uint32_t* __restrict__ long_list,
-    const uint32_t* __restrict__ long_count, uint32_t gx, uint32_t chunk, float* __restrict__ instance_grad,
+    const uint32_t* __restrict__ long_count, const uint32_t* __restrict__ multi_list,
+    const uint32_t* __restrict__ multi_count, uint32_t gx, uint32_t chunk, float* __restrict__ instance_grad,
     float* __restrict__ instance_grad_op, float* __restrict__ grad2d) {
     __shared__ float4 s_rec[kWavesPerBlock][2 * kShortPiece];
     __shared__ float s_op[kWavesPerBlock][kShortPiece];
     const uint32_t long_blocks = gx * kLongChunks;
     if (blockIdx.x < long_blocks) {
-        reduce_long_block(blockIdx.x % gx, blockIdx.x / gx, gx, long_list, long_count, offsets, rank_gaussian, chunk,
-                          instance_grad, instance_grad_op, grad2d);
+        const uint32_t k = blockIdx.x / gx;
+        reduce_long_block(blockIdx.x % gx, k, gx, k == 0 ? long_list : multi_list, k == 0 ? long_count : multi_count,
+                          offsets, rank_gaussian, chunk, instance_grad, instance_grad_op, grad2d);
         return;
     }
     reduce_short_block(blockIdx.x - long_blocks, n, depth_count, offsets, rank_gaussian, instance_grad,
