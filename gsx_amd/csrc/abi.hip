@@ -135,8 +135,9 @@ struct PinnedBuffer {
 
 // Workgroups of the big-box passes (grid-stride over the list of big boxes).
 constexpr unsigned kBigBlocks = 512;
-// Workgroups per chunk column of the long-run reduction (4 waves each, grid-stride over the list
-// of long runs).
+// Workgroups of the long-run reduction (4 waves each, grid-stride over the list of long runs):
+// for chunk 0, which every long run has, and per later chunk.
+constexpr unsigned kLongRunBlocks0 = 2048;
 constexpr unsigned kLongRunBlocks = 512;
 
 // Long instance runs are summed in chunks of this many positions: a run has at most `tiles`
@@ -717,10 +718,11 @@ gsx_hip_status gsx_hip_render_backward(gsx_hip_render_context* ctx, const float*
     GSX_HIP_TRY(hipGetLastError(), "blend_backward_kernel");
     GSX_TRY(record(ctx, 8, stream));
     if (n > 0) {
-        hipLaunchKernelGGL(reduce_instance_grads_kernel, dim3(kLongRunBlocks * kLongChunks + blocks_for(n, 256)),
+        hipLaunchKernelGGL(reduce_instance_grads_kernel,
+                           dim3(kLongRunBlocks0 + kLongRunBlocks * (kLongChunks - 1) + blocks_for(n, 256)),
                            dim3(256), 0, stream, n, counters, ctx->offsets.as<uint32_t>(), ctx->rank_g.as<uint32_t>(),
                            ctx->long_list.as<uint32_t>(), counters + 1, ctx->multi_list.as<uint32_t>(), counters + 4,
-                           kLongRunBlocks, long_chunk,
+                           kLongRunBlocks0, kLongRunBlocks, long_chunk,
                            ctx->inst_grad.as<float>(), inst_grad_op, ctx->grad2d.as<float>());
         GSX_HIP_TRY(hipGetLastError(), "reduce_instance_grads_kernel");
     }

@@ -1059,22 +1059,27 @@ __device__ inline void reduce_long_block(uint32_t x, uint32_t k, uint32_t gx, co
     }
 }
 
-// Both reductions in one launch: workgroups [0, gx * kLongChunks) sum the long runs' chunks
-// (x = index % gx, chunk k = index / gx): chunk 0 of every long run, chunks 1.. of the runs
-// longer than one chunk (their own, short list); the rest sum the short runs (256 ranks each).
+// Both reductions in one launch: workgroups [0, gx0) sum chunk 0 of every long run; the next
+// gx * (kLongChunks - 1) chunks 1.. of the runs longer than one chunk (their own, short list;
+// x = index % gx, chunk k = 1 + index / gx); the rest sum the short runs (256 ranks each).
 __global__ __launch_bounds__(256) void reduce_instance_grads_kernel(
     int64_t n, const uint32_t* __restrict__ depth_count, const uint32_t* __restrict__ offsets,
     const uint32_t* __restrict__ rank_gaussian, const uint32_t* __restrict__ long_list,
     const uint32_t* __restrict__ long_count, const uint32_t* __restrict__ multi_list,
-    const uint32_t* __restrict__ multi_count, uint32_t gx, uint32_t chunk, float* __restrict__ instance_grad,
-    float* __restrict__ instance_grad_op, float* __restrict__ grad2d) {
+    const uint32_t* __restrict__ multi_count, uint32_t gx0, uint32_t gx, uint32_t chunk,
+    float* __restrict__ instance_grad, float* __restrict__ instance_grad_op, float* __restrict__ grad2d) {
     __shared__ float4 s_rec[kWavesPerBlock][2 * kShortPiece];
     __shared__ float s_op[kWavesPerBlock][kShortPiece];
-    const uint32_t long_blocks = gx * kLongChunks;
+    if (blockIdx.x < gx0) {
+        reduce_long_block(blockIdx.x, 0, gx0, long_list, long_count, offsets, rank_gaussian, chunk, instance_grad,
+                          instance_grad_op, grad2d);
+        return;
+    }
+    const uint32_t long_blocks = gx0 + gx * (kLongChunks - 1);
     if (blockIdx.x < long_blocks) {
-        const uint32_t k = blockIdx.x / gx;
-        reduce_long_block(blockIdx.x % gx, k, gx, k == 0 ? long_list : multi_list, k == 0 ? long_count : multi_count,
-                          offsets, rank_gaussian, chunk, instance_grad, instance_grad_op, grad2d);
+        const uint32_t b = blockIdx.x - gx0;
+        reduce_long_block(b % gx, 1 + b / gx, gx, multi_list, multi_count, offsets, rank_gaussian, chunk,
+                          instance_grad, instance_grad_op, grad2d);
         return;
     }
     reduce_short_block(blockIdx.x - long_blocks, n, depth_count, offsets, rank_gaussian, instance_grad,
