@@ -567,11 +567,15 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
                            depth_max, index_bits, big_flag ? kBigKeyFlag : 0ull);
         GSX_HIP_TRY(hipGetLastError(), "preprocess_kernel");
         ctx->big_slot ^= 1;  // the slot this preprocess cleared
-        hipLaunchKernelGGL(big_tiles_count_kernel, dim3(kBigBlocks, big_chunks), dim3(256), 0, stream,
+        const uint32_t big_blocks = kBigBlocks * big_chunks;
+        const int64_t depth_chunks = (n + kCompactingChunk - 1) / kCompactingChunk;
+        hipLaunchKernelGGL(big_count_upsweep_kernel, dim3(big_blocks + (unsigned)depth_chunks), dim3(256), 0, stream,
                            ctx->big_list.as<uint32_t>(), big_count, ctx->rec.as<float4>(), cam.tiles_x, big_chunk,
-                           ctx->tile_count.as<uint32_t>(), ctx->big_chunk_counts.as<uint32_t>(),
-                           reinterpret_cast<unsigned long long*>(static_cast<char*>(ctx->kept_parts.dev) + big_parts_at));
-        GSX_HIP_TRY(hipGetLastError(), "big_tiles_count_kernel");
+                           kBigBlocks, big_blocks, ctx->tile_count.as<uint32_t>(), ctx->big_chunk_counts.as<uint32_t>(),
+                           reinterpret_cast<unsigned long long*>(static_cast<char*>(ctx->kept_parts.dev) + big_parts_at),
+                           ctx->depth_keys.as<uint64_t>(), n, index_bits, depth_chunks,
+                           static_cast<uint32_t*>(ctx->depth_sort_temp.ptr));
+        GSX_HIP_TRY(hipGetLastError(), "big_count_upsweep_kernel");
     }
     // the counting kernels leave the instance count as per-workgroup partials in host memory;
     // the depth order and the count scan are queued behind them, so the GPU keeps working while
@@ -584,7 +588,7 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
         int depth_in_alt = 0;
         GSX_TRY(radix_sort_keys_u64_compacting(ctx->depth_keys.as<uint64_t>(), ctx->depth_keys_alt.as<uint64_t>(), n,
                                                counters, index_bits, depth_end_bit, ctx->depth_sort_temp.ptr,
-                                               &depth_in_alt, stream));
+                                               &depth_in_alt, stream, true));
         if (depth_in_alt) sorted_depth = ctx->depth_keys_alt.as<uint64_t>();
         hipLaunchKernelGGL(rank_gather_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, n, counters,
                            sorted_depth, (uint64_t)((1ull << index_bits) - 1ull), big_flag,

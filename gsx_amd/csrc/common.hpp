@@ -476,6 +476,48 @@ __device__ inline uint32_t block_exclusive_scan_256(uint32_t v, uint32_t* s_wave
     return wave_base + incl - v;
 }
 
+// ---- radix sort building blocks shared with render.hip (sort.hip holds the passes) ----------
+constexpr int kSortThreads = 256;
+constexpr int kChunkWaves = kSortThreads / kWave;  // 4 (upsweep)
+// The depth order sorts about a million keys: 1024-key chunks give ~1000 workgroups per launch
+// (with 4096 a launch has fewer workgroups than the GPU has CUs, one wave per SIMD)
+constexpr int kCompactingChunk = 1024;
+constexpr uint64_t kSentinelKey = ~0ull;  // dropped by a pass with drop_sentinel set
+
+template <int kBits>
+__device__ inline uint32_t digit_of(uint64_t key, int shift) {
+    return (uint32_t)(key >> shift) & ((1u << kBits) - 1u);
+}
+
+// Upsweep of one kChunk-key chunk (workgroup `blk` of kSortThreads threads): its digit counts,
+// counted in wave-private LDS counters, to hist[digit][blk]. n_dev (may be null): live key
+// count, n = min(n, *n_dev); drop_sentinel: keys equal to kSentinelKey are not counted.
+template <int kBits, int kChunk>
+__device__ inline void radix_upsweep_block(uint32_t blk, const uint64_t* __restrict__ keys, int64_t n,
+                                           const uint32_t* __restrict__ n_dev, bool drop_sentinel, int shift,
+                                           int64_t num_chunks, uint32_t* __restrict__ hist,
+                                           uint32_t (*s_hist)[1 << kBits]) {
+    constexpr int kBins = 1 << kBits;
+    if (n_dev != nullptr) n = min(n, (int64_t)*n_dev);
+    const int wave = threadIdx.x / kWave;
+    for (int i = threadIdx.x; i < kChunkWaves * kBins; i += kSortThreads) (&s_hist[0][0])[i] = 0;
+    __syncthreads();
+    const int64_t base = (int64_t)blk * kChunk;
+#pragma unroll 4
+    for (int r = 0; r < kChunk / kSortThreads; ++r) {
+        const int64_t i = base + (int64_t)r * kSortThreads + threadIdx.x;
+        if (i < n) {
+            const uint64_t k = keys[i];
+            if (!drop_sentinel || k != kSentinelKey) atomicAdd(&s_hist[wave][digit_of<kBits>(k, shift)], 1u);
+        }
+    }
+    __syncthreads();
+    for (int d = threadIdx.x; d < kBins; d += kSortThreads) {
+        const uint32_t c = s_hist[0][d] + s_hist[1][d] + s_hist[2][d] + s_hist[3][d];
+        hist[(int64_t)d * num_chunks + blk] = c;
+    }
+}
+
 // Keys-only stable radix sort (sort.hip) that also drops every key equal to ~0: the first pass
 // reads all n keys and moves the others, in input order within each digit, to the front, and
 // stores their number in *n_live (overwritten; no initial value needed); the later passes sort that
@@ -484,9 +526,12 @@ __device__ inline uint32_t block_exclusive_scan_256(uint32_t v, uint32_t* s_wave
 // Its digits are kCompactingRadixBits wide (passes = ceil((end_bit - begin_bit) / 9)), and temp
 // holds radix_sort_keys_u64_compacting_temp_bytes(n) bytes.
 constexpr int kCompactingRadixBits = 9;
+// first_hist_ready: the first pass's digit counts are already in temp (radix_upsweep_block run
+// by the caller over every chunk: hist at the start of temp, [digit][chunk], ceil(n / 1024)
+// chunks), so that pass starts at its row scan.
 gsx_hip_status radix_sort_keys_u64_compacting(uint64_t* keys, uint64_t* keys_alt, int64_t n, uint32_t* n_live,
                                               int begin_bit, int end_bit, void* temp, int* out_in_alt,
-                                              hipStream_t stream);
+                                              hipStream_t stream, bool first_hist_ready);
 size_t radix_sort_keys_u64_compacting_temp_bytes(int64_t n);
 
 // Keys-only stable radix sort (the public sort's kernels) on bits [begin_bit, begin_bit + passes *

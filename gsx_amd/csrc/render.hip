@@ -452,17 +452,30 @@ __device__ inline void big_tiles_block(uint32_t x, uint32_t c, uint32_t gx, cons
     if (!kEmit && threadIdx.x == 0) kept_part[(size_t)c * gx + x] = block_kept;
 }
 
-// Kept-tile counts of the big boxes: grid (gx, chunks).
-__global__ __launch_bounds__(256) void big_tiles_count_kernel(const uint32_t* __restrict__ big_list,
-                                                              const uint32_t* __restrict__ big_count,
-                                                              const float4* __restrict__ rec, int32_t tiles_x,
-                                                              uint32_t chunk, uint32_t* __restrict__ tile_count,
-                                                              uint32_t* __restrict__ chunk_counts,
-                                                              unsigned long long* __restrict__ kept_part) {
+// Two independent jobs after preprocess in one launch: workgroups [0, big_blocks) count the big
+// boxes' kept tiles (x = index % gx, chunk = index / gx), the rest take the depth sort's first
+// upsweep (digit counts of the depth keys' first digit, the invisible keys left out), which
+// then runs beside the longer big-box walks instead of after them.
+__global__ __launch_bounds__(256) void big_count_upsweep_kernel(const uint32_t* __restrict__ big_list,
+                                                                const uint32_t* __restrict__ big_count,
+                                                                const float4* __restrict__ rec, int32_t tiles_x,
+                                                                uint32_t chunk, uint32_t gx, uint32_t big_blocks,
+                                                                uint32_t* __restrict__ tile_count,
+                                                                uint32_t* __restrict__ chunk_counts,
+                                                                unsigned long long* __restrict__ kept_part,
+                                                                const uint64_t* __restrict__ depth_keys, int64_t n,
+                                                                int shift, int64_t depth_chunks,
+                                                                uint32_t* __restrict__ depth_hist) {
     __shared__ uint32_t s_wave[kWavesPerBlock];
-    big_tiles_block<false>(blockIdx.x, blockIdx.y, gridDim.x, big_list, big_count, rec, tiles_x, KeyLayout{}, chunk,
-                           tile_count, chunk_counts, kept_part, nullptr, nullptr, nullptr, nullptr, nullptr, s_wave,
-                           nullptr);
+    __shared__ uint32_t s_hist[kChunkWaves][1 << kCompactingRadixBits];
+    if (blockIdx.x < big_blocks) {
+        big_tiles_block<false>(blockIdx.x % gx, blockIdx.x / gx, gx, big_list, big_count, rec, tiles_x, KeyLayout{},
+                               chunk, tile_count, chunk_counts, kept_part, nullptr, nullptr, nullptr, nullptr, nullptr,
+                               s_wave, nullptr);
+        return;
+    }
+    radix_upsweep_block<kCompactingRadixBits, kCompactingChunk>(blockIdx.x - big_blocks, depth_keys, n, nullptr, true,
+                                                                shift, depth_chunks, depth_hist, s_hist);
 }
 
 // All emission in one launch: workgroups [0, big_blocks) are the big-box workgroups

@@ -17,12 +17,8 @@ constexpr int kScanThreads = 256;
 constexpr int kScanItems = 4;
 constexpr int kScanChunk = kScanThreads * kScanItems;  // 1024 elements per block
 
-constexpr int kSortThreads = 256;
 constexpr int kSortChunk = 4096;  // keys per chunk (one upsweep / downsweep workgroup), public sorts
 constexpr int kRadixBits = 8;     // digit width of the public sorts
-// The depth order sorts about a million keys: 1024-key chunks give ~1000 workgroups per launch
-// (with 4096 a launch has fewer workgroups than the GPU has CUs, one wave per SIMD)
-constexpr int kCompactingChunk = 1024;
 // Chunk of the tile sort's passes (radix_sort_keys_u64_digits)
 constexpr int kDigitsChunk = 4096;
 constexpr int kRowItems = 16;  // row scan: 16 chunk counts per thread and step
@@ -108,15 +104,6 @@ __global__ __launch_bounds__(kScanThreads) void scan_downsweep_kernel(const uint
 // rounds and lanes follow input order), and chunks are laid out in order inside each digit.
 // No workgroup waits on another, so every wave runs to completion.
 // ---------------------------------------------------------------------------------------------
-constexpr int kChunkWaves = kSortThreads / kWave;  // 4 (upsweep)
-
-template <int kBits>
-__device__ inline uint32_t digit_of(uint64_t key, int shift) {
-    return (uint32_t)(key >> shift) & ((1u << kBits) - 1u);
-}
-
-constexpr uint64_t kSentinelKey = ~0ull;  // dropped by a pass with drop_sentinel set
-
 // n_dev (may be null): live key count, n = min(n, *n_dev); chunks past it count nothing.
 // drop_sentinel: keys equal to kSentinelKey are left out (they vanish from the output).
 template <int kBits, int kChunk>
@@ -125,26 +112,8 @@ __global__ __launch_bounds__(kSortThreads) void radix_upsweep_kernel(const uint6
                                                                      bool drop_sentinel, int shift,
                                                                      int64_t num_chunks,
                                                                      uint32_t* __restrict__ hist) {
-    constexpr int kBins = 1 << kBits;
-    __shared__ uint32_t s_hist[kChunkWaves][kBins];
-    if (n_dev != nullptr) n = min(n, (int64_t)*n_dev);
-    const int wave = threadIdx.x / kWave;
-    for (int i = threadIdx.x; i < kChunkWaves * kBins; i += kSortThreads) (&s_hist[0][0])[i] = 0;
-    __syncthreads();
-    const int64_t base = (int64_t)blockIdx.x * kChunk;
-#pragma unroll 4
-    for (int r = 0; r < kChunk / kSortThreads; ++r) {
-        const int64_t i = base + (int64_t)r * kSortThreads + threadIdx.x;
-        if (i < n) {
-            const uint64_t k = keys[i];
-            if (!drop_sentinel || k != kSentinelKey) atomicAdd(&s_hist[wave][digit_of<kBits>(k, shift)], 1u);
-        }
-    }
-    __syncthreads();
-    for (int d = threadIdx.x; d < kBins; d += kSortThreads) {
-        const uint32_t c = s_hist[0][d] + s_hist[1][d] + s_hist[2][d] + s_hist[3][d];
-        hist[(int64_t)d * num_chunks + blockIdx.x] = c;
-    }
+    __shared__ uint32_t s_hist[kChunkWaves][1 << kBits];
+    radix_upsweep_block<kBits, kChunk>(blockIdx.x, keys, n, n_dev, drop_sentinel, shift, num_chunks, hist, s_hist);
 }
 
 // Workgroup d: exclusive scan of hist[d][0..num_chunks) into offsets[d][..], row total into
@@ -339,7 +308,7 @@ size_t radix_temp_bytes(int64_t n) {
 template <bool kPairs, int kBits, int kChunk>
 gsx_hip_status radix_sort_u64(uint64_t* keys, uint32_t* vals, uint64_t* keys_alt, uint32_t* vals_alt, int64_t n,
                               uint32_t* n_dev, bool compact_first, int begin_bit, int end_bit, void* temp,
-                              int* out_in_alt, hipStream_t stream) {
+                              int* out_in_alt, hipStream_t stream, bool first_hist_ready = false) {
     constexpr int kBins = 1 << kBits;
     if (begin_bit < 0 || end_bit > 64 || begin_bit > end_bit) return GSX_HIP_ERROR_INVALID_ARGUMENT;
     if (n > (int64_t)UINT32_MAX) return GSX_HIP_ERROR_OUT_OF_RANGE;
@@ -358,6 +327,7 @@ gsx_hip_status radix_sort_u64(uint64_t* keys, uint32_t* vals, uint64_t* keys_alt
             uint32_t* vout = in_alt ? vals : vals_alt;
             const bool drop = compact_first && shift == begin_bit;
             const uint32_t* live = drop ? nullptr : n_dev;
+            if (!(first_hist_ready && shift == begin_bit))
             hipLaunchKernelGGL((radix_upsweep_kernel<kBits, kChunk>), dim3((unsigned)chunks), dim3(kSortThreads), 0, stream, kin,
                                n, live, drop, shift, chunks, hist);
             hipLaunchKernelGGL(radix_rowscan_kernel, dim3(kBins), dim3(kSortThreads), 0, stream, hist, chunks,
@@ -424,11 +394,11 @@ gsx_hip_status scan_partials_in_place(uint32_t* partials, int64_t count, hipStre
 
 gsx_hip_status radix_sort_keys_u64_compacting(uint64_t* keys, uint64_t* keys_alt, int64_t n, uint32_t* n_live,
                                               int begin_bit, int end_bit, void* temp, int* out_in_alt,
-                                              hipStream_t stream) {
+                                              hipStream_t stream, bool first_hist_ready) {
     if (begin_bit >= end_bit) return GSX_HIP_ERROR_INVALID_ARGUMENT;  // the compacting pass must run
     return radix_sort_u64<false, kCompactingRadixBits, kCompactingChunk>(keys, nullptr, keys_alt, nullptr, n, n_live,
                                                                          true, begin_bit, end_bit, temp, out_in_alt,
-                                                                         stream);
+                                                                         stream, first_hist_ready);
 }
 
 gsx_hip_status radix_sort_keys_u64_digits(uint64_t* keys, uint64_t* keys_alt, int64_t n, int begin_bit, int passes,
