@@ -1005,10 +1005,26 @@ __device__ inline void reduce_short_block(uint32_t blk, int64_t n, const uint32_
         if (p0 == UINT32_MAX) break;  // uniform
         const uint32_t p1 = min(p0 + kShortPiece, span_end);
         wave_lds_sync();  // the previous piece has been read
-        for (uint32_t q = lane; q < p1 - p0; q += kWave) {
-            sr[2 * q] = rec4[2 * (size_t)(p0 + q)];
-            sr[2 * q + 1] = rec4[2 * (size_t)(p0 + q) + 1];
-            so[q] = instance_grad_op[p0 + q];
+        // every load of the piece is issued before the first store waits on one: the loads are
+        // not under a branch (lanes past the piece re-read its last position, p1 > p0)
+        constexpr int kPieceRounds = (int)(kShortPiece / kWave);
+        const uint32_t len = p1 - p0;
+        float4 ra[kPieceRounds], rb[kPieceRounds];
+        float ro[kPieceRounds];
+#pragma unroll
+        for (int u = 0; u < kPieceRounds; ++u) {
+            const uint32_t q = min(lane + (uint32_t)u * kWave, len - 1);
+            ra[u] = rec4[2 * (size_t)(p0 + q)];
+            rb[u] = rec4[2 * (size_t)(p0 + q) + 1];
+            ro[u] = instance_grad_op[p0 + q];
+        }
+        // (unconditional stores: lanes past the piece write its last position's own values again)
+#pragma unroll
+        for (int u = 0; u < kPieceRounds; ++u) {
+            const uint32_t q = min(lane + (uint32_t)u * kWave, len - 1);
+            sr[2 * q] = ra[u];
+            sr[2 * q + 1] = rb[u];
+            so[q] = ro[u];
         }
         wave_lds_sync();
         if (has) {
@@ -1045,11 +1061,26 @@ __device__ inline void reduce_long_block(uint32_t x, uint32_t k, uint32_t gx, co
         float acc[kGrad2d];
 #pragma unroll
         for (int c = 0; c < kGrad2d; ++c) acc[c] = 0.0f;
+        const float4* rec4 = reinterpret_cast<const float4*>(instance_grad);
         for (uint32_t p0 = cb; p0 < ce; p0 += 4 * kWave) {
+            // all loads of the round are in flight together: none sits under a branch (lanes
+            // past the chunk re-read its last position and add nothing)
+            float4 ra[4], rb[4];
+            float ro[4];
 #pragma unroll
             for (uint32_t u = 0; u < 4; ++u) {
-                const uint32_t p = p0 + u * kWave + lane;
-                if (p < ce) add_instance_grad(acc, instance_grad, instance_grad_op, p);
+                const uint32_t p = min(p0 + u * kWave + lane, ce - 1);
+                ra[u] = rec4[2 * (size_t)p];
+                rb[u] = rec4[2 * (size_t)p + 1];
+                ro[u] = instance_grad_op[p];
+            }
+            // lanes past the chunk add -0, the identity of + (an unconditional use keeps the loads
+            // ahead of the adds)
+#pragma unroll
+            for (uint32_t u = 0; u < 4; ++u) {
+                const bool in = p0 + u * kWave + lane < ce;
+                const float4 z = make_float4(-0.0f, -0.0f, -0.0f, -0.0f);
+                add_record(acc, in ? ra[u] : z, in ? rb[u] : z, in ? ro[u] : -0.0f);
             }
         }
 #pragma unroll
