@@ -785,6 +785,16 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
     const uint32_t first_batch = range.x + ((end_all - 1u - range.x) / kBackBatch) * kBackBatch;
     for (int64_t bstart = first_batch; bstart >= (int64_t)range.x; bstart -= kBackBatch) {
         const int count = (int)min((uint32_t)kBackBatch, range.y - (uint32_t)bstart);
+        // the batch's checkpoints load together, ahead of the records (not under branches: a
+        // pixel that needs no checkpoint of a bucket reads the batch's first slot, which exists,
+        // and keeps 0)
+        float ck[kBatchBuckets];
+#pragma unroll
+        for (int b = 0; b < kBatchBuckets; ++b) {
+            const uint32_t j0 = (uint32_t)bstart + (uint32_t)(b * kBucket);
+            const uint32_t js = (inside && j0 < last) ? j0 : (uint32_t)bstart;
+            ck[b] = ckpt[checkpoint_slot(range.x, tile, js) * kBlendThreads + threadIdx.x];
+        }
         if (threadIdx.x < count) {
             const uint32_t j = (uint32_t)bstart + threadIdx.x;
             s_pos[threadIdx.x] = values[j];
@@ -810,9 +820,7 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
 #pragma unroll
         for (int b = 0; b < kBatchBuckets; ++b) {
             const uint32_t j0 = (uint32_t)bstart + (uint32_t)(b * kBucket);
-            s_ck[b][threadIdx.x] = (inside && j0 < last)
-                                       ? ckpt[checkpoint_slot(range.x, tile, j0) * kBlendThreads + threadIdx.x]
-                                       : 0.0f;
+            s_ck[b][threadIdx.x] = (inside && j0 < last) ? ck[b] : 0.0f;
         }
         __syncthreads();
         const int sb_first = (count - 1) / kBucket;
