@@ -503,12 +503,18 @@ __device__ inline void radix_upsweep_block(uint32_t blk, const uint64_t* __restr
     for (int i = threadIdx.x; i < kChunkWaves * kBins; i += kSortThreads) (&s_hist[0][0])[i] = 0;
     __syncthreads();
     const int64_t base = (int64_t)blk * kChunk;
-#pragma unroll 4
-    for (int r = 0; r < kChunk / kSortThreads; ++r) {
-        const int64_t i = base + (int64_t)r * kSortThreads + threadIdx.x;
-        if (i < n) {
-            const uint64_t k = keys[i];
-            if (!drop_sentinel || k != kSentinelKey) atomicAdd(&s_hist[wave][digit_of<kBits>(k, shift)], 1u);
+    if (base < n) {  // uniform; a chunk past the live count counts nothing
+        // every key of the chunk is loaded before the first count waits on one (no load sits
+        // under a branch: lanes past n re-read key n - 1 and count nothing)
+        constexpr int kRounds = kChunk / kSortThreads;
+        uint64_t k[kRounds];
+#pragma unroll
+        for (int r = 0; r < kRounds; ++r) k[r] = keys[min(base + (int64_t)r * kSortThreads + threadIdx.x, n - 1)];
+#pragma unroll
+        for (int r = 0; r < kRounds; ++r) {
+            const int64_t i = base + (int64_t)r * kSortThreads + threadIdx.x;
+            if (i < n && (!drop_sentinel || k[r] != kSentinelKey))
+                atomicAdd(&s_hist[wave][digit_of<kBits>(k[r], shift)], 1u);
         }
     }
     __syncthreads();

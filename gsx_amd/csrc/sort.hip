@@ -203,6 +203,11 @@ __global__ __launch_bounds__(kDownThreads) void radix_downsweep_kernel(
     if (n_dev != nullptr) n = min(n, (int64_t)*n_dev);
     if (base >= n) return;  // uniform: a chunk past the live count has nothing to move
     const int chunk_count = (int)min((int64_t)kChunk, n - base);
+    // this chunk's digit offsets and the digit totals, loaded with the keys (threads past kBins
+    // re-read digit kBins - 1 and ignore it)
+    const int td = min((int)threadIdx.x, kBins - 1);
+    const uint32_t my_total = totals[td];
+    const uint32_t my_offset = offsets[(int64_t)td * num_chunks + blockIdx.x];
     for (int i = threadIdx.x; i < kDownWaves * kBins; i += kDownThreads) (&s_cnt[0][0])[i] = 0;
     __syncthreads();
     // 1. per wave: stable ranks among equal digits (rank = keys of the digit before it in this
@@ -250,13 +255,13 @@ __global__ __launch_bounds__(kDownThreads) void radix_downsweep_kernel(
         }
         uint32_t kept, all_kept;
         const uint32_t start = digit_exclusive_scan<kBins>(cnt, s_wave, kept);
-        const uint32_t digit_base = digit_exclusive_scan<kBins>(t < kBins ? totals[t] : 0u, s_wave, all_kept);
+        const uint32_t digit_base = digit_exclusive_scan<kBins>(t < kBins ? my_total : 0u, s_wave, all_kept);
         if (t == 0) s_kept = kept;
         // the number of keys this pass keeps, for the later passes (a plain store: one writer)
         if (kept_total != nullptr && blockIdx.x == 0 && t == 0) *kept_total = all_kept;
         if (t < kBins) {
             s_local[t] = start;
-            s_global[t] = digit_base + offsets[(int64_t)t * num_chunks + blockIdx.x];
+            s_global[t] = digit_base + my_offset;
             uint32_t run = start;
 #pragma unroll
             for (int w = 0; w < kDownWaves; ++w) {
