@@ -72,6 +72,8 @@ __device__ inline int ssim_tile_of(int block, int tiles) {
     return (block & 7) * per + (block >> 3);
 }
 constexpr int kSsimHW = kSsimTW + 10, kSsimHH = kSsimTH + 10;  // 42 x 26 halo
+constexpr int kHaloItems = kSsimHH * kSsimHW;
+constexpr int kHaloRounds = (kHaloItems + 255) / 256;  // per thread of a 256-thread workgroup
 // Output columns per work item of the horizontal passes: 26 rows x 8 items fill the workgroup
 // once, and each loaded input pixel (and its moments) serves 4 outputs.
 constexpr int kHCols = 4;
@@ -95,16 +97,39 @@ __global__ __launch_bounds__(256) void ssim_forward_kernel(float* __restrict__ m
     const int oy = (tile / tiles_x) * kSsimTH;
     const int64_t plane = blockIdx.y;
     const int64_t pbase = plane * (int64_t)height * width;
-    for (int i = threadIdx.x; i < kSsimHH * kSsimHW; i += 256) {
-        const int hy = i / kSsimHW, hx = i % kSsimHW;
-        const int y = oy + hy - 5, x = ox + hx - 5;
-        float pv = 0.0f, tv = 0.0f;
-        if (y >= 0 && y < height && x >= 0 && x < width) {
-            pv = pred[pbase + (int64_t)y * width + x];
-            tv = target[pbase + (int64_t)y * width + x];
+    const int lx = threadIdx.x % kSsimTW;
+    const int ly0 = 2 * (threadIdx.x / kSsimTW);
+    // the loss map values this thread adds to, loaded up front with the halo (clamped positions
+    // outside the image are never stored; without a map the prediction stands in)
+    float map_in[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const int64_t j = pbase + (int64_t)min(oy + ly0 + r, height - 1) * width + min(ox + lx, width - 1);
+        map_in[r] = (map != nullptr ? map : pred)[j];
+    }
+    {
+        // the whole halo is loaded before the first store waits (no load under a branch: a
+        // position outside the image reads a clamped one and keeps 0; threads past the halo
+        // repeat its last item, same value to the same slot)
+        float pv[kHaloRounds], tv[kHaloRounds];
+#pragma unroll
+        for (int u = 0; u < kHaloRounds; ++u) {
+            const int i = min((int)threadIdx.x + 256 * u, kHaloItems - 1);
+            const int hy = i / kSsimHW, hx = i % kSsimHW;
+            const int y = oy + hy - 5, x = ox + hx - 5;
+            const bool in = y >= 0 && y < height && x >= 0 && x < width;
+            const int64_t j = pbase + (int64_t)min(max(y, 0), height - 1) * width + min(max(x, 0), width - 1);
+            const float p = pred[j], t = target[j];
+            pv[u] = in ? p : 0.0f;
+            tv[u] = in ? t : 0.0f;
         }
-        s_in[0][hy][hx] = pv;
-        s_in[1][hy][hx] = tv;
+#pragma unroll
+        for (int u = 0; u < kHaloRounds; ++u) {
+            const int i = min((int)threadIdx.x + 256 * u, kHaloItems - 1);
+            const int hy = i / kSsimHW, hx = i % kSsimHW;
+            s_in[0][hy][hx] = pv[u];
+            s_in[1][hy][hx] = tv[u];
+        }
     }
     __syncthreads();
     for (int i = threadIdx.x; i < kSsimHH * (kSsimTW / kHCols); i += 256) {
@@ -133,8 +158,6 @@ __global__ __launch_bounds__(256) void ssim_forward_kernel(float* __restrict__ m
             for (int c = 0; c < 5; ++c) s_h[c][hy][cx + j] = a[j][c];
     }
     __syncthreads();
-    const int lx = threadIdx.x % kSsimTW;
-    const int ly0 = 2 * (threadIdx.x / kSsimTW);
     float mom[2][5] = {{0.0f, 0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f, 0.0f}};
 #pragma unroll
     for (int k = 0; k < 12; ++k) {
@@ -167,7 +190,7 @@ __global__ __launch_bounds__(256) void ssim_forward_kernel(float* __restrict__ m
         const bool boundary = y < 5 || y >= height - 5 || x < 5 || x >= width - 5;
         const int64_t idx = pbase + (int64_t)y * width + x;
         if (map != nullptr) {
-            float m = map[idx];
+            float m = map_in[r];
             // exactly the L1 kernel's operations (loss.c:354-371)
             if (fuse_l1) m += l1_scale * fabsf(s_in[0][ly + 5][lx + 5] - s_in[1][ly + 5][lx + 5]);
             map[idx] = boundary ? 0.0f : m + (1.0f - ssim) * scale;
@@ -204,19 +227,41 @@ __global__ __launch_bounds__(256) void ssim_backward_kernel(float* __restrict__ 
     const int64_t plane = blockIdx.y;
     const int64_t total = planes * (int64_t)height * width;
     const int64_t pbase = plane * (int64_t)height * width;
-    for (int i = threadIdx.x; i < kSsimHH * kSsimHW; i += 256) {
-        const int hy = i / kSsimHW, hx = i % kSsimHW;
-        const int y = oy + hy - 5, x = ox + hx - 5;
-        float v0 = 0.0f, v1 = 0.0f, v2 = 0.0f;
-        if (y >= 0 && y < height && x >= 0 && x < width) {
-            const int64_t j = pbase + (int64_t)y * width + x;
-            v0 = dm[j];
-            v1 = dm[total + j];
-            v2 = dm[2 * total + j];
+    const int lx = threadIdx.x % kSsimTW;
+    const int ly0 = 2 * (threadIdx.x / kSsimTW);
+    // this thread's two output pixels (prediction, target, gradient so far), loaded up front with
+    // the halo (clamped positions outside the image are never stored)
+    float pv_in[2], tv_in[2], g_in[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const int64_t j = pbase + (int64_t)min(oy + ly0 + r, height - 1) * width + min(ox + lx, width - 1);
+        pv_in[r] = pred[j];
+        tv_in[r] = target[j];
+        g_in[r] = grad[j];
+    }
+    {
+        // the whole halo is loaded before the first store waits (as in ssim_forward_kernel)
+        float v0[kHaloRounds], v1[kHaloRounds], v2[kHaloRounds];
+#pragma unroll
+        for (int u = 0; u < kHaloRounds; ++u) {
+            const int i = min((int)threadIdx.x + 256 * u, kHaloItems - 1);
+            const int hy = i / kSsimHW, hx = i % kSsimHW;
+            const int y = oy + hy - 5, x = ox + hx - 5;
+            const bool in = y >= 0 && y < height && x >= 0 && x < width;
+            const int64_t j = pbase + (int64_t)min(max(y, 0), height - 1) * width + min(max(x, 0), width - 1);
+            const float a = dm[j], b = dm[total + j], c = dm[2 * total + j];
+            v0[u] = in ? a : 0.0f;
+            v1[u] = in ? b : 0.0f;
+            v2[u] = in ? c : 0.0f;
         }
-        s_m[0][hy][hx] = v0;
-        s_m[1][hy][hx] = v1;
-        s_m[2][hy][hx] = v2;
+#pragma unroll
+        for (int u = 0; u < kHaloRounds; ++u) {
+            const int i = min((int)threadIdx.x + 256 * u, kHaloItems - 1);
+            const int hy = i / kSsimHW, hx = i % kSsimHW;
+            s_m[0][hy][hx] = v0[u];
+            s_m[1][hy][hx] = v1[u];
+            s_m[2][hy][hx] = v2[u];
+        }
     }
     __syncthreads();
     for (int i = threadIdx.x; i < kSsimHH * (kSsimTW / kHCols); i += 256) {
@@ -243,8 +288,6 @@ __global__ __launch_bounds__(256) void ssim_backward_kernel(float* __restrict__ 
             for (int c = 0; c < 3; ++c) s_h[c][hy][cx + j] = a[j][c];
     }
     __syncthreads();
-    const int lx = threadIdx.x % kSsimTW;
-    const int ly0 = 2 * (threadIdx.x / kSsimTW);
     float cv[2][3] = {{0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f}};
 #pragma unroll
     for (int k = 0; k < 12; ++k) {
@@ -260,8 +303,8 @@ __global__ __launch_bounds__(256) void ssim_backward_kernel(float* __restrict__ 
         const int x = ox + lx, y = oy + ly0 + r;
         if (x >= width || y >= height) continue;
         const int64_t idx = pbase + (int64_t)y * width + x;
-        const float pv = pred[idx], tv = target[idx];
-        float g = grad[idx];
+        const float pv = pv_in[r], tv = tv_in[r];
+        float g = g_in[r];
         if (fuse_l1) {  // exactly the L1 kernel's operations
             const float d = pv - tv;
             const float s = d > 0.0f ? 1.0f : (d < 0.0f ? -1.0f : 0.0f);
