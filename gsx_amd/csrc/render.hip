@@ -341,23 +341,23 @@ __device__ inline void emit_block(uint32_t b, int64_t n, const float4* __restric
                                   uint32_t* __restrict__ instance_gaussian, WaveBoxes* s_boxes, uint32_t* s_wave) {
     WaveBoxes& wb = s_boxes[threadIdx.x / kWave];
     const int64_t r = (int64_t)b * blockDim.x + threadIdx.x;
-    const uint32_t cnt = r < n ? rank_count[r] : 0u;
+    // the rank's count and Gaussian load together, then its whole record (one wait each)
+    uint32_t cnt = 0, g = 0;
+    if (r < n) {
+        cnt = rank_count[r];
+        g = rank_gaussian[r];
+    }
     uint32_t block_total;
     const uint32_t o = block_prefix[b] + block_exclusive_scan_256(cnt, s_wave, block_total);
     if (r < n) offsets[r] = o;
     if (r == n - 1) offsets[n] = o + cnt;
-    bool any = cnt > 0;
-    uint32_t g = 0;
     float4 r0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), r1 = r0, r2 = r0;
-    if (any) {
-        g = rank_gaussian[r];
-        r2 = rec[3 * (size_t)g + 2];
-        any = box_tiles(r2) <= kBigTiles;  // big boxes are emitted by big_tiles_block
-    }
-    if (any) {
+    if (cnt > 0) {
         r0 = rec[3 * (size_t)g + 0];
         r1 = rec[3 * (size_t)g + 1];
+        r2 = rec[3 * (size_t)g + 2];
     }
+    const bool any = cnt > 0 && box_tiles(r2) <= kBigTiles;  // big boxes are emitted by big_tiles_block
     const uint32_t total = stage_box(wb, any, r0, r1, r2, g, o);
     walk_wave_tiles<true>(wb, total, tiles_x, layout, keys, instance_gaussian);
 }
@@ -528,6 +528,9 @@ __global__ __launch_bounds__(256) void tile_ranges_kernel(const uint64_t* __rest
     const uint32_t i0 = 4u * (blockIdx.x * blockDim.x + threadIdx.x);
     if (i0 >= count) return;
     const uint32_t m = min(4u, count - i0);
+    // the neighbours' keys load with the thread's own (clamped in-range positions, not branches)
+    const uint64_t k_prev = keys[i0 == 0 ? 0u : i0 - 1u];
+    const uint64_t k_next = keys[min(i0 + m, count - 1u)];
     uint64_t k[4];
     if (m == 4) {
         const ulonglong2* p = reinterpret_cast<const ulonglong2*>(keys + i0);
@@ -543,8 +546,8 @@ __global__ __launch_bounds__(256) void tile_ranges_kernel(const uint64_t* __rest
     uint32_t t[4];
 #pragma unroll
     for (uint32_t j = 0; j < 4; ++j) t[j] = key_tile(layout, k[j]);
-    const uint32_t prev = i0 == 0 ? UINT32_MAX : key_tile(layout, keys[i0 - 1]);
-    const uint32_t next = i0 + m == count ? tiles : key_tile(layout, keys[i0 + m]);
+    const uint32_t prev = i0 == 0 ? UINT32_MAX : key_tile(layout, k_prev);
+    const uint32_t next = i0 + m == count ? tiles : key_tile(layout, k_next);
     if (i0 == 0) {
         for (uint32_t u = 0; u < t[0]; ++u) ranges[u] = make_uint2(0u, 0u);
     }
