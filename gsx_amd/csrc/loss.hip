@@ -59,10 +59,14 @@ __global__ __launch_bounds__(256) void mse_backward_kernel(float* __restrict__ g
     }
 }
 
-// One 32x16 output tile of one image plane per workgroup (256 threads). The window sums use
-// explicit fused multiply-adds: the SSIM bar is a tolerance (the CPU sums in float64), unlike
-// the L1 term fused into the same pass, which keeps the L1 kernel's exact operations.
-constexpr int kSsimTW = 32, kSsimTH = 16;
+// One 32-column output tile of one image plane per workgroup, two output rows per thread: 16
+// rows (256 threads) for the forward, 32 rows (512 threads) for the backward, whose three-map
+// passes leave room for the taller halo (42 halo rows per 32 output rows instead of 26 per 16).
+// The window sums use explicit fused multiply-adds: the SSIM bar is a tolerance (the CPU sums in
+// float64), unlike the L1 term fused into the same pass, which keeps the L1 kernel's exact
+// operations.
+constexpr int kSsimTW = 32;
+constexpr int kSsimFwdTH = 16, kSsimBwdTH = 32;
 
 // Workgroup -> tile of the plane: consecutive workgroups go round-robin to the 8 XCDs, so each
 // XCD takes a contiguous band of tiles and neighbouring tiles' halos meet in the same L2. The
@@ -71,11 +75,16 @@ __device__ inline int ssim_tile_of(int block, int tiles) {
     const int per = (tiles + 7) / 8;
     return (block & 7) * per + (block >> 3);
 }
-constexpr int kSsimHW = kSsimTW + 10, kSsimHH = kSsimTH + 10;  // 42 x 26 halo
-constexpr int kHaloItems = kSsimHH * kSsimHW;
-constexpr int kHaloRounds = (kHaloItems + 255) / 256;  // per thread of a 256-thread workgroup
-// Output columns per work item of the horizontal passes: 26 rows x 8 items fill the workgroup
-// once, and each loaded input pixel (and its moments) serves 4 outputs.
+constexpr int kSsimHW = kSsimTW + 10;  // halo columns
+// The tile geometry of kTH output rows, declared inside each kernel.
+#define GSX_SSIM_TILE(kTH)                                                     \
+    constexpr int kSsimTH = (kTH);                                             \
+    constexpr int kSsimThreads = kSsimTW * kSsimTH / 2;                        \
+    constexpr int kSsimHH = kSsimTH + 10;                                      \
+    constexpr int kHaloItems = kSsimHH * kSsimHW;                              \
+    constexpr int kHaloRounds = (kHaloItems + kSsimThreads - 1) / kSsimThreads;
+// Output columns per work item of the horizontal passes: each loaded input pixel (and its
+// moments) serves 4 outputs.
 constexpr int kHCols = 4;
 
 // Forward: p and t of the halo in LDS; a horizontal 11-tap pass where each thread forms the
@@ -83,10 +92,11 @@ constexpr int kHCols = 4;
 // then a vertical pass where each thread produces two adjacent output rows from 12 loads per
 // moment plane. Writes the loss map (optionally after a fused L1 term) and the three dm maps
 // [3][planes][H][W] that the backward convolves.
-__global__ __launch_bounds__(256) void ssim_forward_kernel(float* __restrict__ map, const float* __restrict__ pred,
+__global__ __launch_bounds__(kSsimTW * kSsimFwdTH / 2) void ssim_forward_kernel(float* __restrict__ map, const float* __restrict__ pred,
                                                            const float* __restrict__ target, int32_t height,
                                                            int32_t width, int64_t planes, float scale, float l1_scale,
                                                            int fuse_l1, float* __restrict__ dm) {
+    GSX_SSIM_TILE(kSsimFwdTH)
     __shared__ float s_in[2][kSsimHH][kSsimHW + 1];
     __shared__ float s_h[5][kSsimHH][kSsimTW + 1];
     const int tiles_x = (width + kSsimTW - 1) / kSsimTW;
@@ -114,7 +124,7 @@ __global__ __launch_bounds__(256) void ssim_forward_kernel(float* __restrict__ m
         float pv[kHaloRounds], tv[kHaloRounds];
 #pragma unroll
         for (int u = 0; u < kHaloRounds; ++u) {
-            const int i = min((int)threadIdx.x + 256 * u, kHaloItems - 1);
+            const int i = min((int)threadIdx.x + kSsimThreads * u, kHaloItems - 1);
             const int hy = i / kSsimHW, hx = i % kSsimHW;
             const int y = oy + hy - 5, x = ox + hx - 5;
             const bool in = y >= 0 && y < height && x >= 0 && x < width;
@@ -125,14 +135,14 @@ __global__ __launch_bounds__(256) void ssim_forward_kernel(float* __restrict__ m
         }
 #pragma unroll
         for (int u = 0; u < kHaloRounds; ++u) {
-            const int i = min((int)threadIdx.x + 256 * u, kHaloItems - 1);
+            const int i = min((int)threadIdx.x + kSsimThreads * u, kHaloItems - 1);
             const int hy = i / kSsimHW, hx = i % kSsimHW;
             s_in[0][hy][hx] = pv[u];
             s_in[1][hy][hx] = tv[u];
         }
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < kSsimHH * (kSsimTW / kHCols); i += 256) {
+    for (int i = threadIdx.x; i < kSsimHH * (kSsimTW / kHCols); i += kSsimThreads) {
         const int hy = i / (kSsimTW / kHCols), cx = kHCols * (i % (kSsimTW / kHCols));
         float a[kHCols][5];
 #pragma unroll
@@ -211,11 +221,12 @@ __global__ __launch_bounds__(256) void ssim_forward_kernel(float* __restrict__ m
     }
 }
 
-__global__ __launch_bounds__(256) void ssim_backward_kernel(float* __restrict__ grad, const float* __restrict__ pred,
+__global__ __launch_bounds__(kSsimTW * kSsimBwdTH / 2) void ssim_backward_kernel(float* __restrict__ grad, const float* __restrict__ pred,
                                                             const float* __restrict__ target, int32_t height,
                                                             int32_t width, int64_t planes, float grad_scale,
                                                             float l1_grad_scale, int fuse_l1,
                                                             const float* __restrict__ dm) {
+    GSX_SSIM_TILE(kSsimBwdTH)
     __shared__ float s_m[3][kSsimHH][kSsimHW + 1];
     __shared__ float s_h[3][kSsimHH][kSsimTW + 1];
     const int tiles_x = (width + kSsimTW - 1) / kSsimTW;
@@ -244,7 +255,7 @@ __global__ __launch_bounds__(256) void ssim_backward_kernel(float* __restrict__ 
         float v0[kHaloRounds], v1[kHaloRounds], v2[kHaloRounds];
 #pragma unroll
         for (int u = 0; u < kHaloRounds; ++u) {
-            const int i = min((int)threadIdx.x + 256 * u, kHaloItems - 1);
+            const int i = min((int)threadIdx.x + kSsimThreads * u, kHaloItems - 1);
             const int hy = i / kSsimHW, hx = i % kSsimHW;
             const int y = oy + hy - 5, x = ox + hx - 5;
             const bool in = y >= 0 && y < height && x >= 0 && x < width;
@@ -256,7 +267,7 @@ __global__ __launch_bounds__(256) void ssim_backward_kernel(float* __restrict__ 
         }
 #pragma unroll
         for (int u = 0; u < kHaloRounds; ++u) {
-            const int i = min((int)threadIdx.x + 256 * u, kHaloItems - 1);
+            const int i = min((int)threadIdx.x + kSsimThreads * u, kHaloItems - 1);
             const int hy = i / kSsimHW, hx = i % kSsimHW;
             s_m[0][hy][hx] = v0[u];
             s_m[1][hy][hx] = v1[u];
@@ -264,7 +275,7 @@ __global__ __launch_bounds__(256) void ssim_backward_kernel(float* __restrict__ 
         }
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < kSsimHH * (kSsimTW / kHCols); i += 256) {
+    for (int i = threadIdx.x; i < kSsimHH * (kSsimTW / kHCols); i += kSsimThreads) {
         const int hy = i / (kSsimTW / kHCols), cx = kHCols * (i % (kSsimTW / kHCols));
         float a[kHCols][3];
 #pragma unroll
@@ -370,8 +381,9 @@ gsx_hip_status gsx_hip_loss_ssim_chw_f32_forward_kernel_launch(float* loss_map, 
     const int64_t planes = outer_count * channels;
     if (planes <= 0 || height <= 0 || width <= 0) return GSX_HIP_ERROR_INVALID_ARGUMENT;
     if (planes > 65535) return GSX_HIP_ERROR_OUT_OF_RANGE;
-    const int tiles = ((width + kSsimTW - 1) / kSsimTW) * ((height + kSsimTH - 1) / kSsimTH);
-    hipLaunchKernelGGL(ssim_forward_kernel, dim3((unsigned)(8 * ((tiles + 7) / 8)), (unsigned)planes), dim3(256), 0, stream, loss_map,
+    const int tiles = ((width + kSsimTW - 1) / kSsimTW) * ((height + kSsimFwdTH - 1) / kSsimFwdTH);
+    hipLaunchKernelGGL(ssim_forward_kernel, dim3((unsigned)(8 * ((tiles + 7) / 8)), (unsigned)planes),
+                       dim3(kSsimTW * kSsimFwdTH / 2), 0, stream, loss_map,
                        prediction, target, height, width, planes, scale, l1_scale, fuse_l1, ssim_workspace);
     return (gsx_hip_status)hipGetLastError();
 }
@@ -384,8 +396,9 @@ gsx_hip_status gsx_hip_loss_ssim_chw_f32_backward_kernel_launch(float* grad_pred
     const int64_t planes = outer_count * channels;
     if (planes <= 0 || height <= 0 || width <= 0) return GSX_HIP_ERROR_INVALID_ARGUMENT;
     if (planes > 65535) return GSX_HIP_ERROR_OUT_OF_RANGE;
-    const int tiles = ((width + kSsimTW - 1) / kSsimTW) * ((height + kSsimTH - 1) / kSsimTH);
-    hipLaunchKernelGGL(ssim_backward_kernel, dim3((unsigned)(8 * ((tiles + 7) / 8)), (unsigned)planes), dim3(256), 0, stream,
+    const int tiles = ((width + kSsimTW - 1) / kSsimTW) * ((height + kSsimBwdTH - 1) / kSsimBwdTH);
+    hipLaunchKernelGGL(ssim_backward_kernel, dim3((unsigned)(8 * ((tiles + 7) / 8)), (unsigned)planes),
+                       dim3(kSsimTW * kSsimBwdTH / 2), 0, stream,
                        grad_prediction, prediction, target, height, width, planes, grad_scale, l1_grad_scale, fuse_l1,
                        ssim_workspace);
     return (gsx_hip_status)hipGetLastError();
