@@ -53,13 +53,15 @@ struct Mat3 {
     float m[3][3];
 };
 
-__device__ inline float sigmoid_render(float x) {
+// exp_table (optional): an LDS copy of the 32-entry exp table (gsx_exp2_table_entry), in place
+// of the global one, for this and the helpers below.
+__device__ inline float sigmoid_render(float x, const uint64_t* exp_table = nullptr) {
     // render.c:397-407
     if (x >= 0.0f) {
-        float z = gsx_expf(-x);
+        float z = gsx_expf_table(-x, exp_table);
         return 1.0f / (1.0f + z);
     }
-    float z = gsx_expf(x);
+    float z = gsx_expf_table(x, exp_table);
     return z / (1.0f + z);
 }
 
@@ -152,11 +154,11 @@ struct Projected {
 };
 
 // Covariance of a Gaussian: Sigma = (R S)(R S)^T with S = diag(exp(logscale)) (render.c:583-601).
-__device__ inline Mat3 cov3d_from(const float4 q, const float ls[3]) {
+__device__ inline Mat3 cov3d_from(const float4 q, const float ls[3], const uint64_t* exp_table = nullptr) {
     Mat3 rs = rotation_from_xyzw(q.x, q.y, q.z, q.w);
-    float sx = gsx_expf(ls[0]);
-    float sy = gsx_expf(ls[1]);
-    float sz = gsx_expf(ls[2]);
+    float sx = gsx_expf_table(ls[0], exp_table);
+    float sy = gsx_expf_table(ls[1], exp_table);
+    float sz = gsx_expf_table(ls[2], exp_table);
 #pragma unroll
     for (int row = 0; row < 3; ++row) {
         rs.m[row][0] *= sx;
@@ -232,7 +234,7 @@ __device__ inline Projected preprocess_one(int64_t g, const float* __restrict__ 
                                            const float* __restrict__ opacity, const float* __restrict__ sh0,
                                            const float* __restrict__ sh1, const float* __restrict__ sh2,
                                            const float* __restrict__ sh3, int sh_degree, const CameraParams& cam,
-                                           bool want_color) {
+                                           bool want_color, const uint64_t* exp_table = nullptr) {
     Projected p;
     p.visible = false;
     const float raw_op = opacity[g];
@@ -240,7 +242,7 @@ __device__ inline Projected preprocess_one(int64_t g, const float* __restrict__ 
     const float mx = mean3d[g * 3 + 0], my = mean3d[g * 3 + 1], mz = mean3d[g * 3 + 2];
     const float4 q = reinterpret_cast<const float4*>(rotation)[g];
     const float ls[3] = {logscale[g * 3 + 0], logscale[g * 3 + 1], logscale[g * 3 + 2]};
-    const Mat3 cov3d = cov3d_from(q, ls);
+    const Mat3 cov3d = cov3d_from(q, ls, exp_table);
     const Mat3 w = camera_rotation(cam);
     // mean_cam = W mean + t
     float xc = w.m[0][0] * mx + w.m[0][1] * my + w.m[0][2] * mz;
@@ -288,7 +290,7 @@ __device__ inline Projected preprocess_one(int64_t g, const float* __restrict__ 
     if (p.x_min > p.x_max || p.y_min > p.y_max) return p;
     p.visible = true;
     p.inv_det = 1.0f / det;
-    p.opacity = sigmoid_render(raw_op);
+    p.opacity = sigmoid_render(raw_op, exp_table);
     if (want_color) {
         // render.c:487-496 normalise(mean - centre)
         float dx = mx - cam.centre[0], dy = my - cam.centre[1], dz = mz - cam.centre[2];

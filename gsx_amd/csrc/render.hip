@@ -1173,12 +1173,18 @@ __global__ __launch_bounds__(256) void projection_backward_kernel(
     float* __restrict__ g_rotation, float* __restrict__ g_logscale, float* __restrict__ g_opacity,
     float* __restrict__ g_sh0, float* __restrict__ g_sh1, float* __restrict__ g_sh2, float* __restrict__ g_sh3) {
     constexpr int sh_degree = kShDegree;
+    // the exp table in LDS: its lookups wait on LDS, not on a global load each
+    __shared__ uint64_t s_exp[GSX_EXP2_TABLE_SIZE];
+    if (threadIdx.x < GSX_EXP2_TABLE_SIZE) s_exp[threadIdx.x] = gsx_exp2_table_entry(threadIdx.x);
+    __syncthreads();
+    const uint64_t* exp_tab = s_exp;
+    __builtin_assume(exp_tab != nullptr);  // no run-time choice of table per lookup
     const int64_t gi = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (gi >= n) return;
     // issued first: its latency overlaps the recomputation below (only visible Gaussians use it)
     const uint32_t run_length = tile_count[gi];
     const Projected p =
-        preprocess_one(gi, mean3d, rotation, logscale, opacity, sh0, sh1, sh2, sh3, sh_degree, cam, true);
+        preprocess_one(gi, mean3d, rotation, logscale, opacity, sh0, sh1, sh2, sh3, sh_degree, cam, true, exp_tab);
     float gm[3] = {0.0f, 0.0f, 0.0f};
     float gr[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     float gl[3] = {0.0f, 0.0f, 0.0f};
@@ -1213,9 +1219,10 @@ __global__ __launch_bounds__(256) void projection_backward_kernel(
         const Mat3 w = camera_rotation(cam);
         const float4 q = reinterpret_cast<const float4*>(rotation)[gi];
         const float ls[3] = {logscale[gi * 3 + 0], logscale[gi * 3 + 1], logscale[gi * 3 + 2]};
-        const Mat3 cov3d = cov3d_from(q, ls);
+        const Mat3 cov3d = cov3d_from(q, ls, exp_tab);
         const Mat3 rot = rotation_from_xyzw(q.x, q.y, q.z, q.w);
-        const float sx = gsx_expf(ls[0]), sy = gsx_expf(ls[1]), sz = gsx_expf(ls[2]);
+        const float sx = gsx_expf_table(ls[0], exp_tab), sy = gsx_expf_table(ls[1], exp_tab),
+                    sz = gsx_expf_table(ls[2], exp_tab);
         const float zc = p.zc, xc = p.xc, yc = p.yc;
         const float j00 = cam.fx / zc;
         const float j02 = -cam.fx * xc / (zc * zc);
@@ -1307,7 +1314,7 @@ __global__ __launch_bounds__(256) void projection_backward_kernel(
         }
         // opacity: render.c:1830
         {
-            const float sg = sigmoid_render(opacity[gi]);
+            const float sg = sigmoid_render(opacity[gi], exp_tab);
             gop += dop * (sg * (1.0f - sg));
         }
         // mean through the projection: render.c:1832-1845
