@@ -81,6 +81,7 @@ struct WaveBoxes {
     uint32_t tx0[kWave], ty0[kWave], wx[kWave], excl[kWave], kept[kWave], out[kWave];
     uint32_t g[kWave];
     uint32_t mark[kWave];  // walk step: base + owner at the lane where that owner's pairs start
+    uint32_t full[kWave];  // nonzero: every tile of the box is kept (no tile test needed)
 };
 
 // Inclusive prefix maximum over the 64 lanes of a wave (DPP row shifts, then the two row
@@ -96,8 +97,9 @@ __device__ inline int wave_inclusive_max(int v) {
 }
 
 // Stores lane's box (zero tiles when !valid) and returns the wave's total tile count.
+// full: every tile of the box is known to be kept (its kept count equals its tile count).
 __device__ inline uint32_t stage_box(WaveBoxes& w, bool valid, float4 r0, float4 r1, float4 r2, uint32_t g,
-                                     uint32_t out) {
+                                     uint32_t out, bool full) {
     const uint32_t lane = __lane_id();
     uint32_t total = 0;
     if (valid) {
@@ -117,6 +119,7 @@ __device__ inline uint32_t stage_box(WaveBoxes& w, bool valid, float4 r0, float4
     }
     w.g[lane] = g;
     w.out[lane] = out;
+    w.full[lane] = valid && full ? 1u : 0u;
     w.kept[lane] = 0;
     // inclusive wave scan of the box sizes
     uint32_t incl = total;
@@ -165,10 +168,15 @@ __device__ inline void walk_wave_tiles(WaveBoxes& w, uint32_t wave_total, int32_
             const uint32_t ty = w.ty0[owner] + row;
             const uint32_t tx = w.tx0[owner] + (k - row * wx);
             tile = ty * (uint32_t)tiles_x + tx;
-            const int px0 = max((int)tx * kTile, w.x0[owner]), px1 = min((int)tx * kTile + kTile - 1, w.x1[owner]);
-            const int py0 = max((int)ty * kTile, w.y0[owner]), py1 = min((int)ty * kTile + kTile - 1, w.y1[owner]);
-            const gsx_tile_conic con = w.conic[owner];
-            keep = gsx_tile_conic_test(&con, px0, px1, py0, py1) != 0;
+            keep = true;
+            if (!kEmit || w.full[owner] == 0u) {  // skipped by the wave when every lane's box is full
+                const int px0 = max((int)tx * kTile, w.x0[owner]);
+                const int px1 = min((int)tx * kTile + kTile - 1, w.x1[owner]);
+                const int py0 = max((int)ty * kTile, w.y0[owner]);
+                const int py1 = min((int)ty * kTile + kTile - 1, w.y1[owner]);
+                const gsx_tile_conic con = w.conic[owner];
+                keep = gsx_tile_conic_test(&con, px0, px1, py0, py1) != 0;
+            }
         }
         const uint64_t mask = wave_ballot(keep);
         // first lane of this step holding the owner's pairs
@@ -253,7 +261,7 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
         depth_keys[g] = key;
     }
     if (big) big_list[atomicAdd(big_count, 1u)] = (uint32_t)g;  // counted by big_tiles_kernel
-    const uint32_t total = stage_box(wb, visible && !big, r0, r1, r2, (uint32_t)g, 0u);
+    const uint32_t total = stage_box(wb, visible && !big, r0, r1, r2, (uint32_t)g, 0u, false);
     walk_wave_tiles<false>(wb, total, cam.tiles_x, KeyLayout{}, nullptr, nullptr);
     const uint32_t kept = big ? 0u : wb.kept[__lane_id()];  // big boxes: counted by big_tiles_kernel
     if (g < n) tile_count[g] = kept;
@@ -358,7 +366,9 @@ __device__ inline void emit_block(uint32_t b, int64_t n, const float4* __restric
         r2 = rec[3 * (size_t)g + 2];
     }
     const bool any = cnt > 0 && box_tiles(r2) <= kBigTiles;  // big boxes are emitted by big_tiles_block
-    const uint32_t total = stage_box(wb, any, r0, r1, r2, g, o);
+    // a box whose kept count (from the counting walk's identical tests) is its tile count keeps
+    // every tile: emission skips its tests
+    const uint32_t total = stage_box(wb, any, r0, r1, r2, g, o, any && cnt == box_tiles(r2));
     walk_wave_tiles<true>(wb, total, tiles_x, layout, keys, instance_gaussian);
 }
 
