@@ -593,17 +593,20 @@ __device__ inline int xcd_tile_index(int block, int tiles) {
     return t;
 }
 
-__device__ inline bool in_box(int px, int py, uint32_t bx, uint32_t by) {
-    return (px >= (int)(bx & 0xffffu)) & (px <= (int)(bx >> 16)) & (py >= (int)(by & 0xffffu)) & (py <= (int)(by >> 16));
+// The box test in packed 16-bit halves, three vector instructions: (px, py) lies in
+// [x0, x1] x [y0, y1] iff both halves of (px | py << 16) - (x0 | y0 << 16) (each wrapping mod
+// 2^16) are at most those of (x1 - x0) | (y1 - y0) << 16. The blend kernels stage each box in
+// this form (box_lo, box_ext; kEmptyBoxLo / 0 for none: no pixel coordinate is 65535).
+typedef uint16_t gsx_u16x2 __attribute__((ext_vector_type(2)));
+constexpr uint32_t kEmptyBoxLo = 0xffffffffu;
+__device__ inline uint32_t box_lo(uint32_t bx, uint32_t by) { return (bx & 0xffffu) | (by << 16); }
+__device__ inline uint32_t box_ext(uint32_t bx, uint32_t by) {
+    return ((bx >> 16) - (bx & 0xffffu)) | (((by >> 16) - (by & 0xffffu)) << 16);
 }
-
-// The lanes for which `open & in_box(...)` holds, as the AND of the ballots of the five
-// conditions: each ballot is its compare's lane mask, so the wave-uniform test costs no vector
-// instruction (a ballot of the combined bool is formed through a vector register).
-// open_mask is the ballot of `open`, taken where `open` is a compare.
-__device__ inline uint64_t in_box_ballot(uint64_t open_mask, int px, int py, uint32_t bx, uint32_t by) {
-    return open_mask & wave_ballot(px >= (int)(bx & 0xffffu)) & wave_ballot(px <= (int)(bx >> 16)) &
-           wave_ballot(py >= (int)(by & 0xffffu)) & wave_ballot(py <= (int)(by >> 16));
+__device__ inline bool in_box_packed(uint32_t pxy, uint32_t lo, uint32_t ext) {
+    const gsx_u16x2 d = __builtin_bit_cast(gsx_u16x2, pxy) - __builtin_bit_cast(gsx_u16x2, lo);
+    const gsx_u16x2 m = __builtin_elementwise_min(d, __builtin_bit_cast(gsx_u16x2, ext));
+    return __builtin_bit_cast(uint32_t, m) == __builtin_bit_cast(uint32_t, d);
 }
 
 // Transmittance checkpoints: the backward needs every contribution's exact T_before (the CPU
@@ -644,6 +647,7 @@ __global__ __launch_bounds__(kBlendThreads) void blend_forward_kernel(
     const uint2 range = ranges[tile];
     const float fpx = (float)px + 0.5f;
     const float fpy = (float)py + 0.5f;
+    const uint32_t pxy = (uint32_t)px | ((uint32_t)py << 16);  // for in_box_packed
     // t only falls, and a pixel is done once an accepted contribution takes it below the
     // threshold, so "done" is t < threshold; pixels outside the image start done (t = 0, never
     // written out)
@@ -657,7 +661,11 @@ __global__ __launch_bounds__(kBlendThreads) void blend_forward_kernel(
             if (sorted_g != nullptr) sorted_g[j] = g;  // TRAIN: the backward reads it
             s_r0[threadIdx.x] = rec[3 * (size_t)g + 0];
             s_r1[threadIdx.x] = rec[3 * (size_t)g + 1];
-            s_r2[threadIdx.x] = rec[3 * (size_t)g + 2];
+            float4 r2 = rec[3 * (size_t)g + 2];
+            const uint32_t bx = __float_as_uint(r2.y), by = __float_as_uint(r2.z);
+            r2.y = __uint_as_float(box_lo(bx, by));
+            r2.z = __uint_as_float(box_ext(bx, by));
+            s_r2[threadIdx.x] = r2;
         }
         __syncthreads();
         // wave-uniform bound, held in a scalar register
@@ -670,9 +678,9 @@ __global__ __launch_bounds__(kBlendThreads) void blend_forward_kernel(
                 ckpt[checkpoint_slot(range.x, tile, base + (uint32_t)k) * kBlendThreads + threadIdx.x] = t;
             }
             const float4 r2 = s_r2[k];
-            const uint32_t bx = __float_as_uint(r2.y), by = __float_as_uint(r2.z);
-            const bool live = open & in_box(px, py, bx, by);  // bitwise: one lane mask
-            if (mask_none(in_box_ballot(open_mask, px, py, bx, by))) continue;  // uniform
+            const bool ib = in_box_packed(pxy, __float_as_uint(r2.y), __float_as_uint(r2.z));
+            const bool live = open & ib;  // bitwise: one lane mask
+            if (mask_none(open_mask & wave_ballot(ib))) continue;  // uniform
             // branch-free evaluation for the wave; lanes outside the box or done keep their state
             const float4 r0 = s_r0[k];
             const float4 r1 = s_r1[k];
@@ -763,6 +771,7 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
     const size_t plane = (size_t)cam.width * (size_t)cam.height;
     const float fpx = (float)px + 0.5f;
     const float fpy = (float)py + 0.5f;
+    const uint32_t pxy = (uint32_t)px | ((uint32_t)py << 16);  // for in_box_packed
     float t_final = 0.0f, d0 = 0.0f, d1 = 0.0f, d2 = 0.0f;
     uint32_t last = range.x;
     if (inside) {
@@ -817,7 +826,11 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
                 const uint32_t g = sorted_g[j];
                 s_r0[threadIdx.x] = rec[3 * (size_t)g + 0];
                 s_r1[threadIdx.x] = rec[3 * (size_t)g + 1];
-                s_r2[threadIdx.x] = rec[3 * (size_t)g + 2];
+                float4 r2 = rec[3 * (size_t)g + 2];
+                const uint32_t bx = __float_as_uint(r2.y), by = __float_as_uint(r2.z);
+                r2.y = __uint_as_float(box_lo(bx, by));
+                r2.z = __uint_as_float(box_ext(bx, by));
+                s_r2[threadIdx.x] = r2;
                 s_k0[threadIdx.x] = cov_coef[2 * (size_t)g + 0];
                 const float4 k1 = cov_coef[2 * (size_t)g + 1];
                 s_k1[threadIdx.x] = make_float2(k1.x, k1.y);
@@ -825,7 +838,7 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
                 const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
                 s_r0[threadIdx.x] = z;
                 s_r1[threadIdx.x] = z;
-                s_r2[threadIdx.x] = make_float4(0.0f, __uint_as_float(1u), 0.0f, 0.0f);  // empty box
+                s_r2[threadIdx.x] = make_float4(0.0f, __uint_as_float(kEmptyBoxLo), 0.0f, 0.0f);  // no pixel
                 s_k0[threadIdx.x] = z;
                 s_k1[threadIdx.x] = make_float2(0.0f, 0.0f);
             }
@@ -855,10 +868,10 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
                     if (i >= n_in) continue;  // uniform
                     const int kk = sb * kBucket + i;
                     const float4 r2 = s_r2[kk];
-                    const uint32_t bx = __float_as_uint(r2.y), by = __float_as_uint(r2.z);
+                    const bool ib = in_box_packed(pxy, __float_as_uint(r2.y), __float_as_uint(r2.z));
                     const bool before_last = j0 + (uint32_t)i < last;
-                    const bool live = pixel_live & before_last & in_box(px, py, bx, by);
-                    if (mask_none(in_box_ballot(pixel_mask & wave_ballot(before_last), px, py, bx, by))) continue;
+                    const bool live = pixel_live & before_last & ib;
+                    if (mask_none(pixel_mask & wave_ballot(before_last) & wave_ballot(ib))) continue;
                     const float4 r0 = s_r0[kk];
                     const float4 r1 = s_r1[kk];
                     const float dx = fpx - r0.x;
