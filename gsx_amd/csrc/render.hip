@@ -670,17 +670,20 @@ __global__ __launch_bounds__(kBlendThreads) void blend_forward_kernel(
         __syncthreads();
         // wave-uniform bound, held in a scalar register
         const int count = __builtin_amdgcn_readfirstlane((int)min((uint32_t)kBlendThreads, range.y - base));
+        // the lanes not done (t only changes where an entry is evaluated, so the mask is
+        // re-formed there, not per entry)
+        uint64_t open_mask = wave_ballot(t >= kTransmittanceThreshold);
         for (int k = 0; k < count; ++k) {
-            const bool open = t >= kTransmittanceThreshold;  // not done
-            const uint64_t open_mask = wave_ballot(open);
             if (mask_none(open_mask)) break;  // uniform: every pixel of this wave is saturated
-            if (ckpt != nullptr && open && (k & (kBucket - 1)) == 0) {
-                ckpt[checkpoint_slot(range.x, tile, base + (uint32_t)k) * kBlendThreads + threadIdx.x] = t;
+            if (ckpt != nullptr && (k & (kBucket - 1)) == 0) {  // uniform
+                if (t >= kTransmittanceThreshold)
+                    ckpt[checkpoint_slot(range.x, tile, base + (uint32_t)k) * kBlendThreads + threadIdx.x] = t;
             }
             const float4 r2 = s_r2[k];
             const bool ib = in_box_packed(pxy, __float_as_uint(r2.y), __float_as_uint(r2.z));
-            const bool live = open & ib;  // bitwise: one lane mask
-            if (mask_none(open_mask & wave_ballot(ib))) continue;  // uniform
+            const uint64_t live_mask = open_mask & wave_ballot(ib);
+            if (mask_none(live_mask)) continue;  // uniform
+            const bool live = __builtin_amdgcn_inverse_ballot_w64(live_mask);
             // branch-free evaluation for the wave; lanes outside the box or done keep their state
             const float4 r0 = s_r0[k];
             const float4 r1 = s_r1[k];
@@ -698,6 +701,7 @@ __global__ __launch_bounds__(kBlendThreads) void blend_forward_kernel(
             c2 = ok ? c2 + w * r2.x : c2;
             t = ok ? t * (1.0f - alpha) : t;
             last = ok ? base + (uint32_t)k + 1u : last;
+            open_mask = wave_ballot(t >= kTransmittanceThreshold);
         }
         __syncthreads();
     }
