@@ -40,23 +40,28 @@ __global__ __launch_bounds__(kScanThreads) void scan_reduce_kernel(const uint32_
 }
 
 // Single workgroup: exclusive scan of `count` partial sums in place; grand total at [count].
+// 16 values per thread and step (4096: the block sums of 1M ranks in one step), all loaded
+// before the first wait (positions past count re-read position 0 and count as 0).
+constexpr int kPartialItems = 16;
 __global__ __launch_bounds__(kScanThreads) void scan_partials_kernel(uint32_t* __restrict__ partials, int64_t count) {
     __shared__ uint32_t s_wave[kScanThreads / kWave];
     uint32_t carry = 0;
-    for (int64_t base = 0; base < count; base += kScanChunk) {
-        uint32_t vals[kScanItems];
+    for (int64_t base = 0; base < count; base += (int64_t)kScanThreads * kPartialItems) {
+        uint32_t vals[kPartialItems];
+#pragma unroll
+        for (int k = 0; k < kPartialItems; ++k) {
+            const int64_t i = base + (int64_t)threadIdx.x * kPartialItems + k;
+            const uint32_t v = partials[i < count ? i : 0];
+            vals[k] = i < count ? v : 0u;
+        }
         uint32_t sum = 0;
 #pragma unroll
-        for (int k = 0; k < kScanItems; ++k) {
-            int64_t i = base + (int64_t)threadIdx.x * kScanItems + k;
-            vals[k] = i < count ? partials[i] : 0u;
-            sum += vals[k];
-        }
+        for (int k = 0; k < kPartialItems; ++k) sum += vals[k];
         uint32_t total;
         uint32_t prefix = block_exclusive_scan_256(sum, s_wave, total) + carry;
 #pragma unroll
-        for (int k = 0; k < kScanItems; ++k) {
-            int64_t i = base + (int64_t)threadIdx.x * kScanItems + k;
+        for (int k = 0; k < kPartialItems; ++k) {
+            const int64_t i = base + (int64_t)threadIdx.x * kPartialItems + k;
             if (i < count) partials[i] = prefix;
             prefix += vals[k];
         }
