@@ -666,42 +666,51 @@ __global__ __launch_bounds__(kBlendThreads) void blend_forward_kernel(
             r2.y = __uint_as_float(box_lo(bx, by));
             r2.z = __uint_as_float(box_ext(bx, by));
             s_r2[threadIdx.x] = r2;
+        } else {
+            // past the list: a box no pixel lies in, so the last bucket can run whole
+            s_r2[threadIdx.x] = make_float4(0.0f, __uint_as_float(kEmptyBoxLo), 0.0f, 0.0f);
         }
         __syncthreads();
-        // wave-uniform bound, held in a scalar register
+        // wave-uniform bound, held in a scalar register, rounded up to whole buckets
         const int count = __builtin_amdgcn_readfirstlane((int)min((uint32_t)kBlendThreads, range.y - base));
+        const int padded = (count + kBucket - 1) & ~(kBucket - 1);
         // the lanes not done (t only changes where an entry is evaluated, so the mask is
         // re-formed there, not per entry)
         uint64_t open_mask = wave_ballot(t >= kTransmittanceThreshold);
-        for (int k = 0; k < count; ++k) {
+        // buckets of kBucket entries, each unrolled: the checkpoint at the bucket's start and
+        // the loop control cost no instructions per entry
+        for (int k0 = 0; k0 < padded; k0 += kBucket) {
             if (mask_none(open_mask)) break;  // uniform: every pixel of this wave is saturated
-            if (ckpt != nullptr && (k & (kBucket - 1)) == 0) {  // uniform
-                if (t >= kTransmittanceThreshold)
-                    ckpt[checkpoint_slot(range.x, tile, base + (uint32_t)k) * kBlendThreads + threadIdx.x] = t;
+            if (ckpt != nullptr && t >= kTransmittanceThreshold)
+                ckpt[checkpoint_slot(range.x, tile, base + (uint32_t)k0) * kBlendThreads + threadIdx.x] = t;
+#pragma unroll
+            for (int i = 0; i < kBucket; ++i) {
+                const int k = k0 + i;
+                const float4 r2 = s_r2[k];
+                const bool ib = in_box_packed(pxy, __float_as_uint(r2.y), __float_as_uint(r2.z));
+                const uint64_t live_mask = open_mask & wave_ballot(ib);
+                if (mask_none(live_mask)) continue;  // uniform
+                const bool live = __builtin_amdgcn_inverse_ballot_w64(live_mask);
+                // branch-free evaluation for the wave; lanes outside the box or done keep their state
+                const float4 r0 = s_r0[k];
+                const float4 r1 = s_r1[k];
+                const float dx = fpx - r0.x;
+                const float dy = fpy - r0.y;
+                float power = -0.5f * (r0.z * dx * dx + r0.w * dx * dy + r1.x * dy * dy);
+                power = power > 0.0f ? 0.0f : power;
+                bool ok = live & (power >= kPowerThreshold);
+                const float gval = gsx_expf_blend(fmaxf(power, kPowerThreshold), s_exp2);
+                const float alpha = fminf(kMaxFragmentAlpha, r1.y * gval);
+                ok = ok & (alpha >= kMinAlpha);
+                const float w = alpha * t;
+                c0 = ok ? c0 + w * r1.z : c0;
+                c1 = ok ? c1 + w * r1.w : c1;
+                c2 = ok ? c2 + w * r2.x : c2;
+                t = ok ? t * (1.0f - alpha) : t;
+                last = ok ? base + (uint32_t)k + 1u : last;
+                open_mask = wave_ballot(t >= kTransmittanceThreshold);
+                if (mask_none(open_mask)) break;  // uniform
             }
-            const float4 r2 = s_r2[k];
-            const bool ib = in_box_packed(pxy, __float_as_uint(r2.y), __float_as_uint(r2.z));
-            const uint64_t live_mask = open_mask & wave_ballot(ib);
-            if (mask_none(live_mask)) continue;  // uniform
-            const bool live = __builtin_amdgcn_inverse_ballot_w64(live_mask);
-            // branch-free evaluation for the wave; lanes outside the box or done keep their state
-            const float4 r0 = s_r0[k];
-            const float4 r1 = s_r1[k];
-            const float dx = fpx - r0.x;
-            const float dy = fpy - r0.y;
-            float power = -0.5f * (r0.z * dx * dx + r0.w * dx * dy + r1.x * dy * dy);
-            power = power > 0.0f ? 0.0f : power;
-            bool ok = live & (power >= kPowerThreshold);
-            const float gval = gsx_expf_blend(fmaxf(power, kPowerThreshold), s_exp2);
-            const float alpha = fminf(kMaxFragmentAlpha, r1.y * gval);
-            ok = ok & (alpha >= kMinAlpha);
-            const float w = alpha * t;
-            c0 = ok ? c0 + w * r1.z : c0;
-            c1 = ok ? c1 + w * r1.w : c1;
-            c2 = ok ? c2 + w * r2.x : c2;
-            t = ok ? t * (1.0f - alpha) : t;
-            last = ok ? base + (uint32_t)k + 1u : last;
-            open_mask = wave_ballot(t >= kTransmittanceThreshold);
         }
         __syncthreads();
     }
