@@ -146,8 +146,8 @@ def main():
                     help="reference CPU steps to time on the full workload (0 disables)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU only; multi-GPU scaling is design-only "
-                                   "(see DESIGN.md, 'How the path would shard')", "n_gpus": args.gpus}))
+        print(json.dumps({"error": "this build runs on one GPU only; multi-GPU scaling (image tile bands "
+                                   "per GPU, one gradient all-reduce) is not built", "n_gpus": args.gpus}))
         sys.exit(2)
 
     import numpy as np
