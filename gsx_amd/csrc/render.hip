@@ -702,14 +702,15 @@ __global__ __launch_bounds__(kBlendThreads) void blend_forward_kernel(
                 const float gval = gsx_expf_blend(fmaxf(power, kPowerThreshold), s_exp2);
                 const float alpha = fminf(kMaxFragmentAlpha, r1.y * gval);
                 ok = ok & (alpha >= kMinAlpha);
-                // a lane that does not take the entry adds (0 * colour) = +-0, which leaves its sums
-                // exactly as they are (they start at +0 and stay finite), so one select serves all
-                // three channels
-                const float w = ok ? alpha * t : 0.0f;
+                // a lane that does not take the entry uses alpha = 0: it adds (0 * colour) = +-0,
+                // which leaves its sums exactly as they are (they start at +0 and stay finite), and
+                // multiplies t by 1, so one select serves the colour sums and t
+                const float a_used = ok ? alpha : 0.0f;
+                const float w = a_used * t;
                 c0 = c0 + w * r1.z;
                 c1 = c1 + w * r1.w;
                 c2 = c2 + w * r2.x;
-                t = ok ? t * (1.0f - alpha) : t;
+                t = t * (1.0f - a_used);
                 last = ok ? base + (uint32_t)k + 1u : last;
                 open_mask = wave_ballot(t >= kTransmittanceThreshold);
                 if (mask_none(open_mask)) break;  // uniform
