@@ -1596,3 +1596,294 @@ uint64_t oracle_expf_mismatches(uint32_t lo_bits, uint32_t hi_bits, uint32_t str
     }
     return bad;
 }
+
+/* ---------------------------------------------------------------------------------------
+ * Tiled evaluation for full-size scenes (configs 3 and 4: 3M and 6M Gaussians at 1080p,
+ * where the per-Gaussian raster above walks 4e9 and 2e11 box pixels). Same arithmetic as
+ * oracle_render_forward and oracle_tile_keys, reorganised so that it runs on all host cores
+ * and stops where the CPU's loop can no longer change a pixel:
+ *   - visible records from collect_visible over chunks of Gaussians in parallel, compacted
+ *     in Gaussian order (render.c:850-1016);
+ *   - the (depth, index) order of render.c:830-848 through a sort of
+ *     bits(depth) << 32 | position keys (depth > near > 0, so the float bits order like the
+ *     values, and positions follow the Gaussian index);
+ *   - per tile, the Gaussians whose box meets the tile, in that order (with `cull`, only the
+ *     instances the tile test keeps, exactly oracle_tile_keys' per-tile lists);
+ *   - per pixel, the CPU's update (render.c:1035-1079) over its tile's list. Transmittance
+ *     never rises, so after T < 1e-4 the CPU's own test skips every later entry and the walk
+ *     stops there.
+ * Pixels equal oracle_render_forward's bit for bit and the cut lists equal oracle_tile_keys'
+ * key for key; the CPU tests check both on scenes that the serial functions finish.
+ * ------------------------------------------------------------------------------------- */
+#include <omp.h>
+
+static int cmp_u64(const void *pa, const void *pb)
+{
+    uint64_t a = *(const uint64_t *)pa, b = *(const uint64_t *)pb;
+
+    return a < b ? -1 : (a > b ? 1 : 0);
+}
+
+typedef struct tiled_lists {
+    int64_t count;          /* visible Gaussians */
+    vis *v;                 /* visible records in (depth, index) order */
+    int32_t tiles_x, tiles_y;
+    int64_t *tile_start;    /* [tiles + 1] */
+    uint32_t *entries;      /* positions into v, per tile in list order */
+} tiled_lists;
+
+static void tiled_free(tiled_lists *t)
+{
+    free(t->v);
+    free(t->tile_start);
+    free(t->entries);
+    memset(t, 0, sizeof(*t));
+}
+
+static int tiled_build(int64_t n, int deg, const float *mean3d, const float *rot, const float *ls,
+    const float *op, const float *sh0, const float *sh1, const float *sh2, const float *sh3, const cam *k,
+    int32_t tile, int cull, tiled_lists *out)
+{
+    const int64_t chunk = 1 << 16;
+    int64_t nchunks = (n + chunk - 1) / chunk;
+    int64_t *ccount = (int64_t *)calloc((size_t)(nchunks > 0 ? nchunks : 1), sizeof(int64_t));
+    vis *all = (vis *)malloc(sizeof(vis) * (size_t)(n > 0 ? n : 1));
+    uint64_t *order = NULL;
+    int64_t count = 0, c, i;
+    const int32_t tiles_x = (k->width + tile - 1) / tile, tiles_y = (k->height + tile - 1) / tile;
+    const int64_t tiles = (int64_t)tiles_x * tiles_y;
+    const int nparts = 256;
+    int64_t *part_counts = NULL, *box_byte = NULL;
+    uint8_t *kept = NULL;
+    int ok = 1;
+
+    memset(out, 0, sizeof(*out));
+    if(ccount == NULL || all == NULL) {
+        free(ccount);
+        free(all);
+        return -1;
+    }
+#pragma omp parallel for schedule(dynamic, 1)
+    for(c = 0; c < nchunks; ++c) {
+        int64_t i0 = c * chunk, m = n - i0 < chunk ? n - i0 : chunk, j;
+
+        ccount[c] = collect_visible(m, deg, mean3d + 3 * i0, rot + 4 * i0, ls + 3 * i0, op + i0, sh0 + 3 * i0,
+            deg >= 1 ? sh1 + 9 * i0 : NULL, deg >= 2 ? sh2 + 15 * i0 : NULL, deg >= 3 ? sh3 + 21 * i0 : NULL, k,
+            all + i0, NULL);
+        for(j = 0; j < ccount[c]; ++j) {
+            all[i0 + j].g += i0;
+        }
+    }
+    for(c = 0; c < nchunks; ++c) {
+        if(count != c * chunk && ccount[c] > 0) {
+            memmove(all + count, all + c * chunk, sizeof(vis) * (size_t)ccount[c]);
+        }
+        count += ccount[c];
+    }
+    free(ccount);
+
+    order = (uint64_t *)malloc(sizeof(uint64_t) * (size_t)(count > 0 ? count : 1));
+    out->v = (vis *)malloc(sizeof(vis) * (size_t)(count > 0 ? count : 1));
+    out->tile_start = (int64_t *)calloc((size_t)tiles + 1, sizeof(int64_t));
+    part_counts = (int64_t *)calloc((size_t)nparts * (size_t)tiles, sizeof(int64_t));
+    box_byte = (int64_t *)malloc(sizeof(int64_t) * (size_t)(count + 1));
+    if(order == NULL || out->v == NULL || out->tile_start == NULL || part_counts == NULL || box_byte == NULL) {
+        ok = 0;
+        goto done;
+    }
+#pragma omp parallel for schedule(static)
+    for(i = 0; i < count; ++i) {
+        order[i] = ((uint64_t)gsx_f32_bits(all[i].rec[ORACLE_REC_DEPTH]) << 32) | (uint64_t)i;
+    }
+    qsort(order, (size_t)count, sizeof(uint64_t), cmp_u64);
+#pragma omp parallel for schedule(static)
+    for(i = 0; i < count; ++i) {
+        out->v[i] = all[order[i] & 0xFFFFFFFFu];
+    }
+    free(all);
+    all = NULL;
+    out->count = count;
+    out->tiles_x = tiles_x;
+    out->tiles_y = tiles_y;
+
+    /* kept flag of every (Gaussian, box tile), one byte each, byte ranges per Gaussian */
+    box_byte[0] = 0;
+    for(i = 0; i < count; ++i) {
+        const int32_t *bb = out->v[i].bb;
+        int64_t bt = (int64_t)(bb[1] / tile - bb[0] / tile + 1) * (int64_t)(bb[3] / tile - bb[2] / tile + 1);
+
+        box_byte[i + 1] = box_byte[i] + (cull ? bt : 0);
+    }
+    if(cull) {
+        kept = (uint8_t *)malloc((size_t)(box_byte[count] > 0 ? box_byte[count] : 1));
+        if(kept == NULL) {
+            ok = 0;
+            goto done;
+        }
+    }
+    /* per part (a contiguous range of the depth order) and tile: entry counts */
+#pragma omp parallel for schedule(dynamic, 1)
+    for(c = 0; c < nparts; ++c) {
+        int64_t lo = count * c / nparts, hi = count * (c + 1) / nparts, g;
+        int64_t *pc = part_counts + (size_t)c * (size_t)tiles;
+
+        for(g = lo; g < hi; ++g) {
+            const int32_t *bb = out->v[g].bb;
+            int64_t b = box_byte[g];
+            int32_t tx, ty;
+
+            for(ty = bb[2] / tile; ty <= bb[3] / tile; ++ty) {
+                for(tx = bb[0] / tile; tx <= bb[1] / tile; ++tx) {
+                    int keep = 1;
+
+                    if(cull) {
+                        keep = tile_kept(&out->v[g], tx, ty, tile);
+                        kept[b++] = (uint8_t)keep;
+                    }
+                    pc[(int64_t)ty * tiles_x + tx] += keep;
+                }
+            }
+        }
+    }
+    /* exclusive prefix over (tile, part): each part's cursor within each tile */
+    {
+        int64_t total = 0, t;
+
+        for(t = 0; t < tiles; ++t) {
+            out->tile_start[t] = total;
+            for(c = 0; c < nparts; ++c) {
+                int64_t v = part_counts[(size_t)c * (size_t)tiles + (size_t)t];
+
+                part_counts[(size_t)c * (size_t)tiles + (size_t)t] = total;
+                total += v;
+            }
+        }
+        out->tile_start[tiles] = total;
+        out->entries = (uint32_t *)malloc(sizeof(uint32_t) * (size_t)(total > 0 ? total : 1));
+        if(out->entries == NULL) {
+            ok = 0;
+            goto done;
+        }
+    }
+#pragma omp parallel for schedule(dynamic, 1)
+    for(c = 0; c < nparts; ++c) {
+        int64_t lo = count * c / nparts, hi = count * (c + 1) / nparts, g;
+        int64_t *pc = part_counts + (size_t)c * (size_t)tiles;
+
+        for(g = lo; g < hi; ++g) {
+            const int32_t *bb = out->v[g].bb;
+            int64_t b = box_byte[g];
+            int32_t tx, ty;
+
+            for(ty = bb[2] / tile; ty <= bb[3] / tile; ++ty) {
+                for(tx = bb[0] / tile; tx <= bb[1] / tile; ++tx) {
+                    if(cull && !kept[b++]) continue;
+                    out->entries[pc[(int64_t)ty * tiles_x + tx]++] = (uint32_t)g;
+                }
+            }
+        }
+    }
+done:
+    free(all);
+    free(order);
+    free(part_counts);
+    free(box_byte);
+    free(kept);
+    if(!ok) {
+        tiled_free(out);
+        return -1;
+    }
+    return 0;
+}
+
+/* Renders with the tiled lists (see above) and/or returns the cut lists as sorted keys:
+ * key = tile << 32 | bits(depth), value = Gaussian index, as oracle_tile_keys. out_keys /
+ * out_values receive malloc'ed arrays (release with oracle_free). Returns the number of list
+ * entries, or -1. */
+int64_t oracle_tiled(int64_t n, int sh_degree, const float *mean3d, const float *rotation,
+    const float *logscale, const float *opacity, const float *sh0, const float *sh1, const float *sh2,
+    const float *sh3, const float *camera, int32_t tile, int cull, float *out_rgb, float *out_t,
+    uint64_t **out_keys, uint32_t **out_values)
+{
+    cam k = cam_from(camera);
+    tiled_lists tl;
+    const size_t pixels = (size_t)k.width * (size_t)k.height;
+    int64_t tiles, total, t;
+
+    if(tiled_build(n, sh_degree, mean3d, rotation, logscale, opacity, sh0, sh1, sh2, sh3, &k, tile, cull, &tl) != 0) {
+        return -1;
+    }
+    tiles = (int64_t)tl.tiles_x * tl.tiles_y;
+    total = tl.tile_start[tiles];
+    if(out_rgb != NULL) {
+#pragma omp parallel for schedule(dynamic, 4)
+        for(t = 0; t < tiles; ++t) {
+            const int32_t tx = (int32_t)(t % tl.tiles_x), ty = (int32_t)(t / tl.tiles_x);
+            const int64_t e0 = tl.tile_start[t], e1 = tl.tile_start[t + 1];
+            int32_t px, py;
+
+            for(py = ty * tile; py < ty * tile + tile && py < k.height; ++py) {
+                for(px = tx * tile; px < tx * tile + tile && px < k.width; ++px) {
+                    size_t pix = (size_t)py * (size_t)k.width + (size_t)px;
+                    float cr = 0.0f, cg = 0.0f, cb = 0.0f, tt = 1.0f;
+                    int64_t e;
+
+                    for(e = e0; e < e1; ++e) {
+                        const vis *g = &tl.v[tl.entries[e]];
+                        const float *r = g->rec;
+                        float inv_a, inv_b, inv_c, dx, dy, power, alpha, wgt;
+
+                        if(tt < T_THRESHOLD) break;
+                        if(px < g->bb[0] || px > g->bb[1] || py < g->bb[2] || py > g->bb[3]) continue;
+                        inv_a = r[ORACLE_REC_COV_C] * r[ORACLE_REC_INV_DET];
+                        inv_b = -r[ORACLE_REC_COV_B] * r[ORACLE_REC_INV_DET];
+                        inv_c = r[ORACLE_REC_COV_A] * r[ORACLE_REC_INV_DET];
+                        dx = ((float)px + 0.5f) - r[ORACLE_REC_MEAN2D_X];
+                        dy = ((float)py + 0.5f) - r[ORACLE_REC_MEAN2D_Y];
+                        power = -0.5f * (inv_a * dx * dx + 2.0f * inv_b * dx * dy + inv_c * dy * dy);
+                        if(power > 0.0f) power = 0.0f;
+                        if(power < POWER_THRESHOLD) continue;
+                        alpha = fminf(MAX_FRAGMENT_ALPHA, r[ORACLE_REC_OPACITY] * expf(power));
+                        if(alpha < MIN_ALPHA) continue;
+                        wgt = alpha * tt;
+                        cr += wgt * r[ORACLE_REC_COLOR_R];
+                        cg += wgt * r[ORACLE_REC_COLOR_G];
+                        cb += wgt * r[ORACLE_REC_COLOR_B];
+                        tt = tt * (1.0f - alpha);
+                    }
+                    out_rgb[0 * pixels + pix] = cr + tt * k.bg[0];
+                    out_rgb[1 * pixels + pix] = cg + tt * k.bg[1];
+                    out_rgb[2 * pixels + pix] = cb + tt * k.bg[2];
+                    if(out_t != NULL) out_t[pix] = tt;
+                }
+            }
+        }
+    }
+    if(out_keys != NULL && out_values != NULL) {
+        *out_keys = (uint64_t *)malloc(sizeof(uint64_t) * (size_t)(total > 0 ? total : 1));
+        *out_values = (uint32_t *)malloc(sizeof(uint32_t) * (size_t)(total > 0 ? total : 1));
+        if(*out_keys == NULL || *out_values == NULL) {
+            free(*out_keys);
+            free(*out_values);
+            *out_keys = NULL;
+            *out_values = NULL;
+            tiled_free(&tl);
+            return -1;
+        }
+#pragma omp parallel for schedule(dynamic, 16)
+        for(t = 0; t < tiles; ++t) {
+            int64_t e;
+
+            for(e = tl.tile_start[t]; e < tl.tile_start[t + 1]; ++e) {
+                const vis *g = &tl.v[tl.entries[e]];
+
+                (*out_keys)[e] = ((uint64_t)t << 32) | (uint64_t)gsx_f32_bits(g->rec[ORACLE_REC_DEPTH]);
+                (*out_values)[e] = (uint32_t)g->g;
+            }
+        }
+    }
+    tiled_free(&tl);
+    return total;
+}
+
+void oracle_free(void *p) { free(p); }

@@ -80,6 +80,10 @@ class Oracle:
         lib.oracle_expf_mismatches.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32]
         lib.oracle_expf_blend_mismatches.restype = ctypes.c_uint64
         lib.oracle_expf_blend_mismatches.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32]
+        lib.oracle_tiled.restype = _i64
+        lib.oracle_tiled.argtypes = [_i64, ctypes.c_int] + [_vp] * 9 + [ctypes.c_int32, ctypes.c_int, _vp, _vp,
+                                                                         _vp, _vp]
+        lib.oracle_free.argtypes = [_vp]
         self.lib = lib
 
     # -- render -----------------------------------------------------------------------------
@@ -124,6 +128,41 @@ class Oracle:
                                             _p(out), _p(t), _p(visible_counter))
         assert rc == 0
         return out, t
+
+    def _tiled(self, scene, camera, cull, render, keys, tile=16):
+        w, h = int(camera[4]), int(camera[5])
+        out = np.zeros((3, h, w), np.float32) if render else None
+        t = np.zeros((h, w), np.float32) if render else None
+        kp, vp = _vp(), _vp()
+        r = self.lib.oracle_tiled(scene.count, scene.sh_degree, *self._scene_args(scene), _p(camera), tile,
+                                  1 if cull else 0, _p(out), _p(t), ctypes.byref(kp) if keys else None,
+                                  ctypes.byref(vp) if keys else None)
+        if r < 0:
+            raise MemoryError("oracle_tiled failed")
+        k = v = None
+        if keys:
+            try:
+                k = np.ctypeslib.as_array(ctypes.cast(kp, ctypes.POINTER(ctypes.c_uint64)), (max(r, 1),))[:r].copy()
+                v = np.ctypeslib.as_array(ctypes.cast(vp, ctypes.POINTER(ctypes.c_uint32)), (max(r, 1),))[:r].copy()
+            finally:
+                self.lib.oracle_free(kp)
+                self.lib.oracle_free(vp)
+        return out, t, k, v, r
+
+    def render_tiled(self, scene, camera, cull=True):
+        """Same pixels as render() (bit for bit), from per-tile lists walked per pixel on all
+        host cores; with cull, over the instances the tile test keeps."""
+        out, t, _, _, _ = self._tiled(scene, camera, cull, True, False)
+        return out, t
+
+    def tile_keys_tiled(self, scene, camera, tile=16):
+        """Same keys and values as tile_keys(), built per tile on all host cores."""
+        _, _, k, v, _ = self._tiled(scene, camera, True, False, True, tile)
+        return k, v
+
+    def render_and_keys_tiled(self, scene, camera):
+        out, t, k, v, _ = self._tiled(scene, camera, True, True, True)
+        return out, t, k, v
 
     def render_backward(self, scene, camera, grad_rgb):
         n = scene.count

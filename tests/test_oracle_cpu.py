@@ -350,3 +350,45 @@ def test_camera_look_at_convention():
     assert abs(abs(q[0]) - 1.0) < 1e-6 and np.allclose(q[1:], 0, atol=1e-6)
     assert np.allclose(pose[4:], (0, 0, 4), atol=1e-6)
     assert math.isclose(float(np.linalg.norm(scenes.orbit_pose(5)[:4])), 1.0, rel_tol=1e-6)
+
+
+@pytest.mark.parametrize("name,kw", [("config0", {}), ("config1", dict(n=60_000, width=640, height=360)),
+                                     ("config3", dict(n=80_000)), ("config4", dict(n=20_000, width=480, height=270)),
+                                     ("config2", dict(n=50_000, size=256))])
+def test_tiled_oracle_matches_serial(oracle, name, kw):
+    """The tiled full-scene paths (per-tile lists walked per pixel on all host cores) against
+    the serial restatement: pixels and final transmittance bit-exact with and without the tile
+    test, keys and values equal to oracle_tile_keys'."""
+    from gsx_amd import scenes
+    w = getattr(scenes, name)(**kw)
+    img, t = oracle.render(w.scene, w.camera)
+    for cull in (False, True):
+        img2, t2 = oracle.render_tiled(w.scene, w.camera, cull=cull)
+        assert np.array_equal(img, img2) and np.array_equal(t, t2), cull
+    k, v = oracle.tile_keys(w.scene, w.camera)
+    k2, v2 = oracle.tile_keys_tiled(w.scene, w.camera)
+    assert np.array_equal(k, k2) and np.array_equal(v, v2)
+    img3, t3, k3, v3 = oracle.render_and_keys_tiled(w.scene, w.camera)
+    assert np.array_equal(img3, img) and np.array_equal(k3, k)
+
+
+def test_tiled_oracle_sh3_and_empty(oracle):
+    from gsx_amd import scenes
+    w = scenes.config1(n=20_000, width=320, height=180)
+    sc = w.scene.copy()
+    rng = np.random.default_rng(5)
+    sc.sh_degree = 3
+    sc.sh1 = (0.2 * rng.standard_normal((sc.count, 3, 3))).astype(np.float32)
+    sc.sh2 = (0.2 * rng.standard_normal((sc.count, 5, 3))).astype(np.float32)
+    sc.sh3 = (0.2 * rng.standard_normal((sc.count, 7, 3))).astype(np.float32)
+    img, t = oracle.render(sc, w.camera)
+    img2, t2 = oracle.render_tiled(sc, w.camera)
+    assert np.array_equal(img, img2) and np.array_equal(t, t2)
+    empty = scenes.Scene(*(np.ascontiguousarray(a[:0]) for a in (sc.mean3d, sc.rotation, sc.logscale, sc.opacity,
+                                                                  sc.sh0)))
+    cam = w.camera.copy()
+    cam[15:18] = (0.1, 0.2, 0.3)
+    img_e, t_e = oracle.render_tiled(empty, cam)
+    assert np.array_equal(img_e, oracle.render(empty, cam)[0]) and np.all(t_e == 1.0)
+    k, v = oracle.tile_keys_tiled(empty, cam)
+    assert len(k) == 0 and len(v) == 0
