@@ -193,11 +193,11 @@ def main():
 
     ev = {k: [] for k in ("loss_forward", "loss_backward", "adam")}
 
-    def step(i, record=False):
+    def step(i, record=False, borrow=True):
         cam = cams[i % args.poses]
         tgt = targets[i % args.poses]
         st = stream_handle()
-        renderer.render(cam, g, train=True, out_rgb=img)
+        renderer.render(cam, g, train=True, out_rgb=img, borrow_train_state=borrow)
         loss_and_grad.zero_()
         e = [torch.cuda.Event(enable_timing=True) for _ in range(4)] if record else None
         if record:
@@ -246,23 +246,37 @@ def main():
 
     snapshot = [t.clone() for t in opt_state()]
     steps_before = [grp["step"] for grp in opt.groups]
+
+    def restore():
+        for t, saved in zip(opt_state(), snapshot):
+            t.copy_(saved)
+        for grp, k in zip(opt.groups, steps_before):
+            grp["step"] = k
+
+    def timed_pass(borrow):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(args.steps):
+            step(args.warmup + i, borrow=borrow)
+        torch.cuda.synchronize()
+        return time.perf_counter() - t0
+
     # 1. throughput: K steps with nothing but the work on the stream (the per-stage HIP events
-    #    of pass 2 cost about 45 us per step, so they stay out of this loop)
-    log(f"timing {args.steps} steps")
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        step(args.warmup + i)
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
+    #    of pass 3 cost about 45 us per step, so they stay out of this loop). The TRAIN state is
+    #    borrowed, as gsx's training session requests (apps/image_fit_demo.c:1305): the backward
+    #    checks the caller's arrays against the forward's copy before differentiating.
+    log(f"timing {args.steps} steps (borrowed train state)")
+    elapsed = timed_pass(True)
     it_s = args.steps / elapsed
-    # 2. per-kernel times: the same K steps from the same state, with HIP events at every stage
+    # 2. the same K steps from the same state with a cloned TRAIN state (borrow_train_state =
+    #    false, the zero-initialised request's choice): no check in the backward
+    restore()
+    log(f"timing {args.steps} steps (cloned train state)")
+    it_s_clone = args.steps / timed_pass(False)
+    # 3. per-kernel times: the same K steps from the same state, with HIP events at every stage
     #    boundary, recorded on the launch stream inside the library and around the loss and
     #    Adam launches here
-    for t, saved in zip(opt_state(), snapshot):
-        t.copy_(saved)
-    for grp, k in zip(opt.groups, steps_before):
-        grp["step"] = k
+    restore()
     del snapshot
     renderer.set_timing(args.steps)
     log(f"per-stage timing over the same {args.steps} steps")
@@ -336,6 +350,7 @@ def main():
                                "fwd+bwd+0.8*L1+0.2*(1-SSIM)+Adam",
                    "gaussians": args.gaussians, "width": W, "height": H, "poses": args.poses,
                    "instances_last_pose": instances, "visible_last_pose": visible},
+        "train_its_cloned_state": round(it_s_clone, 2),
         "render_fps": round(fps, 1),
         "sort_gbps": sort_entry["gbps"],
         "sort_hbm_frac": sort_entry["hbm_frac"],

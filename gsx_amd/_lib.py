@@ -23,6 +23,12 @@ class GsxHipError(RuntimeError):
     pass
 
 
+# forward types of gsx_hip_render_forward (include/gsx_hip.h)
+FORWARD_INFERENCE = 0
+FORWARD_TRAIN_BORROW = 1
+FORWARD_TRAIN_CLONE = 2
+
+
 class Camera(ctypes.Structure):
     _fields_ = [("fx", _f), ("fy", _f), ("cx", _f), ("cy", _f), ("width", _i32), ("height", _i32),
                 ("rot", _f * 4), ("transl", _f * 3), ("near_plane", _f), ("far_plane", _f), ("background", _f * 3)]

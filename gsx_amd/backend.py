@@ -104,13 +104,18 @@ class Renderer:
 
     def render(self, camera: Camera, gaussians: GaussianTensors, train: bool = False,
                out_rgb: torch.Tensor | None = None, visible_counter: torch.Tensor | None = None,
-               stream=None) -> torch.Tensor:
+               stream=None, borrow_train_state: bool = True) -> torch.Tensor:
+        """train=True is GSX_RENDER_FORWARD_TYPE_TRAIN. borrow_train_state (gsx-render.h:101): True
+        differentiates the backward at the values the Gaussian tensors hold when backward() is
+        called, False at the values of this forward."""
         if camera.width != self.width or camera.height != self.height:
             raise GsxHipError("intrinsics geometry must match the renderer output geometry")
         if out_rgb is None:
             out_rgb = torch.empty((3, self.height, self.width), dtype=torch.float32, device="cuda")
         g = gaussians.to_struct()
-        check(self.lib.gsx_hip_render_forward(self.handle, ctypes.byref(camera), ctypes.byref(g), 1 if train else 0,
+        mode = (_lib.FORWARD_TRAIN_BORROW if borrow_train_state else _lib.FORWARD_TRAIN_CLONE) if train else \
+            _lib.FORWARD_INFERENCE
+        check(self.lib.gsx_hip_render_forward(self.handle, ctypes.byref(camera), ctypes.byref(g), mode,
                                               ptr(out_rgb), ptr(visible_counter), stream_handle(stream)),
               "render forward")
         return out_rgb

@@ -34,6 +34,46 @@ __global__ __launch_bounds__(256) void copy_f32_kernel(const float4* __restrict_
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (int64_t)gridDim.x * blockDim.x)
         dst[i] = src[i];
 }
+
+// The Gaussian field arrays a TRAIN forward retains (gsx-cpu/render.c:263-380): up to 8 arrays
+// of floats, compared with the context's copy in one launch, blockIdx.y selecting the array.
+// 16-byte vectors where the caller's array and the copy are both 16-byte aligned.
+constexpr int kStateFields = 8;
+struct StateArrays {
+    const float* live[kStateFields];
+    float* snap[kStateFields];
+    int64_t count[kStateFields];  // floats
+};
+
+__device__ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// *changed = 1 when any bit of live differs from snap (a NaN payload or the sign of a zero
+// counts as a change, as any other write would).
+__global__ __launch_bounds__(256) void train_state_kernel(StateArrays a, uint32_t* __restrict__ changed) {
+    const int f = blockIdx.y;
+    const float* live = a.live[f];
+    const float* snap = a.snap[f];
+    const int64_t n = a.count[f];
+    if (live == nullptr || n == 0) return;  // uniform
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    bool diff = false;
+    if (aligned16(live) && aligned16(snap)) {
+        const int64_t n4 = n / 4;
+        const uint4* l4 = reinterpret_cast<const uint4*>(live);
+        const uint4* s4 = reinterpret_cast<const uint4*>(snap);
+        for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
+            const uint4 v = l4[i];
+            const uint4 w = s4[i];
+            diff |= (v.x != w.x) | (v.y != w.y) | (v.z != w.z) | (v.w != w.w);
+        }
+        for (int64_t i = n4 * 4 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+            diff |= __float_as_uint(live[i]) != __float_as_uint(snap[i]);
+    } else {
+        for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+            diff |= __float_as_uint(live[i]) != __float_as_uint(snap[i]);
+    }
+    if (wave_ballot(diff) != 0ull && __lane_id() == 0) *changed = 1u;
+}
 }  // namespace gsx_amd
 
 namespace {
@@ -214,6 +254,17 @@ struct gsx_hip_render_context {
     // big boxes: one u64 per workgroup), summed on the host after count_ev
     PinnedBuffer kept_parts;
     hipEvent_t count_ev = nullptr;
+    // Retained TRAIN state (gsx-cpu/render.c:263-380): the Gaussian fields as the forward read
+    // them, copied into `snap`, which the backward reads (gs points into it). A borrowed state
+    // also keeps the caller's arrays (`live`): the backward first compares them with `snap`
+    // (`changed`, host-mapped, read after state_ev) and, when the caller has changed them, re-runs
+    // the forward on their current values (into refresh_rgb), as gsx-cuda/render.c:662-756 does.
+    DeviceBuffer snap, refresh_rgb;
+    PinnedBuffer changed;
+    hipEvent_t state_ev = nullptr;
+    gsx_hip_gaussians live{};
+    gsx_hip_camera camera{};
+    int32_t train_mode = GSX_HIP_FORWARD_INFERENCE;
     // counters: [0] visible Gaussians (depth keys), [1] long instance runs, [2 + big_slot] big boxes
     // of the next forward (each forward's preprocess clears the other slot for its successor),
     // [4] runs of more than one long-run chunk
@@ -263,6 +314,55 @@ void release_events(gsx_hip_render_context* ctx) {
     ctx->has_fwd = nullptr;
     ctx->has_bwd = nullptr;
     ctx->ring = 0;
+}
+
+// Field order of the retained state: mean3d, rotation, logscale, opacity, sh0, sh1, sh2, sh3.
+constexpr int kFieldWidth[kStateFields] = {3, 4, 3, 1, 3, 9, 15, 21};
+
+const float* field_ptr(const gsx_hip_gaussians& g, int f) {
+    const float* p[kStateFields] = {g.mean3d, g.rotation, g.logscale, g.opacity, g.sh0, g.sh1, g.sh2, g.sh3};
+    return p[f];
+}
+
+int field_count(const gsx_hip_gaussians& g) { return 5 + g.sh_degree; }
+
+// Lays the snapshot of g out in one buffer (each array 64-byte aligned) and points `snap_gs` at it.
+gsx_hip_status snapshot_layout(gsx_hip_render_context* ctx, const gsx_hip_gaussians& g, gsx_hip_gaussians* snap_gs,
+                               StateArrays* arrays) {
+    size_t off[kStateFields] = {};
+    size_t total = 0;
+    const size_t n = (size_t)g.count;
+    for (int f = 0; f < field_count(g); ++f) {
+        off[f] = total;
+        total += (n * (size_t)kFieldWidth[f] + 15u) / 16u * 16u;
+    }
+    GSX_TRY(ctx->snap.reserve((total > 0 ? total : 1) * sizeof(float), "train state snapshot"));
+    float* base = ctx->snap.as<float>();
+    float* fp[kStateFields] = {};
+    *arrays = StateArrays{};
+    for (int f = 0; f < kStateFields; ++f) {
+        const bool used = f < field_count(g);
+        fp[f] = used ? base + off[f] : nullptr;
+        arrays->live[f] = used ? field_ptr(g, f) : nullptr;
+        arrays->snap[f] = fp[f];
+        arrays->count[f] = used ? (int64_t)(n * (size_t)kFieldWidth[f]) : 0;
+    }
+    *snap_gs = g;
+    snap_gs->mean3d = fp[0];
+    snap_gs->rotation = fp[1];
+    snap_gs->logscale = fp[2];
+    snap_gs->opacity = fp[3];
+    snap_gs->sh0 = fp[4];
+    snap_gs->sh1 = fp[5];
+    snap_gs->sh2 = fp[6];
+    snap_gs->sh3 = fp[7];
+    return GSX_HIP_SUCCESS;
+}
+
+unsigned state_blocks(int64_t n) {
+    // enough workgroups per array to fill the GPU, capped for small sets
+    const int64_t b = (n * 3 + 1023) / 1024;
+    return (unsigned)std::min<int64_t>(std::max<int64_t>(b, 1), 1024);
 }
 
 gsx_hip_status validate_gaussians(const gsx_hip_gaussians* g) {
@@ -380,6 +480,7 @@ gsx_hip_status gsx_hip_render_context_create(gsx_hip_render_context** out_contex
     gsx_hip_render_context* ctx = new (std::nothrow) gsx_hip_render_context();
     if (ctx == nullptr) return fail(GSX_HIP_ERROR_OUT_OF_MEMORY, "render context allocation failed");
     hipError_t e = hipEventCreateWithFlags(&ctx->count_ev, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->state_ev, hipEventDisableTiming);
     if (e != hipSuccess) {
         (void)gsx_hip_render_context_destroy(ctx);
         return hip_fail(e, "render context creation");
@@ -396,10 +497,12 @@ gsx_hip_status gsx_hip_render_context_destroy(gsx_hip_render_context* ctx) {
                            &ctx->sorted_g,   &ctx->final_t,  &ctx->last,      &ctx->grad2d,     &ctx->depth_keys,
                            &ctx->depth_keys_alt, &ctx->rank_g, &ctx->rank_count, &ctx->g_rank,
                            &ctx->long_list, &ctx->multi_list, &ctx->counters, &ctx->big_chunk_counts,
-                           &ctx->depth_sort_temp};
+                           &ctx->depth_sort_temp, &ctx->snap, &ctx->refresh_rgb};
     for (DeviceBuffer* b : all) b->release();
     ctx->kept_parts.release();
+    ctx->changed.release();
     if (ctx->count_ev != nullptr) (void)hipEventDestroy(ctx->count_ev);
+    if (ctx->state_ev != nullptr) (void)hipEventDestroy(ctx->state_ev);
     release_events(ctx);
     delete ctx;
     return GSX_HIP_SUCCESS;
@@ -490,6 +593,10 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     if (!(camera->near_plane > 0.0f) || !(camera->far_plane > camera->near_plane) || !isfinite(camera->far_plane)) {
         return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "near_plane and far_plane must be finite with 0 < near < far");
     }
+    if (train != GSX_HIP_FORWARD_INFERENCE && train != GSX_HIP_FORWARD_TRAIN_BORROW &&
+        train != GSX_HIP_FORWARD_TRAIN_CLONE) {
+        return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "forward type must be a GSX_HIP_FORWARD_* value");
+    }
     ctx->has_train_state = false;
     const CameraParams cam = make_camera_params(*camera);
     const int64_t n = gaussians->count;
@@ -497,7 +604,7 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     const int64_t pixels = (int64_t)cam.width * cam.height;
     const int tile_bits = bits_for((uint32_t)(tiles > 0 ? tiles - 1 : 0));
     ctx->cam = cam;
-    ctx->gs = *gaussians;
+    ctx->gs = *gaussians;  // replaced by the snapshot below for a TRAIN forward
     ctx->gaussian_count = n;
     ctx->tile_count_total = tiles;
 
@@ -550,13 +657,25 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
         ctx->has_bwd[ctx->cur] = 0;
     }
     GSX_TRY(record(ctx, 0, stream));
+    FieldSnapshot snap{};
+    if (train) {
+        // the retained state: preprocess copies the fields as it reads them
+        gsx_hip_gaussians snap_gs;
+        StateArrays arrays;
+        GSX_TRY(snapshot_layout(ctx, *gaussians, &snap_gs, &arrays));
+        for (int f = 0; f < kStateFields; ++f) snap.dst[f] = arrays.snap[f];
+        ctx->gs = snap_gs;
+        ctx->live = *gaussians;
+        ctx->camera = *camera;
+    }
+    ctx->train_mode = train;
     if (n > 0) {
         if (!ctx->counters_ready) {
             hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(64), 0, stream, counters, (int64_t)8, 0u);
             GSX_HIP_TRY(hipGetLastError(), "fill_u32_kernel");
             ctx->counters_ready = true;
         }
-        hipLaunchKernelGGL(preprocess_kernel, dim3(pre_blocks), dim3(256), 0, stream, n, gaussians->mean3d,
+        hipLaunchKernelGGL(preprocess_kernel, dim3(pre_blocks), dim3(256), 0, stream, snap, n, gaussians->mean3d,
                            gaussians->rotation, gaussians->logscale, gaussians->opacity, gaussians->sh0,
                            gaussians->sh1, gaussians->sh2, gaussians->sh3, (int)gaussians->sh_degree, cam,
                            ctx->rec.as<float4>(), train ? ctx->cov_coef.as<float4>() : nullptr,
@@ -682,27 +801,15 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     return GSX_HIP_SUCCESS;
 }
 
-gsx_hip_status gsx_hip_render_backward(gsx_hip_render_context* ctx, const float* grad_rgb,
-                                       const gsx_hip_gaussian_grads* grads, hipStream_t stream) {
-    if (ctx == nullptr || grad_rgb == nullptr || grads == nullptr) {
-        return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "context, grad_rgb and grads must be non-null");
-    }
-    if (!ctx->has_train_state) {
-        return fail(GSX_HIP_ERROR_INVALID_STATE, "backward requires a retained TRAIN forward on the same context");
-    }
+}  // extern "C"
+
+namespace {
+
+// The backward's launches for the retained state (inputs validated by the caller).
+gsx_hip_status enqueue_backward(gsx_hip_render_context* ctx, const float* grad_rgb,
+                                const gsx_hip_gaussian_grads* grads, hipStream_t stream) {
     const int64_t n = ctx->gaussian_count;
     const gsx_hip_gaussians& gs = ctx->gs;
-    if (n > 0 && (grads->mean3d == nullptr || grads->rotation == nullptr || grads->logscale == nullptr ||
-                  grads->opacity == nullptr || grads->sh0 == nullptr)) {
-        return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "gradient sinks mean3d..sh0 must be non-null");
-    }
-    if ((gs.sh_degree >= 1 && grads->sh1 == nullptr) || (gs.sh_degree >= 2 && grads->sh2 == nullptr) ||
-        (gs.sh_degree >= 3 && grads->sh3 == nullptr)) {
-        return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "sh gradient sinks must be non-null up to sh_degree");
-    }
-    if ((reinterpret_cast<uintptr_t>(grads->rotation) & 15u) != 0) {
-        return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "rotation gradient must be 16-byte aligned");
-    }
     GSX_TRY(ctx->grad2d.reserve((size_t)(n > 0 ? n : 1) * 9 * sizeof(float), "grad2d"));
     GSX_TRY(ctx->inst_grad.reserve((size_t)(ctx->instance_count > 0 ? ctx->instance_count : 1) * 9 * sizeof(float),
                                    "instance_grad"));
@@ -751,6 +858,74 @@ gsx_hip_status gsx_hip_render_backward(gsx_hip_render_context* ctx, const float*
     }
     GSX_TRY(record(ctx, 10, stream));
     if (ctx->timing && ctx->cur >= 0) ctx->has_bwd[ctx->cur] = 1;
+    return GSX_HIP_SUCCESS;
+}
+
+}  // namespace
+
+extern "C" {
+
+gsx_hip_status gsx_hip_render_backward(gsx_hip_render_context* ctx, const float* grad_rgb,
+                                       const gsx_hip_gaussian_grads* grads, hipStream_t stream) {
+    if (ctx == nullptr || grad_rgb == nullptr || grads == nullptr) {
+        return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "context, grad_rgb and grads must be non-null");
+    }
+    if (!ctx->has_train_state) {
+        return fail(GSX_HIP_ERROR_INVALID_STATE, "backward requires a retained TRAIN forward on the same context");
+    }
+    const int64_t n = ctx->gaussian_count;
+    const gsx_hip_gaussians& gs = ctx->gs;
+    if (n > 0 && (grads->mean3d == nullptr || grads->rotation == nullptr || grads->logscale == nullptr ||
+                  grads->opacity == nullptr || grads->sh0 == nullptr)) {
+        return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "gradient sinks mean3d..sh0 must be non-null");
+    }
+    if ((gs.sh_degree >= 1 && grads->sh1 == nullptr) || (gs.sh_degree >= 2 && grads->sh2 == nullptr) ||
+        (gs.sh_degree >= 3 && grads->sh3 == nullptr)) {
+        return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "sh gradient sinks must be non-null up to sh_degree");
+    }
+    if ((reinterpret_cast<uintptr_t>(grads->rotation) & 15u) != 0) {
+        return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "rotation gradient must be 16-byte aligned");
+    }
+    if (ctx->train_mode == GSX_HIP_FORWARD_TRAIN_BORROW && n > 0) {
+        // borrowed state: the gradient is taken at the values the caller's arrays hold now. The
+        // comparison with the retained copy is queued first and the backward right behind it, so
+        // the GPU does not wait for the host's look at the result; the backward writes only the
+        // context's scratch and the sinks, which a refresh overwrites.
+        GSX_TRY(ctx->changed.reserve(sizeof(uint32_t), "train state flag"));
+        volatile uint32_t* changed = static_cast<volatile uint32_t*>(ctx->changed.host);
+        *changed = 0u;
+        StateArrays arrays{};
+        for (int f = 0; f < field_count(ctx->live); ++f) {
+            arrays.live[f] = field_ptr(ctx->live, f);
+            arrays.snap[f] = const_cast<float*>(field_ptr(ctx->gs, f));
+            arrays.count[f] = n * kFieldWidth[f];
+        }
+        hipLaunchKernelGGL(train_state_kernel, dim3(state_blocks(n), (unsigned)field_count(ctx->live)), dim3(256), 0,
+                           stream, arrays, static_cast<uint32_t*>(ctx->changed.dev));
+        GSX_HIP_TRY(hipGetLastError(), "train_state_kernel");
+        GSX_HIP_TRY(hipEventRecord(ctx->state_ev, stream), "hipEventRecord(state)");
+        GSX_TRY(enqueue_backward(ctx, grad_rgb, grads, stream));
+        GSX_HIP_TRY(hipEventSynchronize(ctx->state_ev), "train state sync");
+        if (*changed != 0u) {
+            // the caller changed its arrays: re-run the TRAIN forward on the current values (its
+            // image is not returned), then the backward again. The queued backward must finish
+            // first: the refresh may regrow the buffers it reads.
+            GSX_HIP_TRY(hipStreamSynchronize(stream), "train state refresh sync");
+            const bool timing = ctx->timing;
+            const gsx_hip_gaussians live = ctx->live;
+            const gsx_hip_camera camera = ctx->camera;
+            GSX_TRY(ctx->refresh_rgb.reserve((size_t)3 * camera.width * camera.height * sizeof(float),
+                                             "refresh image"));
+            ctx->timing = false;
+            const gsx_hip_status st = gsx_hip_render_forward(ctx, &camera, &live, GSX_HIP_FORWARD_TRAIN_BORROW,
+                                                             ctx->refresh_rgb.as<float>(), nullptr, stream);
+            ctx->timing = timing;
+            if (st != GSX_HIP_SUCCESS) return st;
+            GSX_TRY(enqueue_backward(ctx, grad_rgb, grads, stream));
+        }
+    } else {
+        GSX_TRY(enqueue_backward(ctx, grad_rgb, grads, stream));
+    }
     ctx->has_train_state = false;
     return GSX_HIP_SUCCESS;
 }

@@ -494,11 +494,12 @@ __device__ inline uint32_t digit_of(uint64_t key, int shift) {
 // Upsweep of one kChunk-key chunk (workgroup `blk` of kSortThreads threads): its digit counts,
 // counted in wave-private LDS counters, to hist[digit][blk]. n_dev (may be null): live key
 // count, n = min(n, *n_dev); drop_sentinel: keys equal to kSentinelKey are not counted.
+// dmask keeps the digit's bits below the sort's end bit (a last pass narrower than kBits).
 template <int kBits, int kChunk>
 __device__ inline void radix_upsweep_block(uint32_t blk, const uint64_t* __restrict__ keys, int64_t n,
                                            const uint32_t* __restrict__ n_dev, bool drop_sentinel, int shift,
                                            int64_t num_chunks, uint32_t* __restrict__ hist,
-                                           uint32_t (*s_hist)[1 << kBits]) {
+                                           uint32_t (*s_hist)[1 << kBits], uint32_t dmask = (1u << kBits) - 1u) {
     constexpr int kBins = 1 << kBits;
     if (n_dev != nullptr) n = min(n, (int64_t)*n_dev);
     const int wave = threadIdx.x / kWave;
@@ -516,7 +517,7 @@ __device__ inline void radix_upsweep_block(uint32_t blk, const uint64_t* __restr
         for (int r = 0; r < kRounds; ++r) {
             const int64_t i = base + (int64_t)r * kSortThreads + threadIdx.x;
             if (i < n && (!drop_sentinel || k[r] != kSentinelKey))
-                atomicAdd(&s_hist[wave][digit_of<kBits>(k[r], shift)], 1u);
+                atomicAdd(&s_hist[wave][digit_of<kBits>(k[r], shift) & dmask], 1u);
         }
     }
     __syncthreads();

@@ -196,8 +196,18 @@ __device__ inline void walk_wave_tiles(WaveBoxes& w, uint32_t wave_total, int32_
     }
 }
 
+// Destination of the retained TRAIN state: each field array copied as the forward reads it
+// (null dst[0] in an inference forward). Field order mean3d, rotation, logscale, opacity, sh0..sh3.
+struct FieldSnapshot {
+    float* dst[8];
+};
+
+__device__ inline void copy_floats(const float* __restrict__ src, float* __restrict__ dst, int64_t g, int width) {
+    for (int k = 0; k < width; ++k) dst[g * width + k] = src[g * width + k];
+}
+
 __global__ __launch_bounds__(256) void preprocess_kernel(
-    int64_t n, const float* __restrict__ mean3d, const float* __restrict__ rotation,
+    FieldSnapshot snap, int64_t n, const float* __restrict__ mean3d, const float* __restrict__ rotation,
     const float* __restrict__ logscale, const float* __restrict__ opacity, const float* __restrict__ sh0,
     const float* __restrict__ sh1, const float* __restrict__ sh2, const float* __restrict__ sh3, int sh_degree,
     CameraParams cam, float4* __restrict__ rec, float4* __restrict__ cov_coef, uint32_t* __restrict__ tile_count,
@@ -215,6 +225,17 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
         *clear0 = 0u;
         *clear1 = 0u;
         *clear2 = 0u;
+    }
+    if (snap.dst[0] != nullptr && g < n) {
+        // consecutive lanes copy consecutive rows; preprocess_one then reads them from cache
+        copy_floats(mean3d, snap.dst[0], g, 3);
+        reinterpret_cast<float4*>(snap.dst[1])[g] = reinterpret_cast<const float4*>(rotation)[g];
+        copy_floats(logscale, snap.dst[2], g, 3);
+        snap.dst[3][g] = opacity[g];
+        copy_floats(sh0, snap.dst[4], g, 3);
+        if (sh_degree >= 1) copy_floats(sh1, snap.dst[5], g, 9);
+        if (sh_degree >= 2) copy_floats(sh2, snap.dst[6], g, 15);
+        if (sh_degree >= 3) copy_floats(sh3, snap.dst[7], g, 21);
     }
     bool visible = false;
     float4 r0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), r1 = r0, r2 = r0;

@@ -115,10 +115,11 @@ template <int kBits, int kChunk>
 __global__ __launch_bounds__(kSortThreads) void radix_upsweep_kernel(const uint64_t* __restrict__ keys, int64_t n,
                                                                      const uint32_t* __restrict__ n_dev,
                                                                      bool drop_sentinel, int shift,
-                                                                     int64_t num_chunks,
+                                                                     uint32_t dmask, int64_t num_chunks,
                                                                      uint32_t* __restrict__ hist) {
     __shared__ uint32_t s_hist[kChunkWaves][1 << kBits];
-    radix_upsweep_block<kBits, kChunk>(blockIdx.x, keys, n, n_dev, drop_sentinel, shift, num_chunks, hist, s_hist);
+    radix_upsweep_block<kBits, kChunk>(blockIdx.x, keys, n, n_dev, drop_sentinel, shift, num_chunks, hist, s_hist,
+                                       dmask);
 }
 
 // Workgroup d: exclusive scan of hist[d][0..num_chunks) into offsets[d][..], row total into
@@ -187,7 +188,7 @@ __device__ inline uint32_t digit_exclusive_scan(uint32_t v, uint32_t* s_wave, ui
 template <bool kPairs, int kBits, int kChunk>
 __global__ __launch_bounds__(kDownThreads) void radix_downsweep_kernel(
     const uint64_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, int64_t n,
-    const uint32_t* __restrict__ n_dev, bool drop_sentinel, int shift, int64_t num_chunks,
+    const uint32_t* __restrict__ n_dev, bool drop_sentinel, int shift, uint32_t dmask, int64_t num_chunks,
     const uint32_t* __restrict__ offsets, const uint32_t* __restrict__ totals, uint64_t* __restrict__ keys_out,
     uint32_t* __restrict__ vals_out, uint32_t* __restrict__ kept_total) {
     constexpr int kDownWaveKeys = kChunk / kDownWaves;  // keys ranked by one wave
@@ -232,7 +233,7 @@ __global__ __launch_bounds__(kDownThreads) void radix_downsweep_kernel(
     for (int r = 0; r < kDownRounds; ++r) {
         const int local = wave * kDownWaveKeys + r * kWave + lane;
         const bool valid = local < chunk_count && !(drop_sentinel && key[r] == kSentinelKey);
-        const uint32_t d = digit_of<kBits>(key[r], shift);
+        const uint32_t d = digit_of<kBits>(key[r], shift) & dmask;
         uint64_t peers = wave_ballot(valid);
 #pragma unroll
         for (int b = 0; b < kBits; ++b) {
@@ -290,7 +291,7 @@ __global__ __launch_bounds__(kDownThreads) void radix_downsweep_kernel(
     const int kept_count = (int)s_kept;
     for (int i = threadIdx.x; i < kept_count; i += kDownThreads) {
         const uint64_t k = s_keys[i];
-        const uint32_t d = digit_of<kBits>(k, shift);
+        const uint32_t d = digit_of<kBits>(k, shift) & dmask;
         const uint32_t pos = s_global[d] + ((uint32_t)i - s_local[d]);
         keys_out[pos] = k;
         if (kPairs) vals_out[pos] = s_vals[i];
@@ -322,6 +323,8 @@ gsx_hip_status radix_sort_u64(uint64_t* keys, uint32_t* vals, uint64_t* keys_alt
     constexpr int kBins = 1 << kBits;
     if (begin_bit < 0 || end_bit > 64 || begin_bit > end_bit) return GSX_HIP_ERROR_INVALID_ARGUMENT;
     if (n > (int64_t)UINT32_MAX) return GSX_HIP_ERROR_OUT_OF_RANGE;
+    // precounted first-pass digits are full kBits digits
+    if (first_hist_ready && end_bit - begin_bit < kBits) return GSX_HIP_ERROR_INVALID_ARGUMENT;
     int64_t chunks = (n + kChunk - 1) / kChunk;
     if (chunks < 1) chunks = 1;
     const int64_t hist_count = chunks * kBins;
@@ -337,14 +340,17 @@ gsx_hip_status radix_sort_u64(uint64_t* keys, uint32_t* vals, uint64_t* keys_alt
             uint32_t* vout = in_alt ? vals : vals_alt;
             const bool drop = compact_first && shift == begin_bit;
             const uint32_t* live = drop ? nullptr : n_dev;
+            // the last pass may be narrower than kBits: bits at and above end_bit do not sort
+            const int width = end_bit - shift < kBits ? end_bit - shift : kBits;
+            const uint32_t dmask = (1u << width) - 1u;
             if (!(first_hist_ready && shift == begin_bit))
-            hipLaunchKernelGGL((radix_upsweep_kernel<kBits, kChunk>), dim3((unsigned)chunks), dim3(kSortThreads), 0, stream, kin,
-                               n, live, drop, shift, chunks, hist);
+                hipLaunchKernelGGL((radix_upsweep_kernel<kBits, kChunk>), dim3((unsigned)chunks), dim3(kSortThreads),
+                                   0, stream, kin, n, live, drop, shift, dmask, chunks, hist);
             hipLaunchKernelGGL(radix_rowscan_kernel, dim3(kBins), dim3(kSortThreads), 0, stream, hist, chunks,
                                offsets, totals);
             hipLaunchKernelGGL((radix_downsweep_kernel<kPairs, kBits, kChunk>), dim3((unsigned)chunks),
-                               dim3(kDownThreads), 0, stream, kin, vin, n, live, drop, shift, chunks, offsets, totals,
-                               kout, vout, drop ? n_dev : nullptr);
+                               dim3(kDownThreads), 0, stream, kin, vin, n, live, drop, shift, dmask, chunks, offsets,
+                               totals, kout, vout, drop ? n_dev : nullptr);
             in_alt ^= 1;
         }
     }

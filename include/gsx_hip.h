@@ -130,19 +130,35 @@ typedef struct gsx_hip_render_buffers {
 gsx_hip_status gsx_hip_render_context_create(gsx_hip_render_context** out_context);
 gsx_hip_status gsx_hip_render_context_destroy(gsx_hip_render_context* context);
 
-/* Forward render into out_rgb [3,H,W]. train != 0 retains the state for one backward and, if
- * visible_counter is non-null, adds 1 to it for every visible Gaussian (gsx-cpu/render.c:
- * 980-982). The Gaussian arrays are borrowed: the backward reads them again, so they must be
- * unchanged until then (gsx borrow_train_state = true). One host synchronisation per forward
- * reads the instance count (the GPU keeps working on the depth order meanwhile); a count above
- * 2^32 - 1 (tile, Gaussian) instances fails with GSX_HIP_ERROR_OUT_OF_RANGE before anything is
- * emitted. */
+/* Forward types (gsx_render_forward_type and borrow_train_state of gsx_render_forward_request,
+ * gsx/include/gsx/gsx-render.h:54-58, 101; semantics of gsx/src/gsx-cpu/render.c:263-380,
+ * 1406-1440 and gsx/src/gsx-cuda/render.c:551, 662-756). METRIC is not supported (the CPU
+ * backend rejects it too, gsx-cpu/render.c:1126-1154). */
+enum {
+    GSX_HIP_FORWARD_INFERENCE = 0,    /* image only; no state retained */
+    GSX_HIP_FORWARD_TRAIN_BORROW = 1, /* borrow_train_state = true: the backward differentiates at
+                                         the values the Gaussian arrays hold when it is called */
+    GSX_HIP_FORWARD_TRAIN_CLONE = 2   /* borrow_train_state = false: the backward differentiates at
+                                         the values of this forward, whatever the caller changes */
+};
+
+/* Forward render into out_rgb [3,H,W]. forward_type is a GSX_HIP_FORWARD_* value. A TRAIN forward
+ * retains the state for one backward: it copies the Gaussian fields it reads into the context
+ * (56 B per Gaussian at SH degree 0, 236 B at degree 3), and, if visible_counter is non-null,
+ * adds 1 to it for every visible Gaussian (gsx-cpu/render.c:980-982). The Gaussian arrays are
+ * borrowed for the call. One host synchronisation per forward reads the instance count (the GPU
+ * keeps working on the depth order meanwhile); a count above 2^32 - 1 (tile, Gaussian)
+ * instances fails with GSX_HIP_ERROR_OUT_OF_RANGE before anything is emitted. */
 gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* context, const gsx_hip_camera* camera,
-                                      const gsx_hip_gaussians* gaussians, int32_t train, float* out_rgb,
+                                      const gsx_hip_gaussians* gaussians, int32_t forward_type, float* out_rgb,
                                       float* visible_counter, hipStream_t stream);
 
 /* Backward of the retained TRAIN forward; consumes the state (a second call fails with
- * GSX_HIP_ERROR_INVALID_STATE, as gsx-cpu/render.c:1406-1408, 1973). */
+ * GSX_HIP_ERROR_INVALID_STATE, as gsx-cpu/render.c:1406-1408, 1973). After a TRAIN_BORROW forward
+ * it first compares the caller's Gaussian arrays with the retained copy (one read of both and one
+ * host synchronisation) and, if any bit changed, re-runs the forward on the current values before
+ * differentiating (the reference CUDA backend re-runs it unconditionally,
+ * gsx-cuda/render.c:1451). */
 gsx_hip_status gsx_hip_render_backward(gsx_hip_render_context* context, const float* grad_rgb,
                                        const gsx_hip_gaussian_grads* grads, hipStream_t stream);
 

@@ -183,6 +183,39 @@ def test_radix_sort_keys_stable(n, lo, hi):
     assert np.array_equal(ko, keys[order])
 
 
+@pytest.mark.parametrize("n,lo,hi,pairs", [(5000, 4, 16, True), (70_001, 4, 16, False), (9000, 7, 10, True),
+                                           (40_000, 0, 21, False), (12_345, 30, 35, True)])
+def test_radix_sort_partial_digit_span(n, lo, hi, pairs):
+    """A span that is not a whole number of 8-bit digits, with random bits above end_bit and
+    below begin_bit: only bits [lo, hi) decide the order (a stable sort by them), all other bits
+    travel with the key."""
+    from gsx_amd import _lib
+    lib = _lib.load()
+    rng = np.random.default_rng(n + hi)
+    keys = rng.integers(0, 1 << 62, size=n, dtype=np.uint64) | (rng.integers(0, 2, size=n, dtype=np.uint64) << 63)
+    vals = np.arange(n, dtype=np.uint32)
+    k = torch.from_numpy(keys.view(np.int64).copy()).cuda()
+    v = torch.from_numpy(vals.view(np.int32).copy()).cuda()
+    k2, v2 = torch.empty_like(k), torch.empty_like(v)
+    temp = torch.empty(lib.gsx_hip_radix_sort_temp_bytes(n), dtype=torch.uint8, device="cuda")
+    in_alt = ctypes.c_int(0)
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    print(f"[case] partial-digit sort n={n} bits=[{lo},{hi}) pairs={pairs}", flush=True)
+    if pairs:
+        _lib.check(lib.gsx_hip_radix_sort_pairs_u64(k.data_ptr(), v.data_ptr(), k2.data_ptr(), v2.data_ptr(), n, lo,
+                                                    hi, temp.data_ptr(), ctypes.byref(in_alt), s))
+    else:
+        _lib.check(lib.gsx_hip_radix_sort_keys_u64(k.data_ptr(), k2.data_ptr(), n, lo, hi, temp.data_ptr(),
+                                                   ctypes.byref(in_alt), s))
+    torch.cuda.synchronize()
+    ko = (k2 if in_alt.value else k).cpu().numpy().view(np.uint64)
+    order = np.argsort((keys >> np.uint64(lo)) & np.uint64((1 << (hi - lo)) - 1), kind="stable")
+    assert np.array_equal(ko, keys[order])
+    if pairs:
+        vo = (v2 if in_alt.value else v).cpu().numpy().view(np.uint32)
+        assert np.array_equal(vo, vals[order])
+
+
 def test_scan_exclusive():
     from gsx_amd import _lib
     lib = _lib.load()

@@ -127,11 +127,83 @@ def test_backward_gradients(oracle, name):
         t.fill_(123.0)  # sinks are overwritten, not accumulated
     r.backward(torch.from_numpy(grad_rgb).cuda(), grads)
     torch.cuda.synchronize()
+    # the TRAIN forward's image (it also writes the backward's state) equals the oracle's
+    assert np.array_equal(img.cpu().numpy(), oracle.render(w.scene, w.camera)[0])
     ref = oracle.render_backward(w.scene, w.camera, grad_rgb)
     for field in ("mean3d", "rotation", "logscale", "opacity", "sh0"):
         err = _rel_l2(getattr(grads, field).cpu().numpy(), ref[field])
         assert err <= GRAD_TOL, f"{field}: relative L2 {err:.3e}"
-    del img
+
+
+def _mutated(scene, seed):
+    sc = scene.copy()
+    rng = np.random.default_rng(seed)
+    sc.mean3d += (0.02 * rng.standard_normal(sc.mean3d.shape)).astype(np.float32)
+    sc.logscale += (0.1 * rng.standard_normal(sc.logscale.shape)).astype(np.float32)
+    sc.sh0 += (0.2 * rng.standard_normal(sc.sh0.shape)).astype(np.float32)
+    sc.opacity -= np.float32(0.4)
+    return sc
+
+
+def _train_step_grads(r, cam, g, grad_rgb, borrow, mutate_to=None):
+    from gsx_amd.backend import GaussianTensors
+    r.render(cam, g, train=True, borrow_train_state=borrow)
+    if mutate_to is not None:
+        src = GaussianTensors.from_scene(mutate_to)
+        for name in ("mean3d", "logscale", "sh0", "opacity"):
+            getattr(g, name).copy_(getattr(src, name))
+    grads = g.zeros_like_grads()
+    r.backward(grad_rgb, grads)
+    torch.cuda.synchronize()
+    return {k: getattr(grads, k).cpu().numpy() for k in ("mean3d", "rotation", "logscale", "opacity", "sh0")}
+
+
+@pytest.mark.parametrize("name", ["c0_small", "c3_1080"])
+def test_borrowed_train_state_tracks_input_mutations(oracle, name):
+    """tests/render_runtime.cpp:743-810: after a TRAIN forward with a borrowed state, the caller
+    overwrites mean3d, logscale, sh0 and opacity; the backward's gradients are those of a fresh
+    forward + backward at the new values."""
+    from gsx_amd.backend import GaussianTensors
+    w = _workloads()[name]()
+    print(f"[case] borrowed state {name}", flush=True)
+    mut = _mutated(w.scene, 21)
+    r, cam, g = _setup(w)
+    rng = np.random.default_rng(8)
+    grad_np = rng.standard_normal((3, cam.height, cam.width)).astype(np.float32)
+    grad_rgb = torch.from_numpy(grad_np).cuda()
+    got = _train_step_grads(r, cam, g, grad_rgb, borrow=True, mutate_to=mut)
+    r2, _, _ = _setup(w)
+    expect = _train_step_grads(r2, cam, GaussianTensors.from_scene(mut), grad_rgb, borrow=False)
+    for k in got:
+        assert np.array_equal(got[k], expect[k]), k
+    ref = oracle.render_backward(mut, w.camera, grad_np)
+    for k in got:
+        assert _rel_l2(got[k], ref[k]) <= GRAD_TOL, k
+    # the context keeps working: an unchanged borrowed step next
+    g2 = GaussianTensors.from_scene(mut)
+    again = _train_step_grads(r, cam, g2, grad_rgb, borrow=True)
+    for k in got:
+        assert np.array_equal(again[k], expect[k]), k
+
+
+def test_cloned_train_state_ignores_input_mutations(oracle):
+    """borrow_train_state = false: the backward differentiates at the forward's values even when
+    the caller changes its arrays in between (gsx-cpu/render.c:286-360 clones them)."""
+    from gsx_amd.backend import GaussianTensors
+    w = _workloads()["c1_small"]()
+    r, cam, g = _setup(w)
+    rng = np.random.default_rng(9)
+    grad_np = rng.standard_normal((3, cam.height, cam.width)).astype(np.float32)
+    grad_rgb = torch.from_numpy(grad_np).cuda()
+    got = _train_step_grads(r, cam, g, grad_rgb, borrow=False, mutate_to=_mutated(w.scene, 22))
+    r2, _, g_fresh = _setup(w)
+    expect = _train_step_grads(r2, cam, g_fresh, grad_rgb, borrow=True)
+    for k in got:
+        assert np.array_equal(got[k], expect[k]), k
+    ref = oracle.render_backward(w.scene, w.camera, grad_np)
+    for k in got:
+        assert _rel_l2(got[k], ref[k]) <= GRAD_TOL, k
+    assert not np.array_equal(g.mean3d.cpu().numpy(), w.scene.mean3d)  # the caller's change stands
 
 
 def test_visible_counter_train_forward(oracle):
