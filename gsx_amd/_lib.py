@@ -23,6 +23,13 @@ class GsxHipError(RuntimeError):
     pass
 
 
+# status codes (include/gsx_hip.h)
+ERROR_INVALID_ARGUMENT = -1
+ERROR_INVALID_STATE = -2
+ERROR_OUT_OF_RANGE = -3
+ERROR_OUT_OF_MEMORY = -4
+ERROR_NOT_SUPPORTED = -5
+
 # forward types of gsx_hip_render_forward (include/gsx_hip.h)
 FORWARD_INFERENCE = 0
 FORWARD_TRAIN_BORROW = 1
@@ -118,6 +125,7 @@ SIGNATURES = {
     "gsx_hip_render_context_get_timings": (_st, [_vp, ctypes.POINTER(_f), _i32, ctypes.POINTER(_i32)]),
     "gsx_hip_scan_temp_bytes": (ctypes.c_size_t, [_i64]),
     "gsx_hip_scan_exclusive_u32": (_st, [_vp, _vp, _i64, _vp, _vp]),
+    "gsx_hip_scan_exclusive_u32_noalloc": (_st, [_vp, _vp, _i64, _vp]),
     "gsx_hip_radix_sort_temp_bytes": (ctypes.c_size_t, [_i64]),
     "gsx_hip_radix_sort_pairs_u64": (_st, [_vp, _vp, _vp, _vp, _i64, ctypes.c_int, ctypes.c_int, _vp,
                                            ctypes.POINTER(ctypes.c_int), _vp]),

@@ -8,6 +8,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "common.hpp"
 #include "../../include/gsx_hip.h"
 
@@ -360,6 +362,64 @@ gsx_hip_status radix_sort_u64(uint64_t* keys, uint32_t* vals, uint64_t* keys_alt
 
 }  // namespace
 
+namespace gsx_amd {
+void set_last_error(const char* what);
+}
+
+// Partial sums of gsx_hip_scan_exclusive_u32_noalloc: one per 1024-element block plus the total,
+// for at most kNoallocScanMaxBlocks blocks (256 KiB). Each GPU the library runs on holds its
+// own copy until the process ends; host code reaches it only through the address
+// hipGetSymbolAddress returns for the current device (scratch_address), never by its name.
+constexpr int64_t kNoallocScanMaxBlocks = 65536;
+constexpr int64_t kNoallocScanMaxElements = kNoallocScanMaxBlocks * kScanChunk;
+static __device__ __align__(256) uint32_t scratch[kNoallocScanMaxBlocks + 1];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+uint32_t* g_scratch[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device, looked up once per device.
+gsx_hip_status scratch_address(uint32_t** out) {
+    int device = 0;
+    hipError_t e = hipGetDevice(&device);
+    if (e != hipSuccess) {
+        set_last_error("scan without allocation: hipGetDevice failed");
+        return (gsx_hip_status)e;
+    }
+    if (device < 0 || device >= kMaxDevices) {
+        set_last_error("scan without allocation: device ordinal above 63");
+        return GSX_HIP_ERROR_OUT_OF_RANGE;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch[device] == nullptr) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr) {
+            set_last_error("scan without allocation: hipGetSymbolAddress(scratch) failed");
+            return e != hipSuccess ? (gsx_hip_status)e : GSX_HIP_ERROR_INVALID_STATE;
+        }
+        g_scratch[device] = static_cast<uint32_t*>(p);
+    }
+    *out = g_scratch[device];
+    return GSX_HIP_SUCCESS;
+}
+
+// The three launches of the exclusive scan with the partial sums (blocks + 1 words) at `partials`.
+gsx_hip_status scan_exclusive_u32(const uint32_t* in, uint32_t* out, int64_t n, uint32_t* partials,
+                                  hipStream_t stream) {
+    int64_t blocks = (n + kScanChunk - 1) / kScanChunk;
+    if (blocks < 1) blocks = 1;
+    hipLaunchKernelGGL(scan_reduce_kernel, dim3((unsigned)blocks), dim3(kScanThreads), 0, stream, in, n, partials);
+    hipLaunchKernelGGL(scan_partials_kernel, dim3(1), dim3(kScanThreads), 0, stream, partials, blocks);
+    hipLaunchKernelGGL(scan_downsweep_kernel, dim3((unsigned)blocks), dim3(kScanThreads), 0, stream, in, n, partials,
+                       out);
+    return (gsx_hip_status)hipGetLastError();
+}
+
+}  // namespace
+
 extern "C" {
 
 size_t gsx_hip_scan_temp_bytes(int64_t n) {
@@ -370,14 +430,23 @@ size_t gsx_hip_scan_temp_bytes(int64_t n) {
 
 // out[0..n) = exclusive prefix sums of in[0..n), out[n] = total. out may not alias in.
 gsx_hip_status gsx_hip_scan_exclusive_u32(const uint32_t* in, uint32_t* out, int64_t n, void* temp, hipStream_t stream) {
-    int64_t blocks = (n + kScanChunk - 1) / kScanChunk;
-    if (blocks < 1) blocks = 1;
-    uint32_t* partials = static_cast<uint32_t*>(temp);
-    hipLaunchKernelGGL(scan_reduce_kernel, dim3((unsigned)blocks), dim3(kScanThreads), 0, stream, in, n, partials);
-    hipLaunchKernelGGL(scan_partials_kernel, dim3(1), dim3(kScanThreads), 0, stream, partials, blocks);
-    hipLaunchKernelGGL(scan_downsweep_kernel, dim3((unsigned)blocks), dim3(kScanThreads), 0, stream, in, n, partials,
-                       out);
-    return (gsx_hip_status)hipGetLastError();
+    return scan_exclusive_u32(in, out, n, static_cast<uint32_t*>(temp), stream);
+}
+
+// The same scan with its partial sums in `scratch` (see above): no allocation, no workspace.
+gsx_hip_status gsx_hip_scan_exclusive_u32_noalloc(const uint32_t* in, uint32_t* out, int64_t n, hipStream_t stream) {
+    if (n < 0 || out == nullptr || (in == nullptr && n > 0)) {
+        set_last_error("scan: out must be non-null, in non-null when n > 0, n >= 0");
+        return GSX_HIP_ERROR_INVALID_ARGUMENT;
+    }
+    if (n > kNoallocScanMaxElements) {
+        set_last_error("scan without allocation: n exceeds the static scratch (at most 67108864 elements)");
+        return GSX_HIP_ERROR_OUT_OF_RANGE;
+    }
+    uint32_t* partials = nullptr;
+    const gsx_hip_status st = scratch_address(&partials);
+    if (st != GSX_HIP_SUCCESS) return st;
+    return scan_exclusive_u32(in, out, n, partials, stream);
 }
 
 size_t gsx_hip_radix_sort_temp_bytes(int64_t n) { return radix_temp_bytes<kRadixBits, kSortChunk>(n); }

@@ -185,6 +185,14 @@ gsx_hip_status gsx_hip_render_context_get_timings(gsx_hip_render_context* contex
 size_t gsx_hip_scan_temp_bytes(int64_t n);
 gsx_hip_status gsx_hip_scan_exclusive_u32(const uint32_t* in, uint32_t* out, int64_t n, void* temp,
                                           hipStream_t stream);
+/* The exclusive scan above without allocation or workspace, for callers that cannot allocate
+ * (code under HIP graph capture, serving loops, harnesses that forbid hipMalloc); it has no
+ * counterpart in the reference. The partial sums live in a static device array of 256 KiB per
+ * GPU (held until the process ends), so n may be at most 67,108,864 (2^26) elements; larger n
+ * fails with GSX_HIP_ERROR_OUT_OF_RANGE. Every call on one GPU uses that GPU's array: calls that
+ * overlap on one GPU (different streams or host threads) race and must be serialised by the
+ * caller. Nothing needs clearing between calls (every partial is written before it is read). */
+gsx_hip_status gsx_hip_scan_exclusive_u32_noalloc(const uint32_t* in, uint32_t* out, int64_t n, hipStream_t stream);
 size_t gsx_hip_radix_sort_temp_bytes(int64_t n);
 /* Stable LSD sort of (key, value) pairs on key bits [begin_bit, end_bit), 8 bits per pass. */
 gsx_hip_status gsx_hip_radix_sort_pairs_u64(uint64_t* keys, uint32_t* values, uint64_t* keys_alt,
