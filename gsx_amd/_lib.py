@@ -123,6 +123,28 @@ SIGNATURES = {
     "gsx_hip_render_context_get_buffers": (_st, [_vp, ctypes.POINTER(RenderBuffers)]),
     "gsx_hip_render_context_set_timing": (_st, [_vp, _i32]),
     "gsx_hip_render_context_get_timings": (_st, [_vp, ctypes.POINTER(_f), _i32, ctypes.POINTER(_i32)]),
+    "gsx_hip_memcpy_async": (_st, [_vp, _vp, ctypes.c_size_t, _vp]),
+    "gsx_hip_set_device": (_st, [_i32]),
+    "gsx_hip_device_total_memory": (_st, [_i32, ctypes.POINTER(ctypes.c_size_t)]),
+    "gsx_hip_host_alloc": (_st, [ctypes.POINTER(_vp), ctypes.c_size_t]),
+    "gsx_hip_host_free": (_st, [_vp]),
+    "gsx_hip_host_device_pointer": (_st, [_vp, ctypes.POINTER(_vp)]),
+    "gsx_hip_fill_pattern": (_st, [_vp, ctypes.c_size_t, _vp, ctypes.c_size_t, _vp]),
+    "gsx_hip_fill_rand_f32": (_st, [_vp, _i64, ctypes.c_uint64, ctypes.c_uint64, _vp]),
+    "gsx_hip_fill_randn_f32": (_st, [_vp, _i64, ctypes.c_uint64, ctypes.c_uint64, _f, _vp]),
+    "gsx_hip_fill_randint_temp_bytes": (ctypes.c_size_t, [_i64]),
+    "gsx_hip_fill_randint": (_st, [_vp, _i64, _i32, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint32, _i64, _vp,
+                                   ctypes.POINTER(_i64), _vp]),
+    "gsx_hip_multinomial_i32": (_st, [_vp, _i64, _vp, _i64, ctypes.c_uint64, ctypes.c_uint64, _vp]),
+    "gsx_hip_check_finite_f32": (_st, [_vp, _i64, _vp, _vp]),
+    "gsx_hip_unary_f32": (_st, [_vp, _vp, _i64, _i32, _vp]),
+    "gsx_hip_clamp_inplace": (_st, [_vp, _i64, _i32, _vp, _vp, _vp]),
+    "gsx_hip_reduce_temp_bytes": (ctypes.c_size_t, [_i64, _i64]),
+    "gsx_hip_reduce_f32": (_st, [_vp, _vp, _i64, _i64, _i32, _vp, _vp, _vp]),
+    "gsx_hip_image_colorspace_f32": (_st, [_vp, _vp, _i64, _i32, _i32, _vp]),
+    "gsx_hip_image_storage_convert": (_st, [_vp, _i32, _vp, _i32, _i64, _i64, _i64, _i32, _vp]),
+    "gsx_hip_image_quantize_u8": (_st, [_vp, _vp, _i64, _vp]),
+    "gsx_hip_image_dequantize_u8": (_st, [_vp, _vp, _i64, _vp]),
     "gsx_hip_scan_temp_bytes": (ctypes.c_size_t, [_i64]),
     "gsx_hip_scan_exclusive_u32": (_st, [_vp, _vp, _i64, _vp, _vp]),
     "gsx_hip_scan_exclusive_u32_noalloc": (_st, [_vp, _vp, _i64, _vp]),

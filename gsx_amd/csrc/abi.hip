@@ -435,6 +435,45 @@ gsx_hip_status gsx_hip_memcpy_dtod_async(void* dst, const void* src, size_t byte
     return GSX_HIP_SUCCESS;
 }
 
+gsx_hip_status gsx_hip_memcpy_async(void* dst, const void* src, size_t bytes, hipStream_t stream) {
+    if (bytes == 0) return GSX_HIP_SUCCESS;
+    if (dst == nullptr || src == nullptr) return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "copy pointers must be non-null");
+    GSX_HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDefault, stream), "hipMemcpyAsync");
+    return GSX_HIP_SUCCESS;
+}
+
+gsx_hip_status gsx_hip_set_device(int32_t device) {
+    GSX_HIP_TRY(hipSetDevice(device), "hipSetDevice");
+    return GSX_HIP_SUCCESS;
+}
+
+gsx_hip_status gsx_hip_device_total_memory(int32_t device, size_t* out_bytes) {
+    if (out_bytes == nullptr) return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "out_bytes must be non-null");
+    hipDeviceProp_t prop;
+    GSX_HIP_TRY(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
+    *out_bytes = prop.totalGlobalMem;
+    return GSX_HIP_SUCCESS;
+}
+
+gsx_hip_status gsx_hip_host_alloc(void** out_host, size_t bytes) {
+    if (out_host == nullptr) return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "out_host must be non-null");
+    *out_host = nullptr;
+    GSX_HIP_TRY(hipHostMalloc(out_host, bytes == 0 ? 1 : bytes, hipHostMallocDefault), "hipHostMalloc");
+    return GSX_HIP_SUCCESS;
+}
+
+gsx_hip_status gsx_hip_host_free(void* host) {
+    if (host == nullptr) return GSX_HIP_SUCCESS;
+    GSX_HIP_TRY(hipHostFree(host), "hipHostFree");
+    return GSX_HIP_SUCCESS;
+}
+
+gsx_hip_status gsx_hip_host_device_pointer(void* host, void** out_device) {
+    if (host == nullptr || out_device == nullptr) return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "pointers must be non-null");
+    GSX_HIP_TRY(hipHostGetDevicePointer(out_device, host, 0), "hipHostGetDevicePointer");
+    return GSX_HIP_SUCCESS;
+}
+
 gsx_hip_status gsx_hip_stream_create(hipStream_t* out_stream) {
     if (out_stream == nullptr) return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "out_stream must be non-null");
     GSX_HIP_TRY(hipStreamCreateWithFlags(out_stream, hipStreamNonBlocking), "hipStreamCreateWithFlags");

@@ -50,6 +50,15 @@ gsx_hip_status gsx_hip_free(void* ptr);
 gsx_hip_status gsx_hip_memcpy_htod(void* dst, const void* src, size_t bytes);
 gsx_hip_status gsx_hip_memcpy_dtoh(void* dst, const void* src, size_t bytes);
 gsx_hip_status gsx_hip_memcpy_dtod_async(void* dst, const void* src, size_t bytes, hipStream_t stream);
+/* Ordered copy on `stream` between any two of host, pinned host and device memory (the direction
+ * is taken from the pointers, hipMemcpyDefault); gsx-cuda/buffer.c's cudaMemcpyAsync uses. */
+gsx_hip_status gsx_hip_memcpy_async(void* dst, const void* src, size_t bytes, hipStream_t stream);
+gsx_hip_status gsx_hip_set_device(int32_t device);
+gsx_hip_status gsx_hip_device_total_memory(int32_t device, size_t* out_bytes);
+/* Page-locked host memory (the HOST_PINNED buffer type) and its device-side address. */
+gsx_hip_status gsx_hip_host_alloc(void** out_host, size_t bytes);
+gsx_hip_status gsx_hip_host_free(void* host);
+gsx_hip_status gsx_hip_host_device_pointer(void* host, void** out_device);
 gsx_hip_status gsx_hip_stream_create(hipStream_t* out_stream);
 gsx_hip_status gsx_hip_stream_destroy(hipStream_t stream);
 gsx_hip_status gsx_hip_stream_synchronize(hipStream_t stream);
@@ -203,6 +212,69 @@ gsx_hip_status gsx_hip_radix_sort_pairs_u64(uint64_t* keys, uint32_t* values, ui
  * backend, which always sorts pairs. */
 gsx_hip_status gsx_hip_radix_sort_keys_u64(uint64_t* keys, uint64_t* keys_alt, int64_t n, int begin_bit,
                                            int end_bit, void* temp, int* out_result_in_alt, hipStream_t stream);
+
+/* ---- tensor operations -------------------------------------------------------------------------
+ * The element-wise, random, reduce and image-conversion entries of gsx_backend_buffer_i
+ * (gsx/src/gsx-impl.h:302-458) that the CUDA backend implements in gsx-cuda/buffer.c and
+ * reduce-kernels.cu; semantics of the CPU backend (gsx/src/gsx-cpu/core.c:874-2019). Pointers are
+ * device pointers; nothing here synchronises except where stated. */
+enum { GSX_HIP_DTYPE_F32 = 0, GSX_HIP_DTYPE_U8 = 1, GSX_HIP_DTYPE_I32 = 2 };
+enum {                                   /* gsx_impl_unary_op (gsx-impl.h:295-300) */
+    GSX_HIP_UNARY_EXP = 0,
+    GSX_HIP_UNARY_SIGMOID = 1,
+    GSX_HIP_UNARY_SIGMOID_DERIVATIVE = 2,
+    GSX_HIP_UNARY_ABS = 3
+};
+enum {                                   /* gsx_impl_unary/binary_reduce_op (gsx-impl.h:234-243) */
+    GSX_HIP_REDUCE_SUM = 0,
+    GSX_HIP_REDUCE_MEAN = 1,
+    GSX_HIP_REDUCE_MAX = 2,
+    GSX_HIP_REDUCE_MSE = 3,
+    GSX_HIP_REDUCE_MAE = 4
+};
+/* Repeat a pattern of 1..64 bytes over `bytes` (memset_tensor / fill_tensor / set_zero). */
+gsx_hip_status gsx_hip_fill_pattern(void* dst, size_t bytes, const void* pattern, size_t pattern_bytes,
+                                    hipStream_t stream);
+/* Element i = pcg32_next_float of draw i of the (state, inc) stream (fill_rand_tensor). */
+gsx_hip_status gsx_hip_fill_rand_f32(float* dst, int64_t count, uint64_t state, uint64_t inc, hipStream_t stream);
+/* Box-Muller pairs from draws 2k, 2k+1, times sigma (fill_randn_tensor); log/cos/sin within one
+ * float ulp of glibc's. */
+gsx_hip_status gsx_hip_fill_randn_f32(float* dst, int64_t count, uint64_t state, uint64_t inc, float sigma,
+                                      hipStream_t stream);
+/* fill_randint_tensor: element i = the i-th draw that pcg32_next_uint_bound accepts, mod bound,
+ * for u8 (element_bytes 1) or i32 (4) elements. `draws` >= count draws are examined (temp of
+ * gsx_hip_fill_randint_temp_bytes(draws)); when out_accepted is non-null the call synchronises
+ * the stream and stores how many were accepted (fewer than count: call again with more draws). */
+size_t gsx_hip_fill_randint_temp_bytes(int64_t draws);
+gsx_hip_status gsx_hip_fill_randint(void* dst, int64_t count, int32_t element_bytes, uint64_t state, uint64_t inc,
+                                    uint32_t bound, int64_t draws, void* temp, int64_t* out_accepted,
+                                    hipStream_t stream);
+/* multinomial_tensor: sample i from draw i and the (non-decreasing, positive-ended) cdf. */
+gsx_hip_status gsx_hip_multinomial_i32(int32_t* out, int64_t samples, const float* cdf, int64_t categories,
+                                       uint64_t state, uint64_t inc, hipStream_t stream);
+/* check_finite_tensor: sets *flag (a device word the caller cleared) to 1 on any inf or NaN. */
+gsx_hip_status gsx_hip_check_finite_f32(const float* x, int64_t count, uint32_t* flag, hipStream_t stream);
+/* unary_tensor / unary_tensor_inplace (x may equal out); exp through the glibc-exact expf. */
+gsx_hip_status gsx_hip_unary_f32(const float* x, float* out, int64_t count, int32_t op, hipStream_t stream);
+/* clamp_inplace_tensor for GSX_HIP_DTYPE_*; lo and hi are host pointers to one element. */
+gsx_hip_status gsx_hip_clamp_inplace(void* x, int64_t count, int32_t data_type, const void* lo, const void* hi,
+                                     hipStream_t stream);
+/* unary_reduce_tensor (sum, mean, max over rows of `reduce` elements of x) and
+ * binary_reduce_tensor (mse, mae of x - y); out[outer]. Sums run in double in a fixed order;
+ * max keeps the CPU's first-occurrence and NaN rules. temp: gsx_hip_reduce_temp_bytes. */
+size_t gsx_hip_reduce_temp_bytes(int64_t outer, int64_t reduce);
+gsx_hip_status gsx_hip_reduce_f32(const float* x, const float* y, int64_t outer, int64_t reduce, int32_t op,
+                                  float* out, void* temp, hipStream_t stream);
+/* image_convert_colorspace (sRGB transfer curves, powf within one float ulp of glibc's),
+ * image_convert_storage_format (HWC <-> CHW for 1/2/4-byte elements) and
+ * image_convert_data_type (f32 <-> u8), gsx/src/extra/gsx-image-impl.h:9-170. */
+gsx_hip_status gsx_hip_image_colorspace_f32(const float* src, float* dst, int64_t count, int32_t src_srgb,
+                                            int32_t dst_srgb, hipStream_t stream);
+gsx_hip_status gsx_hip_image_storage_convert(const void* src, int32_t src_hwc, void* dst, int32_t dst_hwc,
+                                             int64_t channels, int64_t height, int64_t width, int32_t element_bytes,
+                                             hipStream_t stream);
+gsx_hip_status gsx_hip_image_quantize_u8(const float* src, uint8_t* dst, int64_t count, hipStream_t stream);
+gsx_hip_status gsx_hip_image_dequantize_u8(const uint8_t* src, float* dst, int64_t count, hipStream_t stream);
 
 /* ---- losses -----------------------------------------------------------------------------------
  * Replace gsx_cuda_loss_*_kernel_launch (gsx/src/gsx-cuda/internal.h:312-369, CHW forms); semantics of

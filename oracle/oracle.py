@@ -250,18 +250,58 @@ class Oracle:
         return int(self.lib.oracle_expf_blend_mismatches(lo_bits, hi_bits, stride))
 
 
+class _OnBackend:
+    """The driver library with every entry point run on one backend: the library keeps the
+    selected backend in a global, so each call selects its own first."""
+
+    _unselected = ("gsxref_use_backend", "gsxref_last_error")
+
+    def __init__(self, lib, which):
+        self._lib, self._which = lib, which
+
+    def __getattr__(self, name):
+        fn = getattr(self._lib, name)
+        if not name.startswith("gsxref_") or name in self._unselected:
+            return fn
+
+        def call(*args):
+            rc = self._lib.gsxref_use_backend(self._which)
+            if rc != 0:
+                raise RuntimeError(f"selecting the backend failed ({rc}): {self._lib.gsxref_last_error().decode()}")
+            return fn(*args)
+        return call
+
+
 class Reference:
-    """The unmodified reference CPU backend (oracle/_ref/libgsxref.so)."""
+    """The unmodified reference core driven through gsx's public API.
+
+    ``Reference()`` loads ``_ref/libgsxref.so`` (core + CPU backend). ``Reference(backend="hip")``
+    loads ``_ref/libgsxref_hip.so``, the same core with the registry's GPU slot filled by the HIP
+    backend plugin (gsx_amd/libgsx_hip_backend.so), and runs every call on that backend;
+    ``backend="cpu"`` on that library runs the CPU backend of the same process.
+    """
 
     path = os.path.join(HERE, "_ref", "libgsxref.so")
+    hip_path = os.path.join(HERE, "_ref", "libgsxref_hip.so")
 
     @classmethod
-    def available(cls) -> bool:
-        return os.path.exists(cls.path)
+    def available(cls, hip: bool = False) -> bool:
+        return os.path.exists(cls.hip_path if hip else cls.path)
 
-    def __init__(self):
-        lib = ctypes.CDLL(self.path)
+    def __init__(self, backend: str | None = None):
+        lib = ctypes.CDLL(self.path if backend is None else self.hip_path)
         lib.gsxref_last_error.restype = ctypes.c_char_p
+        lib.gsxref_reduce.restype = ctypes.c_int
+        lib.gsxref_reduce.argtypes = [ctypes.c_int, ctypes.c_int, _vp, ctypes.c_int, _vp, _vp, _vp]
+        lib.gsxref_elementwise.restype = ctypes.c_int
+        lib.gsxref_elementwise.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp, _vp, _vp]
+        lib.gsxref_gather.restype = ctypes.c_int
+        lib.gsxref_gather.argtypes = [ctypes.c_int, ctypes.c_int, _vp, ctypes.c_int, _vp, _vp]
+        lib.gsxref_random.restype = ctypes.c_int
+        lib.gsxref_random.argtypes = [ctypes.c_int, ctypes.c_uint64, ctypes.c_int, _f, _vp, ctypes.c_int, _vp]
+        lib.gsxref_image.restype = ctypes.c_int
+        lib.gsxref_image.argtypes = [ctypes.c_int] * 4 + [_vp, _vp]
+        lib.gsxref_backend_device_name.restype = ctypes.c_char_p
         lib.gsxref_render.restype = ctypes.c_int
         lib.gsxref_render.argtypes = [ctypes.c_int, ctypes.c_int] + [_vp] * 9 + [ctypes.c_int, _vp, _vp]
         lib.gsxref_render_grad.restype = ctypes.c_int
@@ -274,7 +314,10 @@ class Reference:
         lib.gsxref_adc.argtypes = [ctypes.c_int] + [_vp] * 10 + [ctypes.c_int, _vp] + [_vp] * 6
         lib.gsxref_train_step.restype = ctypes.c_int
         lib.gsxref_train_step.argtypes = [ctypes.c_int, ctypes.c_int] + [_vp] * 7 + [_f, _f, _vp, _vp]
-        self.lib = lib
+        self.lib = lib if backend is None else _OnBackend(lib, {"cpu": 0, "hip": 1}[backend])
+
+    def device_name(self) -> str:
+        return self.lib.gsxref_backend_device_name().decode()
 
     def _check(self, rc):
         if rc != 0:
@@ -345,3 +388,66 @@ class Reference:
                                                _p(sc.opacity), _p(sc.sh0), _p(camera), _p(target), w_l1, w_ssim,
                                                _p(np.asarray(lrs, np.float32)), _p(stages)))
         return sc, stages
+
+    # ---- tensor, random and image operations (gsx-core.h, gsx-random.h, extra/gsx-image.h)
+
+    def reduce(self, op, x, start_axis, y=None):
+        """op in sum/mean/max/mse/mae over axes [start_axis, ndim); returns the leading extents."""
+        x = np.ascontiguousarray(x, np.float32)
+        shape = np.asarray(x.shape, np.int32)
+        out = np.zeros(x.shape[:start_axis] + (1,), np.float32)
+        yy = None if y is None else np.ascontiguousarray(y, np.float32)
+        code = {"sum": 0, "mean": 1, "max": 2, "mse": 3, "mae": 4}[op]
+        self._check(self.lib.gsxref_reduce(code, x.ndim, _p(shape), start_axis, _p(x), _p(yy), _p(out)))
+        return out.reshape(x.shape[:start_axis])
+
+    def unary(self, op, x, inplace=False):
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.zeros_like(x)
+        code = {"exp": 0, "sigmoid": 1, "sigmoid_derivative": 2, "abs": 3}[op]
+        self._check(self.lib.gsxref_elementwise(code, 1 if inplace else 0, x.size, _p(x), None, _p(out)))
+        return out
+
+    def clamp(self, x, lo, hi):
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.zeros_like(x)
+        params = np.array([lo, hi], np.float32)
+        self._check(self.lib.gsxref_elementwise(4, 1, x.size, _p(x), _p(params), _p(out)))
+        return out
+
+    def check_finite(self, x) -> bool:
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.zeros(1, np.float32)
+        self._check(self.lib.gsxref_elementwise(5, 0, x.size, _p(x), None, _p(out)))
+        return bool(out[0] != 0)
+
+    def gather(self, x, index):
+        x = np.ascontiguousarray(x, np.float32)
+        x2 = x.reshape(x.shape[0], -1)
+        index = np.ascontiguousarray(index, np.int32)
+        out = np.zeros((index.size, x2.shape[1]), np.float32)
+        self._check(self.lib.gsxref_gather(x2.shape[0], x2.shape[1], _p(x2), index.size, _p(index), _p(out)))
+        return out.reshape((index.size,) + x.shape[1:])
+
+    def random(self, kind, seed, count, param=0.0, cdf=None):
+        """kind in rand/randn (param = sigma)/randint (param = bound)/multinomial (cdf)."""
+        code = {"rand": 0, "randn": 1, "randint": 2, "multinomial": 3}[kind]
+        out = np.zeros(count, np.float32 if code < 2 else np.int32)
+        c = None if cdf is None else np.ascontiguousarray(cdf, np.float32)
+        self._check(self.lib.gsxref_random(code, seed, count, param, _p(c), 0 if c is None else c.size, _p(out)))
+        return out
+
+    def image(self, kind, src, c, h, w):
+        """kind in to_srgb/to_linear ([3,h,w] f32), hwc_to_chw/chw_to_hwc (f32), to_u8/from_u8 (CHW)."""
+        code = {"to_srgb": 0, "to_linear": 1, "hwc_to_chw": 2, "chw_to_hwc": 3, "to_u8": 4, "from_u8": 5}[kind]
+        src = np.ascontiguousarray(src)
+        if code == 2:
+            out = np.zeros((c, h, w), np.float32)
+        elif code == 3:
+            out = np.zeros((h, w, c), np.float32)
+        elif code == 4:
+            out = np.zeros((c, h, w), np.uint8)
+        else:
+            out = np.zeros((c, h, w), np.float32)
+        self._check(self.lib.gsxref_image(code, c, h, w, _p(src), _p(out)))
+        return out

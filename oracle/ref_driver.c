@@ -14,11 +14,18 @@
  *   - gsxref_adc          gsx_adc_step                 (gsx/src/gsx-adc.c:231)
  *   - gsxref_train_step   one image-fit style step (render, L1+SSIM, backward, Adam) with
  *                         per-stage wall-clock timings, used as the CPU baseline.
+ *   - gsxref_reduce / gsxref_elementwise / gsxref_gather / gsxref_random / gsxref_image
+ *                         the tensor, random and image operations of gsx-core.h, gsx-random.h
+ *                         and extra/gsx-image.h.
+ * gsxref_use_backend selects the backend the entry points run on: the CPU backend, or the
+ * registry's GPU slot in a build linked with the HIP backend plugin (libgsxref_hip.so).
  * Return value: 0 on success, otherwise the gsx_error_code; gsxref_last_error() gives the
  * reference's static message.
  */
 #define _POSIX_C_SOURCE 200809L
 #include "gsx/gsx.h"
+#include "gsx/gsx-random.h"
+#include "gsx/extra/gsx-image.h"
 
 #include <stdint.h>
 #include <stdlib.h>
@@ -26,6 +33,11 @@
 #include <time.h>
 
 static const char *g_last_message = NULL;
+/* One backend per registry slot, created on first use; gsxref_use_backend picks the slot the
+ * entry points below run on (the CPU backend unless told otherwise). */
+static gsx_backend_t g_backends[3] = { NULL, NULL, NULL };
+static gsx_backend_buffer_type_t g_device_types[3] = { NULL, NULL, NULL };
+static int g_which = 0;
 static gsx_backend_t g_backend = NULL;
 static gsx_backend_buffer_type_t g_device_type = NULL;
 
@@ -41,25 +53,52 @@ const char *gsxref_last_error(void) { return g_last_message != NULL ? g_last_mes
         }                                                           \
     } while(0)
 
+/* Downloads are asynchronous on a GPU backend's major stream (gsx-backend.h:114): every entry
+ * point drains it before the caller reads its host arrays. */
+#define FINISH() do { if(g_backend != NULL) (void)gsx_backend_major_stream_sync(g_backend); } while(0)
+
 static int ensure_backend(void)
 {
+    static const gsx_backend_type types[3] = { GSX_BACKEND_TYPE_CPU, GSX_BACKEND_TYPE_CUDA, GSX_BACKEND_TYPE_METAL };
     gsx_backend_device_t device = NULL;
     gsx_backend_desc desc = { 0 };
     gsx_error e;
 
-    if(g_backend != NULL) {
-        return 0;
+    if(g_backends[g_which] == NULL) {
+        e = gsx_backend_registry_init();
+        if(!gsx_error_is_success(e)) { g_last_message = e.message; return (int)e.code; }
+        e = gsx_get_backend_device_by_type(types[g_which], 0, &device);
+        if(!gsx_error_is_success(e)) { g_last_message = e.message; return (int)e.code; }
+        desc.device = device;
+        e = gsx_backend_init(&g_backends[g_which], &desc);
+        if(!gsx_error_is_success(e)) { g_last_message = e.message; return (int)e.code; }
+        e = gsx_backend_find_buffer_type(g_backends[g_which], GSX_BACKEND_BUFFER_TYPE_DEVICE, &g_device_types[g_which]);
+        if(!gsx_error_is_success(e)) { g_last_message = e.message; return (int)e.code; }
     }
-    e = gsx_backend_registry_init();
-    if(!gsx_error_is_success(e)) { g_last_message = e.message; return (int)e.code; }
-    e = gsx_get_backend_device_by_type(GSX_BACKEND_TYPE_CPU, 0, &device);
-    if(!gsx_error_is_success(e)) { g_last_message = e.message; return (int)e.code; }
-    desc.device = device;
-    e = gsx_backend_init(&g_backend, &desc);
-    if(!gsx_error_is_success(e)) { g_last_message = e.message; return (int)e.code; }
-    e = gsx_backend_find_buffer_type(g_backend, GSX_BACKEND_BUFFER_TYPE_DEVICE, &g_device_type);
-    if(!gsx_error_is_success(e)) { g_last_message = e.message; return (int)e.code; }
+    g_backend = g_backends[g_which];
+    g_device_type = g_device_types[g_which];
     return 0;
+}
+
+/* which: 0 the CPU backend, 1 the registry's GPU slot (GSX_BACKEND_TYPE_CUDA: in a build linked
+ * with the HIP backend plugin, the MI355X backend registers there). */
+int gsxref_use_backend(int which)
+{
+    if(which < 0 || which > 1) return (int)GSX_ERROR_OUT_OF_RANGE;
+    g_which = which;
+    return ensure_backend();
+}
+
+/* Name of the device the selected backend runs on. */
+const char *gsxref_backend_device_name(void)
+{
+    gsx_backend_info info;
+    gsx_backend_device_info dinfo;
+
+    if(ensure_backend() != 0) return "";
+    if(!gsx_error_is_success(gsx_backend_get_info(g_backend, &info))) return "";
+    if(!gsx_error_is_success(gsx_backend_device_get_info(info.device, &dinfo))) return "";
+    return dinfo.name;
 }
 
 static gsx_error make_tensor(gsx_arena_t arena, gsx_tensor_t *out, int rank, int d0, int d1, int d2, const void *src)
@@ -231,6 +270,7 @@ int gsxref_render(int n, int sh_degree, const float *mean3d, const float *rotati
         TRY(gsx_tensor_download(counter, visible_counter, (gsx_size_t)n * sizeof(float)));
     }
 done:
+    FINISH();
     if(context != NULL) (void)gsx_render_context_free(context);
     if(renderer != NULL) (void)gsx_renderer_free(renderer);
     if(out != NULL) (void)gsx_tensor_free(out);
@@ -323,6 +363,7 @@ int gsxref_render_grad(int n, int sh_degree, const float *mean3d, const float *r
     if(gs2 != NULL) TRY(gsx_tensor_download(gs2, g_sh2, (gsx_size_t)n * 15u * sizeof(float)));
     if(gs3 != NULL) TRY(gsx_tensor_download(gs3, g_sh3, (gsx_size_t)n * 21u * sizeof(float)));
 done:
+    FINISH();
     if(context != NULL) (void)gsx_render_context_free(context);
     if(renderer != NULL) (void)gsx_renderer_free(renderer);
     {
@@ -394,6 +435,7 @@ int gsxref_loss(int algorithm, int grad_norm, int outer, int channels, int heigh
     }
     TRY(gsx_tensor_download(map, loss_map, bytes));
 done:
+    FINISH();
     if(context != NULL) (void)gsx_loss_context_free(context);
     if(loss != NULL) (void)gsx_loss_free(loss);
     if(pred != NULL) (void)gsx_tensor_free(pred);
@@ -447,6 +489,7 @@ int gsxref_adam(int count, int steps, float *param, const float *grad, const flo
     }
     TRY(gsx_tensor_download(p, param, (gsx_size_t)count * sizeof(float)));
 done:
+    FINISH();
     if(optim != NULL) (void)gsx_optim_free(optim);
     if(p != NULL) (void)gsx_tensor_free(p);
     if(g != NULL) (void)gsx_tensor_free(g);
@@ -582,6 +625,7 @@ int gsxref_adc(int n, const float *mean3d, const float *rotation, const float *l
     TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_SH0, &t));
     TRY(gsx_tensor_download(t, o_sh0, info.count * 3u * sizeof(float)));
 done:
+    FINISH();
     if(adc_renderer != NULL) (void)gsx_renderer_free(adc_renderer);
     if(adc != NULL) (void)gsx_adc_free(adc);
     if(optim != NULL) (void)gsx_optim_free(optim);
@@ -757,6 +801,7 @@ int gsxref_train_step(int n, int iters, float *mean3d, float *rotation, float *l
     TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_SH0, &t));
     TRY(gsx_tensor_download(t, sh0, (gsx_size_t)n * 3u * sizeof(float)));
 done:
+    FINISH();
     if(optim != NULL) (void)gsx_optim_free(optim);
     if(l1ctx != NULL) (void)gsx_loss_context_free(l1ctx);
     if(ssimctx != NULL) (void)gsx_loss_context_free(ssimctx);
@@ -773,5 +818,284 @@ done:
     }
     if(arena != NULL) (void)gsx_arena_free(arena);
     if(gs != NULL) (void)gsx_gs_free(gs);
+    return rc;
+}
+
+/* ---- tensor operations through gsx's public API (gsx-core.h:221-270, gsx-random.h,
+ * extra/gsx-image.h), on the selected backend: the buffer-vtable operations a backend supplies
+ * (gsx-impl.h:302-458) run on byte-identical inputs on both backends. ---------------------------- */
+
+static gsx_error make_typed(gsx_arena_t arena, gsx_tensor_t *out, int rank, const int *shape, gsx_data_type dt,
+    gsx_storage_format fmt, const void *src, size_t bytes)
+{
+    gsx_tensor_desc desc = { 0 };
+    gsx_error e;
+    int d;
+
+    desc.rank = rank;
+    for(d = 0; d < rank; ++d) desc.shape[d] = shape[d];
+    desc.data_type = dt;
+    desc.storage_format = fmt;
+    desc.arena = arena;
+    e = gsx_tensor_init(out, &desc);
+    if(!gsx_error_is_success(e)) return e;
+    if(src != NULL) return gsx_tensor_upload(*out, src, bytes);
+    return gsx_tensor_set_zero(*out);
+}
+
+static size_t shape_count(int rank, const int *shape)
+{
+    size_t n = 1;
+    int d;
+
+    for(d = 0; d < rank; ++d) n *= (size_t)shape[d];
+    return n;
+}
+
+/* op: 0 sum, 1 mean, 2 max (of x), 3 mse, 4 mae (of x - y) over axes [start_axis, rank);
+ * out has the leading extents. */
+int gsxref_reduce(int op, int rank, const int *shape, int start_axis, const float *x, const float *y, float *out)
+{
+    int rc = 0;
+    gsx_arena_t arena = NULL;
+    gsx_arena_desc adesc = { 0 };
+    gsx_tensor_t tx = NULL, ty = NULL, to = NULL;
+    /* the output keeps the leading extents and one unit axis (gsx-core.c:1503-1530) */
+    int out_shape[4] = { 1, 1, 1, 1 };
+    int out_rank = start_axis + 1;
+    size_t n = shape_count(rank, shape);
+    size_t n_out = 1;
+    int d;
+
+    rc = ensure_backend();
+    if(rc != 0) return rc;
+    for(d = 0; d < start_axis; ++d) {
+        out_shape[d] = shape[d];
+        n_out *= (size_t)shape[d];
+    }
+    adesc.initial_capacity_bytes = (gsx_size_t)(2 * n + n_out) * 4u + 65536u;
+    TRY(gsx_arena_init(&arena, g_device_type, &adesc));
+    TRY(make_typed(arena, &tx, rank, shape, GSX_DATA_TYPE_F32, GSX_STORAGE_FORMAT_CHW, x, n * 4));
+    if(op >= 3) TRY(make_typed(arena, &ty, rank, shape, GSX_DATA_TYPE_F32, GSX_STORAGE_FORMAT_CHW, y, n * 4));
+    TRY(make_typed(arena, &to, out_rank, out_shape, GSX_DATA_TYPE_F32, GSX_STORAGE_FORMAT_CHW, NULL, 0));
+    {
+        /* the reduce front-ends take a workspace arena of the same backend */
+        gsx_arena_t ws = NULL;
+        gsx_arena_desc wdesc = { 0 };
+
+        wdesc.initial_capacity_bytes = (gsx_size_t)n * 8u + 65536u;
+        TRY(gsx_arena_init(&ws, g_device_type, &wdesc));
+        gsx_error re = { GSX_ERROR_OUT_OF_RANGE, "unknown reduce op" };
+
+        switch(op) {
+        case 0: re = gsx_tensor_sum(ws, tx, to, start_axis); break;
+        case 1: re = gsx_tensor_mean(ws, tx, to, start_axis); break;
+        case 2: re = gsx_tensor_max(ws, tx, to, start_axis); break;
+        case 3: re = gsx_tensor_mse(ws, tx, ty, to, start_axis); break;
+        case 4: re = gsx_tensor_mae(ws, tx, ty, to, start_axis); break;
+        default: break;
+        }
+        if(!gsx_error_is_success(re)) {
+            g_last_message = re.message;
+            rc = (int)re.code;
+        }
+        FINISH();
+        (void)gsx_arena_free(ws);
+        if(rc != 0) goto done;
+    }
+    TRY(gsx_tensor_download(to, out, n_out * 4));
+done:
+    FINISH();
+    if(tx != NULL) (void)gsx_tensor_free(tx);
+    if(ty != NULL) (void)gsx_tensor_free(ty);
+    if(to != NULL) (void)gsx_tensor_free(to);
+    if(arena != NULL) (void)gsx_arena_free(arena);
+    return rc;
+}
+
+/* op: 0 exp, 1 sigmoid, 2 sigmoid', 3 abs (out = f(x), or in place when inplace != 0);
+ * 4 clamp in place to [params[0], params[1]]; 5 check_finite (out[0] = 1 when all finite). */
+int gsxref_elementwise(int op, int inplace, int count, const float *x, const float *params, float *out)
+{
+    int rc = 0;
+    gsx_arena_t arena = NULL;
+    gsx_arena_desc adesc = { 0 };
+    gsx_tensor_t tx = NULL, to = NULL;
+    int shape[1];
+
+    rc = ensure_backend();
+    if(rc != 0) return rc;
+    shape[0] = count;
+    adesc.initial_capacity_bytes = (gsx_size_t)count * 8u + 65536u;
+    TRY(gsx_arena_init(&arena, g_device_type, &adesc));
+    TRY(make_typed(arena, &tx, 1, shape, GSX_DATA_TYPE_F32, GSX_STORAGE_FORMAT_CHW, x, (size_t)count * 4));
+    if(op <= 3 && !inplace) {
+        TRY(make_typed(arena, &to, 1, shape, GSX_DATA_TYPE_F32, GSX_STORAGE_FORMAT_CHW, NULL, 0));
+        switch(op) {
+        case 0: TRY(gsx_tensor_exp(tx, to)); break;
+        case 1: TRY(gsx_tensor_sigmoid(tx, to)); break;
+        case 2: TRY(gsx_tensor_sigmoid_derivative(tx, to)); break;
+        default: TRY(gsx_tensor_abs(tx, to)); break;
+        }
+        TRY(gsx_tensor_download(to, out, (size_t)count * 4));
+    } else if(op <= 4) {
+        switch(op) {
+        case 0: TRY(gsx_tensor_exp_inplace(tx)); break;
+        case 1: TRY(gsx_tensor_sigmoid_inplace(tx)); break;
+        case 2: TRY(gsx_tensor_sigmoid_derivative_inplace(tx)); break;
+        case 3: TRY(gsx_tensor_abs_inplace(tx)); break;
+        default: {
+            float lo = params[0], hi = params[1];
+
+            TRY(gsx_tensor_clamp_inplace(tx, &lo, &hi));
+        }
+        }
+        TRY(gsx_tensor_download(tx, out, (size_t)count * 4));
+    } else if(op == 5) {
+        bool finite = false;
+
+        TRY(gsx_tensor_check_finite(tx, &finite));
+        out[0] = finite ? 1.0f : 0.0f;
+    } else {
+        rc = (int)GSX_ERROR_OUT_OF_RANGE;
+    }
+done:
+    FINISH();
+    if(tx != NULL) (void)gsx_tensor_free(tx);
+    if(to != NULL) (void)gsx_tensor_free(to);
+    if(arena != NULL) (void)gsx_arena_free(arena);
+    return rc;
+}
+
+/* out[r] = x[index[r]] for rows of `width` floats (gsx_tensor_gather). */
+int gsxref_gather(int rows, int width, const float *x, int count, const int32_t *index, float *out)
+{
+    int rc = 0;
+    gsx_arena_t arena = NULL;
+    gsx_arena_desc adesc = { 0 };
+    gsx_tensor_t tx = NULL, ti = NULL, to = NULL;
+    int xs[2], os[2], is[1];
+
+    rc = ensure_backend();
+    if(rc != 0) return rc;
+    xs[0] = rows;
+    xs[1] = width;
+    os[0] = count;
+    os[1] = width;
+    is[0] = count;
+    adesc.initial_capacity_bytes = (gsx_size_t)(rows + count) * (gsx_size_t)width * 4u + (gsx_size_t)count * 4u + 65536u;
+    TRY(gsx_arena_init(&arena, g_device_type, &adesc));
+    TRY(make_typed(arena, &tx, 2, xs, GSX_DATA_TYPE_F32, GSX_STORAGE_FORMAT_CHW, x, (size_t)rows * width * 4));
+    TRY(make_typed(arena, &ti, 1, is, GSX_DATA_TYPE_I32, GSX_STORAGE_FORMAT_CHW, index, (size_t)count * 4));
+    TRY(make_typed(arena, &to, 2, os, GSX_DATA_TYPE_F32, GSX_STORAGE_FORMAT_CHW, NULL, 0));
+    TRY(gsx_tensor_gather(tx, ti, to));
+    TRY(gsx_tensor_download(to, out, (size_t)count * width * 4));
+done:
+    FINISH();
+    if(tx != NULL) (void)gsx_tensor_free(tx);
+    if(ti != NULL) (void)gsx_tensor_free(ti);
+    if(to != NULL) (void)gsx_tensor_free(to);
+    if(arena != NULL) (void)gsx_arena_free(arena);
+    return rc;
+}
+
+/* kind: 0 rand (float), 1 randn (float, sigma = param), 2 randint (int32, bound = (uint32)param),
+ * 3 multinomial (int32 samples from cdf[categories]); pcg32 seeded with `seed`
+ * (gsx_pcg32_init). out has `count` elements. */
+int gsxref_random(int kind, uint64_t seed, int count, float param, const float *cdf, int categories, void *out)
+{
+    int rc = 0;
+    gsx_arena_t arena = NULL;
+    gsx_arena_desc adesc = { 0 };
+    gsx_tensor_t to = NULL, tc = NULL;
+    gsx_pcg32_t pcg = NULL;
+    int shape[1], cshape[1];
+
+    rc = ensure_backend();
+    if(rc != 0) return rc;
+    shape[0] = count;
+    cshape[0] = categories;
+    adesc.initial_capacity_bytes = (gsx_size_t)count * 4u + (gsx_size_t)categories * 4u + 65536u;
+    TRY(gsx_arena_init(&arena, g_device_type, &adesc));
+    TRY(gsx_pcg32_init(&pcg, (gsx_pcg32_state_t)seed));
+    TRY(make_typed(arena, &to, 1, shape, kind >= 2 ? GSX_DATA_TYPE_I32 : GSX_DATA_TYPE_F32, GSX_STORAGE_FORMAT_CHW,
+        NULL, 0));
+    switch(kind) {
+    case 0: TRY(gsx_pcg32_fill_rand(pcg, to)); break;
+    case 1: TRY(gsx_pcg32_fill_randn(pcg, to, param)); break;
+    case 2: TRY(gsx_pcg32_fill_randint(pcg, to, (uint32_t)param)); break;
+    case 3:
+        TRY(make_typed(arena, &tc, 1, cshape, GSX_DATA_TYPE_F32, GSX_STORAGE_FORMAT_CHW, cdf, (size_t)categories * 4));
+        TRY(gsx_pcg32_multinomial(pcg, to, tc));
+        break;
+    default: rc = (int)GSX_ERROR_OUT_OF_RANGE; goto done;
+    }
+    TRY(gsx_tensor_download(to, out, (size_t)count * 4));
+done:
+    FINISH();
+    if(pcg != NULL) (void)gsx_pcg32_free(pcg);
+    if(to != NULL) (void)gsx_tensor_free(to);
+    if(tc != NULL) (void)gsx_tensor_free(tc);
+    if(arena != NULL) (void)gsx_arena_free(arena);
+    return rc;
+}
+
+/* kind: 0 linear -> sRGB, 1 sRGB -> linear (float32 CHW [3,h,w]); 2 HWC -> CHW, 3 CHW -> HWC
+ * (float32, c channels); 4 float32 -> uint8, 5 uint8 -> float32 (CHW [c,h,w]). */
+int gsxref_image(int kind, int c, int h, int w, const void *src, void *dst)
+{
+    int rc = 0;
+    gsx_arena_t arena = NULL;
+    gsx_arena_desc adesc = { 0 };
+    gsx_tensor_t ts = NULL, td = NULL;
+    int chw[3], hwc[3];
+    size_t n = (size_t)c * h * w;
+
+    rc = ensure_backend();
+    if(rc != 0) return rc;
+    chw[0] = c;
+    chw[1] = h;
+    chw[2] = w;
+    hwc[0] = h;
+    hwc[1] = w;
+    hwc[2] = c;
+    adesc.initial_capacity_bytes = (gsx_size_t)n * 8u + 65536u;
+    TRY(gsx_arena_init(&arena, g_device_type, &adesc));
+    switch(kind) {
+    case 0:
+    case 1:
+        TRY(make_typed(arena, &ts, 3, chw, GSX_DATA_TYPE_F32, GSX_STORAGE_FORMAT_CHW, src, n * 4));
+        TRY(make_typed(arena, &td, 3, chw, GSX_DATA_TYPE_F32, GSX_STORAGE_FORMAT_CHW, NULL, 0));
+        TRY(gsx_tensor_image_convert_colorspace(td, kind == 0 ? GSX_IMAGE_COLOR_SPACE_SRGB : GSX_IMAGE_COLOR_SPACE_LINEAR,
+            ts, kind == 0 ? GSX_IMAGE_COLOR_SPACE_LINEAR : GSX_IMAGE_COLOR_SPACE_SRGB));
+        TRY(gsx_tensor_download(td, dst, n * 4));
+        break;
+    case 2:
+    case 3:
+        TRY(make_typed(arena, &ts, 3, kind == 2 ? hwc : chw, GSX_DATA_TYPE_F32,
+            kind == 2 ? GSX_STORAGE_FORMAT_HWC : GSX_STORAGE_FORMAT_CHW, src, n * 4));
+        TRY(make_typed(arena, &td, 3, kind == 2 ? chw : hwc, GSX_DATA_TYPE_F32,
+            kind == 2 ? GSX_STORAGE_FORMAT_CHW : GSX_STORAGE_FORMAT_HWC, NULL, 0));
+        TRY(gsx_tensor_image_convert_storage_format(td, ts));
+        TRY(gsx_tensor_download(td, dst, n * 4));
+        break;
+    case 4:
+    case 5:
+        TRY(make_typed(arena, &ts, 3, chw, kind == 4 ? GSX_DATA_TYPE_F32 : GSX_DATA_TYPE_U8, GSX_STORAGE_FORMAT_CHW, src,
+            n * (kind == 4 ? 4 : 1)));
+        TRY(make_typed(arena, &td, 3, chw, kind == 4 ? GSX_DATA_TYPE_U8 : GSX_DATA_TYPE_F32, GSX_STORAGE_FORMAT_CHW,
+            NULL, 0));
+        TRY(gsx_tensor_image_convert_data_type(td, ts));
+        TRY(gsx_tensor_download(td, dst, n * (kind == 4 ? 1 : 4)));
+        break;
+    default:
+        rc = (int)GSX_ERROR_OUT_OF_RANGE;
+        break;
+    }
+done:
+    FINISH();
+    if(ts != NULL) (void)gsx_tensor_free(ts);
+    if(td != NULL) (void)gsx_tensor_free(td);
+    if(arena != NULL) (void)gsx_arena_free(arena);
     return rc;
 }

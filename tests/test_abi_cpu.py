@@ -57,3 +57,36 @@ def test_struct_sizes_match_header_layout():
     assert ctypes.sizeof(_lib.AdcParams) == 4 * 9 + 4 + 5 * 8
     assert ctypes.sizeof(_lib.GsRows) == 8 + 8 + 12 * 8 + 16 * 8
     assert ctypes.sizeof(_lib.RenderStats) == 3 * 8 + 6 * 4
+
+
+PLUGIN_PATH = os.path.join(ROOT, "gsx_amd", "libgsx_hip_backend.so")
+
+
+def test_backend_plugin_exports_the_bootstrap():
+    """The gsx backend plugin links libgsx_hip.so and exports the provider bootstrap gsx's
+    registry calls (gsx-backend.c:225-235)."""
+    if not os.path.exists(PLUGIN_PATH):
+        pytest.skip("the plugin is built only where gsx's headers are present")
+    from oracle.oracle import Reference
+    if not Reference.available(hip=True):
+        pytest.skip("oracle/_ref/libgsxref_hip.so was not built")
+    # the plugin's gsx symbols resolve against the core it is linked into
+    lib = ctypes.CDLL(Reference.hip_path)
+    assert hasattr(lib, "gsx_hip_backend_provider_bootstrap")
+
+
+def test_core_with_plugin_runs_cpu_backend_without_device():
+    """Without a device the HIP provider reports NOT_SUPPORTED, the registry keeps the CPU
+    backend, and selecting the GPU slot fails with an error (no fallback)."""
+    import numpy as np
+    import torch
+    from oracle.oracle import Reference
+    if torch.cuda.is_available():
+        pytest.skip("a HIP device is present")
+    if not Reference.available(hip=True):
+        pytest.skip("oracle/_ref/libgsxref_hip.so was not built")
+    cpu = Reference(backend="cpu")
+    assert cpu.device_name() == "cpu0"
+    assert np.array_equal(cpu.reduce("sum", np.ones((2, 5), np.float32), 1), [5.0, 5.0])
+    with pytest.raises(RuntimeError):
+        Reference(backend="hip").device_name()
