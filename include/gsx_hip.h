@@ -295,7 +295,10 @@ gsx_hip_status gsx_hip_loss_mse_f32_backward_kernel_launch(float* grad_predictio
 /* SSIM on [outer, channels, H, W] CHW images; ssim_workspace = 3 * outer*channels*H*W floats
  * written by the forward and read by the backward. fuse_l1 != 0 also applies an L1 term of
  * l1_scale (forward) / l1_grad_scale (backward) first, bit-identical to calling the L1
- * launcher before. */
+ * launcher before. These are not drop-in replacements of gsx_cuda_loss_ssim_* (gsx-cuda/
+ * internal.h:346-369): those take two buffers (ssim_buffer_a/b) and no L1 term; here one
+ * workspace holds the three window moments the backward needs. The gsx loss vtable of this
+ * library (gsx_amd/plugin/hip_loss.c) owns that workspace per loss context. */
 gsx_hip_status gsx_hip_loss_ssim_chw_f32_forward_kernel_launch(float* loss_map, const float* prediction,
                                                                const float* target, int64_t outer_count,
                                                                int32_t channels, int32_t height, int32_t width,
@@ -322,7 +325,12 @@ typedef struct gsx_hip_adam_group {
     double bias_correction1, bias_correction2;
 } gsx_hip_adam_group;
 
-/* Replaces gsx_cuda_adam_step_f32_kernel_launch (gsx/src/gsx-cuda/internal.h:296-311). */
+/* Counterpart of gsx_cuda_adam_step_f32_kernel_launch (gsx/src/gsx-cuda/internal.h:296-311),
+ * with one difference in the contract: this launcher takes the bias corrections themselves,
+ * 1 - beta^step in float64, and divides the moments by them as the CPU backend does
+ * (gsx-cpu/optim.c:740-757); the CUDA vtable passes their float inverses instead
+ * (gsx-cuda/optim.c:792-793), so a caller ported from there must not pass inverses. The gsx
+ * vtable of this library (gsx_amd/plugin/hip_optim.c) calls the multi-group launcher below. */
 gsx_hip_status gsx_hip_adam_step_f32_kernel_launch(float* parameter, const float* gradient, float* first_moment,
                                                    float* second_moment, int64_t total_elements, float beta1,
                                                    float beta2, float learning_rate, float weight_decay,
