@@ -35,10 +35,9 @@ constexpr int kAdcThreads = 256;
 // two-branch sigmoid).
 __device__ inline float adc_sigmoid(float x) { return 1.0f / (1.0f + gsx_expf(-x)); }
 
-// log and cos of float arguments evaluated in double then rounded: correctly rounded for all
-// but astronomically rare inputs, like glibc's logf/cosf.
-__device__ inline float adc_logf(float x) { return (float)log((double)x); }
-__device__ inline float adc_cosf(float x) { return (float)cos((double)x); }
+// glibc's logf and cosf, bit for bit (the restatements of gsx_math.h)
+__device__ inline float adc_logf(float x) { return gsx_logf(x); }
+__device__ inline float adc_cosf(float x) { return gsx_cosf(x); }
 
 __device__ inline float adc_prob_to_logit(float p) {
     // gsx/src/gsx-cpu/adc.c:230-240

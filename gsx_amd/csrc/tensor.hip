@@ -2,10 +2,10 @@
 // buffer (the gsx_backend_buffer_i entries of gsx/src/gsx-impl.h:302-458) as gfx950 kernels.
 //
 // Semantics follow the CPU backend element by element (gsx/src/gsx-cpu/core.c:874-2019):
-//   fills, clamps, gathers, HWC/CHW and u8/f32 conversions, exp / sigmoid / |x| (through the
-//   glibc-exact expf of gsx_math.h) and the pcg32 streams of rand / randint / multinomial are
-//   bit-identical; randn and the sRGB transfer functions call log/cos/sin/pow, evaluated in
-//   double and rounded, within one float ulp of glibc's logf/cosf/sinf/powf; sums (sum, mean,
+//   fills, clamps, gathers, HWC/CHW and u8/f32 conversions, exp / sigmoid / |x|, the pcg32
+//   streams of rand / randn / randint / multinomial and the sRGB transfer functions are
+//   bit-identical (expf, logf, sinf, cosf and powf are the glibc-exact restatements of
+//   gsx_math.h); sums (sum, mean,
 //   mse, mae) accumulate in double in a fixed tree order (deterministic, and at least as
 //   accurate as the CPU's sequential float sum), max keeps the CPU's first-occurrence and NaN
 //   rules exactly.
@@ -87,11 +87,6 @@ __global__ __launch_bounds__(kThreads) void fill_rand_kernel(float* __restrict__
     for (int64_t i = first; i < end; ++i) dst[i] = gsx_pcg32_next_f32(&rng);
 }
 
-// log, cos and sin of float arguments, in double then rounded (within one ulp of glibc's
-// logf/cosf/sinf, which are not correctly rounded either).
-__device__ inline float logf_dr(float x) { return (float)log((double)x); }
-__device__ inline float cosf_dr(float x) { return (float)cos((double)x); }
-__device__ inline float sinf_dr(float x) { return (float)sin((double)x); }
 
 // randn: pair k of elements from draws 2k, 2k+1 by Box-Muller (gsx-cpu/core.c:1009-1064).
 __global__ __launch_bounds__(kThreads) void fill_randn_kernel(float* __restrict__ dst, int64_t count, uint64_t state,
@@ -106,10 +101,10 @@ __global__ __launch_bounds__(kThreads) void fill_randn_kernel(float* __restrict_
         float u1 = gsx_pcg32_next_f32(&rng);
         const float u2 = gsx_pcg32_next_f32(&rng);
         if (u1 < 1e-7f) u1 = 1e-7f;
-        const float radius = sqrtf(-2.0f * logf_dr(u1));
+        const float radius = sqrtf(-2.0f * gsx_logf(u1));
         const float theta = 6.2831853071795864769f * u2;
-        dst[2 * k] = radius * cosf_dr(theta) * sigma;
-        if (2 * k + 1 < count) dst[2 * k + 1] = radius * sinf_dr(theta) * sigma;
+        dst[2 * k] = radius * gsx_cosf(theta) * sigma;
+        if (2 * k + 1 < count) dst[2 * k + 1] = radius * gsx_sinf(theta) * sigma;
     }
 }
 
@@ -329,7 +324,6 @@ __device__ inline float clamp_unit(float v) {
     return v;
 }
 
-__device__ inline float powf_dr(float x, float y) { return (float)pow((double)x, (double)y); }
 
 // gsx-image-impl.h:34-50; DIR 1 linear -> sRGB, 2 sRGB -> linear, 0 copy (a template parameter,
 // as for the unary ops)
@@ -340,10 +334,10 @@ __global__ __launch_bounds__(kThreads) void colorspace_kernel(const float* __res
         float v = src[i];
         if constexpr (DIR == 1) {
             v = clamp_unit(v);
-            v = v <= 0.0031308f ? 12.92f * v : 1.055f * powf_dr(v, 1.0f / 2.4f) - 0.055f;
+            v = v <= 0.0031308f ? 12.92f * v : 1.055f * gsx_powf(v, 1.0f / 2.4f) - 0.055f;
         } else if constexpr (DIR == 2) {
             v = clamp_unit(v);
-            v = v <= 0.04045f ? v / 12.92f : powf_dr((v + 0.055f) / 1.055f, 2.4f);
+            v = v <= 0.04045f ? v / 12.92f : gsx_powf((v + 0.055f) / 1.055f, 2.4f);
         }
         dst[i] = v;
     }

@@ -237,8 +237,8 @@ gsx_hip_status gsx_hip_fill_pattern(void* dst, size_t bytes, const void* pattern
                                     hipStream_t stream);
 /* Element i = pcg32_next_float of draw i of the (state, inc) stream (fill_rand_tensor). */
 gsx_hip_status gsx_hip_fill_rand_f32(float* dst, int64_t count, uint64_t state, uint64_t inc, hipStream_t stream);
-/* Box-Muller pairs from draws 2k, 2k+1, times sigma (fill_randn_tensor); log/cos/sin within one
- * float ulp of glibc's. */
+/* Box-Muller pairs from draws 2k, 2k+1, times sigma (fill_randn_tensor); logf / cosf / sinf are
+ * glibc's, bit for bit, so the fill equals the CPU backend's. */
 gsx_hip_status gsx_hip_fill_randn_f32(float* dst, int64_t count, uint64_t state, uint64_t inc, float sigma,
                                       hipStream_t stream);
 /* fill_randint_tensor: element i = the i-th draw that pcg32_next_uint_bound accepts, mod bound,
@@ -265,7 +265,7 @@ gsx_hip_status gsx_hip_clamp_inplace(void* x, int64_t count, int32_t data_type, 
 size_t gsx_hip_reduce_temp_bytes(int64_t outer, int64_t reduce);
 gsx_hip_status gsx_hip_reduce_f32(const float* x, const float* y, int64_t outer, int64_t reduce, int32_t op,
                                   float* out, void* temp, hipStream_t stream);
-/* image_convert_colorspace (sRGB transfer curves, powf within one float ulp of glibc's),
+/* image_convert_colorspace (sRGB transfer curves with glibc's powf, bit for bit),
  * image_convert_storage_format (HWC <-> CHW for 1/2/4-byte elements) and
  * image_convert_data_type (f32 <-> u8), gsx/src/extra/gsx-image-impl.h:9-170. */
 gsx_hip_status gsx_hip_image_colorspace_f32(const float* src, float* dst, int64_t count, int32_t src_srgb,
@@ -344,8 +344,9 @@ gsx_hip_status gsx_hip_adam_step_multi_launch(const gsx_hip_adam_group* groups, 
 /* ---- adaptive density control -----------------------------------------------------------------
  * Replaces the CUDA thrust pipeline (gsx/src/gsx-cuda/adc.cu:757-927) with the semantics of
  * the CPU default/ABSGS refine and opacity reset (gsx/src/gsx-cpu/adc/default.c:160-527,
- * gsx/src/gsx-cpu/adc.c:48-80, 380-559): identical grow/split/prune decisions and row order;
- * split k draws the CPU's pcg32 stream advanced by 12 * k draws. */
+ * gsx/src/gsx-cpu/adc.c:48-80, 380-559): identical grow/split/prune decisions, row order and
+ * rows (the split normals use glibc's logf / cosf bit for bit); split k draws the CPU's pcg32
+ * stream advanced by 12 * k draws. */
 #define GSX_HIP_ADC_MAX_FIELDS 16
 typedef struct gsx_hip_adc_params {
     int32_t algorithm; /* 0 GSX_ADC_ALGORITHM_DEFAULT, 1 GSX_ADC_ALGORITHM_ABSGS */

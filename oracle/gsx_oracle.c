@@ -1597,6 +1597,81 @@ uint64_t oracle_expf_mismatches(uint32_t lo_bits, uint32_t hi_bits, uint32_t str
     return bad;
 }
 
+/* Mismatches of the logf / sinf / cosf restatements (which: 0 logf, 1 sinf, 2 cosf) against the
+ * host libm over float bit patterns lo..hi in steps of `stride` (both NaN counts as equal).
+ * OpenMP over the range: an exhaustive sweep of all 2^32 patterns takes a few seconds. */
+uint64_t oracle_libm_mismatches(int which, uint32_t lo_bits, uint32_t hi_bits, uint32_t stride)
+{
+    uint64_t bad = 0;
+    int64_t count, j;
+
+    if(stride == 0) stride = 1;
+    if(hi_bits < lo_bits) return 0;
+    count = ((int64_t)hi_bits - (int64_t)lo_bits) / (int64_t)stride + 1;
+#pragma omp parallel for reduction(+ : bad) schedule(static)
+    for(j = 0; j < count; ++j) {
+        const float x = gsx_f32_from_bits((uint32_t)((int64_t)lo_bits + j * (int64_t)stride));
+        const float a = which == 0 ? logf(x) : (which == 1 ? sinf(x) : cosf(x));
+        const float b = which == 0 ? gsx_logf(x) : (which == 1 ? gsx_sinf(x) : gsx_cosf(x));
+
+        if(gsx_f32_bits(a) != gsx_f32_bits(b) && !(a != a && b != b)) {
+            bad += 1;
+        }
+    }
+    return bad;
+}
+
+/* Mismatches of gsx_powf against the host powf: `count` pseudo-random (x, y) bit patterns from
+ * a xorshift64 stream seeded with `seed` (every other y drawn from the quarter-integers in
+ * [-8, 8), so integer exponents and negative bases meet), plus, when domain != 0, every 53rd
+ * float in [0, 1] with y = 1/k and k + 1 for k = 1..51. */
+uint64_t oracle_powf_mismatches(uint64_t seed, int64_t count, int domain)
+{
+    uint64_t bad = 0;
+    int64_t i;
+
+#pragma omp parallel for reduction(+ : bad) schedule(static)
+    for(i = 0; i < count; ++i) {
+        uint64_t s = seed + 0x9e3779b97f4a7c15ull * (uint64_t)(i + 1);
+        float x, y, a, b;
+
+        s ^= s << 13;
+        s ^= s >> 7;
+        s ^= s << 17;
+        x = gsx_f32_from_bits((uint32_t)s);
+        y = gsx_f32_from_bits((uint32_t)(s >> 32));
+        if(i & 1) y = (float)((s >> 40) % 64u) * 0.25f - 8.0f;
+        a = powf(x, y);
+        b = gsx_powf(x, y);
+        if(gsx_f32_bits(a) != gsx_f32_bits(b) && !(a != a && b != b)) {
+            bad += 1;
+        }
+    }
+    if(domain) {
+        int k;
+
+#pragma omp parallel for reduction(+ : bad) schedule(dynamic)
+        for(k = 1; k <= 51; ++k) {
+            const float ys[2] = { 1.0f / (float)k, (float)(k + 1) };
+            int j;
+
+            for(j = 0; j < 2; ++j) {
+                uint32_t u;
+
+                for(u = 0; u <= 0x3f800000u; u += 53) {
+                    const float a = powf(gsx_f32_from_bits(u), ys[j]);
+                    const float b = gsx_powf(gsx_f32_from_bits(u), ys[j]);
+
+                    if(gsx_f32_bits(a) != gsx_f32_bits(b)) {
+                        bad += 1;
+                    }
+                }
+            }
+        }
+    }
+    return bad;
+}
+
 /* ---------------------------------------------------------------------------------------
  * Tiled evaluation for full-size scenes (configs 3 and 4: 3M and 6M Gaussians at 1080p,
  * where the per-Gaussian raster above walks 4e9 and 2e11 box pixels). Same arithmetic as

@@ -80,6 +80,10 @@ class Oracle:
         lib.oracle_expf_mismatches.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32]
         lib.oracle_expf_blend_mismatches.restype = ctypes.c_uint64
         lib.oracle_expf_blend_mismatches.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32]
+        lib.oracle_libm_mismatches.restype = ctypes.c_uint64
+        lib.oracle_libm_mismatches.argtypes = [ctypes.c_int, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32]
+        lib.oracle_powf_mismatches.restype = ctypes.c_uint64
+        lib.oracle_powf_mismatches.argtypes = [ctypes.c_uint64, ctypes.c_int64, ctypes.c_int]
         lib.oracle_tiled.restype = _i64
         lib.oracle_tiled.argtypes = [_i64, ctypes.c_int] + [_vp] * 9 + [ctypes.c_int32, ctypes.c_int, _vp, _vp,
                                                                          _vp, _vp]
@@ -248,6 +252,14 @@ class Oracle:
 
     def expf_blend_mismatches(self, lo_bits, hi_bits, stride=1):
         return int(self.lib.oracle_expf_blend_mismatches(lo_bits, hi_bits, stride))
+
+    def libm_mismatches(self, name, lo_bits=0, hi_bits=0xFFFFFFFF, stride=1):
+        """Mismatches of gsx_logf / gsx_sinf / gsx_cosf against the host libm."""
+        which = {"logf": 0, "sinf": 1, "cosf": 2}[name]
+        return int(self.lib.oracle_libm_mismatches(which, lo_bits, hi_bits, stride))
+
+    def powf_mismatches(self, seed, count, domain=False):
+        return int(self.lib.oracle_powf_mismatches(seed, count, 1 if domain else 0))
 
 
 class _OnBackend:

@@ -2,19 +2,16 @@
 (restatement of gsx/src/gsx-cpu/adc/default.c and adc.c, itself checked bit-exact against the
 reference CPU backend in test_oracle_cpu.py).
 
-Counts, the surviving row order and every non-split row are compared bit-exact. Split rows
-carry Box-Muller offsets and logf results: the GPU evaluates log/cos in float64 and rounds, the
-oracle calls glibc logf/cosf; both are correctly rounded in all but rare inputs, so split rows
-are held to 2 ulp-scale tolerances (rtol 1e-6, atol 1e-7)."""
+Counts, the surviving row order and every row are compared bit-exact, split rows included: the
+split offsets come from Box-Muller normals whose logf / cosf are the glibc-exact restatements of
+gsx_math.h (checked against the host libm in test_oracle_cpu.py), so they equal the oracle's
+glibc results bit for bit."""
 import numpy as np
 import pytest
 
 pytestmark = pytest.mark.gpu
 
 torch = pytest.importorskip("torch")
-
-SPLIT_RTOL = 1e-6
-SPLIT_ATOL = 1e-7
 
 
 def _scene(n, seed):
@@ -78,14 +75,8 @@ def test_adc_step_matches_oracle(oracle, algorithm, step, max_num, n):
                                                {k: v.copy() for k, v in aux.items()}, op, cap)
     assert count == ref_f["mean3d"].shape[0]
     assert list(counts) == list(ref_counts)
-    # rows produced by a split differ only within the log/cos rounding tolerance
-    for k in ("rotation", "sh0"):
+    for k in ("rotation", "sh0", "mean3d", "logscale", "opacity"):
         assert np.array_equal(res_f[k][:count].cpu().numpy().reshape(ref_f[k].shape), ref_f[k]), k
-    for k in ("mean3d", "logscale", "opacity"):
-        got = res_f[k][:count].cpu().numpy().reshape(ref_f[k].shape)
-        exact = got == ref_f[k]
-        assert np.allclose(got, ref_f[k], rtol=SPLIT_RTOL, atol=SPLIT_ATOL), k
-        assert exact.mean() > 0.9, k  # only split rows may differ
     for k in ref_m:
         for j in (0, 1):
             got = res_m[k][j][:count].cpu().numpy().reshape(ref_m[k][j].shape)
@@ -140,7 +131,7 @@ def test_adc_rng_persists_across_steps(oracle):
     assert n2 == f2["mean3d"].shape[0] and list(c2) == list(k2)
     for k in widths:
         got = res[k][:n2].cpu().numpy().reshape(f2[k].shape)
-        assert np.allclose(got, f2[k], rtol=SPLIT_RTOL, atol=SPLIT_ATOL), k
+        assert np.array_equal(got, f2[k]), k
 
 
 def test_gather_rows(oracle):

@@ -208,6 +208,22 @@ def test_expf_restatement_matches_libm(oracle):
     assert oracle.expf_mismatches(0x00000000, 0xFFFFFFFF, 977) == 0  # everything else, sampled
 
 
+@pytest.mark.parametrize("name", ["logf", "sinf", "cosf"])
+def test_logf_sincosf_restatements_match_libm(oracle, name):
+    """gsx_logf / gsx_sinf / gsx_cosf (gsx_math.h, ARM optimized-routines as glibc ships them) ==
+    host libm: every float of the ADC / randn domain [0, 2pi], every 3rd of [-2pi, 0], every
+    97th pattern elsewhere (the full 2^32 sweep was run once with zero mismatches)."""
+    assert oracle.libm_mismatches(name, 0x00000000, 0x40C90FDB) == 0      # [0, 2pi]
+    assert oracle.libm_mismatches(name, 0x80000000, 0xC0C90FDB, 3) == 0   # [-2pi, -0]
+    assert oracle.libm_mismatches(name, 0x00000000, 0xFFFFFFFF, 97) == 0
+
+
+def test_powf_restatement_matches_libm(oracle):
+    """gsx_powf == host powf over 4M random pairs (integer and fractional exponents, negative,
+    subnormal, zero, inf and NaN bases) and the MCMC exponents 1/k, k + 1 over [0, 1]."""
+    assert oracle.powf_mismatches(1234567, 4_000_000, domain=True) == 0
+
+
 def test_expf_blend_table_matches_libm(oracle):
     """gsx_expf_blend (exponent folded into a 209-entry table, the blend kernels' expf) == host
     expf for every float of its domain [-4.5, 0], -0 and the subnormals included; the endpoints
