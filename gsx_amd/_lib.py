@@ -90,7 +90,7 @@ class AdcParams(ctypes.Structure):
                 ("max_world_scale", _f), ("max_screen_scale", _f), ("duplicate_grad_threshold", _f),
                 ("duplicate_scale_threshold", _f), ("duplicate_absgrad_threshold", _f), ("scene_scale", _f),
                 ("refine_every", _i64), ("start_refine", _i64), ("end_refine", _i64), ("max_num_gaussians", _i64),
-                ("reset_every", _i64)]
+                ("reset_every", _i64), ("noise_strength", _f), ("grow_ratio", _f), ("mean3d_learning_rate", _f)]
 
 
 class GsRows(ctypes.Structure):

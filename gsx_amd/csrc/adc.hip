@@ -225,6 +225,171 @@ __global__ __launch_bounds__(kAdcThreads) void adc_reset_opacity_kernel(int64_t 
     if (v != nullptr) v[i] = 0.0f;
 }
 
+// ---- MCMC (gsx/src/gsx-cpu/adc/mcmc.c) ---------------------------------------------------------
+
+// mcmc.c:13-18: logistic gate that lets only nearly transparent Gaussians move
+__device__ inline float mcmc_noise_gate(float opacity) {
+    const float shifted = (1.0f - opacity) - 0.995f;
+    return 1.0f / (1.0f + gsx_expf(-100.0f * shifted));
+}
+
+// mcmc.c:345-451 for Gaussian i: three normals from draws 6i..6i+5 of the step's stream, shaped
+// by R diag(s^2) R^T, scaled by the gate and noise_strength * lr, added to mean3d.
+__global__ __launch_bounds__(kAdcThreads) void mcmc_noise_kernel(int64_t n, float noise_lr,
+                                                                 float* __restrict__ mean3d,
+                                                                 const float* __restrict__ rotation,
+                                                                 const float* __restrict__ logscale,
+                                                                 const float* __restrict__ opacity,
+                                                                 uint64_t rng_state, uint64_t rng_inc) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float op = adc_sigmoid(opacity[i]);
+    const float gate = mcmc_noise_gate(op);
+    const float sx = gsx_expf(logscale[i * 3 + 0]), sy = gsx_expf(logscale[i * 3 + 1]),
+                sz = gsx_expf(logscale[i * 3 + 2]);
+    float qx = rotation[i * 4 + 0], qy = rotation[i * 4 + 1], qz = rotation[i * 4 + 2], qw = rotation[i * 4 + 3];
+    gsx_amd_pcg32 rng;
+    rng.state = rng_state;
+    rng.inc = rng_inc;
+    gsx_pcg32_advance(&rng, 6ull * (uint64_t)i);
+    const float nx = adc_next_normal(&rng), ny = adc_next_normal(&rng), nz = adc_next_normal(&rng);
+    const float qn = sqrtf(qx * qx + qy * qy + qz * qz + qw * qw);
+    if (qn > 1e-8f) {
+        const float iq = 1.0f / qn;
+        qx *= iq;
+        qy *= iq;
+        qz *= iq;
+        qw *= iq;
+    }
+    const float m00 = 1.0f - 2.0f * (qy * qy + qz * qz), m01 = 2.0f * (qx * qy - qw * qz),
+                m02 = 2.0f * (qx * qz + qw * qy);
+    const float m10 = 2.0f * (qx * qy + qw * qz), m11 = 1.0f - 2.0f * (qx * qx + qz * qz),
+                m12 = 2.0f * (qy * qz - qw * qx);
+    const float m20 = 2.0f * (qx * qz - qw * qy), m21 = 2.0f * (qy * qz + qw * qx),
+                m22 = 1.0f - 2.0f * (qx * qx + qy * qy);
+    const float c00 = m00 * m00 * sx * sx + m01 * m01 * sy * sy + m02 * m02 * sz * sz;
+    const float c01 = m00 * m10 * sx * sx + m01 * m11 * sy * sy + m02 * m12 * sz * sz;
+    const float c02 = m00 * m20 * sx * sx + m01 * m21 * sy * sy + m02 * m22 * sz * sz;
+    const float c11 = m10 * m10 * sx * sx + m11 * m11 * sy * sy + m12 * m12 * sz * sz;
+    const float c12 = m10 * m20 * sx * sx + m11 * m21 * sy * sy + m12 * m22 * sz * sz;
+    const float c22 = m20 * m20 * sx * sx + m21 * m21 * sy * sy + m22 * m22 * sz * sz;
+    const float snx = nx * gate * noise_lr, sny = ny * gate * noise_lr, snz = nz * gate * noise_lr;
+    mean3d[i * 3 + 0] = mean3d[i * 3 + 0] + (c00 * snx + c01 * sny + c02 * snz);
+    mean3d[i * 3 + 1] = mean3d[i * 3 + 1] + (c01 * snx + c11 * sny + c12 * snz);
+    mean3d[i * 3 + 2] = mean3d[i * 3 + 2] + (c02 * snx + c12 * sny + c22 * snz);
+}
+
+// draw weight sigmoid(opacity) of every row and whether it is dead (mcmc.c:502-511)
+__global__ __launch_bounds__(kAdcThreads) void mcmc_weight_kernel(int64_t n, float threshold,
+                                                                  const float* __restrict__ opacity,
+                                                                  float* __restrict__ weight,
+                                                                  uint32_t* __restrict__ dead) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float w = adc_sigmoid(opacity[i]);
+    weight[i] = w;
+    if (dead != nullptr) dead[i] = w <= threshold ? 1u : 0u;
+}
+
+// dead rows in index order to dead_idx, live rows (and their weights) to live_idx / live_w
+__global__ __launch_bounds__(kAdcThreads) void mcmc_split_kernel(int64_t n, const uint32_t* __restrict__ dead,
+                                                                 const uint32_t* __restrict__ dead_rank,
+                                                                 const float* __restrict__ weight,
+                                                                 uint32_t* __restrict__ dead_idx,
+                                                                 uint32_t* __restrict__ live_idx,
+                                                                 float* __restrict__ live_w) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const uint32_t r = dead_rank[i];
+    if (dead[i]) {
+        dead_idx[r] = (uint32_t)i;
+    } else {
+        live_idx[i - r] = (uint32_t)i;
+        live_w[i - r] = weight[i];
+    }
+}
+
+// source row of draw j (through the live list when given) and the per-row draw counts
+__global__ __launch_bounds__(kAdcThreads) void mcmc_count_kernel(int64_t draws, const int32_t* __restrict__ sample,
+                                                                 const uint32_t* __restrict__ live_idx,
+                                                                 uint32_t* __restrict__ src,
+                                                                 uint32_t* __restrict__ counts) {
+    const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= draws) return;
+    const uint32_t s = live_idx != nullptr ? live_idx[sample[j]] : (uint32_t)sample[j];
+    src[j] = s;
+    atomicAdd(&counts[s], 1u);
+}
+
+// C(n, k) in double, then float (mcmc.c:20-38)
+__device__ inline float mcmc_binom(uint32_t n, uint32_t k) {
+    if (k > n) return 0.0f;
+    if (k == 0 || k == n) return 1.0f;
+    if (k > n - k) k = n - k;
+    double v = 1.0;
+    for (uint32_t j = 1; j <= k; ++j) v = v * (double)(n - (k - j)) / (double)j;
+    return (float)v;
+}
+
+// mcmc.c:283-343 for a source row drawn c > 0 times (ratio c + 1, at most 51): the opacity that
+// c + 1 copies share, and the scale factor that keeps their summed footprint
+__global__ __launch_bounds__(kAdcThreads) void mcmc_relocate_kernel(int64_t n, float min_opacity,
+                                                                    const uint32_t* __restrict__ counts,
+                                                                    float* __restrict__ opacity,
+                                                                    float* __restrict__ logscale) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const uint32_t c = counts[i];
+    if (c == 0u) return;
+    const float so = adc_sigmoid(opacity[i]);
+    const float sx = gsx_expf(logscale[i * 3 + 0]), sy = gsx_expf(logscale[i * 3 + 1]),
+                sz = gsx_expf(logscale[i * 3 + 2]);
+    uint32_t ratio = c + 1u;
+    if (ratio > 51u) ratio = 51u;
+    float clamped = so;
+    if (clamped < 0.0f) clamped = 0.0f;
+    if (clamped > 1.0f - 1e-6f) clamped = 1.0f - 1e-6f;
+    float new_op = 1.0f - gsx_powf(1.0f - clamped, 1.0f / (float)ratio);
+    float denom = 0.0f;
+    for (uint32_t a = 1; a <= ratio; ++a) {
+        for (uint32_t k = 0; k < a; ++k) {
+            const float sign = (k % 2u) == 0u ? 1.0f : -1.0f;
+            const float coeff = mcmc_binom(a - 1u, k);
+            const float power = gsx_powf(new_op, (float)(k + 1u));
+            denom += coeff * sign * power / sqrtf((float)(k + 1u));
+        }
+    }
+    const float scale_coeff = fabsf(denom) <= 1e-8f ? 1.0f : so / denom;
+    if (new_op < min_opacity) new_op = min_opacity;
+    if (new_op > 1.0f - 1e-6f) new_op = 1.0f - 1e-6f;
+    opacity[i] = adc_prob_to_logit(new_op);
+    logscale[i * 3 + 0] = adc_logf(sx * scale_coeff);
+    logscale[i * 3 + 1] = adc_logf(sy * scale_coeff);
+    logscale[i * 3 + 2] = adc_logf(sz * scale_coeff);
+}
+
+// row dst[j] = row src[j] over the parameter fields (dst = dead_idx for a relocation, or the
+// appended rows n + j when dst is null), and the optimizer moments of row zero[j] (the source of
+// a relocation, the appended row of a growth) cleared
+__global__ __launch_bounds__(kAdcThreads) void mcmc_copy_kernel(int64_t draws, int64_t n,
+                                                                const uint32_t* __restrict__ dst,
+                                                                const uint32_t* __restrict__ src, RowSet rows,
+                                                                RowSet moments, int zero_source_moments) {
+    const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= draws) return;
+    const int64_t s = src[j];
+    const int64_t t = dst != nullptr ? (int64_t)dst[j] : n + j;
+    for (int f = 0; f < rows.count; ++f) {
+        const int w = rows.w[f];
+        for (int c = 0; c < w; ++c) rows.f[f][t * w + c] = rows.f[f][s * w + c];
+    }
+    const int64_t z = zero_source_moments ? s : t;
+    for (int f = 0; f < moments.count; ++f) {
+        const int w = moments.w[f];
+        for (int c = 0; c < w; ++c) moments.f[f][z * w + c] = 0.0f;
+    }
+}
+
 __global__ __launch_bounds__(256) void gather_rows_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
                                                           int64_t row_bytes, int64_t row_count,
                                                           const int32_t* __restrict__ index, int64_t src_rows,
@@ -386,7 +551,175 @@ struct gsx_hip_adc_context {
     gsx_amd_pcg32 rng;
     Scratch scratch;
     uint32_t* host = nullptr;  // pinned readback slots
+    float* host_cdf = nullptr;  // pinned draw weights / cumulative sums of the MCMC draws
+    size_t host_cdf_floats = 0;
 };
+
+namespace {
+
+// MCMC position noise (gsx/src/gsx-cpu/adc/mcmc.c:345-451): none past end_refine or without
+// noise strength; otherwise 6 draws per Gaussian from the context's stream.
+gsx_hip_status mcmc_noise(gsx_hip_adc_context* ctx, const gsx_hip_adc_params& p, uint64_t global_step,
+                          gsx_hip_gs_rows* rows, hipStream_t stream) {
+    const int64_t n = rows->count;
+    if (!(p.noise_strength > 0.0f) || n <= 0) return GSX_HIP_SUCCESS;
+    if (p.end_refine > 0 && global_step >= (uint64_t)p.end_refine) return GSX_HIP_SUCCESS;
+    const float noise_lr = p.noise_strength * p.mean3d_learning_rate;
+    hipLaunchKernelGGL(mcmc_noise_kernel, dim3(adc_blocks(n)), dim3(kAdcThreads), 0, stream, n, noise_lr, rows->mean3d,
+                       rows->rotation, rows->logscale, rows->opacity, ctx->rng.state, ctx->rng.inc);
+    ADC_HIP_TRY(hipGetLastError());
+    gsx_pcg32_advance(&ctx->rng, 6ull * (uint64_t)n);
+    return GSX_HIP_SUCCESS;
+}
+
+// cdf[0..count) = running float sum of max(w, 0) in index order, the exact sums of the CPU
+// backend's sampler (mcmc.c:137-140); the weights come from the device, the sums go back.
+gsx_hip_status mcmc_cdf(gsx_hip_adc_context* ctx, const float* weight, int64_t count, float* cdf, hipStream_t stream) {
+    if ((size_t)count > ctx->host_cdf_floats) {
+        if (ctx->host_cdf != nullptr) {
+            ADC_HIP_TRY(hipStreamSynchronize(stream));
+            (void)hipHostFree(ctx->host_cdf);
+            ctx->host_cdf = nullptr;
+            ctx->host_cdf_floats = 0;
+        }
+        const size_t grow = (size_t)count + (size_t)count / 4 + 1024;
+        ADC_HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&ctx->host_cdf), grow * sizeof(float), hipHostMallocDefault));
+        ctx->host_cdf_floats = grow;
+    }
+    float* h = ctx->host_cdf;
+    ADC_HIP_TRY(hipMemcpyAsync(h, weight, (size_t)count * sizeof(float), hipMemcpyDeviceToHost, stream));
+    ADC_HIP_TRY(hipStreamSynchronize(stream));
+    float total = 0.0f;
+    for (int64_t j = 0; j < count; ++j) {
+        total += h[j] > 0.0f ? h[j] : 0.0f;
+        h[j] = total;
+    }
+    if (!(total > 0.0f)) {
+        return adc_fail(GSX_HIP_ERROR_INVALID_STATE, "mcmc weighted sampling requires positive opacity mass");
+    }
+    ADC_HIP_TRY(hipMemcpyAsync(cdf, h, (size_t)count * sizeof(float), hipMemcpyHostToDevice, stream));
+    return GSX_HIP_SUCCESS;
+}
+
+// MCMC refine (mcmc.c:453-766): relocate the dead rows, then grow; rows are appended in place.
+gsx_hip_status mcmc_refine(gsx_hip_adc_context* ctx, const gsx_hip_adc_params& p, gsx_hip_gs_rows* rows,
+                           int64_t capacity, int64_t* result_count, int64_t* out_counts, hipStream_t stream) {
+    const int64_t n = rows->count;
+    // the growth target: floor(n (1 + grow_ratio)) in double, capped at max_num_gaussians
+    int64_t target = n;
+    if (p.max_num_gaussians > 0 && p.grow_ratio > 0.0f) {
+        double t = floor((double)n * (1.0 + (double)p.grow_ratio));
+        if (t > (double)p.max_num_gaussians) t = (double)p.max_num_gaussians;
+        if (t > (double)n) target = (int64_t)t;
+    }
+    if (capacity < target) return adc_fail(GSX_HIP_ERROR_OUT_OF_RANGE, "row capacity below the mcmc growth target");
+    const int64_t draws_max = n > target - n ? n : target - n;
+    // scratch: weight[n] | dead[n] | dead_rank[n+1] | dead_idx[n] | live_idx[n] | live_w[n] |
+    //          cdf[n] | sample[draws] | src[draws] | counts[n] | scan temp
+    const size_t a = 256;
+    auto up = [&](size_t x) { return (x + a - 1) / a * a; };
+    size_t off = 0;
+    const size_t o_w = off;
+    off += up((size_t)n * 4);
+    const size_t o_dead = off;
+    off += up((size_t)n * 4);
+    const size_t o_drank = off;
+    off += up((size_t)(n + 1) * 4);
+    const size_t o_didx = off;
+    off += up((size_t)n * 4);
+    const size_t o_lidx = off;
+    off += up((size_t)n * 4);
+    const size_t o_lw = off;
+    off += up((size_t)n * 4);
+    const size_t o_cdf = off;
+    off += up((size_t)n * 4);
+    const size_t o_samp = off;
+    off += up((size_t)draws_max * 4);
+    const size_t o_src = off;
+    off += up((size_t)draws_max * 4);
+    const size_t o_cnt = off;
+    off += up((size_t)n * 4);
+    const size_t o_temp = off;
+    off += up(gsx_hip_scan_temp_bytes(n));
+    ADC_TRY(ctx->scratch.reserve(off));
+    uint8_t* base = static_cast<uint8_t*>(ctx->scratch.ptr);
+    float* weight = reinterpret_cast<float*>(base + o_w);
+    uint32_t* dead = reinterpret_cast<uint32_t*>(base + o_dead);
+    uint32_t* drank = reinterpret_cast<uint32_t*>(base + o_drank);
+    uint32_t* didx = reinterpret_cast<uint32_t*>(base + o_didx);
+    uint32_t* lidx = reinterpret_cast<uint32_t*>(base + o_lidx);
+    float* lw = reinterpret_cast<float*>(base + o_lw);
+    float* cdf = reinterpret_cast<float*>(base + o_cdf);
+    int32_t* sample = reinterpret_cast<int32_t*>(base + o_samp);
+    uint32_t* src = reinterpret_cast<uint32_t*>(base + o_src);
+    uint32_t* counts = reinterpret_cast<uint32_t*>(base + o_cnt);
+    void* temp = base + o_temp;
+    int d0, d1, d2, d3;
+    const RowSet prow = param_rows(*rows, &d0, &d1, &d2, &d3, false);
+    const RowSet mrow = moment_rows(*rows);
+
+    hipLaunchKernelGGL(mcmc_weight_kernel, dim3(adc_blocks(n)), dim3(kAdcThreads), 0, stream, n,
+                       p.pruning_opacity_threshold, rows->opacity, weight, dead);
+    ADC_HIP_TRY(hipGetLastError());
+    ADC_TRY(gsx_hip_scan_exclusive_u32(dead, drank, n, temp, stream));
+    ADC_HIP_TRY(hipMemcpyAsync(ctx->host, drank + n, sizeof(uint32_t), hipMemcpyDeviceToHost, stream));
+    ADC_HIP_TRY(hipStreamSynchronize(stream));
+    const int64_t dead_count = ctx->host[0];
+    out_counts[0] = dead_count;
+    if (dead_count == n) {
+        return adc_fail(GSX_HIP_ERROR_INVALID_STATE, "mcmc relocate requires at least one live gaussian");
+    }
+    if (dead_count > 0) {
+        const int64_t live = n - dead_count;
+        hipLaunchKernelGGL(mcmc_split_kernel, dim3(adc_blocks(n)), dim3(kAdcThreads), 0, stream, n, dead, drank,
+                           weight, didx, lidx, lw);
+        ADC_HIP_TRY(hipGetLastError());
+        ADC_TRY(mcmc_cdf(ctx, lw, live, cdf, stream));
+        ADC_TRY(gsx_hip_multinomial_i32(sample, dead_count, cdf, live, ctx->rng.state, ctx->rng.inc, stream));
+        gsx_pcg32_advance(&ctx->rng, (uint64_t)dead_count);
+        hipLaunchKernelGGL(adc_fill_kernel, dim3(adc_blocks(n)), dim3(kAdcThreads), 0, stream,
+                           reinterpret_cast<float*>(counts), n);
+        hipLaunchKernelGGL(mcmc_count_kernel, dim3(adc_blocks(dead_count)), dim3(kAdcThreads), 0, stream, dead_count,
+                           sample, lidx, src, counts);
+        hipLaunchKernelGGL(mcmc_relocate_kernel, dim3(adc_blocks(n)), dim3(kAdcThreads), 0, stream, n,
+                           p.pruning_opacity_threshold, counts, rows->opacity, rows->logscale);
+        hipLaunchKernelGGL(mcmc_copy_kernel, dim3(adc_blocks(dead_count)), dim3(kAdcThreads), 0, stream, dead_count,
+                           n, didx, src, prow, mrow, 1);
+        ADC_HIP_TRY(hipGetLastError());
+        out_counts[2] += dead_count;
+    }
+    if (target > n) {
+        const int64_t growth = target - n;
+        hipLaunchKernelGGL(mcmc_weight_kernel, dim3(adc_blocks(n)), dim3(kAdcThreads), 0, stream, n,
+                           p.pruning_opacity_threshold, rows->opacity, weight, nullptr);
+        ADC_HIP_TRY(hipGetLastError());
+        ADC_TRY(mcmc_cdf(ctx, weight, n, cdf, stream));
+        ADC_TRY(gsx_hip_multinomial_i32(sample, growth, cdf, n, ctx->rng.state, ctx->rng.inc, stream));
+        gsx_pcg32_advance(&ctx->rng, (uint64_t)growth);
+        hipLaunchKernelGGL(adc_fill_kernel, dim3(adc_blocks(n)), dim3(kAdcThreads), 0, stream,
+                           reinterpret_cast<float*>(counts), n);
+        hipLaunchKernelGGL(mcmc_count_kernel, dim3(adc_blocks(growth)), dim3(kAdcThreads), 0, stream, growth, sample,
+                           nullptr, src, counts);
+        hipLaunchKernelGGL(mcmc_relocate_kernel, dim3(adc_blocks(n)), dim3(kAdcThreads), 0, stream, n,
+                           p.pruning_opacity_threshold, counts, rows->opacity, rows->logscale);
+        hipLaunchKernelGGL(mcmc_copy_kernel, dim3(adc_blocks(growth)), dim3(kAdcThreads), 0, stream, growth, n,
+                           nullptr, src, prow, mrow, 0);
+        ADC_HIP_TRY(hipGetLastError());
+        out_counts[2] += growth;
+    }
+    *result_count = target;
+    // gsx/src/gsx-cpu/adc.c:430-436: the auxiliary statistics restart after a refine
+    float* aux[4] = {rows->grad_acc, rows->absgrad_acc, rows->visible_counter, rows->max_screen_radius};
+    for (float* a2 : aux) {
+        if (a2 != nullptr) {
+            hipLaunchKernelGGL(adc_fill_kernel, dim3(adc_blocks(target)), dim3(kAdcThreads), 0, stream, a2, target);
+        }
+    }
+    ADC_HIP_TRY(hipGetLastError());
+    return GSX_HIP_SUCCESS;
+}
+
+}  // namespace
 
 extern "C" {
 
@@ -409,6 +742,7 @@ gsx_hip_status gsx_hip_adc_context_destroy(gsx_hip_adc_context* ctx) {
     if (ctx == nullptr) return adc_fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "context must be non-null");
     if (ctx->scratch.ptr != nullptr) (void)hipFree(ctx->scratch.ptr);
     if (ctx->host != nullptr) (void)hipHostFree(ctx->host);
+    if (ctx->host_cdf != nullptr) (void)hipHostFree(ctx->host_cdf);
     delete ctx;
     return GSX_HIP_SUCCESS;
 }
@@ -421,8 +755,12 @@ gsx_hip_status gsx_hip_adc_step(gsx_hip_adc_context* ctx, const gsx_hip_adc_para
         return adc_fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "adc arguments must be non-null");
     }
     const gsx_hip_adc_params& p = *params;
-    if (p.algorithm != 0 && p.algorithm != 1) return adc_fail(GSX_HIP_ERROR_NOT_SUPPORTED, "adc algorithm");
-    if (!(p.scene_scale > 0.0f)) return adc_fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "scene_scale must be positive");
+    if (p.algorithm != 0 && p.algorithm != 1 && p.algorithm != 2) {
+        return adc_fail(GSX_HIP_ERROR_NOT_SUPPORTED, "adc algorithm");
+    }
+    if (p.algorithm != 2 && !(p.scene_scale > 0.0f)) {
+        return adc_fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "scene_scale must be positive");
+    }
     const int64_t n = rows->count;
     if (rows->mean3d == nullptr || rows->rotation == nullptr || rows->logscale == nullptr || rows->opacity == nullptr ||
         rows->sh0 == nullptr) {
@@ -435,7 +773,11 @@ gsx_hip_status gsx_hip_adc_step(gsx_hip_adc_context* ctx, const gsx_hip_adc_para
     int64_t result_count = n;
     const bool refine = in_refine_window(p, global_step);
     const bool reset = in_reset_window(p, global_step);
-    if (refine && n > 0) {
+    if (p.algorithm == 2) {
+        // gsx/src/gsx-cpu/adc.c:515-547: noise every step, then the refine
+        ADC_TRY(mcmc_noise(ctx, p, global_step, rows, stream));
+        if (refine && n > 0) ADC_TRY(mcmc_refine(ctx, p, rows, capacity, &result_count, out_counts, stream));
+    } else if (refine && n > 0) {
         const float* acc = p.algorithm == 1 ? rows->absgrad_acc : rows->grad_acc;
         if (acc == nullptr) return adc_fail(GSX_HIP_ERROR_NOT_SUPPORTED, "refine requires the grad accumulator");
         const uint64_t cap = p.max_num_gaussians > 0 ? (uint64_t)p.max_num_gaussians : 0;

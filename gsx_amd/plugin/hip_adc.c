@@ -1,11 +1,14 @@
 /*
  * hip_adc.c - adaptive density control vtable of the gsx HIP backend (gsx/src/gsx-impl.h:470-473).
- * The DEFAULT and ABSGS policies run as one gsx_hip_adc_step (the CPU semantics of
- * gsx/src/gsx-cpu/adc.c:380-559 and adc/default.c:160-527: grow candidates up to the budget,
- * duplicate or split, prune, clear the statistics, reset opacity in a reset window), on a working
- * copy of the Gaussian rows and their Adam moments; the result is written back through
- * gsx_gs_resize and the optimizer's resize, so the set and the optimizer stay count-aligned
- * (gsx-impl.h:36-37). MCMC is not offered (create fails with NOT_SUPPORTED).
+ * Every policy runs as one gsx_hip_adc_step with the CPU semantics of gsx/src/gsx-cpu/adc.c:380-559:
+ *   - DEFAULT / ABSGS (adc/default.c:160-527): grow candidates up to the budget, duplicate or
+ *     split, prune, clear the statistics, reset opacity in a reset window;
+ *   - MCMC (adc/mcmc.c:345-766): position noise on every step before end_refine, and in a refine
+ *     window relocation of the dead rows plus growth by grow_ratio.
+ * A refine or reset works on a working copy of the Gaussian rows and their Adam moments; the
+ * result is written back through gsx_gs_resize and the optimizer's resize, so the set and the
+ * optimizer stay count-aligned (gsx-impl.h:36-37). An MCMC step with noise only moves mean3d in
+ * place.
  */
 #include "hip_backend.h"
 
@@ -37,9 +40,10 @@ gsx_error gsx_hip_plugin_create_adc(gsx_backend_t backend, const gsx_adc_desc *d
         return gsx_make_error(GSX_ERROR_INVALID_ARGUMENT, "out_adc and desc must be non-null");
     }
     *out = NULL;
-    if(desc->algorithm != GSX_ADC_ALGORITHM_DEFAULT && desc->algorithm != GSX_ADC_ALGORITHM_ABSGS) {
+    if(desc->algorithm != GSX_ADC_ALGORITHM_DEFAULT && desc->algorithm != GSX_ADC_ALGORITHM_ABSGS
+        && desc->algorithm != GSX_ADC_ALGORITHM_MCMC) {
         return gsx_make_error(GSX_ERROR_NOT_SUPPORTED,
-            "hip adc supports GSX_ADC_ALGORITHM_DEFAULT and GSX_ADC_ALGORITHM_ABSGS");
+            "hip adc supports GSX_ADC_ALGORITHM_DEFAULT, GSX_ADC_ALGORITHM_ABSGS and GSX_ADC_ALGORITHM_MCMC");
     }
     a = (hip_adc *)calloc(1, sizeof(*a));
     if(a == NULL) {
@@ -121,6 +125,29 @@ typedef struct ha_work {
     bool present[HA_FIELDS];
 } ha_work;
 
+static void ha_params(const gsx_adc_desc *d, const gsx_adc_request *request, gsx_float_t lr_mean3d,
+    gsx_hip_adc_params *p)
+{
+    memset(p, 0, sizeof(*p));
+    p->algorithm = d->algorithm == GSX_ADC_ALGORITHM_MCMC ? 2 : (d->algorithm == GSX_ADC_ALGORITHM_ABSGS ? 1 : 0);
+    p->pruning_opacity_threshold = d->pruning_opacity_threshold;
+    p->opacity_clamp_value = d->opacity_clamp_value;
+    p->max_world_scale = d->max_world_scale;
+    p->max_screen_scale = d->max_screen_scale;
+    p->duplicate_grad_threshold = d->duplicate_grad_threshold;
+    p->duplicate_scale_threshold = d->duplicate_scale_threshold;
+    p->duplicate_absgrad_threshold = d->duplicate_absgrad_threshold;
+    p->scene_scale = request->scene_scale;
+    p->refine_every = d->refine_every;
+    p->start_refine = d->start_refine;
+    p->end_refine = d->end_refine;
+    p->max_num_gaussians = d->max_num_gaussians;
+    p->reset_every = d->reset_every;
+    p->noise_strength = d->noise_strength;
+    p->grow_ratio = d->grow_ratio;
+    p->mean3d_learning_rate = lr_mean3d;
+}
+
 static gsx_error ha_step(gsx_adc_t adc, const gsx_adc_request *request, gsx_adc_result *out_result)
 {
     hip_adc *a = (hip_adc *)adc;
@@ -139,6 +166,9 @@ static gsx_error ha_step(gsx_adc_t adc, const gsx_adc_request *request, gsx_adc_
     gsx_error error = { GSX_ERROR_SUCCESS, NULL };
     gsx_hip_status st = GSX_HIP_SUCCESS;
     bool use_optim = request->optim != NULL && request->optim->iface != NULL;
+    bool refine = false, reset = false, noise = false;
+    gsx_size_t copies = 2;
+    gsx_float_t lr_mean3d = 0.0f;
 
     memset(out_result, 0, sizeof(*out_result));
     memset(&w, 0, sizeof(w));
@@ -149,11 +179,23 @@ static gsx_error ha_step(gsx_adc_t adc, const gsx_adc_request *request, gsx_adc_
     n = info.count;
     out_result->gaussians_before = n;
     out_result->gaussians_after = n;
-    if(!ha_in_refine_window(d, request->global_step) && !ha_in_reset_window(d, request->global_step)) {
+    refine = ha_in_refine_window(d, request->global_step);
+    reset = ha_in_reset_window(d, request->global_step);
+    /* MCMC noise: every step before end_refine (gsx-cpu/adc/mcmc.c:357-364) */
+    noise = d->algorithm == GSX_ADC_ALGORITHM_MCMC && d->noise_strength > 0.0f
+        && !(ha_nonneg(d->end_refine) > 0 && request->global_step >= ha_nonneg(d->end_refine));
+    if(!refine && !reset && !noise) {
         return ha_ok();
     }
     if(n == 0) {
         return ha_ok();
+    }
+    if(noise) {
+        /* the noise is scaled by the optimizer's current mean3d rate (mcmc.c:375-380) */
+        error = gsx_optim_get_learning_rate_by_role(request->optim, GSX_OPTIM_PARAM_ROLE_MEAN3D, &lr_mean3d);
+        if(!gsx_error_is_success(error)) {
+            return error;
+        }
     }
 
     /* the fields and moments that exist, all device tensors of this backend */
@@ -173,6 +215,22 @@ static gsx_error ha_step(gsx_adc_t adc, const gsx_adc_request *request, gsx_adc_
         w.present[k] = true;
     }
     sh_degree = w.present[7] ? 3 : (w.present[6] ? 2 : (w.present[5] ? 1 : 0));
+    ha_params(d, request, lr_mean3d, &p);
+    if(!refine && !reset) {
+        /* MCMC noise only: the count stays, mean3d moves in place */
+        gsx_hip_gs_rows rows, unused;
+
+        memset(&rows, 0, sizeof(rows));
+        memset(&unused, 0, sizeof(unused));
+        rows.count = (int64_t)n;
+        rows.sh_degree = sh_degree;
+        for(k = 0; k < HA_FIELDS; ++k) {
+            if(w.present[k]) *ha_slot(&rows, k) = gsx_hip_plugin_tensor_f32(src[k]);
+        }
+        st = gsx_hip_adc_step(a->ctx, &p, (uint64_t)request->global_step, &rows, (int64_t)n, &unused, &in_out, counts,
+            stream);
+        return st == GSX_HIP_SUCCESS ? ha_ok() : gsx_hip_plugin_error(st, "hip adc noise failed");
+    }
     for(k = 0; k < 8; ++k) {
         w.moment_group[k] = -1;
         if(use_optim && w.present[k] && request->optim->role_to_index[ha_role[k]] >= 0) {
@@ -194,9 +252,11 @@ static gsx_error ha_step(gsx_adc_t adc, const gsx_adc_request *request, gsx_adc_
     if(d->max_num_gaussians > 0 && (gsx_size_t)d->max_num_gaussians > capacity) {
         capacity = (gsx_size_t)d->max_num_gaussians;
     }
+    /* MCMC never removes rows: its result stays in the one row set */
+    copies = d->algorithm == GSX_ADC_ALGORITHM_MCMC ? 1u : 2u;
     for(k = 0; k < HA_FIELDS; ++k) {
-        if(w.present[k]) total_floats += 2 * capacity * (gsx_size_t)ha_width[k];
-        if(k < 8 && w.moment_group[k] >= 0) total_floats += 4 * capacity * (gsx_size_t)ha_width[k];
+        if(w.present[k]) total_floats += copies * capacity * (gsx_size_t)ha_width[k];
+        if(k < 8 && w.moment_group[k] >= 0) total_floats += 2 * copies * capacity * (gsx_size_t)ha_width[k];
     }
     st = gsx_hip_malloc(&w.block, (size_t)total_floats * sizeof(float));
     if(st != GSX_HIP_SUCCESS) {
@@ -209,7 +269,7 @@ static gsx_error ha_step(gsx_adc_t adc, const gsx_adc_request *request, gsx_adc_
     for(k = 0; k < HA_FIELDS; ++k) {
         if(!w.present[k]) continue;
         *ha_slot(&w.rows, k) = HA_TAKE(ha_width[k]);
-        *ha_slot(&w.out, k) = HA_TAKE(ha_width[k]);
+        if(copies == 2) *ha_slot(&w.out, k) = HA_TAKE(ha_width[k]);
         st = gsx_hip_memcpy_async(*ha_slot(&w.rows, k), gsx_hip_plugin_tensor_ptr(src[k]),
             (size_t)n * (size_t)ha_width[k] * sizeof(float), stream);
         if(st != GSX_HIP_SUCCESS) break;
@@ -220,8 +280,10 @@ static gsx_error ha_step(gsx_adc_t adc, const gsx_adc_request *request, gsx_adc_
             (void)gsx_hip_plugin_optim_moments(request->optim, w.moment_group[k], &m, &v, &rows);
             w.rows.first_moment[k] = HA_TAKE(ha_width[k]);
             w.rows.second_moment[k] = HA_TAKE(ha_width[k]);
-            w.out.first_moment[k] = HA_TAKE(ha_width[k]);
-            w.out.second_moment[k] = HA_TAKE(ha_width[k]);
+            if(copies == 2) {
+                w.out.first_moment[k] = HA_TAKE(ha_width[k]);
+                w.out.second_moment[k] = HA_TAKE(ha_width[k]);
+            }
             st = gsx_hip_memcpy_async(w.rows.first_moment[k], m, (size_t)n * (size_t)ha_width[k] * sizeof(float), stream);
             if(st == GSX_HIP_SUCCESS) {
                 st = gsx_hip_memcpy_async(w.rows.second_moment[k], v, (size_t)n * (size_t)ha_width[k] * sizeof(float),
@@ -237,21 +299,6 @@ static gsx_error ha_step(gsx_adc_t adc, const gsx_adc_request *request, gsx_adc_
         return gsx_hip_plugin_error(st, "hip adc working copy failed");
     }
 
-    memset(&p, 0, sizeof(p));
-    p.algorithm = d->algorithm == GSX_ADC_ALGORITHM_ABSGS ? 1 : 0;
-    p.pruning_opacity_threshold = d->pruning_opacity_threshold;
-    p.opacity_clamp_value = d->opacity_clamp_value;
-    p.max_world_scale = d->max_world_scale;
-    p.max_screen_scale = d->max_screen_scale;
-    p.duplicate_grad_threshold = d->duplicate_grad_threshold;
-    p.duplicate_scale_threshold = d->duplicate_scale_threshold;
-    p.duplicate_absgrad_threshold = d->duplicate_absgrad_threshold;
-    p.scene_scale = request->scene_scale;
-    p.refine_every = d->refine_every;
-    p.start_refine = d->start_refine;
-    p.end_refine = d->end_refine;
-    p.max_num_gaussians = d->max_num_gaussians;
-    p.reset_every = d->reset_every;
     st = gsx_hip_adc_step(a->ctx, &p, (uint64_t)request->global_step, &w.rows, (int64_t)capacity, &w.out, &in_out,
         counts, stream);
     if(st != GSX_HIP_SUCCESS) {
@@ -302,6 +349,13 @@ static gsx_error ha_step(gsx_adc_t adc, const gsx_adc_request *request, gsx_adc_
     (void)gsx_hip_free(w.block);
     if(st != GSX_HIP_SUCCESS) {
         return gsx_hip_plugin_error(st, "hip adc commit failed");
+    }
+    if(counts[3] != 0 && use_optim) {
+        /* the opacity group restarts with the clamp: moments and step count (default.c:306-311) */
+        error = gsx_optim_reset_param_group_by_role(request->optim, GSX_OPTIM_PARAM_ROLE_OPACITY);
+        if(!gsx_error_is_success(error)) {
+            return error;
+        }
     }
     out_result->gaussians_after = (gsx_size_t)new_count;
     out_result->pruned_count = (gsx_size_t)counts[0];

@@ -359,6 +359,11 @@ typedef struct gsx_hip_adc_params {
     float duplicate_absgrad_threshold;
     float scene_scale;
     int64_t refine_every, start_refine, end_refine, max_num_gaussians, reset_every;
+    /* GSX_ADC_ALGORITHM_MCMC (algorithm 2): position noise scale, target growth ratio per
+     * refine, and the optimizer's current mean3d learning rate (the noise is scaled by it) */
+    float noise_strength;
+    float grow_ratio;
+    float mean3d_learning_rate;
 } gsx_hip_adc_params;
 
 /* Rows of a Gaussian set on the device (the gsx_gs fields, gsx/include/gsx/gsx-core.h:286-308)
@@ -383,7 +388,17 @@ gsx_hip_status gsx_hip_adc_context_destroy(gsx_hip_adc_context* context);
  * is written to `out` (same fields bound) and *out_result_in_out = 1, otherwise the result stays
  * in `rows`. The final count is stored in the result's `count`. out_counts[4] = pruned,
  * duplicated, grown (split), reset, as gsx_adc_result. Synchronises the stream twice per refine
- * (candidate and survivor counts). */
+ * (candidate and survivor counts).
+ * MCMC (algorithm 2, gsx/src/gsx-cpu/adc/mcmc.c:345-766, dispatched as gsx-cpu/adc.c:515-547):
+ * every step before end_refine moves each mean3d by opacity-gated noise shaped by its covariance
+ * (6 draws per Gaussian); a refine relocates the rows whose sigmoid(opacity) <= the pruning
+ * threshold onto live rows drawn in proportion to opacity and grows the set to
+ * min(floor(count * (1 + grow_ratio)), max_num_gaussians) rows drawn the same way (appended in
+ * place: `capacity` >= that count), with the opacity / scale correction of the relocated sources.
+ * Rows are never removed, so the result stays in `rows`; out_counts = relocated (as pruned), 0,
+ * relocated + appended (as grown), reset. The draw weights form their cumulative sums in float
+ * on the host, in index order, as the CPU and Metal backends do (a sequential float sum has no
+ * parallel equivalent with the same rounding); the stream synchronises twice per draw. */
 gsx_hip_status gsx_hip_adc_step(gsx_hip_adc_context* context, const gsx_hip_adc_params* params, uint64_t global_step,
                                 gsx_hip_gs_rows* rows, int64_t capacity, gsx_hip_gs_rows* out,
                                 int32_t* out_result_in_out, int64_t* out_counts, hipStream_t stream);

@@ -372,13 +372,19 @@ class Reference:
         self._check(self.lib.gsxref_adam(param.size, steps, _p(param), _p(grad),
                                          _p(np.asarray(hyper, np.float32)), None, None))
 
-    def adc(self, fields, aux, params: AdcParams, capacity):
+    def adc(self, fields, aux, params: AdcParams, capacity, noise_strength=0.0, grow_ratio=0.0, steps=1,
+            optim_probe=False):
+        """gsx_adc_step on a fresh set and Adam optimizer; `steps` consecutive global steps from
+        params.global_step; optim_probe: an Adam step on normal gradients before and after, so
+        the moments the ADC kept, moved or cleared show in the returned rows."""
         n = fields["mean3d"].shape[0]
         fp = np.array([params.pruning_opacity_threshold, params.opacity_clamp_value, params.max_world_scale, 0.0,
                        params.duplicate_grad_threshold, params.duplicate_scale_threshold,
-                       params.duplicate_absgrad_threshold, params.scene_scale, 0, 0], np.float32)
+                       params.duplicate_absgrad_threshold, params.scene_scale, noise_strength, grow_ratio],
+                      np.float32)
         ip = np.array([params.algorithm, params.refine_every, params.start_refine, params.end_refine,
-                       params.max_num_gaussians, params.reset_every, params.global_step, params.seed], np.int64)
+                       params.max_num_gaussians, params.reset_every, params.global_step, params.seed, steps,
+                       1 if optim_probe else 0], np.int64)
         cap = max(capacity, n)
         out = {"mean3d": np.zeros((cap, 3), np.float32), "rotation": np.zeros((cap, 4), np.float32),
                "logscale": np.zeros((cap, 3), np.float32), "opacity": np.zeros((cap,), np.float32),

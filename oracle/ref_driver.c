@@ -497,15 +497,43 @@ done:
     return rc;
 }
 
-/* One ADC step (DEFAULT or ABSGS) on a Gaussian set with SH0 only and an Adam optimizer over
+/* One Adam step of every group on gradients filled with pcg32 normals (seeded `seed`). */
+static gsx_error adam_probe_step(gsx_gs_t gs, gsx_optim_t optim, uint64_t seed)
+{
+    const gsx_gs_field grads[5] = { GSX_GS_FIELD_GRAD_MEAN3D, GSX_GS_FIELD_GRAD_LOGSCALE, GSX_GS_FIELD_GRAD_ROTATION,
+        GSX_GS_FIELD_GRAD_OPACITY, GSX_GS_FIELD_GRAD_SH0 };
+    gsx_optim_step_request sreq = { 0 };
+    gsx_pcg32_t pcg = NULL;
+    gsx_tensor_t t = NULL;
+    gsx_error e;
+    int k;
+
+    e = gsx_pcg32_init(&pcg, (gsx_pcg32_state_t)seed);
+    if(!gsx_error_is_success(e)) return e;
+    for(k = 0; k < 5; ++k) {
+        e = gsx_gs_get_field(gs, grads[k], &t);
+        if(gsx_error_is_success(e)) e = gsx_pcg32_fill_randn(pcg, t, 0.01f);
+        if(!gsx_error_is_success(e)) {
+            (void)gsx_pcg32_free(pcg);
+            return e;
+        }
+    }
+    (void)gsx_pcg32_free(pcg);
+    sreq.force_all = true;
+    return gsx_optim_step(optim, &sreq);
+}
+
+/* ADC steps (DEFAULT, ABSGS or MCMC) on a Gaussian set with SH0 only and an Adam optimizer over
  * the 5 built-in roles. params[10] = pruning_opacity_threshold, opacity_clamp_value,
  * max_world_scale, max_screen_scale, duplicate_grad_threshold, duplicate_scale_threshold,
- * duplicate_absgrad_threshold, scene_scale, (unused), (unused).
- * iparams[8] = algorithm, refine_every, start_refine, end_refine, max_num_gaussians,
- * reset_every, global_step, seed.
+ * duplicate_absgrad_threshold, scene_scale, noise_strength, grow_ratio.
+ * iparams[10] = algorithm, refine_every, start_refine, end_refine, max_num_gaussians,
+ * reset_every, global_step, seed, step_count (consecutive global steps from global_step; 0 or 1:
+ * one), optim_probe (non-zero: one Adam step on pcg32 normal gradients before the ADC steps and
+ * one after, so the rows' optimizer moments show in the returned parameters).
  * In: n rows of mean3d/rotation/logscale/opacity/sh0 + grad_acc, absgrad_acc, visible_counter.
  * Out: *out_n rows written to out_* (capacity out_capacity rows); counters[4] = pruned,
- * duplicated, grown, reset. */
+ * duplicated, grown, reset, summed over the steps. */
 int gsxref_adc(int n, const float *mean3d, const float *rotation, const float *logscale, const float *opacity,
     const float *sh0, const float *grad_acc, const float *absgrad_acc, const float *visible_counter,
     const float *params, const int64_t *iparams, int out_capacity, int *out_n,
@@ -585,6 +613,8 @@ int gsxref_adc(int n, const float *mean3d, const float *rotation, const float *l
     adesc.max_num_gaussians = (gsx_index_t)iparams[4];
     adesc.reset_every = (gsx_index_t)iparams[5];
     adesc.seed = (gsx_size_t)iparams[7];
+    adesc.noise_strength = params[8];
+    adesc.grow_ratio = params[9];
     TRY(gsx_adc_init(&adc, g_backend, &adesc));
     areq.gs = gs;
     areq.optim = optim;
@@ -600,15 +630,20 @@ int gsxref_adc(int n, const float *mean3d, const float *rotation, const float *l
     }
     areq.dataloader = (gsx_dataloader_t)0x1;
     areq.renderer = adc_renderer;
-    areq.global_step = (gsx_size_t)iparams[6];
     areq.scene_scale = params[7];
-    TRY(gsx_adc_step(adc, &areq, &ares));
+    if(iparams[9] != 0) TRY(adam_probe_step(gs, optim, 101u));
+    counters[0] = counters[1] = counters[2] = counters[3] = 0;
+    for(k = 0; k < (iparams[8] > 1 ? (int)iparams[8] : 1); ++k) {
+        areq.global_step = (gsx_size_t)iparams[6] + (gsx_size_t)k;
+        TRY(gsx_adc_step(adc, &areq, &ares));
+        counters[0] += (int64_t)ares.pruned_count;
+        counters[1] += (int64_t)ares.duplicated_count;
+        counters[2] += (int64_t)ares.grown_count;
+        counters[3] += (int64_t)ares.reset_count;
+    }
+    if(iparams[9] != 0) TRY(adam_probe_step(gs, optim, 202u));
     TRY(gsx_gs_get_info(gs, &info));
     *out_n = (int)info.count;
-    counters[0] = (int64_t)ares.pruned_count;
-    counters[1] = (int64_t)ares.duplicated_count;
-    counters[2] = (int64_t)ares.grown_count;
-    counters[3] = (int64_t)ares.reset_count;
     if((int)info.count > out_capacity) {
         g_last_message = "adc output exceeds out_capacity";
         rc = -2;

@@ -54,7 +54,7 @@ def test_struct_sizes_match_header_layout():
     assert ctypes.sizeof(_lib.Camera) == 4 * 18
     assert ctypes.sizeof(_lib.Gaussians) == 8 + 8 + 8 * 8
     assert ctypes.sizeof(_lib.AdamGroup) == 4 * 8 + 8 + 6 * 4 + 2 * 8
-    assert ctypes.sizeof(_lib.AdcParams) == 4 * 9 + 4 + 5 * 8
+    assert ctypes.sizeof(_lib.AdcParams) == 4 * 9 + 4 + 5 * 8 + 3 * 4 + 4
     assert ctypes.sizeof(_lib.GsRows) == 8 + 8 + 12 * 8 + 16 * 8
     assert ctypes.sizeof(_lib.RenderStats) == 3 * 8 + 6 * 4
 

@@ -151,8 +151,8 @@ def test_adc(backends, algorithm, step, max_num):
                        duplicate_absgrad_threshold=4e-4, scene_scale=1.0, refine_every=100, start_refine=0,
                        end_refine=1000, max_num_gaussians=max_num, reset_every=300, global_step=step, seed=5)
     print(f"[case] plugin adc alg={algorithm} step={step} max={max_num}", flush=True)
-    out_c, cnt_c = cpu.adc(fields, aux, params, max(n, max_num))
-    out_h, cnt_h = hip.adc(fields, aux, params, max(n, max_num))
+    out_c, cnt_c = cpu.adc(fields, aux, params, max(n, max_num), optim_probe=True)
+    out_h, cnt_h = hip.adc(fields, aux, params, max(n, max_num), optim_probe=True)
     assert np.array_equal(cnt_h, cnt_c)
     assert out_h["mean3d"].shape == out_c["mean3d"].shape
     for k in out_c:
@@ -278,3 +278,43 @@ def test_image_conversions(backends):
     assert np.array_equal(hip.image("to_u8", img, 3, 37, 53), cpu.image("to_u8", img, 3, 37, 53))
     u8 = rng.integers(0, 256, (3, 37, 53)).astype(np.uint8)
     assert np.array_equal(hip.image("from_u8", u8, 3, 37, 53), cpu.image("from_u8", u8, 3, 37, 53))
+
+
+MCMC_CASES = [  # rows, grow_ratio, max_num, steps, first step, noise_strength, reset_every
+    (2500, 0.2, 5000, 1, 100, 50.0, 0),          # relocation + growth in one refine
+    (2500, 0.5, 3200, 3, 99, 50.0, 0),           # noise, refine (growth capped by max_num), noise
+    (2500, 0.0, 0, 2, 299, 50.0, 300),           # noise then relocation with an opacity reset window
+    (2500, 0.3, 4000, 2, 999, 50.0, 0),          # noise stops at end_refine (1000): the refine only
+    (2500, 0.25, 4000, 1, 100, 0.0, 0),          # no noise
+    (300_000, 0.1, 400_000, 2, 100, 50.0, 0),    # at scale: 36k relocations, 30k appended rows
+]
+
+
+@pytest.mark.parametrize("n,grow,max_num,steps,first,noise,reset_every", MCMC_CASES)
+def test_adc_mcmc(backends, n, grow, max_num, steps, first, noise, reset_every):
+    """MCMC density control (gsx/src/gsx-cpu/adc/mcmc.c) through gsx_adc_step on both backends:
+    relocated and appended rows, counts and the optimizer state they leave (an Adam step on
+    normal gradients before and after: cleared moments and restarted step counts change it)
+    bit-identical. The checker is the reference CPU backend itself: the C oracle has no MCMC
+    restatement."""
+    from oracle.oracle import AdcParams
+    cpu, hip = backends
+    fields, aux = _adc_inputs(n, 77 + steps)
+    rng = np.random.default_rng(5)
+    dead = rng.random(n) < 0.12
+    fields["opacity"] = np.where(dead, -4.0, np.abs(fields["opacity"]) + 0.5).astype(np.float32)
+    params = AdcParams(algorithm=2, pruning_opacity_threshold=0.05, opacity_clamp_value=0.3, max_world_scale=0.0,
+                       duplicate_grad_threshold=2e-4, duplicate_scale_threshold=0.01,
+                       duplicate_absgrad_threshold=4e-4, scene_scale=1.0, refine_every=100, start_refine=0,
+                       end_refine=1000, max_num_gaussians=max_num, reset_every=reset_every, global_step=first,
+                       seed=11)
+    cap = max(n, max_num)
+    print(f"[case] plugin mcmc grow={grow} max={max_num} steps={steps} from={first} noise={noise}", flush=True)
+    kw = dict(noise_strength=noise, grow_ratio=grow, steps=steps, optim_probe=True)
+    out_c, cnt_c = cpu.adc(fields, aux, params, cap, **kw)
+    out_h, cnt_h = hip.adc(fields, aux, params, cap, **kw)
+    assert cnt_c[0] == int(dead.sum()) or first % 100 != 0 or steps > 1
+    assert np.array_equal(cnt_h, cnt_c)
+    assert out_h["mean3d"].shape == out_c["mean3d"].shape
+    for k in out_c:
+        assert np.array_equal(out_h[k], out_c[k]), k
