@@ -113,6 +113,11 @@ SIGNATURES = {
     "gsx_hip_stream_create": (_st, [ctypes.POINTER(_vp)]),
     "gsx_hip_stream_destroy": (_st, [_vp]),
     "gsx_hip_stream_synchronize": (_st, [_vp]),
+    "gsx_hip_event_create": (_st, [_vp]),
+    "gsx_hip_event_destroy": (_st, [_vp]),
+    "gsx_hip_event_record": (_st, [_vp, _vp]),
+    "gsx_hip_event_synchronize": (_st, [_vp]),
+    "gsx_hip_stream_wait_event": (_st, [_vp, _vp]),
     "gsx_hip_fill_f32": (_st, [_vp, _i64, _f, _vp]),
     "gsx_hip_copy_f32": (_st, [_vp, _vp, _i64, _vp]),
     "gsx_hip_render_context_create": (_st, [ctypes.POINTER(_vp)]),
@@ -141,6 +146,7 @@ SIGNATURES = {
     "gsx_hip_clamp_inplace": (_st, [_vp, _i64, _i32, _vp, _vp, _vp]),
     "gsx_hip_reduce_temp_bytes": (ctypes.c_size_t, [_i64, _i64]),
     "gsx_hip_reduce_f32": (_st, [_vp, _vp, _i64, _i64, _i32, _vp, _vp, _vp]),
+    "gsx_hip_dataloader_to_chw_f32": (_st, [_vp, _i32, _i64, _i64, _i64, _vp, _vp]),
     "gsx_hip_image_colorspace_f32": (_st, [_vp, _vp, _i64, _i32, _i32, _vp]),
     "gsx_hip_image_storage_convert": (_st, [_vp, _i32, _vp, _i32, _i64, _i64, _i64, _i32, _vp]),
     "gsx_hip_image_quantize_u8": (_st, [_vp, _vp, _i64, _vp]),

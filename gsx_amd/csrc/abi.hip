@@ -490,6 +490,32 @@ gsx_hip_status gsx_hip_stream_synchronize(hipStream_t stream) {
     return GSX_HIP_SUCCESS;
 }
 
+gsx_hip_status gsx_hip_event_create(hipEvent_t* out_event) {
+    if (out_event == nullptr) return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "out_event must be non-null");
+    GSX_HIP_TRY(hipEventCreateWithFlags(out_event, hipEventDisableTiming), "hipEventCreateWithFlags");
+    return GSX_HIP_SUCCESS;
+}
+
+gsx_hip_status gsx_hip_event_destroy(hipEvent_t event) {
+    GSX_HIP_TRY(hipEventDestroy(event), "hipEventDestroy");
+    return GSX_HIP_SUCCESS;
+}
+
+gsx_hip_status gsx_hip_event_record(hipEvent_t event, hipStream_t stream) {
+    GSX_HIP_TRY(hipEventRecord(event, stream), "hipEventRecord");
+    return GSX_HIP_SUCCESS;
+}
+
+gsx_hip_status gsx_hip_event_synchronize(hipEvent_t event) {
+    GSX_HIP_TRY(hipEventSynchronize(event), "hipEventSynchronize");
+    return GSX_HIP_SUCCESS;
+}
+
+gsx_hip_status gsx_hip_stream_wait_event(hipStream_t stream, hipEvent_t event) {
+    GSX_HIP_TRY(hipStreamWaitEvent(stream, event, 0), "hipStreamWaitEvent");
+    return GSX_HIP_SUCCESS;
+}
+
 gsx_hip_status gsx_hip_fill_f32(float* dst, int64_t count, float value, hipStream_t stream) {
     if (count <= 0) return GSX_HIP_SUCCESS;
     if (dst == nullptr) return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "dst must be non-null");

@@ -378,6 +378,19 @@ __global__ __launch_bounds__(kThreads) void dequantize_kernel(const uint8_t* __r
         dst[i] = (float)src[i] / 255.0f;
 }
 
+// Dataloader layout: element (c, y, x) of a CHW float tensor from a tightly packed HWC (channels 3)
+// or HW (channels 1) host payload of u8 or f32, value-preserving (u8 v becomes v.0f), as
+// gsx/src/gsx-data-impl.h:173-268 packs it on the CPU.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void to_chw_f32_kernel(const T* __restrict__ src, float* __restrict__ dst,
+                                                              int64_t channels, int64_t pixels) {
+    const int64_t total = channels * pixels;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t c = i / pixels, px = i - c * pixels;
+        dst[i] = (float)src[px * channels + c];
+    }
+}
+
 int64_t reduce_chunks(int64_t reduce) {
     const int64_t c = (reduce + kReduceChunk - 1) / kReduceChunk;
     return c < 1 ? 1 : c;
@@ -600,6 +613,22 @@ gsx_hip_status gsx_hip_image_storage_convert(const void* src, int32_t src_hwc, v
             return invalid("storage convert: element size must be 1, 2 or 4 bytes");
     }
     return launch_status("storage_kernel");
+}
+
+gsx_hip_status gsx_hip_dataloader_to_chw_f32(const void* src, int32_t src_is_u8, int64_t channels, int64_t height,
+                                            int64_t width, float* dst, hipStream_t stream) {
+    const int64_t pixels = height * width;
+    if (channels < 1 || height < 0 || width < 0 || (pixels > 0 && (src == nullptr || dst == nullptr)))
+        return invalid("dataloader layout: bad arguments");
+    if (pixels == 0) return GSX_HIP_SUCCESS;
+    const unsigned g = grid_for(channels * pixels, kThreads * 4);
+    if (src_is_u8)
+        hipLaunchKernelGGL(to_chw_f32_kernel<uint8_t>, dim3(g), dim3(kThreads), 0, stream,
+                           static_cast<const uint8_t*>(src), dst, channels, pixels);
+    else
+        hipLaunchKernelGGL(to_chw_f32_kernel<float>, dim3(g), dim3(kThreads), 0, stream,
+                           static_cast<const float*>(src), dst, channels, pixels);
+    return launch_status("to_chw_f32_kernel");
 }
 
 gsx_hip_status gsx_hip_image_quantize_u8(const float* src, uint8_t* dst, int64_t count, hipStream_t stream) {

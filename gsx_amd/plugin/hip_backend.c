@@ -201,7 +201,7 @@ static gsx_error hip_create_backend(gsx_backend_device_t device, const gsx_backe
         return gsx_hip_plugin_error(st, "hip backend creation failed");
     }
     b->capabilities.supported_data_types = GSX_DATA_TYPE_FLAG_F32;
-    b->capabilities.supports_async_prefetch = false;
+    b->capabilities.supports_async_prefetch = true;
     hip_init_buffer_type(b, &b->device_type, GSX_BACKEND_BUFFER_TYPE_DEVICE, "device", 256);
     hip_init_buffer_type(b, &b->pinned_type, GSX_BACKEND_BUFFER_TYPE_HOST_PINNED, "host_pinned", 64);
     *out = &b->base;

@@ -26,6 +26,7 @@ extern "C" {
 
 #ifndef HIP_INCLUDE_HIP_HIP_RUNTIME_API_H
 typedef struct ihipStream_t* hipStream_t;
+typedef struct ihipEvent_t* hipEvent_t;
 #endif
 
 typedef int gsx_hip_status;
@@ -62,6 +63,14 @@ gsx_hip_status gsx_hip_host_device_pointer(void* host, void** out_device);
 gsx_hip_status gsx_hip_stream_create(hipStream_t* out_stream);
 gsx_hip_status gsx_hip_stream_destroy(hipStream_t stream);
 gsx_hip_status gsx_hip_stream_synchronize(hipStream_t stream);
+/* Events (no timing) ordering work between streams: the async dataloader's helper stream and the
+ * major stream (gsx-cuda/async_dl.cu orders them by host synchronisation instead). An event
+ * never recorded counts as complete. */
+gsx_hip_status gsx_hip_event_create(hipEvent_t* out_event);
+gsx_hip_status gsx_hip_event_destroy(hipEvent_t event);
+gsx_hip_status gsx_hip_event_record(hipEvent_t event, hipStream_t stream);
+gsx_hip_status gsx_hip_event_synchronize(hipEvent_t event);
+gsx_hip_status gsx_hip_stream_wait_event(hipStream_t stream, hipEvent_t event);
 /* Fill `count` floats with `value` (a kernel, not hipMemset, so it is safe under graph capture). */
 gsx_hip_status gsx_hip_fill_f32(float* dst, int64_t count, float value, hipStream_t stream);
 /* Streaming device copy of `count` floats (16-byte aligned, count % 4 == 0); also the known-size
@@ -265,6 +274,12 @@ gsx_hip_status gsx_hip_clamp_inplace(void* x, int64_t count, int32_t data_type, 
 size_t gsx_hip_reduce_temp_bytes(int64_t outer, int64_t reduce);
 gsx_hip_status gsx_hip_reduce_f32(const float* x, const float* y, int64_t outer, int64_t reduce, int32_t op,
                                   float* out, void* temp, hipStream_t stream);
+/* The dataloader's device layout step (replaces the HWC -> CHW kernels of
+ * gsx/src/gsx-cuda/async_dl.cu:45-156): dst [channels, height, width] float32 from a tightly
+ * packed HWC (channels 3) or HW (channels 1) payload of u8 (src_is_u8 != 0, values kept, not
+ * scaled) or float32 already in device-visible memory. */
+gsx_hip_status gsx_hip_dataloader_to_chw_f32(const void* src, int32_t src_is_u8, int64_t channels, int64_t height,
+                                            int64_t width, float* dst, hipStream_t stream);
 /* image_convert_colorspace (sRGB transfer curves with glibc's powf, bit for bit),
  * image_convert_storage_format (HWC <-> CHW for 1/2/4-byte elements) and
  * image_convert_data_type (f32 <-> u8), gsx/src/extra/gsx-image-impl.h:9-170. */

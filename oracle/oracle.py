@@ -314,6 +314,9 @@ class Reference:
         lib.gsxref_image.restype = ctypes.c_int
         lib.gsxref_image.argtypes = [ctypes.c_int] * 4 + [_vp, _vp]
         lib.gsxref_backend_device_name.restype = ctypes.c_char_p
+        lib.gsxref_dataloader.restype = ctypes.c_int
+        lib.gsxref_dataloader.argtypes = [ctypes.c_int] * 4 + [_vp, _vp, ctypes.c_int, ctypes.c_uint64, ctypes.c_int,
+                                                                ctypes.c_int, _vp, _vp, _vp, _vp, _vp]
         lib.gsxref_render.restype = ctypes.c_int
         lib.gsxref_render.argtypes = [ctypes.c_int, ctypes.c_int] + [_vp] * 9 + [ctypes.c_int, _vp, _vp]
         lib.gsxref_render_grad.restype = ctypes.c_int
@@ -469,3 +472,22 @@ class Reference:
             out = np.zeros((c, h, w), np.float32)
         self._check(self.lib.gsxref_image(code, c, h, w, _p(src), _p(out)))
         return out
+
+    def dataloader(self, rgb, alpha=None, shuffle=True, seed=0, prefetch=0, steps=None):
+        """Iterate gsx_dataloader over host images rgb [count, h, w, 3] (u8 or float32) and
+        optional alpha [count, h, w]; returns CHW rgb [steps, 3, h, w], alpha [steps, h, w] or
+        None, stable indices, epochs and the intrinsics' fx (100 + index) of every step."""
+        rgb = np.ascontiguousarray(rgb)
+        count, h, w, _ = rgb.shape
+        is_u8 = rgb.dtype == np.uint8
+        a = None if alpha is None else np.ascontiguousarray(alpha, rgb.dtype)
+        steps = count if steps is None else steps
+        out_rgb = np.zeros((steps, 3, h, w), np.float32)
+        out_alpha = np.zeros((steps, h, w), np.float32) if a is not None else None
+        idx = np.zeros(steps, np.int64)
+        ep = np.zeros(steps, np.int64)
+        fx = np.zeros(steps, np.float32)
+        self._check(self.lib.gsxref_dataloader(count, h, w, 1 if is_u8 else 0, _p(rgb), _p(a), 1 if shuffle else 0,
+                                               seed, prefetch, steps, _p(out_rgb), _p(out_alpha), _p(idx), _p(ep),
+                                               _p(fx)))
+        return out_rgb, out_alpha, idx, ep, fx

@@ -1134,3 +1134,110 @@ done:
     if(arena != NULL) (void)gsx_arena_free(arena);
     return rc;
 }
+
+/* ---- dataloader (gsx-data.h) -------------------------------------------------------------------
+ * A dataset of `count` host images, rgb [count, h, w, 3] HWC and optional alpha [count, h, w], of
+ * u8 (is_u8) or float32 elements, iterated through gsx_dataloader on the selected backend:
+ * prefetch > 0 turns on async prefetch with that depth (the backend's async loader), 0 the
+ * synchronous path. `steps` results are downloaded: rgb CHW floats to out_rgb [steps, 3, h, w],
+ * alpha to out_alpha [steps, h, w] (nullable), stable sample indices to out_index and epochs to
+ * out_epoch; sample k's intrinsics carry fx = 100 + k so out_fx [steps] shows the pairing. */
+typedef struct ref_images {
+    int count, h, w, is_u8;
+    const unsigned char *rgb, *alpha;
+} ref_images;
+
+static gsx_error ref_ok(void)
+{
+    gsx_error ok = { GSX_ERROR_SUCCESS, NULL };
+    return ok;
+}
+
+static gsx_error ref_images_length(void *object, gsx_size_t *out_length)
+{
+    *out_length = (gsx_size_t)((ref_images *)object)->count;
+    return ref_ok();
+}
+
+static gsx_error ref_images_sample(void *object, gsx_size_t index, gsx_dataset_cpu_sample *out)
+{
+    const ref_images *d = (const ref_images *)object;
+    const size_t elem = d->is_u8 ? 1u : 4u;
+    const size_t px = (size_t)d->h * (size_t)d->w;
+
+    memset(out, 0, sizeof(*out));
+    out->intrinsics.model = GSX_CAMERA_MODEL_PINHOLE;
+    out->intrinsics.fx = 100.0f + (float)index;
+    out->intrinsics.fy = 100.0f;
+    out->intrinsics.cx = 0.5f * (float)d->w;
+    out->intrinsics.cy = 0.5f * (float)d->h;
+    out->intrinsics.width = d->w;
+    out->intrinsics.height = d->h;
+    out->pose.rot.w = 1.0f;
+    out->rgb_data = d->rgb + index * px * 3u * elem;
+    out->alpha_data = d->alpha != NULL ? d->alpha + index * px * elem : NULL;
+    return ref_ok();
+}
+
+static void ref_images_release(void *object, gsx_dataset_cpu_sample *sample)
+{
+    (void)object;
+    (void)sample;
+}
+
+int gsxref_dataloader(int count, int h, int w, int is_u8, const void *rgb, const void *alpha, int shuffle,
+    uint64_t seed, int prefetch, int steps, float *out_rgb, float *out_alpha, int64_t *out_index, int64_t *out_epoch,
+    float *out_fx)
+{
+    int rc = 0;
+    ref_images images;
+    gsx_dataset_desc ddesc = { 0 };
+    gsx_dataset_t dataset = NULL;
+    gsx_dataloader_desc ldesc = { 0 };
+    gsx_dataloader_t loader = NULL;
+    gsx_dataloader_result res;
+    const size_t px = (size_t)h * (size_t)w;
+    int s;
+
+    rc = ensure_backend();
+    if(rc != 0) return rc;
+    images.count = count;
+    images.h = h;
+    images.w = w;
+    images.is_u8 = is_u8;
+    images.rgb = (const unsigned char *)rgb;
+    images.alpha = (const unsigned char *)alpha;
+    ddesc.name = "gsxref";
+    ddesc.object = &images;
+    ddesc.image_data_type = is_u8 ? GSX_DATA_TYPE_U8 : GSX_DATA_TYPE_F32;
+    ddesc.width = w;
+    ddesc.height = h;
+    ddesc.has_rgb = true;
+    ddesc.has_alpha = alpha != NULL;
+    ddesc.get_length = ref_images_length;
+    ddesc.get_sample = ref_images_sample;
+    ddesc.release_sample = ref_images_release;
+    TRY(gsx_dataset_init(&dataset, &ddesc));
+    ldesc.shuffle_each_epoch = shuffle != 0;
+    ldesc.enable_async_prefetch = prefetch > 0;
+    ldesc.prefetch_count = prefetch > 0 ? (gsx_size_t)prefetch : 0u;
+    ldesc.seed = (gsx_size_t)seed;
+    ldesc.image_data_type = GSX_DATA_TYPE_F32;
+    TRY(gsx_dataloader_init(&loader, g_backend, dataset, &ldesc));
+    for(s = 0; s < steps; ++s) {
+        TRY(gsx_dataloader_next_ex(loader, &res));
+        TRY(gsx_tensor_download(res.rgb_image, out_rgb + (size_t)s * 3u * px, 3u * px * sizeof(float)));
+        if(out_alpha != NULL && res.alpha_image != NULL) {
+            TRY(gsx_tensor_download(res.alpha_image, out_alpha + (size_t)s * px, px * sizeof(float)));
+        }
+        FINISH();
+        out_index[s] = (int64_t)res.stable_sample_index;
+        out_epoch[s] = (int64_t)res.epoch_index;
+        out_fx[s] = res.intrinsics.fx;
+    }
+done:
+    FINISH();
+    if(loader != NULL) (void)gsx_dataloader_free(loader);
+    if(dataset != NULL) (void)gsx_dataset_free(dataset);
+    return rc;
+}
