@@ -743,7 +743,8 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
         hipLaunchKernelGGL(preprocess_kernel, dim3(pre_blocks), dim3(256), 0, stream, snap, n, gaussians->mean3d,
                            gaussians->rotation, gaussians->logscale, gaussians->opacity, gaussians->sh0,
                            gaussians->sh1, gaussians->sh2, gaussians->sh3, (int)gaussians->sh_degree, cam,
-                           ctx->rec.as<float4>(), train ? ctx->cov_coef.as<float4>() : nullptr,
+                           ctx->rec.as<float4>(), ctx->rec.as<float4>() + 2 * n,
+                           train ? ctx->cov_coef.as<float4>() : nullptr,
                            ctx->tile_count.as<uint32_t>(), train ? visible_counter : nullptr,
                            ctx->big_list.as<uint32_t>(), big_count, counters + 1, counters + 2 + (ctx->big_slot ^ 1),
                            counters + 4,
@@ -856,7 +857,8 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     const int tiles_padded = ((tiles + 7) / 8) * 8;
     hipLaunchKernelGGL(blend_forward_kernel, dim3((unsigned)tiles_padded), dim3(256), 0, stream,
                        ctx->ranges.as<uint2>(), ctx->sorted_vals, ctx->inst_gauss.as<uint32_t>(),
-                       ctx->rec.as<float4>(), train ? ctx->sorted_g.as<uint32_t>() : nullptr, cam, out_rgb,
+                       ctx->rec.as<float4>(), ctx->rec.as<float4>() + 2 * n,
+                       train ? ctx->sorted_g.as<uint32_t>() : nullptr, cam, out_rgb,
                        ctx->final_t.as<float>(),
                        ctx->last.as<uint32_t>(), train ? ctx->ckpt.as<float>() : nullptr);
     GSX_HIP_TRY(hipGetLastError(), "blend_forward_kernel");
@@ -889,7 +891,7 @@ gsx_hip_status enqueue_backward(gsx_hip_render_context* ctx, const float* grad_r
     const int tiles_padded = ((tiles + 7) / 8) * 8;
     hipLaunchKernelGGL(blend_backward_kernel, dim3((unsigned)tiles_padded), dim3(256), 0, stream,
                        ctx->ranges.as<uint2>(), svals, ctx->sorted_g.as<uint32_t>(), ctx->rec.as<float4>(),
-                       ctx->cov_coef.as<float4>(), ctx->ckpt.as<float>(), cam, grad_rgb, ctx->final_t.as<float>(),
+                       ctx->rec.as<float4>() + 2 * n, ctx->cov_coef.as<float4>(), ctx->ckpt.as<float>(), cam, grad_rgb, ctx->final_t.as<float>(),
                        ctx->last.as<uint32_t>(), ctx->inst_grad.as<float>(), inst_grad_op);
     GSX_HIP_TRY(hipGetLastError(), "blend_backward_kernel");
     GSX_TRY(record(ctx, 8, stream));

@@ -7,11 +7,14 @@
 // colour clamp max(c + 0.5, 0). The CUDA design this replaces (fastgs, kernels_forward.cuh /
 // kernels_backward.cuh) differs in all of those, so none of its arithmetic is used here.
 //
-// Data layout in HBM (per Gaussian g, written by preprocess, read by emission and both blends):
-//   rec[3g+0] = {mean2d_x, mean2d_y, inv_a, 2*inv_b}      (conic of the dilated 2D covariance)
-//   rec[3g+1] = {inv_c, opacity, color_r, color_g}
-//   rec[3g+2] = {color_b, x_min | x_max << 16, y_min | y_max << 16, depth}   (ints as f32 bits)
-// 48 B per visible Gaussian, three 16 B loads; culled Gaussians only write tile_count = 0.
+// Data layout in HBM (per Gaussian g, written by preprocess, read by emission and both blends),
+// 48 B per visible Gaussian in two arrays (culled Gaussians only write tile_count = 0):
+//   geo[2g+0] = {mean2d_x, mean2d_y, inv_a, 2*inv_b}      (conic of the dilated 2D covariance)
+//   geo[2g+1] = {inv_c, opacity, x_min | x_max << 16, y_min | y_max << 16}   (ints as f32 bits)
+//   col[g]    = {color_r, color_g, color_b, depth}
+// Emission and tile counting gather records in depth order, one per Gaussian: they need the
+// geometry only, a 32 B-aligned read. The blends read both and stage them in LDS as
+//   {geo0} {inv_c, opacity, color_r, color_g} {color_b, box lo, box extent, depth}.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -61,8 +64,8 @@ __device__ inline uint32_t key_tile(const KeyLayout& k, uint64_t key) {
     return k.tile_shift < 64 ? (uint32_t)(key >> k.tile_shift) : 0u;
 }
 
-__device__ inline uint32_t box_tiles(float4 r2) {
-    const uint32_t bx = __float_as_uint(r2.y), by = __float_as_uint(r2.z);
+__device__ inline uint32_t box_tiles(float4 geo1) {
+    const uint32_t bx = __float_as_uint(geo1.z), by = __float_as_uint(geo1.w);
     return ((bx >> 16) / kTile - (bx & 0xffffu) / kTile + 1) * ((by >> 16) / kTile - (by & 0xffffu) / kTile + 1);
 }
 
@@ -98,12 +101,12 @@ __device__ inline int wave_inclusive_max(int v) {
 
 // Stores lane's box (zero tiles when !valid) and returns the wave's total tile count.
 // full: every tile of the box is known to be kept (its kept count equals its tile count).
-__device__ inline uint32_t stage_box(WaveBoxes& w, bool valid, float4 r0, float4 r1, float4 r2, uint32_t g,
-                                     uint32_t out, bool full) {
+__device__ inline uint32_t stage_box(WaveBoxes& w, bool valid, float4 r0, float4 r1, uint32_t g, uint32_t out,
+                                     bool full) {
     const uint32_t lane = __lane_id();
     uint32_t total = 0;
     if (valid) {
-        const uint32_t bx = __float_as_uint(r2.y), by = __float_as_uint(r2.z);
+        const uint32_t bx = __float_as_uint(r1.z), by = __float_as_uint(r1.w);
         const int x0 = (int)(bx & 0xffffu), x1 = (int)(bx >> 16), y0 = (int)(by & 0xffffu), y1 = (int)(by >> 16);
         // the record holds 2 * inv_b (halving is exact)
         w.conic[lane] = gsx_tile_conic_make(r0.x, r0.y, r0.z, r0.w * 0.5f, r1.x, r1.y);
@@ -210,7 +213,8 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
     FieldSnapshot snap, int64_t n, const float* __restrict__ mean3d, const float* __restrict__ rotation,
     const float* __restrict__ logscale, const float* __restrict__ opacity, const float* __restrict__ sh0,
     const float* __restrict__ sh1, const float* __restrict__ sh2, const float* __restrict__ sh3, int sh_degree,
-    CameraParams cam, float4* __restrict__ rec, float4* __restrict__ cov_coef, uint32_t* __restrict__ tile_count,
+    CameraParams cam, float4* __restrict__ rec, float4* __restrict__ col, float4* __restrict__ cov_coef,
+    uint32_t* __restrict__ tile_count,
     float* __restrict__ visible_counter, uint32_t* __restrict__ big_list, uint32_t* __restrict__ big_count,
     uint32_t* __restrict__ clear0, uint32_t* __restrict__ clear1, uint32_t* __restrict__ clear2,
     uint32_t* __restrict__ kept_part,
@@ -251,11 +255,11 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
             const uint32_t bx = (uint32_t)p.x_min | ((uint32_t)p.x_max << 16);
             const uint32_t by = (uint32_t)p.y_min | ((uint32_t)p.y_max << 16);
             r0 = make_float4(p.mx, p.my, inv_a, 2.0f * inv_b);
-            r1 = make_float4(inv_c, p.opacity, p.color[0], p.color[1]);
-            r2 = make_float4(p.color[2], __uint_as_float(bx), __uint_as_float(by), p.depth);
-            rec[3 * g + 0] = r0;
-            rec[3 * g + 1] = r1;
-            rec[3 * g + 2] = r2;
+            r1 = make_float4(inv_c, p.opacity, __uint_as_float(bx), __uint_as_float(by));
+            r2 = make_float4(p.color[0], p.color[1], p.color[2], p.depth);
+            rec[2 * g + 0] = r0;
+            rec[2 * g + 1] = r1;
+            col[g] = r2;
             if (cov_coef != nullptr) {
                 // d(conic)/d(cov2d) coefficients with the CPU's rounding (render.c:1578-1579,
                 // 1647-1655): the backward applies them per contribution, as the CPU does,
@@ -269,7 +273,7 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
             }
         }
     }
-    const bool big = visible && box_tiles(r2) > kBigTiles;
+    const bool big = visible && box_tiles(r1) > kBigTiles;
     // depth key of every Gaussian (~0 for invisible ones, which the depth sort drops);
     // big_key_flag (kBigKeyFlag or 0, see there) marks the big boxes for rank_gather_kernel
     if (g < n) {
@@ -282,7 +286,7 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
         depth_keys[g] = key;
     }
     if (big) big_list[atomicAdd(big_count, 1u)] = (uint32_t)g;  // counted by big_tiles_kernel
-    const uint32_t total = stage_box(wb, visible && !big, r0, r1, r2, (uint32_t)g, 0u, false);
+    const uint32_t total = stage_box(wb, visible && !big, r0, r1, (uint32_t)g, 0u, false);
     walk_wave_tiles<false>(wb, total, cam.tiles_x, KeyLayout{}, nullptr, nullptr);
     const uint32_t kept = big ? 0u : wb.kept[__lane_id()];  // big boxes: counted by big_tiles_kernel
     if (g < n) tile_count[g] = kept;
@@ -380,16 +384,15 @@ __device__ inline void emit_block(uint32_t b, int64_t n, const float4* __restric
     const uint32_t o = block_prefix[b] + block_exclusive_scan_256(cnt, s_wave, block_total);
     if (r < n) offsets[r] = o;
     if (r == n - 1) offsets[n] = o + cnt;
-    float4 r0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), r1 = r0, r2 = r0;
+    float4 r0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), r1 = r0;
     if (cnt > 0) {
-        r0 = rec[3 * (size_t)g + 0];
-        r1 = rec[3 * (size_t)g + 1];
-        r2 = rec[3 * (size_t)g + 2];
+        r0 = rec[2 * (size_t)g + 0];
+        r1 = rec[2 * (size_t)g + 1];
     }
-    const bool any = cnt > 0 && box_tiles(r2) <= kBigTiles;  // big boxes are emitted by big_tiles_block
+    const bool any = cnt > 0 && box_tiles(r1) <= kBigTiles;  // big boxes are emitted by big_tiles_block
     // a box whose kept count (from the counting walk's identical tests) is its tile count keeps
     // every tile: emission skips its tests
-    const uint32_t total = stage_box(wb, any, r0, r1, r2, g, o, any && cnt == box_tiles(r2));
+    const uint32_t total = stage_box(wb, any, r0, r1, g, o, any && cnt == box_tiles(r1));
     walk_wave_tiles<true>(wb, total, tiles_x, layout, keys, instance_gaussian);
 }
 
@@ -420,8 +423,8 @@ __device__ inline void big_tiles_block(uint32_t x, uint32_t c, uint32_t gx, cons
     unsigned long long block_kept = 0;
     for (uint32_t i = x; i < count; i += gx) {
         const uint32_t g = big_list[i];
-        const float4 r0 = rec[3 * (size_t)g + 0], r1 = rec[3 * (size_t)g + 1], r2 = rec[3 * (size_t)g + 2];
-        const uint32_t bx = __float_as_uint(r2.y), by = __float_as_uint(r2.z);
+        const float4 r0 = rec[2 * (size_t)g + 0], r1 = rec[2 * (size_t)g + 1];
+        const uint32_t bx = __float_as_uint(r1.z), by = __float_as_uint(r1.w);
         const int x0 = (int)(bx & 0xffffu), x1 = (int)(bx >> 16), y0 = (int)(by & 0xffffu), y1 = (int)(by >> 16);
         const uint32_t tx0 = (uint32_t)x0 / kTile, ty0 = (uint32_t)y0 / kTile;
         const uint32_t wx = (uint32_t)x1 / kTile - tx0 + 1;
@@ -650,7 +653,8 @@ __device__ inline size_t checkpoint_slot(uint32_t range_start, int tile, uint32_
 // ---------------------------------------------------------------------------------------------
 __global__ __launch_bounds__(kBlendThreads) void blend_forward_kernel(
     const uint2* __restrict__ ranges, const uint32_t* __restrict__ values,
-    const uint32_t* __restrict__ instance_gaussian, const float4* __restrict__ rec, uint32_t* __restrict__ sorted_g,
+    const uint32_t* __restrict__ instance_gaussian, const float4* __restrict__ rec, const float4* __restrict__ col,
+    uint32_t* __restrict__ sorted_g,
     CameraParams cam, float* __restrict__ out_rgb,
     float* __restrict__ out_t, uint32_t* __restrict__ out_last, float* __restrict__ ckpt) {
     __shared__ float4 s_r0[kBlendThreads];
@@ -680,13 +684,11 @@ __global__ __launch_bounds__(kBlendThreads) void blend_forward_kernel(
         if (j < range.y) {
             const uint32_t g = instance_gaussian[values[j]];
             if (sorted_g != nullptr) sorted_g[j] = g;  // TRAIN: the backward reads it
-            s_r0[threadIdx.x] = rec[3 * (size_t)g + 0];
-            s_r1[threadIdx.x] = rec[3 * (size_t)g + 1];
-            float4 r2 = rec[3 * (size_t)g + 2];
-            const uint32_t bx = __float_as_uint(r2.y), by = __float_as_uint(r2.z);
-            r2.y = __uint_as_float(box_lo(bx, by));
-            r2.z = __uint_as_float(box_ext(bx, by));
-            s_r2[threadIdx.x] = r2;
+            const float4 geo1 = rec[2 * (size_t)g + 1], c = col[g];
+            const uint32_t bx = __float_as_uint(geo1.z), by = __float_as_uint(geo1.w);
+            s_r0[threadIdx.x] = rec[2 * (size_t)g + 0];
+            s_r1[threadIdx.x] = make_float4(geo1.x, geo1.y, c.x, c.y);
+            s_r2[threadIdx.x] = make_float4(c.z, __uint_as_float(box_lo(bx, by)), __uint_as_float(box_ext(bx, by)), c.w);
         } else {
             // past the list: a box no pixel lies in, so the last bucket can run whole
             s_r2[threadIdx.x] = make_float4(0.0f, __uint_as_float(kEmptyBoxLo), 0.0f, 0.0f);
@@ -781,7 +783,8 @@ constexpr int kBatchBuckets = kBackBatch / kBucket;
 
 __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
     const uint2* __restrict__ ranges, const uint32_t* __restrict__ values, const uint32_t* __restrict__ sorted_g,
-    const float4* __restrict__ rec, const float4* __restrict__ cov_coef, const float* __restrict__ ckpt,
+    const float4* __restrict__ rec, const float4* __restrict__ col, const float4* __restrict__ cov_coef,
+    const float* __restrict__ ckpt,
     CameraParams cam, const float* __restrict__ grad_rgb, const float* __restrict__ final_t,
     const uint32_t* __restrict__ last_contrib, float* __restrict__ instance_grad,
     float* __restrict__ instance_grad_op) {
@@ -862,13 +865,12 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
             // below end_all lies in such a batch; entries from end_all on contribute nothing
             if (j < end_all) {
                 const uint32_t g = sorted_g[j];
-                s_r0[threadIdx.x] = rec[3 * (size_t)g + 0];
-                s_r1[threadIdx.x] = rec[3 * (size_t)g + 1];
-                float4 r2 = rec[3 * (size_t)g + 2];
-                const uint32_t bx = __float_as_uint(r2.y), by = __float_as_uint(r2.z);
-                r2.y = __uint_as_float(box_lo(bx, by));
-                r2.z = __uint_as_float(box_ext(bx, by));
-                s_r2[threadIdx.x] = r2;
+                const float4 geo1 = rec[2 * (size_t)g + 1], c = col[g];
+                const uint32_t bx = __float_as_uint(geo1.z), by = __float_as_uint(geo1.w);
+                s_r0[threadIdx.x] = rec[2 * (size_t)g + 0];
+                s_r1[threadIdx.x] = make_float4(geo1.x, geo1.y, c.x, c.y);
+                s_r2[threadIdx.x] =
+                    make_float4(c.z, __uint_as_float(box_lo(bx, by)), __uint_as_float(box_ext(bx, by)), c.w);
                 s_k0[threadIdx.x] = cov_coef[2 * (size_t)g + 0];
                 const float4 k1 = cov_coef[2 * (size_t)g + 1];
                 s_k1[threadIdx.x] = make_float2(k1.x, k1.y);

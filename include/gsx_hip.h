@@ -138,7 +138,7 @@ typedef struct gsx_hip_render_buffers {
     const uint64_t* sorted_keys;   /* [instance_count] see gsx_hip_render_stats for the layout */
     const uint32_t* sorted_values; /* [instance_count] emission position of each sorted key */
     const uint32_t* tile_ranges;   /* [tile_count][2] start, end */
-    const float* records;          /* [N][12] packed per-Gaussian blend records */
+    const float* records;          /* [N][8] geometry then [N][4] colour+depth blend records */
     const uint32_t* tile_counts;   /* [N] tiles touched per Gaussian (0 = culled) */
     const uint32_t* instance_gaussian; /* [instance_count] Gaussian index of each emission position */
     const float* final_transmittance; /* [H*W] */
