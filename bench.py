@@ -35,37 +35,104 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def algorithmic_bytes(stage, n, visible, instances, tiles, pixels, sort_passes, depth_sort_passes, train=True):
-    """Bytes each stage must move at minimum, given this build's data layout (the roofline
-    numerators). n Gaussians, visible V, instances I, tiles T, pixels Px, E = 3 Px elements."""
-    i = instances
+def algorithmic_bytes(stage, geo, train=True):
+    """Minimum HBM bytes of each stage in this build's data layout: every input byte read once and
+    every output byte written once, however often the kernel itself touches it (the roofline
+    numerators; at or below what the FETCH_SIZE / WRITE_SIZE counters show).
+    geo: n Gaussians, V visible (at least one tile), I instances, T tiles, P pixels, R entries the
+    blend must reach (per tile, up to its last contributing entry), U distinct Gaussians among
+    them (the touched Gaussians) and It their instances, C transmittance checkpoints the backward
+    needs (per pixel, one per 8-entry bucket up to its last contribution), S / D tile- and
+    depth-sort passes."""
+    n, v, i, t, p = geo["n"], geo["V"], geo["I"], geo["T"], geo["P"]
+    r, u, c = geo["R"], geo["U"], geo["C"]
     if stage == "preprocess":
-        return 68 * n + (80 if train else 48) * visible
+        # parameters in (SH0: 56 B), the TRAIN snapshot of them out (56 B), tile count + depth key
+        # out (12 B); per visible Gaussian its geometry + colour record (48 B) and, TRAIN, the
+        # conic-gradient coefficients (32 B)
+        return (56 + (56 if train else 0) + 12) * n + (80 if train else 48) * v
     if stage == "depth_order":
-        # depth-key sort (keys only: read for the histogram, read + write to scatter), rank
-        # gather (key, count, three index writes), count scan
-        return depth_sort_passes * 24 * n + 28 * n + 8 * n
+        # depth keys in; the tile counts of the visible ones gathered, their Gaussian and count
+        # out in depth order (the intermediate sort passes may stay on chip)
+        return 8 * n + 12 * v
     if stage == "emit":
-        return 12 * n + 48 * visible + 12 * i
+        # per visible rank: count, Gaussian, geometry record in, offset out; per instance the key
+        # (8 B), its Gaussian (4 B) and, TRAIN, its tile (4 B) out
+        return 44 * v + (16 if train else 12) * i
     if stage == "sort":
-        return sort_passes * 24 * i
+        # the convention of sort bandwidth: per pass each 8-byte key is read twice (histogram,
+        # scatter) and written once
+        return geo["S"] * 24 * i
     if stage == "ranges":
-        return 20 * i + 8 * tiles
+        return 12 * i + 8 * t  # sorted keys in, emission positions out; one range per tile
     if stage == "blend_forward":
-        return 52 * i + 20 * pixels + (32 * i if train else 0)
+        # ranges, reached entries' positions + Gaussians in, each reached Gaussian's record once;
+        # image (12 B) + final T + last position out; TRAIN: each reached entry's Gaussian and the
+        # checkpoints out
+        return 8 * t + 8 * r + 48 * u + 20 * p + ((4 * r + 4 * c) if train else 0)
     if stage == "blend_backward":
-        return 156 * i + 20 * pixels
+        # ranges, per pixel the image gradient + final T + last position, the checkpoints, reached
+        # entries' positions + Gaussians, each reached Gaussian's record + conic-gradient
+        # coefficients once in; a 36-byte partial per reached entry and each tile's cut out
+        return 12 * t + 20 * p + 4 * c + 8 * r + 80 * u + 36 * r
     if stage == "instance_reduce":
-        return 36 * i + 40 * n
+        # per visible rank its Gaussian, offset and touched flag, the tiles of the touched
+        # Gaussians' instances and the reached entries' partials in, 9-float screen gradients out
+        return 9 * v + 4 * geo["It"] + 36 * r + 36 * v
     if stage == "projection_backward":
-        return 148 * n
+        return (36 + 56 + 56) * n  # screen gradients + snapshot in, five parameter gradients out
     if stage == "loss_forward":
-        return 24 * 3 * pixels
+        # prediction + target in, loss map accumulated (in + out), SSIM workspace (3 floats) out
+        return (4 + 4 + 8 + 12) * 3 * p
     if stage == "loss_backward":
-        return 28 * 3 * pixels
+        # prediction + target + workspace in, image gradient accumulated (in + out)
+        return (4 + 4 + 12 + 8) * 3 * p
     if stage == "adam":
-        return 28 * 14 * n
+        return 28 * 14 * n  # 14 floats per Gaussian: parameter, m, v in and out, gradient in
     return 0
+
+
+def render_geometry(lib, renderer, n, width, height):
+    """The byte model's per-step quantities, read from the render context's buffers after a
+    TRAIN forward + backward (one synchronisation; used between timed steps only)."""
+    import torch
+
+    from gsx_amd import _lib
+    st = renderer.stats()
+    buf = renderer.buffers()
+    i_count, t_count, p_count = int(st.instance_count), int(st.tile_count), width * height
+    dev = "cuda"
+
+    def pull(ptr_value, count):
+        out = torch.empty(count, dtype=torch.int32, device=dev)
+        if count > 0:
+            _lib.check(lib.gsx_hip_memcpy_dtod_async(ctypes.c_void_p(out.data_ptr()), ptr_value, count * 4, None),
+                       "copy render buffer")
+        return out
+
+    tc = pull(buf.tile_counts, n)
+    rng = pull(buf.tile_ranges, 2 * t_count).view(t_count, 2).long()
+    last = pull(buf.last_contributor, p_count).long()
+    vals = pull(buf.sorted_values, i_count).long()
+    ig = pull(buf.instance_gaussian, i_count).long()
+    torch.cuda.synchronize()
+    tiles_x = (width + 15) // 16
+    pix = torch.arange(p_count, device=dev)
+    tile_of = (pix // width // 16) * tiles_x + (pix % width) // 16
+    rel = (last - rng[tile_of, 0]).clamp_min(0)
+    reach = torch.zeros(t_count, dtype=torch.long, device=dev).scatter_reduce(0, tile_of, rel, "amax")
+    r_total = int(reach.sum())
+    c_total = int(((rel + 7) // 8).sum())
+    u_total = it_total = 0
+    if r_total > 0:
+        tile_rep = torch.repeat_interleave(torch.arange(t_count, device=dev), reach)
+        first = torch.cumsum(reach, 0) - reach
+        j = rng[tile_rep, 0] + torch.arange(r_total, device=dev) - first[tile_rep]
+        touched = torch.bincount(ig[vals[j]], minlength=n) > 0
+        u_total = int(touched.sum())
+        it_total = int(tc[touched].long().sum())
+    return {"n": n, "V": int((tc > 0).sum()), "I": i_count, "T": t_count, "P": p_count, "R": r_total,
+            "U": u_total, "It": it_total, "C": c_total, "S": int(st.sort_passes), "D": int(st.depth_sort_passes)}
 
 
 CPU_SAMPLE_STRIDE = 10
@@ -77,9 +144,6 @@ STAGE_KERNEL = {"preprocess": "preprocess_kernel", "emit": "emit_kernel", "range
                 "loss_backward": "ssim_backward_kernel", "adam": "adam_multi_kernel"}
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_metric.txt")
 SQ_FILE = os.path.join(ROOT, "profiles", "sq_counters_metric.md")
-# Nominal VALU issue peak: 256 CUs x 4 SIMDs x 2.4 GHz, one wave64 instruction per 4 cycles on a
-# 16-lane SIMD (some instruction mixes issue faster, so this is a reference, not a hard ceiling).
-VALU_PEAK_GINSTR = 256 * 4 * 2.4 / 4.0
 
 
 def measured_traffic(kernel):
@@ -95,27 +159,31 @@ def measured_traffic(kernel):
     return None
 
 
-def profiled_valu_instructions(kernel):
-    """VALU wave instructions per launch of `kernel` from the committed rocprofv3 SQ_INSTS_VALU
-    summary, or None."""
-    if kernel is None or not os.path.exists(SQ_FILE):
+def profiled_pipe_counters(kernel):
+    """VALU busy and LDS bank-conflict percentages of `kernel` (rocprofv3's derived VALUBusy =
+    100 SQ_ACTIVE_INST_VALU 4 / SIMDs / GRBM_GUI_ACTIVE and LDSBankConflict = 100
+    SQ_LDS_BANK_CONFLICT / GRBM_GUI_ACTIVE / CUs) from the committed SQ summary, or None."""
+    if not os.path.exists(SQ_FILE):
         return None
     with open(SQ_FILE) as f:
         for line in f:
             cells = [c.strip() for c in line.strip().strip("|").split("|")]
-            if len(cells) >= 7 and cells[0] == kernel:
+            if len(cells) >= 3 and cells[0] == kernel and cells[1].startswith("pipe"):
                 try:
-                    return int(float(cells[6]))
-                except ValueError:
+                    return {"valu_busy_pct": float(cells[2]), "lds_bank_conflict_pct": float(cells[3]),
+                            "source": os.path.relpath(SQ_FILE, ROOT)}
+                except (ValueError, IndexError):
                     return None
     return None
 
 
 def cpu_baseline(scene, camera_block, target, iters):
     """Time the unmodified gsx CPU backend (oracle/_ref) on a bounded sample of the workload:
-    every 10th Gaussian of the 1M scene (same distributions) at the full 1920x1080, pose 0.
-    The full 1M scene cannot run there: its near-plane Gaussians' pixel boxes cover the image,
-    and the CPU backward's contribution scratch exceeds its int32 tensor limit."""
+    every 10th Gaussian of the 1M scene (same distributions) at the full 1920x1080, pose 0, the
+    whole step. Then one step of the full 1M scene without the render backward: its near-plane
+    Gaussians' pixel boxes cover the image, and the CPU backward's contribution scratch exceeds
+    its int32 tensor limit there (gsx-cpu/render.c:1448-1455, gsx-cpu/render.c:167); the render
+    forward, both losses and Adam run at full size."""
     import numpy as np
 
     from gsx_amd import scenes
@@ -128,7 +196,166 @@ def cpu_baseline(scene, camera_block, target, iters):
     t0 = time.perf_counter()
     _, stages = ref.train_steps(sub, camera_block, target, iters)
     elapsed = time.perf_counter() - t0
-    return elapsed, stages, sub.count
+    _, full_stages = ref.train_steps(scene, camera_block, target, 1, skip_render_backward=True)
+    return elapsed, stages, sub.count, full_stages
+
+
+def train_runner(lib, gaussians, width, height):
+    """One training step of the metric's sequence (TRAIN render, fused 0.8 L1 + 0.2 (1 - SSIM)
+    forward and backward, render backward, Adam) on `gaussians`; returns (step, renderer)."""
+    import numpy as np
+    import torch
+
+    from gsx_amd import _lib
+    from gsx_amd.backend import Adam, GaussianTensors, Renderer, ptr, stream_handle
+
+    grads = gaussians.zeros_like_grads()
+    renderer = Renderer(width, height)
+    img = torch.empty((3, height, width), dtype=torch.float32, device="cuda")
+    loss_and_grad = torch.empty((2,) + tuple(img.shape), dtype=torch.float32, device="cuda")
+    loss_map, grad_img = loss_and_grad[0], loss_and_grad[1]
+    ssim_ws = torch.empty(3 * img.numel(), dtype=torch.float32, device="cuda")
+    opt = Adam([dict(parameter=gaussians.mean3d, gradient=grads.mean3d, learning_rate=1e-3),
+                dict(parameter=gaussians.logscale, gradient=grads.logscale, learning_rate=1e-2),
+                dict(parameter=gaussians.rotation, gradient=grads.rotation, learning_rate=1e-2),
+                dict(parameter=gaussians.opacity, gradient=grads.opacity, learning_rate=1e-2),
+                dict(parameter=gaussians.sh0, gradient=grads.sh0, learning_rate=1e-2)])
+    gs_l1 = float(np.float32(0.8) / np.float32(img.numel()))
+    gs_ssim = float(np.float32(0.2) / np.float32(img.numel()))
+
+    def step(cam, tgt):
+        st = stream_handle()
+        renderer.render(cam, gaussians, train=True, out_rgb=img)
+        loss_and_grad.zero_()
+        _lib.check(lib.gsx_hip_loss_ssim_chw_f32_forward_kernel_launch(
+            ptr(loss_map), ptr(img), ptr(tgt), 1, 3, height, width, 0.2, ptr(ssim_ws), 0.8, 1, st), "loss forward")
+        _lib.check(lib.gsx_hip_loss_ssim_chw_f32_backward_kernel_launch(
+            ptr(grad_img), ptr(img), ptr(tgt), 1, 3, height, width, gs_ssim, ptr(ssim_ws), gs_l1, 1, st),
+            "loss backward")
+        renderer.backward(grad_img, grads)
+        opt.step()
+    return step, renderer
+
+
+def timed_steps(step, inputs, warmup, steps):
+    import torch
+    for i in range(warmup):
+        step(*inputs[i % len(inputs)])
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        step(*inputs[(warmup + i) % len(inputs)])
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def extra_workloads(lib, steps):
+    """Throughput of the other BASELINE configs at their stated sizes (one GPU), the tile sort's
+    bandwidth on config 4's instances, and one density-control refine at 1M rows."""
+    import numpy as np
+    import torch
+
+    from gsx_amd import scenes
+    from gsx_amd.backend import Camera, DensityControl, GaussianTensors
+
+    out = {}
+    # config 2: image fit, 1M Gaussians on z = 0, 1024^2, one camera
+    w = scenes.config2()
+    g = GaussianTensors.from_scene(w.scene)
+    step, r = train_runner(lib, g, 1024, 1024)
+    inputs = [(Camera.from_block(w.camera), torch.from_numpy(w.target).cuda())]
+    ms = 1000.0 * timed_steps(step, inputs, 3, steps)
+    out["c2_image_fit"] = {"gaussians": w.scene.count, "width": 1024, "height": 1024, "ms_per_step": round(ms, 3),
+                           "it_s": round(1000.0 / ms, 1), "instances": int(r.stats().instance_count)}
+    del g, step, r, inputs
+    log(f"config 2: {out['c2_image_fit']}")
+    # config 3: 3M Gaussians, 1080p, 24 orbit poses
+    base = scenes.config3()
+    g = GaussianTensors.from_scene(base.scene)
+    step, r = train_runner(lib, g, 1920, 1080)
+    inputs = []
+    for k in range(24):
+        block = scenes.camera(1920, 1080, 1600.0, pose=tuple(scenes.orbit_pose(k)), near=0.01, far=100.0)
+        tgt = base.target if k == 0 else scenes.target_image(0, 103 + k, 1920, 1080, 2)
+        inputs.append((Camera.from_block(block), torch.from_numpy(tgt).cuda()))
+    ms = 1000.0 * timed_steps(step, inputs, 2, steps)
+    out["c3_scene_training"] = {"gaussians": base.scene.count, "width": 1920, "height": 1080, "poses": 24,
+                                "ms_per_step": round(ms, 3), "it_s": round(1000.0 / ms, 1),
+                                "instances_last_pose": int(r.stats().instance_count)}
+    del g, step, r, inputs, base
+    log(f"config 3: {out['c3_scene_training']}")
+    # config 4: 6M Gaussians, 1080p, the sort / blend stress; stage times from HIP events
+    w = scenes.config4()
+    g = GaussianTensors.from_scene(w.scene)
+    step, r = train_runner(lib, g, 1920, 1080)
+    inputs = [(Camera.from_block(w.camera), torch.from_numpy(w.target).cuda())]
+    c4_steps = max(2, steps // 4)
+    ms = 1000.0 * timed_steps(step, inputs, 1, c4_steps)
+    r.set_timing(1)
+    step(*inputs[0])
+    torch.cuda.synchronize()
+    stage = r.timings()
+    r.set_timing(0)
+    st = r.stats()
+    inst = int(st.instance_count)
+    sort_bytes = int(st.sort_passes) * 24 * inst
+    out["c4_sort_stress"] = {"gaussians": w.scene.count, "width": 1920, "height": 1080, "ms_per_step": round(ms, 3),
+                             "it_s": round(1000.0 / ms, 2), "instances": inst, "sort_passes": int(st.sort_passes),
+                             "sort_ms": round(stage["sort"], 3),
+                             "sort_gbps": round(sort_bytes / (stage["sort"] * 1e-3) / 1e9, 1),
+                             "sort_hbm_frac": round(sort_bytes / (stage["sort"] * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+                             "stage_ms": {k: round(v, 3) for k, v in stage.items()}}
+    del g, step, r, inputs, w
+    log(f"config 4: {out['c4_sort_stress']}")
+    torch.cuda.empty_cache()
+    # density control at 1M rows (the metric scene with seeded statistics), rows in capacity-sized
+    # buffers with Adam moments: one ABSGS refine (prune + duplicate + split) and one MCMC refine
+    # (relocation + 10% growth). Each is timed from the same uploaded state three times after one
+    # untimed call; the upload is outside the timed region.
+    sc = scenes.metric_scene().scene
+    n = sc.count
+    rng = np.random.default_rng(7)
+    host = {"mean3d": sc.mean3d, "rotation": sc.rotation, "logscale": sc.logscale, "opacity": sc.opacity,
+            "sh0": sc.sh0, "grad_acc": (rng.random(n) * 2e-3).astype(np.float32),
+            "absgrad_acc": (rng.random(n) * 8e-3).astype(np.float32),
+            "visible_counter": rng.integers(0, 20, n).astype(np.float32)}
+    widths = {"mean3d": 3, "rotation": 4, "logscale": 3, "opacity": 1, "sh0": 3, "grad_acc": 1, "absgrad_acc": 1,
+              "visible_counter": 1}
+    cap = n + n // 5
+    d = {k: torch.zeros((cap, widths[k]) if widths[k] > 1 else (cap,), dtype=torch.float32, device="cuda")
+         for k in host}
+    src = {k: torch.from_numpy(v.reshape(n, widths[k]) if widths[k] > 1 else v).cuda() for k, v in host.items()}
+    moms = {k: (torch.zeros_like(d[k]), torch.zeros_like(d[k])) for k in ("mean3d", "rotation", "logscale",
+                                                                         "opacity", "sh0")}
+    o = {k: torch.zeros_like(v) for k, v in d.items()}
+    om = {k: (torch.zeros_like(a), torch.zeros_like(b)) for k, (a, b) in moms.items()}
+    common = dict(pruning_opacity_threshold=0.05, opacity_clamp_value=0.3, max_world_scale=0.5,
+                  duplicate_grad_threshold=2e-4, duplicate_scale_threshold=0.01, scene_scale=4.0, refine_every=100,
+                  start_refine=0, end_refine=1000, reset_every=0, max_num_gaussians=cap)
+    for name, params in (("absgs_refine", dict(algorithm=1, duplicate_absgrad_threshold=4e-4)),
+                         ("mcmc_refine", dict(algorithm=2, grow_ratio=0.1, noise_strength=50.0,
+                                              mean3d_learning_rate=1e-3))):
+        adc = DensityControl({**common, **params}, seed=3)
+        times = []
+        for rep in range(4):
+            for k in d:
+                d[k][:n].copy_(src[k])
+            for a, b in moms.values():
+                a.zero_()
+                b.zero_()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            count, _, counts = adc.step(100, n, 0, d, moms, cap, o, om)
+            torch.cuda.synchronize()
+            if rep > 0:
+                times.append(1000.0 * (time.perf_counter() - t0))
+        out[name] = {"rows_before": n, "rows_after": int(count), "ms": round(sum(times) / len(times), 3),
+                     "counts_pruned_duplicated_grown_reset": [int(c) for c in counts]}
+        log(f"{name}: {out[name]}")
+        adc.close()
+    del d, src, moms, o, om
+    torch.cuda.empty_cache()
+    return out
 
 
 def main():
@@ -144,6 +371,8 @@ def main():
                     help="run one plain copy kernel of this size first (reference for traffic counters)")
     ap.add_argument("--cpu-baseline-iters", type=int, default=3,
                     help="reference CPU steps to time on the full workload (0 disables)")
+    ap.add_argument("--extra-steps", type=int, default=10,
+                    help="timed steps of the config 2/3/4 and density-control lines (0 disables them)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; multi-GPU scaling (image tile bands "
@@ -281,23 +510,21 @@ def main():
     renderer.set_timing(args.steps)
     log(f"per-stage timing over the same {args.steps} steps")
     torch.cuda.synchronize()
+    geos = []
     for i in range(args.steps):
         step(args.warmup + i, record=True)  # the poses of pass 1 again
+        # the byte model's inputs of this step (buffer reads outside the stage events)
+        geos.append(render_geometry(lib, renderer, args.gaussians, W, H))
     torch.cuda.synchronize()
     stage_ms = renderer.timings()
     renderer.set_timing(0)
     for k, pairs in ev.items():
         stage_ms[k] = sum(a.elapsed_time(b) for a, b in pairs) / len(pairs)
-    stats = renderer.stats()
-    instances = int(stats.instance_count)
-    visible = int((torch.zeros(1)).item())  # filled below
-    # visible Gaussians of the last pose (tile count > 0), for the byte model
-    buf = renderer.buffers()
-    tc = torch.empty(args.gaussians, dtype=torch.int32, device="cuda")
-    _lib.check(lib.gsx_hip_memcpy_dtod_async(ctypes.c_void_p(tc.data_ptr()), buf.tile_counts, tc.numel() * 4, None))
-    torch.cuda.synchronize()
-    visible = int((tc > 0).sum().item())
-    log(f"train: {it_s:.1f} it/s ({1000.0 / it_s:.3f} ms/step), instances {instances}, visible {visible}")
+    geo_mean = {k: sum(gm[k] for gm in geos) / len(geos) for k in geos[0]}
+    instances = geos[-1]["I"]
+    visible = geos[-1]["V"]
+    log(f"train: {it_s:.1f} it/s ({1000.0 / it_s:.3f} ms/step), instances {instances}, visible {visible}, "
+        f"reached {geos[-1]['R']}, distinct reached {geos[-1]['U']} (last pose)")
 
     # inference forward FPS on the same scene (cycling poses)
     fps_steps = max(args.steps, 20)
@@ -311,27 +538,19 @@ def main():
     fps = fps_steps / (time.perf_counter() - t0)
     log(f"inference forward: {fps:.1f} FPS")
 
-    pixels = H * W
-    tiles = int(stats.tile_count)
     kernels = []
     for name, ms in stage_ms.items():
-        b = algorithmic_bytes(name, args.gaussians, visible, instances, tiles, pixels, int(stats.sort_passes),
-                              int(stats.depth_sort_passes))
+        # the mean over the same steps of each step's minimum bytes
+        b = sum(algorithmic_bytes(name, gm) for gm in geos) / len(geos)
         gbps = b / (ms * 1e-3) / 1e9 if ms > 0 else 0.0
         kernels.append({"stage": name, "ms": round(ms, 4), "algorithmic_bytes": int(b), "gbps": round(gbps, 1),
                         "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4)})
     kernels.sort(key=lambda k: -k["ms"])
     dominant = kernels[0]
     sort_entry = next(k for k in kernels if k["stage"] == "sort")
-    # the dominant kernel is bound by VALU issue rather than HBM: its wave instructions per launch
-    # (committed SQ profile of this workload) over the launch time measured above
-    valu_instr = profiled_valu_instructions(STAGE_KERNEL.get(dominant["stage"]))
-    valu_issue = None
-    if valu_instr is not None and dominant["ms"] > 0:
-        rate = valu_instr / (dominant["ms"] * 1e-3) / 1e9
-        valu_issue = {"kernel": STAGE_KERNEL.get(dominant["stage"]), "instructions": valu_instr,
-                      "achieved": round(rate, 1), "peak": VALU_PEAK_GINSTR, "unit": "G wave-instr/s",
-                      "frac": round(rate / VALU_PEAK_GINSTR, 4)}
+    # the blend kernels are bound by the vector ALU and LDS rather than HBM: their VALU busy and
+    # LDS bank-conflict shares of GPU time from the committed SQ profile of this workload
+    pipe = {k: profiled_pipe_counters(k) for k in ("blend_forward_kernel", "blend_backward_kernel")}
 
     result = {
         "metric": "fwd+bwd train iters/sec @1M Gaussians 1920x1080; fwd render FPS; sort GB/s",
@@ -349,7 +568,8 @@ def main():
         "config": {"workload": "metric: config-3 generator at N=1M, 1920x1080, f=1600, 24 orbit poses, SH0, "
                                "fwd+bwd+0.8*L1+0.2*(1-SSIM)+Adam",
                    "gaussians": args.gaussians, "width": W, "height": H, "poses": args.poses,
-                   "instances_last_pose": instances, "visible_last_pose": visible},
+                   "instances_last_pose": instances, "visible_last_pose": visible,
+                   "mean_per_step": {k: round(v, 1) for k, v in geo_mean.items()}},
         "train_its_cloned_state": round(it_s_clone, 2),
         "render_fps": round(fps, 1),
         "sort_gbps": sort_entry["gbps"],
@@ -359,9 +579,14 @@ def main():
                      "achieved": dominant["gbps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": dominant["hbm_frac"], "traffic": measured_traffic(STAGE_KERNEL.get(dominant["stage"])),
                      "algorithmic_bytes": dominant["algorithmic_bytes"], "launch_ms": dominant["ms"]},
-        "valu_issue": valu_issue,
+        "blend_pipeline": pipe,
         "device": dev_name,
     }
+
+    if args.extra_steps > 0:
+        del renderer, g, grads, opt
+        torch.cuda.empty_cache()
+        result["workloads"] = extra_workloads(lib, args.extra_steps)
 
     if args.cpu_baseline_iters > 0:
         log(f"CPU baseline: reference CPU backend, {args.cpu_baseline_iters} step(s) of the full workload, 1 thread")
@@ -369,7 +594,7 @@ def main():
                           0.01, 100.0, 0, 0, 0], np.float32)
         res = cpu_baseline(base.scene, block, base.target, args.cpu_baseline_iters)
         if res is not None:
-            secs, stages, sub_n = res
+            secs, stages, sub_n, full_stages = res
             result["cpu_baseline"] = {
                 "value": round(args.cpu_baseline_iters / secs, 5), "unit": "it/s", "cores": 1, "kind": "reference",
                 "sample": f"{args.cpu_baseline_iters} step(s) of the same training step through the unmodified "
@@ -379,7 +604,12 @@ def main():
                 "seconds_per_step": round(secs / args.cpu_baseline_iters, 3),
                 "stage_seconds": {k: round(float(v) / args.cpu_baseline_iters, 3) for k, v in
                                   zip(("render_forward", "loss_forward", "loss_backward", "render_backward",
-                                       "adam"), stages)}}
+                                       "adam"), stages)},
+                "full_scene_stage_seconds": {
+                    k: round(float(v), 3) for k, v in zip(("render_forward", "loss_forward", "loss_backward",
+                                                           "adam"), full_stages[[0, 1, 2, 4]])},
+                "full_scene_note": f"one step of the full {base.scene.count}-Gaussian scene at {W}x{H}, pose 0, "
+                                   "without the render backward (Adam on zero gradients)"}
         else:
             result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)

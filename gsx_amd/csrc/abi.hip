@@ -247,7 +247,7 @@ int bits_for(uint32_t v) {
 }  // namespace
 
 struct gsx_hip_render_context {
-    DeviceBuffer rec, cov_coef, ckpt, inst_gauss, inst_grad, tile_count, big_list, offsets, scan_temp, keys, vals,
+    DeviceBuffer rec, cov_coef, ckpt, inst_gauss, inst_tile, tile_cut, touched, inst_grad, tile_count, big_list, offsets, scan_temp, keys, vals,
         keys_alt, sort_temp, ranges, sorted_g, final_t, last, grad2d, depth_keys, depth_keys_alt, rank_g, rank_count,
         g_rank, long_list, multi_list, counters, big_chunk_counts, depth_sort_temp;
     // partial instance counts written by the counting kernels (preprocess: one u32 per workgroup;
@@ -556,7 +556,8 @@ gsx_hip_status gsx_hip_render_context_create(gsx_hip_render_context** out_contex
 
 gsx_hip_status gsx_hip_render_context_destroy(gsx_hip_render_context* ctx) {
     if (ctx == nullptr) return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "context must be non-null");
-    DeviceBuffer* all[] = {&ctx->rec,       &ctx->cov_coef, &ctx->ckpt,      &ctx->inst_gauss, &ctx->inst_grad,
+    DeviceBuffer* all[] = {&ctx->rec,       &ctx->cov_coef, &ctx->ckpt,      &ctx->inst_gauss, &ctx->inst_tile,
+                           &ctx->tile_cut,  &ctx->touched,  &ctx->inst_grad,
                            &ctx->tile_count, &ctx->big_list, &ctx->offsets,   &ctx->scan_temp,  &ctx->keys,
                            &ctx->vals,       &ctx->keys_alt, &ctx->sort_temp,  &ctx->ranges,
                            &ctx->sorted_g,   &ctx->final_t,  &ctx->last,      &ctx->grad2d,     &ctx->depth_keys,
@@ -676,6 +677,7 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     const size_t n1 = (size_t)(n > 0 ? n : 1);
     GSX_TRY(ctx->rec.reserve(n1 * 3 * sizeof(float4), "rec"));
     if (train) GSX_TRY(ctx->cov_coef.reserve(n1 * 2 * sizeof(float4), "cov_coef"));
+    if (train) GSX_TRY(ctx->touched.reserve(n1, "touched"));
     GSX_TRY(ctx->tile_count.reserve(n1 * sizeof(uint32_t), "tile_count"));
     GSX_TRY(ctx->counters.reserve(8 * sizeof(uint32_t), "counters"));
     GSX_TRY(ctx->big_list.reserve(n1 * sizeof(uint32_t), "big_list"));
@@ -749,7 +751,8 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
                            ctx->big_list.as<uint32_t>(), big_count, counters + 1, counters + 2 + (ctx->big_slot ^ 1),
                            counters + 4,
                            static_cast<uint32_t*>(ctx->kept_parts.dev), ctx->depth_keys.as<uint64_t>(), near_bits,
-                           depth_max, index_bits, big_flag ? kBigKeyFlag : 0ull);
+                           depth_max, index_bits, big_flag ? kBigKeyFlag : 0ull,
+                           train ? ctx->touched.as<uint8_t>() : nullptr);
         GSX_HIP_TRY(hipGetLastError(), "preprocess_kernel");
         ctx->big_slot ^= 1;  // the slot this preprocess cleared
         const uint32_t big_blocks = kBigBlocks * big_chunks;
@@ -818,6 +821,7 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
         // bucket checkpoints: at most I/kBucket + tiles + 1 slots of 256 floats
         GSX_TRY(ctx->ckpt.reserve(((size_t)count / kBucket + (size_t)tiles + 2) * 256 * sizeof(float),
                                   "checkpoints"));
+        GSX_TRY(ctx->inst_tile.reserve(c1 * sizeof(uint32_t), "instance_tile"));
     }
     if (n > 0) {
         const uint32_t big_blocks = kBigBlocks * big_chunks;
@@ -825,7 +829,8 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
                            ctx->rank_g.as<uint32_t>(), ctx->rank_count.as<uint32_t>(), ctx->scan_temp.as<uint32_t>(),
                            ctx->offsets.as<uint32_t>(), cam.tiles_x, layout, ctx->big_list.as<uint32_t>(), big_count,
                            kBigBlocks, big_blocks, big_chunk, ctx->big_chunk_counts.as<uint32_t>(),
-                           ctx->g_rank.as<uint32_t>(), ctx->keys.as<uint64_t>(), ctx->inst_gauss.as<uint32_t>());
+                           ctx->g_rank.as<uint32_t>(), ctx->keys.as<uint64_t>(), ctx->inst_gauss.as<uint32_t>(),
+                           train ? ctx->inst_tile.as<uint32_t>() : nullptr);
         GSX_HIP_TRY(hipGetLastError(), "emit_kernel");
     }
     GSX_TRY(record(ctx, 3, stream));
@@ -882,6 +887,7 @@ gsx_hip_status enqueue_backward(gsx_hip_render_context* ctx, const float* grad_r
                                    "instance_grad"));
     const CameraParams& cam = ctx->cam;
     const int32_t tiles = cam.tiles_x * cam.tiles_y;
+    GSX_TRY(ctx->tile_cut.reserve((size_t)(tiles > 0 ? tiles : 1) * sizeof(uint32_t), "tile_cut"));
     const uint32_t* svals = ctx->sorted_vals;
     const uint32_t* counters = ctx->counters.as<uint32_t>();  // as the forward left them
     // per-instance partials: [I][8] records, then the [I] opacity terms
@@ -892,7 +898,8 @@ gsx_hip_status enqueue_backward(gsx_hip_render_context* ctx, const float* grad_r
     hipLaunchKernelGGL(blend_backward_kernel, dim3((unsigned)tiles_padded), dim3(256), 0, stream,
                        ctx->ranges.as<uint2>(), svals, ctx->sorted_g.as<uint32_t>(), ctx->rec.as<float4>(),
                        ctx->rec.as<float4>() + 2 * n, ctx->cov_coef.as<float4>(), ctx->ckpt.as<float>(), cam, grad_rgb, ctx->final_t.as<float>(),
-                       ctx->last.as<uint32_t>(), ctx->inst_grad.as<float>(), inst_grad_op);
+                       ctx->last.as<uint32_t>(), ctx->inst_grad.as<float>(), inst_grad_op,
+                       ctx->tile_cut.as<uint32_t>(), ctx->touched.as<uint8_t>());
     GSX_HIP_TRY(hipGetLastError(), "blend_backward_kernel");
     GSX_TRY(record(ctx, 8, stream));
     if (n > 0) {
@@ -901,7 +908,8 @@ gsx_hip_status enqueue_backward(gsx_hip_render_context* ctx, const float* grad_r
                            dim3(256), 0, stream, n, counters, ctx->offsets.as<uint32_t>(), ctx->rank_g.as<uint32_t>(),
                            ctx->long_list.as<uint32_t>(), counters + 1, ctx->multi_list.as<uint32_t>(), counters + 4,
                            kLongRunBlocks0, kLongRunBlocks, long_chunk,
-                           ctx->inst_grad.as<float>(), inst_grad_op, ctx->grad2d.as<float>());
+                           ctx->inst_grad.as<float>(), inst_grad_op, ctx->inst_tile.as<uint32_t>(),
+                           ctx->tile_cut.as<uint32_t>(), ctx->touched.as<uint8_t>(), ctx->grad2d.as<float>());
         GSX_HIP_TRY(hipGetLastError(), "reduce_instance_grads_kernel");
     }
     GSX_TRY(record(ctx, 9, stream));

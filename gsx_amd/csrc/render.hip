@@ -137,10 +137,12 @@ __device__ inline uint32_t stage_box(WaveBoxes& w, bool valid, float4 r0, float4
 }
 
 // Walks the wave's flattened tiles. kEmit: writes kept instances (key, value = position,
-// instance_gaussian) at out[owner] + rank; always accumulates kept[owner].
+// instance_gaussian and, when non-null, instance_tile) at out[owner] + rank; always accumulates
+// kept[owner].
 template <bool kEmit>
 __device__ inline void walk_wave_tiles(WaveBoxes& w, uint32_t wave_total, int32_t tiles_x, const KeyLayout& layout,
-                                       uint64_t* __restrict__ keys, uint32_t* __restrict__ instance_gaussian) {
+                                       uint64_t* __restrict__ keys, uint32_t* __restrict__ instance_gaussian,
+                                       uint32_t* __restrict__ instance_tile) {
     const uint32_t lane = __lane_id();
     const uint64_t lt = lanemask_lt();
     // the owner of pair p is the last box starting at or before p, i.e. the last non-empty one
@@ -190,6 +192,7 @@ __device__ inline void walk_wave_tiles(WaveBoxes& w, uint32_t wave_total, int32_
             const uint32_t pos = w.out[owner] + before + (uint32_t)__popcll(mask & lt & seg);
             keys[pos] = make_key(layout, tile, pos);
             instance_gaussian[pos] = w.g[owner];
+            if (instance_tile != nullptr) instance_tile[pos] = tile;
         }
         // the last lane of each owner segment advances that owner's running count
         const uint32_t next_owner = (uint32_t)__shfl_down((int)owner, 1, kWave);
@@ -219,7 +222,7 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
     uint32_t* __restrict__ clear0, uint32_t* __restrict__ clear1, uint32_t* __restrict__ clear2,
     uint32_t* __restrict__ kept_part,
     uint64_t* __restrict__ depth_keys, uint32_t depth_base, uint32_t depth_max, int index_bits,
-    uint64_t big_key_flag) {
+    uint64_t big_key_flag, uint8_t* __restrict__ touched) {
     __shared__ WaveBoxes s_boxes[kWavesPerBlock];
     __shared__ uint32_t s_kept[kWavesPerBlock];
     WaveBoxes& wb = s_boxes[threadIdx.x / kWave];
@@ -230,6 +233,8 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
         *clear1 = 0u;
         *clear2 = 0u;
     }
+    // TRAIN: the blend backward marks the Gaussians it reaches (touched[g] = 1)
+    if (touched != nullptr && g < n) touched[g] = 0;
     if (snap.dst[0] != nullptr && g < n) {
         // consecutive lanes copy consecutive rows; preprocess_one then reads them from cache
         copy_floats(mean3d, snap.dst[0], g, 3);
@@ -287,7 +292,7 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
     }
     if (big) big_list[atomicAdd(big_count, 1u)] = (uint32_t)g;  // counted by big_tiles_kernel
     const uint32_t total = stage_box(wb, visible && !big, r0, r1, (uint32_t)g, 0u, false);
-    walk_wave_tiles<false>(wb, total, cam.tiles_x, KeyLayout{}, nullptr, nullptr);
+    walk_wave_tiles<false>(wb, total, cam.tiles_x, KeyLayout{}, nullptr, nullptr, nullptr);
     const uint32_t kept = big ? 0u : wb.kept[__lane_id()];  // big boxes: counted by big_tiles_kernel
     if (g < n) tile_count[g] = kept;
     // the workgroup's kept tiles (at most 256 * kBigTiles) to kept_part[block], host memory that
@@ -359,9 +364,10 @@ __global__ __launch_bounds__(256) void rank_gather_kernel(int64_t n, const uint3
 // ---------------------------------------------------------------------------------------------
 // Key emission in depth order: the Gaussian of rank r owns positions offset[r] .. offset[r+1])
 // of the instance array, one per kept tile of its box in row-major tile order (offsets are the
-// exclusive scan of the counts in rank order). key = tile << tile_shift | position, and
-// instance_gaussian[position] = g. A stable sort on the tile bits then leaves every tile's run
-// in (depth, index) order.
+// exclusive scan of the counts in rank order). key = tile << tile_shift | position,
+// instance_gaussian[position] = g and, for a TRAIN forward, instance_tile[position] = tile (the
+// backward's reduction looks up each position's tile). A stable sort on the tile bits then
+// leaves every tile's run in (depth, index) order, i.e. in ascending position.
 // The offsets are finished here: block_prefix[b] is the exclusive scan of rank_gather_kernel's
 // 256-rank sums, and emission workgroup b (ranks 256 b .. 256 b + 255, rank_gather_kernel's
 // blocking) scans its own 256 counts; offsets[0..n] are stored for the later kernels
@@ -371,7 +377,8 @@ __device__ inline void emit_block(uint32_t b, int64_t n, const float4* __restric
                                   const uint32_t* __restrict__ rank_gaussian, const uint32_t* __restrict__ rank_count,
                                   const uint32_t* __restrict__ block_prefix, uint32_t* __restrict__ offsets,
                                   int32_t tiles_x, KeyLayout layout, uint64_t* __restrict__ keys,
-                                  uint32_t* __restrict__ instance_gaussian, WaveBoxes* s_boxes, uint32_t* s_wave) {
+                                  uint32_t* __restrict__ instance_gaussian, uint32_t* __restrict__ instance_tile,
+                                  WaveBoxes* s_boxes, uint32_t* s_wave) {
     WaveBoxes& wb = s_boxes[threadIdx.x / kWave];
     const int64_t r = (int64_t)b * blockDim.x + threadIdx.x;
     // the rank's count and Gaussian load together, then its whole record (one wait each)
@@ -393,7 +400,7 @@ __device__ inline void emit_block(uint32_t b, int64_t n, const float4* __restric
     // a box whose kept count (from the counting walk's identical tests) is its tile count keeps
     // every tile: emission skips its tests
     const uint32_t total = stage_box(wb, any, r0, r1, g, o, any && cnt == box_tiles(r1));
-    walk_wave_tiles<true>(wb, total, tiles_x, layout, keys, instance_gaussian);
+    walk_wave_tiles<true>(wb, total, tiles_x, layout, keys, instance_gaussian, instance_tile);
 }
 
 // Big boxes: the row-major tile range of each box on big_list is cut into chunks of `chunk`
@@ -417,7 +424,8 @@ __device__ inline void big_tiles_block(uint32_t x, uint32_t c, uint32_t gx, cons
                                        const uint32_t* __restrict__ rank_count,
                                        const uint32_t* __restrict__ block_prefix,
                                        const uint32_t* __restrict__ gaussian_rank, uint64_t* __restrict__ keys,
-                                       uint32_t* __restrict__ instance_gaussian, uint32_t* s_wave, uint32_t* s_red) {
+                                       uint32_t* __restrict__ instance_gaussian,
+                                       uint32_t* __restrict__ instance_tile, uint32_t* s_wave, uint32_t* s_red) {
     const uint32_t count = *big_count;
     const uint32_t lane = __lane_id(), wave = threadIdx.x / kWave;
     unsigned long long block_kept = 0;
@@ -473,6 +481,7 @@ __device__ inline void big_tiles_block(uint32_t x, uint32_t c, uint32_t gx, cons
                 const uint32_t pos = o + running + before + (uint32_t)__popcll(mask & lanemask_lt());
                 keys[pos] = make_key(layout, tile, pos);
                 instance_gaussian[pos] = g;
+                if (instance_tile != nullptr) instance_tile[pos] = tile;
             }
             running += step_total;
             __syncthreads();
@@ -505,7 +514,7 @@ __global__ __launch_bounds__(256) void big_count_upsweep_kernel(const uint32_t* 
     if (blockIdx.x < big_blocks) {
         big_tiles_block<false>(blockIdx.x % gx, blockIdx.x / gx, gx, big_list, big_count, rec, tiles_x, KeyLayout{},
                                chunk, tile_count, chunk_counts, kept_part, nullptr, nullptr, nullptr, nullptr, nullptr,
-                               s_wave, nullptr);
+                               nullptr, s_wave, nullptr);
         return;
     }
     radix_upsweep_block<kCompactingRadixBits, kCompactingChunk>(blockIdx.x - big_blocks, depth_keys, n, nullptr, true,
@@ -525,18 +534,19 @@ __global__ __launch_bounds__(256) void emit_kernel(int64_t n, const float4* __re
                                                    uint32_t big_blocks, uint32_t chunk,
                                                    const uint32_t* __restrict__ chunk_counts,
                                                    const uint32_t* __restrict__ gaussian_rank,
-                                                   uint64_t* __restrict__ keys, uint32_t* __restrict__ instance_gaussian) {
+                                                   uint64_t* __restrict__ keys, uint32_t* __restrict__ instance_gaussian,
+                                                   uint32_t* __restrict__ instance_tile) {
     __shared__ WaveBoxes s_boxes[kWavesPerBlock];
     __shared__ uint32_t s_wave[kWavesPerBlock];
     __shared__ uint32_t s_red[kWavesPerBlock];
     if (blockIdx.x < big_blocks) {
         big_tiles_block<true>(blockIdx.x % gx, blockIdx.x / gx, gx, big_list, big_count, rec, tiles_x, layout, chunk,
                               nullptr, const_cast<uint32_t*>(chunk_counts), nullptr, rank_count, block_prefix,
-                              gaussian_rank, keys, instance_gaussian, s_wave, s_red);
+                              gaussian_rank, keys, instance_gaussian, instance_tile, s_wave, s_red);
         return;
     }
     emit_block(blockIdx.x - big_blocks, n, rec, rank_gaussian, rank_count, block_prefix, offsets, tiles_x, layout, keys,
-               instance_gaussian, s_boxes, s_wave);
+               instance_gaussian, instance_tile, s_boxes, s_wave);
 }
 
 __global__ __launch_bounds__(256) void fill_u32_kernel(uint32_t* __restrict__ p, int64_t count, uint32_t v) {
@@ -766,11 +776,12 @@ constexpr int kGradRecord = 8;  // per-instance partials: channels 0-7 in one 32
 // d(conic)/d(cov2d) map applied per contribution.
 // Reduction without atomics: each 16-pixel row sums its lanes' 9 partials per entry with DPP
 // moves (row_reduce_scatter9), the 16 row totals are combined through LDS, and the tile writes
-// one 9-float partial per instance at its
-// emission position (channels 0-7 as one 32-byte record of instance_grad, channel 8, the
-// opacity term, in instance_grad_op); reduce_instance_grads_kernel then sums each Gaussian's
-// contiguous run of positions. The result is deterministic and immune to the contention of
-// full-screen Gaussians (present in every tile).
+// one 9-float partial per reached instance at its emission position (channels 0-7 as one 32-byte
+// record of instance_grad, channel 8, the opacity term, in instance_grad_op) and its cut
+// position (tile_cut: the instances past it were not reached and have no partial);
+// reduce_instance_grads_kernel then sums each Gaussian's contiguous run of positions. The result
+// is deterministic and immune to the contention of full-screen Gaussians (present in every tile),
+// and the instances behind saturated pixels cost the backward nothing.
 // ---------------------------------------------------------------------------------------------
 constexpr int kWavesPerTile = kBlendThreads / kWave;
 constexpr int kRowsPerTile = kTile;  // 16 pixel rows = 16 DPP rows of 16 lanes
@@ -787,7 +798,7 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
     const float* __restrict__ ckpt,
     CameraParams cam, const float* __restrict__ grad_rgb, const float* __restrict__ final_t,
     const uint32_t* __restrict__ last_contrib, float* __restrict__ instance_grad,
-    float* __restrict__ instance_grad_op) {
+    float* __restrict__ instance_grad_op, uint32_t* __restrict__ tile_cut, uint8_t* __restrict__ touched) {
     __shared__ float4 s_r0[kBackBatch];
     __shared__ float4 s_r1[kBackBatch];
     __shared__ float4 s_r2[kBackBatch];
@@ -831,16 +842,14 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
     const uint32_t end_all = s_max_last;
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
-    // entries no pixel of the tile reaches: their partials are zero
+    // Entries from zero_from on (whole buckets past the last entry any pixel of the tile reaches)
+    // get no partial: their gradient is zero. Positions ascend along the tile's run, so the run's
+    // entries with a partial are exactly those whose position is below tile_cut[tile], the
+    // position of the first entry without one (UINT32_MAX: all have one); the reduction adds +0
+    // for the others instead of reading them.
     const uint32_t zero_from =
         end_all <= range.x ? range.x : range.x + ((end_all - range.x + kBucket - 1) / kBucket) * kBucket;
-    for (uint32_t j = zero_from + threadIdx.x; j < range.y; j += kBlendThreads) {
-        const size_t pos = values[j];
-        float4* dst = reinterpret_cast<float4*>(instance_grad) + 2 * pos;
-        dst[0] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        dst[1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        instance_grad_op[pos] = 0.0f;
-    }
+    if (threadIdx.x == 0) tile_cut[tile] = zero_from < range.y ? values[zero_from] : UINT32_MAX;
     if (end_all <= range.x) return;  // uniform
 
     // Batches of kBackBatch entries are walked back to front; records and the batch's bucket
@@ -865,6 +874,7 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
             // below end_all lies in such a batch; entries from end_all on contribute nothing
             if (j < end_all) {
                 const uint32_t g = sorted_g[j];
+                touched[g] = 1;
                 const float4 geo1 = rec[2 * (size_t)g + 1], c = col[g];
                 const uint32_t bx = __float_as_uint(geo1.z), by = __float_as_uint(geo1.w);
                 s_r0[threadIdx.x] = rec[2 * (size_t)g + 0];
@@ -892,7 +902,7 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
         const int sb_first = (count - 1) / kBucket;
         for (int sb = sb_first; sb >= 0; --sb) {
             const uint32_t j0 = (uint32_t)bstart + (uint32_t)(sb * kBucket);
-            if (j0 < end_all) {  // uniform; entries beyond end_all were zeroed above
+            if (j0 < end_all) {  // uniform; buckets from end_all on get no partial (tile_cut)
             const int n_in = min(kBucket, count - sb * kBucket);
             float tb[kBucket];
             float gv[kBucket];
@@ -1018,6 +1028,9 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
 
 // grad2d[g] = sum of the partials over the emission positions [offset[r], offset[r+1]) of g, r its
 // depth rank; every Gaussian's sum is taken in a fixed order, so the result is deterministic.
+// Position p has a partial iff p < tile_cut[instance_tile[p]] (the blend backward's cut of p's
+// tile); the others count as +0, read from neither array. A Gaussian that no tile reached
+// (touched[g] == 0) has no partial at all: its sums are +0 without a look at its run.
 //  * runs of at most kLaneRun instances (reduce_short_block): the 64 runs of a wave's ranks are
 //    one contiguous span; the wave stages it through its own LDS piece by piece with coalesced
 //    loads, jumping over long runs, and each lane sums its run in position order into grad2d;
@@ -1048,24 +1061,50 @@ __device__ inline void add_instance_grad(float acc[kGrad2d], const float* __rest
     add_record(acc, rec4[0], rec4[1], instance_grad_op[p]);
 }
 
+// Position p's partial (three loads), or +0 where the blend backward wrote none.
+struct InstancePartial {
+    float4 a, b;
+    float op;
+};
+__device__ inline InstancePartial load_partial(const float4* __restrict__ rec4, const float* __restrict__ instance_grad_op,
+                                               const uint32_t* __restrict__ instance_tile,
+                                               const uint32_t* __restrict__ tile_cut, uint32_t p) {
+    InstancePartial v;
+    const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (p < tile_cut[instance_tile[p]]) {
+        v.a = rec4[2 * (size_t)p];
+        v.b = rec4[2 * (size_t)p + 1];
+        v.op = instance_grad_op[p];
+    } else {
+        v.a = z;
+        v.b = z;
+        v.op = 0.0f;
+    }
+    return v;
+}
+
 __device__ inline void reduce_short_block(uint32_t blk, int64_t n, const uint32_t* __restrict__ depth_count,
                                           const uint32_t* __restrict__ offsets,
                                           const uint32_t* __restrict__ rank_gaussian,
                                           const float* __restrict__ instance_grad,
-                                          const float* __restrict__ instance_grad_op, float* __restrict__ grad2d,
-                                          float4 (*s_rec)[2 * kShortPiece], float (*s_op)[kShortPiece]) {
+                                          const float* __restrict__ instance_grad_op,
+                                          const uint32_t* __restrict__ instance_tile,
+                                          const uint32_t* __restrict__ tile_cut, const uint8_t* __restrict__ touched,
+                                          float* __restrict__ grad2d, float4 (*s_rec)[2 * kShortPiece],
+                                          float (*s_op)[kShortPiece]) {
     const uint32_t lane = __lane_id(), wave = threadIdx.x / kWave;
     n = min(n, (int64_t)*depth_count);  // ranks of visible Gaussians
     const int64_t r = (int64_t)blk * blockDim.x + threadIdx.x;
     const int64_t r_first = r - lane;  // first rank of this wave (waves wholly past n find no work)
     const bool valid = r < n;
-    uint32_t b = 0, e = 0;
+    uint32_t b = 0, e = 0, g = 0;
     if (valid) {
         b = offsets[r];
         e = offsets[r + 1];
+        g = rank_gaussian[r];
     }
     const bool mine = valid && e - b <= kLaneRun;
-    const bool has = mine && e > b;
+    const bool has = mine && e > b && touched[g] != 0;
     const uint32_t span_end = offsets[min(r_first + (int64_t)kWave, n)];
     const float4* rec4 = reinterpret_cast<const float4*>(instance_grad);
     float4* sr = s_rec[wave];
@@ -1083,22 +1122,19 @@ __device__ inline void reduce_short_block(uint32_t blk, int64_t n, const uint32_
         // not under a branch (lanes past the piece re-read its last position, p1 > p0)
         constexpr int kPieceRounds = (int)(kShortPiece / kWave);
         const uint32_t len = p1 - p0;
-        float4 ra[kPieceRounds], rb[kPieceRounds];
-        float ro[kPieceRounds];
+        InstancePartial v[kPieceRounds];
 #pragma unroll
         for (int u = 0; u < kPieceRounds; ++u) {
             const uint32_t q = min(lane + (uint32_t)u * kWave, len - 1);
-            ra[u] = rec4[2 * (size_t)(p0 + q)];
-            rb[u] = rec4[2 * (size_t)(p0 + q) + 1];
-            ro[u] = instance_grad_op[p0 + q];
+            v[u] = load_partial(rec4, instance_grad_op, instance_tile, tile_cut, p0 + q);
         }
         // (unconditional stores: lanes past the piece write its last position's own values again)
 #pragma unroll
         for (int u = 0; u < kPieceRounds; ++u) {
             const uint32_t q = min(lane + (uint32_t)u * kWave, len - 1);
-            sr[2 * q] = ra[u];
-            sr[2 * q + 1] = rb[u];
-            so[q] = ro[u];
+            sr[2 * q] = v[u].a;
+            sr[2 * q + 1] = v[u].b;
+            so[q] = v[u].op;
         }
         wave_lds_sync();
         if (has) {
@@ -1108,9 +1144,8 @@ __device__ inline void reduce_short_block(uint32_t blk, int64_t n, const uint32_
         cur = p1;
     }
     if (mine) {
-        const size_t g = rank_gaussian[r];
 #pragma unroll
-        for (int c = 0; c < kGrad2d; ++c) grad2d[g * kGrad2d + c] = acc[c];
+        for (int c = 0; c < kGrad2d; ++c) grad2d[(size_t)g * kGrad2d + c] = acc[c];
     }
 }
 
@@ -1122,6 +1157,8 @@ __device__ inline void reduce_long_block(uint32_t x, uint32_t k, uint32_t gx, co
                                          const uint32_t* __restrict__ offsets,
                                          const uint32_t* __restrict__ rank_gaussian, uint32_t chunk,
                                          float* __restrict__ instance_grad, float* __restrict__ instance_grad_op,
+                                         const uint32_t* __restrict__ instance_tile,
+                                         const uint32_t* __restrict__ tile_cut, const uint8_t* __restrict__ touched,
                                          float* __restrict__ grad2d) {
     const uint32_t count = *long_count;
     const uint32_t lane = __lane_id();
@@ -1129,24 +1166,24 @@ __device__ inline void reduce_long_block(uint32_t x, uint32_t k, uint32_t gx, co
     for (uint32_t i = x * (blockDim.x / kWave) + threadIdx.x / kWave; i < count; i += waves) {
         const uint32_t r = long_list[i];
         const uint32_t b = offsets[r], e = offsets[r + 1];
+        const uint32_t g = rank_gaussian[r];
         const uint32_t cb = b + k * chunk;
         if (cb >= e) continue;  // uniform
         const uint32_t ce = min(e, cb + chunk);
+        // an untouched run sums to +0 without its loads (its chunk sums are still stored)
+        const uint32_t ce_load = touched[g] != 0 ? ce : cb;
         float acc[kGrad2d];
 #pragma unroll
         for (int c = 0; c < kGrad2d; ++c) acc[c] = 0.0f;
         const float4* rec4 = reinterpret_cast<const float4*>(instance_grad);
-        for (uint32_t p0 = cb; p0 < ce; p0 += 4 * kWave) {
+        for (uint32_t p0 = cb; p0 < ce_load; p0 += 4 * kWave) {
             // all loads of the round are in flight together: none sits under a branch (lanes
             // past the chunk re-read its last position and add nothing)
-            float4 ra[4], rb[4];
-            float ro[4];
+            InstancePartial v[4];
 #pragma unroll
             for (uint32_t u = 0; u < 4; ++u) {
                 const uint32_t p = min(p0 + u * kWave + lane, ce - 1);
-                ra[u] = rec4[2 * (size_t)p];
-                rb[u] = rec4[2 * (size_t)p + 1];
-                ro[u] = instance_grad_op[p];
+                v[u] = load_partial(rec4, instance_grad_op, instance_tile, tile_cut, p);
             }
             // lanes past the chunk add -0, the identity of + (an unconditional use keeps the loads
             // ahead of the adds)
@@ -1154,16 +1191,15 @@ __device__ inline void reduce_long_block(uint32_t x, uint32_t k, uint32_t gx, co
             for (uint32_t u = 0; u < 4; ++u) {
                 const bool in = p0 + u * kWave + lane < ce;
                 const float4 z = make_float4(-0.0f, -0.0f, -0.0f, -0.0f);
-                add_record(acc, in ? ra[u] : z, in ? rb[u] : z, in ? ro[u] : -0.0f);
+                add_record(acc, in ? v[u].a : z, in ? v[u].b : z, in ? v[u].op : -0.0f);
             }
         }
 #pragma unroll
         for (int c = 0; c < kGrad2d; ++c) acc[c] = wave_reduce_sum(acc[c]);
         if (e - b <= chunk) {  // uniform: the run is this one chunk
             if (lane == 0) {
-                const size_t g = rank_gaussian[r];
 #pragma unroll
-                for (int c = 0; c < kGrad2d; ++c) grad2d[g * kGrad2d + c] = acc[c];
+                for (int c = 0; c < kGrad2d; ++c) grad2d[(size_t)g * kGrad2d + c] = acc[c];
             }
             continue;
         }
@@ -1185,23 +1221,24 @@ __global__ __launch_bounds__(256) void reduce_instance_grads_kernel(
     const uint32_t* __restrict__ rank_gaussian, const uint32_t* __restrict__ long_list,
     const uint32_t* __restrict__ long_count, const uint32_t* __restrict__ multi_list,
     const uint32_t* __restrict__ multi_count, uint32_t gx0, uint32_t gx, uint32_t chunk,
-    float* __restrict__ instance_grad, float* __restrict__ instance_grad_op, float* __restrict__ grad2d) {
+    float* __restrict__ instance_grad, float* __restrict__ instance_grad_op, const uint32_t* __restrict__ instance_tile,
+    const uint32_t* __restrict__ tile_cut, const uint8_t* __restrict__ touched, float* __restrict__ grad2d) {
     __shared__ float4 s_rec[kWavesPerBlock][2 * kShortPiece];
     __shared__ float s_op[kWavesPerBlock][kShortPiece];
     if (blockIdx.x < gx0) {
         reduce_long_block(blockIdx.x, 0, gx0, long_list, long_count, offsets, rank_gaussian, chunk, instance_grad,
-                          instance_grad_op, grad2d);
+                          instance_grad_op, instance_tile, tile_cut, touched, grad2d);
         return;
     }
     const uint32_t long_blocks = gx0 + gx * (kLongChunks - 1);
     if (blockIdx.x < long_blocks) {
         const uint32_t b = blockIdx.x - gx0;
         reduce_long_block(b % gx, 1 + b / gx, gx, multi_list, multi_count, offsets, rank_gaussian, chunk,
-                          instance_grad, instance_grad_op, grad2d);
+                          instance_grad, instance_grad_op, instance_tile, tile_cut, touched, grad2d);
         return;
     }
     reduce_short_block(blockIdx.x - long_blocks, n, depth_count, offsets, rank_gaussian, instance_grad,
-                       instance_grad_op, grad2d, s_rec, s_op);
+                       instance_grad_op, instance_tile, tile_cut, touched, grad2d, s_rec, s_op);
 }
 
 __device__ inline void add3(float* p, float x, float y, float z) {

@@ -328,7 +328,7 @@ class Reference:
         lib.gsxref_adc.restype = ctypes.c_int
         lib.gsxref_adc.argtypes = [ctypes.c_int] + [_vp] * 10 + [ctypes.c_int, _vp] + [_vp] * 6
         lib.gsxref_train_step.restype = ctypes.c_int
-        lib.gsxref_train_step.argtypes = [ctypes.c_int, ctypes.c_int] + [_vp] * 7 + [_f, _f, _vp, _vp]
+        lib.gsxref_train_step.argtypes = [ctypes.c_int, ctypes.c_int] + [_vp] * 7 + [_f, _f, _vp, ctypes.c_int, _vp]
         self.lib = lib if backend is None else _OnBackend(lib, {"cpu": 0, "hip": 1}[backend])
 
     def device_name(self) -> str:
@@ -402,12 +402,16 @@ class Reference:
         k = out_n.value
         return {name: arr[:k] for name, arr in out.items()}, counters
 
-    def train_steps(self, scene, camera, target, iters, w_l1=0.8, w_ssim=0.2, lrs=(1e-3, 1e-2)):
+    def train_steps(self, scene, camera, target, iters, w_l1=0.8, w_ssim=0.2, lrs=(1e-3, 1e-2),
+                    skip_render_backward=False):
+        """Seconds per stage (render forward, loss forward, loss backward, render backward, Adam)
+        summed over `iters` steps; the updated scene."""
         stages = np.zeros(5, np.float64)
         sc = scene.copy()
         self._check(self.lib.gsxref_train_step(sc.count, iters, _p(sc.mean3d), _p(sc.rotation), _p(sc.logscale),
                                                _p(sc.opacity), _p(sc.sh0), _p(camera), _p(target), w_l1, w_ssim,
-                                               _p(np.asarray(lrs, np.float32)), _p(stages)))
+                                               _p(np.asarray(lrs, np.float32)), int(bool(skip_render_backward)),
+                                               _p(stages)))
         return sc, stages
 
     # ---- tensor, random and image operations (gsx-core.h, gsx-random.h, extra/gsx-image.h)

@@ -13,7 +13,10 @@
  *   - gsxref_adam         gsx_optim_step               (gsx/src/gsx-optim.c:498)
  *   - gsxref_adc          gsx_adc_step                 (gsx/src/gsx-adc.c:231)
  *   - gsxref_train_step   one image-fit style step (render, L1+SSIM, backward, Adam) with
- *                         per-stage wall-clock timings, used as the CPU baseline.
+ *                         per-stage wall-clock timings, used as the CPU baseline; the render
+ *                         backward can be skipped (Adam then steps on zero gradients) to time
+ *                         the other stages on scenes whose backward exceeds the CPU backend's
+ *                         int32 scratch limit.
  *   - gsxref_reduce / gsxref_elementwise / gsxref_gather / gsxref_random / gsxref_image
  *                         the tensor, random and image operations of gsx-core.h, gsx-random.h
  *                         and extra/gsx-image.h.
@@ -682,7 +685,7 @@ static double now_seconds(void)
  * loss bwd, render bwd, Adam (wall clock, single thread). The scene arrays are updated. */
 int gsxref_train_step(int n, int iters, float *mean3d, float *rotation, float *logscale, float *opacity,
     float *sh0, const float *camera, const float *target_rgb, float w_l1, float w_ssim, const float *hyper,
-    double *stage_seconds)
+    int skip_render_backward, double *stage_seconds)
 {
     int rc = 0;
     gsx_gs_t gs = NULL;
@@ -815,7 +818,7 @@ int gsxref_train_step(int n, int iters, float *mean3d, float *rotation, float *l
         TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_GRAD_LOGSCALE, &breq.grad_gs_logscale));
         TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_GRAD_OPACITY, &breq.grad_gs_opacity));
         TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_GRAD_SH0, &breq.grad_gs_sh0));
-        TRY(gsx_renderer_backward(renderer, rctx, &breq));
+        if(!skip_render_backward) TRY(gsx_renderer_backward(renderer, rctx, &breq));
         t4 = now_seconds();
         TRY(gsx_optim_step(optim, &sreq));
         t5 = now_seconds();
