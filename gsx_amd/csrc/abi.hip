@@ -175,10 +175,10 @@ struct PinnedBuffer {
 
 // Workgroups of the big-box passes (grid-stride over the list of big boxes).
 constexpr unsigned kBigBlocks = 512;
-// Workgroups of the long-run reduction (4 waves each, grid-stride over the list of long runs):
-// for chunk 0, which every long run has, and per later chunk.
-constexpr unsigned kLongRunBlocks0 = 2048;
-constexpr unsigned kLongRunBlocks = 512;
+// Workgroups of the long-run reduction (4 waves each, each wave 64 list entries at a time): for
+// chunk 0, which every long run has, and per later chunk.
+constexpr unsigned kLongRunBlocks0 = 1024;
+constexpr unsigned kLongRunBlocks = 128;
 
 // Long instance runs are summed in chunks of this many positions: a run has at most `tiles`
 // instances, so at most kLongChunks chunks.
@@ -265,7 +265,7 @@ struct gsx_hip_render_context {
     gsx_hip_gaussians live{};
     gsx_hip_camera camera{};
     int32_t train_mode = GSX_HIP_FORWARD_INFERENCE;
-    // counters: [0] visible Gaussians (depth keys), [1] long instance runs, [2 + big_slot] big boxes
+    // counters: [0] visible Gaussians (depth keys), [1] unused, [2 + big_slot] big boxes
     // of the next forward (each forward's preprocess clears the other slot for its successor),
     // [4] runs of more than one long-run chunk
     bool counters_ready = false;
@@ -683,13 +683,14 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     GSX_TRY(ctx->big_list.reserve(n1 * sizeof(uint32_t), "big_list"));
     GSX_TRY(ctx->big_chunk_counts.reserve(n1 * kBigChunks * sizeof(uint32_t), "big_chunk_counts"));
     GSX_TRY(ctx->offsets.reserve((size_t)(n + 1) * sizeof(uint32_t), "offsets"));
-    GSX_TRY(ctx->scan_temp.reserve(((size_t)blocks_for(n, 256) + 1) * sizeof(uint32_t), "rank_block_sums"));
+    // per 256-rank workgroup: its tile-count sum, then its long-run count (two scanned arrays)
+    GSX_TRY(ctx->scan_temp.reserve(2 * ((size_t)blocks_for(n, 256) + 1) * sizeof(uint32_t), "rank_block_sums"));
+    GSX_TRY(ctx->long_list.reserve(n1 * sizeof(uint32_t), "long_list"));
     GSX_TRY(ctx->depth_keys.reserve(n1 * sizeof(uint64_t), "depth_keys"));
     GSX_TRY(ctx->depth_keys_alt.reserve(n1 * sizeof(uint64_t), "depth_keys_alt"));
     GSX_TRY(ctx->rank_g.reserve(n1 * sizeof(uint32_t), "rank_gaussian"));
     GSX_TRY(ctx->rank_count.reserve(n1 * sizeof(uint32_t), "rank_count"));
     GSX_TRY(ctx->g_rank.reserve(n1 * sizeof(uint32_t), "gaussian_rank"));
-    GSX_TRY(ctx->long_list.reserve(n1 * sizeof(uint32_t), "long_list"));
     GSX_TRY(ctx->multi_list.reserve(n1 * sizeof(uint32_t), "multi_list"));
     GSX_TRY(ctx->depth_sort_temp.reserve(radix_sort_keys_u64_compacting_temp_bytes(n), "depth_sort_temp"));
     GSX_TRY(ctx->ranges.reserve((size_t)tiles * sizeof(uint2), "ranges"));
@@ -782,11 +783,11 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
                            sorted_depth, (uint64_t)((1ull << index_bits) - 1ull), big_flag,
                            ctx->tile_count.as<uint32_t>(),
                            ctx->rank_g.as<uint32_t>(), ctx->rank_count.as<uint32_t>(), ctx->g_rank.as<uint32_t>(),
-                           ctx->long_list.as<uint32_t>(), counters + 1, long_chunk_of(tiles),
+                           long_chunk_of(tiles),
                            ctx->multi_list.as<uint32_t>(), counters + 4, ctx->scan_temp.as<uint32_t>());
         GSX_HIP_TRY(hipGetLastError(), "rank_gather_kernel");
         // exclusive scan of the 256-rank sums; emit_keys_kernel completes the offsets
-        GSX_TRY(scan_partials_in_place(ctx->scan_temp.as<uint32_t>(), pre_blocks, stream));
+        GSX_TRY(scan_partials_in_place(ctx->scan_temp.as<uint32_t>(), pre_blocks, stream, 2));
     }
     GSX_TRY(record(ctx, 2, stream));
     GSX_HIP_TRY(hipEventSynchronize(ctx->count_ev), "instance count sync");
@@ -830,7 +831,8 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
                            ctx->offsets.as<uint32_t>(), cam.tiles_x, layout, ctx->big_list.as<uint32_t>(), big_count,
                            kBigBlocks, big_blocks, big_chunk, ctx->big_chunk_counts.as<uint32_t>(),
                            ctx->g_rank.as<uint32_t>(), ctx->keys.as<uint64_t>(), ctx->inst_gauss.as<uint32_t>(),
-                           train ? ctx->inst_tile.as<uint32_t>() : nullptr);
+                           train ? ctx->inst_tile.as<uint32_t>() : nullptr,
+                           ctx->scan_temp.as<uint32_t>() + pre_blocks + 1, ctx->long_list.as<uint32_t>());
         GSX_HIP_TRY(hipGetLastError(), "emit_kernel");
     }
     GSX_TRY(record(ctx, 3, stream));
@@ -893,6 +895,7 @@ gsx_hip_status enqueue_backward(gsx_hip_render_context* ctx, const float* grad_r
     // per-instance partials: [I][8] records, then the [I] opacity terms
     float* inst_grad_op = ctx->inst_grad.as<float>() + (size_t)ctx->instance_count * 8;
     const uint32_t long_chunk = long_chunk_of(tiles);
+    const unsigned pre_blocks = blocks_for(n, 256);  // the forward's rank workgroups
     GSX_TRY(record(ctx, 7, stream));
     const int tiles_padded = ((tiles + 7) / 8) * 8;
     hipLaunchKernelGGL(blend_backward_kernel, dim3((unsigned)tiles_padded), dim3(256), 0, stream,
@@ -906,8 +909,8 @@ gsx_hip_status enqueue_backward(gsx_hip_render_context* ctx, const float* grad_r
         hipLaunchKernelGGL(reduce_instance_grads_kernel,
                            dim3(kLongRunBlocks0 + kLongRunBlocks * (kLongChunks - 1) + blocks_for(n, 256)),
                            dim3(256), 0, stream, n, counters, ctx->offsets.as<uint32_t>(), ctx->rank_g.as<uint32_t>(),
-                           ctx->long_list.as<uint32_t>(), counters + 1, ctx->multi_list.as<uint32_t>(), counters + 4,
-                           kLongRunBlocks0, kLongRunBlocks, long_chunk,
+                           ctx->long_list.as<uint32_t>(), ctx->scan_temp.as<uint32_t>() + 2 * (size_t)pre_blocks + 1,
+                           ctx->multi_list.as<uint32_t>(), counters + 4, kLongRunBlocks0, kLongRunBlocks, long_chunk,
                            ctx->inst_grad.as<float>(), inst_grad_op, ctx->inst_tile.as<uint32_t>(),
                            ctx->tile_cut.as<uint32_t>(), ctx->touched.as<uint8_t>(), ctx->grad2d.as<float>());
         GSX_HIP_TRY(hipGetLastError(), "reduce_instance_grads_kernel");

@@ -337,6 +337,19 @@ __device__ inline uint64_t lanemask_lt() {
     return lane == 0 ? 0ull : (~0ull >> (64 - lane));
 }
 
+// Slot of each lane with `take` in a list whose length is *count: one atomic add per wave (by
+// the lowest taking lane, a vector atomic) instead of one per lane; every lane of the wave must
+// call it. Lanes without `take` get an unspecified value.
+__device__ inline uint32_t wave_append_slot(uint32_t* count, bool take) {
+    const uint64_t mask = __ballot(take);
+    if (mask == 0ull) return 0u;
+    const uint32_t leader = (uint32_t)__builtin_ctzll(mask);
+    uint32_t base = 0u;
+    if (__lane_id() == leader) base = atomicAdd(count, (uint32_t)__popcll(mask));
+    base = (uint32_t)__builtin_amdgcn_readlane((int)base, (int)leader);
+    return base + (uint32_t)__popcll(mask & lanemask_lt());
+}
+
 __device__ inline uint32_t wave_min_u32(uint32_t v) {
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
@@ -551,7 +564,8 @@ gsx_hip_status radix_sort_keys_u64_digits(uint64_t* keys, uint64_t* keys_alt, in
                                          int digit_bits, void* temp, int* out_in_alt, hipStream_t stream);
 size_t radix_sort_keys_u64_digits_temp_bytes(int64_t n);
 
-// Single-workgroup exclusive scan of partials[0..count) in place, the total stored at [count].
-gsx_hip_status scan_partials_in_place(uint32_t* partials, int64_t count, hipStream_t stream);
+// Exclusive scan of partials[0..count) in place, the total stored at [count], by one workgroup;
+// with arrays > 1, the arrays of count + 1 entries that follow it too (one workgroup each).
+gsx_hip_status scan_partials_in_place(uint32_t* partials, int64_t count, hipStream_t stream, int arrays = 1);
 
 }  // namespace gsx_amd

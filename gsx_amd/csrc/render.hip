@@ -39,9 +39,11 @@ constexpr int kBlendThreads = kTilePixels;  // 256: one pixel per thread, 4 wave
 // ---------------------------------------------------------------------------------------------
 constexpr int kWavesPerBlock = 4;
 // Boxes of more tiles than this are walked by a whole workgroup in a pass of their own (see
-// big_tiles_kernel): a wave holding a full-image box would otherwise serialise hundreds of steps.
-constexpr uint32_t kBigTiles = 256;
-static_assert(kBigTiles <= 256, "the tile walk divides indices below 2^8 by box widths of at most 2^8");
+// big_tiles_block): a wave holding a full-image box would otherwise serialise hundreds of steps.
+// Below it the wave walk is the faster one (no workgroup barriers per step), and scenes can hold
+// millions of boxes of a few hundred tiles.
+constexpr uint32_t kBigTiles = 1024;
+static_assert(kBigTiles <= 1024, "the tile walk divides indices below 2^10 by box widths of at most 2^10");
 
 // Sort keys. Gaussians are first sorted by depth: key = (bits(depth) - bits(near)) << index_bits
 // | index (visible depths lie in [near, far], where positive floats order like their bit
@@ -79,7 +81,7 @@ __device__ inline uint32_t div_small(uint32_t k, uint32_t d, float rd) {
 
 struct WaveBoxes {
     gsx_tile_conic conic[kWave];
-    uint32_t mdiv[kWave];  // ceil(2^16 / wx): row of flattened index k (< 256) = (k * mdiv) >> 16
+    uint32_t mdiv[kWave];  // ceil(2^20 / wx): row of flattened index k (< 1024) = (k * mdiv) >> 20
     int32_t x0[kWave], x1[kWave], y0[kWave], y1[kWave];
     uint32_t tx0[kWave], ty0[kWave], wx[kWave], excl[kWave], kept[kWave], out[kWave];
     uint32_t g[kWave];
@@ -117,7 +119,7 @@ __device__ inline uint32_t stage_box(WaveBoxes& w, bool valid, float4 r0, float4
         w.tx0[lane] = (uint32_t)x0 / kTile;
         w.ty0[lane] = (uint32_t)y0 / kTile;
         w.wx[lane] = (uint32_t)x1 / kTile - (uint32_t)x0 / kTile + 1;
-        w.mdiv[lane] = 65535u / w.wx[lane] + 1u;
+        w.mdiv[lane] = 1048575u / w.wx[lane] + 1u;
         total = w.wx[lane] * ((uint32_t)y1 / kTile - (uint32_t)y0 / kTile + 1);
     }
     w.g[lane] = g;
@@ -167,9 +169,10 @@ __device__ inline void walk_wave_tiles(WaveBoxes& w, uint32_t wave_total, int32_
         if (active) {
             const uint32_t k = p - w.excl[owner];
             const uint32_t wx = w.wx[owner];
-            // exact for k < 2^8 and wx <= 2^8: ceil(2^16 / wx) * wx - 2^16 < wx <= 2^(16 - 8)
-            // (Granlund-Montgomery); the walked boxes have at most kBigTiles = 256 tiles
-            const uint32_t row = (k * w.mdiv[owner]) >> 16;
+            // exact when k * wx < 2^20 (Granlund-Montgomery: m = ceil(2^20 / wx) overshoots k / wx
+            // by k (m wx - 2^20) / (wx 2^20) < k / 2^20 < 1 / wx); the walked boxes have at most
+            // kBigTiles = 1024 tiles, so k < 1024 and wx <= 1024, and k * m < 2^30
+            const uint32_t row = (k * w.mdiv[owner]) >> 20;
             const uint32_t ty = w.ty0[owner] + row;
             const uint32_t tx = w.tx0[owner] + (k - row * wx);
             tile = ty * (uint32_t)tiles_x + tx;
@@ -290,7 +293,9 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
         }
         depth_keys[g] = key;
     }
-    if (big) big_list[atomicAdd(big_count, 1u)] = (uint32_t)g;  // counted by big_tiles_kernel
+    // counted by big_tiles_block; one atomic per wave (a scene can hold millions of big boxes)
+    const uint32_t big_slot = wave_append_slot(big_count, big);
+    if (big) big_list[big_slot] = (uint32_t)g;
     const uint32_t total = stage_box(wb, visible && !big, r0, r1, (uint32_t)g, 0u, false);
     walk_wave_tiles<false>(wb, total, cam.tiles_x, KeyLayout{}, nullptr, nullptr, nullptr);
     const uint32_t kept = big ? 0u : wb.kept[__lane_id()];  // big boxes: counted by big_tiles_kernel
@@ -318,11 +323,13 @@ constexpr uint32_t kLaneRun = 32;
 
 // After the depth sort of the V visible Gaussians (V = *depth_count): the Gaussian of every
 // depth rank, its kept-tile count, the rank of each big box and of each Gaussian whose count
-// exceeds kLaneRun (the only ranks looked up by Gaussian; every Gaussian's when flagged_only is
-// false), the list of ranks whose count exceeds kLaneRun, and the list of those longer than one
-// long_chunk (the backward sums long runs in chunks of that many positions). Ranks V..n-1 get
-// count 0 and no Gaussian. Each workgroup also stores the sum of its 256 counts in
-// block_sums[block], the first step of the offsets scan (emit_block finishes it).
+// exceeds long_chunk (the only ranks looked up by Gaussian: by big-box emission and by the
+// projection backward for runs of several chunks; every Gaussian's when flagged_only is false)
+// and the list of ranks whose count exceeds long_chunk (the backward sums long runs in chunks of
+// that many positions). Ranks V..n-1 get count 0 and no Gaussian. Each workgroup also stores the
+// sum of its 256 counts in block_sums[block] and its number of counts above kLaneRun in
+// block_sums[gridDim.x + 1 + block], the first steps of the offsets scan and of the long-run
+// list (emit_block finishes both).
 __global__ __launch_bounds__(256) void rank_gather_kernel(int64_t n, const uint32_t* __restrict__ depth_count,
                                                           const uint64_t* __restrict__ sorted_depth_keys,
                                                           uint64_t index_mask, bool flagged_only,
@@ -330,12 +337,12 @@ __global__ __launch_bounds__(256) void rank_gather_kernel(int64_t n, const uint3
                                                           uint32_t* __restrict__ rank_gaussian,
                                                           uint32_t* __restrict__ rank_count,
                                                           uint32_t* __restrict__ gaussian_rank,
-                                                          uint32_t* __restrict__ long_list,
-                                                          uint32_t* __restrict__ long_count, uint32_t long_chunk,
+                                                          uint32_t long_chunk,
                                                           uint32_t* __restrict__ multi_list,
                                                           uint32_t* __restrict__ multi_count,
                                                           uint32_t* __restrict__ block_sums) {
     __shared__ uint32_t s_sum[kWavesPerBlock];
+    __shared__ uint32_t s_long[kWavesPerBlock];
     const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     uint32_t c = 0;
     if (r < n) {
@@ -344,20 +351,30 @@ __global__ __launch_bounds__(256) void rank_gather_kernel(int64_t n, const uint3
             const uint32_t g = (uint32_t)(key & index_mask);
             c = tile_count[g];
             rank_gaussian[r] = g;
-            if (!flagged_only || (key & kBigKeyFlag) != 0 || c > kLaneRun) gaussian_rank[g] = (uint32_t)r;
-            if (c > kLaneRun) long_list[atomicAdd(long_count, 1u)] = (uint32_t)r;
-            if (c > long_chunk) multi_list[atomicAdd(multi_count, 1u)] = (uint32_t)r;
+            if (!flagged_only || (key & kBigKeyFlag) != 0 || c > long_chunk) gaussian_rank[g] = (uint32_t)r;
         }
         rank_count[r] = c;
     }
+    // runs of several chunks are listed (rare: their boxes span more than long_chunk tiles); one
+    // atomic per wave that has any (c is 0 past the visible ranks)
+    const uint32_t multi_slot = wave_append_slot(multi_count, c > long_chunk);
+    if (c > long_chunk) multi_list[multi_slot] = (uint32_t)r;
     const uint32_t wave_sum = wave_reduce_sum_u32(c);
-    if (__lane_id() == 0) s_sum[threadIdx.x / kWave] = wave_sum;
+    const uint32_t wave_long = (uint32_t)__popcll(__ballot(c > kLaneRun));
+    if (__lane_id() == 0) {
+        s_sum[threadIdx.x / kWave] = wave_sum;
+        s_long[threadIdx.x / kWave] = wave_long;
+    }
     __syncthreads();
     if (threadIdx.x == 0) {
-        uint32_t sum = 0;
+        uint32_t sum = 0, longs = 0;
 #pragma unroll
-        for (int w = 0; w < kWavesPerBlock; ++w) sum += s_sum[w];
+        for (int w = 0; w < kWavesPerBlock; ++w) {
+            sum += s_sum[w];
+            longs += s_long[w];
+        }
         block_sums[blockIdx.x] = sum;
+        block_sums[gridDim.x + 1 + blockIdx.x] = longs;
     }
 }
 
@@ -378,6 +395,7 @@ __device__ inline void emit_block(uint32_t b, int64_t n, const float4* __restric
                                   const uint32_t* __restrict__ block_prefix, uint32_t* __restrict__ offsets,
                                   int32_t tiles_x, KeyLayout layout, uint64_t* __restrict__ keys,
                                   uint32_t* __restrict__ instance_gaussian, uint32_t* __restrict__ instance_tile,
+                                  const uint32_t* __restrict__ long_prefix, uint32_t* __restrict__ long_list,
                                   WaveBoxes* s_boxes, uint32_t* s_wave) {
     WaveBoxes& wb = s_boxes[threadIdx.x / kWave];
     const int64_t r = (int64_t)b * blockDim.x + threadIdx.x;
@@ -391,6 +409,18 @@ __device__ inline void emit_block(uint32_t b, int64_t n, const float4* __restric
     const uint32_t o = block_prefix[b] + block_exclusive_scan_256(cnt, s_wave, block_total);
     if (r < n) offsets[r] = o;
     if (r == n - 1) offsets[n] = o + cnt;
+    // the long-run list in rank order: long_prefix[b] (scanned per-workgroup counts of
+    // rank_gather_kernel) + the rank's place among the workgroup's long runs (s_wave is free
+    // again after the scan's last barrier)
+    {
+        const bool is_long = cnt > kLaneRun;
+        const uint64_t lm = __ballot(is_long);
+        if (__lane_id() == 0) s_wave[threadIdx.x / kWave] = (uint32_t)__popcll(lm);
+        __syncthreads();
+        uint32_t at = long_prefix[b] + (uint32_t)__popcll(lm & lanemask_lt());
+        for (int w = 0; w < (int)(threadIdx.x / kWave); ++w) at += s_wave[w];
+        if (is_long) long_list[at] = (uint32_t)r;
+    }
     float4 r0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), r1 = r0;
     if (cnt > 0) {
         r0 = rec[2 * (size_t)g + 0];
@@ -535,7 +565,9 @@ __global__ __launch_bounds__(256) void emit_kernel(int64_t n, const float4* __re
                                                    const uint32_t* __restrict__ chunk_counts,
                                                    const uint32_t* __restrict__ gaussian_rank,
                                                    uint64_t* __restrict__ keys, uint32_t* __restrict__ instance_gaussian,
-                                                   uint32_t* __restrict__ instance_tile) {
+                                                   uint32_t* __restrict__ instance_tile,
+                                                   const uint32_t* __restrict__ long_prefix,
+                                                   uint32_t* __restrict__ long_list) {
     __shared__ WaveBoxes s_boxes[kWavesPerBlock];
     __shared__ uint32_t s_wave[kWavesPerBlock];
     __shared__ uint32_t s_red[kWavesPerBlock];
@@ -546,7 +578,7 @@ __global__ __launch_bounds__(256) void emit_kernel(int64_t n, const float4* __re
         return;
     }
     emit_block(blockIdx.x - big_blocks, n, rec, rank_gaussian, rank_count, block_prefix, offsets, tiles_x, layout, keys,
-               instance_gaussian, instance_tile, s_boxes, s_wave);
+               instance_gaussian, instance_tile, long_prefix, long_list, s_boxes, s_wave);
 }
 
 __global__ __launch_bounds__(256) void fill_u32_kernel(uint32_t* __restrict__ p, int64_t count, uint32_t v) {
@@ -1034,12 +1066,15 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
 //  * runs of at most kLaneRun instances (reduce_short_block): the 64 runs of a wave's ranks are
 //    one contiguous span; the wave stages it through its own LDS piece by piece with coalesced
 //    loads, jumping over long runs, and each lane sums its run in position order into grad2d;
-//  * longer runs (listed by rank_gather_kernel; in depth order the near, large Gaussians sit
-//    side by side, and the largest cover nearly every tile): each run is cut into at most
-//    kLongChunks chunks of `chunk` positions, one wave sums a chunk (DPP tree); a run of one
-//    chunk is done, the others leave each chunk's sums in place at its first position
-//    (reduce_long_block), and projection_backward_kernel adds them in chunk order.
-// Both run in one launch (reduce_instance_grads_kernel).
+//  * longer runs (in depth order the near, large Gaussians sit side by side, and the largest
+//    cover nearly every tile) are cut into at most kLongChunks chunks of `chunk` positions, and
+//    one wave sums a chunk (DPP tree, reduce_run_chunk). reduce_long_block takes chunk 0 of every
+//    long run (long_list, in rank order, written by emit_block) and chunks 1.. of the runs longer
+//    than one chunk (multi_list, from rank_gather_kernel), the entries dealt round-robin over the
+//    waves: the near, large Gaussians are neighbours in depth order, and a wave of their own
+//    would serialise them. A run of one chunk is done; the others leave each chunk's sums in
+//    place at its first position, and projection_backward_kernel adds them in chunk order.
+// All of it runs in one launch (reduce_instance_grads_kernel).
 constexpr uint32_t kShortPiece = 256;  // instances per LDS piece and wave (9 KB)
 constexpr uint32_t kLongChunks = 16;
 
@@ -1083,11 +1118,93 @@ __device__ inline InstancePartial load_partial(const float4* __restrict__ rec4, 
     return v;
 }
 
+// Chunk k of the long run [b, e) of Gaussian g, summed by the whole wave (b, e, g, k wave-uniform).
+// A run of one chunk gets its sums in grad2d, a longer one its chunk's sums at the chunk's first
+// position.
+__device__ inline void reduce_run_chunk(uint32_t b, uint32_t e, uint32_t g, uint32_t k, uint32_t chunk,
+                                        float* __restrict__ instance_grad, float* __restrict__ instance_grad_op,
+                                        const uint32_t* __restrict__ instance_tile,
+                                        const uint32_t* __restrict__ tile_cut, float* __restrict__ grad2d) {
+    const uint32_t lane = __lane_id();
+    const float4* rec4 = reinterpret_cast<const float4*>(instance_grad);
+    const uint32_t cb = b + k * chunk;
+    const uint32_t ce = min(e, cb + chunk);
+    float acc[kGrad2d];
+#pragma unroll
+    for (int c = 0; c < kGrad2d; ++c) acc[c] = 0.0f;
+    for (uint32_t p0 = cb; p0 < ce; p0 += 4 * kWave) {
+        // all loads of the round are in flight together: none sits under a branch (lanes past
+        // the chunk re-read its last position and add nothing)
+        InstancePartial v[4];
+#pragma unroll
+        for (uint32_t u = 0; u < 4; ++u) {
+            const uint32_t p = min(p0 + u * kWave + lane, ce - 1);
+            v[u] = load_partial(rec4, instance_grad_op, instance_tile, tile_cut, p);
+        }
+        // lanes past the chunk add -0, the identity of + (an unconditional use keeps the loads
+        // ahead of the adds)
+#pragma unroll
+        for (uint32_t u = 0; u < 4; ++u) {
+            const bool in = p0 + u * kWave + lane < ce;
+            const float4 z = make_float4(-0.0f, -0.0f, -0.0f, -0.0f);
+            add_record(acc, in ? v[u].a : z, in ? v[u].b : z, in ? v[u].op : -0.0f);
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < kGrad2d; ++c) acc[c] = wave_reduce_sum(acc[c]);
+    if (lane != 0) return;
+    if (e - b <= chunk) {
+#pragma unroll
+        for (int c = 0; c < kGrad2d; ++c) grad2d[(size_t)g * kGrad2d + c] = acc[c];
+        return;
+    }
+    // every lane's loads of the chunk fed the sums above, so overwriting position cb is safe
+    float4* dst = reinterpret_cast<float4*>(instance_grad) + 2 * (size_t)cb;
+    dst[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    dst[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+    instance_grad_op[cb] = acc[8];
+}
+
+// The +0 sums of chunk k of a long run that no tile reached, stored by one lane.
+__device__ inline void zero_run_chunk(uint32_t b, uint32_t e, uint32_t g, uint32_t k, uint32_t chunk,
+                                      float* __restrict__ instance_grad, float* __restrict__ instance_grad_op,
+                                      float* __restrict__ grad2d) {
+    if (e - b <= chunk) {
+#pragma unroll
+        for (int c = 0; c < kGrad2d; ++c) grad2d[(size_t)g * kGrad2d + c] = 0.0f;
+        return;
+    }
+    const uint32_t cb = b + k * chunk;
+    float4* dst = reinterpret_cast<float4*>(instance_grad) + 2 * (size_t)cb;
+    dst[0] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    dst[1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    instance_grad_op[cb] = 0.0f;
+}
+
+// Chunk k of the long runs of the wave's lanes (run [b, e) of Gaussian g where `live`): the
+// untouched ones get their +0 sums from their lanes, the touched ones are summed by the wave one
+// after another.
+__device__ inline void reduce_wave_long_runs(bool live, uint32_t b, uint32_t e, uint32_t g, uint32_t k,
+                                             uint32_t chunk, float* __restrict__ instance_grad,
+                                             float* __restrict__ instance_grad_op,
+                                             const uint32_t* __restrict__ instance_tile,
+                                             const uint32_t* __restrict__ tile_cut,
+                                             const uint8_t* __restrict__ touched, float* __restrict__ grad2d) {
+    const bool hit = live && touched[g] != 0;
+    if (live && !hit) zero_run_chunk(b, e, g, k, chunk, instance_grad, instance_grad_op, grad2d);
+    for (uint64_t todo = __ballot(hit); todo != 0ull; todo &= todo - 1ull) {
+        const int src = __builtin_ctzll(todo);
+        reduce_run_chunk((uint32_t)__builtin_amdgcn_readlane((int)b, src),
+                         (uint32_t)__builtin_amdgcn_readlane((int)e, src),
+                         (uint32_t)__builtin_amdgcn_readlane((int)g, src), k, chunk, instance_grad, instance_grad_op,
+                         instance_tile, tile_cut, grad2d);
+    }
+}
+
 __device__ inline void reduce_short_block(uint32_t blk, int64_t n, const uint32_t* __restrict__ depth_count,
                                           const uint32_t* __restrict__ offsets,
-                                          const uint32_t* __restrict__ rank_gaussian,
-                                          const float* __restrict__ instance_grad,
-                                          const float* __restrict__ instance_grad_op,
+                                          const uint32_t* __restrict__ rank_gaussian, uint32_t chunk,
+                                          float* __restrict__ instance_grad, float* __restrict__ instance_grad_op,
                                           const uint32_t* __restrict__ instance_tile,
                                           const uint32_t* __restrict__ tile_cut, const uint8_t* __restrict__ touched,
                                           float* __restrict__ grad2d, float4 (*s_rec)[2 * kShortPiece],
@@ -1149,79 +1266,46 @@ __device__ inline void reduce_short_block(uint32_t blk, int64_t n, const uint32_
     }
 }
 
-// Chunk k of the listed long runs, by the waves of the gx workgroups of column k (grid-stride over
-// the list). A run of one chunk gets its sums in grad2d; otherwise the 9 sums of each chunk replace
-// the chunk's first partial and projection_backward_kernel adds the run's chunk sums.
-__device__ inline void reduce_long_block(uint32_t x, uint32_t k, uint32_t gx, const uint32_t* __restrict__ long_list,
-                                         const uint32_t* __restrict__ long_count,
+// Chunk k of the runs on `list`, by the gx * 4 waves of the workgroups of column k: lane l of
+// wave w takes entries w + W (l + 64 j), j = 0, 1, ... (W waves), so neighbouring entries go to
+// different waves.
+__device__ inline void reduce_long_block(uint32_t x, uint32_t k, uint32_t gx, const uint32_t* __restrict__ list,
+                                         const uint32_t* __restrict__ list_count,
                                          const uint32_t* __restrict__ offsets,
                                          const uint32_t* __restrict__ rank_gaussian, uint32_t chunk,
                                          float* __restrict__ instance_grad, float* __restrict__ instance_grad_op,
                                          const uint32_t* __restrict__ instance_tile,
                                          const uint32_t* __restrict__ tile_cut, const uint8_t* __restrict__ touched,
                                          float* __restrict__ grad2d) {
-    const uint32_t count = *long_count;
-    const uint32_t lane = __lane_id();
+    const uint32_t count = *list_count;
     const uint32_t waves = gx * (blockDim.x / kWave);
-    for (uint32_t i = x * (blockDim.x / kWave) + threadIdx.x / kWave; i < count; i += waves) {
-        const uint32_t r = long_list[i];
-        const uint32_t b = offsets[r], e = offsets[r + 1];
-        const uint32_t g = rank_gaussian[r];
-        const uint32_t cb = b + k * chunk;
-        if (cb >= e) continue;  // uniform
-        const uint32_t ce = min(e, cb + chunk);
-        // an untouched run sums to +0 without its loads (its chunk sums are still stored)
-        const uint32_t ce_load = touched[g] != 0 ? ce : cb;
-        float acc[kGrad2d];
-#pragma unroll
-        for (int c = 0; c < kGrad2d; ++c) acc[c] = 0.0f;
-        const float4* rec4 = reinterpret_cast<const float4*>(instance_grad);
-        for (uint32_t p0 = cb; p0 < ce_load; p0 += 4 * kWave) {
-            // all loads of the round are in flight together: none sits under a branch (lanes
-            // past the chunk re-read its last position and add nothing)
-            InstancePartial v[4];
-#pragma unroll
-            for (uint32_t u = 0; u < 4; ++u) {
-                const uint32_t p = min(p0 + u * kWave + lane, ce - 1);
-                v[u] = load_partial(rec4, instance_grad_op, instance_tile, tile_cut, p);
-            }
-            // lanes past the chunk add -0, the identity of + (an unconditional use keeps the loads
-            // ahead of the adds)
-#pragma unroll
-            for (uint32_t u = 0; u < 4; ++u) {
-                const bool in = p0 + u * kWave + lane < ce;
-                const float4 z = make_float4(-0.0f, -0.0f, -0.0f, -0.0f);
-                add_record(acc, in ? v[u].a : z, in ? v[u].b : z, in ? v[u].op : -0.0f);
-            }
+    const uint32_t w = x * (blockDim.x / kWave) + threadIdx.x / kWave;
+    for (uint32_t j = 0; w + waves * j * kWave < count; ++j) {
+        const uint32_t i = w + waves * (j * kWave + __lane_id());
+        uint32_t b = 0, e = 0, g = 0;
+        bool live = false;
+        if (i < count) {
+            const uint32_t r = list[i];
+            b = offsets[r];
+            e = offsets[r + 1];
+            g = rank_gaussian[r];
+            live = b + k * chunk < e;
         }
-#pragma unroll
-        for (int c = 0; c < kGrad2d; ++c) acc[c] = wave_reduce_sum(acc[c]);
-        if (e - b <= chunk) {  // uniform: the run is this one chunk
-            if (lane == 0) {
-#pragma unroll
-                for (int c = 0; c < kGrad2d; ++c) grad2d[(size_t)g * kGrad2d + c] = acc[c];
-            }
-            continue;
-        }
-        // every lane's loads of the chunk fed the sums above, so overwriting position cb is safe
-        if (lane == 0) {
-            float4* dst = reinterpret_cast<float4*>(instance_grad) + 2 * (size_t)cb;
-            dst[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
-            dst[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
-            instance_grad_op[cb] = acc[8];
-        }
+        reduce_wave_long_runs(live, b, e, g, k, chunk, instance_grad, instance_grad_op, instance_tile, tile_cut,
+                              touched, grad2d);
     }
 }
 
-// Both reductions in one launch: workgroups [0, gx0) sum chunk 0 of every long run; the next
-// gx * (kLongChunks - 1) chunks 1.. of the runs longer than one chunk (their own, short list;
-// x = index % gx, chunk k = 1 + index / gx); the rest sum the short runs (256 ranks each).
+// Both reductions in one launch: workgroups [0, gx0) take chunk 0 of the long runs, the next
+// gx * (kLongChunks - 1) chunks 1.. of the runs longer than one chunk (x = index % gx, chunk
+// k = 1 + index / gx), the rest the short runs of the ranks (256 each).
 __global__ __launch_bounds__(256) void reduce_instance_grads_kernel(
     int64_t n, const uint32_t* __restrict__ depth_count, const uint32_t* __restrict__ offsets,
     const uint32_t* __restrict__ rank_gaussian, const uint32_t* __restrict__ long_list,
     const uint32_t* __restrict__ long_count, const uint32_t* __restrict__ multi_list,
     const uint32_t* __restrict__ multi_count, uint32_t gx0, uint32_t gx, uint32_t chunk,
-    float* __restrict__ instance_grad, float* __restrict__ instance_grad_op, const uint32_t* __restrict__ instance_tile,
+    float* __restrict__ instance_grad,
+    float* __restrict__ instance_grad_op, const uint32_t* __restrict__ instance_tile,
     const uint32_t* __restrict__ tile_cut, const uint8_t* __restrict__ touched, float* __restrict__ grad2d) {
     __shared__ float4 s_rec[kWavesPerBlock][2 * kShortPiece];
     __shared__ float s_op[kWavesPerBlock][kShortPiece];
@@ -1232,12 +1316,12 @@ __global__ __launch_bounds__(256) void reduce_instance_grads_kernel(
     }
     const uint32_t long_blocks = gx0 + gx * (kLongChunks - 1);
     if (blockIdx.x < long_blocks) {
-        const uint32_t b = blockIdx.x - gx0;
-        reduce_long_block(b % gx, 1 + b / gx, gx, multi_list, multi_count, offsets, rank_gaussian, chunk,
+        const uint32_t bi = blockIdx.x - gx0;
+        reduce_long_block(bi % gx, 1 + bi / gx, gx, multi_list, multi_count, offsets, rank_gaussian, chunk,
                           instance_grad, instance_grad_op, instance_tile, tile_cut, touched, grad2d);
         return;
     }
-    reduce_short_block(blockIdx.x - long_blocks, n, depth_count, offsets, rank_gaussian, instance_grad,
+    reduce_short_block(blockIdx.x - long_blocks, n, depth_count, offsets, rank_gaussian, chunk, instance_grad,
                        instance_grad_op, instance_tile, tile_cut, touched, grad2d, s_rec, s_op);
 }
 

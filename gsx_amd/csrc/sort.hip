@@ -45,8 +45,10 @@ __global__ __launch_bounds__(kScanThreads) void scan_reduce_kernel(const uint32_
 // 16 values per thread and step (4096: the block sums of 1M ranks in one step), all loaded
 // before the first wait (positions past count re-read position 0 and count as 0).
 constexpr int kPartialItems = 16;
+// Workgroup b scans the b-th of gridDim.x arrays of count + 1 entries laid out back to back.
 __global__ __launch_bounds__(kScanThreads) void scan_partials_kernel(uint32_t* __restrict__ partials, int64_t count) {
     __shared__ uint32_t s_wave[kScanThreads / kWave];
+    partials += (int64_t)blockIdx.x * (count + 1);
     uint32_t carry = 0;
     for (int64_t base = 0; base < count; base += (int64_t)kScanThreads * kPartialItems) {
         uint32_t vals[kPartialItems];
@@ -472,8 +474,8 @@ gsx_hip_status gsx_hip_radix_sort_keys_u64(uint64_t* keys, uint64_t* keys_alt, i
 
 namespace gsx_amd {
 
-gsx_hip_status scan_partials_in_place(uint32_t* partials, int64_t count, hipStream_t stream) {
-    hipLaunchKernelGGL(scan_partials_kernel, dim3(1), dim3(kScanThreads), 0, stream, partials, count);
+gsx_hip_status scan_partials_in_place(uint32_t* partials, int64_t count, hipStream_t stream, int arrays) {
+    hipLaunchKernelGGL(scan_partials_kernel, dim3((unsigned)arrays), dim3(kScanThreads), 0, stream, partials, count);
     return (gsx_hip_status)hipGetLastError();
 }
 
