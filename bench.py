@@ -56,15 +56,13 @@ def algorithmic_bytes(stage, geo, train=True):
         # out in depth order (the intermediate sort passes may stay on chip)
         return 8 * n + 12 * v
     if stage == "emit":
-        # per visible rank: count, Gaussian, geometry record in, offset out; per instance the key
-        # (8 B), its Gaussian (4 B) and, TRAIN, its tile (4 B) out
-        return 44 * v + (16 if train else 12) * i
+        # per visible rank: count, Gaussian, geometry record in, offset and long-run entry out;
+        # per instance its tile (4 B) and its Gaussian (4 B) out
+        return 48 * v + 8 * i
     if stage == "sort":
-        # the convention of sort bandwidth: per pass each 8-byte key is read twice (histogram,
-        # scatter) and written once
-        return geo["S"] * 24 * i
+        return sort_bytes(geo["S"], i)
     if stage == "ranges":
-        return 12 * i + 8 * t  # sorted keys in, emission positions out; one range per tile
+        return 4 * i + 8 * t  # sorted tiles in, one range per tile out
     if stage == "blend_forward":
         # ranges, reached entries' positions + Gaussians in, each reached Gaussian's record once;
         # image (12 B) + final T + last position out; TRAIN: each reached entry's Gaussian and the
@@ -90,6 +88,15 @@ def algorithmic_bytes(stage, geo, train=True):
     if stage == "adam":
         return 28 * 14 * n  # 14 floats per Gaussian: parameter, m, v in and out, gradient in
     return 0
+
+
+def sort_bytes(passes, instances):
+    """Bytes the tile sort moves: per pass each 4-byte tile is read twice (digit counts, then
+    scatter) and written once with its 4-byte position; the first pass reads no positions (they
+    are the input order), the later ones read them once."""
+    if passes <= 0:
+        return 0
+    return instances * (16 * passes + 4 * (passes - 1))
 
 
 def render_geometry(lib, renderer, n, width, height):
@@ -298,12 +305,12 @@ def extra_workloads(lib, steps):
     r.set_timing(0)
     st = r.stats()
     inst = int(st.instance_count)
-    sort_bytes = int(st.sort_passes) * 24 * inst
+    moved = sort_bytes(int(st.sort_passes), inst)
     out["c4_sort_stress"] = {"gaussians": w.scene.count, "width": 1920, "height": 1080, "ms_per_step": round(ms, 3),
                              "it_s": round(1000.0 / ms, 2), "instances": inst, "sort_passes": int(st.sort_passes),
                              "sort_ms": round(stage["sort"], 3),
-                             "sort_gbps": round(sort_bytes / (stage["sort"] * 1e-3) / 1e9, 1),
-                             "sort_hbm_frac": round(sort_bytes / (stage["sort"] * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+                             "sort_gbps": round(moved / (stage["sort"] * 1e-3) / 1e9, 1),
+                             "sort_hbm_frac": round(moved / (stage["sort"] * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
                              "stage_ms": {k: round(v, 3) for k, v in stage.items()}}
     del g, step, r, inputs, w
     log(f"config 4: {out['c4_sort_stress']}")

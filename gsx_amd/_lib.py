@@ -66,12 +66,12 @@ class GaussianGrads(ctypes.Structure):
 
 class RenderStats(ctypes.Structure):
     _fields_ = [("gaussian_count", _i64), ("visible_count", _i64), ("instance_count", _i64), ("tile_count", _i32),
-                ("sort_passes", _i32), ("depth_sort_passes", _i32), ("key_tile_shift", _i32),
-                ("key_payload_bits", _i32)]
+                ("sort_passes", _i32), ("depth_sort_passes", _i32), ("tile_bits", _i32),
+                ("sorted_tile_bytes", _i32)]
 
 
 class RenderBuffers(ctypes.Structure):
-    _fields_ = [("sorted_keys", _vp), ("sorted_values", _vp), ("tile_ranges", _vp), ("records", _vp),
+    _fields_ = [("sorted_tiles", _vp), ("sorted_values", _vp), ("tile_ranges", _vp), ("records", _vp),
                 ("tile_counts", _vp), ("instance_gaussian", _vp), ("final_transmittance", _vp),
                 ("last_contributor", _vp)]
 

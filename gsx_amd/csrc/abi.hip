@@ -247,9 +247,10 @@ int bits_for(uint32_t v) {
 }  // namespace
 
 struct gsx_hip_render_context {
-    DeviceBuffer rec, cov_coef, ckpt, inst_gauss, inst_tile, tile_cut, touched, inst_grad, tile_count, big_list, offsets, scan_temp, keys, vals,
-        keys_alt, sort_temp, ranges, sorted_g, final_t, last, grad2d, depth_keys, depth_keys_alt, rank_g, rank_count,
-        g_rank, long_list, multi_list, counters, big_chunk_counts, depth_sort_temp;
+    DeviceBuffer rec, cov_coef, ckpt, inst_gauss, inst_tile, tiles_alt, tiles_sorted, vals_alt, vals, tile_cut, touched,
+        inst_grad, tile_count, big_list, offsets, scan_temp, sort_temp, ranges, sorted_g, final_t, last, grad2d,
+        depth_keys, depth_keys_alt, rank_g, rank_count, g_rank, long_list, multi_list, counters, big_chunk_counts,
+        depth_sort_temp;
     // partial instance counts written by the counting kernels (preprocess: one u32 per workgroup;
     // big boxes: one u64 per workgroup), summed on the host after count_ev
     PinnedBuffer kept_parts;
@@ -277,9 +278,8 @@ struct gsx_hip_render_context {
     int32_t tile_count_total = 0;
     int32_t sort_passes = 0;
     int32_t depth_sort_passes = 0;
-    bool sorted_in_alt = false;
-    KeyLayout layout{};
-    uint32_t* sorted_vals = nullptr;  // emission position of each sorted key
+    int32_t tile_bits = 0;            // bits of the tile index the sort orders
+    uint32_t* sorted_vals = nullptr;  // emission position of each sorted instance
     bool has_train_state = false;
     // Stage timing: a ring of event sets, one set per forward/backward pair, so that a timed
     // loop records without synchronising; get_timings averages over the recorded sets.
@@ -557,9 +557,10 @@ gsx_hip_status gsx_hip_render_context_create(gsx_hip_render_context** out_contex
 gsx_hip_status gsx_hip_render_context_destroy(gsx_hip_render_context* ctx) {
     if (ctx == nullptr) return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "context must be non-null");
     DeviceBuffer* all[] = {&ctx->rec,       &ctx->cov_coef, &ctx->ckpt,      &ctx->inst_gauss, &ctx->inst_tile,
+                           &ctx->tiles_alt, &ctx->tiles_sorted, &ctx->vals_alt, &ctx->vals,
                            &ctx->tile_cut,  &ctx->touched,  &ctx->inst_grad,
-                           &ctx->tile_count, &ctx->big_list, &ctx->offsets,   &ctx->scan_temp,  &ctx->keys,
-                           &ctx->vals,       &ctx->keys_alt, &ctx->sort_temp,  &ctx->ranges,
+                           &ctx->tile_count, &ctx->big_list, &ctx->offsets,   &ctx->scan_temp,
+                           &ctx->sort_temp,  &ctx->ranges,
                            &ctx->sorted_g,   &ctx->final_t,  &ctx->last,      &ctx->grad2d,     &ctx->depth_keys,
                            &ctx->depth_keys_alt, &ctx->rank_g, &ctx->rank_count, &ctx->g_rank,
                            &ctx->long_list, &ctx->multi_list, &ctx->counters, &ctx->big_chunk_counts,
@@ -806,54 +807,47 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     const int64_t count = (int64_t)total;
     ctx->instance_count = count;
     const size_t c1 = (size_t)(count > 0 ? count : 1);
-    GSX_TRY(ctx->keys.reserve(c1 * sizeof(uint64_t), "keys"));
-    GSX_TRY(ctx->keys_alt.reserve(c1 * sizeof(uint64_t), "keys_alt"));
+    // per instance: its tile (emission order, the sort's input, kept for the backward), the middle
+    // pass's tiles and positions, the sorted tiles and positions, its Gaussian
+    GSX_TRY(ctx->inst_tile.reserve(c1 * sizeof(uint32_t), "instance_tile"));
+    GSX_TRY(ctx->tiles_alt.reserve(c1 * sizeof(uint32_t), "tiles_alt"));
+    GSX_TRY(ctx->tiles_sorted.reserve(c1 * sizeof(uint32_t), "tiles_sorted"));
+    GSX_TRY(ctx->vals_alt.reserve(c1 * sizeof(uint32_t), "vals_alt"));
     GSX_TRY(ctx->vals.reserve(c1 * sizeof(uint32_t), "vals"));
     GSX_TRY(ctx->inst_gauss.reserve(c1 * sizeof(uint32_t), "instance_gaussian"));
     GSX_TRY(ctx->sorted_g.reserve(c1 * sizeof(uint32_t), "sorted_g"));
-    GSX_TRY(ctx->sort_temp.reserve(radix_sort_keys_u64_digits_temp_bytes(count), "sort_temp"));
-    // instance keys: tile << payload_bits | emission position (at most 32 + 32 bits)
-    const int pos_bits = std::max(1, bits_for((uint32_t)(count > 0 ? count - 1 : 0)));
-    KeyLayout layout{};
-    layout.payload_bits = pos_bits;
-    layout.tile_shift = pos_bits;
-    ctx->layout = layout;
+    GSX_TRY(ctx->sort_temp.reserve(tile_sort_u32_temp_bytes(count), "sort_temp"));
     if (train) {
         // bucket checkpoints: at most I/kBucket + tiles + 1 slots of 256 floats
         GSX_TRY(ctx->ckpt.reserve(((size_t)count / kBucket + (size_t)tiles + 2) * 256 * sizeof(float),
                                   "checkpoints"));
-        GSX_TRY(ctx->inst_tile.reserve(c1 * sizeof(uint32_t), "instance_tile"));
     }
     if (n > 0) {
         const uint32_t big_blocks = kBigBlocks * big_chunks;
         hipLaunchKernelGGL(emit_kernel, dim3(big_blocks + pre_blocks), dim3(256), 0, stream, n, ctx->rec.as<float4>(),
                            ctx->rank_g.as<uint32_t>(), ctx->rank_count.as<uint32_t>(), ctx->scan_temp.as<uint32_t>(),
-                           ctx->offsets.as<uint32_t>(), cam.tiles_x, layout, ctx->big_list.as<uint32_t>(), big_count,
+                           ctx->offsets.as<uint32_t>(), cam.tiles_x, ctx->big_list.as<uint32_t>(), big_count,
                            kBigBlocks, big_blocks, big_chunk, ctx->big_chunk_counts.as<uint32_t>(),
-                           ctx->g_rank.as<uint32_t>(), ctx->keys.as<uint64_t>(), ctx->inst_gauss.as<uint32_t>(),
-                           train ? ctx->inst_tile.as<uint32_t>() : nullptr,
+                           ctx->g_rank.as<uint32_t>(), ctx->inst_gauss.as<uint32_t>(), ctx->inst_tile.as<uint32_t>(),
                            ctx->scan_temp.as<uint32_t>() + pre_blocks + 1, ctx->long_list.as<uint32_t>());
         GSX_HIP_TRY(hipGetLastError(), "emit_kernel");
     }
     GSX_TRY(record(ctx, 3, stream));
-    int in_alt = 0;
-    // tile bits in ceil(bits / 8) passes of equal digits of 6 to 8 bits (1080p: 13 bits, 2 x 7)
-    ctx->sort_passes = (tile_bits + 7) / 8;
+    // tile bits in ceil(bits / 8) passes (at least one) of equal digits of 6 to 8 bits (1080p:
+    // 13 bits, 2 x 7)
+    ctx->sort_passes = std::max(1, (tile_bits + 7) / 8);
+    ctx->tile_bits = tile_bits;
     {
-        const int digit_bits =
-            ctx->sort_passes == 0 ? 8 : std::max(6, (tile_bits + ctx->sort_passes - 1) / ctx->sort_passes);
-        GSX_TRY(radix_sort_keys_u64_digits(ctx->keys.as<uint64_t>(), ctx->keys_alt.as<uint64_t>(), count,
-                                           layout.tile_shift, ctx->sort_passes, digit_bits, ctx->sort_temp.ptr,
-                                           &in_alt, stream));
-        ctx->sorted_vals = ctx->vals.as<uint32_t>();  // written by tile_ranges_kernel
+        const int digit_bits = std::max(6, (tile_bits + ctx->sort_passes - 1) / ctx->sort_passes);
+        GSX_TRY(tile_sort_u32(ctx->inst_tile.as<uint32_t>(), ctx->tiles_alt.as<uint32_t>(),
+                              ctx->tiles_sorted.as<uint32_t>(), ctx->vals_alt.as<uint32_t>(), ctx->vals.as<uint32_t>(),
+                              count, tile_bits, ctx->sort_passes, digit_bits, ctx->sort_temp.ptr, stream));
+        ctx->sorted_vals = ctx->vals.as<uint32_t>();
     }
-    ctx->sorted_in_alt = in_alt != 0;
     GSX_TRY(record(ctx, 4, stream));
-    const uint64_t* skeys = ctx->sorted_in_alt ? ctx->keys_alt.as<uint64_t>() : ctx->keys.as<uint64_t>();
     if (count > 0) {
-        hipLaunchKernelGGL(tile_ranges_kernel, dim3(blocks_for((count + 3) / 4, 256)), dim3(256), 0, stream, skeys,
-                           layout,
-                           ctx->sorted_vals, ctx->offsets.as<uint32_t>() + n, (uint32_t)tiles,
+        hipLaunchKernelGGL(tile_ranges_kernel, dim3(blocks_for((count + 3) / 4, 256)), dim3(256), 0, stream,
+                           ctx->tiles_sorted.as<uint32_t>(), ctx->offsets.as<uint32_t>() + n, (uint32_t)tiles,
                            ctx->ranges.as<uint2>());
     } else {
         hipLaunchKernelGGL(fill_u32_kernel, dim3(blocks_for((int64_t)tiles * 2, 256)), dim3(256), 0, stream,
@@ -1016,14 +1010,14 @@ gsx_hip_status gsx_hip_render_context_get_stats(const gsx_hip_render_context* ct
     out->tile_count = ctx->tile_count_total;
     out->sort_passes = ctx->sort_passes;
     out->depth_sort_passes = ctx->depth_sort_passes;
-    out->key_tile_shift = ctx->layout.tile_shift;
-    out->key_payload_bits = ctx->layout.payload_bits;
+    out->tile_bits = ctx->tile_bits;
+    out->sorted_tile_bytes = (int32_t)sizeof(uint32_t);
     return GSX_HIP_SUCCESS;
 }
 
 gsx_hip_status gsx_hip_render_context_get_buffers(const gsx_hip_render_context* ctx, gsx_hip_render_buffers* out) {
     if (ctx == nullptr || out == nullptr) return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "context/out must be non-null");
-    out->sorted_keys = ctx->sorted_in_alt ? ctx->keys_alt.as<uint64_t>() : ctx->keys.as<uint64_t>();
+    out->sorted_tiles = ctx->tiles_sorted.as<uint32_t>();
     out->sorted_values = ctx->sorted_vals;
     out->tile_ranges = ctx->ranges.as<uint32_t>();
     out->records = ctx->rec.as<float>();

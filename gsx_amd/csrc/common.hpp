@@ -499,17 +499,18 @@ constexpr int kChunkWaves = kSortThreads / kWave;  // 4 (upsweep)
 constexpr int kCompactingChunk = 1024;
 constexpr uint64_t kSentinelKey = ~0ull;  // dropped by a pass with drop_sentinel set
 
-template <int kBits>
-__device__ inline uint32_t digit_of(uint64_t key, int shift) {
+template <int kBits, typename KeyT>
+__device__ inline uint32_t digit_of(KeyT key, int shift) {
     return (uint32_t)(key >> shift) & ((1u << kBits) - 1u);
 }
 
 // Upsweep of one kChunk-key chunk (workgroup `blk` of kSortThreads threads): its digit counts,
 // counted in wave-private LDS counters, to hist[digit][blk]. n_dev (may be null): live key
 // count, n = min(n, *n_dev); drop_sentinel: keys equal to kSentinelKey are not counted.
-// dmask keeps the digit's bits below the sort's end bit (a last pass narrower than kBits).
-template <int kBits, int kChunk>
-__device__ inline void radix_upsweep_block(uint32_t blk, const uint64_t* __restrict__ keys, int64_t n,
+// dmask keeps the digit's bits below the sort's end bit (a last pass narrower than kBits). KeyT:
+// uint64_t (the depth order and the public sorts) or uint32_t (tile indices).
+template <int kBits, int kChunk, typename KeyT = uint64_t>
+__device__ inline void radix_upsweep_block(uint32_t blk, const KeyT* __restrict__ keys, int64_t n,
                                            const uint32_t* __restrict__ n_dev, bool drop_sentinel, int shift,
                                            int64_t num_chunks, uint32_t* __restrict__ hist,
                                            uint32_t (*s_hist)[1 << kBits], uint32_t dmask = (1u << kBits) - 1u) {
@@ -523,13 +524,13 @@ __device__ inline void radix_upsweep_block(uint32_t blk, const uint64_t* __restr
         // every key of the chunk is loaded before the first count waits on one (no load sits
         // under a branch: lanes past n re-read key n - 1 and count nothing)
         constexpr int kRounds = kChunk / kSortThreads;
-        uint64_t k[kRounds];
+        KeyT k[kRounds];
 #pragma unroll
         for (int r = 0; r < kRounds; ++r) k[r] = keys[min(base + (int64_t)r * kSortThreads + threadIdx.x, n - 1)];
 #pragma unroll
         for (int r = 0; r < kRounds; ++r) {
             const int64_t i = base + (int64_t)r * kSortThreads + threadIdx.x;
-            if (i < n && (!drop_sentinel || k[r] != kSentinelKey))
+            if (i < n && (!drop_sentinel || (uint64_t)k[r] != kSentinelKey))
                 atomicAdd(&s_hist[wave][digit_of<kBits>(k[r], shift) & dmask], 1u);
         }
     }
@@ -556,13 +557,16 @@ gsx_hip_status radix_sort_keys_u64_compacting(uint64_t* keys, uint64_t* keys_alt
                                               hipStream_t stream, bool first_hist_ready);
 size_t radix_sort_keys_u64_compacting_temp_bytes(int64_t n);
 
-// Keys-only stable radix sort (the public sort's kernels) on bits [begin_bit, begin_bit + passes *
-// digit_bits) with digits of 6, 7 or 8 bits: a key field of b bits sorts in ceil(b / 8) passes of
-// ceil(b / passes) bits, fewer ballots and bins than 8-bit digits (13-bit tiles: 2 passes of 7).
-// temp holds radix_sort_keys_u64_digits_temp_bytes(n) bytes (the 8-bit need, the largest).
-gsx_hip_status radix_sort_keys_u64_digits(uint64_t* keys, uint64_t* keys_alt, int64_t n, int begin_bit, int passes,
-                                         int digit_bits, void* temp, int* out_in_alt, hipStream_t stream);
-size_t radix_sort_keys_u64_digits_temp_bytes(int64_t n);
+// Stable LSD radix sort of n u32 tile indices (bits [0, tile_bits)) with their input positions
+// as values, in `passes` passes of digit_bits (6, 7 or 8) bits: a tile field of b bits sorts in
+// ceil(b / 8) passes of ceil(b / passes) bits, fewer ballots and bins than 8-bit digits (13-bit
+// tiles: 2 passes of 7). The first pass reads `tiles` (left unchanged) and no values; the result
+// lands in tiles_sorted / vals_sorted (the alternates hold a middle pass). temp holds
+// tile_sort_u32_temp_bytes(n) bytes (the 8-bit need, the largest).
+gsx_hip_status tile_sort_u32(const uint32_t* tiles, uint32_t* tiles_alt, uint32_t* tiles_sorted, uint32_t* vals_alt,
+                             uint32_t* vals_sorted, int64_t n, int tile_bits, int passes, int digit_bits, void* temp,
+                             hipStream_t stream);
+size_t tile_sort_u32_temp_bytes(int64_t n);
 
 // Exclusive scan of partials[0..count) in place, the total stored at [count], by one workgroup;
 // with arrays > 1, the arrays of count + 1 entries that follow it too (one workgroup each).

@@ -49,22 +49,9 @@ static_assert(kBigTiles <= 1024, "the tile walk divides indices below 2^10 by bo
 // | index (visible depths lie in [near, far], where positive floats order like their bit
 // patterns, so the offset keeps the order in fewer bits; invisible Gaussians get the offset
 // bits(far) - bits(near) + 1 and sort last). Instances are then emitted in that depth order,
-// key = tile << tile_shift | emission position, and sorted stably on the tile bits alone: each
-// tile's run is in (depth, index) order, the CPU backend's order, after two passes at 1080p.
-struct KeyLayout {
-    int tile_shift;    // = payload bits (emission position)
-    int payload_bits;
-};
-
-__device__ inline uint64_t make_key(const KeyLayout& k, uint32_t tile, uint32_t pos) {
-    uint64_t key = (uint64_t)pos;
-    if (k.tile_shift < 64) key |= (uint64_t)tile << k.tile_shift;
-    return key;
-}
-
-__device__ inline uint32_t key_tile(const KeyLayout& k, uint64_t key) {
-    return k.tile_shift < 64 ? (uint32_t)(key >> k.tile_shift) : 0u;
-}
+// instance_tile[position] = tile, and the tile indices are sorted stably (u32 keys, the emission
+// positions as values, implicit in the first pass): each tile's run is in (depth, index) order,
+// the CPU backend's order, after two passes at 1080p.
 
 __device__ inline uint32_t box_tiles(float4 geo1) {
     const uint32_t bx = __float_as_uint(geo1.z), by = __float_as_uint(geo1.w);
@@ -138,13 +125,11 @@ __device__ inline uint32_t stage_box(WaveBoxes& w, bool valid, float4 r0, float4
     return (uint32_t)__shfl((int)incl, kWave - 1, kWave);
 }
 
-// Walks the wave's flattened tiles. kEmit: writes kept instances (key, value = position,
-// instance_gaussian and, when non-null, instance_tile) at out[owner] + rank; always accumulates
-// kept[owner].
+// Walks the wave's flattened tiles. kEmit: writes kept instances (instance_tile,
+// instance_gaussian) at position out[owner] + rank; always accumulates kept[owner].
 template <bool kEmit>
-__device__ inline void walk_wave_tiles(WaveBoxes& w, uint32_t wave_total, int32_t tiles_x, const KeyLayout& layout,
-                                       uint64_t* __restrict__ keys, uint32_t* __restrict__ instance_gaussian,
-                                       uint32_t* __restrict__ instance_tile) {
+__device__ inline void walk_wave_tiles(WaveBoxes& w, uint32_t wave_total, int32_t tiles_x,
+                                       uint32_t* __restrict__ instance_gaussian, uint32_t* __restrict__ instance_tile) {
     const uint32_t lane = __lane_id();
     const uint64_t lt = lanemask_lt();
     // the owner of pair p is the last box starting at or before p, i.e. the last non-empty one
@@ -193,9 +178,8 @@ __device__ inline void walk_wave_tiles(WaveBoxes& w, uint32_t wave_total, int32_
         const uint32_t before = w.kept[owner];
         if (kEmit && keep) {
             const uint32_t pos = w.out[owner] + before + (uint32_t)__popcll(mask & lt & seg);
-            keys[pos] = make_key(layout, tile, pos);
             instance_gaussian[pos] = w.g[owner];
-            if (instance_tile != nullptr) instance_tile[pos] = tile;
+            instance_tile[pos] = tile;
         }
         // the last lane of each owner segment advances that owner's running count
         const uint32_t next_owner = (uint32_t)__shfl_down((int)owner, 1, kWave);
@@ -297,7 +281,7 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
     const uint32_t big_slot = wave_append_slot(big_count, big);
     if (big) big_list[big_slot] = (uint32_t)g;
     const uint32_t total = stage_box(wb, visible && !big, r0, r1, (uint32_t)g, 0u, false);
-    walk_wave_tiles<false>(wb, total, cam.tiles_x, KeyLayout{}, nullptr, nullptr, nullptr);
+    walk_wave_tiles<false>(wb, total, cam.tiles_x, nullptr, nullptr);
     const uint32_t kept = big ? 0u : wb.kept[__lane_id()];  // big boxes: counted by big_tiles_kernel
     if (g < n) tile_count[g] = kept;
     // the workgroup's kept tiles (at most 256 * kBigTiles) to kept_part[block], host memory that
@@ -379,11 +363,11 @@ __global__ __launch_bounds__(256) void rank_gather_kernel(int64_t n, const uint3
 }
 
 // ---------------------------------------------------------------------------------------------
-// Key emission in depth order: the Gaussian of rank r owns positions offset[r] .. offset[r+1])
-// of the instance array, one per kept tile of its box in row-major tile order (offsets are the
-// exclusive scan of the counts in rank order). key = tile << tile_shift | position,
-// instance_gaussian[position] = g and, for a TRAIN forward, instance_tile[position] = tile (the
-// backward's reduction looks up each position's tile). A stable sort on the tile bits then
+// Instance emission in depth order: the Gaussian of rank r owns positions offset[r] ..
+// offset[r+1]) of the instance array, one per kept tile of its box in row-major tile order
+// (offsets are the exclusive scan of the counts in rank order). instance_tile[position] = tile
+// (the sort's keys; the backward's reduction also looks up each position's tile) and
+// instance_gaussian[position] = g. A stable sort of the tiles with the positions as values then
 // leaves every tile's run in (depth, index) order, i.e. in ascending position.
 // The offsets are finished here: block_prefix[b] is the exclusive scan of rank_gather_kernel's
 // 256-rank sums, and emission workgroup b (ranks 256 b .. 256 b + 255, rank_gather_kernel's
@@ -393,8 +377,8 @@ __global__ __launch_bounds__(256) void rank_gather_kernel(int64_t n, const uint3
 __device__ inline void emit_block(uint32_t b, int64_t n, const float4* __restrict__ rec,
                                   const uint32_t* __restrict__ rank_gaussian, const uint32_t* __restrict__ rank_count,
                                   const uint32_t* __restrict__ block_prefix, uint32_t* __restrict__ offsets,
-                                  int32_t tiles_x, KeyLayout layout, uint64_t* __restrict__ keys,
-                                  uint32_t* __restrict__ instance_gaussian, uint32_t* __restrict__ instance_tile,
+                                  int32_t tiles_x, uint32_t* __restrict__ instance_gaussian,
+                                  uint32_t* __restrict__ instance_tile,
                                   const uint32_t* __restrict__ long_prefix, uint32_t* __restrict__ long_list,
                                   WaveBoxes* s_boxes, uint32_t* s_wave) {
     WaveBoxes& wb = s_boxes[threadIdx.x / kWave];
@@ -430,7 +414,7 @@ __device__ inline void emit_block(uint32_t b, int64_t n, const float4* __restric
     // a box whose kept count (from the counting walk's identical tests) is its tile count keeps
     // every tile: emission skips its tests
     const uint32_t total = stage_box(wb, any, r0, r1, g, o, any && cnt == box_tiles(r1));
-    walk_wave_tiles<true>(wb, total, tiles_x, layout, keys, instance_gaussian, instance_tile);
+    walk_wave_tiles<true>(wb, total, tiles_x, instance_gaussian, instance_tile);
 }
 
 // Big boxes: the row-major tile range of each box on big_list is cut into chunks of `chunk`
@@ -448,12 +432,12 @@ constexpr uint32_t kBigChunks = 16;
 template <bool kEmit>
 __device__ inline void big_tiles_block(uint32_t x, uint32_t c, uint32_t gx, const uint32_t* __restrict__ big_list,
                                        const uint32_t* __restrict__ big_count, const float4* __restrict__ rec,
-                                       int32_t tiles_x, KeyLayout layout, uint32_t chunk,
+                                       int32_t tiles_x, uint32_t chunk,
                                        uint32_t* __restrict__ tile_count, uint32_t* __restrict__ chunk_counts,
                                        unsigned long long* __restrict__ kept_part,
                                        const uint32_t* __restrict__ rank_count,
                                        const uint32_t* __restrict__ block_prefix,
-                                       const uint32_t* __restrict__ gaussian_rank, uint64_t* __restrict__ keys,
+                                       const uint32_t* __restrict__ gaussian_rank,
                                        uint32_t* __restrict__ instance_gaussian,
                                        uint32_t* __restrict__ instance_tile, uint32_t* s_wave, uint32_t* s_red) {
     const uint32_t count = *big_count;
@@ -509,9 +493,8 @@ __device__ inline void big_tiles_block(uint32_t x, uint32_t c, uint32_t gx, cons
             }
             if (kEmit && keep) {
                 const uint32_t pos = o + running + before + (uint32_t)__popcll(mask & lanemask_lt());
-                keys[pos] = make_key(layout, tile, pos);
                 instance_gaussian[pos] = g;
-                if (instance_tile != nullptr) instance_tile[pos] = tile;
+                instance_tile[pos] = tile;
             }
             running += step_total;
             __syncthreads();
@@ -542,9 +525,9 @@ __global__ __launch_bounds__(256) void big_count_upsweep_kernel(const uint32_t* 
     __shared__ uint32_t s_wave[kWavesPerBlock];
     __shared__ uint32_t s_hist[kChunkWaves][1 << kCompactingRadixBits];
     if (blockIdx.x < big_blocks) {
-        big_tiles_block<false>(blockIdx.x % gx, blockIdx.x / gx, gx, big_list, big_count, rec, tiles_x, KeyLayout{},
-                               chunk, tile_count, chunk_counts, kept_part, nullptr, nullptr, nullptr, nullptr, nullptr,
-                               nullptr, s_wave, nullptr);
+        big_tiles_block<false>(blockIdx.x % gx, blockIdx.x / gx, gx, big_list, big_count, rec, tiles_x, chunk,
+                               tile_count, chunk_counts, kept_part, nullptr, nullptr, nullptr, nullptr, nullptr, s_wave,
+                               nullptr);
         return;
     }
     radix_upsweep_block<kCompactingRadixBits, kCompactingChunk>(blockIdx.x - big_blocks, depth_keys, n, nullptr, true,
@@ -558,13 +541,13 @@ __global__ __launch_bounds__(256) void emit_kernel(int64_t n, const float4* __re
                                                    const uint32_t* __restrict__ rank_gaussian,
                                                    const uint32_t* __restrict__ rank_count,
                                                    const uint32_t* __restrict__ block_prefix,
-                                                   uint32_t* __restrict__ offsets, int32_t tiles_x, KeyLayout layout,
+                                                   uint32_t* __restrict__ offsets, int32_t tiles_x,
                                                    const uint32_t* __restrict__ big_list,
                                                    const uint32_t* __restrict__ big_count, uint32_t gx,
                                                    uint32_t big_blocks, uint32_t chunk,
                                                    const uint32_t* __restrict__ chunk_counts,
                                                    const uint32_t* __restrict__ gaussian_rank,
-                                                   uint64_t* __restrict__ keys, uint32_t* __restrict__ instance_gaussian,
+                                                   uint32_t* __restrict__ instance_gaussian,
                                                    uint32_t* __restrict__ instance_tile,
                                                    const uint32_t* __restrict__ long_prefix,
                                                    uint32_t* __restrict__ long_list) {
@@ -572,12 +555,12 @@ __global__ __launch_bounds__(256) void emit_kernel(int64_t n, const float4* __re
     __shared__ uint32_t s_wave[kWavesPerBlock];
     __shared__ uint32_t s_red[kWavesPerBlock];
     if (blockIdx.x < big_blocks) {
-        big_tiles_block<true>(blockIdx.x % gx, blockIdx.x / gx, gx, big_list, big_count, rec, tiles_x, layout, chunk,
+        big_tiles_block<true>(blockIdx.x % gx, blockIdx.x / gx, gx, big_list, big_count, rec, tiles_x, chunk,
                               nullptr, const_cast<uint32_t*>(chunk_counts), nullptr, rank_count, block_prefix,
-                              gaussian_rank, keys, instance_gaussian, instance_tile, s_wave, s_red);
+                              gaussian_rank, instance_gaussian, instance_tile, s_wave, s_red);
         return;
     }
-    emit_block(blockIdx.x - big_blocks, n, rec, rank_gaussian, rank_count, block_prefix, offsets, tiles_x, layout, keys,
+    emit_block(blockIdx.x - big_blocks, n, rec, rank_gaussian, rank_count, block_prefix, offsets, tiles_x,
                instance_gaussian, instance_tile, long_prefix, long_list, s_boxes, s_wave);
 }
 
@@ -591,39 +574,34 @@ __global__ __launch_bounds__(256) void fill_f32_kernel(float* __restrict__ p, in
     if (i < count) p[i] = v;
 }
 
-// [start, end) of each tile's run in the sorted keys, and the emission position of every sorted
-// key (values[i], the payload bits). Tiles without keys get (0, 0): the thread of the last key
-// before such a gap (or of the first key, for the tiles before it) writes them, so no fill of
-// all tiles is needed beforehand. count >= 1 (with no keys the caller fills the ranges).
-// Each thread takes 4 consecutive sorted keys (two 16-byte loads, one 16-byte store of their
-// positions), plus the keys just before and after them for the boundaries.
-__global__ __launch_bounds__(256) void tile_ranges_kernel(const uint64_t* __restrict__ keys, KeyLayout layout,
-                                                          uint32_t* __restrict__ values, const uint32_t* count_ptr,
-                                                          uint32_t tiles, uint2* __restrict__ ranges) {
+// [start, end) of each tile's run in the sorted tile indices. Tiles without instances get
+// (0, 0): the thread of the last instance before such a gap (or of the first instance, for the
+// tiles before it) writes them, so no fill of all tiles is needed beforehand. count >= 1 (with
+// no instances the caller fills the ranges). Each thread takes 4 consecutive sorted tiles (one
+// 16-byte load), plus the tiles just before and after them for the boundaries.
+__global__ __launch_bounds__(256) void tile_ranges_kernel(const uint32_t* __restrict__ sorted_tiles,
+                                                          const uint32_t* count_ptr, uint32_t tiles,
+                                                          uint2* __restrict__ ranges) {
     const uint32_t count = *count_ptr;
     const uint32_t i0 = 4u * (blockIdx.x * blockDim.x + threadIdx.x);
     if (i0 >= count) return;
     const uint32_t m = min(4u, count - i0);
-    // the neighbours' keys load with the thread's own (clamped in-range positions, not branches)
-    const uint64_t k_prev = keys[i0 == 0 ? 0u : i0 - 1u];
-    const uint64_t k_next = keys[min(i0 + m, count - 1u)];
-    uint64_t k[4];
+    // the neighbours load with the thread's own (clamped in-range positions, not branches)
+    const uint32_t t_prev = sorted_tiles[i0 == 0 ? 0u : i0 - 1u];
+    const uint32_t t_next = sorted_tiles[min(i0 + m, count - 1u)];
+    uint32_t t[4];
     if (m == 4) {
-        const ulonglong2* p = reinterpret_cast<const ulonglong2*>(keys + i0);
-        const ulonglong2 a = p[0], b = p[1];
-        k[0] = a.x;
-        k[1] = a.y;
-        k[2] = b.x;
-        k[3] = b.y;
+        const uint4 q = *reinterpret_cast<const uint4*>(sorted_tiles + i0);
+        t[0] = q.x;
+        t[1] = q.y;
+        t[2] = q.z;
+        t[3] = q.w;
     } else {
 #pragma unroll
-        for (uint32_t j = 0; j < 4; ++j) k[j] = j < m ? keys[i0 + j] : 0ull;
+        for (uint32_t j = 0; j < 4; ++j) t[j] = j < m ? sorted_tiles[i0 + j] : 0u;
     }
-    uint32_t t[4];
-#pragma unroll
-    for (uint32_t j = 0; j < 4; ++j) t[j] = key_tile(layout, k[j]);
-    const uint32_t prev = i0 == 0 ? UINT32_MAX : key_tile(layout, k_prev);
-    const uint32_t next = i0 + m == count ? tiles : key_tile(layout, k_next);
+    const uint32_t prev = i0 == 0 ? UINT32_MAX : t_prev;
+    const uint32_t next = i0 + m == count ? tiles : t_next;
     if (i0 == 0) {
         for (uint32_t u = 0; u < t[0]; ++u) ranges[u] = make_uint2(0u, 0u);
     }
@@ -638,13 +616,6 @@ __global__ __launch_bounds__(256) void tile_ranges_kernel(const uint64_t* __rest
                 for (uint32_t u = t[j] + 1; u < after; ++u) ranges[u] = make_uint2(0u, 0u);
             }
         }
-    }
-    const uint64_t payload = (1ull << layout.payload_bits) - 1ull;
-    if (m == 4) {
-        *reinterpret_cast<uint4*>(values + i0) = make_uint4((uint32_t)(k[0] & payload), (uint32_t)(k[1] & payload),
-                                                            (uint32_t)(k[2] & payload), (uint32_t)(k[3] & payload));
-    } else {
-        for (uint32_t j = 0; j < m; ++j) values[i0 + j] = (uint32_t)(k[j] & payload);
     }
 }
 

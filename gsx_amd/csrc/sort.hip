@@ -21,7 +21,7 @@ constexpr int kScanChunk = kScanThreads * kScanItems;  // 1024 elements per bloc
 
 constexpr int kSortChunk = 4096;  // keys per chunk (one upsweep / downsweep workgroup), public sorts
 constexpr int kRadixBits = 8;     // digit width of the public sorts
-// Chunk of the tile sort's passes (radix_sort_keys_u64_digits)
+// Chunk of the tile sort's passes (tile_sort_u32)
 constexpr int kDigitsChunk = 4096;
 constexpr int kRowItems = 16;  // row scan: 16 chunk counts per thread and step
 constexpr int kRowChunk = kSortThreads * kRowItems;
@@ -115,15 +115,15 @@ __global__ __launch_bounds__(kScanThreads) void scan_downsweep_kernel(const uint
 // ---------------------------------------------------------------------------------------------
 // n_dev (may be null): live key count, n = min(n, *n_dev); chunks past it count nothing.
 // drop_sentinel: keys equal to kSentinelKey are left out (they vanish from the output).
-template <int kBits, int kChunk>
-__global__ __launch_bounds__(kSortThreads) void radix_upsweep_kernel(const uint64_t* __restrict__ keys, int64_t n,
+template <int kBits, int kChunk, typename KeyT = uint64_t>
+__global__ __launch_bounds__(kSortThreads) void radix_upsweep_kernel(const KeyT* __restrict__ keys, int64_t n,
                                                                      const uint32_t* __restrict__ n_dev,
                                                                      bool drop_sentinel, int shift,
                                                                      uint32_t dmask, int64_t num_chunks,
                                                                      uint32_t* __restrict__ hist) {
     __shared__ uint32_t s_hist[kChunkWaves][1 << kBits];
-    radix_upsweep_block<kBits, kChunk>(blockIdx.x, keys, n, n_dev, drop_sentinel, shift, num_chunks, hist, s_hist,
-                                       dmask);
+    radix_upsweep_block<kBits, kChunk, KeyT>(blockIdx.x, keys, n, n_dev, drop_sentinel, shift, num_chunks, hist,
+                                             s_hist, dmask);
 }
 
 // Workgroup d: exclusive scan of hist[d][0..num_chunks) into offsets[d][..], row total into
@@ -189,16 +189,18 @@ __device__ inline uint32_t digit_exclusive_scan(uint32_t v, uint32_t* s_wave, ui
     return wave_base + incl - v;
 }
 
-template <bool kPairs, int kBits, int kChunk>
+// KeyT: uint64_t or uint32_t keys. kPairs with vals_in == nullptr: each key's value is its input
+// position (the first pass of the tile sort, whose values are the emission positions).
+template <bool kPairs, int kBits, int kChunk, typename KeyT = uint64_t>
 __global__ __launch_bounds__(kDownThreads) void radix_downsweep_kernel(
-    const uint64_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, int64_t n,
+    const KeyT* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, int64_t n,
     const uint32_t* __restrict__ n_dev, bool drop_sentinel, int shift, uint32_t dmask, int64_t num_chunks,
-    const uint32_t* __restrict__ offsets, const uint32_t* __restrict__ totals, uint64_t* __restrict__ keys_out,
+    const uint32_t* __restrict__ offsets, const uint32_t* __restrict__ totals, KeyT* __restrict__ keys_out,
     uint32_t* __restrict__ vals_out, uint32_t* __restrict__ kept_total) {
     constexpr int kDownWaveKeys = kChunk / kDownWaves;  // keys ranked by one wave
     constexpr int kDownRounds = kDownWaveKeys / kWave;
     static_assert(kDownRounds >= 1 && kDownWaveKeys % kWave == 0, "whole rounds per wave");
-    __shared__ uint64_t s_keys[kChunk];
+    __shared__ KeyT s_keys[kChunk];
     __shared__ uint32_t s_vals[kPairs ? kChunk : 1];
     constexpr int kBins = 1 << kBits;
     static_assert(kBins <= kDownThreads, "one thread per digit");
@@ -223,20 +225,21 @@ __global__ __launch_bounds__(kDownThreads) void radix_downsweep_kernel(
     // 1. per wave: stable ranks among equal digits (rank = keys of the digit before it in this
     //    wave's eighth of the chunk), packed as digit << 16 | rank
     const uint64_t lt = lanemask_lt();
-    uint64_t key[kDownRounds];
+    KeyT key[kDownRounds];
     uint32_t val[kDownRounds];
     uint32_t dr[kDownRounds];
 #pragma unroll
     for (int r = 0; r < kDownRounds; ++r) {
         const int local = wave * kDownWaveKeys + r * kWave + lane;
         const bool valid = local < chunk_count;
-        key[r] = valid ? keys_in[base + local] : 0ull;
-        val[r] = (kPairs && valid) ? vals_in[base + local] : 0u;
+        key[r] = valid ? keys_in[base + local] : (KeyT)0;
+        if (kPairs) val[r] = vals_in == nullptr ? (uint32_t)(base + local) : (valid ? vals_in[base + local] : 0u);
+        else val[r] = 0u;
     }
 #pragma unroll
     for (int r = 0; r < kDownRounds; ++r) {
         const int local = wave * kDownWaveKeys + r * kWave + lane;
-        const bool valid = local < chunk_count && !(drop_sentinel && key[r] == kSentinelKey);
+        const bool valid = local < chunk_count && !(drop_sentinel && (uint64_t)key[r] == kSentinelKey);
         const uint32_t d = digit_of<kBits>(key[r], shift) & dmask;
         uint64_t peers = wave_ballot(valid);
 #pragma unroll
@@ -294,7 +297,7 @@ __global__ __launch_bounds__(kDownThreads) void radix_downsweep_kernel(
     // 4. write out in order: runs of one digit go to consecutive addresses
     const int kept_count = (int)s_kept;
     for (int i = threadIdx.x; i < kept_count; i += kDownThreads) {
-        const uint64_t k = s_keys[i];
+        const KeyT k = s_keys[i];
         const uint32_t d = digit_of<kBits>(k, shift) & dmask;
         const uint32_t pos = s_global[d] + ((uint32_t)i - s_local[d]);
         keys_out[pos] = k;
@@ -488,25 +491,65 @@ gsx_hip_status radix_sort_keys_u64_compacting(uint64_t* keys, uint64_t* keys_alt
                                                                          stream, first_hist_ready);
 }
 
-gsx_hip_status radix_sort_keys_u64_digits(uint64_t* keys, uint64_t* keys_alt, int64_t n, int begin_bit, int passes,
-                                         int digit_bits, void* temp, int* out_in_alt, hipStream_t stream) {
-    const int end_bit = begin_bit + passes * digit_bits;
+template <int kBits>
+gsx_hip_status tile_sort_passes(const uint32_t* tiles, uint32_t* tiles_alt, uint32_t* tiles_sorted, uint32_t* vals_alt,
+                                uint32_t* vals_sorted, int64_t n, int tile_bits, int passes, void* temp,
+                                hipStream_t stream) {
+    constexpr int kBins = 1 << kBits;
+    int64_t chunks = (n + kDigitsChunk - 1) / kDigitsChunk;
+    if (chunks < 1) chunks = 1;
+    const int64_t hist_count = chunks * kBins;
+    uint32_t* hist = static_cast<uint32_t*>(temp);
+    uint32_t* offsets = hist + hist_count;
+    uint32_t* totals = offsets + hist_count;
+    const uint32_t* kin = tiles;
+    const uint32_t* vin = nullptr;  // first pass: the values are the input positions
+    for (int k = 0; k < passes; ++k) {
+        // the last pass lands in the sorted arrays, the one before it in the alternates, ...
+        const bool to_sorted = (passes - 1 - k) % 2 == 0;
+        uint32_t* kout = to_sorted ? tiles_sorted : tiles_alt;
+        uint32_t* vout = to_sorted ? vals_sorted : vals_alt;
+        const int shift = k * kBits;
+        const int width = tile_bits - shift < kBits ? tile_bits - shift : kBits;
+        const uint32_t dmask = width > 0 ? (1u << width) - 1u : 0u;
+        hipLaunchKernelGGL((radix_upsweep_kernel<kBits, kDigitsChunk, uint32_t>), dim3((unsigned)chunks),
+                           dim3(kSortThreads), 0, stream, kin, n, nullptr, false, shift, dmask, chunks, hist);
+        hipLaunchKernelGGL(radix_rowscan_kernel, dim3(kBins), dim3(kSortThreads), 0, stream, hist, chunks, offsets,
+                           totals);
+        hipLaunchKernelGGL((radix_downsweep_kernel<true, kBits, kDigitsChunk, uint32_t>), dim3((unsigned)chunks),
+                           dim3(kDownThreads), 0, stream, kin, vin, n, nullptr, false, shift, dmask, chunks, offsets,
+                           totals, kout, vout, nullptr);
+        kin = kout;
+        vin = vout;
+    }
+    return (gsx_hip_status)hipGetLastError();
+}
+
+gsx_hip_status tile_sort_u32(const uint32_t* tiles, uint32_t* tiles_alt, uint32_t* tiles_sorted, uint32_t* vals_alt,
+                             uint32_t* vals_sorted, int64_t n, int tile_bits, int passes, int digit_bits, void* temp,
+                             hipStream_t stream) {
+    if (n < 0 || n > (int64_t)UINT32_MAX || passes < 1 || tile_bits < 0 || tile_bits > passes * digit_bits ||
+        tiles == tiles_sorted || tiles == tiles_alt) {
+        return GSX_HIP_ERROR_INVALID_ARGUMENT;
+    }
+    if (n == 0) return GSX_HIP_SUCCESS;
     switch (digit_bits) {
         case 6:
-            return radix_sort_u64<false, 6, kDigitsChunk>(keys, nullptr, keys_alt, nullptr, n, nullptr, false,
-                                                           begin_bit, end_bit, temp, out_in_alt, stream);
+            return tile_sort_passes<6>(tiles, tiles_alt, tiles_sorted, vals_alt, vals_sorted, n, tile_bits, passes, temp,
+                                       stream);
         case 7:
-            return radix_sort_u64<false, 7, kDigitsChunk>(keys, nullptr, keys_alt, nullptr, n, nullptr, false,
-                                                           begin_bit, end_bit, temp, out_in_alt, stream);
+            return tile_sort_passes<7>(tiles, tiles_alt, tiles_sorted, vals_alt, vals_sorted, n, tile_bits, passes, temp,
+                                       stream);
         case 8:
-            return radix_sort_u64<false, 8, kDigitsChunk>(keys, nullptr, keys_alt, nullptr, n, nullptr, false,
-                                                           begin_bit, end_bit, temp, out_in_alt, stream);
+            return tile_sort_passes<8>(tiles, tiles_alt, tiles_sorted, vals_alt, vals_sorted, n, tile_bits, passes, temp,
+                                       stream);
         default:
             return GSX_HIP_ERROR_INVALID_ARGUMENT;
     }
 }
 
-size_t radix_sort_keys_u64_digits_temp_bytes(int64_t n) { return radix_temp_bytes<8, kDigitsChunk>(n); }
+size_t tile_sort_u32_temp_bytes(int64_t n) { return radix_temp_bytes<8, kDigitsChunk>(n); }
+
 
 size_t radix_sort_keys_u64_compacting_temp_bytes(int64_t n) {
     return radix_temp_bytes<kCompactingRadixBits, kCompactingChunk>(n);

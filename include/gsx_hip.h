@@ -124,19 +124,19 @@ typedef struct gsx_hip_render_stats {
     int64_t visible_count;   /* Gaussians with at least one tile (-1 until computed) */
     int64_t instance_count;  /* (tile, Gaussian) pairs sorted */
     int32_t tile_count;
-    int32_t sort_passes;       /* radix passes over the instance keys (tile bits) */
+    int32_t sort_passes;       /* radix passes over the instance tiles */
     int32_t depth_sort_passes; /* radix passes over the per-Gaussian depth keys */
-    /* layout of sorted_keys: tile << key_tile_shift | emission position in the low
-     * key_payload_bits bits; instances are emitted in (depth, index) order of their Gaussians,
-     * so a stable sort on the tile bits yields the gsx per-tile (depth, index) order */
-    int32_t key_tile_shift;
-    int32_t key_payload_bits;
+    /* instances are emitted in (depth, index) order of their Gaussians and their tile indices
+     * (tile_bits bits) sorted stably with the emission positions as values, which yields the gsx
+     * per-tile (depth, index) order */
+    int32_t tile_bits;
+    int32_t sorted_tile_bytes; /* element size of sorted_tiles (4) */
 } gsx_hip_render_stats;
 
 /* Device pointers of the intermediates a forward retains (valid until the next forward). */
 typedef struct gsx_hip_render_buffers {
-    const uint64_t* sorted_keys;   /* [instance_count] see gsx_hip_render_stats for the layout */
-    const uint32_t* sorted_values; /* [instance_count] emission position of each sorted key */
+    const uint32_t* sorted_tiles;  /* [instance_count] tile index of each sorted instance */
+    const uint32_t* sorted_values; /* [instance_count] emission position of each sorted instance */
     const uint32_t* tile_ranges;   /* [tile_count][2] start, end */
     const float* records;          /* [N][8] geometry then [N][4] colour+depth blend records */
     const uint32_t* tile_counts;   /* [N] tiles touched per Gaussian (0 = culled) */

@@ -79,26 +79,28 @@ def test_sorted_keys_and_ranges_bit_exact(oracle, name):
     keys_ref, vals_ref = oracle.tile_keys(w.scene, w.camera, 16)
     assert st.instance_count == len(keys_ref)
     buf = r.buffers()
-    keys = np.empty(st.instance_count, np.uint64)
+    assert st.sorted_tile_bytes == 4
+    tile = np.empty(st.instance_count, np.uint32)
     vals = np.empty(st.instance_count, np.uint32)
     ranges = np.empty((st.tile_count, 2), np.uint32)
     lib = r.lib
     if st.instance_count:
-        lib.gsx_hip_memcpy_dtoh(keys.ctypes.data_as(ctypes.c_void_p), buf.sorted_keys, keys.nbytes)
+        lib.gsx_hip_memcpy_dtoh(tile.ctypes.data_as(ctypes.c_void_p), buf.sorted_tiles, tile.nbytes)
         lib.gsx_hip_memcpy_dtoh(vals.ctypes.data_as(ctypes.c_void_p), buf.sorted_values, vals.nbytes)
     lib.gsx_hip_memcpy_dtoh(ranges.ctypes.data_as(ctypes.c_void_p), buf.tile_ranges, ranges.nbytes)
     inst_g = np.empty(st.instance_count, np.uint32)
     if st.instance_count:
         lib.gsx_hip_memcpy_dtoh(inst_g.ctypes.data_as(ctypes.c_void_p), buf.instance_gaussian, inst_g.nbytes)
-    # sorted keys: tile << key_tile_shift | emission position (key_payload_bits bits); the
-    # oracle's keys are tile << 32 | bits(depth) with the Gaussian index as value
-    assert st.key_tile_shift == st.key_payload_bits
-    tile = keys >> np.uint64(st.key_tile_shift) if st.key_tile_shift < 64 else np.zeros_like(keys)
-    assert np.array_equal(keys & np.uint64((1 << st.key_payload_bits) - 1), vals.astype(np.uint64))
+    # sorted tiles with the emission positions as values; the oracle's keys are
+    # tile << 32 | bits(depth) with the Gaussian index as value
+    assert st.tile_bits == max(int(st.tile_count - 1).bit_length(), 0)
+    assert np.array_equal(np.sort(vals), np.arange(st.instance_count, dtype=np.uint32))  # a permutation
     assert np.array_equal(inst_g[vals], vals_ref)  # sorted values are emission positions
+    # stable: within a tile the emission positions ascend
+    assert np.all((tile[1:] != tile[:-1]) | (vals[1:] > vals[:-1]))
     depth_of = np.zeros(w.scene.count, np.uint64)
     depth_of[vals_ref] = keys_ref & np.uint64(0xFFFFFFFF)
-    assert np.array_equal((tile << np.uint64(32)) | depth_of[inst_g[vals]], keys_ref)
+    assert np.array_equal((tile.astype(np.uint64) << np.uint64(32)) | depth_of[inst_g[vals]], keys_ref)
     # emission order: each Gaussian's positions are one contiguous run, runs in (depth, index)
     # order of their Gaussians
     if st.instance_count:

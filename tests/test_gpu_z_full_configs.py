@@ -56,21 +56,19 @@ def _check_keys_and_ranges(r, scene_count, keys_ref, vals_ref, oracle):
     assert st.instance_count == len(keys_ref)
     buf = r.buffers()
     n_inst = st.instance_count
-    keys = _dtoh(r.lib, buf.sorted_keys, n_inst, np.uint64)
+    assert st.sorted_tile_bytes == 4
+    tile = _dtoh(r.lib, buf.sorted_tiles, n_inst, np.uint32)
     vals = _dtoh(r.lib, buf.sorted_values, n_inst, np.uint32)
     inst_g = _dtoh(r.lib, buf.instance_gaussian, n_inst, np.uint32)
     ranges = _dtoh(r.lib, buf.tile_ranges, 2 * st.tile_count, np.uint32).reshape(st.tile_count, 2)
-    assert st.key_tile_shift == st.key_payload_bits
-    shift = np.uint64(st.key_tile_shift)
-    assert np.array_equal(keys & np.uint64((1 << st.key_payload_bits) - 1), vals.astype(np.uint64))
     g_sorted = inst_g[vals]
+    # stable: within a tile the emission positions ascend
+    assert np.all((tile[1:] != tile[:-1]) | (vals[1:] > vals[:-1]))
     del vals
     assert np.array_equal(g_sorted, vals_ref)
     depth_of = np.zeros(scene_count, np.uint64)
     depth_of[vals_ref] = keys_ref & np.uint64(0xFFFFFFFF)
-    tile = keys >> shift
-    del keys
-    assert np.array_equal((tile << np.uint64(32)) | depth_of[g_sorted], keys_ref)
+    assert np.array_equal((tile.astype(np.uint64) << np.uint64(32)) | depth_of[g_sorted], keys_ref)
     del g_sorted
     assert np.all(tile[1:] >= tile[:-1])
     del tile
