@@ -39,26 +39,28 @@ def algorithmic_bytes(stage, geo, train=True):
     """Minimum HBM bytes of each stage in this build's data layout: every input byte read once and
     every output byte written once, however often the kernel itself touches it (the roofline
     numerators; at or below what the FETCH_SIZE / WRITE_SIZE counters show).
-    geo: n Gaussians, V visible (at least one tile), I instances, T tiles, P pixels, R entries the
+    geo: n Gaussians, Vp past the projection culls (depth-sorted), V of them with at least one
+    tile, I instances, T tiles, P pixels, R entries the
     blend must reach (per tile, up to its last contributing entry), U distinct Gaussians among
     them (the touched Gaussians) and It their instances, C transmittance checkpoints the backward
     needs (per pixel, one per 8-entry bucket up to its last contribution), S / D tile- and
     depth-sort passes."""
     n, v, i, t, p = geo["n"], geo["V"], geo["I"], geo["T"], geo["P"]
+    vp = geo["Vp"]
     r, u, c = geo["R"], geo["U"], geo["C"]
     if stage == "preprocess":
         # parameters in (SH0: 56 B), the TRAIN snapshot of them out (56 B), tile count + depth key
-        # out (12 B); per visible Gaussian its geometry + colour record (48 B) and, TRAIN, the
+        # out (12 B); per projected Gaussian its geometry + colour record (48 B) and, TRAIN, the
         # conic-gradient coefficients (32 B)
-        return (56 + (56 if train else 0) + 12) * n + (80 if train else 48) * v
+        return (56 + (56 if train else 0) + 12) * n + (80 if train else 48) * vp
     if stage == "depth_order":
-        # depth keys in; the tile counts of the visible ones gathered, their Gaussian and count
-        # out in depth order (the intermediate sort passes may stay on chip)
-        return 8 * n + 12 * v
+        # depth keys in; the tile counts of the projected ones gathered, their Gaussian and
+        # count out in depth order (the intermediate sort passes may stay on chip)
+        return 8 * n + 12 * vp
     if stage == "emit":
-        # per visible rank: count, Gaussian, geometry record in, offset and long-run entry out;
-        # per instance its tile (4 B) and its Gaussian (4 B) out
-        return 48 * v + 8 * i
+        # per depth rank: count, Gaussian in, offset out; the geometry record of each Gaussian
+        # with tiles in; per instance its tile (4 B) and its Gaussian (4 B) out
+        return 12 * vp + 32 * v + 8 * i
     if stage == "sort":
         return sort_bytes(geo["S"], i)
     if stage == "ranges":
@@ -74,9 +76,9 @@ def algorithmic_bytes(stage, geo, train=True):
         # coefficients once in; a 36-byte partial per reached entry and each tile's cut out
         return 12 * t + 20 * p + 4 * c + 8 * r + 80 * u + 36 * r
     if stage == "instance_reduce":
-        # per visible rank its Gaussian, offset and touched flag, the tiles of the touched
+        # per depth rank its Gaussian, offset and touched flag, the tiles of the touched
         # Gaussians' instances and the reached entries' partials in, 9-float screen gradients out
-        return 9 * v + 4 * geo["It"] + 36 * r + 36 * v
+        return 9 * vp + 4 * geo["It"] + 36 * r + 36 * vp
     if stage == "projection_backward":
         return (36 + 56 + 56) * n  # screen gradients + snapshot in, five parameter gradients out
     if stage == "loss_forward":
@@ -138,7 +140,8 @@ def render_geometry(lib, renderer, n, width, height):
         touched = torch.bincount(ig[vals[j]], minlength=n) > 0
         u_total = int(touched.sum())
         it_total = int(tc[touched].long().sum())
-    return {"n": n, "V": int((tc > 0).sum()), "I": i_count, "T": t_count, "P": p_count, "R": r_total,
+    return {"n": n, "Vp": int(st.visible_count), "V": int((tc > 0).sum()), "I": i_count, "T": t_count,
+            "P": p_count, "R": r_total,
             "U": u_total, "It": it_total, "C": c_total, "S": int(st.sort_passes), "D": int(st.depth_sort_passes)}
 
 
@@ -378,6 +381,8 @@ def main():
                     help="run one plain copy kernel of this size first (reference for traffic counters)")
     ap.add_argument("--cpu-baseline-iters", type=int, default=3,
                     help="reference CPU steps to time on the full workload (0 disables)")
+    ap.add_argument("--fps-steps", type=int, default=-1,
+                    help="inference renders timed for render_fps (default max(steps, 20); 0 skips them)")
     ap.add_argument("--extra-steps", type=int, default=10,
                     help="timed steps of the config 2/3/4 and density-control lines (0 disables them)")
     args = ap.parse_args()
@@ -534,16 +539,18 @@ def main():
         f"reached {geos[-1]['R']}, distinct reached {geos[-1]['U']} (last pose)")
 
     # inference forward FPS on the same scene (cycling poses)
-    fps_steps = max(args.steps, 20)
-    for i in range(3):
-        renderer.render(cams[i % args.poses], g, train=False, out_rgb=img)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(fps_steps):
-        renderer.render(cams[i % args.poses], g, train=False, out_rgb=img)
-    torch.cuda.synchronize()
-    fps = fps_steps / (time.perf_counter() - t0)
-    log(f"inference forward: {fps:.1f} FPS")
+    fps_steps = max(args.steps, 20) if args.fps_steps < 0 else args.fps_steps
+    fps = None
+    if fps_steps > 0:
+        for i in range(3):
+            renderer.render(cams[i % args.poses], g, train=False, out_rgb=img)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(fps_steps):
+            renderer.render(cams[i % args.poses], g, train=False, out_rgb=img)
+        torch.cuda.synchronize()
+        fps = fps_steps / (time.perf_counter() - t0)
+        log(f"inference forward: {fps:.1f} FPS")
 
     kernels = []
     for name, ms in stage_ms.items():
@@ -578,7 +585,7 @@ def main():
                    "instances_last_pose": instances, "visible_last_pose": visible,
                    "mean_per_step": {k: round(v, 1) for k, v in geo_mean.items()}},
         "train_its_cloned_state": round(it_s_clone, 2),
-        "render_fps": round(fps, 1),
+        "render_fps": round(fps, 1) if fps is not None else None,
         "sort_gbps": sort_entry["gbps"],
         "sort_hbm_frac": sort_entry["hbm_frac"],
         "kernels": kernels,

@@ -1005,7 +1005,14 @@ gsx_hip_status gsx_hip_render_backward(gsx_hip_render_context* ctx, const float*
 gsx_hip_status gsx_hip_render_context_get_stats(const gsx_hip_render_context* ctx, gsx_hip_render_stats* out) {
     if (ctx == nullptr || out == nullptr) return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "context/out must be non-null");
     out->gaussian_count = ctx->gaussian_count;
-    out->visible_count = -1;
+    out->visible_count = 0;
+    if (ctx->gaussian_count > 0 && ctx->counters_ready) {
+        // counters[0]: the depth sort's count of kept keys (a synchronous read)
+        uint32_t visible = 0;
+        GSX_HIP_TRY(hipMemcpy(&visible, ctx->counters.as<uint32_t>(), sizeof(visible), hipMemcpyDeviceToHost),
+                    "read visible count");
+        out->visible_count = visible;
+    }
     out->instance_count = ctx->instance_count;
     out->tile_count = ctx->tile_count_total;
     out->sort_passes = ctx->sort_passes;

@@ -121,7 +121,8 @@ typedef struct gsx_hip_render_context gsx_hip_render_context;
 
 typedef struct gsx_hip_render_stats {
     int64_t gaussian_count;
-    int64_t visible_count;   /* Gaussians with at least one tile (-1 until computed) */
+    int64_t visible_count;   /* Gaussians that pass the projection culls (depth-sorted); read
+                                from the device: get_stats waits for the context's last forward */
     int64_t instance_count;  /* (tile, Gaussian) pairs sorted */
     int32_t tile_count;
     int32_t sort_passes;       /* radix passes over the instance tiles */
