@@ -1,4 +1,5 @@
-"""The reference's own image-fit application (apps/image_fit_demo.c, unmodified) on the HIP backend.
+"""The reference's own applications (apps/*.c, unmodified) on the HIP backend: image-fit-demo,
+render-pcd, gsx-info, multi-gaussian-render, banana-optim and ssim-numerical-diff.
 
 oracle/_ref/image-fit-demo is that source compiled and linked with the reference core whose
 registry GPU slot holds the HIP backend plugin, so `--backend cuda` selects the MI355X and
@@ -71,3 +72,110 @@ def test_image_fit_demo_cpu_and_hip_backends(tmp_path):
     assert abs(curve_h[20] - curve_c[20]) <= 0.02 * curve_c[20]
     assert curve_h[100] < 0.1 * curve_h[20]
     assert final_h <= 1.5 * final_c + 1e-6
+
+
+# ---- the reference's other C apps, unmodified, on the HIP backend (registry GPU slot) ----------
+
+def _ref_app(name):
+    path = os.path.join(ROOT, "oracle", "_ref", name)
+    if not os.path.exists(path):
+        pytest.skip(f"oracle/_ref/{name} was not built (needs the reference tree at build time)")
+    return path
+
+
+def _run_app(name, args, timeout=240, cwd=None):
+    print(f"[case] {name} {' '.join(args)}", flush=True)
+    res = subprocess.run([_ref_app(name), *args], capture_output=True, text=True, timeout=timeout, cwd=cwd)
+    return res.returncode, res.stdout + res.stderr
+
+
+def test_gsx_info_lists_the_hip_device():
+    rc, out = _run_app("gsx-info", [])
+    assert rc == 0, out[-3000:]
+    print(out[-2000:], flush=True)
+    # the HIP backend fills the registry's GPU slot: one device, a runtime backend on it
+    m = re.search(r"CUDA devices: (\d+)", out)
+    assert m is not None and int(m.group(1)) >= 1, out
+    gpu_part = out[m.start():]
+    assert "Runtime backend type: CUDA" in gpu_part
+    assert "DEVICE=yes" in gpu_part and "HOST_PINNED=yes" in gpu_part
+
+
+def _write_gaussian_ply(path, n, seed):
+    """ASCII PLY with the 3DGS property names gsx_read_ply reads (gsx/src/extra/gsx-io-ply.cpp:257-268)."""
+    rng = np.random.default_rng(seed)
+    xyz = rng.uniform(-1.0, 1.0, (n, 3))
+    scale = rng.uniform(-4.5, -2.5, (n, 3))
+    opacity = rng.normal(0.0, 1.5, n)
+    rot = rng.normal(0.0, 1.0, (n, 4))
+    dc = rng.normal(0.0, 0.6, (n, 3))
+    props = ["x", "y", "z", "scale_0", "scale_1", "scale_2", "opacity", "rot_w", "rot_x", "rot_y", "rot_z",
+             "f_dc_r", "f_dc_g", "f_dc_b"]
+    cols = np.concatenate([xyz, scale, opacity[:, None], rot, dc], axis=1)
+    with open(path, "w") as f:
+        f.write("ply\nformat ascii 1.0\nelement vertex %d\n" % n)
+        for p in props:
+            f.write(f"property float {p}\n")
+        f.write("end_header\n")
+        for row in cols:
+            f.write(" ".join(f"{v:.7g}" for v in row) + "\n")
+
+
+@pytest.mark.parametrize("flann", [False, True])
+def test_render_pcd_cpu_and_hip_write_the_same_image(tmp_path, flann):
+    """apps/render_pcd.c: PLY in, INFERENCE render, PNG out. The two backends' images are
+    bit-identical, so the PNG files (same encoder, same pixels) are byte-identical; the FLANN
+    variant also recomputes scales and rotations from nearest neighbours on the host."""
+    ply = str(tmp_path / "cloud.ply")
+    _write_gaussian_ply(ply, 3000, 11)
+    common = ["--input", ply, "--width", "320", "--height", "240", "--fx", "300", "--fy", "300",
+              "--qvec", "1,0,0,0", "--tvec", "0,0,4"] + (["--flann", "--flann-knn", "8"] if flann else [])
+    outs = {}
+    for backend in ("cpu", "cuda"):
+        out_png = str(tmp_path / f"{backend}.png")
+        rc, log = _run_app("render-pcd", common + ["--backend", backend, "--output", out_png])
+        assert rc == 0, log[-3000:]
+        outs[backend] = open(out_png, "rb").read()
+    assert len(outs["cuda"]) > 100
+    assert outs["cuda"] == outs["cpu"]
+
+
+@pytest.mark.parametrize("forward_type,sh_degree", [("inference", 0), ("train", 3)])
+def test_multi_gaussian_render_matches_cpu_and_numerical_diff(tmp_path, forward_type, sh_degree):
+    """apps/multi-gaussian-render.c with its own checks: the HIP render against a CPU render of
+    the same request (max |diff|), and its numerical-difference test of the HIP backward."""
+    args = ["--backend", "cuda", "--gaussian-count", "256", "--gaussian-seed", "5", "--width", "160",
+            "--height", "120", "--sh-degree", str(sh_degree), "--forward-type", forward_type,
+            "--output", str(tmp_path / "hip.png"), "--compare-with-cpu", "true",
+            "--cpu-reference-output", str(tmp_path / "cpu.png"), "--compare-max-abs-tol", "1e-4",
+            "--numerical-diff", "true"]
+    rc, out = _run_app("multi-gaussian-render", args)
+    print(out[-2500:], flush=True)
+    assert rc == 0, out[-3000:]
+    m = re.search(r"cpu reference compare: max_abs=([0-9.eE+-]+)", out)
+    assert m is not None and float(m.group(1)) <= 1e-4
+    assert "PASSED: backward numerical diff within tolerance" in out
+
+
+def test_banana_optim_adam_on_hip():
+    """apps/banana-optim.c: Adam through gsx_optim_step on device tensors, the gradient from the
+    host each step; the HIP run follows the CPU run."""
+    res = {}
+    for backend in ("cpu", "cuda"):
+        rc, out = _run_app("banana-optim", ["--backend", backend])
+        assert rc == 0, out[-3000:]
+        m = re.search(r"result: x=([0-9.eE+-]+) y=([0-9.eE+-]+)", out)
+        assert m is not None, out[-2000:]
+        res[backend] = (float(m.group(1)), float(m.group(2)))
+    print(f"[banana] {res}", flush=True)
+    assert abs(res["cuda"][0] - res["cpu"][0]) <= 1e-5 and abs(res["cuda"][1] - res["cpu"][1]) <= 1e-5
+    assert abs(res["cuda"][0] - 1.0) < 1e-3 and abs(res["cuda"][1] - 1.0) < 1e-3
+
+
+def test_ssim_numerical_diff_on_hip():
+    """apps/ssim-numerical-diff.c: the SSIM loss backward against central differences, on the HIP
+    backend (CHW layout)."""
+    rc, out = _run_app("ssim-numerical-diff", ["--backend", "cuda", "--layout", "chw"])
+    print(out[-1500:], flush=True)
+    assert rc == 0, out[-3000:]
+    assert "PASSED" in out
