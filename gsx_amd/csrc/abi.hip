@@ -594,7 +594,9 @@ gsx_hip_status gsx_hip_render_context_set_timing(gsx_hip_render_context* ctx, in
         return fail(GSX_HIP_ERROR_OUT_OF_MEMORY, "timing ring allocation failed");
     }
     for (int i = 0; i < total; ++i) {
-        hipError_t e = hipEventCreate(&ctx->events[i]);
+        // timing only: no system-scope fence at each stage boundary (its cache writeback would be
+        // counted in the stage it follows, and would slow the next one)
+        hipError_t e = hipEventCreateWithFlags(&ctx->events[i], hipEventDisableSystemFence);
         if (e != hipSuccess) {
             for (int k = 0; k < i; ++k) (void)hipEventDestroy(ctx->events[k]);
             delete[] ctx->events;
@@ -602,7 +604,7 @@ gsx_hip_status gsx_hip_render_context_set_timing(gsx_hip_render_context* ctx, in
             ctx->ring = 0;
             release_events(ctx);
             ctx->timing = false;
-            return hip_fail(e, "hipEventCreate");
+            return hip_fail(e, "hipEventCreateWithFlags");
         }
     }
     ctx->ring = capacity;
