@@ -167,7 +167,13 @@ enum {
  * adds 1 to it for every visible Gaussian (gsx-cpu/render.c:980-982). The Gaussian arrays are
  * borrowed for the call. One host synchronisation per forward reads the instance count (the GPU
  * keeps working on the depth order meanwhile); a count above 2^32 - 1 (tile, Gaussian)
- * instances fails with GSX_HIP_ERROR_OUT_OF_RANGE before anything is emitted. */
+ * instances fails with GSX_HIP_ERROR_OUT_OF_RANGE before anything is emitted.
+ * Precondition: finite inputs (Gaussian fields, and grad_rgb in the backward). The blend kernels
+ * evaluate an entry for the 64 pixels of a wave at once, and a pixel that does not take it adds
+ * 0 x its colour (or its gradient term): with finite values that changes nothing, but a
+ * non-finite colour or image gradient then turns the other pixels of those waves into NaN as
+ * well, where the CPU backend leaves them finite. Every pixel the CPU renders finite and this
+ * build renders finite is bit-identical. */
 gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* context, const gsx_hip_camera* camera,
                                       const gsx_hip_gaussians* gaussians, int32_t forward_type, float* out_rgb,
                                       float* visible_counter, hipStream_t stream);

@@ -67,6 +67,32 @@ def test_forward_image_bit_exact(oracle, name):
     assert np.array_equal(t.cpu().numpy().reshape(ref_t.shape), ref_t)
 
 
+def test_nonfinite_colour_stays_non_finite_and_the_rest_bit_exact(oracle):
+    """The finite-input precondition of gsx_hip_render_forward: Gaussians with an infinite SH0
+    colour make the CPU's pixels that take them infinite; the blend kernels may also turn other
+    pixels of the waves that evaluate them into NaN. Every pixel the CPU renders non-finite is
+    non-finite here, and every pixel finite here equals the CPU's bit for bit."""
+    from gsx_amd import scenes
+    w = _workloads()["c0_small"]()
+    fields = [np.array(a, copy=True) for a in (w.scene.mean3d, w.scene.rotation, w.scene.logscale, w.scene.opacity,
+                                               w.scene.sh0)]
+    rng = np.random.default_rng(9)
+    hot = rng.choice(w.scene.count, 6, replace=False)
+    fields[4][hot] = np.inf
+    sc = scenes.Scene(*fields)
+    print(f"[case] non-finite colour, Gaussians {hot.tolist()}", flush=True)
+    r, cam, g = _setup(scenes.Workload("nonfinite", sc, w.camera))
+    img = r.render(cam, g, train=False)
+    torch.cuda.synchronize()
+    ref, _ = oracle.render(sc, w.camera)
+    got = img.cpu().numpy()
+    assert (~np.isfinite(ref)).any()  # the case is exercised
+    assert np.all(~np.isfinite(got)[~np.isfinite(ref)])
+    fin = np.isfinite(got)
+    assert np.array_equal(got[fin], ref[fin])
+    print(f"[nonfinite] CPU {int((~np.isfinite(ref)).sum())} pixels, HIP {int((~fin).sum())}", flush=True)
+
+
 @pytest.mark.parametrize("name", ["c0_small", "c3_small", "c4_small", "c3_1080", "ties"])
 def test_sorted_keys_and_ranges_bit_exact(oracle, name):
     import ctypes
