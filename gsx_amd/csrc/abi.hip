@@ -61,10 +61,20 @@ __global__ __launch_bounds__(256) void train_state_kernel(StateArrays a, uint32_
         const int64_t n4 = n / 4;
         const uint4* l4 = reinterpret_cast<const uint4*>(live);
         const uint4* s4 = reinterpret_cast<const uint4*>(snap);
-        for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
-            const uint4 v = l4[i];
-            const uint4 w = s4[i];
-            diff |= (v.x != w.x) | (v.y != w.y) | (v.z != w.z) | (v.w != w.w);
+        // four 16-byte pairs per thread and round, all loads issued before the first compare
+        // (positions past the end re-read the last vector, which cannot differ from itself)
+        constexpr int kRound = 4;
+        for (int64_t i0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i0 < n4; i0 += kRound * stride) {
+            uint4 v[kRound], w[kRound];
+#pragma unroll
+            for (int u = 0; u < kRound; ++u) {
+                const int64_t i = min(i0 + u * stride, n4 - 1);
+                v[u] = l4[i];
+                w[u] = s4[i];
+            }
+#pragma unroll
+            for (int u = 0; u < kRound; ++u)
+                diff |= (v[u].x != w[u].x) | (v[u].y != w[u].y) | (v[u].z != w[u].z) | (v[u].w != w[u].w);
         }
         for (int64_t i = n4 * 4 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
             diff |= __float_as_uint(live[i]) != __float_as_uint(snap[i]);
