@@ -314,6 +314,7 @@ def extra_workloads(lib, steps):
                              "sort_ms": round(stage["sort"], 3),
                              "sort_gbps": round(moved / (stage["sort"] * 1e-3) / 1e9, 1),
                              "sort_hbm_frac": round(moved / (stage["sort"] * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+                             "sort_gkeys_s": round(inst / (stage["sort"] * 1e-3) / 1e9, 2),
                              "stage_ms": {k: round(v, 3) for k, v in stage.items()}}
     del g, step, r, inputs, w
     log(f"config 4: {out['c4_sort_stress']}")
@@ -588,6 +589,8 @@ def main():
         "render_fps": round(fps, 1) if fps is not None else None,
         "sort_gbps": sort_entry["gbps"],
         "sort_hbm_frac": sort_entry["hbm_frac"],
+        # sorted (tile, position) pairs per second over the same steps
+        "sort_gkeys_s": round(geo_mean["I"] / (sort_entry["ms"] * 1e-3) / 1e9, 2),
         "kernels": kernels,
         "roofline": {"bound": "hbm", "kernel": STAGE_KERNEL.get(dominant["stage"], dominant["stage"]),
                      "achieved": dominant["gbps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
