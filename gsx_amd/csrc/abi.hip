@@ -183,8 +183,6 @@ struct PinnedBuffer {
     }
 };
 
-// Workgroups of the big-box passes (grid-stride over the list of big boxes).
-constexpr unsigned kBigBlocks = 512;
 // Workgroups of the long-run reduction (4 waves each, each wave 64 list entries at a time): for
 // chunk 0, which every long run has, and per later chunk.
 constexpr unsigned kLongRunBlocks0 = 1024;
@@ -259,10 +257,10 @@ int bits_for(uint32_t v) {
 struct gsx_hip_render_context {
     DeviceBuffer rec, cov_coef, ckpt, inst_gauss, inst_tile, tiles_alt, tiles_sorted, vals_alt, vals, tile_cut, touched,
         inst_grad, tile_count, big_list, offsets, scan_temp, sort_temp, ranges, sorted_g, final_t, last, grad2d,
-        depth_keys, depth_keys_alt, rank_g, rank_count, g_rank, long_list, multi_list, counters, big_chunk_counts,
+        depth_keys, depth_keys_alt, rank_g, rank_count, g_rank, long_list, multi_list, counters,
         depth_sort_temp;
-    // partial instance counts written by the counting kernels (preprocess: one u32 per workgroup;
-    // big boxes: one u64 per workgroup), summed on the host after count_ev
+    // partial instance counts written by preprocess (one u64 per workgroup), summed on the host
+    // after count_ev
     PinnedBuffer kept_parts;
     hipEvent_t count_ev = nullptr;
     // Retained TRAIN state (gsx-cpu/render.c:263-380): the Gaussian fields as the forward read
@@ -573,7 +571,7 @@ gsx_hip_status gsx_hip_render_context_destroy(gsx_hip_render_context* ctx) {
                            &ctx->sort_temp,  &ctx->ranges,
                            &ctx->sorted_g,   &ctx->final_t,  &ctx->last,      &ctx->grad2d,     &ctx->depth_keys,
                            &ctx->depth_keys_alt, &ctx->rank_g, &ctx->rank_count, &ctx->g_rank,
-                           &ctx->long_list, &ctx->multi_list, &ctx->counters, &ctx->big_chunk_counts,
+                           &ctx->long_list, &ctx->multi_list, &ctx->counters,
                            &ctx->depth_sort_temp, &ctx->snap, &ctx->refresh_rgb};
     for (DeviceBuffer* b : all) b->release();
     ctx->kept_parts.release();
@@ -694,7 +692,6 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     GSX_TRY(ctx->tile_count.reserve(n1 * sizeof(uint32_t), "tile_count"));
     GSX_TRY(ctx->counters.reserve(8 * sizeof(uint32_t), "counters"));
     GSX_TRY(ctx->big_list.reserve(n1 * sizeof(uint32_t), "big_list"));
-    GSX_TRY(ctx->big_chunk_counts.reserve(n1 * kBigChunks * sizeof(uint32_t), "big_chunk_counts"));
     GSX_TRY(ctx->offsets.reserve((size_t)(n + 1) * sizeof(uint32_t), "offsets"));
     // per 256-rank workgroup: its tile-count sum, then its long-run count (two scanned arrays)
     GSX_TRY(ctx->scan_temp.reserve(2 * ((size_t)blocks_for(n, 256) + 1) * sizeof(uint32_t), "rank_block_sums"));
@@ -710,15 +707,8 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     GSX_TRY(ctx->final_t.reserve((size_t)pixels * sizeof(float), "final_t"));
     GSX_TRY(ctx->last.reserve((size_t)pixels * sizeof(uint32_t), "last"));
     uint32_t* counters = ctx->counters.as<uint32_t>();
-    // big boxes: chunks of at least 1024 tiles, at most kBigChunks per box (a box has at most
-    // `tiles` tiles)
-    const uint32_t big_chunk =
-        std::max<uint32_t>(1024u, ((uint32_t)(tiles + (int)kBigChunks - 1) / kBigChunks + 255u) / 256u * 256u);
-    const unsigned big_chunks = (unsigned)std::max<uint32_t>(1u, ((uint32_t)tiles + big_chunk - 1) / big_chunk);
     const unsigned pre_blocks = blocks_for(n, 256);
-    const size_t big_parts_at = ((size_t)pre_blocks * sizeof(uint32_t) + 7u) / 8u * 8u;
-    const size_t big_parts = (size_t)kBigBlocks * big_chunks;
-    GSX_TRY(ctx->kept_parts.reserve(big_parts_at + big_parts * sizeof(unsigned long long), "kept_parts"));
+    GSX_TRY(ctx->kept_parts.reserve((size_t)pre_blocks * sizeof(unsigned long long), "kept_parts"));
     uint32_t* big_count = counters + 2 + ctx->big_slot;
 
     // depth keys of the visible Gaussians: (bits(depth) - bits(near)) << index_bits | index (see
@@ -764,20 +754,12 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
                            ctx->tile_count.as<uint32_t>(), train ? visible_counter : nullptr,
                            ctx->big_list.as<uint32_t>(), big_count, counters + 1, counters + 2 + (ctx->big_slot ^ 1),
                            counters + 4,
-                           static_cast<uint32_t*>(ctx->kept_parts.dev), ctx->depth_keys.as<uint64_t>(), near_bits,
+                           static_cast<unsigned long long*>(ctx->kept_parts.dev), ctx->depth_keys.as<uint64_t>(),
+                           near_bits,
                            depth_max, index_bits, big_flag ? kBigKeyFlag : 0ull,
                            train ? ctx->touched.as<uint8_t>() : nullptr);
         GSX_HIP_TRY(hipGetLastError(), "preprocess_kernel");
         ctx->big_slot ^= 1;  // the slot this preprocess cleared
-        const uint32_t big_blocks = kBigBlocks * big_chunks;
-        const int64_t depth_chunks = (n + kCompactingChunk - 1) / kCompactingChunk;
-        hipLaunchKernelGGL(big_count_upsweep_kernel, dim3(big_blocks + (unsigned)depth_chunks), dim3(256), 0, stream,
-                           ctx->big_list.as<uint32_t>(), big_count, ctx->rec.as<float4>(), cam.tiles_x, big_chunk,
-                           kBigBlocks, big_blocks, ctx->tile_count.as<uint32_t>(), ctx->big_chunk_counts.as<uint32_t>(),
-                           reinterpret_cast<unsigned long long*>(static_cast<char*>(ctx->kept_parts.dev) + big_parts_at),
-                           ctx->depth_keys.as<uint64_t>(), n, index_bits, depth_chunks,
-                           static_cast<uint32_t*>(ctx->depth_sort_temp.ptr));
-        GSX_HIP_TRY(hipGetLastError(), "big_count_upsweep_kernel");
     }
     // the counting kernels leave the instance count as per-workgroup partials in host memory;
     // the depth order and the count scan are queued behind them, so the GPU keeps working while
@@ -790,7 +772,7 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
         int depth_in_alt = 0;
         GSX_TRY(radix_sort_keys_u64_compacting(ctx->depth_keys.as<uint64_t>(), ctx->depth_keys_alt.as<uint64_t>(), n,
                                                counters, index_bits, depth_end_bit, ctx->depth_sort_temp.ptr,
-                                               &depth_in_alt, stream, true));
+                                               &depth_in_alt, stream, false));
         if (depth_in_alt) sorted_depth = ctx->depth_keys_alt.as<uint64_t>();
         hipLaunchKernelGGL(rank_gather_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, n, counters,
                            sorted_depth, (uint64_t)((1ull << index_bits) - 1ull), big_flag,
@@ -804,13 +786,13 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     }
     GSX_TRY(record(ctx, 2, stream));
     GSX_HIP_TRY(hipEventSynchronize(ctx->count_ev), "instance count sync");
-    unsigned long long total = 0;
+    unsigned long long total = 0, big_total = 0;
     if (n > 0) {
-        const uint32_t* pre = static_cast<const uint32_t*>(ctx->kept_parts.host);
-        const unsigned long long* big =
-            reinterpret_cast<const unsigned long long*>(static_cast<const char*>(ctx->kept_parts.host) + big_parts_at);
-        for (unsigned b = 0; b < pre_blocks; ++b) total += pre[b];
-        for (size_t b = 0; b < big_parts; ++b) total += big[b];
+        const unsigned long long* pre = static_cast<const unsigned long long*>(ctx->kept_parts.host);
+        for (unsigned b = 0; b < pre_blocks; ++b) {
+            total += pre[b] & ((1ull << kKeptPartBigShift) - 1ull);
+            big_total += pre[b] >> kKeptPartBigShift;
+        }
     }
     if (total > (unsigned long long)UINT32_MAX) {
         // positions, offsets and the sort run in 32 bits; nothing has been emitted yet
@@ -835,12 +817,12 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
                                   "checkpoints"));
     }
     if (n > 0) {
-        const uint32_t big_blocks = kBigBlocks * big_chunks;
+        // one wave per big box
+        const uint32_t big_blocks = (uint32_t)((big_total + kWavesPerBlock - 1) / kWavesPerBlock);
         hipLaunchKernelGGL(emit_kernel, dim3(big_blocks + pre_blocks), dim3(256), 0, stream, n, ctx->rec.as<float4>(),
                            ctx->rank_g.as<uint32_t>(), ctx->rank_count.as<uint32_t>(), ctx->scan_temp.as<uint32_t>(),
                            ctx->offsets.as<uint32_t>(), cam.tiles_x, ctx->big_list.as<uint32_t>(), big_count,
-                           kBigBlocks, big_blocks, big_chunk, ctx->big_chunk_counts.as<uint32_t>(),
-                           ctx->g_rank.as<uint32_t>(), ctx->inst_gauss.as<uint32_t>(), ctx->inst_tile.as<uint32_t>(),
+                           big_blocks, ctx->g_rank.as<uint32_t>(), ctx->inst_gauss.as<uint32_t>(), ctx->inst_tile.as<uint32_t>(),
                            ctx->scan_temp.as<uint32_t>() + pre_blocks + 1, ctx->long_list.as<uint32_t>());
         GSX_HIP_TRY(hipGetLastError(), "emit_kernel");
     }

@@ -29,21 +29,22 @@ constexpr int kBlendThreads = kTilePixels;  // 256: one pixel per thread, 4 wave
 // plus the tile count of the box and, for TRAIN forwards, visible_counter += 1 (:980-982).
 // ---------------------------------------------------------------------------------------------
 // ---------------------------------------------------------------------------------------------
-// Kept tiles (tile_cull.h). The tiles of the boxes of a wave's 64 Gaussians are walked as one
-// flattened sequence, 64 (Gaussian, tile) pairs per step, so lanes stay busy whatever the box
-// sizes (a near-plane Gaussian can cover the whole image, most cover a handful of tiles). Each
-// lane's box lives in LDS; a lane finds the owner of its pair by binary search over the wave's
-// exclusive prefix of box sizes. Owners occupy contiguous lanes of a step, so ranks among kept
-// pairs come from one ballot; per-owner running counts live in LDS (LDS operations of one wave
-// complete in order).
+// Kept tiles (tile_cull.h): each tile row of a box keeps one contiguous run of tiles, given in
+// closed form by the row's band columns. A wave walks the rows of its 64 Gaussians' boxes as one
+// flattened sequence, 64 (Gaussian, row) items per step, so lanes stay busy whatever the box
+// heights (a near-plane Gaussian's box can span the whole image, most span a row or two). Each
+// lane's span constants live in LDS; a lane finds the owner of its item from the wave's
+// exclusive prefix of row counts (marks at the lanes where a box's rows start, and a prefix
+// maximum over the lanes). Counting adds each run's length to its owner's count; emission writes
+// the runs of a step, 64 instances per sub-step, with a second owner search over the runs.
 // ---------------------------------------------------------------------------------------------
 constexpr int kWavesPerBlock = 4;
-// Boxes of more tiles than this are walked by a whole workgroup in a pass of their own (see
-// big_tiles_block): a wave holding a full-image box would otherwise serialise hundreds of steps.
-// Below it the wave walk is the faster one (no workgroup barriers per step), and scenes can hold
-// millions of boxes of a few hundred tiles.
+// Boxes of more tiles than this are emitted by a wave of their own (big_box_wave): in depth order
+// the near, large boxes are neighbours, and a wave holding many full-image boxes would serialise
+// their instances. Counting walks every box in the waves (rows are few).
 constexpr uint32_t kBigTiles = 1024;
-static_assert(kBigTiles <= 1024, "the tile walk divides indices below 2^10 by box widths of at most 2^10");
+// preprocess's per-workgroup partials: kept tiles in bits 0..47, big boxes from bit 48
+constexpr int kKeptPartBigShift = 48;
 
 // Sort keys. Gaussians are first sorted by depth: key = (bits(depth) - bits(near)) << index_bits
 // | index (visible depths lie in [near, far], where positive floats order like their bit
@@ -58,22 +59,38 @@ __device__ inline uint32_t box_tiles(float4 geo1) {
     return ((bx >> 16) / kTile - (bx & 0xffffu) / kTile + 1) * ((by >> 16) / kTile - (by & 0xffffu) / kTile + 1);
 }
 
-// k / d for k < 2^24 and 1 <= d from a float reciprocal, corrected to the exact quotient.
-__device__ inline uint32_t div_small(uint32_t k, uint32_t d, float rd) {
-    uint32_t q = (uint32_t)((float)k * rd);
-    if (q * d > k) q -= 1;
-    if ((q + 1) * d <= k) q += 1;
-    return q;
+// The Gaussian's span constants from its geometry record (the record holds 2 * inv_b; halving
+// is exact), as every pass that tests tiles forms them.
+__device__ inline gsx_tile_span span_of(float4 r0, float4 r1) {
+    const uint32_t bx = __float_as_uint(r1.z), by = __float_as_uint(r1.w);
+    return gsx_tile_span_make(r0.x, r0.y, r0.z, r0.w * 0.5f, r1.x, r1.y, (int)(bx & 0xffffu), (int)(bx >> 16),
+                              (int)(by & 0xffffu), (int)(by >> 16));
 }
 
-struct WaveBoxes {
-    gsx_tile_conic conic[kWave];
-    uint32_t mdiv[kWave];  // ceil(2^20 / wx): row of flattened index k (< 1024) = (k * mdiv) >> 20
-    int32_t x0[kWave], x1[kWave], y0[kWave], y1[kWave];
-    uint32_t tx0[kWave], ty0[kWave], wx[kWave], excl[kWave], kept[kWave], out[kWave];
-    uint32_t g[kWave];
-    uint32_t mark[kWave];  // walk step: base + owner at the lane where that owner's pairs start
-    uint32_t full[kWave];  // nonzero: every tile of the box is kept (no tile test needed)
+// Kept run of tile row ty of a box: len tiles from tile0 (len = 0 when none).
+__device__ inline void row_run(const gsx_tile_span& k, uint32_t bx, uint32_t by, int ty, int32_t tiles_x,
+                               uint32_t& len, uint32_t& tile0) {
+    const int x0 = (int)(bx & 0xffffu), x1 = (int)(bx >> 16), y0 = (int)(by & 0xffffu), y1 = (int)(by >> 16);
+    const int py0 = max(ty * kTile, y0), py1 = min(ty * kTile + kTile - 1, y1);
+    int xa, xb;
+    gsx_tile_band_columns(&k, x0, x1, py0, py1, &xa, &xb);
+    len = 0u;
+    tile0 = 0u;
+    if (xa <= xb) {
+        len = (uint32_t)(xb / kTile - xa / kTile + 1);
+        tile0 = (uint32_t)ty * (uint32_t)tiles_x + (uint32_t)(xa / kTile);
+    }
+}
+
+struct WaveSpans {
+    float mx[kWave], my[kWave], b[kWave], ra[kWave], det[kWave], vr[kWave], aqs[kWave];  // gsx_tile_span
+    uint32_t bx[kWave], by[kWave];  // box: x0 | x1 << 16, y0 | y1 << 16
+    uint32_t excl[kWave];           // exclusive prefix of the lanes' row counts
+    uint32_t mark[kWave];           // walk step: base + owner at the lane where that owner's rows start
+    uint32_t kept[kWave];           // counting: kept tiles of the lane's box
+    uint32_t base[kWave], g[kWave];  // emission: position of the lane's first instance less the walked
+                                     // instances of the lanes before it; its Gaussian
+    uint32_t run_tile[kWave], run_pos[kWave], run_g[kWave], mark2[kWave];  // emission: a step's runs
 };
 
 // Inclusive prefix maximum over the 64 lanes of a wave (DPP row shifts, then the two row
@@ -88,105 +105,113 @@ __device__ inline int wave_inclusive_max(int v) {
     return v;
 }
 
-// Stores lane's box (zero tiles when !valid) and returns the wave's total tile count.
-// full: every tile of the box is known to be kept (its kept count equals its tile count).
-__device__ inline uint32_t stage_box(WaveBoxes& w, bool valid, float4 r0, float4 r1, uint32_t g, uint32_t out,
-                                     bool full) {
-    const uint32_t lane = __lane_id();
-    uint32_t total = 0;
-    if (valid) {
-        const uint32_t bx = __float_as_uint(r1.z), by = __float_as_uint(r1.w);
-        const int x0 = (int)(bx & 0xffffu), x1 = (int)(bx >> 16), y0 = (int)(by & 0xffffu), y1 = (int)(by >> 16);
-        // the record holds 2 * inv_b (halving is exact)
-        w.conic[lane] = gsx_tile_conic_make(r0.x, r0.y, r0.z, r0.w * 0.5f, r1.x, r1.y);
-        w.x0[lane] = x0;
-        w.x1[lane] = x1;
-        w.y0[lane] = y0;
-        w.y1[lane] = y1;
-        w.tx0[lane] = (uint32_t)x0 / kTile;
-        w.ty0[lane] = (uint32_t)y0 / kTile;
-        w.wx[lane] = (uint32_t)x1 / kTile - (uint32_t)x0 / kTile + 1;
-        w.mdiv[lane] = 1048575u / w.wx[lane] + 1u;
-        total = w.wx[lane] * ((uint32_t)y1 / kTile - (uint32_t)y0 / kTile + 1);
-    }
-    w.g[lane] = g;
-    w.out[lane] = out;
-    w.full[lane] = valid && full ? 1u : 0u;
-    w.kept[lane] = 0;
-    // inclusive wave scan of the box sizes
-    uint32_t incl = total;
-#pragma unroll
-    for (int d = 1; d < kWave; d <<= 1) {
-        const uint32_t t = (uint32_t)__shfl_up((int)incl, d, kWave);
-        if ((int)lane >= d) incl += t;
-    }
-    w.excl[lane] = incl - total;
-    __builtin_amdgcn_wave_barrier();
-    return (uint32_t)__shfl((int)incl, kWave - 1, kWave);
+// Inclusive prefix sum over the 64 lanes of a wave, the same DPP pattern; every lane must be
+// active.
+__device__ inline uint32_t wave_inclusive_sum_u32(uint32_t v) {
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf, true);
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf, true);
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xf, true);
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xf, 0xf, true);
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false);
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false);
+    return v;
 }
 
-// Walks the wave's flattened tiles. kEmit: writes kept instances (instance_tile,
-// instance_gaussian) at position out[owner] + rank; always accumulates kept[owner].
-template <bool kEmit>
-__device__ inline void walk_wave_tiles(WaveBoxes& w, uint32_t wave_total, int32_t tiles_x,
-                                       uint32_t* __restrict__ instance_gaussian, uint32_t* __restrict__ instance_tile) {
+// Stores lane's span constants and box (no rows when !valid) and returns the wave's total row
+// count.
+__device__ inline uint32_t stage_spans(WaveSpans& w, bool valid, float4 r0, float4 r1) {
     const uint32_t lane = __lane_id();
-    const uint64_t lt = lanemask_lt();
-    // the owner of pair p is the last box starting at or before p, i.e. the last non-empty one
-    // (an empty box shares its start with the next box): each non-empty box whose pairs start in
+    uint32_t rows = 0;
+    if (valid) {
+        const gsx_tile_span k = span_of(r0, r1);
+        const uint32_t bx = __float_as_uint(r1.z), by = __float_as_uint(r1.w);
+        w.mx[lane] = k.mx;
+        w.my[lane] = k.my;
+        w.b[lane] = k.b;
+        w.ra[lane] = k.ra;
+        w.det[lane] = k.det;
+        w.vr[lane] = k.vr;
+        w.aqs[lane] = k.aqs;
+        w.bx[lane] = bx;
+        w.by[lane] = by;
+        rows = (by >> 16) / kTile - (by & 0xffffu) / kTile + 1;
+    }
+    w.kept[lane] = 0;
+    const uint32_t incl = wave_inclusive_sum_u32(rows);
+    w.excl[lane] = incl - rows;
+    wave_lds_sync();
+    return (uint32_t)__builtin_amdgcn_readlane((int)incl, kWave - 1);
+}
+
+// Walks the wave's flattened rows. kEmit = false adds each row's kept tiles to kept[owner];
+// kEmit = true writes the kept instances (instance_tile, instance_gaussian) of every row, the
+// rows of a box in order, at base[owner] + the instances of the walked rows before it.
+template <bool kEmit>
+__device__ inline void walk_wave_rows(WaveSpans& w, uint32_t wave_rows, int32_t tiles_x,
+                                      uint32_t* __restrict__ instance_gaussian, uint32_t* __restrict__ instance_tile) {
+    const uint32_t lane = __lane_id();
+    // the owner of item p is the last box starting at or before p, i.e. the last non-empty one
+    // (an empty box shares its start with the next box): each non-empty box whose rows start in
     // the step marks that lane with base + its lane, and a prefix maximum over the lanes, carried
     // from step to step, names every lane's owner (marks of earlier steps fall below base)
     const uint32_t my_start = w.excl[lane];
-    const uint32_t my_count = (lane + 1 < kWave ? w.excl[lane + 1] : wave_total) - my_start;
+    const uint32_t my_count = (lane + 1 < kWave ? w.excl[lane + 1] : wave_rows) - my_start;
     w.mark[lane] = UINT32_MAX;
-    uint32_t carry = 0;
-    for (uint32_t base = 0; base < wave_total; base += kWave) {
+    uint32_t carry = 0, walked = 0;
+    for (uint32_t base = 0; base < wave_rows; base += kWave) {
         const uint32_t p = base + lane;
-        const bool active = p < wave_total;
         wave_lds_sync();  // the previous step's reads of the marks are done
         if (my_count > 0 && my_start - base < (uint32_t)kWave) w.mark[my_start - base] = base + lane;
         wave_lds_sync();
         const uint32_t m = w.mark[lane] - base;
         const uint32_t owner = max(carry, (uint32_t)wave_inclusive_max(m < (uint32_t)kWave ? (int)m : 0));
         carry = (uint32_t)__builtin_amdgcn_readlane((int)owner, kWave - 1);
-        bool keep = false;
-        uint32_t tile = 0;
-        if (active) {
-            const uint32_t k = p - w.excl[owner];
-            const uint32_t wx = w.wx[owner];
-            // exact when k * wx < 2^20 (Granlund-Montgomery: m = ceil(2^20 / wx) overshoots k / wx
-            // by k (m wx - 2^20) / (wx 2^20) < k / 2^20 < 1 / wx); the walked boxes have at most
-            // kBigTiles = 1024 tiles, so k < 1024 and wx <= 1024, and k * m < 2^30
-            const uint32_t row = (k * w.mdiv[owner]) >> 20;
-            const uint32_t ty = w.ty0[owner] + row;
-            const uint32_t tx = w.tx0[owner] + (k - row * wx);
-            tile = ty * (uint32_t)tiles_x + tx;
-            keep = true;
-            if (!kEmit || w.full[owner] == 0u) {  // skipped by the wave when every lane's box is full
-                const int px0 = max((int)tx * kTile, w.x0[owner]);
-                const int px1 = min((int)tx * kTile + kTile - 1, w.x1[owner]);
-                const int py0 = max((int)ty * kTile, w.y0[owner]);
-                const int py1 = min((int)ty * kTile + kTile - 1, w.y1[owner]);
-                const gsx_tile_conic con = w.conic[owner];
-                keep = gsx_tile_conic_test(&con, px0, px1, py0, py1) != 0;
+        uint32_t len = 0, tile0 = 0;
+        if (p < wave_rows) {
+            gsx_tile_span k;
+            k.mx = w.mx[owner];
+            k.my = w.my[owner];
+            k.b = w.b[owner];
+            k.ra = w.ra[owner];
+            k.det = w.det[owner];
+            k.vr = w.vr[owner];
+            k.aqs = w.aqs[owner];
+            const uint32_t by = w.by[owner];
+            const int ty = (int)((by & 0xffffu) / kTile + (p - w.excl[owner]));
+            row_run(k, w.bx[owner], by, ty, tiles_x, len, tile0);
+        }
+        if (!kEmit) {
+            if (len > 0) atomicAdd(&w.kept[owner], len);
+        } else {
+            // the step's runs, numbered q = start2 .. start2 + len - 1 in row order: run r holds
+            // position run_pos[r] + q and tile run_tile[r] + q
+            const uint32_t incl = wave_inclusive_sum_u32(len);
+            const uint32_t start2 = incl - len;
+            const uint32_t total2 = (uint32_t)__builtin_amdgcn_readlane((int)incl, kWave - 1);
+            w.run_tile[lane] = tile0 - start2;
+            w.run_pos[lane] = w.base[owner] + walked;
+            w.run_g[lane] = w.g[owner];
+            w.mark2[lane] = UINT32_MAX;
+            uint32_t carry2 = 0;
+            for (uint32_t base2 = 0; base2 < total2; base2 += kWave) {
+                const uint32_t q = base2 + lane;
+                wave_lds_sync();  // the run records are stored, the previous sub-step's marks read
+                if (len > 0 && start2 - base2 < (uint32_t)kWave) w.mark2[start2 - base2] = base2 + lane;
+                wave_lds_sync();
+                const uint32_t m2 = w.mark2[lane] - base2;
+                const uint32_t run = max(carry2, (uint32_t)wave_inclusive_max(m2 < (uint32_t)kWave ? (int)m2 : 0));
+                carry2 = (uint32_t)__builtin_amdgcn_readlane((int)run, kWave - 1);
+                if (q < total2) {
+                    const uint32_t pos = w.run_pos[run] + q;
+                    instance_gaussian[pos] = w.run_g[run];
+                    instance_tile[pos] = w.run_tile[run] + q;
+                }
             }
+            walked += total2;
         }
-        const uint64_t mask = wave_ballot(keep);
-        // first lane of this step holding the owner's pairs
-        const uint32_t seg_first = w.excl[owner] > base ? w.excl[owner] - base : 0u;
-        const uint64_t seg = ~((seg_first == 0 ? 0ull : (~0ull >> (64 - seg_first))));
-        const uint32_t before = w.kept[owner];
-        if (kEmit && keep) {
-            const uint32_t pos = w.out[owner] + before + (uint32_t)__popcll(mask & lt & seg);
-            instance_gaussian[pos] = w.g[owner];
-            instance_tile[pos] = tile;
-        }
-        // the last lane of each owner segment advances that owner's running count
-        const uint32_t next_owner = (uint32_t)__shfl_down((int)owner, 1, kWave);
-        const bool seg_last = active && (lane == kWave - 1 || p + 1 >= wave_total || next_owner != owner);
-        if (seg_last) w.kept[owner] = before + (uint32_t)__popcll(mask & (lt | (1ull << lane)) & seg);
         __builtin_amdgcn_wave_barrier();
     }
+    wave_lds_sync();
 }
 
 // Destination of the retained TRAIN state: each field array copied as the forward reads it
@@ -207,12 +232,12 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
     uint32_t* __restrict__ tile_count,
     float* __restrict__ visible_counter, uint32_t* __restrict__ big_list, uint32_t* __restrict__ big_count,
     uint32_t* __restrict__ clear0, uint32_t* __restrict__ clear1, uint32_t* __restrict__ clear2,
-    uint32_t* __restrict__ kept_part,
+    unsigned long long* __restrict__ kept_part,
     uint64_t* __restrict__ depth_keys, uint32_t depth_base, uint32_t depth_max, int index_bits,
     uint64_t big_key_flag, uint8_t* __restrict__ touched) {
-    __shared__ WaveBoxes s_boxes[kWavesPerBlock];
-    __shared__ uint32_t s_kept[kWavesPerBlock];
-    WaveBoxes& wb = s_boxes[threadIdx.x / kWave];
+    __shared__ WaveSpans s_spans[kWavesPerBlock];
+    __shared__ uint32_t s_kept[kWavesPerBlock], s_big[kWavesPerBlock];
+    WaveSpans& ws = s_spans[threadIdx.x / kWave];
     const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     // counters that later kernels accumulate into start at zero (plain stores, no fill launch)
     if (blockIdx.x == 0 && threadIdx.x == 0) {
@@ -277,27 +302,35 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
         }
         depth_keys[g] = key;
     }
-    // counted by big_tiles_block; one atomic per wave (a scene can hold millions of big boxes)
+    // emitted by big_box_wave; one atomic per wave (a scene can hold millions of big boxes)
     const uint32_t big_slot = wave_append_slot(big_count, big);
     if (big) big_list[big_slot] = (uint32_t)g;
-    const uint32_t total = stage_box(wb, visible && !big, r0, r1, (uint32_t)g, 0u, false);
-    walk_wave_tiles<false>(wb, total, cam.tiles_x, nullptr, nullptr);
-    const uint32_t kept = big ? 0u : wb.kept[__lane_id()];  // big boxes: counted by big_tiles_kernel
+    const uint32_t rows = stage_spans(ws, visible, r0, r1);
+    walk_wave_rows<false>(ws, rows, cam.tiles_x, nullptr, nullptr);
+    const uint32_t kept = ws.kept[__lane_id()];
     if (g < n) tile_count[g] = kept;
-    // the workgroup's kept tiles (at most 256 * kBigTiles) to kept_part[block], host memory that
-    // the host sums for the instance count
+    // the workgroup's kept tiles and big boxes to kept_part[block], host memory that the host
+    // sums for the instance count and the big-box launch (a wave's kept sum is below 64 * 2^24
+    // tiles, a workgroup's below 2^32 + 2^32, under the big count in bits 48..63)
     const uint32_t wave_kept = wave_reduce_sum_u32(kept);
-    if (__lane_id() == 0) s_kept[threadIdx.x / kWave] = wave_kept;
+    const uint32_t wave_big = (uint32_t)__popcll(wave_ballot(big));
+    if (__lane_id() == 0) {
+        s_kept[threadIdx.x / kWave] = wave_kept;
+        s_big[threadIdx.x / kWave] = wave_big;
+    }
     __syncthreads();
     if (threadIdx.x == 0) {
-        uint32_t sum = 0;
+        unsigned long long sum = 0, bigs = 0;
 #pragma unroll
-        for (int w = 0; w < kWavesPerBlock; ++w) sum += s_kept[w];
-        kept_part[blockIdx.x] = sum;
+        for (int w = 0; w < kWavesPerBlock; ++w) {
+            sum += s_kept[w];
+            bigs += s_big[w];
+        }
+        kept_part[blockIdx.x] = sum | (bigs << kKeptPartBigShift);
     }
 }
 
-// Marks a big box's depth key (big_tiles_block needs its rank). Used only when the sorted depth
+// Marks a big box's depth key (big_box_wave needs its rank). Used only when the sorted depth
 // bits end below bit 63, which holds for fewer than 2^31 Gaussians.
 constexpr uint64_t kBigKeyFlag = 1ull << 63;
 
@@ -380,8 +413,8 @@ __device__ inline void emit_block(uint32_t b, int64_t n, const float4* __restric
                                   int32_t tiles_x, uint32_t* __restrict__ instance_gaussian,
                                   uint32_t* __restrict__ instance_tile,
                                   const uint32_t* __restrict__ long_prefix, uint32_t* __restrict__ long_list,
-                                  WaveBoxes* s_boxes, uint32_t* s_wave) {
-    WaveBoxes& wb = s_boxes[threadIdx.x / kWave];
+                                  WaveSpans* s_spans, uint32_t* s_wave) {
+    WaveSpans& ws = s_spans[threadIdx.x / kWave];
     const int64_t r = (int64_t)b * blockDim.x + threadIdx.x;
     // the rank's count and Gaussian load together, then its whole record (one wait each)
     uint32_t cnt = 0, g = 0;
@@ -410,158 +443,68 @@ __device__ inline void emit_block(uint32_t b, int64_t n, const float4* __restric
         r0 = rec[2 * (size_t)g + 0];
         r1 = rec[2 * (size_t)g + 1];
     }
-    const bool any = cnt > 0 && box_tiles(r1) <= kBigTiles;  // big boxes are emitted by big_tiles_block
-    // a box whose kept count (from the counting walk's identical tests) is its tile count keeps
-    // every tile: emission skips its tests
-    const uint32_t total = stage_box(wb, any, r0, r1, g, o, any && cnt == box_tiles(r1));
-    walk_wave_tiles<true>(wb, total, tiles_x, instance_gaussian, instance_tile);
+    // big boxes are emitted by big_rows_block; the walk numbers the wave's other instances
+    // consecutively, so a lane's base is its offset less the walked instances of the lanes
+    // before it (the counting walk's identical runs gave the counts)
+    const bool walked = cnt > 0 && box_tiles(r1) <= kBigTiles;
+    const uint32_t wcnt = walked ? cnt : 0u;
+    const uint32_t lane = __lane_id();
+    ws.base[lane] = o - (wave_inclusive_sum_u32(wcnt) - wcnt);
+    ws.g[lane] = g;
+    const uint32_t rows = stage_spans(ws, walked, r0, r1);
+    walk_wave_rows<true>(ws, rows, tiles_x, instance_gaussian, instance_tile);
 }
 
-// Big boxes: the row-major tile range of each box on big_list is cut into chunks of `chunk`
-// tiles (at most kBigChunks per box); workgroup (x, c) of the gx * chunks big-box workgroups
-// takes chunk c of the boxes x, x + gx, ... and walks it 256 tiles per step.
-// kEmit = false stores the chunk's kept-tile count in chunk_counts[i][c] and adds it to
-// tile_count[g] (zeroed by preprocess), and the workgroup's kept tiles in total to
-// kept_part[c * gx + x] (host memory). kEmit = true writes the chunk's kept instances at
-// offset(rank of g) + the counts of the box's earlier chunks + their rank within the chunk
-// (per-wave ballots and a 4-wave prefix), i.e. in the same row-major order as a single walk;
-// it runs beside emit_block in one launch, so it forms the offset itself: block_prefix of the
-// rank's 256-rank block plus the counts of the ranks before it in that block.
-constexpr uint32_t kBigChunks = 16;
-
-template <bool kEmit>
-__device__ inline void big_tiles_block(uint32_t x, uint32_t c, uint32_t gx, const uint32_t* __restrict__ big_list,
-                                       const uint32_t* __restrict__ big_count, const float4* __restrict__ rec,
-                                       int32_t tiles_x, uint32_t chunk,
-                                       uint32_t* __restrict__ tile_count, uint32_t* __restrict__ chunk_counts,
-                                       unsigned long long* __restrict__ kept_part,
-                                       const uint32_t* __restrict__ rank_count,
-                                       const uint32_t* __restrict__ block_prefix,
-                                       const uint32_t* __restrict__ gaussian_rank,
-                                       uint32_t* __restrict__ instance_gaussian,
-                                       uint32_t* __restrict__ instance_tile, uint32_t* s_wave, uint32_t* s_red) {
-    const uint32_t count = *big_count;
-    const uint32_t lane = __lane_id(), wave = threadIdx.x / kWave;
-    unsigned long long block_kept = 0;
-    for (uint32_t i = x; i < count; i += gx) {
-        const uint32_t g = big_list[i];
-        const float4 r0 = rec[2 * (size_t)g + 0], r1 = rec[2 * (size_t)g + 1];
-        const uint32_t bx = __float_as_uint(r1.z), by = __float_as_uint(r1.w);
-        const int x0 = (int)(bx & 0xffffu), x1 = (int)(bx >> 16), y0 = (int)(by & 0xffffu), y1 = (int)(by >> 16);
-        const uint32_t tx0 = (uint32_t)x0 / kTile, ty0 = (uint32_t)y0 / kTile;
-        const uint32_t wx = (uint32_t)x1 / kTile - tx0 + 1;
-        const uint32_t total = wx * ((uint32_t)y1 / kTile - ty0 + 1);
-        const uint32_t t0 = c * chunk;
-        if (t0 >= total) continue;  // uniform: the box has fewer chunks
-        const uint32_t t1 = min(total, t0 + chunk);
-        const gsx_tile_conic con = gsx_tile_conic_make(r0.x, r0.y, r0.z, r0.w * 0.5f, r1.x, r1.y);
-        const float rwx = 1.0f / (float)wx;
-        uint32_t o = 0;
-        if (kEmit) {
-            // offset of the box's rank; s_red is rewritten only after the tile loop's barriers
-            const uint32_t rr = gaussian_rank[g];
-            const uint32_t b0 = rr & ~255u;
-            const uint32_t v = b0 + threadIdx.x < rr ? rank_count[b0 + threadIdx.x] : 0u;
-            const uint32_t ws = wave_reduce_sum_u32(v);
-            if (lane == 0) s_red[wave] = ws;
-            __syncthreads();
-            o = block_prefix[rr >> 8];
+// Big boxes: one wave per box of big_list, walking its rows as walk_wave_rows walks a wave's
+// boxes (the box in lane 0, the others empty). It runs beside emit_block in one launch, so it
+// forms the box's offset itself: block_prefix of the rank's 256-rank block plus the counts of the
+// ranks before it in that block. The host sizes the launch with one wave per big box.
+__device__ inline void big_box_wave(uint32_t i, const uint32_t* __restrict__ big_list, const float4* __restrict__ rec,
+                                    int32_t tiles_x, const uint32_t* __restrict__ rank_count,
+                                    const uint32_t* __restrict__ block_prefix,
+                                    const uint32_t* __restrict__ gaussian_rank,
+                                    uint32_t* __restrict__ instance_gaussian, uint32_t* __restrict__ instance_tile,
+                                    WaveSpans& ws) {
+    const uint32_t lane = __lane_id();
+    const uint32_t g = big_list[i];
+    const float4 r0 = rec[2 * (size_t)g + 0], r1 = rec[2 * (size_t)g + 1];
+    const uint32_t rr = gaussian_rank[g];
+    const uint32_t b0 = rr & ~255u;
+    uint32_t v = 0;
 #pragma unroll
-            for (int w = 0; w < kWavesPerBlock; ++w) o += s_red[w];
-            for (uint32_t cc = 0; cc < c; ++cc) o += chunk_counts[(size_t)i * kBigChunks + cc];
-        }
-        uint32_t running = 0;
-        for (uint32_t base = t0; base < t1; base += blockDim.x) {
-            const uint32_t k = base + threadIdx.x;
-            bool keep = false;
-            uint32_t tile = 0;
-            if (k < t1) {
-                const uint32_t row = div_small(k, wx, rwx);
-                const uint32_t ty = ty0 + row, tx = tx0 + (k - row * wx);
-                tile = ty * (uint32_t)tiles_x + tx;
-                const int px0 = max((int)tx * kTile, x0), px1 = min((int)tx * kTile + kTile - 1, x1);
-                const int py0 = max((int)ty * kTile, y0), py1 = min((int)ty * kTile + kTile - 1, y1);
-                keep = gsx_tile_conic_test(&con, px0, px1, py0, py1) != 0;
-            }
-            const uint64_t mask = wave_ballot(keep);
-            if (lane == 0) s_wave[wave] = (uint32_t)__popcll(mask);
-            __syncthreads();
-            uint32_t before = 0, step_total = 0;
-            for (int w = 0; w < kWavesPerBlock; ++w) {
-                before += w < (int)wave ? s_wave[w] : 0u;
-                step_total += s_wave[w];
-            }
-            if (kEmit && keep) {
-                const uint32_t pos = o + running + before + (uint32_t)__popcll(mask & lanemask_lt());
-                instance_gaussian[pos] = g;
-                instance_tile[pos] = tile;
-            }
-            running += step_total;
-            __syncthreads();
-        }
-        if (!kEmit && threadIdx.x == 0) {
-            chunk_counts[(size_t)i * kBigChunks + c] = running;
-            if (running > 0) atomicAdd(&tile_count[g], running);
-        }
-        block_kept += running;
-    }
-    if (!kEmit && threadIdx.x == 0) kept_part[(size_t)c * gx + x] = block_kept;
+    for (uint32_t k = 0; k < 256; k += kWave) v += b0 + k + lane < rr ? rank_count[b0 + k + lane] : 0u;
+    ws.base[lane] = block_prefix[rr >> 8] + wave_reduce_sum_u32(v);
+    ws.g[lane] = g;
+    const uint32_t rows = stage_spans(ws, lane == 0, r0, r1);
+    walk_wave_rows<true>(ws, rows, tiles_x, instance_gaussian, instance_tile);
 }
 
-// Two independent jobs after preprocess in one launch: workgroups [0, big_blocks) count the big
-// boxes' kept tiles (x = index % gx, chunk = index / gx), the rest take the depth sort's first
-// upsweep (digit counts of the depth keys' first digit, the invisible keys left out), which
-// then runs beside the longer big-box walks instead of after them.
-__global__ __launch_bounds__(256) void big_count_upsweep_kernel(const uint32_t* __restrict__ big_list,
-                                                                const uint32_t* __restrict__ big_count,
-                                                                const float4* __restrict__ rec, int32_t tiles_x,
-                                                                uint32_t chunk, uint32_t gx, uint32_t big_blocks,
-                                                                uint32_t* __restrict__ tile_count,
-                                                                uint32_t* __restrict__ chunk_counts,
-                                                                unsigned long long* __restrict__ kept_part,
-                                                                const uint64_t* __restrict__ depth_keys, int64_t n,
-                                                                int shift, int64_t depth_chunks,
-                                                                uint32_t* __restrict__ depth_hist) {
-    __shared__ uint32_t s_wave[kWavesPerBlock];
-    __shared__ uint32_t s_hist[kChunkWaves][1 << kCompactingRadixBits];
-    if (blockIdx.x < big_blocks) {
-        big_tiles_block<false>(blockIdx.x % gx, blockIdx.x / gx, gx, big_list, big_count, rec, tiles_x, chunk,
-                               tile_count, chunk_counts, kept_part, nullptr, nullptr, nullptr, nullptr, nullptr, s_wave,
-                               nullptr);
-        return;
-    }
-    radix_upsweep_block<kCompactingRadixBits, kCompactingChunk>(blockIdx.x - big_blocks, depth_keys, n, nullptr, true,
-                                                                shift, depth_chunks, depth_hist, s_hist);
-}
-
-// All emission in one launch: workgroups [0, big_blocks) are the big-box workgroups
-// (x = index % gx, chunk = index / gx), first so that their longer walks start early; the rest
-// are the emission workgroups of the ranks.
+// All emission in one launch: workgroups [0, big_blocks) hold one wave per big box, first so
+// that their longer walks start early; the rest are the emission workgroups of the ranks.
 __global__ __launch_bounds__(256) void emit_kernel(int64_t n, const float4* __restrict__ rec,
                                                    const uint32_t* __restrict__ rank_gaussian,
                                                    const uint32_t* __restrict__ rank_count,
                                                    const uint32_t* __restrict__ block_prefix,
                                                    uint32_t* __restrict__ offsets, int32_t tiles_x,
                                                    const uint32_t* __restrict__ big_list,
-                                                   const uint32_t* __restrict__ big_count, uint32_t gx,
-                                                   uint32_t big_blocks, uint32_t chunk,
-                                                   const uint32_t* __restrict__ chunk_counts,
+                                                   const uint32_t* __restrict__ big_count, uint32_t big_blocks,
                                                    const uint32_t* __restrict__ gaussian_rank,
                                                    uint32_t* __restrict__ instance_gaussian,
                                                    uint32_t* __restrict__ instance_tile,
                                                    const uint32_t* __restrict__ long_prefix,
                                                    uint32_t* __restrict__ long_list) {
-    __shared__ WaveBoxes s_boxes[kWavesPerBlock];
+    __shared__ WaveSpans s_spans[kWavesPerBlock];
     __shared__ uint32_t s_wave[kWavesPerBlock];
-    __shared__ uint32_t s_red[kWavesPerBlock];
     if (blockIdx.x < big_blocks) {
-        big_tiles_block<true>(blockIdx.x % gx, blockIdx.x / gx, gx, big_list, big_count, rec, tiles_x, chunk,
-                              nullptr, const_cast<uint32_t*>(chunk_counts), nullptr, rank_count, block_prefix,
-                              gaussian_rank, instance_gaussian, instance_tile, s_wave, s_red);
+        // no workgroup barrier on this path: each wave takes its own box
+        const uint32_t i = blockIdx.x * kWavesPerBlock + threadIdx.x / kWave;
+        if (i < *big_count)
+            big_box_wave(i, big_list, rec, tiles_x, rank_count, block_prefix, gaussian_rank, instance_gaussian,
+                         instance_tile, s_spans[threadIdx.x / kWave]);
         return;
     }
     emit_block(blockIdx.x - big_blocks, n, rec, rank_gaussian, rank_count, block_prefix, offsets, tiles_x,
-               instance_gaussian, instance_tile, long_prefix, long_list, s_boxes, s_wave);
+               instance_gaussian, instance_tile, long_prefix, long_list, s_spans, s_wave);
 }
 
 __global__ __launch_bounds__(256) void fill_u32_kernel(uint32_t* __restrict__ p, int64_t count, uint32_t v) {

@@ -1,25 +1,21 @@
 /*
  * tile_cull.h - the conservative tile test of key emission, shared by the gfx950 kernels and the
- * CPU restatement in oracle/ (both compile it with -ffp-contract=off and IEEE division, so they
- * take the same decision bit for bit).
+ * CPU restatement in oracle/ (both compile it with -ffp-contract=off and correctly rounded
+ * division and square root, so they take the same decision bit for bit).
  *
  * The gsx CPU backend visits every pixel of a Gaussian's 3-sigma box (gsx/src/gsx-cpu/render.c:
  * 1042-1079) and skips the pixel when power < -4.5 or opacity * expf(power) < 1/255, with
  * power = -0.5 * (inv_a dx^2 + 2 inv_b dx dy + inv_c dy^2) in float. A tile of the box whose
  * pixels all fail those tests contributes nothing to the image or to any gradient, so its
- * (tile, Gaussian) instance can be left out of the sort. The test drops an instance only when a
- * bound of power over the whole clipped tile rectangle (continuous, so it covers every pixel
- * centre) lies below the skip threshold with room to spare:
+ * (tile, Gaussian) instance can be left out of the sort. With
  *   thr    = max(-4.5, ln(1/255) - ln(opacity)) - 1e-3     (per Gaussian; the pixel is skipped
  *            when power < thr + 1e-3, and the 1e-3 dwarfs every float rounding in between),
  *   q_cut  = -2 * thr,
- *   q_min  = minimum of the quadratic form over the rectangle (0 when it holds the centre,
- *            otherwise the least of its four corner values and the values at the edges'
- *            interior stationary points),
- *   margin = 1e-4 * (largest term magnitude over the rectangle) + 1e-3, which exceeds the float
- *            rounding of both q_min and the per-pixel power by orders of magnitude,
- *   drop   iff q_min - margin > q_cut.
- * Then every pixel centre has power <= -0.5 * (q_min - margin) < thr, so it fails a cut.
+ * a pixel that contributes has its quadratic form q = -2 power at most q_cut. The test keeps,
+ * for each tile row of the box, the tiles that hold a pixel column where the set {q <= Q}
+ * (Q = q_cut plus an allowance for rounding) meets the row's band of pixel rows: one contiguous
+ * run of tiles per row, from a closed form (gsx_tile_band_columns). Every dropped tile's pixels
+ * therefore fail a cut.
  */
 #ifndef GSX_AMD_TILE_CULL_H
 #define GSX_AMD_TILE_CULL_H
@@ -77,87 +73,129 @@ GSX_HD float gsx_tile_qcut(float opacity)
     return -2.0f * (thr - 1e-3f);
 }
 
-/* Per-Gaussian constants of the test: conic (A, B, C) = (inv_a, inv_b, inv_c), their
- * reciprocals for the edge minima, and q_cut. */
-typedef struct gsx_tile_conic {
-    float mx, my, A, B, C, rA, rC, qcut;
-} gsx_tile_conic;
+/* Per-Gaussian constants of the row-span test. Every kept tile of a tile row of the box is one
+ * contiguous run: the pixel centres of the row's band (its pixel rows within the box) that may
+ * receive a contribution lie inside the convex set {q(u, v) <= Q}, whose part over the band
+ * projects onto one interval of columns. With q = A u^2 + 2 B u v + C v^2 (A, C > 0,
+ * det = A C - B^2 > 0) and D(v) = A Q - det v^2, the set's right boundary at height v is
+ * u+(v) = (sqrt(D(v)) - B v) / A, a concave function of v largest at vr = -B sqrt(Q / (det C))
+ * (the ellipse's rightmost point), so over the band [v0, v1] it is largest at clamp(vr, v0, v1);
+ * by symmetry (q(u, v) = q(-u, -v)) the left boundary is least at -clamp(vr, -v1, -v0) mirrored.
+ * The band misses the set exactly when D < 0 at that point.
+ *   Q    = q_cut + 1e-5 S + 1e-3, S = A X^2 + 2 |B| X Y + C Y^2 with X, Y the largest |offsets| of
+ *          the box's pixel centres from the mean: the kernels' power evaluation at a pixel of the
+ *          box is within 4 eps S of the exact form (eps = 2^-24), 1e-5 S covers it 40 times over;
+ *   aqs  = A Q (1 + 2^-14 + kappa 2^-19), kappa = A C / det: the rounding of D(v) for |v| within
+ *          the set is below (3 + 2 kappa) eps A Q, and the factor adds at least 8 times that, so
+ *          the computed D is never below the exact one and sqrt(D) never short;
+ *   the remaining roundings (of -B v + sqrt(D), of the product with 1 / A) are below
+ *          3 eps (sqrt(kappa) + 1) sqrt(Q / A), and the factor widens the span by at least
+ *          2^-15 sqrt(Q / A), 8 times more.
+ * A pixel column x is kept when its centre offset fl(fl(x + 0.5) - mx), the value the kernels
+ * evaluate, lies in [u-, u+]; fl is monotone, so the kept columns are one interval, found from
+ * floor / ceil of mx + u -/+ 0.5 and one exact check on each side. A Gaussian whose form is not
+ * positive definite, whose kappa exceeds 2^16 (det then carries more than 1% rounding) or whose
+ * mean lies beyond 2^21 pixels, or any non-finite constant, keeps every column of its box:
+ * aqs = +inf, det = vr = B = 0 and ra = 1 make every band span the box without a branch. */
+typedef struct gsx_tile_span {
+    float mx, my; /* mean2d */
+    float b;      /* inv_b */
+    float ra;     /* 1 / inv_a */
+    float det;    /* inv_a inv_c - inv_b^2 */
+    float vr;     /* v of the rightmost point of the set */
+    float aqs;    /* inv_a Q with the rounding allowance */
+} gsx_tile_span;
 
-GSX_HD gsx_tile_conic gsx_tile_conic_make(float mx, float my, float inv_a, float inv_b, float inv_c, float opacity)
+/* Constants of the Gaussian with conic (inv_a, inv_b, inv_c), activated opacity `opacity` and
+ * inclusive pixel box [x0, x1] x [y0, y1]. */
+GSX_HD gsx_tile_span gsx_tile_span_make(float mx, float my, float inv_a, float inv_b, float inv_c, float opacity,
+    int x0, int x1, int y0, int y1)
 {
-    gsx_tile_conic k;
+    gsx_tile_span k;
+    const float A = inv_a, B = inv_b, C = inv_c;
+    const float dx0 = ((float)x0 + 0.5f) - mx, dx1 = ((float)x1 + 0.5f) - mx;
+    const float dy0 = ((float)y0 + 0.5f) - my, dy1 = ((float)y1 + 0.5f) - my;
+    const float X = gsx_cull_maxf(gsx_cull_absf(dx0), gsx_cull_absf(dx1));
+    const float Y = gsx_cull_maxf(gsx_cull_absf(dy0), gsx_cull_absf(dy1));
+    const float S = gsx_cull_absf(A) * X * X + 2.0f * gsx_cull_absf(B) * X * Y + gsx_cull_absf(C) * Y * Y;
+    const float Q = gsx_tile_qcut(opacity) + (1e-5f * S + 1e-3f);
+    const float ac = A * C;
+    const float det = ac - B * B;
+    const float kappa = ac / det;
+    const float slack = 6.103515625e-05f + kappa * 1.9073486328125e-06f; /* 2^-14 + kappa 2^-19 */
 
     k.mx = mx;
     k.my = my;
-    k.A = inv_a;
-    k.B = inv_b;
-    k.C = inv_c;
-    k.rA = 1.0f / inv_a;
-    k.rC = 1.0f / inv_c;
-    k.qcut = gsx_tile_qcut(opacity);
+    k.b = B;
+    k.ra = 1.0f / A;
+    k.det = det;
+    k.vr = -B * sqrtf(Q / (det * C));
+    k.aqs = (A * Q) * (1.0f + slack);
+    /* the comparisons are false for NaN, which therefore keeps every column too */
+    if(!(A > 0.0f && C > 0.0f && det > 0.0f && det * 65536.0f >= ac && gsx_cull_absf(mx) < 2097152.0f &&
+           gsx_cull_absf(my) < 2097152.0f && gsx_cull_absf(k.vr) <= 3.0e38f && k.aqs <= 3.0e38f && k.ra <= 3.0e38f)) {
+        k.b = 0.0f;
+        k.ra = 1.0f;
+        k.det = 0.0f;
+        k.vr = 0.0f;
+        k.aqs = __builtin_inff();
+    }
     return k;
 }
 
-/* Nonzero when some pixel centre of the inclusive pixel rectangle [px0, px1] x [py0, py1] (the
- * tile clipped to the Gaussian's box) may receive a contribution from the Gaussian.
- * q(u, v) = A u^2 + 2 B u v + C v^2 is evaluated as fma(C v, v, fma(2 B u, v, (A u) u)); the four
- * corner values are shared by the two edges through each corner, and each edge adds the value at
- * its interior stationary point (clamped to the edge) when the quadratic is convex along it. */
-GSX_HD int gsx_tile_conic_test(const gsx_tile_conic *k, int px0, int px1, int py0, int py1)
+/* The pixel columns [*xa, *xb] of the box [x0, x1] whose centres may receive a contribution in
+ * the band of pixel rows [py0, py1] (within the box); *xa > *xb when none. */
+GSX_HD void gsx_tile_band_columns(const gsx_tile_span *k, int x0, int x1, int py0, int py1, int *xa, int *xb)
 {
-    const float A = k->A, B = k->B, C = k->C, rA = k->rA, rC = k->rC, qcut = k->qcut;
-    const float B2 = 2.0f * B;
-    const float dx0 = ((float)px0 + 0.5f) - k->mx;
-    const float dx1 = ((float)px1 + 0.5f) - k->mx;
-    const float dy0 = ((float)py0 + 0.5f) - k->my;
-    const float dy1 = ((float)py1 + 0.5f) - k->my;
-    const float X = gsx_cull_maxf(gsx_cull_absf(dx0), gsx_cull_absf(dx1));
-    const float Y = gsx_cull_maxf(gsx_cull_absf(dy0), gsx_cull_absf(dy1));
-    const float scale = gsx_cull_absf(A) * X * X + 2.0f * gsx_cull_absf(B) * X * Y + gsx_cull_absf(C) * Y * Y;
-    const float margin = 1e-4f * scale + 1e-3f;
-    float au0, au1, bu0, bu1, cv0, cv1, qmin, s, q;
+    const float v0 = ((float)py0 + 0.5f) - k->my, v1 = ((float)py1 + 0.5f) - k->my;
+    const float vh = gsx_cull_clampf(k->vr, v0, v1);
+    const float vl = gsx_cull_clampf(k->vr, -v1, -v0);
+    const float dh = k->aqs - (k->det * vh) * vh;
+    const float dl = gsx_cull_maxf(k->aqs - (k->det * vl) * vl, 0.0f);
+    const float uh = (sqrtf(dh) - k->b * vh) * k->ra;
+    const float ul = -((sqrtf(dl) - k->b * vl) * k->ra);
+    const float sh = (k->mx + uh) - 0.5f, sl = (k->mx + ul) - 0.5f;
+    int c;
 
-    if(dx0 <= 0.0f && dx1 >= 0.0f && dy0 <= 0.0f && dy1 >= 0.0f) {
-        return 1;
+    if(dh < 0.0f) { /* the band misses the set */
+        *xa = 1;
+        *xb = 0;
+        return;
     }
-    au0 = (A * dx0) * dx0;
-    au1 = (A * dx1) * dx1;
-    bu0 = B2 * dx0;
-    bu1 = B2 * dx1;
-    cv0 = C * dy0;
-    cv1 = C * dy1;
-    /* corners */
-    qmin = GSX_FMAF(cv0, dy0, GSX_FMAF(bu0, dy0, au0));
-    qmin = gsx_cull_minf(qmin, GSX_FMAF(cv1, dy1, GSX_FMAF(bu0, dy1, au0)));
-    qmin = gsx_cull_minf(qmin, GSX_FMAF(cv0, dy0, GSX_FMAF(bu1, dy0, au1)));
-    qmin = gsx_cull_minf(qmin, GSX_FMAF(cv1, dy1, GSX_FMAF(bu1, dy1, au1)));
-    /* vertical edges u = dx0, dx1: stationary point v = -(B u) / C */
-    if(C > 0.0f) {
-        s = gsx_cull_clampf(-(B * dx0) * rC, dy0, dy1);
-        q = GSX_FMAF(C * s, s, GSX_FMAF(bu0, s, au0));
-        qmin = gsx_cull_minf(qmin, q);
-        s = gsx_cull_clampf(-(B * dx1) * rC, dy0, dy1);
-        q = GSX_FMAF(C * s, s, GSX_FMAF(bu1, s, au1));
-        qmin = gsx_cull_minf(qmin, q);
+    /* last column whose centre offset is at most uh */
+    if(!(sh < (float)x1)) {
+        c = x1;
+    } else if(!(sh >= (float)x0 - 1.0f)) {
+        c = x0 - 1;
+    } else {
+        c = (int)floorf(sh);
+        if(c + 1 <= x1 && (((float)(c + 1) + 0.5f) - k->mx) <= uh) c += 1;
+        if(c >= x0 && !((((float)c + 0.5f) - k->mx) <= uh)) c -= 1;
     }
-    /* horizontal edges v = dy0, dy1: stationary point u = -(B v) / A */
-    if(A > 0.0f) {
-        s = gsx_cull_clampf(-(B * dy0) * rA, dx0, dx1);
-        q = GSX_FMAF(cv0, dy0, GSX_FMAF(B2 * s, dy0, (A * s) * s));
-        qmin = gsx_cull_minf(qmin, q);
-        s = gsx_cull_clampf(-(B * dy1) * rA, dx0, dx1);
-        q = GSX_FMAF(cv1, dy1, GSX_FMAF(B2 * s, dy1, (A * s) * s));
-        qmin = gsx_cull_minf(qmin, q);
+    *xb = c;
+    /* first column whose centre offset is at least ul */
+    if(!(sl > (float)x0)) {
+        c = x0;
+    } else if(!(sl <= (float)x1 + 1.0f)) {
+        c = x1 + 1;
+    } else {
+        c = (int)ceilf(sl);
+        if(c - 1 >= x0 && (((float)(c - 1) + 0.5f) - k->mx) >= ul) c -= 1;
+        if(c <= x1 && !((((float)c + 0.5f) - k->mx) >= ul)) c += 1;
     }
-    return !(qmin - margin > qcut); /* keeps the instance for NaN input too */
+    *xa = c;
 }
 
+/* Nonzero when some pixel centre of the inclusive pixel rectangle [px0, px1] x [py0, py1] may
+ * receive a contribution from the Gaussian (the rectangle taken as its box). */
 GSX_HD int gsx_tile_may_contribute(float mx, float my, float inv_a, float inv_b, float inv_c, float opacity, int px0,
     int px1, int py0, int py1)
 {
-    const gsx_tile_conic k = gsx_tile_conic_make(mx, my, inv_a, inv_b, inv_c, opacity);
+    const gsx_tile_span k = gsx_tile_span_make(mx, my, inv_a, inv_b, inv_c, opacity, px0, px1, py0, py1);
+    int xa, xb;
 
-    return gsx_tile_conic_test(&k, px0, px1, py0, py1);
+    gsx_tile_band_columns(&k, px0, px1, py0, py1, &xa, &xb);
+    return xa <= xb;
 }
 
 #endif /* GSX_AMD_TILE_CULL_H */

@@ -463,25 +463,38 @@ static int cmp_kv(const void *pa, const void *pb)
     return 0;
 }
 
-/* Whether visible Gaussian v keeps its instance for tile (tx, ty): the tile clipped to the
- * pixel box, tested with the conservative contribution bound shared with the kernels
- * (gsx_amd/csrc/tile_cull.h). Dropped instances are ones whose pixels all fail the power or
- * alpha cut of render.c:1055-1066, so the per-pixel lists lose only entries that are skipped. */
-static int tile_kept(const vis *v, int32_t tx, int32_t ty, int32_t tile_size)
+/* The row-span constants of visible Gaussian v (gsx_amd/csrc/tile_cull.h), from its conic and
+ * box as the kernels form them. */
+static gsx_tile_span vis_span(const vis *v)
 {
     const float inv_det = v->rec[ORACLE_REC_INV_DET];
     const float inv_a = v->rec[ORACLE_REC_COV_C] * inv_det;
     const float inv_b = -v->rec[ORACLE_REC_COV_B] * inv_det;
     const float inv_c = v->rec[ORACLE_REC_COV_A] * inv_det;
-    int32_t px0 = tx * tile_size, px1 = tx * tile_size + tile_size - 1;
-    int32_t py0 = ty * tile_size, py1 = ty * tile_size + tile_size - 1;
 
-    if(px0 < v->bb[0]) px0 = v->bb[0];
-    if(px1 > v->bb[1]) px1 = v->bb[1];
+    return gsx_tile_span_make(v->rec[ORACLE_REC_MEAN2D_X], v->rec[ORACLE_REC_MEAN2D_Y], inv_a, inv_b, inv_c,
+        v->rec[ORACLE_REC_OPACITY], v->bb[0], v->bb[1], v->bb[2], v->bb[3]);
+}
+
+/* The kept tiles [*txa, *txb] of tile row ty of visible Gaussian v (*txa > *txb when none): the
+ * tiles holding a pixel column of the box where the row's band may receive a contribution
+ * (tile_cull.h). Dropped instances are ones whose pixels all fail the power or alpha cut of
+ * render.c:1055-1066, so the per-pixel lists lose only entries that are skipped. */
+static void row_tiles(const vis *v, const gsx_tile_span *k, int32_t ty, int32_t tile_size, int32_t *txa, int32_t *txb)
+{
+    int32_t py0 = ty * tile_size, py1 = ty * tile_size + tile_size - 1;
+    int xa, xb;
+
     if(py0 < v->bb[2]) py0 = v->bb[2];
     if(py1 > v->bb[3]) py1 = v->bb[3];
-    return gsx_tile_may_contribute(v->rec[ORACLE_REC_MEAN2D_X], v->rec[ORACLE_REC_MEAN2D_Y], inv_a, inv_b, inv_c,
-        v->rec[ORACLE_REC_OPACITY], px0, px1, py0, py1);
+    gsx_tile_band_columns(k, v->bb[0], v->bb[1], py0, py1, &xa, &xb);
+    if(xa > xb) {
+        *txa = 1;
+        *txb = 0;
+    } else {
+        *txa = xa / tile_size;
+        *txb = xb / tile_size;
+    }
 }
 
 /* Tile-key restatement (no CPU counterpart): visible Gaussians in Gaussian-index order, each
@@ -503,10 +516,12 @@ int64_t oracle_tile_keys(int64_t n, int sh_degree, const float *mean3d, const fl
     if(v == NULL) return -1;
     count = collect_visible(n, sh_degree, mean3d, rotation, logscale, opacity, sh0, sh1, sh2, sh3, &k, v, NULL);
     for(i = 0; i < count; ++i) {
+        const gsx_tile_span sp = vis_span(&v[i]);
+        int32_t txa, txb;
+
         for(ty = v[i].bb[2] / tile_size; ty <= v[i].bb[3] / tile_size; ++ty) {
-            for(tx = v[i].bb[0] / tile_size; tx <= v[i].bb[1] / tile_size; ++tx) {
-                total += tile_kept(&v[i], tx, ty, tile_size);
-            }
+            row_tiles(&v[i], &sp, ty, tile_size, &txa, &txb);
+            if(txa <= txb) total += txb - txa + 1;
         }
     }
     if(total > capacity) {
@@ -521,12 +536,14 @@ int64_t oracle_tile_keys(int64_t n, int sh_degree, const float *mean3d, const fl
     total = 0;
     for(i = 0; i < count; ++i) {
         uint32_t depth_bits = gsx_f32_bits(v[i].rec[ORACLE_REC_DEPTH]);
+        const gsx_tile_span sp = vis_span(&v[i]);
+        int32_t txa, txb;
 
         for(ty = v[i].bb[2] / tile_size; ty <= v[i].bb[3] / tile_size; ++ty) {
-            for(tx = v[i].bb[0] / tile_size; tx <= v[i].bb[1] / tile_size; ++tx) {
+            row_tiles(&v[i], &sp, ty, tile_size, &txa, &txb);
+            for(tx = txa; tx <= txb; ++tx) {
                 uint64_t tile = (uint64_t)ty * (uint64_t)tiles_x + (uint64_t)tx;
 
-                if(!tile_kept(&v[i], tx, ty, tile_size)) continue;
                 pairs[total].key = (tile << 32) | (uint64_t)depth_bits;
                 pairs[total].value = (uint32_t)v[i].g;
                 pairs[total].seq = (uint64_t)total;
@@ -1805,14 +1822,16 @@ static int tiled_build(int64_t n, int deg, const float *mean3d, const float *rot
         for(g = lo; g < hi; ++g) {
             const int32_t *bb = out->v[g].bb;
             int64_t b = box_byte[g];
-            int32_t tx, ty;
+            int32_t tx, ty, txa = bb[0] / tile, txb = bb[1] / tile;
+            const gsx_tile_span sp = vis_span(&out->v[g]);
 
             for(ty = bb[2] / tile; ty <= bb[3] / tile; ++ty) {
+                if(cull) row_tiles(&out->v[g], &sp, ty, tile, &txa, &txb);
                 for(tx = bb[0] / tile; tx <= bb[1] / tile; ++tx) {
                     int keep = 1;
 
                     if(cull) {
-                        keep = tile_kept(&out->v[g], tx, ty, tile);
+                        keep = txa <= tx && tx <= txb;
                         kept[b++] = (uint8_t)keep;
                     }
                     pc[(int64_t)ty * tiles_x + tx] += keep;
