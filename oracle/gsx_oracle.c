@@ -570,6 +570,17 @@ int oracle_tile_may_contribute(float mx, float my, float inv_a, float inv_b, flo
     return gsx_tile_may_contribute(mx, my, inv_a, inv_b, inv_c, opacity, px0, px1, py0, py1);
 }
 
+/* The band columns of tile_cull.h for the Gaussian with pixel box [x0, x1] x [y0, y1] and the
+ * band of pixel rows [py0, py1]: out[0] = first, out[1] = last kept column (out[0] > out[1]
+ * when none). */
+void oracle_tile_band_columns(float mx, float my, float inv_a, float inv_b, float inv_c, float opacity, int x0,
+    int x1, int y0, int y1, int py0, int py1, int *out)
+{
+    const gsx_tile_span k = gsx_tile_span_make(mx, my, inv_a, inv_b, inv_c, opacity, x0, x1, y0, y1);
+
+    gsx_tile_band_columns(&k, x0, x1, py0, py1, &out[0], &out[1]);
+}
+
 /* [start, end) of every tile in the sorted key array; empty tiles get (0, 0). */
 void oracle_tile_ranges(int64_t instance_count, const uint64_t *keys, int64_t tile_count, uint32_t *out_ranges)
 {

@@ -61,6 +61,8 @@ class Oracle:
         lib.oracle_tile_ranges.argtypes = [_i64, _vp, _i64, _vp]
         lib.oracle_tile_may_contribute.restype = ctypes.c_int
         lib.oracle_tile_may_contribute.argtypes = [_f] * 6 + [ctypes.c_int] * 4
+        lib.oracle_tile_band_columns.restype = None
+        lib.oracle_tile_band_columns.argtypes = [_f] * 6 + [ctypes.c_int] * 6 + [ctypes.POINTER(ctypes.c_int)]
         lib.oracle_tile_logf.restype = _f
         lib.oracle_tile_logf.argtypes = [_f]
         lib.oracle_render_forward.restype = ctypes.c_int
@@ -118,6 +120,13 @@ class Oracle:
 
     def tile_may_contribute(self, mx, my, inv_a, inv_b, inv_c, opacity, px0, px1, py0, py1) -> bool:
         return bool(self.lib.oracle_tile_may_contribute(mx, my, inv_a, inv_b, inv_c, opacity, px0, px1, py0, py1))
+
+    def tile_band_columns(self, mx, my, inv_a, inv_b, inv_c, opacity, box, py0, py1) -> tuple:
+        """(first, last) kept pixel column of the band of rows [py0, py1] of the pixel box
+        box = (x0, x1, y0, y1); first > last when none (tile_cull.h)."""
+        out = (ctypes.c_int * 2)()
+        self.lib.oracle_tile_band_columns(mx, my, inv_a, inv_b, inv_c, opacity, *box, py0, py1, out)
+        return int(out[0]), int(out[1])
 
     def tile_ranges(self, keys, tile_count):
         ranges = np.zeros((tile_count, 2), np.uint32)

@@ -350,6 +350,66 @@ def test_tile_test_is_conservative_and_effective(oracle):
     assert kept_empty < 0.1 * empty
 
 
+def test_tile_band_columns_cover_every_contributing_pixel(oracle):
+    """The closed-form row runs of the tile test (tile_cull.h) against per-pixel brute force over
+    whole boxes: for every 16-row band of the box, every pixel that passes the CPU's cuts lies in
+    the band's kept columns. Cases: ordinary Gaussians, needles up to 400:1 at any angle, huge
+    Gaussians with means far off the image, and opacities just above the 1/255 cut."""
+    rng = np.random.default_rng(31)
+    f = np.float32
+    checked = slack = 0
+    for case in range(1200):
+        mode = case % 4
+        sx, sy = np.exp(rng.uniform(-1.0, 4.5, 2))
+        if mode == 1:
+            sx, sy = np.exp(rng.uniform(2.0, 6.0)), np.exp(rng.uniform(-1.0, 0.5))
+        if mode == 2:
+            sx = np.exp(rng.uniform(5.0, 9.0))
+            sy = sx * np.exp(-rng.uniform(0.0, 2.0))
+        th = rng.uniform(0, np.pi)
+        c, s_ = np.cos(th), np.sin(th)
+        cov = np.array([[c, -s_], [s_, c]]) @ np.diag([sx * sx, sy * sy]) @ np.array([[c, s_], [-s_, c]])
+        cov = cov.astype(np.float32) + np.eye(2, dtype=np.float32) * f(0.3)
+        a, b, cc = f(cov[0, 0]), f(cov[0, 1]), f(cov[1, 1])
+        det = a * cc - b * b
+        if not det > 0:
+            continue
+        inv_det = f(1.0) / det
+        inv_a, inv_b, inv_c = cc * inv_det, -b * inv_det, a * inv_det
+        op = f(1.0 / (1.0 + np.exp(-rng.normal(0, 3))))
+        if mode == 3:
+            op = f(1.0 / 255.0 * (1.0 + 0.02 * rng.uniform()))
+        if not op >= f(1.0 / 255.0):
+            continue
+        mx, my = f(rng.uniform(-150, 280)), f(rng.uniform(-150, 280))
+        if mode == 2 and case % 8 == 2:
+            mx = f(rng.uniform(-2e5, 2e5))
+        ex, ey = 3.0 * np.sqrt(float(a)), 3.0 * np.sqrt(float(cc))
+        x0, x1 = int(max(0, np.floor(mx - ex))), int(min(127, np.ceil(mx + ex)))
+        y0, y1 = int(max(0, np.floor(my - ey))), int(min(127, np.ceil(my + ey)))
+        if x0 > x1 or y0 > y1:
+            continue
+        xs = np.arange(x0, x1 + 1, dtype=np.float32)
+        ys = np.arange(y0, y1 + 1, dtype=np.float32)
+        dx = (xs[None, :] + f(0.5)) - mx
+        dy = (ys[:, None] + f(0.5)) - my
+        power = np.minimum(f(-0.5) * ((inv_a * dx * dx + f(2.0) * inv_b * dx * dy) + inv_c * dy * dy), f(0.0))
+        alpha = np.minimum(f(0.999), op * np.exp(power.astype(np.float64)).astype(np.float32))
+        contributes = (power >= f(-4.5)) & (alpha >= f(1.0) / f(255.0))
+        for ty in range(y0 // 16, y1 // 16 + 1):
+            py0, py1 = max(ty * 16, y0), min(ty * 16 + 15, y1)
+            xa, xb = oracle.tile_band_columns(mx, my, inv_a, inv_b, inv_c, op, (x0, x1, y0, y1), py0, py1)
+            cols = np.nonzero(contributes[py0 - y0:py1 - y0 + 1].any(axis=0))[0] + x0
+            if len(cols):
+                assert xa <= cols[0] and cols[-1] <= xb, (case, mode, ty, xa, xb, cols[0], cols[-1])
+                checked += 1
+                slack += (cols[0] - xa) + (xb - cols[-1])
+            assert x0 <= xa or xa > xb
+            assert xb <= x1
+    assert checked > 1500
+    assert slack / checked < 2.0  # the runs hug the contributing columns
+
+
 def test_gather_rows(oracle):
     src = np.arange(40, dtype=np.float32).reshape(10, 4)
     idx = np.array([3, 3, 0, 9], np.int32)
