@@ -101,6 +101,20 @@ def sort_bytes(passes, instances):
     return instances * (16 * passes + 4 * (passes - 1))
 
 
+def sort_scope_model(instances, tiles, ms):
+    """The sort rate by the scope's own byte model for this metric: a sort of 64-bit
+    (tile << 32 | depth) keys with 4-byte values in P = ceil((32 + ceil(log2 T)) / 8) passes of
+    8-bit digits, 8 bytes of digit counting plus 24 bytes of scatter per pair and pass (152 bytes
+    per pair at 1080p). This build's two-level order sorts 13-bit tiles in two passes and moves
+    36 bytes per pair (sort_bytes); the model's bytes over the measured time say how the sort's
+    time compares with that design's at the same bandwidth, so its fraction can exceed 1."""
+    passes = -(-(32 + max(1, (max(tiles, 2) - 1).bit_length())) // 8)
+    per_pair = 8 + 24 * passes
+    gbps = per_pair * instances / (ms * 1e-3) / 1e9
+    return {"bytes_per_pair": per_pair, "passes": passes, "gbps": round(gbps, 1),
+            "frac_of_peak": round(gbps / HBM_PEAK_GBPS, 3)}
+
+
 def render_geometry(lib, renderer, n, width, height):
     """The byte model's per-step quantities, read from the render context's buffers after a
     TRAIN forward + backward (one synchronisation; used between timed steps only)."""
@@ -315,6 +329,7 @@ def extra_workloads(lib, steps):
                              "sort_gbps": round(moved / (stage["sort"] * 1e-3) / 1e9, 1),
                              "sort_hbm_frac": round(moved / (stage["sort"] * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
                              "sort_gkeys_s": round(inst / (stage["sort"] * 1e-3) / 1e9, 2),
+                             "sort_scope_model": sort_scope_model(inst, 120 * 68, stage["sort"]),
                              "stage_ms": {k: round(v, 3) for k, v in stage.items()}}
     del g, step, r, inputs, w
     log(f"config 4: {out['c4_sort_stress']}")
@@ -591,6 +606,7 @@ def main():
         "sort_hbm_frac": sort_entry["hbm_frac"],
         # sorted (tile, position) pairs per second over the same steps
         "sort_gkeys_s": round(geo_mean["I"] / (sort_entry["ms"] * 1e-3) / 1e9, 2),
+        "sort_scope_model": sort_scope_model(geo_mean["I"], geo_mean["T"], sort_entry["ms"]),
         "kernels": kernels,
         "roofline": {"bound": "hbm", "kernel": STAGE_KERNEL.get(dominant["stage"], dominant["stage"]),
                      "achieved": dominant["gbps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
