@@ -108,7 +108,7 @@ def sort_scope_model(instances, tiles, ms):
     per pair at 1080p). This build's two-level order sorts 13-bit tiles in two passes and moves
     36 bytes per pair (sort_bytes); the model's bytes over the measured time say how the sort's
     time compares with that design's at the same bandwidth, so its fraction can exceed 1."""
-    passes = -(-(32 + max(1, (max(tiles, 2) - 1).bit_length())) // 8)
+    passes = -(-(32 + max(1, (max(int(round(tiles)), 2) - 1).bit_length())) // 8)
     per_pair = 8 + 24 * passes
     gbps = per_pair * instances / (ms * 1e-3) / 1e9
     return {"bytes_per_pair": per_pair, "passes": passes, "gbps": round(gbps, 1),

@@ -192,7 +192,7 @@ __device__ inline uint32_t digit_exclusive_scan(uint32_t v, uint32_t* s_wave, ui
 // KeyT: uint64_t or uint32_t keys. kPairs with vals_in == nullptr: each key's value is its input
 // position (the first pass of the tile sort, whose values are the emission positions).
 template <bool kPairs, int kBits, int kChunk, typename KeyT = uint64_t>
-__global__ __launch_bounds__(kDownThreads) void radix_downsweep_kernel(
+__global__ __launch_bounds__(kDownThreads, 8) void radix_downsweep_kernel(
     const KeyT* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, int64_t n,
     const uint32_t* __restrict__ n_dev, bool drop_sentinel, int shift, uint32_t dmask, int64_t num_chunks,
     const uint32_t* __restrict__ offsets, const uint32_t* __restrict__ totals, KeyT* __restrict__ keys_out,
@@ -241,13 +241,19 @@ __global__ __launch_bounds__(kDownThreads) void radix_downsweep_kernel(
         const int local = wave * kDownWaveKeys + r * kWave + lane;
         const bool valid = local < chunk_count && !(drop_sentinel && (uint64_t)key[r] == kSentinelKey);
         const uint32_t d = digit_of<kBits>(key[r], shift) & dmask;
-        uint64_t peers = wave_ballot(valid);
+        const uint64_t vm = wave_ballot(valid);
+        uint32_t plo = (uint32_t)vm, phi = (uint32_t)(vm >> 32);
 #pragma unroll
         for (int b = 0; b < kBits; ++b) {
-            const bool bit = ((d >> b) & 1u) != 0;
-            const uint64_t m = wave_ballot(bit);
-            peers &= bit ? m : ~m;
+            // the bit as 0 / all ones (a signed bit-field extract); the lanes that agree with this
+            // lane in bit b are ~(m ^ ext), one three-input bitwise operation per half
+            uint32_t ext = (uint32_t)((int32_t)(d << (31 - b)) >> 31);
+            asm volatile("" : "+v"(ext));  // the ballot compares the extracted bit itself
+            const uint64_t m = wave_ballot(ext != 0u);
+            plo &= ~((uint32_t)m ^ ext);
+            phi &= ~((uint32_t)(m >> 32) ^ ext);
         }
+        const uint64_t peers = (uint64_t)plo | ((uint64_t)phi << 32);
         const uint32_t before = s_cnt[wave][d];  // read by all lanes before the leader updates
         const uint32_t rank = (uint32_t)__popcll(peers & lt);
         if (valid && rank == 0) s_cnt[wave][d] = before + (uint32_t)__popcll(peers);
@@ -259,13 +265,9 @@ __global__ __launch_bounds__(kDownThreads) void radix_downsweep_kernel(
     //    and the digit's output position for this chunk
     {
         const int t = threadIdx.x;
-        uint32_t c[kDownWaves];
         uint32_t cnt = 0;
 #pragma unroll
-        for (int w = 0; w < kDownWaves; ++w) {
-            c[w] = t < kBins ? s_cnt[w][t] : 0u;
-            cnt += c[w];
-        }
+        for (int w = 0; w < kDownWaves; ++w) cnt += t < kBins ? s_cnt[w][t] : 0u;
         uint32_t kept, all_kept;
         const uint32_t start = digit_exclusive_scan<kBins>(cnt, s_wave, kept);
         const uint32_t digit_base = digit_exclusive_scan<kBins>(t < kBins ? my_total : 0u, s_wave, all_kept);
@@ -278,8 +280,9 @@ __global__ __launch_bounds__(kDownThreads) void radix_downsweep_kernel(
             uint32_t run = start;
 #pragma unroll
             for (int w = 0; w < kDownWaves; ++w) {
+                const uint32_t c = s_cnt[w][t];
                 s_cnt[w][t] = run;
-                run += c[w];
+                run += c;
             }
         }
     }
