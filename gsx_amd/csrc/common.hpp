@@ -350,6 +350,18 @@ __device__ inline uint32_t wave_append_slot(uint32_t* count, bool take) {
     return base + (uint32_t)__popcll(mask & lanemask_lt());
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave (DPP row shifts, then the two row broadcasts);
+// every lane must be active.
+__device__ inline uint32_t wave_inclusive_sum_u32(uint32_t v) {
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf, true);  // row_shr:1
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf, true);  // row_shr:2
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xf, true);  // row_shr:4
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xf, 0xf, true);  // row_shr:8
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false);  // row_bcast:15
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false);  // row_bcast:31
+    return v;
+}
+
 __device__ inline uint32_t wave_min_u32(uint32_t v) {
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {

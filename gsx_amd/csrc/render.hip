@@ -105,18 +105,6 @@ __device__ inline int wave_inclusive_max(int v) {
     return v;
 }
 
-// Inclusive prefix sum over the 64 lanes of a wave, the same DPP pattern; every lane must be
-// active.
-__device__ inline uint32_t wave_inclusive_sum_u32(uint32_t v) {
-    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf, true);
-    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf, true);
-    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xf, true);
-    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xf, 0xf, true);
-    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false);
-    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false);
-    return v;
-}
-
 // Stores lane's span constants and box (no rows when !valid) and returns the wave's total row
 // count.
 __device__ inline uint32_t stage_spans(WaveSpans& w, bool valid, float4 r0, float4 r1) {

@@ -127,35 +127,76 @@ __global__ __launch_bounds__(kSortThreads) void radix_upsweep_kernel(const KeyT*
 }
 
 // Workgroup d: exclusive scan of hist[d][0..num_chunks) into offsets[d][..], row total into
-// totals[d].
-__global__ __launch_bounds__(kSortThreads) void radix_rowscan_kernel(const uint32_t* __restrict__ hist,
-                                                                     int64_t num_chunks,
-                                                                     uint32_t* __restrict__ offsets,
-                                                                     uint32_t* __restrict__ totals) {
-    __shared__ uint32_t s_wave[kSortThreads / kWave];
+// totals[d]. A step covers kThreads * kRowItems counts; wave w takes the step's w-th run of
+// 64 * kRowItems, as kRowItems coalesced groups of 64 (one count per lane), each scanned with DPP
+// and carried into the next. The next step's counts are loaded before the current step's scan,
+// so the row's serial steps overlap their loads. Long rows (config 4's tile sort: 82k chunks) run
+// 1024 threads, short ones 256.
+template <int kThreads>
+__global__ __launch_bounds__(kThreads) void radix_rowscan_kernel(const uint32_t* __restrict__ hist,
+                                                                 int64_t num_chunks,
+                                                                 uint32_t* __restrict__ offsets,
+                                                                 uint32_t* __restrict__ totals) {
+    constexpr int kWaveRun = kWave * kRowItems;
+    constexpr int kStep = kThreads * kRowItems;
+    constexpr int kWaves = kThreads / kWave;
+    __shared__ uint32_t s_wave[kWaves];
     const uint32_t* row = hist + (int64_t)blockIdx.x * num_chunks;
     uint32_t* out = offsets + (int64_t)blockIdx.x * num_chunks;
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const int64_t first = (int64_t)wave * kWaveRun + lane;  // this lane's first count of a step
     uint32_t carry = 0;
-    for (int64_t base = 0; base < num_chunks; base += kRowChunk) {
-        uint32_t vals[kRowItems];
-        uint32_t sum = 0;
+    uint32_t next[kRowItems];
 #pragma unroll
-        for (int k = 0; k < kRowItems; ++k) {
-            const int64_t i = base + (int64_t)threadIdx.x * kRowItems + k;
-            vals[k] = i < num_chunks ? row[i] : 0u;
-            sum += vals[k];
+    for (int j = 0; j < kRowItems; ++j) {
+        const int64_t i = first + j * kWave;
+        next[j] = i < num_chunks ? row[i] : 0u;
+    }
+    for (int64_t base = 0; base < num_chunks; base += kStep) {
+        uint32_t excl[kRowItems];
+        uint32_t run = 0;
+#pragma unroll
+        for (int j = 0; j < kRowItems; ++j) {
+            const uint32_t v = next[j];
+            const uint32_t incl = wave_inclusive_sum_u32(v);
+            excl[j] = run + incl - v;
+            run += (uint32_t)__builtin_amdgcn_readlane((int)incl, kWave - 1);
         }
-        uint32_t total;
-        uint32_t prefix = block_exclusive_scan_256(sum, s_wave, total) + carry;
 #pragma unroll
-        for (int k = 0; k < kRowItems; ++k) {
-            const int64_t i = base + (int64_t)threadIdx.x * kRowItems + k;
-            if (i < num_chunks) out[i] = prefix;
-            prefix += vals[k];
+        for (int j = 0; j < kRowItems; ++j) {
+            const int64_t i = base + kStep + first + j * kWave;
+            next[j] = i < num_chunks ? row[i] : 0u;
+        }
+        if (lane == 0) s_wave[wave] = run;
+        __syncthreads();
+        uint32_t wave_base = carry, total = 0;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            const uint32_t sw = s_wave[w];
+            if (w < wave) wave_base += sw;
+            total += sw;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < kRowItems; ++j) {
+            const int64_t i = base + first + j * kWave;
+            if (i < num_chunks) out[i] = wave_base + excl[j];
         }
         carry += total;
     }
     if (threadIdx.x == 0) totals[blockIdx.x] = carry;
+}
+
+// Row scan launch for `bins` rows of num_chunks counts.
+inline void launch_rowscan(int bins, const uint32_t* hist, int64_t num_chunks, uint32_t* offsets, uint32_t* totals,
+                           hipStream_t stream) {
+    if (num_chunks > 4 * kRowChunk) {
+        hipLaunchKernelGGL(radix_rowscan_kernel<1024>, dim3(bins), dim3(1024), 0, stream, hist, num_chunks, offsets,
+                           totals);
+    } else {
+        hipLaunchKernelGGL(radix_rowscan_kernel<kSortThreads>, dim3(bins), dim3(kSortThreads), 0, stream, hist,
+                           num_chunks, offsets, totals);
+    }
 }
 
 // The downsweep runs 512 threads (8 waves of 512 keys, 8 rounds each): the serial ranking chain
@@ -356,8 +397,7 @@ gsx_hip_status radix_sort_u64(uint64_t* keys, uint32_t* vals, uint64_t* keys_alt
             if (!(first_hist_ready && shift == begin_bit))
                 hipLaunchKernelGGL((radix_upsweep_kernel<kBits, kChunk>), dim3((unsigned)chunks), dim3(kSortThreads),
                                    0, stream, kin, n, live, drop, shift, dmask, chunks, hist);
-            hipLaunchKernelGGL(radix_rowscan_kernel, dim3(kBins), dim3(kSortThreads), 0, stream, hist, chunks,
-                               offsets, totals);
+            launch_rowscan(kBins, hist, chunks, offsets, totals, stream);
             hipLaunchKernelGGL((radix_downsweep_kernel<kPairs, kBits, kChunk>), dim3((unsigned)chunks),
                                dim3(kDownThreads), 0, stream, kin, vin, n, live, drop, shift, dmask, chunks, offsets,
                                totals, kout, vout, drop ? n_dev : nullptr);
@@ -517,8 +557,7 @@ gsx_hip_status tile_sort_passes(const uint32_t* tiles, uint32_t* tiles_alt, uint
         const uint32_t dmask = width > 0 ? (1u << width) - 1u : 0u;
         hipLaunchKernelGGL((radix_upsweep_kernel<kBits, kDigitsChunk, uint32_t>), dim3((unsigned)chunks),
                            dim3(kSortThreads), 0, stream, kin, n, nullptr, false, shift, dmask, chunks, hist);
-        hipLaunchKernelGGL(radix_rowscan_kernel, dim3(kBins), dim3(kSortThreads), 0, stream, hist, chunks, offsets,
-                           totals);
+        launch_rowscan(kBins, hist, chunks, offsets, totals, stream);
         hipLaunchKernelGGL((radix_downsweep_kernel<true, kBits, kDigitsChunk, uint32_t>), dim3((unsigned)chunks),
                            dim3(kDownThreads), 0, stream, kin, vin, n, nullptr, false, shift, dmask, chunks, offsets,
                            totals, kout, vout, nullptr);
