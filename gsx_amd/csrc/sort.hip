@@ -42,32 +42,54 @@ __global__ __launch_bounds__(kScanThreads) void scan_reduce_kernel(const uint32_
 }
 
 // Single workgroup: exclusive scan of `count` partial sums in place; grand total at [count].
-// 16 values per thread and step (4096: the block sums of 1M ranks in one step), all loaded
-// before the first wait (positions past count re-read position 0 and count as 0).
+// A step covers 16 values per thread (4096: the block sums of 1M ranks in one step); wave w
+// takes the step's w-th run of 1024 as 16 coalesced groups of 64, each scanned with DPP, and the
+// next step's values are loaded before the current step's are written.
 constexpr int kPartialItems = 16;
 // Workgroup b scans the b-th of gridDim.x arrays of count + 1 entries laid out back to back.
 __global__ __launch_bounds__(kScanThreads) void scan_partials_kernel(uint32_t* __restrict__ partials, int64_t count) {
-    __shared__ uint32_t s_wave[kScanThreads / kWave];
+    constexpr int kWaves = kScanThreads / kWave;
+    constexpr int64_t kStep = (int64_t)kScanThreads * kPartialItems;
+    __shared__ uint32_t s_wave[kWaves];
     partials += (int64_t)blockIdx.x * (count + 1);
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const int64_t first = (int64_t)wave * kWave * kPartialItems + lane;
     uint32_t carry = 0;
-    for (int64_t base = 0; base < count; base += (int64_t)kScanThreads * kPartialItems) {
-        uint32_t vals[kPartialItems];
+    uint32_t next[kPartialItems];
 #pragma unroll
-        for (int k = 0; k < kPartialItems; ++k) {
-            const int64_t i = base + (int64_t)threadIdx.x * kPartialItems + k;
-            const uint32_t v = partials[i < count ? i : 0];
-            vals[k] = i < count ? v : 0u;
+    for (int j = 0; j < kPartialItems; ++j) {
+        const int64_t i = first + j * kWave;
+        next[j] = i < count ? partials[i] : 0u;
+    }
+    for (int64_t base = 0; base < count; base += kStep) {
+        uint32_t excl[kPartialItems];
+        uint32_t run = 0;
+#pragma unroll
+        for (int j = 0; j < kPartialItems; ++j) {
+            const uint32_t v = next[j];
+            const uint32_t incl = wave_inclusive_sum_u32(v);
+            excl[j] = run + incl - v;
+            run += (uint32_t)__builtin_amdgcn_readlane((int)incl, kWave - 1);
         }
-        uint32_t sum = 0;
 #pragma unroll
-        for (int k = 0; k < kPartialItems; ++k) sum += vals[k];
-        uint32_t total;
-        uint32_t prefix = block_exclusive_scan_256(sum, s_wave, total) + carry;
+        for (int j = 0; j < kPartialItems; ++j) {
+            const int64_t i = base + kStep + first + j * kWave;
+            next[j] = i < count ? partials[i] : 0u;
+        }
+        if (lane == 0) s_wave[wave] = run;
+        __syncthreads();
+        uint32_t wave_base = carry, total = 0;
 #pragma unroll
-        for (int k = 0; k < kPartialItems; ++k) {
-            const int64_t i = base + (int64_t)threadIdx.x * kPartialItems + k;
-            if (i < count) partials[i] = prefix;
-            prefix += vals[k];
+        for (int w = 0; w < kWaves; ++w) {
+            const uint32_t sw = s_wave[w];
+            if (w < wave) wave_base += sw;
+            total += sw;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < kPartialItems; ++j) {
+            const int64_t i = base + first + j * kWave;
+            if (i < count) partials[i] = wave_base + excl[j];
         }
         carry += total;
     }
