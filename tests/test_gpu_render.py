@@ -40,6 +40,9 @@ def _workloads():
         # 1080p with few Gaussians: five near-plane boxes cover all 8160 tiles (emitted in 1024-tile
         # chunks, their instance runs summed in 16 chunks), fifteen runs exceed 32 instances
         "c3_1080": lambda: scenes.config3(n=20_000, width=1920, height=1080),
+        # 4096 x 4096: 65536 tiles (16 tile bits, two 8-bit sort passes); near-plane boxes span
+        # 256 tile rows, so one box's rows take several steps of the row walks
+        "c3_4k": lambda: scenes.config3(n=6_000, width=4096, height=4096),
         # every Gaussian at depth exactly 4 (z = 0 facing the default camera): each tile's list is
         # ordered by Gaussian index alone, which the depth sort must keep through its compaction
         "ties": lambda: scenes.Workload("ties", scenes.plane_scene(5, 3_000, logscale=(-4.0, -3.0), z_sd=0.0),
@@ -93,7 +96,7 @@ def test_nonfinite_colour_stays_non_finite_and_the_rest_bit_exact(oracle):
     print(f"[nonfinite] CPU {int((~np.isfinite(ref)).sum())} pixels, HIP {int((~fin).sum())}", flush=True)
 
 
-@pytest.mark.parametrize("name", ["c0_small", "c3_small", "c4_small", "c3_1080", "ties"])
+@pytest.mark.parametrize("name", ["c0_small", "c3_small", "c4_small", "c3_1080", "c3_4k", "ties"])
 def test_sorted_keys_and_ranges_bit_exact(oracle, name):
     import ctypes
     w = _workloads()[name]()
