@@ -37,8 +37,8 @@ def _workloads():
         "c2_small": lambda: scenes.config2(n=20_000, size=128),
         "c3_small": lambda: scenes.config3(n=30_000, width=240, height=135),
         "c4_small": lambda: scenes.config4(n=3_000, width=160, height=96),
-        # 1080p with few Gaussians: five near-plane boxes cover all 8160 tiles (emitted in 1024-tile
-        # chunks, their instance runs summed in 16 chunks), fifteen runs exceed 32 instances
+        # 1080p with few Gaussians: five near-plane boxes cover all 8160 tiles (emitted by a wave
+        # each, their instance runs summed in 16 chunks), fifteen runs exceed 32 instances
         "c3_1080": lambda: scenes.config3(n=20_000, width=1920, height=1080),
         # 4096 x 4096: 65536 tiles (16 tile bits, two 8-bit sort passes); near-plane boxes span
         # 256 tile rows, so one box's rows take several steps of the row walks
