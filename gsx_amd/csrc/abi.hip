@@ -271,6 +271,11 @@ struct gsx_hip_render_context {
     DeviceBuffer snap, refresh_rgb;
     PinnedBuffer changed;
     hipEvent_t state_ev = nullptr;
+    // the comparison runs on a stream of its own (default priority), forked from the caller's
+    // stream at fork_ev, beside the backward: it reads HBM while the blend kernels are bound by
+    // their vector ALUs
+    hipStream_t check_stream = nullptr;
+    hipEvent_t fork_ev = nullptr;
     gsx_hip_gaussians live{};
     gsx_hip_camera camera{};
     int32_t train_mode = GSX_HIP_FORWARD_INFERENCE;
@@ -554,6 +559,8 @@ gsx_hip_status gsx_hip_render_context_create(gsx_hip_render_context** out_contex
     if (ctx == nullptr) return fail(GSX_HIP_ERROR_OUT_OF_MEMORY, "render context allocation failed");
     hipError_t e = hipEventCreateWithFlags(&ctx->count_ev, hipEventDisableTiming);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->state_ev, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->fork_ev, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->check_stream, hipStreamNonBlocking);
     if (e != hipSuccess) {
         (void)gsx_hip_render_context_destroy(ctx);
         return hip_fail(e, "render context creation");
@@ -578,6 +585,8 @@ gsx_hip_status gsx_hip_render_context_destroy(gsx_hip_render_context* ctx) {
     ctx->changed.release();
     if (ctx->count_ev != nullptr) (void)hipEventDestroy(ctx->count_ev);
     if (ctx->state_ev != nullptr) (void)hipEventDestroy(ctx->state_ev);
+    if (ctx->fork_ev != nullptr) (void)hipEventDestroy(ctx->fork_ev);
+    if (ctx->check_stream != nullptr) (void)hipStreamDestroy(ctx->check_stream);
     release_events(ctx);
     delete ctx;
     return GSX_HIP_SUCCESS;
@@ -954,9 +963,11 @@ gsx_hip_status gsx_hip_render_backward(gsx_hip_render_context* ctx, const float*
     }
     if (ctx->train_mode == GSX_HIP_FORWARD_TRAIN_BORROW && n > 0) {
         // borrowed state: the gradient is taken at the values the caller's arrays hold now. The
-        // comparison with the retained copy is queued first and the backward right behind it, so
+        // comparison with the retained copy runs on check_stream, after everything queued so far
+        // on the caller's stream, while the backward is queued on the caller's stream at once, so
         // the GPU does not wait for the host's look at the result; the backward writes only the
-        // context's scratch and the sinks, which a refresh overwrites.
+        // context's scratch and the sinks, which a refresh overwrites, and reads neither array
+        // the comparison reads.
         GSX_TRY(ctx->changed.reserve(sizeof(uint32_t), "train state flag"));
         volatile uint32_t* changed = static_cast<volatile uint32_t*>(ctx->changed.host);
         *changed = 0u;
@@ -966,10 +977,12 @@ gsx_hip_status gsx_hip_render_backward(gsx_hip_render_context* ctx, const float*
             arrays.snap[f] = const_cast<float*>(field_ptr(ctx->gs, f));
             arrays.count[f] = n * kFieldWidth[f];
         }
+        GSX_HIP_TRY(hipEventRecord(ctx->fork_ev, stream), "hipEventRecord(fork)");
+        GSX_HIP_TRY(hipStreamWaitEvent(ctx->check_stream, ctx->fork_ev, 0), "hipStreamWaitEvent(check)");
         hipLaunchKernelGGL(train_state_kernel, dim3(state_blocks(n), (unsigned)field_count(ctx->live)), dim3(256), 0,
-                           stream, arrays, static_cast<uint32_t*>(ctx->changed.dev));
+                           ctx->check_stream, arrays, static_cast<uint32_t*>(ctx->changed.dev));
         GSX_HIP_TRY(hipGetLastError(), "train_state_kernel");
-        GSX_HIP_TRY(hipEventRecord(ctx->state_ev, stream), "hipEventRecord(state)");
+        GSX_HIP_TRY(hipEventRecord(ctx->state_ev, ctx->check_stream), "hipEventRecord(state)");
         GSX_TRY(enqueue_backward(ctx, grad_rgb, grads, stream));
         GSX_HIP_TRY(hipEventSynchronize(ctx->state_ev), "train state sync");
         if (*changed != 0u) {
