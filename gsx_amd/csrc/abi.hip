@@ -920,8 +920,8 @@ gsx_hip_status enqueue_backward(gsx_hip_render_context* ctx, const float* grad_r
     hipLaunchKernelGGL(projection_backward_kernel<D>, dim3(pblocks), dim3(256), 0, stream, n, gs.mean3d, gs.rotation, \
                        gs.logscale, gs.opacity, gs.sh0, gs.sh1, gs.sh2, gs.sh3, cam, ctx->grad2d.as<float>(),        \
                        ctx->tile_count.as<uint32_t>(), ctx->g_rank.as<uint32_t>(), ctx->offsets.as<uint32_t>(),      \
-                       long_chunk, ctx->inst_grad.as<float>(), gi_op, grads->mean3d, grads->rotation,                  \
-                       grads->logscale, grads->opacity, grads->sh0, grads->sh1, grads->sh2, grads->sh3)
+                       long_chunk, ctx->inst_grad.as<float>(), gi_op, ctx->touched.as<uint8_t>(), grads->mean3d,      \
+                       grads->rotation, grads->logscale, grads->opacity, grads->sh0, grads->sh1, grads->sh2, grads->sh3)
         switch (gs.sh_degree) {
             case 0: GSX_PROJECTION_BACKWARD(0); break;
             case 1: GSX_PROJECTION_BACKWARD(1); break;

@@ -1255,7 +1255,8 @@ __global__ __launch_bounds__(256) void projection_backward_kernel(
     const float* __restrict__ sh1, const float* __restrict__ sh2, const float* __restrict__ sh3,
     CameraParams cam, const float* __restrict__ grad2d, const uint32_t* __restrict__ tile_count,
     const uint32_t* __restrict__ gaussian_rank, const uint32_t* __restrict__ offsets, uint32_t chunk,
-    const float* __restrict__ instance_grad, const float* __restrict__ instance_grad_op, float* __restrict__ g_mean3d,
+    const float* __restrict__ instance_grad, const float* __restrict__ instance_grad_op,
+    const uint8_t* __restrict__ touched, float* __restrict__ g_mean3d,
     float* __restrict__ g_rotation, float* __restrict__ g_logscale, float* __restrict__ g_opacity,
     float* __restrict__ g_sh0, float* __restrict__ g_sh1, float* __restrict__ g_sh2, float* __restrict__ g_sh3) {
     constexpr int sh_degree = kShDegree;
@@ -1267,10 +1268,17 @@ __global__ __launch_bounds__(256) void projection_backward_kernel(
     __builtin_assume(exp_tab != nullptr);  // no run-time choice of table per lookup
     const int64_t gi = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (gi >= n) return;
-    // issued first: its latency overlaps the recomputation below (only visible Gaussians use it)
-    const uint32_t run_length = tile_count[gi];
-    const Projected p =
-        preprocess_one(gi, mean3d, rotation, logscale, opacity, sh0, sh1, sh2, sh3, sh_degree, cam, true, exp_tab);
+    // a Gaussian that no tile's backward reached (touched[gi] == 0: invisible ones included) has
+    // a +0 screen-space gradient and so zero parameter gradients, written below as for an
+    // invisible one without recomputing its projection
+    Projected p{};
+    p.visible = false;
+    uint32_t run_length = 0;
+    if (touched[gi] != 0) {
+        // issued first: its latency overlaps the recomputation below
+        run_length = tile_count[gi];
+        p = preprocess_one(gi, mean3d, rotation, logscale, opacity, sh0, sh1, sh2, sh3, sh_degree, cam, true, exp_tab);
+    }
     float gm[3] = {0.0f, 0.0f, 0.0f};
     float gr[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     float gl[3] = {0.0f, 0.0f, 0.0f};
