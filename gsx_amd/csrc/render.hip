@@ -964,7 +964,8 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
 // depth rank; every Gaussian's sum is taken in a fixed order, so the result is deterministic.
 // Position p has a partial iff p < tile_cut[instance_tile[p]] (the blend backward's cut of p's
 // tile); the others count as +0, read from neither array. A Gaussian that no tile reached
-// (touched[g] == 0) has no partial at all: its sums are +0 without a look at its run.
+// (touched[g] == 0) has no partial at all: its sums are not formed, and projection_backward_kernel
+// writes its zero gradients without reading them.
 //  * runs of at most kLaneRun instances (reduce_short_block): the 64 runs of a wave's ranks are
 //    one contiguous span; the wave stages it through its own LDS piece by piece with coalesced
 //    loads, jumping over long runs, and each lane sums its run in position order into grad2d;
@@ -1068,24 +1069,9 @@ __device__ inline void reduce_run_chunk(uint32_t b, uint32_t e, uint32_t g, uint
 }
 
 // The +0 sums of chunk k of a long run that no tile reached, stored by one lane.
-__device__ inline void zero_run_chunk(uint32_t b, uint32_t e, uint32_t g, uint32_t k, uint32_t chunk,
-                                      float* __restrict__ instance_grad, float* __restrict__ instance_grad_op,
-                                      float* __restrict__ grad2d) {
-    if (e - b <= chunk) {
-#pragma unroll
-        for (int c = 0; c < kGrad2d; ++c) grad2d[(size_t)g * kGrad2d + c] = 0.0f;
-        return;
-    }
-    const uint32_t cb = b + k * chunk;
-    float4* dst = reinterpret_cast<float4*>(instance_grad) + 2 * (size_t)cb;
-    dst[0] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    dst[1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    instance_grad_op[cb] = 0.0f;
-}
-
 // Chunk k of the long runs of the wave's lanes (run [b, e) of Gaussian g where `live`): the
-// untouched ones get their +0 sums from their lanes, the touched ones are summed by the wave one
-// after another.
+// touched ones are summed by the wave one after another (the untouched ones have no sums: the
+// projection backward skips their Gaussians).
 __device__ inline void reduce_wave_long_runs(bool live, uint32_t b, uint32_t e, uint32_t g, uint32_t k,
                                              uint32_t chunk, float* __restrict__ instance_grad,
                                              float* __restrict__ instance_grad_op,
@@ -1093,7 +1079,6 @@ __device__ inline void reduce_wave_long_runs(bool live, uint32_t b, uint32_t e, 
                                              const uint32_t* __restrict__ tile_cut,
                                              const uint8_t* __restrict__ touched, float* __restrict__ grad2d) {
     const bool hit = live && touched[g] != 0;
-    if (live && !hit) zero_run_chunk(b, e, g, k, chunk, instance_grad, instance_grad_op, grad2d);
     for (uint64_t todo = __ballot(hit); todo != 0ull; todo &= todo - 1ull) {
         const int src = __builtin_ctzll(todo);
         reduce_run_chunk((uint32_t)__builtin_amdgcn_readlane((int)b, src),
@@ -1162,7 +1147,7 @@ __device__ inline void reduce_short_block(uint32_t blk, int64_t n, const uint32_
         }
         cur = p1;
     }
-    if (mine) {
+    if (has) {
 #pragma unroll
         for (int c = 0; c < kGrad2d; ++c) grad2d[(size_t)g * kGrad2d + c] = acc[c];
     }
