@@ -183,6 +183,9 @@ struct PinnedBuffer {
     }
 };
 
+// Instance counts from which the tile ranges come from a binary search per tile rather than a
+// pass over the sorted tiles (the search's cost does not grow with the count)
+constexpr int64_t kRangesSearchMin = (int64_t)1 << 25;
 // Workgroups of the long-run reduction (4 waves each, each wave 64 list entries at a time): for
 // chunk 0, which every long run has, and per later chunk.
 constexpr unsigned kLongRunBlocks0 = 1024;
@@ -848,7 +851,13 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
         ctx->sorted_vals = ctx->vals.as<uint32_t>();
     }
     GSX_TRY(record(ctx, 4, stream));
-    if (count > 0) {
+    if (count >= kRangesSearchMin) {
+        int steps = 0;
+        while (((uint64_t)1 << steps) <= (uint64_t)count) ++steps;  // ceil(log2(count + 1))
+        hipLaunchKernelGGL(tile_ranges_search_kernel, dim3(blocks_for(tiles, 256)), dim3(256), 0, stream,
+                           ctx->tiles_sorted.as<uint32_t>(), (uint32_t)count, (uint32_t)tiles, steps,
+                           ctx->ranges.as<uint2>());
+    } else if (count > 0) {
         hipLaunchKernelGGL(tile_ranges_kernel, dim3(blocks_for((count + 3) / 4, 256)), dim3(256), 0, stream,
                            ctx->tiles_sorted.as<uint32_t>(), ctx->offsets.as<uint32_t>() + n, (uint32_t)tiles,
                            ctx->ranges.as<uint2>());

@@ -550,6 +550,30 @@ __global__ __launch_bounds__(256) void tile_ranges_kernel(const uint32_t* __rest
     }
 }
 
+// The same ranges for large instance counts: one thread per tile finds the lower bounds of its
+// tile and of the next in the sorted tiles by binary search, the two searches in lockstep
+// (ceil(log2(count + 1)) steps of two loads each, the same for every lane) instead of a pass over
+// every instance. Tiles without instances get (0, 0).
+__global__ __launch_bounds__(256) void tile_ranges_search_kernel(const uint32_t* __restrict__ sorted_tiles,
+                                                                 uint32_t count, uint32_t tiles, int steps,
+                                                                 uint2* __restrict__ ranges) {
+    const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= tiles) return;
+    uint32_t lo0 = 0, hi0 = count, lo1 = 0, hi1 = count;
+    for (int k = 0; k < steps; ++k) {
+        const uint32_t m0 = lo0 + ((hi0 - lo0) >> 1), m1 = lo1 + ((hi1 - lo1) >> 1);
+        // both loads in flight (positions clamped into the array; a finished search keeps lo = hi)
+        const uint32_t v0 = sorted_tiles[min(m0, count - 1u)], v1 = sorted_tiles[min(m1, count - 1u)];
+        if (lo0 < hi0) {
+            if (v0 < t) lo0 = m0 + 1u; else hi0 = m0;
+        }
+        if (lo1 < hi1) {
+            if (v1 < t + 1u) lo1 = m1 + 1u; else hi1 = m1;
+        }
+    }
+    ranges[t] = lo0 < lo1 ? make_uint2(lo0, lo1) : make_uint2(0u, 0u);
+}
+
 // Workgroup -> tile mapping: consecutive workgroups are dealt round-robin to the 8 XCDs, so give
 // each XCD a contiguous band of tiles (neighbouring tiles share Gaussians, and each XCD has its
 // own L2).
