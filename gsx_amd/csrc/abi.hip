@@ -733,6 +733,11 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     const int depth_end_bit = std::min(64, index_bits + ctx->depth_sort_passes * kCompactingRadixBits);
     // big boxes are flagged in bit 63 of their depth key when the sort never reaches that bit
     const bool big_flag = depth_end_bit <= 63;
+    // the kept-tile count (at most `tiles`) rides in the bits above the sorted ones when they fit
+    // below the big-box flag; its field is never all ones, so no visible key is the all-ones key
+    // the depth sort drops
+    const int count_bits = bits_for((uint32_t)tiles + 1u);
+    const int count_shift = (big_flag && depth_end_bit + count_bits <= 63) ? depth_end_bit : 0;
 
     if (ctx->timing) {
         ctx->cur = (ctx->cur + 1) % ctx->ring;
@@ -768,7 +773,7 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
                            counters + 4,
                            static_cast<unsigned long long*>(ctx->kept_parts.dev), ctx->depth_keys.as<uint64_t>(),
                            near_bits,
-                           depth_max, index_bits, big_flag ? kBigKeyFlag : 0ull,
+                           depth_max, index_bits, big_flag ? kBigKeyFlag : 0ull, count_shift,
                            train ? ctx->touched.as<uint8_t>() : nullptr);
         GSX_HIP_TRY(hipGetLastError(), "preprocess_kernel");
         ctx->big_slot ^= 1;  // the slot this preprocess cleared
@@ -787,8 +792,8 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
                                                &depth_in_alt, stream, false));
         if (depth_in_alt) sorted_depth = ctx->depth_keys_alt.as<uint64_t>();
         hipLaunchKernelGGL(rank_gather_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, n, counters,
-                           sorted_depth, (uint64_t)((1ull << index_bits) - 1ull), big_flag,
-                           ctx->tile_count.as<uint32_t>(),
+                           sorted_depth, (uint64_t)((1ull << index_bits) - 1ull), big_flag, count_shift,
+                           (uint32_t)((1ull << count_bits) - 1ull), ctx->tile_count.as<uint32_t>(),
                            ctx->rank_g.as<uint32_t>(), ctx->rank_count.as<uint32_t>(), ctx->g_rank.as<uint32_t>(),
                            long_chunk_of(tiles),
                            ctx->multi_list.as<uint32_t>(), counters + 4, ctx->scan_temp.as<uint32_t>());

@@ -222,7 +222,7 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
     uint32_t* __restrict__ clear0, uint32_t* __restrict__ clear1, uint32_t* __restrict__ clear2,
     unsigned long long* __restrict__ kept_part,
     uint64_t* __restrict__ depth_keys, uint32_t depth_base, uint32_t depth_max, int index_bits,
-    uint64_t big_key_flag, uint8_t* __restrict__ touched) {
+    uint64_t big_key_flag, int count_shift, uint8_t* __restrict__ touched) {
     __shared__ WaveSpans s_spans[kWavesPerBlock];
     __shared__ uint32_t s_kept[kWavesPerBlock], s_big[kWavesPerBlock];
     WaveSpans& ws = s_spans[threadIdx.x / kWave];
@@ -279,17 +279,6 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
         }
     }
     const bool big = visible && box_tiles(r1) > kBigTiles;
-    // depth key of every Gaussian (~0 for invisible ones, which the depth sort drops);
-    // big_key_flag (kBigKeyFlag or 0, see there) marks the big boxes for rank_gather_kernel
-    if (g < n) {
-        uint64_t key = ~0ull;
-        if (visible) {
-            uint32_t rel = __float_as_uint(r2.w) - depth_base;
-            if (rel > depth_max) rel = depth_max;  // only for non-finite depths
-            key = ((uint64_t)rel << index_bits) | (uint64_t)g | (big ? big_key_flag : 0ull);
-        }
-        depth_keys[g] = key;
-    }
     // emitted by big_box_wave; one atomic per wave (a scene can hold millions of big boxes)
     const uint32_t big_slot = wave_append_slot(big_count, big);
     if (big) big_list[big_slot] = (uint32_t)g;
@@ -297,6 +286,20 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
     walk_wave_rows<false>(ws, rows, cam.tiles_x, nullptr, nullptr);
     const uint32_t kept = ws.kept[__lane_id()];
     if (g < n) tile_count[g] = kept;
+    // depth key of every Gaussian (~0 for invisible ones, which the depth sort drops);
+    // big_key_flag (kBigKeyFlag or 0, see there) marks the big boxes for rank_gather_kernel;
+    // count_shift > 0: the kept-tile count rides above the sorted bits, so rank_gather_kernel
+    // reads it from the sorted key instead of gathering tile_count at random Gaussians
+    if (g < n) {
+        uint64_t key = ~0ull;
+        if (visible) {
+            uint32_t rel = __float_as_uint(r2.w) - depth_base;
+            if (rel > depth_max) rel = depth_max;  // only for non-finite depths
+            key = ((uint64_t)rel << index_bits) | (uint64_t)g | (big ? big_key_flag : 0ull);
+            if (count_shift > 0) key |= (uint64_t)kept << count_shift;
+        }
+        depth_keys[g] = key;
+    }
     // the workgroup's kept tiles and big boxes to kept_part[block], host memory that the host
     // sums for the instance count and the big-box launch (a wave's kept sum is below 64 * 2^24
     // tiles, a workgroup's below 2^32 + 2^32, under the big count in bits 48..63)
@@ -338,6 +341,7 @@ constexpr uint32_t kLaneRun = 32;
 __global__ __launch_bounds__(256) void rank_gather_kernel(int64_t n, const uint32_t* __restrict__ depth_count,
                                                           const uint64_t* __restrict__ sorted_depth_keys,
                                                           uint64_t index_mask, bool flagged_only,
+                                                          int count_shift, uint32_t count_mask,
                                                           const uint32_t* __restrict__ tile_count,
                                                           uint32_t* __restrict__ rank_gaussian,
                                                           uint32_t* __restrict__ rank_count,
@@ -354,7 +358,7 @@ __global__ __launch_bounds__(256) void rank_gather_kernel(int64_t n, const uint3
         if (r < (int64_t)*depth_count) {
             const uint64_t key = sorted_depth_keys[r];
             const uint32_t g = (uint32_t)(key & index_mask);
-            c = tile_count[g];
+            c = count_shift > 0 ? (uint32_t)(key >> count_shift) & count_mask : tile_count[g];
             rank_gaussian[r] = g;
             if (!flagged_only || (key & kBigKeyFlag) != 0 || c > long_chunk) gaussian_rank[g] = (uint32_t)r;
         }
