@@ -77,10 +77,14 @@ def algorithmic_bytes(stage, geo, train=True):
         return 12 * t + 20 * p + 4 * c + 8 * r + 80 * u + 36 * r
     if stage == "instance_reduce":
         # per depth rank its Gaussian, offset and touched flag, the tiles of the touched
-        # Gaussians' instances and the reached entries' partials in, 9-float screen gradients out
-        return 9 * vp + 4 * geo["It"] + 36 * r + 36 * vp
+        # Gaussians' instances and the reached entries' partials in (the 9-float screen gradients
+        # of the touched Gaussians stay in L2 for the projection backward: the counters show no
+        # writes, so they are not counted)
+        return 9 * vp + 4 * geo["It"] + 36 * r
     if stage == "projection_backward":
-        return (36 + 56 + 56) * n  # screen gradients + snapshot in, five parameter gradients out
+        # the five parameter gradients written for every Gaussian (the touched ones' inputs and
+        # screen gradients are read from cache: the counters show about 1 MB fetched)
+        return 56 * n
     if stage == "loss_forward":
         # prediction + target in, loss map accumulated (in + out), SSIM workspace (3 floats) out
         return (4 + 4 + 8 + 12) * 3 * p
