@@ -375,6 +375,9 @@ gsx_hip_status snapshot_layout(gsx_hip_render_context* ctx, const gsx_hip_gaussi
     return GSX_HIP_SUCCESS;
 }
 
+// Workgroups per field array of the borrowed-state comparison, which runs beside the backward
+constexpr unsigned kCheckBlocks = 16;
+
 unsigned state_blocks(int64_t n) {
     // enough workgroups per array to fill the GPU, capped for small sets
     const int64_t b = (n * 3 + 1023) / 1024;
@@ -993,8 +996,11 @@ gsx_hip_status gsx_hip_render_backward(gsx_hip_render_context* ctx, const float*
         }
         GSX_HIP_TRY(hipEventRecord(ctx->fork_ev, stream), "hipEventRecord(fork)");
         GSX_HIP_TRY(hipStreamWaitEvent(ctx->check_stream, ctx->fork_ev, 0), "hipStreamWaitEvent(check)");
-        hipLaunchKernelGGL(train_state_kernel, dim3(state_blocks(n), (unsigned)field_count(ctx->live)), dim3(256), 0,
-                           ctx->check_stream, arrays, static_cast<uint32_t*>(ctx->changed.dev));
+        // few workgroups: the comparison needs a fraction of the HBM bandwidth to finish well inside
+        // the backward, and leaves the blend kernels their CU slots
+        hipLaunchKernelGGL(train_state_kernel, dim3(std::min(state_blocks(n), kCheckBlocks),
+                                                    (unsigned)field_count(ctx->live)),
+                           dim3(256), 0, ctx->check_stream, arrays, static_cast<uint32_t*>(ctx->changed.dev));
         GSX_HIP_TRY(hipGetLastError(), "train_state_kernel");
         GSX_HIP_TRY(hipEventRecord(ctx->state_ev, ctx->check_stream), "hipEventRecord(state)");
         GSX_TRY(enqueue_backward(ctx, grad_rgb, grads, stream));
