@@ -792,7 +792,7 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
         int depth_in_alt = 0;
         GSX_TRY(radix_sort_keys_u64_compacting(ctx->depth_keys.as<uint64_t>(), ctx->depth_keys_alt.as<uint64_t>(), n,
                                                counters, index_bits, depth_end_bit, ctx->depth_sort_temp.ptr,
-                                               &depth_in_alt, stream, false));
+                                               &depth_in_alt, stream));
         if (depth_in_alt) sorted_depth = ctx->depth_keys_alt.as<uint64_t>();
         hipLaunchKernelGGL(rank_gather_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, n, counters,
                            sorted_depth, (uint64_t)((1ull << index_bits) - 1ull), big_flag, count_shift,

@@ -511,6 +511,17 @@ constexpr int kChunkWaves = kSortThreads / kWave;  // 4 (upsweep)
 constexpr int kCompactingChunk = 1024;
 constexpr uint64_t kSentinelKey = ~0ull;  // dropped by a pass with drop_sentinel set
 
+// Workgroup -> sort chunk. Consecutive workgroups go round-robin to the 8 XCDs, so workgroup b
+// takes chunk (b % 8) * per + b / 8 (per = ceil(chunks / 8)): each XCD holds a contiguous band of
+// chunks, and what neighbouring chunks write next to each other (their counts in one histogram
+// row, their runs of one digit in the output) meets in the same L2 and leaves it as whole lines.
+// The grid has sort_chunk_grid(chunks) workgroups; those past the last chunk exit.
+__device__ inline int64_t sort_chunk_of(uint32_t block, int64_t chunks) {
+    const int64_t per = (chunks + 7) / 8;
+    return (int64_t)(block & 7u) * per + (int64_t)(block >> 3);
+}
+inline unsigned sort_chunk_grid(int64_t chunks) { return (unsigned)(8 * ((chunks + 7) / 8)); }
+
 template <int kBits, typename KeyT>
 __device__ inline uint32_t digit_of(KeyT key, int shift) {
     return (uint32_t)(key >> shift) & ((1u << kBits) - 1u);
@@ -561,12 +572,9 @@ __device__ inline void radix_upsweep_block(uint32_t blk, const KeyT* __restrict_
 // Its digits are kCompactingRadixBits wide (passes = ceil((end_bit - begin_bit) / 9)), and temp
 // holds radix_sort_keys_u64_compacting_temp_bytes(n) bytes.
 constexpr int kCompactingRadixBits = 9;
-// first_hist_ready: the first pass's digit counts are already in temp (radix_upsweep_block run
-// by the caller over every chunk: hist at the start of temp, [digit][chunk], ceil(n / 1024)
-// chunks), so that pass starts at its row scan.
 gsx_hip_status radix_sort_keys_u64_compacting(uint64_t* keys, uint64_t* keys_alt, int64_t n, uint32_t* n_live,
                                               int begin_bit, int end_bit, void* temp, int* out_in_alt,
-                                              hipStream_t stream, bool first_hist_ready);
+                                              hipStream_t stream);
 size_t radix_sort_keys_u64_compacting_temp_bytes(int64_t n);
 
 // Stable LSD radix sort of n u32 tile indices (bits [0, tile_bits)) with their input positions

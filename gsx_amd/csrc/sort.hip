@@ -144,7 +144,9 @@ __global__ __launch_bounds__(kSortThreads) void radix_upsweep_kernel(const KeyT*
                                                                      uint32_t dmask, int64_t num_chunks,
                                                                      uint32_t* __restrict__ hist) {
     __shared__ uint32_t s_hist[kChunkWaves][1 << kBits];
-    radix_upsweep_block<kBits, kChunk, KeyT>(blockIdx.x, keys, n, n_dev, drop_sentinel, shift, num_chunks, hist,
+    const int64_t chunk = sort_chunk_of(blockIdx.x, num_chunks);
+    if (chunk >= num_chunks) return;  // uniform
+    radix_upsweep_block<kBits, kChunk, KeyT>((uint32_t)chunk, keys, n, n_dev, drop_sentinel, shift, num_chunks, hist,
                                              s_hist, dmask);
 }
 
@@ -274,7 +276,9 @@ __global__ __launch_bounds__(kDownThreads, 8) void radix_downsweep_kernel(
     __shared__ uint32_t s_kept;                     // keys of the chunk that are moved
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
-    const int64_t base = (int64_t)blockIdx.x * kChunk;
+    const int64_t chunk = sort_chunk_of(blockIdx.x, num_chunks);
+    if (chunk >= num_chunks) return;  // uniform
+    const int64_t base = chunk * kChunk;
     if (n_dev != nullptr) n = min(n, (int64_t)*n_dev);
     if (base >= n) return;  // uniform: a chunk past the live count has nothing to move
     const int chunk_count = (int)min((int64_t)kChunk, n - base);
@@ -282,7 +286,7 @@ __global__ __launch_bounds__(kDownThreads, 8) void radix_downsweep_kernel(
     // re-read digit kBins - 1 and ignore it)
     const int td = min((int)threadIdx.x, kBins - 1);
     const uint32_t my_total = totals[td];
-    const uint32_t my_offset = offsets[(int64_t)td * num_chunks + blockIdx.x];
+    const uint32_t my_offset = offsets[(int64_t)td * num_chunks + chunk];
     for (int i = threadIdx.x; i < kDownWaves * kBins; i += kDownThreads) (&s_cnt[0][0])[i] = 0;
     __syncthreads();
     // 1. per wave: stable ranks among equal digits (rank = keys of the digit before it in this
@@ -336,7 +340,7 @@ __global__ __launch_bounds__(kDownThreads, 8) void radix_downsweep_kernel(
         const uint32_t digit_base = digit_exclusive_scan<kBins>(t < kBins ? my_total : 0u, s_wave, all_kept);
         if (t == 0) s_kept = kept;
         // the number of keys this pass keeps, for the later passes (a plain store: one writer)
-        if (kept_total != nullptr && blockIdx.x == 0 && t == 0) *kept_total = all_kept;
+        if (kept_total != nullptr && chunk == 0 && t == 0) *kept_total = all_kept;
         if (t < kBins) {
             s_local[t] = start;
             s_global[t] = digit_base + my_offset;
@@ -392,12 +396,10 @@ size_t radix_temp_bytes(int64_t n) {
 template <bool kPairs, int kBits, int kChunk>
 gsx_hip_status radix_sort_u64(uint64_t* keys, uint32_t* vals, uint64_t* keys_alt, uint32_t* vals_alt, int64_t n,
                               uint32_t* n_dev, bool compact_first, int begin_bit, int end_bit, void* temp,
-                              int* out_in_alt, hipStream_t stream, bool first_hist_ready = false) {
+                              int* out_in_alt, hipStream_t stream) {
     constexpr int kBins = 1 << kBits;
     if (begin_bit < 0 || end_bit > 64 || begin_bit > end_bit) return GSX_HIP_ERROR_INVALID_ARGUMENT;
     if (n > (int64_t)UINT32_MAX) return GSX_HIP_ERROR_OUT_OF_RANGE;
-    // precounted first-pass digits are full kBits digits
-    if (first_hist_ready && end_bit - begin_bit < kBits) return GSX_HIP_ERROR_INVALID_ARGUMENT;
     int64_t chunks = (n + kChunk - 1) / kChunk;
     if (chunks < 1) chunks = 1;
     const int64_t hist_count = chunks * kBins;
@@ -416,11 +418,10 @@ gsx_hip_status radix_sort_u64(uint64_t* keys, uint32_t* vals, uint64_t* keys_alt
             // the last pass may be narrower than kBits: bits at and above end_bit do not sort
             const int width = end_bit - shift < kBits ? end_bit - shift : kBits;
             const uint32_t dmask = (1u << width) - 1u;
-            if (!(first_hist_ready && shift == begin_bit))
-                hipLaunchKernelGGL((radix_upsweep_kernel<kBits, kChunk>), dim3((unsigned)chunks), dim3(kSortThreads),
-                                   0, stream, kin, n, live, drop, shift, dmask, chunks, hist);
+            hipLaunchKernelGGL((radix_upsweep_kernel<kBits, kChunk>), dim3(sort_chunk_grid(chunks)), dim3(kSortThreads),
+                               0, stream, kin, n, live, drop, shift, dmask, chunks, hist);
             launch_rowscan(kBins, hist, chunks, offsets, totals, stream);
-            hipLaunchKernelGGL((radix_downsweep_kernel<kPairs, kBits, kChunk>), dim3((unsigned)chunks),
+            hipLaunchKernelGGL((radix_downsweep_kernel<kPairs, kBits, kChunk>), dim3(sort_chunk_grid(chunks)),
                                dim3(kDownThreads), 0, stream, kin, vin, n, live, drop, shift, dmask, chunks, offsets,
                                totals, kout, vout, drop ? n_dev : nullptr);
             in_alt ^= 1;
@@ -549,11 +550,11 @@ gsx_hip_status scan_partials_in_place(uint32_t* partials, int64_t count, hipStre
 
 gsx_hip_status radix_sort_keys_u64_compacting(uint64_t* keys, uint64_t* keys_alt, int64_t n, uint32_t* n_live,
                                               int begin_bit, int end_bit, void* temp, int* out_in_alt,
-                                              hipStream_t stream, bool first_hist_ready) {
+                                              hipStream_t stream) {
     if (begin_bit >= end_bit) return GSX_HIP_ERROR_INVALID_ARGUMENT;  // the compacting pass must run
     return radix_sort_u64<false, kCompactingRadixBits, kCompactingChunk>(keys, nullptr, keys_alt, nullptr, n, n_live,
                                                                          true, begin_bit, end_bit, temp, out_in_alt,
-                                                                         stream, first_hist_ready);
+                                                                         stream);
 }
 
 template <int kBits>
@@ -577,10 +578,10 @@ gsx_hip_status tile_sort_passes(const uint32_t* tiles, uint32_t* tiles_alt, uint
         const int shift = k * kBits;
         const int width = tile_bits - shift < kBits ? tile_bits - shift : kBits;
         const uint32_t dmask = width > 0 ? (1u << width) - 1u : 0u;
-        hipLaunchKernelGGL((radix_upsweep_kernel<kBits, kDigitsChunk, uint32_t>), dim3((unsigned)chunks),
+        hipLaunchKernelGGL((radix_upsweep_kernel<kBits, kDigitsChunk, uint32_t>), dim3(sort_chunk_grid(chunks)),
                            dim3(kSortThreads), 0, stream, kin, n, nullptr, false, shift, dmask, chunks, hist);
         launch_rowscan(kBins, hist, chunks, offsets, totals, stream);
-        hipLaunchKernelGGL((radix_downsweep_kernel<true, kBits, kDigitsChunk, uint32_t>), dim3((unsigned)chunks),
+        hipLaunchKernelGGL((radix_downsweep_kernel<true, kBits, kDigitsChunk, uint32_t>), dim3(sort_chunk_grid(chunks)),
                            dim3(kDownThreads), 0, stream, kin, vin, n, nullptr, false, shift, dmask, chunks, offsets,
                            totals, kout, vout, nullptr);
         kin = kout;
