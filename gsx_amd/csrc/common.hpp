@@ -506,9 +506,10 @@ __device__ inline uint32_t block_exclusive_scan_256(uint32_t v, uint32_t* s_wave
 // ---- radix sort building blocks shared with render.hip (sort.hip holds the passes) ----------
 constexpr int kSortThreads = 256;
 constexpr int kChunkWaves = kSortThreads / kWave;  // 4 (upsweep)
-// The depth order sorts about a million keys: 1024-key chunks give ~1000 workgroups per launch
-// (with 4096 a launch has fewer workgroups than the GPU has CUs, one wave per SIMD)
-constexpr int kCompactingChunk = 1024;
+// The depth order sorts about a million keys: 2048-key chunks give ~500 workgroups per launch
+// (with 4096 a launch has fewer workgroups than the GPU has CUs, one wave per SIMD; 1024 doubles
+// the histogram and row-scan work for no gain in the passes)
+constexpr int kCompactingChunk = 2048;
 constexpr uint64_t kSentinelKey = ~0ull;  // dropped by a pass with drop_sentinel set
 
 // Workgroup -> sort chunk. Consecutive workgroups go round-robin to the 8 XCDs, so workgroup b

@@ -125,7 +125,7 @@ __global__ __launch_bounds__(kScanThreads) void scan_downsweep_kernel(const uint
 // ---------------------------------------------------------------------------------------------
 // One LSD pass on the kBits-bit digit at `shift` (8, or 9 for the compacting sort: 512 bins,
 // three passes for 27 depth bits), reduce-then-scan, three launches:
-//   upsweep: digit counts of each chunk (4096 keys, 1024 in the depth order) -> hist[digit][chunk]
+//   upsweep: digit counts of each chunk (4096 keys, 2048 in the depth order) -> hist[digit][chunk]
 //   rowscan: one workgroup per digit scans its row over the chunks    -> offsets, totals[digit]
 //   downsweep: 8 waves each rank an eighth of the chunk (rounds of 64 keys) stably with kBits
 //      ballots per round and wave-private digit counters; the chunk is then reordered by digit
