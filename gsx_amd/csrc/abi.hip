@@ -266,6 +266,9 @@ struct gsx_hip_render_context {
     // after count_ev
     PinnedBuffer kept_parts;
     hipEvent_t count_ev = nullptr;
+    // recorded on the forward's stream once the depth sort has stored the visible count
+    // (counters[0]); get_stats waits for it before reading the count
+    hipEvent_t stats_ev = nullptr;
     // Retained TRAIN state (gsx-cpu/render.c:263-380): the Gaussian fields as the forward read
     // them, copied into `snap`, which the backward reads (gs points into it). A borrowed state
     // also keeps the caller's arrays (`live`): the backward first compares them with `snap`
@@ -564,6 +567,7 @@ gsx_hip_status gsx_hip_render_context_create(gsx_hip_render_context** out_contex
     gsx_hip_render_context* ctx = new (std::nothrow) gsx_hip_render_context();
     if (ctx == nullptr) return fail(GSX_HIP_ERROR_OUT_OF_MEMORY, "render context allocation failed");
     hipError_t e = hipEventCreateWithFlags(&ctx->count_ev, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->stats_ev, hipEventDisableTiming);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->state_ev, hipEventDisableTiming);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->fork_ev, hipEventDisableTiming);
     if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->check_stream, hipStreamNonBlocking);
@@ -590,6 +594,7 @@ gsx_hip_status gsx_hip_render_context_destroy(gsx_hip_render_context* ctx) {
     ctx->kept_parts.release();
     ctx->changed.release();
     if (ctx->count_ev != nullptr) (void)hipEventDestroy(ctx->count_ev);
+    if (ctx->stats_ev != nullptr) (void)hipEventDestroy(ctx->stats_ev);
     if (ctx->state_ev != nullptr) (void)hipEventDestroy(ctx->state_ev);
     if (ctx->fork_ev != nullptr) (void)hipEventDestroy(ctx->fork_ev);
     if (ctx->check_stream != nullptr) (void)hipStreamDestroy(ctx->check_stream);
@@ -794,6 +799,7 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
                                                counters, index_bits, depth_end_bit, ctx->depth_sort_temp.ptr,
                                                &depth_in_alt, stream));
         if (depth_in_alt) sorted_depth = ctx->depth_keys_alt.as<uint64_t>();
+        GSX_HIP_TRY(hipEventRecord(ctx->stats_ev, stream), "hipEventRecord(stats)");
         hipLaunchKernelGGL(rank_gather_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, n, counters,
                            sorted_depth, (uint64_t)((1ull << index_bits) - 1ull), big_flag, count_shift,
                            (uint32_t)((1ull << count_bits) - 1ull), ctx->tile_count.as<uint32_t>(),
@@ -1034,8 +1040,11 @@ gsx_hip_status gsx_hip_render_context_get_stats(const gsx_hip_render_context* ct
     out->gaussian_count = ctx->gaussian_count;
     out->visible_count = 0;
     if (ctx->gaussian_count > 0 && ctx->counters_ready) {
-        // counters[0]: the depth sort's count of kept keys (a synchronous read)
+        // counters[0]: the depth sort's count of kept keys. The forward ran on the caller's
+        // stream, which may not be ordered with the null stream: wait for the event recorded
+        // after the sort, then read
         uint32_t visible = 0;
+        GSX_HIP_TRY(hipEventSynchronize(ctx->stats_ev), "visible count sync");
         GSX_HIP_TRY(hipMemcpy(&visible, ctx->counters.as<uint32_t>(), sizeof(visible), hipMemcpyDeviceToHost),
                     "read visible count");
         out->visible_count = visible;

@@ -22,6 +22,16 @@
  *
  * Every function here is pure IEEE arithmetic and must be compiled without floating-point
  * contraction (-ffp-contract=off): the explicit fma() calls are the only fused operations.
+ *
+ * Third-party notice. The lookup tables, polynomial coefficients, bit windows and reduction
+ * steps of expf, logf, sincosf and powf below follow Arm's optimized-routines
+ * (https://github.com/ARM-software/optimized-routines, math/), which carries:
+ *   Copyright (c) 2017-2024, Arm Limited.
+ *   SPDX-License-Identifier: MIT OR Apache-2.0 WITH LLVM-exception
+ * Those parts are used under the MIT licence; its terms travel with this notice: permission
+ * is granted to use, copy, modify, merge, publish, distribute, sublicense and/or sell copies,
+ * provided that the copyright notice and this permission notice are included in all copies or
+ * substantial portions; the software is provided "as is", without warranty of any kind.
  */
 #ifndef GSX_AMD_MATH_H
 #define GSX_AMD_MATH_H

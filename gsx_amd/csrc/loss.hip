@@ -8,7 +8,8 @@
 //     adds -(conv_mu + 2 p conv_s1 + t conv_s12) * grad_scale.
 // The CPU evaluates SSIM as a direct 2D sum in float64; here the window is applied as two
 // separable 11-tap passes of fused multiply-adds in float32 through LDS (32x16 output tile,
-// 42x26 halo), which is within 1e-5 of the float64 value on [0,1] images.
+// 42x26 halo) over inputs shifted by a per-tile value (against the cancellation in
+// E[x^2] - mu^2 on smooth images), which is within 1e-5 of the float64 value on [0,1] images.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -142,6 +143,16 @@ __global__ __launch_bounds__(kSsimTW * kSsimFwdTH / 2) void ssim_forward_kernel(
         }
     }
     __syncthreads();
+    // The moments are formed from inputs shifted by one value per image and tile (the tile's
+    // centre pixel): sigma^2 = E[x^2] - mu^2 loses the bits of E[x^2] to cancellation when mu is
+    // large and the window nearly flat, and variances and covariances do not change under a
+    // shift. The windows of the outputs that are kept (5 or more pixels from the edge) hold no
+    // padding, so shifting the padding's zeros changes only outputs the map and dm overwrite
+    // with 0. The means are the shifted means plus the shift. The shift pixel is the tile's
+    // centre clamped into the image (a partial last tile's centre can lie in the padding).
+    const int shift_hy = min(oy + kSsimTH / 2, height - 1) - oy + 5;
+    const int shift_hx = min(ox + kSsimTW / 2, width - 1) - ox + 5;
+    const float shift_p = s_in[0][shift_hy][shift_hx], shift_t = s_in[1][shift_hy][shift_hx];
     for (int i = threadIdx.x; i < kSsimHH * (kSsimTW / kHCols); i += kSsimThreads) {
         const int hy = i / (kSsimTW / kHCols), cx = kHCols * (i % (kSsimTW / kHCols));
         float a[kHCols][5];
@@ -151,7 +162,7 @@ __global__ __launch_bounds__(kSsimTW * kSsimFwdTH / 2) void ssim_forward_kernel(
             for (int c = 0; c < 5; ++c) a[j][c] = 0.0f;
 #pragma unroll
         for (int k = 0; k < 10 + kHCols; ++k) {
-            const float pv = s_in[0][hy][cx + k], tv = s_in[1][hy][cx + k];
+            const float pv = s_in[0][hy][cx + k] - shift_p, tv = s_in[1][hy][cx + k] - shift_t;
             const float m[5] = {pv, tv, pv * pv, tv * tv, pv * tv};
 #pragma unroll
             for (int j = 0; j < kHCols; ++j) {
@@ -184,10 +195,12 @@ __global__ __launch_bounds__(kSsimTW * kSsimFwdTH / 2) void ssim_forward_kernel(
         const int ly = ly0 + r;
         const int x = ox + lx, y = oy + ly;
         if (x >= width || y >= height) continue;
-        const float mu1 = mom[r][0], mu2 = mom[r][1], ex2 = mom[r][2], ey2 = mom[r][3], exy = mom[r][4];
+        // shifted moments: d1 = mu1 - shift_p, d2 = mu2 - shift_t, e.. = E[shifted products]
+        const float d1 = mom[r][0], d2 = mom[r][1], ex2 = mom[r][2], ey2 = mom[r][3], exy = mom[r][4];
+        const float mu1 = d1 + shift_p, mu2 = d2 + shift_t;
         const float c1 = 0.01f * 0.01f, c2 = 0.03f * 0.03f;
         const float m1s = mu1 * mu1, m2s = mu2 * mu2;
-        const float s1 = ex2 - m1s, s2 = ey2 - m2s, s12 = exy - mu1 * mu2;
+        const float s1 = ex2 - d1 * d1, s2 = ey2 - d2 * d2, s12 = exy - d1 * d2;
         const float a = m1s + m2s + c1;
         const float b = s1 + s2 + c2;
         const float ct = 2.0f * mu1 * mu2 + c1;

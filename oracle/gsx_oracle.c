@@ -703,6 +703,309 @@ static v3 v3_scale(v3 a, float s)
     return mk3(a.x * s, a.y * s, a.z * s);
 }
 
+/* The nine screen-space sums of one Gaussian's contributions (render.c:1603-1606): colour
+ * (3), mean2d (2), cov2d (3), opacity. */
+typedef struct screen_grad {
+    float dc[3];
+    float dm[2];
+    float dcov[3];
+    float dop;
+} screen_grad;
+
+/* Conic and d(conic)/d(cov2d) factors of one visible record (render.c:1590-1602). */
+typedef struct conic_terms {
+    float inv_a, inv_b, inv_c;
+    float ca, cb, cc, inv_det2;
+} conic_terms;
+
+static conic_terms conic_of(const float *r)
+{
+    conic_terms c;
+    float det;
+
+    c.ca = r[ORACLE_REC_COV_A];
+    c.cb = r[ORACLE_REC_COV_B];
+    c.cc = r[ORACLE_REC_COV_C];
+    c.inv_a = c.cc * r[ORACLE_REC_INV_DET];
+    c.inv_b = -c.cb * r[ORACLE_REC_INV_DET];
+    c.inv_c = c.ca * r[ORACLE_REC_INV_DET];
+    det = c.ca * c.cc - c.cb * c.cb;
+    c.inv_det2 = 1.0f / (det * det);
+    return c;
+}
+
+/* One contribution's terms of the nine sums (render.c:1608-1656), in the CPU's float
+ * expressions: out[0..2] colour, [3..4] mean2d, [5..7] cov2d, [8] opacity. Returns whether the
+ * opacity term applies (op * G below the alpha cap, render.c:1631-1634). s = the pixel's suffix
+ * (the colour behind this contribution). */
+static int contrib_terms(const float *r, const conic_terms *c, int32_t px, int32_t py, float dox, float doy,
+    float doz, float alpha, float tb, v3 s, float out[9])
+{
+    float dx = ((float)px + 0.5f) - r[ORACLE_REC_MEAN2D_X];
+    float dy = ((float)py + 0.5f) - r[ORACLE_REC_MEAN2D_Y];
+    float power = -0.5f * (c->inv_a * dx * dx + 2.0f * c->inv_b * dx * dy + c->inv_c * dy * dy);
+    float gv = expf(power > 0.0f ? 0.0f : power);
+    float wgt = alpha * tb;
+    float dalpha = tb * (r[ORACLE_REC_COLOR_R] * dox + r[ORACLE_REC_COLOR_G] * doy + r[ORACLE_REC_COLOR_B] * doz);
+    float dg = 0.0f, dpow, dia, dib, dic;
+    int op_ok = 0;
+
+    out[0] = wgt * dox;
+    out[1] = wgt * doy;
+    out[2] = wgt * doz;
+    if(fabsf(1.0f - alpha) > 1.0e-6f) {
+        dalpha -= (s.x * dox + s.y * doy + s.z * doz) / (1.0f - alpha);
+    }
+    out[8] = 0.0f;
+    if(r[ORACLE_REC_OPACITY] * gv < MAX_FRAGMENT_ALPHA) {
+        dg = dalpha * r[ORACLE_REC_OPACITY];
+        out[8] = dalpha * gv;
+        op_ok = 1;
+    }
+    dpow = dg * gv;
+    out[3] = dpow * (c->inv_a * dx + c->inv_b * dy);
+    out[4] = dpow * (c->inv_b * dx + c->inv_c * dy);
+    dia = dpow * (-0.5f * dx * dx);
+    dib = dpow * (-dx * dy);
+    dic = dpow * (-0.5f * dy * dy);
+    out[5] = dia * (-c->cc * c->cc * c->inv_det2) + dib * (c->cb * c->cc * c->inv_det2)
+        + dic * (-c->cb * c->cb * c->inv_det2);
+    out[6] = dia * (2.0f * c->cb * c->cc * c->inv_det2) + dib * (-(c->ca * c->cc + c->cb * c->cb) * c->inv_det2)
+        + dic * (2.0f * c->ca * c->cb * c->inv_det2);
+    out[7] = dia * (-c->cb * c->cb * c->inv_det2) + dib * (c->ca * c->cb * c->inv_det2)
+        + dic * (-c->ca * c->ca * c->inv_det2);
+    return op_ok;
+}
+
+/* Gradient sinks of a backward call. */
+typedef struct grad_sinks {
+    float *mean3d, *rotation, *logscale, *opacity, *sh0, *sh1, *sh2, *sh3;
+} grad_sinks;
+
+/* Parameter gradients of one visible Gaussian from its nine sums (render.c:1667-1969): colour
+ * clamp mask, SH and view-direction terms, opacity through the sigmoid, mean through the
+ * projection, cov2d -> cov3d -> scale and rotation (through the quaternion normalisation),
+ * and the Jacobian's dependence on the camera-space mean. Adds into the sinks. */
+static void project_grad_tail(const vis *e, const screen_grad *sg, int deg, const cam *kp, m3 w, v3 cc,
+    const float *mean3d, const float *rotation, const float *logscale, const float *sh1, const float *sh2,
+    const float *sh3, const grad_sinks *gs)
+{
+    const cam k = *kp;
+    const float *r = e->rec;
+    const int64_t gi = e->g;
+    const float dcx = sg->dc[0], dcy = sg->dc[1], dcz = sg->dc[2], dmx = sg->dm[0], dmy = sg->dm[1];
+    const float dca = sg->dcov[0], dcb = sg->dcov[1], dcc = sg->dcov[2], dop = sg->dop;
+    const float *q = rotation + gi * 4;
+    const float *ls = logscale + gi * 3;
+    m3 cov3d = cov3d_from(q, ls);
+    m3 rot = rotation_from_xyzw(q[0], q[1], q[2], q[3]);
+    m3 srot = rot;
+    m3 d_cov3d, d_rs, d_r, dsum;
+    float sx = expf(ls[0]), sy = expf(ls[1]), sz = expf(ls[2]);
+    float zc = r[ORACLE_REC_Z_CAM], xc = r[ORACLE_REC_X_CAM], yc = r[ORACLE_REC_Y_CAM];
+    float j00 = k.fx / zc;
+    float j02 = -k.fx * xc / (zc * zc);
+    float j11 = k.fy / zc;
+    float j12 = -k.fy * yc / (zc * zc);
+    float mm[2][3];
+    int row, col;
+    float *g_mean3d = gs->mean3d, *g_rotation = gs->rotation, *g_logscale = gs->logscale;
+    float *g_opacity = gs->opacity, *g_sh0 = gs->sh0, *g_sh1 = gs->sh1, *g_sh2 = gs->sh2, *g_sh3 = gs->sh3;
+
+    /* render.c:1667-1828: colour clamp mask, SH and view-direction gradients. */
+    {
+        v3 dcol = mk3(dcx * (r[ORACLE_REC_COLOR_R] > 0.0f ? 1.0f : 0.0f),
+            dcy * (r[ORACLE_REC_COLOR_G] > 0.0f ? 1.0f : 0.0f),
+            dcz * (r[ORACLE_REC_COLOR_B] > 0.0f ? 1.0f : 0.0f));
+        v3 ddir = mk3(0.0f, 0.0f, 0.0f);
+        float x = r[ORACLE_REC_DIR_X], y = r[ORACLE_REC_DIR_Y], z = r[ORACLE_REC_DIR_Z];
+        float xx = x * x, yy = y * y, zz = z * z, xy = x * y, yz = y * z, xz = x * z;
+
+        g_sh0[gi * 3 + 0] += SH_C0 * dcol.x;
+        g_sh0[gi * 3 + 1] += SH_C0 * dcol.y;
+        g_sh0[gi * 3 + 2] += SH_C0 * dcol.z;
+        if(deg >= 1 && g_sh1 != NULL) {
+            add_sh_grad(g_sh1, gi, 3, 0, v3_scale(dcol, -SH_C1 * y));
+            add_sh_grad(g_sh1, gi, 3, 1, v3_scale(dcol, SH_C1 * z));
+            add_sh_grad(g_sh1, gi, 3, 2, v3_scale(dcol, -SH_C1 * x));
+            add_dir_grad(&ddir, dcol, sh_coeff(sh1, gi, 3, 0), 0.0f, -SH_C1, 0.0f);
+            add_dir_grad(&ddir, dcol, sh_coeff(sh1, gi, 3, 1), 0.0f, 0.0f, SH_C1);
+            add_dir_grad(&ddir, dcol, sh_coeff(sh1, gi, 3, 2), -SH_C1, 0.0f, 0.0f);
+        }
+        if(deg >= 2 && g_sh2 != NULL) {
+            add_sh_grad(g_sh2, gi, 5, 0, v3_scale(dcol, k_sh_c2[0] * xy));
+            add_dir_grad(&ddir, dcol, sh_coeff(sh2, gi, 5, 0), k_sh_c2[0] * y, k_sh_c2[0] * x, 0.0f);
+            add_sh_grad(g_sh2, gi, 5, 1, v3_scale(dcol, k_sh_c2[1] * yz));
+            add_dir_grad(&ddir, dcol, sh_coeff(sh2, gi, 5, 1), 0.0f, k_sh_c2[1] * z, k_sh_c2[1] * y);
+            add_sh_grad(g_sh2, gi, 5, 2, v3_scale(dcol, k_sh_c2[2] * (2.0f * zz - xx - yy)));
+            add_dir_grad(&ddir, dcol, sh_coeff(sh2, gi, 5, 2), -2.0f * k_sh_c2[2] * x, -2.0f * k_sh_c2[2] * y,
+                4.0f * k_sh_c2[2] * z);
+            add_sh_grad(g_sh2, gi, 5, 3, v3_scale(dcol, k_sh_c2[3] * xz));
+            add_dir_grad(&ddir, dcol, sh_coeff(sh2, gi, 5, 3), k_sh_c2[3] * z, 0.0f, k_sh_c2[3] * x);
+            add_sh_grad(g_sh2, gi, 5, 4, v3_scale(dcol, k_sh_c2[4] * (xx - yy)));
+            add_dir_grad(&ddir, dcol, sh_coeff(sh2, gi, 5, 4), 2.0f * k_sh_c2[4] * x, -2.0f * k_sh_c2[4] * y, 0.0f);
+        }
+        if(deg >= 3 && g_sh3 != NULL) {
+            add_sh_grad(g_sh3, gi, 7, 0, v3_scale(dcol, k_sh_c3[0] * y * (3.0f * xx - yy)));
+            add_dir_grad(&ddir, dcol, sh_coeff(sh3, gi, 7, 0), 6.0f * k_sh_c3[0] * x * y,
+                3.0f * k_sh_c3[0] * (xx - yy), 0.0f);
+            add_sh_grad(g_sh3, gi, 7, 1, v3_scale(dcol, k_sh_c3[1] * xy * z));
+            add_dir_grad(&ddir, dcol, sh_coeff(sh3, gi, 7, 1), k_sh_c3[1] * y * z, k_sh_c3[1] * x * z,
+                k_sh_c3[1] * xy);
+            add_sh_grad(g_sh3, gi, 7, 2, v3_scale(dcol, k_sh_c3[2] * y * (4.0f * zz - xx - yy)));
+            add_dir_grad(&ddir, dcol, sh_coeff(sh3, gi, 7, 2), -2.0f * k_sh_c3[2] * x * y,
+                k_sh_c3[2] * (4.0f * zz - xx - 3.0f * yy), 8.0f * k_sh_c3[2] * y * z);
+            add_sh_grad(g_sh3, gi, 7, 3, v3_scale(dcol, k_sh_c3[3] * z * (2.0f * zz - 3.0f * xx - 3.0f * yy)));
+            add_dir_grad(&ddir, dcol, sh_coeff(sh3, gi, 7, 3), -6.0f * k_sh_c3[3] * x * z,
+                -6.0f * k_sh_c3[3] * y * z, k_sh_c3[3] * (6.0f * zz - 3.0f * xx - 3.0f * yy));
+            add_sh_grad(g_sh3, gi, 7, 4, v3_scale(dcol, k_sh_c3[4] * x * (4.0f * zz - xx - yy)));
+            add_dir_grad(&ddir, dcol, sh_coeff(sh3, gi, 7, 4), k_sh_c3[4] * (4.0f * zz - 3.0f * xx - yy),
+                -2.0f * k_sh_c3[4] * x * y, 8.0f * k_sh_c3[4] * x * z);
+            add_sh_grad(g_sh3, gi, 7, 5, v3_scale(dcol, k_sh_c3[5] * z * (xx - yy)));
+            add_dir_grad(&ddir, dcol, sh_coeff(sh3, gi, 7, 5), 2.0f * k_sh_c3[5] * x * z,
+                -2.0f * k_sh_c3[5] * y * z, k_sh_c3[5] * (xx - yy));
+            add_sh_grad(g_sh3, gi, 7, 6, v3_scale(dcol, k_sh_c3[6] * x * (xx - 3.0f * yy)));
+            add_dir_grad(&ddir, dcol, sh_coeff(sh3, gi, 7, 6), 3.0f * k_sh_c3[6] * (xx - yy),
+                -6.0f * k_sh_c3[6] * x * y, 0.0f);
+        }
+        if(deg >= 1) {
+            v3 view = mk3(mean3d[gi * 3 + 0] - cc.x, mean3d[gi * 3 + 1] - cc.y, mean3d[gi * 3 + 2] - cc.z);
+            float vn = sqrtf(view.x * view.x + view.y * view.y + view.z * view.z);
+
+            if(vn > 0.0f) {
+                float dd = ddir.x * x + ddir.y * y + ddir.z * z;
+                v3 dv = mk3(ddir.x - x * dd, ddir.y - y * dd, ddir.z - z * dd);
+                float s = 1.0f / vn;
+
+                g_mean3d[gi * 3 + 0] += dv.x * s;
+                g_mean3d[gi * 3 + 1] += dv.y * s;
+                g_mean3d[gi * 3 + 2] += dv.z * s;
+            }
+        }
+    }
+    /* render.c:1830 */
+    {
+        float sg = sigmoid_render(r[ORACLE_REC_RAW_OPACITY]);
+
+        g_opacity[gi] += dop * (sg * (1.0f - sg));
+    }
+    /* render.c:1832-1845 */
+    {
+        float inv_z = 1.0f / zc;
+        float inv_z2 = inv_z * inv_z;
+        v3 dmc = mk3(dmx * k.fx * inv_z, dmy * k.fy * inv_z,
+            dmx * (-k.fx * xc * inv_z2) + dmy * (-k.fy * yc * inv_z2));
+        v3 dmw = m3_v(m3_t(w), dmc);
+
+        g_mean3d[gi * 3 + 0] += dmw.x;
+        g_mean3d[gi * 3 + 1] += dmw.y;
+        g_mean3d[gi * 3 + 2] += dmw.z;
+    }
+    /* render.c:1847-1875 */
+    for(col = 0; col < 3; ++col) {
+        mm[0][col] = j00 * w.m[0][col] + j02 * w.m[2][col];
+        mm[1][col] = j11 * w.m[1][col] + j12 * w.m[2][col];
+    }
+    for(row = 0; row < 3; ++row) {
+        for(col = 0; col < 3; ++col) {
+            d_cov3d.m[row][col] = mm[0][row] * (dca * mm[0][col] + 0.5f * dcb * mm[1][col])
+                + mm[1][row] * (0.5f * dcb * mm[0][col] + dcc * mm[1][col]);
+        }
+    }
+    for(row = 0; row < 3; ++row) {
+        srot.m[row][0] *= sx;
+        srot.m[row][1] *= sy;
+        srot.m[row][2] *= sz;
+    }
+    for(row = 0; row < 3; ++row) {
+        for(col = 0; col < 3; ++col) {
+            dsum.m[row][col] = d_cov3d.m[row][col] + d_cov3d.m[col][row];
+        }
+    }
+    d_rs = m3_mul(dsum, srot);
+    g_logscale[gi * 3 + 0] += (d_rs.m[0][0] * rot.m[0][0] + d_rs.m[1][0] * rot.m[1][0] + d_rs.m[2][0] * rot.m[2][0]) * sx;
+    g_logscale[gi * 3 + 1] += (d_rs.m[0][1] * rot.m[0][1] + d_rs.m[1][1] * rot.m[1][1] + d_rs.m[2][1] * rot.m[2][1]) * sy;
+    g_logscale[gi * 3 + 2] += (d_rs.m[0][2] * rot.m[0][2] + d_rs.m[1][2] * rot.m[1][2] + d_rs.m[2][2] * rot.m[2][2]) * sz;
+    for(row = 0; row < 3; ++row) {
+        d_r.m[row][0] = d_rs.m[row][0] * sx;
+        d_r.m[row][1] = d_rs.m[row][1] * sy;
+        d_r.m[row][2] = d_rs.m[row][2] * sz;
+    }
+    /* render.c:1877-1937: through the quaternion normalisation. */
+    {
+        float nx, ny, nz, nw;
+
+        if(quat_normalize(q[0], q[1], q[2], q[3], &nx, &ny, &nz, &nw)) {
+            float inv_norm = 1.0f / sqrtf(q[0] * q[0] + q[1] * q[1] + q[2] * q[2] + q[3] * q[3]);
+            float dqw = 0.0f, dqx = 0.0f, dqy = 0.0f, dqz = 0.0f, dot;
+
+            dqw += d_r.m[0][1] * (-2.0f * nz);
+            dqw += d_r.m[0][2] * (2.0f * ny);
+            dqw += d_r.m[1][0] * (2.0f * nz);
+            dqw += d_r.m[1][2] * (-2.0f * nx);
+            dqw += d_r.m[2][0] * (-2.0f * ny);
+            dqw += d_r.m[2][1] * (2.0f * nx);
+
+            dqx += d_r.m[0][1] * (2.0f * ny);
+            dqx += d_r.m[0][2] * (2.0f * nz);
+            dqx += d_r.m[1][0] * (2.0f * ny);
+            dqx += d_r.m[1][1] * (-4.0f * nx);
+            dqx += d_r.m[1][2] * (-2.0f * nw);
+            dqx += d_r.m[2][0] * (2.0f * nz);
+            dqx += d_r.m[2][1] * (2.0f * nw);
+            dqx += d_r.m[2][2] * (-4.0f * nx);
+
+            dqy += d_r.m[0][0] * (-4.0f * ny);
+            dqy += d_r.m[0][1] * (2.0f * nx);
+            dqy += d_r.m[0][2] * (2.0f * nw);
+            dqy += d_r.m[1][0] * (2.0f * nx);
+            dqy += d_r.m[1][2] * (2.0f * nz);
+            dqy += d_r.m[2][0] * (-2.0f * nw);
+            dqy += d_r.m[2][1] * (2.0f * nz);
+            dqy += d_r.m[2][2] * (-4.0f * ny);
+
+            dqz += d_r.m[0][0] * (-4.0f * nz);
+            dqz += d_r.m[0][1] * (-2.0f * nw);
+            dqz += d_r.m[0][2] * (2.0f * nx);
+            dqz += d_r.m[1][0] * (2.0f * nw);
+            dqz += d_r.m[1][1] * (-4.0f * nz);
+            dqz += d_r.m[1][2] * (2.0f * ny);
+            dqz += d_r.m[2][0] * (2.0f * nx);
+            dqz += d_r.m[2][1] * (2.0f * ny);
+
+            dot = nx * dqx + ny * dqy + nz * dqz + nw * dqw;
+            g_rotation[gi * 4 + 0] += (dqx - nx * dot) * inv_norm;
+            g_rotation[gi * 4 + 1] += (dqy - ny * dot) * inv_norm;
+            g_rotation[gi * 4 + 2] += (dqz - nz * dot) * inv_norm;
+            g_rotation[gi * 4 + 3] += (dqw - nw * dot) * inv_norm;
+        }
+    }
+    /* render.c:1939-1969: the Jacobian's dependence on the camera-space mean. */
+    {
+        m3 cov_cam = m3_mul(m3_mul(w, cov3d), m3_t(w));
+        float dj[2][3];
+        float inv_z = 1.0f / zc;
+        float inv_z2 = inv_z * inv_z;
+        float inv_z3 = inv_z2 * inv_z;
+        v3 dmj, dmwj;
+
+        for(col = 0; col < 3; ++col) {
+            dj[0][col] = 2.0f * dca * (j00 * cov_cam.m[0][col] + j02 * cov_cam.m[2][col])
+                + dcb * (j11 * cov_cam.m[1][col] + j12 * cov_cam.m[2][col]);
+            dj[1][col] = dcb * (j00 * cov_cam.m[0][col] + j02 * cov_cam.m[2][col])
+                + 2.0f * dcc * (j11 * cov_cam.m[1][col] + j12 * cov_cam.m[2][col]);
+        }
+        dmj.x = dj[0][2] * (-k.fx * inv_z2);
+        dmj.y = dj[1][2] * (-k.fy * inv_z2);
+        dmj.z = dj[0][0] * (-k.fx * inv_z2) + dj[0][2] * (2.0f * k.fx * xc * inv_z3)
+            + dj[1][1] * (-k.fy * inv_z2) + dj[1][2] * (2.0f * k.fy * yc * inv_z3);
+        dmwj = m3_v(m3_t(w), dmj);
+        g_mean3d[gi * 3 + 0] += dmwj.x;
+        g_mean3d[gi * 3 + 1] += dmwj.y;
+        g_mean3d[gi * 3 + 2] += dmwj.z;
+    }
+}
+
 int oracle_render_backward(int64_t n, int deg, const float *mean3d, const float *rotation, const float *logscale,
     const float *opacity, const float *sh0, const float *sh1, const float *sh2, const float *sh3,
     const float *camera, const float *grad_rgb, float *g_mean3d, float *g_rotation, float *g_logscale,
@@ -719,6 +1022,7 @@ int oracle_render_backward(int64_t n, int deg, const float *mean3d, const float 
     contrib *contribs = NULL;
     int64_t count, vi, capacity = 0, total = 0;
     size_t p;
+    const grad_sinks gs = { g_mean3d, g_rotation, g_logscale, g_opacity, g_sh0, g_sh1, g_sh2, g_sh3 };
 
     if(v == NULL || t == NULL || suffix == NULL) {
         free(v);
@@ -791,72 +1095,29 @@ int oracle_render_backward(int64_t n, int deg, const float *mean3d, const float 
     for(vi = count; vi > 0; --vi) {
         const vis *e = &v[vi - 1];
         const float *r = e->rec;
-        int64_t gi = e->g;
-        float ca = r[ORACLE_REC_COV_A], cb = r[ORACLE_REC_COV_B], cc2 = r[ORACLE_REC_COV_C];
-        float inv_det = r[ORACLE_REC_INV_DET];
-        float inv_a = cc2 * inv_det;
-        float inv_b = -cb * inv_det;
-        float inv_c = ca * inv_det;
-        float det = ca * cc2 - cb * cb;
-        float inv_det2 = 1.0f / (det * det);
-        float dcx = 0.0f, dcy = 0.0f, dcz = 0.0f, dmx = 0.0f, dmy = 0.0f;
-        float dca = 0.0f, dcb = 0.0f, dcc = 0.0f, dop = 0.0f;
-        const float *q = rotation + gi * 4;
-        const float *ls = logscale + gi * 3;
-        m3 cov3d = cov3d_from(q, ls);
-        m3 rot = rotation_from_xyzw(q[0], q[1], q[2], q[3]);
-        m3 srot = rot;
-        m3 d_cov3d, d_rs, d_r, dsum;
-        float sx = expf(ls[0]), sy = expf(ls[1]), sz = expf(ls[2]);
-        float zc = r[ORACLE_REC_Z_CAM], xc = r[ORACLE_REC_X_CAM], yc = r[ORACLE_REC_Y_CAM];
-        float j00 = k.fx / zc;
-        float j02 = -k.fx * xc / (zc * zc);
-        float j11 = k.fy / zc;
-        float j12 = -k.fy * yc / (zc * zc);
-        float mm[2][3];
-        int row, col;
+        const conic_terms ct = conic_of(r);
+        screen_grad sg;
         int64_t ci;
 
+        memset(&sg, 0, sizeof(sg));
         /* render.c:1608-1656 */
         for(ci = offsets[vi - 1]; ci < offsets[vi]; ++ci) {
             const contrib *c = &contribs[ci];
             size_t pix = (size_t)c->pixel;
-            int32_t py = c->pixel / k.width;
-            int32_t px = c->pixel % k.width;
-            float dox = grad_rgb[0 * pixels + pix];
-            float doy = grad_rgb[1 * pixels + pix];
-            float doz = grad_rgb[2 * pixels + pix];
-            float dx = ((float)px + 0.5f) - r[ORACLE_REC_MEAN2D_X];
-            float dy = ((float)py + 0.5f) - r[ORACLE_REC_MEAN2D_Y];
-            float power = -0.5f * (inv_a * dx * dx + 2.0f * inv_b * dx * dy + inv_c * dy * dy);
-            float gv = expf(power > 0.0f ? 0.0f : power);
-            float alpha = c->alpha;
-            float tb = c->t_before;
-            float wgt = alpha * tb;
-            v3 s = suffix[pix];
-            float dalpha = tb * (r[ORACLE_REC_COLOR_R] * dox + r[ORACLE_REC_COLOR_G] * doy + r[ORACLE_REC_COLOR_B] * doz);
-            float dg = 0.0f, dpow, dia, dib, dic;
+            float t9[9];
 
-            dcx += wgt * dox;
-            dcy += wgt * doy;
-            dcz += wgt * doz;
-            if(fabsf(1.0f - alpha) > 1.0e-6f) {
-                dalpha -= (s.x * dox + s.y * doy + s.z * doz) / (1.0f - alpha);
+            if(contrib_terms(r, &ct, c->pixel % k.width, c->pixel / k.width, grad_rgb[0 * pixels + pix],
+                   grad_rgb[1 * pixels + pix], grad_rgb[2 * pixels + pix], c->alpha, c->t_before, suffix[pix], t9)) {
+                sg.dop += t9[8];
             }
-            if(r[ORACLE_REC_OPACITY] * gv < MAX_FRAGMENT_ALPHA) {
-                dg = dalpha * r[ORACLE_REC_OPACITY];
-                dop += dalpha * gv;
-            }
-            dpow = dg * gv;
-            dmx += dpow * (inv_a * dx + inv_b * dy);
-            dmy += dpow * (inv_b * dx + inv_c * dy);
-            dia = dpow * (-0.5f * dx * dx);
-            dib = dpow * (-dx * dy);
-            dic = dpow * (-0.5f * dy * dy);
-            dca += dia * (-cc2 * cc2 * inv_det2) + dib * (cb * cc2 * inv_det2) + dic * (-cb * cb * inv_det2);
-            dcb += dia * (2.0f * cb * cc2 * inv_det2) + dib * (-(ca * cc2 + cb * cb) * inv_det2)
-                + dic * (2.0f * ca * cb * inv_det2);
-            dcc += dia * (-cb * cb * inv_det2) + dib * (ca * cb * inv_det2) + dic * (-ca * ca * inv_det2);
+            sg.dc[0] += t9[0];
+            sg.dc[1] += t9[1];
+            sg.dc[2] += t9[2];
+            sg.dm[0] += t9[3];
+            sg.dm[1] += t9[4];
+            sg.dcov[0] += t9[5];
+            sg.dcov[1] += t9[6];
+            sg.dcov[2] += t9[7];
         }
         /* render.c:1658-1665 */
         for(ci = offsets[vi - 1]; ci < offsets[vi]; ++ci) {
@@ -867,198 +1128,7 @@ int oracle_render_backward(int64_t n, int deg, const float *mean3d, const float 
             suffix[pix].y += wgt * r[ORACLE_REC_COLOR_G];
             suffix[pix].z += wgt * r[ORACLE_REC_COLOR_B];
         }
-        /* render.c:1667-1828: colour clamp mask, SH and view-direction gradients. */
-        {
-            v3 dcol = mk3(dcx * (r[ORACLE_REC_COLOR_R] > 0.0f ? 1.0f : 0.0f),
-                dcy * (r[ORACLE_REC_COLOR_G] > 0.0f ? 1.0f : 0.0f),
-                dcz * (r[ORACLE_REC_COLOR_B] > 0.0f ? 1.0f : 0.0f));
-            v3 ddir = mk3(0.0f, 0.0f, 0.0f);
-            float x = r[ORACLE_REC_DIR_X], y = r[ORACLE_REC_DIR_Y], z = r[ORACLE_REC_DIR_Z];
-            float xx = x * x, yy = y * y, zz = z * z, xy = x * y, yz = y * z, xz = x * z;
-
-            g_sh0[gi * 3 + 0] += SH_C0 * dcol.x;
-            g_sh0[gi * 3 + 1] += SH_C0 * dcol.y;
-            g_sh0[gi * 3 + 2] += SH_C0 * dcol.z;
-            if(deg >= 1 && g_sh1 != NULL) {
-                add_sh_grad(g_sh1, gi, 3, 0, v3_scale(dcol, -SH_C1 * y));
-                add_sh_grad(g_sh1, gi, 3, 1, v3_scale(dcol, SH_C1 * z));
-                add_sh_grad(g_sh1, gi, 3, 2, v3_scale(dcol, -SH_C1 * x));
-                add_dir_grad(&ddir, dcol, sh_coeff(sh1, gi, 3, 0), 0.0f, -SH_C1, 0.0f);
-                add_dir_grad(&ddir, dcol, sh_coeff(sh1, gi, 3, 1), 0.0f, 0.0f, SH_C1);
-                add_dir_grad(&ddir, dcol, sh_coeff(sh1, gi, 3, 2), -SH_C1, 0.0f, 0.0f);
-            }
-            if(deg >= 2 && g_sh2 != NULL) {
-                add_sh_grad(g_sh2, gi, 5, 0, v3_scale(dcol, k_sh_c2[0] * xy));
-                add_dir_grad(&ddir, dcol, sh_coeff(sh2, gi, 5, 0), k_sh_c2[0] * y, k_sh_c2[0] * x, 0.0f);
-                add_sh_grad(g_sh2, gi, 5, 1, v3_scale(dcol, k_sh_c2[1] * yz));
-                add_dir_grad(&ddir, dcol, sh_coeff(sh2, gi, 5, 1), 0.0f, k_sh_c2[1] * z, k_sh_c2[1] * y);
-                add_sh_grad(g_sh2, gi, 5, 2, v3_scale(dcol, k_sh_c2[2] * (2.0f * zz - xx - yy)));
-                add_dir_grad(&ddir, dcol, sh_coeff(sh2, gi, 5, 2), -2.0f * k_sh_c2[2] * x, -2.0f * k_sh_c2[2] * y,
-                    4.0f * k_sh_c2[2] * z);
-                add_sh_grad(g_sh2, gi, 5, 3, v3_scale(dcol, k_sh_c2[3] * xz));
-                add_dir_grad(&ddir, dcol, sh_coeff(sh2, gi, 5, 3), k_sh_c2[3] * z, 0.0f, k_sh_c2[3] * x);
-                add_sh_grad(g_sh2, gi, 5, 4, v3_scale(dcol, k_sh_c2[4] * (xx - yy)));
-                add_dir_grad(&ddir, dcol, sh_coeff(sh2, gi, 5, 4), 2.0f * k_sh_c2[4] * x, -2.0f * k_sh_c2[4] * y, 0.0f);
-            }
-            if(deg >= 3 && g_sh3 != NULL) {
-                add_sh_grad(g_sh3, gi, 7, 0, v3_scale(dcol, k_sh_c3[0] * y * (3.0f * xx - yy)));
-                add_dir_grad(&ddir, dcol, sh_coeff(sh3, gi, 7, 0), 6.0f * k_sh_c3[0] * x * y,
-                    3.0f * k_sh_c3[0] * (xx - yy), 0.0f);
-                add_sh_grad(g_sh3, gi, 7, 1, v3_scale(dcol, k_sh_c3[1] * xy * z));
-                add_dir_grad(&ddir, dcol, sh_coeff(sh3, gi, 7, 1), k_sh_c3[1] * y * z, k_sh_c3[1] * x * z,
-                    k_sh_c3[1] * xy);
-                add_sh_grad(g_sh3, gi, 7, 2, v3_scale(dcol, k_sh_c3[2] * y * (4.0f * zz - xx - yy)));
-                add_dir_grad(&ddir, dcol, sh_coeff(sh3, gi, 7, 2), -2.0f * k_sh_c3[2] * x * y,
-                    k_sh_c3[2] * (4.0f * zz - xx - 3.0f * yy), 8.0f * k_sh_c3[2] * y * z);
-                add_sh_grad(g_sh3, gi, 7, 3, v3_scale(dcol, k_sh_c3[3] * z * (2.0f * zz - 3.0f * xx - 3.0f * yy)));
-                add_dir_grad(&ddir, dcol, sh_coeff(sh3, gi, 7, 3), -6.0f * k_sh_c3[3] * x * z,
-                    -6.0f * k_sh_c3[3] * y * z, k_sh_c3[3] * (6.0f * zz - 3.0f * xx - 3.0f * yy));
-                add_sh_grad(g_sh3, gi, 7, 4, v3_scale(dcol, k_sh_c3[4] * x * (4.0f * zz - xx - yy)));
-                add_dir_grad(&ddir, dcol, sh_coeff(sh3, gi, 7, 4), k_sh_c3[4] * (4.0f * zz - 3.0f * xx - yy),
-                    -2.0f * k_sh_c3[4] * x * y, 8.0f * k_sh_c3[4] * x * z);
-                add_sh_grad(g_sh3, gi, 7, 5, v3_scale(dcol, k_sh_c3[5] * z * (xx - yy)));
-                add_dir_grad(&ddir, dcol, sh_coeff(sh3, gi, 7, 5), 2.0f * k_sh_c3[5] * x * z,
-                    -2.0f * k_sh_c3[5] * y * z, k_sh_c3[5] * (xx - yy));
-                add_sh_grad(g_sh3, gi, 7, 6, v3_scale(dcol, k_sh_c3[6] * x * (xx - 3.0f * yy)));
-                add_dir_grad(&ddir, dcol, sh_coeff(sh3, gi, 7, 6), 3.0f * k_sh_c3[6] * (xx - yy),
-                    -6.0f * k_sh_c3[6] * x * y, 0.0f);
-            }
-            if(deg >= 1) {
-                v3 view = mk3(mean3d[gi * 3 + 0] - cc.x, mean3d[gi * 3 + 1] - cc.y, mean3d[gi * 3 + 2] - cc.z);
-                float vn = sqrtf(view.x * view.x + view.y * view.y + view.z * view.z);
-
-                if(vn > 0.0f) {
-                    float dd = ddir.x * x + ddir.y * y + ddir.z * z;
-                    v3 dv = mk3(ddir.x - x * dd, ddir.y - y * dd, ddir.z - z * dd);
-                    float s = 1.0f / vn;
-
-                    g_mean3d[gi * 3 + 0] += dv.x * s;
-                    g_mean3d[gi * 3 + 1] += dv.y * s;
-                    g_mean3d[gi * 3 + 2] += dv.z * s;
-                }
-            }
-        }
-        /* render.c:1830 */
-        {
-            float sg = sigmoid_render(r[ORACLE_REC_RAW_OPACITY]);
-
-            g_opacity[gi] += dop * (sg * (1.0f - sg));
-        }
-        /* render.c:1832-1845 */
-        {
-            float inv_z = 1.0f / zc;
-            float inv_z2 = inv_z * inv_z;
-            v3 dmc = mk3(dmx * k.fx * inv_z, dmy * k.fy * inv_z,
-                dmx * (-k.fx * xc * inv_z2) + dmy * (-k.fy * yc * inv_z2));
-            v3 dmw = m3_v(m3_t(w), dmc);
-
-            g_mean3d[gi * 3 + 0] += dmw.x;
-            g_mean3d[gi * 3 + 1] += dmw.y;
-            g_mean3d[gi * 3 + 2] += dmw.z;
-        }
-        /* render.c:1847-1875 */
-        for(col = 0; col < 3; ++col) {
-            mm[0][col] = j00 * w.m[0][col] + j02 * w.m[2][col];
-            mm[1][col] = j11 * w.m[1][col] + j12 * w.m[2][col];
-        }
-        for(row = 0; row < 3; ++row) {
-            for(col = 0; col < 3; ++col) {
-                d_cov3d.m[row][col] = mm[0][row] * (dca * mm[0][col] + 0.5f * dcb * mm[1][col])
-                    + mm[1][row] * (0.5f * dcb * mm[0][col] + dcc * mm[1][col]);
-            }
-        }
-        for(row = 0; row < 3; ++row) {
-            srot.m[row][0] *= sx;
-            srot.m[row][1] *= sy;
-            srot.m[row][2] *= sz;
-        }
-        for(row = 0; row < 3; ++row) {
-            for(col = 0; col < 3; ++col) {
-                dsum.m[row][col] = d_cov3d.m[row][col] + d_cov3d.m[col][row];
-            }
-        }
-        d_rs = m3_mul(dsum, srot);
-        g_logscale[gi * 3 + 0] += (d_rs.m[0][0] * rot.m[0][0] + d_rs.m[1][0] * rot.m[1][0] + d_rs.m[2][0] * rot.m[2][0]) * sx;
-        g_logscale[gi * 3 + 1] += (d_rs.m[0][1] * rot.m[0][1] + d_rs.m[1][1] * rot.m[1][1] + d_rs.m[2][1] * rot.m[2][1]) * sy;
-        g_logscale[gi * 3 + 2] += (d_rs.m[0][2] * rot.m[0][2] + d_rs.m[1][2] * rot.m[1][2] + d_rs.m[2][2] * rot.m[2][2]) * sz;
-        for(row = 0; row < 3; ++row) {
-            d_r.m[row][0] = d_rs.m[row][0] * sx;
-            d_r.m[row][1] = d_rs.m[row][1] * sy;
-            d_r.m[row][2] = d_rs.m[row][2] * sz;
-        }
-        /* render.c:1877-1937: through the quaternion normalisation. */
-        {
-            float nx, ny, nz, nw;
-
-            if(quat_normalize(q[0], q[1], q[2], q[3], &nx, &ny, &nz, &nw)) {
-                float inv_norm = 1.0f / sqrtf(q[0] * q[0] + q[1] * q[1] + q[2] * q[2] + q[3] * q[3]);
-                float dqw = 0.0f, dqx = 0.0f, dqy = 0.0f, dqz = 0.0f, dot;
-
-                dqw += d_r.m[0][1] * (-2.0f * nz);
-                dqw += d_r.m[0][2] * (2.0f * ny);
-                dqw += d_r.m[1][0] * (2.0f * nz);
-                dqw += d_r.m[1][2] * (-2.0f * nx);
-                dqw += d_r.m[2][0] * (-2.0f * ny);
-                dqw += d_r.m[2][1] * (2.0f * nx);
-
-                dqx += d_r.m[0][1] * (2.0f * ny);
-                dqx += d_r.m[0][2] * (2.0f * nz);
-                dqx += d_r.m[1][0] * (2.0f * ny);
-                dqx += d_r.m[1][1] * (-4.0f * nx);
-                dqx += d_r.m[1][2] * (-2.0f * nw);
-                dqx += d_r.m[2][0] * (2.0f * nz);
-                dqx += d_r.m[2][1] * (2.0f * nw);
-                dqx += d_r.m[2][2] * (-4.0f * nx);
-
-                dqy += d_r.m[0][0] * (-4.0f * ny);
-                dqy += d_r.m[0][1] * (2.0f * nx);
-                dqy += d_r.m[0][2] * (2.0f * nw);
-                dqy += d_r.m[1][0] * (2.0f * nx);
-                dqy += d_r.m[1][2] * (2.0f * nz);
-                dqy += d_r.m[2][0] * (-2.0f * nw);
-                dqy += d_r.m[2][1] * (2.0f * nz);
-                dqy += d_r.m[2][2] * (-4.0f * ny);
-
-                dqz += d_r.m[0][0] * (-4.0f * nz);
-                dqz += d_r.m[0][1] * (-2.0f * nw);
-                dqz += d_r.m[0][2] * (2.0f * nx);
-                dqz += d_r.m[1][0] * (2.0f * nw);
-                dqz += d_r.m[1][1] * (-4.0f * nz);
-                dqz += d_r.m[1][2] * (2.0f * ny);
-                dqz += d_r.m[2][0] * (2.0f * nx);
-                dqz += d_r.m[2][1] * (2.0f * ny);
-
-                dot = nx * dqx + ny * dqy + nz * dqz + nw * dqw;
-                g_rotation[gi * 4 + 0] += (dqx - nx * dot) * inv_norm;
-                g_rotation[gi * 4 + 1] += (dqy - ny * dot) * inv_norm;
-                g_rotation[gi * 4 + 2] += (dqz - nz * dot) * inv_norm;
-                g_rotation[gi * 4 + 3] += (dqw - nw * dot) * inv_norm;
-            }
-        }
-        /* render.c:1939-1969: the Jacobian's dependence on the camera-space mean. */
-        {
-            m3 cov_cam = m3_mul(m3_mul(w, cov3d), m3_t(w));
-            float dj[2][3];
-            float inv_z = 1.0f / zc;
-            float inv_z2 = inv_z * inv_z;
-            float inv_z3 = inv_z2 * inv_z;
-            v3 dmj, dmwj;
-
-            for(col = 0; col < 3; ++col) {
-                dj[0][col] = 2.0f * dca * (j00 * cov_cam.m[0][col] + j02 * cov_cam.m[2][col])
-                    + dcb * (j11 * cov_cam.m[1][col] + j12 * cov_cam.m[2][col]);
-                dj[1][col] = dcb * (j00 * cov_cam.m[0][col] + j02 * cov_cam.m[2][col])
-                    + 2.0f * dcc * (j11 * cov_cam.m[1][col] + j12 * cov_cam.m[2][col]);
-            }
-            dmj.x = dj[0][2] * (-k.fx * inv_z2);
-            dmj.y = dj[1][2] * (-k.fy * inv_z2);
-            dmj.z = dj[0][0] * (-k.fx * inv_z2) + dj[0][2] * (2.0f * k.fx * xc * inv_z3)
-                + dj[1][1] * (-k.fy * inv_z2) + dj[1][2] * (2.0f * k.fy * yc * inv_z3);
-            dmwj = m3_v(m3_t(w), dmj);
-            g_mean3d[gi * 3 + 0] += dmwj.x;
-            g_mean3d[gi * 3 + 1] += dmwj.y;
-            g_mean3d[gi * 3 + 2] += dmwj.z;
-        }
+        project_grad_tail(e, &sg, deg, &k, w, cc, mean3d, rotation, logscale, sh1, sh2, sh3, &gs);
     }
     free(contribs);
     free(offsets);
@@ -1992,3 +2062,225 @@ int64_t oracle_tiled(int64_t n, int sh_degree, const float *mean3d, const float 
 }
 
 void oracle_free(void *p) { free(p); }
+
+/* ---------------------------------------------------------------------------------------
+ * Tiled backward for full-size scenes (config 4: 6M Gaussians at 1080p, whose serial
+ * backward would record every box pixel of 2e11). Same per-contribution arithmetic as
+ * oracle_render_backward (render.c:1472-1969), reorganised per tile on all host cores:
+ *   - the tile lists of tiled_build (with the tile test: it drops only instances that no
+ *     pixel of the tile takes, so every pixel sees the same contributions as the CPU);
+ *   - per pixel, the CPU's re-raster (render.c:1476-1515) over its tile's list, recording
+ *     (entry, alpha, T_before) up to T < 1e-4 (the CPU's own test skips everything after);
+ *   - per pixel, back to front, each contribution's terms (contrib_terms, render.c:1608-1656)
+ *     with the pixel's suffix, which starts at T_final * bg and gains w * colour after each
+ *     contribution (render.c:1658-1665), as the CPU's Gaussian-major loop updates it;
+ *   - per Gaussian, its terms summed in double in a fixed order (tiles ascending, pixels in
+ *     row-major order within a tile), then rounded to float. The CPU sums the same terms in
+ *     float in box-raster order; the two sums differ only by the CPU's float rounding;
+ *   - the parameter gradients of every visible Gaussian through project_grad_tail.
+ * Per-pixel values (alpha, T_before, suffix, every term) equal the serial backward's bit for
+ * bit; the CPU tests compare the gradients with oracle_render_backward on scenes it finishes.
+ * ------------------------------------------------------------------------------------- */
+typedef struct tile_sums {
+    int64_t count;
+    uint32_t *entry;   /* position in the depth-ordered visible records */
+    double *sum;       /* [count][9] */
+} tile_sums;
+
+typedef struct tiled_pixel_contrib {
+    uint32_t e;        /* entry within the tile's list */
+    float alpha, tb;
+} tiled_pixel_contrib;
+
+int oracle_tiled_backward(int64_t n, int sh_degree, const float *mean3d, const float *rotation,
+    const float *logscale, const float *opacity, const float *sh0, const float *sh1, const float *sh2,
+    const float *sh3, const float *camera, int32_t tile, const float *grad_rgb, float *g_mean3d, float *g_rotation,
+    float *g_logscale, float *g_opacity, float *g_sh0, float *g_sh1, float *g_sh2, float *g_sh3)
+{
+    cam k = cam_from(camera);
+    m3 w = rotation_from_xyzw(k.qx, k.qy, k.qz, k.qw);
+    v3 cc = camera_centre(&k, w);
+    const size_t pixels = (size_t)k.width * (size_t)k.height;
+    const grad_sinks gs = { g_mean3d, g_rotation, g_logscale, g_opacity, g_sh0, g_sh1, g_sh2, g_sh3 };
+    tiled_lists tl;
+    tile_sums *ts = NULL;
+    double *gsum = NULL;
+    int64_t tiles, t, i;
+    int ok = 1;
+
+    if(tiled_build(n, sh_degree, mean3d, rotation, logscale, opacity, sh0, sh1, sh2, sh3, &k, tile, 1, &tl) != 0) {
+        return -1;
+    }
+    tiles = (int64_t)tl.tiles_x * tl.tiles_y;
+    ts = (tile_sums *)calloc((size_t)(tiles > 0 ? tiles : 1), sizeof(tile_sums));
+    gsum = (double *)calloc((size_t)(tl.count > 0 ? tl.count : 1) * 9u, sizeof(double));
+    if(ts == NULL || gsum == NULL) {
+        ok = 0;
+        goto done;
+    }
+
+#pragma omp parallel reduction(&& : ok)
+    {
+        double *acc = NULL;            /* [list length][9] per entry of the current tile */
+        uint8_t *hit = NULL;
+        tiled_pixel_contrib *pc = NULL;
+        int64_t cap = 0;
+
+#pragma omp for schedule(dynamic, 2)
+        for(t = 0; t < tiles; ++t) {
+            const int32_t tx = (int32_t)(t % tl.tiles_x), ty = (int32_t)(t / tl.tiles_x);
+            const int64_t e0 = tl.tile_start[t], len = tl.tile_start[t + 1] - e0;
+            int64_t zeroed = 0, j, m;
+            int32_t px, py;
+
+            if(!ok || len == 0) continue;
+            if(len > cap) {
+                free(acc);
+                free(hit);
+                free(pc);
+                cap = len;
+                acc = (double *)malloc(sizeof(double) * 9u * (size_t)cap);
+                hit = (uint8_t *)malloc((size_t)cap);
+                pc = (tiled_pixel_contrib *)malloc(sizeof(tiled_pixel_contrib) * (size_t)cap);
+                if(acc == NULL || hit == NULL || pc == NULL) {
+                    ok = 0;
+                    cap = 0;
+                    continue;
+                }
+            }
+            for(py = ty * tile; py < ty * tile + tile && py < k.height; ++py) {
+                for(px = tx * tile; px < tx * tile + tile && px < k.width; ++px) {
+                    const size_t pix = (size_t)py * (size_t)k.width + (size_t)px;
+                    const float dox = grad_rgb[0 * pixels + pix], doy = grad_rgb[1 * pixels + pix];
+                    const float doz = grad_rgb[2 * pixels + pix];
+                    float tt = 1.0f;
+                    int64_t nc = 0, q;
+                    v3 s;
+
+                    /* render.c:1476-1515 over the tile's list */
+                    for(j = 0; j < len; ++j) {
+                        const vis *g = &tl.v[tl.entries[e0 + j]];
+                        const float *r = g->rec;
+                        float inv_a, inv_b, inv_c, dx, dy, power, alpha;
+
+                        if(tt < T_THRESHOLD) break;
+                        if(px < g->bb[0] || px > g->bb[1] || py < g->bb[2] || py > g->bb[3]) continue;
+                        inv_a = r[ORACLE_REC_COV_C] * r[ORACLE_REC_INV_DET];
+                        inv_b = -r[ORACLE_REC_COV_B] * r[ORACLE_REC_INV_DET];
+                        inv_c = r[ORACLE_REC_COV_A] * r[ORACLE_REC_INV_DET];
+                        dx = ((float)px + 0.5f) - r[ORACLE_REC_MEAN2D_X];
+                        dy = ((float)py + 0.5f) - r[ORACLE_REC_MEAN2D_Y];
+                        power = -0.5f * (inv_a * dx * dx + 2.0f * inv_b * dx * dy + inv_c * dy * dy);
+                        if(power > 0.0f) power = 0.0f;
+                        if(power < POWER_THRESHOLD) continue;
+                        alpha = fminf(MAX_FRAGMENT_ALPHA, r[ORACLE_REC_OPACITY] * expf(power));
+                        if(alpha < MIN_ALPHA) continue;
+                        pc[nc].e = (uint32_t)j;
+                        pc[nc].alpha = alpha;
+                        pc[nc].tb = tt;
+                        nc += 1;
+                        tt = tt * (1.0f - alpha);
+                    }
+                    if(nc == 0) continue;
+                    for(; zeroed <= (int64_t)pc[nc - 1].e; ++zeroed) {
+                        memset(acc + 9 * zeroed, 0, sizeof(double) * 9u);
+                        hit[zeroed] = 0;
+                    }
+                    /* render.c:1547-1550 suffix start, then back to front */
+                    s = mk3(tt * k.bg[0], tt * k.bg[1], tt * k.bg[2]);
+                    for(q = nc; q > 0; --q) {
+                        const tiled_pixel_contrib *c = &pc[q - 1];
+                        const float *r = tl.v[tl.entries[e0 + c->e]].rec;
+                        const conic_terms ct = conic_of(r);
+                        double *a = acc + 9 * (int64_t)c->e;
+                        float t9[9], wgt;
+                        int op_ok = contrib_terms(r, &ct, px, py, dox, doy, doz, c->alpha, c->tb, s, t9);
+
+                        for(m = 0; m < 8; ++m) {
+                            a[m] += (double)t9[m];
+                        }
+                        if(op_ok) a[8] += (double)t9[8];
+                        hit[c->e] = 1;
+                        wgt = c->alpha * c->tb;
+                        s.x += wgt * r[ORACLE_REC_COLOR_R];
+                        s.y += wgt * r[ORACLE_REC_COLOR_G];
+                        s.z += wgt * r[ORACLE_REC_COLOR_B];
+                    }
+                }
+            }
+            /* the tile's reached entries, in list order */
+            {
+                int64_t nh = 0, o = 0;
+
+                for(j = 0; j < zeroed; ++j) nh += hit[j];
+                ts[t].count = nh;
+                if(nh == 0) continue;
+                ts[t].entry = (uint32_t *)malloc(sizeof(uint32_t) * (size_t)nh);
+                ts[t].sum = (double *)malloc(sizeof(double) * 9u * (size_t)nh);
+                if(ts[t].entry == NULL || ts[t].sum == NULL) {
+                    ok = 0;
+                    continue;
+                }
+                for(j = 0; j < zeroed; ++j) {
+                    if(!hit[j]) continue;
+                    ts[t].entry[o] = tl.entries[e0 + j];
+                    memcpy(ts[t].sum + 9 * o, acc + 9 * j, sizeof(double) * 9u);
+                    o += 1;
+                }
+            }
+        }
+        free(acc);
+        free(hit);
+        free(pc);
+    }
+    if(!ok) goto done;
+
+    /* per Gaussian, tiles ascending */
+    for(t = 0; t < tiles; ++t) {
+        int64_t j, m;
+
+        for(j = 0; j < ts[t].count; ++j) {
+            double *d = gsum + 9 * (int64_t)ts[t].entry[j];
+
+            for(m = 0; m < 9; ++m) {
+                d[m] += ts[t].sum[9 * j + m];
+            }
+        }
+    }
+
+    memset(g_mean3d, 0, sizeof(float) * 3u * (size_t)n);
+    memset(g_rotation, 0, sizeof(float) * 4u * (size_t)n);
+    memset(g_logscale, 0, sizeof(float) * 3u * (size_t)n);
+    memset(g_sh0, 0, sizeof(float) * 3u * (size_t)n);
+    memset(g_opacity, 0, sizeof(float) * (size_t)n);
+    if(sh_degree >= 1 && g_sh1 != NULL) memset(g_sh1, 0, sizeof(float) * 9u * (size_t)n);
+    if(sh_degree >= 2 && g_sh2 != NULL) memset(g_sh2, 0, sizeof(float) * 15u * (size_t)n);
+    if(sh_degree >= 3 && g_sh3 != NULL) memset(g_sh3, 0, sizeof(float) * 21u * (size_t)n);
+#pragma omp parallel for schedule(static)
+    for(i = 0; i < tl.count; ++i) {
+        const double *d = gsum + 9 * i;
+        screen_grad sg;
+
+        sg.dc[0] = (float)d[0];
+        sg.dc[1] = (float)d[1];
+        sg.dc[2] = (float)d[2];
+        sg.dm[0] = (float)d[3];
+        sg.dm[1] = (float)d[4];
+        sg.dcov[0] = (float)d[5];
+        sg.dcov[1] = (float)d[6];
+        sg.dcov[2] = (float)d[7];
+        sg.dop = (float)d[8];
+        project_grad_tail(&tl.v[i], &sg, sh_degree, &k, w, cc, mean3d, rotation, logscale, sh1, sh2, sh3, &gs);
+    }
+done:
+    if(ts != NULL) {
+        for(t = 0; t < tiles; ++t) {
+            free(ts[t].entry);
+            free(ts[t].sum);
+        }
+    }
+    free(ts);
+    free(gsum);
+    tiled_free(&tl);
+    return ok ? 0 : -1;
+}

@@ -89,6 +89,8 @@ class Oracle:
         lib.oracle_tiled.restype = _i64
         lib.oracle_tiled.argtypes = [_i64, ctypes.c_int] + [_vp] * 9 + [ctypes.c_int32, ctypes.c_int, _vp, _vp,
                                                                          _vp, _vp]
+        lib.oracle_tiled_backward.restype = ctypes.c_int
+        lib.oracle_tiled_backward.argtypes = [_i64, ctypes.c_int] + [_vp] * 9 + [ctypes.c_int32] + [_vp] * 9
         lib.oracle_free.argtypes = [_vp]
         self.lib = lib
 
@@ -176,6 +178,30 @@ class Oracle:
     def render_and_keys_tiled(self, scene, camera):
         out, t, k, v, _ = self._tiled(scene, camera, True, True, True)
         return out, t, k, v
+
+    @staticmethod
+    def _grad_sinks(scene):
+        n = scene.count
+        g = {"mean3d": np.zeros((n, 3), np.float32), "rotation": np.zeros((n, 4), np.float32),
+             "logscale": np.zeros((n, 3), np.float32), "opacity": np.zeros((n,), np.float32),
+             "sh0": np.zeros((n, 3), np.float32)}
+        for k, c in ((1, 3), (2, 5), (3, 7)):
+            if scene.sh_degree >= k:
+                g[f"sh{k}"] = np.zeros((n, c, 3), np.float32)
+        return g
+
+    def render_backward_tiled(self, scene, camera, grad_rgb, tile=16):
+        """The serial render_backward's gradients from per-tile walks on all host cores: the
+        same per-contribution terms, each Gaussian's terms summed in double (tiles ascending)
+        instead of the CPU's float sum in box-raster order."""
+        g = self._grad_sinks(scene)
+        rc = self.lib.oracle_tiled_backward(
+            scene.count, scene.sh_degree, *self._scene_args(scene), _p(camera), tile,
+            _p(np.ascontiguousarray(grad_rgb, dtype=np.float32)), _p(g["mean3d"]), _p(g["rotation"]),
+            _p(g["logscale"]), _p(g["opacity"]), _p(g["sh0"]), _p(g.get("sh1")), _p(g.get("sh2")), _p(g.get("sh3")))
+        if rc != 0:
+            raise MemoryError("oracle_tiled_backward failed")
+        return g
 
     def render_backward(self, scene, camera, grad_rgb):
         n = scene.count
@@ -304,13 +330,21 @@ class Reference:
 
     path = os.path.join(HERE, "_ref", "libgsxref.so")
     hip_path = os.path.join(HERE, "_ref", "libgsxref_hip.so")
+    hiptype_path = os.path.join(HERE, "_ref", "libgsxref_hiptype.so")
+    BACKEND_TYPE = {"cpu": 0, "cuda": 1, "metal": 2, "hip": 3}  # gsx_backend_type + GSX_BACKEND_TYPE_HIP
 
     @classmethod
-    def available(cls, hip: bool = False) -> bool:
-        return os.path.exists(cls.hip_path if hip else cls.path)
+    def available(cls, hip: bool = False, hip_type: bool = False) -> bool:
+        return os.path.exists(cls.hiptype_path if hip_type else (cls.hip_path if hip else cls.path))
 
-    def __init__(self, backend: str | None = None):
-        lib = ctypes.CDLL(self.path if backend is None else self.hip_path)
+    def __init__(self, backend: str | None = None, hip_type: bool = False):
+        """hip_type: load ``_ref/libgsxref_hiptype.so`` instead, where the plugin registers under
+        GSX_BACKEND_TYPE_HIP (a backend type of its own) and the CUDA slot stays empty;
+        ``backend="hip"`` then selects the HIP-type device."""
+        if hip_type:
+            lib = ctypes.CDLL(self.hiptype_path)
+        else:
+            lib = ctypes.CDLL(self.path if backend is None else self.hip_path)
         lib.gsxref_last_error.restype = ctypes.c_char_p
         lib.gsxref_reduce.restype = ctypes.c_int
         lib.gsxref_reduce.argtypes = [ctypes.c_int, ctypes.c_int, _vp, ctypes.c_int, _vp, _vp, _vp]
@@ -338,7 +372,24 @@ class Reference:
         lib.gsxref_adc.argtypes = [ctypes.c_int] + [_vp] * 10 + [ctypes.c_int, _vp] + [_vp] * 6
         lib.gsxref_train_step.restype = ctypes.c_int
         lib.gsxref_train_step.argtypes = [ctypes.c_int, ctypes.c_int] + [_vp] * 7 + [_f, _f, _vp, ctypes.c_int, _vp]
-        self.lib = lib if backend is None else _OnBackend(lib, {"cpu": 0, "hip": 1}[backend])
+        lib.gsxref_count_devices.restype = ctypes.c_int
+        lib.gsxref_count_devices.argtypes = [ctypes.c_int]
+        lib.gsxref_backend_type.restype = ctypes.c_int
+        lib.gsxref_backend_family_name.restype = ctypes.c_char_p
+        self._raw = lib
+        slots = {"cpu": 0, "hip": 2 if hip_type else 1}
+        self.lib = lib if backend is None else _OnBackend(lib, slots[backend])
+
+    def count_devices(self, backend_type: str) -> int:
+        """Registered devices of a backend type (gsx_count_backend_devices_by_type)."""
+        n = self._raw.gsxref_count_devices(self.BACKEND_TYPE[backend_type])
+        if n < 0:
+            raise RuntimeError(f"counting devices failed ({-n}): {self._raw.gsxref_last_error().decode()}")
+        return n
+
+    def backend_type(self) -> tuple:
+        """(gsx_backend_type value, backend family name) of the selected backend's device."""
+        return int(self.lib.gsxref_backend_type()), self.lib.gsxref_backend_family_name().decode()
 
     def device_name(self) -> str:
         return self.lib.gsxref_backend_device_name().decode()

@@ -29,6 +29,9 @@
 #include "gsx/gsx.h"
 #include "gsx/gsx-random.h"
 #include "gsx/extra/gsx-image.h"
+#ifdef GSXREF_HIP_TYPE
+#include "gsx_hip_type.h" /* HIP as a backend type of its own (libgsxref_hiptype.so) */
+#endif
 
 #include <stdint.h>
 #include <stdlib.h>
@@ -62,7 +65,12 @@ const char *gsxref_last_error(void) { return g_last_message != NULL ? g_last_mes
 
 static int ensure_backend(void)
 {
+#ifdef GSX_BACKEND_TYPE_HIP
+    /* built with gsx_hip_type.h: slot 2 is the HIP backend type of its own */
+    static const gsx_backend_type types[3] = { GSX_BACKEND_TYPE_CPU, GSX_BACKEND_TYPE_CUDA, GSX_BACKEND_TYPE_HIP };
+#else
     static const gsx_backend_type types[3] = { GSX_BACKEND_TYPE_CPU, GSX_BACKEND_TYPE_CUDA, GSX_BACKEND_TYPE_METAL };
+#endif
     gsx_backend_device_t device = NULL;
     gsx_backend_desc desc = { 0 };
     gsx_error e;
@@ -84,12 +92,53 @@ static int ensure_backend(void)
 }
 
 /* which: 0 the CPU backend, 1 the registry's GPU slot (GSX_BACKEND_TYPE_CUDA: in a build linked
- * with the HIP backend plugin, the MI355X backend registers there). */
+ * with the HIP backend plugin, the MI355X backend registers there), 2 GSX_BACKEND_TYPE_HIP (only
+ * in a build with gsx_hip_type.h, where the plugin registers under that type). */
 int gsxref_use_backend(int which)
 {
+#ifdef GSX_BACKEND_TYPE_HIP
+    if(which < 0 || which > 2) return (int)GSX_ERROR_OUT_OF_RANGE;
+#else
     if(which < 0 || which > 1) return (int)GSX_ERROR_OUT_OF_RANGE;
+#endif
     g_which = which;
     return ensure_backend();
+}
+
+/* Number of registered devices of a backend type (gsx_count_backend_devices_by_type), or a
+ * negative gsx error code. */
+int gsxref_count_devices(int backend_type)
+{
+    gsx_index_t count = 0;
+    gsx_error e = gsx_backend_registry_init();
+
+    if(!gsx_error_is_success(e)) { g_last_message = e.message; return -(int)e.code; }
+    e = gsx_count_backend_devices_by_type((gsx_backend_type)backend_type, &count);
+    if(!gsx_error_is_success(e)) { g_last_message = e.message; return -(int)e.code; }
+    return (int)count;
+}
+
+/* Backend type and family name of the device the selected backend runs on. */
+int gsxref_backend_type(void)
+{
+    gsx_backend_info info;
+    gsx_backend_device_info dinfo;
+
+    if(ensure_backend() != 0) return -1;
+    if(!gsx_error_is_success(gsx_backend_get_info(g_backend, &info))) return -1;
+    if(!gsx_error_is_success(gsx_backend_device_get_info(info.device, &dinfo))) return -1;
+    return (int)dinfo.backend_type;
+}
+
+const char *gsxref_backend_family_name(void)
+{
+    gsx_backend_info info;
+    gsx_backend_device_info dinfo;
+
+    if(ensure_backend() != 0) return "";
+    if(!gsx_error_is_success(gsx_backend_get_info(g_backend, &info))) return "";
+    if(!gsx_error_is_success(gsx_backend_device_get_info(info.device, &dinfo))) return "";
+    return dinfo.backend_name != NULL ? dinfo.backend_name : "";
 }
 
 /* Name of the device the selected backend runs on. */
@@ -1242,5 +1291,212 @@ done:
     FINISH();
     if(loader != NULL) (void)gsx_dataloader_free(loader);
     if(dataset != NULL) (void)gsx_dataset_free(dataset);
+    return rc;
+}
+
+/* ---- the session path (gsx-runtime.h: gsx_session_step) -------------------------------------
+ * `warmup` + `iters` steps of gsx_session_step on the selected backend, configured as
+ * image-fit-demo configures its session (apps/image_fit_demo.c:1286-1330): a one-image dataset
+ * served by gsx_dataloader (async prefetch of depth `prefetch` when > 0), L1 (w_l1) + SSIM
+ * (w_ssim) loss items, Adam over the five SH0 roles (hyper[0] mean3d, hyper[1] the others),
+ * borrowed train state, SH degree 0, no ADC, session-owned device workspace, and per-stage
+ * timings collected only when collect_timings is set (each timed stage then synchronises,
+ * gsx-runtime.c:629-684). target_hwc is the image as the dataset hands it over: [h, w, 3]
+ * float32. out_seconds[0] = wall-clock seconds of the `iters` timed steps (the major stream is
+ * drained before and after); out_stage_us[8] = the last step's report timings (dataloader,
+ * render fwd, loss fwd, loss bwd, render bwd, optim, adc, total), zeros without timings. The
+ * scene arrays are updated with the trained values. */
+typedef struct ref_one_image {
+    const float *camera;
+    const float *rgb;
+} ref_one_image;
+
+static gsx_error ref_one_length(void *object, gsx_size_t *out_length)
+{
+    (void)object;
+    *out_length = 1u;
+    return ref_ok();
+}
+
+static gsx_error ref_one_sample(void *object, gsx_size_t index, gsx_dataset_cpu_sample *out)
+{
+    const ref_one_image *d = (const ref_one_image *)object;
+    float near_plane, far_plane;
+    gsx_vec3 bg;
+
+    (void)index;
+    memset(out, 0, sizeof(*out));
+    unpack_camera(d->camera, &out->intrinsics, &out->pose, &near_plane, &far_plane, &bg);
+    out->rgb_data = d->rgb;
+    out->alpha_data = NULL;
+    return ref_ok();
+}
+
+int gsxref_session_fit(int n, int warmup, int iters, float *mean3d, float *rotation, float *logscale, float *opacity,
+    float *sh0, const float *camera, const float *target_hwc, float w_l1, float w_ssim, const float *hyper,
+    int collect_timings, int prefetch, double *out_seconds, double *out_stage_us)
+{
+    int rc = 0;
+    gsx_gs_t gs = NULL;
+    gsx_gs_desc gdesc = { 0 };
+    gsx_tensor_t t = NULL;
+    gsx_renderer_t renderer = NULL;
+    gsx_renderer_desc rdesc = { 0 };
+    gsx_loss_t l1 = NULL, ssim = NULL;
+    gsx_loss_context_t l1ctx = NULL, ssimctx = NULL;
+    gsx_loss_desc ldesc = { 0 };
+    gsx_optim_t optim = NULL;
+    gsx_optim_desc odesc = { 0 };
+    gsx_optim_param_group_desc groups[5];
+    gsx_dataset_desc ddesc = { 0 };
+    gsx_dataset_t dataset = NULL;
+    gsx_dataloader_desc dl = { 0 };
+    gsx_dataloader_t loader = NULL;
+    gsx_session_desc sdesc;
+    gsx_session_t session = NULL;
+    gsx_loss_item items[2];
+    gsx_session_step_report report;
+    ref_one_image image;
+    gsx_camera_intrinsics intr;
+    gsx_camera_pose pose;
+    float near_plane, far_plane;
+    gsx_vec3 bg;
+    const gsx_gs_field fields[5] = { GSX_GS_FIELD_MEAN3D, GSX_GS_FIELD_LOGSCALE, GSX_GS_FIELD_ROTATION,
+        GSX_GS_FIELD_OPACITY, GSX_GS_FIELD_SH0 };
+    const gsx_gs_field grad_fields[5] = { GSX_GS_FIELD_GRAD_MEAN3D, GSX_GS_FIELD_GRAD_LOGSCALE,
+        GSX_GS_FIELD_GRAD_ROTATION, GSX_GS_FIELD_GRAD_OPACITY, GSX_GS_FIELD_GRAD_SH0 };
+    const gsx_optim_param_role roles[5] = { GSX_OPTIM_PARAM_ROLE_MEAN3D, GSX_OPTIM_PARAM_ROLE_LOGSCALE,
+        GSX_OPTIM_PARAM_ROLE_ROTATION, GSX_OPTIM_PARAM_ROLE_OPACITY, GSX_OPTIM_PARAM_ROLE_SH0 };
+    double t0;
+    int k, it;
+
+    out_seconds[0] = 0.0;
+    for(k = 0; k < 8; ++k) out_stage_us[k] = 0.0;
+    rc = ensure_backend();
+    if(rc != 0) return rc;
+    unpack_camera(camera, &intr, &pose, &near_plane, &far_plane, &bg);
+    gdesc.buffer_type = g_device_type;
+    gdesc.count = (gsx_size_t)n;
+    gdesc.aux_flags = GSX_GS_AUX_NONE;
+    TRY(gsx_gs_init(&gs, &gdesc));
+    TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_MEAN3D, &t));
+    TRY(gsx_tensor_upload(t, mean3d, (gsx_size_t)n * 3u * sizeof(float)));
+    TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_ROTATION, &t));
+    TRY(gsx_tensor_upload(t, rotation, (gsx_size_t)n * 4u * sizeof(float)));
+    TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_LOGSCALE, &t));
+    TRY(gsx_tensor_upload(t, logscale, (gsx_size_t)n * 3u * sizeof(float)));
+    TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_OPACITY, &t));
+    TRY(gsx_tensor_upload(t, opacity, (gsx_size_t)n * sizeof(float)));
+    TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_SH0, &t));
+    TRY(gsx_tensor_upload(t, sh0, (gsx_size_t)n * 3u * sizeof(float)));
+    rdesc.width = intr.width;
+    rdesc.height = intr.height;
+    rdesc.output_data_type = GSX_DATA_TYPE_F32;
+    TRY(gsx_renderer_init(&renderer, g_backend, &rdesc));
+    ldesc.grad_normalization = GSX_LOSS_GRAD_NORMALIZATION_TYPE_MEAN;
+    ldesc.algorithm = GSX_LOSS_ALGORITHM_L1;
+    TRY(gsx_loss_init(&l1, g_backend, &ldesc));
+    TRY(gsx_loss_context_init(&l1ctx, l1));
+    ldesc.algorithm = GSX_LOSS_ALGORITHM_SSIM;
+    TRY(gsx_loss_init(&ssim, g_backend, &ldesc));
+    TRY(gsx_loss_context_init(&ssimctx, ssim));
+    memset(groups, 0, sizeof(groups));
+    for(k = 0; k < 5; ++k) {
+        TRY(gsx_gs_get_field(gs, fields[k], &groups[k].parameter));
+        TRY(gsx_gs_get_field(gs, grad_fields[k], &groups[k].gradient));
+        groups[k].role = roles[k];
+        groups[k].label = "g";
+        groups[k].learning_rate = k == 0 ? hyper[0] : hyper[1];
+        groups[k].beta1 = 0.9f;
+        groups[k].beta2 = 0.999f;
+        groups[k].epsilon = 1e-8f;
+    }
+    odesc.algorithm = GSX_OPTIM_ALGORITHM_ADAM;
+    odesc.param_groups = groups;
+    odesc.param_group_count = 5;
+    TRY(gsx_optim_init(&optim, g_backend, &odesc));
+    image.camera = camera;
+    image.rgb = target_hwc;
+    ddesc.name = "gsxref-session";
+    ddesc.object = &image;
+    ddesc.image_data_type = GSX_DATA_TYPE_F32;
+    ddesc.width = intr.width;
+    ddesc.height = intr.height;
+    ddesc.has_rgb = true;
+    ddesc.has_alpha = false;
+    ddesc.get_length = ref_one_length;
+    ddesc.get_sample = ref_one_sample;
+    ddesc.release_sample = ref_images_release;
+    TRY(gsx_dataset_init(&dataset, &ddesc));
+    dl.shuffle_each_epoch = false;
+    dl.enable_async_prefetch = prefetch > 0;
+    dl.prefetch_count = prefetch > 0 ? (gsx_size_t)prefetch : 0u;
+    dl.image_data_type = GSX_DATA_TYPE_F32;
+    TRY(gsx_dataloader_init(&loader, g_backend, dataset, &dl));
+    items[0].loss = l1;
+    items[0].context = l1ctx;
+    items[0].scale = w_l1;
+    items[1].loss = ssim;
+    items[1].context = ssimctx;
+    items[1].scale = w_ssim;
+    memset(&sdesc, 0, sizeof(sdesc));
+    sdesc.backend = g_backend;
+    sdesc.gs = gs;
+    sdesc.optim = optim;
+    sdesc.renderer = renderer;
+    sdesc.train_dataloader = loader;
+    sdesc.loss_count = 2;
+    sdesc.loss_items = items;
+    sdesc.render.near_plane = near_plane;
+    sdesc.render.far_plane = far_plane;
+    sdesc.render.background_color = bg;
+    sdesc.render.precision = GSX_RENDER_PRECISION_FLOAT32;
+    sdesc.render.sh_degree_mode = GSX_SESSION_SH_DEGREE_MODE_EXPLICIT;
+    sdesc.render.sh_degree = 0;
+    sdesc.render.borrow_train_state = true;
+    sdesc.optim_step.force_all = true;
+    sdesc.adc_step.enabled = false;
+    sdesc.workspace.buffer_type_class = GSX_BACKEND_BUFFER_TYPE_DEVICE;
+    sdesc.workspace.auto_plan = true;
+    sdesc.reporting.collect_timings = collect_timings != 0;
+    TRY(gsx_session_init(&session, &sdesc));
+    for(it = 0; it < warmup; ++it) TRY(gsx_session_step(session));
+    FINISH();
+    t0 = now_seconds();
+    for(it = 0; it < iters; ++it) TRY(gsx_session_step(session));
+    FINISH();
+    out_seconds[0] = now_seconds() - t0;
+    memset(&report, 0, sizeof(report));
+    TRY(gsx_session_get_last_step_report(session, &report));
+    out_stage_us[0] = report.timings.dataloader_us;
+    out_stage_us[1] = report.timings.render_forward_us;
+    out_stage_us[2] = report.timings.loss_forward_us;
+    out_stage_us[3] = report.timings.loss_backward_us;
+    out_stage_us[4] = report.timings.render_backward_us;
+    out_stage_us[5] = report.timings.optim_step_us;
+    out_stage_us[6] = report.timings.adc_step_us;
+    out_stage_us[7] = report.timings.total_step_us;
+    TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_MEAN3D, &t));
+    TRY(gsx_tensor_download(t, mean3d, (gsx_size_t)n * 3u * sizeof(float)));
+    TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_ROTATION, &t));
+    TRY(gsx_tensor_download(t, rotation, (gsx_size_t)n * 4u * sizeof(float)));
+    TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_LOGSCALE, &t));
+    TRY(gsx_tensor_download(t, logscale, (gsx_size_t)n * 3u * sizeof(float)));
+    TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_OPACITY, &t));
+    TRY(gsx_tensor_download(t, opacity, (gsx_size_t)n * sizeof(float)));
+    TRY(gsx_gs_get_field(gs, GSX_GS_FIELD_SH0, &t));
+    TRY(gsx_tensor_download(t, sh0, (gsx_size_t)n * 3u * sizeof(float)));
+done:
+    FINISH();
+    if(session != NULL) (void)gsx_session_free(session);
+    if(loader != NULL) (void)gsx_dataloader_free(loader);
+    if(dataset != NULL) (void)gsx_dataset_free(dataset);
+    if(optim != NULL) (void)gsx_optim_free(optim);
+    if(l1ctx != NULL) (void)gsx_loss_context_free(l1ctx);
+    if(ssimctx != NULL) (void)gsx_loss_context_free(ssimctx);
+    if(l1 != NULL) (void)gsx_loss_free(l1);
+    if(ssim != NULL) (void)gsx_loss_free(ssim);
+    if(renderer != NULL) (void)gsx_renderer_free(renderer);
+    if(gs != NULL) (void)gsx_gs_free(gs);
     return rc;
 }

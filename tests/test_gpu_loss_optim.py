@@ -43,7 +43,8 @@ def test_pointwise_losses_bit_exact(oracle, alg):
     assert np.array_equal(gm.cpu().numpy(), ref_grad)
 
 
-@pytest.mark.parametrize("shape", [(3, 64, 80), (2, 3, 33, 47), (3, 11, 12), (3, 1080 // 8, 1920 // 8)])
+@pytest.mark.parametrize("shape", [(3, 64, 80), (2, 3, 33, 47), (3, 11, 12), (3, 1080 // 8, 1920 // 8),
+                                   (3, 1080, 1920), (3, 1024, 1024)])
 def test_ssim_forward_backward(oracle, shape):
     from gsx_amd.backend import Loss
     p, t = _images(4, shape)
@@ -64,6 +65,34 @@ def test_ssim_forward_backward(oracle, shape):
     d = gm.cpu().numpy().astype(np.float64) - base_grad
     dr = ref_grad.astype(np.float64) - base_grad
     assert np.linalg.norm(d - dr) / max(np.linalg.norm(dr), 1e-30) <= SSIM_GRAD_TOL
+
+
+@pytest.mark.parametrize("shape", [(3, 1024, 1024), (3, 1080, 1920)])
+def test_ssim_smooth_images(oracle, shape):
+    """Smooth, low-variance images (the image-fit target and a slightly shifted copy, values
+    near 0.5): window variances are far below the means' squares, the case where a float32
+    E[x^2] - mu^2 cancels. Same bars as above, against the oracle's float64 SSIM."""
+    from gsx_amd import scenes
+    from gsx_amd.backend import Loss
+    c, h, w = shape
+    t = scenes.config2(n=1, size=max(h, w)).target[:, :h, :w].copy()
+    yy, xx = np.mgrid[0:h, 0:w].astype(np.float32)
+    p = np.clip(0.9 * t + 0.05 + 0.02 * np.sin(xx / 37.0 + yy / 53.0)[None], 0, 1).astype(np.float32)
+    base_map = np.zeros(shape, np.float32)
+    base_grad = np.zeros(shape, np.float32)
+    loss = Loss("ssim")
+    pm, gm = torch.from_numpy(base_map).cuda(), torch.from_numpy(base_grad).cuda()
+    loss.forward(torch.from_numpy(p).cuda(), torch.from_numpy(t).cuda(), pm, 0.2)
+    loss.backward(gm, 0.2)
+    torch.cuda.synchronize()
+    ref_map, ref_grad = base_map.copy(), base_grad.copy()
+    oracle.loss("ssim", p, t, 0.2, ref_map, ref_grad)
+    map_err = float(np.abs(pm.cpu().numpy() - ref_map).max())
+    g = gm.cpu().numpy().astype(np.float64)
+    grad_err = np.linalg.norm(g - ref_grad) / max(np.linalg.norm(ref_grad), 1e-30)
+    print(f"[ssim smooth {shape}] map max-abs {map_err:.2e}, grad rel L2 {grad_err:.2e}", flush=True)
+    assert map_err <= SSIM_MAP_TOL
+    assert grad_err <= SSIM_GRAD_TOL
 
 
 def test_ssim_identical_images_zero_interior():

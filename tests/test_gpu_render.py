@@ -330,3 +330,27 @@ def test_background_only_pixels(oracle):
     img = r.render(cam, g).cpu().numpy()
     ref = oracle.render(w.scene, cam_block)[0]
     assert np.array_equal(img, ref)
+
+
+def test_stats_right_after_forward_on_a_side_stream(oracle):
+    """get_stats called straight after a forward queued on a non-blocking stream (no host wait in
+    between) reports that forward's visible count: two scenes with different counts, rendered one
+    after the other by one context, each against the oracle's count of Gaussians that pass the
+    culls (gsx-cpu/render.c:850-1016)."""
+    from gsx_amd import scenes
+    from gsx_amd.backend import Camera, GaussianTensors, Renderer
+    side = torch.cuda.Stream()
+    works = [scenes.config1(n=40_000, width=320, height=180), scenes.config1(n=9_000, width=320, height=180)]
+    expected = [len(oracle.preprocess(w.scene, w.camera)[0]) for w in works]
+    assert expected[0] != expected[1]
+    r = Renderer(320, 180)
+    for w, want in zip(works + works, expected + expected):
+        cam = Camera.from_block(w.camera)
+        g = GaussianTensors.from_scene(w.scene)
+        torch.cuda.synchronize()
+        print(f"[case] stats after forward n={w.scene.count} on a side stream", flush=True)
+        with torch.cuda.stream(side):
+            r.render(cam, g, train=True, stream=side)
+            got = r.stats().visible_count
+        assert got == want
+    torch.cuda.synchronize()

@@ -446,6 +446,30 @@ def test_tiled_oracle_matches_serial(oracle, name, kw):
     assert np.array_equal(k, k2) and np.array_equal(v, v2)
     img3, t3, k3, v3 = oracle.render_and_keys_tiled(w.scene, w.camera)
     assert np.array_equal(img3, img) and np.array_equal(k3, k)
+    _check_tiled_backward(oracle, w.scene, w.camera)
+
+
+# The tiled backward sums each Gaussian's terms in double, the serial one (bit-exact with the
+# reference CPU backend) in float in box-raster order; the difference is the CPU's float
+# summation error, measured below 4e-5 on these scenes. A dropped term, a wrong suffix or a
+# misplaced pixel moves a field by orders of magnitude more.
+TILED_BACKWARD_TOL = 1e-4
+
+
+def _check_tiled_backward(oracle, scene, camera):
+    h, w = int(camera[5]), int(camera[4])
+    grad_rgb = np.random.default_rng(3).standard_normal((3, h, w)).astype(np.float32)
+    ref = oracle.render_backward(scene, camera, grad_rgb)
+    got = oracle.render_backward_tiled(scene, camera, grad_rgb)
+    assert set(got) == set(ref)
+    for k in ref:
+        a = ref[k].astype(np.float64).ravel()
+        d = np.linalg.norm(got[k].astype(np.float64).ravel() - a) / max(np.linalg.norm(a), 1e-30)
+        assert d <= TILED_BACKWARD_TOL, (k, d)
+        # the same Gaussians (invisible, or visible with no contribution) get all-zero rows
+        rows_ref = (ref[k].reshape(len(ref[k]), -1) == 0).all(axis=1)
+        rows_got = (got[k].reshape(len(got[k]), -1) == 0).all(axis=1)
+        assert np.array_equal(rows_ref, rows_got), k
 
 
 def test_tiled_oracle_sh3_and_empty(oracle):
@@ -460,6 +484,7 @@ def test_tiled_oracle_sh3_and_empty(oracle):
     img, t = oracle.render(sc, w.camera)
     img2, t2 = oracle.render_tiled(sc, w.camera)
     assert np.array_equal(img, img2) and np.array_equal(t, t2)
+    _check_tiled_backward(oracle, sc, w.camera)
     empty = scenes.Scene(*(np.ascontiguousarray(a[:0]) for a in (sc.mean3d, sc.rotation, sc.logscale, sc.opacity,
                                                                   sc.sh0)))
     cam = w.camera.copy()
@@ -468,3 +493,5 @@ def test_tiled_oracle_sh3_and_empty(oracle):
     assert np.array_equal(img_e, oracle.render(empty, cam)[0]) and np.all(t_e == 1.0)
     k, v = oracle.tile_keys_tiled(empty, cam)
     assert len(k) == 0 and len(v) == 0
+    ge = oracle.render_backward_tiled(empty, cam, np.ones((3, 180, 320), np.float32))
+    assert all(a.size == 0 for a in ge.values())
