@@ -19,7 +19,6 @@ from __future__ import annotations
 import argparse
 import ctypes
 import json
-import math
 import os
 import sys
 import time
@@ -103,20 +102,6 @@ def sort_bytes(passes, instances):
     if passes <= 0:
         return 0
     return instances * (16 * passes + 4 * (passes - 1))
-
-
-def sort_scope_model(instances, tiles, ms):
-    """The sort rate by the scope's own byte model for this metric: a sort of 64-bit
-    (tile << 32 | depth) keys with 4-byte values in P = ceil((32 + ceil(log2 T)) / 8) passes of
-    8-bit digits, 8 bytes of digit counting plus 24 bytes of scatter per pair and pass (152 bytes
-    per pair at 1080p). This build's two-level order sorts 13-bit tiles in two passes and moves
-    36 bytes per pair (sort_bytes); the model's bytes over the measured time say how the sort's
-    time compares with that design's at the same bandwidth, so its fraction can exceed 1."""
-    passes = -(-(32 + max(1, (max(int(round(tiles)), 2) - 1).bit_length())) // 8)
-    per_pair = 8 + 24 * passes
-    gbps = per_pair * instances / (ms * 1e-3) / 1e9
-    return {"bytes_per_pair": per_pair, "passes": passes, "gbps": round(gbps, 1),
-            "frac_of_peak": round(gbps / HBM_PEAK_GBPS, 3)}
 
 
 def render_geometry(lib, renderer, n, width, height):
@@ -221,48 +206,158 @@ def cpu_baseline(scene, camera_block, target, iters):
     sub = scenes.Scene(*(np.ascontiguousarray(a[::CPU_SAMPLE_STRIDE]) for a in
                          (scene.mean3d, scene.rotation, scene.logscale, scene.opacity, scene.sh0)))
     ref = Reference()
-    t0 = time.perf_counter()
-    _, stages = ref.train_steps(sub, camera_block, target, iters)
-    elapsed = time.perf_counter() - t0
-    _, full_stages = ref.train_steps(scene, camera_block, target, 1, skip_render_backward=True)
-    return elapsed, stages, sub.count, full_stages
+    # the CPU backend runs on this (calling) thread: pin it to one core, as `taskset -c` would,
+    # for the timed calls, and restore the mask afterwards
+    allowed = sorted(os.sched_getaffinity(0))
+    core = allowed[-1]
+    os.sched_setaffinity(0, {core})
+    try:
+        t0 = time.perf_counter()
+        _, stages = ref.train_steps(sub, camera_block, target, iters)
+        elapsed = time.perf_counter() - t0
+        _, full_stages = ref.train_steps(scene, camera_block, target, 1, skip_render_backward=True)
+    finally:
+        os.sched_setaffinity(0, set(allowed))
+    return elapsed, stages, sub.count, full_stages, core, len(allowed)
 
 
-def train_runner(lib, gaussians, width, height):
+def host_description():
+    """CPU model (/proc/cpuinfo), logical CPUs of the machine and of this process, glibc."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        glibc = os.confstr("CS_GNU_LIBC_VERSION")
+    except (ValueError, OSError):
+        glibc = None
+    return {"cpu_model": model, "nproc_machine": os.cpu_count(), "nproc_process": len(os.sched_getaffinity(0)),
+            "glibc": glibc}
+
+
+class TrainRunner:
     """One training step of the metric's sequence (TRAIN render, fused 0.8 L1 + 0.2 (1 - SSIM)
-    forward and backward, render backward, Adam) on `gaussians`; returns (step, renderer)."""
-    import numpy as np
-    import torch
+    forward and backward, render backward, Adam over the five SH0 groups) on `gaussians`.
+    step(cam, tgt, record=True) also records torch events around the loss and Adam launches
+    (their stage times; the render stages are timed by the library's own events)."""
 
-    from gsx_amd import _lib
-    from gsx_amd.backend import Adam, GaussianTensors, Renderer, ptr, stream_handle
+    def __init__(self, lib, gaussians, width, height):
+        import numpy as np
+        import torch
 
-    grads = gaussians.zeros_like_grads()
-    renderer = Renderer(width, height)
-    img = torch.empty((3, height, width), dtype=torch.float32, device="cuda")
-    loss_and_grad = torch.empty((2,) + tuple(img.shape), dtype=torch.float32, device="cuda")
-    loss_map, grad_img = loss_and_grad[0], loss_and_grad[1]
-    ssim_ws = torch.empty(3 * img.numel(), dtype=torch.float32, device="cuda")
-    opt = Adam([dict(parameter=gaussians.mean3d, gradient=grads.mean3d, learning_rate=1e-3),
-                dict(parameter=gaussians.logscale, gradient=grads.logscale, learning_rate=1e-2),
-                dict(parameter=gaussians.rotation, gradient=grads.rotation, learning_rate=1e-2),
-                dict(parameter=gaussians.opacity, gradient=grads.opacity, learning_rate=1e-2),
-                dict(parameter=gaussians.sh0, gradient=grads.sh0, learning_rate=1e-2)])
-    gs_l1 = float(np.float32(0.8) / np.float32(img.numel()))
-    gs_ssim = float(np.float32(0.2) / np.float32(img.numel()))
+        from gsx_amd.backend import Adam, Renderer
 
-    def step(cam, tgt):
+        self.lib, self.g, self.width, self.height = lib, gaussians, width, height
+        self.grads = gaussians.zeros_like_grads()
+        self.renderer = Renderer(width, height)
+        self.img = torch.empty((3, height, width), dtype=torch.float32, device="cuda")
+        # the loss launchers accumulate (+=) into the loss map and the image gradient, so both
+        # start each step at zero: one allocation, cleared by one fill
+        self.loss_and_grad = torch.empty((2,) + tuple(self.img.shape), dtype=torch.float32, device="cuda")
+        self.ssim_ws = torch.empty(3 * self.img.numel(), dtype=torch.float32, device="cuda")
+        self.opt = Adam(self.groups_for(gaussians, self.grads))
+        self.gs_l1 = float(np.float32(0.8) / np.float32(self.img.numel()))
+        self.gs_ssim = float(np.float32(0.2) / np.float32(self.img.numel()))
+        self.events = {k: [] for k in ("loss_forward", "loss_backward", "adam")}
+
+    @staticmethod
+    def groups_for(g, grads):
+        return [dict(parameter=g.mean3d, gradient=grads.mean3d, learning_rate=1e-3),
+                dict(parameter=g.logscale, gradient=grads.logscale, learning_rate=1e-2),
+                dict(parameter=g.rotation, gradient=grads.rotation, learning_rate=1e-2),
+                dict(parameter=g.opacity, gradient=grads.opacity, learning_rate=1e-2),
+                dict(parameter=g.sh0, gradient=grads.sh0, learning_rate=1e-2)]
+
+    def step(self, cam, tgt, record=False, borrow=True):
+        import torch
+
+        from gsx_amd import _lib
+        from gsx_amd.backend import ptr, stream_handle
+        lib, h, w = self.lib, self.height, self.width
+        loss_map, grad_img = self.loss_and_grad[0], self.loss_and_grad[1]
         st = stream_handle()
-        renderer.render(cam, gaussians, train=True, out_rgb=img)
-        loss_and_grad.zero_()
+        self.renderer.render(cam, self.g, train=True, out_rgb=self.img, borrow_train_state=borrow)
+        self.loss_and_grad.zero_()
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(5)] if record else None
+        if record:
+            e[0].record()
+        # 0.8 L1 + 0.2 (1 - SSIM), fused in one pass each way (bit-identical to separate calls)
         _lib.check(lib.gsx_hip_loss_ssim_chw_f32_forward_kernel_launch(
-            ptr(loss_map), ptr(img), ptr(tgt), 1, 3, height, width, 0.2, ptr(ssim_ws), 0.8, 1, st), "loss forward")
+            ptr(loss_map), ptr(self.img), ptr(tgt), 1, 3, h, w, 0.2, ptr(self.ssim_ws), 0.8, 1, st), "loss forward")
+        if record:
+            e[1].record()
         _lib.check(lib.gsx_hip_loss_ssim_chw_f32_backward_kernel_launch(
-            ptr(grad_img), ptr(img), ptr(tgt), 1, 3, height, width, gs_ssim, ptr(ssim_ws), gs_l1, 1, st),
+            ptr(grad_img), ptr(self.img), ptr(tgt), 1, 3, h, w, self.gs_ssim, ptr(self.ssim_ws), self.gs_l1, 1, st),
             "loss backward")
-        renderer.backward(grad_img, grads)
-        opt.step()
-    return step, renderer
+        if record:
+            e[2].record()
+        self.renderer.backward(grad_img, self.grads)
+        if record:
+            e[3].record()
+        self.opt.step()
+        if record:
+            e[4].record()
+            self.events["loss_forward"].append((e[0], e[1]))
+            self.events["loss_backward"].append((e[1], e[2]))
+            self.events["adam"].append((e[3], e[4]))
+
+    def stage_pass(self, inputs, first, steps):
+        """`steps` steps with HIP events at every stage boundary and the byte model's geometry
+        read after each (outside the events): (stage_ms, per-step geometries)."""
+        import torch
+        for v in self.events.values():
+            v.clear()
+        self.renderer.set_timing(steps)
+        torch.cuda.synchronize()
+        geos = []
+        for i in range(steps):
+            self.step(*inputs[(first + i) % len(inputs)], record=True)
+            geos.append(render_geometry(self.lib, self.renderer, self.g.count, self.width, self.height))
+        torch.cuda.synchronize()
+        stage_ms = self.renderer.timings()
+        self.renderer.set_timing(0)
+        for k, pairs in self.events.items():
+            stage_ms[k] = sum(a.elapsed_time(b) for a, b in pairs) / len(pairs)
+        return stage_ms, geos
+
+
+def stage_table(stage_ms, geos):
+    """Per stage: event time, the mean over the same steps of each step's minimum bytes, GB/s
+    and fraction of the HBM peak; sorted by time."""
+    kernels = []
+    for name, ms in stage_ms.items():
+        b = sum(algorithmic_bytes(name, gm) for gm in geos) / len(geos)
+        gbps = b / (ms * 1e-3) / 1e9 if ms > 0 else 0.0
+        kernels.append({"stage": name, "ms": round(ms, 4), "algorithmic_bytes": int(b), "gbps": round(gbps, 1),
+                        "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4)})
+    kernels.sort(key=lambda k: -k["ms"])
+    return kernels
+
+
+def config_measurement(runner, inputs, warmup, steps):
+    """A config's throughput (K steps with nothing else on the stream) and, from K more steps,
+    its stage times, minimum bytes per stage, the dominant stage's roofline entry and the step's
+    HBM fraction (all stages' minimum bytes over the step time)."""
+    ms = 1000.0 * timed_steps(runner.step, inputs, warmup, steps)
+    stage_ms, geos = runner.stage_pass(inputs, warmup + steps, steps)
+    kernels = stage_table(stage_ms, geos)
+    dom = kernels[0]
+    step_bytes = sum(k["algorithmic_bytes"] for k in kernels)
+    geo_mean = {k: round(sum(gm[k] for gm in geos) / len(geos), 1) for k in geos[0]}
+    return {"ms_per_step": round(ms, 3), "it_s": round(1000.0 / ms, 1),
+            "stage_ms": {k["stage"]: k["ms"] for k in kernels},
+            "kernels": kernels,
+            "roofline": {"bound": "hbm", "kernel": STAGE_KERNEL.get(dom["stage"], dom["stage"]),
+                         "achieved": dom["gbps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": dom["hbm_frac"],
+                         "algorithmic_bytes": dom["algorithmic_bytes"], "launch_ms": dom["ms"]},
+            "step_algorithmic_bytes": int(step_bytes),
+            "step_hbm_frac": round(step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+            "mean_per_step": geo_mean}
 
 
 def timed_steps(step, inputs, warmup, steps):
@@ -277,113 +372,241 @@ def timed_steps(step, inputs, warmup, steps):
     return (time.perf_counter() - t0) / steps
 
 
-def extra_workloads(lib, steps):
-    """Throughput of the other BASELINE configs at their stated sizes (one GPU), the tile sort's
-    bandwidth on config 4's instances, and one density-control refine at 1M rows."""
+def adc_rows(sc, rng, cap):
+    """Density-control rows of a scene in capacity-sized device buffers, with seeded
+    statistics (accumulated gradients, absolute gradients, visibility counts) and zero Adam
+    moments: (fields, moments, host copies to restore from)."""
+    import numpy as np
+    import torch
+    n = sc.count
+    host = {"mean3d": sc.mean3d, "rotation": sc.rotation, "logscale": sc.logscale, "opacity": sc.opacity,
+            "sh0": sc.sh0, "grad_acc": (rng.random(n) * 2e-3).astype(np.float32),
+            "absgrad_acc": (rng.random(n) * 8e-3).astype(np.float32),
+            "visible_counter": rng.integers(0, 20, n).astype(np.float32)}
+    d = {k: torch.zeros((cap, ADC_WIDTHS[k]) if ADC_WIDTHS[k] > 1 else (cap,), dtype=torch.float32, device="cuda")
+         for k in host}
+    src = {k: torch.from_numpy(v.reshape(n, ADC_WIDTHS[k]) if ADC_WIDTHS[k] > 1 else v).cuda()
+           for k, v in host.items()}
+    moms = {k: (torch.zeros_like(d[k]), torch.zeros_like(d[k])) for k in PARAM_ROLES}
+    return d, moms, src
+
+
+ADC_WIDTHS = {"mean3d": 3, "rotation": 4, "logscale": 3, "opacity": 1, "sh0": 3, "grad_acc": 1, "absgrad_acc": 1,
+              "visible_counter": 1}
+PARAM_ROLES = ("mean3d", "rotation", "logscale", "opacity", "sh0")
+ADC_COMMON = dict(pruning_opacity_threshold=0.05, opacity_clamp_value=0.3, max_world_scale=0.5,
+                  duplicate_grad_threshold=2e-4, duplicate_scale_threshold=0.01, scene_scale=4.0, refine_every=100,
+                  start_refine=0, end_refine=1000, reset_every=0)
+
+
+def time_refine(sc, params, cap, seed, reps=3):
+    """One density-control refine of `sc`'s rows (moments included), timed `reps` times from
+    the same uploaded state after one untimed call; the upload is outside the timed region."""
+    import numpy as np
+    import torch
+
+    from gsx_amd.backend import DensityControl
+    n = sc.count
+    d, moms, src = adc_rows(sc, np.random.default_rng(7), cap)
+    o = {k: torch.zeros_like(v) for k, v in d.items()}
+    om = {k: (torch.zeros_like(a), torch.zeros_like(b)) for k, (a, b) in moms.items()}
+    adc = DensityControl({**ADC_COMMON, **params, "max_num_gaussians": cap}, seed=seed)
+    times = []
+    for rep in range(reps + 1):
+        for k in d:
+            d[k][:n].copy_(src[k])
+        for a, b in moms.values():
+            a.zero_()
+            b.zero_()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        count, _, counts = adc.step(100, n, 0, d, moms, cap, o, om)
+        torch.cuda.synchronize()
+        if rep > 0:
+            times.append(1000.0 * (time.perf_counter() - t0))
+    adc.close()
+    return {"rows_before": n, "rows_after": int(count), "ms": round(sum(times) / len(times), 3),
+            "counts_pruned_duplicated_grown_reset": [int(c) for c in counts]}
+
+
+def c4_refine_loop(lib, iters=500, every=100):
+    """Config 4 as the config states it: `iters` training steps on the 6M scene at 1080p with an
+    ABSGS refine (clone / split / prune, moments included) after every `every`-th step, timed
+    end to end. The renderer and Adam run on the current rows of capacity-sized buffers; each
+    refine reads seeded accumulated absolute gradients and visibility counts (the CPU backend's
+    backward leaves the accumulators to the caller), and its result becomes the next steps'
+    Gaussian set and Adam state."""
     import numpy as np
     import torch
 
     from gsx_amd import scenes
     from gsx_amd.backend import Camera, DensityControl, GaussianTensors
+    w = scenes.config4()
+    n0 = w.scene.count
+    cap = n0 + n0 // 2
+    rng = np.random.default_rng(44)
+    bufs = [adc_rows(w.scene, rng, cap)[:2], None]
+    bufs[1] = ({k: torch.zeros_like(v) for k, v in bufs[0][0].items()},
+               {k: (torch.zeros_like(a), torch.zeros_like(b)) for k, (a, b) in bufs[0][1].items()})
+    for k in bufs[0][0]:
+        src = getattr(w.scene, k, None)
+        if src is not None:
+            bufs[0][0][k][:n0].copy_(torch.from_numpy(src.reshape(n0, -1) if ADC_WIDTHS[k] > 1 else src))
+    adc = DensityControl({**ADC_COMMON, "algorithm": 1, "duplicate_absgrad_threshold": 4e-4,
+                          "max_num_gaussians": cap, "start_refine": every, "end_refine": iters + 1}, seed=9)
+    cam = Camera.from_block(w.camera)
+    tgt = torch.from_numpy(w.target).cuda()
+    cur, count = 0, n0
+    counts_log = []
+
+    def bind(count, cur):
+        f, m = bufs[cur]
+        view = lambda t: t[:count]  # noqa: E731
+        g = GaussianTensors(*(view(f[k]) for k in PARAM_ROLES))
+        runner.g = g
+        runner.grads = g.zeros_like_grads()
+        runner.opt.groups = [dict(grp, parameter=getattr(g, k), gradient=getattr(runner.grads, k),
+                                  m=view(m[k][0]), v=view(m[k][1]))
+                             for grp, k in zip(runner.opt.groups, ("mean3d", "logscale", "rotation", "opacity",
+                                                                    "sh0"))]
+
+    f0 = bufs[0][0]
+    runner = TrainRunner(lib, GaussianTensors(*(f0[k][:n0] for k in PARAM_ROLES)), 1920, 1080)
+    bind(count, cur)
+    runner.step(cam, tgt)  # warm-up: buffers sized for the first step's instances
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for it in range(1, iters + 1):
+        runner.step(cam, tgt)
+        if it % every == 0:
+            f, m = bufs[cur]
+            # the refine's statistics: seeded, as BASELINE config 4 states
+            f["absgrad_acc"][:count].uniform_(0.0, 8e-3)
+            f["grad_acc"][:count].uniform_(0.0, 2e-3)
+            f["visible_counter"][:count].random_(0, 20)
+            o, om = bufs[1 - cur]
+            new_count, in_out, counts = adc.step(it, count, 0, f, m, cap, o, om)
+            counts_log.append([int(c) for c in counts])
+            if in_out:
+                cur = 1 - cur
+            count = new_count
+            bind(count, cur)
+    torch.cuda.synchronize()
+    secs = time.perf_counter() - t0
+    adc.close()
+    return {"gaussians_start": n0, "gaussians_end": int(count), "iterations": iters, "refine_every": every,
+            "seconds": round(secs, 3), "ms_per_iteration": round(1000.0 * secs / iters, 3),
+            "it_s": round(iters / secs, 2), "refine_counts_pruned_duplicated_grown_reset": counts_log}
+
+
+def extra_workloads(lib, steps, only=None):
+    """Throughput of the other BASELINE configs at their stated sizes (one GPU) with per-stage
+    times and rooflines, the tile sort's bandwidth on config 4's instances, config 4's
+    500-iteration loop with its refines, and density-control refines at 1M and 6M rows."""
+    import torch
 
     out = {}
+
+    def want(name):
+        return only is None or only == name
+
     # config 2: image fit, 1M Gaussians on z = 0, 1024^2, one camera
+    if want("c2"):
+        out.update(_config2(lib, steps))
+    if want("c3"):
+        out.update(_config3(lib, steps))
+    if want("c4"):
+        out.update(_config4(lib, steps))
+    if want("c4loop"):
+        out["c4_refine_loop"] = c4_refine_loop(lib)
+        torch.cuda.empty_cache()
+        log(f"config 4 loop: {out['c4_refine_loop']}")
+    if want("adc"):
+        out.update(_refines())
+    return out
+
+
+def _config2(lib, steps):
+    import torch
+
+    from gsx_amd import scenes
+    from gsx_amd.backend import Camera, GaussianTensors
+    out = {}
     w = scenes.config2()
-    g = GaussianTensors.from_scene(w.scene)
-    step, r = train_runner(lib, g, 1024, 1024)
+    runner = TrainRunner(lib, GaussianTensors.from_scene(w.scene), 1024, 1024)
     inputs = [(Camera.from_block(w.camera), torch.from_numpy(w.target).cuda())]
-    ms = 1000.0 * timed_steps(step, inputs, 3, steps)
-    out["c2_image_fit"] = {"gaussians": w.scene.count, "width": 1024, "height": 1024, "ms_per_step": round(ms, 3),
-                           "it_s": round(1000.0 / ms, 1), "instances": int(r.stats().instance_count)}
-    del g, step, r, inputs
-    log(f"config 2: {out['c2_image_fit']}")
+    out["c2_image_fit"] = {"gaussians": w.scene.count, "width": 1024, "height": 1024,
+                           **config_measurement(runner, inputs, 3, steps),
+                           "instances": int(runner.renderer.stats().instance_count)}
+    del runner, inputs
+    log(f"config 2: {out['c2_image_fit']['it_s']} it/s, stages {out['c2_image_fit']['stage_ms']}")
+    return out
+
+
+def _config3(lib, steps):
+    import torch
+
+    from gsx_amd import scenes
+    from gsx_amd.backend import Camera, GaussianTensors
+    out = {}
     # config 3: 3M Gaussians, 1080p, 24 orbit poses
     base = scenes.config3()
-    g = GaussianTensors.from_scene(base.scene)
-    step, r = train_runner(lib, g, 1920, 1080)
+    runner = TrainRunner(lib, GaussianTensors.from_scene(base.scene), 1920, 1080)
     inputs = []
     for k in range(24):
         block = scenes.camera(1920, 1080, 1600.0, pose=tuple(scenes.orbit_pose(k)), near=0.01, far=100.0)
         tgt = base.target if k == 0 else scenes.target_image(0, 103 + k, 1920, 1080, 2)
         inputs.append((Camera.from_block(block), torch.from_numpy(tgt).cuda()))
-    ms = 1000.0 * timed_steps(step, inputs, 2, steps)
     out["c3_scene_training"] = {"gaussians": base.scene.count, "width": 1920, "height": 1080, "poses": 24,
-                                "ms_per_step": round(ms, 3), "it_s": round(1000.0 / ms, 1),
-                                "instances_last_pose": int(r.stats().instance_count)}
-    del g, step, r, inputs, base
-    log(f"config 3: {out['c3_scene_training']}")
-    # config 4: 6M Gaussians, 1080p, the sort / blend stress; stage times from HIP events
+                                **config_measurement(runner, inputs, 2, steps)}
+    del runner, inputs, base
+    log(f"config 3: {out['c3_scene_training']['it_s']} it/s, stages {out['c3_scene_training']['stage_ms']}")
+    return out
+
+
+def _config4(lib, steps):
+    import torch
+
+    from gsx_amd import scenes
+    from gsx_amd.backend import Camera, GaussianTensors
+    out = {}
+    # config 4: 6M Gaussians, 1080p, the sort / blend stress
     w = scenes.config4()
-    g = GaussianTensors.from_scene(w.scene)
-    step, r = train_runner(lib, g, 1920, 1080)
+    runner = TrainRunner(lib, GaussianTensors.from_scene(w.scene), 1920, 1080)
     inputs = [(Camera.from_block(w.camera), torch.from_numpy(w.target).cuda())]
-    c4_steps = max(2, steps // 4)
-    ms = 1000.0 * timed_steps(step, inputs, 1, c4_steps)
-    r.set_timing(1)
-    step(*inputs[0])
-    torch.cuda.synchronize()
-    stage = r.timings()
-    r.set_timing(0)
-    st = r.stats()
+    c4 = config_measurement(runner, inputs, 1, max(2, steps // 4))
+    st = runner.renderer.stats()
     inst = int(st.instance_count)
     moved = sort_bytes(int(st.sort_passes), inst)
-    out["c4_sort_stress"] = {"gaussians": w.scene.count, "width": 1920, "height": 1080, "ms_per_step": round(ms, 3),
-                             "it_s": round(1000.0 / ms, 2), "instances": inst, "sort_passes": int(st.sort_passes),
-                             "sort_ms": round(stage["sort"], 3),
-                             "sort_gbps": round(moved / (stage["sort"] * 1e-3) / 1e9, 1),
-                             "sort_hbm_frac": round(moved / (stage["sort"] * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
-                             "sort_gkeys_s": round(inst / (stage["sort"] * 1e-3) / 1e9, 2),
-                             "sort_scope_model": sort_scope_model(inst, 120 * 68, stage["sort"]),
-                             "stage_ms": {k: round(v, 3) for k, v in stage.items()}}
-    del g, step, r, inputs, w
-    log(f"config 4: {out['c4_sort_stress']}")
+    sort_ms = c4["stage_ms"]["sort"]
+    out["c4_sort_stress"] = {"gaussians": w.scene.count, "width": 1920, "height": 1080, **c4, "instances": inst,
+                             "sort_passes": int(st.sort_passes),
+                             "sort_gbps": round(moved / (sort_ms * 1e-3) / 1e9, 1),
+                             "sort_hbm_frac": round(moved / (sort_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+                             "sort_gkeys_s": round(inst / (sort_ms * 1e-3) / 1e9, 2)}
+    del runner, inputs, w
     torch.cuda.empty_cache()
-    # density control at 1M rows (the metric scene with seeded statistics), rows in capacity-sized
-    # buffers with Adam moments: one ABSGS refine (prune + duplicate + split) and one MCMC refine
-    # (relocation + 10% growth). Each is timed from the same uploaded state three times after one
-    # untimed call; the upload is outside the timed region.
-    sc = scenes.metric_scene().scene
-    n = sc.count
-    rng = np.random.default_rng(7)
-    host = {"mean3d": sc.mean3d, "rotation": sc.rotation, "logscale": sc.logscale, "opacity": sc.opacity,
-            "sh0": sc.sh0, "grad_acc": (rng.random(n) * 2e-3).astype(np.float32),
-            "absgrad_acc": (rng.random(n) * 8e-3).astype(np.float32),
-            "visible_counter": rng.integers(0, 20, n).astype(np.float32)}
-    widths = {"mean3d": 3, "rotation": 4, "logscale": 3, "opacity": 1, "sh0": 3, "grad_acc": 1, "absgrad_acc": 1,
-              "visible_counter": 1}
-    cap = n + n // 5
-    d = {k: torch.zeros((cap, widths[k]) if widths[k] > 1 else (cap,), dtype=torch.float32, device="cuda")
-         for k in host}
-    src = {k: torch.from_numpy(v.reshape(n, widths[k]) if widths[k] > 1 else v).cuda() for k, v in host.items()}
-    moms = {k: (torch.zeros_like(d[k]), torch.zeros_like(d[k])) for k in ("mean3d", "rotation", "logscale",
-                                                                         "opacity", "sh0")}
-    o = {k: torch.zeros_like(v) for k, v in d.items()}
-    om = {k: (torch.zeros_like(a), torch.zeros_like(b)) for k, (a, b) in moms.items()}
-    common = dict(pruning_opacity_threshold=0.05, opacity_clamp_value=0.3, max_world_scale=0.5,
-                  duplicate_grad_threshold=2e-4, duplicate_scale_threshold=0.01, scene_scale=4.0, refine_every=100,
-                  start_refine=0, end_refine=1000, reset_every=0, max_num_gaussians=cap)
-    for name, params in (("absgs_refine", dict(algorithm=1, duplicate_absgrad_threshold=4e-4)),
-                         ("mcmc_refine", dict(algorithm=2, grow_ratio=0.1, noise_strength=50.0,
-                                              mean3d_learning_rate=1e-3))):
-        adc = DensityControl({**common, **params}, seed=3)
-        times = []
-        for rep in range(4):
-            for k in d:
-                d[k][:n].copy_(src[k])
-            for a, b in moms.values():
-                a.zero_()
-                b.zero_()
-            torch.cuda.synchronize()
-            t0 = time.perf_counter()
-            count, _, counts = adc.step(100, n, 0, d, moms, cap, o, om)
-            torch.cuda.synchronize()
-            if rep > 0:
-                times.append(1000.0 * (time.perf_counter() - t0))
-        out[name] = {"rows_before": n, "rows_after": int(count), "ms": round(sum(times) / len(times), 3),
-                     "counts_pruned_duplicated_grown_reset": [int(c) for c in counts]}
-        log(f"{name}: {out[name]}")
-        adc.close()
-    del d, src, moms, o, om
+    log(f"config 4: {out['c4_sort_stress']['it_s']} it/s, sort {out['c4_sort_stress']['sort_hbm_frac']} of HBM")
+    return out
+
+
+def _refines():
+    import torch
+
+    from gsx_amd import scenes
+    out = {}
+    # density control: one ABSGS refine (prune + duplicate + split) at 1M rows (the metric
+    # scene) and at config 4's 6M, one MCMC refine (relocation + 10% growth) at 1M
+    sc1 = scenes.metric_scene().scene
+    out["absgs_refine"] = time_refine(sc1, dict(algorithm=1, duplicate_absgrad_threshold=4e-4),
+                                      sc1.count + sc1.count // 5, 3)
+    out["mcmc_refine"] = time_refine(sc1, dict(algorithm=2, grow_ratio=0.1, noise_strength=50.0,
+                                               mean3d_learning_rate=1e-3), sc1.count + sc1.count // 5, 3)
+    sc4 = scenes.config4().scene
+    out["absgs_refine_c4"] = time_refine(sc4, dict(algorithm=1, duplicate_absgrad_threshold=4e-4),
+                                         sc4.count + sc4.count // 5, 3)
+    for k in ("absgs_refine", "mcmc_refine", "absgs_refine_c4"):
+        log(f"{k}: {out[k]}")
     torch.cuda.empty_cache()
     return out
 
@@ -405,6 +628,8 @@ def main():
                     help="inference renders timed for render_fps (default max(steps, 20); 0 skips them)")
     ap.add_argument("--extra-steps", type=int, default=10,
                     help="timed steps of the config 2/3/4 and density-control lines (0 disables them)")
+    ap.add_argument("--only", choices=("c2", "c3", "c4", "c4loop", "adc"), default=None,
+                    help="run just one of the config workloads (for profiling) and print its JSON")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; multi-GPU scaling (image tile bands "
@@ -419,6 +644,19 @@ def main():
 
     lib = _lib.load()
     dev_name = torch.cuda.get_device_name(0)
+    if args.calibrate_copy_mib > 0:
+        nf = args.calibrate_copy_mib * (1 << 20) // 4
+        a = torch.ones(nf, dtype=torch.float32, device="cuda")
+        b = torch.empty_like(a)
+        torch.cuda.synchronize()
+        _lib.check(lib.gsx_hip_copy_f32(ptr(b), ptr(a), nf, stream_handle()), "calibration copy")
+        torch.cuda.synchronize()
+        log(f"calibration copy: {args.calibrate_copy_mib} MiB read + {args.calibrate_copy_mib} MiB written")
+        del a, b
+    if args.only is not None:
+        print(json.dumps({"workload": args.only, "device": dev_name,
+                          **extra_workloads(lib, args.steps, only=args.only)}), flush=True)
+        return
     log(f"device {dev_name}; generating the metric scene (N={args.gaussians})")
     t0 = time.perf_counter()
     base = scenes.metric_scene(args.gaussians, args.width, args.height, 0)
@@ -483,15 +721,6 @@ def main():
             ev["loss_backward"].append((e[1], e[2]))
             ev["adam"].append((e[3], e4))
 
-    if args.calibrate_copy_mib > 0:
-        nf = args.calibrate_copy_mib * (1 << 20) // 4
-        a = torch.ones(nf, dtype=torch.float32, device="cuda")
-        b = torch.empty_like(a)
-        torch.cuda.synchronize()
-        _lib.check(lib.gsx_hip_copy_f32(ptr(b), ptr(a), nf, stream_handle()), "calibration copy")
-        torch.cuda.synchronize()
-        log(f"calibration copy: {args.calibrate_copy_mib} MiB read + {args.calibrate_copy_mib} MiB written")
-        del a, b
 
     log(f"warmup {args.warmup} steps")
     for i in range(args.warmup):
@@ -572,14 +801,7 @@ def main():
         fps = fps_steps / (time.perf_counter() - t0)
         log(f"inference forward: {fps:.1f} FPS")
 
-    kernels = []
-    for name, ms in stage_ms.items():
-        # the mean over the same steps of each step's minimum bytes
-        b = sum(algorithmic_bytes(name, gm) for gm in geos) / len(geos)
-        gbps = b / (ms * 1e-3) / 1e9 if ms > 0 else 0.0
-        kernels.append({"stage": name, "ms": round(ms, 4), "algorithmic_bytes": int(b), "gbps": round(gbps, 1),
-                        "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4)})
-    kernels.sort(key=lambda k: -k["ms"])
+    kernels = stage_table(stage_ms, geos)
     dominant = kernels[0]
     sort_entry = next(k for k in kernels if k["stage"] == "sort")
     # the blend kernels are bound by the vector ALU and LDS rather than HBM: their VALU busy and
@@ -610,7 +832,6 @@ def main():
         "sort_hbm_frac": sort_entry["hbm_frac"],
         # sorted (tile, position) pairs per second over the same steps
         "sort_gkeys_s": round(geo_mean["I"] / (sort_entry["ms"] * 1e-3) / 1e9, 2),
-        "sort_scope_model": sort_scope_model(geo_mean["I"], geo_mean["T"], sort_entry["ms"]),
         "kernels": kernels,
         "roofline": {"bound": "hbm", "kernel": STAGE_KERNEL.get(dominant["stage"], dominant["stage"]),
                      "achieved": dominant["gbps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
@@ -631,9 +852,10 @@ def main():
                           0.01, 100.0, 0, 0, 0], np.float32)
         res = cpu_baseline(base.scene, block, base.target, args.cpu_baseline_iters)
         if res is not None:
-            secs, stages, sub_n, full_stages = res
+            secs, stages, sub_n, full_stages, core, allowed = res
             result["cpu_baseline"] = {
                 "value": round(args.cpu_baseline_iters / secs, 5), "unit": "it/s", "cores": 1, "kind": "reference",
+                "pinned_core": core, "host": {**host_description(), "nproc_process": allowed},
                 "sample": f"{args.cpu_baseline_iters} step(s) of the same training step through the unmodified "
                           f"gsx CPU backend (single-threaded by construction) on every {CPU_SAMPLE_STRIDE}th "
                           f"Gaussian of the 1M scene ({sub_n} Gaussians) at the full {W}x{H}, pose 0; the "

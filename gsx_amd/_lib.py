@@ -100,6 +100,12 @@ class GsRows(ctypes.Structure):
                 ("first_moment", _vp * 8), ("second_moment", _vp * 8)]
 
 
+class PoolStats(ctypes.Structure):
+    _fields_ = [("requests", ctypes.c_uint64), ("reuses", ctypes.c_uint64), ("device_allocations", ctypes.c_uint64),
+                ("device_releases", ctypes.c_uint64), ("bytes_in_use", ctypes.c_uint64),
+                ("bytes_cached", ctypes.c_uint64)]
+
+
 # name -> (restype, argtypes); this table is also the symbol list tests check against the header.
 SIGNATURES = {
     "gsx_hip_last_error_message": (ctypes.c_char_p, []),
@@ -107,6 +113,10 @@ SIGNATURES = {
     "gsx_hip_device_name": (_st, [_i32, ctypes.c_char_p, ctypes.c_size_t]),
     "gsx_hip_malloc": (_st, [ctypes.POINTER(_vp), ctypes.c_size_t]),
     "gsx_hip_free": (_st, [_vp]),
+    "gsx_hip_pool_malloc": (_st, [ctypes.POINTER(_vp), ctypes.c_size_t, _vp]),
+    "gsx_hip_pool_free": (_st, [_vp, _vp]),
+    "gsx_hip_pool_trim": (_st, []),
+    "gsx_hip_pool_get_stats": (_st, [ctypes.POINTER(PoolStats)]),
     "gsx_hip_memcpy_htod": (_st, [_vp, _vp, ctypes.c_size_t]),
     "gsx_hip_memcpy_dtoh": (_st, [_vp, _vp, ctypes.c_size_t]),
     "gsx_hip_memcpy_dtod_async": (_st, [_vp, _vp, ctypes.c_size_t, _vp]),

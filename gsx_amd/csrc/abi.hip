@@ -122,30 +122,34 @@ gsx_hip_status hip_fail(hipError_t e, const char* what) {
 
 // Grow-only device buffer: the render context keeps its intermediates across calls, so steady
 // state training performs no allocation (gsx's CPU/CUDA contexts reset and re-grow arenas on
-// every forward, gsx/src/gsx-cuda/render.c:346-377).
+// every forward, gsx/src/gsx-cuda/render.c:346-377). Memory comes from the stream-ordered pool
+// (pool.hip): every call reserves each buffer it uses on its stream, and an outgrown or released
+// buffer returns to the pool behind that stream's queued work.
 struct DeviceBuffer {
     void* ptr = nullptr;
     size_t bytes = 0;
+    hipStream_t stream = nullptr;  // the stream of the last call that reserved it
 
-    gsx_hip_status reserve(size_t need, const char* what) {
+    gsx_hip_status reserve(size_t need, const char* what, hipStream_t s) {
+        stream = s;
         if (need <= bytes) return GSX_HIP_SUCCESS;
         size_t grow = need + need / 4 + 4096;
         if (ptr != nullptr) {
-            hipError_t e = hipFree(ptr);
+            gsx_hip_status st = gsx_hip_pool_free(ptr, s);
             ptr = nullptr;
             bytes = 0;
-            if (e != hipSuccess) return hip_fail(e, what);
+            if (st != GSX_HIP_SUCCESS) return st;
         }
-        hipError_t e = hipMalloc(&ptr, grow);
-        if (e != hipSuccess) {
+        gsx_hip_status st = gsx_hip_pool_malloc(&ptr, grow, s);
+        if (st != GSX_HIP_SUCCESS) {
             ptr = nullptr;
-            return hip_fail(e, what);
+            return st == GSX_HIP_ERROR_OUT_OF_MEMORY ? fail(st, what) : st;
         }
         bytes = grow;
         return GSX_HIP_SUCCESS;
     }
     void release() {
-        if (ptr != nullptr) (void)hipFree(ptr);
+        if (ptr != nullptr) (void)gsx_hip_pool_free(ptr, stream);
         ptr = nullptr;
         bytes = 0;
     }
@@ -281,6 +285,8 @@ struct gsx_hip_render_context {
     // stream at fork_ev, beside the backward: it reads HBM while the blend kernels are bound by
     // their vector ALUs
     hipStream_t check_stream = nullptr;
+    // the stream of the current forward or backward call: its buffer reserves are ordered on it
+    hipStream_t call_stream = nullptr;
     hipEvent_t fork_ev = nullptr;
     gsx_hip_gaussians live{};
     gsx_hip_camera camera{};
@@ -355,7 +361,7 @@ gsx_hip_status snapshot_layout(gsx_hip_render_context* ctx, const gsx_hip_gaussi
         off[f] = total;
         total += (n * (size_t)kFieldWidth[f] + 15u) / 16u * 16u;
     }
-    GSX_TRY(ctx->snap.reserve((total > 0 ? total : 1) * sizeof(float), "train state snapshot"));
+    GSX_TRY(ctx->snap.reserve((total > 0 ? total : 1) * sizeof(float), "train state snapshot", ctx->call_stream));
     float* base = ctx->snap.as<float>();
     float* fp[kStateFields] = {};
     *arrays = StateArrays{};
@@ -695,6 +701,7 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
         return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "forward type must be a GSX_HIP_FORWARD_* value");
     }
     ctx->has_train_state = false;
+    ctx->call_stream = stream;
     const CameraParams cam = make_camera_params(*camera);
     const int64_t n = gaussians->count;
     const int32_t tiles = cam.tiles_x * cam.tiles_y;
@@ -706,26 +713,26 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     ctx->tile_count_total = tiles;
 
     const size_t n1 = (size_t)(n > 0 ? n : 1);
-    GSX_TRY(ctx->rec.reserve(n1 * 3 * sizeof(float4), "rec"));
-    if (train) GSX_TRY(ctx->cov_coef.reserve(n1 * 2 * sizeof(float4), "cov_coef"));
-    if (train) GSX_TRY(ctx->touched.reserve(n1, "touched"));
-    GSX_TRY(ctx->tile_count.reserve(n1 * sizeof(uint32_t), "tile_count"));
-    GSX_TRY(ctx->counters.reserve(8 * sizeof(uint32_t), "counters"));
-    GSX_TRY(ctx->big_list.reserve(n1 * sizeof(uint32_t), "big_list"));
-    GSX_TRY(ctx->offsets.reserve((size_t)(n + 1) * sizeof(uint32_t), "offsets"));
+    GSX_TRY(ctx->rec.reserve(n1 * 3 * sizeof(float4), "rec", ctx->call_stream));
+    if (train) GSX_TRY(ctx->cov_coef.reserve(n1 * 2 * sizeof(float4), "cov_coef", ctx->call_stream));
+    if (train) GSX_TRY(ctx->touched.reserve(n1, "touched", ctx->call_stream));
+    GSX_TRY(ctx->tile_count.reserve(n1 * sizeof(uint32_t), "tile_count", ctx->call_stream));
+    GSX_TRY(ctx->counters.reserve(8 * sizeof(uint32_t), "counters", ctx->call_stream));
+    GSX_TRY(ctx->big_list.reserve(n1 * sizeof(uint32_t), "big_list", ctx->call_stream));
+    GSX_TRY(ctx->offsets.reserve((size_t)(n + 1) * sizeof(uint32_t), "offsets", ctx->call_stream));
     // per 256-rank workgroup: its tile-count sum, then its long-run count (two scanned arrays)
-    GSX_TRY(ctx->scan_temp.reserve(2 * ((size_t)blocks_for(n, 256) + 1) * sizeof(uint32_t), "rank_block_sums"));
-    GSX_TRY(ctx->long_list.reserve(n1 * sizeof(uint32_t), "long_list"));
-    GSX_TRY(ctx->depth_keys.reserve(n1 * sizeof(uint64_t), "depth_keys"));
-    GSX_TRY(ctx->depth_keys_alt.reserve(n1 * sizeof(uint64_t), "depth_keys_alt"));
-    GSX_TRY(ctx->rank_g.reserve(n1 * sizeof(uint32_t), "rank_gaussian"));
-    GSX_TRY(ctx->rank_count.reserve(n1 * sizeof(uint32_t), "rank_count"));
-    GSX_TRY(ctx->g_rank.reserve(n1 * sizeof(uint32_t), "gaussian_rank"));
-    GSX_TRY(ctx->multi_list.reserve(n1 * sizeof(uint32_t), "multi_list"));
-    GSX_TRY(ctx->depth_sort_temp.reserve(radix_sort_keys_u64_compacting_temp_bytes(n), "depth_sort_temp"));
-    GSX_TRY(ctx->ranges.reserve((size_t)tiles * sizeof(uint2), "ranges"));
-    GSX_TRY(ctx->final_t.reserve((size_t)pixels * sizeof(float), "final_t"));
-    GSX_TRY(ctx->last.reserve((size_t)pixels * sizeof(uint32_t), "last"));
+    GSX_TRY(ctx->scan_temp.reserve(2 * ((size_t)blocks_for(n, 256) + 1) * sizeof(uint32_t), "rank_block_sums", ctx->call_stream));
+    GSX_TRY(ctx->long_list.reserve(n1 * sizeof(uint32_t), "long_list", ctx->call_stream));
+    GSX_TRY(ctx->depth_keys.reserve(n1 * sizeof(uint64_t), "depth_keys", ctx->call_stream));
+    GSX_TRY(ctx->depth_keys_alt.reserve(n1 * sizeof(uint64_t), "depth_keys_alt", ctx->call_stream));
+    GSX_TRY(ctx->rank_g.reserve(n1 * sizeof(uint32_t), "rank_gaussian", ctx->call_stream));
+    GSX_TRY(ctx->rank_count.reserve(n1 * sizeof(uint32_t), "rank_count", ctx->call_stream));
+    GSX_TRY(ctx->g_rank.reserve(n1 * sizeof(uint32_t), "gaussian_rank", ctx->call_stream));
+    GSX_TRY(ctx->multi_list.reserve(n1 * sizeof(uint32_t), "multi_list", ctx->call_stream));
+    GSX_TRY(ctx->depth_sort_temp.reserve(radix_sort_keys_u64_compacting_temp_bytes(n), "depth_sort_temp", ctx->call_stream));
+    GSX_TRY(ctx->ranges.reserve((size_t)tiles * sizeof(uint2), "ranges", ctx->call_stream));
+    GSX_TRY(ctx->final_t.reserve((size_t)pixels * sizeof(float), "final_t", ctx->call_stream));
+    GSX_TRY(ctx->last.reserve((size_t)pixels * sizeof(uint32_t), "last", ctx->call_stream));
     uint32_t* counters = ctx->counters.as<uint32_t>();
     const unsigned pre_blocks = blocks_for(n, 256);
     GSX_TRY(ctx->kept_parts.reserve((size_t)pre_blocks * sizeof(unsigned long long), "kept_parts"));
@@ -829,18 +836,18 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     const size_t c1 = (size_t)(count > 0 ? count : 1);
     // per instance: its tile (emission order, the sort's input, kept for the backward), the middle
     // pass's tiles and positions, the sorted tiles and positions, its Gaussian
-    GSX_TRY(ctx->inst_tile.reserve(c1 * sizeof(uint32_t), "instance_tile"));
-    GSX_TRY(ctx->tiles_alt.reserve(c1 * sizeof(uint32_t), "tiles_alt"));
-    GSX_TRY(ctx->tiles_sorted.reserve(c1 * sizeof(uint32_t), "tiles_sorted"));
-    GSX_TRY(ctx->vals_alt.reserve(c1 * sizeof(uint32_t), "vals_alt"));
-    GSX_TRY(ctx->vals.reserve(c1 * sizeof(uint32_t), "vals"));
-    GSX_TRY(ctx->inst_gauss.reserve(c1 * sizeof(uint32_t), "instance_gaussian"));
-    GSX_TRY(ctx->sorted_g.reserve(c1 * sizeof(uint32_t), "sorted_g"));
-    GSX_TRY(ctx->sort_temp.reserve(tile_sort_u32_temp_bytes(count), "sort_temp"));
+    GSX_TRY(ctx->inst_tile.reserve(c1 * sizeof(uint32_t), "instance_tile", ctx->call_stream));
+    GSX_TRY(ctx->tiles_alt.reserve(c1 * sizeof(uint32_t), "tiles_alt", ctx->call_stream));
+    GSX_TRY(ctx->tiles_sorted.reserve(c1 * sizeof(uint32_t), "tiles_sorted", ctx->call_stream));
+    GSX_TRY(ctx->vals_alt.reserve(c1 * sizeof(uint32_t), "vals_alt", ctx->call_stream));
+    GSX_TRY(ctx->vals.reserve(c1 * sizeof(uint32_t), "vals", ctx->call_stream));
+    GSX_TRY(ctx->inst_gauss.reserve(c1 * sizeof(uint32_t), "instance_gaussian", ctx->call_stream));
+    GSX_TRY(ctx->sorted_g.reserve(c1 * sizeof(uint32_t), "sorted_g", ctx->call_stream));
+    GSX_TRY(ctx->sort_temp.reserve(tile_sort_u32_temp_bytes(count), "sort_temp", ctx->call_stream));
     if (train) {
         // bucket checkpoints: at most I/kBucket + tiles + 1 slots of 256 floats
         GSX_TRY(ctx->ckpt.reserve(((size_t)count / kBucket + (size_t)tiles + 2) * 256 * sizeof(float),
-                                  "checkpoints"));
+                                  "checkpoints", ctx->call_stream));
     }
     if (n > 0) {
         // one wave per big box
@@ -904,12 +911,12 @@ gsx_hip_status enqueue_backward(gsx_hip_render_context* ctx, const float* grad_r
                                 const gsx_hip_gaussian_grads* grads, hipStream_t stream) {
     const int64_t n = ctx->gaussian_count;
     const gsx_hip_gaussians& gs = ctx->gs;
-    GSX_TRY(ctx->grad2d.reserve((size_t)(n > 0 ? n : 1) * 9 * sizeof(float), "grad2d"));
+    GSX_TRY(ctx->grad2d.reserve((size_t)(n > 0 ? n : 1) * 9 * sizeof(float), "grad2d", ctx->call_stream));
     GSX_TRY(ctx->inst_grad.reserve((size_t)(ctx->instance_count > 0 ? ctx->instance_count : 1) * 9 * sizeof(float),
-                                   "instance_grad"));
+                                   "instance_grad", ctx->call_stream));
     const CameraParams& cam = ctx->cam;
     const int32_t tiles = cam.tiles_x * cam.tiles_y;
-    GSX_TRY(ctx->tile_cut.reserve((size_t)(tiles > 0 ? tiles : 1) * sizeof(uint32_t), "tile_cut"));
+    GSX_TRY(ctx->tile_cut.reserve((size_t)(tiles > 0 ? tiles : 1) * sizeof(uint32_t), "tile_cut", ctx->call_stream));
     const uint32_t* svals = ctx->sorted_vals;
     const uint32_t* counters = ctx->counters.as<uint32_t>();  // as the forward left them
     // per-instance partials: [I][8] records, then the [I] opacity terms
@@ -984,6 +991,7 @@ gsx_hip_status gsx_hip_render_backward(gsx_hip_render_context* ctx, const float*
     if ((reinterpret_cast<uintptr_t>(grads->rotation) & 15u) != 0) {
         return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "rotation gradient must be 16-byte aligned");
     }
+    ctx->call_stream = stream;
     if (ctx->train_mode == GSX_HIP_FORWARD_TRAIN_BORROW && n > 0) {
         // borrowed state: the gradient is taken at the values the caller's arrays hold now. The
         // comparison with the retained copy runs on check_stream, after everything queued so far
@@ -1020,7 +1028,7 @@ gsx_hip_status gsx_hip_render_backward(gsx_hip_render_context* ctx, const float*
             const gsx_hip_gaussians live = ctx->live;
             const gsx_hip_camera camera = ctx->camera;
             GSX_TRY(ctx->refresh_rgb.reserve((size_t)3 * camera.width * camera.height * sizeof(float),
-                                             "refresh image"));
+                                             "refresh image", ctx->call_stream));
             ctx->timing = false;
             const gsx_hip_status st = gsx_hip_render_forward(ctx, &camera, &live, GSX_HIP_FORWARD_TRAIN_BORROW,
                                                              ctx->refresh_rgb.as<float>(), nullptr, stream);

@@ -442,19 +442,28 @@ gsx_hip_status adc_fail(gsx_hip_status code, const char* what) {
         if (s_ != GSX_HIP_SUCCESS) return s_;  \
     } while (0)
 
+// Grow-only scratch from the stream-ordered pool (pool.hip); an outgrown or released block returns
+// to the pool behind the queued work of the stream of the call that last reserved it.
 struct Scratch {
     void* ptr = nullptr;
     size_t bytes = 0;
-    gsx_hip_status reserve(size_t need) {
+    hipStream_t stream = nullptr;
+    gsx_hip_status reserve(size_t need, hipStream_t s) {
+        stream = s;
         if (need <= bytes) return GSX_HIP_SUCCESS;
-        if (ptr != nullptr) (void)hipFree(ptr);
+        if (ptr != nullptr) (void)gsx_hip_pool_free(ptr, s);
         ptr = nullptr;
         bytes = 0;
         const size_t grow = need + need / 4 + 4096;
-        hipError_t e = hipMalloc(&ptr, grow);
-        if (e != hipSuccess) return adc_fail((gsx_hip_status)e, "adc scratch allocation");
+        gsx_hip_status st = gsx_hip_pool_malloc(&ptr, grow, s);
+        if (st != GSX_HIP_SUCCESS) return st;
         bytes = grow;
         return GSX_HIP_SUCCESS;
+    }
+    void release() {
+        if (ptr != nullptr) (void)gsx_hip_pool_free(ptr, stream);
+        ptr = nullptr;
+        bytes = 0;
     }
 };
 
@@ -641,7 +650,7 @@ gsx_hip_status mcmc_refine(gsx_hip_adc_context* ctx, const gsx_hip_adc_params& p
     off += up((size_t)n * 4);
     const size_t o_temp = off;
     off += up(gsx_hip_scan_temp_bytes(n));
-    ADC_TRY(ctx->scratch.reserve(off));
+    ADC_TRY(ctx->scratch.reserve(off, stream));
     uint8_t* base = static_cast<uint8_t*>(ctx->scratch.ptr);
     float* weight = reinterpret_cast<float*>(base + o_w);
     uint32_t* dead = reinterpret_cast<uint32_t*>(base + o_dead);
@@ -740,7 +749,7 @@ gsx_hip_status gsx_hip_adc_context_create(gsx_hip_adc_context** out, uint64_t se
 
 gsx_hip_status gsx_hip_adc_context_destroy(gsx_hip_adc_context* ctx) {
     if (ctx == nullptr) return adc_fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "context must be non-null");
-    if (ctx->scratch.ptr != nullptr) (void)hipFree(ctx->scratch.ptr);
+    ctx->scratch.release();
     if (ctx->host != nullptr) (void)hipHostFree(ctx->host);
     if (ctx->host_cdf != nullptr) (void)hipHostFree(ctx->host_cdf);
     delete ctx;
@@ -807,7 +816,7 @@ gsx_hip_status gsx_hip_adc_step(gsx_hip_adc_context* ctx, const gsx_hip_adc_para
         off += a;
         const size_t o_temp = off;
         off += up(gsx_hip_scan_temp_bytes(max_rows > n ? max_rows : n));
-        ADC_TRY(ctx->scratch.reserve(off));
+        ADC_TRY(ctx->scratch.reserve(off, stream));
         uint8_t* base = static_cast<uint8_t*>(ctx->scratch.ptr);
         uint8_t* mode = base + o_mode;
         uint32_t* grow = reinterpret_cast<uint32_t*>(base + o_grow);

@@ -258,7 +258,8 @@ static gsx_error ha_step(gsx_adc_t adc, const gsx_adc_request *request, gsx_adc_
         if(w.present[k]) total_floats += copies * capacity * (gsx_size_t)ha_width[k];
         if(k < 8 && w.moment_group[k] >= 0) total_floats += 2 * copies * capacity * (gsx_size_t)ha_width[k];
     }
-    st = gsx_hip_malloc(&w.block, (size_t)total_floats * sizeof(float));
+    /* from the stream-ordered pool: returned behind the step's queued copies, no host wait */
+    st = gsx_hip_pool_malloc(&w.block, (size_t)total_floats * sizeof(float), stream);
     if(st != GSX_HIP_SUCCESS) {
         return gsx_make_error(GSX_ERROR_OUT_OF_MEMORY, "hip adc working rows allocation failed");
     }
@@ -294,16 +295,14 @@ static gsx_error ha_step(gsx_adc_t adc, const gsx_adc_request *request, gsx_adc_
     }
 #undef HA_TAKE
     if(st != GSX_HIP_SUCCESS) {
-        (void)gsx_hip_stream_synchronize(stream);
-        (void)gsx_hip_free(w.block);
+        (void)gsx_hip_pool_free(w.block, stream);
         return gsx_hip_plugin_error(st, "hip adc working copy failed");
     }
 
     st = gsx_hip_adc_step(a->ctx, &p, (uint64_t)request->global_step, &w.rows, (int64_t)capacity, &w.out, &in_out,
         counts, stream);
     if(st != GSX_HIP_SUCCESS) {
-        (void)gsx_hip_stream_synchronize(stream);
-        (void)gsx_hip_free(w.block);
+        (void)gsx_hip_pool_free(w.block, stream);
         return gsx_hip_plugin_error(st, "hip adc step failed");
     }
     new_count = in_out ? w.out.count : w.rows.count;
@@ -316,8 +315,7 @@ static gsx_error ha_step(gsx_adc_t adc, const gsx_adc_request *request, gsx_adc_
             if(gsx_error_is_success(error)) error = gsx_optim_resize(request->optim, (gsx_size_t)new_count);
         }
         if(!gsx_error_is_success(error)) {
-            (void)gsx_hip_stream_synchronize(stream);
-            (void)gsx_hip_free(w.block);
+            (void)gsx_hip_pool_free(w.block, stream);
             return error;
         }
     }
@@ -345,8 +343,7 @@ static gsx_error ha_step(gsx_adc_t adc, const gsx_adc_request *request, gsx_adc_
             }
         }
     }
-    (void)gsx_hip_stream_synchronize(stream);
-    (void)gsx_hip_free(w.block);
+    (void)gsx_hip_pool_free(w.block, stream);
     if(st != GSX_HIP_SUCCESS) {
         return gsx_hip_plugin_error(st, "hip adc commit failed");
     }

@@ -450,14 +450,16 @@ static gsx_error hip_buffer_type_init_buffer(gsx_backend_buffer_type_t buffer_ty
         return gsx_make_error(GSX_ERROR_OUT_OF_MEMORY, "failed to allocate hip buffer object");
     }
     if(t->info.type == GSX_BACKEND_BUFFER_TYPE_DEVICE) {
-        st = gsx_hip_malloc(&buf->ptr, (size_t)alloc);
+        /* from the stream-ordered pool: gsx_gs_resize reallocates whole Gaussian sets on every
+         * density-control commit (gsx-core.c:2811-2869) */
+        st = gsx_hip_pool_malloc(&buf->ptr, (size_t)alloc, gsx_hip_plugin_stream(buffer_type->backend));
     } else {
         st = gsx_hip_host_alloc(&buf->host, (size_t)alloc);
         if(st == GSX_HIP_SUCCESS) st = gsx_hip_host_device_pointer(buf->host, &buf->ptr);
     }
     if(st != GSX_HIP_SUCCESS) {
         if(buf->host != NULL) (void)gsx_hip_host_free(buf->host);
-        else if(buf->ptr != NULL) (void)gsx_hip_free(buf->ptr);
+        else if(buf->ptr != NULL) (void)gsx_hip_pool_free(buf->ptr, gsx_hip_plugin_stream(buffer_type->backend));
         free(buf);
         return gsx_make_error(GSX_ERROR_OUT_OF_MEMORY, "hip buffer allocation failed");
     }
@@ -532,12 +534,14 @@ static gsx_error hb_free(gsx_backend_buffer_t buffer)
     if(buffer == NULL) {
         return gsx_make_error(GSX_ERROR_INVALID_ARGUMENT, "buffer must be non-null");
     }
-    /* queued work may still read or write the buffer */
-    (void)gsx_hip_stream_synchronize(hb_stream(buffer));
     if(b->host != NULL) {
+        /* queued work may still read or write the buffer, and the host touches pinned memory
+         * directly: wait for the stream before the memory goes */
+        (void)gsx_hip_stream_synchronize(hb_stream(buffer));
         (void)gsx_hip_host_free(b->host);
     } else {
-        (void)gsx_hip_free(b->ptr);
+        /* device memory returns to the pool behind the queued work (no host wait) */
+        (void)gsx_hip_pool_free(b->ptr, hb_stream(buffer));
     }
     free(b);
     return ok();
@@ -760,10 +764,10 @@ static gsx_error hb_fill_randint(gsx_backend_buffer_t buffer, const gsx_backend_
     for(;;) {
         size_t bytes = gsx_hip_fill_randint_temp_bytes(draws);
 
-        HIP_TRY(gsx_hip_malloc(&temp, bytes), "hip randint workspace allocation failed");
+        HIP_TRY(gsx_hip_pool_malloc(&temp, bytes, hb_stream(buffer)), "hip randint workspace allocation failed");
         st = gsx_hip_fill_randint(hb_view_ptr(view), count, elem, state, inc, bound, draws, temp, &accepted,
             hb_stream(buffer));
-        (void)gsx_hip_free(temp);
+        (void)gsx_hip_pool_free(temp, hb_stream(buffer));
         HIP_TRY(st, "hip randint fill failed");
         if(accepted >= count) break;
         if(draws > INT64_MAX / 4) {

@@ -96,8 +96,7 @@ static gsx_error hlc_destroy(gsx_loss_context_t context)
         return gsx_make_error(GSX_ERROR_INVALID_ARGUMENT, "context must be non-null");
     }
     if(c->workspace != NULL) {
-        (void)gsx_hip_stream_synchronize(gsx_hip_plugin_stream(context->loss->backend));
-        (void)gsx_hip_free(c->workspace);
+        (void)gsx_hip_pool_free(c->workspace, gsx_hip_plugin_stream(context->loss->backend));
     }
     gsx_loss_context_base_deinit(&c->base);
     free(c);
@@ -173,12 +172,11 @@ static gsx_error hl_forward(gsx_loss_t loss, gsx_loss_context_t context, const g
         if(!gsx_error_is_success(e)) return e;
         if(request->train && c->workspace_floats < 3 * n) {
             if(c->workspace != NULL) {
-                (void)gsx_hip_stream_synchronize(stream);
-                (void)gsx_hip_free(c->workspace);
+                (void)gsx_hip_pool_free(c->workspace, stream);
                 c->workspace = NULL;
                 c->workspace_floats = 0;
             }
-            st = gsx_hip_malloc((void **)&c->workspace, (size_t)(3 * n) * sizeof(float));
+            st = gsx_hip_pool_malloc((void **)&c->workspace, (size_t)(3 * n) * sizeof(float), stream);
             if(st != GSX_HIP_SUCCESS) {
                 return gsx_make_error(GSX_ERROR_OUT_OF_MEMORY, "hip ssim workspace allocation failed");
             }

@@ -90,9 +90,10 @@ static gsx_error ho_alloc_zero(hipStream_t stream, gsx_size_t floats, float **m,
 
     *m = NULL;
     *v = NULL;
-    if(gsx_hip_malloc((void **)m, bytes) != GSX_HIP_SUCCESS || gsx_hip_malloc((void **)v, bytes) != GSX_HIP_SUCCESS) {
-        if(*m != NULL) (void)gsx_hip_free(*m);
-        if(*v != NULL) (void)gsx_hip_free(*v);
+    if(gsx_hip_pool_malloc((void **)m, bytes, stream) != GSX_HIP_SUCCESS
+        || gsx_hip_pool_malloc((void **)v, bytes, stream) != GSX_HIP_SUCCESS) {
+        if(*m != NULL) (void)gsx_hip_pool_free(*m, stream);
+        if(*v != NULL) (void)gsx_hip_pool_free(*v, stream);
         *m = NULL;
         *v = NULL;
         return gsx_make_error(GSX_ERROR_OUT_OF_MEMORY, "hip optimizer moment allocation failed");
@@ -108,12 +109,10 @@ static void ho_free_arrays(hip_optim *o)
 {
     gsx_index_t i = 0;
 
-    if(o->m != NULL || o->v != NULL) {
-        (void)gsx_hip_stream_synchronize(ho_stream(o));
-    }
+    /* the pool takes the moments back behind the major stream's queued work (no host wait) */
     for(i = 0; i < o->base.param_group_count; ++i) {
-        if(o->m != NULL && o->m[i] != NULL) (void)gsx_hip_free(o->m[i]);
-        if(o->v != NULL && o->v[i] != NULL) (void)gsx_hip_free(o->v[i]);
+        if(o->m != NULL && o->m[i] != NULL) (void)gsx_hip_pool_free(o->m[i], ho_stream(o));
+        if(o->v != NULL && o->v[i] != NULL) (void)gsx_hip_pool_free(o->v[i], ho_stream(o));
     }
     free(o->steps);
     free(o->m);
@@ -354,9 +353,9 @@ static gsx_error ho_relayout(hip_optim *o, gsx_tensor_t index, gsx_size_t new_ro
                 return gsx_make_error(GSX_ERROR_UNKNOWN, "hip optimizer resize copy failed");
             }
         }
-        (void)gsx_hip_stream_synchronize(ho_stream(o));
-        (void)gsx_hip_free(o->m[i]);
-        (void)gsx_hip_free(o->v[i]);
+        /* the old moments return to the pool behind the gathers queued above */
+        (void)gsx_hip_pool_free(o->m[i], ho_stream(o));
+        (void)gsx_hip_pool_free(o->v[i], ho_stream(o));
         o->m[i] = m;
         o->v[i] = v;
         o->rows[i] = new_rows;

@@ -48,6 +48,29 @@ gsx_hip_status gsx_hip_device_count(int32_t* out_count);
 gsx_hip_status gsx_hip_device_name(int32_t device, char* out_name, size_t capacity);
 gsx_hip_status gsx_hip_malloc(void** out_ptr, size_t bytes);
 gsx_hip_status gsx_hip_free(void* ptr);
+
+/* Stream-ordered caching device allocator (the backend's device buffers, optimizer moments and
+ * density-control workspaces; replaces the cudaMalloc / synchronising cudaFree pairs of
+ * gsx-cuda/buffer.c and gsx-cuda/optim.c that every gsx_gs_resize commit,
+ * gsx/src/gsx-core.c:2811-2869, goes through). A request is rounded up to one of 8 size classes per
+ * power of two (at least 512 bytes) and served from cached blocks of its class or the next two
+ * when one is free; otherwise hipMalloc (on running out of memory the cache is released and the
+ * request retried). pool_free returns a block to the cache behind an event recorded on `stream`
+ * (no host synchronisation): reuse on the same stream is ordered by the stream, reuse on another
+ * stream waits on that event. Blocks stay cached until gsx_hip_pool_trim (current device; it
+ * synchronises the device first) or process exit. Thread-safe. */
+typedef struct gsx_hip_pool_stats {
+    uint64_t requests;            /* pool_malloc calls */
+    uint64_t reuses;              /* requests served from cached blocks */
+    uint64_t device_allocations;  /* hipMalloc calls made by the pool */
+    uint64_t device_releases;     /* hipFree calls made by the pool (trim, out-of-memory retry) */
+    uint64_t bytes_in_use;        /* rounded sizes of the blocks handed out */
+    uint64_t bytes_cached;        /* rounded sizes of the cached blocks */
+} gsx_hip_pool_stats;
+gsx_hip_status gsx_hip_pool_malloc(void** out_ptr, size_t bytes, hipStream_t stream);
+gsx_hip_status gsx_hip_pool_free(void* ptr, hipStream_t stream);
+gsx_hip_status gsx_hip_pool_trim(void);
+gsx_hip_status gsx_hip_pool_get_stats(gsx_hip_pool_stats* out_stats);
 gsx_hip_status gsx_hip_memcpy_htod(void* dst, const void* src, size_t bytes);
 gsx_hip_status gsx_hip_memcpy_dtoh(void* dst, const void* src, size_t bytes);
 gsx_hip_status gsx_hip_memcpy_dtod_async(void* dst, const void* src, size_t bytes, hipStream_t stream);

@@ -372,6 +372,12 @@ class Reference:
         lib.gsxref_adc.argtypes = [ctypes.c_int] + [_vp] * 10 + [ctypes.c_int, _vp] + [_vp] * 6
         lib.gsxref_train_step.restype = ctypes.c_int
         lib.gsxref_train_step.argtypes = [ctypes.c_int, ctypes.c_int] + [_vp] * 7 + [_f, _f, _vp, ctypes.c_int, _vp]
+        lib.gsxref_session_fit.restype = ctypes.c_int
+        lib.gsxref_session_fit.argtypes = [ctypes.c_int] * 3 + [_vp] * 7 + [_f, _f, _vp, ctypes.c_int, ctypes.c_int,
+                                                                          _vp, _vp]
+        self.StepHook = ctypes.CFUNCTYPE(None, ctypes.c_int, ctypes.c_double)
+        lib.gsxref_set_step_hook.restype = None
+        lib.gsxref_set_step_hook.argtypes = [self.StepHook]
         lib.gsxref_count_devices.restype = ctypes.c_int
         lib.gsxref_count_devices.argtypes = [ctypes.c_int]
         lib.gsxref_backend_type.restype = ctypes.c_int
@@ -379,6 +385,33 @@ class Reference:
         self._raw = lib
         slots = {"cpu": 0, "hip": 2 if hip_type else 1}
         self.lib = lib if backend is None else _OnBackend(lib, slots[backend])
+
+    def session_fit(self, scene, camera, target_chw, warmup, iters, w_l1=0.8, w_ssim=0.2, lrs=(1e-3, 1e-2),
+                    collect_timings=False, prefetch=0):
+        """`warmup` + `iters` gsx_session_step calls configured as image-fit-demo's session (one
+        image served by gsx_dataloader, L1 + SSIM loss items, Adam over the five SH0 roles,
+        borrowed train state, no ADC). Returns (trained scene copy, seconds of the timed `iters`
+        steps, the last step's report timings in us: dataloader, render fwd, loss fwd, loss bwd,
+        render bwd, optim, adc, total)."""
+        from gsx_amd import scenes as _scenes
+        sc = _scenes.Scene(*(a.copy() for a in (scene.mean3d, scene.rotation, scene.logscale, scene.opacity,
+                                                 scene.sh0)))
+        hwc = np.ascontiguousarray(np.transpose(target_chw, (1, 2, 0)), dtype=np.float32)
+        secs = np.zeros(1, np.float64)
+        stage_us = np.zeros(8, np.float64)
+        hyper = np.array(lrs, np.float32)
+        self._check(self.lib.gsxref_session_fit(
+            sc.count, warmup, iters, _p(sc.mean3d), _p(sc.rotation), _p(sc.logscale), _p(sc.opacity), _p(sc.sh0),
+            _p(np.ascontiguousarray(camera, dtype=np.float32)), _p(hwc), w_l1, w_ssim, _p(hyper),
+            1 if collect_timings else 0, prefetch, _p(secs), _p(stage_us)))
+        return sc, float(secs[0]), stage_us
+
+    def set_step_hook(self, fn):
+        """fn(step, seconds) after each ADC step of adc() (the stream drained around the step), or
+        None. The returned ctypes callback must stay referenced while it is installed."""
+        cb = self.StepHook(fn) if fn is not None else self.StepHook()
+        self._raw.gsxref_set_step_hook(cb)
+        return cb
 
     def count_devices(self, backend_type: str) -> int:
         """Registered devices of a backend type (gsx_count_backend_devices_by_type)."""

@@ -39,6 +39,15 @@
 #include <time.h>
 
 static const char *g_last_message = NULL;
+
+static double now_seconds(void);
+
+/* Optional callback after each ADC step of gsxref_adc: the step's index and its wall-clock
+ * seconds, the major stream drained before and after the step (NULL: no hook, no drains). */
+typedef void (*gsxref_step_hook)(int step, double seconds);
+static gsxref_step_hook g_step_hook = NULL;
+
+void gsxref_set_step_hook(gsxref_step_hook hook) { g_step_hook = hook; }
 /* One backend per registry slot, created on first use; gsxref_use_backend picks the slot the
  * entry points below run on (the CPU backend unless told otherwise). */
 static gsx_backend_t g_backends[3] = { NULL, NULL, NULL };
@@ -686,8 +695,18 @@ int gsxref_adc(int n, const float *mean3d, const float *rotation, const float *l
     if(iparams[9] != 0) TRY(adam_probe_step(gs, optim, 101u));
     counters[0] = counters[1] = counters[2] = counters[3] = 0;
     for(k = 0; k < (iparams[8] > 1 ? (int)iparams[8] : 1); ++k) {
+        double t0 = 0.0;
+
         areq.global_step = (gsx_size_t)iparams[6] + (gsx_size_t)k;
+        if(g_step_hook != NULL) {
+            FINISH();
+            t0 = now_seconds();
+        }
         TRY(gsx_adc_step(adc, &areq, &ares));
+        if(g_step_hook != NULL) {
+            FINISH();
+            g_step_hook(k, now_seconds() - t0);
+        }
         counters[0] += (int64_t)ares.pruned_count;
         counters[1] += (int64_t)ares.duplicated_count;
         counters[2] += (int64_t)ares.grown_count;
