@@ -713,7 +713,8 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     ctx->tile_count_total = tiles;
 
     const size_t n1 = (size_t)(n > 0 ? n : 1);
-    GSX_TRY(ctx->rec.reserve(n1 * 3 * sizeof(float4), "rec", ctx->call_stream));
+    // per Gaussian: geometry (2 float4), colour / depth (float4) at 2n, contribution box (uint2) at 3n
+    GSX_TRY(ctx->rec.reserve(n1 * (3 * sizeof(float4) + sizeof(uint2)), "rec", ctx->call_stream));
     if (train) GSX_TRY(ctx->cov_coef.reserve(n1 * 2 * sizeof(float4), "cov_coef", ctx->call_stream));
     if (train) GSX_TRY(ctx->touched.reserve(n1, "touched", ctx->call_stream));
     GSX_TRY(ctx->tile_count.reserve(n1 * sizeof(uint32_t), "tile_count", ctx->call_stream));
@@ -782,6 +783,7 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
                            gaussians->rotation, gaussians->logscale, gaussians->opacity, gaussians->sh0,
                            gaussians->sh1, gaussians->sh2, gaussians->sh3, (int)gaussians->sh_degree, cam,
                            ctx->rec.as<float4>(), ctx->rec.as<float4>() + 2 * n,
+                           reinterpret_cast<uint2*>(ctx->rec.as<float4>() + 3 * n),
                            train ? ctx->cov_coef.as<float4>() : nullptr,
                            ctx->tile_count.as<uint32_t>(), train ? visible_counter : nullptr,
                            ctx->big_list.as<uint32_t>(), big_count, counters + 1, counters + 2 + (ctx->big_slot ^ 1),
@@ -892,6 +894,7 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     hipLaunchKernelGGL(blend_forward_kernel, dim3((unsigned)tiles_padded), dim3(256), 0, stream,
                        ctx->ranges.as<uint2>(), ctx->sorted_vals, ctx->inst_gauss.as<uint32_t>(),
                        ctx->rec.as<float4>(), ctx->rec.as<float4>() + 2 * n,
+                       reinterpret_cast<const uint2*>(ctx->rec.as<float4>() + 3 * n),
                        train ? ctx->sorted_g.as<uint32_t>() : nullptr, cam, out_rgb,
                        ctx->final_t.as<float>(),
                        ctx->last.as<uint32_t>(), train ? ctx->ckpt.as<float>() : nullptr);
@@ -927,7 +930,8 @@ gsx_hip_status enqueue_backward(gsx_hip_render_context* ctx, const float* grad_r
     const int tiles_padded = ((tiles + 7) / 8) * 8;
     hipLaunchKernelGGL(blend_backward_kernel, dim3((unsigned)tiles_padded), dim3(256), 0, stream,
                        ctx->ranges.as<uint2>(), svals, ctx->sorted_g.as<uint32_t>(), ctx->rec.as<float4>(),
-                       ctx->rec.as<float4>() + 2 * n, ctx->cov_coef.as<float4>(), ctx->ckpt.as<float>(), cam, grad_rgb, ctx->final_t.as<float>(),
+                       ctx->rec.as<float4>() + 2 * n, reinterpret_cast<const uint2*>(ctx->rec.as<float4>() + 3 * n),
+                       ctx->cov_coef.as<float4>(), ctx->ckpt.as<float>(), cam, grad_rgb, ctx->final_t.as<float>(),
                        ctx->last.as<uint32_t>(), ctx->inst_grad.as<float>(), inst_grad_op,
                        ctx->tile_cut.as<uint32_t>(), ctx->touched.as<uint8_t>());
     GSX_HIP_TRY(hipGetLastError(), "blend_backward_kernel");

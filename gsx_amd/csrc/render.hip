@@ -67,6 +67,24 @@ __device__ inline gsx_tile_span span_of(float4 r0, float4 r1) {
                               (int)(by & 0xffffu), (int)(by >> 16));
 }
 
+// A packed pixel box (box_lo / box_ext form, see in_box_packed) that no pixel lies in.
+constexpr uint32_t kEmptyBoxLo = 0xffffffffu;
+
+// The box the blend kernels test pixels against, in packed form (x0 | y0 << 16 and
+// (x1 - x0) | (y1 - y0) << 16): the rectangle of the record's box that can hold a contributing
+// pixel (gsx_contribution_box, from the record's mean, conic, opacity and box). It leaves out the
+// corners of the 3-sigma box and, for all but the most opaque Gaussians, its rim, where every pixel
+// fails the CPU's power or alpha cut; fewer pixels, and fewer waves of a tile, meet the entry.
+// Preprocess stores it per visible Gaussian; key emission keeps using the record's box.
+__device__ inline uint2 contribution_box_packed(float4 r0, float4 r1) {
+    const uint32_t bx = __float_as_uint(r1.z), by = __float_as_uint(r1.w);
+    int xa, xb, ya, yb;
+    gsx_contribution_box(r0.x, r0.y, r0.z, r0.w * 0.5f, r1.x, r1.y, (int)(bx & 0xffffu), (int)(bx >> 16),
+                         (int)(by & 0xffffu), (int)(by >> 16), &xa, &xb, &ya, &yb);
+    if (xa > xb || ya > yb) return make_uint2(kEmptyBoxLo, 0u);
+    return make_uint2((uint32_t)xa | ((uint32_t)ya << 16), (uint32_t)(xb - xa) | ((uint32_t)(yb - ya) << 16));
+}
+
 // Kept run of tile row ty of a box: len tiles from tile0 (len = 0 when none).
 __device__ inline void row_run(const gsx_tile_span& k, uint32_t bx, uint32_t by, int ty, int32_t tiles_x,
                                uint32_t& len, uint32_t& tile0) {
@@ -216,8 +234,8 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
     FieldSnapshot snap, int64_t n, const float* __restrict__ mean3d, const float* __restrict__ rotation,
     const float* __restrict__ logscale, const float* __restrict__ opacity, const float* __restrict__ sh0,
     const float* __restrict__ sh1, const float* __restrict__ sh2, const float* __restrict__ sh3, int sh_degree,
-    CameraParams cam, float4* __restrict__ rec, float4* __restrict__ col, float4* __restrict__ cov_coef,
-    uint32_t* __restrict__ tile_count,
+    CameraParams cam, float4* __restrict__ rec, float4* __restrict__ col, uint2* __restrict__ cbox,
+    float4* __restrict__ cov_coef, uint32_t* __restrict__ tile_count,
     float* __restrict__ visible_counter, uint32_t* __restrict__ big_list, uint32_t* __restrict__ big_count,
     uint32_t* __restrict__ clear0, uint32_t* __restrict__ clear1, uint32_t* __restrict__ clear2,
     unsigned long long* __restrict__ kept_part,
@@ -265,6 +283,7 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
             rec[2 * g + 0] = r0;
             rec[2 * g + 1] = r1;
             col[g] = r2;
+            cbox[g] = contribution_box_packed(r0, r1);
             if (cov_coef != nullptr) {
                 // d(conic)/d(cov2d) coefficients with the CPU's rounding (render.c:1578-1579,
                 // 1647-1655): the backward applies them per contribution, as the CPU does,
@@ -274,7 +293,10 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
                 const float k = 1.0f / (det * det);
                 cov_coef[2 * g + 0] =
                     make_float4(-p.c * p.c * k, p.b * p.c * k, -p.b * p.b * k, -(p.a * p.c + p.b * p.b) * k);
-                cov_coef[2 * g + 1] = make_float4(p.a * p.b * k, -p.a * p.a * k, 0.0f, 0.0f);
+                // with the doubled coefficients of the b row (exact: a power-of-two scaling) in the
+                // free slots, so the backward forms none of them per pixel
+                const float k0y = p.b * p.c * k, k1x = p.a * p.b * k;
+                cov_coef[2 * g + 1] = make_float4(k1x, -p.a * p.a * k, 2.0f * k0y, 2.0f * k1x);
             }
         }
     }
@@ -591,14 +613,10 @@ __device__ inline int xcd_tile_index(int block, int tiles) {
 
 // The box test in packed 16-bit halves, three vector instructions: (px, py) lies in
 // [x0, x1] x [y0, y1] iff both halves of (px | py << 16) - (x0 | y0 << 16) (each wrapping mod
-// 2^16) are at most those of (x1 - x0) | (y1 - y0) << 16. The blend kernels stage each box in
-// this form (box_lo, box_ext; kEmptyBoxLo / 0 for none: no pixel coordinate is 65535).
+// 2^16) are at most those of (x1 - x0) | (y1 - y0) << 16. The blend kernels stage each
+// contribution box (contribution_box_packed) in this form (kEmptyBoxLo / 0 for none: no pixel
+// coordinate is 65535).
 typedef uint16_t gsx_u16x2 __attribute__((ext_vector_type(2)));
-constexpr uint32_t kEmptyBoxLo = 0xffffffffu;
-__device__ inline uint32_t box_lo(uint32_t bx, uint32_t by) { return (bx & 0xffffu) | (by << 16); }
-__device__ inline uint32_t box_ext(uint32_t bx, uint32_t by) {
-    return ((bx >> 16) - (bx & 0xffffu)) | (((by >> 16) - (by & 0xffffu)) << 16);
-}
 __device__ inline bool in_box_packed(uint32_t pxy, uint32_t lo, uint32_t ext) {
     const gsx_u16x2 d = __builtin_bit_cast(gsx_u16x2, pxy) - __builtin_bit_cast(gsx_u16x2, lo);
     const gsx_u16x2 m = __builtin_elementwise_min(d, __builtin_bit_cast(gsx_u16x2, ext));
@@ -626,7 +644,7 @@ __device__ inline size_t checkpoint_slot(uint32_t range_start, int tile, uint32_
 __global__ __launch_bounds__(kBlendThreads) void blend_forward_kernel(
     const uint2* __restrict__ ranges, const uint32_t* __restrict__ values,
     const uint32_t* __restrict__ instance_gaussian, const float4* __restrict__ rec, const float4* __restrict__ col,
-    uint32_t* __restrict__ sorted_g,
+    const uint2* __restrict__ cbox, uint32_t* __restrict__ sorted_g,
     CameraParams cam, float* __restrict__ out_rgb,
     float* __restrict__ out_t, uint32_t* __restrict__ out_last, float* __restrict__ ckpt) {
     __shared__ float4 s_r0[kBlendThreads];
@@ -657,10 +675,10 @@ __global__ __launch_bounds__(kBlendThreads) void blend_forward_kernel(
             const uint32_t g = instance_gaussian[values[j]];
             if (sorted_g != nullptr) sorted_g[j] = g;  // TRAIN: the backward reads it
             const float4 geo1 = rec[2 * (size_t)g + 1], c = col[g];
-            const uint32_t bx = __float_as_uint(geo1.z), by = __float_as_uint(geo1.w);
+            const uint2 box = cbox[g];
             s_r0[threadIdx.x] = rec[2 * (size_t)g + 0];
             s_r1[threadIdx.x] = make_float4(geo1.x, geo1.y, c.x, c.y);
-            s_r2[threadIdx.x] = make_float4(c.z, __uint_as_float(box_lo(bx, by)), __uint_as_float(box_ext(bx, by)), c.w);
+            s_r2[threadIdx.x] = make_float4(c.z, __uint_as_float(box.x), __uint_as_float(box.y), c.w);
         } else {
             // past the list: a box no pixel lies in, so the last bucket can run whole
             s_r2[threadIdx.x] = make_float4(0.0f, __uint_as_float(kEmptyBoxLo), 0.0f, 0.0f);
@@ -756,8 +774,8 @@ constexpr int kBatchBuckets = kBackBatch / kBucket;
 
 __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
     const uint2* __restrict__ ranges, const uint32_t* __restrict__ values, const uint32_t* __restrict__ sorted_g,
-    const float4* __restrict__ rec, const float4* __restrict__ col, const float4* __restrict__ cov_coef,
-    const float* __restrict__ ckpt,
+    const float4* __restrict__ rec, const float4* __restrict__ col, const uint2* __restrict__ cbox,
+    const float4* __restrict__ cov_coef, const float* __restrict__ ckpt,
     CameraParams cam, const float* __restrict__ grad_rgb, const float* __restrict__ final_t,
     const uint32_t* __restrict__ last_contrib, float* __restrict__ instance_grad,
     float* __restrict__ instance_grad_op, uint32_t* __restrict__ tile_cut, uint8_t* __restrict__ touched) {
@@ -765,7 +783,7 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
     __shared__ float4 s_r1[kBackBatch];
     __shared__ float4 s_r2[kBackBatch];
     __shared__ float4 s_k0[kBackBatch];
-    __shared__ float2 s_k1[kBackBatch];
+    __shared__ float4 s_k1[kBackBatch];
     __shared__ uint32_t s_pos[kBackBatch];
     __shared__ float s_ck[kBatchBuckets][kBlendThreads];
     __shared__ float s_acc[kRowsPerTile][kBucket][kGrad2d];
@@ -838,21 +856,19 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
                 const uint32_t g = sorted_g[j];
                 touched[g] = 1;
                 const float4 geo1 = rec[2 * (size_t)g + 1], c = col[g];
-                const uint32_t bx = __float_as_uint(geo1.z), by = __float_as_uint(geo1.w);
+                const uint2 box = cbox[g];
                 s_r0[threadIdx.x] = rec[2 * (size_t)g + 0];
                 s_r1[threadIdx.x] = make_float4(geo1.x, geo1.y, c.x, c.y);
-                s_r2[threadIdx.x] =
-                    make_float4(c.z, __uint_as_float(box_lo(bx, by)), __uint_as_float(box_ext(bx, by)), c.w);
+                s_r2[threadIdx.x] = make_float4(c.z, __uint_as_float(box.x), __uint_as_float(box.y), c.w);
                 s_k0[threadIdx.x] = cov_coef[2 * (size_t)g + 0];
-                const float4 k1 = cov_coef[2 * (size_t)g + 1];
-                s_k1[threadIdx.x] = make_float2(k1.x, k1.y);
+                s_k1[threadIdx.x] = cov_coef[2 * (size_t)g + 1];
             } else {
                 const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
                 s_r0[threadIdx.x] = z;
                 s_r1[threadIdx.x] = z;
                 s_r2[threadIdx.x] = make_float4(0.0f, __uint_as_float(kEmptyBoxLo), 0.0f, 0.0f);  // no pixel
                 s_k0[threadIdx.x] = z;
-                s_k1[threadIdx.x] = make_float2(0.0f, 0.0f);
+                s_k1[threadIdx.x] = z;
             }
         }
 #pragma unroll
@@ -939,13 +955,13 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
                 const float dib = dpow * (-dx * dy);
                 const float dic = dpow * (-0.5f * dy * dy);
                 const float4 k0 = s_k0[kk];
-                const float2 k1 = s_k1[kk];
+                const float4 k1 = s_k1[kk];  // k1.z = 2 k0.y, k1.w = 2 k1.x
                 // the mean2d terms may fuse; the covariance terms keep the CPU's rounding, since
                 // near-plane Gaussians' covariance maps are close to singular
                 float v[kGrad2d] = {dpow * __builtin_fmaf(inv_a, dx, inv_b * dy),
                                     dpow * __builtin_fmaf(inv_b, dx, inv_c * dy),
                                     dia * k0.x + dib * k0.y + dic * k0.z,
-                                    dia * (2.0f * k0.y) + dib * k0.w + dic * (2.0f * k1.x),
+                                    dia * k1.z + dib * k0.w + dic * k1.w,
                                     dia * k0.z + dib * k1.x + dic * k1.y,
                                     w * d0,
                                     w * d1,

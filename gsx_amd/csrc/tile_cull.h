@@ -186,6 +186,22 @@ GSX_HD void gsx_tile_band_columns(const gsx_tile_span *k, int x0, int x1, int py
     *xa = c;
 }
 
+/* The pixel rectangle [*xa, *xb] x [*ya, *yb] of the box [x0, x1] x [y0, y1] that holds every
+ * pixel centre which may receive a contribution from the Gaussian: the columns from the row-span
+ * test with the whole box as one band, the rows from the same test with the roles of x and y
+ * exchanged (q(u, v) is the same form with A and C swapped, and the rounding allowances are
+ * symmetric in u and v). Empty when *xa > *xb or *ya > *yb. The blend kernels test pixels
+ * against this rectangle instead of the 3-sigma box: a pixel outside it fails the CPU's cuts. */
+GSX_HD void gsx_contribution_box(float mx, float my, float inv_a, float inv_b, float inv_c, float opacity, int x0,
+    int x1, int y0, int y1, int *xa, int *xb, int *ya, int *yb)
+{
+    const gsx_tile_span kx = gsx_tile_span_make(mx, my, inv_a, inv_b, inv_c, opacity, x0, x1, y0, y1);
+    const gsx_tile_span ky = gsx_tile_span_make(my, mx, inv_c, inv_b, inv_a, opacity, y0, y1, x0, x1);
+
+    gsx_tile_band_columns(&kx, x0, x1, y0, y1, xa, xb);
+    gsx_tile_band_columns(&ky, y0, y1, x0, x1, ya, yb);
+}
+
 /* Nonzero when some pixel centre of the inclusive pixel rectangle [px0, px1] x [py0, py1] may
  * receive a contribution from the Gaussian (the rectangle taken as its box). */
 GSX_HD int gsx_tile_may_contribute(float mx, float my, float inv_a, float inv_b, float inv_c, float opacity, int px0,

@@ -581,6 +581,14 @@ void oracle_tile_band_columns(float mx, float my, float inv_a, float inv_b, floa
     gsx_tile_band_columns(&k, x0, x1, py0, py1, &out[0], &out[1]);
 }
 
+/* The contribution box of tile_cull.h (gsx_contribution_box) for the Gaussian with pixel box
+ * [x0, x1] x [y0, y1]: out = xa, xb, ya, yb (empty when xa > xb or ya > yb). */
+void oracle_contribution_box(float mx, float my, float inv_a, float inv_b, float inv_c, float opacity, int x0,
+    int x1, int y0, int y1, int *out)
+{
+    gsx_contribution_box(mx, my, inv_a, inv_b, inv_c, opacity, x0, x1, y0, y1, &out[0], &out[1], &out[2], &out[3]);
+}
+
 /* [start, end) of every tile in the sorted key array; empty tiles get (0, 0). */
 void oracle_tile_ranges(int64_t instance_count, const uint64_t *keys, int64_t tile_count, uint32_t *out_ranges)
 {

@@ -63,6 +63,8 @@ class Oracle:
         lib.oracle_tile_may_contribute.argtypes = [_f] * 6 + [ctypes.c_int] * 4
         lib.oracle_tile_band_columns.restype = None
         lib.oracle_tile_band_columns.argtypes = [_f] * 6 + [ctypes.c_int] * 6 + [ctypes.POINTER(ctypes.c_int)]
+        lib.oracle_contribution_box.restype = None
+        lib.oracle_contribution_box.argtypes = [_f] * 6 + [ctypes.c_int] * 4 + [ctypes.POINTER(ctypes.c_int)]
         lib.oracle_tile_logf.restype = _f
         lib.oracle_tile_logf.argtypes = [_f]
         lib.oracle_render_forward.restype = ctypes.c_int
@@ -129,6 +131,14 @@ class Oracle:
         out = (ctypes.c_int * 2)()
         self.lib.oracle_tile_band_columns(mx, my, inv_a, inv_b, inv_c, opacity, *box, py0, py1, out)
         return int(out[0]), int(out[1])
+
+    def contribution_box(self, mx, my, inv_a, inv_b, inv_c, opacity, box) -> tuple:
+        """(xa, xb, ya, yb): the rectangle of the pixel box (x0, x1, y0, y1) that holds every pixel
+        that may receive a contribution (tile_cull.h gsx_contribution_box); empty when xa > xb or
+        ya > yb."""
+        out = (ctypes.c_int * 4)()
+        self.lib.oracle_contribution_box(mx, my, inv_a, inv_b, inv_c, opacity, *box, out)
+        return tuple(int(v) for v in out)
 
     def tile_ranges(self, keys, tile_count):
         ranges = np.zeros((tile_count, 2), np.uint32)

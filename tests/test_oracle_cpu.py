@@ -350,15 +350,15 @@ def test_tile_test_is_conservative_and_effective(oracle):
     assert kept_empty < 0.1 * empty
 
 
-def test_tile_band_columns_cover_every_contributing_pixel(oracle):
-    """The closed-form row runs of the tile test (tile_cull.h) against per-pixel brute force over
-    whole boxes: for every 16-row band of the box, every pixel that passes the CPU's cuts lies in
-    the band's kept columns. Cases: ordinary Gaussians, needles up to 400:1 at any angle, huge
-    Gaussians with means far off the image, and opacities just above the 1/255 cut."""
-    rng = np.random.default_rng(31)
+def _random_gaussians(seed, count):
+    """Gaussians for the brute-force checks of tile_cull.h, with the pixels of their 3-sigma box
+    (clipped to 128 x 128) that pass the CPU's power and alpha cuts. Modes: ordinary Gaussians,
+    needles up to 400:1 at any angle, huge Gaussians with means far off the image, and opacities
+    just above the 1/255 cut. Yields (case, mode, (mx, my, inv_a, inv_b, inv_c, op), box,
+    contributes[y, x])."""
+    rng = np.random.default_rng(seed)
     f = np.float32
-    checked = slack = 0
-    for case in range(1200):
+    for case in range(count):
         mode = case % 4
         sx, sy = np.exp(rng.uniform(-1.0, 4.5, 2))
         if mode == 1:
@@ -396,9 +396,19 @@ def test_tile_band_columns_cover_every_contributing_pixel(oracle):
         power = np.minimum(f(-0.5) * ((inv_a * dx * dx + f(2.0) * inv_b * dx * dy) + inv_c * dy * dy), f(0.0))
         alpha = np.minimum(f(0.999), op * np.exp(power.astype(np.float64)).astype(np.float32))
         contributes = (power >= f(-4.5)) & (alpha >= f(1.0) / f(255.0))
+        yield case, mode, (mx, my, inv_a, inv_b, inv_c, op), (x0, x1, y0, y1), contributes
+
+
+def test_tile_band_columns_cover_every_contributing_pixel(oracle):
+    """The closed-form row runs of the tile test (tile_cull.h) against per-pixel brute force over
+    whole boxes: for every 16-row band of the box, every pixel that passes the CPU's cuts lies in
+    the band's kept columns."""
+    checked = slack = 0
+    for case, mode, g, box, contributes in _random_gaussians(31, 1200):
+        x0, x1, y0, y1 = box
         for ty in range(y0 // 16, y1 // 16 + 1):
             py0, py1 = max(ty * 16, y0), min(ty * 16 + 15, y1)
-            xa, xb = oracle.tile_band_columns(mx, my, inv_a, inv_b, inv_c, op, (x0, x1, y0, y1), py0, py1)
+            xa, xb = oracle.tile_band_columns(*g, box, py0, py1)
             cols = np.nonzero(contributes[py0 - y0:py1 - y0 + 1].any(axis=0))[0] + x0
             if len(cols):
                 assert xa <= cols[0] and cols[-1] <= xb, (case, mode, ty, xa, xb, cols[0], cols[-1])
@@ -408,6 +418,34 @@ def test_tile_band_columns_cover_every_contributing_pixel(oracle):
             assert xb <= x1
     assert checked > 1500
     assert slack / checked < 2.0  # the runs hug the contributing columns
+
+
+def test_contribution_box_covers_every_contributing_pixel(oracle):
+    """The blend kernels' per-pixel box (tile_cull.h gsx_contribution_box) against per-pixel brute
+    force: every pixel of the 3-sigma box that passes the CPU's cuts lies inside it, it lies inside
+    the 3-sigma box, and it hugs the contributing pixels (the rows are found with x and y
+    exchanged: a wrong exchange of inv_a and inv_c, which planted in the restatement fails this
+    test, gives the transposed ellipse's rows)."""
+    checked = 0
+    area_box = area_tight = 0
+    slack = 0
+    for case, mode, g, box, contributes in _random_gaussians(47, 1600):
+        x0, x1, y0, y1 = box
+        xa, xb, ya, yb = oracle.contribution_box(*g, box)
+        rows = np.nonzero(contributes.any(axis=1))[0] + y0
+        cols = np.nonzero(contributes.any(axis=0))[0] + x0
+        if len(cols):
+            assert xa <= cols[0] and cols[-1] <= xb, (case, mode, xa, xb, cols[0], cols[-1])
+            assert ya <= rows[0] and rows[-1] <= yb, (case, mode, ya, yb, rows[0], rows[-1])
+            checked += 1
+            slack += (cols[0] - xa) + (xb - cols[-1]) + (rows[0] - ya) + (yb - rows[-1])
+        if xa <= xb and ya <= yb:
+            assert x0 <= xa and xb <= x1 and y0 <= ya and yb <= y1
+            area_tight += (xb - xa + 1) * (yb - ya + 1)
+        area_box += (x1 - x0 + 1) * (y1 - y0 + 1)
+    assert checked > 350
+    assert slack / checked < 2.0  # measured 0.46 pixels over the four sides
+    assert area_tight < 0.7 * area_box  # the corners and the rim of the 3-sigma box go (measured 0.56)
 
 
 def test_gather_rows(oracle):
