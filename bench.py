@@ -523,7 +523,40 @@ def extra_workloads(lib, steps, only=None):
         log(f"config 4 loop: {out['c4_refine_loop']}")
     if want("adc"):
         out.update(_refines())
+    if only == "gather32":  # a probe for profiling, not part of the default line
+        out["gather32"] = gather32_probe(lib, steps)
     return out
+
+
+def gather32_probe(lib, steps, rows=1_000_000, count=579_321):
+    """The floor of emission's record reads: gsx_hip_gather_rows_kernel_launch moving `count`
+    random 32-byte rows out of `rows` (the metric scene's Gaussians and its projected count, the
+    geometry records emission gathers in depth order), `steps` launches timed with HIP events.
+    Profiled under FETCH_SIZE / WRITE_SIZE, it shows the bytes a random 32-byte read costs."""
+    import numpy as np
+    import torch
+
+    from gsx_amd import _lib
+    from gsx_amd.backend import ptr, stream_handle
+    src = torch.rand((rows, 8), dtype=torch.float32, device="cuda")
+    dst = torch.empty((count, 8), dtype=torch.float32, device="cuda")
+    idx = torch.from_numpy(np.random.default_rng(5).permutation(rows)[:count].astype(np.int32)).cuda()
+    st = stream_handle()
+    for _ in range(3):
+        _lib.check(lib.gsx_hip_gather_rows_kernel_launch(ptr(src), ptr(dst), 32, count, ptr(idx), rows, None, st),
+                   "gather")
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        _lib.check(lib.gsx_hip_gather_rows_kernel_launch(ptr(src), ptr(dst), 32, count, ptr(idx), rows, None, st),
+                   "gather")
+    e1.record()
+    torch.cuda.synchronize()
+    assert torch.equal(dst, src[idx.long()])
+    ms = e0.elapsed_time(e1) / steps
+    moved = count * (32 + 32 + 4)  # row read, row written, index read
+    return {"rows": rows, "count": count, "row_bytes": 32, "ms": round(ms, 4),
+            "algorithmic_bytes": moved, "gbps": round(moved / (ms * 1e-3) / 1e9, 1)}
 
 
 def _config2(lib, steps):
@@ -628,7 +661,7 @@ def main():
                     help="inference renders timed for render_fps (default max(steps, 20); 0 skips them)")
     ap.add_argument("--extra-steps", type=int, default=10,
                     help="timed steps of the config 2/3/4 and density-control lines (0 disables them)")
-    ap.add_argument("--only", choices=("c2", "c3", "c4", "c4loop", "adc"), default=None,
+    ap.add_argument("--only", choices=("c2", "c3", "c4", "c4loop", "adc", "gather32"), default=None,
                     help="run just one of the config workloads (for profiling) and print its JSON")
     args = ap.parse_args()
     if args.gpus != 1:

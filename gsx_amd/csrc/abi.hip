@@ -955,7 +955,14 @@ gsx_hip_status enqueue_backward(gsx_hip_render_context* ctx, const float* grad_r
                        gs.logscale, gs.opacity, gs.sh0, gs.sh1, gs.sh2, gs.sh3, cam, ctx->grad2d.as<float>(),        \
                        ctx->tile_count.as<uint32_t>(), ctx->g_rank.as<uint32_t>(), ctx->offsets.as<uint32_t>(),      \
                        long_chunk, ctx->inst_grad.as<float>(), gi_op, ctx->touched.as<uint8_t>(), grads->mean3d,      \
-                       grads->rotation, grads->logscale, grads->opacity, grads->sh0, grads->sh1, grads->sh2, grads->sh3)
+                       grads->rotation, grads->logscale, grads->opacity, grads->sh0, grads->sh1, grads->sh2, grads->sh3, \
+                       vector_stores)
+        // the 3-float and SH sinks take whole 16-byte vector stores when they are 16-byte aligned
+        auto aligned16 = [](const float* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+        const int vector_stores = aligned16(grads->mean3d) && aligned16(grads->logscale) && aligned16(grads->sh0) &&
+                                  (gs.sh_degree < 1 || aligned16(grads->sh1)) &&
+                                  (gs.sh_degree < 2 || aligned16(grads->sh2)) &&
+                                  (gs.sh_degree < 3 || aligned16(grads->sh3));
         switch (gs.sh_degree) {
             case 0: GSX_PROJECTION_BACKWARD(0); break;
             case 1: GSX_PROJECTION_BACKWARD(1); break;

@@ -611,6 +611,23 @@ __device__ inline int xcd_tile_index(int block, int tiles) {
     return t;
 }
 
+// Pixel of thread t of a tile's 256-thread workgroup. Each wave takes an 8 x 8 quadrant of the
+// tile (wave w: quadrant (w & 1, w >> 1), lane l: pixel (l & 7, l >> 3) in it), not four 16-pixel
+// rows: a Gaussian's footprint meets fewer waves of a tile when the waves are square, and each
+// wave that meets it works on every lane. The DPP rows of 16 lanes are two pixel rows of a
+// quadrant; the backward's per-row partial sums do not depend on which pixels a row holds.
+#ifndef GSX_BLEND_SQUARE_WAVES
+#define GSX_BLEND_SQUARE_WAVES 1
+#endif
+__device__ inline int2 tile_pixel_of_thread(int t) {
+#if GSX_BLEND_SQUARE_WAVES
+    const int w = t >> 6, l = t & 63;
+    return make_int2(((w & 1) << 3) | (l & 7), ((w >> 1) << 3) | (l >> 3));
+#else
+    return make_int2(t & (kTile - 1), t / kTile);
+#endif
+}
+
 // The box test in packed 16-bit halves, three vector instructions: (px, py) lies in
 // [x0, x1] x [y0, y1] iff both halves of (px | py << 16) - (x0 | y0 << 16) (each wrapping mod
 // 2^16) are at most those of (x1 - x0) | (y1 - y0) << 16. The blend kernels stage each
@@ -656,8 +673,9 @@ __global__ __launch_bounds__(kBlendThreads) void blend_forward_kernel(
     if (tile >= tiles) return;
     if (threadIdx.x < GSX_EXPF_BLEND_TABLE_SIZE) s_exp2[threadIdx.x] = gsx_expf_blend_entry(threadIdx.x);
     const int tx = tile % cam.tiles_x, ty = tile / cam.tiles_x;
-    const int px = tx * kTile + (threadIdx.x & (kTile - 1));
-    const int py = ty * kTile + (threadIdx.x / kTile);
+    const int2 tp = tile_pixel_of_thread((int)threadIdx.x);
+    const int px = tx * kTile + tp.x;
+    const int py = ty * kTile + tp.y;
     const bool inside = px < cam.width && py < cam.height;
     const uint2 range = ranges[tile];
     const float fpx = (float)px + 0.5f;
@@ -764,7 +782,7 @@ constexpr int kGradRecord = 8;  // per-instance partials: channels 0-7 in one 32
 // and the instances behind saturated pixels cost the backward nothing.
 // ---------------------------------------------------------------------------------------------
 constexpr int kWavesPerTile = kBlendThreads / kWave;
-constexpr int kRowsPerTile = kTile;  // 16 pixel rows = 16 DPP rows of 16 lanes
+constexpr int kRowsPerTile = kTile;  // 16 DPP rows of 16 lanes per workgroup
 
 // The backward stages 64 entries per batch (8 buckets of 8): the kernel fits 71 VGPRs and 19 KB
 // of LDS, i.e. 7 waves per SIMD (16-entry buckets need 87 VGPRs and 28 KB: 5 waves; the
@@ -794,9 +812,10 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
     if (tile >= tiles) return;
     if (threadIdx.x < GSX_EXPF_BLEND_TABLE_SIZE) s_exp2[threadIdx.x] = gsx_expf_blend_entry(threadIdx.x);
     const int tx = tile % cam.tiles_x, ty = tile / cam.tiles_x;
-    const int px = tx * kTile + (threadIdx.x & (kTile - 1));
-    const int py = ty * kTile + (threadIdx.x / kTile);
-    const int row = threadIdx.x / kTile;  // pixel row of the tile = DPP row of the wave
+    const int2 tp = tile_pixel_of_thread((int)threadIdx.x);
+    const int px = tx * kTile + tp.x;
+    const int py = ty * kTile + tp.y;
+    const int row = threadIdx.x / kTile;  // DPP row of the workgroup (16 lanes)
     const bool inside = px < cam.width && py < cam.height;
     const uint2 range = ranges[tile];
     const size_t pix = (size_t)py * (size_t)cam.width + (size_t)px;
@@ -1277,6 +1296,27 @@ __device__ inline void add_dir(float ddir[3], const float dcol[3], const float* 
 // ---------------------------------------------------------------------------------------------
 // Instantiated per SH degree (0-3): the higher degrees' gradient arrays then exist only where
 // they are used (degree 0 needs 45 fewer live registers).
+// Stores the rows of a kWidth-float field for the workgroup's Gaussians [first, first + count)
+// (thread t holds row first + t) as whole 16-byte vectors: the rows go through LDS, then
+// consecutive threads store consecutive vectors of the block's contiguous span (a row of 3, 9, 15
+// or 21 floats would otherwise take that many 4-byte stores at a stride of the row). dst must be
+// 16-byte aligned; the span's last floats past its last whole vector are stored one by one. Every
+// thread of the workgroup calls it.
+template <int kWidth>
+__device__ inline void block_store_rows(float* __restrict__ dst, int64_t first, int count, const float (&row)[kWidth],
+                                        float* s_stage) {
+    __syncthreads();  // the previous field's stores have read s_stage
+#pragma unroll
+    for (int k = 0; k < kWidth; ++k) s_stage[threadIdx.x * kWidth + k] = row[k];
+    __syncthreads();
+    const int total = count * kWidth;
+    const int vecs = total / 4;
+    float* base = dst + first * kWidth;
+    for (int i = threadIdx.x; i < vecs; i += blockDim.x)
+        reinterpret_cast<float4*>(base)[i] = reinterpret_cast<const float4*>(s_stage)[i];
+    for (int i = vecs * 4 + (int)threadIdx.x; i < total; i += blockDim.x) base[i] = s_stage[i];
+}
+
 template <int kShDegree>
 __global__ __launch_bounds__(256) void projection_backward_kernel(
     int64_t n, const float* __restrict__ mean3d, const float* __restrict__ rotation,
@@ -1287,23 +1327,50 @@ __global__ __launch_bounds__(256) void projection_backward_kernel(
     const float* __restrict__ instance_grad, const float* __restrict__ instance_grad_op,
     const uint8_t* __restrict__ touched, float* __restrict__ g_mean3d,
     float* __restrict__ g_rotation, float* __restrict__ g_logscale, float* __restrict__ g_opacity,
-    float* __restrict__ g_sh0, float* __restrict__ g_sh1, float* __restrict__ g_sh2, float* __restrict__ g_sh3) {
+    float* __restrict__ g_sh0, float* __restrict__ g_sh1, float* __restrict__ g_sh2, float* __restrict__ g_sh3,
+    int vector_stores) {
     constexpr int sh_degree = kShDegree;
+    constexpr int kStageWidth = kShDegree >= 3 ? 21 : (kShDegree == 2 ? 15 : (kShDegree == 1 ? 9 : 3));
     // the exp table in LDS: its lookups wait on LDS, not on a global load each
     __shared__ uint64_t s_exp[GSX_EXP2_TABLE_SIZE];
+    // the block's rows of one gradient field on their way to whole-vector stores
+    __shared__ __align__(16) float s_stage[256 * kStageWidth];
+    const int64_t first = (int64_t)blockIdx.x * blockDim.x;
+    const int64_t gi = first + threadIdx.x;
+    const bool valid = gi < n;  // every thread stays for the block's staged stores
+    // a Gaussian that no tile's backward reached (touched[gi] == 0: invisible ones included) has
+    // a +0 screen-space gradient and so zero parameter gradients, written below as for an
+    // invisible one without recomputing its projection
+    const bool reached = valid && touched[gi] != 0;
+    if (!__syncthreads_or(reached ? 1 : 0)) {
+        // no Gaussian of the block was reached (most blocks when a few large Gaussians cover the
+        // image): its rows of every sink are zero, stored as whole vectors where aligned
+        const int count = (int)min((int64_t)blockDim.x, n - first);
+        if (valid) {
+            reinterpret_cast<float4*>(g_rotation)[gi] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            g_opacity[gi] = 0.0f;
+        }
+        float* const rows3[3] = {g_mean3d, g_logscale, g_sh0};
+        float* const rows_sh[3] = {g_sh1, g_sh2, g_sh3};
+        for (int f = 0; f < 3 + sh_degree; ++f) {
+            const int width = f < 3 ? 3 : 3 * (2 * (f - 2) + 1);  // 3, 3, 3, then 9, 15, 21
+            float* base = (f < 3 ? rows3[f] : rows_sh[f - 3]) + first * width;
+            const int total = count * width;
+            const int vecs = vector_stores ? total / 4 : 0;
+            for (int i = threadIdx.x; i < vecs; i += blockDim.x)
+                reinterpret_cast<float4*>(base)[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            for (int i = vecs * 4 + (int)threadIdx.x; i < total; i += blockDim.x) base[i] = 0.0f;
+        }
+        return;
+    }
     if (threadIdx.x < GSX_EXP2_TABLE_SIZE) s_exp[threadIdx.x] = gsx_exp2_table_entry(threadIdx.x);
     __syncthreads();
     const uint64_t* exp_tab = s_exp;
     __builtin_assume(exp_tab != nullptr);  // no run-time choice of table per lookup
-    const int64_t gi = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (gi >= n) return;
-    // a Gaussian that no tile's backward reached (touched[gi] == 0: invisible ones included) has
-    // a +0 screen-space gradient and so zero parameter gradients, written below as for an
-    // invisible one without recomputing its projection
     Projected p{};
     p.visible = false;
     uint32_t run_length = 0;
-    if (touched[gi] != 0) {
+    if (reached) {
         // issued first: its latency overlaps the recomputation below
         run_length = tile_count[gi];
         p = preprocess_one(gi, mean3d, rotation, logscale, opacity, sh0, sh1, sh2, sh3, sh_degree, cam, true, exp_tab);
@@ -1553,22 +1620,36 @@ __global__ __launch_bounds__(256) void projection_backward_kernel(
             gm[2] += w.m[0][2] * m0 + w.m[1][2] * m1 + w.m[2][2] * m2;
         }
     }
+    if (valid) {
+        // rows of 16 and 4 bytes: consecutive lanes already store consecutive addresses
+        reinterpret_cast<float4*>(g_rotation)[gi] = make_float4(gr[0], gr[1], gr[2], gr[3]);
+        g_opacity[gi] = gop;
+    }
+    if (vector_stores) {  // uniform: every 3-float (and SH) sink is 16-byte aligned
+        const int count = (int)min((int64_t)blockDim.x, n - first);
+        block_store_rows<3>(g_mean3d, first, count, gm, s_stage);
+        block_store_rows<3>(g_logscale, first, count, gl, s_stage);
+        block_store_rows<3>(g_sh0, first, count, gs0, s_stage);
+        if (sh_degree >= 1) block_store_rows<9>(g_sh1, first, count, gs1, s_stage);
+        if (sh_degree >= 2) block_store_rows<15>(g_sh2, first, count, gs2, s_stage);
+        if (sh_degree >= 3) block_store_rows<21>(g_sh3, first, count, gs3, s_stage);
+        return;
+    }
+    if (!valid) return;
     g_mean3d[gi * 3 + 0] = gm[0];
     g_mean3d[gi * 3 + 1] = gm[1];
     g_mean3d[gi * 3 + 2] = gm[2];
-    reinterpret_cast<float4*>(g_rotation)[gi] = make_float4(gr[0], gr[1], gr[2], gr[3]);
     g_logscale[gi * 3 + 0] = gl[0];
     g_logscale[gi * 3 + 1] = gl[1];
     g_logscale[gi * 3 + 2] = gl[2];
-    g_opacity[gi] = gop;
     g_sh0[gi * 3 + 0] = gs0[0];
     g_sh0[gi * 3 + 1] = gs0[1];
     g_sh0[gi * 3 + 2] = gs0[2];
-    if (sh_degree >= 1 && g_sh1 != nullptr)
+    if (sh_degree >= 1)
         for (int i = 0; i < 9; ++i) g_sh1[gi * 9 + i] = gs1[i];
-    if (sh_degree >= 2 && g_sh2 != nullptr)
+    if (sh_degree >= 2)
         for (int i = 0; i < 15; ++i) g_sh2[gi * 15 + i] = gs2[i];
-    if (sh_degree >= 3 && g_sh3 != nullptr)
+    if (sh_degree >= 3)
         for (int i = 0; i < 21; ++i) g_sh3[gi * 21 + i] = gs3[i];
 }
 
