@@ -63,6 +63,9 @@ def algorithmic_bytes(stage, geo, train=True):
     if stage == "sort":
         return sort_bytes(geo["S"], i)
     if stage == "ranges":
+        if i >= RANGES_SEARCH_MIN:
+            # per tile two binary searches of ceil(log2(I + 1)) 4-byte probes, one range out
+            return t * (8 * int(i).bit_length() + 8)
         return 4 * i + 8 * t  # sorted tiles in, one range per tile out
     if stage == "blend_forward":
         # ranges, reached entries' positions + Gaussians in, each reached Gaussian's record once;
@@ -93,6 +96,10 @@ def algorithmic_bytes(stage, geo, train=True):
     if stage == "adam":
         return 28 * 14 * n  # 14 floats per Gaussian: parameter, m, v in and out, gradient in
     return 0
+
+
+# instance count from which the ranges come from per-tile binary searches (abi.hip kRangesSearchMin)
+RANGES_SEARCH_MIN = 1 << 25
 
 
 def sort_bytes(passes, instances):
@@ -525,7 +532,76 @@ def extra_workloads(lib, steps, only=None):
         out.update(_refines())
     if only == "gather32":  # a probe for profiling, not part of the default line
         out["gather32"] = gather32_probe(lib, steps)
+    if only == "probes":  # calibration kernels for profiling, not part of the default line
+        out["probes"] = calibration_probes()
     return out
+
+
+def calibration_probes():
+    """Kernels of known work from libgsx_probe.so, timed with HIP events on torch's stream:
+    - valu_fma: 16 independent FMAs per loop step per lane on the scalar loop counter, at 4 and 8
+      waves per SIMD; the time gives the cycles one wave-level VALU instruction occupies a SIMD
+      (at the 2.4 GHz peak engine clock), and under rocprofv3 --pmc the counters' reading of a
+      kernel that does nothing but VALU work;
+    - store_zero: 16-byte zero stores over 56 MB (the metric's five SH0 parameter gradients,
+      the projection backward's writes) and 336 MB (config 4's), beside torch's fill of the same
+      bytes: the store-only floor of those sizes."""
+    import torch
+
+    from gsx_amd.backend import stream_handle
+    plib = ctypes.CDLL(os.path.join(ROOT, "gsx_amd", "libgsx_probe.so"))
+    plib.gsx_probe_valu_fma.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    plib.gsx_probe_store_zero.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p]
+    st = stream_handle()
+    out = {"engine_clock_ghz_assumed": 2.4, "simds": 1024}
+
+    def timed(fn, reps):
+        fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    iters = 20000
+    per_iter = plib.gsx_probe_valu_fma_per_iter()
+    rows = []
+    for waves_per_simd in (4, 8):
+        blocks = 256 * waves_per_simd  # 4 waves per workgroup, 4 SIMDs per CU, 256 CUs
+        buf = torch.empty(blocks * 256, dtype=torch.float32, device="cuda")
+        ms = timed(lambda: _probe_check(plib.gsx_probe_valu_fma(blocks, iters, buf.data_ptr(), st)), 3)
+        instr = blocks * 4 * iters * per_iter
+        cycles = ms * 1e-3 * 2.4e9 * 1024 / instr
+        rows.append({"waves_per_simd": waves_per_simd, "blocks": blocks, "iters": iters,
+                     "wave_valu_instructions": instr, "ms": round(ms, 4),
+                     "simd_cycles_per_wave_instruction": round(cycles, 3)})
+        log(f"valu probe: {rows[-1]}")
+    out["valu_fma"] = rows
+    stores = []
+    for mb, label in ((56, "metric projection backward"), (336, "config 4 projection backward")):
+        count = mb * 1_000_000 // 4
+        buf = torch.empty(count, dtype=torch.float32, device="cuda")
+        row = {"bytes": mb * 1_000_000, "sinks_of": label}
+        for blocks in (2048, 4096, 16384):
+            ms = timed(lambda: _probe_check(plib.gsx_probe_store_zero(buf.data_ptr(), count, blocks, st)), 20)
+            row[f"store_zero_{blocks}wg_us"] = round(ms * 1e3, 2)
+        ms = timed(lambda: buf.zero_(), 20)
+        row["torch_zero_us"] = round(ms * 1e3, 2)
+        best = min(v for k, v in row.items() if k.endswith("_us"))
+        row["best_gbps"] = round(row["bytes"] / (best * 1e-6) / 1e9, 1)
+        stores.append(row)
+        log(f"store probe: {row}")
+        del buf
+    out["store_zero"] = stores
+    return out
+
+
+def _probe_check(rc):
+    if rc != 0:
+        raise RuntimeError(f"probe launch failed: hipError {rc}")
 
 
 def gather32_probe(lib, steps, rows=1_000_000, count=579_321):
@@ -661,7 +737,7 @@ def main():
                     help="inference renders timed for render_fps (default max(steps, 20); 0 skips them)")
     ap.add_argument("--extra-steps", type=int, default=10,
                     help="timed steps of the config 2/3/4 and density-control lines (0 disables them)")
-    ap.add_argument("--only", choices=("c2", "c3", "c4", "c4loop", "adc", "gather32"), default=None,
+    ap.add_argument("--only", choices=("c2", "c3", "c4", "c4loop", "adc", "gather32", "probes"), default=None,
                     help="run just one of the config workloads (for profiling) and print its JSON")
     args = ap.parse_args()
     if args.gpus != 1:

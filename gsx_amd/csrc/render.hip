@@ -1056,12 +1056,6 @@ __device__ inline void add_record(float acc[kGrad2d], float4 a, float4 b, float 
     acc[8] += op;
 }
 
-__device__ inline void add_instance_grad(float acc[kGrad2d], const float* __restrict__ instance_grad,
-                                         const float* __restrict__ instance_grad_op, uint32_t p) {
-    const float4* rec4 = reinterpret_cast<const float4*>(instance_grad) + 2 * (size_t)p;
-    add_record(acc, rec4[0], rec4[1], instance_grad_op[p]);
-}
-
 // Position p's partial (three loads), or +0 where the blend backward wrote none.
 struct InstancePartial {
     float4 a, b;
@@ -1389,19 +1383,56 @@ __global__ __launch_bounds__(256) void projection_backward_kernel(
     for (int i = 0; i < 15; ++i) gs2[i] = 0.0f;
 #pragma unroll
     for (int i = 0; i < 21; ++i) gs3[i] = 0.0f;
-    if (p.visible) {
-        float a2[kGrad2d];
-        if (run_length > chunk) {
-            // a run of several chunks: the sums of its chunks, in chunk order (reduce_long_block)
+    float a2[kGrad2d];
+#pragma unroll
+    for (int c = 0; c < kGrad2d; ++c) a2[c] = 0.0f;
+    const bool multi = p.visible && run_length > chunk;
+    if (p.visible && !multi) {
+#pragma unroll
+        for (int c = 0; c < kGrad2d; ++c) a2[c] = grad2d[(size_t)gi * kGrad2d + c];
+    }
+    {
+        // A run of several chunks: the sums of its chunks (reduce_long_block), added in chunk
+        // order from +0. The wave loads one such run's chunk sums at once, lane k taking chunk k,
+        // and every lane adds them in lane order (the owner keeps the result): one load round per
+        // run instead of one per chunk, whose serial latency would set the kernel's time.
+        const int lane = (int)(threadIdx.x & (kWave - 1));
+        uint32_t rb = 0, re = 0;
+        if (multi) {
             const uint32_t r = gaussian_rank[gi];
-            const uint32_t b = offsets[r], e = offsets[r + 1];
-#pragma unroll
-            for (int c = 0; c < kGrad2d; ++c) a2[c] = 0.0f;
-            for (uint32_t cb = b; cb < e; cb += chunk) add_instance_grad(a2, instance_grad, instance_grad_op, cb);
-        } else {
-#pragma unroll
-            for (int c = 0; c < kGrad2d; ++c) a2[c] = grad2d[(size_t)gi * kGrad2d + c];
+            rb = offsets[r];
+            re = offsets[r + 1];
         }
+        for (uint64_t runs = wave_ballot(multi); runs != 0; runs &= runs - 1) {
+            const int src = __builtin_ctzll(runs);
+            const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)rb, src);
+            const uint32_t len = (uint32_t)__builtin_amdgcn_readlane((int)re, src) - b;
+            float v[kGrad2d];
+#pragma unroll
+            for (int c = 0; c < kGrad2d; ++c) v[c] = 0.0f;
+            if ((uint32_t)lane * chunk < len) {
+                const uint32_t cb = b + (uint32_t)lane * chunk;
+                const float4* rec4 = reinterpret_cast<const float4*>(instance_grad) + 2 * (size_t)cb;
+                const float4 x = rec4[0], y = rec4[1];
+                v[0] = x.x, v[1] = x.y, v[2] = x.z, v[3] = x.w;
+                v[4] = y.x, v[5] = y.y, v[6] = y.z, v[7] = y.w;
+                v[8] = instance_grad_op[cb];
+            }
+            float acc[kGrad2d];
+#pragma unroll
+            for (int c = 0; c < kGrad2d; ++c) acc[c] = 0.0f;
+            for (int k = 0; k < kWave && (uint32_t)k * chunk < len; ++k) {
+#pragma unroll
+                for (int c = 0; c < kGrad2d; ++c)
+                    acc[c] += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[c]), k));
+            }
+            if (lane == src) {
+#pragma unroll
+                for (int c = 0; c < kGrad2d; ++c) a2[c] = acc[c];
+            }
+        }
+    }
+    if (p.visible) {
         const float dmx = a2[0], dmy = a2[1];
         const float dca = a2[2], dcb = a2[3], dcc = a2[4];
         const float dcx = a2[5], dcy = a2[6], dcz = a2[7];

@@ -21,8 +21,14 @@ constexpr int kScanChunk = kScanThreads * kScanItems;  // 1024 elements per bloc
 
 constexpr int kSortChunk = 4096;  // keys per chunk (one upsweep / downsweep workgroup), public sorts
 constexpr int kRadixBits = 8;     // digit width of the public sorts
-// Chunk of the tile sort's passes (tile_sort_u32)
+// Chunks of the tile sort's passes (tile_sort_u32): 4096 keys below kLargeTileSort keys, 8192
+// from there on (runs of a digit twice as long per workgroup: each workgroup's writes meet half as
+// many distinct places of the output per byte, and the histograms and row scans halve; below it
+// the larger chunk leaves too few workgroups to fill the GPU). The downsweep runs chunk / 8
+// threads, 8 keys per thread.
 constexpr int kDigitsChunk = 4096;
+constexpr int kDigitsChunkLarge = 8192;
+constexpr int64_t kLargeTileSort = (int64_t)1 << 24;
 constexpr int kRowItems = 16;  // row scan: 16 chunk counts per thread and step
 constexpr int kRowChunk = kSortThreads * kRowItems;
 
@@ -226,9 +232,8 @@ inline void launch_rowscan(int bins, const uint32_t* hist, int64_t num_chunks, u
 // The downsweep runs 512 threads (8 waves of 512 keys, 8 rounds each): the serial ranking chain
 // of a chunk is half as long as with 4 waves.
 constexpr int kDownThreads = 512;
-constexpr int kDownWaves = kDownThreads / kWave;           // 8
 
-// Exclusive scan over the kBins digits held by threads 0..kBins-1 of a 512-thread workgroup
+// Exclusive scan over the kBins digits held by threads 0..kBins-1 of the workgroup
 // (threads past kBins pass 0 and get garbage); `total` receives the sum over the digits.
 template <int kBins>
 __device__ inline uint32_t digit_exclusive_scan(uint32_t v, uint32_t* s_wave, uint32_t& total) {
@@ -255,24 +260,29 @@ __device__ inline uint32_t digit_exclusive_scan(uint32_t v, uint32_t* s_wave, ui
 }
 
 // KeyT: uint64_t or uint32_t keys. kPairs with vals_in == nullptr: each key's value is its input
-// position (the first pass of the tile sort, whose values are the emission positions).
-template <bool kPairs, int kBits, int kChunk, typename KeyT = uint64_t>
-__global__ __launch_bounds__(kDownThreads, 8) void radix_downsweep_kernel(
+// position (the first pass of the tile sort, whose values are the emission positions). kNarrow:
+// n * sizeof(KeyT) <= 2^32, so every output byte offset fits in 32 bits. kThreads: workgroup size
+// (kChunk / kThreads keys per thread).
+template <bool kPairs, int kBits, int kChunk, typename KeyT = uint64_t, bool kNarrow = false,
+          int kThreads = kDownThreads>
+__global__ __launch_bounds__(kThreads, 8) void radix_downsweep_kernel(
     const KeyT* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, int64_t n,
     const uint32_t* __restrict__ n_dev, bool drop_sentinel, int shift, uint32_t dmask, int64_t num_chunks,
     const uint32_t* __restrict__ offsets, const uint32_t* __restrict__ totals, KeyT* __restrict__ keys_out,
     uint32_t* __restrict__ vals_out, uint32_t* __restrict__ kept_total) {
-    constexpr int kDownWaveKeys = kChunk / kDownWaves;  // keys ranked by one wave
+    constexpr int kWaves = kThreads / kWave;
+    constexpr int kDownWaveKeys = kChunk / kWaves;  // keys ranked by one wave
     constexpr int kDownRounds = kDownWaveKeys / kWave;
     static_assert(kDownRounds >= 1 && kDownWaveKeys % kWave == 0, "whole rounds per wave");
     __shared__ KeyT s_keys[kChunk];
     __shared__ uint32_t s_vals[kPairs ? kChunk : 1];
     constexpr int kBins = 1 << kBits;
-    static_assert(kBins <= kDownThreads, "one thread per digit");
-    __shared__ uint32_t s_cnt[kDownWaves][kBins];  // wave-private counters, then wave starts
-    __shared__ uint32_t s_local[kBins];            // start of each digit in the reordered chunk
-    __shared__ uint32_t s_global[kBins];           // output position of that start
-    __shared__ uint32_t s_wave[kDownWaves];
+    static_assert(kBins <= kThreads, "one thread per digit");
+    __shared__ uint32_t s_cnt[kWaves][kBins];  // wave-private counters, then wave starts
+    // output position of the reordered chunk's position 0 as counted in each digit: the digit's
+    // run starts at s_out[d] + (its start in the reordered chunk) (modulo 2^32)
+    __shared__ uint32_t s_out[kBins];
+    __shared__ uint32_t s_wave[kWaves];
     __shared__ uint32_t s_kept;                     // keys of the chunk that are moved
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
@@ -287,7 +297,7 @@ __global__ __launch_bounds__(kDownThreads, 8) void radix_downsweep_kernel(
     const int td = min((int)threadIdx.x, kBins - 1);
     const uint32_t my_total = totals[td];
     const uint32_t my_offset = offsets[(int64_t)td * num_chunks + chunk];
-    for (int i = threadIdx.x; i < kDownWaves * kBins; i += kDownThreads) (&s_cnt[0][0])[i] = 0;
+    for (int i = threadIdx.x; i < kWaves * kBins; i += kThreads) (&s_cnt[0][0])[i] = 0;
     __syncthreads();
     // 1. per wave: stable ranks among equal digits (rank = keys of the digit before it in this
     //    wave's eighth of the chunk), packed as digit << 16 | rank
@@ -309,16 +319,24 @@ __global__ __launch_bounds__(kDownThreads, 8) void radix_downsweep_kernel(
         const bool valid = local < chunk_count && !(drop_sentinel && (uint64_t)key[r] == kSentinelKey);
         const uint32_t d = digit_of<kBits>(key[r], shift) & dmask;
         const uint64_t vm = wave_ballot(valid);
+        // per digit bit: the bit as 0 / all ones (a signed bit-field extract) and the wave's ballot
+        // of it; the lanes that agree with this lane in bit b are ~(ballot ^ ext), folded into the
+        // peer mask with one three-input bitwise operation per half (truth table 0x90:
+        // p & ~(m ^ e))
+        uint32_t ext[kBits];
+        uint64_t m[kBits];
+#pragma unroll
+        for (int b = 0; b < kBits; ++b) {
+            ext[b] = (uint32_t)((int32_t)(d << (31 - b)) >> 31);
+            asm volatile("" : "+v"(ext[b]));  // the ballot compares the extracted bit itself
+        }
+#pragma unroll
+        for (int b = 0; b < kBits; ++b) m[b] = wave_ballot(ext[b] != 0u);
         uint32_t plo = (uint32_t)vm, phi = (uint32_t)(vm >> 32);
 #pragma unroll
         for (int b = 0; b < kBits; ++b) {
-            // the bit as 0 / all ones (a signed bit-field extract); the lanes that agree with this
-            // lane in bit b are ~(m ^ ext), one three-input bitwise operation per half
-            uint32_t ext = (uint32_t)((int32_t)(d << (31 - b)) >> 31);
-            asm volatile("" : "+v"(ext));  // the ballot compares the extracted bit itself
-            const uint64_t m = wave_ballot(ext != 0u);
-            plo &= ~((uint32_t)m ^ ext);
-            phi &= ~((uint32_t)(m >> 32) ^ ext);
+            plo = __builtin_amdgcn_bitop3_b32(plo, (uint32_t)m[b], ext[b], 0x90);
+            phi = __builtin_amdgcn_bitop3_b32(phi, (uint32_t)(m[b] >> 32), ext[b], 0x90);
         }
         const uint64_t peers = (uint64_t)plo | ((uint64_t)phi << 32);
         const uint32_t before = s_cnt[wave][d];  // read by all lanes before the leader updates
@@ -326,6 +344,8 @@ __global__ __launch_bounds__(kDownThreads, 8) void radix_downsweep_kernel(
         if (valid && rank == 0) s_cnt[wave][d] = before + (uint32_t)__popcll(peers);
         __builtin_amdgcn_wave_barrier();
         dr[r] = valid ? (d << 16) | (before + rank) : 0xffffffffu;
+        // formed here, so that the peer masks die with the round (not kept alive for the reorder)
+        asm volatile("" : "+v"(dr[r]));
     }
     __syncthreads();
     // 2. threads 0..255 = digits: wave starts inside the digit, digit starts inside the chunk,
@@ -334,7 +354,7 @@ __global__ __launch_bounds__(kDownThreads, 8) void radix_downsweep_kernel(
         const int t = threadIdx.x;
         uint32_t cnt = 0;
 #pragma unroll
-        for (int w = 0; w < kDownWaves; ++w) cnt += t < kBins ? s_cnt[w][t] : 0u;
+        for (int w = 0; w < kWaves; ++w) cnt += t < kBins ? s_cnt[w][t] : 0u;
         uint32_t kept, all_kept;
         const uint32_t start = digit_exclusive_scan<kBins>(cnt, s_wave, kept);
         const uint32_t digit_base = digit_exclusive_scan<kBins>(t < kBins ? my_total : 0u, s_wave, all_kept);
@@ -342,11 +362,10 @@ __global__ __launch_bounds__(kDownThreads, 8) void radix_downsweep_kernel(
         // the number of keys this pass keeps, for the later passes (a plain store: one writer)
         if (kept_total != nullptr && chunk == 0 && t == 0) *kept_total = all_kept;
         if (t < kBins) {
-            s_local[t] = start;
-            s_global[t] = digit_base + my_offset;
+            s_out[t] = digit_base + my_offset - start;
             uint32_t run = start;
 #pragma unroll
-            for (int w = 0; w < kDownWaves; ++w) {
+            for (int w = 0; w < kWaves; ++w) {
                 const uint32_t c = s_cnt[w][t];
                 s_cnt[w][t] = run;
                 run += c;
@@ -364,14 +383,38 @@ __global__ __launch_bounds__(kDownThreads, 8) void radix_downsweep_kernel(
         }
     }
     __syncthreads();
-    // 4. write out in order: runs of one digit go to consecutive addresses
+    // 4. write out in order: runs of one digit go to consecutive addresses. Every LDS read of the
+    //    thread's keys is issued before the first store; kNarrow: byte offsets of the output fit
+    //    in 32 bits (stores address a scalar base plus a 32-bit offset).
+    constexpr int kOutRounds = kChunk / kThreads;
     const int kept_count = (int)s_kept;
-    for (int i = threadIdx.x; i < kept_count; i += kDownThreads) {
-        const KeyT k = s_keys[i];
-        const uint32_t d = digit_of<kBits>(k, shift) & dmask;
-        const uint32_t pos = s_global[d] + ((uint32_t)i - s_local[d]);
-        keys_out[pos] = k;
-        if (kPairs) vals_out[pos] = s_vals[i];
+    KeyT ok[kOutRounds];
+    uint32_t ov[kOutRounds];
+    uint32_t opos[kOutRounds];
+#pragma unroll
+    for (int j = 0; j < kOutRounds; ++j) {
+        const int i = (int)threadIdx.x + j * kThreads;
+        ok[j] = s_keys[i];
+        ov[j] = kPairs ? s_vals[i] : 0u;
+    }
+#pragma unroll
+    for (int j = 0; j < kOutRounds; ++j) {
+        const int i = (int)threadIdx.x + j * kThreads;
+        opos[j] = s_out[digit_of<kBits>(ok[j], shift) & dmask] + (uint32_t)i;
+    }
+#pragma unroll
+    for (int j = 0; j < kOutRounds; ++j) {
+        const int i = (int)threadIdx.x + j * kThreads;
+        if (i < kept_count) {
+            if (kNarrow) {
+                *reinterpret_cast<KeyT*>(reinterpret_cast<char*>(keys_out) + (uint32_t)(opos[j] * sizeof(KeyT))) =
+                    ok[j];
+                if (kPairs) *reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(vals_out) + (opos[j] << 2)) = ov[j];
+            } else {
+                keys_out[opos[j]] = ok[j];
+                if (kPairs) vals_out[opos[j]] = ov[j];
+            }
+        }
     }
 }
 
@@ -384,6 +427,11 @@ namespace {
 // n_dev: see radix_upsweep_kernel. compact_first: the first pass reads all n keys and drops the
 // sentinel keys (stably compacting the rest to the front), its downsweep stores the number of
 // kept keys in *n_dev, and the later passes sort that many.
+// Output byte offsets of n keys of key_bytes bytes (and of their 4-byte values) fit in 32 bits.
+inline bool narrow_offsets(int64_t n, size_t key_bytes) {
+    return (uint64_t)n * key_bytes <= (uint64_t)1 << 32;
+}
+
 template <int kBits, int kChunk>
 size_t radix_temp_bytes(int64_t n) {
     int64_t chunks = (n + kChunk - 1) / kChunk;
@@ -421,9 +469,15 @@ gsx_hip_status radix_sort_u64(uint64_t* keys, uint32_t* vals, uint64_t* keys_alt
             hipLaunchKernelGGL((radix_upsweep_kernel<kBits, kChunk>), dim3(sort_chunk_grid(chunks)), dim3(kSortThreads),
                                0, stream, kin, n, live, drop, shift, dmask, chunks, hist);
             launch_rowscan(kBins, hist, chunks, offsets, totals, stream);
-            hipLaunchKernelGGL((radix_downsweep_kernel<kPairs, kBits, kChunk>), dim3(sort_chunk_grid(chunks)),
-                               dim3(kDownThreads), 0, stream, kin, vin, n, live, drop, shift, dmask, chunks, offsets,
-                               totals, kout, vout, drop ? n_dev : nullptr);
+            if (narrow_offsets(n, sizeof(uint64_t))) {
+                hipLaunchKernelGGL((radix_downsweep_kernel<kPairs, kBits, kChunk, uint64_t, true>),
+                                   dim3(sort_chunk_grid(chunks)), dim3(kDownThreads), 0, stream, kin, vin, n, live,
+                                   drop, shift, dmask, chunks, offsets, totals, kout, vout, drop ? n_dev : nullptr);
+            } else {
+                hipLaunchKernelGGL((radix_downsweep_kernel<kPairs, kBits, kChunk, uint64_t, false>),
+                                   dim3(sort_chunk_grid(chunks)), dim3(kDownThreads), 0, stream, kin, vin, n, live,
+                                   drop, shift, dmask, chunks, offsets, totals, kout, vout, drop ? n_dev : nullptr);
+            }
             in_alt ^= 1;
         }
     }
@@ -557,12 +611,12 @@ gsx_hip_status radix_sort_keys_u64_compacting(uint64_t* keys, uint64_t* keys_alt
                                                                          stream);
 }
 
-template <int kBits>
+template <int kBits, int kChunk>
 gsx_hip_status tile_sort_passes(const uint32_t* tiles, uint32_t* tiles_alt, uint32_t* tiles_sorted, uint32_t* vals_alt,
                                 uint32_t* vals_sorted, int64_t n, int tile_bits, int passes, void* temp,
                                 hipStream_t stream) {
     constexpr int kBins = 1 << kBits;
-    int64_t chunks = (n + kDigitsChunk - 1) / kDigitsChunk;
+    int64_t chunks = (n + kChunk - 1) / kChunk;
     if (chunks < 1) chunks = 1;
     const int64_t hist_count = chunks * kBins;
     uint32_t* hist = static_cast<uint32_t*>(temp);
@@ -578,12 +632,18 @@ gsx_hip_status tile_sort_passes(const uint32_t* tiles, uint32_t* tiles_alt, uint
         const int shift = k * kBits;
         const int width = tile_bits - shift < kBits ? tile_bits - shift : kBits;
         const uint32_t dmask = width > 0 ? (1u << width) - 1u : 0u;
-        hipLaunchKernelGGL((radix_upsweep_kernel<kBits, kDigitsChunk, uint32_t>), dim3(sort_chunk_grid(chunks)),
+        hipLaunchKernelGGL((radix_upsweep_kernel<kBits, kChunk, uint32_t>), dim3(sort_chunk_grid(chunks)),
                            dim3(kSortThreads), 0, stream, kin, n, nullptr, false, shift, dmask, chunks, hist);
         launch_rowscan(kBins, hist, chunks, offsets, totals, stream);
-        hipLaunchKernelGGL((radix_downsweep_kernel<true, kBits, kDigitsChunk, uint32_t>), dim3(sort_chunk_grid(chunks)),
-                           dim3(kDownThreads), 0, stream, kin, vin, n, nullptr, false, shift, dmask, chunks, offsets,
-                           totals, kout, vout, nullptr);
+        if (narrow_offsets(n, sizeof(uint32_t))) {
+            hipLaunchKernelGGL((radix_downsweep_kernel<true, kBits, kChunk, uint32_t, true, kChunk / 8>),
+                               dim3(sort_chunk_grid(chunks)), dim3(kChunk / 8), 0, stream, kin, vin, n, nullptr,
+                               false, shift, dmask, chunks, offsets, totals, kout, vout, nullptr);
+        } else {
+            hipLaunchKernelGGL((radix_downsweep_kernel<true, kBits, kChunk, uint32_t, false, kChunk / 8>),
+                               dim3(sort_chunk_grid(chunks)), dim3(kChunk / 8), 0, stream, kin, vin, n, nullptr,
+                               false, shift, dmask, chunks, offsets, totals, kout, vout, nullptr);
+        }
         kin = kout;
         vin = vout;
     }
@@ -598,19 +658,16 @@ gsx_hip_status tile_sort_u32(const uint32_t* tiles, uint32_t* tiles_alt, uint32_
         return GSX_HIP_ERROR_INVALID_ARGUMENT;
     }
     if (n == 0) return GSX_HIP_SUCCESS;
+#define GSX_TILE_SORT(B, C) \
+    tile_sort_passes<B, C>(tiles, tiles_alt, tiles_sorted, vals_alt, vals_sorted, n, tile_bits, passes, temp, stream)
+    const bool large = n >= kLargeTileSort;
     switch (digit_bits) {
-        case 6:
-            return tile_sort_passes<6>(tiles, tiles_alt, tiles_sorted, vals_alt, vals_sorted, n, tile_bits, passes, temp,
-                                       stream);
-        case 7:
-            return tile_sort_passes<7>(tiles, tiles_alt, tiles_sorted, vals_alt, vals_sorted, n, tile_bits, passes, temp,
-                                       stream);
-        case 8:
-            return tile_sort_passes<8>(tiles, tiles_alt, tiles_sorted, vals_alt, vals_sorted, n, tile_bits, passes, temp,
-                                       stream);
-        default:
-            return GSX_HIP_ERROR_INVALID_ARGUMENT;
+        case 6: return large ? GSX_TILE_SORT(6, kDigitsChunkLarge) : GSX_TILE_SORT(6, kDigitsChunk);
+        case 7: return large ? GSX_TILE_SORT(7, kDigitsChunkLarge) : GSX_TILE_SORT(7, kDigitsChunk);
+        case 8: return large ? GSX_TILE_SORT(8, kDigitsChunkLarge) : GSX_TILE_SORT(8, kDigitsChunk);
+        default: return GSX_HIP_ERROR_INVALID_ARGUMENT;
     }
+#undef GSX_TILE_SORT
 }
 
 size_t tile_sort_u32_temp_bytes(int64_t n) { return radix_temp_bytes<8, kDigitsChunk>(n); }
