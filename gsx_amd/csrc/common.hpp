@@ -310,6 +310,46 @@ __device__ inline Projected preprocess_one(int64_t g, const float* __restrict__ 
     return p;
 }
 
+// The part of preprocess_one's projection that the projection backward uses for a Gaussian
+// already known visible: the camera-space mean, the view direction and the clamped SH colour,
+// by the same operations in the same order (so the same values).
+struct ProjectedView {
+    bool visible;
+    float xc, yc, zc;
+    float color[3];
+    float dir[3];
+};
+
+__device__ inline ProjectedView project_view(int64_t g, const float* __restrict__ mean3d,
+                                             const float* __restrict__ sh0, const float* __restrict__ sh1,
+                                             const float* __restrict__ sh2, const float* __restrict__ sh3,
+                                             int sh_degree, const CameraParams& cam) {
+    ProjectedView p;
+    p.visible = true;
+    const float mx = mean3d[g * 3 + 0], my = mean3d[g * 3 + 1], mz = mean3d[g * 3 + 2];
+    const Mat3 w = camera_rotation(cam);
+    float xc = w.m[0][0] * mx + w.m[0][1] * my + w.m[0][2] * mz;
+    float yc = w.m[1][0] * mx + w.m[1][1] * my + w.m[1][2] * mz;
+    float zc = w.m[2][0] * mx + w.m[2][1] * my + w.m[2][2] * mz;
+    p.xc = xc + cam.t[0];
+    p.yc = yc + cam.t[1];
+    p.zc = zc + cam.t[2];
+    const float dx = mx - cam.centre[0], dy = my - cam.centre[1], dz = mz - cam.centre[2];
+    const float len = sqrtf(dx * dx + dy * dy + dz * dz);
+    if (len <= 0.0f) {
+        p.dir[0] = 0.0f;
+        p.dir[1] = 0.0f;
+        p.dir[2] = 0.0f;
+    } else {
+        const float s = 1.0f / len;
+        p.dir[0] = dx * s;
+        p.dir[1] = dy * s;
+        p.dir[2] = dz * s;
+    }
+    eval_sh(g, sh_degree, p.dir, sh0, sh1, sh2, sh3, p.color);
+    return p;
+}
+
 // ---- wave64 helpers ------------------------------------------------------------------------
 
 // Mask of the active lanes whose p is true. A bool that the compiler already holds as a lane

@@ -1357,18 +1357,32 @@ __global__ __launch_bounds__(256) void projection_backward_kernel(
         }
         return;
     }
+    // A reached Gaussian was emitted, so preprocess_one found it visible in the forward; of its
+    // projection the backward uses only the camera-space mean, the view direction and the clamped
+    // colour, recomputed here by the same operations (not the covariance, conic and box, whose
+    // dependent chain would set the time of a block holding one of the few reached Gaussians).
+    // Every input is loaded before the exp table's barrier, so their latency overlaps it.
+    ProjectedView p{};
+    p.visible = reached;
+    uint32_t run_length = 0;
+    uint32_t rank = 0;
+    float4 q = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float ls[3] = {0.0f, 0.0f, 0.0f};
+    if (reached) {
+        // the rank is used only by a run of several chunks; read here, coalesced, it takes a load
+        // round off that chain
+        run_length = tile_count[gi];
+        rank = gaussian_rank[gi];
+        q = reinterpret_cast<const float4*>(rotation)[gi];
+        ls[0] = logscale[gi * 3 + 0];
+        ls[1] = logscale[gi * 3 + 1];
+        ls[2] = logscale[gi * 3 + 2];
+        p = project_view(gi, mean3d, sh0, sh1, sh2, sh3, sh_degree, cam);
+    }
     if (threadIdx.x < GSX_EXP2_TABLE_SIZE) s_exp[threadIdx.x] = gsx_exp2_table_entry(threadIdx.x);
     __syncthreads();
     const uint64_t* exp_tab = s_exp;
     __builtin_assume(exp_tab != nullptr);  // no run-time choice of table per lookup
-    Projected p{};
-    p.visible = false;
-    uint32_t run_length = 0;
-    if (reached) {
-        // issued first: its latency overlaps the recomputation below
-        run_length = tile_count[gi];
-        p = preprocess_one(gi, mean3d, rotation, logscale, opacity, sh0, sh1, sh2, sh3, sh_degree, cam, true, exp_tab);
-    }
     float gm[3] = {0.0f, 0.0f, 0.0f};
     float gr[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     float gl[3] = {0.0f, 0.0f, 0.0f};
@@ -1399,9 +1413,8 @@ __global__ __launch_bounds__(256) void projection_backward_kernel(
         const int lane = (int)(threadIdx.x & (kWave - 1));
         uint32_t rb = 0, re = 0;
         if (multi) {
-            const uint32_t r = gaussian_rank[gi];
-            rb = offsets[r];
-            re = offsets[r + 1];
+            rb = offsets[rank];
+            re = offsets[rank + 1];
         }
         for (uint64_t runs = wave_ballot(multi); runs != 0; runs &= runs - 1) {
             const int src = __builtin_ctzll(runs);
@@ -1438,12 +1451,18 @@ __global__ __launch_bounds__(256) void projection_backward_kernel(
         const float dcx = a2[5], dcy = a2[6], dcz = a2[7];
         const float dop = a2[8];
         const Mat3 w = camera_rotation(cam);
-        const float4 q = reinterpret_cast<const float4*>(rotation)[gi];
-        const float ls[3] = {logscale[gi * 3 + 0], logscale[gi * 3 + 1], logscale[gi * 3 + 2]};
-        const Mat3 cov3d = cov3d_from(q, ls, exp_tab);
         const Mat3 rot = rotation_from_xyzw(q.x, q.y, q.z, q.w);
         const float sx = gsx_expf_table(ls[0], exp_tab), sy = gsx_expf_table(ls[1], exp_tab),
                     sz = gsx_expf_table(ls[2], exp_tab);
+        // R S, and the covariance (R S)(R S)^T by cov3d_from's operations
+        Mat3 srot = rot;
+#pragma unroll
+        for (int row = 0; row < 3; ++row) {
+            srot.m[row][0] *= sx;
+            srot.m[row][1] *= sy;
+            srot.m[row][2] *= sz;
+        }
+        const Mat3 cov3d = mat3_mul_t(srot, srot);
         const float zc = p.zc, xc = p.xc, yc = p.yc;
         const float j00 = cam.fx / zc;
         const float j02 = -cam.fx * xc / (zc * zc);
@@ -1564,13 +1583,6 @@ __global__ __launch_bounds__(256) void projection_backward_kernel(
                 for (int col = 0; col < 3; ++col)
                     dcov3.m[row][col] = mm[0][row] * (dca * mm[0][col] + 0.5f * dcb * mm[1][col]) +
                                         mm[1][row] * (0.5f * dcb * mm[0][col] + dcc * mm[1][col]);
-            Mat3 srot = rot;
-#pragma unroll
-            for (int row = 0; row < 3; ++row) {
-                srot.m[row][0] *= sx;
-                srot.m[row][1] *= sy;
-                srot.m[row][2] *= sz;
-            }
             Mat3 dsum;
 #pragma unroll
             for (int row = 0; row < 3; ++row)
