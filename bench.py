@@ -197,6 +197,46 @@ def profiled_pipe_counters(kernel):
     return None
 
 
+def profiled_valu_instructions(kernel):
+    """Wave-level VALU instructions per dispatch of `kernel` (SQ_INSTS_VALU) from the committed SQ
+    summary, or None."""
+    if not os.path.exists(SQ_FILE):
+        return None
+    with open(SQ_FILE) as f:
+        for line in f:
+            cells = [c.strip() for c in line.strip().strip("|").split("|")]
+            if len(cells) >= 8 and cells[0] == kernel and cells[1] != "pipe":
+                try:
+                    return int(float(cells[6]))
+                except ValueError:
+                    return None
+    return None
+
+
+def probe_valu_rate():
+    """Wave-level VALU instructions per second of a kernel that does nothing but independent FMAs
+    (libgsx_probe.so, 8 waves per SIMD on every SIMD), on this GPU, now; None without the probe."""
+    import torch
+
+    from gsx_amd.backend import stream_handle
+    path = os.path.join(ROOT, "gsx_amd", "libgsx_probe.so")
+    if not os.path.exists(path):
+        return None
+    plib = ctypes.CDLL(path)
+    plib.gsx_probe_valu_fma.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    blocks, iters = 2048, 20000
+    buf = torch.empty(blocks * 256, dtype=torch.float32, device="cuda")
+    st = stream_handle()
+    _probe_check(plib.gsx_probe_valu_fma(blocks, iters, buf.data_ptr(), st))
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    _probe_check(plib.gsx_probe_valu_fma(blocks, iters, buf.data_ptr(), st))
+    e1.record()
+    torch.cuda.synchronize()
+    return blocks * 4 * iters * plib.gsx_probe_valu_fma_per_iter() / (e0.elapsed_time(e1) * 1e-3)
+
+
 def cpu_baseline(scene, camera_block, target, iters):
     """Time the unmodified gsx CPU backend (oracle/_ref) on a bounded sample of the workload:
     every 10th Gaussian of the 1M scene (same distributions) at the full 1920x1080, pose 0, the
@@ -913,9 +953,23 @@ def main():
     kernels = stage_table(stage_ms, geos)
     dominant = kernels[0]
     sort_entry = next(k for k in kernels if k["stage"] == "sort")
-    # the blend kernels are bound by the vector ALU and LDS rather than HBM: their VALU busy and
-    # LDS bank-conflict shares of GPU time from the committed SQ profile of this workload
+    # the blend kernels are bound by the vector ALU and LDS rather than HBM: rocprofv3's VALU busy
+    # and LDS bank-conflict shares from the committed SQ profile of this workload, and the VALU
+    # issue rate (the profile's instructions per dispatch over this run's launch time) against the
+    # rate of a kernel that does nothing but VALU work, timed now (rocprofv3's VALUBusy assumes 4
+    # cycles per wave-level instruction, which part of the blend kernels' instructions undercut,
+    # so it reads above 100)
     pipe = {k: profiled_pipe_counters(k) for k in ("blend_forward_kernel", "blend_backward_kernel")}
+    probe_rate = probe_valu_rate()
+    for k, stage in (("blend_forward_kernel", "blend_forward"), ("blend_backward_kernel", "blend_backward")):
+        instr = profiled_valu_instructions(k)
+        ms = next((x["ms"] for x in kernels if x["stage"] == stage), None)
+        if pipe[k] is not None and instr is not None and ms:
+            rate = instr / (ms * 1e-3)
+            pipe[k].update({"valu_instructions_per_launch": instr, "valu_issue_g_per_s": round(rate / 1e9, 1)})
+            if probe_rate:
+                pipe[k].update({"probe_valu_g_per_s": round(probe_rate / 1e9, 1),
+                                "valu_issue_vs_probe": round(rate / probe_rate, 3)})
 
     result = {
         "metric": "fwd+bwd train iters/sec @1M Gaussians 1920x1080; fwd render FPS; sort GB/s",
