@@ -616,16 +616,9 @@ __device__ inline int xcd_tile_index(int block, int tiles) {
 // rows: a Gaussian's footprint meets fewer waves of a tile when the waves are square, and each
 // wave that meets it works on every lane. The DPP rows of 16 lanes are two pixel rows of a
 // quadrant; the backward's per-row partial sums do not depend on which pixels a row holds.
-#ifndef GSX_BLEND_SQUARE_WAVES
-#define GSX_BLEND_SQUARE_WAVES 1
-#endif
 __device__ inline int2 tile_pixel_of_thread(int t) {
-#if GSX_BLEND_SQUARE_WAVES
     const int w = t >> 6, l = t & 63;
     return make_int2(((w & 1) << 3) | (l & 7), ((w >> 1) << 3) | (l >> 3));
-#else
-    return make_int2(t & (kTile - 1), t / kTile);
-#endif
 }
 
 // The box test in packed 16-bit halves, three vector instructions: (px, py) lies in
