@@ -270,9 +270,6 @@ struct gsx_hip_render_context {
     // after count_ev
     PinnedBuffer kept_parts;
     hipEvent_t count_ev = nullptr;
-    // recorded on the forward's stream once the depth sort has stored the visible count
-    // (counters[0]); get_stats waits for it before reading the count
-    hipEvent_t stats_ev = nullptr;
     // Retained TRAIN state (gsx-cpu/render.c:263-380): the Gaussian fields as the forward read
     // them, copied into `snap`, which the backward reads (gs points into it). A borrowed state
     // also keeps the caller's arrays (`live`): the backward first compares them with `snap`
@@ -300,6 +297,7 @@ struct gsx_hip_render_context {
     gsx_hip_gaussians gs{};
     int64_t instance_count = 0;
     int64_t gaussian_count = 0;
+    int64_t visible_count = 0;  // Gaussians past the projection culls in the last forward
     int32_t tile_count_total = 0;
     int32_t sort_passes = 0;
     int32_t depth_sort_passes = 0;
@@ -573,7 +571,6 @@ gsx_hip_status gsx_hip_render_context_create(gsx_hip_render_context** out_contex
     gsx_hip_render_context* ctx = new (std::nothrow) gsx_hip_render_context();
     if (ctx == nullptr) return fail(GSX_HIP_ERROR_OUT_OF_MEMORY, "render context allocation failed");
     hipError_t e = hipEventCreateWithFlags(&ctx->count_ev, hipEventDisableTiming);
-    if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->stats_ev, hipEventDisableTiming);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->state_ev, hipEventDisableTiming);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->fork_ev, hipEventDisableTiming);
     if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->check_stream, hipStreamNonBlocking);
@@ -600,7 +597,6 @@ gsx_hip_status gsx_hip_render_context_destroy(gsx_hip_render_context* ctx) {
     ctx->kept_parts.release();
     ctx->changed.release();
     if (ctx->count_ev != nullptr) (void)hipEventDestroy(ctx->count_ev);
-    if (ctx->stats_ev != nullptr) (void)hipEventDestroy(ctx->stats_ev);
     if (ctx->state_ev != nullptr) (void)hipEventDestroy(ctx->state_ev);
     if (ctx->fork_ev != nullptr) (void)hipEventDestroy(ctx->fork_ev);
     if (ctx->check_stream != nullptr) (void)hipStreamDestroy(ctx->check_stream);
@@ -710,6 +706,7 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     ctx->cam = cam;
     ctx->gs = *gaussians;  // replaced by the snapshot below for a TRAIN forward
     ctx->gaussian_count = n;
+    ctx->visible_count = 0;
     ctx->tile_count_total = tiles;
 
     const size_t n1 = (size_t)(n > 0 ? n : 1);
@@ -808,7 +805,6 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
                                                counters, index_bits, depth_end_bit, ctx->depth_sort_temp.ptr,
                                                &depth_in_alt, stream));
         if (depth_in_alt) sorted_depth = ctx->depth_keys_alt.as<uint64_t>();
-        GSX_HIP_TRY(hipEventRecord(ctx->stats_ev, stream), "hipEventRecord(stats)");
         hipLaunchKernelGGL(rank_gather_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, n, counters,
                            sorted_depth, (uint64_t)((1ull << index_bits) - 1ull), big_flag, count_shift,
                            (uint32_t)((1ull << count_bits) - 1ull), ctx->tile_count.as<uint32_t>(),
@@ -821,14 +817,16 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
     }
     GSX_TRY(record(ctx, 2, stream));
     GSX_HIP_TRY(hipEventSynchronize(ctx->count_ev), "instance count sync");
-    unsigned long long total = 0, big_total = 0;
+    unsigned long long total = 0, big_total = 0, visible_total = 0;
     if (n > 0) {
         const unsigned long long* pre = static_cast<const unsigned long long*>(ctx->kept_parts.host);
         for (unsigned b = 0; b < pre_blocks; ++b) {
             total += pre[b] & ((1ull << kKeptPartBigShift) - 1ull);
-            big_total += pre[b] >> kKeptPartBigShift;
+            big_total += (pre[b] >> kKeptPartBigShift) & ((1ull << (kKeptPartVisibleShift - kKeptPartBigShift)) - 1ull);
+            visible_total += pre[b] >> kKeptPartVisibleShift;
         }
     }
+    ctx->visible_count = (int64_t)visible_total;
     if (total > (unsigned long long)UINT32_MAX) {
         // positions, offsets and the sort run in 32 bits; nothing has been emitted yet
         return fail(GSX_HIP_ERROR_OUT_OF_RANGE, "more than 2^32 - 1 (tile, Gaussian) instances");
@@ -1057,17 +1055,8 @@ gsx_hip_status gsx_hip_render_backward(gsx_hip_render_context* ctx, const float*
 gsx_hip_status gsx_hip_render_context_get_stats(const gsx_hip_render_context* ctx, gsx_hip_render_stats* out) {
     if (ctx == nullptr || out == nullptr) return fail(GSX_HIP_ERROR_INVALID_ARGUMENT, "context/out must be non-null");
     out->gaussian_count = ctx->gaussian_count;
-    out->visible_count = 0;
-    if (ctx->gaussian_count > 0 && ctx->counters_ready) {
-        // counters[0]: the depth sort's count of kept keys. The forward ran on the caller's
-        // stream, which may not be ordered with the null stream: wait for the event recorded
-        // after the sort, then read
-        uint32_t visible = 0;
-        GSX_HIP_TRY(hipEventSynchronize(ctx->stats_ev), "visible count sync");
-        GSX_HIP_TRY(hipMemcpy(&visible, ctx->counters.as<uint32_t>(), sizeof(visible), hipMemcpyDeviceToHost),
-                    "read visible count");
-        out->visible_count = visible;
-    }
+    // summed on the host from preprocess's partials when the forward read back its instance count
+    out->visible_count = ctx->visible_count;
     out->instance_count = ctx->instance_count;
     out->tile_count = ctx->tile_count_total;
     out->sort_passes = ctx->sort_passes;

@@ -43,8 +43,10 @@ constexpr int kWavesPerBlock = 4;
 // the near, large boxes are neighbours, and a wave holding many full-image boxes would serialise
 // their instances. Counting walks every box in the waves (rows are few).
 constexpr uint32_t kBigTiles = 1024;
-// preprocess's per-workgroup partials: kept tiles in bits 0..47, big boxes from bit 48
-constexpr int kKeptPartBigShift = 48;
+// preprocess's per-workgroup partials: kept tiles in bits 0..39 (a workgroup keeps fewer than
+// 2^34), big boxes in bits 40..51 and visible Gaussians from bit 52 (at most 256 each)
+constexpr int kKeptPartBigShift = 40;
+constexpr int kKeptPartVisibleShift = 52;
 
 // Sort keys. Gaussians are first sorted by depth: key = (bits(depth) - bits(near)) << index_bits
 // | index (visible depths lie in [near, far], where positive floats order like their bit
@@ -322,24 +324,26 @@ __global__ __launch_bounds__(256) void preprocess_kernel(
         }
         depth_keys[g] = key;
     }
-    // the workgroup's kept tiles and big boxes to kept_part[block], host memory that the host
-    // sums for the instance count and the big-box launch (a wave's kept sum is below 64 * 2^24
-    // tiles, a workgroup's below 2^32 + 2^32, under the big count in bits 48..63)
+    // the workgroup's kept tiles, big boxes and visible Gaussians to kept_part[block], host
+    // memory that the host sums for the instance count, the big-box launch and the visible count
+    // (a wave's kept sum is below 64 * 2^24 tiles, a workgroup's below 2^34)
     const uint32_t wave_kept = wave_reduce_sum_u32(kept);
     const uint32_t wave_big = (uint32_t)__popcll(wave_ballot(big));
+    const uint32_t wave_visible = (uint32_t)__popcll(wave_ballot(visible && g < n));
     if (__lane_id() == 0) {
         s_kept[threadIdx.x / kWave] = wave_kept;
-        s_big[threadIdx.x / kWave] = wave_big;
+        s_big[threadIdx.x / kWave] = wave_big | (wave_visible << 16);
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        unsigned long long sum = 0, bigs = 0;
+        unsigned long long sum = 0, bigs = 0, vis = 0;
 #pragma unroll
         for (int w = 0; w < kWavesPerBlock; ++w) {
             sum += s_kept[w];
-            bigs += s_big[w];
+            bigs += s_big[w] & 0xffffu;
+            vis += s_big[w] >> 16;
         }
-        kept_part[blockIdx.x] = sum | (bigs << kKeptPartBigShift);
+        kept_part[blockIdx.x] = sum | (bigs << kKeptPartBigShift) | (vis << kKeptPartVisibleShift);
     }
 }
 

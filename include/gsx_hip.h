@@ -144,8 +144,9 @@ typedef struct gsx_hip_render_context gsx_hip_render_context;
 
 typedef struct gsx_hip_render_stats {
     int64_t gaussian_count;
-    int64_t visible_count;   /* Gaussians that pass the projection culls (depth-sorted); read
-                                from the device: get_stats waits for the context's last forward */
+    int64_t visible_count;   /* Gaussians that pass the projection culls (depth-sorted) in the
+                                context's last forward, summed on the host when the forward read
+                                back its instance count: get_stats reads no device memory */
     int64_t instance_count;  /* (tile, Gaussian) pairs sorted */
     int32_t tile_count;
     int32_t sort_passes;       /* radix passes over the instance tiles */
