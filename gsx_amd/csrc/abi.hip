@@ -572,7 +572,9 @@ gsx_hip_status gsx_hip_render_context_create(gsx_hip_render_context** out_contex
     if (ctx == nullptr) return fail(GSX_HIP_ERROR_OUT_OF_MEMORY, "render context allocation failed");
     hipError_t e = hipEventCreateWithFlags(&ctx->count_ev, hipEventDisableTiming);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->state_ev, hipEventDisableTiming);
-    if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->fork_ev, hipEventDisableTiming);
+    // fork_ev only orders the comparison's stream after the caller's (device-side): no
+    // system-scope fence (its cache flush would idle the GPU before every borrowed backward)
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->fork_ev, hipEventDisableTiming | hipEventDisableSystemFence);
     if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->check_stream, hipStreamNonBlocking);
     if (e != hipSuccess) {
         (void)gsx_hip_render_context_destroy(ctx);
