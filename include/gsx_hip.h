@@ -344,7 +344,9 @@ gsx_hip_status gsx_hip_loss_mse_f32_backward_kernel_launch(float* grad_predictio
  * launcher before. These are not drop-in replacements of gsx_cuda_loss_ssim_* (gsx-cuda/
  * internal.h:346-369): those take two buffers (ssim_buffer_a/b) and no L1 term; here one
  * workspace holds the three window moments the backward needs. The gsx loss vtable of this
- * library (gsx_amd/plugin/hip_loss.c) owns that workspace per loss context. */
+ * library (gsx_amd/plugin/hip_loss.c) owns that workspace per loss context. Limits: at most 65535
+ * planes (outer_count * channels) and height * width <= UINT32_MAX, else
+ * GSX_HIP_ERROR_OUT_OF_RANGE. */
 gsx_hip_status gsx_hip_loss_ssim_chw_f32_forward_kernel_launch(float* loss_map, const float* prediction,
                                                                const float* target, int64_t outer_count,
                                                                int32_t channels, int32_t height, int32_t width,

@@ -106,6 +106,38 @@ def test_ssim_identical_images_zero_interior():
     assert float(m.abs().max()) <= 1e-6
 
 
+def test_ssim_vector_and_scalar_halo_agree():
+    """The SSIM kernels stage their halos with 16-byte loads when the width is a multiple of 4
+    and the arrays are 16-byte aligned, and one float at a time otherwise. The same images in
+    storage shifted by one float take the scalar path; map, dm workspace and gradient must be
+    bit-identical to the aligned run's (the two stagings differ only outside the image, where
+    no kept output looks)."""
+    from gsx_amd import _lib
+    from gsx_amd.backend import ptr
+    lib = _lib.load()
+    p, t = _images(7, (3, 64, 80))
+    n = p.size
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    outs = []
+    for off in (0, 1):
+        buf = torch.zeros(8 * n + 8, device="cuda")
+        pt, tt, m, g = (buf[off + k * n: off + (k + 1) * n].view(p.shape) for k in range(4))
+        ws = buf[off + 4 * n: off + 7 * n]
+        pt.copy_(torch.from_numpy(p))
+        tt.copy_(torch.from_numpy(t))
+        m.fill_(0.5)
+        g.fill_(-0.25)
+        assert (ptr(pt).value % 16 == 0) == (off == 0)
+        _lib.check(lib.gsx_hip_loss_ssim_chw_f32_forward_kernel_launch(ptr(m), ptr(pt), ptr(tt), 1, 3, 64, 80, 0.2,
+                                                                       ptr(ws), 0.8, 1, s))
+        _lib.check(lib.gsx_hip_loss_ssim_chw_f32_backward_kernel_launch(ptr(g), ptr(pt), ptr(tt), 1, 3, 64, 80,
+                                                                        1e-3, ptr(ws), 2e-3, 1, s))
+        torch.cuda.synchronize()
+        outs.append((m.clone(), ws.clone(), g.clone()))
+    for a, b in zip(outs[0], outs[1]):
+        assert torch.equal(a, b)
+
+
 def test_fused_l1_ssim_matches_sequential():
     from gsx_amd import _lib
     from gsx_amd.backend import ptr
