@@ -183,65 +183,83 @@ __device__ inline void ssim_row_window(const float* row, int cx, float (&w)[10 +
     for (int k = 0; k < 10 + kHCols; ++k) w[k] = r[3 + k];
 }
 
-// Forward: p and t of the halo in LDS, less a per-tile shift; a horizontal 11-tap pass where
-// each work item forms the five moments (p, t, p^2, t^2, p t) of four adjacent output columns
-// from 14 staged columns per plane; then a vertical pass where each thread produces two
-// adjacent output rows from 12 loads per moment plane. Writes the loss map (optionally after a
-// fused L1 term) and the three dm maps [3][planes][H][W] that the backward convolves.
-template <bool kVec>
+// Forward: p and t of the halo in LDS; a horizontal 11-tap pass where each thread forms the
+// five moments (p, t, p^2, t^2, p t) of four adjacent output columns from 14 loads per plane;
+// then a vertical pass where each thread produces two adjacent output rows from 12 loads per
+// moment plane. Writes the loss map (optionally after a fused L1 term) and the three dm maps
+// [3][planes][H][W] that the backward convolves.
+// The halo is staged one float per load and the shift applied per work item. The backward's
+// 16-byte staging, used here, cut this kernel's instructions by a quarter and ran it at 52.7 us
+// instead of 62 with a cached target, but a training target comes from HBM (one of many images),
+// and with its loads' latency exposed it ran at 65.6 us against this version's 60.0 (metric
+// training step, one box): here the larger arithmetic share covers that latency.
 __global__ __launch_bounds__(kSsimTW * kSsimFwdTH / 2) void ssim_forward_kernel(float* __restrict__ map, const float* __restrict__ pred,
                                                            const float* __restrict__ target, int32_t height,
                                                            int32_t width, int64_t planes, float scale, float l1_scale,
                                                            int fuse_l1, float* __restrict__ dm) {
-    GSX_SSIM_TILE(kSsimFwdTH)
-    __shared__ __align__(16) float s_in[2 * kSsimHH * kSsimInW];
-    __shared__ __align__(16) float s_h[5][kSsimHPlane];
+    constexpr int kSsimTH = kSsimFwdTH;
+    constexpr int kSsimThreads = kSsimTW * kSsimTH / 2;
+    constexpr int kSsimHH = kSsimTH + 10;
+    constexpr int kSsimHW = kSsimTW + 10;  // halo columns
+    constexpr int kHaloItems = kSsimHH * kSsimHW;
+    constexpr int kHaloRounds = (kHaloItems + kSsimThreads - 1) / kSsimThreads;
+    __shared__ float s_in[2][kSsimHH][kSsimHW + 1];
+    __shared__ float s_h[5][kSsimHH][kSsimTW + 1];
     const int tiles_x = (width + kSsimTW - 1) / kSsimTW;
     const int tiles = tiles_x * ((height + kSsimTH - 1) / kSsimTH);
     const int tile = ssim_tile_of((int)blockIdx.x, tiles);
     if (tile >= tiles) return;
     const int ox = (tile % tiles_x) * kSsimTW;
     const int oy = (tile / tiles_x) * kSsimTH;
-    // this plane's arrays (uniform bases; in-plane offsets are 32-bit)
-    const int64_t pbase = (int64_t)blockIdx.y * height * width;
-    const int64_t total = planes * (int64_t)height * width;
-    const float* const pp = pred + pbase;
-    const float* const tp = target + pbase;
+    const int64_t plane = blockIdx.y;
+    const int64_t pbase = plane * (int64_t)height * width;
     const int lx = threadIdx.x % kSsimTW;
     const int ly0 = 2 * (threadIdx.x / kSsimTW);
-    // The moments are formed from inputs shifted by one value per image and tile (the tile's
-    // centre pixel, clamped into the image: a partial last tile's centre can lie outside it):
-    // sigma^2 = E[x^2] - mu^2 loses the bits of E[x^2] to cancellation when mu is large and the
-    // window nearly flat, and variances and covariances do not change under a shift. The means
-    // are the shifted means plus the shift.
-    const uint32_t jshift =
-        (uint32_t)min(oy + kSsimTH / 2, height - 1) * (uint32_t)width + (uint32_t)min(ox + kSsimTW / 2, width - 1);
-    const float shift[2] = {pp[jshift], tp[jshift]};
-    // this thread's output pixels: the loss map values it adds to and, for the fused L1 term, the
-    // unshifted prediction and target (clamped positions outside the image are never stored;
-    // without a map the prediction stands in)
-    float map_in[2], p_own[2] = {0.0f, 0.0f}, t_own[2] = {0.0f, 0.0f};
+    // the loss map values this thread adds to, loaded up front with the halo (clamped positions
+    // outside the image are never stored; without a map the prediction stands in)
+    float map_in[2];
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
-        const uint32_t j = (uint32_t)min(oy + ly0 + r, height - 1) * (uint32_t)width + (uint32_t)min(ox + lx, width - 1);
-        map_in[r] = (map != nullptr ? map + pbase : pp)[j];
-        if (fuse_l1) {
-            p_own[r] = pp[j];
-            t_own[r] = tp[j];
+        const int64_t j = pbase + (int64_t)min(oy + ly0 + r, height - 1) * width + min(ox + lx, width - 1);
+        map_in[r] = (map != nullptr ? map : pred)[j];
+    }
+    {
+        // the whole halo is loaded before the first store waits (no load under a branch: a
+        // position outside the image reads a clamped one and keeps 0; threads past the halo
+        // repeat its last item, same value to the same slot)
+        float pv[kHaloRounds], tv[kHaloRounds];
+#pragma unroll
+        for (int u = 0; u < kHaloRounds; ++u) {
+            const int i = min((int)threadIdx.x + kSsimThreads * u, kHaloItems - 1);
+            const int hy = i / kSsimHW, hx = i % kSsimHW;
+            const int y = oy + hy - 5, x = ox + hx - 5;
+            const bool in = y >= 0 && y < height && x >= 0 && x < width;
+            const int64_t j = pbase + (int64_t)min(max(y, 0), height - 1) * width + min(max(x, 0), width - 1);
+            const float p = pred[j], t = target[j];
+            pv[u] = in ? p : 0.0f;
+            tv[u] = in ? t : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < kHaloRounds; ++u) {
+            const int i = min((int)threadIdx.x + kSsimThreads * u, kHaloItems - 1);
+            const int hy = i / kSsimHW, hx = i % kSsimHW;
+            s_in[0][hy][hx] = pv[u];
+            s_in[1][hy][hx] = tv[u];
         }
     }
-    // Positions outside the image hold the nearest pixel's value instead of the zero padding:
-    // an output whose window reaches outside the image is 5 or fewer pixels from the edge, and
-    // the map and the dm maps store 0 there, whatever the window holds.
-    const float* const src[2] = {pp, tp};
-    ssim_stage_halo<kVec, 2, kSsimHH, kSsimThreads>(s_in, src, ox, oy, height, width, shift);
     __syncthreads();
-    for (int i = threadIdx.x; i < (kSsimHH + 7) / 8 * 64; i += kSsimThreads) {
-        const int hy = ssim_item_row(i), cx = kHCols * (i & 7);
-        if (hy >= kSsimHH) continue;
-        float wp[10 + kHCols], wt[10 + kHCols];
-        ssim_row_window(s_in + hy * kSsimInW, cx, wp);
-        ssim_row_window(s_in + (kSsimHH + hy) * kSsimInW, cx, wt);
+    // The moments are formed from inputs shifted by one value per image and tile (the tile's
+    // centre pixel): sigma^2 = E[x^2] - mu^2 loses the bits of E[x^2] to cancellation when mu is
+    // large and the window nearly flat, and variances and covariances do not change under a
+    // shift. The windows of the outputs that are kept (5 or more pixels from the edge) hold no
+    // padding, so shifting the padding's zeros changes only outputs the map and dm overwrite
+    // with 0. The means are the shifted means plus the shift. The shift pixel is the tile's
+    // centre clamped into the image (a partial last tile's centre can lie in the padding).
+    const int shift_hy = min(oy + kSsimTH / 2, height - 1) - oy + 5;
+    const int shift_hx = min(ox + kSsimTW / 2, width - 1) - ox + 5;
+    const float shift_p = s_in[0][shift_hy][shift_hx], shift_t = s_in[1][shift_hy][shift_hx];
+    for (int i = threadIdx.x; i < kSsimHH * (kSsimTW / kHCols); i += kSsimThreads) {
+        const int hy = i / (kSsimTW / kHCols), cx = kHCols * (i % (kSsimTW / kHCols));
         float a[kHCols][5];
 #pragma unroll
         for (int j = 0; j < kHCols; ++j)
@@ -249,7 +267,7 @@ __global__ __launch_bounds__(kSsimTW * kSsimFwdTH / 2) void ssim_forward_kernel(
             for (int c = 0; c < 5; ++c) a[j][c] = 0.0f;
 #pragma unroll
         for (int k = 0; k < 10 + kHCols; ++k) {
-            const float pv = wp[k], tv = wt[k];
+            const float pv = s_in[0][hy][cx + k] - shift_p, tv = s_in[1][hy][cx + k] - shift_t;
             const float m[5] = {pv, tv, pv * pv, tv * tv, pv * tv};
 #pragma unroll
             for (int j = 0; j < kHCols; ++j) {
@@ -261,8 +279,9 @@ __global__ __launch_bounds__(kSsimTW * kSsimFwdTH / 2) void ssim_forward_kernel(
             }
         }
 #pragma unroll
-        for (int c = 0; c < 5; ++c)
-            *reinterpret_cast<float4*>(&s_h[c][hy * kSsimTW + cx]) = make_float4(a[0][c], a[1][c], a[2][c], a[3][c]);
+        for (int j = 0; j < kHCols; ++j)
+#pragma unroll
+            for (int c = 0; c < 5; ++c) s_h[c][hy][cx + j] = a[j][c];
     }
     __syncthreads();
     float mom[2][5] = {{0.0f, 0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f, 0.0f}};
@@ -270,53 +289,52 @@ __global__ __launch_bounds__(kSsimTW * kSsimFwdTH / 2) void ssim_forward_kernel(
     for (int k = 0; k < 12; ++k) {
 #pragma unroll
         for (int c = 0; c < 5; ++c) {
-            const float v = s_h[c][(ly0 + k) * kSsimTW + lx];
+            const float v = s_h[c][ly0 + k][lx];
             if (k < 11) mom[0][c] = __builtin_fmaf(kSsimW[k], v, mom[0][c]);
             if (k > 0) mom[1][c] = __builtin_fmaf(kSsimW[k - 1], v, mom[1][c]);
         }
     }
-    const int x = ox + lx;
+    const int64_t total = planes * (int64_t)height * width;
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
-        const int y = oy + ly0 + r;
+        const int ly = ly0 + r;
+        const int x = ox + lx, y = oy + ly;
         if (x >= width || y >= height) continue;
         // shifted moments: d1 = mu1 - shift_p, d2 = mu2 - shift_t, e.. = E[shifted products]
         const float d1 = mom[r][0], d2 = mom[r][1], ex2 = mom[r][2], ey2 = mom[r][3], exy = mom[r][4];
-        const float mu1 = d1 + shift[0], mu2 = d2 + shift[1];
+        const float mu1 = d1 + shift_p, mu2 = d2 + shift_t;
         const float c1 = 0.01f * 0.01f, c2 = 0.03f * 0.03f;
-        // fused multiply-adds throughout (each rounds once, never less accurately than the
-        // separate product and sum)
-        const float s1 = __builtin_fmaf(-d1, d1, ex2), s2 = __builtin_fmaf(-d2, d2, ey2);
-        const float s12 = __builtin_fmaf(-d1, d2, exy);
-        const float a = __builtin_fmaf(mu1, mu1, __builtin_fmaf(mu2, mu2, c1));
+        const float m1s = mu1 * mu1, m2s = mu2 * mu2;
+        const float s1 = ex2 - d1 * d1, s2 = ey2 - d2 * d2, s12 = exy - d1 * d2;
+        const float a = m1s + m2s + c1;
         const float b = s1 + s2 + c2;
-        const float ct = __builtin_fmaf(2.0f * mu1, mu2, c1);
-        const float dt = __builtin_fmaf(2.0f, s12, c2);
+        const float ct = 2.0f * mu1 * mu2 + c1;
+        const float dt = 2.0f * s12 + c2;
         const float ab = a * b;
         // one hardware reciprocal serves all quotients (the SSIM bar is a tolerance): 1/ab,
         // 1/(a ab) = r/a and 1/(ab b) = r/b with r = 1/ab
         const float r_ab = __builtin_amdgcn_rcpf(ab);
-        const float ctdt = ct * dt;
-        const float ssim = ab == 0.0f ? 1.0f : ctdt * r_ab;
+        const float ssim = ab == 0.0f ? 1.0f : (ct * dt) * r_ab;
         const bool boundary = y < 5 || y >= height - 5 || x < 5 || x >= width - 5;
-        const uint32_t j = (uint32_t)y * (uint32_t)width + (uint32_t)x;
+        const int64_t idx = pbase + (int64_t)y * width + x;
         if (map != nullptr) {
             float m = map_in[r];
             // exactly the L1 kernel's operations (loss.c:354-371)
-            if (fuse_l1) m += l1_scale * fabsf(p_own[r] - t_own[r]);
-            map[pbase + j] = boundary ? 0.0f : m + (1.0f - ssim) * scale;
+            if (fuse_l1) m += l1_scale * fabsf(s_in[0][ly + 5][lx + 5] - s_in[1][ly + 5][lx + 5]);
+            map[idx] = boundary ? 0.0f : m + (1.0f - ssim) * scale;
         }
         if (dm != nullptr) {
             float g_mu = 0.0f, g_s1 = 0.0f, g_s12 = 0.0f;
             if (!(boundary || a == 0.0f || b == 0.0f)) {
                 const float r_aab = r_ab * __builtin_amdgcn_rcpf(a), r_abb = r_ab * __builtin_amdgcn_rcpf(b);
+                const float ctdt = ct * dt;
                 g_mu = 2.0f * mu2 * (dt - ct) * r_ab + 2.0f * mu1 * ctdt * (r_abb - r_aab);
                 g_s1 = -ctdt * r_abb;
                 g_s12 = 2.0f * ct * r_ab;
             }
-            dm[pbase + j] = g_mu;
-            dm[total + pbase + j] = g_s1;
-            dm[2 * total + pbase + j] = g_s12;
+            dm[idx] = g_mu;
+            dm[total + idx] = g_s1;
+            dm[2 * total + idx] = g_s12;
         }
     }
 }
@@ -470,11 +488,9 @@ gsx_hip_status gsx_hip_loss_ssim_chw_f32_forward_kernel_launch(float* loss_map, 
     if (planes <= 0 || height <= 0 || width <= 0) return GSX_HIP_ERROR_INVALID_ARGUMENT;
     if (planes > 65535 || (int64_t)height * width > (int64_t)UINT32_MAX) return GSX_HIP_ERROR_OUT_OF_RANGE;
     const int tiles = ((width + kSsimTW - 1) / kSsimTW) * ((height + kSsimFwdTH - 1) / kSsimFwdTH);
-    const bool vec = ssim_vector_halo(width, prediction, target);
-    hipLaunchKernelGGL(vec ? ssim_forward_kernel<true> : ssim_forward_kernel<false>,
-                       dim3((unsigned)(8 * ((tiles + 7) / 8)), (unsigned)planes), dim3(kSsimTW * kSsimFwdTH / 2), 0,
-                       stream, loss_map, prediction, target, height, width, planes, scale, l1_scale, fuse_l1,
-                       ssim_workspace);
+    hipLaunchKernelGGL(ssim_forward_kernel, dim3((unsigned)(8 * ((tiles + 7) / 8)), (unsigned)planes),
+                       dim3(kSsimTW * kSsimFwdTH / 2), 0, stream, loss_map, prediction, target, height, width, planes,
+                       scale, l1_scale, fuse_l1, ssim_workspace);
     return (gsx_hip_status)hipGetLastError();
 }
 
