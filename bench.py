@@ -166,6 +166,12 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_metric.txt")
 SQ_FILE = os.path.join(ROOT, "profiles", "sq_counters_metric.md")
 
 
+def _kernel_base(name):
+    """A profiled kernel name without its template arguments (ssim_backward_kernel<true> ->
+    ssim_backward_kernel): the byte model and the stage map name kernels, not instantiations."""
+    return name.split("<", 1)[0]
+
+
 def measured_traffic(kernel):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
     summary (already scaled by the copy-kernel calibration there), or None."""
@@ -174,7 +180,7 @@ def measured_traffic(kernel):
     with open(TRAFFIC_FILE) as f:
         for line in f:
             parts = line.split()
-            if len(parts) >= 4 and parts[0] == "traffic" and parts[1] == kernel:
+            if len(parts) >= 4 and parts[0] == "traffic" and _kernel_base(parts[1]) == kernel:
                 return int(float(parts[-1]))
     return None
 
@@ -188,7 +194,7 @@ def profiled_pipe_counters(kernel):
     with open(SQ_FILE) as f:
         for line in f:
             cells = [c.strip() for c in line.strip().strip("|").split("|")]
-            if len(cells) >= 3 and cells[0] == kernel and cells[1].startswith("pipe"):
+            if len(cells) >= 3 and _kernel_base(cells[0]) == kernel and cells[1].startswith("pipe"):
                 try:
                     return {"valu_busy_pct": float(cells[2]), "lds_bank_conflict_pct": float(cells[3]),
                             "source": os.path.relpath(SQ_FILE, ROOT)}
@@ -205,7 +211,7 @@ def profiled_valu_instructions(kernel):
     with open(SQ_FILE) as f:
         for line in f:
             cells = [c.strip() for c in line.strip().strip("|").split("|")]
-            if len(cells) >= 8 and cells[0] == kernel and cells[1] != "pipe":
+            if len(cells) >= 8 and _kernel_base(cells[0]) == kernel and cells[1] != "pipe":
                 try:
                     return int(float(cells[6]))
                 except ValueError:
