@@ -227,6 +227,19 @@ __device__ inline void eval_sh(int64_t g, int deg, const float d[3], const float
     out[2] = fmaxf(r2 + 0.5f, 0.0f);
 }
 
+// mean_cam = W mean + t (render.c:611-620), the one sequence of operations that every kernel
+// uses for it (so a pre-test and the full projection see the same camera-space mean).
+__device__ inline void camera_space_mean(float mx, float my, float mz, const CameraParams& cam, float& xc, float& yc,
+                                         float& zc) {
+    const Mat3 w = camera_rotation(cam);
+    xc = w.m[0][0] * mx + w.m[0][1] * my + w.m[0][2] * mz;
+    yc = w.m[1][0] * mx + w.m[1][1] * my + w.m[1][2] * mz;
+    zc = w.m[2][0] * mx + w.m[2][1] * my + w.m[2][2] * mz;
+    xc = xc + cam.t[0];
+    yc = yc + cam.t[1];
+    zc = zc + cam.t[2];
+}
+
 // One Gaussian through the CPU's visibility culls, EWA projection, pixel box and colour
 // (render.c:850-1016 per entry; projection :611-668, box :670-694).
 __device__ inline Projected preprocess_one(int64_t g, const float* __restrict__ mean3d,
@@ -244,13 +257,8 @@ __device__ inline Projected preprocess_one(int64_t g, const float* __restrict__ 
     const float ls[3] = {logscale[g * 3 + 0], logscale[g * 3 + 1], logscale[g * 3 + 2]};
     const Mat3 cov3d = cov3d_from(q, ls, exp_table);
     const Mat3 w = camera_rotation(cam);
-    // mean_cam = W mean + t
-    float xc = w.m[0][0] * mx + w.m[0][1] * my + w.m[0][2] * mz;
-    float yc = w.m[1][0] * mx + w.m[1][1] * my + w.m[1][2] * mz;
-    float zc = w.m[2][0] * mx + w.m[2][1] * my + w.m[2][2] * mz;
-    xc = xc + cam.t[0];
-    yc = yc + cam.t[1];
-    zc = zc + cam.t[2];
+    float xc, yc, zc;
+    camera_space_mean(mx, my, mz, cam, xc, yc, zc);
     const Mat3 cov_cam = mat3_mul_t(mat3_mul(w, cov3d), w);
     if (fabsf(zc) < kMinAbsZ) return p;
     const float inv_z = 1.0f / zc;
@@ -327,13 +335,7 @@ __device__ inline ProjectedView project_view(int64_t g, const float* __restrict_
     ProjectedView p;
     p.visible = true;
     const float mx = mean3d[g * 3 + 0], my = mean3d[g * 3 + 1], mz = mean3d[g * 3 + 2];
-    const Mat3 w = camera_rotation(cam);
-    float xc = w.m[0][0] * mx + w.m[0][1] * my + w.m[0][2] * mz;
-    float yc = w.m[1][0] * mx + w.m[1][1] * my + w.m[1][2] * mz;
-    float zc = w.m[2][0] * mx + w.m[2][1] * my + w.m[2][2] * mz;
-    p.xc = xc + cam.t[0];
-    p.yc = yc + cam.t[1];
-    p.zc = zc + cam.t[2];
+    camera_space_mean(mx, my, mz, cam, p.xc, p.yc, p.zc);
     const float dx = mx - cam.centre[0], dy = my - cam.centre[1], dz = mz - cam.centre[2];
     const float len = sqrtf(dx * dx + dy * dy + dz * dz);
     if (len <= 0.0f) {

@@ -96,6 +96,72 @@ def test_nonfinite_colour_stays_non_finite_and_the_rest_bit_exact(oracle):
     print(f"[nonfinite] CPU {int((~np.isfinite(ref)).sum())} pixels, HIP {int((~fin).sum())}", flush=True)
 
 
+def _border_scene(seed, n, fx, width, height):
+    """Gaussians whose centres lie around and beyond the screen edges of the default camera
+    (at (0, 0, 4) facing the origin), with scales up to radii of about 130 pixels: many boxes
+    reach into the screen from outside, and many just miss it."""
+    from gsx_amd import scenes
+    rng = np.random.default_rng(seed)
+    zc = rng.uniform(2.0, 8.0, n)
+    sx = rng.uniform(-140.0, width + 140.0, n)
+    sy = rng.uniform(-140.0, height + 140.0, n)
+    xc = (sx - width / 2) * zc / fx
+    yc = (sy - height / 2) * zc / fx
+    mean = np.stack([xc, -yc, 4.0 - zc], 1).astype(np.float32)  # camera: y and z flipped
+    rot = rng.normal(size=(n, 4)).astype(np.float32)
+    ls = rng.uniform(-3.5, 0.3, (n, 3)).astype(np.float32)
+    op = rng.uniform(-1.0, 3.0, (n, 1)).astype(np.float32)
+    sh0 = rng.normal(0.0, 0.5, (n, 3)).astype(np.float32)
+    return scenes.Scene(mean, rot, ls, op, sh0)
+
+
+def _visible_set_parity(oracle, sc, camera):
+    from gsx_amd import scenes
+    r, cam, g = _setup(scenes.Workload("border", sc, camera))
+    counter = torch.zeros(sc.count, dtype=torch.float32, device="cuda")
+    img = r.render(cam, g, train=True, visible_counter=counter)  # only a TRAIN forward counts
+    torch.cuda.synchronize()
+    ref_counter = np.zeros(sc.count, np.float32)
+    ref, _ = oracle.render(sc, camera, visible_counter=ref_counter)
+    got = counter.cpu().numpy()
+    print(f"[visible] CPU {int(ref_counter.sum())}, HIP {int(got.sum())} of {sc.count}", flush=True)
+    assert np.array_equal(got, ref_counter)
+    return r, img, ref
+
+
+def test_visibility_at_the_screen_edges(oracle):
+    """Visibility at the screen edges: the visible set, the image and the instance count equal
+    the CPU's on a scene of Gaussians around and beyond the edges (centres up to 140 pixels
+    outside the screen, radii up to ~130, 1322 of the 1784 visible ones centred off-screen)."""
+    from gsx_amd import scenes
+    cam_block = scenes.camera(160, 120, 125.0)
+    sc = _border_scene(21, 4000, 125.0, 160, 120)
+    print("[case] border scene 4000 Gaussians 160x120", flush=True)
+    r, img, ref = _visible_set_parity(oracle, sc, cam_block)
+    assert np.array_equal(img.cpu().numpy(), ref)
+    keys_ref, _ = oracle.tile_keys(sc, cam_block, 16)
+    assert r.stats().instance_count == len(keys_ref)
+
+
+def test_visibility_of_non_finite_shapes(oracle):
+    """A non-finite rotation or scale gives the CPU's projection a NaN radius and a box that
+    covers the screen (visible) even where the centre lies far outside the screen: the visible
+    set equals the CPU's."""
+    from gsx_amd import scenes
+    cam_block = scenes.camera(160, 120, 125.0)
+    sc = _border_scene(22, 600, 125.0, 160, 120)
+    rng = np.random.default_rng(23)
+    bad = rng.choice(sc.count, 12, replace=False)
+    rot, ls = sc.rotation.copy(), sc.logscale.copy()
+    rot[bad[:4], 1] = np.nan
+    ls[bad[4:8], 2] = np.nan
+    ls[bad[8:10], 0] = np.inf
+    rot[bad[10:], 3] = np.inf
+    sc = scenes.Scene(sc.mean3d, rot, ls, sc.opacity, sc.sh0)
+    print(f"[case] non-finite shapes {bad.tolist()}", flush=True)
+    _visible_set_parity(oracle, sc, cam_block)
+
+
 @pytest.mark.parametrize("name", ["c0_small", "c3_small", "c4_small", "c3_1080", "c3_4k", "ties"])
 def test_sorted_keys_and_ranges_bit_exact(oracle, name):
     import ctypes
