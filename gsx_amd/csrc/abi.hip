@@ -852,9 +852,10 @@ gsx_hip_status gsx_hip_render_forward(gsx_hip_render_context* ctx, const gsx_hip
                                   "checkpoints", ctx->call_stream));
     }
     if (n > 0) {
-        // one wave per big box
+        // one wave per big box; rank workgroups up to one rank past the visible ones
         const uint32_t big_blocks = (uint32_t)((big_total + kWavesPerBlock - 1) / kWavesPerBlock);
-        hipLaunchKernelGGL(emit_kernel, dim3(big_blocks + pre_blocks), dim3(256), 0, stream, n, ctx->rec.as<float4>(),
+        const unsigned emit_blocks = std::min(pre_blocks, (unsigned)(visible_total / 256u + 1u));
+        hipLaunchKernelGGL(emit_kernel, dim3(big_blocks + emit_blocks), dim3(256), 0, stream, n, ctx->rec.as<float4>(),
                            ctx->rank_g.as<uint32_t>(), ctx->rank_count.as<uint32_t>(), ctx->scan_temp.as<uint32_t>(),
                            ctx->offsets.as<uint32_t>(), cam.tiles_x, ctx->big_list.as<uint32_t>(), big_count,
                            big_blocks, ctx->g_rank.as<uint32_t>(), ctx->inst_gauss.as<uint32_t>(), ctx->inst_tile.as<uint32_t>(),

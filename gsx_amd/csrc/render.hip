@@ -425,7 +425,7 @@ __global__ __launch_bounds__(256) void rank_gather_kernel(int64_t n, const uint3
 // blocking) scans its own 256 counts; offsets[0..n] are stored for the later kernels
 // (offsets[n] = total).
 // ---------------------------------------------------------------------------------------------
-__device__ inline void emit_block(uint32_t b, int64_t n, const float4* __restrict__ rec,
+__device__ inline void emit_block(uint32_t b, int64_t n, int64_t rank_end, const float4* __restrict__ rec,
                                   const uint32_t* __restrict__ rank_gaussian, const uint32_t* __restrict__ rank_count,
                                   const uint32_t* __restrict__ block_prefix, uint32_t* __restrict__ offsets,
                                   int32_t tiles_x, uint32_t* __restrict__ instance_gaussian,
@@ -443,7 +443,9 @@ __device__ inline void emit_block(uint32_t b, int64_t n, const float4* __restric
     uint32_t block_total;
     const uint32_t o = block_prefix[b] + block_exclusive_scan_256(cnt, s_wave, block_total);
     if (r < n) offsets[r] = o;
-    if (r == n - 1) offsets[n] = o + cnt;
+    // offsets[n] (the instance total, read by the ranges pass) from the last rank launched: the
+    // launch covers the visible ranks and at least one more, whose counts are 0
+    if (r == rank_end - 1) offsets[n] = o + cnt;
     // the long-run list in rank order: long_prefix[b] (scanned per-workgroup counts of
     // rank_gather_kernel) + the rank's place among the workgroup's long runs (s_wave is free
     // again after the scan's last barrier)
@@ -521,7 +523,10 @@ __global__ __launch_bounds__(256) void emit_kernel(int64_t n, const float4* __re
                          instance_tile, s_spans[threadIdx.x / kWave]);
         return;
     }
-    emit_block(blockIdx.x - big_blocks, n, rec, rank_gaussian, rank_count, block_prefix, offsets, tiles_x,
+    // the rank workgroups cover ranks [0, rank_end): the visible ones and at least one past them
+    // (ranks of invisible Gaussians emit nothing, and no kernel reads their offsets)
+    const int64_t rank_end = min(n, (int64_t)(gridDim.x - big_blocks) * blockDim.x);
+    emit_block(blockIdx.x - big_blocks, n, rank_end, rec, rank_gaussian, rank_count, block_prefix, offsets, tiles_x,
                instance_gaussian, instance_tile, long_prefix, long_list, s_spans, s_wave);
 }
 
