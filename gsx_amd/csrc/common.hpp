@@ -575,15 +575,28 @@ __device__ inline uint32_t digit_of(KeyT key, int shift) {
 // count, n = min(n, *n_dev); drop_sentinel: keys equal to kSentinelKey are not counted.
 // dmask keeps the digit's bits below the sort's end bit (a last pass narrower than kBits). KeyT:
 // uint64_t (the depth order and the public sorts) or uint32_t (tile indices).
-template <int kBits, int kChunk, typename KeyT = uint64_t>
+// Digit histograms of an upsweep workgroup: per wave, kUpsweepCopies<kBits> copies (one per
+// group of 64 / copies lanes), so that lanes of one wave that count the same digit in the same
+// round mostly add to different words; each copy kBins + 64 / copies words long, so that a digit's
+// copies lie on different banks. (Up to 8-bit digits; the depth sort's 512 digits keep one copy.)
+template <int kBits>
+constexpr int kUpsweepCopies = kBits <= 8 ? 8 : 1;
+template <int kBits>
+constexpr int kUpsweepCopyWords = (1 << kBits) + (kUpsweepCopies<kBits> > 1 ? 64 / kUpsweepCopies<kBits> : 0);
+template <int kBits>
+constexpr int kUpsweepHistWords = kChunkWaves * kUpsweepCopies<kBits> * kUpsweepCopyWords<kBits>;
+
+template <int kBits, int kChunk, typename KeyT>
 __device__ inline void radix_upsweep_block(uint32_t blk, const KeyT* __restrict__ keys, int64_t n,
                                            const uint32_t* __restrict__ n_dev, bool drop_sentinel, int shift,
                                            int64_t num_chunks, uint32_t* __restrict__ hist,
-                                           uint32_t (*s_hist)[1 << kBits], uint32_t dmask = (1u << kBits) - 1u) {
+                                           uint32_t* s_hist, uint32_t dmask = (1u << kBits) - 1u) {
     constexpr int kBins = 1 << kBits;
+    constexpr int kCopies = kUpsweepCopies<kBits>;
+    constexpr int kCopyWords = kUpsweepCopyWords<kBits>;
     if (n_dev != nullptr) n = min(n, (int64_t)*n_dev);
     const int wave = threadIdx.x / kWave;
-    for (int i = threadIdx.x; i < kChunkWaves * kBins; i += kSortThreads) (&s_hist[0][0])[i] = 0;
+    for (int i = threadIdx.x; i < kUpsweepHistWords<kBits>; i += kSortThreads) s_hist[i] = 0;
     __syncthreads();
     const int64_t base = (int64_t)blk * kChunk;
     if (base < n) {  // uniform; a chunk past the live count counts nothing
@@ -593,16 +606,19 @@ __device__ inline void radix_upsweep_block(uint32_t blk, const KeyT* __restrict_
         KeyT k[kRounds];
 #pragma unroll
         for (int r = 0; r < kRounds; ++r) k[r] = keys[min(base + (int64_t)r * kSortThreads + threadIdx.x, n - 1)];
+        uint32_t* my_hist = s_hist + (wave * kCopies + (int)(__lane_id() / (kWave / kCopies))) * kCopyWords;
 #pragma unroll
         for (int r = 0; r < kRounds; ++r) {
             const int64_t i = base + (int64_t)r * kSortThreads + threadIdx.x;
             if (i < n && (!drop_sentinel || (uint64_t)k[r] != kSentinelKey))
-                atomicAdd(&s_hist[wave][digit_of<kBits>(k[r], shift) & dmask], 1u);
+                atomicAdd(&my_hist[digit_of<kBits>(k[r], shift) & dmask], 1u);
         }
     }
     __syncthreads();
     for (int d = threadIdx.x; d < kBins; d += kSortThreads) {
-        const uint32_t c = s_hist[0][d] + s_hist[1][d] + s_hist[2][d] + s_hist[3][d];
+        uint32_t c = 0;
+#pragma unroll
+        for (int h = 0; h < kChunkWaves * kCopies; ++h) c += s_hist[h * kCopyWords + d];
         hist[(int64_t)d * num_chunks + blk] = c;
     }
 }

@@ -150,7 +150,7 @@ __global__ __launch_bounds__(kSortThreads) void radix_upsweep_kernel(const KeyT*
                                                                      bool drop_sentinel, int shift,
                                                                      uint32_t dmask, int64_t num_chunks,
                                                                      uint32_t* __restrict__ hist) {
-    __shared__ uint32_t s_hist[kChunkWaves][1 << kBits];
+    __shared__ uint32_t s_hist[kUpsweepHistWords<kBits>];
     const int64_t chunk = sort_chunk_of(blockIdx.x, num_chunks);
     if (chunk >= num_chunks) return;  // uniform
     radix_upsweep_block<kBits, kChunk, KeyT>((uint32_t)chunk, keys, n, n_dev, drop_sentinel, shift, num_chunks, hist,
