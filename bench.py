@@ -75,8 +75,10 @@ def algorithmic_bytes(stage, geo, train=True):
     if stage == "blend_backward":
         # ranges, per pixel the image gradient + final T + last position, the checkpoints, reached
         # entries' positions + Gaussians, each reached Gaussian's record + conic-gradient
-        # coefficients once in; a 36-byte partial per reached entry and each tile's cut out
-        return 12 * t + 20 * p + 4 * c + 8 * r + 80 * u + 36 * r
+        # coefficients once in; a 36-byte partial per reached entry and each tile's cut out; the
+        # five parameter gradient sinks zeroed (56 bytes per Gaussian at SH0), which its
+        # workgroups store beside their own work
+        return 12 * t + 20 * p + 4 * c + 8 * r + 80 * u + 36 * r + 56 * n
     if stage == "instance_reduce":
         # per depth rank its Gaussian, offset and touched flag, the tiles of the touched
         # Gaussians' instances and the reached entries' partials in (the 9-float screen gradients
@@ -84,9 +86,10 @@ def algorithmic_bytes(stage, geo, train=True):
         # writes, so they are not counted)
         return 9 * vp + 4 * geo["It"] + 36 * r
     if stage == "projection_backward":
-        # the five parameter gradients written for every Gaussian (the touched ones' inputs and
-        # screen gradients are read from cache: the counters show about 1 MB fetched)
-        return 56 * n
+        # every Gaussian's touched flag in, the five parameter gradients of the reached Gaussians
+        # out (the blend backward has zeroed the others; the reached ones' inputs and screen
+        # gradients are read from cache)
+        return n + 56 * u
     if stage == "loss_forward":
         # prediction + target in, loss map accumulated (in + out), SSIM workspace (3 floats) out
         return (4 + 4 + 8 + 12) * 3 * p

@@ -928,13 +928,31 @@ gsx_hip_status enqueue_backward(gsx_hip_render_context* ctx, const float* grad_r
     const uint32_t long_chunk = long_chunk_of(tiles);
     const unsigned pre_blocks = blocks_for(n, 256);  // the forward's rank workgroups
     GSX_TRY(record(ctx, 7, stream));
+    // the gradient sinks, zeroed by the blend backward's workgroups beside their own work (the
+    // projection backward then writes only the rows of reached Gaussians)
+    SinkZeroing sinks{};
+    if (n > 0) {
+        float* const fields[8] = {grads->mean3d, grads->rotation, grads->logscale, grads->opacity,
+                                  grads->sh0,    grads->sh1,      grads->sh2,      grads->sh3};
+        const int widths[8] = {3, 4, 3, 1, 3, 9, 15, 21};
+        const int arrays = 5 + (int)gs.sh_degree;
+        const int64_t blocks = ((tiles + 7) / 8) * 8;  // the launch below
+        const int64_t slices = blocks / arrays;        // workgroups per array (at least 1: blocks >= 8)
+        for (int f = 0; f < arrays; ++f) {
+            sinks.ptr[f] = fields[f];
+            sinks.count[f] = n * widths[f];
+            sinks.per[f] = (((sinks.count[f] + slices - 1) / slices) + 3) & ~(int64_t)3;
+            if ((reinterpret_cast<uintptr_t>(fields[f]) & 15u) == 0) sinks.vec4 |= 1u << f;
+        }
+        sinks.arrays = arrays;
+    }
     const int tiles_padded = ((tiles + 7) / 8) * 8;
     hipLaunchKernelGGL(blend_backward_kernel, dim3((unsigned)tiles_padded), dim3(256), 0, stream,
                        ctx->ranges.as<uint2>(), svals, ctx->sorted_g.as<uint32_t>(), ctx->rec.as<float4>(),
                        ctx->rec.as<float4>() + 2 * n, reinterpret_cast<const uint2*>(ctx->rec.as<float4>() + 3 * n),
                        ctx->cov_coef.as<float4>(), ctx->ckpt.as<float>(), cam, grad_rgb, ctx->final_t.as<float>(),
                        ctx->last.as<uint32_t>(), ctx->inst_grad.as<float>(), inst_grad_op,
-                       ctx->tile_cut.as<uint32_t>(), ctx->touched.as<uint8_t>());
+                       ctx->tile_cut.as<uint32_t>(), ctx->touched.as<uint8_t>(), sinks);
     GSX_HIP_TRY(hipGetLastError(), "blend_backward_kernel");
     GSX_TRY(record(ctx, 8, stream));
     if (n > 0) {

@@ -222,6 +222,37 @@ __device__ inline void walk_wave_rows(WaveSpans& w, uint32_t wave_rows, int32_t 
     wave_lds_sync();
 }
 
+// The parameter gradient sinks (mean3d, rotation, logscale, opacity, sh0..sh3: `arrays` of
+// them, count[a] floats each), zeroed by the blend backward so that the projection backward
+// writes only the rows of Gaussians some tile's backward reached. Workgroup b zeroes slice
+// b / arrays of array b % arrays; per[a] floats per slice, a multiple of 4, and vec4 bit a when
+// the array is 16-byte aligned (16-byte stores); all set by the host.
+struct SinkZeroing {
+    float* ptr[8];
+    int64_t count[8];
+    int64_t per[8];
+    int arrays;
+    uint32_t vec4;
+};
+
+// This workgroup's slice: no load and no wait, so the stores leave beside the kernel's own work.
+__device__ inline void zero_sink_slice(const SinkZeroing& z, uint32_t blk) {
+    if (z.arrays == 0) return;
+    const uint32_t a = blk % (uint32_t)z.arrays;
+    float* const p = z.ptr[a];
+    const int64_t lo = (int64_t)(blk / (uint32_t)z.arrays) * z.per[a];
+    const int64_t hi = min(z.count[a], lo + z.per[a]);
+    if (lo >= hi) return;  // uniform
+    int64_t done = lo;
+    if ((z.vec4 >> a) & 1u) {
+        const int vecs = (int)((hi - lo) >> 2);
+        float4* const q = reinterpret_cast<float4*>(p + lo);
+        for (int i = threadIdx.x; i < vecs; i += blockDim.x) q[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        done = lo + 4 * (int64_t)vecs;
+    }
+    for (int64_t i = done + threadIdx.x; i < hi; i += blockDim.x) p[i] = 0.0f;
+}
+
 // Destination of the retained TRAIN state: each field array copied as the forward reads it
 // (null dst[0] in an inference forward). Field order mean3d, rotation, logscale, opacity, sh0..sh3.
 struct FieldSnapshot {
@@ -798,7 +829,8 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
     const float4* __restrict__ cov_coef, const float* __restrict__ ckpt,
     CameraParams cam, const float* __restrict__ grad_rgb, const float* __restrict__ final_t,
     const uint32_t* __restrict__ last_contrib, float* __restrict__ instance_grad,
-    float* __restrict__ instance_grad_op, uint32_t* __restrict__ tile_cut, uint8_t* __restrict__ touched) {
+    float* __restrict__ instance_grad_op, uint32_t* __restrict__ tile_cut, uint8_t* __restrict__ touched,
+    SinkZeroing sinks) {
     __shared__ float4 s_r0[kBackBatch];
     __shared__ float4 s_r1[kBackBatch];
     __shared__ float4 s_r2[kBackBatch];
@@ -809,6 +841,8 @@ __global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
     __shared__ float s_acc[kRowsPerTile][kBucket][kGrad2d];
     __shared__ uint64_t s_exp2[GSX_EXPF_BLEND_TABLE_SIZE];
     __shared__ uint32_t s_max_last;
+    // every workgroup, the padding ones included, zeroes its slice of the gradient sinks first
+    zero_sink_slice(sinks, blockIdx.x);
     const int tiles = cam.tiles_x * cam.tiles_y;
     const int tile = xcd_tile_index(blockIdx.x, tiles);
     if (tile >= tiles) return;
@@ -1335,30 +1369,10 @@ __global__ __launch_bounds__(256) void projection_backward_kernel(
     const int64_t gi = first + threadIdx.x;
     const bool valid = gi < n;  // every thread stays for the block's staged stores
     // a Gaussian that no tile's backward reached (touched[gi] == 0: invisible ones included) has
-    // a +0 screen-space gradient and so zero parameter gradients, written below as for an
-    // invisible one without recomputing its projection
+    // a +0 screen-space gradient and so zero parameter gradients, which the blend backward has
+    // already stored in every sink (zero_sink_slice): a block with no reached Gaussian is done
     const bool reached = valid && touched[gi] != 0;
-    if (!__syncthreads_or(reached ? 1 : 0)) {
-        // no Gaussian of the block was reached (most blocks when a few large Gaussians cover the
-        // image): its rows of every sink are zero, stored as whole vectors where aligned
-        const int count = (int)min((int64_t)blockDim.x, n - first);
-        if (valid) {
-            reinterpret_cast<float4*>(g_rotation)[gi] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            g_opacity[gi] = 0.0f;
-        }
-        float* const rows3[3] = {g_mean3d, g_logscale, g_sh0};
-        float* const rows_sh[3] = {g_sh1, g_sh2, g_sh3};
-        for (int f = 0; f < 3 + sh_degree; ++f) {
-            const int width = f < 3 ? 3 : 3 * (2 * (f - 2) + 1);  // 3, 3, 3, then 9, 15, 21
-            float* base = (f < 3 ? rows3[f] : rows_sh[f - 3]) + first * width;
-            const int total = count * width;
-            const int vecs = vector_stores ? total / 4 : 0;
-            for (int i = threadIdx.x; i < vecs; i += blockDim.x)
-                reinterpret_cast<float4*>(base)[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            for (int i = vecs * 4 + (int)threadIdx.x; i < total; i += blockDim.x) base[i] = 0.0f;
-        }
-        return;
-    }
+    if (!__syncthreads_or(reached ? 1 : 0)) return;
     // A reached Gaussian was emitted, so preprocess_one found it visible in the forward; of its
     // projection the backward uses only the camera-space mean, the view direction and the clamped
     // colour, recomputed here by the same operations (not the covariance, conic and box, whose
