@@ -263,10 +263,11 @@ __device__ inline uint32_t digit_exclusive_scan(uint32_t v, uint32_t* s_wave, ui
 // KeyT: uint64_t or uint32_t keys. kPairs with vals_in == nullptr: each key's value is its input
 // position (the first pass of the tile sort, whose values are the emission positions). kNarrow:
 // n * sizeof(KeyT) <= 2^32, so every output byte offset fits in 32 bits. kThreads: workgroup size
-// (kChunk / kThreads keys per thread).
+// (kChunk / kThreads keys per thread). Register target: 8 waves per SIMD, except for 64-bit keys
+// with values, whose 54 KB of LDS admits two workgroups (4 waves per SIMD) per CU anyway.
 template <bool kPairs, int kBits, int kChunk, typename KeyT = uint64_t, bool kNarrow = false,
           int kThreads = kDownThreads>
-__global__ __launch_bounds__(kThreads, 8) void radix_downsweep_kernel(
+__global__ __launch_bounds__(kThreads, (kPairs && sizeof(KeyT) == 8) ? 4 : 8) void radix_downsweep_kernel(
     const KeyT* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, int64_t n,
     const uint32_t* __restrict__ n_dev, bool drop_sentinel, int shift, uint32_t dmask, int64_t num_chunks,
     const uint32_t* __restrict__ offsets, const uint32_t* __restrict__ totals, KeyT* __restrict__ keys_out,
