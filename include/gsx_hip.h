@@ -120,7 +120,7 @@ typedef struct gsx_hip_gaussians {
     int64_t count;
     int32_t sh_degree;      /* 0..3; sh1..sh3 required up to this degree, ignored above */
     const float* mean3d;
-    const float* rotation;
+    const float* rotation;  /* 16-byte aligned (one float4 per Gaussian); the others 4-byte */
     const float* logscale;
     const float* opacity;
     const float* sh0;
@@ -131,7 +131,7 @@ typedef struct gsx_hip_gaussians {
 
 typedef struct gsx_hip_gaussian_grads {
     float* mean3d;          /* sinks are overwritten, as gsx-cpu/render.c:1537-1550 */
-    float* rotation;
+    float* rotation;        /* 16-byte aligned, as gsx_hip_gaussians.rotation; the others 4-byte */
     float* logscale;
     float* opacity;
     float* sh0;

@@ -232,6 +232,56 @@ def test_backward_gradients(oracle, name):
         assert err <= GRAD_TOL, f"{field}: relative L2 {err:.3e}"
 
 
+def _with_sh(scene, degree, seed):
+    sc = scene.copy()
+    rng = np.random.default_rng(seed)
+    sc.sh_degree = degree
+    for k, c in ((1, 3), (2, 5), (3, 7)):
+        setattr(sc, f"sh{k}", (0.2 * rng.standard_normal((sc.count, c, 3))).astype(np.float32) if degree >= k else None)
+    return sc
+
+
+@pytest.mark.parametrize("degree", [1, 3])
+@pytest.mark.parametrize("offset", [0, 1])
+def test_backward_overwrites_every_sink(oracle, degree, offset):
+    """Every gradient sink, the SH bands' included, starts at 123 and ends as the oracle's gradient.
+    The blend backward's workgroups zero the sinks (16-byte stores where a sink is 16-byte aligned,
+    offset 0; scalar stores where it is not, offset 1: every sink but the rotation gradient, which
+    the ABI requires 16-byte aligned), and the projection backward writes the rows of the Gaussians
+    some tile reached. The scene has Gaussians that no tile reaches, whose
+    rows only the zeroing sets."""
+    from gsx_amd import scenes
+    from gsx_amd.backend import GaussianTensors
+    base = scenes.config3(n=30_000, width=240, height=135)
+    w = scenes.Workload("c3_sh", _with_sh(base.scene, degree, 11), base.camera)
+    print(f"[case] sinks degree={degree} offset={offset}", flush=True)
+    r, cam, g = _setup(w)
+    r.render(cam, g, train=True)
+    rng = np.random.default_rng(5)
+    grad_rgb = rng.standard_normal((3, cam.height, cam.width)).astype(np.float32)
+
+    def sink(t, off=offset):
+        if t is None:
+            return None
+        buf = torch.full((t.numel() + off,), 123.0, dtype=torch.float32, device="cuda")
+        return buf[off:].view(t.shape)
+
+    z = g.zeros_like_grads()
+    grads = GaussianTensors(sink(z.mean3d), sink(z.rotation, 0), sink(z.logscale), sink(z.opacity), sink(z.sh0),
+                            z.sh_degree, sink(z.sh1), sink(z.sh2), sink(z.sh3))
+    r.backward(torch.from_numpy(grad_rgb).cuda(), grads)
+    torch.cuda.synchronize()
+    ref = oracle.render_backward(w.scene, w.camera, grad_rgb)
+    unreached = np.all(ref["mean3d"] == 0.0, axis=1) & (ref["opacity"] == 0.0)
+    assert unreached.sum() > 1000, "the scene must hold Gaussians no tile reaches"
+    fields = ["mean3d", "rotation", "logscale", "opacity", "sh0"] + [f"sh{k}" for k in range(1, degree + 1)]
+    for field in fields:
+        got = getattr(grads, field).cpu().numpy()
+        assert np.all(got.reshape(g.mean3d.shape[0], -1)[unreached] == 0.0), f"{field}: unreached rows not zeroed"
+        err = _rel_l2(got, ref[field])
+        assert err <= GRAD_TOL, f"{field}: relative L2 {err:.3e}"
+
+
 def _mutated(scene, seed):
     sc = scene.copy()
     rng = np.random.default_rng(seed)
