@@ -43,8 +43,11 @@ def test_pointwise_losses_bit_exact(oracle, alg):
     assert np.array_equal(gm.cpu().numpy(), ref_grad)
 
 
+# images narrower or lower than the 11-pixel window (every output is boundary: map 0, no gradient),
+# with widths that take the 16-byte halo path (multiples of 4) and the one-float path
 @pytest.mark.parametrize("shape", [(3, 64, 80), (2, 3, 33, 47), (3, 11, 12), (3, 1080 // 8, 1920 // 8),
-                                   (3, 1080, 1920), (3, 1024, 1024)])
+                                   (3, 1080, 1920), (3, 1024, 1024), (1, 1, 1), (3, 4, 7), (2, 2, 10, 10),
+                                   (3, 16, 4), (3, 9, 64)])
 def test_ssim_forward_backward(oracle, shape):
     from gsx_amd.backend import Loss
     p, t = _images(4, shape)
