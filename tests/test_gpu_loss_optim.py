@@ -173,14 +173,22 @@ def test_fused_l1_ssim_matches_sequential():
 
 
 @pytest.mark.parametrize("hyper", [(1e-3, 0.9, 0.999, 0.0, 1e-8, 0.0), (1e-2, 0.8, 0.99, 0.01, 1e-6, 0.05)])
-def test_adam_bit_exact(oracle, hyper):
+# "large": 24.5M elements, above the 256 MiB of traffic from which the launch streams its accesses
+# (two float4 per thread, non-temporal), with partial last chunks and one group whose parameter
+# is not 16-byte aligned (element-wise path)
+@pytest.mark.parametrize("size_set", ["small", "large"])
+def test_adam_bit_exact(oracle, hyper, size_set):
     from gsx_amd.backend import Adam
     lr, b1, b2, wd, eps, mg = hyper
     rng = np.random.default_rng(8)
-    sizes = [3001, 4 * 1000, 17]
+    sizes = [3001, 4 * 1000, 17] if size_set == "small" else [5_250_009, 7_000_012, 5_250_009, 1_750_003, 5_250_009]
     params = [rng.standard_normal(s).astype(np.float32) for s in sizes]
     grads = [rng.standard_normal(s).astype(np.float32) * 0.1 for s in sizes]
     pt = [torch.from_numpy(x.copy()).cuda() for x in params]
+    if size_set == "large":
+        shifted = torch.empty(sizes[3] + 1, dtype=torch.float32, device="cuda")[1:]
+        shifted.copy_(pt[3])
+        pt[3] = shifted
     gt = [torch.from_numpy(x).cuda() for x in grads]
     opt = Adam([dict(parameter=p, gradient=g, learning_rate=lr, beta1=b1, beta2=b2, weight_decay=wd, epsilon=eps,
                      max_grad=mg) for p, g in zip(pt, gt)])
