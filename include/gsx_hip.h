@@ -385,7 +385,9 @@ gsx_hip_status gsx_hip_adam_step_f32_kernel_launch(float* parameter, const float
                                                    float epsilon, float max_grad, double bias_correction1,
                                                    double bias_correction2, hipStream_t stream);
 /* All groups of one optimizer step in a single launch (the CUDA backend issues one launch
- * per group, gsx/src/gsx-cuda/optim.c:757-796). */
+ * per group, gsx/src/gsx-cuda/optim.c:757-796). Above 256 MiB of traffic (28 bytes per element
+ * over all groups) the launch reads and writes with non-temporal accesses; the results are the
+ * same bits either way. */
 gsx_hip_status gsx_hip_adam_step_multi_launch(const gsx_hip_adam_group* groups, int32_t group_count,
                                               hipStream_t stream);
 
